@@ -1,0 +1,82 @@
+/* TEST INFRASTRUCTURE — the CPU oracle for the FastGS training path.
+ * Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may
+ * load liboracle.so; the product never does.
+ *
+ * Instantiates oracle_impl.inc twice:
+ *   orc_f_*  float, deterministic exp/log, explicit fmaf  (the oracle)
+ *   orc_d_*  double, libm exp/log                          (FD checks only)
+ *
+ * Parity pins (see tests/test_oracle.py):
+ *   orc_expf / orc_logf        vs libm double exp/log (ulp bound), special cases
+ *   orc_float_to_half_bits     vs numpy float16 (RNE) over a sweep
+ *   preprocess                 closed-form EWA in double (conic * cov2d = I),
+ *                              rotation invariance, SH constants vs a double
+ *                              brute-force real-SH evaluation
+ *   tile culling               brute force over pixel centres (no dropped tile
+ *                              holds a pixel with alpha >= 1/255)
+ *   bin                        numpy stable sort of 64-bit (tile<<32|depth) keys
+ *   blend_forward              independent per-pixel numpy loop
+ *   blend/preprocess backward  double-precision central differences of the
+ *                              orc_d_ forward (exact_grad mode), plus closed-form
+ *                              checks of the reference-specific quirks
+ *   l1 / ssim                  closed form, FD (double), brute-force convolution
+ *   adam                       closed form (Kingma & Ba 2015)
+ */
+#include <math.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include "detmath.h"
+
+/* ---------------- float instance (the oracle) ---------------- */
+#define REAL float
+#define SFX(name) orc_f_##name
+#define R_EXP(x) orc_expf(x)
+#define R_LOG(x) orc_logf(x)
+#define R_SQRT(x) sqrtf(x)
+#define R_FMA(a, b, c) fmaf(a, b, c)
+#define R_FLOOR(x) floorf(x)
+#define R_CEIL(x) ceilf(x)
+#define R_FMIN(a, b) fminf(a, b)
+#define R_FMAX(a, b) fmaxf(a, b)
+#define R_FABS(a) fabsf(a)
+#define R_COPYSIGN(a, b) copysignf(a, b)
+#define R_HALF_ROUND(x) orc_round_half(x)
+#include "oracle_impl.inc"
+#undef REAL
+#undef SFX
+#undef R_EXP
+#undef R_LOG
+#undef R_SQRT
+#undef R_FMA
+#undef R_FLOOR
+#undef R_CEIL
+#undef R_FMIN
+#undef R_FMAX
+#undef R_FABS
+#undef R_COPYSIGN
+#undef R_HALF_ROUND
+
+/* ---------------- double instance (finite-difference checker) ---------------- */
+#define REAL double
+#define SFX(name) orc_d_##name
+#define R_EXP(x) exp(x)
+#define R_LOG(x) log(x)
+#define R_SQRT(x) sqrt(x)
+#define R_FMA(a, b, c) ((a) * (b) + (c))
+#define R_FLOOR(x) floor(x)
+#define R_CEIL(x) ceil(x)
+#define R_FMIN(a, b) fmin(a, b)
+#define R_FMAX(a, b) fmax(a, b)
+#define R_FABS(a) fabs(a)
+#define R_COPYSIGN(a, b) copysign(a, b)
+#define R_HALF_ROUND(x) (x)
+#include "oracle_impl.inc"
+
+/* ---------------- exported helpers ---------------- */
+void orc_expf_array(int64_t n, const float* x, float* y) { for (int64_t i = 0; i < n; ++i) y[i] = orc_expf(x[i]); }
+void orc_logf_array(int64_t n, const float* x, float* y) { for (int64_t i = 0; i < n; ++i) y[i] = orc_logf(x[i]); }
+void orc_half_bits_array(int64_t n, const float* x, uint16_t* y) { for (int64_t i = 0; i < n; ++i) y[i] = orc_float_to_half_bits(x[i]); }
+void orc_round_half_array(int64_t n, const float* x, float* y) { for (int64_t i = 0; i < n; ++i) y[i] = orc_round_half(x[i]); }
+int orc_version(void) { return 1; }
