@@ -1,0 +1,168 @@
+/* tinygs_amd — C ABI of the MI355X (gfx950) FastGS training path.
+ *
+ * This is the drop-in boundary for tinygs's rasterizer / loss / optimizer
+ * plugin interfaces. Every entry point takes plain device pointers, sizes and
+ * a hipStream_t (passed as void*), returns a status code (0 = success) and
+ * leaves a message for tgs_last_error() on failure. The C++ classes in
+ * include/tinygs_amd/tinygs.hpp wrap these calls with the reference's class
+ * names and signatures and rethrow failures as std::runtime_error, as the
+ * reference does (CUDA_CHECK_THROW, tinygs/include/tinygs/cuda/common_host.hpp:104).
+ *
+ * Threading: a handle is not re-entrant (as FastGSRasterizer::Impl). Calls on
+ * different handles may run concurrently on different streams.
+ * Memory: parameters, gradients, images and loss buffers are owned by the
+ * caller; every handle owns its grow-only device scratch.
+ * Images are fp32, channel-planar, padded to multiples of 8 and 8x8-tiled
+ * (tinygs/include/tinygs/common.hpp:366-414).
+ */
+#ifndef TINYGS_AMD_H
+#define TINYGS_AMD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define TGS_OK 0
+#define TGS_ERR_INVALID 1
+#define TGS_ERR_HIP 2
+#define TGS_ERR_STATE 3
+#define TGS_ERR_UNSUPPORTED 4
+
+#define TGS_DTYPE_FLOAT32 0
+#define TGS_DTYPE_FLOAT16 1
+
+/* SoA Gaussian parameters (or their gradients), as GPUGaussian3d
+ * (tinygs/include/tinygs/core/gpu_gaussian.hpp:9-73): means[3n], scales[3n]
+ * (log), rotations[4n] (r,x,y,z), opacities[n] (logit), sh0[3n],
+ * sh_rest[45n] (15 bases per Gaussian whatever the degree). sh_dtype applies
+ * to sh0 and sh_rest of parameters; gradients are always float32. */
+typedef struct tgs_gaussians {
+    void* means;
+    void* scales;
+    void* rotations;
+    void* opacities;
+    void* sh0;
+    void* sh_rest;
+    int64_t n;
+    int32_t sh_degree;
+    int32_t sh_dtype;
+    float scene_scale;
+} tgs_gaussians;
+
+/* Camera as GPUBatchInput (tinygs/include/tinygs/dataloader/dataloader.hpp:8-14):
+ * K and w2c in glm column-major memory order (fx = K[0], fy = K[4],
+ * cx = K[6], cy = K[7]; translation in w2c[12..14]). */
+typedef struct tgs_camera {
+    uint32_t width;
+    uint32_t height;
+    float near_plane;
+    float far_plane;
+    float K[9];
+    float w2c[16];
+} tgs_camera;
+
+/* DensificationInfo per Gaussian (tinygs/include/tinygs/core/gaussian.hpp:18-23):
+ * {accum_counter, accum_grad_mean2d, accum_absgrad_mean2d, max_radii_screen}. */
+
+typedef struct tgs_rasterizer tgs_rasterizer;
+typedef struct tgs_loss tgs_loss;
+typedef struct tgs_adam tgs_adam;
+
+/* Thread-local message of the last failing call on this thread. */
+const char* tgs_last_error(void);
+/* Library version (monotonic integer). */
+int tgs_version(void);
+
+/* ---- rasterizer: replaces create_rasterizer("fastgs") / FastGSRasterizer
+ * (tinygs/src/rasterizer/rasterizer.cpp:44-53, tinygs/src/rasterizer/fastgs.cu:85-398). */
+int tgs_rasterizer_create(const char* type, tgs_rasterizer** out);
+int tgs_rasterizer_destroy(tgs_rasterizer* r);
+/* FastGSRasterizer::set_gaussians (fastgs.cu:388-392). Pointers are kept, not copied. */
+int tgs_rasterizer_set_gaussians(tgs_rasterizer* r, const tgs_gaussians* g);
+/* FastGSRasterizer::forward (fastgs.cu:89-236). image: fp32 [3 * channel_stride].
+ * densification_info: optional device float4[n] (max_radii_screen updated). */
+int tgs_rasterizer_forward(tgs_rasterizer* r, const tgs_camera* cam, void* image, int32_t image_dtype,
+                           void* densification_info, void* stream);
+/* FastGSRasterizer::backward (fastgs.cu:238-384). Accumulates (+=) into grads.
+ * Must follow a forward on the same Gaussians and camera. */
+int tgs_rasterizer_backward(tgs_rasterizer* r, const void* grad_image, const void* image,
+                            const tgs_gaussians* grads, void* densification_info, void* stream);
+/* Counts of the last forward: visible primitives, instances, tiles. */
+int tgs_rasterizer_counts(tgs_rasterizer* r, int64_t* n_visible, int64_t* n_instances, int64_t* n_tiles);
+
+/* Internal buffers of the last forward, for parity tests (device pointers). */
+typedef struct tgs_debug_view {
+    const uint32_t* n_touched;     /* [n] */
+    const uint32_t* bounds;        /* [2n]: x_min | x_max << 16, y_min | y_max << 16 */
+    const float* mean2d;           /* [2n] */
+    const float* conic_opacity;    /* [4n] */
+    const float* color;            /* [4n]: r, g, b (unclamped), ln(255 * opacity) */
+    const uint32_t* depth_sorted_keys;  /* [n_visible] depth bits, ascending */
+    const uint32_t* depth_sorted_prims; /* [n_visible] */
+    const uint32_t* instance_tiles;     /* [n_instances] sorted */
+    const uint32_t* instance_prims;     /* [n_instances] */
+    const uint32_t* tile_ranges;        /* [2 * n_tiles] */
+    const uint32_t* n_contrib;          /* [channel_stride] */
+    const uint32_t* tile_max;           /* [n_tiles] */
+    const float* grad2d;                /* [12n] after backward */
+    int64_t n_visible;
+    int64_t n_instances;
+    int64_t n_tiles;
+} tgs_debug_view;
+int tgs_rasterizer_debug_view(tgs_rasterizer* r, tgs_debug_view* out);
+
+/* ---- losses: replace create_loss("l1" | "fused_ssim") and LossBase::evaluate
+ * (tinygs/src/loss/loss.cu:13-27, tinygs/include/tinygs/loss/loss.hpp:6-28).
+ * Accumulate: loss[i] += ..., grad[i] += ... (loss and grad may be NULL for l1,
+ * grad may be NULL for fused_ssim). */
+typedef struct tgs_loss_context {
+    const void* pred;
+    const void* target;
+    void* loss;
+    void* grad;
+    uint32_t width;
+    uint32_t height;
+    uint32_t channel;
+    int32_t dtype;
+} tgs_loss_context;
+int tgs_loss_create(const char* type, tgs_loss** out);
+int tgs_loss_destroy(tgs_loss* l);
+int tgs_loss_evaluate(tgs_loss* l, const tgs_loss_context* ctx, float scale, void* stream);
+
+/* ---- SimpleAdam: replaces create_optimizer("simple_adam") / SimpleAdam
+ * (tinygs/src/optim/optim.cu:86-105, tinygs/src/optim/simple_adam.cu:406-580). */
+typedef struct tgs_adam_params {
+    float beta1, beta2, epsilon;
+    float means_lr, shs_lr, opacities_lr, scales_lr, rotations_lr;
+    float max_grad_1;
+    float opacities_l1, scales_l1;
+    int32_t decay_mean;  /* decay_reduction == "mean": L1 decay scaled by 1/n */
+} tgs_adam_params;
+int tgs_adam_create(const tgs_gaussians* params, const tgs_gaussians* grads, tgs_adam** out);
+int tgs_adam_destroy(tgs_adam* a);
+int tgs_adam_set_params(tgs_adam* a, const tgs_adam_params* p);
+int tgs_adam_get_params(tgs_adam* a, tgs_adam_params* p);
+int tgs_adam_set_lr(tgs_adam* a, float global_lr);
+float tgs_adam_get_lr(tgs_adam* a);
+/* Rebind parameter / gradient pointers (sizes must match the moments). */
+int tgs_adam_set_gaussians(tgs_adam* a, const tgs_gaussians* params, const tgs_gaussians* grads);
+/* OptimizerBase::step(scale, stream): gradients multiplied by scale. */
+int tgs_adam_step(tgs_adam* a, float scale, void* stream);
+/* OptimizerBase::reset(): zero moments and the step counter. */
+int tgs_adam_reset(tgs_adam* a, void* stream);
+int64_t tgs_adam_global_steps(tgs_adam* a);
+/* Device pointers of a group's moments; group in 0..5 =
+ * means, opacities, rotations, scales, sh0, sh_rest. */
+int tgs_adam_moments(tgs_adam* a, int32_t group, float** first, float** second);
+
+/* ---- self tests (device): deterministic exp/log over arrays, wave primitives. */
+int tgs_selftest_detmath(int32_t op, const float* in, float* out, int64_t n, void* stream);
+int tgs_selftest_wave(const uint32_t* in, uint32_t* out, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

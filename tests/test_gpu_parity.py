@@ -1,0 +1,312 @@
+"""Parity of the HIP path (called through the C ABI) with the CPU oracle.
+
+Bars: tile assignment, sorted key lists and
+per-tile ranges bit-exact; fp32 pixels within 1e-5 relative; gradients within
+1e-4 relative (normwise per parameter group; atomic summation order differs).
+"""
+import numpy as np
+import pytest
+
+from tinygs_amd import scenes
+from tinygs_amd.image import ImageShape, tiled_index
+
+from helpers import (PIXEL_ATOL, PIXEL_RTOL, assert_grads_close, gpu_backward, gpu_render, normwise_err)
+
+pytestmark = pytest.mark.gpu
+
+
+def _dev(x):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(x)).cuda()
+
+
+# ---------------------------------------------------------------- primitives
+
+def test_wave_primitives(hip):
+    import torch
+    from tinygs_amd import _lib
+    L = _lib.load()
+    rng = np.random.default_rng(0)
+    vals = rng.integers(0, 1000, 64).astype(np.uint32)
+    inp = _dev(vals.view(np.int32))
+    out = torch.zeros(256, dtype=torch.int32, device="cuda")
+    _lib.check(L.tgs_selftest_wave(inp.data_ptr(), out.data_ptr(), None))
+    torch.cuda.synchronize()
+    o = out.cpu().numpy().view(np.uint32)
+    assert np.array_equal(o[:64], np.cumsum(vals).astype(np.uint32))
+    assert o[64] == vals.sum() and o[65] == vals.max()
+    assert np.float32(o[66:67].view(np.float32)[0]) == np.float32(vals.astype(np.float64).sum())
+    odd = (vals & 1) != 0
+    assert o[67] == odd.sum()
+    assert np.array_equal(o[128:192], np.concatenate([[0], np.cumsum(odd)[:-1]]).astype(np.uint32))
+
+
+@pytest.mark.parametrize("op", [0, 1, 2, 3, 4, 5])
+def test_detmath_bit_exact_vs_oracle(hip, orc, op):
+    import torch
+    from tinygs_amd import _lib
+    rng = np.random.default_rng(op)
+    if op in (0, 2):
+        x = np.concatenate([rng.uniform(-110, 90, 1 << 20), rng.uniform(-12, 0, 1 << 20)]).astype(np.float32)
+    elif op == 1:
+        x = np.concatenate([rng.uniform(1.0, 255.0, 1 << 20), np.exp(rng.uniform(-87, 88, 1 << 20))]).astype(np.float32)
+    else:
+        x = np.concatenate([rng.standard_normal(1 << 20) * 100, np.abs(rng.standard_normal(1 << 20))]).astype(np.float32)
+    xin = _dev(x)
+    out = torch.empty_like(xin)
+    _lib.check(_lib.load().tgs_selftest_detmath(op, xin.data_ptr(), out.data_ptr(), x.size, None))
+    torch.cuda.synchronize()
+    y = out.cpu().numpy()
+    if op == 0:
+        ref = orc.expf(x)
+    elif op == 1:
+        ref = orc.logf(x)
+    elif op == 2:
+        ref = orc.expf(np.where(x <= 0, x, -x).astype(np.float32))
+    elif op == 3:
+        ref = (x / (x * np.float32(0.7) + np.float32(1.3))).astype(np.float32)
+    elif op == 4:
+        ref = np.sqrt(np.abs(x)).astype(np.float32)
+        x = np.abs(x)
+        xin = _dev(x)
+        _lib.check(_lib.load().tgs_selftest_detmath(op, xin.data_ptr(), out.data_ptr(), x.size, None))
+        torch.cuda.synchronize()
+        y = out.cpu().numpy()
+    else:
+        ref = orc.round_half(x)
+    assert np.array_equal(y.view(np.uint32), ref.view(np.uint32)), (op, np.sum(y.view(np.uint32) != ref.view(np.uint32)))
+
+
+# ---------------------------------------------------------------- forward
+
+def _check_forward(scene, orc):
+    run = gpu_render(scene)
+    pre, bins, fwd = orc.render(scene, "f")
+    dv = run["dv"]
+    n = scene.n
+    vis = pre["n_touched"] > 0
+    # visibility and exact tile counts
+    assert np.array_equal(dv["n_touched"].view(np.uint32), pre["n_touched"])
+    # bounds, mean2d, conic/opacity, colour, power threshold (visible only)
+    b = dv["bounds"].view(np.uint32).reshape(n, 2)
+    ob = pre["bounds"].reshape(n, 4).astype(np.uint32)
+    assert np.array_equal(b[vis, 0] & 0xffff, ob[vis, 0]) and np.array_equal(b[vis, 0] >> 16, ob[vis, 1])
+    assert np.array_equal(b[vis, 1] & 0xffff, ob[vis, 2]) and np.array_equal(b[vis, 1] >> 16, ob[vis, 3])
+    assert np.array_equal(dv["mean2d"].reshape(n, 2)[vis].view(np.uint32), pre["mean2d"].reshape(n, 2)[vis].view(np.uint32))
+    assert np.array_equal(dv["conic_opacity"].reshape(n, 4)[vis].view(np.uint32),
+                          pre["conic_opacity"].reshape(n, 4)[vis].view(np.uint32))
+    col = dv["color"].reshape(n, 4)
+    assert np.array_equal(col[vis, :3].view(np.uint32), pre["color"].reshape(n, 3)[vis].view(np.uint32))
+    assert np.array_equal(col[vis, 3].view(np.uint32), pre["power_thr"][vis].view(np.uint32))
+    # depth order, instances, ranges: bit-exact
+    assert dv["n_visible"] == bins["n_visible"] and dv["n_instances"] == bins["n_instances"]
+    assert np.array_equal(dv["depth_sorted_prims"].view(np.uint32), bins["sorted_prims"])
+    assert np.array_equal(dv["depth_sorted_keys"].view(np.uint32),
+                          pre["depth"][bins["sorted_prims"]].astype(np.float32).view(np.uint32))
+    assert np.array_equal(dv["instance_tiles"].view(np.uint32), bins["inst_tile"])
+    assert np.array_equal(dv["instance_prims"].view(np.uint32), bins["inst_prim"])
+    assert np.array_equal(dv["tile_ranges"].view(np.uint32), bins["ranges"])
+    # pixels and per-pixel contributor counts
+    img = run["image"]
+    err = np.abs(img - fwd["image"])
+    assert np.all(err <= PIXEL_RTOL * np.abs(fwd["image"]) + PIXEL_ATOL), err.max()
+    assert np.array_equal(run["n_contrib"], fwd["n_contrib"])
+    assert np.array_equal(dv["tile_max"].view(np.uint32), fwd["tile_max"])
+    return run, (pre, bins, fwd)
+
+
+def test_forward_config1(hip, orc):
+    _check_forward(scenes.config1(), orc)
+
+
+@pytest.mark.parametrize("seed", [11, 12])
+def test_forward_config2_reduced(hip, orc, seed):
+    s = scenes.config2(seed=seed, n=20000, width=320, height=240)
+    _check_forward(s, orc)
+
+
+def test_forward_odd_size_and_outliers(hip, orc):
+    s = scenes.config1(seed=5, n=800)
+    cam = scenes.Camera(83, 57, 70.0, 70.0, 41.0, 29.0, s.camera.w2c)
+    scales = s.scales.copy()
+    scales[::50] = -0.8        # large Gaussians: wave-cooperative tile counting / emission
+    s = scenes.Scene(s.means, scales, s.rotations, s.opacities, s.sh0, s.sh_rest, 0, cam,
+                     np.zeros(cam.shape.padded_size, np.float32))
+    run, _ = _check_forward(s, orc)
+    assert np.all(np.isfinite(run["image"]))   # padding written (0), nothing left as NaN
+
+
+def test_forward_nothing_visible(hip, orc):
+    s = scenes.config1(seed=3, n=100)
+    w2c = np.eye(4)
+    w2c[2, 3] = -5.0   # all Gaussians behind the camera
+    cam = scenes.Camera(64, 64, 64.0, 64.0, 32.0, 32.0, w2c)
+    s = scenes.Scene(s.means, s.scales, s.rotations, s.opacities, s.sh0, s.sh_rest, 0, cam, s.target)
+    run = gpu_render(s)
+    assert run["dv"]["n_visible"] == 0 and run["dv"]["n_instances"] == 0
+    assert np.all(run["image"] == 0)
+
+
+# ---------------------------------------------------------------- backward
+
+def _grad_image(scene, seed=9):
+    return scenes.grad_image(seed, scene.camera.shape)
+
+
+def _check_backward(scene, orc, gimg, rtol=1e-4):
+    run = gpu_render(scene)
+    pre, bins, fwd = orc.render(scene, "f")
+    g2d = orc.blend_backward(scene, pre, bins, fwd, gimg, "f")
+    ref = orc.preprocess_backward(scene, pre, g2d, "f")
+    got = gpu_backward(run, gimg)
+    worst = assert_grads_close(got, ref, rtol=rtol)
+    return worst
+
+
+def test_backward_config1(hip, orc):
+    s = scenes.config1()
+    _check_backward(s, orc, _grad_image(s))
+
+
+def test_backward_config2_reduced(hip, orc):
+    s = scenes.config2(seed=13, n=20000, width=320, height=240)
+    _check_backward(s, orc, _grad_image(s))
+
+
+def test_backward_sh_degrees(hip, orc):
+    base = scenes.config2(seed=14, n=5000, width=160, height=128)
+    for deg in (0, 1, 2, 3):
+        s = scenes.perturb_sh_degree(base, deg)
+        _check_backward(s, orc, _grad_image(s, 3 + deg))
+
+
+def test_backward_accumulates(hip, orc):
+    """backward adds into the gradient buffers (fastgs.cu:325-370 contract)."""
+    import torch
+    from tinygs_amd.core import Image
+    s = scenes.config1(seed=2)
+    run = gpu_render(s)
+    gimg = _grad_image(s)
+    g1 = gpu_backward(run, gimg)
+    ctx = run["ctx"]
+    grads = run["g"].gradient_like()
+    for t in grads.tensors():
+        t.fill_(1.0)
+    ctx.gaussians_grad = grads
+    ctx.grad_output.image = Image(ctx.fwd_output.image.shape, "float32", torch.from_numpy(gimg).cuda())
+    run["r"].backward(ctx)
+    torch.cuda.synchronize()
+    got = grads.means().cpu().numpy().reshape(-1) - 1.0
+    assert normwise_err(got, g1["means"]) < 1e-5
+
+
+def test_densification_info(hip, orc):
+    s = scenes.config1(seed=4)
+    run = gpu_render(s, densif=True)
+    gimg = _grad_image(s)
+    pre, bins, fwd = orc.render(s, "f")
+    g2d = orc.blend_backward(s, pre, bins, fwd, gimg, "f")
+    dens = np.zeros(4 * s.n, np.float32)
+    mr = np.zeros(s.n, np.float32)
+    orc.preprocess(s, "f", max_radii=mr)
+    orc.preprocess_backward(s, pre, g2d, "f", densif=dens)
+    gpu_backward(run, gimg)
+    d = run["ctx"].densification_info.cpu().numpy()
+    assert np.array_equal(d[:, 3], mr)
+    assert np.array_equal(d[:, 0], dens.reshape(-1, 4)[:, 0])
+    assert normwise_err(d[:, 1], dens.reshape(-1, 4)[:, 1]) < 1e-4
+    assert normwise_err(d[:, 2], dens.reshape(-1, 4)[:, 2]) < 1e-4
+
+
+# ---------------------------------------------------------------- losses
+
+def _loss_gpu(kind, pred, targ, shape, scale):
+    import torch
+    from tinygs_amd.core import Image, LossContext
+    from tinygs_amd.loss import create_loss
+    L = create_loss(kind)
+    ctx = LossContext(Image(shape, "float32", _dev(pred)), Image(shape, "float32", _dev(targ)),
+                      Image.empty(shape), Image.empty(shape))
+    L.evaluate(ctx, scale)
+    torch.cuda.synchronize()
+    return ctx.loss.data.cpu().numpy(), ctx.grad.data.cpu().numpy()
+
+
+@pytest.mark.parametrize("wh", [(64, 64), (61, 45), (800, 600)])
+def test_l1_and_ssim(hip, orc, wh):
+    shape = ImageShape(*wh)
+    rng = np.random.default_rng(wh[0])
+    targ = rng.random(shape.padded_size).astype(np.float32)
+    pred = np.clip(targ + rng.normal(0, 0.3, shape.padded_size), -0.2, 1.2).astype(np.float32)
+    lg, gg = _loss_gpu("l1", pred, targ, shape, 0.8)
+    lo, go = orc.l1(pred, targ, shape, np.float32(0.8))
+    assert np.array_equal(lg, lo) and np.array_equal(gg, go)
+    lg, gg = _loss_gpu("fused_ssim", pred, targ, shape, 0.2)
+    lo, go = orc.ssim(pred, targ, shape, np.float32(0.2))
+    idx = np.concatenate([c * shape.channel_stride + tiled_index(shape).reshape(-1) for c in range(3)])
+    assert np.allclose(lg[idx], lo[idx], rtol=1e-5, atol=1e-9), np.abs(lg[idx] - lo[idx]).max()
+    assert normwise_err(gg[idx], go[idx]) < 1e-5
+
+
+# ---------------------------------------------------------------- adam
+
+def test_adam_matches_oracle(hip, orc):
+    import torch
+    from tinygs_amd.core import GPUGaussian3d
+    from tinygs_amd.optim import create_optimizer
+    s = scenes.config2(seed=15, n=3000, width=64, height=64)
+    g = GPUGaussian3d.from_scene(s)
+    g.set_scene_scale(1.7)
+    grads = g.gradient_like()
+    rng = np.random.default_rng(1)
+    host_grads = {}
+    for name, t in zip(("means", "scales", "rotations", "opacities", "sh0", "sh_rest"), grads.tensors()):
+        v = (rng.standard_normal(t.numel()) * 0.7).astype(np.float32)
+        host_grads[name] = v
+        t.copy_(torch.from_numpy(v.reshape(t.shape)))
+    opt = create_optimizer("simple_adam", g, grads)
+    opt.set_params({"epsilon": 1e-15, "shs_lr": 5e-3, "opacities_l1": 0.01})
+    theta = orc.params(s, "f")
+    m1 = {k: np.zeros_like(v) for k, v in theta.items()}
+    m2 = {k: np.zeros_like(v) for k, v in theta.items()}
+    lr = {"means": 1.6e-4, "scene_scale": 1.7, "opacities": 5e-2, "rotations": 1e-3, "scales": 5e-3, "shs": 5e-3}
+    for step in (1, 2, 3):
+        opt.step(0.5)
+        orc.adam_step(theta, host_grads, m1, m2, lr, step, grad_scale=0.5, eps=1e-15,
+                      decay={"opacities": np.float32(0.01) * np.float32(1.0 / s.n)})
+    torch.cuda.synchronize()
+    got = {"means": g.means(), "scales": g.scales(), "rotations": g.rotations(), "opacities": g.opacities(),
+           "sh0": g.sh_coefficient_0(), "sh_rest": g.sh_coefficients_rest()}
+    for k, t in got.items():
+        a = t.float().cpu().numpy().reshape(-1)
+        assert np.array_equal(a.view(np.uint32), theta[k].view(np.uint32)), (k, np.abs(a - theta[k]).max())
+        gm1, gm2 = opt.moments(k)
+        assert np.array_equal(gm1.cpu().numpy(), m1[k]) and np.array_equal(gm2.cpu().numpy(), m2[k])
+    assert opt.global_steps() == 3
+
+
+# ---------------------------------------------------------------- full iteration
+
+def test_train_step_config2_reduced(hip, orc):
+    """fwd + 0.8 L1 + 0.2 (1 - SSIM) + bwd + SimpleAdam, as Orchestrator::train_step."""
+    import torch
+    from tinygs_amd.train import TrainStep
+    s = scenes.config2(seed=16, n=20000, width=320, height=240)
+    lr = {"means": 1.6e-4, "scene_scale": 1.0, "opacities": 5e-2, "rotations": 1e-3, "scales": 5e-3, "shs": 5e-3}
+    ts = TrainStep(s, l1_weight=0.8, ssim_weight=0.2, eps=1e-15, shs_lr=5e-3)
+    ts.step()
+    torch.cuda.synchronize()
+    ref = orc.run_iteration(s, 0.8, 0.2, lr=lr, eps=1e-15)
+    # pixels and loss gradient image
+    assert np.allclose(ts.image(), ref["fwd"]["image"], rtol=PIXEL_RTOL, atol=PIXEL_ATOL)
+    shape = s.camera.shape
+    idx = np.concatenate([c * shape.channel_stride + tiled_index(shape).reshape(-1) for c in range(3)])
+    assert normwise_err(ts.grad_image()[idx], ref["grad_image"][idx]) < 1e-5
+    # parameters after one Adam step: the update is ~lr * sign(g), so compare the step
+    theta0 = orc.params(s, "f")
+    th = ts.params()
+    for k in theta0:
+        d_gpu = th[k] - theta0[k]
+        d_ref = ref["theta"][k] - theta0[k]
+        assert normwise_err(d_gpu, d_ref) < 2e-2, k   # sign flips only where |g| ~ 0
+        assert np.mean(np.sign(d_gpu) == np.sign(d_ref)) > 0.995, k

@@ -1,0 +1,633 @@
+// C ABI (include/tinygs_amd.h): handles, grow-only device scratch, the
+// forward / backward stage order of FastGSRasterizer and the loss and
+// optimizer plugins.
+//
+// Stage order follows tinygs/src/rasterizer/fastgs_ours/forward.cu:20-292 and
+// backward.cu:211-349. Differences, each deliberate:
+//   * one host synchronisation per forward (to size the instance buffers)
+//     instead of three; no helper stream or events;
+//   * the pose block is not copied to the device: w2c rows and the camera
+//     centre travel as kernel arguments;
+//   * visible primitives are compacted by prefix scan (deterministic order);
+//   * no per-bucket checkpoints (the backward recomputes them).
+#include <math.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <string>
+
+#include "../../include/tinygs_amd.h"
+#include "common.h"
+#include "kernels.h"
+
+using namespace tgs;
+
+namespace {
+
+thread_local std::string g_error;
+
+int fail(int code, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof(buf), fmt, ap);
+    va_end(ap);
+    g_error = buf;
+    return code;
+}
+
+#define TGS_HIP(call)                                                                                  \
+    do {                                                                                               \
+        hipError_t e_ = (call);                                                                        \
+        if (e_ != hipSuccess) return fail(TGS_ERR_HIP, "%s failed at %s:%d: %s", #call, __FILE__, __LINE__, \
+                                          hipGetErrorString(e_));                                      \
+    } while (0)
+
+#define TGS_CHECK_LAUNCH()                                                                             \
+    do {                                                                                               \
+        hipError_t e_ = hipGetLastError();                                                             \
+        if (e_ != hipSuccess) return fail(TGS_ERR_HIP, "kernel launch failed at %s:%d: %s", __FILE__, __LINE__, \
+                                          hipGetErrorString(e_));                                      \
+    } while (0)
+
+struct DevBuf {
+    void* p = nullptr;
+    size_t bytes = 0;
+    template <typename T>
+    T* as() const { return (T*)p; }
+};
+
+// Grow-only device allocation. A grown buffer is released only after the
+// stream has drained, so kernels of earlier calls never see freed memory.
+int ensure(DevBuf& b, size_t bytes, hipStream_t s) {
+    if (bytes <= b.bytes && b.p) return TGS_OK;
+    if (b.p) {
+        TGS_HIP(hipStreamSynchronize(s));
+        TGS_HIP(hipFree(b.p));
+        b.p = nullptr;
+        b.bytes = 0;
+    }
+    size_t nb = bytes + bytes / 4 + 256;
+    TGS_HIP(hipMalloc(&b.p, nb));
+    b.bytes = nb;
+    return TGS_OK;
+}
+
+void release(DevBuf& b) {
+    if (b.p) (void)hipFree(b.p);
+    b.p = nullptr;
+    b.bytes = 0;
+}
+
+#define TGS_TRY(expr)                  \
+    do {                               \
+        int rc_ = (expr);              \
+        if (rc_ != TGS_OK) return rc_; \
+    } while (0)
+
+int build_camera(const tgs_camera* c, CamParams& cp) {
+    if (!c) return fail(TGS_ERR_INVALID, "camera is NULL");
+    if (c->width == 0 || c->height == 0) return fail(TGS_ERR_INVALID, "image size %ux%u", c->width, c->height);
+    if (c->width > 65535u * 16u || c->height > 65535u * 16u)
+        return fail(TGS_ERR_INVALID, "image too large for 16-bit tile bounds");
+    memset(&cp, 0, sizeof(cp));
+    cp.fx = c->K[0];
+    cp.fy = c->K[4];
+    cp.cx = c->K[6];
+    cp.cy = c->K[7];
+    cp.near_ = c->near_plane;
+    cp.far_ = c->far_plane;
+    // glm column-major: element (row r, col k) at w2c[k * 4 + r]; rows are
+    // glm::transpose(w2c) as uploaded by fastgs.cu:99.
+    for (int k = 0; k < 4; ++k) {
+        cp.r1[k] = c->w2c[k * 4 + 0];
+        cp.r2[k] = c->w2c[k * 4 + 1];
+        cp.r3[k] = c->w2c[k * 4 + 2];
+    }
+    // camera centre = column 3 of inverse(w2c) (fastgs.cu:96,100), in double
+    double m[16], inv[16];
+    for (int r = 0; r < 4; ++r)
+        for (int k = 0; k < 4; ++k) m[r * 4 + k] = c->w2c[k * 4 + r];
+    // Gauss-Jordan with partial pivoting on the row-major copy
+    double a[4][8];
+    for (int r = 0; r < 4; ++r) {
+        for (int k = 0; k < 4; ++k) a[r][k] = m[r * 4 + k];
+        for (int k = 0; k < 4; ++k) a[r][4 + k] = (r == k) ? 1.0 : 0.0;
+    }
+    for (int col = 0; col < 4; ++col) {
+        int piv = col;
+        for (int r = col + 1; r < 4; ++r)
+            if (fabs(a[r][col]) > fabs(a[piv][col])) piv = r;
+        if (fabs(a[piv][col]) < 1e-30) return fail(TGS_ERR_INVALID, "w2c is singular");
+        if (piv != col)
+            for (int k = 0; k < 8; ++k) {
+                double t = a[col][k];
+                a[col][k] = a[piv][k];
+                a[piv][k] = t;
+            }
+        const double d = a[col][col];
+        for (int k = 0; k < 8; ++k) a[col][k] /= d;
+        for (int r = 0; r < 4; ++r) {
+            if (r == col) continue;
+            const double f = a[r][col];
+            for (int k = 0; k < 8; ++k) a[r][k] -= f * a[col][k];
+        }
+    }
+    for (int r = 0; r < 4; ++r)
+        for (int k = 0; k < 4; ++k) inv[r * 4 + k] = a[r][4 + k];
+    cp.cam_pos[0] = (float)inv[0 * 4 + 3];
+    cp.cam_pos[1] = (float)inv[1 * 4 + 3];
+    cp.cam_pos[2] = (float)inv[2 * 4 + 3];
+    cp.w = (float)c->width;
+    cp.h = (float)c->height;
+    cp.width = c->width;
+    cp.height = c->height;
+    cp.grid_w = (c->width + 15u) / 16u;
+    cp.grid_h = (c->height + 15u) / 16u;
+    cp.tiled_w = (c->width + 7u) >> 3;
+    cp.tiled_h = (c->height + 7u) >> 3;
+    return TGS_OK;
+}
+
+int check_gaussians(const tgs_gaussians* g, bool is_grad) {
+    if (!g) return fail(TGS_ERR_INVALID, "gaussians is NULL");
+    if (g->n < 0 || g->n > (int64_t)0xffffffffll) return fail(TGS_ERR_INVALID, "invalid gaussian count %lld", (long long)g->n);
+    if (g->n > 0 && (!g->means || !g->scales || !g->rotations || !g->opacities || !g->sh0 || !g->sh_rest))
+        return fail(TGS_ERR_INVALID, "a gaussian SoA pointer is NULL");
+    if (!is_grad && (g->sh_degree < 0 || g->sh_degree > 3)) return fail(TGS_ERR_INVALID, "sh_degree %d", g->sh_degree);
+    if (!is_grad && g->sh_dtype != TGS_DTYPE_FLOAT32 && g->sh_dtype != TGS_DTYPE_FLOAT16)
+        return fail(TGS_ERR_INVALID, "sh_dtype %d", g->sh_dtype);
+    return TGS_OK;
+}
+
+}  // namespace
+
+struct tgs_rasterizer {
+    tgs_gaussians g{};
+    bool has_g = false;
+    // per primitive
+    DevBuf n_touched, bounds, mean2d, conic_opacity, color, depth_key, offsets;
+    DevBuf pkeys[2], pvals[2];
+    // per instance
+    DevBuf ikeys[2], ivals[2];
+    // per tile / pixel
+    DevBuf ranges, tile_max, n_contrib;
+    // temp
+    DevBuf scan_tmp, radix_tmp, grad2d;
+    DevBuf counters;
+    uint32_t* h_counters = nullptr;
+    // state of the last forward
+    bool fwd_done = false;
+    CamParams cam{};
+    int64_t n = 0, V = 0, I = 0;
+    int psel = 0, isel = 0;
+};
+
+struct tgs_loss {
+    int type = 0;  // 0 l1, 1 fused_ssim
+    DevBuf dm[3];
+};
+
+struct tgs_adam {
+    tgs_gaussians params{};
+    tgs_gaussians grads{};
+    DevBuf m1[6], m2[6];
+    tgs_adam_params p{};
+    float global_lr = 1.0f;
+    int64_t steps = 0;
+};
+
+extern "C" {
+
+const char* tgs_last_error(void) { return g_error.c_str(); }
+int tgs_version(void) { return 1; }
+
+// ------------------------------------------------------------------ rasterizer
+
+int tgs_rasterizer_create(const char* type, tgs_rasterizer** out) {
+    if (!out) return fail(TGS_ERR_INVALID, "out is NULL");
+    *out = nullptr;
+    std::string t = type ? type : "";
+    for (auto& ch : t) ch = (char)tolower(ch);
+    if (t != "fastgs") return fail(TGS_ERR_UNSUPPORTED, "Unknown rasterizer type: %s", type ? type : "(null)");
+    tgs_rasterizer* r = new tgs_rasterizer();
+    hipError_t e = hipHostMalloc((void**)&r->h_counters, 64, hipHostMallocDefault);
+    if (e != hipSuccess) {
+        delete r;
+        return fail(TGS_ERR_HIP, "hipHostMalloc: %s", hipGetErrorString(e));
+    }
+    *out = r;
+    return TGS_OK;
+}
+
+int tgs_rasterizer_destroy(tgs_rasterizer* r) {
+    if (!r) return TGS_OK;
+    (void)hipDeviceSynchronize();
+    DevBuf* all[] = {&r->n_touched, &r->bounds, &r->mean2d, &r->conic_opacity, &r->color, &r->depth_key,
+                     &r->offsets, &r->pkeys[0], &r->pkeys[1], &r->pvals[0], &r->pvals[1], &r->ikeys[0],
+                     &r->ikeys[1], &r->ivals[0], &r->ivals[1], &r->ranges, &r->tile_max, &r->n_contrib,
+                     &r->scan_tmp, &r->radix_tmp, &r->grad2d, &r->counters};
+    for (DevBuf* b : all) release(*b);
+    if (r->h_counters) (void)hipHostFree(r->h_counters);
+    delete r;
+    return TGS_OK;
+}
+
+int tgs_rasterizer_set_gaussians(tgs_rasterizer* r, const tgs_gaussians* g) {
+    if (!r) return fail(TGS_ERR_INVALID, "rasterizer is NULL");
+    TGS_TRY(check_gaussians(g, false));
+    r->g = *g;
+    r->has_g = true;
+    r->fwd_done = false;
+    return TGS_OK;
+}
+
+static GaussianView view_of(const tgs_gaussians& g) {
+    GaussianView v;
+    v.means = (const float*)g.means;
+    v.scales = (const float*)g.scales;
+    v.rotations = (const float*)g.rotations;
+    v.opacities = (const float*)g.opacities;
+    v.sh0 = g.sh0;
+    v.sh_rest = g.sh_rest;
+    v.n = g.n;
+    v.sh_degree = g.sh_degree;
+    v.sh_dtype = g.sh_dtype;
+    return v;
+}
+
+int tgs_rasterizer_forward(tgs_rasterizer* r, const tgs_camera* camera, void* image, int32_t image_dtype,
+                           void* densification_info, void* stream) {
+    if (!r) return fail(TGS_ERR_INVALID, "rasterizer is NULL");
+    if (!r->has_g) return fail(TGS_ERR_STATE, "Gaussians not set");
+    if (!image) return fail(TGS_ERR_INVALID, "image is NULL");
+    if (image_dtype != TGS_DTYPE_FLOAT32)
+        return fail(TGS_ERR_UNSUPPORTED, "image dtype %d: only float32 images are supported", image_dtype);
+    hipStream_t s = (hipStream_t)stream;
+    CamParams cam;
+    TGS_TRY(build_camera(camera, cam));
+    r->fwd_done = false;
+    const int64_t n = r->g.n;
+    const uint32_t T = cam.grid_w * cam.grid_h;
+    const size_t cs = (size_t)cam.tiled_w * cam.tiled_h * 64u;
+    const int64_t nn = n > 0 ? n : 1;
+    TGS_TRY(ensure(r->n_touched, 4 * nn, s));
+    TGS_TRY(ensure(r->bounds, 8 * nn, s));
+    TGS_TRY(ensure(r->mean2d, 8 * nn, s));
+    TGS_TRY(ensure(r->conic_opacity, 16 * nn, s));
+    TGS_TRY(ensure(r->color, 16 * nn, s));
+    TGS_TRY(ensure(r->depth_key, 4 * nn, s));
+    TGS_TRY(ensure(r->offsets, 4 * nn, s));
+    for (int k = 0; k < 2; ++k) {
+        TGS_TRY(ensure(r->pkeys[k], 4 * nn, s));
+        TGS_TRY(ensure(r->pvals[k], 4 * nn, s));
+    }
+    TGS_TRY(ensure(r->ranges, 8 * (size_t)T, s));
+    TGS_TRY(ensure(r->tile_max, 4 * (size_t)T, s));
+    TGS_TRY(ensure(r->n_contrib, 4 * cs, s));
+    TGS_TRY(ensure(r->scan_tmp, scan_temp_bytes(nn), s));
+    TGS_TRY(ensure(r->radix_tmp, radix_temp_bytes(nn), s));
+    TGS_TRY(ensure(r->counters, 64, s));
+
+    GaussianView gv = view_of(r->g);
+    uint32_t* d_cnt = r->counters.as<uint32_t>();
+    launch_preprocess(gv, cam, r->n_touched.as<uint32_t>(), r->bounds.as<uint2>(), r->mean2d.as<float2>(),
+                      r->conic_opacity.as<float4>(), r->color.as<float4>(), r->depth_key.as<uint32_t>(),
+                      (float*)densification_info, s);
+    TGS_CHECK_LAUNCH();
+    launch_compact_visible(r->n_touched.as<uint32_t>(), r->depth_key.as<uint32_t>(), n, r->pkeys[0].as<uint32_t>(),
+                           r->pvals[0].as<uint32_t>(), d_cnt + 0, r->scan_tmp.as<uint32_t>(), s);
+    uint32_t* pk[2] = {r->pkeys[0].as<uint32_t>(), r->pkeys[1].as<uint32_t>()};
+    uint32_t* pv[2] = {r->pvals[0].as<uint32_t>(), r->pvals[1].as<uint32_t>()};
+    const int psel = radix_sort_pairs(pk, pv, d_cnt + 0, n, 32, r->radix_tmp.as<uint32_t>(), s);
+    launch_instance_offsets(r->n_touched.as<uint32_t>(), pv[psel], d_cnt + 0, n, r->offsets.as<uint32_t>(), d_cnt + 1,
+                            r->scan_tmp.as<uint32_t>(), s);
+    TGS_CHECK_LAUNCH();
+    TGS_HIP(hipMemcpyAsync(r->h_counters, d_cnt, 2 * sizeof(uint32_t), hipMemcpyDeviceToHost, s));
+    TGS_HIP(hipStreamSynchronize(s));
+    const int64_t V = r->h_counters[0];
+    const int64_t I = r->h_counters[1];
+    const int64_t ii = I > 0 ? I : 1;
+    for (int k = 0; k < 2; ++k) {
+        TGS_TRY(ensure(r->ikeys[k], 4 * ii, s));
+        TGS_TRY(ensure(r->ivals[k], 4 * ii, s));
+    }
+    TGS_TRY(ensure(r->radix_tmp, radix_temp_bytes(ii > nn ? ii : nn), s));
+    launch_emit_instances(r->n_touched.as<uint32_t>(), pv[psel], r->offsets.as<uint32_t>(), d_cnt + 0, n, r->bounds.as<uint2>(),
+                          r->mean2d.as<float2>(), r->conic_opacity.as<float4>(), r->color.as<float4>(), cam.grid_w,
+                          r->ikeys[0].as<uint32_t>(), r->ivals[0].as<uint32_t>(), s);
+    int bits = 1;
+    while ((1u << bits) < T) ++bits;
+    uint32_t* ik[2] = {r->ikeys[0].as<uint32_t>(), r->ikeys[1].as<uint32_t>()};
+    uint32_t* iv[2] = {r->ivals[0].as<uint32_t>(), r->ivals[1].as<uint32_t>()};
+    const int isel = radix_sort_pairs(ik, iv, nullptr, I, bits, r->radix_tmp.as<uint32_t>(), s);
+    launch_tile_ranges(ik[isel], I, r->ranges.as<uint2>(), T, s);
+    launch_blend_forward(cam, r->ranges.as<uint2>(), iv[isel], r->mean2d.as<float2>(), r->conic_opacity.as<float4>(),
+                         r->color.as<float4>(), (float*)image, r->n_contrib.as<uint32_t>(), r->tile_max.as<uint32_t>(),
+                         s);
+    TGS_CHECK_LAUNCH();
+    r->cam = cam;
+    r->n = n;
+    r->V = V;
+    r->I = I;
+    r->psel = psel;
+    r->isel = isel;
+    r->fwd_done = true;
+    return TGS_OK;
+}
+
+int tgs_rasterizer_backward(tgs_rasterizer* r, const void* grad_image, const void* image, const tgs_gaussians* grads,
+                            void* densification_info, void* stream) {
+    if (!r) return fail(TGS_ERR_INVALID, "rasterizer is NULL");
+    if (!r->has_g || !grads) return fail(TGS_ERR_STATE, "Gaussians or gradient gaussians not set");
+    if (!r->fwd_done) return fail(TGS_ERR_STATE, "backward called without a preceding forward");
+    TGS_TRY(check_gaussians(grads, true));
+    if (grads->n != r->g.n) return fail(TGS_ERR_INVALID, "gradient count %lld != %lld", (long long)grads->n,
+                                        (long long)r->g.n);
+    if (!grad_image || !image) return fail(TGS_ERR_INVALID, "grad_image / image is NULL");
+    hipStream_t s = (hipStream_t)stream;
+    const int64_t n = r->n;
+    TGS_TRY(ensure(r->grad2d, sizeof(float) * kGradStride * (size_t)(n > 0 ? n : 1), s));
+    launch_fill_u32(r->grad2d.as<uint32_t>(), 0u, (int64_t)kGradStride * n, s);
+    const CamParams& cam = r->cam;
+    launch_blend_backward(cam, r->ranges.as<uint2>(), r->ivals[r->isel].as<uint32_t>(), r->mean2d.as<float2>(),
+                          r->conic_opacity.as<float4>(), r->color.as<float4>(), (const float*)image,
+                          (const float*)grad_image, r->n_contrib.as<uint32_t>(), r->tile_max.as<uint32_t>(),
+                          r->grad2d.as<float>(), s);
+    TGS_CHECK_LAUNCH();
+    GradView gv{(float*)grads->means, (float*)grads->scales, (float*)grads->rotations, (float*)grads->opacities,
+                (float*)grads->sh0, (float*)grads->sh_rest};
+    launch_preprocess_backward(view_of(r->g), cam, r->n_touched.as<uint32_t>(), r->conic_opacity.as<float4>(),
+                               r->grad2d.as<float>(), gv, (float*)densification_info, s);
+    TGS_CHECK_LAUNCH();
+    return TGS_OK;
+}
+
+int tgs_rasterizer_counts(tgs_rasterizer* r, int64_t* n_visible, int64_t* n_instances, int64_t* n_tiles) {
+    if (!r) return fail(TGS_ERR_INVALID, "rasterizer is NULL");
+    if (!r->fwd_done) return fail(TGS_ERR_STATE, "no forward yet");
+    if (n_visible) *n_visible = r->V;
+    if (n_instances) *n_instances = r->I;
+    if (n_tiles) *n_tiles = (int64_t)r->cam.grid_w * r->cam.grid_h;
+    return TGS_OK;
+}
+
+int tgs_rasterizer_debug_view(tgs_rasterizer* r, tgs_debug_view* out) {
+    if (!r || !out) return fail(TGS_ERR_INVALID, "NULL argument");
+    if (!r->fwd_done) return fail(TGS_ERR_STATE, "no forward yet");
+    out->n_touched = r->n_touched.as<uint32_t>();
+    out->bounds = r->bounds.as<uint32_t>();
+    out->mean2d = r->mean2d.as<float>();
+    out->conic_opacity = r->conic_opacity.as<float>();
+    out->color = r->color.as<float>();
+    out->depth_sorted_keys = r->pkeys[r->psel].as<uint32_t>();
+    out->depth_sorted_prims = r->pvals[r->psel].as<uint32_t>();
+    out->instance_tiles = r->ikeys[r->isel].as<uint32_t>();
+    out->instance_prims = r->ivals[r->isel].as<uint32_t>();
+    out->tile_ranges = r->ranges.as<uint32_t>();
+    out->n_contrib = r->n_contrib.as<uint32_t>();
+    out->tile_max = r->tile_max.as<uint32_t>();
+    out->grad2d = r->grad2d.as<float>();
+    out->n_visible = r->V;
+    out->n_instances = r->I;
+    out->n_tiles = (int64_t)r->cam.grid_w * r->cam.grid_h;
+    return TGS_OK;
+}
+
+// ------------------------------------------------------------------ losses
+
+int tgs_loss_create(const char* type, tgs_loss** out) {
+    if (!out) return fail(TGS_ERR_INVALID, "out is NULL");
+    *out = nullptr;
+    std::string t = type ? type : "";
+    for (auto& ch : t) ch = (char)tolower(ch);
+    int kind;
+    if (t == "l1")
+        kind = 0;
+    else if (t == "fused_ssim")
+        kind = 1;
+    else
+        return fail(TGS_ERR_UNSUPPORTED, "Unknown loss type: %s", type ? type : "(null)");
+    tgs_loss* l = new tgs_loss();
+    l->type = kind;
+    *out = l;
+    return TGS_OK;
+}
+
+int tgs_loss_destroy(tgs_loss* l) {
+    if (!l) return TGS_OK;
+    (void)hipDeviceSynchronize();
+    for (auto& b : l->dm) release(b);
+    delete l;
+    return TGS_OK;
+}
+
+int tgs_loss_evaluate(tgs_loss* l, const tgs_loss_context* c, float scale, void* stream) {
+    if (!l || !c) return fail(TGS_ERR_INVALID, "NULL argument");
+    if (c->dtype != TGS_DTYPE_FLOAT32)
+        return fail(TGS_ERR_UNSUPPORTED, "loss dtype %d: only float32 is supported", c->dtype);
+    if (!c->pred || !c->target) return fail(TGS_ERR_INVALID, "pred / target is NULL");
+    if (c->width == 0 || c->height == 0 || c->channel == 0) return fail(TGS_ERR_INVALID, "empty image");
+    hipStream_t s = (hipStream_t)stream;
+    const uint32_t tw = (c->width + 7u) >> 3, th = (c->height + 7u) >> 3;
+    const int64_t padded = (int64_t)tw * th * 64 * c->channel;
+    if (l->type == 0) {
+        // l1.cu:117-121: scale / (W * H * C)
+        const int npix = (int)(c->width * c->height * c->channel);
+        launch_l1((const float*)c->pred, (const float*)c->target, (float*)c->loss, (float*)c->grad, padded,
+                  scale / (float)npix, s);
+        TGS_CHECK_LAUNCH();
+        return TGS_OK;
+    }
+    if (c->channel != 3) return fail(TGS_ERR_UNSUPPORTED, "fused_ssim needs 3 channels");
+    // fused_ssim.cu:811: scale / (H * W)
+    const float actual = scale / (float)(int)(c->height * c->width);
+    const float C1 = 0.01f * 0.01f, C2 = 0.03f * 0.03f;
+    if (c->grad) {
+        for (auto& b : l->dm) TGS_TRY(ensure(b, sizeof(float) * (size_t)padded, s));
+        launch_ssim_forward(c->width, c->height, C1, C2, actual, (const float*)c->pred, (const float*)c->target,
+                            (float*)c->loss, l->dm[0].as<float>(), l->dm[1].as<float>(), l->dm[2].as<float>(), s);
+        launch_ssim_backward(c->width, c->height, actual, (const float*)c->pred, (const float*)c->target,
+                             (float*)c->grad, l->dm[0].as<float>(), l->dm[1].as<float>(), l->dm[2].as<float>(), s);
+    } else {
+        launch_ssim_forward(c->width, c->height, C1, C2, actual, (const float*)c->pred, (const float*)c->target,
+                            (float*)c->loss, nullptr, nullptr, nullptr, s);
+    }
+    TGS_CHECK_LAUNCH();
+    return TGS_OK;
+}
+
+// ------------------------------------------------------------------ SimpleAdam
+
+static void default_adam_params(tgs_adam_params& p) {
+    // SimpleAdamParameters (simple_adam.hpp:8-27) and GaussianOptimizationParams (optim.hpp:12-24)
+    p.beta1 = 0.9f;
+    p.beta2 = 0.999f;
+    p.epsilon = 1e-8f;
+    p.means_lr = 1.6e-4f;
+    p.shs_lr = 2.5e-3f;
+    p.opacities_lr = 5.0e-2f;
+    p.scales_lr = 5.0e-3f;
+    p.rotations_lr = 1.0e-3f;
+    p.max_grad_1 = 1.0f;
+    p.opacities_l1 = 0.0f;
+    p.scales_l1 = 0.0f;
+    p.decay_mean = 1;
+}
+
+static const int kGroupMult[6] = {3, 1, 4, 3, 3, 45};
+
+int tgs_adam_create(const tgs_gaussians* params, const tgs_gaussians* grads, tgs_adam** out) {
+    if (!out) return fail(TGS_ERR_INVALID, "out is NULL");
+    *out = nullptr;
+    TGS_TRY(check_gaussians(params, false));
+    TGS_TRY(check_gaussians(grads, true));
+    if (params->n != grads->n)
+        return fail(TGS_ERR_INVALID, "SimpleAdam::step: gaussians and gaussians_grad must have same size");
+    tgs_adam* a = new tgs_adam();
+    a->params = *params;
+    a->grads = *grads;
+    default_adam_params(a->p);
+    for (int k = 0; k < 6; ++k) {
+        const size_t bytes = sizeof(float) * (size_t)kGroupMult[k] * (size_t)(params->n > 0 ? params->n : 1);
+        if (ensure(a->m1[k], bytes, nullptr) != TGS_OK || ensure(a->m2[k], bytes, nullptr) != TGS_OK ||
+            hipMemset(a->m1[k].p, 0, a->m1[k].bytes) != hipSuccess ||
+            hipMemset(a->m2[k].p, 0, a->m2[k].bytes) != hipSuccess) {
+            for (int q = 0; q < 6; ++q) {
+                release(a->m1[q]);
+                release(a->m2[q]);
+            }
+            delete a;
+            return fail(TGS_ERR_HIP, "moment allocation failed");
+        }
+    }
+    *out = a;
+    return TGS_OK;
+}
+
+int tgs_adam_destroy(tgs_adam* a) {
+    if (!a) return TGS_OK;
+    (void)hipDeviceSynchronize();
+    for (int k = 0; k < 6; ++k) {
+        release(a->m1[k]);
+        release(a->m2[k]);
+    }
+    delete a;
+    return TGS_OK;
+}
+
+int tgs_adam_set_params(tgs_adam* a, const tgs_adam_params* p) {
+    if (!a || !p) return fail(TGS_ERR_INVALID, "NULL argument");
+    a->p = *p;
+    return TGS_OK;
+}
+
+int tgs_adam_get_params(tgs_adam* a, tgs_adam_params* p) {
+    if (!a || !p) return fail(TGS_ERR_INVALID, "NULL argument");
+    *p = a->p;
+    return TGS_OK;
+}
+
+int tgs_adam_set_lr(tgs_adam* a, float lr) {
+    if (!a) return fail(TGS_ERR_INVALID, "NULL argument");
+    a->global_lr = lr;
+    return TGS_OK;
+}
+
+float tgs_adam_get_lr(tgs_adam* a) { return a ? a->global_lr : 0.0f; }
+
+int tgs_adam_set_gaussians(tgs_adam* a, const tgs_gaussians* params, const tgs_gaussians* grads) {
+    if (!a) return fail(TGS_ERR_INVALID, "NULL argument");
+    TGS_TRY(check_gaussians(params, false));
+    TGS_TRY(check_gaussians(grads, true));
+    if (params->n != a->params.n || grads->n != a->params.n)
+        return fail(TGS_ERR_INVALID, "size change needs a new optimizer (moments sized for %lld)",
+                    (long long)a->params.n);
+    a->params = *params;
+    a->grads = *grads;
+    return TGS_OK;
+}
+
+int tgs_adam_step(tgs_adam* a, float scale, void* stream) {
+    if (!a) return fail(TGS_ERR_INVALID, "NULL argument");
+    const int64_t n = a->params.n;
+    a->steps += 1;
+    // simple_adam.cu:475-480: bias corrections in double, rounded to float
+    const double st = (double)a->steps;
+    const float bc1 = (float)(1.0 - pow((double)a->p.beta1, st));
+    const float bc2 = (float)sqrt(1.0 - pow((double)a->p.beta2, st));
+    const float g_scale = a->p.decay_mean ? 1.0f / (float)(n > 0 ? n : 1) : 1.0f;
+    const float glr = a->global_lr;
+    AdamArgs args;
+    memset(&args, 0, sizeof(args));
+    args.n_groups = 6;
+    args.beta1 = a->p.beta1;
+    args.beta2 = a->p.beta2;
+    args.eps = a->p.epsilon;
+    args.grad_scale = scale;
+    args.bc1 = bc1;
+    args.bc2_sqrt = bc2;
+    args.max_grad = a->p.max_grad_1;
+    void* th[6] = {a->params.means, a->params.opacities, a->params.rotations, a->params.scales, a->params.sh0,
+                   a->params.sh_rest};
+    const float* gr[6] = {(const float*)a->grads.means, (const float*)a->grads.opacities,
+                          (const float*)a->grads.rotations, (const float*)a->grads.scales,
+                          (const float*)a->grads.sh0, (const float*)a->grads.sh_rest};
+    // learning rates as formed in simple_adam.cu:493,508,524,540,556,571
+    const float lrs[6] = {a->p.means_lr * a->params.scene_scale * glr, a->p.opacities_lr * glr,
+                          a->p.rotations_lr * glr, a->p.scales_lr * glr, a->p.shs_lr * glr,
+                          a->p.shs_lr * 0.05f * glr};
+    for (int k = 0; k < 6; ++k) {
+        AdamGroup& g = args.groups[k];
+        g.theta = th[k];
+        g.grad = gr[k];
+        g.m1 = a->m1[k].as<float>();
+        g.m2 = a->m2[k].as<float>();
+        g.count = (int64_t)kGroupMult[k] * n;
+        g.lr = lrs[k];
+        g.theta_half = (k >= 4 && a->params.sh_dtype == TGS_DTYPE_FLOAT16) ? 1 : 0;
+        g.lerp_form = (k == 1) ? 1 : 0;
+        g.decay_kind = (k == 1) ? 1 : (k == 3 ? 2 : 0);
+        g.decay_coef = (k == 1) ? a->p.opacities_l1 * g_scale : (k == 3 ? a->p.scales_l1 * g_scale : 0.0f);
+    }
+    launch_adam(args, (hipStream_t)stream);
+    TGS_CHECK_LAUNCH();
+    return TGS_OK;
+}
+
+int tgs_adam_reset(tgs_adam* a, void* stream) {
+    if (!a) return fail(TGS_ERR_INVALID, "NULL argument");
+    for (int k = 0; k < 6; ++k) {
+        launch_fill_u32(a->m1[k].as<uint32_t>(), 0u, (int64_t)(a->m1[k].bytes / 4), (hipStream_t)stream);
+        launch_fill_u32(a->m2[k].as<uint32_t>(), 0u, (int64_t)(a->m2[k].bytes / 4), (hipStream_t)stream);
+    }
+    TGS_CHECK_LAUNCH();
+    a->steps = 0;
+    return TGS_OK;
+}
+
+int64_t tgs_adam_global_steps(tgs_adam* a) { return a ? a->steps : -1; }
+
+int tgs_adam_moments(tgs_adam* a, int32_t group, float** first, float** second) {
+    if (!a || group < 0 || group >= 6) return fail(TGS_ERR_INVALID, "bad group");
+    if (first) *first = a->m1[group].as<float>();
+    if (second) *second = a->m2[group].as<float>();
+    return TGS_OK;
+}
+
+// ------------------------------------------------------------------ self tests
+
+int tgs_selftest_detmath(int32_t op, const float* in, float* out, int64_t n, void* stream) {
+    launch_detmath(op, in, out, n, (hipStream_t)stream);
+    TGS_CHECK_LAUNCH();
+    return TGS_OK;
+}
+
+int tgs_selftest_wave(const uint32_t* in, uint32_t* out, void* stream) {
+    launch_wave_selftest(in, out, (hipStream_t)stream);
+    TGS_CHECK_LAUNCH();
+    return TGS_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,117 @@
+// Shared device helpers for the gfx950 (CDNA4, wave64) kernels.
+#pragma once
+
+#include <hip/hip_fp16.h>
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "detmath.h"
+
+namespace tgs {
+
+constexpr int kWave = 64;
+constexpr int kTile = 16;               // screen tile edge (rasterization_config.h:31-35)
+constexpr int kTilePixels = 256;
+constexpr float kMinAlpha = 1.0f / 255.0f;
+constexpr float kMaxAlpha = 0.999f;
+constexpr float kTransmittanceMin = 1e-4f;
+constexpr float kDilation = 0.3f;
+constexpr int kGradStride = 12;         // floats of per-primitive 2D gradient record
+
+// Camera and image parameters, passed to kernels by value (no pose-block copy).
+struct CamParams {
+    float fx, fy, cx, cy, near_, far_;
+    float r1[4], r2[4], r3[4];   // rows 0..2 of the row-major world-to-camera matrix
+    float cam_pos[3];
+    float w, h;                  // image size as float (frustum clamp)
+    uint32_t width, height;
+    uint32_t grid_w, grid_h;     // 16x16 tiles
+    uint32_t tiled_w, tiled_h;   // 8x8 image blocks
+};
+
+// Physical index of pixel (row, col) in one plane of the 8x8-tiled layout
+// (tinygs/include/tinygs/common.hpp:404-408).
+TGS_HD uint32_t tiled_index(uint32_t row, uint32_t col, uint32_t tiled_width) {
+    return ((((row >> 3) * tiled_width) + (col >> 3)) << 6) + ((row & 7u) << 3) + (col & 7u);
+}
+
+__device__ __forceinline__ uint32_t lane_id() { return __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u)); }
+
+// number of set bits of a 64-bit lane mask strictly below this lane
+__device__ __forceinline__ uint32_t mask_rank(uint64_t m) {
+    return __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+}
+
+__device__ __forceinline__ uint64_t ballot(bool p) { return __ballot(p); }
+
+__device__ __forceinline__ uint32_t readlane_u32(uint32_t v, uint32_t lane) {
+    return (uint32_t)__builtin_amdgcn_readlane((int)v, (int)lane);
+}
+__device__ __forceinline__ float readlane_f32(float v, uint32_t lane) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), (int)lane));
+}
+
+// DPP move: lanes whose source is disabled (row_mask / bank_mask) read 0.
+template <int CTRL, int ROW_MASK = 0xF, int BANK_MASK = 0xF>
+__device__ __forceinline__ float dpp_f32(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, ROW_MASK,
+                                                                 BANK_MASK, false));
+}
+template <int CTRL, int ROW_MASK = 0xF, int BANK_MASK = 0xF>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, ROW_MASK, BANK_MASK, false);
+}
+
+// Wave-wide sum; the total is valid in lanes 48..63 (row 3), read lane 63.
+// Row butterfly with row_ror 8/4/2/1, then row_bcast15 / row_bcast31 across
+// the four 16-lane rows. Fixed order: deterministic for a given input.
+__device__ __forceinline__ float wave_sum_row3(float v) {
+    v += dpp_f32<0x128>(v);        // row_ror:8
+    v += dpp_f32<0x124>(v);        // row_ror:4
+    v += dpp_f32<0x122>(v);        // row_ror:2
+    v += dpp_f32<0x121>(v);        // row_ror:1
+    v += dpp_f32<0x142, 0xA>(v);   // row_bcast:15 -> rows 1, 3
+    v += dpp_f32<0x143, 0xC>(v);   // row_bcast:31 -> rows 2, 3
+    return v;
+}
+
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+    v = max(v, dpp_u32<0x128>(v));
+    v = max(v, dpp_u32<0x124>(v));
+    v = max(v, dpp_u32<0x122>(v));
+    v = max(v, dpp_u32<0x121>(v));
+    v = max(v, dpp_u32<0x142, 0xA>(v));
+    v = max(v, dpp_u32<0x143, 0xC>(v));
+    return readlane_u32(v, 63);
+}
+
+__device__ __forceinline__ uint32_t wave_sum_u32(uint32_t v) {
+    v += dpp_u32<0x128>(v);
+    v += dpp_u32<0x124>(v);
+    v += dpp_u32<0x122>(v);
+    v += dpp_u32<0x121>(v);
+    v += dpp_u32<0x142, 0xA>(v);
+    v += dpp_u32<0x143, 0xC>(v);
+    return readlane_u32(v, 63);
+}
+
+// Inclusive prefix sum across the wave (Hillis-Steele with ds_bpermute-free
+// DPP row shifts plus row broadcasts).
+__device__ __forceinline__ uint32_t wave_inclusive_scan_u32(uint32_t v) {
+    v += dpp_u32<0x111>(v);          // row_shr:1
+    v += dpp_u32<0x112>(v);          // row_shr:2
+    v += dpp_u32<0x114>(v);          // row_shr:4
+    v += dpp_u32<0x118>(v);          // row_shr:8
+    v += dpp_u32<0x142, 0xA>(v);     // row_bcast:15
+    v += dpp_u32<0x143, 0xC>(v);     // row_bcast:31
+    return v;
+}
+
+template <typename T>
+__device__ __forceinline__ float load_as_float(const T* p, int64_t i);
+template <>
+__device__ __forceinline__ float load_as_float<float>(const float* p, int64_t i) { return p[i]; }
+template <>
+__device__ __forceinline__ float load_as_float<__half>(const __half* p, int64_t i) { return __half2float(p[i]); }
+
+}  // namespace tgs

@@ -1,0 +1,249 @@
+// Per-Gaussian preprocess: projection, EWA covariance, conic, tile bounds,
+// exact tile count and SH -> RGB.
+// Follows tinygs/src/rasterizer/fastgs_ours/kernels_forward.cuh:157-412
+// (with will_primitive_contribute :49-84, compute_exact_n_touched_tiles
+// :87-153, convert_sh_to_color :22-46).
+//
+// MI355X layout: one thread per Gaussian, 256-thread workgroups (4 wave64).
+// Per-primitive outputs are SoA with 8/16-byte records so the blend's LDS
+// staging loads are single dwordx2/x4 transactions. Gaussians whose bounds
+// rectangle exceeds 8 tiles are counted cooperatively by the whole wave
+// (ballot + readlane broadcast), so one outlier does not serialise 63 lanes.
+//
+// Every floating-point expression here mirrors the CPU oracle operation for
+// operation (this file is compiled with -ffp-contract=off), so visibility,
+// bounds and tile counts are bit-identical to it.
+#include "common.h"
+#include "kernels.h"
+
+namespace tgs {
+
+// kernels_forward.cuh:49-84, on the mean shifted by -0.5 (:94).
+__device__ __forceinline__ bool will_contribute(float mx, float my, float ca, float cb, float cc, uint32_t tile_x,
+                                                uint32_t tile_y, float power_threshold) {
+    const float rminx = (float)(tile_x * 16u), rminy = (float)(tile_y * 16u);
+    const float rmaxx = (float)((tile_x + 1u) * 16u - 1u), rmaxy = (float)((tile_y + 1u) * 16u - 1u);
+    const float x_min_diff = rminx - mx;
+    const float x_left = x_min_diff > 0.0f ? 1.0f : 0.0f;
+    const float not_in_x = x_left + (mx > rmaxx ? 1.0f : 0.0f);
+    const float y_min_diff = rminy - my;
+    const float y_above = y_min_diff > 0.0f ? 1.0f : 0.0f;
+    const float not_in_y = y_above + (my > rmaxy ? 1.0f : 0.0f);
+    if (not_in_y + not_in_x == 0.0f) return true;
+    const float ccx = rmaxx + x_left * (rminx - rmaxx);
+    const float ccy = rmaxy + y_above * (rminy - rmaxy);
+    const float diffx = mx - ccx, diffy = my - ccy;
+    const float dx = __builtin_copysignf(15.0f, x_min_diff);
+    const float dy = __builtin_copysignf(15.0f, y_min_diff);
+    const float tx = not_in_y * saturate((dx * ca * diffx + dx * cb * diffy) / (dx * ca * dx));
+    const float ty = not_in_x * saturate((dy * cb * diffx + dy * cc * diffy) / (dy * cc * dy));
+    const float px = ccx + tx * dx, py = ccy + ty * dy;
+    const float ddx = mx - px, ddy = my - py;
+    const float max_power = 0.5f * (ca * ddx * ddx + cc * ddy * ddy) + cb * ddx * ddy;
+    return max_power <= power_threshold;
+}
+
+template <typename ShT>
+__device__ __forceinline__ void sh_to_color(const ShT* __restrict__ sh0, const ShT* __restrict__ shr, int64_t i,
+                                            float px, float py, float pz, const CamParams& cam, int bases,
+                                            float* out) {
+    for (int c = 0; c < 3; ++c) out[c] = 0.5f + 0.28209479177387814f * load_as_float(sh0, 3 * i + c);
+    if (bases <= 1) return;
+    const ShT* r = shr + 45 * i;
+    const float vx = px - cam.cam_pos[0], vy = py - cam.cam_pos[1], vz = pz - cam.cam_pos[2];
+    const float inv = 1.0f / __builtin_sqrtf(vx * vx + vy * vy + vz * vz);
+    const float x = vx * inv, y = vy * inv, z = vz * inv;
+    float k[15];
+    k[0] = -0.48860251190291987f * y;
+    k[1] = 0.48860251190291987f * z;
+    k[2] = -0.48860251190291987f * x;
+    int nb = 3;
+    if (bases > 4) {
+        const float xx = x * x, yy = y * y, zz = z * z;
+        const float xy = x * y, xz = x * z, yz = y * z;
+        k[3] = 1.0925484305920792f * xy;
+        k[4] = -1.0925484305920792f * yz;
+        k[5] = 0.94617469575755997f * zz - 0.31539156525251999f;
+        k[6] = -1.0925484305920792f * xz;
+        k[7] = 0.54627421529603959f * xx - 0.54627421529603959f * yy;
+        nb = 8;
+        if (bases > 9) {
+            k[8] = 0.59004358992664352f * y * (-3.0f * xx + yy);
+            k[9] = 2.8906114426405538f * xy * z;
+            k[10] = 0.45704579946446572f * y * (1.0f - 5.0f * zz);
+            k[11] = 0.3731763325901154f * z * (5.0f * zz - 3.0f);
+            k[12] = 0.45704579946446572f * x * (1.0f - 5.0f * zz);
+            k[13] = 1.4453057213202769f * z * (xx - yy);
+            k[14] = 0.59004358992664352f * x * (-xx + 3.0f * yy);
+            nb = 15;
+        }
+    }
+    for (int b = 0; b < nb; ++b)
+        for (int c = 0; c < 3; ++c) out[c] = out[c] + k[b] * load_as_float(r, 3 * b + c);
+}
+
+template <typename ShT>
+__global__ void __launch_bounds__(256) preprocess_kernel(
+    const float* __restrict__ means, const float* __restrict__ scales, const float* __restrict__ rots,
+    const float* __restrict__ opac, const ShT* __restrict__ sh0, const ShT* __restrict__ shr, int64_t n, int bases,
+    CamParams cam, uint32_t* __restrict__ n_touched, uint2* __restrict__ bounds, float2* __restrict__ mean2d,
+    float4* __restrict__ conic_opacity, float4* __restrict__ color_pt, uint32_t* __restrict__ depth_key,
+    float4* __restrict__ densif) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    bool active = i < n;
+    const int64_t ii = active ? i : n - 1;
+    const uint32_t lane = lane_id();
+
+    const float mx = means[3 * ii], my = means[3 * ii + 1], mz = means[3 * ii + 2];
+    const float depth = cam.r3[0] * mx + cam.r3[1] * my + cam.r3[2] * mz + cam.r3[3];
+    if (depth < cam.near_ || depth > cam.far_) active = false;
+    const float opacity = 1.0f / (1.0f + det_expf(-opac[ii]));
+    if (opacity < kMinAlpha) active = false;
+    const float e0 = det_expf(scales[3 * ii]), e1 = det_expf(scales[3 * ii + 1]), e2 = det_expf(scales[3 * ii + 2]);
+    const float vx = e0 * e0, vy = e1 * e1, vz = e2 * e2;
+    const float qr = rots[4 * ii], qx = rots[4 * ii + 1], qy = rots[4 * ii + 2], qz = rots[4 * ii + 3];
+    const float qrr = qr * qr, qxx_r = qx * qx, qyy_r = qy * qy, qzz_r = qz * qz;
+    const float qn = qrr + qxx_r + qyy_r + qzz_r;
+    if (qn < 1e-8f) active = false;
+
+    uint32_t xmin = 0, xmax = 0, ymin = 0, ymax = 0, nmax = 0;
+    float ca = 0.f, cb = 0.f, cc = 0.f, m2x = 0.f, m2y = 0.f, pthr = 0.f;
+    if (active) {
+        const float qxx = 2.0f * qxx_r / qn, qyy = 2.0f * qyy_r / qn, qzz = 2.0f * qzz_r / qn;
+        const float qxy = 2.0f * qx * qy / qn, qxz = 2.0f * qx * qz / qn, qyz = 2.0f * qy * qz / qn;
+        const float qrx = 2.0f * qr * qx / qn, qry = 2.0f * qr * qy / qn, qrz = 2.0f * qr * qz / qn;
+        const float R11 = 1.0f - (qyy + qzz), R12 = qxy - qrz, R13 = qry + qxz;
+        const float R21 = qrz + qxy, R22 = 1.0f - (qxx + qzz), R23 = qyz - qrx;
+        const float R31 = qxz - qry, R32 = qrx + qyz, R33 = 1.0f - (qxx + qyy);
+        const float S11 = R11 * vx, S12 = R12 * vy, S13 = R13 * vz;
+        const float S21 = R21 * vx, S22 = R22 * vy, S23 = R23 * vz;
+        const float S31 = R31 * vx, S32 = R32 * vy, S33 = R33 * vz;
+        const float c11 = S11 * R11 + S12 * R12 + S13 * R13;
+        const float c12 = S11 * R21 + S12 * R22 + S13 * R23;
+        const float c13 = S11 * R31 + S12 * R32 + S13 * R33;
+        const float c22 = S21 * R21 + S22 * R22 + S23 * R23;
+        const float c23 = S21 * R31 + S22 * R32 + S23 * R33;
+        const float c33 = S31 * R31 + S32 * R32 + S33 * R33;
+        const float x = (cam.r1[0] * mx + cam.r1[1] * my + cam.r1[2] * mz + cam.r1[3]) / depth;
+        const float y = (cam.r2[0] * mx + cam.r2[1] * my + cam.r2[2] * mz + cam.r2[3]) / depth;
+        const float clip_left = (-0.15f * cam.w - cam.cx) / cam.fx;
+        const float clip_right = (1.15f * cam.w - cam.cx) / cam.fx;
+        const float clip_top = (-0.15f * cam.h - cam.cy) / cam.fy;
+        const float clip_bottom = (1.15f * cam.h - cam.cy) / cam.fy;
+        const float tx = __builtin_fmaxf(clip_left, __builtin_fminf(x, clip_right));
+        const float ty = __builtin_fmaxf(clip_top, __builtin_fminf(y, clip_bottom));
+        const float j11 = cam.fx / depth, j13 = -j11 * tx, j22 = cam.fy / depth, j23 = -j22 * ty;
+        const float jw1x = j11 * cam.r1[0] + j13 * cam.r3[0], jw1y = j11 * cam.r1[1] + j13 * cam.r3[1],
+                    jw1z = j11 * cam.r1[2] + j13 * cam.r3[2];
+        const float jw2x = j22 * cam.r2[0] + j23 * cam.r3[0], jw2y = j22 * cam.r2[1] + j23 * cam.r3[1],
+                    jw2z = j22 * cam.r2[2] + j23 * cam.r3[2];
+        const float a1x = jw1x * c11 + jw1y * c12 + jw1z * c13;
+        const float a1y = jw1x * c12 + jw1y * c22 + jw1z * c23;
+        const float a1z = jw1x * c13 + jw1y * c23 + jw1z * c33;
+        const float a2x = jw2x * c11 + jw2y * c12 + jw2z * c13;
+        const float a2y = jw2x * c12 + jw2y * c22 + jw2z * c23;
+        const float a2z = jw2x * c13 + jw2y * c23 + jw2z * c33;
+        float cv_a = a1x * jw1x + a1y * jw1y + a1z * jw1z;
+        const float cv_b = a1x * jw2x + a1y * jw2y + a1z * jw2z;
+        float cv_c = a2x * jw2x + a2y * jw2y + a2z * jw2z;
+        cv_a += kDilation;
+        cv_c += kDilation;
+        const float det = cv_a * cv_c - cv_b * cv_b;
+        if (det < 1e-8f) {
+            active = false;
+        } else {
+            ca = cv_c / det;
+            cb = -cv_b / det;
+            cc = cv_a / det;
+            m2x = x * cam.fx + cam.cx;
+            m2y = y * cam.fy + cam.cy;
+            pthr = det_logf(opacity * 255.0f);
+            const float pfac = __builtin_sqrtf(2.0f * pthr);
+            const float ext_x = __builtin_fmaxf(pfac * __builtin_sqrtf(cv_a) - 0.5f, 0.0f);
+            const float ext_y = __builtin_fmaxf(pfac * __builtin_sqrtf(cv_c) - 0.5f, 0.0f);
+            const int32_t bx0 = sat_floor_i32((m2x - ext_x) / 16.0f);
+            const int32_t bx1 = sat_ceil_i32((m2x + ext_x) / 16.0f);
+            const int32_t by0 = sat_floor_i32((m2y - ext_y) / 16.0f);
+            const int32_t by1 = sat_ceil_i32((m2y + ext_y) / 16.0f);
+            xmin = min((uint32_t)max(bx0, 0), cam.grid_w);
+            xmax = min((uint32_t)max(bx1, 0), cam.grid_w);
+            ymin = min((uint32_t)max(by0, 0), cam.grid_h);
+            ymax = min((uint32_t)max(by1, 0), cam.grid_h);
+            if (densif) {
+                // kernels_forward.cuh:342-348, for primitives still active here
+                const float mid = 0.5f * (cv_a + cv_c);
+                const float l1 = mid + __builtin_sqrtf(__builtin_fmaxf(0.1f, mid * mid - det));
+                const float l2 = mid - __builtin_sqrtf(__builtin_fmaxf(0.1f, mid * mid - det));
+                const float rad = __builtin_ceilf(3.0f * __builtin_sqrtf(__builtin_fmaxf(l1, l2)));
+                if (rad > densif[ii].w) densif[ii].w = rad;
+            }
+            nmax = (xmax - xmin) * (ymax - ymin);
+            if (nmax == 0) active = false;
+        }
+    }
+
+    // exact tile count: first 8 tiles per lane, the rest wave-cooperatively
+    const float smx = m2x - 0.5f, smy = m2y - 0.5f;
+    const uint32_t bw = xmax - xmin;
+    uint32_t cnt = 0;
+    if (active) {
+        const uint32_t first = nmax < 8u ? nmax : 8u;
+        for (uint32_t k = 0; k < first; ++k) {
+            const uint32_t ty_ = ymin + k / bw, tx_ = xmin + k % bw;
+            cnt += will_contribute(smx, smy, ca, cb, cc, tx_, ty_, pthr) ? 1u : 0u;
+        }
+    }
+    uint64_t coop = ballot(active && nmax > 8u);
+    while (coop) {
+        const uint32_t src = (uint32_t)__builtin_ctzll(coop);
+        coop &= coop - 1;
+        const float s_mx = readlane_f32(smx, src), s_my = readlane_f32(smy, src);
+        const float s_a = readlane_f32(ca, src), s_b = readlane_f32(cb, src), s_c = readlane_f32(cc, src);
+        const float s_t = readlane_f32(pthr, src);
+        const uint32_t s_x0 = readlane_u32(xmin, src), s_y0 = readlane_u32(ymin, src);
+        const uint32_t s_bw = readlane_u32(bw, src), s_n = readlane_u32(nmax, src);
+        uint32_t c = 0;
+        for (uint32_t base = 8u; base < s_n; base += kWave) {
+            const uint32_t k = base + lane;
+            bool hit = false;
+            if (k < s_n) hit = will_contribute(s_mx, s_my, s_a, s_b, s_c, s_x0 + k % s_bw, s_y0 + k / s_bw, s_t);
+            c += (uint32_t)__builtin_popcountll(ballot(hit));
+        }
+        if (lane == src) cnt += c;
+    }
+
+    if (i >= n) return;
+    if (!active || cnt == 0) {
+        n_touched[i] = 0;
+        return;
+    }
+    n_touched[i] = cnt;
+    bounds[i] = make_uint2(xmin | (xmax << 16), ymin | (ymax << 16));
+    mean2d[i] = make_float2(m2x, m2y);
+    conic_opacity[i] = make_float4(ca, cb, cc, opacity);
+    float col[3];
+    sh_to_color(sh0, shr, i, mx, my, mz, cam, bases, col);
+    color_pt[i] = make_float4(col[0], col[1], col[2], pthr);
+    depth_key[i] = f2u(depth);
+}
+
+void launch_preprocess(const GaussianView& g, const CamParams& cam, uint32_t* n_touched, uint2* bounds,
+                       float2* mean2d, float4* conic_opacity, float4* color_pt, uint32_t* depth_key, float* densif,
+                       hipStream_t s) {
+    if (g.n <= 0) return;
+    const int bases = (g.sh_degree + 1) * (g.sh_degree + 1);
+    const unsigned grid = (unsigned)((g.n + 255) / 256);
+    if (g.sh_dtype == kShF16) {
+        preprocess_kernel<__half><<<grid, 256, 0, s>>>(g.means, g.scales, g.rotations, g.opacities,
+                                                       (const __half*)g.sh0, (const __half*)g.sh_rest, g.n, bases,
+                                                       cam, n_touched, bounds, mean2d, conic_opacity, color_pt,
+                                                       depth_key, (float4*)densif);
+    } else {
+        preprocess_kernel<float><<<grid, 256, 0, s>>>(g.means, g.scales, g.rotations, g.opacities,
+                                                      (const float*)g.sh0, (const float*)g.sh_rest, g.n, bases, cam,
+                                                      n_touched, bounds, mean2d, conic_opacity, color_pt, depth_key,
+                                                      (float4*)densif);
+    }
+}
+
+}  // namespace tgs

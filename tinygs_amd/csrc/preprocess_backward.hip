@@ -1,0 +1,258 @@
+// Per-Gaussian backward: 2D gradients -> 3D mean, log-scale, quaternion,
+// SH coefficients (and the opacity logit).
+// Follows tinygs/src/rasterizer/fastgs_ours/kernels_backward.cuh:88-352 with
+// convert_sh_to_color_backward :22-86. Runs only for primitives with
+// n_touched > 0 (:117). Parameter gradients are accumulated (+=) as in the
+// reference; the caller zeroes them.
+//
+// Reference semantics kept: dSigma2 with (det + 1e-8)^-2 and the symmetric-
+// matrix off-diagonal convention (:204-214); tx/ty clamp mask (:244-247);
+// quaternion gradient divided by |q|^3 (:332); the three double-precision
+// literals of the SH direction gradient (:55-57). The opacity gradient is
+// (sum of alpha * dL/dalpha) * (1 - opacity) (:921-922); the blend backward
+// leaves the sum in grad2d[10] and it is applied here.
+#include "common.h"
+#include "kernels.h"
+
+namespace tgs {
+
+template <typename ShT>
+__global__ void __launch_bounds__(256) preprocess_backward_kernel(
+    const float* __restrict__ means, const float* __restrict__ scales, const float* __restrict__ rots,
+    const ShT* __restrict__ shr_all, int64_t n, int bases, CamParams cam, const uint32_t* __restrict__ n_touched,
+    const float4* __restrict__ conic_opacity, const float* __restrict__ grad2d, float* __restrict__ g_means,
+    float* __restrict__ g_scales, float* __restrict__ g_rots, float* __restrict__ g_opac, float* __restrict__ g_sh0,
+    float* __restrict__ g_shr_all, float4* __restrict__ densif) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n || n_touched[i] == 0) return;
+    const float* gr = grad2d + (size_t)i * kGradStride;
+    const float4 gA = *(const float4*)(gr);       // dmx, dmy, absx, absy
+    const float4 gB = *(const float4*)(gr + 4);   // dca, dcb, dcc, dr
+    const float4 gC = *(const float4*)(gr + 8);   // dg, db, alpha partial, -
+    const float mx = means[3 * i], my = means[3 * i + 1], mz = means[3 * i + 2];
+
+    // ---- SH backward (kernels_backward.cuh:22-86)
+    const float gc[3] = {gB.w, gC.x, gC.y};
+    for (int c = 0; c < 3; ++c) g_sh0[3 * i + c] += 0.28209479177387814f * gc[c];
+    float dmc0 = 0.f, dmc1 = 0.f, dmc2 = 0.f;
+    if (bases > 1) {
+        const ShT* shr = shr_all + 45 * i;
+        float* gshr = g_shr_all + 45 * i;
+        const float xr = mx - cam.cam_pos[0], yr = my - cam.cam_pos[1], zr = mz - cam.cam_pos[2];
+        const float inv = 1.0f / __builtin_sqrtf(xr * xr + yr * yr + zr * zr);
+        const float x = xr * inv, y = yr * inv, z = zr * inv;
+        float k[15];
+        float gdx[3], gdy[3], gdz[3];
+        k[0] = -0.48860251190291987f * y;
+        k[1] = 0.48860251190291987f * z;
+        k[2] = -0.48860251190291987f * x;
+        int nb = 3;
+        for (int c = 0; c < 3; ++c) {
+            gdx[c] = -0.48860251190291987f * load_as_float(shr, 3 * 2 + c);
+            gdy[c] = -0.48860251190291987f * load_as_float(shr, 3 * 0 + c);
+            gdz[c] = 0.48860251190291987f * load_as_float(shr, 3 * 1 + c);
+        }
+        if (bases > 4) {
+            const float xx = x * x, yy = y * y, zz = z * z;
+            const float xy = x * y, xz = x * z, yz = y * z;
+            k[3] = 1.0925484305920792f * xy;
+            k[4] = -1.0925484305920792f * yz;
+            k[5] = 0.94617469575755997f * zz - 0.31539156525251999f;
+            k[6] = -1.0925484305920792f * xz;
+            k[7] = 0.54627421529603959f * xx - 0.54627421529603959f * yy;
+            nb = 8;
+            const float f7x = (float)(1.0925484305920792 * (double)x);
+            const float f7y = (float)(-1.0925484305920792 * (double)y);
+            const float f5z = (float)(1.8923493915151202 * (double)z);
+            for (int c = 0; c < 3; ++c) {
+                const float s3 = load_as_float(shr, 9 + c), s4 = load_as_float(shr, 12 + c);
+                const float s5 = load_as_float(shr, 15 + c), s6 = load_as_float(shr, 18 + c);
+                const float s7 = load_as_float(shr, 21 + c);
+                gdx[c] = gdx[c] + (1.0925484305920792f * y) * s3 + (-1.0925484305920792f * z) * s6 + f7x * s7;
+                gdy[c] = gdy[c] + (1.0925484305920792f * x) * s3 + (-1.0925484305920792f * z) * s4 + f7y * s7;
+                gdz[c] = gdz[c] + (-1.0925484305920792f * y) * s4 + f5z * s5 + (-1.0925484305920792f * x) * s6;
+            }
+            if (bases > 9) {
+                k[8] = 0.59004358992664352f * y * (-3.0f * xx + yy);
+                k[9] = 2.8906114426405538f * xy * z;
+                k[10] = 0.45704579946446572f * y * (1.0f - 5.0f * zz);
+                k[11] = 0.3731763325901154f * z * (5.0f * zz - 3.0f);
+                k[12] = 0.45704579946446572f * x * (1.0f - 5.0f * zz);
+                k[13] = 1.4453057213202769f * z * (xx - yy);
+                k[14] = 0.59004358992664352f * x * (-xx + 3.0f * yy);
+                nb = 15;
+                for (int c = 0; c < 3; ++c) {
+                    const float s8 = load_as_float(shr, 24 + c), s9 = load_as_float(shr, 27 + c);
+                    const float s10 = load_as_float(shr, 30 + c), s11 = load_as_float(shr, 33 + c);
+                    const float s12 = load_as_float(shr, 36 + c), s13 = load_as_float(shr, 39 + c);
+                    const float s14 = load_as_float(shr, 42 + c);
+                    gdx[c] = gdx[c] + (-3.5402615395598609f * xy) * s8 + (2.8906114426405538f * yz) * s9 +
+                             (0.45704579946446572f - 2.2852289973223288f * zz) * s12 +
+                             (2.8906114426405538f * xz) * s13 +
+                             (-1.7701307697799304f * xx + 1.7701307697799304f * yy) * s14;
+                    gdy[c] = gdy[c] + (-1.7701307697799304f * xx + 1.7701307697799304f * yy) * s8 +
+                             (2.8906114426405538f * xz) * s9 +
+                             (0.45704579946446572f - 2.2852289973223288f * zz) * s10 +
+                             (-2.8906114426405538f * yz) * s13 + (3.5402615395598609f * xy) * s14;
+                    gdz[c] = gdz[c] + (2.8906114426405538f * xy) * s9 + (-4.5704579946446566f * yz) * s10 +
+                             (5.597644988851731f * zz - 1.1195289977703462f) * s11 +
+                             (-4.5704579946446566f * xz) * s12 +
+                             (1.4453057213202769f * xx - 1.4453057213202769f * yy) * s13;
+                }
+            }
+        }
+        for (int b = 0; b < nb; ++b)
+            for (int c = 0; c < 3; ++c) gshr[3 * b + c] += k[b] * gc[c];
+        const float gx = gdx[0] * gc[0] + gdx[1] * gc[1] + gdx[2] * gc[2];
+        const float gy = gdy[0] * gc[0] + gdy[1] * gc[1] + gdy[2] * gc[2];
+        const float gz = gdz[0] * gc[0] + gdz[1] * gc[1] + gdz[2] * gc[2];
+        const float xx_ = xr * xr, yy_ = yr * yr, zz_ = zr * zr;
+        const float xy_ = xr * yr, xz_ = xr * zr, yz_ = yr * zr;
+        const float nsq = xx_ + yy_ + zz_;
+        const float sc = 1.0f / __builtin_sqrtf(nsq * nsq * nsq);
+        dmc0 = ((yy_ + zz_) * gx - xy_ * gy - xz_ * gz) * sc;
+        dmc1 = (-xy_ * gx + (xx_ + zz_) * gy - yz_ * gz) * sc;
+        dmc2 = (-xz_ * gx - yz_ * gy + (xx_ + yy_) * gz) * sc;
+    }
+
+    // ---- projection / covariance backward (kernels_backward.cuh:132-336)
+    const float* r1 = cam.r1;
+    const float* r2 = cam.r2;
+    const float* r3 = cam.r3;
+    const float depth = r3[0] * mx + r3[1] * my + r3[2] * mz + r3[3];
+    const float x = (r1[0] * mx + r1[1] * my + r1[2] * mz + r1[3]) / depth;
+    const float y = (r2[0] * mx + r2[1] * my + r2[2] * mz + r2[3]) / depth;
+    const float e0 = det_expf(scales[3 * i]), e1 = det_expf(scales[3 * i + 1]), e2 = det_expf(scales[3 * i + 2]);
+    const float vx = e0 * e0, vy = e1 * e1, vz = e2 * e2;
+    const float qr = rots[4 * i], qx = rots[4 * i + 1], qy = rots[4 * i + 2], qz = rots[4 * i + 3];
+    const float qrr = qr * qr, qxx_r = qx * qx, qyy_r = qy * qy, qzz_r = qz * qz;
+    const float qn = qrr + qxx_r + qyy_r + qzz_r;
+    const float qxx = 2.0f * qxx_r / qn, qyy = 2.0f * qyy_r / qn, qzz = 2.0f * qzz_r / qn;
+    const float qxy = 2.0f * qx * qy / qn, qxz = 2.0f * qx * qz / qn, qyz = 2.0f * qy * qz / qn;
+    const float qrx = 2.0f * qr * qx / qn, qry = 2.0f * qr * qy / qn, qrz = 2.0f * qr * qz / qn;
+    const float R11 = 1.0f - (qyy + qzz), R12 = qxy - qrz, R13 = qry + qxz;
+    const float R21 = qrz + qxy, R22 = 1.0f - (qxx + qzz), R23 = qyz - qrx;
+    const float R31 = qxz - qry, R32 = qrx + qyz, R33 = 1.0f - (qxx + qyy);
+    const float S11 = R11 * vx, S12 = R12 * vy, S13 = R13 * vz;
+    const float S21 = R21 * vx, S22 = R22 * vy, S23 = R23 * vz;
+    const float S31 = R31 * vx, S32 = R32 * vy, S33 = R33 * vz;
+    const float c11 = S11 * R11 + S12 * R12 + S13 * R13;
+    const float c12 = S11 * R21 + S12 * R22 + S13 * R23;
+    const float c13 = S11 * R31 + S12 * R32 + S13 * R33;
+    const float c22 = S21 * R21 + S22 * R22 + S23 * R23;
+    const float c23 = S21 * R31 + S22 * R32 + S23 * R33;
+    const float c33 = S31 * R31 + S32 * R32 + S33 * R33;
+    const float clip_left = (-0.15f * cam.w - cam.cx) / cam.fx;
+    const float clip_right = (1.15f * cam.w - cam.cx) / cam.fx;
+    const float clip_top = (-0.15f * cam.h - cam.cy) / cam.fy;
+    const float clip_bottom = (1.15f * cam.h - cam.cy) / cam.fy;
+    const float tx = __builtin_fmaxf(clip_left, __builtin_fminf(x, clip_right));
+    const float ty = __builtin_fmaxf(clip_top, __builtin_fminf(y, clip_bottom));
+    const float j11 = cam.fx / depth, j13 = -j11 * tx, j22 = cam.fy / depth, j23 = -j22 * ty;
+    const float jw1x = j11 * r1[0] + j13 * r3[0], jw1y = j11 * r1[1] + j13 * r3[1], jw1z = j11 * r1[2] + j13 * r3[2];
+    const float jw2x = j22 * r2[0] + j23 * r3[0], jw2y = j22 * r2[1] + j23 * r3[1], jw2z = j22 * r2[2] + j23 * r3[2];
+    const float a1x = jw1x * c11 + jw1y * c12 + jw1z * c13;
+    const float a1y = jw1x * c12 + jw1y * c22 + jw1z * c23;
+    const float a1z = jw1x * c13 + jw1y * c23 + jw1z * c33;
+    const float a2x = jw2x * c11 + jw2y * c12 + jw2z * c13;
+    const float a2y = jw2x * c12 + jw2y * c22 + jw2z * c23;
+    const float a2z = jw2x * c13 + jw2y * c23 + jw2z * c33;
+    const float a = (a1x * jw1x + a1y * jw1y + a1z * jw1z) + kDilation;
+    const float b = a1x * jw2x + a1y * jw2y + a1z * jw2z;
+    const float c = (a2x * jw2x + a2y * jw2y + a2z * jw2z) + kDilation;
+    const float aa = a * a, bb = b * b, cc_ = c * c;
+    const float ac = a * c, ab = a * b, bc = b * c;
+    const float det = ac - bb;
+    const float drcp = 1.0f / (det + 1e-8f);
+    const float drcp2 = drcp * drcp;
+    const float gca = gB.x, gcb = gB.y, gcc = gB.z;
+    const float dca = drcp2 * (2.0f * bc * gcb - cc_ * gca - bb * gcc);
+    const float dcb = drcp2 * (bc * gca - (ac + bb) * gcb + ab * gcc);
+    const float dcc = drcp2 * (2.0f * ab * gcb - bb * gca - aa * gcc);
+    const float d11 = (jw1x * jw1x) * dca + 2.0f * (jw1x * jw2x) * dcb + (jw2x * jw2x) * dcc;
+    const float d12 = (jw1x * jw1y) * dca + (jw1x * jw2y + jw1y * jw2x) * dcb + (jw2x * jw2y) * dcc;
+    const float d13 = (jw1x * jw1z) * dca + (jw1x * jw2z + jw1z * jw2x) * dcb + (jw2x * jw2z) * dcc;
+    const float d22 = (jw1y * jw1y) * dca + 2.0f * (jw1y * jw2y) * dcb + (jw2y * jw2y) * dcc;
+    const float d23 = (jw1y * jw1z) * dca + (jw1y * jw2z + jw1z * jw2y) * dcb + (jw2y * jw2z) * dcc;
+    const float d33 = (jw1z * jw1z) * dca + 2.0f * (jw1z * jw2z) * dcb + (jw2z * jw2z) * dcc;
+    const float dj1x = 2.0f * (a1x * dca + a2x * dcb), dj1y = 2.0f * (a1y * dca + a2y * dcb),
+                dj1z = 2.0f * (a1z * dca + a2z * dcb);
+    const float dj2x = 2.0f * (a1x * dcb + a2x * dcc), dj2y = 2.0f * (a1y * dcb + a2y * dcc),
+                dj2z = 2.0f * (a1z * dcb + a2z * dcc);
+    const float dL_dj11 = r1[0] * dj1x + r1[1] * dj1y + r1[2] * dj1z;
+    const float dL_dj22 = r2[0] * dj2x + r2[1] * dj2y + r2[2] * dj2z;
+    const float dL_dj13 = r3[0] * dj1x + r3[1] * dj1y + r3[2] * dj1z;
+    const float dL_dj23 = r3[0] * dj2x + r3[1] * dj2y + r3[2] * dj2z;
+    const float mask_x = (x > clip_left && x < clip_right) ? 1.0f : 0.0f;
+    const float mask_y = (y > clip_top && y < clip_bottom) ? 1.0f : 0.0f;
+    const float dj13c = dL_dj13 * mask_x, dj23c = dL_dj23 * mask_y;
+    const float h1 = dL_dj11 - 2.0f * tx * dj13c;
+    const float h2 = dL_dj22 - 2.0f * ty * dj23c;
+    const float gm2x = gA.x, gm2y = gA.y;
+    const float dcx = j11 * (gm2x - dj13c / depth);
+    const float dcy = j22 * (gm2y - dj23c / depth);
+    const float dcz = -j11 * (x * gm2x + h1 / depth) - j22 * (y * gm2y + h2 / depth);
+    const float gmx = r1[0] * dcx + r2[0] * dcy + r3[0] * dcz;
+    const float gmy = r1[1] * dcx + r2[1] * dcy + r3[1] * dcz;
+    const float gmz = r1[2] * dcx + r2[2] * dcy + r3[2] * dcz;
+    g_means[3 * i] += gmx + dmc0;
+    g_means[3 * i + 1] += gmy + dmc1;
+    g_means[3 * i + 2] += gmz + dmc2;
+    const float dvx = R11 * R11 * d11 + R21 * R21 * d22 + R31 * R31 * d33 +
+                      2.0f * (R11 * R21 * d12 + R11 * R31 * d13 + R21 * R31 * d23);
+    const float dvy = R12 * R12 * d11 + R22 * R22 * d22 + R32 * R32 * d33 +
+                      2.0f * (R12 * R22 * d12 + R12 * R32 * d13 + R22 * R32 * d23);
+    const float dvz = R13 * R13 * d11 + R23 * R23 * d22 + R33 * R33 * d33 +
+                      2.0f * (R13 * R23 * d12 + R13 * R33 * d13 + R23 * R33 * d23);
+    g_scales[3 * i] += 2.0f * e0 * e0 * dvx;
+    g_scales[3 * i + 1] += 2.0f * e1 * e1 * dvy;
+    g_scales[3 * i + 2] += 2.0f * e2 * e2 * dvz;
+    const float D11 = 2.0f * (S11 * d11 + S21 * d12 + S31 * d13);
+    const float D12 = 2.0f * (S12 * d11 + S22 * d12 + S32 * d13);
+    const float D13 = 2.0f * (S13 * d11 + S23 * d12 + S33 * d13);
+    const float D21 = 2.0f * (S11 * d12 + S21 * d22 + S31 * d23);
+    const float D22 = 2.0f * (S12 * d12 + S22 * d22 + S32 * d23);
+    const float D23 = 2.0f * (S13 * d12 + S23 * d22 + S33 * d23);
+    const float D31 = 2.0f * (S11 * d13 + S21 * d23 + S31 * d33);
+    const float D32 = 2.0f * (S12 * d13 + S22 * d23 + S32 * d33);
+    const float D33 = 2.0f * (S13 * d13 + S23 * d23 + S33 * d33);
+    const float gqxx = -D22 - D33, gqyy = -D11 - D33, gqzz = -D11 - D22;
+    const float gqxy = D12 + D21, gqxz = D13 + D31, gqyz = D23 + D32;
+    const float gqrx = D32 - D23, gqry = D13 - D31, gqrz = D21 - D12;
+    const float hlp = qxx * gqxx + qyy * gqyy + qzz * gqzz + qxy * gqxy + qxz * gqxz + qyz * gqyz + qrx * gqrx +
+                      qry * gqry + qrz * gqrz;
+    const float den = qn * __builtin_sqrtf(qn);
+    g_rots[4 * i] += 2.0f * (qx * gqrx + qy * gqry + qz * gqrz - qr * hlp) / den;
+    g_rots[4 * i + 1] += 2.0f * (2.0f * qx * gqxx + qy * gqxy + qz * gqxz + qr * gqrx - qx * hlp) / den;
+    g_rots[4 * i + 2] += 2.0f * (2.0f * qy * gqyy + qx * gqxy + qz * gqyz + qr * gqry - qy * hlp) / den;
+    g_rots[4 * i + 3] += 2.0f * (2.0f * qz * gqzz + qx * gqxz + qy * gqyz + qr * gqrz - qz * hlp) / den;
+    g_opac[i] += gC.z * (1.0f - conic_opacity[i].w);
+    if (densif) {
+        float4 d = densif[i];
+        d.x += 1.0f;
+        const float ux = gm2x * (0.5f * cam.w), uy = gm2y * (0.5f * cam.h);
+        d.y += __builtin_sqrtf(ux * ux + uy * uy);
+        const float wx = gA.z * (0.5f * cam.w), wy = gA.w * (0.5f * cam.h);
+        d.z += __builtin_sqrtf(wx * wx + wy * wy);
+        densif[i] = d;
+    }
+}
+
+void launch_preprocess_backward(const GaussianView& g, const CamParams& cam, const uint32_t* n_touched,
+                                const float4* conic_opacity, const float* grad2d, const GradView& out, float* densif,
+                                hipStream_t s) {
+    if (g.n <= 0) return;
+    const int bases = (g.sh_degree + 1) * (g.sh_degree + 1);
+    const unsigned grid = (unsigned)((g.n + 255) / 256);
+    if (g.sh_dtype == kShF16) {
+        preprocess_backward_kernel<__half><<<grid, 256, 0, s>>>(
+            g.means, g.scales, g.rotations, (const __half*)g.sh_rest, g.n, bases, cam, n_touched, conic_opacity,
+            grad2d, out.means, out.scales, out.rotations, out.opacities, out.sh0, out.sh_rest, (float4*)densif);
+    } else {
+        preprocess_backward_kernel<float><<<grid, 256, 0, s>>>(
+            g.means, g.scales, g.rotations, (const float*)g.sh_rest, g.n, bases, cam, n_touched, conic_opacity,
+            grad2d, out.means, out.scales, out.rotations, out.opacities, out.sh0, out.sh_rest, (float4*)densif);
+    }
+}
+
+}  // namespace tgs

@@ -1,0 +1,57 @@
+// Device self tests: the deterministic exp/log evaluated on the GPU (checked
+// bit for bit against the CPU oracle's copy) and the wave64 DPP primitives
+// (checked against plain host arithmetic).
+#include "common.h"
+#include "kernels.h"
+
+namespace tgs {
+
+__global__ void detmath_kernel(int op, const float* in, float* out, int64_t n) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const float x = in[i];
+    float y;
+    switch (op) {
+        case 0: y = det_expf(x); break;
+        case 1: y = det_logf(x); break;
+        case 2: y = det_expf_nonpos(x <= 0.f ? x : -x); break;
+        case 3: y = x / (x * 0.7f + 1.3f); break;       // correctly rounded division
+        case 4: y = __builtin_sqrtf(x); break;           // correctly rounded sqrt
+        case 5: y = __half2float(__float2half_rn(x)); break;
+        default: y = 0.f; break;
+    }
+    out[i] = y;
+}
+
+void launch_detmath(int op, const float* in, float* out, int64_t n, hipStream_t s) {
+    if (n <= 0) return;
+    detmath_kernel<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(op, in, out, n);
+}
+
+// One wave of 64 inputs -> out[0..63] inclusive scan, out[64] sum,
+// out[65] max, out[66] float-sum of (float)in as bits, out[67] lane id check.
+__global__ void wave_selftest_kernel(const uint32_t* in, uint32_t* out) {
+    const uint32_t lane = lane_id();
+    const uint32_t v = in[lane];
+    const uint32_t scan = wave_inclusive_scan_u32(v);
+    out[lane] = scan;
+    const uint32_t sum = wave_sum_u32(v);
+    const uint32_t mx = wave_max_u32(v);
+    const float fs = wave_sum_row3((float)v);
+    const float fs63 = readlane_f32(fs, 63);
+    const uint64_t m = ballot((v & 1u) != 0u);
+    const uint32_t rank = mask_rank(m);
+    out[128 + lane] = rank;
+    if (lane == 0) {
+        out[64] = sum;
+        out[65] = mx;
+        out[66] = f2u(fs63);
+        out[67] = (uint32_t)__builtin_popcountll(m);
+    }
+}
+
+void launch_wave_selftest(const uint32_t* in, uint32_t* out, hipStream_t s) {
+    wave_selftest_kernel<<<1, 64, 0, s>>>(in, out);
+}
+
+}  // namespace tgs

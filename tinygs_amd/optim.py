@@ -1,0 +1,108 @@
+"""SimpleAdam over the C ABI.
+
+Mirrors tinygs's OptimizerBase / SimpleAdam / create_optimizer
+(tinygs/include/tinygs/optim/optim.hpp:39-106,
+tinygs/include/tinygs/optim/simple_adam.hpp:30-87, tinygs/src/optim/optim.cu:86-105).
+"""
+from __future__ import annotations
+
+import ctypes as C
+
+from . import _lib
+from .core import GPUGaussian3d, stream_ptr
+
+GROUPS = ("means", "opacities", "rotations", "scales", "sh0", "sh_rest")
+
+
+class OptimizerBase:
+    def __init__(self, gaussians: GPUGaussian3d, gaussians_grad: GPUGaussian3d):
+        self.m_gaussians = gaussians
+        self.m_gaussians_grad = gaussians_grad
+
+    def get_gaussians(self):
+        return self.m_gaussians
+
+    def get_gaussians_grad(self):
+        return self.m_gaussians_grad
+
+
+class SimpleAdam(OptimizerBase):
+    def __init__(self, gaussians: GPUGaussian3d, gaussians_grad: GPUGaussian3d):
+        super().__init__(gaussians, gaussians_grad)
+        if gaussians.size() != gaussians_grad.size():
+            raise RuntimeError("SimpleAdam::step: gaussians and gaussians_grad must have same size")
+        self._cp = gaussians.to_c()
+        self._cg = gaussians_grad.to_c()
+        h = C.c_void_p()
+        _lib.check(_lib.load().tgs_adam_create(C.byref(self._cp), C.byref(self._cg), C.byref(h)), "create_optimizer")
+        self._h = h
+
+    def __del__(self):
+        h = getattr(self, "_h", None)
+        if h is not None and h.value:
+            try:
+                _lib.load().tgs_adam_destroy(h)
+            except Exception:
+                pass
+            self._h = None
+
+    def _rebind(self):
+        self._cp = self.m_gaussians.to_c()
+        self._cg = self.m_gaussians_grad.to_c()
+        _lib.check(_lib.load().tgs_adam_set_gaussians(self._h, C.byref(self._cp), C.byref(self._cg)), "set_gaussians")
+
+    def step(self, scale: float, stream=None):
+        self._rebind()
+        _lib.check(_lib.load().tgs_adam_step(self._h, float(scale), stream_ptr(stream)), "SimpleAdam::step")
+
+    def reset(self, stream=None):
+        _lib.check(_lib.load().tgs_adam_reset(self._h, stream_ptr(stream)), "SimpleAdam::reset")
+
+    def set_lr(self, lr: float):
+        _lib.check(_lib.load().tgs_adam_set_lr(self._h, float(lr)), "set_lr")
+
+    def get_lr(self) -> float:
+        return float(_lib.load().tgs_adam_get_lr(self._h))
+
+    def global_steps(self) -> int:
+        return int(_lib.load().tgs_adam_global_steps(self._h))
+
+    def get_params(self) -> dict:
+        p = _lib.tgs_adam_params()
+        _lib.check(_lib.load().tgs_adam_get_params(self._h, C.byref(p)), "get_params")
+        return {f: getattr(p, f) for f, _ in p._fields_}
+
+    def set_params(self, config: dict):
+        p = _lib.tgs_adam_params()
+        _lib.check(_lib.load().tgs_adam_get_params(self._h, C.byref(p)), "get_params")
+        alias = {"eps": "epsilon"}
+        for k, v in config.items():
+            k = alias.get(k, k)
+            if k == "decay_reduction":
+                p.decay_mean = 1 if v == "mean" else 0
+            elif hasattr(p, k):
+                setattr(p, k, v)
+            else:
+                raise RuntimeError(f"SimpleAdam: unknown parameter {k}")
+        _lib.check(_lib.load().tgs_adam_set_params(self._h, C.byref(p)), "set_params")
+
+    def moments(self, group: str):
+        import torch
+        k = GROUPS.index(group)
+        a, b = C.c_void_p(), C.c_void_p()
+        _lib.check(_lib.load().tgs_adam_moments(self._h, k, C.byref(a), C.byref(b)), "moments")
+        mult = (3, 1, 4, 3, 3, 45)[k]
+        n = mult * self.m_gaussians.size()
+        dev = self.m_gaussians.means().device
+        m1 = torch.empty(n, dtype=torch.float32, device=dev)
+        m2 = torch.empty(n, dtype=torch.float32, device=dev)
+        _lib.copy_device(a.value, 4 * n, m1)
+        _lib.copy_device(b.value, 4 * n, m2)
+        return m1, m2
+
+
+def create_optimizer(optimizer_type: str, gaussians: GPUGaussian3d, gaussians_grad: GPUGaussian3d):
+    t = optimizer_type.lower()
+    if t == "simple_adam":
+        return SimpleAdam(gaussians, gaussians_grad)
+    raise RuntimeError(f"Unknown optimizer type: {optimizer_type}")

@@ -1,0 +1,145 @@
+"""FastGSRasterizer over the C ABI.
+
+Mirrors tinygs's RasterizerBase / FastGSRasterizer / create_rasterizer
+(tinygs/include/tinygs/rasterizer/rasterizer.hpp:38-61,
+tinygs/include/tinygs/rasterizer/fastgs.hpp:14-37,
+tinygs/src/rasterizer/rasterizer.cpp:44-53): same method names, same
+accumulation and error behaviour (RuntimeError where the reference throws
+std::runtime_error).
+"""
+from __future__ import annotations
+
+import ctypes as C
+
+from . import _lib
+from .core import DataType, GPUGaussian3d, RasterizeContext, ptr, stream_ptr
+
+
+class RasterizerBase:
+    def forward(self, ctx: RasterizeContext):
+        raise NotImplementedError
+
+    def backward(self, ctx: RasterizeContext):
+        raise NotImplementedError
+
+    def set_gaussians(self, gaussians: GPUGaussian3d):
+        self.m_gaussians = gaussians
+
+    def get_params(self) -> dict:
+        raise NotImplementedError
+
+    def set_params(self, params: dict):
+        raise NotImplementedError
+
+
+class FastGSRasterizer(RasterizerBase):
+    def __init__(self):
+        L = _lib.load()
+        h = C.c_void_p()
+        _lib.check(L.tgs_rasterizer_create(b"fastgs", C.byref(h)), "create_rasterizer")
+        self._h = h
+        self.m_gaussians = None
+        self.m_params = {"f16_grad_scaler": 1.0, "enable_pose_opt": False}
+
+    def __del__(self):
+        h = getattr(self, "_h", None)
+        if h is not None and h.value:
+            try:
+                _lib.load().tgs_rasterizer_destroy(h)
+            except Exception:
+                pass
+            self._h = None
+
+    def set_gaussians(self, gaussians: GPUGaussian3d):
+        self.m_gaussians = gaussians
+        self._cg = gaussians.to_c()
+        _lib.check(_lib.load().tgs_rasterizer_set_gaussians(self._h, C.byref(self._cg)), "set_gaussians")
+
+    def forward(self, ctx: RasterizeContext):
+        if self.m_gaussians is None:
+            raise RuntimeError("Gaussians not set")
+        # the pointers may have changed (e.g. tensors replaced); rebind
+        self._cg = self.m_gaussians.to_c()
+        L = _lib.load()
+        _lib.check(L.tgs_rasterizer_set_gaussians(self._h, C.byref(self._cg)), "set_gaussians")
+        img = ctx.fwd_output.image
+        if img.data_type != DataType.Float32:
+            raise RuntimeError("FastGSRasterizer: only float32 images are supported")
+        cam = ctx.fwd_input.to_c()
+        _lib.check(L.tgs_rasterizer_forward(self._h, C.byref(cam), ptr(img.data), _lib.TGS_DTYPE_FLOAT32,
+                                            ptr(ctx.densification_info), stream_ptr(ctx.stream)), "forward")
+
+    def backward(self, ctx: RasterizeContext):
+        if self.m_gaussians is None or ctx.gaussians_grad is None:
+            raise RuntimeError("Gaussians or gradient gaussians not set")
+        g = ctx.gaussians_grad.to_c()
+        L = _lib.load()
+        _lib.check(L.tgs_rasterizer_backward(self._h, ptr(ctx.grad_output.image.data), ptr(ctx.fwd_output.image.data),
+                                             C.byref(g), ptr(ctx.densification_info), stream_ptr(ctx.stream)),
+                   "backward")
+
+    def counts(self):
+        v, i, t = C.c_int64(), C.c_int64(), C.c_int64()
+        _lib.check(_lib.load().tgs_rasterizer_counts(self._h, C.byref(v), C.byref(i), C.byref(t)), "counts")
+        return v.value, i.value, t.value
+
+    def debug_view(self) -> dict:
+        """Copies of the internal buffers of the last forward (tests only)."""
+        import torch
+        dv = _lib.tgs_debug_view()
+        _lib.check(_lib.load().tgs_rasterizer_debug_view(self._h, C.byref(dv)), "debug_view")
+        n = self.m_gaussians.size()
+        V, I, T = dv.n_visible, dv.n_instances, dv.n_tiles
+        dev = self.m_gaussians.means().device
+        cs = None
+
+        def grab(p, count, dtype):
+            t = torch.empty(max(int(count), 0), dtype=dtype, device=dev)
+            if p and count:
+                _lib.copy_device(p, t.numel() * t.element_size(), t)
+            return t
+
+        out = {
+            "n_touched": grab(dv.n_touched, n, torch.int32),
+            "bounds": grab(dv.bounds, 2 * n, torch.int32),
+            "mean2d": grab(dv.mean2d, 2 * n, torch.float32),
+            "conic_opacity": grab(dv.conic_opacity, 4 * n, torch.float32),
+            "color": grab(dv.color, 4 * n, torch.float32),
+            "depth_sorted_keys": grab(dv.depth_sorted_keys, V, torch.int32),
+            "depth_sorted_prims": grab(dv.depth_sorted_prims, V, torch.int32),
+            "instance_tiles": grab(dv.instance_tiles, I, torch.int32),
+            "instance_prims": grab(dv.instance_prims, I, torch.int32),
+            "tile_ranges": grab(dv.tile_ranges, 2 * T, torch.int32),
+            "tile_max": grab(dv.tile_max, T, torch.int32),
+            "n_visible": V, "n_instances": I, "n_tiles": T,
+        }
+        del cs
+        return out
+
+    def debug_n_contrib(self, shape) -> "object":
+        import torch
+        dv = _lib.tgs_debug_view()
+        _lib.check(_lib.load().tgs_rasterizer_debug_view(self._h, C.byref(dv)), "debug_view")
+        t = torch.empty(shape.channel_stride, dtype=torch.int32, device=self.m_gaussians.means().device)
+        return _lib.copy_device(dv.n_contrib, t.numel() * 4, t)
+
+    def debug_grad2d(self):
+        import torch
+        dv = _lib.tgs_debug_view()
+        _lib.check(_lib.load().tgs_rasterizer_debug_view(self._h, C.byref(dv)), "debug_view")
+        n = self.m_gaussians.size()
+        t = torch.empty(12 * n, dtype=torch.float32, device=self.m_gaussians.means().device)
+        return _lib.copy_device(dv.grad2d, t.numel() * 4, t)
+
+    def get_params(self) -> dict:
+        return {"type": "fastgs"}
+
+    def set_params(self, params: dict):
+        pass
+
+
+def create_rasterizer(rasterizer_type: str) -> RasterizerBase:
+    t = rasterizer_type.lower()
+    if t == "fastgs":
+        return FastGSRasterizer()
+    raise RuntimeError(f"Unknown rasterizer type: {rasterizer_type}")

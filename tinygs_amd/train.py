@@ -1,0 +1,109 @@
+"""One training iteration of the FastGS path, in the order of
+Orchestrator::train_step (tinygs/src/orchestrator.cu:335-439):
+
+  zero parameter gradients (:351-353) and loss / gradient images (:354-355)
+  -> FastGSRasterizer::forward (:371)
+  -> losses: L1 weight * grad_scaler, fused SSIM weight * grad_scaler (:763-782)
+  -> FastGSRasterizer::backward with grad_output = loss gradient (:377-380)
+  -> SimpleAdam::step(1 / (grad_scaler * accumulate_grad_steps)) (:393-404)
+
+Everything runs on one HIP stream; the only host synchronisation is the one
+inside the forward that sizes the instance buffers.
+"""
+from __future__ import annotations
+
+from .core import GPUBatchInput, GPUGaussian3d, Image, LossContext, RasterizeContext
+from .loss import create_loss
+from .optim import create_optimizer
+from .rasterizer import create_rasterizer
+
+
+class TrainStep:
+    def __init__(self, scene, l1_weight: float = 0.8, ssim_weight: float = 0.2, grad_scaler: float = 1.0,
+                 eps: float = 1e-15, shs_lr: float | None = None, means_lr: float | None = None,
+                 max_grad_1: float | None = None, device: str = "cuda", stream=None):
+        import torch
+        self.scene = scene
+        self.stream = stream
+        self.gaussians = GPUGaussian3d.from_scene(scene, device)
+        self.grads = self.gaussians.gradient_like()
+        self.rasterizer = create_rasterizer("fastgs")
+        self.rasterizer.set_gaussians(self.gaussians)
+        shape = scene.camera.shape
+        self.shape = shape
+        self.pred = Image.empty(shape, device)
+        self.target = Image(shape, "float32", torch.from_numpy(scene.target).to(device))
+        self.loss_img = Image.empty(shape, device)
+        self.grad_img = Image.empty(shape, device)
+        self.losses = []
+        if l1_weight:
+            self.losses.append((create_loss("l1"), float(l1_weight)))
+        if ssim_weight:
+            self.losses.append((create_loss("fused_ssim"), float(ssim_weight)))
+        self.grad_scaler = float(grad_scaler)
+        self.optimizer = create_optimizer("simple_adam", self.gaussians, self.grads)
+        params = {"epsilon": eps}
+        if shs_lr is not None:
+            params["shs_lr"] = shs_lr
+        if means_lr is not None:
+            params["means_lr"] = means_lr
+        if max_grad_1 is not None:
+            params["max_grad_1"] = max_grad_1
+        self.optimizer.set_params(params)
+        self.ctx = RasterizeContext(stream=stream, grad_scaler=self.grad_scaler)
+        self.ctx.fwd_input = GPUBatchInput.from_camera(scene.camera)
+        self.ctx.fwd_output.image = self.pred
+        self.ctx.gaussians_grad = self.grads
+        self.ctx.grad_output.image = self.grad_img
+        self.loss_ctx = LossContext(self.pred, self.target, self.loss_img, self.grad_img, stream)
+
+    def zero(self):
+        import torch
+        s = self.stream
+        with torch.cuda.stream(s) if s is not None else _null():
+            self.grads.memset(0)
+            self.loss_img.data.zero_()
+            self.grad_img.data.zero_()
+
+    def forward(self):
+        self.rasterizer.forward(self.ctx)
+
+    def losses_and_grad(self):
+        for loss, w in self.losses:
+            loss.evaluate(self.loss_ctx, w * self.grad_scaler)
+
+    def backward(self):
+        self.rasterizer.backward(self.ctx)
+
+    def optimize(self):
+        self.optimizer.step(1.0 / self.grad_scaler, self.stream)
+
+    def step(self):
+        self.zero()
+        self.forward()
+        self.losses_and_grad()
+        self.backward()
+        self.optimize()
+
+    # host copies (tests / diagnostics)
+    def image(self):
+        return self.pred.data.cpu().numpy()
+
+    def grad_image(self):
+        return self.grad_img.data.cpu().numpy()
+
+    def params(self):
+        g = self.gaussians
+        return {"means": g.means().cpu().numpy().reshape(-1), "scales": g.scales().cpu().numpy().reshape(-1),
+                "rotations": g.rotations().cpu().numpy().reshape(-1),
+                "opacities": g.opacities().cpu().numpy().reshape(-1),
+                "sh0": g.sh_coefficient_0().float().cpu().numpy().reshape(-1),
+                "sh_rest": g.sh_coefficients_rest().float().cpu().numpy().reshape(-1)}
+
+
+class _null:
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *a):
+        return False
