@@ -1,0 +1,180 @@
+"""Headline benchmark: ms per training iteration (fwd + L1/SSIM + bwd + Adam)
+of the FastGS path at 1M Gaussians, 1920x1080, SH degree 3 with fp16 SH
+storage, on one MI355X, plus the HBM roofline of the
+dominant kernel and the CPU oracle's time on the same workload.
+
+  python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 3] [--no-cpu-baseline]
+
+Prints one JSON line on stdout; a per-stage table goes to stderr.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "ms per fwd+bwd+Adam iter at 1M Gaussians 1080p; % of HBM roofline"
+HBM_PEAK_GBS = 8000.0
+
+STAGES = ["preprocess", "depth_sort", "emit_instances", "tile_sort", "blend_forward", "l1", "fused_ssim",
+          "blend_backward", "preprocess_backward", "adam"]
+SINGLE_KERNEL = {"preprocess", "blend_forward", "l1", "blend_backward", "preprocess_backward", "adam"}
+
+
+def algorithmic_bytes(stage, c):
+    """Compulsory HBM bytes of one launch (each input read once, each output
+    written once; implementation scratch excluded)."""
+    N, V, I, T, P = c["N"], c["V"], c["I"], c["T"], c["P"]
+    s, K, e = c["sh_bytes"], c["sh_bases"], 4
+    if stage == "preprocess":
+        return 44 * N + 3 * K * s * V + 4 * N + 52 * V
+    if stage == "blend_forward":
+        return 8 * T + 40 * c["I_f"] + P * (3 * e + 4)
+    if stage == "blend_backward":
+        return 8 * T + P * (6 * e + 4) + 40 * c["I_b"] + 44 * c["I_b"]
+    if stage == "preprocess_backward":
+        return 48 * N + V * (3 * K * s + 44) + 2 * V * (40 + 12 * K)
+    if stage == "adam":
+        return (11 * 28 + 48 * 24) * N if s == 2 else 28 * 59 * N
+    if stage == "l1":
+        return 4 * 3 * P * e          # read pred, target; read-modify-write grad, loss
+    if stage == "fused_ssim":
+        return 3 * 3 * P * e
+    if stage == "depth_sort":
+        return 8 * V + 8 * V + 8 * V   # read keys/values once, write one permutation
+    if stage == "emit_instances":
+        return 44 * V + 12 * I
+    if stage == "tile_sort":
+        return 24 * I + 8 * I + 8 * T
+    return 0
+
+
+def cpu_baseline(scene_fn):
+    from oracle import oracle as O
+    scene = scene_fn()
+    lr = {"means": 1.6e-4, "scene_scale": 1.0, "opacities": 5e-2, "rotations": 1e-3, "scales": 5e-3, "shs": 5e-3}
+    O.lib()
+    t0 = time.perf_counter()
+    O.run_iteration(scene, 0.8, 0.2, lr=lr, eps=1e-15)
+    dt = time.perf_counter() - t0
+    return dt * 1e3
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--config", type=int, default=3)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+
+    if args.gpus != 1:
+        print(f"bench.py runs on exactly one GPU (got --gpus {args.gpus}); multi-GPU sharding of this path "
+              "is a design in DESIGN.md, not a measured configuration", file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+
+    from tinygs_amd import _lib, scenes
+    from tinygs_amd.train import TrainStep
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        sys.exit(1)
+
+    scene_fn = {1: scenes.config1, 2: scenes.config2, 3: scenes.config3}[args.config]
+    t0 = time.time()
+    scene = scene_fn()
+    print(f"[bench] scene config{args.config}: N={scene.n} {scene.camera.width}x{scene.camera.height} "
+          f"sh_degree={scene.sh_degree} sh_storage={scene.sh_dtype} (generated in {time.time() - t0:.1f}s)",
+          file=sys.stderr, flush=True)
+    ts = TrainStep(scene, l1_weight=0.8, ssim_weight=0.2, eps=1e-15, shs_lr=5e-3)
+    L = _lib.load()
+    stream = torch.cuda.current_stream()
+
+    for _ in range(args.warmup):
+        ts.step()
+    torch.cuda.synchronize()
+
+    # stage events during the timed region (one event pair per stage per step)
+    L.tgs_profiling_set((1 << len(STAGES)) - 1)
+    for k in range(len(STAGES)):
+        L.tgs_profiling_read(k, None, None, 1)
+    import ctypes as C
+    _lib.check(L.tgs_rasterizer_work_stats(ts.rasterizer._h, None, None, 1))
+
+    start = torch.cuda.Event(enable_timing=True)
+    stop = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record(stream)
+    for _ in range(args.steps):
+        ts.step()
+    stop.record(stream)
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(stop) / args.steps
+
+    L.tgs_profiling_set(0)
+    stage_ms = {}
+    for k, name in enumerate(STAGES):
+        tot, cnt = C.c_double(), C.c_int64()
+        _lib.check(L.tgs_profiling_read(k, C.byref(tot), C.byref(cnt), 1))
+        stage_ms[name] = (tot.value / cnt.value) if cnt.value else 0.0
+    fl, bp = C.c_int64(), C.c_int64()
+    _lib.check(L.tgs_rasterizer_work_stats(ts.rasterizer._h, C.byref(fl), C.byref(bp), 1))
+    V, I, T = ts.rasterizer.counts()
+    cam = scene.camera
+    counts = {"N": scene.n, "V": V, "I": I, "T": T, "P": cam.width * cam.height,
+              "I_f": fl.value / args.steps, "I_b": bp.value / args.steps,
+              "sh_bytes": 2 if scene.sh_dtype == "float16" else 4, "sh_bases": (scene.sh_degree + 1) ** 2}
+
+    print(f"[bench] {ms:.3f} ms/iter over {args.steps} steps; V={V} I={I} T={T} "
+          f"I_f={counts['I_f']:.0f} I_b={counts['I_b']:.0f}", file=sys.stderr)
+    print(f"[bench] {'stage':22s} {'ms':>8s} {'GB/s':>8s} {'%HBM':>6s}", file=sys.stderr)
+    rows = []
+    for name in STAGES:
+        t = stage_ms[name]
+        b = algorithmic_bytes(name, counts)
+        gbs = b / (t * 1e-3) / 1e9 if t > 0 else 0.0
+        rows.append((name, t, b, gbs))
+        print(f"[bench] {name:22s} {t:8.4f} {gbs:8.1f} {100 * gbs / HBM_PEAK_GBS:6.1f}", file=sys.stderr)
+    print(f"[bench] sum of stages {sum(r[1] for r in rows):.3f} ms", file=sys.stderr, flush=True)
+
+    dom = max((r for r in rows if r[0] in SINGLE_KERNEL), key=lambda r: r[1])
+    roofline = {"bound": "hbm", "kernel": dom[0], "achieved": round(dom[3], 2), "peak": HBM_PEAK_GBS,
+                "unit": "GB/s", "frac": round(dom[3] / HBM_PEAK_GBS, 4), "traffic": None,
+                "algorithmic_bytes": int(dom[2]), "avg_launch_ms": round(dom[1], 5)}
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        print("[bench] cpu baseline: one full iteration of the CPU oracle on the same scene, 1 thread",
+              file=sys.stderr, flush=True)
+        cpu_ms = cpu_baseline(scene_fn)
+        cpu = {"value": round(cpu_ms, 1), "unit": "ms/iter", "cores": 1, "kind": "port",
+               "sample": f"one full config{args.config} iteration (preprocess, bin, blend fwd, L1+SSIM, blend bwd, "
+                         "preprocess bwd, SimpleAdam) of the scalar C oracle, single thread, same seeded scene"}
+        print(f"[bench] cpu baseline {cpu_ms:.0f} ms/iter ({cpu_ms / ms:.0f}x the GPU)", file=sys.stderr)
+
+    out = {
+        "metric": METRIC, "value": round(ms, 4), "unit": "ms/iter", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": False, "scaling": "weak",
+        "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+        "config": {"workload": f"config{args.config}: fwd + 0.8 L1 + 0.2 (1-SSIM) + bwd + SimpleAdam",
+                   "n_gaussians": scene.n, "width": cam.width, "height": cam.height, "sh_degree": scene.sh_degree,
+                   "sh_storage": scene.sh_dtype, "n_visible": V, "n_instances": I, "n_tiles": T,
+                   "parallelism": "single GPU"},
+        "stages_ms": {r[0]: round(r[1], 5) for r in rows},
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -157,6 +157,19 @@ int64_t tgs_adam_global_steps(tgs_adam* a);
  * means, opacities, rotations, scales, sh0, sh_rest. */
 int tgs_adam_moments(tgs_adam* a, int32_t group, float** first, float** second);
 
+/* ---- measurement (no counterpart in the reference, which uses NVTX ranges,
+ * tinygs/src/rasterizer/fastgs_ours/nvtx_gs.h): HIP events recorded on the
+ * launch stream around the selected stages; stage ids 0..9 = preprocess,
+ * depth_sort, emit_instances, tile_sort, blend_forward, l1, fused_ssim,
+ * blend_backward, preprocess_backward, adam. Process-wide, one host thread. */
+int tgs_profiling_set(uint32_t stage_mask);
+int tgs_profiling_read(int32_t stage, double* total_ms, int64_t* count, int32_t reset);
+const char* tgs_stage_name(int32_t stage);
+/* Work counters accumulated over forwards / backwards: Gaussians staged by
+ * the blend forward (summed over tiles) and Gaussians processed by the blend
+ * backward (sum over tiles of min(list length, tile max contributor)). */
+int tgs_rasterizer_work_stats(tgs_rasterizer* r, int64_t* fwd_loaded, int64_t* bwd_processed, int32_t reset);
+
 /* ---- self tests (device): deterministic exp/log over arrays, wave primitives. */
 int tgs_selftest_detmath(int32_t op, const float* in, float* out, int64_t n, void* stream);
 int tgs_selftest_wave(const uint32_t* in, uint32_t* out, void* stream);

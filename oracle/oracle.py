@@ -74,7 +74,7 @@ def _declare(L):
         fn.argtypes = [C.c_int, C.c_int, rp, rp, C.c_void_p, C.c_void_p, R]
         fn.restype = None
         fn = getattr(L, pfx + "adam")
-        fn.argtypes = [C.c_int64, rp, rp, rp, rp, R, R, R, R, R, R, R, R, C.c_int, C.c_int, R]
+        fn.argtypes = [C.c_int64, rp, rp, rp, rp, R, R, R, R, R, R, R, R, C.c_int, C.c_int, R, C.c_int]
         fn.restype = None
     for name, argt in (("orc_expf_array", [C.c_int64, f32p, f32p]),
                        ("orc_logf_array", [C.c_int64, f32p, f32p]),
@@ -123,7 +123,7 @@ def round_half(x):
 def cam_array(camera, prec="f"):
     a = camera.as_array().astype(np.float64)
     if prec == "d":
-        a[6:18] = camera.w2c[:3, :].reshape(-1)
+        a[6:18] = camera.w2c[:3, :].astype(np.float32).reshape(-1)
         a[18:21] = camera.cam_pos
     return np.ascontiguousarray(a, dtype=_dt(prec))
 
@@ -283,16 +283,18 @@ def bias_corrections(step, beta1=0.9, beta2=0.999):
 
 
 def adam_step(theta, grads, m1, m2, lr, step, grad_scale=1.0, beta1=0.9, beta2=0.999, eps=1e-15,
-              max_grad=1.0, decay=None):
-    """In-place SimpleAdam step over the six groups (dicts of flat float32 arrays)."""
+              max_grad=1.0, decay=None, sh_half=False):
+    """In-place SimpleAdam step over the six groups (dicts of flat float32 arrays).
+    sh_half: SH groups are stored as fp16 (results rounded to fp16)."""
     L = lib()
     bc1, bc2 = bias_corrections(step, beta1, beta2)
     lrs = adam_lrs(lr)
     decay = decay or {}
     for name, _, form, kind in ADAM_GROUPS:
+        half = int(sh_half and name in ("sh0", "sh_rest"))
         L.orc_f_adam(theta[name].size, theta[name], np.ascontiguousarray(grads[name], np.float32), m1[name], m2[name],
                      lrs[name], beta1, beta2, eps, grad_scale, bc1, bc2, max_grad, form, kind,
-                     float(decay.get(name, 0.0)))
+                     float(decay.get(name, 0.0)), half)
 
 
 def render(scene, prec="f", with_ckpt=True):
@@ -322,6 +324,7 @@ def run_iteration(scene, l1_w=0.8, ssim_w=0.2, grad_scaler=1.0, lr=None, step=1,
         st = adam_state or {k: (np.zeros_like(v), np.zeros_like(v)) for k, v in theta.items()}
         m1 = {k: v[0] for k, v in st.items()}
         m2 = {k: v[1] for k, v in st.items()}
-        adam_step(theta, grads, m1, m2, lr, step, grad_scale=1.0 / grad_scaler, eps=eps, max_grad=max_grad)
+        adam_step(theta, grads, m1, m2, lr, step, grad_scale=1.0 / grad_scaler, eps=eps, max_grad=max_grad,
+                  sh_half=getattr(scene, "sh_dtype", "float32") == "float16")
         out["theta"], out["m1"], out["m2"] = theta, m1, m2
     return out

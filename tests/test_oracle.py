@@ -490,7 +490,7 @@ def test_adam_closed_form(orc):
     lr, b1, b2, eps, clip = np.float32(1e-2), 0.9, 0.999, 1e-15, 1.0
     for step in (1, 2, 3):
         bc1, bc2 = orc.bias_corrections(step, b1, b2)
-        orc.lib().orc_f_adam(n, theta, grad, m1, m2, lr, b1, b2, eps, 1.0, bc1, bc2, clip, 0, 0, 0.0)
+        orc.lib().orc_f_adam(n, theta, grad, m1, m2, lr, b1, b2, eps, 1.0, bc1, bc2, clip, 0, 0, 0.0, 0)
     # double-precision Kingma & Ba with clipped gradient, same gradient each step
     g = np.clip(grad.astype(np.float64), -clip, clip)
     m = np.zeros(n)

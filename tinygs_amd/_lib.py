@@ -80,6 +80,10 @@ SIGNATURES = {
     "tgs_adam_reset": ([P, P], C.c_int),
     "tgs_adam_global_steps": ([P], C.c_int64),
     "tgs_adam_moments": ([P, C.c_int32, C.POINTER(C.c_void_p), C.POINTER(C.c_void_p)], C.c_int),
+    "tgs_profiling_set": ([C.c_uint32], C.c_int),
+    "tgs_profiling_read": ([C.c_int32, C.POINTER(C.c_double), C.POINTER(C.c_int64), C.c_int32], C.c_int),
+    "tgs_stage_name": ([C.c_int32], C.c_char_p),
+    "tgs_rasterizer_work_stats": ([P, C.POINTER(C.c_int64), C.POINTER(C.c_int64), C.c_int32], C.c_int),
     "tgs_selftest_detmath": ([C.c_int32, P, P, C.c_int64, P], C.c_int),
     "tgs_selftest_wave": ([P, P, P], C.c_int),
 }

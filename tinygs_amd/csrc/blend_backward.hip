@@ -33,7 +33,7 @@ __global__ void __launch_bounds__(256) blend_backward_kernel(
     CamParams cam, const uint2* __restrict__ ranges, const uint32_t* __restrict__ inst_vals,
     const float2* __restrict__ mean2d, const float4* __restrict__ conic_opacity, const float4* __restrict__ color_pt,
     const float* __restrict__ image, const float* __restrict__ grad_image, const uint32_t* __restrict__ n_contrib,
-    const uint32_t* __restrict__ tile_max, float* __restrict__ grad2d) {
+    const uint32_t* __restrict__ tile_max, float* __restrict__ grad2d, unsigned long long* __restrict__ stats) {
     __shared__ float4 s_a[kBwdBatch];   // mx, my, a/2, b
     __shared__ float4 s_b[kBwdBatch];   // c/2, opacity, a, c
     __shared__ float4 s_c[kBwdBatch];   // clamped colour, colour >= 0 mask bits
@@ -46,6 +46,7 @@ __global__ void __launch_bounds__(256) blend_backward_kernel(
     const int32_t len = (int32_t)(range.y - range.x);
     const int32_t nproc = min(len, (int32_t)tile_max[tile]);
     if (nproc <= 0) return;
+    if (stats && threadIdx.x == 0) atomicAdd(stats, (unsigned long long)nproc);
 
     const uint32_t gx = tile % cam.grid_w, gy = tile / cam.grid_w;
     const uint32_t tid = threadIdx.x, w = tid >> 6, lane = tid & 63u;
@@ -177,11 +178,11 @@ __global__ void __launch_bounds__(256) blend_backward_kernel(
 void launch_blend_backward(const CamParams& cam, const uint2* ranges, const uint32_t* inst_vals, const float2* mean2d,
                            const float4* conic_opacity, const float4* color_pt, const float* image,
                            const float* grad_image, const uint32_t* n_contrib, const uint32_t* tile_max, float* grad2d,
-                           hipStream_t s) {
+                           unsigned long long* stats, hipStream_t s) {
     const uint32_t n_tiles = cam.grid_w * cam.grid_h;
     if (n_tiles == 0) return;
     blend_backward_kernel<<<n_tiles, 256, 0, s>>>(cam, ranges, inst_vals, mean2d, conic_opacity, color_pt, image,
-                                                  grad_image, n_contrib, tile_max, grad2d);
+                                                  grad_image, n_contrib, tile_max, grad2d, stats);
 }
 
 }  // namespace tgs

@@ -21,12 +21,6 @@
 
 namespace tgs {
 
-struct alignas(16) BlendRec {
-    float mx, my, ha, b;   // mean, a/2, b
-    float hc, o, pad0, pad1;
-    float r, g, bl, pad2;  // colour clamped at 0
-};
-
 __global__ void __launch_bounds__(256) blend_forward_kernel(CamParams cam, const uint2* __restrict__ ranges,
                                                             const uint32_t* __restrict__ inst_vals,
                                                             const float2* __restrict__ mean2d,
@@ -34,7 +28,8 @@ __global__ void __launch_bounds__(256) blend_forward_kernel(CamParams cam, const
                                                             const float4* __restrict__ color_pt,
                                                             float* __restrict__ image,
                                                             uint32_t* __restrict__ n_contrib,
-                                                            uint32_t* __restrict__ tile_max) {
+                                                            uint32_t* __restrict__ tile_max,
+                                                            unsigned long long* __restrict__ stats) {
     __shared__ float4 s_a[256];   // mx, my, a/2, b
     __shared__ float2 s_b[256];   // c/2, opacity
     __shared__ float4 s_c[256];   // r, g, b (clamped), unused
@@ -53,6 +48,7 @@ __global__ void __launch_bounds__(256) blend_forward_kernel(CamParams cam, const
 
     float C0 = 0.f, C1 = 0.f, C2 = 0.f, T = 1.f;
     uint32_t ncontrib = 0;
+    uint32_t loaded = 0;
     bool done = !inside;
 
     for (int32_t base = 0; base < len; base += 256) {
@@ -69,6 +65,7 @@ __global__ void __launch_bounds__(256) blend_forward_kernel(CamParams cam, const
         }
         __syncthreads();
         const int32_t nb = min(256, len - base);
+        loaded += (uint32_t)nb;
         for (int32_t k = 0; k < nb; ++k) {
             if (!__any(!done)) break;   // whole wave finished
             if (done) continue;
@@ -107,16 +104,19 @@ __global__ void __launch_bounds__(256) blend_forward_kernel(CamParams cam, const
     const uint32_t wmax = wave_max_u32(ncontrib);
     if (lane == 0) s_max[w] = wmax;
     __syncthreads();
-    if (tid == 0) tile_max[tile] = max(max(s_max[0], s_max[1]), max(s_max[2], s_max[3]));
+    if (tid == 0) {
+        tile_max[tile] = max(max(s_max[0], s_max[1]), max(s_max[2], s_max[3]));
+        if (stats && loaded) atomicAdd(stats, (unsigned long long)loaded);
+    }
 }
 
 void launch_blend_forward(const CamParams& cam, const uint2* ranges, const uint32_t* inst_vals, const float2* mean2d,
                           const float4* conic_opacity, const float4* color_pt, float* image, uint32_t* n_contrib,
-                          uint32_t* tile_max, hipStream_t s) {
+                          uint32_t* tile_max, unsigned long long* stats, hipStream_t s) {
     const uint32_t n_tiles = cam.grid_w * cam.grid_h;
     if (n_tiles == 0) return;
     blend_forward_kernel<<<n_tiles, 256, 0, s>>>(cam, ranges, inst_vals, mean2d, conic_opacity, color_pt, image,
-                                                 n_contrib, tile_max);
+                                                 n_contrib, tile_max, stats);
 }
 
 }  // namespace tgs

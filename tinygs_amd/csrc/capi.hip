@@ -16,6 +16,7 @@
 #include <string.h>
 
 #include <string>
+#include <vector>
 
 #include "../../include/tinygs_amd.h"
 #include "common.h"
@@ -85,6 +86,47 @@ void release(DevBuf& b) {
         int rc_ = (expr);              \
         if (rc_ != TGS_OK) return rc_; \
     } while (0)
+
+// ---- stage timing: HIP events recorded on the launch stream around the
+// stages selected by tgs_profiling_set (process-wide, single host thread).
+constexpr int kStageCount = 10;
+const char* const kStageNames[kStageCount] = {
+    "preprocess", "depth_sort", "emit_instances", "tile_sort", "blend_forward",
+    "l1", "fused_ssim", "blend_backward", "preprocess_backward", "adam"};
+enum { ST_PRE = 0, ST_DEPTH, ST_EMIT, ST_TILES, ST_BLENDF, ST_L1, ST_SSIM, ST_BLENDB, ST_PREB, ST_ADAM };
+
+struct EventPair {
+    hipEvent_t a, b;
+};
+struct Profiler {
+    uint32_t mask = 0;
+    std::vector<EventPair> pending[kStageCount];
+    std::vector<EventPair> pool;
+    double total_ms[kStageCount] = {};
+    int64_t count[kStageCount] = {};
+};
+Profiler g_prof;
+
+struct StageScope {
+    int st;
+    hipStream_t s;
+    bool on = false;
+    EventPair p{};
+    StageScope(int stage, hipStream_t stream) : st(stage), s(stream) {
+        if (!(g_prof.mask & (1u << stage))) return;
+        if (!g_prof.pool.empty()) {
+            p = g_prof.pool.back();
+            g_prof.pool.pop_back();
+        } else if (hipEventCreate(&p.a) != hipSuccess || hipEventCreate(&p.b) != hipSuccess) {
+            return;
+        }
+        on = hipEventRecord(p.a, s) == hipSuccess;
+    }
+    ~StageScope() {
+        if (!on) return;
+        if (hipEventRecord(p.b, s) == hipSuccess) g_prof.pending[st].push_back(p);
+    }
+};
 
 int build_camera(const tgs_camera* c, CamParams& cp) {
     if (!c) return fail(TGS_ERR_INVALID, "camera is NULL");
@@ -175,7 +217,7 @@ struct tgs_rasterizer {
     DevBuf ranges, tile_max, n_contrib;
     // temp
     DevBuf scan_tmp, radix_tmp, grad2d;
-    DevBuf counters;
+    DevBuf counters;    // [0] V, [1] I (u32); [8..9] u64 work counters at byte 32
     uint32_t* h_counters = nullptr;
     // state of the last forward
     bool fwd_done = false;
@@ -213,9 +255,16 @@ int tgs_rasterizer_create(const char* type, tgs_rasterizer** out) {
     if (t != "fastgs") return fail(TGS_ERR_UNSUPPORTED, "Unknown rasterizer type: %s", type ? type : "(null)");
     tgs_rasterizer* r = new tgs_rasterizer();
     hipError_t e = hipHostMalloc((void**)&r->h_counters, 64, hipHostMallocDefault);
+    if (e == hipSuccess) e = hipMalloc(&r->counters.p, 64);
+    if (e == hipSuccess) {
+        r->counters.bytes = 64;
+        e = hipMemset(r->counters.p, 0, 64);
+    }
     if (e != hipSuccess) {
+        if (r->h_counters) (void)hipHostFree(r->h_counters);
+        release(r->counters);
         delete r;
-        return fail(TGS_ERR_HIP, "hipHostMalloc: %s", hipGetErrorString(e));
+        return fail(TGS_ERR_HIP, "counter allocation: %s", hipGetErrorString(e));
     }
     *out = r;
     return TGS_OK;
@@ -288,14 +337,17 @@ int tgs_rasterizer_forward(tgs_rasterizer* r, const tgs_camera* camera, void* im
     TGS_TRY(ensure(r->n_contrib, 4 * cs, s));
     TGS_TRY(ensure(r->scan_tmp, scan_temp_bytes(nn), s));
     TGS_TRY(ensure(r->radix_tmp, radix_temp_bytes(nn), s));
-    TGS_TRY(ensure(r->counters, 64, s));
 
     GaussianView gv = view_of(r->g);
     uint32_t* d_cnt = r->counters.as<uint32_t>();
-    launch_preprocess(gv, cam, r->n_touched.as<uint32_t>(), r->bounds.as<uint2>(), r->mean2d.as<float2>(),
-                      r->conic_opacity.as<float4>(), r->color.as<float4>(), r->depth_key.as<uint32_t>(),
-                      (float*)densification_info, s);
+    {
+        StageScope sc(ST_PRE, s);
+        launch_preprocess(gv, cam, r->n_touched.as<uint32_t>(), r->bounds.as<uint2>(), r->mean2d.as<float2>(),
+                          r->conic_opacity.as<float4>(), r->color.as<float4>(), r->depth_key.as<uint32_t>(),
+                          (float*)densification_info, s);
+    }
     TGS_CHECK_LAUNCH();
+    StageScope* depth_scope = new StageScope(ST_DEPTH, s);
     launch_compact_visible(r->n_touched.as<uint32_t>(), r->depth_key.as<uint32_t>(), n, r->pkeys[0].as<uint32_t>(),
                            r->pvals[0].as<uint32_t>(), d_cnt + 0, r->scan_tmp.as<uint32_t>(), s);
     uint32_t* pk[2] = {r->pkeys[0].as<uint32_t>(), r->pkeys[1].as<uint32_t>()};
@@ -303,6 +355,7 @@ int tgs_rasterizer_forward(tgs_rasterizer* r, const tgs_camera* camera, void* im
     const int psel = radix_sort_pairs(pk, pv, d_cnt + 0, n, 32, r->radix_tmp.as<uint32_t>(), s);
     launch_instance_offsets(r->n_touched.as<uint32_t>(), pv[psel], d_cnt + 0, n, r->offsets.as<uint32_t>(), d_cnt + 1,
                             r->scan_tmp.as<uint32_t>(), s);
+    delete depth_scope;
     TGS_CHECK_LAUNCH();
     TGS_HIP(hipMemcpyAsync(r->h_counters, d_cnt, 2 * sizeof(uint32_t), hipMemcpyDeviceToHost, s));
     TGS_HIP(hipStreamSynchronize(s));
@@ -314,18 +367,30 @@ int tgs_rasterizer_forward(tgs_rasterizer* r, const tgs_camera* camera, void* im
         TGS_TRY(ensure(r->ivals[k], 4 * ii, s));
     }
     TGS_TRY(ensure(r->radix_tmp, radix_temp_bytes(ii > nn ? ii : nn), s));
-    launch_emit_instances(r->n_touched.as<uint32_t>(), pv[psel], r->offsets.as<uint32_t>(), d_cnt + 0, n, r->bounds.as<uint2>(),
-                          r->mean2d.as<float2>(), r->conic_opacity.as<float4>(), r->color.as<float4>(), cam.grid_w,
-                          r->ikeys[0].as<uint32_t>(), r->ivals[0].as<uint32_t>(), s);
+    {
+        StageScope sc(ST_EMIT, s);
+        launch_emit_instances(r->n_touched.as<uint32_t>(), pv[psel], r->offsets.as<uint32_t>(), d_cnt + 0, n,
+                              r->bounds.as<uint2>(), r->mean2d.as<float2>(), r->conic_opacity.as<float4>(),
+                              r->color.as<float4>(), cam.grid_w, r->ikeys[0].as<uint32_t>(),
+                              r->ivals[0].as<uint32_t>(), s);
+    }
     int bits = 1;
     while ((1u << bits) < T) ++bits;
     uint32_t* ik[2] = {r->ikeys[0].as<uint32_t>(), r->ikeys[1].as<uint32_t>()};
     uint32_t* iv[2] = {r->ivals[0].as<uint32_t>(), r->ivals[1].as<uint32_t>()};
-    const int isel = radix_sort_pairs(ik, iv, nullptr, I, bits, r->radix_tmp.as<uint32_t>(), s);
-    launch_tile_ranges(ik[isel], I, r->ranges.as<uint2>(), T, s);
-    launch_blend_forward(cam, r->ranges.as<uint2>(), iv[isel], r->mean2d.as<float2>(), r->conic_opacity.as<float4>(),
-                         r->color.as<float4>(), (float*)image, r->n_contrib.as<uint32_t>(), r->tile_max.as<uint32_t>(),
-                         s);
+    int isel;
+    {
+        StageScope sc(ST_TILES, s);
+        isel = radix_sort_pairs(ik, iv, nullptr, I, bits, r->radix_tmp.as<uint32_t>(), s);
+        launch_tile_ranges(ik[isel], I, r->ranges.as<uint2>(), T, s);
+    }
+    {
+        StageScope sc(ST_BLENDF, s);
+        launch_blend_forward(cam, r->ranges.as<uint2>(), iv[isel], r->mean2d.as<float2>(),
+                             r->conic_opacity.as<float4>(), r->color.as<float4>(), (float*)image,
+                             r->n_contrib.as<uint32_t>(), r->tile_max.as<uint32_t>(),
+                             (unsigned long long*)(r->counters.as<char>() + 32), s);
+    }
     TGS_CHECK_LAUNCH();
     r->cam = cam;
     r->n = n;
@@ -351,15 +416,21 @@ int tgs_rasterizer_backward(tgs_rasterizer* r, const void* grad_image, const voi
     TGS_TRY(ensure(r->grad2d, sizeof(float) * kGradStride * (size_t)(n > 0 ? n : 1), s));
     launch_fill_u32(r->grad2d.as<uint32_t>(), 0u, (int64_t)kGradStride * n, s);
     const CamParams& cam = r->cam;
-    launch_blend_backward(cam, r->ranges.as<uint2>(), r->ivals[r->isel].as<uint32_t>(), r->mean2d.as<float2>(),
-                          r->conic_opacity.as<float4>(), r->color.as<float4>(), (const float*)image,
-                          (const float*)grad_image, r->n_contrib.as<uint32_t>(), r->tile_max.as<uint32_t>(),
-                          r->grad2d.as<float>(), s);
+    {
+        StageScope sc(ST_BLENDB, s);
+        launch_blend_backward(cam, r->ranges.as<uint2>(), r->ivals[r->isel].as<uint32_t>(), r->mean2d.as<float2>(),
+                              r->conic_opacity.as<float4>(), r->color.as<float4>(), (const float*)image,
+                              (const float*)grad_image, r->n_contrib.as<uint32_t>(), r->tile_max.as<uint32_t>(),
+                              r->grad2d.as<float>(), (unsigned long long*)(r->counters.as<char>() + 40), s);
+    }
     TGS_CHECK_LAUNCH();
     GradView gv{(float*)grads->means, (float*)grads->scales, (float*)grads->rotations, (float*)grads->opacities,
                 (float*)grads->sh0, (float*)grads->sh_rest};
-    launch_preprocess_backward(view_of(r->g), cam, r->n_touched.as<uint32_t>(), r->conic_opacity.as<float4>(),
-                               r->grad2d.as<float>(), gv, (float*)densification_info, s);
+    {
+        StageScope sc(ST_PREB, s);
+        launch_preprocess_backward(view_of(r->g), cam, r->n_touched.as<uint32_t>(), r->conic_opacity.as<float4>(),
+                                   r->grad2d.as<float>(), gv, (float*)densification_info, s);
+    }
     TGS_CHECK_LAUNCH();
     return TGS_OK;
 }
@@ -435,6 +506,7 @@ int tgs_loss_evaluate(tgs_loss* l, const tgs_loss_context* c, float scale, void*
     if (l->type == 0) {
         // l1.cu:117-121: scale / (W * H * C)
         const int npix = (int)(c->width * c->height * c->channel);
+        StageScope sc(ST_L1, s);
         launch_l1((const float*)c->pred, (const float*)c->target, (float*)c->loss, (float*)c->grad, padded,
                   scale / (float)npix, s);
         TGS_CHECK_LAUNCH();
@@ -444,6 +516,7 @@ int tgs_loss_evaluate(tgs_loss* l, const tgs_loss_context* c, float scale, void*
     // fused_ssim.cu:811: scale / (H * W)
     const float actual = scale / (float)(int)(c->height * c->width);
     const float C1 = 0.01f * 0.01f, C2 = 0.03f * 0.03f;
+    StageScope sc(ST_SSIM, s);
     if (c->grad) {
         for (auto& b : l->dm) TGS_TRY(ensure(b, sizeof(float) * (size_t)padded, s));
         launch_ssim_forward(c->width, c->height, C1, C2, actual, (const float*)c->pred, (const float*)c->target,
@@ -591,7 +664,10 @@ int tgs_adam_step(tgs_adam* a, float scale, void* stream) {
         g.decay_kind = (k == 1) ? 1 : (k == 3 ? 2 : 0);
         g.decay_coef = (k == 1) ? a->p.opacities_l1 * g_scale : (k == 3 ? a->p.scales_l1 * g_scale : 0.0f);
     }
-    launch_adam(args, (hipStream_t)stream);
+    {
+        StageScope sc(ST_ADAM, (hipStream_t)stream);
+        launch_adam(args, (hipStream_t)stream);
+    }
     TGS_CHECK_LAUNCH();
     return TGS_OK;
 }
@@ -613,6 +689,48 @@ int tgs_adam_moments(tgs_adam* a, int32_t group, float** first, float** second) 
     if (!a || group < 0 || group >= 6) return fail(TGS_ERR_INVALID, "bad group");
     if (first) *first = a->m1[group].as<float>();
     if (second) *second = a->m2[group].as<float>();
+    return TGS_OK;
+}
+
+// ------------------------------------------------------------------ measurement
+
+int tgs_profiling_set(uint32_t stage_mask) {
+    g_prof.mask = stage_mask;
+    return TGS_OK;
+}
+
+int tgs_profiling_read(int32_t stage, double* total_ms, int64_t* count, int32_t reset) {
+    if (stage < 0 || stage >= kStageCount) return fail(TGS_ERR_INVALID, "bad stage %d", stage);
+    for (EventPair& p : g_prof.pending[stage]) {
+        float ms = 0.f;
+        TGS_HIP(hipEventSynchronize(p.b));
+        TGS_HIP(hipEventElapsedTime(&ms, p.a, p.b));
+        g_prof.total_ms[stage] += ms;
+        g_prof.count[stage] += 1;
+        g_prof.pool.push_back(p);
+    }
+    g_prof.pending[stage].clear();
+    if (total_ms) *total_ms = g_prof.total_ms[stage];
+    if (count) *count = g_prof.count[stage];
+    if (reset) {
+        g_prof.total_ms[stage] = 0.0;
+        g_prof.count[stage] = 0;
+    }
+    return TGS_OK;
+}
+
+const char* tgs_stage_name(int32_t stage) {
+    return (stage >= 0 && stage < kStageCount) ? kStageNames[stage] : "";
+}
+
+int tgs_rasterizer_work_stats(tgs_rasterizer* r, int64_t* fwd_loaded, int64_t* bwd_processed, int32_t reset) {
+    if (!r) return fail(TGS_ERR_INVALID, "rasterizer is NULL");
+    unsigned long long h[2] = {0, 0};
+    TGS_HIP(hipDeviceSynchronize());
+    TGS_HIP(hipMemcpy(h, r->counters.as<char>() + 32, sizeof(h), hipMemcpyDeviceToHost));
+    if (fwd_loaded) *fwd_loaded = (int64_t)h[0];
+    if (bwd_processed) *bwd_processed = (int64_t)h[1];
+    if (reset) TGS_HIP(hipMemset(r->counters.as<char>() + 32, 0, sizeof(h)));
     return TGS_OK;
 }
 

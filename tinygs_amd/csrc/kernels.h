@@ -59,11 +59,11 @@ void launch_tile_ranges(const uint32_t* inst_keys, int64_t n_inst, uint2* ranges
 // ---- blend (kernels_forward.cuh:569-715, kernels_backward.cuh:675-927)
 void launch_blend_forward(const CamParams& cam, const uint2* ranges, const uint32_t* inst_vals, const float2* mean2d,
                           const float4* conic_opacity, const float4* color_pt, float* image, uint32_t* n_contrib,
-                          uint32_t* tile_max, hipStream_t s);
+                          uint32_t* tile_max, unsigned long long* stats, hipStream_t s);
 void launch_blend_backward(const CamParams& cam, const uint2* ranges, const uint32_t* inst_vals,
                            const float2* mean2d, const float4* conic_opacity, const float4* color_pt,
                            const float* image, const float* grad_image, const uint32_t* n_contrib,
-                           const uint32_t* tile_max, float* grad2d, hipStream_t s);
+                           const uint32_t* tile_max, float* grad2d, unsigned long long* stats, hipStream_t s);
 
 // ---- preprocess backward (kernels_backward.cuh:88-352)
 void launch_preprocess_backward(const GaussianView& g, const CamParams& cam, const uint32_t* n_touched,

@@ -43,8 +43,9 @@ class Camera:
 
     @property
     def cam_pos(self) -> np.ndarray:
-        """Camera centre = column 3 of inverse(w2c) (fastgs.cu:96,100)."""
-        return np.linalg.inv(self.w2c.astype(np.float64))[:3, 3]
+        """Camera centre = column 3 of inverse(w2c) (fastgs.cu:96,100), from the
+        float32 matrix the rasterizer receives, inverted in double."""
+        return np.linalg.inv(self.w2c.astype(np.float32).astype(np.float64))[:3, 3]
 
     @property
     def shape(self) -> ImageShape:
