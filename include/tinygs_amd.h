@@ -37,7 +37,8 @@ extern "C" {
  * (tinygs/include/tinygs/core/gpu_gaussian.hpp:9-73): means[3n], scales[3n]
  * (log), rotations[4n] (r,x,y,z), opacities[n] (logit), sh0[3n],
  * sh_rest[45n] (15 bases per Gaussian whatever the degree). sh_dtype applies
- * to sh0 and sh_rest of parameters; gradients are always float32. */
+ * to sh0 and sh_rest of parameters; gradients are always float32. Every array
+ * must be 16-byte aligned (hipMalloc and torch allocations are). */
 typedef struct tgs_gaussians {
     void* means;
     void* scales;

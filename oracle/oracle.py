@@ -136,7 +136,8 @@ def params(scene, prec="f", overrides=None):
     }
     if overrides:
         p.update(overrides)
-    return {k: np.ascontiguousarray(v, dtype=dt).reshape(-1) for k, v in p.items()}
+    # always copies: Adam updates these arrays in place and must not touch the scene
+    return {k: np.array(v, dtype=dt, copy=True).reshape(-1) for k, v in p.items()}
 
 
 def preprocess(scene, prec="f", prm=None, cam=None, max_radii=None):

@@ -39,6 +39,10 @@ def test_wave_primitives(hip):
     odd = (vals & 1) != 0
     assert o[67] == odd.sum()
     assert np.array_equal(o[128:192], np.concatenate([[0], np.cumsum(odd)[:-1]]).astype(np.uint32))
+    # transposed 12-value reduction (v_permlane32_swap / v_permlane16_swap + DPP)
+    red = o[192:204].view(np.float32)
+    for q in range(12):
+        assert red[q] == np.float32(vals.astype(np.float64).sum() + 64 * q), (q, red[q])
 
 
 @pytest.mark.parametrize("op", [0, 1, 2, 3, 4, 5])

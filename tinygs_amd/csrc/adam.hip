@@ -4,7 +4,7 @@
 // kernels, four of them through a float4 view that can read and write up to
 // three floats past the end of a vec3 array (:176,487); here a single launch
 // walks the groups with exact bounds, every access coalesced (lane-strided
-// dwords), 28 bytes of HBM traffic per fp32 scalar.
+// vectors), 28 bytes of HBM traffic per fp32 scalar.
 //
 // Per-group specifics kept: the lerp form (fma(t, g - m, m) for the groups the
 // reference runs through helper_math's float4 lerp, fma(t, g, fma(-t, m, m))
@@ -22,9 +22,36 @@ struct AdamLaunch {
 };
 
 constexpr int kAdamThreads = 256;
-constexpr int kAdamPerThread = 8;
-constexpr int kAdamChunk = kAdamThreads * kAdamPerThread;
+constexpr int kAdamVecPerThread = 2;                       // 4-element vectors per thread
+constexpr int kAdamChunk = kAdamThreads * kAdamVecPerThread * 4;
 
+__device__ __forceinline__ float adam_one(float th, float gr_raw, float& m, float& v, const AdamGroup& g,
+                                          const AdamArgs& a, float t1, float t2) {
+    float gr = a.grad_scale * gr_raw;
+    if (g.decay_coef != 0.0f) {
+        if (g.decay_kind == 1) {
+            const float o = 1.0f / (1.0f + det_expf(-th));
+            gr = __builtin_fmaf(g.decay_coef, o * (1.0f - o), gr);
+        } else if (g.decay_kind == 2) {
+            gr = __builtin_fmaf(g.decay_coef, det_expf(th), gr);
+        }
+    }
+    if (a.max_grad != 0.0f) gr = __builtin_copysignf(__builtin_fminf(__builtin_fabsf(gr), a.max_grad), gr);
+    const float gg = gr * gr;
+    if (g.lerp_form == 0) {
+        m = __builtin_fmaf(t1, gr - m, m);
+        v = __builtin_fmaf(t2, gg - v, v);
+    } else {
+        m = __builtin_fmaf(t1, gr, __builtin_fmaf(-t1, m, m));
+        v = __builtin_fmaf(t2, gg, __builtin_fmaf(-t2, v, v));
+    }
+    const float mh = m / a.bc1;
+    const float den = __builtin_sqrtf(v) / a.bc2_sqrt + a.eps;
+    return th - (mh * g.lr) / den;
+}
+
+// Each thread updates 4-element vectors with 16-byte loads/stores (8-byte for
+// fp16 theta); lanes of a wave cover consecutive vectors.
 __global__ void __launch_bounds__(kAdamThreads) adam_kernel(AdamLaunch L) {
     const int64_t b = blockIdx.x;
     int gi = 0;
@@ -32,41 +59,52 @@ __global__ void __launch_bounds__(kAdamThreads) adam_kernel(AdamLaunch L) {
     for (int k = 1; k < 6; ++k)
         if (k < L.a.n_groups && b >= L.block_start[k]) gi = k;
     const AdamGroup& g = L.a.groups[gi];
-    const int64_t base = (b - L.block_start[gi]) * kAdamChunk + threadIdx.x;
     const float t1 = 1.0f - L.a.beta1, t2 = 1.0f - L.a.beta2;
+    const int64_t vbase = (b - L.block_start[gi]) * (kAdamChunk / 4) + threadIdx.x;
 #pragma unroll
-    for (int k = 0; k < kAdamPerThread; ++k) {
-        const int64_t i = base + (int64_t)k * kAdamThreads;
-        if (i >= g.count) break;
-        float th = g.theta_half ? __half2float(((const __half*)g.theta)[i]) : ((const float*)g.theta)[i];
-        float gr = L.a.grad_scale * g.grad[i];
-        if (g.decay_coef != 0.0f) {
-            if (g.decay_kind == 1) {
-                const float o = 1.0f / (1.0f + det_expf(-th));
-                gr = __builtin_fmaf(g.decay_coef, o * (1.0f - o), gr);
-            } else if (g.decay_kind == 2) {
-                gr = __builtin_fmaf(g.decay_coef, det_expf(th), gr);
+    for (int k = 0; k < kAdamVecPerThread; ++k) {
+        const int64_t e0 = 4 * (vbase + (int64_t)k * kAdamThreads);
+        if (e0 >= g.count) break;
+        if (e0 + 3 < g.count) {
+            float th[4];
+            if (g.theta_half) {
+                const uint2 hv = *(const uint2*)((const __half*)g.theta + e0);
+                const __half* h = (const __half*)&hv;
+                for (int q = 0; q < 4; ++q) th[q] = __half2float(h[q]);
+            } else {
+                const float4 tv = *(const float4*)((const float*)g.theta + e0);
+                th[0] = tv.x; th[1] = tv.y; th[2] = tv.z; th[3] = tv.w;
+            }
+            const float4 gv = *(const float4*)(g.grad + e0);
+            float4 mv = *(const float4*)(g.m1 + e0);
+            float4 vv = *(const float4*)(g.m2 + e0);
+            th[0] = adam_one(th[0], gv.x, mv.x, vv.x, g, L.a, t1, t2);
+            th[1] = adam_one(th[1], gv.y, mv.y, vv.y, g, L.a, t1, t2);
+            th[2] = adam_one(th[2], gv.z, mv.z, vv.z, g, L.a, t1, t2);
+            th[3] = adam_one(th[3], gv.w, mv.w, vv.w, g, L.a, t1, t2);
+            if (g.theta_half) {
+                uint2 hv;
+                __half* h = (__half*)&hv;
+                for (int q = 0; q < 4; ++q) h[q] = __float2half_rn(th[q]);
+                *(uint2*)((__half*)g.theta + e0) = hv;
+            } else {
+                *(float4*)((float*)g.theta + e0) = make_float4(th[0], th[1], th[2], th[3]);
+            }
+            *(float4*)(g.m1 + e0) = mv;
+            *(float4*)(g.m2 + e0) = vv;
+        } else {
+            for (int64_t i = e0; i < g.count; ++i) {
+                float th = g.theta_half ? __half2float(((const __half*)g.theta)[i]) : ((const float*)g.theta)[i];
+                float m = g.m1[i], v = g.m2[i];
+                th = adam_one(th, g.grad[i], m, v, g, L.a, t1, t2);
+                if (g.theta_half)
+                    ((__half*)g.theta)[i] = __float2half_rn(th);
+                else
+                    ((float*)g.theta)[i] = th;
+                g.m1[i] = m;
+                g.m2[i] = v;
             }
         }
-        if (L.a.max_grad != 0.0f) gr = __builtin_copysignf(__builtin_fminf(__builtin_fabsf(gr), L.a.max_grad), gr);
-        float m = g.m1[i], v = g.m2[i];
-        const float gg = gr * gr;
-        if (g.lerp_form == 0) {
-            m = __builtin_fmaf(t1, gr - m, m);
-            v = __builtin_fmaf(t2, gg - v, v);
-        } else {
-            m = __builtin_fmaf(t1, gr, __builtin_fmaf(-t1, m, m));
-            v = __builtin_fmaf(t2, gg, __builtin_fmaf(-t2, v, v));
-        }
-        const float mh = m / L.a.bc1;
-        const float den = __builtin_sqrtf(v) / L.a.bc2_sqrt + L.a.eps;
-        th = th - (mh * g.lr) / den;
-        if (g.theta_half)
-            ((__half*)g.theta)[i] = __float2half_rn(th);
-        else
-            ((float*)g.theta)[i] = th;
-        g.m1[i] = m;
-        g.m2[i] = v;
     }
 }
 

@@ -15,8 +15,10 @@
 //     clamped at 0, no 1/255 test, state restarted at the bucket boundary),
 //     which keeps the reference's bucket semantics exactly.
 // Per-Gaussian gradient sums (11 values) are reduced across the wave with a
-// fixed DPP butterfly, the four waves' partials combined in LDS, and one
-// float atomic per value and tile is issued to the per-primitive record.
+// transposed reduction (gfx950 v_permlane32_swap / v_permlane16_swap, then a
+// DPP row butterfly; fixed order), the four waves' partials combined in LDS,
+// and one float atomic per value and tile is issued to the per-primitive
+// record.
 //
 // grad2d record (12 floats per primitive): [0,1] dL/dmean2d, [2,3] |.| sums
 // (absgrad), [4..6] dL/dconic (a, b, c), [7..9] dL/dcolour (masked by
@@ -116,7 +118,7 @@ __global__ void __launch_bounds__(256) blend_backward_kernel(
             // reference backward step (kernels_backward.cuh:839-902)
             const float ab = act ? __builtin_fminf(araw, kMaxAlpha) : 0.f;
             const float wgt = Tb * ab;
-            float v[kBwdVals];
+            float v[12];
             v[0] = wgt * g0;
             v[1] = wgt * g1;
             v[2] = wgt * g2;
@@ -139,11 +141,16 @@ __global__ void __launch_bounds__(256) blend_backward_kernel(
             v[8] = -gmy;
             v[9] = __builtin_fabsf(gmx);
             v[10] = __builtin_fabsf(gmy);
+            v[11] = 0.f;
             Tb *= oma;
-#pragma unroll
-            for (int q = 0; q < kBwdVals; ++q) {
-                const float sum = wave_sum_row3(v[q]);
-                if (lane == 63u) s_part[w][q][k] = sum;
+            float t[3];
+            wave_reduce12(v, t);
+            if ((lane & 15u) == 0u) {
+                const int row = (int)(lane >> 4);
+                const int q0 = kRowValue[row];
+                s_part[w][q0][k] = t[0];
+                s_part[w][4 + q0][k] = t[1];
+                if (8 + q0 < kBwdVals) s_part[w][8 + q0][k] = t[2];
             }
         }
         __syncthreads();

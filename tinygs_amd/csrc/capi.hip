@@ -197,6 +197,10 @@ int check_gaussians(const tgs_gaussians* g, bool is_grad) {
     if (g->n < 0 || g->n > (int64_t)0xffffffffll) return fail(TGS_ERR_INVALID, "invalid gaussian count %lld", (long long)g->n);
     if (g->n > 0 && (!g->means || !g->scales || !g->rotations || !g->opacities || !g->sh0 || !g->sh_rest))
         return fail(TGS_ERR_INVALID, "a gaussian SoA pointer is NULL");
+    // kernels move whole blocks of these arrays with 16-byte vector accesses
+    const uintptr_t al = (uintptr_t)g->means | (uintptr_t)g->scales | (uintptr_t)g->rotations |
+                         (uintptr_t)g->opacities | (uintptr_t)g->sh0 | (uintptr_t)g->sh_rest;
+    if (al & 15u) return fail(TGS_ERR_INVALID, "gaussian SoA arrays must be 16-byte aligned");
     if (!is_grad && (g->sh_degree < 0 || g->sh_degree > 3)) return fail(TGS_ERR_INVALID, "sh_degree %d", g->sh_degree);
     if (!is_grad && g->sh_dtype != TGS_DTYPE_FLOAT32 && g->sh_dtype != TGS_DTYPE_FLOAT16)
         return fail(TGS_ERR_INVALID, "sh_dtype %d", g->sh_dtype);

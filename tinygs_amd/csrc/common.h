@@ -107,6 +107,55 @@ __device__ __forceinline__ uint32_t wave_inclusive_scan_u32(uint32_t v) {
     return v;
 }
 
+// gfx950 cross-half swaps (v_permlane32_swap / v_permlane16_swap):
+//   swap32(a, b) -> (x, y) with x = [a.lanes 0-31, b.lanes 0-31],
+//                            y = [a.lanes 32-63, b.lanes 32-63];
+//   swap16(a, b) -> (x, y) with x = rows (a0, b0, a2, b2), y = (a1, b1, a3, b3)
+// (rows = 16-lane groups).
+__device__ __forceinline__ void swap32(float& a, float& b) {
+    auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, a), __builtin_bit_cast(uint32_t, b), false,
+                                              false);
+    a = __builtin_bit_cast(float, (uint32_t)r[0]);
+    b = __builtin_bit_cast(float, (uint32_t)r[1]);
+}
+__device__ __forceinline__ void swap16(float& a, float& b) {
+    auto r = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(uint32_t, a), __builtin_bit_cast(uint32_t, b), false,
+                                              false);
+    a = __builtin_bit_cast(float, (uint32_t)r[0]);
+    b = __builtin_bit_cast(float, (uint32_t)r[1]);
+}
+
+// Transposed wave reduction of 12 per-lane values v[0..11] into 12 wave sums.
+// After the call, lane L of t[m] holds the sum of value 4m + kRowValue[L >> 4]
+// (every lane of a 16-lane row holds the same total).
+//   step 1: swap32 + add folds value pairs across the two 32-lane halves,
+//   step 2: swap16 + add folds the results across rows 0/1 and 2/3,
+//   step 3: row butterfly (row_ror 8, 4, 2, 1) on the three survivors.
+// 6 + 3 swaps, 9 adds and 12 DPP adds instead of 12 x 6 dependent DPP adds.
+constexpr int kRowValue[4] = {0, 2, 1, 3};
+__device__ __forceinline__ void wave_reduce12(float v[12], float t[3]) {
+#pragma unroll
+    for (int k = 0; k < 6; ++k) {
+        float a = v[2 * k], b = v[2 * k + 1];
+        swap32(a, b);
+        v[k] = a + b;   // lanes 0-31: value 2k, lanes 32-63: value 2k+1 (half sums)
+    }
+#pragma unroll
+    for (int m = 0; m < 3; ++m) {
+        float a = v[2 * m], b = v[2 * m + 1];
+        swap16(a, b);
+        t[m] = a + b;   // rows: values 4m, 4m+2, 4m+1, 4m+3 (quarter sums)
+    }
+#pragma unroll
+    for (int m = 0; m < 3; ++m) t[m] += dpp_f32<0x128>(t[m]);
+#pragma unroll
+    for (int m = 0; m < 3; ++m) t[m] += dpp_f32<0x124>(t[m]);
+#pragma unroll
+    for (int m = 0; m < 3; ++m) t[m] += dpp_f32<0x122>(t[m]);
+#pragma unroll
+    for (int m = 0; m < 3; ++m) t[m] += dpp_f32<0x121>(t[m]);
+}
+
 template <typename T>
 __device__ __forceinline__ float load_as_float(const T* p, int64_t i);
 template <>

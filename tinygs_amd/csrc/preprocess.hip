@@ -44,12 +44,10 @@ __device__ __forceinline__ bool will_contribute(float mx, float my, float ca, fl
 }
 
 template <typename ShT>
-__device__ __forceinline__ void sh_to_color(const ShT* __restrict__ sh0, const ShT* __restrict__ shr, int64_t i,
-                                            float px, float py, float pz, const CamParams& cam, int bases,
-                                            float* out) {
+__device__ __forceinline__ void sh_to_color(const ShT* __restrict__ sh0, const ShT* r, int64_t i, float px, float py,
+                                            float pz, const CamParams& cam, int bases, float* out) {
     for (int c = 0; c < 3; ++c) out[c] = 0.5f + 0.28209479177387814f * load_as_float(sh0, 3 * i + c);
     if (bases <= 1) return;
-    const ShT* r = shr + 45 * i;
     const float vx = px - cam.cam_pos[0], vy = py - cam.cam_pos[1], vz = pz - cam.cam_pos[2];
     const float inv = 1.0f / __builtin_sqrtf(vx * vx + vy * vy + vz * vz);
     const float x = vx * inv, y = vy * inv, z = vz * inv;
@@ -89,6 +87,23 @@ __global__ void __launch_bounds__(256) preprocess_kernel(
     CamParams cam, uint32_t* __restrict__ n_touched, uint2* __restrict__ bounds, float2* __restrict__ mean2d,
     float4* __restrict__ conic_opacity, float4* __restrict__ color_pt, uint32_t* __restrict__ depth_key,
     float4* __restrict__ densif) {
+    // SH-rest coefficients of the block's 256 primitives are one contiguous
+    // run: stage it in LDS with 16-byte lane-contiguous loads.
+    __shared__ __align__(16) ShT s_sh[256 * 45];
+    {
+        const int64_t blk0 = (int64_t)blockIdx.x * 256;
+        const int nblk = (int)min((int64_t)256, n - blk0);
+        if (bases > 1) {
+            const int count = nblk * 45;
+            const int nvec = (count * (int)sizeof(ShT)) >> 4;
+            const uint4* s4 = (const uint4*)(shr + blk0 * 45);
+            uint4* d4 = (uint4*)s_sh;
+            for (int v = (int)threadIdx.x; v < nvec; v += 256) d4[v] = s4[v];
+            for (int e = (nvec << 4) / (int)sizeof(ShT) + (int)threadIdx.x; e < count; e += 256)
+                s_sh[e] = shr[blk0 * 45 + e];
+        }
+        __syncthreads();
+    }
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     bool active = i < n;
     const int64_t ii = active ? i : n - 1;
@@ -222,7 +237,7 @@ __global__ void __launch_bounds__(256) preprocess_kernel(
     mean2d[i] = make_float2(m2x, m2y);
     conic_opacity[i] = make_float4(ca, cb, cc, opacity);
     float col[3];
-    sh_to_color(sh0, shr, i, mx, my, mz, cam, bases, col);
+    sh_to_color(sh0, s_sh + 45 * threadIdx.x, i, mx, my, mz, cam, bases, col);
     color_pt[i] = make_float4(col[0], col[1], col[2], pthr);
     depth_key[i] = f2u(depth);
 }

@@ -16,15 +16,27 @@
 
 namespace tgs {
 
+// Copies count elements (a multiple of 8 bytes apart from a tail) from global
+// to LDS with 16-byte lane-contiguous loads.
 template <typename ShT>
-__global__ void __launch_bounds__(256) preprocess_backward_kernel(
-    const float* __restrict__ means, const float* __restrict__ scales, const float* __restrict__ rots,
-    const ShT* __restrict__ shr_all, int64_t n, int bases, CamParams cam, const uint32_t* __restrict__ n_touched,
-    const float4* __restrict__ conic_opacity, const float* __restrict__ grad2d, float* __restrict__ g_means,
-    float* __restrict__ g_scales, float* __restrict__ g_rots, float* __restrict__ g_opac, float* __restrict__ g_sh0,
-    float* __restrict__ g_shr_all, float4* __restrict__ densif) {
-    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= n || n_touched[i] == 0) return;
+__device__ __forceinline__ void stage_block(ShT* dst, const ShT* src, int count) {
+    const int bytes = count * (int)sizeof(ShT);
+    const int nvec = bytes >> 4;
+    const uint4* s4 = (const uint4*)src;
+    uint4* d4 = (uint4*)dst;
+    for (int v = (int)threadIdx.x; v < nvec; v += 256) d4[v] = s4[v];
+    for (int e = (nvec << 4) / (int)sizeof(ShT) + (int)threadIdx.x; e < count; e += 256) dst[e] = src[e];
+}
+
+// Per-primitive part: everything except the SH-rest gradient write, which the
+// block performs cooperatively from k[] (basis values) and gc[] (dL/dcolour).
+template <typename ShT>
+__device__ __forceinline__ void preprocess_backward_one(
+    int64_t i, const float* __restrict__ means, const float* __restrict__ scales, const float* __restrict__ rots,
+    const ShT* shr, int bases, const CamParams& cam, const float4* __restrict__ conic_opacity,
+    const float* __restrict__ grad2d, float* __restrict__ g_means, float* __restrict__ g_scales,
+    float* __restrict__ g_rots, float* __restrict__ g_opac, float* __restrict__ g_sh0, float4* __restrict__ densif,
+    float gc_out[3], float k[15], int& nb_out) {
     const float* gr = grad2d + (size_t)i * kGradStride;
     const float4 gA = *(const float4*)(gr);       // dmx, dmy, absx, absy
     const float4 gB = *(const float4*)(gr + 4);   // dca, dcb, dcc, dr
@@ -33,15 +45,14 @@ __global__ void __launch_bounds__(256) preprocess_backward_kernel(
 
     // ---- SH backward (kernels_backward.cuh:22-86)
     const float gc[3] = {gB.w, gC.x, gC.y};
+    for (int c = 0; c < 3; ++c) gc_out[c] = gc[c];
     for (int c = 0; c < 3; ++c) g_sh0[3 * i + c] += 0.28209479177387814f * gc[c];
     float dmc0 = 0.f, dmc1 = 0.f, dmc2 = 0.f;
+    nb_out = 0;
     if (bases > 1) {
-        const ShT* shr = shr_all + 45 * i;
-        float* gshr = g_shr_all + 45 * i;
         const float xr = mx - cam.cam_pos[0], yr = my - cam.cam_pos[1], zr = mz - cam.cam_pos[2];
         const float inv = 1.0f / __builtin_sqrtf(xr * xr + yr * yr + zr * zr);
         const float x = xr * inv, y = yr * inv, z = zr * inv;
-        float k[15];
         float gdx[3], gdy[3], gdz[3];
         k[0] = -0.48860251190291987f * y;
         k[1] = 0.48860251190291987f * z;
@@ -101,8 +112,7 @@ __global__ void __launch_bounds__(256) preprocess_backward_kernel(
                 }
             }
         }
-        for (int b = 0; b < nb; ++b)
-            for (int c = 0; c < 3; ++c) gshr[3 * b + c] += k[b] * gc[c];
+        nb_out = nb;
         const float gx = gdx[0] * gc[0] + gdx[1] * gc[1] + gdx[2] * gc[2];
         const float gy = gdy[0] * gc[0] + gdy[1] * gc[1] + gdy[2] * gc[2];
         const float gz = gdz[0] * gc[0] + gdz[1] * gc[1] + gdz[2] * gc[2];
@@ -235,6 +245,66 @@ __global__ void __launch_bounds__(256) preprocess_backward_kernel(
         const float wx = gA.z * (0.5f * cam.w), wy = gA.w * (0.5f * cam.h);
         d.z += __builtin_sqrtf(wx * wx + wy * wy);
         densif[i] = d;
+    }
+}
+
+template <typename ShT>
+__global__ void __launch_bounds__(256) preprocess_backward_kernel(
+    const float* __restrict__ means, const float* __restrict__ scales, const float* __restrict__ rots,
+    const ShT* __restrict__ shr_all, int64_t n, int bases, CamParams cam, const uint32_t* __restrict__ n_touched,
+    const float4* __restrict__ conic_opacity, const float* __restrict__ grad2d, float* __restrict__ g_means,
+    float* __restrict__ g_scales, float* __restrict__ g_rots, float* __restrict__ g_opac, float* __restrict__ g_sh0,
+    float* __restrict__ g_shr_all, float4* __restrict__ densif) {
+    // This block's 256 primitives own a contiguous run of 256 * 45 SH-rest
+    // parameters and gradients. Both are moved through LDS with 16-byte
+    // lane-contiguous accesses instead of 45 lane-strided accesses per thread.
+    __shared__ __align__(16) ShT s_sh[256 * 45];
+    __shared__ float s_k[256 * 15];
+    __shared__ float s_gc[256 * 3];
+    __shared__ uint32_t s_nb[256];
+    const int64_t blk0 = (int64_t)blockIdx.x * 256;
+    const int nblk = (int)min((int64_t)256, n - blk0);
+    const int t = (int)threadIdx.x;
+    const int64_t i = blk0 + t;
+    if (bases > 1) stage_block(s_sh, shr_all + blk0 * 45, nblk * 45);
+    __syncthreads();
+    const bool vis = t < nblk && n_touched[i] != 0;
+    float gc[3] = {0.f, 0.f, 0.f};
+    float k[15];
+    for (int b = 0; b < 15; ++b) k[b] = 0.f;
+    int nb = 0;
+    if (vis) preprocess_backward_one<ShT>(i, means, scales, rots, s_sh + 45 * t, bases, cam, conic_opacity, grad2d,
+                                          g_means, g_scales, g_rots, g_opac, g_sh0, densif, gc, k, nb);
+    if (bases > 1) {
+        for (int b = 0; b < 15; ++b) s_k[15 * t + b] = k[b];
+        for (int c = 0; c < 3; ++c) s_gc[3 * t + c] = gc[c];
+        s_nb[t] = vis ? (uint32_t)nb : 0u;
+        __syncthreads();
+        // grad_sh_rest[i][b][c] += k_b * gc_c (kernels_backward.cuh:41-65), b < active bases - 1
+        float* gbase = g_shr_all + blk0 * 45;
+        const int total = nblk * 45;
+        for (int e0 = 4 * t; e0 < total; e0 += 4 * 256) {
+            if (e0 + 3 < total) {
+                float4 g4 = *(const float4*)(gbase + e0);
+                float* gv = (float*)&g4;
+                bool any = false;
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const int e = e0 + q;
+                    const int gi = e / 45, r = e - 45 * gi, b = r / 3, c = r - 3 * b;
+                    if ((uint32_t)b < s_nb[gi]) {
+                        gv[q] = gv[q] + s_k[15 * gi + b] * s_gc[3 * gi + c];
+                        any = true;
+                    }
+                }
+                if (any) *(float4*)(gbase + e0) = g4;
+            } else {
+                for (int e = e0; e < total; ++e) {
+                    const int gi = e / 45, r = e - 45 * gi, b = r / 3, c = r - 3 * b;
+                    if ((uint32_t)b < s_nb[gi]) gbase[e] = gbase[e] + s_k[15 * gi + b] * s_gc[3 * gi + c];
+                }
+            }
+        }
     }
 }
 

@@ -42,6 +42,14 @@ __global__ void wave_selftest_kernel(const uint32_t* in, uint32_t* out) {
     const uint64_t m = ballot((v & 1u) != 0u);
     const uint32_t rank = mask_rank(m);
     out[128 + lane] = rank;
+    // transposed 12-value reduction: value q of lane L = in[(L + 5 q) & 63] + q
+    float vv[12], t[3];
+    for (int q = 0; q < 12; ++q) vv[q] = (float)(in[(lane + 5u * (uint32_t)q) & 63u] + (uint32_t)q);
+    wave_reduce12(vv, t);
+    if ((lane & 15u) == 0u) {
+        const uint32_t row = lane >> 4;
+        for (int m = 0; m < 3; ++m) out[192 + 4 * m + kRowValue[row]] = f2u(t[m]);
+    }
     if (lane == 0) {
         out[64] = sum;
         out[65] = mx;
