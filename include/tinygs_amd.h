@@ -90,6 +90,13 @@ int tgs_rasterizer_forward(tgs_rasterizer* r, const tgs_camera* cam, void* image
  * Must follow a forward on the same Gaussians and camera. */
 int tgs_rasterizer_backward(tgs_rasterizer* r, const void* grad_image, const void* image,
                             const tgs_gaussians* grads, void* densification_info, void* stream);
+/* Same as tgs_rasterizer_backward with flags. TGS_BACKWARD_ASSIGN: gradients
+ * are assigned (zero for culled primitives) instead of accumulated, i.e. the
+ * caller's zeroing (tinygs/src/orchestrator.cu:351-353) fused into the write.
+ * No counterpart in the reference; for callers that zero before every backward. */
+#define TGS_BACKWARD_ASSIGN 1
+int tgs_rasterizer_backward_ex(tgs_rasterizer* r, const void* grad_image, const void* image,
+                               const tgs_gaussians* grads, void* densification_info, int32_t flags, void* stream);
 /* Counts of the last forward: visible primitives, instances, tiles. */
 int tgs_rasterizer_counts(tgs_rasterizer* r, int64_t* n_visible, int64_t* n_instances, int64_t* n_tiles);
 

@@ -204,6 +204,31 @@ def test_backward_accumulates(hip, orc):
     assert normwise_err(got, g1["means"]) < 1e-5
 
 
+def test_backward_assign_mode(hip, orc):
+    """backward with assign=True overwrites every gradient (zero for culled
+    Gaussians): equal to zero-then-accumulate, whatever the buffers held."""
+    import torch
+    from tinygs_amd.core import Image
+    for s in (scenes.config1(seed=6), scenes.config2(seed=18, n=8000, width=200, height=152)):
+        run = gpu_render(s)
+        gimg = _grad_image(s)
+        acc = gpu_backward(run, gimg)
+        ctx = run["ctx"]
+        grads = run["g"].gradient_like()
+        for t in grads.tensors():
+            t.fill_(float("nan"))
+        ctx.gaussians_grad = grads
+        ctx.grad_output.image = Image(ctx.fwd_output.image.shape, "float32", torch.from_numpy(gimg).cuda())
+        run["r"].backward(ctx, assign=True)
+        torch.cuda.synchronize()
+        got = {"means": grads.means(), "scales": grads.scales(), "rotations": grads.rotations(),
+               "opacities": grads.opacities(), "sh0": grads.sh_coefficient_0(), "sh_rest": grads.sh_coefficients_rest()}
+        for k, t in got.items():
+            a = t.cpu().numpy().reshape(-1)
+            assert np.all(np.isfinite(a)), k
+            assert normwise_err(a, acc[k]) < 1e-6, k
+
+
 def test_densification_info(hip, orc):
     s = scenes.config1(seed=4)
     run = gpu_render(s, densif=True)

@@ -64,6 +64,7 @@ SIGNATURES = {
     "tgs_rasterizer_set_gaussians": ([P, C.POINTER(tgs_gaussians)], C.c_int),
     "tgs_rasterizer_forward": ([P, C.POINTER(tgs_camera), P, C.c_int32, P, P], C.c_int),
     "tgs_rasterizer_backward": ([P, P, P, C.POINTER(tgs_gaussians), P, P], C.c_int),
+    "tgs_rasterizer_backward_ex": ([P, P, P, C.POINTER(tgs_gaussians), P, C.c_int32, P], C.c_int),
     "tgs_rasterizer_counts": ([P, C.POINTER(C.c_int64), C.POINTER(C.c_int64), C.POINTER(C.c_int64)], C.c_int),
     "tgs_rasterizer_debug_view": ([P, C.POINTER(tgs_debug_view)], C.c_int),
     "tgs_loss_create": ([C.c_char_p, PP], C.c_int),

@@ -22,7 +22,7 @@ struct AdamLaunch {
 };
 
 constexpr int kAdamThreads = 256;
-constexpr int kAdamVecPerThread = 2;                       // 4-element vectors per thread
+constexpr int kAdamVecPerThread = 4;                       // 4-element vectors per thread
 constexpr int kAdamChunk = kAdamThreads * kAdamVecPerThread * 4;
 
 __device__ __forceinline__ float adam_one(float th, float gr_raw, float& m, float& v, const AdamGroup& g,
@@ -50,8 +50,9 @@ __device__ __forceinline__ float adam_one(float th, float gr_raw, float& m, floa
     return th - (mh * g.lr) / den;
 }
 
-// Each thread updates 4-element vectors with 16-byte loads/stores (8-byte for
-// fp16 theta); lanes of a wave cover consecutive vectors.
+// Each thread updates kAdamVecPerThread 4-element vectors with 16-byte loads
+// and stores (8-byte for fp16 theta); lanes of a wave cover consecutive
+// vectors. All loads of a thread are issued before any arithmetic.
 __global__ void __launch_bounds__(kAdamThreads) adam_kernel(AdamLaunch L) {
     const int64_t b = blockIdx.x;
     int gi = 0;
@@ -61,46 +62,54 @@ __global__ void __launch_bounds__(kAdamThreads) adam_kernel(AdamLaunch L) {
     const AdamGroup& g = L.a.groups[gi];
     const float t1 = 1.0f - L.a.beta1, t2 = 1.0f - L.a.beta2;
     const int64_t vbase = (b - L.block_start[gi]) * (kAdamChunk / 4) + threadIdx.x;
+    float th[kAdamVecPerThread][4];
+    float4 gv[kAdamVecPerThread], mv[kAdamVecPerThread], vv[kAdamVecPerThread];
+    bool full[kAdamVecPerThread];
 #pragma unroll
     for (int k = 0; k < kAdamVecPerThread; ++k) {
         const int64_t e0 = 4 * (vbase + (int64_t)k * kAdamThreads);
-        if (e0 >= g.count) break;
-        if (e0 + 3 < g.count) {
-            float th[4];
+        full[k] = e0 + 3 < g.count;
+        if (full[k]) {
             if (g.theta_half) {
                 const uint2 hv = *(const uint2*)((const __half*)g.theta + e0);
                 const __half* h = (const __half*)&hv;
-                for (int q = 0; q < 4; ++q) th[q] = __half2float(h[q]);
+                for (int q = 0; q < 4; ++q) th[k][q] = __half2float(h[q]);
             } else {
                 const float4 tv = *(const float4*)((const float*)g.theta + e0);
-                th[0] = tv.x; th[1] = tv.y; th[2] = tv.z; th[3] = tv.w;
+                th[k][0] = tv.x; th[k][1] = tv.y; th[k][2] = tv.z; th[k][3] = tv.w;
             }
-            const float4 gv = *(const float4*)(g.grad + e0);
-            float4 mv = *(const float4*)(g.m1 + e0);
-            float4 vv = *(const float4*)(g.m2 + e0);
-            th[0] = adam_one(th[0], gv.x, mv.x, vv.x, g, L.a, t1, t2);
-            th[1] = adam_one(th[1], gv.y, mv.y, vv.y, g, L.a, t1, t2);
-            th[2] = adam_one(th[2], gv.z, mv.z, vv.z, g, L.a, t1, t2);
-            th[3] = adam_one(th[3], gv.w, mv.w, vv.w, g, L.a, t1, t2);
+            gv[k] = *(const float4*)(g.grad + e0);
+            mv[k] = *(const float4*)(g.m1 + e0);
+            vv[k] = *(const float4*)(g.m2 + e0);
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < kAdamVecPerThread; ++k) {
+        const int64_t e0 = 4 * (vbase + (int64_t)k * kAdamThreads);
+        if (full[k]) {
+            th[k][0] = adam_one(th[k][0], gv[k].x, mv[k].x, vv[k].x, g, L.a, t1, t2);
+            th[k][1] = adam_one(th[k][1], gv[k].y, mv[k].y, vv[k].y, g, L.a, t1, t2);
+            th[k][2] = adam_one(th[k][2], gv[k].z, mv[k].z, vv[k].z, g, L.a, t1, t2);
+            th[k][3] = adam_one(th[k][3], gv[k].w, mv[k].w, vv[k].w, g, L.a, t1, t2);
             if (g.theta_half) {
                 uint2 hv;
                 __half* h = (__half*)&hv;
-                for (int q = 0; q < 4; ++q) h[q] = __float2half_rn(th[q]);
+                for (int q = 0; q < 4; ++q) h[q] = __float2half_rn(th[k][q]);
                 *(uint2*)((__half*)g.theta + e0) = hv;
             } else {
-                *(float4*)((float*)g.theta + e0) = make_float4(th[0], th[1], th[2], th[3]);
+                *(float4*)((float*)g.theta + e0) = make_float4(th[k][0], th[k][1], th[k][2], th[k][3]);
             }
-            *(float4*)(g.m1 + e0) = mv;
-            *(float4*)(g.m2 + e0) = vv;
-        } else {
+            *(float4*)(g.m1 + e0) = mv[k];
+            *(float4*)(g.m2 + e0) = vv[k];
+        } else if (e0 < g.count) {
             for (int64_t i = e0; i < g.count; ++i) {
-                float th = g.theta_half ? __half2float(((const __half*)g.theta)[i]) : ((const float*)g.theta)[i];
+                float t = g.theta_half ? __half2float(((const __half*)g.theta)[i]) : ((const float*)g.theta)[i];
                 float m = g.m1[i], v = g.m2[i];
-                th = adam_one(th, g.grad[i], m, v, g, L.a, t1, t2);
+                t = adam_one(t, g.grad[i], m, v, g, L.a, t1, t2);
                 if (g.theta_half)
-                    ((__half*)g.theta)[i] = __float2half_rn(th);
+                    ((__half*)g.theta)[i] = __float2half_rn(t);
                 else
-                    ((float*)g.theta)[i] = th;
+                    ((float*)g.theta)[i] = t;
                 g.m1[i] = m;
                 g.m2[i] = v;
             }

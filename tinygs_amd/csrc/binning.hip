@@ -188,29 +188,41 @@ __global__ void __launch_bounds__(256) radix_hist_kernel(const uint32_t* __restr
     hist[(size_t)d * nblocks + blockIdx.x] = s_hist[0][d] + s_hist[1][d] + s_hist[2][d] + s_hist[3][d];
 }
 
+// Stable scatter of one 8-bit digit. Wave w of the workgroup owns keys
+// [w * 1024, (w + 1) * 1024) of the workgroup's 4096-key chunk and ranks them
+// in 16 rounds of 64 with ballot matching against a wave-private LDS
+// histogram (a wave's LDS operations complete in issue order, so no barrier
+// is needed between rounds). One barrier then turns the four private
+// histograms into per-wave bases, and every key is written to
+// global offset(digit, workgroup) + wave base + rank within the wave.
 __global__ void __launch_bounds__(256) radix_scatter_kernel(const uint32_t* __restrict__ keys_in,
                                                             const uint32_t* __restrict__ vals_in,
                                                             uint32_t* __restrict__ keys_out,
                                                             uint32_t* __restrict__ vals_out, const uint32_t* d_n,
                                                             int64_t max_n, int shift,
                                                             const uint32_t* __restrict__ offsets, uint32_t nblocks) {
-    __shared__ uint32_t s_gofs[kRadixBins];
-    __shared__ uint32_t s_base[kRadixBins];
-    __shared__ uint32_t s_wcnt[4][kRadixBins];
+    __shared__ uint32_t s_cnt[4][kRadixBins];
     const uint32_t lane = threadIdx.x & 63u, w = threadIdx.x >> 6, t = threadIdx.x;
-    s_gofs[t] = offsets[(size_t)t * nblocks + blockIdx.x];
-    s_base[t] = 0;
     const int64_t n = resolve_n(d_n, max_n);
-    const int64_t base = (int64_t)blockIdx.x * kRadixChunk;
-    if (base >= n) return;
+    const int64_t blk = (int64_t)blockIdx.x * kRadixChunk;
+    if (blk >= n) return;
+    for (int k = t; k < 4 * kRadixBins; k += 256) (&s_cnt[0][0])[k] = 0;
+    const uint32_t gofs = offsets[(size_t)t * nblocks + blockIdx.x];
+    __syncthreads();
+    const int64_t base = blk + (int64_t)w * (kRadixChunk / 4);
+    uint32_t key[kRadixRounds], val[kRadixRounds], pos[kRadixRounds];
+#pragma unroll
     for (int r = 0; r < kRadixRounds; ++r) {
-        const int64_t i = base + (int64_t)r * 256 + t;
+        const int64_t i = base + (int64_t)r * 64 + lane;
         const bool valid = i < n;
-        const uint32_t key = valid ? keys_in[i] : 0u;
-        const uint32_t val = valid ? vals_in[i] : 0u;
-        const uint32_t d = (key >> shift) & 0xffu;
-        for (int k = t; k < 4 * kRadixBins; k += 256) (&s_wcnt[0][0])[k] = 0;
-        __syncthreads();
+        key[r] = valid ? keys_in[i] : 0u;
+        val[r] = valid ? vals_in[i] : 0u;
+    }
+#pragma unroll
+    for (int r = 0; r < kRadixRounds; ++r) {
+        const int64_t i = base + (int64_t)r * 64 + lane;
+        const bool valid = i < n;
+        const uint32_t d = (key[r] >> shift) & 0xffu;
         uint64_t peers = ballot(valid);
 #pragma unroll
         for (int b = 0; b < kRadixBits; ++b) {
@@ -219,25 +231,28 @@ __global__ void __launch_bounds__(256) radix_scatter_kernel(const uint32_t* __re
             peers &= bit ? m : ~m;
         }
         const uint32_t rank = mask_rank(peers);
-        if (valid && rank == 0u) s_wcnt[w][d] = (uint32_t)__builtin_popcountll(peers);
-        __syncthreads();
-        {
-            const uint32_t c0 = s_wcnt[0][t], c1 = s_wcnt[1][t], c2 = s_wcnt[2][t], c3 = s_wcnt[3][t];
-            const uint32_t b0 = s_base[t];
-            s_wcnt[0][t] = b0;
-            s_wcnt[1][t] = b0 + c0;
-            s_wcnt[2][t] = b0 + c0 + c1;
-            s_wcnt[3][t] = b0 + c0 + c1 + c2;
-            s_base[t] = b0 + c0 + c1 + c2 + c3;
+        const uint32_t running = s_cnt[w][d];
+        pos[r] = running + rank;
+        if (valid && rank == 0u) s_cnt[w][d] = running + (uint32_t)__builtin_popcountll(peers);
+    }
+    __syncthreads();
+    {
+        const uint32_t c0 = s_cnt[0][t], c1 = s_cnt[1][t], c2 = s_cnt[2][t];
+        s_cnt[0][t] = gofs;
+        s_cnt[1][t] = gofs + c0;
+        s_cnt[2][t] = gofs + c0 + c1;
+        s_cnt[3][t] = gofs + c0 + c1 + c2;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < kRadixRounds; ++r) {
+        const int64_t i = base + (int64_t)r * 64 + lane;
+        if (i < n) {
+            const uint32_t d = (key[r] >> shift) & 0xffu;
+            const uint32_t o = s_cnt[w][d] + pos[r];
+            keys_out[o] = key[r];
+            vals_out[o] = val[r];
         }
-        __syncthreads();
-        if (valid) {
-            const uint32_t pos = s_gofs[d] + s_wcnt[w][d] + rank;
-            keys_out[pos] = key;
-            vals_out[pos] = val;
-        }
-        __syncthreads();
-        (void)lane;
     }
 }
 

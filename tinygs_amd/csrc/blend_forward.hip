@@ -32,7 +32,7 @@ __global__ void __launch_bounds__(256) blend_forward_kernel(CamParams cam, const
                                                             unsigned long long* __restrict__ stats) {
     __shared__ float4 s_a[256];   // mx, my, a/2, b
     __shared__ float2 s_b[256];   // c/2, opacity
-    __shared__ float4 s_c[256];   // r, g, b (clamped), unused
+    __shared__ float4 s_c[256];   // r, g, b (clamped), skip bound
     __shared__ uint32_t s_max[4];
 
     const uint32_t tile = blockIdx.x;
@@ -61,18 +61,25 @@ __global__ void __launch_bounds__(256) blend_forward_kernel(CamParams cam, const
             const float4 c = color_pt[p];
             s_a[tid] = make_float4(m.x, m.y, 0.5f * co.x, co.y);
             s_b[tid] = make_float2(0.5f * co.z, co.w);
-            s_c[tid] = make_float4(__builtin_fmaxf(c.x, 0.f), __builtin_fmaxf(c.y, 0.f), __builtin_fmaxf(c.z, 0.f), 0.f);
+            // w: ln(255 * opacity) + 1e-3, the wave-skip bound (see below)
+            s_c[tid] = make_float4(__builtin_fmaxf(c.x, 0.f), __builtin_fmaxf(c.y, 0.f), __builtin_fmaxf(c.z, 0.f),
+                                   c.w + 1e-3f);
         }
         __syncthreads();
         const int32_t nb = min(256, len - base);
         loaded += (uint32_t)nb;
         for (int32_t k = 0; k < nb; ++k) {
             if (!__any(!done)) break;   // whole wave finished
-            if (done) continue;
             const float4 a = s_a[k];
             const float2 bb = s_b[k];
             const float dx = a.x - pcx, dy = a.y - pcy;
             const float sigma = __builtin_fmaf(dx, __builtin_fmaf(a.z, dx, a.w * dy), (bb.x * dy) * dy);
+            // Exact wave-level skip: sigma > ln(255 o) + 1e-3 implies
+            // o * exp(-sigma) < exp(-1e-3) / 255, below the 1/255 cut by far
+            // more than the error of the deterministic exp / log (< 1e-6
+            // relative), so such pixels would all take the alpha < 1/255 path.
+            if (!__any(!done && sigma <= s_c[k].w)) continue;
+            if (done) continue;
             if (sigma < 0.f) continue;
             const float alpha = __builtin_fminf(bb.y * det_expf_nonpos(-sigma), kMaxAlpha);
             if (alpha < kMinAlpha) continue;

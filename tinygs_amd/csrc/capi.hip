@@ -408,6 +408,11 @@ int tgs_rasterizer_forward(tgs_rasterizer* r, const tgs_camera* camera, void* im
 
 int tgs_rasterizer_backward(tgs_rasterizer* r, const void* grad_image, const void* image, const tgs_gaussians* grads,
                             void* densification_info, void* stream) {
+    return tgs_rasterizer_backward_ex(r, grad_image, image, grads, densification_info, 0, stream);
+}
+
+int tgs_rasterizer_backward_ex(tgs_rasterizer* r, const void* grad_image, const void* image,
+                               const tgs_gaussians* grads, void* densification_info, int32_t flags, void* stream) {
     if (!r) return fail(TGS_ERR_INVALID, "rasterizer is NULL");
     if (!r->has_g || !grads) return fail(TGS_ERR_STATE, "Gaussians or gradient gaussians not set");
     if (!r->fwd_done) return fail(TGS_ERR_STATE, "backward called without a preceding forward");
@@ -433,7 +438,8 @@ int tgs_rasterizer_backward(tgs_rasterizer* r, const void* grad_image, const voi
     {
         StageScope sc(ST_PREB, s);
         launch_preprocess_backward(view_of(r->g), cam, r->n_touched.as<uint32_t>(), r->conic_opacity.as<float4>(),
-                                   r->grad2d.as<float>(), gv, (float*)densification_info, s);
+                                   r->grad2d.as<float>(), gv, (float*)densification_info,
+                                   (flags & TGS_BACKWARD_ASSIGN) != 0, s);
     }
     TGS_CHECK_LAUNCH();
     return TGS_OK;

@@ -68,7 +68,7 @@ void launch_blend_backward(const CamParams& cam, const uint2* ranges, const uint
 // ---- preprocess backward (kernels_backward.cuh:88-352)
 void launch_preprocess_backward(const GaussianView& g, const CamParams& cam, const uint32_t* n_touched,
                                 const float4* conic_opacity, const float* grad2d, const GradView& out,
-                                float* densif, hipStream_t s);
+                                float* densif, bool assign, hipStream_t s);
 
 // ---- utilities
 void launch_fill_u32(uint32_t* p, uint32_t value, int64_t n, hipStream_t s);

@@ -28,6 +28,10 @@ __device__ __forceinline__ void stage_block(ShT* dst, const ShT* src, int count)
     for (int e = (nvec << 4) / (int)sizeof(ShT) + (int)threadIdx.x; e < count; e += 256) dst[e] = src[e];
 }
 
+// Gradient update: accumulate (+=, the reference contract) or assign (the
+// caller's zeroing fused into this write).
+__device__ __forceinline__ void gadd(float* p, float v, bool assign) { *p = assign ? v : *p + v; }
+
 // Per-primitive part: everything except the SH-rest gradient write, which the
 // block performs cooperatively from k[] (basis values) and gc[] (dL/dcolour).
 template <typename ShT>
@@ -36,7 +40,7 @@ __device__ __forceinline__ void preprocess_backward_one(
     const ShT* shr, int bases, const CamParams& cam, const float4* __restrict__ conic_opacity,
     const float* __restrict__ grad2d, float* __restrict__ g_means, float* __restrict__ g_scales,
     float* __restrict__ g_rots, float* __restrict__ g_opac, float* __restrict__ g_sh0, float4* __restrict__ densif,
-    float gc_out[3], float k[15], int& nb_out) {
+    float gc_out[3], float k[15], int& nb_out, bool assign) {
     const float* gr = grad2d + (size_t)i * kGradStride;
     const float4 gA = *(const float4*)(gr);       // dmx, dmy, absx, absy
     const float4 gB = *(const float4*)(gr + 4);   // dca, dcb, dcc, dr
@@ -46,7 +50,7 @@ __device__ __forceinline__ void preprocess_backward_one(
     // ---- SH backward (kernels_backward.cuh:22-86)
     const float gc[3] = {gB.w, gC.x, gC.y};
     for (int c = 0; c < 3; ++c) gc_out[c] = gc[c];
-    for (int c = 0; c < 3; ++c) g_sh0[3 * i + c] += 0.28209479177387814f * gc[c];
+    for (int c = 0; c < 3; ++c) gadd(g_sh0 + 3 * i + c, 0.28209479177387814f * gc[c], assign);
     float dmc0 = 0.f, dmc1 = 0.f, dmc2 = 0.f;
     nb_out = 0;
     if (bases > 1) {
@@ -205,18 +209,18 @@ __device__ __forceinline__ void preprocess_backward_one(
     const float gmx = r1[0] * dcx + r2[0] * dcy + r3[0] * dcz;
     const float gmy = r1[1] * dcx + r2[1] * dcy + r3[1] * dcz;
     const float gmz = r1[2] * dcx + r2[2] * dcy + r3[2] * dcz;
-    g_means[3 * i] += gmx + dmc0;
-    g_means[3 * i + 1] += gmy + dmc1;
-    g_means[3 * i + 2] += gmz + dmc2;
+    gadd(g_means + 3 * i, gmx + dmc0, assign);
+    gadd(g_means + 3 * i + 1, gmy + dmc1, assign);
+    gadd(g_means + 3 * i + 2, gmz + dmc2, assign);
     const float dvx = R11 * R11 * d11 + R21 * R21 * d22 + R31 * R31 * d33 +
                       2.0f * (R11 * R21 * d12 + R11 * R31 * d13 + R21 * R31 * d23);
     const float dvy = R12 * R12 * d11 + R22 * R22 * d22 + R32 * R32 * d33 +
                       2.0f * (R12 * R22 * d12 + R12 * R32 * d13 + R22 * R32 * d23);
     const float dvz = R13 * R13 * d11 + R23 * R23 * d22 + R33 * R33 * d33 +
                       2.0f * (R13 * R23 * d12 + R13 * R33 * d13 + R23 * R33 * d23);
-    g_scales[3 * i] += 2.0f * e0 * e0 * dvx;
-    g_scales[3 * i + 1] += 2.0f * e1 * e1 * dvy;
-    g_scales[3 * i + 2] += 2.0f * e2 * e2 * dvz;
+    gadd(g_scales + 3 * i, 2.0f * e0 * e0 * dvx, assign);
+    gadd(g_scales + 3 * i + 1, 2.0f * e1 * e1 * dvy, assign);
+    gadd(g_scales + 3 * i + 2, 2.0f * e2 * e2 * dvz, assign);
     const float D11 = 2.0f * (S11 * d11 + S21 * d12 + S31 * d13);
     const float D12 = 2.0f * (S12 * d11 + S22 * d12 + S32 * d13);
     const float D13 = 2.0f * (S13 * d11 + S23 * d12 + S33 * d13);
@@ -232,11 +236,11 @@ __device__ __forceinline__ void preprocess_backward_one(
     const float hlp = qxx * gqxx + qyy * gqyy + qzz * gqzz + qxy * gqxy + qxz * gqxz + qyz * gqyz + qrx * gqrx +
                       qry * gqry + qrz * gqrz;
     const float den = qn * __builtin_sqrtf(qn);
-    g_rots[4 * i] += 2.0f * (qx * gqrx + qy * gqry + qz * gqrz - qr * hlp) / den;
-    g_rots[4 * i + 1] += 2.0f * (2.0f * qx * gqxx + qy * gqxy + qz * gqxz + qr * gqrx - qx * hlp) / den;
-    g_rots[4 * i + 2] += 2.0f * (2.0f * qy * gqyy + qx * gqxy + qz * gqyz + qr * gqry - qy * hlp) / den;
-    g_rots[4 * i + 3] += 2.0f * (2.0f * qz * gqzz + qx * gqxz + qy * gqyz + qr * gqrz - qz * hlp) / den;
-    g_opac[i] += gC.z * (1.0f - conic_opacity[i].w);
+    gadd(g_rots + 4 * i, 2.0f * (qx * gqrx + qy * gqry + qz * gqrz - qr * hlp) / den, assign);
+    gadd(g_rots + 4 * i + 1, 2.0f * (2.0f * qx * gqxx + qy * gqxy + qz * gqxz + qr * gqrx - qx * hlp) / den, assign);
+    gadd(g_rots + 4 * i + 2, 2.0f * (2.0f * qy * gqyy + qx * gqxy + qz * gqyz + qr * gqry - qy * hlp) / den, assign);
+    gadd(g_rots + 4 * i + 3, 2.0f * (2.0f * qz * gqzz + qx * gqxz + qy * gqyz + qr * gqrz - qz * hlp) / den, assign);
+    gadd(g_opac + i, gC.z * (1.0f - conic_opacity[i].w), assign);
     if (densif) {
         float4 d = densif[i];
         d.x += 1.0f;
@@ -254,7 +258,7 @@ __global__ void __launch_bounds__(256) preprocess_backward_kernel(
     const ShT* __restrict__ shr_all, int64_t n, int bases, CamParams cam, const uint32_t* __restrict__ n_touched,
     const float4* __restrict__ conic_opacity, const float* __restrict__ grad2d, float* __restrict__ g_means,
     float* __restrict__ g_scales, float* __restrict__ g_rots, float* __restrict__ g_opac, float* __restrict__ g_sh0,
-    float* __restrict__ g_shr_all, float4* __restrict__ densif) {
+    float* __restrict__ g_shr_all, float4* __restrict__ densif, int assign_flag) {
     // This block's 256 primitives own a contiguous run of 256 * 45 SH-rest
     // parameters and gradients. Both are moved through LDS with 16-byte
     // lane-contiguous accesses instead of 45 lane-strided accesses per thread.
@@ -273,9 +277,20 @@ __global__ void __launch_bounds__(256) preprocess_backward_kernel(
     float k[15];
     for (int b = 0; b < 15; ++b) k[b] = 0.f;
     int nb = 0;
-    if (vis) preprocess_backward_one<ShT>(i, means, scales, rots, s_sh + 45 * t, bases, cam, conic_opacity, grad2d,
-                                          g_means, g_scales, g_rots, g_opac, g_sh0, densif, gc, k, nb);
-    if (bases > 1) {
+    const bool assign = assign_flag != 0;
+    if (vis) {
+        preprocess_backward_one<ShT>(i, means, scales, rots, s_sh + 45 * t, bases, cam, conic_opacity, grad2d,
+                                     g_means, g_scales, g_rots, g_opac, g_sh0, densif, gc, k, nb, assign);
+    } else if (assign && t < nblk) {
+        for (int c = 0; c < 3; ++c) {
+            g_means[3 * i + c] = 0.f;
+            g_scales[3 * i + c] = 0.f;
+            g_sh0[3 * i + c] = 0.f;
+        }
+        for (int c = 0; c < 4; ++c) g_rots[4 * i + c] = 0.f;
+        g_opac[i] = 0.f;
+    }
+    if (bases > 1 || assign) {
         for (int b = 0; b < 15; ++b) s_k[15 * t + b] = k[b];
         for (int c = 0; c < 3; ++c) s_gc[3 * t + c] = gc[c];
         s_nb[t] = vis ? (uint32_t)nb : 0u;
@@ -284,7 +299,17 @@ __global__ void __launch_bounds__(256) preprocess_backward_kernel(
         float* gbase = g_shr_all + blk0 * 45;
         const int total = nblk * 45;
         for (int e0 = 4 * t; e0 < total; e0 += 4 * 256) {
-            if (e0 + 3 < total) {
+            if (assign && e0 + 3 < total) {
+                float4 g4;
+                float* gv = (float*)&g4;
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const int e = e0 + q;
+                    const int gi = e / 45, r = e - 45 * gi, b = r / 3, c = r - 3 * b;
+                    gv[q] = ((uint32_t)b < s_nb[gi]) ? s_k[15 * gi + b] * s_gc[3 * gi + c] : 0.f;
+                }
+                *(float4*)(gbase + e0) = g4;
+            } else if (e0 + 3 < total) {
                 float4 g4 = *(const float4*)(gbase + e0);
                 float* gv = (float*)&g4;
                 bool any = false;
@@ -301,7 +326,11 @@ __global__ void __launch_bounds__(256) preprocess_backward_kernel(
             } else {
                 for (int e = e0; e < total; ++e) {
                     const int gi = e / 45, r = e - 45 * gi, b = r / 3, c = r - 3 * b;
-                    if ((uint32_t)b < s_nb[gi]) gbase[e] = gbase[e] + s_k[15 * gi + b] * s_gc[3 * gi + c];
+                    if ((uint32_t)b < s_nb[gi])
+                        gbase[e] = assign ? s_k[15 * gi + b] * s_gc[3 * gi + c]
+                                          : gbase[e] + s_k[15 * gi + b] * s_gc[3 * gi + c];
+                    else if (assign)
+                        gbase[e] = 0.f;
                 }
             }
         }
@@ -310,18 +339,20 @@ __global__ void __launch_bounds__(256) preprocess_backward_kernel(
 
 void launch_preprocess_backward(const GaussianView& g, const CamParams& cam, const uint32_t* n_touched,
                                 const float4* conic_opacity, const float* grad2d, const GradView& out, float* densif,
-                                hipStream_t s) {
+                                bool assign, hipStream_t s) {
     if (g.n <= 0) return;
     const int bases = (g.sh_degree + 1) * (g.sh_degree + 1);
     const unsigned grid = (unsigned)((g.n + 255) / 256);
     if (g.sh_dtype == kShF16) {
         preprocess_backward_kernel<__half><<<grid, 256, 0, s>>>(
             g.means, g.scales, g.rotations, (const __half*)g.sh_rest, g.n, bases, cam, n_touched, conic_opacity,
-            grad2d, out.means, out.scales, out.rotations, out.opacities, out.sh0, out.sh_rest, (float4*)densif);
+            grad2d, out.means, out.scales, out.rotations, out.opacities, out.sh0, out.sh_rest, (float4*)densif,
+            assign ? 1 : 0);
     } else {
         preprocess_backward_kernel<float><<<grid, 256, 0, s>>>(
             g.means, g.scales, g.rotations, (const float*)g.sh_rest, g.n, bases, cam, n_touched, conic_opacity,
-            grad2d, out.means, out.scales, out.rotations, out.opacities, out.sh0, out.sh_rest, (float4*)densif);
+            grad2d, out.means, out.scales, out.rotations, out.opacities, out.sh0, out.sh_rest, (float4*)densif,
+            assign ? 1 : 0);
     }
 }
 

@@ -69,14 +69,18 @@ class FastGSRasterizer(RasterizerBase):
         _lib.check(L.tgs_rasterizer_forward(self._h, C.byref(cam), ptr(img.data), _lib.TGS_DTYPE_FLOAT32,
                                             ptr(ctx.densification_info), stream_ptr(ctx.stream)), "forward")
 
-    def backward(self, ctx: RasterizeContext):
+    def backward(self, ctx: RasterizeContext, assign: bool = False):
+        """Accumulates into ctx.gaussians_grad (reference contract). assign=True
+        writes the gradients instead (zero for culled Gaussians): the caller's
+        zeroing fused into the backward."""
         if self.m_gaussians is None or ctx.gaussians_grad is None:
             raise RuntimeError("Gaussians or gradient gaussians not set")
         g = ctx.gaussians_grad.to_c()
         L = _lib.load()
-        _lib.check(L.tgs_rasterizer_backward(self._h, ptr(ctx.grad_output.image.data), ptr(ctx.fwd_output.image.data),
-                                             C.byref(g), ptr(ctx.densification_info), stream_ptr(ctx.stream)),
-                   "backward")
+        _lib.check(L.tgs_rasterizer_backward_ex(self._h, ptr(ctx.grad_output.image.data),
+                                                ptr(ctx.fwd_output.image.data), C.byref(g),
+                                                ptr(ctx.densification_info), 1 if assign else 0,
+                                                stream_ptr(ctx.stream)), "backward")
 
     def counts(self):
         v, i, t = C.c_int64(), C.c_int64(), C.c_int64()

@@ -58,10 +58,12 @@ class TrainStep:
         self.loss_ctx = LossContext(self.pred, self.target, self.loss_img, self.grad_img, stream)
 
     def zero(self):
+        """Zero the loss and loss-gradient images. The parameter gradients are
+        not zeroed here: the backward runs in assign mode, which writes every
+        gradient (zero for culled Gaussians), equivalent to zero + accumulate."""
         import torch
         s = self.stream
         with torch.cuda.stream(s) if s is not None else _null():
-            self.grads.memset(0)
             self.loss_img.data.zero_()
             self.grad_img.data.zero_()
 
@@ -73,7 +75,7 @@ class TrainStep:
             loss.evaluate(self.loss_ctx, w * self.grad_scaler)
 
     def backward(self):
-        self.rasterizer.backward(self.ctx)
+        self.rasterizer.backward(self.ctx, assign=True)
 
     def optimize(self):
         self.optimizer.step(1.0 / self.grad_scaler, self.stream)
