@@ -226,7 +226,7 @@ def test_backward_assign_mode(hip, orc):
         for k, t in got.items():
             a = t.cpu().numpy().reshape(-1)
             assert np.all(np.isfinite(a)), k
-            assert normwise_err(a, acc[k]) < 1e-6, k
+            assert normwise_err(a, acc[k]) < 2e-5, k   # two runs differ only by atomic order
 
 
 def test_densification_info(hip, orc):
