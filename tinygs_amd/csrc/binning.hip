@@ -13,16 +13,28 @@
 // per primitive (V elements) before duplication; duplication preserves that
 // order, so the remaining passes only sort the ceil(log2 T) tile bits over
 // the I instances.
+//
+// MI355X notes that shaped this file (measured): a store or load instruction
+// whose 64 lanes touch 64 different cache lines runs at a small fraction of
+// HBM bandwidth, so every kernel here reads and writes lane-contiguous runs
+// (striped element assignment, LDS staging before the radix scatter); and a
+// decoupled look-back whose predecessors all start at once is a serial chain
+// of cross-XCD loads, so the radix passes use reduce-then-scan (per-workgroup
+// digit counts, one row-scan launch, then the ranked scatter) and only the
+// two single-value scans use look-back, with a 64-wide window read by a whole
+// wave.
 #include "common.h"
 #include "kernels.h"
 
 namespace tgs {
 
-constexpr int kScanThreads = 256;
-constexpr int kScanItems = 16;
-constexpr int kScanChunk = kScanThreads * kScanItems;  // 4096 elements per workgroup
+constexpr int kThreads = 256;
+constexpr int kScanRounds = 16;
+constexpr int kScanChunk = kThreads * kScanRounds;     // 4096 elements per scan workgroup
+constexpr int kDepthKeysPerThread = 8;                  // depth passes: 2048 keys per workgroup
+constexpr int kTileKeysPerThread = 16;                  // tile passes: 4096 keys per workgroup
 
-// ---------------------------------------------------------------- workgroup scan
+// ---------------------------------------------------------------- workgroup scans
 
 // Exclusive scan of one value per thread across a 256-thread workgroup.
 // Returns the exclusive prefix; *total receives the workgroup sum.
@@ -42,242 +54,409 @@ __device__ __forceinline__ uint32_t block_exclusive_scan(uint32_t v, uint32_t* s
     return wave_off + incl - v;
 }
 
-// ---------------------------------------------------------------- generic 3-phase scan
+// Exclusive scan of 16 striped values per thread: value r of thread t is
+// element r * 256 + t of the workgroup's chunk, so consecutive lanes hold
+// consecutive elements in every round. s_rw: 64 words of LDS.
+__device__ __forceinline__ void striped_scan16(const uint32_t v[kScanRounds], uint32_t ex[kScanRounds],
+                                               uint32_t* total, uint32_t* s_rw) {
+    const uint32_t lane = threadIdx.x & 63u, w = threadIdx.x >> 6;
+#pragma unroll
+    for (int r = 0; r < kScanRounds; ++r) {
+        const uint32_t incl = wave_inclusive_scan_u32(v[r]);
+        ex[r] = incl - v[r];
+        if (lane == 63u) s_rw[r * 4 + w] = incl;
+    }
+    __syncthreads();
+    // (round, wave) partial sums in element order; every wave scans them itself
+    const uint32_t x = s_rw[lane];
+    const uint32_t xi = wave_inclusive_scan_u32(x);
+    *total = readlane_u32(xi, 63);
+    const uint32_t xe = xi - x;
+#pragma unroll
+    for (int r = 0; r < kScanRounds; ++r) ex[r] += readlane_u32(xe, (uint32_t)(r * 4) + w);
+    __syncthreads();   // s_rw may be reused after this
+}
 
-struct LoadPlain {
-    const uint32_t* p;
-    __device__ uint32_t operator()(int64_t i) const { return p[i]; }
-};
-struct LoadVisible {
-    const uint32_t* n_touched;
-    __device__ uint32_t operator()(int64_t i) const { return n_touched[i] > 0u ? 1u : 0u; }
-};
-struct LoadTouchedByPrim {
-    const uint32_t* n_touched;
-    const uint32_t* prims;
-    __device__ uint32_t operator()(int64_t i) const { return n_touched[prims[i]]; }
-};
+// ---------------------------------------------------------------- decoupled look-back (single value)
+
+// status word: [63:62] flag (0 not ready, 1 aggregate, 2 inclusive prefix),
+// [61:32] epoch of the launch that wrote it, [31:0] value.
+constexpr uint64_t kFlagMask = 3ull << 62;
+constexpr uint64_t kFlagAggregate = 1ull << 62;
+constexpr uint64_t kFlagPrefix = 2ull << 62;
+constexpr uint32_t kSpinLimit = 1u << 22;
+
+__device__ __forceinline__ uint64_t status_word(uint64_t flag, uint32_t epoch, uint32_t value) {
+    return flag | ((uint64_t)(epoch & kEpochMask) << 32) | (uint64_t)value;
+}
+__device__ __forceinline__ uint64_t load_status(const uint64_t* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void store_status(uint64_t* p, uint64_t v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Ticket in launch order, broadcast to the workgroup (contains a barrier).
+__device__ __forceinline__ uint32_t take_ticket(uint32_t* ticket, uint32_t* s_bid) {
+    if (threadIdx.x == 0) *s_bid = atomicAdd(ticket, 1u);
+    __syncthreads();
+    return *s_bid;
+}
+
+// Called by one whole wave: publishes the workgroup total for ticket `bid`
+// and returns (in every lane) the exclusive prefix over smaller tickets.
+// Lane q reads the status of ticket bid - 1 - q - 64 m in window m; the
+// window is consumed up to its nearest inclusive prefix once every word up
+// to that one is ready. Every predecessor is already running and publishes
+// its aggregate before it waits on anything, so each wait ends; the spin
+// bound only turns a broken invariant into an error flag (checked by the
+// host) instead of a hang.
+__device__ uint32_t wave_look_back(uint64_t* status, uint32_t bid, uint32_t total, uint32_t epoch, uint32_t* err) {
+    const uint32_t lane = lane_id();
+    if (lane == 0) store_status(status + bid, status_word(bid == 0 ? kFlagPrefix : kFlagAggregate, epoch, total));
+    if (bid == 0) return 0;
+    const uint32_t ep = epoch & kEpochMask;
+    uint32_t excl = 0, spins = 0;
+    int64_t j = (int64_t)bid - 1;
+    while (true) {
+        const int64_t src = j - (int64_t)lane;
+        const uint64_t v = src >= 0 ? load_status(status + src) : kFlagPrefix;   // before ticket 0: prefix 0
+        const uint64_t fl = v & kFlagMask;
+        const bool ready = fl != 0 && (src < 0 || ((uint32_t)(v >> 32) & kEpochMask) == ep);
+        const uint64_t pm = ballot(ready && fl == kFlagPrefix);
+        const uint64_t rm = ballot(ready);
+        const uint32_t first = pm ? (uint32_t)__builtin_ctzll(pm) : 64u;
+        const uint64_t need = first >= 63u ? ~0ull : ((2ull << first) - 1ull);
+        if ((rm & need) == need) {
+            excl += wave_sum_u32(lane <= first ? (uint32_t)v : 0u);
+            if (first < 64u) break;
+            j -= 64;
+            continue;
+        }
+        if (++spins > kSpinLimit) {
+            if (lane == 0) atomicOr(err, 1u);
+            break;
+        }
+        __builtin_amdgcn_s_sleep(1);
+    }
+    if (lane == 0) store_status(status + bid, status_word(kFlagPrefix, epoch, excl + total));
+    return excl;
+}
 
 __device__ __forceinline__ int64_t resolve_n(const uint32_t* d_n, int64_t max_n) {
     return d_n ? (int64_t)min((int64_t)*d_n, max_n) : max_n;
 }
 
-// phase 1: per-chunk sums
-template <class Load>
-__global__ void __launch_bounds__(kScanThreads) scan_reduce_kernel(Load load, const uint32_t* d_n, int64_t max_n,
-                                                                   uint32_t* block_sums) {
-    __shared__ uint32_t s_wave[4];
-    const int64_t n = resolve_n(d_n, max_n);
-    const int64_t base = (int64_t)blockIdx.x * kScanChunk;
-    uint32_t acc = 0;
-    for (int k = 0; k < kScanItems; ++k) {
-        const int64_t i = base + (int64_t)k * kScanThreads + threadIdx.x;
-        if (i < n) acc += load(i);
+// Ballot match of an n-bit digit: lanes of the wave with the same digit
+// (among `valid` lanes).
+__device__ __forceinline__ uint64_t match_digit(uint32_t d, int bits, bool valid) {
+    uint64_t peers = ballot(valid);
+    for (int b = 0; b < bits; ++b) {
+        const bool bit = (d >> b) & 1u;
+        const uint64_t m = ballot(bit);
+        peers &= bit ? m : ~m;
     }
-    uint32_t total;
-    block_exclusive_scan(acc, s_wave, &total);
-    if (threadIdx.x == 0) block_sums[blockIdx.x] = total;
+    return peers;
 }
 
-// phase 2: exclusive scan of the block sums in place (one workgroup), total
-__global__ void __launch_bounds__(kScanThreads) scan_partials_kernel(uint32_t* block_sums, uint32_t nblocks,
-                                                                     uint32_t* d_total) {
-    __shared__ uint32_t s_wave[4];
-    uint32_t carry = 0;
-    for (uint32_t base = 0; base < nblocks; base += kScanThreads) {
-        const uint32_t i = base + threadIdx.x;
-        const uint32_t v = i < nblocks ? block_sums[i] : 0u;
-        uint32_t total;
-        const uint32_t ex = block_exclusive_scan(v, s_wave, &total);
-        if (i < nblocks) block_sums[i] = carry + ex;
-        carry += total;
-    }
-    if (threadIdx.x == 0 && d_total) *d_total = carry;
-}
+// ---------------------------------------------------------------- compaction
 
-// phase 3: blocked per-thread scan of 16 consecutive items + workgroup scan
-template <class Load, class Store>
-__global__ void __launch_bounds__(kScanThreads) scan_apply_kernel(Load load, Store store, const uint32_t* d_n,
-                                                                  int64_t max_n, const uint32_t* block_offsets) {
-    __shared__ uint32_t s_wave[4];
-    const int64_t n = resolve_n(d_n, max_n);
-    const int64_t base = (int64_t)blockIdx.x * kScanChunk + (int64_t)threadIdx.x * kScanItems;
-    uint32_t vals[kScanItems];
-    uint32_t acc = 0;
+// Visible primitives (n_touched > 0) in index order -> (depth key, index,
+// n_touched) triples; V; I = sum of n_touched.
+__global__ void __launch_bounds__(kThreads) compact_kernel(const uint32_t* __restrict__ n_touched,
+                                                           const uint32_t* __restrict__ depth_key, int64_t n,
+                                                           uint32_t* __restrict__ keys_out,
+                                                           uint32_t* __restrict__ vals_out,
+                                                           uint32_t* __restrict__ nt_out, BinCtl* ctl,
+                                                           uint64_t* status, uint32_t epoch) {
+    __shared__ uint32_t s_rw[64];
+    __shared__ uint32_t s_nt[4];
+    __shared__ uint32_t s_bid, s_base;
+    const uint32_t t = threadIdx.x, lane = t & 63u, w = t >> 6;
+    const uint32_t bid = take_ticket(&ctl->tickets[kTicketCompact], &s_bid);
+    const int64_t base = (int64_t)bid * kScanChunk + t;
+    uint32_t key[kScanRounds], nt[kScanRounds], vis[kScanRounds], ex[kScanRounds];
+    uint32_t ntsum = 0;
 #pragma unroll
-    for (int k = 0; k < kScanItems; ++k) {
-        const int64_t i = base + k;
-        vals[k] = i < n ? load(i) : 0u;
-        acc += vals[k];
+    for (int r = 0; r < kScanRounds; ++r) {
+        const int64_t i = base + (int64_t)r * kThreads;
+        nt[r] = i < n ? n_touched[i] : 0u;
+        key[r] = i < n ? depth_key[i] : 0u;
     }
-    uint32_t total;
-    uint32_t run = block_exclusive_scan(acc, s_wave, &total) + block_offsets[blockIdx.x];
 #pragma unroll
-    for (int k = 0; k < kScanItems; ++k) {
-        const int64_t i = base + k;
-        if (i < n) store(i, run, vals[k]);
-        run += vals[k];
+    for (int r = 0; r < kScanRounds; ++r) {
+        vis[r] = nt[r] > 0u ? 1u : 0u;
+        ntsum += nt[r];
     }
-}
-
-struct StoreCompact {
-    const uint32_t* depth_key;
-    uint32_t* keys_out;
-    uint32_t* vals_out;
-    __device__ void operator()(int64_t i, uint32_t pos, uint32_t flag) const {
-        if (flag) {
-            keys_out[pos] = depth_key[i];
-            vals_out[pos] = (uint32_t)i;
+    const uint32_t wnt = wave_sum_u32(ntsum);
+    if (lane == 0) s_nt[w] = wnt;
+    uint32_t total;
+    striped_scan16(vis, ex, &total, s_rw);   // barriers inside: s_nt visible after it
+    if (w == 0) {
+        const uint32_t excl = wave_look_back(status, bid, total, epoch, &ctl->err);
+        if (lane == 0) {
+            s_base = excl;
+            if ((int64_t)(bid + 1) * kScanChunk >= n) ctl->V = excl + total;
+            const uint32_t bsum = s_nt[0] + s_nt[1] + s_nt[2] + s_nt[3];
+            if (bsum) atomicAdd(&ctl->I, bsum);
         }
     }
-};
-struct StorePlain {
-    uint32_t* out;
-    __device__ void operator()(int64_t i, uint32_t pos, uint32_t) const { out[i] = pos; }
-};
-
-static inline uint32_t n_chunks(int64_t n) { return (uint32_t)((n + kScanChunk - 1) / kScanChunk); }
-
-size_t scan_temp_bytes(int64_t n) { return sizeof(uint32_t) * ((size_t)n_chunks(n) + 64); }
-
-template <class Load, class Store>
-static void scan3(Load load, Store store, const uint32_t* d_n, int64_t max_n, uint32_t* d_total, uint32_t* temp,
-                  hipStream_t s) {
-    const uint32_t nb = n_chunks(max_n);
-    if (nb == 0) {
-        if (d_total) launch_fill_u32(d_total, 0u, 1, s);
-        return;
+    __syncthreads();
+    const uint32_t b0 = s_base;
+#pragma unroll
+    for (int r = 0; r < kScanRounds; ++r) {
+        if (vis[r]) {
+            const uint32_t pos = b0 + ex[r];
+            keys_out[pos] = key[r];
+            vals_out[pos] = (uint32_t)(base + (int64_t)r * kThreads);
+            nt_out[pos] = nt[r];
+        }
     }
-    scan_reduce_kernel<<<nb, kScanThreads, 0, s>>>(load, d_n, max_n, temp);
-    scan_partials_kernel<<<1, kScanThreads, 0, s>>>(temp, nb, d_total);
-    scan_apply_kernel<<<nb, kScanThreads, 0, s>>>(load, store, d_n, max_n, temp);
 }
 
 void launch_compact_visible(const uint32_t* n_touched, const uint32_t* depth_key, int64_t n, uint32_t* keys_out,
-                            uint32_t* vals_out, uint32_t* d_count, uint32_t* temp, hipStream_t s) {
-    scan3(LoadVisible{n_touched}, StoreCompact{depth_key, keys_out, vals_out}, nullptr, n, d_count, temp, s);
+                            uint32_t* vals_out, uint32_t* nt_out, BinCtl* ctl, uint64_t* status, uint32_t& epoch,
+                            hipStream_t s) {
+    if (n <= 0) return;
+    const uint32_t nb = (uint32_t)((n + kScanChunk - 1) / kScanChunk);
+    compact_kernel<<<nb, kThreads, 0, s>>>(n_touched, depth_key, n, keys_out, vals_out, nt_out, ctl, status, ++epoch);
 }
 
-void launch_instance_offsets(const uint32_t* n_touched, const uint32_t* prims, const uint32_t* d_count,
-                             int64_t max_count, uint32_t* offsets, uint32_t* d_total, uint32_t* temp, hipStream_t s) {
-    scan3(LoadTouchedByPrim{n_touched, prims}, StorePlain{offsets}, d_count, max_count, d_total, temp, s);
-}
+// ---------------------------------------------------------------- instance offsets
 
-// ---------------------------------------------------------------- radix sort
-
-constexpr int kRadixBits = 8;
-constexpr int kRadixBins = 256;
-constexpr int kRadixRounds = 16;
-constexpr int kRadixChunk = 256 * kRadixRounds;  // 4096 keys per workgroup
-
-__global__ void __launch_bounds__(256) radix_hist_kernel(const uint32_t* __restrict__ keys, const uint32_t* d_n,
-                                                         int64_t max_n, int shift, uint32_t* __restrict__ hist,
-                                                         uint32_t nblocks) {
-    __shared__ uint32_t s_hist[4][kRadixBins];
-    const uint32_t w = threadIdx.x >> 6;
-    for (int k = threadIdx.x; k < 4 * kRadixBins; k += 256) (&s_hist[0][0])[k] = 0;
-    __syncthreads();
-    const int64_t n = resolve_n(d_n, max_n);
-    const int64_t base = (int64_t)blockIdx.x * kRadixChunk;
-    for (int r = 0; r < kRadixRounds; ++r) {
-        const int64_t i = base + (int64_t)r * 256 + threadIdx.x;
-        if (i < n) atomicAdd(&s_hist[w][(keys[i] >> shift) & 0xffu], 1u);
+// offs[k] = exclusive scan of nt[k] (n_touched in depth order) over k < V;
+// offs[V] = the total.
+__global__ void __launch_bounds__(kThreads) offsets_kernel(const uint32_t* __restrict__ nt, int64_t max_count,
+                                                           uint32_t* __restrict__ offs, BinCtl* ctl,
+                                                           uint64_t* status, uint32_t epoch) {
+    __shared__ uint32_t s_rw[64];
+    __shared__ uint32_t s_bid, s_base;
+    const uint32_t t = threadIdx.x, lane = t & 63u, w = t >> 6;
+    const uint32_t bid = take_ticket(&ctl->tickets[kTicketOffsets], &s_bid);
+    const int64_t n = resolve_n(&ctl->V, max_count);
+    if ((int64_t)bid * kScanChunk >= n) return;
+    const int64_t base = (int64_t)bid * kScanChunk + t;
+    uint32_t c[kScanRounds], ex[kScanRounds];
+#pragma unroll
+    for (int r = 0; r < kScanRounds; ++r) {
+        const int64_t i = base + (int64_t)r * kThreads;
+        c[r] = i < n ? nt[i] : 0u;
     }
-    __syncthreads();
-    const uint32_t d = threadIdx.x;
-    hist[(size_t)d * nblocks + blockIdx.x] = s_hist[0][d] + s_hist[1][d] + s_hist[2][d] + s_hist[3][d];
-}
-
-// Stable scatter of one 8-bit digit. Wave w of the workgroup owns keys
-// [w * 1024, (w + 1) * 1024) of the workgroup's 4096-key chunk and ranks them
-// in 16 rounds of 64 with ballot matching against a wave-private LDS
-// histogram (a wave's LDS operations complete in issue order, so no barrier
-// is needed between rounds). One barrier then turns the four private
-// histograms into per-wave bases, and every key is written to
-// global offset(digit, workgroup) + wave base + rank within the wave.
-__global__ void __launch_bounds__(256) radix_scatter_kernel(const uint32_t* __restrict__ keys_in,
-                                                            const uint32_t* __restrict__ vals_in,
-                                                            uint32_t* __restrict__ keys_out,
-                                                            uint32_t* __restrict__ vals_out, const uint32_t* d_n,
-                                                            int64_t max_n, int shift,
-                                                            const uint32_t* __restrict__ offsets, uint32_t nblocks) {
-    __shared__ uint32_t s_cnt[4][kRadixBins];
-    const uint32_t lane = threadIdx.x & 63u, w = threadIdx.x >> 6, t = threadIdx.x;
-    const int64_t n = resolve_n(d_n, max_n);
-    const int64_t blk = (int64_t)blockIdx.x * kRadixChunk;
-    if (blk >= n) return;
-    for (int k = t; k < 4 * kRadixBins; k += 256) (&s_cnt[0][0])[k] = 0;
-    const uint32_t gofs = offsets[(size_t)t * nblocks + blockIdx.x];
-    __syncthreads();
-    const int64_t base = blk + (int64_t)w * (kRadixChunk / 4);
-    uint32_t key[kRadixRounds], val[kRadixRounds], pos[kRadixRounds];
-#pragma unroll
-    for (int r = 0; r < kRadixRounds; ++r) {
-        const int64_t i = base + (int64_t)r * 64 + lane;
-        const bool valid = i < n;
-        key[r] = valid ? keys_in[i] : 0u;
-        val[r] = valid ? vals_in[i] : 0u;
-    }
-#pragma unroll
-    for (int r = 0; r < kRadixRounds; ++r) {
-        const int64_t i = base + (int64_t)r * 64 + lane;
-        const bool valid = i < n;
-        const uint32_t d = (key[r] >> shift) & 0xffu;
-        uint64_t peers = ballot(valid);
-#pragma unroll
-        for (int b = 0; b < kRadixBits; ++b) {
-            const bool bit = (d >> b) & 1u;
-            const uint64_t m = ballot(bit);
-            peers &= bit ? m : ~m;
+    uint32_t total;
+    striped_scan16(c, ex, &total, s_rw);
+    if (w == 0) {
+        const uint32_t excl = wave_look_back(status, bid, total, epoch, &ctl->err);
+        if (lane == 0) {
+            s_base = excl;
+            if ((int64_t)(bid + 1) * kScanChunk >= n) offs[n] = excl + total;
         }
+    }
+    __syncthreads();
+    const uint32_t b0 = s_base;
+#pragma unroll
+    for (int r = 0; r < kScanRounds; ++r) {
+        const int64_t i = base + (int64_t)r * kThreads;
+        if (i < n) offs[i] = b0 + ex[r];
+    }
+}
+
+void launch_instance_offsets(const uint32_t* nt_sorted, int64_t max_count, uint32_t* offs, BinCtl* ctl,
+                             uint64_t* status, uint32_t& epoch, hipStream_t s) {
+    if (max_count <= 0) return;
+    const uint32_t nb = (uint32_t)((max_count + kScanChunk - 1) / kScanChunk);
+    offsets_kernel<<<nb, kThreads, 0, s>>>(nt_sorted, max_count, offs, ctl, status, ++epoch);
+}
+
+int64_t scan_status_entries(int64_t max_n) { return (max_n + kScanChunk - 1) / kScanChunk; }
+
+// ---------------------------------------------------------------- radix sort (reduce-then-scan)
+
+// Wave w of a workgroup owns 64 * KPT consecutive keys: round r, lane l is
+// key blk + w * 64 * KPT + r * 64 + l. Digit ranks come from ballot matching
+// against a wave-private LDS histogram (a wave's LDS operations complete in
+// issue order, so rounds need no barrier).
+template <int KPT>
+__device__ __forceinline__ void rank_keys(const uint32_t key[KPT], int64_t base, int64_t n, int shift, int bits,
+                                          uint32_t (*s_cnt)[256], uint32_t pos[KPT]) {
+    const uint32_t lane = threadIdx.x & 63u, w = threadIdx.x >> 6;
+    const uint32_t dmask = (1u << bits) - 1u;
+#pragma unroll
+    for (int r = 0; r < KPT; ++r) {
+        const bool valid = base + (int64_t)r * 64 + lane < n;
+        const uint32_t d = (key[r] >> shift) & dmask;
+        const uint64_t peers = match_digit(d, bits, valid);
         const uint32_t rank = mask_rank(peers);
         const uint32_t running = s_cnt[w][d];
         pos[r] = running + rank;
         if (valid && rank == 0u) s_cnt[w][d] = running + (uint32_t)__builtin_popcountll(peers);
     }
+}
+
+// Per-workgroup digit counts: counts[d * nb + b] (digit-major). Workgroups
+// past the end write zeros.
+template <int KPT>
+__global__ void __launch_bounds__(kThreads) radix_upsweep_kernel(const uint32_t* __restrict__ keys,
+                                                                 const uint32_t* d_n, int64_t max_n, int shift,
+                                                                 int bits, uint32_t* __restrict__ counts,
+                                                                 uint32_t nb) {
+    __shared__ uint32_t s_cnt[4][256];
+    const uint32_t t = threadIdx.x, lane = t & 63u, w = t >> 6;
+    const uint32_t bins = 1u << bits;
+    for (int k = t; k < 4 * 256; k += kThreads) (&s_cnt[0][0])[k] = 0;
     __syncthreads();
-    {
-        const uint32_t c0 = s_cnt[0][t], c1 = s_cnt[1][t], c2 = s_cnt[2][t];
-        s_cnt[0][t] = gofs;
-        s_cnt[1][t] = gofs + c0;
-        s_cnt[2][t] = gofs + c0 + c1;
-        s_cnt[3][t] = gofs + c0 + c1 + c2;
+    const int64_t n = resolve_n(d_n, max_n);
+    const int64_t base = (int64_t)blockIdx.x * (kThreads * KPT) + (int64_t)w * (64 * KPT);
+    uint32_t key[KPT], pos[KPT];
+#pragma unroll
+    for (int r = 0; r < KPT; ++r) {
+        const int64_t i = base + (int64_t)r * 64 + lane;
+        key[r] = i < n ? keys[i] : 0u;
+    }
+    rank_keys<KPT>(key, base, n, shift, bits, s_cnt, pos);
+    __syncthreads();
+    if (t < bins) counts[(size_t)t * nb + blockIdx.x] = s_cnt[0][t] + s_cnt[1][t] + s_cnt[2][t] + s_cnt[3][t];
+}
+
+// In-place exclusive scan of a u32 array of n elements (single pass,
+// decoupled look-back). Applied to the digit-major count matrix it yields
+// every (digit, workgroup) output offset: digit start + counts of earlier
+// workgroups for that digit.
+__global__ void __launch_bounds__(kThreads) exclusive_scan_kernel(uint32_t* __restrict__ data, int64_t n,
+                                                                  uint32_t* ticket, uint64_t* status, uint32_t epoch,
+                                                                  uint32_t* err) {
+    __shared__ uint32_t s_rw[64];
+    __shared__ uint32_t s_bid, s_base;
+    const uint32_t t = threadIdx.x, lane = t & 63u, w = t >> 6;
+    const uint32_t bid = take_ticket(ticket, &s_bid);
+    const int64_t base = (int64_t)bid * kScanChunk + t;
+    uint32_t c[kScanRounds], ex[kScanRounds];
+#pragma unroll
+    for (int r = 0; r < kScanRounds; ++r) {
+        const int64_t i = base + (int64_t)r * kThreads;
+        c[r] = i < n ? data[i] : 0u;
+    }
+    uint32_t total;
+    striped_scan16(c, ex, &total, s_rw);
+    if (w == 0) {
+        const uint32_t excl = wave_look_back(status, bid, total, epoch, err);
+        if (lane == 0) s_base = excl;
+    }
+    __syncthreads();
+    const uint32_t b0 = s_base;
+#pragma unroll
+    for (int r = 0; r < kScanRounds; ++r) {
+        const int64_t i = base + (int64_t)r * kThreads;
+        if (i < n) data[i] = b0 + ex[r];
+    }
+}
+
+// Ranked scatter of one pass: keys (and one or two u32 payloads) go to
+// offset(digit, workgroup) + rank within the workgroup's run of that digit.
+// The workgroup's keys are first placed in LDS in digit order and written
+// out by consecutive threads, so each store instruction covers contiguous
+// runs.
+template <int KPT, bool PAYLOAD2>
+__global__ void __launch_bounds__(kThreads) radix_downsweep_kernel(
+    const uint32_t* __restrict__ keys_in, const uint32_t* __restrict__ vals_in, const uint32_t* __restrict__ v2_in,
+    uint32_t* __restrict__ keys_out, uint32_t* __restrict__ vals_out, uint32_t* __restrict__ v2_out,
+    const uint32_t* d_n, int64_t max_n, int shift, int bits, const uint32_t* __restrict__ offsets, uint32_t nb) {
+    constexpr int kChunk = kThreads * KPT;
+    __shared__ uint32_t s_cnt[4][256];
+    __shared__ uint32_t s_gofs[256];
+    __shared__ uint32_t s_key[kChunk], s_val[kChunk], s_v2[PAYLOAD2 ? kChunk : 1];
+    __shared__ uint32_t s_wave[4];
+    const uint32_t t = threadIdx.x, lane = t & 63u, w = t >> 6;
+    const uint32_t bins = 1u << bits, dmask = bins - 1u;
+    const int64_t n = resolve_n(d_n, max_n);
+    const int64_t blk = (int64_t)blockIdx.x * kChunk;
+    if (blk >= n) return;
+    for (int k = t; k < 4 * 256; k += kThreads) (&s_cnt[0][0])[k] = 0;
+    const uint32_t gofs = t < bins ? offsets[(size_t)t * nb + blockIdx.x] : 0u;
+    __syncthreads();
+    const int64_t base = blk + (int64_t)w * (64 * KPT);
+    uint32_t key[KPT], val[KPT], v2[PAYLOAD2 ? KPT : 1], pos[KPT];
+#pragma unroll
+    for (int r = 0; r < KPT; ++r) {
+        const int64_t i = base + (int64_t)r * 64 + lane;
+        const bool valid = i < n;
+        key[r] = valid ? keys_in[i] : 0u;
+        val[r] = valid ? vals_in[i] : 0u;
+        if constexpr (PAYLOAD2) v2[r] = valid ? v2_in[i] : 0u;
+    }
+    rank_keys<KPT>(key, base, n, shift, bits, s_cnt, pos);
+    __syncthreads();
+    const uint32_t c0 = s_cnt[0][t], c1 = s_cnt[1][t], c2 = s_cnt[2][t];
+    const uint32_t total = t < bins ? c0 + c1 + c2 + s_cnt[3][t] : 0u;
+    uint32_t unused;
+    const uint32_t lstart = block_exclusive_scan(total, s_wave, &unused);   // digit start inside the workgroup
+    if (t < bins) {
+        s_gofs[t] = gofs - lstart;
+        s_cnt[0][t] = lstart;
+        s_cnt[1][t] = lstart + c0;
+        s_cnt[2][t] = lstart + c0 + c1;
+        s_cnt[3][t] = lstart + c0 + c1 + c2;
     }
     __syncthreads();
 #pragma unroll
-    for (int r = 0; r < kRadixRounds; ++r) {
-        const int64_t i = base + (int64_t)r * 64 + lane;
-        if (i < n) {
-            const uint32_t d = (key[r] >> shift) & 0xffu;
-            const uint32_t o = s_cnt[w][d] + pos[r];
-            keys_out[o] = key[r];
-            vals_out[o] = val[r];
+    for (int r = 0; r < KPT; ++r) {
+        if (base + (int64_t)r * 64 + lane < n) {
+            const uint32_t l = s_cnt[w][(key[r] >> shift) & dmask] + pos[r];
+            s_key[l] = key[r];
+            s_val[l] = val[r];
+            if constexpr (PAYLOAD2) s_v2[l] = v2[r];
+        }
+    }
+    __syncthreads();
+    const uint32_t cnt = (uint32_t)min((int64_t)kChunk, n - blk);
+    for (uint32_t i = t; i < cnt; i += kThreads) {
+        const uint32_t k = s_key[i];
+        const uint32_t o = s_gofs[(k >> shift) & dmask] + i;
+        if (o < (uint64_t)max_n) {   // always true when the counts match the keys
+            keys_out[o] = k;
+            vals_out[o] = s_val[i];
+            if constexpr (PAYLOAD2) v2_out[o] = s_v2[i];
         }
     }
 }
 
-size_t radix_temp_bytes(int64_t max_n) {
-    const size_t nb = (size_t)((max_n + kRadixChunk - 1) / kRadixChunk);
-    const size_t hist = nb * kRadixBins;
-    return sizeof(uint32_t) * (hist + (hist + kScanChunk - 1) / kScanChunk + 64);
+int64_t radix_count_entries(int64_t max_n, bool depth) {
+    const int64_t chunk = kThreads * (depth ? kDepthKeysPerThread : kTileKeysPerThread);
+    return ((max_n + chunk - 1) / chunk) * 256;
 }
 
-int radix_sort_pairs(uint32_t* keys[2], uint32_t* vals[2], const uint32_t* d_n, int64_t max_n, int end_bit,
-                     uint32_t* temp, hipStream_t s) {
-    const uint32_t nb = (uint32_t)((max_n + kRadixChunk - 1) / kRadixChunk);
-    if (nb == 0) return 0;
-    const int64_t hist_n = (int64_t)nb * kRadixBins;
-    uint32_t* hist = temp;
-    uint32_t* scan_tmp = temp + hist_n;
+template <int KPT>
+static int radix_passes(uint32_t* keys[2], uint32_t* vals[2], uint32_t* v2[2], const uint32_t* d_n, int64_t max_n,
+                        int n_passes, const int* shifts, const int* bits, uint32_t* counts, uint32_t* tickets,
+                        uint64_t* status, uint32_t& epoch, uint32_t* err, hipStream_t s) {
     int cur = 0;
-    for (int shift = 0; shift < end_bit; shift += kRadixBits) {
-        radix_hist_kernel<<<nb, 256, 0, s>>>(keys[cur], d_n, max_n, shift, hist, nb);
-        scan3(LoadPlain{hist}, StorePlain{hist}, nullptr, hist_n, nullptr, scan_tmp, s);
-        radix_scatter_kernel<<<nb, 256, 0, s>>>(keys[cur], vals[cur], keys[cur ^ 1], vals[cur ^ 1], d_n, max_n,
-                                                shift, hist, nb);
+    if (max_n <= 0) return cur;
+    const uint32_t nb = (uint32_t)((max_n + kThreads * KPT - 1) / (kThreads * KPT));
+    for (int p = 0; p < n_passes; ++p) {
+        const int64_t cn = (int64_t)nb << bits[p];
+        radix_upsweep_kernel<KPT><<<nb, kThreads, 0, s>>>(keys[cur], d_n, max_n, shifts[p], bits[p], counts, nb);
+        exclusive_scan_kernel<<<(unsigned)((cn + kScanChunk - 1) / kScanChunk), kThreads, 0, s>>>(
+            counts, cn, tickets + p, status, ++epoch, err);
+        if (v2)
+            radix_downsweep_kernel<KPT, true><<<nb, kThreads, 0, s>>>(
+                keys[cur], vals[cur], v2[cur], keys[cur ^ 1], vals[cur ^ 1], v2[cur ^ 1], d_n, max_n, shifts[p],
+                bits[p], counts, nb);
+        else
+            radix_downsweep_kernel<KPT, false><<<nb, kThreads, 0, s>>>(
+                keys[cur], vals[cur], nullptr, keys[cur ^ 1], vals[cur ^ 1], nullptr, d_n, max_n, shifts[p], bits[p],
+                counts, nb);
         cur ^= 1;
     }
     return cur;
+}
+
+int radix_sort(uint32_t* keys[2], uint32_t* vals[2], uint32_t* v2[2], const uint32_t* d_n, int64_t max_n, bool depth,
+               int n_passes, const int* shifts, const int* bits, uint32_t* counts, uint32_t* tickets,
+               uint64_t* status, uint32_t& epoch, uint32_t* err, hipStream_t s) {
+    if (depth)
+        return radix_passes<kDepthKeysPerThread>(keys, vals, v2, d_n, max_n, n_passes, shifts, bits, counts, tickets,
+                                                 status, epoch, err, s);
+    return radix_passes<kTileKeysPerThread>(keys, vals, v2, d_n, max_n, n_passes, shifts, bits, counts, tickets,
+                                            status, epoch, err, s);
 }
 
 // ---------------------------------------------------------------- instance emission
@@ -307,34 +486,49 @@ __device__ __forceinline__ bool will_contribute_e(float mx, float my, float ca, 
     return max_power <= power_threshold;
 }
 
-__global__ void __launch_bounds__(256) emit_kernel(const uint32_t* __restrict__ n_touched,
-                                                   const uint32_t* __restrict__ prims,
-                                                   const uint32_t* __restrict__ offsets, const uint32_t* d_count,
-                                                   int64_t max_count, const uint2* __restrict__ bounds,
-                                                   const float2* __restrict__ mean2d,
-                                                   const float4* __restrict__ conic_opacity,
-                                                   const float4* __restrict__ color_pt, uint32_t grid_w,
+// Thread per depth-sorted primitive: its 32-byte binning record is gathered
+// once (one aligned 32-byte read) and its instances fill the slots
+// [offs[k], offs[k + 1]), so the instance array comes out in depth order.
+// The workgroup's 256 primitives own one contiguous slot range; when it fits
+// in LDS the instances are staged there and written out by consecutive
+// threads (contiguous stores), otherwise written directly.
+constexpr uint32_t kEmitStage = 4096;
+
+__global__ void __launch_bounds__(256) emit_kernel(const uint32_t* __restrict__ prims,
+                                                   const uint32_t* __restrict__ offs, const BinCtl* ctl,
+                                                   int64_t max_count, const uint4* __restrict__ rec, uint32_t grid_w,
                                                    uint32_t* __restrict__ inst_keys,
                                                    uint32_t* __restrict__ inst_vals) {
-    const int64_t count = resolve_n(d_count, max_count);
-    const int64_t k = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if ((int64_t)blockIdx.x * blockDim.x >= count) return;  // whole workgroup idle
-    const bool active = k < count;
+    __shared__ uint32_t s_key[kEmitStage], s_val[kEmitStage];
+    const uint32_t t = threadIdx.x;
+    const int64_t n = min((int64_t)ctl->V, max_count);
+    const int64_t k0 = (int64_t)blockIdx.x * blockDim.x;
+    if (k0 >= n) return;
+    const uint32_t range_a = offs[k0], range_b = offs[min(k0 + (int64_t)blockDim.x, n)];
+    const bool staged = range_b - range_a <= kEmitStage;
+    auto put = [&](uint32_t pos, uint32_t tile, uint32_t prim) {
+        if (staged) {
+            s_key[pos - range_a] = tile;
+            s_val[pos - range_a] = prim;
+        } else {
+            inst_keys[pos] = tile;
+            inst_vals[pos] = prim;
+        }
+    };
+    const int64_t k = k0 + t;
+    const bool active = k < n;
     const uint32_t lane = lane_id();
     uint32_t p = 0, off = 0, cap = 0, x0 = 0, x1 = 0, y0 = 0, y1 = 0;
     float smx = 0.f, smy = 0.f, ca = 0.f, cb = 0.f, cc = 0.f, pt = 0.f;
     if (active) {
         p = prims[k];
-        off = offsets[k];
-        cap = n_touched[p];   // slots reserved for this primitive
-        const uint2 b = bounds[p];
-        x0 = b.x & 0xffffu; x1 = b.x >> 16; y0 = b.y & 0xffffu; y1 = b.y >> 16;
-        const float2 m = mean2d[p];
-        smx = m.x - 0.5f;
-        smy = m.y - 0.5f;
-        const float4 co = conic_opacity[p];
-        ca = co.x; cb = co.y; cc = co.z;
-        pt = color_pt[p].w;
+        off = offs[k];
+        cap = offs[k + 1] - off;   // slots reserved for this primitive (= its n_touched)
+        const uint4 r0 = rec[2 * (size_t)p], r1 = rec[2 * (size_t)p + 1];
+        x0 = r0.x & 0xffffu; x1 = r0.x >> 16; y0 = r0.y & 0xffffu; y1 = r0.y >> 16;
+        smx = u2f(r0.z) - 0.5f;
+        smy = u2f(r0.w) - 0.5f;
+        ca = u2f(r1.x); cb = u2f(r1.y); cc = u2f(r1.z); pt = u2f(r1.w);
     }
     const uint32_t bw = x1 - x0;
     const uint32_t nrect = bw * (y1 - y0);
@@ -344,8 +538,7 @@ __global__ void __launch_bounds__(256) emit_kernel(const uint32_t* __restrict__ 
         for (uint32_t q = 0; q < first; ++q) {
             const uint32_t tx = x0 + q % bw, ty = y0 + q / bw;
             if (will_contribute_e(smx, smy, ca, cb, cc, tx, ty, pt) && written < cap) {
-                inst_keys[off + written] = ty * grid_w + tx;
-                inst_vals[off + written] = p;
+                put(off + written, ty * grid_w + tx, p);
                 ++written;
             }
         }
@@ -373,23 +566,25 @@ __global__ void __launch_bounds__(256) emit_kernel(const uint32_t* __restrict__ 
             }
             const uint64_t m = ballot(hit);
             const uint32_t pos = s_off + mask_rank(m);
-            if (hit && pos < s_end) {
-                inst_keys[pos] = ty * grid_w + tx;
-                inst_vals[pos] = s_p;
-            }
+            if (hit && pos < s_end) put(pos, ty * grid_w + tx, s_p);
             s_off += (uint32_t)__builtin_popcountll(m);
+        }
+    }
+    if (staged) {
+        __syncthreads();
+        for (uint32_t i = t; i < range_b - range_a; i += blockDim.x) {
+            inst_keys[range_a + i] = s_key[i];
+            inst_vals[range_a + i] = s_val[i];
         }
     }
 }
 
-void launch_emit_instances(const uint32_t* n_touched, const uint32_t* prims, const uint32_t* offsets, const uint32_t* d_count, int64_t max_count,
-                           const uint2* bounds, const float2* mean2d, const float4* conic_opacity,
-                           const float4* color_pt, uint32_t grid_w, uint32_t* inst_keys, uint32_t* inst_vals,
+void launch_emit_instances(const uint32_t* prims, const uint32_t* offs, const BinCtl* ctl, int64_t max_count,
+                           const uint4* rec, uint32_t grid_w, uint32_t* inst_keys, uint32_t* inst_vals,
                            hipStream_t s) {
     if (max_count <= 0) return;
-    emit_kernel<<<(unsigned)((max_count + 255) / 256), 256, 0, s>>>(n_touched, prims, offsets, d_count, max_count, bounds, mean2d,
-                                                                   conic_opacity, color_pt, grid_w, inst_keys,
-                                                                   inst_vals);
+    emit_kernel<<<(unsigned)((max_count + 255) / 256), 256, 0, s>>>(prims, offs, ctl, max_count, rec, grid_w,
+                                                                    inst_keys, inst_vals);
 }
 
 // ---------------------------------------------------------------- ranges
@@ -399,32 +594,42 @@ __global__ void fill_u32_kernel(uint32_t* p, uint32_t v, int64_t n) {
     if (i < n) p[i] = v;
 }
 
+__global__ void bin_ctl_reset_kernel(uint32_t* p, uint32_t n_words, uint32_t keep) {
+    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n_words && i != keep) p[i] = 0u;
+}
+
+void launch_bin_ctl_reset(BinCtl* ctl, hipStream_t s) {
+    constexpr uint32_t words = sizeof(BinCtl) / 4;
+    bin_ctl_reset_kernel<<<(words + 255) / 256, 256, 0, s>>>((uint32_t*)ctl, words,
+                                                             (uint32_t)(offsetof(BinCtl, err) / 4));
+}
+
 void launch_fill_u32(uint32_t* p, uint32_t value, int64_t n, hipStream_t s) {
     if (n <= 0) return;
     fill_u32_kernel<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(p, value, n);
 }
 
-// kernels_forward.cuh:532-551
-__global__ void tile_ranges_kernel(const uint32_t* __restrict__ keys, int64_t n, uint2* __restrict__ ranges) {
+// kernels_forward.cuh:532-551, plus (0, 0) for the empty tiles: thread i
+// (0 <= i <= n) sits on the boundary between keys[i - 1] and keys[i]
+// (sentinels -1 and n_tiles), closes the previous tile's range, opens the
+// next one and clears the tiles strictly between them.
+__global__ void tile_ranges_kernel(const uint32_t* __restrict__ keys, int64_t n, uint2* __restrict__ ranges,
+                                   uint32_t n_tiles) {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= n) return;
-    const uint32_t t = keys[i];
-    if (i == 0) {
-        ranges[t].x = 0;
-    } else {
-        const uint32_t prev = keys[i - 1];
-        if (t != prev) {
-            ranges[prev].y = (uint32_t)i;
-            ranges[t].x = (uint32_t)i;
-        }
-    }
-    if (i == n - 1) ranges[t].y = (uint32_t)n;
+    if (i > n) return;
+    // keys are tile ids < n_tiles; min() keeps a corrupt key from writing out of range
+    const int64_t cur = i < n ? (int64_t)min(keys[i], n_tiles) : (int64_t)n_tiles;
+    const int64_t prev = i > 0 ? (int64_t)min(keys[i - 1], n_tiles) : -1;
+    if (prev == (int64_t)n_tiles) return;
+    if (cur == prev) return;
+    if (i > 0) ranges[prev].y = (uint32_t)i;
+    if (i < n) ranges[cur].x = (uint32_t)i;
+    for (int64_t tt = prev + 1; tt < cur; ++tt) ranges[tt] = make_uint2(0u, 0u);
 }
 
 void launch_tile_ranges(const uint32_t* inst_keys, int64_t n_inst, uint2* ranges, uint32_t n_tiles, hipStream_t s) {
-    launch_fill_u32((uint32_t*)ranges, 0u, 2 * (int64_t)n_tiles, s);
-    if (n_inst <= 0) return;
-    tile_ranges_kernel<<<(unsigned)((n_inst + 255) / 256), 256, 0, s>>>(inst_keys, n_inst, ranges);
+    tile_ranges_kernel<<<(unsigned)((n_inst + 1 + 255) / 256), 256, 0, s>>>(inst_keys, n_inst, ranges, n_tiles);
 }
 
 }  // namespace tgs

@@ -15,6 +15,7 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <algorithm>
 #include <string>
 #include <vector>
 
@@ -213,22 +214,40 @@ struct tgs_rasterizer {
     tgs_gaussians g{};
     bool has_g = false;
     // per primitive
-    DevBuf n_touched, bounds, mean2d, conic_opacity, color, depth_key, offsets;
-    DevBuf pkeys[2], pvals[2];
+    DevBuf n_touched, rec, mean2d, conic_opacity, color, depth_key, offs;
+    DevBuf pkeys[2], pvals[2], pnt[2];   // depth sort: key, primitive, n_touched
     // per instance
     DevBuf ikeys[2], ivals[2];
     // per tile / pixel
     DevBuf ranges, tile_max, n_contrib;
     // temp
-    DevBuf scan_tmp, radix_tmp, grad2d;
-    DevBuf counters;    // [0] V, [1] I (u32); [8..9] u64 work counters at byte 32
-    uint32_t* h_counters = nullptr;
+    DevBuf grad2d;
+    DevBuf radix_counts;   // per-workgroup digit counts of the radix passes
+    DevBuf bin_ctl;     // BinCtl (zeroed at creation; all but err cleared every forward)
+    hipEvent_t ev_counts = nullptr;   // recorded after the counts copy of a forward
+    DevBuf lb_status;   // look-back status words (u64), epoch-tagged
+    uint32_t epoch = 0; // last look-back epoch used on lb_status
+    DevBuf counters;    // u64 work counters at byte 32 (forward) and 40 (backward)
+    uint32_t* h_counters = nullptr;   // pinned copy of BinCtl {V, I, err}
     // state of the last forward
     bool fwd_done = false;
     CamParams cam{};
     int64_t n = 0, V = 0, I = 0;
     int psel = 0, isel = 0;
 };
+
+// Look-back status words for `entries` slots. A (re)allocated array is
+// cleared (all words "not ready"); the epoch restarts before it could wrap.
+static int ensure_status(tgs_rasterizer* r, int64_t entries, hipStream_t s) {
+    const void* before = r->lb_status.p;
+    TGS_TRY(ensure(r->lb_status, sizeof(uint64_t) * (size_t)(entries > 0 ? entries : 1), s));
+    const bool wrap = r->epoch > kEpochMask - 64u;
+    if (r->lb_status.p != before || wrap) {
+        launch_fill_u32(r->lb_status.as<uint32_t>(), 0u, (int64_t)(r->lb_status.bytes / 4), s);
+        if (wrap) r->epoch = 0;
+    }
+    return TGS_OK;
+}
 
 struct tgs_loss {
     int type = 0;  // 0 l1, 1 fused_ssim
@@ -264,11 +283,20 @@ int tgs_rasterizer_create(const char* type, tgs_rasterizer** out) {
         r->counters.bytes = 64;
         e = hipMemset(r->counters.p, 0, 64);
     }
+    if (e == hipSuccess) e = hipMalloc(&r->bin_ctl.p, sizeof(BinCtl));
+    if (e == hipSuccess) {
+        r->bin_ctl.bytes = sizeof(BinCtl);
+        e = hipMemset(r->bin_ctl.p, 0, sizeof(BinCtl));
+    }
+    if (e == hipSuccess) e = hipEventCreateWithFlags(&r->ev_counts, hipEventDisableTiming);
+    if (e == hipSuccess) e = hipDeviceSynchronize();
     if (e != hipSuccess) {
         if (r->h_counters) (void)hipHostFree(r->h_counters);
+        if (r->ev_counts) (void)hipEventDestroy(r->ev_counts);
         release(r->counters);
+        release(r->bin_ctl);
         delete r;
-        return fail(TGS_ERR_HIP, "counter allocation: %s", hipGetErrorString(e));
+        return fail(TGS_ERR_HIP, "rasterizer allocation: %s", hipGetErrorString(e));
     }
     *out = r;
     return TGS_OK;
@@ -277,12 +305,14 @@ int tgs_rasterizer_create(const char* type, tgs_rasterizer** out) {
 int tgs_rasterizer_destroy(tgs_rasterizer* r) {
     if (!r) return TGS_OK;
     (void)hipDeviceSynchronize();
-    DevBuf* all[] = {&r->n_touched, &r->bounds, &r->mean2d, &r->conic_opacity, &r->color, &r->depth_key,
-                     &r->offsets, &r->pkeys[0], &r->pkeys[1], &r->pvals[0], &r->pvals[1], &r->ikeys[0],
+    DevBuf* all[] = {&r->n_touched, &r->rec, &r->mean2d, &r->conic_opacity, &r->color, &r->depth_key,
+                     &r->offs, &r->pkeys[0], &r->pkeys[1], &r->pvals[0], &r->pvals[1], &r->pnt[0], &r->pnt[1],
+                     &r->radix_counts, &r->ikeys[0],
                      &r->ikeys[1], &r->ivals[0], &r->ivals[1], &r->ranges, &r->tile_max, &r->n_contrib,
-                     &r->scan_tmp, &r->radix_tmp, &r->grad2d, &r->counters};
+                     &r->grad2d, &r->bin_ctl, &r->lb_status, &r->counters};
     for (DevBuf* b : all) release(*b);
     if (r->h_counters) (void)hipHostFree(r->h_counters);
+    if (r->ev_counts) (void)hipEventDestroy(r->ev_counts);
     delete r;
     return TGS_OK;
 }
@@ -326,43 +356,54 @@ int tgs_rasterizer_forward(tgs_rasterizer* r, const tgs_camera* camera, void* im
     const size_t cs = (size_t)cam.tiled_w * cam.tiled_h * 64u;
     const int64_t nn = n > 0 ? n : 1;
     TGS_TRY(ensure(r->n_touched, 4 * nn, s));
-    TGS_TRY(ensure(r->bounds, 8 * nn, s));
+    TGS_TRY(ensure(r->rec, 32 * nn, s));
     TGS_TRY(ensure(r->mean2d, 8 * nn, s));
     TGS_TRY(ensure(r->conic_opacity, 16 * nn, s));
     TGS_TRY(ensure(r->color, 16 * nn, s));
     TGS_TRY(ensure(r->depth_key, 4 * nn, s));
-    TGS_TRY(ensure(r->offsets, 4 * nn, s));
+    TGS_TRY(ensure(r->offs, 4 * (nn + 1), s));
     for (int k = 0; k < 2; ++k) {
         TGS_TRY(ensure(r->pkeys[k], 4 * nn, s));
         TGS_TRY(ensure(r->pvals[k], 4 * nn, s));
+        TGS_TRY(ensure(r->pnt[k], 4 * nn, s));
     }
     TGS_TRY(ensure(r->ranges, 8 * (size_t)T, s));
     TGS_TRY(ensure(r->tile_max, 4 * (size_t)T, s));
     TGS_TRY(ensure(r->n_contrib, 4 * cs, s));
-    TGS_TRY(ensure(r->scan_tmp, scan_temp_bytes(nn), s));
-    TGS_TRY(ensure(r->radix_tmp, radix_temp_bytes(nn), s));
+    TGS_TRY(ensure(r->radix_counts, 4 * (size_t)radix_count_entries(nn, true), s));
+    TGS_TRY(ensure_status(r, std::max(scan_status_entries(nn), scan_status_entries(radix_count_entries(nn, true))), s));
 
     GaussianView gv = view_of(r->g);
-    uint32_t* d_cnt = r->counters.as<uint32_t>();
+    BinCtl* ctl = r->bin_ctl.as<BinCtl>();
+    uint64_t* status = r->lb_status.as<uint64_t>();
+    launch_bin_ctl_reset(ctl, s);
     {
         StageScope sc(ST_PRE, s);
-        launch_preprocess(gv, cam, r->n_touched.as<uint32_t>(), r->bounds.as<uint2>(), r->mean2d.as<float2>(),
+        launch_preprocess(gv, cam, r->n_touched.as<uint32_t>(), r->rec.as<uint4>(), r->mean2d.as<float2>(),
                           r->conic_opacity.as<float4>(), r->color.as<float4>(), r->depth_key.as<uint32_t>(),
                           (float*)densification_info, s);
     }
     TGS_CHECK_LAUNCH();
-    StageScope* depth_scope = new StageScope(ST_DEPTH, s);
-    launch_compact_visible(r->n_touched.as<uint32_t>(), r->depth_key.as<uint32_t>(), n, r->pkeys[0].as<uint32_t>(),
-                           r->pvals[0].as<uint32_t>(), d_cnt + 0, r->scan_tmp.as<uint32_t>(), s);
     uint32_t* pk[2] = {r->pkeys[0].as<uint32_t>(), r->pkeys[1].as<uint32_t>()};
     uint32_t* pv[2] = {r->pvals[0].as<uint32_t>(), r->pvals[1].as<uint32_t>()};
-    const int psel = radix_sort_pairs(pk, pv, d_cnt + 0, n, 32, r->radix_tmp.as<uint32_t>(), s);
-    launch_instance_offsets(r->n_touched.as<uint32_t>(), pv[psel], d_cnt + 0, n, r->offsets.as<uint32_t>(), d_cnt + 1,
-                            r->scan_tmp.as<uint32_t>(), s);
-    delete depth_scope;
+    uint32_t* pn[2] = {r->pnt[0].as<uint32_t>(), r->pnt[1].as<uint32_t>()};
+    int psel;
+    {
+        StageScope sc(ST_DEPTH, s);
+        launch_compact_visible(r->n_touched.as<uint32_t>(), r->depth_key.as<uint32_t>(), n, pk[0], pv[0], pn[0], ctl,
+                               status, r->epoch, s);
+        // V, I and the sticky error flag go to the host while the depth sort runs
+        TGS_HIP(hipMemcpyAsync(r->h_counters, ctl, 3 * sizeof(uint32_t), hipMemcpyDeviceToHost, s));
+        TGS_HIP(hipEventRecord(r->ev_counts, s));
+        const int shifts[4] = {0, 8, 16, 24}, bits[4] = {8, 8, 8, 8};
+        psel = radix_sort(pk, pv, pn, &ctl->V, n, true, 4, shifts, bits, r->radix_counts.as<uint32_t>(),
+                          ctl->tickets + kTicketDepth, status, r->epoch, &ctl->err, s);
+        launch_instance_offsets(pn[psel], n, r->offs.as<uint32_t>(), ctl, status, r->epoch, s);
+    }
     TGS_CHECK_LAUNCH();
-    TGS_HIP(hipMemcpyAsync(r->h_counters, d_cnt, 2 * sizeof(uint32_t), hipMemcpyDeviceToHost, s));
-    TGS_HIP(hipStreamSynchronize(s));
+    TGS_HIP(hipEventSynchronize(r->ev_counts));
+    if (r->h_counters[2]) return fail(TGS_ERR_STATE, "binning look-back did not complete (error flag %u)",
+                                      r->h_counters[2]);
     const int64_t V = r->h_counters[0];
     const int64_t I = r->h_counters[1];
     const int64_t ii = I > 0 ? I : 1;
@@ -370,22 +411,28 @@ int tgs_rasterizer_forward(tgs_rasterizer* r, const tgs_camera* camera, void* im
         TGS_TRY(ensure(r->ikeys[k], 4 * ii, s));
         TGS_TRY(ensure(r->ivals[k], 4 * ii, s));
     }
-    TGS_TRY(ensure(r->radix_tmp, radix_temp_bytes(ii > nn ? ii : nn), s));
-    {
-        StageScope sc(ST_EMIT, s);
-        launch_emit_instances(r->n_touched.as<uint32_t>(), pv[psel], r->offsets.as<uint32_t>(), d_cnt + 0, n,
-                              r->bounds.as<uint2>(), r->mean2d.as<float2>(), r->conic_opacity.as<float4>(),
-                              r->color.as<float4>(), cam.grid_w, r->ikeys[0].as<uint32_t>(),
-                              r->ivals[0].as<uint32_t>(), s);
-    }
+    TGS_TRY(ensure(r->radix_counts, 4 * (size_t)std::max(radix_count_entries(ii, false), radix_count_entries(nn, true)),
+                   s));
+    TGS_TRY(ensure_status(r, scan_status_entries(radix_count_entries(ii, false)), s));
+    status = r->lb_status.as<uint64_t>();
+    // tile key bits: one pass up to 8 bits, else two passes of ceil(bits/2) and the rest
     int bits = 1;
     while ((1u << bits) < T) ++bits;
+    const int n_tile_passes = bits <= 8 ? 1 : 2;
+    const int tbits[2] = {n_tile_passes == 1 ? bits : (bits + 1) / 2, bits - (bits + 1) / 2};
+    const int tshifts[2] = {0, tbits[0]};
+    {
+        StageScope sc(ST_EMIT, s);
+        launch_emit_instances(pv[psel], r->offs.as<uint32_t>(), ctl, n, r->rec.as<uint4>(), cam.grid_w,
+                              r->ikeys[0].as<uint32_t>(), r->ivals[0].as<uint32_t>(), s);
+    }
     uint32_t* ik[2] = {r->ikeys[0].as<uint32_t>(), r->ikeys[1].as<uint32_t>()};
     uint32_t* iv[2] = {r->ivals[0].as<uint32_t>(), r->ivals[1].as<uint32_t>()};
     int isel;
     {
         StageScope sc(ST_TILES, s);
-        isel = radix_sort_pairs(ik, iv, nullptr, I, bits, r->radix_tmp.as<uint32_t>(), s);
+        isel = radix_sort(ik, iv, nullptr, nullptr, I, false, n_tile_passes, tshifts, tbits,
+                          r->radix_counts.as<uint32_t>(), ctl->tickets + kTicketTile, status, r->epoch, &ctl->err, s);
         launch_tile_ranges(ik[isel], I, r->ranges.as<uint2>(), T, s);
     }
     {
@@ -458,7 +505,7 @@ int tgs_rasterizer_debug_view(tgs_rasterizer* r, tgs_debug_view* out) {
     if (!r || !out) return fail(TGS_ERR_INVALID, "NULL argument");
     if (!r->fwd_done) return fail(TGS_ERR_STATE, "no forward yet");
     out->n_touched = r->n_touched.as<uint32_t>();
-    out->bounds = r->bounds.as<uint32_t>();
+    out->bounds = r->rec.as<uint32_t>();
     out->mean2d = r->mean2d.as<float>();
     out->conic_opacity = r->conic_opacity.as<float>();
     out->color = r->color.as<float>();

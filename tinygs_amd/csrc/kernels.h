@@ -32,28 +32,51 @@ struct GradView {
 };
 
 // ---- preprocess (kernels_forward.cuh:157-412)
-void launch_preprocess(const GaussianView& g, const CamParams& cam, uint32_t* n_touched, uint2* bounds,
+// rec: 2 x uint4 per visible primitive: {x_min | x_max << 16, y_min | y_max << 16, mean2d.x, mean2d.y},
+// {conic a, b, c, ln(255 opacity)} (float bits).
+void launch_preprocess(const GaussianView& g, const CamParams& cam, uint32_t* n_touched, uint4* rec,
                        float2* mean2d, float4* conic_opacity, float4* color_pt, uint32_t* depth_key,
                        float* densif, hipStream_t s);
 
 // ---- scans / compaction / sort / binning
-size_t scan_temp_bytes(int64_t n);
-// exclusive scan of (n_touched[i] > 0) over [0, n); writes depth keys and
-// indices of visible primitives in index order; *d_count = V.
+// Device control block of the binning launches. Everything but `err` is
+// cleared at the start of every forward; err (look-back error flag) is
+// sticky so that a failure is reported by the next host check.
+enum { kTicketCompact = 0, kTicketOffsets = 1, kTicketDepth = 2, kTicketTile = 6, kTicketCount = 8 };
+struct BinCtl {
+    uint32_t V, I, err, pad;
+    uint32_t tickets[kTicketCount];
+};
+// Clears every BinCtl word except err.
+void launch_bin_ctl_reset(BinCtl* ctl, hipStream_t s);
+constexpr uint32_t kEpochMask = 0x3fffffffu;   // 30-bit launch epoch of look-back status words
+
+// Status-word entries (u64) needed by a look-back scan over max_n elements.
+int64_t scan_status_entries(int64_t max_n);
+// Visible primitives (n_touched > 0) in index order -> (depth key, index,
+// n_touched) triples; ctl->V, ctl->I; depth-key digit histograms.
 void launch_compact_visible(const uint32_t* n_touched, const uint32_t* depth_key, int64_t n, uint32_t* keys_out,
-                            uint32_t* vals_out, uint32_t* d_count, uint32_t* temp, hipStream_t s);
-// offsets[k] = exclusive scan of n_touched[prims[k]] over k < *d_count; *d_total = I.
-void launch_instance_offsets(const uint32_t* n_touched, const uint32_t* prims, const uint32_t* d_count,
-                             int64_t max_count, uint32_t* offsets, uint32_t* d_total, uint32_t* temp, hipStream_t s);
-// Stable LSD radix sort of (key, value) u32 pairs on bits [0, end_bit).
-// Ping-pongs between buffers; returns the index (0/1) holding the result.
-size_t radix_temp_bytes(int64_t max_n);
-int radix_sort_pairs(uint32_t* keys[2], uint32_t* vals[2], const uint32_t* d_n, int64_t max_n, int end_bit,
-                     uint32_t* temp, hipStream_t s);
-void launch_emit_instances(const uint32_t* n_touched, const uint32_t* prims, const uint32_t* offsets, const uint32_t* d_count, int64_t max_count,
-                           const uint2* bounds, const float2* mean2d, const float4* conic_opacity,
-                           const float4* color_pt, uint32_t grid_w, uint32_t* inst_keys, uint32_t* inst_vals,
+                            uint32_t* vals_out, uint32_t* nt_out, BinCtl* ctl, uint64_t* status, uint32_t& epoch,
+                            hipStream_t s);
+// offs[k] = exclusive scan of nt_sorted[k] over k < ctl->V; offs[V] = total.
+void launch_instance_offsets(const uint32_t* nt_sorted, int64_t max_count, uint32_t* offs, BinCtl* ctl,
+                             uint64_t* status, uint32_t& epoch, hipStream_t s);
+// Entries of the per-workgroup digit-count matrix of radix_sort.
+int64_t radix_count_entries(int64_t max_n, bool depth);
+// Stable LSD radix sort of (key, value[, value2]) u32 triples; pass p sorts
+// bits[p] bits at shifts[p]. v2 may be NULL. depth selects the workgroup
+// size class. Each pass uses one ticket (tickets[p]) and one epoch for the
+// scan of its count matrix. Ping-pongs between the buffers; returns the
+// index (0/1) of the result.
+int radix_sort(uint32_t* keys[2], uint32_t* vals[2], uint32_t* v2[2], const uint32_t* d_n, int64_t max_n, bool depth,
+               int n_passes, const int* shifts, const int* bits, uint32_t* counts, uint32_t* tickets,
+               uint64_t* status, uint32_t& epoch, uint32_t* err, hipStream_t s);
+// Instances in depth order: thread per depth-sorted primitive k < ctl->V,
+// slots [offs[k], offs[k + 1]).
+void launch_emit_instances(const uint32_t* prims, const uint32_t* offs, const BinCtl* ctl, int64_t max_count,
+                           const uint4* rec, uint32_t grid_w, uint32_t* inst_keys, uint32_t* inst_vals,
                            hipStream_t s);
+// [start, end) per tile, (0, 0) for empty tiles; every entry written.
 void launch_tile_ranges(const uint32_t* inst_keys, int64_t n_inst, uint2* ranges, uint32_t n_tiles, hipStream_t s);
 
 // ---- blend (kernels_forward.cuh:569-715, kernels_backward.cuh:675-927)

@@ -84,7 +84,7 @@ template <typename ShT>
 __global__ void __launch_bounds__(256) preprocess_kernel(
     const float* __restrict__ means, const float* __restrict__ scales, const float* __restrict__ rots,
     const float* __restrict__ opac, const ShT* __restrict__ sh0, const ShT* __restrict__ shr, int64_t n, int bases,
-    CamParams cam, uint32_t* __restrict__ n_touched, uint2* __restrict__ bounds, float2* __restrict__ mean2d,
+    CamParams cam, uint32_t* __restrict__ n_touched, uint4* __restrict__ rec, float2* __restrict__ mean2d,
     float4* __restrict__ conic_opacity, float4* __restrict__ color_pt, uint32_t* __restrict__ depth_key,
     float4* __restrict__ densif) {
     // SH-rest coefficients of the block's 256 primitives are one contiguous
@@ -233,7 +233,9 @@ __global__ void __launch_bounds__(256) preprocess_kernel(
         return;
     }
     n_touched[i] = cnt;
-    bounds[i] = make_uint2(xmin | (xmax << 16), ymin | (ymax << 16));
+    // 32-byte binning record, gathered once per primitive by the emission
+    rec[2 * i] = make_uint4(xmin | (xmax << 16), ymin | (ymax << 16), f2u(m2x), f2u(m2y));
+    rec[2 * i + 1] = make_uint4(f2u(ca), f2u(cb), f2u(cc), f2u(pthr));
     mean2d[i] = make_float2(m2x, m2y);
     conic_opacity[i] = make_float4(ca, cb, cc, opacity);
     float col[3];
@@ -242,7 +244,7 @@ __global__ void __launch_bounds__(256) preprocess_kernel(
     depth_key[i] = f2u(depth);
 }
 
-void launch_preprocess(const GaussianView& g, const CamParams& cam, uint32_t* n_touched, uint2* bounds,
+void launch_preprocess(const GaussianView& g, const CamParams& cam, uint32_t* n_touched, uint4* rec,
                        float2* mean2d, float4* conic_opacity, float4* color_pt, uint32_t* depth_key, float* densif,
                        hipStream_t s) {
     if (g.n <= 0) return;
@@ -251,12 +253,12 @@ void launch_preprocess(const GaussianView& g, const CamParams& cam, uint32_t* n_
     if (g.sh_dtype == kShF16) {
         preprocess_kernel<__half><<<grid, 256, 0, s>>>(g.means, g.scales, g.rotations, g.opacities,
                                                        (const __half*)g.sh0, (const __half*)g.sh_rest, g.n, bases,
-                                                       cam, n_touched, bounds, mean2d, conic_opacity, color_pt,
+                                                       cam, n_touched, rec, mean2d, conic_opacity, color_pt,
                                                        depth_key, (float4*)densif);
     } else {
         preprocess_kernel<float><<<grid, 256, 0, s>>>(g.means, g.scales, g.rotations, g.opacities,
                                                       (const float*)g.sh0, (const float*)g.sh_rest, g.n, bases, cam,
-                                                      n_touched, bounds, mean2d, conic_opacity, color_pt, depth_key,
+                                                      n_touched, rec, mean2d, conic_opacity, color_pt, depth_key,
                                                       (float4*)densif);
     }
 }
