@@ -12,6 +12,7 @@ from __future__ import annotations
 import argparse
 import json
 import os
+import re
 import sys
 import time
 
@@ -23,7 +24,25 @@ HBM_PEAK_GBS = 8000.0
 
 STAGES = ["preprocess", "depth_sort", "emit_instances", "tile_sort", "blend_forward", "l1", "fused_ssim",
           "blend_backward", "preprocess_backward", "adam"]
-SINGLE_KERNEL = {"preprocess", "blend_forward", "l1", "blend_backward", "preprocess_backward", "adam"}
+# stages that are one kernel launch, and that kernel's symbol in rocprofv3 output
+SINGLE_KERNEL = {"preprocess": "tgs::preprocess_kernel", "blend_forward": "tgs::blend_forward_kernel",
+                 "l1": "tgs::l1_kernel", "blend_backward": "tgs::blend_backward_kernel",
+                 "preprocess_backward": "tgs::preprocess_backward_kernel", "adam": "tgs::adam_kernel"}
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "hbm_traffic_config{}.md")
+
+
+def measured_traffic(config, kernel):
+    """HBM bytes per launch of `kernel` from the committed FETCH_SIZE /
+    WRITE_SIZE summary of this workload (two rocprofv3 --pmc runs of this
+    script, scaled by a copy of known size), or None if there is none."""
+    path = TRAFFIC_FILE.format(config)
+    if not os.path.exists(path):
+        return None
+    for line in open(path):
+        m = re.match(r"\|\s*`([^`]+)`\s*\|\s*\d+\s*\|[^|]*\|[^|]*\|\s*(\d+)\s*\|", line)
+        if m and (m.group(1) == kernel or m.group(1).startswith(kernel + "<")):
+            return int(m.group(2))
+    return None
 
 
 def algorithmic_bytes(stage, c):
@@ -65,6 +84,22 @@ def cpu_baseline(scene_fn):
     return dt * 1e3
 
 
+def calibrate_copy(mib):
+    """Copies `mib` MiB device to device five times. Under `rocprofv3 --pmc
+    FETCH_SIZE` (or WRITE_SIZE) each dispatch should read (write) exactly
+    mib MiB; the ratio of the counter to that is the scale applied to the
+    same counter of the path's kernels."""
+    import torch
+    n = mib * (1 << 20) // 4
+    src = torch.rand(n, device="cuda")
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(5):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"calibrate_copy_bytes": n * 4, "copies": 5}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -72,7 +107,12 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
+                    help="instead of the benchmark, run 5 device-to-device copies of MIB MiB (the known-size kernel "
+                         "that scales the FETCH_SIZE / WRITE_SIZE counters of a --pmc run)")
     args = ap.parse_args()
+    if args.calibrate_copy:
+        return calibrate_copy(args.calibrate_copy)
 
     if args.gpus != 1:
         print(f"bench.py runs on exactly one GPU (got --gpus {args.gpus}); multi-GPU sharding of this path "
@@ -148,7 +188,8 @@ def main():
 
     dom = max((r for r in rows if r[0] in SINGLE_KERNEL), key=lambda r: r[1])
     roofline = {"bound": "hbm", "kernel": dom[0], "achieved": round(dom[3], 2), "peak": HBM_PEAK_GBS,
-                "unit": "GB/s", "frac": round(dom[3] / HBM_PEAK_GBS, 4), "traffic": None,
+                "unit": "GB/s", "frac": round(dom[3] / HBM_PEAK_GBS, 4),
+                "traffic": measured_traffic(args.config, SINGLE_KERNEL[dom[0]]),
                 "algorithmic_bytes": int(dom[2]), "avg_launch_ms": round(dom[1], 5)}
 
     cpu = None
