@@ -148,7 +148,6 @@ def main():
     for k in range(len(STAGES)):
         L.tgs_profiling_read(k, None, None, 1)
     import ctypes as C
-    _lib.check(L.tgs_rasterizer_work_stats(ts.rasterizer._h, None, None, 1))
 
     start = torch.cuda.Event(enable_timing=True)
     stop = torch.cuda.Event(enable_timing=True)
@@ -171,7 +170,7 @@ def main():
     V, I, T = ts.rasterizer.counts()
     cam = scene.camera
     counts = {"N": scene.n, "V": V, "I": I, "T": T, "P": cam.width * cam.height,
-              "I_f": fl.value / args.steps, "I_b": bp.value / args.steps,
+              "I_f": fl.value, "I_b": bp.value,
               "sh_bytes": 2 if scene.sh_dtype == "float16" else 4, "sh_bases": (scene.sh_degree + 1) ** 2}
 
     print(f"[bench] {ms:.3f} ms/iter over {args.steps} steps; V={V} I={I} T={T} "

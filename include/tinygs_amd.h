@@ -174,9 +174,10 @@ int tgs_adam_moments(tgs_adam* a, int32_t group, float** first, float** second);
 int tgs_profiling_set(uint32_t stage_mask);
 int tgs_profiling_read(int32_t stage, double* total_ms, int64_t* count, int32_t reset);
 const char* tgs_stage_name(int32_t stage);
-/* Work counters accumulated over forwards / backwards: Gaussians staged by
- * the blend forward (summed over tiles) and Gaussians processed by the blend
- * backward (sum over tiles of min(list length, tile max contributor)). */
+/* Work counters of the last forward: Gaussians staged by the blend forward
+ * (summed over tiles) and Gaussians the blend backward processes (sum over
+ * tiles of min(list length, tile max contributor)). Synchronises the device.
+ * `reset` is ignored (kept for ABI compatibility). */
 int tgs_rasterizer_work_stats(tgs_rasterizer* r, int64_t* fwd_loaded, int64_t* bwd_processed, int32_t reset);
 
 /* ---- self tests (device): deterministic exp/log over arrays, wave primitives. */

@@ -1,24 +1,32 @@
-// Backward of the blend, one 16x16 tile per workgroup, pixel-parallel.
+// Backward of the blend: one (tile, 32-Gaussian bucket) work item per wave64,
+// four pixels per lane.
 //
 // Reference: blend_backward_cu2 (tinygs/src/rasterizer/fastgs_ours/
-// kernels_backward.cuh:675-927) assigns one warp per 32-Gaussian bucket,
-// restarts each bucket from a (colour, transmittance) checkpoint written by
-// the forward, and pipelines the 256 pixels through the lanes.
+// kernels_backward.cuh:675-927) assigns one warp per 32-Gaussian bucket and
+// restarts each bucket from the (colour, transmittance) checkpoint written by
+// the forward (kernels_forward.cuh:644-653); inside a bucket it runs the
+// backward recurrence with sigma clamped at 0 and no 1/255 test.
 //
-// MI355X design: a wave64 owns an 8x8 image block (one contiguous 256-byte
-// run per plane), every lane one pixel. The workgroup walks the tile's
-// Gaussians front to back; each pixel
-//   * re-runs the forward recurrence (alpha >= 1/255 test, sigma < 0 skip) to
-//     obtain the checkpoint state at every 32-Gaussian boundary, so the
-//     forward stores no checkpoints (saves 2 x 128 B of HBM per instance);
-//   * runs the reference backward recurrence inside each bucket (sigma
-//     clamped at 0, no 1/255 test, state restarted at the bucket boundary),
-//     which keeps the reference's bucket semantics exactly.
-// Per-Gaussian gradient sums (11 values) are reduced across the wave with a
-// transposed reduction (gfx950 v_permlane32_swap / v_permlane16_swap, then a
-// DPP row butterfly; fixed order), the four waves' partials combined in LDS,
-// and one float atomic per value and tile is issued to the per-primitive
-// record.
+// MI355X design:
+//   * the work item is the same bucket, but the wave is pixel-parallel: lane
+//     l owns pixels l, 64 + l, 128 + l, 192 + l of the tile, i.e. one lane of
+//     each 8x8 block, so every image / gradient / checkpoint access of a
+//     block is one contiguous 256-byte (1 KiB for checkpoints) run;
+//   * the 32 records of the bucket are staged in a wave-private LDS slice and
+//     read back as three broadcast float4 per Gaussian;
+//   * per Gaussian, each lane first sums its four pixels in registers, then
+//     the 11 sums are reduced across the wave once (gfx950
+//     v_permlane32_swap / v_permlane16_swap + DPP row butterfly), so the
+//     cross-lane work is shared by 256 pixels;
+//   * waves take items from a device-side list (built by the forward, one
+//     entry per bucket below the tile's last contributor, carrying its first
+//     instance and count) through 64 queue counters on separate cache lines,
+//     so long and short tiles balance across the CUs without every wave
+//     contending for one address; the next index is fetched while the
+//     current item runs;
+//   * no deterministic exp is needed here (the backward makes no threshold
+//     decision): exp(-sigma) is v_exp_f32 of sigma * log2(e), with log2(e)
+//     folded into the staged conic.
 //
 // grad2d record (12 floats per primitive): [0,1] dL/dmean2d, [2,3] |.| sums
 // (absgrad), [4..6] dL/dconic (a, b, c), [7..9] dL/dcolour (masked by
@@ -28,168 +36,189 @@
 
 namespace tgs {
 
-constexpr int kBwdBatch = 64;
 constexpr int kBwdVals = 11;
+constexpr float kLog2e = 1.4426950408889634f;
+
+__device__ __forceinline__ void wave_lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
 
 __global__ void __launch_bounds__(256) blend_backward_kernel(
-    CamParams cam, const uint2* __restrict__ ranges, const uint32_t* __restrict__ inst_vals,
-    const float2* __restrict__ mean2d, const float4* __restrict__ conic_opacity, const float4* __restrict__ color_pt,
-    const float* __restrict__ image, const float* __restrict__ grad_image, const uint32_t* __restrict__ n_contrib,
-    const uint32_t* __restrict__ tile_max, float* __restrict__ grad2d, unsigned long long* __restrict__ stats) {
-    __shared__ float4 s_a[kBwdBatch];   // mx, my, a/2, b
-    __shared__ float4 s_b[kBwdBatch];   // c/2, opacity, a, c
-    __shared__ float4 s_c[kBwdBatch];   // clamped colour, colour >= 0 mask bits
-    __shared__ uint32_t s_p[kBwdBatch];
-    __shared__ float s_part[4][kBwdVals][kBwdBatch];
-    __shared__ uint32_t s_wmax[4];
+    CamParams cam, const uint32_t* __restrict__ inst_vals, const float2* __restrict__ mean2d,
+    const float4* __restrict__ conic_opacity, const float4* __restrict__ color_pt, const float* __restrict__ image,
+    const float* __restrict__ grad_image, const uint32_t* __restrict__ n_contrib, const float4* __restrict__ ckpt,
+    const uint4* __restrict__ items, BinCtl* __restrict__ ctl, float* __restrict__ grad2d) {
+    __shared__ float4 s_rec[4][3][kBucket];
+    __shared__ float s_part[4][kBwdVals + 1][kBucket + 1];   // +1: the four row writers hit four banks
+    __shared__ uint32_t s_prim[4][kBucket];
 
-    const uint32_t tile = blockIdx.x;
-    const uint2 range = ranges[tile];
-    const int32_t len = (int32_t)(range.y - range.x);
-    const int32_t nproc = min(len, (int32_t)tile_max[tile]);
-    if (nproc <= 0) return;
-    if (stats && threadIdx.x == 0) atomicAdd(stats, (unsigned long long)nproc);
+    const uint32_t w = threadIdx.x >> 6, lane = threadIdx.x & 63u;
+    const int q0 = row_value(lane >> 4);   // first value index this lane's row holds after wave_reduce12
+    const uint32_t n_items = ctl->n_items;
+    const uint32_t cs = cam.tiled_w * cam.tiled_h * 64u;
+    // this wave's queue: items q, q + Q, q + 2Q, ...; its counter has a cache line to itself
+    const uint32_t queue = (blockIdx.x * 4u + w) % (uint32_t)kBwdQueues;
+    uint32_t* qctr = &ctl->bwd_queue[queue * 32u];
+    uint32_t next = 0;
+    if (lane == 0) next = atomicAdd(qctr, 1u);
+    next = (uint32_t)__builtin_amdgcn_readfirstlane((int)next);
 
-    const uint32_t gx = tile % cam.grid_w, gy = tile / cam.grid_w;
-    const uint32_t tid = threadIdx.x, w = tid >> 6, lane = tid & 63u;
-    const uint32_t px = gx * 16u + (w & 1u) * 8u + (lane & 7u);
-    const uint32_t py = gy * 16u + (w >> 1) * 8u + (lane >> 3);
-    const bool inside = px < cam.width && py < cam.height;
-    const float pcx = (float)px + 0.5f, pcy = (float)py + 0.5f;
+    while (true) {
+        const uint32_t it = queue + next * (uint32_t)kBwdQueues;
+        if (it >= n_items) break;
+        // fetch the following index now; its latency hides behind this item
+        uint32_t after = 0;
+        if (lane == 0) after = atomicAdd(qctr, 1u);
+        const uint4 item = items[it];
+        const uint32_t tile = item.x, b = item.y, first = item.z;
+        const int32_t j0 = (int32_t)(b * kBucket);
+        const int32_t cnt = (int32_t)item.w;
 
-    float I0 = 0.f, I1 = 0.f, I2 = 0.f, g0 = 0.f, g1 = 0.f, g2 = 0.f;
-    uint32_t last = 0;
-    if (inside) {
-        const uint32_t cs = cam.tiled_w * cam.tiled_h * 64u;
-        const uint32_t pi = tiled_index(py, px, cam.tiled_w);
-        I0 = image[pi]; I1 = image[pi + cs]; I2 = image[pi + 2 * cs];
-        g0 = grad_image[pi]; g1 = grad_image[pi + cs]; g2 = grad_image[pi + 2 * cs];
-        last = n_contrib[pi];
-    }
-    const uint32_t wmax = wave_max_u32(last);
-    if (lane == 0) s_wmax[w] = wmax;
-
-    // forward state (checkpoint source) and bucket-local backward state
-    float Tf = 1.f, F0 = 0.f, F1 = 0.f, F2 = 0.f;
-    float Tb = 1.f, A0 = 0.f, A1 = 0.f, A2 = 0.f;
-
-    for (int32_t base = 0; base < nproc; base += kBwdBatch) {
-        const int32_t nb = min(kBwdBatch, nproc - base);
-        if ((int32_t)tid < nb) {
-            const uint32_t p = inst_vals[range.x + (uint32_t)(base + (int32_t)tid)];
+        // ---- stage the bucket's records (wave-private LDS slice)
+        if ((int32_t)lane < cnt) {
+            const uint32_t p = inst_vals[first + lane];
             const float2 m = mean2d[p];
             const float4 co = conic_opacity[p];
             const float4 c = color_pt[p];
-            s_p[tid] = p;
-            s_a[tid] = make_float4(m.x, m.y, 0.5f * co.x, co.y);
-            s_b[tid] = make_float4(0.5f * co.z, co.w, co.x, co.z);
+            s_prim[w][lane] = p;
+            const float hl = 0.5f * kLog2e;
+            s_rec[w][0][lane] = make_float4(m.x, m.y, hl * co.x, kLog2e * co.y);
+            s_rec[w][1][lane] = make_float4(hl * co.z, co.w, co.x, co.z);
             const uint32_t mask = (c.x >= 0.f ? 1u : 0u) | (c.y >= 0.f ? 2u : 0u) | (c.z >= 0.f ? 4u : 0u);
-            s_c[tid] = make_float4(__builtin_fmaxf(c.x, 0.f), __builtin_fmaxf(c.y, 0.f), __builtin_fmaxf(c.z, 0.f),
-                                   u2f(mask));
+            s_rec[w][2][lane] = make_float4(__builtin_fmaxf(c.x, 0.f), __builtin_fmaxf(c.y, 0.f),
+                                            __builtin_fmaxf(c.z, 0.f), co.y);
+            s_part[w][kBwdVals][lane] = u2f(mask);
         }
-        __syncthreads();
-        const int32_t wend = min(nb, max(0, (int32_t)wmax - base));
-        for (int32_t k = 0; k < wend; ++k) {
-            const int32_t j = base + k;
-            if ((j & 31) == 0) {
-                Tb = Tf;
-                A0 = I0 - F0; A1 = I1 - F1; A2 = I2 - F2;
+
+        // ---- per-pixel state at the bucket start
+        const uint32_t gx = tile % cam.grid_w, gy = tile / cam.grid_w;
+        const uint32_t slot0 = (first - (uint32_t)j0) / (uint32_t)kBucket + tile;   // tile's first checkpoint slot
+        float pcx[4], pcy[4], g0[4], g1[4], g2[4], Tb[4], A0[4], A1[4], A2[4];
+        int32_t lk[4];
+        uint32_t pix[4];
+        bool in[4];
+        // two dependent rounds of loads for all four pixels: contributor
+        // counts, then colour / gradient / checkpoint (a checkpoint slot of
+        // an existing bucket is always allocated, whatever the pixel)
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            const uint32_t px = gx * 16u + (uint32_t)(s & 1) * 8u + (lane & 7u);
+            const uint32_t py = gy * 16u + (uint32_t)(s >> 1) * 8u + (lane >> 3);
+            pcx[s] = (float)px + 0.5f;
+            pcy[s] = (float)py + 0.5f;
+            in[s] = px < cam.width && py < cam.height;
+            // outside pixels read element 0 (always allocated) and are masked below
+            pix[s] = in[s] ? tiled_index(py, px, cam.tiled_w) : 0u;
+            lk[s] = (int32_t)n_contrib[pix[s]] - j0;
+        }
+        const size_t ck_base = (size_t)(b > 0 ? slot0 + b - 1u : 0u) * kTilePixels + lane;
+        int32_t kmax = 0;
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            const uint32_t pi = pix[s];
+            const float i0 = image[pi], i1 = image[pi + cs], i2 = image[pi + 2 * cs];
+            const float q0v = grad_image[pi], q1v = grad_image[pi + cs], q2v = grad_image[pi + 2 * cs];
+            float4 ck = ckpt[ck_base + (uint32_t)s * 64u];
+            if (b == 0) ck = make_float4(0.f, 0.f, 0.f, 1.f);
+            const bool act = in[s] && lk[s] > 0;
+            lk[s] = act ? lk[s] : 0;
+            kmax = max(kmax, lk[s]);
+            g0[s] = act ? q0v : 0.f; g1[s] = act ? q1v : 0.f; g2[s] = act ? q2v : 0.f;
+            Tb[s] = act ? ck.w : 0.f;
+            A0[s] = act ? i0 - ck.x : 0.f; A1[s] = act ? i1 - ck.y : 0.f; A2[s] = act ? i2 - ck.z : 0.f;
+        }
+        kmax = min((int32_t)wave_max_u32((uint32_t)kmax), cnt);
+        wave_lds_sync();
+
+        for (int32_t k = 0; k < kmax; ++k) {
+            const float4 r0 = s_rec[w][0][k];   // mx, my, a/2 L, b L
+            const float4 r1 = s_rec[w][1][k];   // c/2 L, opacity, a, c
+            const float4 r2 = s_rec[w][2][k];   // clamped colour, b
+            float acc[12];
+#pragma unroll
+            for (int q = 0; q < 12; ++q) acc[q] = 0.f;
+#pragma unroll
+            for (int s = 0; s < 4; ++s) {
+                const float dx = r0.x - pcx[s], dy = r0.y - pcy[s];
+                const float sg = __builtin_fmaf(dx, __builtin_fmaf(r0.z, dx, r0.w * dy), (r1.x * dy) * dy);
+                const float G = __builtin_amdgcn_exp2f(-__builtin_fmaxf(sg, 0.f));
+                const float ab = k < lk[s] ? __builtin_fminf(r1.y * G, kMaxAlpha) : 0.f;
+                const float wgt = Tb[s] * ab;
+                acc[0] = __builtin_fmaf(wgt, g0[s], acc[0]);
+                acc[1] = __builtin_fmaf(wgt, g1[s], acc[1]);
+                acc[2] = __builtin_fmaf(wgt, g2[s], acc[2]);
+                A0[s] = __builtin_fmaf(-wgt, r2.x, A0[s]);
+                A1[s] = __builtin_fmaf(-wgt, r2.y, A1[s]);
+                A2[s] = __builtin_fmaf(-wgt, r2.z, A2[s]);
+                const float cg = __builtin_fmaf(r2.z, g2[s], __builtin_fmaf(r2.y, g1[s], r2.x * g0[s]));
+                const float ag = __builtin_fmaf(A2[s], g2[s], __builtin_fmaf(A1[s], g1[s], A0[s] * g0[s]));
+                const float oma = 1.0f - ab;
+                const float dalpha = __builtin_fmaf(Tb[s], cg, -(ag * __builtin_amdgcn_rcpf(oma)));
+                const float pp = ab * dalpha;
+                acc[3] += pp;
+                const float hp = pp * dx, hq = pp * dy;
+                acc[4] = __builtin_fmaf(hp, dx, acc[4]);
+                acc[5] = __builtin_fmaf(hp, dy, acc[5]);
+                acc[6] = __builtin_fmaf(hq, dy, acc[6]);
+                const float gmx = __builtin_fmaf(hp, r1.z, hq * r2.w);
+                const float gmy = __builtin_fmaf(hp, r2.w, hq * r1.w);
+                acc[7] += gmx;
+                acc[8] += gmy;
+                acc[9] += __builtin_fabsf(gmx);
+                acc[10] += __builtin_fabsf(gmy);
+                Tb[s] *= oma;
             }
-            const bool act = (uint32_t)j < last;
-            const float4 a = s_a[k];
-            const float4 b = s_b[k];
-            const float4 c = s_c[k];
-            const float dx = a.x - pcx, dy = a.y - pcy;
-            const float sigma = __builtin_fmaf(dx, __builtin_fmaf(a.z, dx, a.w * dy), (b.x * dy) * dy);
-            const float G = det_expf_nonpos(-__builtin_fmaxf(sigma, 0.f));
-            const float araw = b.y * G;
-            // forward recurrence (bit-identical to blend_forward for j < last)
-            if (act && sigma >= 0.f) {
-                const float af = __builtin_fminf(araw, kMaxAlpha);
-                if (af >= kMinAlpha) {
-                    const float nT = Tf * (1.0f - af);
-                    const float wf = Tf * af;
-                    F0 = __builtin_fmaf(wf, c.x, F0);
-                    F1 = __builtin_fmaf(wf, c.y, F1);
-                    F2 = __builtin_fmaf(wf, c.z, F2);
-                    Tf = nT;
-                }
-            }
-            // reference backward step (kernels_backward.cuh:839-902)
-            const float ab = act ? __builtin_fminf(araw, kMaxAlpha) : 0.f;
-            const float wgt = Tb * ab;
-            float v[12];
-            v[0] = wgt * g0;
-            v[1] = wgt * g1;
-            v[2] = wgt * g2;
-            A0 -= wgt * c.x;
-            A1 -= wgt * c.y;
-            A2 -= wgt * c.z;
-            const float cg = c.x * g0 + c.y * g1 + c.z * g2;
-            const float ag = A0 * g0 + A1 * g1 + A2 * g2;
-            const float oma = 1.0f - ab;
-            const float dalpha = Tb * cg - ag * __builtin_amdgcn_rcpf(oma);
-            const float pp = ab * dalpha;
-            const float hp = -0.5f * pp;
-            v[3] = pp;
-            v[4] = hp * (dx * dx);
-            v[5] = hp * (dx * dy);
-            v[6] = hp * (dy * dy);
-            const float gmx = pp * (b.z * dx + a.w * dy);
-            const float gmy = pp * (a.w * dx + b.w * dy);
-            v[7] = -gmx;
-            v[8] = -gmy;
-            v[9] = __builtin_fabsf(gmx);
-            v[10] = __builtin_fabsf(gmy);
-            v[11] = 0.f;
-            Tb *= oma;
             float t[3];
-            wave_reduce12(v, t);
+            wave_reduce12(acc, t);
             if ((lane & 15u) == 0u) {
-                const int row = (int)(lane >> 4);
-                const int q0 = kRowValue[row];
                 s_part[w][q0][k] = t[0];
                 s_part[w][4 + q0][k] = t[1];
                 if (8 + q0 < kBwdVals) s_part[w][8 + q0][k] = t[2];
             }
         }
-        __syncthreads();
-        if ((int32_t)tid < nb) {
-            const int32_t k = (int32_t)tid;
-            float acc[kBwdVals];
-#pragma unroll
-            for (int q = 0; q < kBwdVals; ++q) acc[q] = 0.f;
-            for (int ww = 0; ww < 4; ++ww) {
-                const int32_t we = min(nb, max(0, (int32_t)s_wmax[ww] - base));
-                if (k < we) {
-#pragma unroll
-                    for (int q = 0; q < kBwdVals; ++q) acc[q] += s_part[ww][q][k];
-                }
-            }
-            const uint32_t mask = f2u(s_c[k].w);
-            if (!(mask & 1u)) acc[0] = 0.f;
-            if (!(mask & 2u)) acc[1] = 0.f;
-            if (!(mask & 4u)) acc[2] = 0.f;
-            float* dst = grad2d + (size_t)s_p[k] * kGradStride;
+        wave_lds_sync();
+
+        if ((int32_t)lane < kmax) {
+            const uint32_t k = lane;
+            const uint32_t mask = f2u(s_part[w][kBwdVals][k]);
+            float* dst = grad2d + (size_t)s_prim[w][k] * kGradStride;
             // record order: mean2d(2), abs(2), conic(3), colour(3), alpha partial
-            const float outv[11] = {acc[7], acc[8], acc[9], acc[10], acc[4], acc[5], acc[6],
-                                    acc[0], acc[1], acc[2], acc[3]};
+            const float outv[11] = {-s_part[w][7][k], -s_part[w][8][k], s_part[w][9][k], s_part[w][10][k],
+                                    -0.5f * s_part[w][4][k], -0.5f * s_part[w][5][k], -0.5f * s_part[w][6][k],
+                                    (mask & 1u) ? s_part[w][0][k] : 0.f, (mask & 2u) ? s_part[w][1][k] : 0.f,
+                                    (mask & 4u) ? s_part[w][2][k] : 0.f, s_part[w][3][k]};
 #pragma unroll
             for (int q = 0; q < 11; ++q)
                 if (outv[q] != 0.f) unsafeAtomicAdd(dst + q, outv[q]);
         }
-        __syncthreads();
+        next = (uint32_t)__builtin_amdgcn_readfirstlane((int)after);
+        wave_lds_sync();
     }
 }
 
-void launch_blend_backward(const CamParams& cam, const uint2* ranges, const uint32_t* inst_vals, const float2* mean2d,
+static int g_blocks = 0;
+
+void launch_blend_backward(const CamParams& cam, const uint32_t* inst_vals, const float2* mean2d,
                            const float4* conic_opacity, const float4* color_pt, const float* image,
-                           const float* grad_image, const uint32_t* n_contrib, const uint32_t* tile_max, float* grad2d,
-                           unsigned long long* stats, hipStream_t s) {
+                           const float* grad_image, const uint32_t* n_contrib, const float4* ckpt,
+                           const uint4* items, BinCtl* ctl, float* grad2d, hipStream_t s) {
     const uint32_t n_tiles = cam.grid_w * cam.grid_h;
     if (n_tiles == 0) return;
-    blend_backward_kernel<<<n_tiles, 256, 0, s>>>(cam, ranges, inst_vals, mean2d, conic_opacity, color_pt, image,
-                                                  grad_image, n_contrib, tile_max, grad2d, stats);
+    if (g_blocks <= 0) {
+        // persistent workgroups: exactly as many as can be resident at once
+        int dev = 0, cus = 0, per_cu = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+            cus = 256;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, blend_backward_kernel, 256, 0) != hipSuccess ||
+            per_cu <= 0)
+            per_cu = 4;
+        g_blocks = cus * per_cu;
+    }
+    blend_backward_kernel<<<(uint32_t)g_blocks, 256, 0, s>>>(cam, inst_vals, mean2d, conic_opacity, color_pt, image,
+                                                             grad_image, n_contrib, ckpt, items, ctl, grad2d);
 }
 
 }  // namespace tgs

@@ -9,9 +9,11 @@
 // as all of its 64 pixels have terminated and the workgroup stops fetching
 // once all four waves have.
 //
-// No per-bucket checkpoints are written: the backward kernel recomputes the
-// forward transmittance itself (see blend_backward.hip), which removes
-// 128 bytes per instance of HBM writes and reads.
+// Checkpoints: before Gaussian j of the tile's list with j % 32 == 0, j > 0,
+// every still-active wave stores its pixels' (C, T) (kernels_forward.cuh:
+// 644-653), one contiguous 1 KiB run per wave. At the end the tile appends one
+// backward work item per 32-Gaussian bucket below its last contributor
+// (tmax <= len, so every bucket of an item is inside the list).
 //
 // Numerics mirror the CPU oracle: sigma = fma(dx, fma(a/2, dx, b*dy),
 // (c/2)*dy*dy), the deterministic exp, fminf alpha clamp, the 1/255 cut and
@@ -29,7 +31,10 @@ __global__ void __launch_bounds__(256) blend_forward_kernel(CamParams cam, const
                                                             float* __restrict__ image,
                                                             uint32_t* __restrict__ n_contrib,
                                                             uint32_t* __restrict__ tile_max,
-                                                            unsigned long long* __restrict__ stats) {
+                                                            uint32_t* __restrict__ tile_loaded,
+                                                            float4* __restrict__ ckpt,
+                                                            uint4* __restrict__ items,
+                                                            BinCtl* __restrict__ ctl) {
     __shared__ float4 s_a[256];   // mx, my, a/2, b
     __shared__ float2 s_b[256];   // c/2, opacity
     __shared__ float4 s_c[256];   // r, g, b (clamped), skip bound
@@ -45,6 +50,7 @@ __global__ void __launch_bounds__(256) blend_forward_kernel(CamParams cam, const
 
     const uint2 range = ranges[tile];
     const int32_t len = (int32_t)(range.y - range.x);
+    const uint32_t slot0 = range.x / (uint32_t)kBucket + tile;   // first checkpoint slot of this tile
 
     float C0 = 0.f, C1 = 0.f, C2 = 0.f, T = 1.f;
     uint32_t ncontrib = 0;
@@ -70,6 +76,9 @@ __global__ void __launch_bounds__(256) blend_forward_kernel(CamParams cam, const
         loaded += (uint32_t)nb;
         for (int32_t k = 0; k < nb; ++k) {
             if (!__any(!done)) break;   // whole wave finished
+            const int32_t j = base + k;
+            if ((j & (kBucket - 1)) == 0 && j > 0)
+                ckpt[(size_t)(slot0 + (uint32_t)(j / kBucket) - 1u) * kTilePixels + tid] = make_float4(C0, C1, C2, T);
             const float4 a = s_a[k];
             const float2 bb = s_b[k];
             const float dx = a.x - pcx, dy = a.y - pcy;
@@ -111,19 +120,34 @@ __global__ void __launch_bounds__(256) blend_forward_kernel(CamParams cam, const
     const uint32_t wmax = wave_max_u32(ncontrib);
     if (lane == 0) s_max[w] = wmax;
     __syncthreads();
-    if (tid == 0) {
-        tile_max[tile] = max(max(s_max[0], s_max[1]), max(s_max[2], s_max[3]));
-        if (stats && loaded) atomicAdd(stats, (unsigned long long)loaded);
+    if (w == 0) {
+        const uint32_t tmax = max(max(s_max[0], s_max[1]), max(s_max[2], s_max[3]));
+        const uint32_t nbk = (tmax + (uint32_t)kBucket - 1u) / (uint32_t)kBucket;
+        uint32_t off = 0;
+        if (lane == 0) {
+            tile_max[tile] = tmax;
+            tile_loaded[tile] = loaded;
+            if (nbk) off = atomicAdd(&ctl->n_items, nbk);
+        }
+        off = (uint32_t)__builtin_amdgcn_readfirstlane((int)off);
+        for (uint32_t b = lane; b < nbk; b += 64u)
+            items[off + b] = make_uint4(tile, b, range.x + b * (uint32_t)kBucket,
+                                        min((uint32_t)kBucket, tmax - b * (uint32_t)kBucket));
     }
+}
+
+size_t blend_ckpt_slots(int64_t n_instances, uint32_t n_tiles) {
+    return (size_t)(n_instances > 0 ? n_instances : 0) / kBucket + n_tiles + 1;
 }
 
 void launch_blend_forward(const CamParams& cam, const uint2* ranges, const uint32_t* inst_vals, const float2* mean2d,
                           const float4* conic_opacity, const float4* color_pt, float* image, uint32_t* n_contrib,
-                          uint32_t* tile_max, unsigned long long* stats, hipStream_t s) {
+                          uint32_t* tile_max, uint32_t* tile_loaded, float4* ckpt, uint4* items, BinCtl* ctl,
+                          hipStream_t s) {
     const uint32_t n_tiles = cam.grid_w * cam.grid_h;
     if (n_tiles == 0) return;
     blend_forward_kernel<<<n_tiles, 256, 0, s>>>(cam, ranges, inst_vals, mean2d, conic_opacity, color_pt, image,
-                                                 n_contrib, tile_max, stats);
+                                                 n_contrib, tile_max, tile_loaded, ckpt, items, ctl);
 }
 
 }  // namespace tgs

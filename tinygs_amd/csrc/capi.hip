@@ -220,6 +220,8 @@ struct tgs_rasterizer {
     DevBuf ikeys[2], ivals[2];
     // per tile / pixel
     DevBuf ranges, tile_max, n_contrib;
+    DevBuf ckpt, items;   // blend checkpoints (float4 x 256 per slot), backward work items (uint4)
+    DevBuf tile_loaded;   // Gaussians staged per tile by the last forward (work statistic)
     // temp
     DevBuf grad2d;
     DevBuf radix_counts;   // per-workgroup digit counts of the radix passes
@@ -227,10 +229,10 @@ struct tgs_rasterizer {
     hipEvent_t ev_counts = nullptr;   // recorded after the counts copy of a forward
     DevBuf lb_status;   // look-back status words (u64), epoch-tagged
     uint32_t epoch = 0; // last look-back epoch used on lb_status
-    DevBuf counters;    // u64 work counters at byte 32 (forward) and 40 (backward)
     uint32_t* h_counters = nullptr;   // pinned copy of BinCtl {V, I, err}
     // state of the last forward
     bool fwd_done = false;
+    bool bwd_queues_clear = false;   // backward queue counters still zero since the last forward
     CamParams cam{};
     int64_t n = 0, V = 0, I = 0;
     int psel = 0, isel = 0;
@@ -278,11 +280,6 @@ int tgs_rasterizer_create(const char* type, tgs_rasterizer** out) {
     if (t != "fastgs") return fail(TGS_ERR_UNSUPPORTED, "Unknown rasterizer type: %s", type ? type : "(null)");
     tgs_rasterizer* r = new tgs_rasterizer();
     hipError_t e = hipHostMalloc((void**)&r->h_counters, 64, hipHostMallocDefault);
-    if (e == hipSuccess) e = hipMalloc(&r->counters.p, 64);
-    if (e == hipSuccess) {
-        r->counters.bytes = 64;
-        e = hipMemset(r->counters.p, 0, 64);
-    }
     if (e == hipSuccess) e = hipMalloc(&r->bin_ctl.p, sizeof(BinCtl));
     if (e == hipSuccess) {
         r->bin_ctl.bytes = sizeof(BinCtl);
@@ -293,7 +290,6 @@ int tgs_rasterizer_create(const char* type, tgs_rasterizer** out) {
     if (e != hipSuccess) {
         if (r->h_counters) (void)hipHostFree(r->h_counters);
         if (r->ev_counts) (void)hipEventDestroy(r->ev_counts);
-        release(r->counters);
         release(r->bin_ctl);
         delete r;
         return fail(TGS_ERR_HIP, "rasterizer allocation: %s", hipGetErrorString(e));
@@ -309,7 +305,7 @@ int tgs_rasterizer_destroy(tgs_rasterizer* r) {
                      &r->offs, &r->pkeys[0], &r->pkeys[1], &r->pvals[0], &r->pvals[1], &r->pnt[0], &r->pnt[1],
                      &r->radix_counts, &r->ikeys[0],
                      &r->ikeys[1], &r->ivals[0], &r->ivals[1], &r->ranges, &r->tile_max, &r->n_contrib,
-                     &r->grad2d, &r->bin_ctl, &r->lb_status, &r->counters};
+                     &r->ckpt, &r->items, &r->tile_loaded, &r->grad2d, &r->bin_ctl, &r->lb_status};
     for (DevBuf* b : all) release(*b);
     if (r->h_counters) (void)hipHostFree(r->h_counters);
     if (r->ev_counts) (void)hipEventDestroy(r->ev_counts);
@@ -369,6 +365,7 @@ int tgs_rasterizer_forward(tgs_rasterizer* r, const tgs_camera* camera, void* im
     }
     TGS_TRY(ensure(r->ranges, 8 * (size_t)T, s));
     TGS_TRY(ensure(r->tile_max, 4 * (size_t)T, s));
+    TGS_TRY(ensure(r->tile_loaded, 4 * (size_t)T, s));
     TGS_TRY(ensure(r->n_contrib, 4 * cs, s));
     TGS_TRY(ensure(r->radix_counts, 4 * (size_t)radix_count_entries(nn, true), s));
     TGS_TRY(ensure_status(r, std::max(scan_status_entries(nn), scan_status_entries(radix_count_entries(nn, true))), s));
@@ -414,6 +411,9 @@ int tgs_rasterizer_forward(tgs_rasterizer* r, const tgs_camera* camera, void* im
     TGS_TRY(ensure(r->radix_counts, 4 * (size_t)std::max(radix_count_entries(ii, false), radix_count_entries(nn, true)),
                    s));
     TGS_TRY(ensure_status(r, scan_status_entries(radix_count_entries(ii, false)), s));
+    const size_t slots = blend_ckpt_slots(I, T);
+    TGS_TRY(ensure(r->ckpt, sizeof(float4) * kTilePixels * slots, s));
+    TGS_TRY(ensure(r->items, sizeof(uint4) * slots, s));
     status = r->lb_status.as<uint64_t>();
     // tile key bits: one pass up to 8 bits, else two passes of ceil(bits/2) and the rest
     int bits = 1;
@@ -440,7 +440,7 @@ int tgs_rasterizer_forward(tgs_rasterizer* r, const tgs_camera* camera, void* im
         launch_blend_forward(cam, r->ranges.as<uint2>(), iv[isel], r->mean2d.as<float2>(),
                              r->conic_opacity.as<float4>(), r->color.as<float4>(), (float*)image,
                              r->n_contrib.as<uint32_t>(), r->tile_max.as<uint32_t>(),
-                             (unsigned long long*)(r->counters.as<char>() + 32), s);
+                             r->tile_loaded.as<uint32_t>(), r->ckpt.as<float4>(), r->items.as<uint4>(), ctl, s);
     }
     TGS_CHECK_LAUNCH();
     r->cam = cam;
@@ -450,6 +450,7 @@ int tgs_rasterizer_forward(tgs_rasterizer* r, const tgs_camera* camera, void* im
     r->psel = psel;
     r->isel = isel;
     r->fwd_done = true;
+    r->bwd_queues_clear = true;
     return TGS_OK;
 }
 
@@ -472,13 +473,17 @@ int tgs_rasterizer_backward_ex(tgs_rasterizer* r, const void* grad_image, const 
     TGS_TRY(ensure(r->grad2d, sizeof(float) * kGradStride * (size_t)(n > 0 ? n : 1), s));
     launch_fill_u32(r->grad2d.as<uint32_t>(), 0u, (int64_t)kGradStride * n, s);
     const CamParams& cam = r->cam;
+    BinCtl* ctl = r->bin_ctl.as<BinCtl>();
+    if (!r->bwd_queues_clear)   // a second backward after one forward: clear the work-queue counters again
+        launch_fill_u32(ctl->bwd_queue, 0u, (int64_t)kBwdQueues * 32, s);
     {
         StageScope sc(ST_BLENDB, s);
-        launch_blend_backward(cam, r->ranges.as<uint2>(), r->ivals[r->isel].as<uint32_t>(), r->mean2d.as<float2>(),
+        launch_blend_backward(cam, r->ivals[r->isel].as<uint32_t>(), r->mean2d.as<float2>(),
                               r->conic_opacity.as<float4>(), r->color.as<float4>(), (const float*)image,
-                              (const float*)grad_image, r->n_contrib.as<uint32_t>(), r->tile_max.as<uint32_t>(),
-                              r->grad2d.as<float>(), (unsigned long long*)(r->counters.as<char>() + 40), s);
+                              (const float*)grad_image, r->n_contrib.as<uint32_t>(), r->ckpt.as<float4>(),
+                              r->items.as<uint4>(), ctl, r->grad2d.as<float>(), s);
     }
+    r->bwd_queues_clear = false;
     TGS_CHECK_LAUNCH();
     GradView gv{(float*)grads->means, (float*)grads->scales, (float*)grads->rotations, (float*)grads->opacities,
                 (float*)grads->sh0, (float*)grads->sh_rest};
@@ -781,13 +786,24 @@ const char* tgs_stage_name(int32_t stage) {
 }
 
 int tgs_rasterizer_work_stats(tgs_rasterizer* r, int64_t* fwd_loaded, int64_t* bwd_processed, int32_t reset) {
+    (void)reset;
     if (!r) return fail(TGS_ERR_INVALID, "rasterizer is NULL");
-    unsigned long long h[2] = {0, 0};
+    if (!r->fwd_done) return fail(TGS_ERR_STATE, "no forward yet");
+    const size_t T = (size_t)r->cam.grid_w * r->cam.grid_h;
+    std::vector<uint32_t> loaded(T), tmax(T), ranges(2 * T);
     TGS_HIP(hipDeviceSynchronize());
-    TGS_HIP(hipMemcpy(h, r->counters.as<char>() + 32, sizeof(h), hipMemcpyDeviceToHost));
-    if (fwd_loaded) *fwd_loaded = (int64_t)h[0];
-    if (bwd_processed) *bwd_processed = (int64_t)h[1];
-    if (reset) TGS_HIP(hipMemset(r->counters.as<char>() + 32, 0, sizeof(h)));
+    if (T) {
+        TGS_HIP(hipMemcpy(loaded.data(), r->tile_loaded.p, 4 * T, hipMemcpyDeviceToHost));
+        TGS_HIP(hipMemcpy(tmax.data(), r->tile_max.p, 4 * T, hipMemcpyDeviceToHost));
+        TGS_HIP(hipMemcpy(ranges.data(), r->ranges.p, 8 * T, hipMemcpyDeviceToHost));
+    }
+    int64_t fl = 0, bp = 0;
+    for (size_t t = 0; t < T; ++t) {
+        fl += loaded[t];
+        bp += std::min<int64_t>((int64_t)ranges[2 * t + 1] - (int64_t)ranges[2 * t], tmax[t]);
+    }
+    if (fwd_loaded) *fwd_loaded = fl;
+    if (bwd_processed) *bwd_processed = bp;
     return TGS_OK;
 }
 

@@ -12,6 +12,7 @@ namespace tgs {
 constexpr int kWave = 64;
 constexpr int kTile = 16;               // screen tile edge (rasterization_config.h:31-35)
 constexpr int kTilePixels = 256;
+constexpr int kBucket = 32;            // Gaussians per backward checkpoint bucket (kernels_forward.cuh:644-653)
 constexpr float kMinAlpha = 1.0f / 255.0f;
 constexpr float kMaxAlpha = 0.999f;
 constexpr float kTransmittanceMin = 1e-4f;
@@ -126,13 +127,16 @@ __device__ __forceinline__ void swap16(float& a, float& b) {
 }
 
 // Transposed wave reduction of 12 per-lane values v[0..11] into 12 wave sums.
-// After the call, lane L of t[m] holds the sum of value 4m + kRowValue[L >> 4]
+// After the call, lane L of t[m] holds the sum of value 4m + row_value(L >> 4)
 // (every lane of a 16-lane row holds the same total).
 //   step 1: swap32 + add folds value pairs across the two 32-lane halves,
 //   step 2: swap16 + add folds the results across rows 0/1 and 2/3,
 //   step 3: row butterfly (row_ror 8, 4, 2, 1) on the three survivors.
 // 6 + 3 swaps, 9 adds and 12 DPP adds instead of 12 x 6 dependent DPP adds.
-constexpr int kRowValue[4] = {0, 2, 1, 3};
+// Value offset held by 16-lane row r after the swaps: rows 0..3 -> 0, 2, 1, 3.
+// Arithmetic on purpose: a lane-indexed constant table becomes a global
+// memory load inside the caller's loop.
+__device__ __forceinline__ int row_value(uint32_t row) { return (int)(((row & 1u) << 1) | (row >> 1)); }
 __device__ __forceinline__ void wave_reduce12(float v[12], float t[3]) {
 #pragma unroll
     for (int k = 0; k < 6; ++k) {

@@ -43,9 +43,13 @@ void launch_preprocess(const GaussianView& g, const CamParams& cam, uint32_t* n_
 // cleared at the start of every forward; err (look-back error flag) is
 // sticky so that a failure is reported by the next host check.
 enum { kTicketCompact = 0, kTicketOffsets = 1, kTicketDepth = 2, kTicketTile = 6, kTicketCount = 8 };
+constexpr int kBwdQueues = 64;   // backward work queues; item i belongs to queue i % kBwdQueues
 struct BinCtl {
     uint32_t V, I, err, pad;
     uint32_t tickets[kTicketCount];
+    uint32_t n_items;                     // backward work items listed by the blend forward
+    uint32_t pad2[19];                    // queue counters start on a 128-byte line
+    uint32_t bwd_queue[kBwdQueues * 32];  // next local index of queue q at [32 q] (one line each)
 };
 // Clears every BinCtl word except err.
 void launch_bin_ctl_reset(BinCtl* ctl, hipStream_t s);
@@ -80,13 +84,23 @@ void launch_emit_instances(const uint32_t* prims, const uint32_t* offs, const Bi
 void launch_tile_ranges(const uint32_t* inst_keys, int64_t n_inst, uint2* ranges, uint32_t n_tiles, hipStream_t s);
 
 // ---- blend (kernels_forward.cuh:569-715, kernels_backward.cuh:675-927)
+// Checkpoints: the state (C, T) of every pixel before Gaussian 32 b of its
+// tile's list, b >= 1, at slot (range.x / 32 + tile + b - 1), 256 float4 per
+// slot in tile pixel order; slots of different tiles never overlap and stay
+// below I / 32 + T. Work items: one uint4 {tile, b, first instance, count}
+// per 32-Gaussian bucket below the tile's last contributor, appended through
+// ctl->n_items (at most I / 32 + T entries). tile_loaded[t]: Gaussians the
+// tile staged before it finished (a work statistic).
+size_t blend_ckpt_slots(int64_t n_instances, uint32_t n_tiles);
 void launch_blend_forward(const CamParams& cam, const uint2* ranges, const uint32_t* inst_vals, const float2* mean2d,
                           const float4* conic_opacity, const float4* color_pt, float* image, uint32_t* n_contrib,
-                          uint32_t* tile_max, unsigned long long* stats, hipStream_t s);
-void launch_blend_backward(const CamParams& cam, const uint2* ranges, const uint32_t* inst_vals,
-                           const float2* mean2d, const float4* conic_opacity, const float4* color_pt,
-                           const float* image, const float* grad_image, const uint32_t* n_contrib,
-                           const uint32_t* tile_max, float* grad2d, unsigned long long* stats, hipStream_t s);
+                          uint32_t* tile_max, uint32_t* tile_loaded, float4* ckpt, uint4* items, BinCtl* ctl,
+                          hipStream_t s);
+// ctl->bwd_queue must be zero on entry (the forward's control reset clears it).
+void launch_blend_backward(const CamParams& cam, const uint32_t* inst_vals, const float2* mean2d,
+                           const float4* conic_opacity, const float4* color_pt, const float* image,
+                           const float* grad_image, const uint32_t* n_contrib, const float4* ckpt,
+                           const uint4* items, BinCtl* ctl, float* grad2d, hipStream_t s);
 
 // ---- preprocess backward (kernels_backward.cuh:88-352)
 void launch_preprocess_backward(const GaussianView& g, const CamParams& cam, const uint32_t* n_touched,

@@ -48,7 +48,7 @@ __global__ void wave_selftest_kernel(const uint32_t* in, uint32_t* out) {
     wave_reduce12(vv, t);
     if ((lane & 15u) == 0u) {
         const uint32_t row = lane >> 4;
-        for (int m = 0; m < 3; ++m) out[192 + 4 * m + kRowValue[row]] = f2u(t[m]);
+        for (int m = 0; m < 3; ++m) out[192 + 4 * m + row_value((uint32_t)row)] = f2u(t[m]);
     }
     if (lane == 0) {
         out[64] = sum;
