@@ -115,7 +115,7 @@ typedef struct tgs_debug_view {
     const uint32_t* tile_ranges;        /* [2 * n_tiles] */
     const uint32_t* n_contrib;          /* [channel_stride] */
     const uint32_t* tile_max;           /* [n_tiles] */
-    const float* grad2d;                /* [12n] after backward */
+    const float* grad2d;                /* NULL: 2D gradients are transient records inside a backward */
     int64_t n_visible;
     int64_t n_instances;
     int64_t n_tiles;

@@ -498,7 +498,8 @@ __global__ void __launch_bounds__(256) emit_kernel(const uint32_t* __restrict__ 
                                                    const uint32_t* __restrict__ offs, const BinCtl* ctl,
                                                    int64_t max_count, const uint4* __restrict__ rec, uint32_t grid_w,
                                                    uint32_t* __restrict__ inst_keys,
-                                                   uint32_t* __restrict__ inst_vals) {
+                                                   uint32_t* __restrict__ inst_vals,
+                                                   uint32_t* __restrict__ first_slot) {
     __shared__ uint32_t s_key[kEmitStage], s_val[kEmitStage];
     const uint32_t t = threadIdx.x;
     const int64_t n = min((int64_t)ctl->V, max_count);
@@ -524,6 +525,7 @@ __global__ void __launch_bounds__(256) emit_kernel(const uint32_t* __restrict__ 
         p = prims[k];
         off = offs[k];
         cap = offs[k + 1] - off;   // slots reserved for this primitive (= its n_touched)
+        first_slot[p] = off;
         const uint4 r0 = rec[2 * (size_t)p], r1 = rec[2 * (size_t)p + 1];
         x0 = r0.x & 0xffffu; x1 = r0.x >> 16; y0 = r0.y & 0xffffu; y1 = r0.y >> 16;
         smx = u2f(r0.z) - 0.5f;
@@ -581,10 +583,10 @@ __global__ void __launch_bounds__(256) emit_kernel(const uint32_t* __restrict__ 
 
 void launch_emit_instances(const uint32_t* prims, const uint32_t* offs, const BinCtl* ctl, int64_t max_count,
                            const uint4* rec, uint32_t grid_w, uint32_t* inst_keys, uint32_t* inst_vals,
-                           hipStream_t s) {
+                           uint32_t* first_slot, hipStream_t s) {
     if (max_count <= 0) return;
     emit_kernel<<<(unsigned)((max_count + 255) / 256), 256, 0, s>>>(prims, offs, ctl, max_count, rec, grid_w,
-                                                                    inst_keys, inst_vals);
+                                                                    inst_keys, inst_vals, first_slot);
 }
 
 // ---------------------------------------------------------------- ranges

@@ -28,9 +28,14 @@
 //     decision): exp(-sigma) is v_exp_f32 of sigma * log2(e), with log2(e)
 //     folded into the staged conic.
 //
-// grad2d record (12 floats per primitive): [0,1] dL/dmean2d, [2,3] |.| sums
+// Output: one 12-float record per (primitive, bucket) instead of float
+// atomics (device-scope atomics on MI355X are performed at the memory side,
+// one DRAM read-modify-write each): [0,1] dL/dmean2d, [2,3] |.| sums
 // (absgrad), [4..6] dL/dconic (a, b, c), [7..9] dL/dcolour (masked by
 // colour >= 0), [10] sum of alpha * dL/dalpha (times (1 - opacity) later).
+// The record index comes from one counter atomic per (primitive, bucket) into
+// the instance slots binning reserved for the primitive; the per-primitive
+// sums are formed by gather_heavy / the preprocess backward.
 #include "common.h"
 #include "kernels.h"
 
@@ -49,10 +54,10 @@ __global__ void __launch_bounds__(256) blend_backward_kernel(
     CamParams cam, const uint32_t* __restrict__ inst_vals, const float2* __restrict__ mean2d,
     const float4* __restrict__ conic_opacity, const float4* __restrict__ color_pt, const float* __restrict__ image,
     const float* __restrict__ grad_image, const uint32_t* __restrict__ n_contrib, const float4* __restrict__ ckpt,
-    const uint4* __restrict__ items, BinCtl* __restrict__ ctl, float* __restrict__ grad2d) {
+    const uint4* __restrict__ items, BinCtl* __restrict__ ctl, uint32_t* __restrict__ rec_count,
+    const uint32_t* __restrict__ first_slot, float4* __restrict__ records, uint32_t* __restrict__ heavy) {
     __shared__ float4 s_rec[4][3][kBucket];
     __shared__ float s_part[4][kBwdVals + 1][kBucket + 1];   // +1: the four row writers hit four banks
-    __shared__ uint32_t s_prim[4][kBucket];
 
     const uint32_t w = threadIdx.x >> 6, lane = threadIdx.x & 63u;
     const int q0 = row_value(lane >> 4);   // first value index this lane's row holds after wave_reduce12
@@ -76,13 +81,17 @@ __global__ void __launch_bounds__(256) blend_backward_kernel(
         const int32_t j0 = (int32_t)(b * kBucket);
         const int32_t cnt = (int32_t)item.w;
 
-        // ---- stage the bucket's records (wave-private LDS slice)
+        // ---- stage the bucket's records (wave-private LDS slice); each of
+        // its primitives takes one 2D-gradient record index now and fills it
+        // at the end of the item
+        uint32_t p = 0, sub = 0, slot = 0;
         if ((int32_t)lane < cnt) {
-            const uint32_t p = inst_vals[first + lane];
+            p = inst_vals[first + lane];
+            sub = atomicAdd(rec_count + p, 1u);
+            slot = first_slot[p];
             const float2 m = mean2d[p];
             const float4 co = conic_opacity[p];
             const float4 c = color_pt[p];
-            s_prim[w][lane] = p;
             const float hl = 0.5f * kLog2e;
             s_rec[w][0][lane] = make_float4(m.x, m.y, hl * co.x, kLog2e * co.y);
             s_rec[w][1][lane] = make_float4(hl * co.z, co.w, co.x, co.z);
@@ -180,18 +189,17 @@ __global__ void __launch_bounds__(256) blend_backward_kernel(
         }
         wave_lds_sync();
 
-        if ((int32_t)lane < kmax) {
+        if ((int32_t)lane < cnt) {
             const uint32_t k = lane;
+            const bool ev = (int32_t)lane < kmax;   // evaluated (always true: kmax == cnt by construction)
             const uint32_t mask = f2u(s_part[w][kBwdVals][k]);
-            float* dst = grad2d + (size_t)s_prim[w][k] * kGradStride;
-            // record order: mean2d(2), abs(2), conic(3), colour(3), alpha partial
-            const float outv[11] = {-s_part[w][7][k], -s_part[w][8][k], s_part[w][9][k], s_part[w][10][k],
-                                    -0.5f * s_part[w][4][k], -0.5f * s_part[w][5][k], -0.5f * s_part[w][6][k],
-                                    (mask & 1u) ? s_part[w][0][k] : 0.f, (mask & 2u) ? s_part[w][1][k] : 0.f,
-                                    (mask & 4u) ? s_part[w][2][k] : 0.f, s_part[w][3][k]};
-#pragma unroll
-            for (int q = 0; q < 11; ++q)
-                if (outv[q] != 0.f) unsafeAtomicAdd(dst + q, outv[q]);
+            auto val = [&](int q) { return ev ? s_part[w][q][k] : 0.f; };
+            // record order: mean2d(2), abs(2), conic(3), colour(3), alpha partial, 0
+            float4* dst = records + 3 * (size_t)(slot + sub);
+            dst[0] = make_float4(-val(7), -val(8), val(9), val(10));
+            dst[1] = make_float4(-0.5f * val(4), -0.5f * val(5), -0.5f * val(6), (mask & 1u) ? val(0) : 0.f);
+            dst[2] = make_float4((mask & 2u) ? val(1) : 0.f, (mask & 4u) ? val(2) : 0.f, val(3), 0.f);
+            if (sub == kLightRecords) heavy[atomicAdd(&ctl->heavy_n, 1u)] = p;
         }
         next = (uint32_t)__builtin_amdgcn_readfirstlane((int)after);
         wave_lds_sync();
@@ -203,7 +211,8 @@ static int g_blocks = 0;
 void launch_blend_backward(const CamParams& cam, const uint32_t* inst_vals, const float2* mean2d,
                            const float4* conic_opacity, const float4* color_pt, const float* image,
                            const float* grad_image, const uint32_t* n_contrib, const float4* ckpt,
-                           const uint4* items, BinCtl* ctl, float* grad2d, hipStream_t s) {
+                           const uint4* items, BinCtl* ctl, uint32_t* rec_count, const uint32_t* first_slot,
+                           float4* records, uint32_t* heavy, hipStream_t s) {
     const uint32_t n_tiles = cam.grid_w * cam.grid_h;
     if (n_tiles == 0) return;
     if (g_blocks <= 0) {
@@ -218,7 +227,49 @@ void launch_blend_backward(const CamParams& cam, const uint32_t* inst_vals, cons
         g_blocks = cus * per_cu;
     }
     blend_backward_kernel<<<(uint32_t)g_blocks, 256, 0, s>>>(cam, inst_vals, mean2d, conic_opacity, color_pt, image,
-                                                             grad_image, n_contrib, ckpt, items, ctl, grad2d);
+                                                             grad_image, n_contrib, ckpt, items, ctl, rec_count,
+                                                             first_slot, records, heavy);
+}
+
+// Sums the 2D-gradient records of each listed primitive (more than
+// kLightRecords of them) into grad2d[12 p]: one wave per primitive, lanes
+// over records, then the transposed wave reduction.
+__global__ void __launch_bounds__(256) gather_heavy_kernel(const uint32_t* __restrict__ heavy,
+                                                           const BinCtl* __restrict__ ctl,
+                                                           const uint32_t* __restrict__ rec_count,
+                                                           const uint32_t* __restrict__ first_slot,
+                                                           const float4* __restrict__ records,
+                                                           float* __restrict__ grad2d) {
+    const uint32_t w = threadIdx.x >> 6, lane = threadIdx.x & 63u;
+    const uint32_t nh = ctl->heavy_n;
+    const int q0 = row_value(lane >> 4);
+    for (uint32_t h = blockIdx.x * 4u + w; h < nh; h += gridDim.x * 4u) {
+        const uint32_t p = heavy[h];
+        const uint32_t c = rec_count[p], base = first_slot[p];
+        float v[12];
+#pragma unroll
+        for (int q = 0; q < 12; ++q) v[q] = 0.f;
+        for (uint32_t r = lane; r < c; r += 64u) {
+            const float4* src = records + 3 * (size_t)(base + r);
+            const float4 a = src[0], b = src[1], d = src[2];
+            v[0] += a.x; v[1] += a.y; v[2] += a.z; v[3] += a.w;
+            v[4] += b.x; v[5] += b.y; v[6] += b.z; v[7] += b.w;
+            v[8] += d.x; v[9] += d.y; v[10] += d.z; v[11] += d.w;
+        }
+        float t[3];
+        wave_reduce12(v, t);
+        if ((lane & 15u) == 0u) {
+            float* g = grad2d + (size_t)p * kGradStride;
+            g[q0] = t[0];
+            g[4 + q0] = t[1];
+            g[8 + q0] = t[2];
+        }
+    }
+}
+
+void launch_gather_heavy(const uint32_t* heavy, const BinCtl* ctl, const uint32_t* rec_count,
+                         const uint32_t* first_slot, const float4* records, float* grad2d, hipStream_t s) {
+    gather_heavy_kernel<<<512, 256, 0, s>>>(heavy, ctl, rec_count, first_slot, records, grad2d);
 }
 
 }  // namespace tgs

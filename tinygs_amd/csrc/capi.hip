@@ -222,6 +222,10 @@ struct tgs_rasterizer {
     DevBuf ranges, tile_max, n_contrib;
     DevBuf ckpt, items;   // blend checkpoints (float4 x 256 per slot), backward work items (uint4)
     DevBuf tile_loaded;   // Gaussians staged per tile by the last forward (work statistic)
+    // backward 2D-gradient records: per primitive first instance slot, record
+    // count (kept zero between backwards), records (3 float4 per instance
+    // slot), heavy-gather list
+    DevBuf first_slot, rec_count, records, heavy;
     // temp
     DevBuf grad2d;
     DevBuf radix_counts;   // per-workgroup digit counts of the radix passes
@@ -305,7 +309,8 @@ int tgs_rasterizer_destroy(tgs_rasterizer* r) {
                      &r->offs, &r->pkeys[0], &r->pkeys[1], &r->pvals[0], &r->pvals[1], &r->pnt[0], &r->pnt[1],
                      &r->radix_counts, &r->ikeys[0],
                      &r->ikeys[1], &r->ivals[0], &r->ivals[1], &r->ranges, &r->tile_max, &r->n_contrib,
-                     &r->ckpt, &r->items, &r->tile_loaded, &r->grad2d, &r->bin_ctl, &r->lb_status};
+                     &r->ckpt, &r->items, &r->tile_loaded, &r->first_slot,
+                     &r->rec_count, &r->records, &r->heavy, &r->grad2d, &r->bin_ctl, &r->lb_status};
     for (DevBuf* b : all) release(*b);
     if (r->h_counters) (void)hipHostFree(r->h_counters);
     if (r->ev_counts) (void)hipEventDestroy(r->ev_counts);
@@ -358,6 +363,13 @@ int tgs_rasterizer_forward(tgs_rasterizer* r, const tgs_camera* camera, void* im
     TGS_TRY(ensure(r->color, 16 * nn, s));
     TGS_TRY(ensure(r->depth_key, 4 * nn, s));
     TGS_TRY(ensure(r->offs, 4 * (nn + 1), s));
+    TGS_TRY(ensure(r->first_slot, 4 * nn, s));
+    {
+        const void* before = r->rec_count.p;
+        TGS_TRY(ensure(r->rec_count, 4 * nn, s));
+        if (r->rec_count.p != before)   // counters are zero between backwards; a new buffer starts so
+            launch_fill_u32(r->rec_count.as<uint32_t>(), 0u, (int64_t)(r->rec_count.bytes / 4), s);
+    }
     for (int k = 0; k < 2; ++k) {
         TGS_TRY(ensure(r->pkeys[k], 4 * nn, s));
         TGS_TRY(ensure(r->pvals[k], 4 * nn, s));
@@ -414,6 +426,7 @@ int tgs_rasterizer_forward(tgs_rasterizer* r, const tgs_camera* camera, void* im
     const size_t slots = blend_ckpt_slots(I, T);
     TGS_TRY(ensure(r->ckpt, sizeof(float4) * kTilePixels * slots, s));
     TGS_TRY(ensure(r->items, sizeof(uint4) * slots, s));
+    TGS_TRY(ensure(r->records, 3 * sizeof(float4) * (size_t)ii, s));
     status = r->lb_status.as<uint64_t>();
     // tile key bits: one pass up to 8 bits, else two passes of ceil(bits/2) and the rest
     int bits = 1;
@@ -424,7 +437,8 @@ int tgs_rasterizer_forward(tgs_rasterizer* r, const tgs_camera* camera, void* im
     {
         StageScope sc(ST_EMIT, s);
         launch_emit_instances(pv[psel], r->offs.as<uint32_t>(), ctl, n, r->rec.as<uint4>(), cam.grid_w,
-                              r->ikeys[0].as<uint32_t>(), r->ivals[0].as<uint32_t>(), s);
+                              r->ikeys[0].as<uint32_t>(), r->ivals[0].as<uint32_t>(), r->first_slot.as<uint32_t>(),
+                              s);
     }
     uint32_t* ik[2] = {r->ikeys[0].as<uint32_t>(), r->ikeys[1].as<uint32_t>()};
     uint32_t* iv[2] = {r->ivals[0].as<uint32_t>(), r->ivals[1].as<uint32_t>()};
@@ -471,17 +485,20 @@ int tgs_rasterizer_backward_ex(tgs_rasterizer* r, const void* grad_image, const 
     hipStream_t s = (hipStream_t)stream;
     const int64_t n = r->n;
     TGS_TRY(ensure(r->grad2d, sizeof(float) * kGradStride * (size_t)(n > 0 ? n : 1), s));
-    launch_fill_u32(r->grad2d.as<uint32_t>(), 0u, (int64_t)kGradStride * n, s);
+    TGS_TRY(ensure(r->heavy, sizeof(uint32_t) * (size_t)(n > 0 ? n : 1), s));
     const CamParams& cam = r->cam;
     BinCtl* ctl = r->bin_ctl.as<BinCtl>();
-    if (!r->bwd_queues_clear)   // a second backward after one forward: clear the work-queue counters again
-        launch_fill_u32(ctl->bwd_queue, 0u, (int64_t)kBwdQueues * 32, s);
+    if (!r->bwd_queues_clear)   // a second backward after one forward: clear the queue / heavy counters again
+        launch_fill_u32(&ctl->heavy_n, 0u, kBwdCtlWords, s);
     {
         StageScope sc(ST_BLENDB, s);
         launch_blend_backward(cam, r->ivals[r->isel].as<uint32_t>(), r->mean2d.as<float2>(),
                               r->conic_opacity.as<float4>(), r->color.as<float4>(), (const float*)image,
                               (const float*)grad_image, r->n_contrib.as<uint32_t>(), r->ckpt.as<float4>(),
-                              r->items.as<uint4>(), ctl, r->grad2d.as<float>(), s);
+                              r->items.as<uint4>(), ctl, r->rec_count.as<uint32_t>(), r->first_slot.as<uint32_t>(),
+                              r->records.as<float4>(), r->heavy.as<uint32_t>(), s);
+        launch_gather_heavy(r->heavy.as<uint32_t>(), ctl, r->rec_count.as<uint32_t>(), r->first_slot.as<uint32_t>(),
+                            r->records.as<float4>(), r->grad2d.as<float>(), s);
     }
     r->bwd_queues_clear = false;
     TGS_CHECK_LAUNCH();
@@ -490,6 +507,7 @@ int tgs_rasterizer_backward_ex(tgs_rasterizer* r, const void* grad_image, const 
     {
         StageScope sc(ST_PREB, s);
         launch_preprocess_backward(view_of(r->g), cam, r->n_touched.as<uint32_t>(), r->conic_opacity.as<float4>(),
+                                   r->rec_count.as<uint32_t>(), r->first_slot.as<uint32_t>(), r->records.as<float4>(),
                                    r->grad2d.as<float>(), gv, (float*)densification_info,
                                    (flags & TGS_BACKWARD_ASSIGN) != 0, s);
     }
@@ -521,7 +539,7 @@ int tgs_rasterizer_debug_view(tgs_rasterizer* r, tgs_debug_view* out) {
     out->tile_ranges = r->ranges.as<uint32_t>();
     out->n_contrib = r->n_contrib.as<uint32_t>();
     out->tile_max = r->tile_max.as<uint32_t>();
-    out->grad2d = r->grad2d.as<float>();
+    out->grad2d = nullptr;   // 2D gradients live in per-(primitive, bucket) records during a backward only
     out->n_visible = r->V;
     out->n_instances = r->I;
     out->n_tiles = (int64_t)r->cam.grid_w * r->cam.grid_h;

@@ -48,9 +48,12 @@ struct BinCtl {
     uint32_t V, I, err, pad;
     uint32_t tickets[kTicketCount];
     uint32_t n_items;                     // backward work items listed by the blend forward
-    uint32_t pad2[19];                    // queue counters start on a 128-byte line
-    uint32_t bwd_queue[kBwdQueues * 32];  // next local index of queue q at [32 q] (one line each)
+    uint32_t pad2[18];
+    uint32_t heavy_n;                     // primitives on the backward's heavy-gather list
+    uint32_t bwd_queue[kBwdQueues * 32];  // next local index of queue q at [32 q] (one line each, from byte 128)
 };
+// Words from heavy_n to the end of bwd_queue: what a backward needs cleared.
+constexpr int kBwdCtlWords = 1 + kBwdQueues * 32;
 // Clears every BinCtl word except err.
 void launch_bin_ctl_reset(BinCtl* ctl, hipStream_t s);
 constexpr uint32_t kEpochMask = 0x3fffffffu;   // 30-bit launch epoch of look-back status words
@@ -77,9 +80,11 @@ int radix_sort(uint32_t* keys[2], uint32_t* vals[2], uint32_t* v2[2], const uint
                uint64_t* status, uint32_t& epoch, uint32_t* err, hipStream_t s);
 // Instances in depth order: thread per depth-sorted primitive k < ctl->V,
 // slots [offs[k], offs[k + 1]).
+// Also writes first_slot[p] = offs[k] for every visible primitive p = prims[k]:
+// the first of the n_touched[p] instance slots reserved for p.
 void launch_emit_instances(const uint32_t* prims, const uint32_t* offs, const BinCtl* ctl, int64_t max_count,
                            const uint4* rec, uint32_t grid_w, uint32_t* inst_keys, uint32_t* inst_vals,
-                           hipStream_t s);
+                           uint32_t* first_slot, hipStream_t s);
 // [start, end) per tile, (0, 0) for empty tiles; every entry written.
 void launch_tile_ranges(const uint32_t* inst_keys, int64_t n_inst, uint2* ranges, uint32_t n_tiles, hipStream_t s);
 
@@ -96,16 +101,30 @@ void launch_blend_forward(const CamParams& cam, const uint2* ranges, const uint3
                           const float4* conic_opacity, const float4* color_pt, float* image, uint32_t* n_contrib,
                           uint32_t* tile_max, uint32_t* tile_loaded, float4* ckpt, uint4* items, BinCtl* ctl,
                           hipStream_t s);
-// ctl->bwd_queue must be zero on entry (the forward's control reset clears it).
+// 2D gradient records: each (primitive p, bucket) the backward processes
+// takes record index first_slot[p] + atomicAdd(rec_count[p], 1) (below
+// first_slot[p] + n_touched[p]: a primitive is in a tile's list once) and
+// writes 12 floats there: dL/dmean2d (2), |.| sums (2), dL/dconic (3),
+// dL/dcolour (3), sum of alpha dL/dalpha, 0. Primitives reaching
+// kLightRecords + 1 records are listed in `heavy` (count ctl->heavy_n);
+// gather_heavy sums their records into grad2d[12 p]; the preprocess backward
+// sums the others itself and clears rec_count.
+constexpr uint32_t kLightRecords = 4;
+// ctl->heavy_n and ctl->bwd_queue must be zero on entry (the forward's control
+// reset clears them).
 void launch_blend_backward(const CamParams& cam, const uint32_t* inst_vals, const float2* mean2d,
                            const float4* conic_opacity, const float4* color_pt, const float* image,
                            const float* grad_image, const uint32_t* n_contrib, const float4* ckpt,
-                           const uint4* items, BinCtl* ctl, float* grad2d, hipStream_t s);
+                           const uint4* items, BinCtl* ctl, uint32_t* rec_count, const uint32_t* first_slot,
+                           float4* records, uint32_t* heavy, hipStream_t s);
+void launch_gather_heavy(const uint32_t* heavy, const BinCtl* ctl, const uint32_t* rec_count,
+                         const uint32_t* first_slot, const float4* records, float* grad2d, hipStream_t s);
 
 // ---- preprocess backward (kernels_backward.cuh:88-352)
 void launch_preprocess_backward(const GaussianView& g, const CamParams& cam, const uint32_t* n_touched,
-                                const float4* conic_opacity, const float* grad2d, const GradView& out,
-                                float* densif, bool assign, hipStream_t s);
+                                const float4* conic_opacity, uint32_t* rec_count, const uint32_t* first_slot,
+                                const float4* records, const float* grad2d, const GradView& out, float* densif,
+                                bool assign, hipStream_t s);
 
 // ---- utilities
 void launch_fill_u32(uint32_t* p, uint32_t value, int64_t n, hipStream_t s);

@@ -10,7 +10,7 @@
 // quaternion gradient divided by |q|^3 (:332); the three double-precision
 // literals of the SH direction gradient (:55-57). The opacity gradient is
 // (sum of alpha * dL/dalpha) * (1 - opacity) (:921-922); the blend backward
-// leaves the sum in grad2d[10] and it is applied here.
+// leaves the sum in its 2D-gradient records and it is applied here.
 #include "common.h"
 #include "kernels.h"
 
@@ -38,13 +38,32 @@ template <typename ShT>
 __device__ __forceinline__ void preprocess_backward_one(
     int64_t i, const float* __restrict__ means, const float* __restrict__ scales, const float* __restrict__ rots,
     const ShT* shr, int bases, const CamParams& cam, const float4* __restrict__ conic_opacity,
+    uint32_t* __restrict__ rec_count, const uint32_t* __restrict__ first_slot, const float4* __restrict__ records,
     const float* __restrict__ grad2d, float* __restrict__ g_means, float* __restrict__ g_scales,
     float* __restrict__ g_rots, float* __restrict__ g_opac, float* __restrict__ g_sh0, float4* __restrict__ densif,
     float gc_out[3], float k[15], int& nb_out, bool assign) {
-    const float* gr = grad2d + (size_t)i * kGradStride;
-    const float4 gA = *(const float4*)(gr);       // dmx, dmy, absx, absy
-    const float4 gB = *(const float4*)(gr + 4);   // dca, dcb, dcc, dr
-    const float4 gC = *(const float4*)(gr + 8);   // dg, db, alpha partial, -
+    // 2D gradient sums: up to kLightRecords per-(primitive, bucket) records
+    // are summed here; a primitive with more was summed into grad2d by
+    // gather_heavy. The record counter is cleared for the next backward.
+    const uint32_t nrec = rec_count[i];
+    float4 gA = make_float4(0.f, 0.f, 0.f, 0.f);   // dmx, dmy, absx, absy
+    float4 gB = gA;                                // dca, dcb, dcc, dr
+    float4 gC = gA;                                // dg, db, alpha partial, -
+    if (nrec > kLightRecords) {
+        const float* gr = grad2d + (size_t)i * kGradStride;
+        gA = *(const float4*)(gr);
+        gB = *(const float4*)(gr + 4);
+        gC = *(const float4*)(gr + 8);
+    } else if (nrec > 0) {
+        const float4* rec = records + 3 * (size_t)first_slot[i];
+        for (uint32_t r = 0; r < nrec; ++r) {
+            const float4 a = rec[3 * r], b = rec[3 * r + 1], c = rec[3 * r + 2];
+            gA.x += a.x; gA.y += a.y; gA.z += a.z; gA.w += a.w;
+            gB.x += b.x; gB.y += b.y; gB.z += b.z; gB.w += b.w;
+            gC.x += c.x; gC.y += c.y; gC.z += c.z;
+        }
+    }
+    if (nrec) rec_count[i] = 0u;
     const float mx = means[3 * i], my = means[3 * i + 1], mz = means[3 * i + 2];
 
     // ---- SH backward (kernels_backward.cuh:22-86)
@@ -256,9 +275,10 @@ template <typename ShT>
 __global__ void __launch_bounds__(256) preprocess_backward_kernel(
     const float* __restrict__ means, const float* __restrict__ scales, const float* __restrict__ rots,
     const ShT* __restrict__ shr_all, int64_t n, int bases, CamParams cam, const uint32_t* __restrict__ n_touched,
-    const float4* __restrict__ conic_opacity, const float* __restrict__ grad2d, float* __restrict__ g_means,
-    float* __restrict__ g_scales, float* __restrict__ g_rots, float* __restrict__ g_opac, float* __restrict__ g_sh0,
-    float* __restrict__ g_shr_all, float4* __restrict__ densif, int assign_flag) {
+    const float4* __restrict__ conic_opacity, uint32_t* __restrict__ rec_count,
+    const uint32_t* __restrict__ first_slot, const float4* __restrict__ records, const float* __restrict__ grad2d,
+    float* __restrict__ g_means, float* __restrict__ g_scales, float* __restrict__ g_rots, float* __restrict__ g_opac,
+    float* __restrict__ g_sh0, float* __restrict__ g_shr_all, float4* __restrict__ densif, int assign_flag) {
     // This block's 256 primitives own a contiguous run of 256 * 45 SH-rest
     // parameters and gradients. Both are moved through LDS with 16-byte
     // lane-contiguous accesses instead of 45 lane-strided accesses per thread.
@@ -279,8 +299,9 @@ __global__ void __launch_bounds__(256) preprocess_backward_kernel(
     int nb = 0;
     const bool assign = assign_flag != 0;
     if (vis) {
-        preprocess_backward_one<ShT>(i, means, scales, rots, s_sh + 45 * t, bases, cam, conic_opacity, grad2d,
-                                     g_means, g_scales, g_rots, g_opac, g_sh0, densif, gc, k, nb, assign);
+        preprocess_backward_one<ShT>(i, means, scales, rots, s_sh + 45 * t, bases, cam, conic_opacity, rec_count,
+                                     first_slot, records, grad2d, g_means, g_scales, g_rots, g_opac, g_sh0, densif,
+                                     gc, k, nb, assign);
     } else if (assign && t < nblk) {
         for (int c = 0; c < 3; ++c) {
             g_means[3 * i + c] = 0.f;
@@ -338,7 +359,8 @@ __global__ void __launch_bounds__(256) preprocess_backward_kernel(
 }
 
 void launch_preprocess_backward(const GaussianView& g, const CamParams& cam, const uint32_t* n_touched,
-                                const float4* conic_opacity, const float* grad2d, const GradView& out, float* densif,
+                                const float4* conic_opacity, uint32_t* rec_count, const uint32_t* first_slot,
+                                const float4* records, const float* grad2d, const GradView& out, float* densif,
                                 bool assign, hipStream_t s) {
     if (g.n <= 0) return;
     const int bases = (g.sh_degree + 1) * (g.sh_degree + 1);
@@ -346,12 +368,12 @@ void launch_preprocess_backward(const GaussianView& g, const CamParams& cam, con
     if (g.sh_dtype == kShF16) {
         preprocess_backward_kernel<__half><<<grid, 256, 0, s>>>(
             g.means, g.scales, g.rotations, (const __half*)g.sh_rest, g.n, bases, cam, n_touched, conic_opacity,
-            grad2d, out.means, out.scales, out.rotations, out.opacities, out.sh0, out.sh_rest, (float4*)densif,
+            rec_count, first_slot, records, grad2d, out.means, out.scales, out.rotations, out.opacities, out.sh0, out.sh_rest, (float4*)densif,
             assign ? 1 : 0);
     } else {
         preprocess_backward_kernel<float><<<grid, 256, 0, s>>>(
             g.means, g.scales, g.rotations, (const float*)g.sh_rest, g.n, bases, cam, n_touched, conic_opacity,
-            grad2d, out.means, out.scales, out.rotations, out.opacities, out.sh0, out.sh_rest, (float4*)densif,
+            rec_count, first_slot, records, grad2d, out.means, out.scales, out.rotations, out.opacities, out.sh0, out.sh_rest, (float4*)densif,
             assign ? 1 : 0);
     }
 }

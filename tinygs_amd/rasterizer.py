@@ -127,14 +127,6 @@ class FastGSRasterizer(RasterizerBase):
         t = torch.empty(shape.channel_stride, dtype=torch.int32, device=self.m_gaussians.means().device)
         return _lib.copy_device(dv.n_contrib, t.numel() * 4, t)
 
-    def debug_grad2d(self):
-        import torch
-        dv = _lib.tgs_debug_view()
-        _lib.check(_lib.load().tgs_rasterizer_debug_view(self._h, C.byref(dv)), "debug_view")
-        n = self.m_gaussians.size()
-        t = torch.empty(12 * n, dtype=torch.float32, device=self.m_gaussians.means().device)
-        return _lib.copy_device(dv.grad2d, t.numel() * 4, t)
-
     def get_params(self) -> dict:
         return {"type": "fastgs"}
 
