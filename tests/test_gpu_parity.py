@@ -114,6 +114,8 @@ def _check_forward(scene, orc):
     img = run["image"]
     err = np.abs(img - fwd["image"])
     assert np.all(err <= PIXEL_RTOL * np.abs(fwd["image"]) + PIXEL_ATOL), err.max()
+    # stronger than the tolerance: the deterministic exp and IEEE ops make every pixel bit-identical
+    assert np.array_equal(img.view(np.uint32), fwd["image"].astype(np.float32).view(np.uint32))
     assert np.array_equal(run["n_contrib"], fwd["n_contrib"])
     assert np.array_equal(dv["tile_max"].view(np.uint32), fwd["tile_max"])
     return run, (pre, bins, fwd)

@@ -5,9 +5,16 @@
 // (w & 1, w >> 1) of the tile, which is exactly one 64-float run of the 8x8
 // tiled image layout, so every image / n_contrib store of a wave is one
 // contiguous 256-byte transaction per plane. Gaussians are staged through LDS
-// in batches of 256 (one record per thread); a wave stops evaluating as soon
-// as all of its 64 pixels have terminated and the workgroup stops fetching
-// once all four waves have.
+// in batches of 256 (one record per thread).
+//
+// Per-block culling at staging: the staging thread bounds sigma from below
+// over each 8x8 block's pixel-centre rectangle (minimum of the conic's
+// quadratic form over the rectangle, minus a rounding allowance) and marks
+// the blocks where alpha >= 1/255 is possible. Each wave then walks a
+// compacted LDS list of only its marked Gaussians with a branch-free body, so
+// Gaussians that miss a block cost that wave nothing. The cut is
+// conservative: a skipped Gaussian would have taken the alpha < 1/255 path in
+// every pixel of the block, so results are unchanged.
 //
 // Checkpoints: before Gaussian j of the tile's list with j % 32 == 0, j > 0,
 // every still-active wave stores its pixels' (C, T) (kernels_forward.cuh:
@@ -23,6 +30,32 @@
 
 namespace tgs {
 
+// Lower bound of sigma(dx, dy) = a/2 dx^2 + b dx dy + c/2 dy^2 over the box
+// [dx0, dx1] x [dy0, dy1] (dx = mean - pixel centre), valid for the float
+// evaluation the blend uses at any pixel centre in the box. Convex case
+// (a > 0, c > 0, ac > b^2): 0 if the box holds the origin, else the least of
+// the four edge minima (clamped 1-D minimisers); then minus 2^-16 of the
+// largest term magnitude, far above the few-ulp rounding of either
+// evaluation. Returns -inf (never cull) for a non-convex conic.
+__device__ __forceinline__ float sigma_box_lower_bound(float a, float b, float c, float dx0, float dx1, float dy0,
+                                                       float dy1) {
+    if (!(a > 0.f) || !(c > 0.f) || !(a * c > b * b)) return -__builtin_inff();
+    const float mx = __builtin_fmaxf(__builtin_fabsf(dx0), __builtin_fabsf(dx1));
+    const float my = __builtin_fmaxf(__builtin_fabsf(dy0), __builtin_fabsf(dy1));
+    const float slack = 1.52587890625e-05f * (0.5f * a * mx * mx + __builtin_fabsf(b) * mx * my + 0.5f * c * my * my);
+    if (dx0 <= 0.f && dx1 >= 0.f && dy0 <= 0.f && dy1 >= 0.f) return -slack;
+    auto q = [&](float x, float y) { return 0.5f * a * x * x + b * x * y + 0.5f * c * y * y; };
+    const float ia = 1.0f / a, ic = 1.0f / c;
+    float m = __builtin_inff();
+    // edges x = dx0, dx1: minimiser y = -b x / c
+    m = __builtin_fminf(m, q(dx0, __builtin_fminf(__builtin_fmaxf(-b * dx0 * ic, dy0), dy1)));
+    m = __builtin_fminf(m, q(dx1, __builtin_fminf(__builtin_fmaxf(-b * dx1 * ic, dy0), dy1)));
+    // edges y = dy0, dy1: minimiser x = -b y / a
+    m = __builtin_fminf(m, q(__builtin_fminf(__builtin_fmaxf(-b * dy0 * ia, dx0), dx1), dy0));
+    m = __builtin_fminf(m, q(__builtin_fminf(__builtin_fmaxf(-b * dy1 * ia, dx0), dx1), dy1));
+    return m - slack;
+}
+
 __global__ void __launch_bounds__(256) blend_forward_kernel(CamParams cam, const uint2* __restrict__ ranges,
                                                             const uint32_t* __restrict__ inst_vals,
                                                             const float2* __restrict__ mean2d,
@@ -35,9 +68,11 @@ __global__ void __launch_bounds__(256) blend_forward_kernel(CamParams cam, const
                                                             float4* __restrict__ ckpt,
                                                             uint4* __restrict__ items,
                                                             BinCtl* __restrict__ ctl) {
-    __shared__ float4 s_a[256];   // mx, my, a/2, b
-    __shared__ float2 s_b[256];   // c/2, opacity
-    __shared__ float4 s_c[256];   // r, g, b (clamped), skip bound
+    __shared__ float4 s_a[256];       // mx, my, a/2, b
+    __shared__ float4 s_b[256];       // c/2, opacity, r, g (clamped colour)
+    __shared__ float s_c[256];        // b (clamped colour)
+    __shared__ uint32_t s_mask[256];  // bit q: may reach alpha >= 1/255 in 8x8 block q
+    __shared__ uint16_t s_list[4][256];
     __shared__ uint32_t s_max[4];
 
     const uint32_t tile = blockIdx.x;
@@ -56,54 +91,86 @@ __global__ void __launch_bounds__(256) blend_forward_kernel(CamParams cam, const
     uint32_t ncontrib = 0;
     uint32_t loaded = 0;
     bool done = !inside;
+    int32_t next_ck = kBucket;   // next bucket boundary whose checkpoint this wave still owes
 
     for (int32_t base = 0; base < len; base += 256) {
         if (__syncthreads_and(done)) break;
-        const int32_t j = base + (int32_t)tid;
-        if (j < len) {
-            const uint32_t p = inst_vals[range.x + (uint32_t)j];
-            const float2 m = mean2d[p];
-            const float4 co = conic_opacity[p];
-            const float4 c = color_pt[p];
-            s_a[tid] = make_float4(m.x, m.y, 0.5f * co.x, co.y);
-            s_b[tid] = make_float2(0.5f * co.z, co.w);
-            // w: ln(255 * opacity) + 1e-3, the wave-skip bound (see below)
-            s_c[tid] = make_float4(__builtin_fmaxf(c.x, 0.f), __builtin_fmaxf(c.y, 0.f), __builtin_fmaxf(c.z, 0.f),
-                                   c.w + 1e-3f);
+        const int32_t nb = min(256, len - base);
+        {
+            const int32_t j = base + (int32_t)tid;
+            uint32_t mask = 0;
+            if (j < len) {
+                const uint32_t p = inst_vals[range.x + (uint32_t)j];
+                const float2 m = mean2d[p];
+                const float4 co = conic_opacity[p];
+                const float4 c = color_pt[p];
+                s_a[tid] = make_float4(m.x, m.y, 0.5f * co.x, co.y);
+                s_b[tid] = make_float4(0.5f * co.z, co.w, __builtin_fmaxf(c.x, 0.f), __builtin_fmaxf(c.y, 0.f));
+                s_c[tid] = __builtin_fmaxf(c.z, 0.f);
+                // sigma > ln(255 o) + 1e-3 implies o exp(-sigma) < exp(-1e-3) / 255, below the 1/255 cut by far
+                // more than the error of the deterministic exp / log (< 1e-6 relative)
+                const float bound = c.w + 1e-3f;
+#pragma unroll
+                for (uint32_t q = 0; q < 4; ++q) {
+                    const float x0 = (float)(gx * 16u + (q & 1u) * 8u) + 0.5f;
+                    const float y0 = (float)(gy * 16u + (q >> 1) * 8u) + 0.5f;
+                    const float lb = sigma_box_lower_bound(co.x, co.y, co.z, m.x - (x0 + 7.f), m.x - x0,
+                                                           m.y - (y0 + 7.f), m.y - y0);
+                    if (lb <= bound) mask |= 1u << q;
+                }
+            }
+            s_mask[tid] = mask;
         }
         __syncthreads();
-        const int32_t nb = min(256, len - base);
         loaded += (uint32_t)nb;
-        for (int32_t k = 0; k < nb; ++k) {
-            if (!__any(!done)) break;   // whole wave finished
-            const int32_t j = base + k;
-            if ((j & (kBucket - 1)) == 0 && j > 0)
-                ckpt[(size_t)(slot0 + (uint32_t)(j / kBucket) - 1u) * kTilePixels + tid] = make_float4(C0, C1, C2, T);
-            const float4 a = s_a[k];
-            const float2 bb = s_b[k];
+        // this wave's compacted list of Gaussians (batch positions) that may touch its block
+        int32_t cnt = 0;
+        for (int32_t c0 = 0; c0 < nb; c0 += 64) {
+            const int32_t e = c0 + (int32_t)lane;
+            const bool hit = e < nb && ((s_mask[e] >> w) & 1u);
+            const uint64_t bal = ballot(hit);
+            if (hit) s_list[w][cnt + (int32_t)mask_rank(bal)] = (uint16_t)e;
+            cnt += (int32_t)__builtin_popcountll(bal);
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+        // two marked Gaussians per step: both records are read before either is blended
+        auto blend = [&](int32_t e, const float4& a, const float4& bb, float cz) {
+            const int32_t j = base + e;
+            while (next_ck <= j) {   // bucket boundaries passed since the last marked Gaussian
+                ckpt[(size_t)(slot0 + (uint32_t)(next_ck / kBucket) - 1u) * kTilePixels + tid] =
+                    make_float4(C0, C1, C2, T);
+                next_ck += kBucket;
+            }
             const float dx = a.x - pcx, dy = a.y - pcy;
             const float sigma = __builtin_fmaf(dx, __builtin_fmaf(a.z, dx, a.w * dy), (bb.x * dy) * dy);
-            // Exact wave-level skip: sigma > ln(255 o) + 1e-3 implies
-            // o * exp(-sigma) < exp(-1e-3) / 255, below the 1/255 cut by far
-            // more than the error of the deterministic exp / log (< 1e-6
-            // relative), so such pixels would all take the alpha < 1/255 path.
-            if (!__any(!done && sigma <= s_c[k].w)) continue;
-            if (done) continue;
-            if (sigma < 0.f) continue;
-            const float alpha = __builtin_fminf(bb.y * det_expf_nonpos(-sigma), kMaxAlpha);
-            if (alpha < kMinAlpha) continue;
+            const float alpha = __builtin_fminf(bb.y * det_expf_nonpos(__builtin_fminf(-sigma, 0.f)), kMaxAlpha);
+            const bool ok = !done && sigma >= 0.f && alpha >= kMinAlpha;
             const float nT = T * (1.0f - alpha);
-            if (nT < kTransmittanceMin) {
-                done = true;
-                continue;
-            }
+            const bool term = ok && nT < kTransmittanceMin;
+            const bool acc = ok && !term;
+            done = done || term;
             const float wgt = T * alpha;
-            const float4 c = s_c[k];
-            C0 = __builtin_fmaf(wgt, c.x, C0);
-            C1 = __builtin_fmaf(wgt, c.y, C1);
-            C2 = __builtin_fmaf(wgt, c.z, C2);
-            T = nT;
-            ncontrib = (uint32_t)(base + k + 1);
+            C0 = acc ? __builtin_fmaf(wgt, bb.z, C0) : C0;
+            C1 = acc ? __builtin_fmaf(wgt, bb.w, C1) : C1;
+            C2 = acc ? __builtin_fmaf(wgt, cz, C2) : C2;
+            T = acc ? nT : T;
+            ncontrib = acc ? (uint32_t)(j + 1) : ncontrib;
+        };
+        for (int32_t i = 0; i < cnt; i += 2) {
+            if (!__any(!done)) break;   // whole wave finished
+            const uint32_t pair = *(const uint32_t*)&s_list[w][i];   // i is even: 4-byte aligned
+            const int32_t e0 = __builtin_amdgcn_readfirstlane((int)(pair & 0xffffu));
+            const bool two = i + 1 < cnt;
+            const int32_t e1 = two ? __builtin_amdgcn_readfirstlane((int)(pair >> 16)) : e0;
+            const float4 a0 = s_a[e0], b0 = s_b[e0];
+            const float c0 = s_c[e0];
+            const float4 a1 = s_a[e1], b1 = s_b[e1];
+            const float c1 = s_c[e1];
+            blend(e0, a0, b0, c0);
+            if (two) blend(e1, a1, b1, c1);
         }
         __syncthreads();
     }
