@@ -11,22 +11,16 @@
 // literals of the SH direction gradient (:55-57). The opacity gradient is
 // (sum of alpha * dL/dalpha) * (1 - opacity) (:921-922); the blend backward
 // leaves the sum in its 2D-gradient records and it is applied here.
+//
+// Only primitives that some tile's blend backward reached (a nonzero record
+// count) run the chain; for the other visible ones every gradient is exactly
+// zero, so their parameters are never read (at 1M Gaussians most visible
+// primitives sit behind others and fall in this class). Their SH-rest rows
+// are read per thread from global memory only when needed.
 #include "common.h"
 #include "kernels.h"
 
 namespace tgs {
-
-// Copies count elements (a multiple of 8 bytes apart from a tail) from global
-// to LDS with 16-byte lane-contiguous loads.
-template <typename ShT>
-__device__ __forceinline__ void stage_block(ShT* dst, const ShT* src, int count) {
-    const int bytes = count * (int)sizeof(ShT);
-    const int nvec = bytes >> 4;
-    const uint4* s4 = (const uint4*)src;
-    uint4* d4 = (uint4*)dst;
-    for (int v = (int)threadIdx.x; v < nvec; v += 256) d4[v] = s4[v];
-    for (int e = (nvec << 4) / (int)sizeof(ShT) + (int)threadIdx.x; e < count; e += 256) dst[e] = src[e];
-}
 
 // Gradient update: accumulate (+=, the reference contract) or assign (the
 // caller's zeroing fused into this write).
@@ -37,33 +31,11 @@ __device__ __forceinline__ void gadd(float* p, float v, bool assign) { *p = assi
 template <typename ShT>
 __device__ __forceinline__ void preprocess_backward_one(
     int64_t i, const float* __restrict__ means, const float* __restrict__ scales, const float* __restrict__ rots,
-    const ShT* shr, int bases, const CamParams& cam, const float4* __restrict__ conic_opacity,
-    uint32_t* __restrict__ rec_count, const uint32_t* __restrict__ first_slot, const float4* __restrict__ records,
-    const float* __restrict__ grad2d, float* __restrict__ g_means, float* __restrict__ g_scales,
+    const ShT* shr, int bases, const CamParams& cam, const float4* __restrict__ conic_opacity, const float4 gA,
+    const float4 gB, const float4 gC, float* __restrict__ g_means, float* __restrict__ g_scales,
     float* __restrict__ g_rots, float* __restrict__ g_opac, float* __restrict__ g_sh0, float4* __restrict__ densif,
     float gc_out[3], float k[15], int& nb_out, bool assign) {
-    // 2D gradient sums: up to kLightRecords per-(primitive, bucket) records
-    // are summed here; a primitive with more was summed into grad2d by
-    // gather_heavy. The record counter is cleared for the next backward.
-    const uint32_t nrec = rec_count[i];
-    float4 gA = make_float4(0.f, 0.f, 0.f, 0.f);   // dmx, dmy, absx, absy
-    float4 gB = gA;                                // dca, dcb, dcc, dr
-    float4 gC = gA;                                // dg, db, alpha partial, -
-    if (nrec > kLightRecords) {
-        const float* gr = grad2d + (size_t)i * kGradStride;
-        gA = *(const float4*)(gr);
-        gB = *(const float4*)(gr + 4);
-        gC = *(const float4*)(gr + 8);
-    } else if (nrec > 0) {
-        const float4* rec = records + 3 * (size_t)first_slot[i];
-        for (uint32_t r = 0; r < nrec; ++r) {
-            const float4 a = rec[3 * r], b = rec[3 * r + 1], c = rec[3 * r + 2];
-            gA.x += a.x; gA.y += a.y; gA.z += a.z; gA.w += a.w;
-            gB.x += b.x; gB.y += b.y; gB.z += b.z; gB.w += b.w;
-            gC.x += c.x; gC.y += c.y; gC.z += c.z;
-        }
-    }
-    if (nrec) rec_count[i] = 0u;
+    // gA: dmx, dmy, absx, absy; gB: dca, dcb, dcc, dr; gC: dg, db, alpha partial, -
     const float mx = means[3 * i], my = means[3 * i + 1], mz = means[3 * i + 2];
 
     // ---- SH backward (kernels_backward.cuh:22-86)
@@ -279,10 +251,9 @@ __global__ void __launch_bounds__(256) preprocess_backward_kernel(
     const uint32_t* __restrict__ first_slot, const float4* __restrict__ records, const float* __restrict__ grad2d,
     float* __restrict__ g_means, float* __restrict__ g_scales, float* __restrict__ g_rots, float* __restrict__ g_opac,
     float* __restrict__ g_sh0, float* __restrict__ g_shr_all, float4* __restrict__ densif, int assign_flag) {
-    // This block's 256 primitives own a contiguous run of 256 * 45 SH-rest
-    // parameters and gradients. Both are moved through LDS with 16-byte
-    // lane-contiguous accesses instead of 45 lane-strided accesses per thread.
-    __shared__ __align__(16) ShT s_sh[256 * 45];
+    // The SH-rest gradient rows of this block's 256 primitives are one
+    // contiguous run of 256 * 45 floats, written cooperatively from LDS with
+    // 16-byte lane-contiguous accesses instead of 45 lane-strided ones.
     __shared__ float s_k[256 * 15];
     __shared__ float s_gc[256 * 3];
     __shared__ uint32_t s_nb[256];
@@ -290,31 +261,55 @@ __global__ void __launch_bounds__(256) preprocess_backward_kernel(
     const int nblk = (int)min((int64_t)256, n - blk0);
     const int t = (int)threadIdx.x;
     const int64_t i = blk0 + t;
-    if (bases > 1) stage_block(s_sh, shr_all + blk0 * 45, nblk * 45);
-    __syncthreads();
     const bool vis = t < nblk && n_touched[i] != 0;
+    // 2D gradient sums: up to kLightRecords per-(primitive, bucket) records
+    // are summed here; a primitive with more was summed into grad2d by
+    // gather_heavy. The record counter is cleared for the next backward.
+    const uint32_t nrec = vis ? rec_count[i] : 0u;
+    float4 gA = make_float4(0.f, 0.f, 0.f, 0.f), gB = gA, gC = gA;
+    if (nrec > kLightRecords) {
+        const float* gr = grad2d + (size_t)i * kGradStride;
+        gA = *(const float4*)(gr);
+        gB = *(const float4*)(gr + 4);
+        gC = *(const float4*)(gr + 8);
+    } else if (nrec > 0) {
+        const float4* rec = records + 3 * (size_t)first_slot[i];
+        for (uint32_t r = 0; r < nrec; ++r) {
+            const float4 a = rec[3 * r], b = rec[3 * r + 1], c = rec[3 * r + 2];
+            gA.x += a.x; gA.y += a.y; gA.z += a.z; gA.w += a.w;
+            gB.x += b.x; gB.y += b.y; gB.z += b.z; gB.w += b.w;
+            gC.x += c.x; gC.y += c.y; gC.z += c.z;
+        }
+    }
+    if (nrec) rec_count[i] = 0u;
     float gc[3] = {0.f, 0.f, 0.f};
     float k[15];
     for (int b = 0; b < 15; ++b) k[b] = 0.f;
     int nb = 0;
     const bool assign = assign_flag != 0;
-    if (vis) {
-        preprocess_backward_one<ShT>(i, means, scales, rots, s_sh + 45 * t, bases, cam, conic_opacity, rec_count,
-                                     first_slot, records, grad2d, g_means, g_scales, g_rots, g_opac, g_sh0, densif,
-                                     gc, k, nb, assign);
-    } else if (assign && t < nblk) {
-        for (int c = 0; c < 3; ++c) {
-            g_means[3 * i + c] = 0.f;
-            g_scales[3 * i + c] = 0.f;
-            g_sh0[3 * i + c] = 0.f;
+    if (nrec) {
+        preprocess_backward_one<ShT>(i, means, scales, rots, shr_all + 45 * i, bases, cam, conic_opacity, gA, gB, gC,
+                                     g_means, g_scales, g_rots, g_opac, g_sh0, densif, gc, k, nb, assign);
+    } else {
+        // no bucket of any tile reached this primitive: every gradient is
+        // exactly zero (products with zero 2D gradients), so its parameters
+        // are not read; densification still counts a visible primitive
+        // (kernels_backward.cuh:345), adding 0 to the gradient-norm sums
+        if (vis && densif) densif[i].x += 1.0f;
+        if (assign && t < nblk) {
+            for (int c = 0; c < 3; ++c) {
+                g_means[3 * i + c] = 0.f;
+                g_scales[3 * i + c] = 0.f;
+                g_sh0[3 * i + c] = 0.f;
+            }
+            for (int c = 0; c < 4; ++c) g_rots[4 * i + c] = 0.f;
+            g_opac[i] = 0.f;
         }
-        for (int c = 0; c < 4; ++c) g_rots[4 * i + c] = 0.f;
-        g_opac[i] = 0.f;
     }
     if (bases > 1 || assign) {
         for (int b = 0; b < 15; ++b) s_k[15 * t + b] = k[b];
         for (int c = 0; c < 3; ++c) s_gc[3 * t + c] = gc[c];
-        s_nb[t] = vis ? (uint32_t)nb : 0u;
+        s_nb[t] = nrec ? (uint32_t)nb : 0u;
         __syncthreads();
         // grad_sh_rest[i][b][c] += k_b * gc_c (kernels_backward.cuh:41-65), b < active bases - 1
         float* gbase = g_shr_all + blk0 * 45;
@@ -331,19 +326,24 @@ __global__ void __launch_bounds__(256) preprocess_backward_kernel(
                 }
                 *(float4*)(gbase + e0) = g4;
             } else if (e0 + 3 < total) {
-                float4 g4 = *(const float4*)(gbase + e0);
-                float* gv = (float*)&g4;
                 bool any = false;
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
                     const int e = e0 + q;
-                    const int gi = e / 45, r = e - 45 * gi, b = r / 3, c = r - 3 * b;
-                    if ((uint32_t)b < s_nb[gi]) {
-                        gv[q] = gv[q] + s_k[15 * gi + b] * s_gc[3 * gi + c];
-                        any = true;
-                    }
+                    const int gi = e / 45, r = e - 45 * gi, b = r / 3;
+                    any = any || (uint32_t)b < s_nb[gi];
                 }
-                if (any) *(float4*)(gbase + e0) = g4;
+                if (any) {   // read-modify-write only the vectors that change
+                    float4 g4 = *(const float4*)(gbase + e0);
+                    float* gv = (float*)&g4;
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        const int e = e0 + q;
+                        const int gi = e / 45, r = e - 45 * gi, b = r / 3, c = r - 3 * b;
+                        if ((uint32_t)b < s_nb[gi]) gv[q] = gv[q] + s_k[15 * gi + b] * s_gc[3 * gi + c];
+                    }
+                    *(float4*)(gbase + e0) = g4;
+                }
             } else {
                 for (int e = e0; e < total; ++e) {
                     const int gi = e / 45, r = e - 45 * gi, b = r / 3, c = r - 3 * b;
