@@ -15,16 +15,17 @@
 // Only primitives that some tile's blend backward reached (a nonzero record
 // count) run the chain; for the other visible ones every gradient is exactly
 // zero, so their parameters are never read (at 1M Gaussians most visible
-// primitives sit behind others and fall in this class). Their SH-rest rows
-// are read per thread from global memory only when needed.
+// primitives sit behind others and fall in this class). SH-rest parameter
+// rows are read per thread, and only for primitives with gradients.
 #include "common.h"
 #include "kernels.h"
 
 namespace tgs {
 
-// Gradient update: accumulate (+=, the reference contract) or assign (the
-// caller's zeroing fused into this write).
-__device__ __forceinline__ void gadd(float* p, float v, bool assign) { *p = assign ? v : *p + v; }
+// Gradients of one primitive's parameters (all but SH-rest).
+struct PrimGrad {
+    float m[3], s[3], sh0[3], r[4], o;
+};
 
 // Per-primitive part: everything except the SH-rest gradient write, which the
 // block performs cooperatively from k[] (basis values) and gc[] (dL/dcolour).
@@ -32,16 +33,15 @@ template <typename ShT>
 __device__ __forceinline__ void preprocess_backward_one(
     int64_t i, const float* __restrict__ means, const float* __restrict__ scales, const float* __restrict__ rots,
     const ShT* shr, int bases, const CamParams& cam, const float4* __restrict__ conic_opacity, const float4 gA,
-    const float4 gB, const float4 gC, float* __restrict__ g_means, float* __restrict__ g_scales,
-    float* __restrict__ g_rots, float* __restrict__ g_opac, float* __restrict__ g_sh0, float4* __restrict__ densif,
-    float gc_out[3], float k[15], int& nb_out, bool assign) {
+    const float4 gB, const float4 gC, float4* __restrict__ densif, PrimGrad& out, float gc_out[3], float k[15],
+    int& nb_out) {
     // gA: dmx, dmy, absx, absy; gB: dca, dcb, dcc, dr; gC: dg, db, alpha partial, -
     const float mx = means[3 * i], my = means[3 * i + 1], mz = means[3 * i + 2];
 
     // ---- SH backward (kernels_backward.cuh:22-86)
     const float gc[3] = {gB.w, gC.x, gC.y};
     for (int c = 0; c < 3; ++c) gc_out[c] = gc[c];
-    for (int c = 0; c < 3; ++c) gadd(g_sh0 + 3 * i + c, 0.28209479177387814f * gc[c], assign);
+    for (int c = 0; c < 3; ++c) out.sh0[c] = 0.28209479177387814f * gc[c];
     float dmc0 = 0.f, dmc1 = 0.f, dmc2 = 0.f;
     nb_out = 0;
     if (bases > 1) {
@@ -200,18 +200,18 @@ __device__ __forceinline__ void preprocess_backward_one(
     const float gmx = r1[0] * dcx + r2[0] * dcy + r3[0] * dcz;
     const float gmy = r1[1] * dcx + r2[1] * dcy + r3[1] * dcz;
     const float gmz = r1[2] * dcx + r2[2] * dcy + r3[2] * dcz;
-    gadd(g_means + 3 * i, gmx + dmc0, assign);
-    gadd(g_means + 3 * i + 1, gmy + dmc1, assign);
-    gadd(g_means + 3 * i + 2, gmz + dmc2, assign);
+    out.m[0] = (gmx + dmc0);
+    out.m[1] = (gmy + dmc1);
+    out.m[2] = (gmz + dmc2);
     const float dvx = R11 * R11 * d11 + R21 * R21 * d22 + R31 * R31 * d33 +
                       2.0f * (R11 * R21 * d12 + R11 * R31 * d13 + R21 * R31 * d23);
     const float dvy = R12 * R12 * d11 + R22 * R22 * d22 + R32 * R32 * d33 +
                       2.0f * (R12 * R22 * d12 + R12 * R32 * d13 + R22 * R32 * d23);
     const float dvz = R13 * R13 * d11 + R23 * R23 * d22 + R33 * R33 * d33 +
                       2.0f * (R13 * R23 * d12 + R13 * R33 * d13 + R23 * R33 * d23);
-    gadd(g_scales + 3 * i, 2.0f * e0 * e0 * dvx, assign);
-    gadd(g_scales + 3 * i + 1, 2.0f * e1 * e1 * dvy, assign);
-    gadd(g_scales + 3 * i + 2, 2.0f * e2 * e2 * dvz, assign);
+    out.s[0] = (2.0f * e0 * e0 * dvx);
+    out.s[1] = (2.0f * e1 * e1 * dvy);
+    out.s[2] = (2.0f * e2 * e2 * dvz);
     const float D11 = 2.0f * (S11 * d11 + S21 * d12 + S31 * d13);
     const float D12 = 2.0f * (S12 * d11 + S22 * d12 + S32 * d13);
     const float D13 = 2.0f * (S13 * d11 + S23 * d12 + S33 * d13);
@@ -227,11 +227,11 @@ __device__ __forceinline__ void preprocess_backward_one(
     const float hlp = qxx * gqxx + qyy * gqyy + qzz * gqzz + qxy * gqxy + qxz * gqxz + qyz * gqyz + qrx * gqrx +
                       qry * gqry + qrz * gqrz;
     const float den = qn * __builtin_sqrtf(qn);
-    gadd(g_rots + 4 * i, 2.0f * (qx * gqrx + qy * gqry + qz * gqrz - qr * hlp) / den, assign);
-    gadd(g_rots + 4 * i + 1, 2.0f * (2.0f * qx * gqxx + qy * gqxy + qz * gqxz + qr * gqrx - qx * hlp) / den, assign);
-    gadd(g_rots + 4 * i + 2, 2.0f * (2.0f * qy * gqyy + qx * gqxy + qz * gqyz + qr * gqry - qy * hlp) / den, assign);
-    gadd(g_rots + 4 * i + 3, 2.0f * (2.0f * qz * gqzz + qx * gqxz + qy * gqyz + qr * gqrz - qz * hlp) / den, assign);
-    gadd(g_opac + i, gC.z * (1.0f - conic_opacity[i].w), assign);
+    out.r[0] = (2.0f * (qx * gqrx + qy * gqry + qz * gqrz - qr * hlp) / den);
+    out.r[1] = (2.0f * (2.0f * qx * gqxx + qy * gqxy + qz * gqxz + qr * gqrx - qx * hlp) / den);
+    out.r[2] = (2.0f * (2.0f * qy * gqyy + qx * gqxy + qz * gqyz + qr * gqry - qy * hlp) / den);
+    out.r[3] = (2.0f * (2.0f * qz * gqzz + qx * gqxz + qy * gqyz + qr * gqrz - qz * hlp) / den);
+    out.o = (gC.z * (1.0f - conic_opacity[i].w));
     if (densif) {
         float4 d = densif[i];
         d.x += 1.0f;
@@ -243,6 +243,14 @@ __device__ __forceinline__ void preprocess_backward_one(
     }
 }
 
+// Writes n floats from LDS to global memory with 16-byte stores (the global
+// run starts 16-byte aligned), scalar stores for the tail.
+__device__ __forceinline__ void block_store(float* __restrict__ dst, const float* src, int n) {
+    const int nv = n >> 2;
+    for (int v = (int)threadIdx.x; v < nv; v += 256) ((float4*)dst)[v] = ((const float4*)src)[v];
+    for (int e = (nv << 2) + (int)threadIdx.x; e < n; e += 256) dst[e] = src[e];
+}
+
 template <typename ShT>
 __global__ void __launch_bounds__(256) preprocess_backward_kernel(
     const float* __restrict__ means, const float* __restrict__ scales, const float* __restrict__ rots,
@@ -251,66 +259,105 @@ __global__ void __launch_bounds__(256) preprocess_backward_kernel(
     const uint32_t* __restrict__ first_slot, const float4* __restrict__ records, const float* __restrict__ grad2d,
     float* __restrict__ g_means, float* __restrict__ g_scales, float* __restrict__ g_rots, float* __restrict__ g_opac,
     float* __restrict__ g_sh0, float* __restrict__ g_shr_all, float4* __restrict__ densif, int assign_flag) {
-    // The SH-rest gradient rows of this block's 256 primitives are one
-    // contiguous run of 256 * 45 floats, written cooperatively from LDS with
-    // 16-byte lane-contiguous accesses instead of 45 lane-strided ones.
+    // Block of 256 consecutive primitives; each gradient array's rows of the
+    // block are one contiguous run (3, 3, 3, 4, 1 and 45 floats per
+    // primitive). Phase 1 compacts the primitives with 2D-gradient records
+    // into an LDS list; phase 2 runs the gradient chain for them on
+    // consecutive threads (one wave carries a typical block's few live
+    // primitives instead of four waves idling around them); phase 3 writes
+    // the block's rows from LDS with 16-byte stores (assign mode) or
+    // read-modify-writes only what changes (accumulate mode).
     __shared__ float s_k[256 * 15];
     __shared__ float s_gc[256 * 3];
     __shared__ uint32_t s_nb[256];
+    __shared__ __align__(16) float s_m[256 * 3], s_s[256 * 3], s_h[256 * 3], s_r[256 * 4], s_o[256];
+    __shared__ uint32_t s_live[256];
+    __shared__ uint32_t s_wcnt[4];
     const int64_t blk0 = (int64_t)blockIdx.x * 256;
     const int nblk = (int)min((int64_t)256, n - blk0);
     const int t = (int)threadIdx.x;
+    const uint32_t lane = (uint32_t)t & 63u, w = (uint32_t)t >> 6;
     const int64_t i = blk0 + t;
+    const bool assign = assign_flag != 0;
     const bool vis = t < nblk && n_touched[i] != 0;
-    // 2D gradient sums: up to kLightRecords per-(primitive, bucket) records
-    // are summed here; a primitive with more was summed into grad2d by
-    // gather_heavy. The record counter is cleared for the next backward.
     const uint32_t nrec = vis ? rec_count[i] : 0u;
-    float4 gA = make_float4(0.f, 0.f, 0.f, 0.f), gB = gA, gC = gA;
-    if (nrec > kLightRecords) {
-        const float* gr = grad2d + (size_t)i * kGradStride;
-        gA = *(const float4*)(gr);
-        gB = *(const float4*)(gr + 4);
-        gC = *(const float4*)(gr + 8);
-    } else if (nrec > 0) {
-        const float4* rec = records + 3 * (size_t)first_slot[i];
-        for (uint32_t r = 0; r < nrec; ++r) {
-            const float4 a = rec[3 * r], b = rec[3 * r + 1], c = rec[3 * r + 2];
-            gA.x += a.x; gA.y += a.y; gA.z += a.z; gA.w += a.w;
-            gB.x += b.x; gB.y += b.y; gB.z += b.z; gB.w += b.w;
-            gC.x += c.x; gC.y += c.y; gC.z += c.z;
+    s_nb[t] = 0u;
+    if (assign) {
+        for (int c = 0; c < 3; ++c) s_m[3 * t + c] = s_s[3 * t + c] = s_h[3 * t + c] = 0.f;
+        for (int c = 0; c < 4; ++c) s_r[4 * t + c] = 0.f;
+        s_o[t] = 0.f;
+    }
+    // no bucket of any tile reached this primitive: every gradient is exactly
+    // zero (products with zero 2D gradients); densification still counts a
+    // visible primitive (kernels_backward.cuh:345), adding 0 to its sums
+    if (vis && !nrec && densif) densif[i].x += 1.0f;
+    const uint64_t lm = ballot(nrec != 0u);
+    if (lane == 0) s_wcnt[w] = (uint32_t)__builtin_popcountll(lm);
+    __syncthreads();
+    uint32_t woff = 0;
+    for (uint32_t q = 0; q < w; ++q) woff += s_wcnt[q];
+    const uint32_t n_live = s_wcnt[0] + s_wcnt[1] + s_wcnt[2] + s_wcnt[3];
+    if (nrec) s_live[woff + mask_rank(lm)] = (uint32_t)t;
+    __syncthreads();
+    for (uint32_t idx = (uint32_t)t; idx < n_live; idx += 256u) {
+        const uint32_t tl = s_live[idx];
+        const int64_t ip = blk0 + tl;
+        // 2D gradient sums: up to kLightRecords per-(primitive, bucket)
+        // records are summed here; a primitive with more was summed into
+        // grad2d by gather_heavy. The counter is cleared for the next backward.
+        const uint32_t nr = rec_count[ip];
+        float4 gA = make_float4(0.f, 0.f, 0.f, 0.f), gB = gA, gC = gA;
+        if (nr > kLightRecords) {
+            const float* gr = grad2d + (size_t)ip * kGradStride;
+            gA = *(const float4*)(gr);
+            gB = *(const float4*)(gr + 4);
+            gC = *(const float4*)(gr + 8);
+        } else {
+            const float4* rec = records + 3 * (size_t)first_slot[ip];
+            for (uint32_t r = 0; r < nr; ++r) {
+                const float4 a = rec[3 * r], b = rec[3 * r + 1], c = rec[3 * r + 2];
+                gA.x += a.x; gA.y += a.y; gA.z += a.z; gA.w += a.w;
+                gB.x += b.x; gB.y += b.y; gB.z += b.z; gB.w += b.w;
+                gC.x += c.x; gC.y += c.y; gC.z += c.z;
+            }
+        }
+        rec_count[ip] = 0u;
+        PrimGrad g;
+        float gc[3], k[15];
+        for (int b = 0; b < 15; ++b) k[b] = 0.f;
+        int nb = 0;
+        preprocess_backward_one<ShT>(ip, means, scales, rots, shr_all + 45 * ip, bases, cam, conic_opacity, gA, gB, gC,
+                                     densif, g, gc, k, nb);
+        for (int b = 0; b < 15; ++b) s_k[15 * tl + b] = k[b];
+        for (int c = 0; c < 3; ++c) s_gc[3 * tl + c] = gc[c];
+        s_nb[tl] = (uint32_t)nb;
+        if (assign) {
+            for (int c = 0; c < 3; ++c) {
+                s_m[3 * tl + c] = g.m[c];
+                s_s[3 * tl + c] = g.s[c];
+                s_h[3 * tl + c] = g.sh0[c];
+            }
+            for (int c = 0; c < 4; ++c) s_r[4 * tl + c] = g.r[c];
+            s_o[tl] = g.o;
+        } else {
+            for (int c = 0; c < 3; ++c) {
+                g_means[3 * ip + c] += g.m[c];
+                g_scales[3 * ip + c] += g.s[c];
+                g_sh0[3 * ip + c] += g.sh0[c];
+            }
+            for (int c = 0; c < 4; ++c) g_rots[4 * ip + c] += g.r[c];
+            g_opac[ip] += g.o;
         }
     }
-    if (nrec) rec_count[i] = 0u;
-    float gc[3] = {0.f, 0.f, 0.f};
-    float k[15];
-    for (int b = 0; b < 15; ++b) k[b] = 0.f;
-    int nb = 0;
-    const bool assign = assign_flag != 0;
-    if (nrec) {
-        preprocess_backward_one<ShT>(i, means, scales, rots, shr_all + 45 * i, bases, cam, conic_opacity, gA, gB, gC,
-                                     g_means, g_scales, g_rots, g_opac, g_sh0, densif, gc, k, nb, assign);
-    } else {
-        // no bucket of any tile reached this primitive: every gradient is
-        // exactly zero (products with zero 2D gradients), so its parameters
-        // are not read; densification still counts a visible primitive
-        // (kernels_backward.cuh:345), adding 0 to the gradient-norm sums
-        if (vis && densif) densif[i].x += 1.0f;
-        if (assign && t < nblk) {
-            for (int c = 0; c < 3; ++c) {
-                g_means[3 * i + c] = 0.f;
-                g_scales[3 * i + c] = 0.f;
-                g_sh0[3 * i + c] = 0.f;
-            }
-            for (int c = 0; c < 4; ++c) g_rots[4 * i + c] = 0.f;
-            g_opac[i] = 0.f;
-        }
+    __syncthreads();
+    if (assign) {
+        block_store(g_means + 3 * blk0, s_m, 3 * nblk);
+        block_store(g_scales + 3 * blk0, s_s, 3 * nblk);
+        block_store(g_sh0 + 3 * blk0, s_h, 3 * nblk);
+        block_store(g_rots + 4 * blk0, s_r, 4 * nblk);
+        block_store(g_opac + blk0, s_o, nblk);
     }
     if (bases > 1 || assign) {
-        for (int b = 0; b < 15; ++b) s_k[15 * t + b] = k[b];
-        for (int c = 0; c < 3; ++c) s_gc[3 * t + c] = gc[c];
-        s_nb[t] = nrec ? (uint32_t)nb : 0u;
-        __syncthreads();
         // grad_sh_rest[i][b][c] += k_b * gc_c (kernels_backward.cuh:41-65), b < active bases - 1
         float* gbase = g_shr_all + blk0 * 45;
         const int total = nblk * 45;
@@ -333,7 +380,7 @@ __global__ void __launch_bounds__(256) preprocess_backward_kernel(
                     const int gi = e / 45, r = e - 45 * gi, b = r / 3;
                     any = any || (uint32_t)b < s_nb[gi];
                 }
-                if (any) {   // read-modify-write only the vectors that change
+                if (any) {
                     float4 g4 = *(const float4*)(gbase + e0);
                     float* gv = (float*)&g4;
 #pragma unroll
@@ -368,12 +415,14 @@ void launch_preprocess_backward(const GaussianView& g, const CamParams& cam, con
     if (g.sh_dtype == kShF16) {
         preprocess_backward_kernel<__half><<<grid, 256, 0, s>>>(
             g.means, g.scales, g.rotations, (const __half*)g.sh_rest, g.n, bases, cam, n_touched, conic_opacity,
-            rec_count, first_slot, records, grad2d, out.means, out.scales, out.rotations, out.opacities, out.sh0, out.sh_rest, (float4*)densif,
+            rec_count, first_slot, records, grad2d, out.means, out.scales, out.rotations, out.opacities, out.sh0,
+            out.sh_rest, (float4*)densif,
             assign ? 1 : 0);
     } else {
         preprocess_backward_kernel<float><<<grid, 256, 0, s>>>(
             g.means, g.scales, g.rotations, (const float*)g.sh_rest, g.n, bases, cam, n_touched, conic_opacity,
-            rec_count, first_slot, records, grad2d, out.means, out.scales, out.rotations, out.opacities, out.sh0, out.sh_rest, (float4*)densif,
+            rec_count, first_slot, records, grad2d, out.means, out.scales, out.rotations, out.opacities, out.sh0,
+            out.sh_rest, (float4*)densif,
             assign ? 1 : 0);
     }
 }
