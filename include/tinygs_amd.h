@@ -140,6 +140,20 @@ int tgs_loss_create(const char* type, tgs_loss** out);
 int tgs_loss_destroy(tgs_loss* l);
 int tgs_loss_evaluate(tgs_loss* l, const tgs_loss_context* ctx, float scale, void* stream);
 
+/* Fused 0.8-L1 + 0.2-SSIM style evaluation: the L1 term (scale l1_scale,
+ * normalised by W*H*3 as l1.cu:117-121) and the SSIM term (scale ssim_scale,
+ * normalised by H*W as fused_ssim.cu:811) of one prediction in two launches,
+ * equal to tgs_loss_evaluate of an "l1" and then a "fused_ssim" loss (the
+ * L1 term is added first). No counterpart method in the reference: it is the
+ * loss_l1_ssim entry of the boundary, for callers that evaluate both losses
+ * of Orchestrator::evaluate_losses (tinygs/src/orchestrator.cu:763-807)
+ * together. Any loss handle works (it supplies the SSIM scratch maps).
+ * flags: TGS_LOSS_ASSIGN writes loss / grad instead of accumulating, the same
+ * as zeroing them first (orchestrator.cu:354-355). */
+#define TGS_LOSS_ASSIGN 1
+int tgs_loss_l1_ssim(tgs_loss* l, const tgs_loss_context* ctx, float l1_scale, float ssim_scale, int32_t flags,
+                     void* stream);
+
 /* ---- SimpleAdam: replaces create_optimizer("simple_adam") / SimpleAdam
  * (tinygs/src/optim/optim.cu:86-105, tinygs/src/optim/simple_adam.cu:406-580). */
 typedef struct tgs_adam_params {

@@ -279,6 +279,43 @@ def test_l1_and_ssim(hip, orc, wh):
     assert normwise_err(gg[idx], go[idx]) < 1e-5
 
 
+@pytest.mark.parametrize("wh", [(64, 64), (61, 45), (1920, 1080)])
+@pytest.mark.parametrize("assign", [False, True])
+def test_fused_l1_ssim(hip, orc, wh, assign):
+    """tgs_loss_l1_ssim == L1 then fused SSIM; assign mode == zeroed buffers
+    (the buffers start as NaN there, so every padded element must be written)."""
+    import torch
+    from tinygs_amd.core import Image, LossContext
+    from tinygs_amd.loss import create_loss, evaluate_l1_ssim
+    shape = ImageShape(*wh)
+    rng = np.random.default_rng(wh[0] + 7)
+    targ = rng.random(shape.padded_size).astype(np.float32)
+    pred = np.clip(targ + rng.normal(0, 0.3, shape.padded_size), -0.2, 1.2).astype(np.float32)
+    if assign:
+        l0 = np.full(shape.padded_size, np.nan, np.float32)
+        g0 = np.full(shape.padded_size, np.nan, np.float32)
+    else:
+        l0 = rng.random(shape.padded_size).astype(np.float32)
+        g0 = rng.normal(0, 1e-3, shape.padded_size).astype(np.float32)
+    L = create_loss("l1")
+    ctx = LossContext(Image(shape, "float32", _dev(pred)), Image(shape, "float32", _dev(targ)),
+                      Image(shape, "float32", _dev(l0)), Image(shape, "float32", _dev(g0)))
+    evaluate_l1_ssim(L, ctx, 0.8, 0.2, assign=assign)
+    torch.cuda.synchronize()
+    lg, gg = ctx.loss.data.cpu().numpy(), ctx.grad.data.cpu().numpy()
+    lo = np.zeros_like(l0) if assign else l0.copy()
+    go = np.zeros_like(g0) if assign else g0.copy()
+    orc.l1(pred, targ, shape, np.float32(0.8), lo, go)
+    orc.ssim(pred, targ, shape, np.float32(0.2), lo, go)
+    assert np.all(np.isfinite(lg)) and np.all(np.isfinite(gg))
+    inside = np.zeros(shape.padded_size, bool)
+    inside[np.concatenate([c * shape.channel_stride + tiled_index(shape).reshape(-1) for c in range(3)])] = True
+    # padding: the L1 term only, bit-exact
+    assert np.array_equal(lg[~inside], lo[~inside]) and np.array_equal(gg[~inside], go[~inside])
+    assert np.allclose(lg[inside], lo[inside], rtol=1e-5, atol=1e-9), np.abs(lg[inside] - lo[inside]).max()
+    assert normwise_err(gg[inside], go[inside]) < 1e-5
+
+
 # ---------------------------------------------------------------- adam
 
 def test_adam_matches_oracle(hip, orc):

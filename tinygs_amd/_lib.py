@@ -16,6 +16,7 @@ LIB_PATH = os.path.join(HERE, "libtinygs_amd.so")
 
 TGS_DTYPE_FLOAT32 = 0
 TGS_DTYPE_FLOAT16 = 1
+TGS_LOSS_ASSIGN = 1
 
 _lib = None
 _hip = None
@@ -70,6 +71,7 @@ SIGNATURES = {
     "tgs_loss_create": ([C.c_char_p, PP], C.c_int),
     "tgs_loss_destroy": ([P], C.c_int),
     "tgs_loss_evaluate": ([P, C.POINTER(tgs_loss_context), C.c_float, P], C.c_int),
+    "tgs_loss_l1_ssim": ([P, C.POINTER(tgs_loss_context), C.c_float, C.c_float, C.c_int32, P], C.c_int),
     "tgs_adam_create": ([C.POINTER(tgs_gaussians), C.POINTER(tgs_gaussians), PP], C.c_int),
     "tgs_adam_destroy": ([P], C.c_int),
     "tgs_adam_set_params": ([P, C.POINTER(tgs_adam_params)], C.c_int),

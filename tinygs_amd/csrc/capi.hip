@@ -599,13 +599,47 @@ int tgs_loss_evaluate(tgs_loss* l, const tgs_loss_context* c, float scale, void*
     StageScope sc(ST_SSIM, s);
     if (c->grad) {
         for (auto& b : l->dm) TGS_TRY(ensure(b, sizeof(float) * (size_t)padded, s));
-        launch_ssim_forward(c->width, c->height, C1, C2, actual, (const float*)c->pred, (const float*)c->target,
-                            (float*)c->loss, l->dm[0].as<float>(), l->dm[1].as<float>(), l->dm[2].as<float>(), s);
+        launch_l1_ssim_forward(c->width, c->height, C1, C2, actual, 0.0f, false, (const float*)c->pred,
+                               (const float*)c->target, (float*)c->loss, nullptr, l->dm[0].as<float>(),
+                               l->dm[1].as<float>(), l->dm[2].as<float>(), s);
         launch_ssim_backward(c->width, c->height, actual, (const float*)c->pred, (const float*)c->target,
                              (float*)c->grad, l->dm[0].as<float>(), l->dm[1].as<float>(), l->dm[2].as<float>(), s);
     } else {
-        launch_ssim_forward(c->width, c->height, C1, C2, actual, (const float*)c->pred, (const float*)c->target,
-                            (float*)c->loss, nullptr, nullptr, nullptr, s);
+        launch_l1_ssim_forward(c->width, c->height, C1, C2, actual, 0.0f, false, (const float*)c->pred,
+                               (const float*)c->target, (float*)c->loss, nullptr, nullptr, nullptr, nullptr, s);
+    }
+    TGS_CHECK_LAUNCH();
+    return TGS_OK;
+}
+
+int tgs_loss_l1_ssim(tgs_loss* l, const tgs_loss_context* c, float l1_scale, float ssim_scale, int32_t flags,
+                     void* stream) {
+    if (!l || !c) return fail(TGS_ERR_INVALID, "NULL argument");
+    if (c->dtype != TGS_DTYPE_FLOAT32)
+        return fail(TGS_ERR_UNSUPPORTED, "loss dtype %d: only float32 is supported", c->dtype);
+    if (!c->pred || !c->target) return fail(TGS_ERR_INVALID, "pred / target is NULL");
+    if (c->width == 0 || c->height == 0) return fail(TGS_ERR_INVALID, "empty image");
+    if (c->channel != 3) return fail(TGS_ERR_UNSUPPORTED, "fused L1 + SSIM needs 3 channels");
+    if (flags & ~TGS_LOSS_ASSIGN) return fail(TGS_ERR_INVALID, "unknown loss flags 0x%x", flags);
+    hipStream_t s = (hipStream_t)stream;
+    const bool assign = (flags & TGS_LOSS_ASSIGN) != 0;
+    const uint32_t tw = (c->width + 7u) >> 3, th = (c->height + 7u) >> 3;
+    const int64_t padded = (int64_t)tw * th * 64 * 3;
+    // the two reference normalisations: l1.cu:117-121 (W H C), fused_ssim.cu:811 (H W)
+    const float s_l1 = l1_scale / (float)(int)(c->width * c->height * 3u);
+    const float s_ssim = ssim_scale / (float)(int)(c->height * c->width);
+    const float C1 = 0.01f * 0.01f, C2 = 0.03f * 0.03f;
+    StageScope sc(ST_SSIM, s);
+    if (c->grad) {
+        for (auto& b : l->dm) TGS_TRY(ensure(b, sizeof(float) * (size_t)padded, s));
+        launch_l1_ssim_forward(c->width, c->height, C1, C2, s_ssim, s_l1, assign, (const float*)c->pred,
+                               (const float*)c->target, (float*)c->loss, (float*)c->grad, l->dm[0].as<float>(),
+                               l->dm[1].as<float>(), l->dm[2].as<float>(), s);
+        launch_ssim_backward(c->width, c->height, s_ssim, (const float*)c->pred, (const float*)c->target,
+                             (float*)c->grad, l->dm[0].as<float>(), l->dm[1].as<float>(), l->dm[2].as<float>(), s);
+    } else {
+        launch_l1_ssim_forward(c->width, c->height, C1, C2, s_ssim, s_l1, assign, (const float*)c->pred,
+                               (const float*)c->target, (float*)c->loss, nullptr, nullptr, nullptr, nullptr, s);
     }
     TGS_CHECK_LAUNCH();
     return TGS_OK;

@@ -132,8 +132,12 @@ void launch_fill_u32(uint32_t* p, uint32_t value, int64_t n, hipStream_t s);
 // ---- losses (l1.cu:19-42, fused_ssim.cu:55-442)
 void launch_l1(const float* pred, const float* target, float* loss, float* grad, int64_t n_padded, float s,
                hipStream_t st);
-void launch_ssim_forward(uint32_t width, uint32_t height, float c1, float c2, float s, const float* pred,
-                         const float* target, float* loss, float* dm_mu, float* dm_s1, float* dm_s12, hipStream_t st);
+// Fused L1 + SSIM forward: s_l1 == 0 disables L1; assign writes loss / grad
+// instead of accumulating (grad gets the L1 part, or 0); dm_* may be NULL
+// (loss only). The SSIM backward then adds its part to grad.
+void launch_l1_ssim_forward(uint32_t width, uint32_t height, float c1, float c2, float s_ssim, float s_l1,
+                            bool assign, const float* pred, const float* target, float* loss, float* grad,
+                            float* dm_mu, float* dm_s1, float* dm_s12, hipStream_t st);
 void launch_ssim_backward(uint32_t width, uint32_t height, float s, const float* pred, const float* target,
                           float* grad, const float* dm_mu, const float* dm_s1, const float* dm_s12, hipStream_t st);
 

@@ -1,13 +1,26 @@
 // L1 and fused-SSIM loss / gradient on the 8x8-tiled channel-planar image.
 // L1 follows tinygs/src/loss/l1.cu:19-42 (+ host scaling :109-151);
 // SSIM follows tinygs/src/loss/fused_ssim.cu:55-267 (forward),
-// :275-442 (backward), :797-916 (host): per channel, 16x16 output tiles with a
-// 5-pixel halo in LDS, inputs rounded to fp16 for the statistics, zero
-// padding outside the image, separable 11-tap Gaussian (sigma 1.5), and the
-// three partial-derivative maps convolved back in fp32.
-// Both accumulate into loss / grad (loss[i] += ..., grad[i] += ...).
-// Sums use explicit fma in the order of the reference loops so the results
-// match the CPU oracle's evaluation.
+// :275-442 (backward), :797-916 (host): per channel, inputs rounded to fp16
+// for the statistics, zero padding outside the image, separable 11-tap
+// Gaussian (sigma 1.5), and the three partial-derivative maps convolved back
+// in fp32 with the fp32 prediction and target.
+//
+// MI355X design: one workgroup per 32x32 output tile (42x42 with the 5-pixel
+// halo, filled through whole 8x8 blocks: coalesced 256-byte runs), all three
+// channels in turn. The horizontal pass gives each thread
+// four adjacent output columns of one row (14 inputs feed 4 x 11 taps), the
+// vertical pass four adjacent rows of one column (14 rows of horizontal sums
+// feed 4 x 11 taps), so every LDS value read is used several times. The SSIM
+// forward also evaluates L1 on the same pixels when asked (one launch for
+// 0.8 L1 + 0.2 (1 - SSIM) and its gradient's L1 part), and in assign mode
+// writes loss / gradient instead of accumulating, which spares the caller
+// zeroing them.
+//
+// Results accumulate unless assign: loss[i] += ..., grad[i] += ...; the L1
+// term is added before the SSIM term, as two separate reference launches
+// would. SSIM sums differ from the reference's summation order by rounding
+// only (the oracle comparison is normwise 1e-5).
 #include "common.h"
 #include "kernels.h"
 
@@ -18,178 +31,290 @@ __constant__ float kGauss[11] = {0.001028380123898387f,  0.0075987582094967365f,
                                  0.21300552785396576f,   0.10936068743467331f,   0.036000773310661316f,
                                  0.0075987582094967365f, 0.001028380123898387f};
 
-__global__ void l1_kernel(const float* __restrict__ pred, const float* __restrict__ target, float* __restrict__ loss,
-                          float* __restrict__ grad, int64_t n, float s) {
+// Vectorised over 16-byte groups (the padded image is a multiple of 64
+// floats per channel); kernels_forward of the same numerics: p = sat(pred),
+// loss += |p - t| s, grad += sign(p - t) s with sign(+0) = +1 (l1.cu:28-41).
+__global__ void l1_kernel(const float4* __restrict__ pred, const float4* __restrict__ target,
+                          float4* __restrict__ loss, float4* __restrict__ grad, int64_t n4, float s) {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= n) return;
-    const float p = saturate(pred[i]);
-    const float d = p - target[i];
-    if (loss) loss[i] = __builtin_fmaf(__builtin_fabsf(d), s, loss[i]);
-    if (grad) grad[i] = __builtin_fmaf(__builtin_copysignf(1.0f, d), s, grad[i]);
+    if (i >= n4) return;
+    const float4 p4 = pred[i], t4 = target[i];
+    const float pv[4] = {p4.x, p4.y, p4.z, p4.w}, tv[4] = {t4.x, t4.y, t4.z, t4.w};
+    float l[4], g[4];
+    float4 lo = loss ? loss[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+    float4 go = grad ? grad[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+    const float lv[4] = {lo.x, lo.y, lo.z, lo.w}, gv[4] = {go.x, go.y, go.z, go.w};
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const float d = saturate(pv[q]) - tv[q];
+        l[q] = __builtin_fmaf(__builtin_fabsf(d), s, lv[q]);
+        g[q] = __builtin_fmaf(__builtin_copysignf(1.0f, d), s, gv[q]);
+    }
+    if (loss) loss[i] = make_float4(l[0], l[1], l[2], l[3]);
+    if (grad) grad[i] = make_float4(g[0], g[1], g[2], g[3]);
 }
 
 void launch_l1(const float* pred, const float* target, float* loss, float* grad, int64_t n_padded, float s,
                hipStream_t st) {
     if (n_padded <= 0) return;
-    l1_kernel<<<(unsigned)((n_padded + 255) / 256), 256, 0, st>>>(pred, target, loss, grad, n_padded, s);
+    const int64_t n4 = n_padded / 4;   // padded planes hold whole 8x8 blocks
+    l1_kernel<<<(unsigned)((n4 + 255) / 256), 256, 0, st>>>((const float4*)pred, (const float4*)target,
+                                                            (float4*)loss, (float4*)grad, n4, s);
 }
 
-constexpr int kSX = 26;  // 16 + 2 * 5
+constexpr int kOT = 32;           // output tile edge
+constexpr int kIT = kOT + 10;     // input tile edge (5-pixel halo)
 
-__device__ __forceinline__ float round_half(float x) { return __half2float(__float2half_rn(x)); }
+// Halo fill through whole 8x8 blocks of the tiled layout: the 42x42 region
+// at (bx - 5, by - 5) lies inside the 6x6 blocks starting at block
+// (bx / 8 - 1, by / 8 - 1) (bx, by multiples of 32). Wave w loads blocks
+// w, w + 4, ... (one contiguous 256-byte run per plane each), lane = pixel of
+// the block. Every load is issued before any value is used. Round r of this
+// thread covers LDS cell (ly[r], lx[r]), or none (lx[r] = -1); pixels outside
+// W x H read as 0 (the reference's zero padding).
+constexpr int kHaloBlocks = 36;
+constexpr int kHaloRounds = kHaloBlocks / 4;   // 9 blocks per wave
+__device__ __forceinline__ bool halo_cell(int r, int bx, int by, uint32_t W, uint32_t H, uint32_t tw, uint32_t& q,
+                                          int& lx, int& ly) {
+    const int w = (int)(threadIdx.x >> 6), lane = (int)(threadIdx.x & 63u);
+    const int b = w + 4 * r;
+    const int bcx = bx / 8 - 1 + b % 6, bcy = by / 8 - 1 + b / 6;
+    const int gx = bcx * 8 + (lane & 7), gy = bcy * 8 + (lane >> 3);
+    lx = gx - (bx - 5);
+    ly = gy - (by - 5);
+    const bool cell = lx >= 0 && lx < kIT && ly >= 0 && ly < kIT;
+    if (!cell) lx = -1;
+    const bool in = cell && gx >= 0 && gy >= 0 && gx < (int)W && gy < (int)H;
+    q = in ? ((uint32_t)bcy * tw + (uint32_t)bcx) * 64u + (uint32_t)lane : 0u;
+    return in;
+}
+__device__ __forceinline__ void halo_load2(const float* __restrict__ a, const float* __restrict__ b, int bx, int by,
+                                           uint32_t W, uint32_t H, uint32_t tw, float av[kHaloRounds],
+                                           float bv[kHaloRounds], int lx[kHaloRounds], int ly[kHaloRounds]) {
+#pragma unroll
+    for (int r = 0; r < kHaloRounds; ++r) {
+        uint32_t q;
+        const bool in = halo_cell(r, bx, by, W, H, tw, q, lx[r], ly[r]);
+        const float x = a[q], y = b[q];   // q = 0 (always allocated) when outside
+        av[r] = in ? x : 0.f;
+        bv[r] = in ? y : 0.f;
+    }
+}
+__device__ __forceinline__ void halo_load1(const float* __restrict__ a, int bx, int by, uint32_t W, uint32_t H,
+                                           uint32_t tw, float av[kHaloRounds]) {
+#pragma unroll
+    for (int r = 0; r < kHaloRounds; ++r) {
+        uint32_t q;
+        int lx, ly;
+        const bool in = halo_cell(r, bx, by, W, H, tw, q, lx, ly);
+        const float x = a[q];
+        av[r] = in ? x : 0.f;
+    }
+}
 
-__global__ void __launch_bounds__(256) ssim_forward_kernel(uint32_t W, uint32_t H, float C1, float C2, float s,
-                                                           const float* __restrict__ pred,
-                                                           const float* __restrict__ target,
-                                                           float* __restrict__ loss, float* __restrict__ dm_mu,
-                                                           float* __restrict__ dm_s1, float* __restrict__ dm_s12) {
-    __shared__ float2 sT[kSX][kSX];
-    __shared__ float xc[kSX][16][5];
-    const int tx = threadIdx.x & 15, ty = threadIdx.x >> 4;
-    const int bx = blockIdx.x * 16, by = blockIdx.y * 16;
+// Fused L1 + SSIM forward. s_l1 == 0 disables L1; assign writes loss / grad
+// instead of accumulating (grad then holds the L1 part, or 0). dm_* may be
+// NULL (loss only). SSIM terms only inside W x H; L1 over the whole padded
+// image, like the reference's L1 over all padded elements.
+__global__ void __launch_bounds__(256) l1_ssim_forward_kernel(uint32_t W, uint32_t H, float C1, float C2,
+                                                              float s_ssim, float s_l1, int assign,
+                                                              const float* __restrict__ pred,
+                                                              const float* __restrict__ target,
+                                                              float* __restrict__ loss, float* __restrict__ grad,
+                                                              float* __restrict__ dm_mu, float* __restrict__ dm_s1,
+                                                              float* __restrict__ dm_s12) {
+    __shared__ __half2 s_in[kIT][kIT];         // fp16-rounded (pred, target), exactly the values the sums use
+    __shared__ float s_h[5][kIT][kOT + 1];     // horizontal sums: x, x^2, y, y^2, xy
+    const int t = (int)threadIdx.x;
+    const int bx = (int)blockIdx.x * kOT, by = (int)blockIdx.y * kOT;
     const uint32_t tw = (W + 7u) >> 3, th = (H + 7u) >> 3;
     const uint32_t cs = tw * th * 64u;
-    const int pxx = bx + tx, pyy = by + ty;
-    const bool inside = pxx < (int)W && pyy < (int)H;
-    const uint32_t pi = inside ? tiled_index((uint32_t)pyy, (uint32_t)pxx, tw) : 0u;
+    const int pw = (int)tw * 8, ph = (int)th * 8;
+    // vertical-pass ownership: column vc, rows 4 vr .. 4 vr + 3
+    const int vc = t & 31, vr = t >> 5;
     for (int c = 0; c < 3; ++c) {
-        for (int k = threadIdx.x; k < kSX * kSX; k += 256) {
-            const int ly = k / kSX, lx = k % kSX;
-            const int gx = bx + lx - 5, gy = by + ly - 5;
-            float2 v = make_float2(0.f, 0.f);
-            if (gx >= 0 && gy >= 0 && gx < (int)W && gy < (int)H) {
-                const uint32_t q = tiled_index((uint32_t)gy, (uint32_t)gx, tw) + (uint32_t)c * cs;
-                v = make_float2(round_half(pred[q]), round_half(target[q]));
-            }
-            sT[ly][lx] = v;
+        const float* pc = pred + (size_t)c * cs;
+        const float* tc = target + (size_t)c * cs;
+        {
+            float pv[kHaloRounds], tv[kHaloRounds];
+            int lx[kHaloRounds], ly[kHaloRounds];
+            halo_load2(pc, tc, bx, by, W, H, tw, pv, tv, lx, ly);
+#pragma unroll
+            for (int r = 0; r < kHaloRounds; ++r)
+                if (lx[r] >= 0) s_in[ly[r]][lx[r]] = __floats2half2_rn(pv[r], tv[r]);
         }
         __syncthreads();
-        for (int ly = ty; ly < kSX; ly += 16) {
-            float sx = 0.f, sx2 = 0.f, sy = 0.f, sy2 = 0.f, sxy = 0.f;
+        // horizontal: row r, output columns 4 g .. 4 g + 3
+        for (int wi = t; wi < kIT * 8; wi += 256) {
+            const int r = wi >> 3, g = wi & 7;
+            float x[14], y[14];
 #pragma unroll
-            for (int d = 0; d < 11; ++d) {
-                const float wv = kGauss[d];
-                const float2 v = sT[ly][tx + d];
-                sx = __builtin_fmaf(v.x, wv, sx);
-                sx2 = __builtin_fmaf(v.x * v.x, wv, sx2);
-                sy = __builtin_fmaf(v.y, wv, sy);
-                sy2 = __builtin_fmaf(v.y * v.y, wv, sy2);
-                sxy = __builtin_fmaf(v.x * v.y, wv, sxy);
+            for (int d = 0; d < 14; ++d) {
+                const float2 v = __half22float2(s_in[r][4 * g + d]);
+                x[d] = v.x;
+                y[d] = v.y;
             }
-            xc[ly][tx][0] = sx; xc[ly][tx][1] = sx2; xc[ly][tx][2] = sy; xc[ly][tx][3] = sy2; xc[ly][tx][4] = sxy;
+#pragma unroll
+            for (int o = 0; o < 4; ++o) {
+                float sx = 0.f, sxx = 0.f, sy = 0.f, syy = 0.f, sxy = 0.f;
+#pragma unroll
+                for (int d = 0; d < 11; ++d) {
+                    const float wv = kGauss[d];
+                    const float a = x[o + d], b = y[o + d];
+                    sx = __builtin_fmaf(a, wv, sx);
+                    sxx = __builtin_fmaf(a * a, wv, sxx);
+                    sy = __builtin_fmaf(b, wv, sy);
+                    syy = __builtin_fmaf(b * b, wv, syy);
+                    sxy = __builtin_fmaf(a * b, wv, sxy);
+                }
+                s_h[0][r][4 * g + o] = sx;
+                s_h[1][r][4 * g + o] = sxx;
+                s_h[2][r][4 * g + o] = sy;
+                s_h[3][r][4 * g + o] = syy;
+                s_h[4][r][4 * g + o] = sxy;
+            }
         }
         __syncthreads();
-        if (inside) {
-            float o0 = 0.f, o1 = 0.f, o2 = 0.f, o3 = 0.f, o4 = 0.f;
+        // vertical: column vc, output rows 4 vr .. 4 vr + 3
+        float o[5][4];
 #pragma unroll
-            for (int d = 0; d < 11; ++d) {
-                const float wv = kGauss[d];
-                const float* cur = xc[ty + d][tx];
-                o0 = __builtin_fmaf(cur[0], wv, o0);
-                o1 = __builtin_fmaf(cur[1], wv, o1);
-                o2 = __builtin_fmaf(cur[2], wv, o2);
-                o3 = __builtin_fmaf(cur[3], wv, o3);
-                o4 = __builtin_fmaf(cur[4], wv, o4);
+        for (int v = 0; v < 5; ++v) {
+            float col[14];
+#pragma unroll
+            for (int d = 0; d < 14; ++d) col[d] = s_h[v][4 * vr + d][vc];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                float acc = 0.f;
+#pragma unroll
+                for (int d = 0; d < 11; ++d) acc = __builtin_fmaf(col[q + d], kGauss[d], acc);
+                o[v][q] = acc;
             }
-            const float mu1 = o0, mu2 = o2;
-            const float mu1_sq = mu1 * mu1, mu2_sq = mu2 * mu2;
-            const float s1 = o1 - mu1_sq, s2 = o3 - mu2_sq, s12 = o4 - mu1 * mu2;
-            const float A = mu1_sq + mu2_sq + C1;
-            const float B = s1 + s2 + C2;
-            const float Cc = 2.0f * mu1 * mu2 + C1;
-            const float D = 2.0f * s12 + C2;
-            const float val = (Cc * D) / (A * B);
-            const uint32_t q = pi + (uint32_t)c * cs;
-            if (loss) loss[q] = __builtin_fmaf(1.0f - val, s, loss[q]);
-            if (dm_mu) {
-                dm_mu[q] = (mu2 * 2.0f * D) / (A * B) - (mu2 * 2.0f * Cc) / (A * B) -
-                           (mu1 * 2.0f * Cc * D) / (A * A * B) + (mu1 * 2.0f * Cc * D) / (A * B * B);
-                dm_s1[q] = (-Cc * D) / (A * B * B);
-                dm_s12[q] = (2.0f * Cc) / (A * B);
+        }
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int px = bx + vc, py = by + 4 * vr + q;
+            if (px >= pw || py >= ph) continue;
+            const uint32_t idx = tiled_index((uint32_t)py, (uint32_t)px, tw) + (uint32_t)c * cs;
+            float lv = assign ? 0.f : (loss ? loss[idx] : 0.f);
+            float gv = assign ? 0.f : (grad ? grad[idx] : 0.f);
+            if (s_l1 != 0.f) {
+                const float d = saturate(pred[idx]) - target[idx];
+                lv = __builtin_fmaf(__builtin_fabsf(d), s_l1, lv);
+                gv = __builtin_fmaf(__builtin_copysignf(1.0f, d), s_l1, gv);
             }
+            if (px < (int)W && py < (int)H) {
+                const float mu1 = o[0][q], mu2 = o[2][q];
+                const float mu1_sq = mu1 * mu1, mu2_sq = mu2 * mu2;
+                const float s1 = o[1][q] - mu1_sq, s2 = o[3][q] - mu2_sq, s12 = o[4][q] - mu1 * mu2;
+                const float A = mu1_sq + mu2_sq + C1;
+                const float B = s1 + s2 + C2;
+                const float Cc = 2.0f * mu1 * mu2 + C1;
+                const float D = 2.0f * s12 + C2;
+                // one reciprocal each of A and B replaces the reference's seven divisions
+                const float iA = __builtin_amdgcn_rcpf(A), iB = __builtin_amdgcn_rcpf(B);
+                const float inv = iA * iB;
+                const float val = (Cc * D) * inv;
+                lv = __builtin_fmaf(1.0f - val, s_ssim, lv);
+                if (dm_mu) {
+                    dm_mu[idx] = 2.0f * inv * (mu2 * (D - Cc) + mu1 * (Cc * D) * (iB - iA));
+                    dm_s1[idx] = -(Cc * D) * inv * iB;
+                    dm_s12[idx] = 2.0f * Cc * inv;
+                }
+            }
+            if (loss) loss[idx] = lv;
+            if (grad && (assign || s_l1 != 0.f)) grad[idx] = gv;
         }
         __syncthreads();
     }
 }
 
+// SSIM backward: grad += -s (dm_mu * w + 2 p (dm_s1 * w) + t (dm_s12 * w))
+// with * the 11x11 separable convolution (fused_ssim.cu:366-438).
 __global__ void __launch_bounds__(256) ssim_backward_kernel(uint32_t W, uint32_t H, float s,
                                                             const float* __restrict__ pred,
                                                             const float* __restrict__ target,
                                                             float* __restrict__ grad, const float* __restrict__ dm_mu,
                                                             const float* __restrict__ dm_s1,
                                                             const float* __restrict__ dm_s12) {
-    __shared__ float sD[3][kSX][kSX];
-    __shared__ float sS[kSX][16][3];
-    const int tx = threadIdx.x & 15, ty = threadIdx.x >> 4;
-    const int bx = blockIdx.x * 16, by = blockIdx.y * 16;
+    __shared__ float s_d[3][kIT][kIT];
+    __shared__ float s_h[3][kIT][kOT + 1];
+    const int t = (int)threadIdx.x;
+    const int bx = (int)blockIdx.x * kOT, by = (int)blockIdx.y * kOT;
     const uint32_t tw = (W + 7u) >> 3, th = (H + 7u) >> 3;
     const uint32_t cs = tw * th * 64u;
-    const int pxx = bx + tx, pyy = by + ty;
-    const bool inside = pxx < (int)W && pyy < (int)H;
-    const uint32_t pi = inside ? tiled_index((uint32_t)pyy, (uint32_t)pxx, tw) : 0u;
+    const int vc = t & 31, vr = t >> 5;
     for (int c = 0; c < 3; ++c) {
-        for (int k = threadIdx.x; k < kSX * kSX; k += 256) {
-            const int ly = k / kSX, lx = k % kSX;
-            const int gx = bx + lx - 5, gy = by + ly - 5;
-            float a = 0.f, b = 0.f, d = 0.f;
-            if (gx >= 0 && gy >= 0 && gx < (int)W && gy < (int)H) {
-                const uint32_t q = tiled_index((uint32_t)gy, (uint32_t)gx, tw) + (uint32_t)c * cs;
-                a = dm_mu[q]; b = dm_s1[q]; d = dm_s12[q];
-            }
-            sD[0][ly][lx] = a; sD[1][ly][lx] = b; sD[2][ly][lx] = d;
+        {
+            float av[kHaloRounds], bv[kHaloRounds], dv[kHaloRounds];
+            int lx[kHaloRounds], ly[kHaloRounds];
+            halo_load2(dm_mu + (size_t)c * cs, dm_s1 + (size_t)c * cs, bx, by, W, H, tw, av, bv, lx, ly);
+            halo_load1(dm_s12 + (size_t)c * cs, bx, by, W, H, tw, dv);
+#pragma unroll
+            for (int r = 0; r < kHaloRounds; ++r)
+                if (lx[r] >= 0) {
+                    s_d[0][ly[r]][lx[r]] = av[r];
+                    s_d[1][ly[r]][lx[r]] = bv[r];
+                    s_d[2][ly[r]][lx[r]] = dv[r];
+                }
         }
         __syncthreads();
-        for (int yy = ty; yy < kSX; yy += 16) {
-            const int lx = tx + 5;
-            float a0 = 0.f, a1 = 0.f, a2 = 0.f;
+        for (int wi = t; wi < kIT * 8; wi += 256) {
+            const int r = wi >> 3, g = wi & 7;
 #pragma unroll
-            for (int d = 1; d <= 5; ++d) {
-                const float wv = kGauss[5 - d];
-                a0 = __builtin_fmaf(sD[0][yy][lx - d] + sD[0][yy][lx + d], wv, a0);
-                a1 = __builtin_fmaf(sD[1][yy][lx - d] + sD[1][yy][lx + d], wv, a1);
-                a2 = __builtin_fmaf(sD[2][yy][lx - d] + sD[2][yy][lx + d], wv, a2);
+            for (int v = 0; v < 3; ++v) {
+                float x[14];
+#pragma unroll
+                for (int d = 0; d < 14; ++d) x[d] = s_d[v][r][4 * g + d];
+#pragma unroll
+                for (int o = 0; o < 4; ++o) {
+                    float acc = 0.f;
+#pragma unroll
+                    for (int d = 0; d < 11; ++d) acc = __builtin_fmaf(x[o + d], kGauss[d], acc);
+                    s_h[v][r][4 * g + o] = acc;
+                }
             }
-            const float wc = kGauss[5];
-            a0 = __builtin_fmaf(sD[0][yy][lx], wc, a0);
-            a1 = __builtin_fmaf(sD[1][yy][lx], wc, a1);
-            a2 = __builtin_fmaf(sD[2][yy][lx], wc, a2);
-            sS[yy][tx][0] = a0; sS[yy][tx][1] = a1; sS[yy][tx][2] = a2;
         }
         __syncthreads();
-        if (inside) {
-            const int ly = ty + 5;
-            float a0 = 0.f, a1 = 0.f, a2 = 0.f;
+        float o[3][4];
 #pragma unroll
-            for (int d = 1; d <= 5; ++d) {
-                const float wv = kGauss[5 - d];
-                a0 = __builtin_fmaf(sS[ly - d][tx][0] + sS[ly + d][tx][0], wv, a0);
-                a1 = __builtin_fmaf(sS[ly - d][tx][1] + sS[ly + d][tx][1], wv, a1);
-                a2 = __builtin_fmaf(sS[ly - d][tx][2] + sS[ly + d][tx][2], wv, a2);
+        for (int v = 0; v < 3; ++v) {
+            float col[14];
+#pragma unroll
+            for (int d = 0; d < 14; ++d) col[d] = s_h[v][4 * vr + d][vc];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                float acc = 0.f;
+#pragma unroll
+                for (int d = 0; d < 11; ++d) acc = __builtin_fmaf(col[q + d], kGauss[d], acc);
+                o[v][q] = acc;
             }
-            const float wc = kGauss[5];
-            a0 = __builtin_fmaf(sS[ly][tx][0], wc, a0);
-            a1 = __builtin_fmaf(sS[ly][tx][1], wc, a1);
-            a2 = __builtin_fmaf(sS[ly][tx][2], wc, a2);
-            const uint32_t q = pi + (uint32_t)c * cs;
-            const float p1 = pred[q], p2 = target[q];
-            const float dl = __builtin_fmaf(p2, a2, __builtin_fmaf(2.0f * p1, a1, a0));
-            grad[q] = __builtin_fmaf(-s, dl, grad[q]);
+        }
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int px = bx + vc, py = by + 4 * vr + q;
+            if (px >= (int)W || py >= (int)H) continue;
+            const uint32_t idx = tiled_index((uint32_t)py, (uint32_t)px, tw) + (uint32_t)c * cs;
+            const float p1 = pred[idx], p2 = target[idx];
+            const float dl = __builtin_fmaf(p2, o[2][q], __builtin_fmaf(2.0f * p1, o[1][q], o[0][q]));
+            grad[idx] = __builtin_fmaf(-s, dl, grad[idx]);
         }
         __syncthreads();
     }
 }
 
-void launch_ssim_forward(uint32_t width, uint32_t height, float c1, float c2, float s, const float* pred,
-                         const float* target, float* loss, float* dm_mu, float* dm_s1, float* dm_s12, hipStream_t st) {
+void launch_l1_ssim_forward(uint32_t width, uint32_t height, float c1, float c2, float s_ssim, float s_l1,
+                            bool assign, const float* pred, const float* target, float* loss, float* grad,
+                            float* dm_mu, float* dm_s1, float* dm_s12, hipStream_t st) {
     if (width == 0 || height == 0) return;
-    dim3 grid((width + 15) / 16, (height + 15) / 16);
-    ssim_forward_kernel<<<grid, 256, 0, st>>>(width, height, c1, c2, s, pred, target, loss, dm_mu, dm_s1, dm_s12);
+    dim3 grid((width + kOT - 1) / kOT, (height + kOT - 1) / kOT);
+    l1_ssim_forward_kernel<<<grid, 256, 0, st>>>(width, height, c1, c2, s_ssim, s_l1, assign ? 1 : 0, pred, target,
+                                                 loss, grad, dm_mu, dm_s1, dm_s12);
 }
 
 void launch_ssim_backward(uint32_t width, uint32_t height, float s, const float* pred, const float* target,
                           float* grad, const float* dm_mu, const float* dm_s1, const float* dm_s12, hipStream_t st) {
     if (width == 0 || height == 0) return;
-    dim3 grid((width + 15) / 16, (height + 15) / 16);
+    dim3 grid((width + kOT - 1) / kOT, (height + kOT - 1) / kOT);
     ssim_backward_kernel<<<grid, 256, 0, st>>>(width, height, s, pred, target, grad, dm_mu, dm_s1, dm_s12);
 }
 

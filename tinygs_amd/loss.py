@@ -37,6 +37,17 @@ class _CLoss(LossBase):
                 pass
             self._h = None
 
+    def _context(self, ctx: LossContext):
+        if ctx.pred.data_type != ctx.target.data_type:
+            raise RuntimeError(f"{self.name()}: prediction and target data type must be the same")
+        if ctx.pred.data_type != DataType.Float32:
+            raise RuntimeError(f"{self.name()}: only float32 is supported")
+        shape = ctx.pred.shape
+        return _lib.tgs_loss_context(ptr(ctx.pred.data), ptr(ctx.target.data),
+                                     ptr(ctx.loss.data) if ctx.loss else None,
+                                     ptr(ctx.grad.data) if ctx.grad else None,
+                                     shape.width, shape.height, shape.channel, _lib.TGS_DTYPE_FLOAT32)
+
     def evaluate(self, ctx: LossContext, scale: float):
         if ctx.pred.data_type != ctx.target.data_type:
             raise RuntimeError(f"{self.name()}: prediction and target data type must be the same")
@@ -49,6 +60,18 @@ class _CLoss(LossBase):
                                   shape.width, shape.height, shape.channel, _lib.TGS_DTYPE_FLOAT32)
         _lib.check(_lib.load().tgs_loss_evaluate(self._h, C.byref(c), float(scale), stream_ptr(ctx.stream)),
                    self.name())
+
+
+def evaluate_l1_ssim(loss: LossBase, ctx: LossContext, l1_scale: float, ssim_scale: float, assign: bool = False):
+    """L1 (scale l1_scale) then fused SSIM (scale ssim_scale) of one prediction
+    in two launches: the same result as evaluating an L1Loss and then a
+    FusedSSIMLoss with those scales. assign=True writes the loss / gradient
+    images instead of accumulating (as if they had been zeroed first).
+    `loss` is any loss object of this module (it holds the SSIM scratch)."""
+    c = loss._context(ctx)
+    flags = _lib.TGS_LOSS_ASSIGN if assign else 0
+    _lib.check(_lib.load().tgs_loss_l1_ssim(loss._h, C.byref(c), float(l1_scale), float(ssim_scale), flags,
+                                            stream_ptr(ctx.stream)), "l1_ssim")
 
 
 class L1Loss(_CLoss):

@@ -3,7 +3,9 @@ Orchestrator::train_step (tinygs/src/orchestrator.cu:335-439):
 
   zero parameter gradients (:351-353) and loss / gradient images (:354-355)
   -> FastGSRasterizer::forward (:371)
-  -> losses: L1 weight * grad_scaler, fused SSIM weight * grad_scaler (:763-782)
+  -> losses: L1 weight * grad_scaler, fused SSIM weight * grad_scaler (:763-782);
+     with both on, one fused evaluation that assigns the loss / gradient images
+     (the zeroing of :354-355 folded in)
   -> FastGSRasterizer::backward with grad_output = loss gradient (:377-380)
   -> SimpleAdam::step(1 / (grad_scaler * accumulate_grad_steps)) (:393-404)
 
@@ -13,7 +15,7 @@ inside the forward that sizes the instance buffers.
 from __future__ import annotations
 
 from .core import GPUBatchInput, GPUGaussian3d, Image, LossContext, RasterizeContext
-from .loss import create_loss
+from .loss import create_loss, evaluate_l1_ssim
 from .optim import create_optimizer
 from .rasterizer import create_rasterizer
 
@@ -57,10 +59,19 @@ class TrainStep:
         self.ctx.grad_output.image = self.grad_img
         self.loss_ctx = LossContext(self.pred, self.target, self.loss_img, self.grad_img, stream)
 
+    @property
+    def fused_losses(self) -> bool:
+        """Both L1 and SSIM are on: they run as one fused evaluation in
+        assign mode (no separate zeroing of the loss / gradient images)."""
+        return len(self.losses) == 2
+
     def zero(self):
-        """Zero the loss and loss-gradient images. The parameter gradients are
-        not zeroed here: the backward runs in assign mode, which writes every
-        gradient (zero for culled Gaussians), equivalent to zero + accumulate."""
+        """Zero the loss and loss-gradient images (unless the fused loss
+        evaluation assigns them). The parameter gradients are not zeroed here:
+        the backward runs in assign mode, which writes every gradient (zero for
+        culled Gaussians), equivalent to zero + accumulate."""
+        if self.fused_losses:
+            return
         import torch
         s = self.stream
         with torch.cuda.stream(s) if s is not None else _null():
@@ -71,6 +82,10 @@ class TrainStep:
         self.rasterizer.forward(self.ctx)
 
     def losses_and_grad(self):
+        if self.fused_losses:
+            (l1, w1), (_, w2) = self.losses
+            evaluate_l1_ssim(l1, self.loss_ctx, w1 * self.grad_scaler, w2 * self.grad_scaler, assign=True)
+            return
         for loss, w in self.losses:
             loss.evaluate(self.loss_ctx, w * self.grad_scaler)
 
