@@ -90,11 +90,12 @@ __device__ __forceinline__ bool halo_cell(int r, int bx, int by, uint32_t W, uin
 }
 __device__ __forceinline__ void halo_load2(const float* __restrict__ a, const float* __restrict__ b, int bx, int by,
                                            uint32_t W, uint32_t H, uint32_t tw, float av[kHaloRounds],
-                                           float bv[kHaloRounds], int lx[kHaloRounds], int ly[kHaloRounds]) {
+                                           float bv[kHaloRounds]) {
 #pragma unroll
     for (int r = 0; r < kHaloRounds; ++r) {
         uint32_t q;
-        const bool in = halo_cell(r, bx, by, W, H, tw, q, lx[r], ly[r]);
+        int lx, ly;
+        const bool in = halo_cell(r, bx, by, W, H, tw, q, lx, ly);
         const float x = a[q], y = b[q];   // q = 0 (always allocated) when outside
         av[r] = in ? x : 0.f;
         bv[r] = in ? y : 0.f;
@@ -132,18 +133,32 @@ __global__ void __launch_bounds__(256) l1_ssim_forward_kernel(uint32_t W, uint32
     const int pw = (int)tw * 8, ph = (int)th * 8;
     // vertical-pass ownership: column vc, rows 4 vr .. 4 vr + 3
     const int vc = t & 31, vr = t >> 5;
+    // software pipeline over the channels: channel c + 1's halo is loaded
+    // while channel c is convolved, and each channel's per-pixel operands are
+    // loaded before its passes
+    float pv[kHaloRounds], tv[kHaloRounds];
+    halo_load2(pred, target, bx, by, W, H, tw, pv, tv);
     for (int c = 0; c < 3; ++c) {
-        const float* pc = pred + (size_t)c * cs;
-        const float* tc = target + (size_t)c * cs;
-        {
-            float pv[kHaloRounds], tv[kHaloRounds];
-            int lx[kHaloRounds], ly[kHaloRounds];
-            halo_load2(pc, tc, bx, by, W, H, tw, pv, tv, lx, ly);
 #pragma unroll
-            for (int r = 0; r < kHaloRounds; ++r)
-                if (lx[r] >= 0) s_in[ly[r]][lx[r]] = __floats2half2_rn(pv[r], tv[r]);
+        for (int r = 0; r < kHaloRounds; ++r) {
+            uint32_t q;
+            int lx, ly;
+            halo_cell(r, bx, by, W, H, tw, q, lx, ly);
+            if (lx >= 0) s_in[ly][lx] = __floats2half2_rn(pv[r], tv[r]);
+        }
+        float ep[4], et[4], el[4], eg[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int px = bx + vc, py = by + 4 * vr + q;
+            const bool pad_ok = px < pw && py < ph;
+            const uint32_t idx = pad_ok ? tiled_index((uint32_t)py, (uint32_t)px, tw) + (uint32_t)c * cs : 0u;
+            ep[q] = pred[idx];
+            et[q] = target[idx];
+            el[q] = (!assign && loss) ? loss[idx] : 0.f;
+            eg[q] = (!assign && grad) ? grad[idx] : 0.f;
         }
         __syncthreads();
+        if (c < 2) halo_load2(pred + (size_t)(c + 1) * cs, target + (size_t)(c + 1) * cs, bx, by, W, H, tw, pv, tv);
         // horizontal: row r, output columns 4 g .. 4 g + 3
         for (int wi = t; wi < kIT * 8; wi += 256) {
             const int r = wi >> 3, g = wi & 7;
@@ -195,10 +210,10 @@ __global__ void __launch_bounds__(256) l1_ssim_forward_kernel(uint32_t W, uint32
             const int px = bx + vc, py = by + 4 * vr + q;
             if (px >= pw || py >= ph) continue;
             const uint32_t idx = tiled_index((uint32_t)py, (uint32_t)px, tw) + (uint32_t)c * cs;
-            float lv = assign ? 0.f : (loss ? loss[idx] : 0.f);
-            float gv = assign ? 0.f : (grad ? grad[idx] : 0.f);
+            float lv = el[q];
+            float gv = eg[q];
             if (s_l1 != 0.f) {
-                const float d = saturate(pred[idx]) - target[idx];
+                const float d = saturate(ep[q]) - et[q];
                 lv = __builtin_fmaf(__builtin_fabsf(d), s_l1, lv);
                 gv = __builtin_fmaf(__builtin_copysignf(1.0f, d), s_l1, gv);
             }
@@ -243,21 +258,37 @@ __global__ void __launch_bounds__(256) ssim_backward_kernel(uint32_t W, uint32_t
     const uint32_t tw = (W + 7u) >> 3, th = (H + 7u) >> 3;
     const uint32_t cs = tw * th * 64u;
     const int vc = t & 31, vr = t >> 5;
+    float av[kHaloRounds], bv[kHaloRounds], dv[kHaloRounds];
+    halo_load2(dm_mu, dm_s1, bx, by, W, H, tw, av, bv);
+    halo_load1(dm_s12, bx, by, W, H, tw, dv);
     for (int c = 0; c < 3; ++c) {
-        {
-            float av[kHaloRounds], bv[kHaloRounds], dv[kHaloRounds];
-            int lx[kHaloRounds], ly[kHaloRounds];
-            halo_load2(dm_mu + (size_t)c * cs, dm_s1 + (size_t)c * cs, bx, by, W, H, tw, av, bv, lx, ly);
-            halo_load1(dm_s12 + (size_t)c * cs, bx, by, W, H, tw, dv);
 #pragma unroll
-            for (int r = 0; r < kHaloRounds; ++r)
-                if (lx[r] >= 0) {
-                    s_d[0][ly[r]][lx[r]] = av[r];
-                    s_d[1][ly[r]][lx[r]] = bv[r];
-                    s_d[2][ly[r]][lx[r]] = dv[r];
-                }
+        for (int r = 0; r < kHaloRounds; ++r) {
+            uint32_t q;
+            int lx, ly;
+            halo_cell(r, bx, by, W, H, tw, q, lx, ly);
+            if (lx >= 0) {
+                s_d[0][ly][lx] = av[r];
+                s_d[1][ly][lx] = bv[r];
+                s_d[2][ly][lx] = dv[r];
+            }
+        }
+        float ep[4], et[4], eg[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int px = bx + vc, py = by + 4 * vr + q;
+            const bool ok = px < (int)W && py < (int)H;
+            const uint32_t idx = ok ? tiled_index((uint32_t)py, (uint32_t)px, tw) + (uint32_t)c * cs : 0u;
+            ep[q] = pred[idx];
+            et[q] = target[idx];
+            eg[q] = grad[idx];
         }
         __syncthreads();
+        if (c < 2) {
+            const size_t o = (size_t)(c + 1) * cs;
+            halo_load2(dm_mu + o, dm_s1 + o, bx, by, W, H, tw, av, bv);
+            halo_load1(dm_s12 + o, bx, by, W, H, tw, dv);
+        }
         for (int wi = t; wi < kIT * 8; wi += 256) {
             const int r = wi >> 3, g = wi & 7;
 #pragma unroll
@@ -294,9 +325,8 @@ __global__ void __launch_bounds__(256) ssim_backward_kernel(uint32_t W, uint32_t
             const int px = bx + vc, py = by + 4 * vr + q;
             if (px >= (int)W || py >= (int)H) continue;
             const uint32_t idx = tiled_index((uint32_t)py, (uint32_t)px, tw) + (uint32_t)c * cs;
-            const float p1 = pred[idx], p2 = target[idx];
-            const float dl = __builtin_fmaf(p2, o[2][q], __builtin_fmaf(2.0f * p1, o[1][q], o[0][q]));
-            grad[idx] = __builtin_fmaf(-s, dl, grad[idx]);
+            const float dl = __builtin_fmaf(et[q], o[2][q], __builtin_fmaf(2.0f * ep[q], o[1][q], o[0][q]));
+            grad[idx] = __builtin_fmaf(-s, dl, eg[q]);
         }
         __syncthreads();
     }
