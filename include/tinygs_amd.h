@@ -95,8 +95,20 @@ int tgs_rasterizer_backward(tgs_rasterizer* r, const void* grad_image, const voi
  * caller's zeroing (tinygs/src/orchestrator.cu:351-353) fused into the write.
  * No counterpart in the reference; for callers that zero before every backward. */
 #define TGS_BACKWARD_ASSIGN 1
+/* TGS_BACKWARD_SPARSE: rows (per primitive, every gradient array) that
+ * received a nonzero 2D gradient are assigned; all other rows are left as they
+ * were (their true gradient is exactly zero) and the per-primitive byte mask
+ * returned by tgs_rasterizer_grad_row_mask marks the assigned rows (1) and
+ * the skipped ones (0). Pair it with tgs_adam_step_masked, which then reads
+ * only the marked rows. No counterpart in the reference: it spares writing
+ * and re-reading the zero rows (most rows at 1M Gaussians). */
+#define TGS_BACKWARD_SPARSE 2
 int tgs_rasterizer_backward_ex(tgs_rasterizer* r, const void* grad_image, const void* image,
                                const tgs_gaussians* grads, void* densification_info, int32_t flags, void* stream);
+/* Device byte mask [n] of the last TGS_BACKWARD_SPARSE backward (1: row
+ * assigned, 0: row skipped, its gradient is zero). Valid until the next
+ * backward or the next forward that grows the Gaussian count. */
+int tgs_rasterizer_grad_row_mask(tgs_rasterizer* r, const uint8_t** mask);
 /* Counts of the last forward: visible primitives, instances, tiles. */
 int tgs_rasterizer_counts(tgs_rasterizer* r, int64_t* n_visible, int64_t* n_instances, int64_t* n_tiles);
 
@@ -173,6 +185,11 @@ float tgs_adam_get_lr(tgs_adam* a);
 int tgs_adam_set_gaussians(tgs_adam* a, const tgs_gaussians* params, const tgs_gaussians* grads);
 /* OptimizerBase::step(scale, stream): gradients multiplied by scale. */
 int tgs_adam_step(tgs_adam* a, float scale, void* stream);
+/* tgs_adam_step where row i of every gradient array is read only if
+ * row_mask[i] != 0 and is taken as zero otherwise (the mask of a
+ * TGS_BACKWARD_SPARSE backward). Same results as tgs_adam_step on gradients
+ * whose unmarked rows are zero. No counterpart in the reference. */
+int tgs_adam_step_masked(tgs_adam* a, float scale, const uint8_t* row_mask, void* stream);
 /* OptimizerBase::reset(): zero moments and the step counter. */
 int tgs_adam_reset(tgs_adam* a, void* stream);
 int64_t tgs_adam_global_steps(tgs_adam* a);

@@ -361,7 +361,7 @@ def test_train_step_config2_reduced(hip, orc):
     from tinygs_amd.train import TrainStep
     s = scenes.config2(seed=16, n=20000, width=320, height=240)
     lr = {"means": 1.6e-4, "scene_scale": 1.0, "opacities": 5e-2, "rotations": 1e-3, "scales": 5e-3, "shs": 5e-3}
-    ts = TrainStep(s, l1_weight=0.8, ssim_weight=0.2, eps=1e-15, shs_lr=5e-3)
+    ts = TrainStep(s, l1_weight=0.8, ssim_weight=0.2, eps=1e-15, shs_lr=5e-3, sparse_grads=False)
     ts.step()
     torch.cuda.synchronize()
     ref = orc.run_iteration(s, 0.8, 0.2, lr=lr, eps=1e-15)
@@ -419,3 +419,63 @@ def test_config3_fp16_sh_mode(hip, orc):
     th = ts.params()
     for k in theta:
         assert np.array_equal(th[k].view(np.uint32), theta[k].view(np.uint32)), k
+
+
+def test_sparse_gradient_handoff_matches_dense(hip):
+    """Sparse backward + masked Adam against assign-mode backward + Adam over
+    several steps. The record sums' order follows atomic order, so the two
+    runs agree to rounding, not bit for bit; the mask must mark exactly the
+    nonzero gradient rows."""
+    import torch
+    from tinygs_amd import _lib
+    from tinygs_amd.train import TrainStep
+    s = scenes.config2(seed=21, n=20000, width=320, height=240)
+    dense = TrainStep(s, l1_weight=0.8, ssim_weight=0.2, eps=1e-15, shs_lr=5e-3, sparse_grads=False)
+    sparse = TrainStep(s, l1_weight=0.8, ssim_weight=0.2, eps=1e-15, shs_lr=5e-3, sparse_grads=True)
+    p0 = dense.params()
+    for step in range(4):
+        dense.step()
+        sparse.step()
+        torch.cuda.synchronize()
+        mask = torch.empty(s.n, dtype=torch.uint8, device="cuda")
+        _lib.copy_device(sparse.rasterizer.grad_row_mask(), s.n, mask)
+        live = mask.cpu().numpy() != 0
+        assert 0 < live.sum() < s.n
+        g = dense.grads
+        for t, w in ((g.means(), 3), (g.scales(), 3), (g.rotations(), 4), (g.opacities(), 1),
+                     (g.sh_coefficient_0(), 3), (g.sh_coefficients_rest(), 45)):
+            rows = t.reshape(s.n, w).cpu().numpy()
+            assert np.all(rows[~live] == 0)
+    a, b = dense.params(), sparse.params()
+    for k in a:
+        d = np.abs(a[k] - b[k]).max()
+        moved = np.abs(a[k] - p0[k]).max()
+        assert d <= 1e-3 * moved + 1e-7, (k, d, moved)
+
+
+def test_adam_masked_matches_zeroed_rows(hip):
+    """tgs_adam_step_masked == tgs_adam_step on gradients whose unmarked rows
+    are zeroed, bit for bit (stale contents in unmarked rows are ignored)."""
+    import torch
+    from tinygs_amd.core import GPUGaussian3d
+    from tinygs_amd.optim import create_optimizer
+    s = scenes.config3(seed=22, n=5003, width=64, height=64)   # fp16 SH storage, odd count
+    rng = np.random.default_rng(3)
+    mask = (rng.random(s.n) < 0.1).astype(np.uint8)
+    ga, gb = GPUGaussian3d.from_scene(s), GPUGaussian3d.from_scene(s)
+    da, db = ga.gradient_like(), gb.gradient_like()
+    for ta, tb, w in zip(da.tensors(), db.tensors(), (3, 3, 4, 1, 3, 45)):
+        v = rng.standard_normal(ta.numel()).astype(np.float32).reshape(s.n, w)
+        ta.copy_(torch.from_numpy(np.where(mask[:, None] != 0, v, 0.0).astype(np.float32).reshape(ta.shape)))
+        tb.copy_(torch.from_numpy(v.reshape(tb.shape)))   # unmarked rows hold garbage
+    oa, ob = create_optimizer("simple_adam", ga, da), create_optimizer("simple_adam", gb, db)
+    for o in (oa, ob):
+        o.set_params({"epsilon": 1e-15, "shs_lr": 5e-3, "opacities_l1": 0.01, "scales_l1": 0.02})
+    dmask = torch.from_numpy(mask).cuda()
+    for _ in range(3):
+        oa.step(0.5)
+        ob.step(0.5, row_mask=dmask.data_ptr())
+    torch.cuda.synchronize()
+    for ta, tb in zip(ga.tensors(), gb.tensors()):
+        x, y = ta.float().cpu().numpy(), tb.float().cpu().numpy()
+        assert np.array_equal(x.view(np.uint32), y.view(np.uint32))

@@ -17,6 +17,8 @@ LIB_PATH = os.path.join(HERE, "libtinygs_amd.so")
 TGS_DTYPE_FLOAT32 = 0
 TGS_DTYPE_FLOAT16 = 1
 TGS_LOSS_ASSIGN = 1
+TGS_BACKWARD_ASSIGN = 1
+TGS_BACKWARD_SPARSE = 2
 
 _lib = None
 _hip = None
@@ -80,6 +82,8 @@ SIGNATURES = {
     "tgs_adam_get_lr": ([P], C.c_float),
     "tgs_adam_set_gaussians": ([P, C.POINTER(tgs_gaussians), C.POINTER(tgs_gaussians)], C.c_int),
     "tgs_adam_step": ([P, C.c_float, P], C.c_int),
+    "tgs_adam_step_masked": ([P, C.c_float, P, P], C.c_int),
+    "tgs_rasterizer_grad_row_mask": ([P, PP], C.c_int),
     "tgs_adam_reset": ([P, P], C.c_int),
     "tgs_adam_global_steps": ([P], C.c_int64),
     "tgs_adam_moments": ([P, C.c_int32, C.POINTER(C.c_void_p), C.POINTER(C.c_void_p)], C.c_int),

@@ -50,6 +50,16 @@ __device__ __forceinline__ float adam_one(float th, float gr_raw, float& m, floa
     return th - (mh * g.lr) / den;
 }
 
+// Primitive (row) of element e of a group whose rows hold w elements.
+__device__ __forceinline__ uint32_t row_of(uint32_t e, int w) {
+    switch (w) {
+        case 1: return e;
+        case 3: return e / 3u;
+        case 4: return e >> 2;
+        default: return e / 45u;
+    }
+}
+
 // Each thread updates kAdamVecPerThread 4-element vectors with 16-byte loads
 // and stores (8-byte for fp16 theta); lanes of a wave cover consecutive
 // vectors. All loads of a thread are issued before any arithmetic.
@@ -78,7 +88,17 @@ __global__ void __launch_bounds__(kAdamThreads) adam_kernel(AdamLaunch L) {
                 const float4 tv = *(const float4*)((const float*)g.theta + e0);
                 th[k][0] = tv.x; th[k][1] = tv.y; th[k][2] = tv.z; th[k][3] = tv.w;
             }
-            gv[k] = *(const float4*)(g.grad + e0);
+            if (L.a.row_mask) {
+                // rows without gradient are zero and not read
+                bool lv[4];
+#pragma unroll
+                for (int q = 0; q < 4; ++q) lv[q] = L.a.row_mask[row_of((uint32_t)(e0 + q), g.row_width)] != 0;
+                float4 gg = make_float4(0.f, 0.f, 0.f, 0.f);
+                if (lv[0] || lv[1] || lv[2] || lv[3]) gg = *(const float4*)(g.grad + e0);
+                gv[k] = make_float4(lv[0] ? gg.x : 0.f, lv[1] ? gg.y : 0.f, lv[2] ? gg.z : 0.f, lv[3] ? gg.w : 0.f);
+            } else {
+                gv[k] = *(const float4*)(g.grad + e0);
+            }
             mv[k] = *(const float4*)(g.m1 + e0);
             vv[k] = *(const float4*)(g.m2 + e0);
         }
@@ -105,7 +125,8 @@ __global__ void __launch_bounds__(kAdamThreads) adam_kernel(AdamLaunch L) {
             for (int64_t i = e0; i < g.count; ++i) {
                 float t = g.theta_half ? __half2float(((const __half*)g.theta)[i]) : ((const float*)g.theta)[i];
                 float m = g.m1[i], v = g.m2[i];
-                t = adam_one(t, g.grad[i], m, v, g, L.a, t1, t2);
+                const bool live = !L.a.row_mask || L.a.row_mask[row_of((uint32_t)i, g.row_width)] != 0;
+                t = adam_one(t, live ? g.grad[i] : 0.f, m, v, g, L.a, t1, t2);
                 if (g.theta_half)
                     ((__half*)g.theta)[i] = __float2half_rn(t);
                 else

@@ -226,6 +226,8 @@ struct tgs_rasterizer {
     // count (kept zero between backwards), records (3 float4 per instance
     // slot), heavy-gather list
     DevBuf first_slot, rec_count, records, heavy;
+    DevBuf row_mask;     // per-primitive byte mask of the last sparse backward
+    bool row_mask_valid = false;
     // temp
     DevBuf grad2d;
     DevBuf radix_counts;   // per-workgroup digit counts of the radix passes
@@ -310,7 +312,7 @@ int tgs_rasterizer_destroy(tgs_rasterizer* r) {
                      &r->radix_counts, &r->ikeys[0],
                      &r->ikeys[1], &r->ivals[0], &r->ivals[1], &r->ranges, &r->tile_max, &r->n_contrib,
                      &r->ckpt, &r->items, &r->tile_loaded, &r->first_slot,
-                     &r->rec_count, &r->records, &r->heavy, &r->grad2d, &r->bin_ctl, &r->lb_status};
+                     &r->rec_count, &r->records, &r->heavy, &r->row_mask, &r->grad2d, &r->bin_ctl, &r->lb_status};
     for (DevBuf* b : all) release(*b);
     if (r->h_counters) (void)hipHostFree(r->h_counters);
     if (r->ev_counts) (void)hipEventDestroy(r->ev_counts);
@@ -352,6 +354,7 @@ int tgs_rasterizer_forward(tgs_rasterizer* r, const tgs_camera* camera, void* im
     CamParams cam;
     TGS_TRY(build_camera(camera, cam));
     r->fwd_done = false;
+    r->row_mask_valid = false;
     const int64_t n = r->g.n;
     const uint32_t T = cam.grid_w * cam.grid_h;
     const size_t cs = (size_t)cam.tiled_w * cam.tiled_h * 64u;
@@ -486,6 +489,13 @@ int tgs_rasterizer_backward_ex(tgs_rasterizer* r, const void* grad_image, const 
     const int64_t n = r->n;
     TGS_TRY(ensure(r->grad2d, sizeof(float) * kGradStride * (size_t)(n > 0 ? n : 1), s));
     TGS_TRY(ensure(r->heavy, sizeof(uint32_t) * (size_t)(n > 0 ? n : 1), s));
+    if (flags & ~(TGS_BACKWARD_ASSIGN | TGS_BACKWARD_SPARSE))
+        return fail(TGS_ERR_INVALID, "unknown backward flags 0x%x", flags);
+    if ((flags & TGS_BACKWARD_ASSIGN) && (flags & TGS_BACKWARD_SPARSE))
+        return fail(TGS_ERR_INVALID, "TGS_BACKWARD_ASSIGN and TGS_BACKWARD_SPARSE are exclusive");
+    const int mode = (flags & TGS_BACKWARD_SPARSE) ? kGradSparse : ((flags & TGS_BACKWARD_ASSIGN) ? kGradAssign : kGradAccumulate);
+    if (mode == kGradSparse) TGS_TRY(ensure(r->row_mask, (size_t)(n > 0 ? n : 1), s));
+    r->row_mask_valid = false;
     const CamParams& cam = r->cam;
     BinCtl* ctl = r->bin_ctl.as<BinCtl>();
     if (!r->bwd_queues_clear)   // a second backward after one forward: clear the queue / heavy counters again
@@ -508,10 +518,18 @@ int tgs_rasterizer_backward_ex(tgs_rasterizer* r, const void* grad_image, const 
         StageScope sc(ST_PREB, s);
         launch_preprocess_backward(view_of(r->g), cam, r->n_touched.as<uint32_t>(), r->conic_opacity.as<float4>(),
                                    r->rec_count.as<uint32_t>(), r->first_slot.as<uint32_t>(), r->records.as<float4>(),
-                                   r->grad2d.as<float>(), gv, (float*)densification_info,
-                                   (flags & TGS_BACKWARD_ASSIGN) != 0, s);
+                                   r->grad2d.as<float>(), gv, (float*)densification_info, mode,
+                                   r->row_mask.as<uint8_t>(), s);
     }
     TGS_CHECK_LAUNCH();
+    r->row_mask_valid = mode == kGradSparse;
+    return TGS_OK;
+}
+
+int tgs_rasterizer_grad_row_mask(tgs_rasterizer* r, const uint8_t** mask) {
+    if (!r || !mask) return fail(TGS_ERR_INVALID, "NULL argument");
+    if (!r->row_mask_valid) return fail(TGS_ERR_STATE, "no TGS_BACKWARD_SPARSE backward since the last forward");
+    *mask = r->row_mask.as<uint8_t>();
     return TGS_OK;
 }
 
@@ -736,7 +754,9 @@ int tgs_adam_set_gaussians(tgs_adam* a, const tgs_gaussians* params, const tgs_g
     return TGS_OK;
 }
 
-int tgs_adam_step(tgs_adam* a, float scale, void* stream) {
+int tgs_adam_step(tgs_adam* a, float scale, void* stream) { return tgs_adam_step_masked(a, scale, nullptr, stream); }
+
+int tgs_adam_step_masked(tgs_adam* a, float scale, const uint8_t* row_mask, void* stream) {
     if (!a) return fail(TGS_ERR_INVALID, "NULL argument");
     const int64_t n = a->params.n;
     a->steps += 1;
@@ -756,6 +776,7 @@ int tgs_adam_step(tgs_adam* a, float scale, void* stream) {
     args.bc1 = bc1;
     args.bc2_sqrt = bc2;
     args.max_grad = a->p.max_grad_1;
+    args.row_mask = row_mask;
     void* th[6] = {a->params.means, a->params.opacities, a->params.rotations, a->params.scales, a->params.sh0,
                    a->params.sh_rest};
     const float* gr[6] = {(const float*)a->grads.means, (const float*)a->grads.opacities,
@@ -777,6 +798,7 @@ int tgs_adam_step(tgs_adam* a, float scale, void* stream) {
         g.lerp_form = (k == 1) ? 1 : 0;
         g.decay_kind = (k == 1) ? 1 : (k == 3 ? 2 : 0);
         g.decay_coef = (k == 1) ? a->p.opacities_l1 * g_scale : (k == 3 ? a->p.scales_l1 * g_scale : 0.0f);
+        g.row_width = kGroupMult[k];
     }
     {
         StageScope sc(ST_ADAM, (hipStream_t)stream);

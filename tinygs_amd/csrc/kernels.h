@@ -121,10 +121,13 @@ void launch_gather_heavy(const uint32_t* heavy, const BinCtl* ctl, const uint32_
                          const uint32_t* first_slot, const float4* records, float* grad2d, hipStream_t s);
 
 // ---- preprocess backward (kernels_backward.cuh:88-352)
+// mode: 0 accumulate, 1 assign, 2 sparse (assign rows with gradient, write
+// row_mask[i] = 1 for them and 0 for the others, leave the others untouched).
+enum { kGradAccumulate = 0, kGradAssign = 1, kGradSparse = 2 };
 void launch_preprocess_backward(const GaussianView& g, const CamParams& cam, const uint32_t* n_touched,
                                 const float4* conic_opacity, uint32_t* rec_count, const uint32_t* first_slot,
                                 const float4* records, const float* grad2d, const GradView& out, float* densif,
-                                bool assign, hipStream_t s);
+                                int mode, uint8_t* row_mask, hipStream_t s);
 
 // ---- utilities
 void launch_fill_u32(uint32_t* p, uint32_t value, int64_t n, hipStream_t s);
@@ -153,9 +156,11 @@ struct AdamGroup {
     int lerp_form;        // 0: fma(t, g - m, m); 1: fma(t, g, fma(-t, m, m))
     int decay_kind;       // 0 none, 1 opacity logistic', 2 scale exp
     float decay_coef;
+    int row_width;        // elements per primitive: 3, 1, 4, 3, 3 or 45
 };
 struct AdamArgs {
     AdamGroup groups[6];
+    const uint8_t* row_mask;   // optional: row i's gradient read only if row_mask[i] != 0, else zero
     int n_groups;
     float beta1, beta2, eps, grad_scale, bc1, bc2_sqrt, max_grad;
 };

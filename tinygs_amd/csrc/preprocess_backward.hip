@@ -258,14 +258,16 @@ __global__ void __launch_bounds__(256) preprocess_backward_kernel(
     const float4* __restrict__ conic_opacity, uint32_t* __restrict__ rec_count,
     const uint32_t* __restrict__ first_slot, const float4* __restrict__ records, const float* __restrict__ grad2d,
     float* __restrict__ g_means, float* __restrict__ g_scales, float* __restrict__ g_rots, float* __restrict__ g_opac,
-    float* __restrict__ g_sh0, float* __restrict__ g_shr_all, float4* __restrict__ densif, int assign_flag) {
+    float* __restrict__ g_sh0, float* __restrict__ g_shr_all, float4* __restrict__ densif, int mode,
+    uint8_t* __restrict__ row_mask) {
     // Block of 256 consecutive primitives; each gradient array's rows of the
     // block are one contiguous run (3, 3, 3, 4, 1 and 45 floats per
     // primitive). Phase 1 compacts the primitives with 2D-gradient records
     // into an LDS list; phase 2 runs the gradient chain for them on
     // consecutive threads (one wave carries a typical block's few live
     // primitives instead of four waves idling around them); phase 3 writes
-    // the block's rows from LDS with 16-byte stores (assign mode) or
+    // the block's rows from LDS with 16-byte stores (assign mode), assigns
+    // only the live rows and writes the block's row mask (sparse mode), or
     // read-modify-writes only what changes (accumulate mode).
     __shared__ float s_k[256 * 15];
     __shared__ float s_gc[256 * 3];
@@ -278,7 +280,8 @@ __global__ void __launch_bounds__(256) preprocess_backward_kernel(
     const int t = (int)threadIdx.x;
     const uint32_t lane = (uint32_t)t & 63u, w = (uint32_t)t >> 6;
     const int64_t i = blk0 + t;
-    const bool assign = assign_flag != 0;
+    const bool assign = mode == kGradAssign;
+    const bool sparse = mode == kGradSparse;
     const bool vis = t < nblk && n_touched[i] != 0;
     const uint32_t nrec = vis ? rec_count[i] : 0u;
     s_nb[t] = 0u;
@@ -291,6 +294,7 @@ __global__ void __launch_bounds__(256) preprocess_backward_kernel(
     // zero (products with zero 2D gradients); densification still counts a
     // visible primitive (kernels_backward.cuh:345), adding 0 to its sums
     if (vis && !nrec && densif) densif[i].x += 1.0f;
+    if (sparse && t < nblk) row_mask[i] = nrec ? 1u : 0u;
     const uint64_t lm = ballot(nrec != 0u);
     if (lane == 0) s_wcnt[w] = (uint32_t)__builtin_popcountll(lm);
     __syncthreads();
@@ -339,6 +343,14 @@ __global__ void __launch_bounds__(256) preprocess_backward_kernel(
             }
             for (int c = 0; c < 4; ++c) s_r[4 * tl + c] = g.r[c];
             s_o[tl] = g.o;
+        } else if (sparse) {
+            for (int c = 0; c < 3; ++c) {
+                g_means[3 * ip + c] = g.m[c];
+                g_scales[3 * ip + c] = g.s[c];
+                g_sh0[3 * ip + c] = g.sh0[c];
+            }
+            for (int c = 0; c < 4; ++c) g_rots[4 * ip + c] = g.r[c];
+            g_opac[ip] = g.o;
         } else {
             for (int c = 0; c < 3; ++c) {
                 g_means[3 * ip + c] += g.m[c];
@@ -357,7 +369,15 @@ __global__ void __launch_bounds__(256) preprocess_backward_kernel(
         block_store(g_rots + 4 * blk0, s_r, 4 * nblk);
         block_store(g_opac + blk0, s_o, nblk);
     }
-    if (bases > 1 || assign) {
+    if (sparse) {
+        // SH-rest rows of the live primitives only, consecutive threads along each row
+        for (int e = t; e < (int)n_live * 45; e += 256) {
+            const int idx = e / 45, r = e - 45 * idx, b = r / 3, c = r - 3 * b;
+            const uint32_t tl = s_live[idx];
+            g_shr_all[(blk0 + (int64_t)tl) * 45 + r] =
+                ((uint32_t)b < s_nb[tl]) ? s_k[15 * tl + b] * s_gc[3 * tl + c] : 0.f;
+        }
+    } else if (bases > 1 || assign) {
         // grad_sh_rest[i][b][c] += k_b * gc_c (kernels_backward.cuh:41-65), b < active bases - 1
         float* gbase = g_shr_all + blk0 * 45;
         const int total = nblk * 45;
@@ -408,7 +428,7 @@ __global__ void __launch_bounds__(256) preprocess_backward_kernel(
 void launch_preprocess_backward(const GaussianView& g, const CamParams& cam, const uint32_t* n_touched,
                                 const float4* conic_opacity, uint32_t* rec_count, const uint32_t* first_slot,
                                 const float4* records, const float* grad2d, const GradView& out, float* densif,
-                                bool assign, hipStream_t s) {
+                                int mode, uint8_t* row_mask, hipStream_t s) {
     if (g.n <= 0) return;
     const int bases = (g.sh_degree + 1) * (g.sh_degree + 1);
     const unsigned grid = (unsigned)((g.n + 255) / 256);
@@ -416,14 +436,12 @@ void launch_preprocess_backward(const GaussianView& g, const CamParams& cam, con
         preprocess_backward_kernel<__half><<<grid, 256, 0, s>>>(
             g.means, g.scales, g.rotations, (const __half*)g.sh_rest, g.n, bases, cam, n_touched, conic_opacity,
             rec_count, first_slot, records, grad2d, out.means, out.scales, out.rotations, out.opacities, out.sh0,
-            out.sh_rest, (float4*)densif,
-            assign ? 1 : 0);
+            out.sh_rest, (float4*)densif, mode, row_mask);
     } else {
         preprocess_backward_kernel<float><<<grid, 256, 0, s>>>(
             g.means, g.scales, g.rotations, (const float*)g.sh_rest, g.n, bases, cam, n_touched, conic_opacity,
             rec_count, first_slot, records, grad2d, out.means, out.scales, out.rotations, out.opacities, out.sh0,
-            out.sh_rest, (float4*)densif,
-            assign ? 1 : 0);
+            out.sh_rest, (float4*)densif, mode, row_mask);
     }
 }
 

@@ -51,9 +51,17 @@ class SimpleAdam(OptimizerBase):
         self._cg = self.m_gaussians_grad.to_c()
         _lib.check(_lib.load().tgs_adam_set_gaussians(self._h, C.byref(self._cp), C.byref(self._cg)), "set_gaussians")
 
-    def step(self, scale: float, stream=None):
+    def step(self, scale: float, stream=None, row_mask: int | None = None):
+        """OptimizerBase::step. row_mask: device address of a per-Gaussian
+        byte mask (a sparse backward's); unmarked gradient rows are taken as
+        zero without being read."""
         self._rebind()
-        _lib.check(_lib.load().tgs_adam_step(self._h, float(scale), stream_ptr(stream)), "SimpleAdam::step")
+        L = _lib.load()
+        if row_mask is None:
+            _lib.check(L.tgs_adam_step(self._h, float(scale), stream_ptr(stream)), "SimpleAdam::step")
+        else:
+            _lib.check(L.tgs_adam_step_masked(self._h, float(scale), C.c_void_p(row_mask), stream_ptr(stream)),
+                       "SimpleAdam::step")
 
     def reset(self, stream=None):
         _lib.check(_lib.load().tgs_adam_reset(self._h, stream_ptr(stream)), "SimpleAdam::reset")

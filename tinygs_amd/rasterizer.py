@@ -69,18 +69,30 @@ class FastGSRasterizer(RasterizerBase):
         _lib.check(L.tgs_rasterizer_forward(self._h, C.byref(cam), ptr(img.data), _lib.TGS_DTYPE_FLOAT32,
                                             ptr(ctx.densification_info), stream_ptr(ctx.stream)), "forward")
 
-    def backward(self, ctx: RasterizeContext, assign: bool = False):
+    def backward(self, ctx: RasterizeContext, assign: bool = False, sparse: bool = False):
         """Accumulates into ctx.gaussians_grad (reference contract). assign=True
         writes the gradients instead (zero for culled Gaussians): the caller's
-        zeroing fused into the backward."""
+        zeroing fused into the backward. sparse=True writes only the rows that
+        received a gradient (see grad_row_mask); the others keep their old
+        contents and stand for zero."""
         if self.m_gaussians is None or ctx.gaussians_grad is None:
             raise RuntimeError("Gaussians or gradient gaussians not set")
+        if assign and sparse:
+            raise RuntimeError("assign and sparse are exclusive")
         g = ctx.gaussians_grad.to_c()
         L = _lib.load()
+        flags = (_lib.TGS_BACKWARD_ASSIGN if assign else 0) | (_lib.TGS_BACKWARD_SPARSE if sparse else 0)
         _lib.check(L.tgs_rasterizer_backward_ex(self._h, ptr(ctx.grad_output.image.data),
                                                 ptr(ctx.fwd_output.image.data), C.byref(g),
-                                                ptr(ctx.densification_info), 1 if assign else 0,
+                                                ptr(ctx.densification_info), flags,
                                                 stream_ptr(ctx.stream)), "backward")
+
+    def grad_row_mask(self) -> int:
+        """Device address of the byte mask [n] of the last sparse backward
+        (1: the row was written, 0: its gradient is zero and was not written)."""
+        m = C.c_void_p()
+        _lib.check(_lib.load().tgs_rasterizer_grad_row_mask(self._h, C.byref(m)), "grad_row_mask")
+        return m.value
 
     def counts(self):
         v, i, t = C.c_int64(), C.c_int64(), C.c_int64()

@@ -9,6 +9,11 @@ Orchestrator::train_step (tinygs/src/orchestrator.cu:335-439):
   -> FastGSRasterizer::backward with grad_output = loss gradient (:377-380)
   -> SimpleAdam::step(1 / (grad_scaler * accumulate_grad_steps)) (:393-404)
 
+The parameter-gradient zeroing of :351-353 is folded into the backward:
+assign mode writes every row; sparse mode (the default here) writes only
+rows that received a gradient and hands Adam the row mask, so zero rows are
+neither written nor read.
+
 Everything runs on one HIP stream; the only host synchronisation is the one
 inside the forward that sizes the instance buffers.
 """
@@ -23,9 +28,13 @@ from .rasterizer import create_rasterizer
 class TrainStep:
     def __init__(self, scene, l1_weight: float = 0.8, ssim_weight: float = 0.2, grad_scaler: float = 1.0,
                  eps: float = 1e-15, shs_lr: float | None = None, means_lr: float | None = None,
-                 max_grad_1: float | None = None, device: str = "cuda", stream=None):
+                 max_grad_1: float | None = None, device: str = "cuda", stream=None, sparse_grads: bool = True):
         import torch
         self.scene = scene
+        # sparse_grads: the backward writes only gradient rows that received a
+        # gradient and Adam reads only those (the others are zero); same
+        # parameters as assigning every row, without moving the zero rows
+        self.sparse_grads = bool(sparse_grads)
         self.stream = stream
         self.gaussians = GPUGaussian3d.from_scene(scene, device)
         self.grads = self.gaussians.gradient_like()
@@ -90,10 +99,14 @@ class TrainStep:
             loss.evaluate(self.loss_ctx, w * self.grad_scaler)
 
     def backward(self):
-        self.rasterizer.backward(self.ctx, assign=True)
+        if self.sparse_grads:
+            self.rasterizer.backward(self.ctx, sparse=True)
+        else:
+            self.rasterizer.backward(self.ctx, assign=True)
 
     def optimize(self):
-        self.optimizer.step(1.0 / self.grad_scaler, self.stream)
+        mask = self.rasterizer.grad_row_mask() if self.sparse_grads else None
+        self.optimizer.step(1.0 / self.grad_scaler, self.stream, row_mask=mask)
 
     def step(self):
         self.zero()
