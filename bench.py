@@ -27,7 +27,7 @@ STAGES = ["preprocess", "depth_sort", "emit_instances", "tile_sort", "blend_forw
 # stages that are one kernel launch, and that kernel's symbol in rocprofv3 output
 SINGLE_KERNEL = {"preprocess": "tgs::preprocess_kernel", "blend_forward": "tgs::blend_forward_kernel",
                  "l1": "tgs::l1_kernel", "blend_backward": "tgs::blend_backward_kernel",
-                 "preprocess_backward": "tgs::preprocess_backward_kernel", "adam": "tgs::adam_kernel"}
+                 "adam": "tgs::adam_kernel"}
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "hbm_traffic_config{}.md")
 
 
@@ -47,8 +47,12 @@ def measured_traffic(config, kernel):
 
 def algorithmic_bytes(stage, c):
     """Compulsory HBM bytes of one launch (each input read once, each output
-    written once; implementation scratch excluded)."""
+    written once; implementation scratch excluded). With the sparse gradient
+    handoff (TrainStep's default) only the L rows that receive a gradient are
+    read / written by the preprocess backward and read by Adam; the dense
+    formulas are the sparse ones with L = N."""
     N, V, I, T, P = c["N"], c["V"], c["I"], c["T"], c["P"]
+    L = c["L"]
     s, K, e = c["sh_bytes"], c["sh_bases"], 4
     if stage == "preprocess":
         return 44 * N + 3 * K * s * V + 4 * N + 52 * V
@@ -57,13 +61,19 @@ def algorithmic_bytes(stage, c):
     if stage == "blend_backward":
         return 8 * T + P * (6 * e + 4) + 40 * c["I_b"] + 44 * c["I_b"]
     if stage == "preprocess_backward":
-        return 48 * N + V * (3 * K * s + 44) + 2 * V * (40 + 12 * K)
+        # per Gaussian: n_touched, row mask; per gradient row: means, scales, rotations, conic+opacity,
+        # SH rest (45 scalars), the 2D gradient sums (11 floats) read, 59 fp32 gradients written
+        return 5 * N + L * (12 + 12 + 16 + 16 + 45 * s + 44 + 236)
     if stage == "adam":
-        return (11 * 28 + 48 * 24) * N if s == 2 else 28 * 59 * N
+        # theta (11 fp32 + 48 SH scalars) and m, v (59 fp32 each) read and written; gradient rows read;
+        # the row mask read
+        theta = 11 * 4 + 48 * s
+        return N * (2 * theta + 4 * 59 * 4 + 1) + 236 * L
     if stage == "l1":
         return 4 * 3 * P * e          # read pred, target; read-modify-write grad, loss
     if stage == "fused_ssim":
-        return 3 * 3 * P * e
+        # fused L1 + SSIM in assign mode: read pred, target; write loss, grad
+        return 4 * 3 * P * e
     if stage == "depth_sort":
         return 8 * V + 8 * V + 8 * V   # read keys/values once, write one permutation
     if stage == "emit_instances":
@@ -169,12 +179,18 @@ def main():
     _lib.check(L.tgs_rasterizer_work_stats(ts.rasterizer._h, C.byref(fl), C.byref(bp), 1))
     V, I, T = ts.rasterizer.counts()
     cam = scene.camera
-    counts = {"N": scene.n, "V": V, "I": I, "T": T, "P": cam.width * cam.height,
+    if ts.sparse_grads:
+        mask = torch.empty(scene.n, dtype=torch.uint8, device="cuda")
+        _lib.copy_device(ts.rasterizer.grad_row_mask(), scene.n, mask)
+        live = int(mask.sum().item())
+    else:
+        live = scene.n
+    counts = {"N": scene.n, "V": V, "I": I, "T": T, "P": cam.width * cam.height, "L": live,
               "I_f": fl.value, "I_b": bp.value,
               "sh_bytes": 2 if scene.sh_dtype == "float16" else 4, "sh_bases": (scene.sh_degree + 1) ** 2}
 
     print(f"[bench] {ms:.3f} ms/iter over {args.steps} steps; V={V} I={I} T={T} "
-          f"I_f={counts['I_f']:.0f} I_b={counts['I_b']:.0f}", file=sys.stderr)
+          f"I_f={counts['I_f']:.0f} I_b={counts['I_b']:.0f} gradient rows L={live}", file=sys.stderr)
     print(f"[bench] {'stage':22s} {'ms':>8s} {'GB/s':>8s} {'%HBM':>6s}", file=sys.stderr)
     rows = []
     for name in STAGES:
@@ -208,6 +224,7 @@ def main():
         "config": {"workload": f"config{args.config}: fwd + 0.8 L1 + 0.2 (1-SSIM) + bwd + SimpleAdam",
                    "n_gaussians": scene.n, "width": cam.width, "height": cam.height, "sh_degree": scene.sh_degree,
                    "sh_storage": scene.sh_dtype, "n_visible": V, "n_instances": I, "n_tiles": T,
+                   "gradient_rows": live, "sparse_gradients": ts.sparse_grads,
                    "parallelism": "single GPU"},
         "stages_ms": {r[0]: round(r[1], 5) for r in rows},
         "roofline": roofline,

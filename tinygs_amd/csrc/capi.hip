@@ -507,8 +507,6 @@ int tgs_rasterizer_backward_ex(tgs_rasterizer* r, const void* grad_image, const 
                               (const float*)grad_image, r->n_contrib.as<uint32_t>(), r->ckpt.as<float4>(),
                               r->items.as<uint4>(), ctl, r->rec_count.as<uint32_t>(), r->first_slot.as<uint32_t>(),
                               r->records.as<float4>(), r->heavy.as<uint32_t>(), s);
-        launch_gather_heavy(r->heavy.as<uint32_t>(), ctl, r->rec_count.as<uint32_t>(), r->first_slot.as<uint32_t>(),
-                            r->records.as<float4>(), r->grad2d.as<float>(), s);
     }
     r->bwd_queues_clear = false;
     TGS_CHECK_LAUNCH();
@@ -516,6 +514,8 @@ int tgs_rasterizer_backward_ex(tgs_rasterizer* r, const void* grad_image, const 
                 (float*)grads->sh0, (float*)grads->sh_rest};
     {
         StageScope sc(ST_PREB, s);
+        launch_gather_heavy(r->heavy.as<uint32_t>(), ctl, r->rec_count.as<uint32_t>(), r->first_slot.as<uint32_t>(),
+                            r->records.as<float4>(), r->grad2d.as<float>(), s);
         launch_preprocess_backward(view_of(r->g), cam, r->n_touched.as<uint32_t>(), r->conic_opacity.as<float4>(),
                                    r->rec_count.as<uint32_t>(), r->first_slot.as<uint32_t>(), r->records.as<float4>(),
                                    r->grad2d.as<float>(), gv, (float*)densification_info, mode,
