@@ -16,13 +16,27 @@
 
 namespace tgs {
 
+// Non-temporal 16-byte access for the streams nothing reads again soon
+// (gradients, moments): measured 0.245 -> 0.19 ms at 1M Gaussians. theta
+// keeps ordinary accesses (the next forward reads it; non-temporal theta
+// measured slower).
+typedef float v4f __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ float4 ntld(const float* p) {
+    const v4f v = __builtin_nontemporal_load((const v4f*)p);
+    return make_float4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ void ntst(float* p, float4 a) {
+    v4f v = {a.x, a.y, a.z, a.w};
+    __builtin_nontemporal_store(v, (v4f*)p);
+}
+
 struct AdamLaunch {
     AdamArgs a;
     int64_t block_start[7];
 };
 
 constexpr int kAdamThreads = 256;
-constexpr int kAdamVecPerThread = 4;                       // 4-element vectors per thread
+constexpr int kAdamVecPerThread = 2;                       // 4-element vectors per thread (2 beat 1, 4, 8)
 constexpr int kAdamChunk = kAdamThreads * kAdamVecPerThread * 4;
 
 __device__ __forceinline__ float adam_one(float th, float gr_raw, float& m, float& v, const AdamGroup& g,
@@ -94,13 +108,13 @@ __global__ void __launch_bounds__(kAdamThreads) adam_kernel(AdamLaunch L) {
 #pragma unroll
                 for (int q = 0; q < 4; ++q) lv[q] = L.a.row_mask[row_of((uint32_t)(e0 + q), g.row_width)] != 0;
                 float4 gg = make_float4(0.f, 0.f, 0.f, 0.f);
-                if (lv[0] || lv[1] || lv[2] || lv[3]) gg = *(const float4*)(g.grad + e0);
+                if (lv[0] || lv[1] || lv[2] || lv[3]) gg = ntld(g.grad + e0);
                 gv[k] = make_float4(lv[0] ? gg.x : 0.f, lv[1] ? gg.y : 0.f, lv[2] ? gg.z : 0.f, lv[3] ? gg.w : 0.f);
             } else {
-                gv[k] = *(const float4*)(g.grad + e0);
+                gv[k] = ntld(g.grad + e0);
             }
-            mv[k] = *(const float4*)(g.m1 + e0);
-            vv[k] = *(const float4*)(g.m2 + e0);
+            mv[k] = ntld(g.m1 + e0);
+            vv[k] = ntld(g.m2 + e0);
         }
     }
 #pragma unroll
@@ -119,8 +133,8 @@ __global__ void __launch_bounds__(kAdamThreads) adam_kernel(AdamLaunch L) {
             } else {
                 *(float4*)((float*)g.theta + e0) = make_float4(th[k][0], th[k][1], th[k][2], th[k][3]);
             }
-            *(float4*)(g.m1 + e0) = mv[k];
-            *(float4*)(g.m2 + e0) = vv[k];
+            ntst(g.m1 + e0, mv[k]);
+            ntst(g.m2 + e0, vv[k]);
         } else if (e0 < g.count) {
             for (int64_t i = e0; i < g.count; ++i) {
                 float t = g.theta_half ? __half2float(((const __half*)g.theta)[i]) : ((const float*)g.theta)[i];

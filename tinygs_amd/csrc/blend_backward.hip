@@ -50,6 +50,9 @@ __device__ __forceinline__ void wave_lds_sync() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
+// ABS: also sum |dL/dmean2d| per pixel (the densification statistic); the
+// sums are only read when densification info is requested.
+template <bool ABS>
 __global__ void __launch_bounds__(256) blend_backward_kernel(
     CamParams cam, const uint32_t* __restrict__ inst_vals, const float2* __restrict__ mean2d,
     const float4* __restrict__ conic_opacity, const float4* __restrict__ color_pt, const float* __restrict__ image,
@@ -171,12 +174,17 @@ __global__ void __launch_bounds__(256) blend_backward_kernel(
                 acc[4] = __builtin_fmaf(hp, dx, acc[4]);
                 acc[5] = __builtin_fmaf(hp, dy, acc[5]);
                 acc[6] = __builtin_fmaf(hq, dy, acc[6]);
-                const float gmx = __builtin_fmaf(hp, r1.z, hq * r2.w);
-                const float gmy = __builtin_fmaf(hp, r2.w, hq * r1.w);
-                acc[7] += gmx;
-                acc[8] += gmy;
-                acc[9] += __builtin_fabsf(gmx);
-                acc[10] += __builtin_fabsf(gmy);
+                if constexpr (ABS) {
+                    const float gmx = __builtin_fmaf(hp, r1.z, hq * r2.w);
+                    const float gmy = __builtin_fmaf(hp, r2.w, hq * r1.w);
+                    acc[7] += gmx;
+                    acc[8] += gmy;
+                    acc[9] += __builtin_fabsf(gmx);
+                    acc[10] += __builtin_fabsf(gmy);
+                } else {
+                    acc[7] = __builtin_fmaf(hq, r2.w, __builtin_fmaf(hp, r1.z, acc[7]));
+                    acc[8] = __builtin_fmaf(hq, r1.w, __builtin_fmaf(hp, r2.w, acc[8]));
+                }
                 Tb[s] *= oma;
             }
             float t[3];
@@ -212,7 +220,7 @@ void launch_blend_backward(const CamParams& cam, const uint32_t* inst_vals, cons
                            const float4* conic_opacity, const float4* color_pt, const float* image,
                            const float* grad_image, const uint32_t* n_contrib, const float4* ckpt,
                            const uint4* items, BinCtl* ctl, uint32_t* rec_count, const uint32_t* first_slot,
-                           float4* records, uint32_t* heavy, hipStream_t s) {
+                           float4* records, uint32_t* heavy, bool with_abs, hipStream_t s) {
     const uint32_t n_tiles = cam.grid_w * cam.grid_h;
     if (n_tiles == 0) return;
     if (g_blocks <= 0) {
@@ -221,14 +229,22 @@ void launch_blend_backward(const CamParams& cam, const uint32_t* inst_vals, cons
         if (hipGetDevice(&dev) != hipSuccess ||
             hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
             cus = 256;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, blend_backward_kernel, 256, 0) != hipSuccess ||
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, blend_backward_kernel<true>, 256, 0) !=
+                hipSuccess ||
             per_cu <= 0)
             per_cu = 4;
         g_blocks = cus * per_cu;
     }
-    blend_backward_kernel<<<(uint32_t)g_blocks, 256, 0, s>>>(cam, inst_vals, mean2d, conic_opacity, color_pt, image,
-                                                             grad_image, n_contrib, ckpt, items, ctl, rec_count,
-                                                             first_slot, records, heavy);
+    if (with_abs)
+        blend_backward_kernel<true><<<(uint32_t)g_blocks, 256, 0, s>>>(cam, inst_vals, mean2d, conic_opacity,
+                                                                       color_pt, image, grad_image, n_contrib, ckpt,
+                                                                       items, ctl, rec_count, first_slot, records,
+                                                                       heavy);
+    else
+        blend_backward_kernel<false><<<(uint32_t)g_blocks, 256, 0, s>>>(cam, inst_vals, mean2d, conic_opacity,
+                                                                        color_pt, image, grad_image, n_contrib, ckpt,
+                                                                        items, ctl, rec_count, first_slot, records,
+                                                                        heavy);
 }
 
 // Sums the 2D-gradient records of each listed primitive (more than

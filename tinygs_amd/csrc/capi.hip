@@ -506,7 +506,7 @@ int tgs_rasterizer_backward_ex(tgs_rasterizer* r, const void* grad_image, const 
                               r->conic_opacity.as<float4>(), r->color.as<float4>(), (const float*)image,
                               (const float*)grad_image, r->n_contrib.as<uint32_t>(), r->ckpt.as<float4>(),
                               r->items.as<uint4>(), ctl, r->rec_count.as<uint32_t>(), r->first_slot.as<uint32_t>(),
-                              r->records.as<float4>(), r->heavy.as<uint32_t>(), s);
+                              r->records.as<float4>(), r->heavy.as<uint32_t>(), densification_info != nullptr, s);
     }
     r->bwd_queues_clear = false;
     TGS_CHECK_LAUNCH();

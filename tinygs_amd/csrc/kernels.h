@@ -104,7 +104,8 @@ void launch_blend_forward(const CamParams& cam, const uint2* ranges, const uint3
 // 2D gradient records: each (primitive p, bucket) the backward processes
 // takes record index first_slot[p] + atomicAdd(rec_count[p], 1) (below
 // first_slot[p] + n_touched[p]: a primitive is in a tile's list once) and
-// writes 12 floats there: dL/dmean2d (2), |.| sums (2), dL/dconic (3),
+// writes 12 floats there: dL/dmean2d (2), |.| sums (2; 0 unless with_abs:
+// only densification reads them), dL/dconic (3),
 // dL/dcolour (3), sum of alpha dL/dalpha, 0. Primitives reaching
 // kLightRecords + 1 records are listed in `heavy` (count ctl->heavy_n);
 // gather_heavy sums their records into grad2d[12 p]; the preprocess backward
@@ -116,7 +117,7 @@ void launch_blend_backward(const CamParams& cam, const uint32_t* inst_vals, cons
                            const float4* conic_opacity, const float4* color_pt, const float* image,
                            const float* grad_image, const uint32_t* n_contrib, const float4* ckpt,
                            const uint4* items, BinCtl* ctl, uint32_t* rec_count, const uint32_t* first_slot,
-                           float4* records, uint32_t* heavy, hipStream_t s);
+                           float4* records, uint32_t* heavy, bool with_abs, hipStream_t s);
 void launch_gather_heavy(const uint32_t* heavy, const BinCtl* ctl, const uint32_t* rec_count,
                          const uint32_t* first_slot, const float4* records, float* grad2d, hipStream_t s);
 
