@@ -496,7 +496,8 @@ constexpr uint32_t kEmitStage = 4096;
 
 __global__ void __launch_bounds__(256) emit_kernel(const uint32_t* __restrict__ prims,
                                                    const uint32_t* __restrict__ offs, const BinCtl* ctl,
-                                                   int64_t max_count, const uint4* __restrict__ rec, uint32_t grid_w,
+                                                   int64_t max_count, const uint4* __restrict__ rec,
+                                                   const uint32_t* __restrict__ tile_bits, uint32_t grid_w,
                                                    uint32_t* __restrict__ inst_keys,
                                                    uint32_t* __restrict__ inst_vals,
                                                    uint32_t* __restrict__ first_slot) {
@@ -519,13 +520,14 @@ __global__ void __launch_bounds__(256) emit_kernel(const uint32_t* __restrict__ 
     const int64_t k = k0 + t;
     const bool active = k < n;
     const uint32_t lane = lane_id();
-    uint32_t p = 0, off = 0, cap = 0, x0 = 0, x1 = 0, y0 = 0, y1 = 0;
+    uint32_t p = 0, off = 0, cap = 0, x0 = 0, x1 = 0, y0 = 0, y1 = 0, bits = 0;
     float smx = 0.f, smy = 0.f, ca = 0.f, cb = 0.f, cc = 0.f, pt = 0.f;
     if (active) {
         p = prims[k];
         off = offs[k];
         cap = offs[k + 1] - off;   // slots reserved for this primitive (= its n_touched)
         first_slot[p] = off;
+        bits = tile_bits[p];
         const uint4 r0 = rec[2 * (size_t)p], r1 = rec[2 * (size_t)p + 1];
         x0 = r0.x & 0xffffu; x1 = r0.x >> 16; y0 = r0.y & 0xffffu; y1 = r0.y >> 16;
         smx = u2f(r0.z) - 0.5f;
@@ -537,9 +539,10 @@ __global__ void __launch_bounds__(256) emit_kernel(const uint32_t* __restrict__ 
     uint32_t written = 0;
     if (active) {
         const uint32_t first = nrect < 8u ? nrect : 8u;
+        // rect tiles 0..31 were tested by the preprocess (tile_bits)
         for (uint32_t q = 0; q < first; ++q) {
             const uint32_t tx = x0 + q % bw, ty = y0 + q / bw;
-            if (will_contribute_e(smx, smy, ca, cb, cc, tx, ty, pt) && written < cap) {
+            if (((bits >> q) & 1u) && written < cap) {
                 put(off + written, ty * grid_w + tx, p);
                 ++written;
             }
@@ -555,6 +558,7 @@ __global__ void __launch_bounds__(256) emit_kernel(const uint32_t* __restrict__ 
         const uint32_t s_x0 = readlane_u32(x0, src), s_y0 = readlane_u32(y0, src);
         const uint32_t s_bw = readlane_u32(bw, src), s_n = readlane_u32(nrect, src);
         const uint32_t s_p = readlane_u32(p, src);
+        const uint32_t s_bits = readlane_u32(bits, src);
         const uint32_t s_end = readlane_u32(off, src) + readlane_u32(cap, src);
         uint32_t s_off = readlane_u32(off, src) + readlane_u32(written, src);
         for (uint32_t base = 8u; base < s_n; base += kWave) {
@@ -564,7 +568,7 @@ __global__ void __launch_bounds__(256) emit_kernel(const uint32_t* __restrict__ 
             if (q < s_n) {
                 tx = s_x0 + q % s_bw;
                 ty = s_y0 + q / s_bw;
-                hit = will_contribute_e(s_mx, s_my, s_a, s_b, s_c, tx, ty, s_t);
+                hit = q < 32u ? ((s_bits >> q) & 1u) != 0u : will_contribute_e(s_mx, s_my, s_a, s_b, s_c, tx, ty, s_t);
             }
             const uint64_t m = ballot(hit);
             const uint32_t pos = s_off + mask_rank(m);
@@ -582,11 +586,11 @@ __global__ void __launch_bounds__(256) emit_kernel(const uint32_t* __restrict__ 
 }
 
 void launch_emit_instances(const uint32_t* prims, const uint32_t* offs, const BinCtl* ctl, int64_t max_count,
-                           const uint4* rec, uint32_t grid_w, uint32_t* inst_keys, uint32_t* inst_vals,
-                           uint32_t* first_slot, hipStream_t s) {
+                           const uint4* rec, const uint32_t* tile_bits, uint32_t grid_w, uint32_t* inst_keys,
+                           uint32_t* inst_vals, uint32_t* first_slot, hipStream_t s) {
     if (max_count <= 0) return;
-    emit_kernel<<<(unsigned)((max_count + 255) / 256), 256, 0, s>>>(prims, offs, ctl, max_count, rec, grid_w,
-                                                                    inst_keys, inst_vals, first_slot);
+    emit_kernel<<<(unsigned)((max_count + 255) / 256), 256, 0, s>>>(prims, offs, ctl, max_count, rec, tile_bits,
+                                                                    grid_w, inst_keys, inst_vals, first_slot);
 }
 
 // ---------------------------------------------------------------- ranges

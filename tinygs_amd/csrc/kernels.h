@@ -34,7 +34,9 @@ struct GradView {
 // ---- preprocess (kernels_forward.cuh:157-412)
 // rec: 2 x uint4 per visible primitive: {x_min | x_max << 16, y_min | y_max << 16, mean2d.x, mean2d.y},
 // {conic a, b, c, ln(255 opacity)} (float bits).
-void launch_preprocess(const GaussianView& g, const CamParams& cam, uint32_t* n_touched, uint4* rec,
+// tile_bits[i]: exact-test outcome of the primitive's rect tiles 0..31 (row-major in the rect).
+void launch_preprocess(const GaussianView& g, const CamParams& cam, uint32_t* n_touched, uint32_t* tile_bits,
+                       uint4* rec,
                        float2* mean2d, float4* conic_opacity, float4* color_pt, uint32_t* depth_key,
                        float* densif, hipStream_t s);
 
@@ -83,8 +85,8 @@ int radix_sort(uint32_t* keys[2], uint32_t* vals[2], uint32_t* v2[2], const uint
 // Also writes first_slot[p] = offs[k] for every visible primitive p = prims[k]:
 // the first of the n_touched[p] instance slots reserved for p.
 void launch_emit_instances(const uint32_t* prims, const uint32_t* offs, const BinCtl* ctl, int64_t max_count,
-                           const uint4* rec, uint32_t grid_w, uint32_t* inst_keys, uint32_t* inst_vals,
-                           uint32_t* first_slot, hipStream_t s);
+                           const uint4* rec, const uint32_t* tile_bits, uint32_t grid_w, uint32_t* inst_keys,
+                           uint32_t* inst_vals, uint32_t* first_slot, hipStream_t s);
 // [start, end) per tile, (0, 0) for empty tiles; every entry written.
 void launch_tile_ranges(const uint32_t* inst_keys, int64_t n_inst, uint2* ranges, uint32_t n_tiles, hipStream_t s);
 

@@ -84,8 +84,8 @@ template <typename ShT>
 __global__ void __launch_bounds__(256) preprocess_kernel(
     const float* __restrict__ means, const float* __restrict__ scales, const float* __restrict__ rots,
     const float* __restrict__ opac, const ShT* __restrict__ sh0, const ShT* __restrict__ shr, int64_t n, int bases,
-    CamParams cam, uint32_t* __restrict__ n_touched, uint4* __restrict__ rec, float2* __restrict__ mean2d,
-    float4* __restrict__ conic_opacity, float4* __restrict__ color_pt, uint32_t* __restrict__ depth_key,
+    CamParams cam, uint32_t* __restrict__ n_touched, uint32_t* __restrict__ tile_bits, uint4* __restrict__ rec,
+    float2* __restrict__ mean2d, float4* __restrict__ conic_opacity, float4* __restrict__ color_pt, uint32_t* __restrict__ depth_key,
     float4* __restrict__ densif) {
     // SH-rest coefficients of the block's 256 primitives are one contiguous
     // run: stage it in LDS with 16-byte lane-contiguous loads.
@@ -197,15 +197,19 @@ __global__ void __launch_bounds__(256) preprocess_kernel(
         }
     }
 
-    // exact tile count: first 8 tiles per lane, the rest wave-cooperatively
+    // exact tile count: first 8 tiles per lane, the rest wave-cooperatively.
+    // The outcomes for rect tiles 0..31 (row-major in the rect) are kept as a
+    // bit mask, so the instance emission need not repeat the test there.
     const float smx = m2x - 0.5f, smy = m2y - 0.5f;
     const uint32_t bw = xmax - xmin;
-    uint32_t cnt = 0;
+    uint32_t cnt = 0, bits = 0;
     if (active) {
         const uint32_t first = nmax < 8u ? nmax : 8u;
         for (uint32_t k = 0; k < first; ++k) {
             const uint32_t ty_ = ymin + k / bw, tx_ = xmin + k % bw;
-            cnt += will_contribute(smx, smy, ca, cb, cc, tx_, ty_, pthr) ? 1u : 0u;
+            const bool hit = will_contribute(smx, smy, ca, cb, cc, tx_, ty_, pthr);
+            cnt += hit ? 1u : 0u;
+            bits |= hit ? (1u << k) : 0u;
         }
     }
     uint64_t coop = ballot(active && nmax > 8u);
@@ -217,14 +221,19 @@ __global__ void __launch_bounds__(256) preprocess_kernel(
         const float s_t = readlane_f32(pthr, src);
         const uint32_t s_x0 = readlane_u32(xmin, src), s_y0 = readlane_u32(ymin, src);
         const uint32_t s_bw = readlane_u32(bw, src), s_n = readlane_u32(nmax, src);
-        uint32_t c = 0;
+        uint32_t c = 0, b32 = 0;
         for (uint32_t base = 8u; base < s_n; base += kWave) {
             const uint32_t k = base + lane;
             bool hit = false;
             if (k < s_n) hit = will_contribute(s_mx, s_my, s_a, s_b, s_c, s_x0 + k % s_bw, s_y0 + k / s_bw, s_t);
-            c += (uint32_t)__builtin_popcountll(ballot(hit));
+            const uint64_t hm = ballot(hit);
+            if (base == 8u) b32 = (uint32_t)(hm & 0xffffffu) << 8;   // rect tiles 8..31
+            c += (uint32_t)__builtin_popcountll(hm);
         }
-        if (lane == src) cnt += c;
+        if (lane == src) {
+            cnt += c;
+            bits |= b32;
+        }
     }
 
     if (i >= n) return;
@@ -233,6 +242,7 @@ __global__ void __launch_bounds__(256) preprocess_kernel(
         return;
     }
     n_touched[i] = cnt;
+    tile_bits[i] = bits;
     // 32-byte binning record, gathered once per primitive by the emission
     rec[2 * i] = make_uint4(xmin | (xmax << 16), ymin | (ymax << 16), f2u(m2x), f2u(m2y));
     rec[2 * i + 1] = make_uint4(f2u(ca), f2u(cb), f2u(cc), f2u(pthr));
@@ -244,8 +254,8 @@ __global__ void __launch_bounds__(256) preprocess_kernel(
     depth_key[i] = f2u(depth);
 }
 
-void launch_preprocess(const GaussianView& g, const CamParams& cam, uint32_t* n_touched, uint4* rec,
-                       float2* mean2d, float4* conic_opacity, float4* color_pt, uint32_t* depth_key, float* densif,
+void launch_preprocess(const GaussianView& g, const CamParams& cam, uint32_t* n_touched, uint32_t* tile_bits,
+                       uint4* rec, float2* mean2d, float4* conic_opacity, float4* color_pt, uint32_t* depth_key, float* densif,
                        hipStream_t s) {
     if (g.n <= 0) return;
     const int bases = (g.sh_degree + 1) * (g.sh_degree + 1);
@@ -253,12 +263,13 @@ void launch_preprocess(const GaussianView& g, const CamParams& cam, uint32_t* n_
     if (g.sh_dtype == kShF16) {
         preprocess_kernel<__half><<<grid, 256, 0, s>>>(g.means, g.scales, g.rotations, g.opacities,
                                                        (const __half*)g.sh0, (const __half*)g.sh_rest, g.n, bases,
-                                                       cam, n_touched, rec, mean2d, conic_opacity, color_pt,
-                                                       depth_key, (float4*)densif);
+                                                       cam, n_touched, tile_bits, rec, mean2d, conic_opacity,
+                                                       color_pt, depth_key, (float4*)densif);
     } else {
         preprocess_kernel<float><<<grid, 256, 0, s>>>(g.means, g.scales, g.rotations, g.opacities,
                                                       (const float*)g.sh0, (const float*)g.sh_rest, g.n, bases, cam,
-                                                      n_touched, rec, mean2d, conic_opacity, color_pt, depth_key,
+                                                      n_touched, tile_bits, rec, mean2d, conic_opacity, color_pt,
+                                                      depth_key,
                                                       (float4*)densif);
     }
 }
