@@ -107,7 +107,7 @@ __global__ void __launch_bounds__(256) blend_backward_kernel(
         // ---- per-pixel state at the bucket start
         const uint32_t gx = tile % cam.grid_w, gy = tile / cam.grid_w;
         const uint32_t slot0 = (first - (uint32_t)j0) / (uint32_t)kBucket + tile;   // tile's first checkpoint slot
-        float pcx[4], pcy[4], g0[4], g1[4], g2[4], Tb[4], A0[4], A1[4], A2[4];
+        float pcx[4], pcy[4], g0[4], g1[4], g2[4], Tb[4], AG[4];
         int32_t lk[4];
         uint32_t pix[4];
         bool in[4];
@@ -139,15 +139,32 @@ __global__ void __launch_bounds__(256) blend_backward_kernel(
             kmax = max(kmax, lk[s]);
             g0[s] = act ? q0v : 0.f; g1[s] = act ? q1v : 0.f; g2[s] = act ? q2v : 0.f;
             Tb[s] = act ? ck.w : 0.f;
-            A0[s] = act ? i0 - ck.x : 0.f; A1[s] = act ? i1 - ck.y : 0.f; A2[s] = act ? i2 - ck.z : 0.f;
+            // (colour still to come behind this Gaussian) . dL/dpixel, carried as
+            // one scalar: it drops by wgt * (colour . dL/dpixel) per Gaussian
+            AG[s] = act ? __builtin_fmaf(i2 - ck.z, q2v, __builtin_fmaf(i1 - ck.y, q1v, (i0 - ck.x) * q0v)) : 0.f;
         }
         kmax = min((int32_t)wave_max_u32((uint32_t)kmax), cnt);
+        // bit k: some pixel's last contributor in this bucket is k - 1; from
+        // Gaussian k on its transmittance and remaining colour are zero, which
+        // makes every later term of that pixel exactly zero
+        uint32_t stops = 0;
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+            stops |= (lk[s] > 0 && lk[s] < kmax) ? 1u << lk[s] : 0u;
+        stops = wave_or_u32(stops);
         wave_lds_sync();
 
         for (int32_t k = 0; k < kmax; ++k) {
             const float4 r0 = s_rec[w][0][k];   // mx, my, a/2 L, b L
             const float4 r1 = s_rec[w][1][k];   // c/2 L, opacity, a, c
             const float4 r2 = s_rec[w][2][k];   // clamped colour, b
+            if ((stops >> k) & 1u) {
+#pragma unroll
+                for (int s = 0; s < 4; ++s) {
+                    Tb[s] = lk[s] == k ? 0.f : Tb[s];
+                    AG[s] = lk[s] == k ? 0.f : AG[s];
+                }
+            }
             float acc[12];
 #pragma unroll
             for (int q = 0; q < 12; ++q) acc[q] = 0.f;
@@ -156,16 +173,14 @@ __global__ void __launch_bounds__(256) blend_backward_kernel(
                 const float dx = r0.x - pcx[s], dy = r0.y - pcy[s];
                 const float sg = __builtin_fmaf(dx, __builtin_fmaf(r0.z, dx, r0.w * dy), (r1.x * dy) * dy);
                 const float G = __builtin_amdgcn_exp2f(-__builtin_fmaxf(sg, 0.f));
-                const float ab = k < lk[s] ? __builtin_fminf(r1.y * G, kMaxAlpha) : 0.f;
+                const float ab = __builtin_fminf(r1.y * G, kMaxAlpha);
                 const float wgt = Tb[s] * ab;
                 acc[0] = __builtin_fmaf(wgt, g0[s], acc[0]);
                 acc[1] = __builtin_fmaf(wgt, g1[s], acc[1]);
                 acc[2] = __builtin_fmaf(wgt, g2[s], acc[2]);
-                A0[s] = __builtin_fmaf(-wgt, r2.x, A0[s]);
-                A1[s] = __builtin_fmaf(-wgt, r2.y, A1[s]);
-                A2[s] = __builtin_fmaf(-wgt, r2.z, A2[s]);
                 const float cg = __builtin_fmaf(r2.z, g2[s], __builtin_fmaf(r2.y, g1[s], r2.x * g0[s]));
-                const float ag = __builtin_fmaf(A2[s], g2[s], __builtin_fmaf(A1[s], g1[s], A0[s] * g0[s]));
+                AG[s] = __builtin_fmaf(-wgt, cg, AG[s]);
+                const float ag = AG[s];
                 const float oma = 1.0f - ab;
                 const float dalpha = __builtin_fmaf(Tb[s], cg, -(ag * __builtin_amdgcn_rcpf(oma)));
                 const float pp = ab * dalpha;
@@ -181,9 +196,9 @@ __global__ void __launch_bounds__(256) blend_backward_kernel(
                     acc[8] += gmy;
                     acc[9] += __builtin_fabsf(gmx);
                     acc[10] += __builtin_fabsf(gmy);
-                } else {
-                    acc[7] = __builtin_fmaf(hq, r2.w, __builtin_fmaf(hp, r1.z, acc[7]));
-                    acc[8] = __builtin_fmaf(hq, r1.w, __builtin_fmaf(hp, r2.w, acc[8]));
+                } else {   // sums of pp dx, pp dy; the conic is applied per Gaussian at the end
+                    acc[7] += hp;
+                    acc[8] += hq;
                 }
                 Tb[s] *= oma;
             }
@@ -204,7 +219,13 @@ __global__ void __launch_bounds__(256) blend_backward_kernel(
             auto val = [&](int q) { return ev ? s_part[w][q][k] : 0.f; };
             // record order: mean2d(2), abs(2), conic(3), colour(3), alpha partial, 0
             float4* dst = records + 3 * (size_t)(slot + sub);
-            dst[0] = make_float4(-val(7), -val(8), val(9), val(10));
+            float gmx = val(7), gmy = val(8);
+            if constexpr (!ABS) {
+                const float a = s_rec[w][1][k].z, c = s_rec[w][1][k].w, bq = s_rec[w][2][k].w;
+                gmx = __builtin_fmaf(a, val(7), bq * val(8));
+                gmy = __builtin_fmaf(bq, val(7), c * val(8));
+            }
+            dst[0] = make_float4(-gmx, -gmy, val(9), val(10));
             dst[1] = make_float4(-0.5f * val(4), -0.5f * val(5), -0.5f * val(6), (mask & 1u) ? val(0) : 0.f);
             dst[2] = make_float4((mask & 2u) ? val(1) : 0.f, (mask & 4u) ? val(2) : 0.f, val(3), 0.f);
             if (sub == kLightRecords) heavy[atomicAdd(&ctl->heavy_n, 1u)] = p;

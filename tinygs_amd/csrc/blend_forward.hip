@@ -146,7 +146,10 @@ __global__ void __launch_bounds__(256) blend_forward_kernel(CamParams cam, const
             }
             const float dx = a.x - pcx, dy = a.y - pcy;
             const float sigma = __builtin_fmaf(dx, __builtin_fmaf(a.z, dx, a.w * dy), (bb.x * dy) * dy);
-            const float alpha = __builtin_fminf(bb.y * det_expf_nonpos(__builtin_fminf(-sigma, 0.f)), kMaxAlpha);
+            // exp(-clamp(sigma, 0, 104)): the alpha decisions are those of
+            // det_expf_nonpos(min(-sigma, 0)) (beyond sigma 103.97 both give 0)
+            const float alpha =
+                __builtin_fminf(bb.y * det_expf_core(-__builtin_amdgcn_fmed3f(sigma, 0.f, 104.f)), kMaxAlpha);
             const bool ok = !done && sigma >= 0.f && alpha >= kMinAlpha;
             const float nT = T * (1.0f - alpha);
             const bool term = ok && nT < kTransmittanceMin;

@@ -86,6 +86,16 @@ __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
     return readlane_u32(v, 63);
 }
 
+__device__ __forceinline__ uint32_t wave_or_u32(uint32_t v) {
+    v |= dpp_u32<0x128>(v);
+    v |= dpp_u32<0x124>(v);
+    v |= dpp_u32<0x122>(v);
+    v |= dpp_u32<0x121>(v);
+    v |= dpp_u32<0x142, 0xA>(v);
+    v |= dpp_u32<0x143, 0xC>(v);
+    return readlane_u32(v, 63);
+}
+
 __device__ __forceinline__ uint32_t wave_sum_u32(uint32_t v) {
     v += dpp_u32<0x128>(v);
     v += dpp_u32<0x124>(v);

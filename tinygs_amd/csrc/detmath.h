@@ -45,9 +45,9 @@ TGS_HD float det_expf(float x) {
     return __builtin_ldexpf(p, (int)k);
 }
 
-// e^x for x <= 0 (the blend's exp(-sigma)); same bits as det_expf there.
-TGS_HD float det_expf_nonpos(float x) {
-    x = x < -103.97208404541015625f ? -104.0f : x;  // -104 -> k=-150, ldexp gives 0
+// e^x for -104 <= x <= 0 without range checks; same bits as det_expf for
+// x >= -103.97208 and 0 below it (k = -150 there and p < 1).
+TGS_HD float det_expf_core(float x) {
     const float k = __builtin_rintf(x * 1.44269502162933349609375f);
     float r = __builtin_fmaf(k, -0.693145751953125f, x);
     r = __builtin_fmaf(k, -1.428606765330187045037746429443359375e-06f, r);
@@ -60,6 +60,12 @@ TGS_HD float det_expf_nonpos(float x) {
     p = __builtin_fmaf(p, r, 1.0f);
     p = __builtin_fmaf(p, r, 1.0f);
     return __builtin_ldexpf(p, (int)k);
+}
+
+// e^x for x <= 0 (the blend's exp(-sigma)); same bits as det_expf there.
+TGS_HD float det_expf_nonpos(float x) {
+    x = x < -103.97208404541015625f ? -104.0f : x;  // -104 -> k=-150, ldexp gives 0
+    return det_expf_core(x);
 }
 
 // natural log, x > 0; 0 -> -inf, negative / NaN -> NaN.
