@@ -86,6 +86,18 @@ __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
     return readlane_u32(v, 63);
 }
 
+// Workgroups are dispatched in linear-id order, round-robin over the 8
+// XCDs (each with its own L2). This maps the dispatch index to a work index
+// so that XCD x receives one contiguous run of work indices: neighbouring
+// tiles then share an L2 and their halos are re-read from it, not from HBM.
+// A bijection on [0, n).
+__device__ __forceinline__ uint32_t xcd_contiguous_index(uint32_t linear, uint32_t n) {
+    constexpr uint32_t kXcds = 8;
+    const uint32_t per = n / kXcds, rem = n % kXcds;
+    const uint32_t x = linear % kXcds, j = linear / kXcds;
+    return x * per + min(x, rem) + j;
+}
+
 __device__ __forceinline__ uint32_t wave_or_u32(uint32_t v) {
     v |= dpp_u32<0x128>(v);
     v |= dpp_u32<0x124>(v);

@@ -7,8 +7,8 @@
 // in fp32 with the fp32 prediction and target.
 //
 // MI355X design: one workgroup per 32x32 output tile (42x42 with the 5-pixel
-// halo, filled through whole 8x8 blocks: coalesced 256-byte runs), all three
-// channels in turn. The horizontal pass gives each thread
+// halo, filled through whole 8x8 blocks: coalesced 256-byte runs) and
+// channel. The horizontal pass gives each thread
 // four adjacent output columns of one row (14 inputs feed 4 x 11 taps), the
 // vertical pass four adjacent rows of one column (14 rows of horizontal sums
 // feed 4 x 11 taps), so every LDS value read is used several times. The SSIM
@@ -67,56 +67,55 @@ constexpr int kIT = kOT + 10;     // input tile edge (5-pixel halo)
 
 // Halo fill through whole 8x8 blocks of the tiled layout: the 42x42 region
 // at (bx - 5, by - 5) lies inside the 6x6 blocks starting at block
-// (bx / 8 - 1, by / 8 - 1) (bx, by multiples of 32). Wave w loads blocks
-// w, w + 4, ... (one contiguous 256-byte run per plane each), lane = pixel of
-// the block. Every load is issued before any value is used. Round r of this
-// thread covers LDS cell (ly[r], lx[r]), or none (lx[r] = -1); pixels outside
+// (bx / 8 - 1, by / 8 - 1) (bx, by multiples of 32), at offset 3 in both
+// directions. Wave w loads blocks w, w + 4, ... (one contiguous 256-byte run
+// per plane each), lane = pixel of the block. The block of a round is
+// wave-uniform, so its base address and bounds are scalar and a lane only
+// compares its own (x, y) inside the block against them; pixels outside
 // W x H read as 0 (the reference's zero padding).
 constexpr int kHaloBlocks = 36;
 constexpr int kHaloRounds = kHaloBlocks / 4;   // 9 blocks per wave
-__device__ __forceinline__ bool halo_cell(int r, int bx, int by, uint32_t W, uint32_t H, uint32_t tw, uint32_t& q,
-                                          int& lx, int& ly) {
-    const int w = (int)(threadIdx.x >> 6), lane = (int)(threadIdx.x & 63u);
+constexpr int kHT = 48;                        // 6 blocks of 8
+
+struct HaloRound {
+    size_t base;   // element offset of the block in a plane (0 when the block lies outside the planes)
+    int cx, cy;    // block position among the 6 x 6
+    bool in;       // this lane's pixel lies inside W x H
+};
+
+__device__ __forceinline__ HaloRound halo_round(int r, int bx, int by, uint32_t W, uint32_t H, uint32_t tw,
+                                                uint32_t th) {
+    const int w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const int lane = (int)(threadIdx.x & 63u);
     const int b = w + 4 * r;
-    const int bcx = bx / 8 - 1 + b % 6, bcy = by / 8 - 1 + b / 6;
-    const int gx = bcx * 8 + (lane & 7), gy = bcy * 8 + (lane >> 3);
-    lx = gx - (bx - 5);
-    ly = gy - (by - 5);
-    const bool cell = lx >= 0 && lx < kIT && ly >= 0 && ly < kIT;
-    if (!cell) lx = -1;
-    const bool in = cell && gx >= 0 && gy >= 0 && gx < (int)W && gy < (int)H;
-    q = in ? ((uint32_t)bcy * tw + (uint32_t)bcx) * 64u + (uint32_t)lane : 0u;
-    return in;
+    HaloRound h;
+    h.cx = b % 6;
+    h.cy = b / 6;
+    const int bcx = bx / 8 - 1 + h.cx, bcy = by / 8 - 1 + h.cy;
+    const bool blk = bcx >= 0 && bcy >= 0 && bcx < (int)tw && bcy < (int)th;
+    h.base = blk ? ((size_t)bcy * tw + (size_t)bcx) * 64u : 0u;
+    h.in = blk && (lane & 7) < (int)W - bcx * 8 && (lane >> 3) < (int)H - bcy * 8;
+    return h;
 }
-__device__ __forceinline__ void halo_load2(const float* __restrict__ a, const float* __restrict__ b, int bx, int by,
-                                           uint32_t W, uint32_t H, uint32_t tw, float av[kHaloRounds],
-                                           float bv[kHaloRounds]) {
-#pragma unroll
-    for (int r = 0; r < kHaloRounds; ++r) {
-        uint32_t q;
-        int lx, ly;
-        const bool in = halo_cell(r, bx, by, W, H, tw, q, lx, ly);
-        const float x = a[q], y = b[q];   // q = 0 (always allocated) when outside
-        av[r] = in ? x : 0.f;
-        bv[r] = in ? y : 0.f;
-    }
-}
-__device__ __forceinline__ void halo_load1(const float* __restrict__ a, int bx, int by, uint32_t W, uint32_t H,
-                                           uint32_t tw, float av[kHaloRounds]) {
-#pragma unroll
-    for (int r = 0; r < kHaloRounds; ++r) {
-        uint32_t q;
-        int lx, ly;
-        const bool in = halo_cell(r, bx, by, W, H, tw, q, lx, ly);
-        const float x = a[q];
-        av[r] = in ? x : 0.f;
-    }
+
+// (tile x, tile y, channel) of this workgroup: the grid is (tiles x, tiles
+// y, 3) and tiles are taken in row-major order per channel, each XCD a
+// contiguous run of them.
+__device__ __forceinline__ void ssim_tile_of(uint32_t& tx, uint32_t& ty, uint32_t& ch) {
+    const uint32_t gx = gridDim.x, gy = gridDim.y;
+    const uint32_t linear = blockIdx.x + gx * (blockIdx.y + gy * blockIdx.z);
+    const uint32_t k = xcd_contiguous_index(linear, gx * gy * gridDim.z);
+    tx = k % gx;
+    ty = (k / gx) % gy;
+    ch = k / (gx * gy);
 }
 
 // Fused L1 + SSIM forward. s_l1 == 0 disables L1; assign writes loss / grad
 // instead of accumulating (grad then holds the L1 part, or 0). dm_* may be
 // NULL (loss only). SSIM terms only inside W x H; L1 over the whole padded
-// image, like the reference's L1 over all padded elements.
+// image, like the reference's L1 over all padded elements. One workgroup per
+// (32x32 tile, channel): no state is carried across channels, which keeps
+// the register footprint small enough for four workgroups per CU.
 __global__ void __launch_bounds__(256) l1_ssim_forward_kernel(uint32_t W, uint32_t H, float C1, float C2,
                                                               float s_ssim, float s_l1, int assign,
                                                               const float* __restrict__ pred,
@@ -124,127 +123,130 @@ __global__ void __launch_bounds__(256) l1_ssim_forward_kernel(uint32_t W, uint32
                                                               float* __restrict__ loss, float* __restrict__ grad,
                                                               float* __restrict__ dm_mu, float* __restrict__ dm_s1,
                                                               float* __restrict__ dm_s12) {
-    __shared__ __half2 s_in[kIT][kIT];         // fp16-rounded (pred, target), exactly the values the sums use
+    __shared__ __half2 s_in[kHT][kHT];         // fp16-rounded (pred, target), exactly the values the sums use
     __shared__ float s_h[5][kIT][kOT + 1];     // horizontal sums: x, x^2, y, y^2, xy
     const int t = (int)threadIdx.x;
-    const int bx = (int)blockIdx.x * kOT, by = (int)blockIdx.y * kOT;
+    uint32_t tx, ty, ch;
+    ssim_tile_of(tx, ty, ch);
+    const int bx = (int)tx * kOT, by = (int)ty * kOT;
     const uint32_t tw = (W + 7u) >> 3, th = (H + 7u) >> 3;
     const uint32_t cs = tw * th * 64u;
     const int pw = (int)tw * 8, ph = (int)th * 8;
-    // vertical-pass ownership: column vc, rows 4 vr .. 4 vr + 3
-    const int vc = t & 31, vr = t >> 5;
-    // software pipeline over the channels: channel c + 1's halo is loaded
-    // while channel c is convolved, and each channel's per-pixel operands are
-    // loaded before its passes
-    float pv[kHaloRounds], tv[kHaloRounds];
-    halo_load2(pred, target, bx, by, W, H, tw, pv, tv);
-    for (int c = 0; c < 3; ++c) {
+    const size_t co = (size_t)ch * cs;
+    pred += co;
+    target += co;
+    {
+        const int lane = t & 63;
+        float pv[kHaloRounds], tv[kHaloRounds];
 #pragma unroll
         for (int r = 0; r < kHaloRounds; ++r) {
-            uint32_t q;
-            int lx, ly;
-            halo_cell(r, bx, by, W, H, tw, q, lx, ly);
-            if (lx >= 0) s_in[ly][lx] = __floats2half2_rn(pv[r], tv[r]);
+            const HaloRound h = halo_round(r, bx, by, W, H, tw, th);
+            const float* __restrict__ pp = pred + h.base;   // wave-uniform block base
+            const float* __restrict__ tp = target + h.base;
+            const float x = pp[lane], y = tp[lane];
+            pv[r] = h.in ? x : 0.f;
+            tv[r] = h.in ? y : 0.f;
         }
-        float ep[4], et[4], el[4], eg[4];
+#pragma unroll
+        for (int r = 0; r < kHaloRounds; ++r) {
+            const HaloRound h = halo_round(r, bx, by, W, H, tw, th);
+            s_in[h.cy * 8 + (lane >> 3)][h.cx * 8 + (lane & 7)] = __floats2half2_rn(pv[r], tv[r]);
+        }
+    }
+    __syncthreads();
+    // horizontal: row r, output columns 4 g .. 4 g + 3
+    for (int wi = t; wi < kIT * 8; wi += 256) {
+        const int r = wi >> 3, g = wi & 7;
+        float x[14], y[14];
+#pragma unroll
+        for (int d = 0; d < 14; ++d) {
+            const float2 v = __half22float2(s_in[r + 3][4 * g + d + 3]);
+            x[d] = v.x;
+            y[d] = v.y;
+        }
+#pragma unroll
+        for (int o = 0; o < 4; ++o) {
+            float sx = 0.f, sxx = 0.f, sy = 0.f, syy = 0.f, sxy = 0.f;
+#pragma unroll
+            for (int d = 0; d < 11; ++d) {
+                const float wv = kGauss[d];
+                const float a = x[o + d], b = y[o + d];
+                sx = __builtin_fmaf(a, wv, sx);
+                sxx = __builtin_fmaf(a * a, wv, sxx);
+                sy = __builtin_fmaf(b, wv, sy);
+                syy = __builtin_fmaf(b * b, wv, syy);
+                sxy = __builtin_fmaf(a * b, wv, sxy);
+            }
+            s_h[0][r][4 * g + o] = sx;
+            s_h[1][r][4 * g + o] = sxx;
+            s_h[2][r][4 * g + o] = sy;
+            s_h[3][r][4 * g + o] = syy;
+            s_h[4][r][4 * g + o] = sxy;
+        }
+    }
+    __syncthreads();
+    // vertical: column vc, output rows 4 vr .. 4 vr + 3
+    const int vc = t & 31, vr = t >> 5;
+    float o[5][4];
+#pragma unroll
+    for (int v = 0; v < 5; ++v) {
+        float col[14];
+#pragma unroll
+        for (int d = 0; d < 14; ++d) col[d] = s_h[v][4 * vr + d][vc];
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-            const int px = bx + vc, py = by + 4 * vr + q;
-            const bool pad_ok = px < pw && py < ph;
-            const uint32_t idx = pad_ok ? tiled_index((uint32_t)py, (uint32_t)px, tw) + (uint32_t)c * cs : 0u;
-            ep[q] = pred[idx];
-            et[q] = target[idx];
-            el[q] = (!assign && loss) ? loss[idx] : 0.f;
-            eg[q] = (!assign && grad) ? grad[idx] : 0.f;
+            float acc = 0.f;
+#pragma unroll
+            for (int d = 0; d < 11; ++d) acc = __builtin_fmaf(col[q + d], kGauss[d], acc);
+            o[v][q] = acc;
         }
-        __syncthreads();
-        if (c < 2) halo_load2(pred + (size_t)(c + 1) * cs, target + (size_t)(c + 1) * cs, bx, by, W, H, tw, pv, tv);
-        // horizontal: row r, output columns 4 g .. 4 g + 3
-        for (int wi = t; wi < kIT * 8; wi += 256) {
-            const int r = wi >> 3, g = wi & 7;
-            float x[14], y[14];
+    }
+    if (dm_mu) {
+        dm_mu += co;
+        dm_s1 += co;
+        dm_s12 += co;
+    }
+    if (loss) loss += co;
+    if (grad) grad += co;
 #pragma unroll
-            for (int d = 0; d < 14; ++d) {
-                const float2 v = __half22float2(s_in[r][4 * g + d]);
-                x[d] = v.x;
-                y[d] = v.y;
-            }
-#pragma unroll
-            for (int o = 0; o < 4; ++o) {
-                float sx = 0.f, sxx = 0.f, sy = 0.f, syy = 0.f, sxy = 0.f;
-#pragma unroll
-                for (int d = 0; d < 11; ++d) {
-                    const float wv = kGauss[d];
-                    const float a = x[o + d], b = y[o + d];
-                    sx = __builtin_fmaf(a, wv, sx);
-                    sxx = __builtin_fmaf(a * a, wv, sxx);
-                    sy = __builtin_fmaf(b, wv, sy);
-                    syy = __builtin_fmaf(b * b, wv, syy);
-                    sxy = __builtin_fmaf(a * b, wv, sxy);
-                }
-                s_h[0][r][4 * g + o] = sx;
-                s_h[1][r][4 * g + o] = sxx;
-                s_h[2][r][4 * g + o] = sy;
-                s_h[3][r][4 * g + o] = syy;
-                s_h[4][r][4 * g + o] = sxy;
-            }
+    for (int q = 0; q < 4; ++q) {
+        const int px = bx + vc, py = by + 4 * vr + q;
+        if (px >= pw || py >= ph) continue;
+        const uint32_t idx = tiled_index((uint32_t)py, (uint32_t)px, tw);
+        float lv = (!assign && loss) ? loss[idx] : 0.f;
+        float gv = (!assign && grad) ? grad[idx] : 0.f;
+        if (s_l1 != 0.f) {
+            const float d = saturate(pred[idx]) - target[idx];
+            lv = __builtin_fmaf(__builtin_fabsf(d), s_l1, lv);
+            gv = __builtin_fmaf(__builtin_copysignf(1.0f, d), s_l1, gv);
         }
-        __syncthreads();
-        // vertical: column vc, output rows 4 vr .. 4 vr + 3
-        float o[5][4];
-#pragma unroll
-        for (int v = 0; v < 5; ++v) {
-            float col[14];
-#pragma unroll
-            for (int d = 0; d < 14; ++d) col[d] = s_h[v][4 * vr + d][vc];
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                float acc = 0.f;
-#pragma unroll
-                for (int d = 0; d < 11; ++d) acc = __builtin_fmaf(col[q + d], kGauss[d], acc);
-                o[v][q] = acc;
+        if (px < (int)W && py < (int)H) {
+            const float mu1 = o[0][q], mu2 = o[2][q];
+            const float mu1_sq = mu1 * mu1, mu2_sq = mu2 * mu2;
+            const float s1 = o[1][q] - mu1_sq, s2 = o[3][q] - mu2_sq, s12 = o[4][q] - mu1 * mu2;
+            const float A = mu1_sq + mu2_sq + C1;
+            const float B = s1 + s2 + C2;
+            const float Cc = 2.0f * mu1 * mu2 + C1;
+            const float D = 2.0f * s12 + C2;
+            // one reciprocal each of A and B replaces the reference's seven divisions
+            const float iA = __builtin_amdgcn_rcpf(A), iB = __builtin_amdgcn_rcpf(B);
+            const float inv = iA * iB;
+            const float val = (Cc * D) * inv;
+            lv = __builtin_fmaf(1.0f - val, s_ssim, lv);
+            if (dm_mu) {
+                dm_mu[idx] = 2.0f * inv * (mu2 * (D - Cc) + mu1 * (Cc * D) * (iB - iA));
+                dm_s1[idx] = -(Cc * D) * inv * iB;
+                dm_s12[idx] = 2.0f * Cc * inv;
             }
         }
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const int px = bx + vc, py = by + 4 * vr + q;
-            if (px >= pw || py >= ph) continue;
-            const uint32_t idx = tiled_index((uint32_t)py, (uint32_t)px, tw) + (uint32_t)c * cs;
-            float lv = el[q];
-            float gv = eg[q];
-            if (s_l1 != 0.f) {
-                const float d = saturate(ep[q]) - et[q];
-                lv = __builtin_fmaf(__builtin_fabsf(d), s_l1, lv);
-                gv = __builtin_fmaf(__builtin_copysignf(1.0f, d), s_l1, gv);
-            }
-            if (px < (int)W && py < (int)H) {
-                const float mu1 = o[0][q], mu2 = o[2][q];
-                const float mu1_sq = mu1 * mu1, mu2_sq = mu2 * mu2;
-                const float s1 = o[1][q] - mu1_sq, s2 = o[3][q] - mu2_sq, s12 = o[4][q] - mu1 * mu2;
-                const float A = mu1_sq + mu2_sq + C1;
-                const float B = s1 + s2 + C2;
-                const float Cc = 2.0f * mu1 * mu2 + C1;
-                const float D = 2.0f * s12 + C2;
-                // one reciprocal each of A and B replaces the reference's seven divisions
-                const float iA = __builtin_amdgcn_rcpf(A), iB = __builtin_amdgcn_rcpf(B);
-                const float inv = iA * iB;
-                const float val = (Cc * D) * inv;
-                lv = __builtin_fmaf(1.0f - val, s_ssim, lv);
-                if (dm_mu) {
-                    dm_mu[idx] = 2.0f * inv * (mu2 * (D - Cc) + mu1 * (Cc * D) * (iB - iA));
-                    dm_s1[idx] = -(Cc * D) * inv * iB;
-                    dm_s12[idx] = 2.0f * Cc * inv;
-                }
-            }
-            if (loss) loss[idx] = lv;
-            if (grad && (assign || s_l1 != 0.f)) grad[idx] = gv;
-        }
-        __syncthreads();
+        if (loss) loss[idx] = lv;
+        if (grad && (assign || s_l1 != 0.f)) grad[idx] = gv;
     }
 }
 
 // SSIM backward: grad += -s (dm_mu * w + 2 p (dm_s1 * w) + t (dm_s12 * w))
-// with * the 11x11 separable convolution (fused_ssim.cu:366-438).
+// with * the 11x11 separable convolution (fused_ssim.cu:366-438). One
+// workgroup per (32x32 tile, channel).
 __global__ void __launch_bounds__(256) ssim_backward_kernel(uint32_t W, uint32_t H, float s,
                                                             const float* __restrict__ pred,
                                                             const float* __restrict__ target,
@@ -254,81 +256,84 @@ __global__ void __launch_bounds__(256) ssim_backward_kernel(uint32_t W, uint32_t
     __shared__ float s_d[3][kIT][kIT];
     __shared__ float s_h[3][kIT][kOT + 1];
     const int t = (int)threadIdx.x;
-    const int bx = (int)blockIdx.x * kOT, by = (int)blockIdx.y * kOT;
+    uint32_t tx, ty, ch;
+    ssim_tile_of(tx, ty, ch);
+    const int bx = (int)tx * kOT, by = (int)ty * kOT;
     const uint32_t tw = (W + 7u) >> 3, th = (H + 7u) >> 3;
     const uint32_t cs = tw * th * 64u;
-    const int vc = t & 31, vr = t >> 5;
-    float av[kHaloRounds], bv[kHaloRounds], dv[kHaloRounds];
-    halo_load2(dm_mu, dm_s1, bx, by, W, H, tw, av, bv);
-    halo_load1(dm_s12, bx, by, W, H, tw, dv);
-    for (int c = 0; c < 3; ++c) {
+    const size_t co = (size_t)ch * cs;
+    {
+        const int lane = t & 63;
+        const float* __restrict__ m0 = dm_mu + co;
+        const float* __restrict__ m1 = dm_s1 + co;
+        const float* __restrict__ m2 = dm_s12 + co;
+        float av[kHaloRounds], bv[kHaloRounds], dv[kHaloRounds];
 #pragma unroll
         for (int r = 0; r < kHaloRounds; ++r) {
-            uint32_t q;
-            int lx, ly;
-            halo_cell(r, bx, by, W, H, tw, q, lx, ly);
-            if (lx >= 0) {
+            const HaloRound h = halo_round(r, bx, by, W, H, tw, th);
+            const float* __restrict__ p0 = m0 + h.base;   // wave-uniform block base
+            const float* __restrict__ p1 = m1 + h.base;
+            const float* __restrict__ p2 = m2 + h.base;
+            const float x = p0[lane], y = p1[lane], z = p2[lane];
+            av[r] = h.in ? x : 0.f;
+            bv[r] = h.in ? y : 0.f;
+            dv[r] = h.in ? z : 0.f;
+        }
+#pragma unroll
+        for (int r = 0; r < kHaloRounds; ++r) {
+            const HaloRound h = halo_round(r, bx, by, W, H, tw, th);
+            // the 42x42 region starts 3 pixels into the 6x6 blocks
+            const int lx = h.cx * 8 + (lane & 7) - 3, ly = h.cy * 8 + (lane >> 3) - 3;
+            if ((unsigned)lx < (unsigned)kIT && (unsigned)ly < (unsigned)kIT) {
                 s_d[0][ly][lx] = av[r];
                 s_d[1][ly][lx] = bv[r];
                 s_d[2][ly][lx] = dv[r];
             }
         }
-        float ep[4], et[4], eg[4];
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const int px = bx + vc, py = by + 4 * vr + q;
-            const bool ok = px < (int)W && py < (int)H;
-            const uint32_t idx = ok ? tiled_index((uint32_t)py, (uint32_t)px, tw) + (uint32_t)c * cs : 0u;
-            ep[q] = pred[idx];
-            et[q] = target[idx];
-            eg[q] = grad[idx];
-        }
-        __syncthreads();
-        if (c < 2) {
-            const size_t o = (size_t)(c + 1) * cs;
-            halo_load2(dm_mu + o, dm_s1 + o, bx, by, W, H, tw, av, bv);
-            halo_load1(dm_s12 + o, bx, by, W, H, tw, dv);
-        }
-        for (int wi = t; wi < kIT * 8; wi += 256) {
-            const int r = wi >> 3, g = wi & 7;
-#pragma unroll
-            for (int v = 0; v < 3; ++v) {
-                float x[14];
-#pragma unroll
-                for (int d = 0; d < 14; ++d) x[d] = s_d[v][r][4 * g + d];
-#pragma unroll
-                for (int o = 0; o < 4; ++o) {
-                    float acc = 0.f;
-#pragma unroll
-                    for (int d = 0; d < 11; ++d) acc = __builtin_fmaf(x[o + d], kGauss[d], acc);
-                    s_h[v][r][4 * g + o] = acc;
-                }
-            }
-        }
-        __syncthreads();
-        float o[3][4];
+    }
+    __syncthreads();
+    for (int wi = t; wi < kIT * 8; wi += 256) {
+        const int r = wi >> 3, g = wi & 7;
 #pragma unroll
         for (int v = 0; v < 3; ++v) {
-            float col[14];
+            float x[14];
 #pragma unroll
-            for (int d = 0; d < 14; ++d) col[d] = s_h[v][4 * vr + d][vc];
+            for (int d = 0; d < 14; ++d) x[d] = s_d[v][r][4 * g + d];
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
+            for (int o = 0; o < 4; ++o) {
                 float acc = 0.f;
 #pragma unroll
-                for (int d = 0; d < 11; ++d) acc = __builtin_fmaf(col[q + d], kGauss[d], acc);
-                o[v][q] = acc;
+                for (int d = 0; d < 11; ++d) acc = __builtin_fmaf(x[o + d], kGauss[d], acc);
+                s_h[v][r][4 * g + o] = acc;
             }
         }
+    }
+    __syncthreads();
+    const int vc = t & 31, vr = t >> 5;
+    float o[3][4];
+#pragma unroll
+    for (int v = 0; v < 3; ++v) {
+        float col[14];
+#pragma unroll
+        for (int d = 0; d < 14; ++d) col[d] = s_h[v][4 * vr + d][vc];
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-            const int px = bx + vc, py = by + 4 * vr + q;
-            if (px >= (int)W || py >= (int)H) continue;
-            const uint32_t idx = tiled_index((uint32_t)py, (uint32_t)px, tw) + (uint32_t)c * cs;
-            const float dl = __builtin_fmaf(et[q], o[2][q], __builtin_fmaf(2.0f * ep[q], o[1][q], o[0][q]));
-            grad[idx] = __builtin_fmaf(-s, dl, eg[q]);
+            float acc = 0.f;
+#pragma unroll
+            for (int d = 0; d < 11; ++d) acc = __builtin_fmaf(col[q + d], kGauss[d], acc);
+            o[v][q] = acc;
         }
-        __syncthreads();
+    }
+    pred += co;
+    target += co;
+    grad += co;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const int px = bx + vc, py = by + 4 * vr + q;
+        if (px >= (int)W || py >= (int)H) continue;
+        const uint32_t idx = tiled_index((uint32_t)py, (uint32_t)px, tw);
+        const float dl = __builtin_fmaf(target[idx], o[2][q], __builtin_fmaf(2.0f * pred[idx], o[1][q], o[0][q]));
+        grad[idx] = __builtin_fmaf(-s, dl, grad[idx]);
     }
 }
 
@@ -336,7 +341,7 @@ void launch_l1_ssim_forward(uint32_t width, uint32_t height, float c1, float c2,
                             bool assign, const float* pred, const float* target, float* loss, float* grad,
                             float* dm_mu, float* dm_s1, float* dm_s12, hipStream_t st) {
     if (width == 0 || height == 0) return;
-    dim3 grid((width + kOT - 1) / kOT, (height + kOT - 1) / kOT);
+    dim3 grid((width + kOT - 1) / kOT, (height + kOT - 1) / kOT, 3);
     l1_ssim_forward_kernel<<<grid, 256, 0, st>>>(width, height, c1, c2, s_ssim, s_l1, assign ? 1 : 0, pred, target,
                                                  loss, grad, dm_mu, dm_s1, dm_s12);
 }
@@ -344,7 +349,7 @@ void launch_l1_ssim_forward(uint32_t width, uint32_t height, float c1, float c2,
 void launch_ssim_backward(uint32_t width, uint32_t height, float s, const float* pred, const float* target,
                           float* grad, const float* dm_mu, const float* dm_s1, const float* dm_s12, hipStream_t st) {
     if (width == 0 || height == 0) return;
-    dim3 grid((width + kOT - 1) / kOT, (height + kOT - 1) / kOT);
+    dim3 grid((width + kOT - 1) / kOT, (height + kOT - 1) / kOT, 3);
     ssim_backward_kernel<<<grid, 256, 0, st>>>(width, height, s, pred, target, grad, dm_mu, dm_s1, dm_s12);
 }
 
