@@ -54,29 +54,6 @@ __device__ __forceinline__ uint32_t block_exclusive_scan(uint32_t v, uint32_t* s
     return wave_off + incl - v;
 }
 
-// Exclusive scan of 16 striped values per thread: value r of thread t is
-// element r * 256 + t of the workgroup's chunk, so consecutive lanes hold
-// consecutive elements in every round. s_rw: 64 words of LDS.
-__device__ __forceinline__ void striped_scan16(const uint32_t v[kScanRounds], uint32_t ex[kScanRounds],
-                                               uint32_t* total, uint32_t* s_rw) {
-    const uint32_t lane = threadIdx.x & 63u, w = threadIdx.x >> 6;
-#pragma unroll
-    for (int r = 0; r < kScanRounds; ++r) {
-        const uint32_t incl = wave_inclusive_scan_u32(v[r]);
-        ex[r] = incl - v[r];
-        if (lane == 63u) s_rw[r * 4 + w] = incl;
-    }
-    __syncthreads();
-    // (round, wave) partial sums in element order; every wave scans them itself
-    const uint32_t x = s_rw[lane];
-    const uint32_t xi = wave_inclusive_scan_u32(x);
-    *total = readlane_u32(xi, 63);
-    const uint32_t xe = xi - x;
-#pragma unroll
-    for (int r = 0; r < kScanRounds; ++r) ex[r] += readlane_u32(xe, (uint32_t)(r * 4) + w);
-    __syncthreads();   // s_rw may be reused after this
-}
-
 // ---------------------------------------------------------------- decoupled look-back (single value)
 
 // status word: [63:62] flag (0 not ready, 1 aggregate, 2 inclusive prefix),
@@ -191,7 +168,7 @@ __global__ void __launch_bounds__(kThreads) compact_kernel(const uint32_t* __res
     const uint32_t wnt = wave_sum_u32(ntsum);
     if (lane == 0) s_nt[w] = wnt;
     uint32_t total;
-    striped_scan16(vis, ex, &total, s_rw);   // barriers inside: s_nt visible after it
+    striped_scan16_u32(vis, ex, &total, s_rw);   // barriers inside: s_nt visible after it
     if (w == 0) {
         const uint32_t excl = wave_look_back(status, bid, total, epoch, &ctl->err);
         if (lane == 0) {
@@ -243,7 +220,7 @@ __global__ void __launch_bounds__(kThreads) offsets_kernel(const uint32_t* __res
         c[r] = i < n ? nt[i] : 0u;
     }
     uint32_t total;
-    striped_scan16(c, ex, &total, s_rw);
+    striped_scan16_u32(c, ex, &total, s_rw);
     if (w == 0) {
         const uint32_t excl = wave_look_back(status, bid, total, epoch, &ctl->err);
         if (lane == 0) {
@@ -336,7 +313,7 @@ __global__ void __launch_bounds__(kThreads) exclusive_scan_kernel(uint32_t* __re
         c[r] = i < n ? data[i] : 0u;
     }
     uint32_t total;
-    striped_scan16(c, ex, &total, s_rw);
+    striped_scan16_u32(c, ex, &total, s_rw);
     if (w == 0) {
         const uint32_t excl = wave_look_back(status, bid, total, epoch, err);
         if (lane == 0) s_base = excl;

@@ -35,7 +35,7 @@
 // colour >= 0), [10] sum of alpha * dL/dalpha (times (1 - opacity) later).
 // The record index comes from one counter atomic per (primitive, bucket) into
 // the instance slots binning reserved for the primitive; the per-primitive
-// sums are formed by gather_heavy / the preprocess backward.
+// sums are formed by the preprocess backward.
 #include "common.h"
 #include "kernels.h"
 
@@ -58,7 +58,7 @@ __global__ void __launch_bounds__(256) blend_backward_kernel(
     const float4* __restrict__ conic_opacity, const float4* __restrict__ color_pt, const float* __restrict__ image,
     const float* __restrict__ grad_image, const uint32_t* __restrict__ n_contrib, const float4* __restrict__ ckpt,
     const uint4* __restrict__ items, BinCtl* __restrict__ ctl, uint32_t* __restrict__ rec_count,
-    const uint32_t* __restrict__ first_slot, float4* __restrict__ records, uint32_t* __restrict__ heavy) {
+    const uint32_t* __restrict__ first_slot, float4* __restrict__ records) {
     __shared__ float4 s_rec[4][3][kBucket];
     __shared__ float s_part[4][kBwdVals + 1][kBucket + 1];   // +1: the four row writers hit four banks
 
@@ -228,7 +228,6 @@ __global__ void __launch_bounds__(256) blend_backward_kernel(
             dst[0] = make_float4(-gmx, -gmy, val(9), val(10));
             dst[1] = make_float4(-0.5f * val(4), -0.5f * val(5), -0.5f * val(6), (mask & 1u) ? val(0) : 0.f);
             dst[2] = make_float4((mask & 2u) ? val(1) : 0.f, (mask & 4u) ? val(2) : 0.f, val(3), 0.f);
-            if (sub == kLightRecords) heavy[atomicAdd(&ctl->heavy_n, 1u)] = p;
         }
         next = (uint32_t)__builtin_amdgcn_readfirstlane((int)after);
         wave_lds_sync();
@@ -241,7 +240,7 @@ void launch_blend_backward(const CamParams& cam, const uint32_t* inst_vals, cons
                            const float4* conic_opacity, const float4* color_pt, const float* image,
                            const float* grad_image, const uint32_t* n_contrib, const float4* ckpt,
                            const uint4* items, BinCtl* ctl, uint32_t* rec_count, const uint32_t* first_slot,
-                           float4* records, uint32_t* heavy, bool with_abs, hipStream_t s) {
+                           float4* records, bool with_abs, hipStream_t s) {
     const uint32_t n_tiles = cam.grid_w * cam.grid_h;
     if (n_tiles == 0) return;
     if (g_blocks <= 0) {
@@ -259,54 +258,11 @@ void launch_blend_backward(const CamParams& cam, const uint32_t* inst_vals, cons
     if (with_abs)
         blend_backward_kernel<true><<<(uint32_t)g_blocks, 256, 0, s>>>(cam, inst_vals, mean2d, conic_opacity,
                                                                        color_pt, image, grad_image, n_contrib, ckpt,
-                                                                       items, ctl, rec_count, first_slot, records,
-                                                                       heavy);
+                                                                       items, ctl, rec_count, first_slot, records);
     else
         blend_backward_kernel<false><<<(uint32_t)g_blocks, 256, 0, s>>>(cam, inst_vals, mean2d, conic_opacity,
                                                                         color_pt, image, grad_image, n_contrib, ckpt,
-                                                                        items, ctl, rec_count, first_slot, records,
-                                                                        heavy);
-}
-
-// Sums the 2D-gradient records of each listed primitive (more than
-// kLightRecords of them) into grad2d[12 p]: one wave per primitive, lanes
-// over records, then the transposed wave reduction.
-__global__ void __launch_bounds__(256) gather_heavy_kernel(const uint32_t* __restrict__ heavy,
-                                                           const BinCtl* __restrict__ ctl,
-                                                           const uint32_t* __restrict__ rec_count,
-                                                           const uint32_t* __restrict__ first_slot,
-                                                           const float4* __restrict__ records,
-                                                           float* __restrict__ grad2d) {
-    const uint32_t w = threadIdx.x >> 6, lane = threadIdx.x & 63u;
-    const uint32_t nh = ctl->heavy_n;
-    const int q0 = row_value(lane >> 4);
-    for (uint32_t h = blockIdx.x * 4u + w; h < nh; h += gridDim.x * 4u) {
-        const uint32_t p = heavy[h];
-        const uint32_t c = rec_count[p], base = first_slot[p];
-        float v[12];
-#pragma unroll
-        for (int q = 0; q < 12; ++q) v[q] = 0.f;
-        for (uint32_t r = lane; r < c; r += 64u) {
-            const float4* src = records + 3 * (size_t)(base + r);
-            const float4 a = src[0], b = src[1], d = src[2];
-            v[0] += a.x; v[1] += a.y; v[2] += a.z; v[3] += a.w;
-            v[4] += b.x; v[5] += b.y; v[6] += b.z; v[7] += b.w;
-            v[8] += d.x; v[9] += d.y; v[10] += d.z; v[11] += d.w;
-        }
-        float t[3];
-        wave_reduce12(v, t);
-        if ((lane & 15u) == 0u) {
-            float* g = grad2d + (size_t)p * kGradStride;
-            g[q0] = t[0];
-            g[4 + q0] = t[1];
-            g[8 + q0] = t[2];
-        }
-    }
-}
-
-void launch_gather_heavy(const uint32_t* heavy, const BinCtl* ctl, const uint32_t* rec_count,
-                         const uint32_t* first_slot, const float4* records, float* grad2d, hipStream_t s) {
-    gather_heavy_kernel<<<512, 256, 0, s>>>(heavy, ctl, rec_count, first_slot, records, grad2d);
+                                                                        items, ctl, rec_count, first_slot, records);
 }
 
 }  // namespace tgs

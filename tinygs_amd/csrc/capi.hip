@@ -225,7 +225,8 @@ struct tgs_rasterizer {
     // backward 2D-gradient records: per primitive first instance slot, record
     // count (kept zero between backwards), records (3 float4 per instance
     // slot), heavy-gather list
-    DevBuf first_slot, rec_count, records, heavy;
+    DevBuf first_slot, rec_count, records;
+    DevBuf live, heavy, chunk_counts;   // preprocess backward: per-chunk lists of primitives with records
     DevBuf row_mask;     // per-primitive byte mask of the last sparse backward
     bool row_mask_valid = false;
     // temp
@@ -312,7 +313,8 @@ int tgs_rasterizer_destroy(tgs_rasterizer* r) {
                      &r->radix_counts, &r->ikeys[0],
                      &r->ikeys[1], &r->ivals[0], &r->ivals[1], &r->ranges, &r->tile_max, &r->n_contrib,
                      &r->ckpt, &r->items, &r->tile_loaded, &r->first_slot,
-                     &r->rec_count, &r->records, &r->heavy, &r->row_mask, &r->grad2d, &r->bin_ctl, &r->lb_status};
+                     &r->rec_count, &r->records, &r->heavy, &r->live, &r->chunk_counts, &r->row_mask, &r->grad2d,
+                     &r->bin_ctl, &r->lb_status};
     for (DevBuf* b : all) release(*b);
     if (r->h_counters) (void)hipHostFree(r->h_counters);
     if (r->ev_counts) (void)hipEventDestroy(r->ev_counts);
@@ -492,6 +494,8 @@ int tgs_rasterizer_backward_ex(tgs_rasterizer* r, const void* grad_image, const 
     const int64_t n = r->n;
     TGS_TRY(ensure(r->grad2d, sizeof(float) * kGradStride * (size_t)(n > 0 ? n : 1), s));
     TGS_TRY(ensure(r->heavy, sizeof(uint32_t) * (size_t)(n > 0 ? n : 1), s));
+    TGS_TRY(ensure(r->live, sizeof(uint4) * (size_t)(n > 0 ? n : 1), s));
+    TGS_TRY(ensure(r->chunk_counts, sizeof(uint2) * (size_t)std::max<int64_t>(pb_chunks(n), 1), s));
     if (flags & ~(TGS_BACKWARD_ASSIGN | TGS_BACKWARD_SPARSE))
         return fail(TGS_ERR_INVALID, "unknown backward flags 0x%x", flags);
     if ((flags & TGS_BACKWARD_ASSIGN) && (flags & TGS_BACKWARD_SPARSE))
@@ -501,15 +505,15 @@ int tgs_rasterizer_backward_ex(tgs_rasterizer* r, const void* grad_image, const 
     r->row_mask_valid = false;
     const CamParams& cam = r->cam;
     BinCtl* ctl = r->bin_ctl.as<BinCtl>();
-    if (!r->bwd_queues_clear)   // a second backward after one forward: clear the queue / heavy counters again
-        launch_fill_u32(&ctl->heavy_n, 0u, kBwdCtlWords, s);
+    if (!r->bwd_queues_clear)   // a second backward after one forward: clear the queue counters again
+        launch_fill_u32(ctl->bwd_queue, 0u, kBwdCtlWords, s);
     {
         StageScope sc(ST_BLENDB, s);
         launch_blend_backward(cam, r->ivals[r->isel].as<uint32_t>(), r->mean2d.as<float2>(),
                               r->conic_opacity.as<float4>(), r->color.as<float4>(), (const float*)image,
                               (const float*)grad_image, r->n_contrib.as<uint32_t>(), r->ckpt.as<float4>(),
                               r->items.as<uint4>(), ctl, r->rec_count.as<uint32_t>(), r->first_slot.as<uint32_t>(),
-                              r->records.as<float4>(), r->heavy.as<uint32_t>(), densification_info != nullptr, s);
+                              r->records.as<float4>(), densification_info != nullptr, s);
     }
     r->bwd_queues_clear = false;
     TGS_CHECK_LAUNCH();
@@ -517,12 +521,11 @@ int tgs_rasterizer_backward_ex(tgs_rasterizer* r, const void* grad_image, const 
                 (float*)grads->sh0, (float*)grads->sh_rest};
     {
         StageScope sc(ST_PREB, s);
-        launch_gather_heavy(r->heavy.as<uint32_t>(), ctl, r->rec_count.as<uint32_t>(), r->first_slot.as<uint32_t>(),
-                            r->records.as<float4>(), r->grad2d.as<float>(), s);
         launch_preprocess_backward(view_of(r->g), cam, r->n_touched.as<uint32_t>(), r->conic_opacity.as<float4>(),
                                    r->rec_count.as<uint32_t>(), r->first_slot.as<uint32_t>(), r->records.as<float4>(),
                                    r->grad2d.as<float>(), gv, (float*)densification_info, mode,
-                                   r->row_mask.as<uint8_t>(), s);
+                                   r->row_mask.as<uint8_t>(), r->live.as<uint4>(), r->heavy.as<uint32_t>(),
+                                   r->chunk_counts.as<uint2>(), s);
     }
     TGS_CHECK_LAUNCH();
     r->row_mask_valid = mode == kGradSparse;

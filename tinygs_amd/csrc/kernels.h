@@ -1,6 +1,8 @@
 // Host-side launchers of the HIP kernels (internal C++ interface of the library).
 #pragma once
 
+#include <cstddef>
+
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -50,12 +52,12 @@ struct BinCtl {
     uint32_t V, I, err, pad;
     uint32_t tickets[kTicketCount];
     uint32_t n_items;                     // backward work items listed by the blend forward
-    uint32_t pad2[18];
-    uint32_t heavy_n;                     // primitives on the backward's heavy-gather list
+    uint32_t pad2[19];
     uint32_t bwd_queue[kBwdQueues * 32];  // next local index of queue q at [32 q] (one line each, from byte 128)
 };
-// Words from heavy_n to the end of bwd_queue: what a backward needs cleared.
-constexpr int kBwdCtlWords = 1 + kBwdQueues * 32;
+static_assert(offsetof(BinCtl, bwd_queue) == 128, "backward queue counters start on their own cache line");
+// Words of bwd_queue: what a backward needs cleared.
+constexpr int kBwdCtlWords = kBwdQueues * 32;
 // Clears every BinCtl word except err.
 void launch_bin_ctl_reset(BinCtl* ctl, hipStream_t s);
 constexpr uint32_t kEpochMask = 0x3fffffffu;   // 30-bit launch epoch of look-back status words
@@ -108,29 +110,28 @@ void launch_blend_forward(const CamParams& cam, const uint2* ranges, const uint3
 // first_slot[p] + n_touched[p]: a primitive is in a tile's list once) and
 // writes 12 floats there: dL/dmean2d (2), |.| sums (2; 0 unless with_abs:
 // only densification reads them), dL/dconic (3),
-// dL/dcolour (3), sum of alpha dL/dalpha, 0. Primitives reaching
-// kLightRecords + 1 records are listed in `heavy` (count ctl->heavy_n);
-// gather_heavy sums their records into grad2d[12 p]; the preprocess backward
-// sums the others itself and clears rec_count.
+// dL/dcolour (3), sum of alpha dL/dalpha, 0. The preprocess backward sums
+// each primitive's records (a wave per primitive above kLightRecords of
+// them, into grad2d[12 p]) and clears rec_count.
 constexpr uint32_t kLightRecords = 4;
-// ctl->heavy_n and ctl->bwd_queue must be zero on entry (the forward's control
-// reset clears them).
+// ctl->bwd_queue must be zero on entry (the forward's control reset clears it).
 void launch_blend_backward(const CamParams& cam, const uint32_t* inst_vals, const float2* mean2d,
                            const float4* conic_opacity, const float4* color_pt, const float* image,
                            const float* grad_image, const uint32_t* n_contrib, const float4* ckpt,
                            const uint4* items, BinCtl* ctl, uint32_t* rec_count, const uint32_t* first_slot,
-                           float4* records, uint32_t* heavy, bool with_abs, hipStream_t s);
-void launch_gather_heavy(const uint32_t* heavy, const BinCtl* ctl, const uint32_t* rec_count,
-                         const uint32_t* first_slot, const float4* records, float* grad2d, hipStream_t s);
+                           float4* records, bool with_abs, hipStream_t s);
 
 // ---- preprocess backward (kernels_backward.cuh:88-352)
 // mode: 0 accumulate, 1 assign, 2 sparse (assign rows with gradient, write
 // row_mask[i] = 1 for them and 0 for the others, leave the others untouched).
 enum { kGradAccumulate = 0, kGradAssign = 1, kGradSparse = 2 };
+// Scratch: live (n uint4) and heavy (n u32) lists of the primitives with
+// records, chunk_counts (pb_chunks(n) uint2), grad2d (12 n floats).
+int64_t pb_chunks(int64_t n);
 void launch_preprocess_backward(const GaussianView& g, const CamParams& cam, const uint32_t* n_touched,
                                 const float4* conic_opacity, uint32_t* rec_count, const uint32_t* first_slot,
-                                const float4* records, const float* grad2d, const GradView& out, float* densif,
-                                int mode, uint8_t* row_mask, hipStream_t s);
+                                const float4* records, float* grad2d, const GradView& out, float* densif, int mode,
+                                uint8_t* row_mask, uint4* live, uint32_t* heavy, uint2* chunk_counts, hipStream_t s);
 
 // ---- utilities
 void launch_fill_u32(uint32_t* p, uint32_t value, int64_t n, hipStream_t s);

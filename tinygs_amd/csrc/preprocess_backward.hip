@@ -29,14 +29,15 @@ struct PrimGrad {
 
 // Per-primitive part: everything except the SH-rest gradient write, which the
 // block performs cooperatively from k[] (basis values) and gc[] (dL/dcolour).
-template <typename ShT>
+// The primitive's parameters come in registers: mean pm, log-scale ps,
+// quaternion pq, SH-rest coefficients shr (45, used up to the active
+// bases) and opacity.
 __device__ __forceinline__ void preprocess_backward_one(
-    int64_t i, const float* __restrict__ means, const float* __restrict__ scales, const float* __restrict__ rots,
-    const ShT* shr, int bases, const CamParams& cam, const float4* __restrict__ conic_opacity, const float4 gA,
-    const float4 gB, const float4 gC, float4* __restrict__ densif, PrimGrad& out, float gc_out[3], float k[15],
-    int& nb_out) {
+    int64_t i, const float pm[3], const float ps[3], const float pq[4], const float shr[45], float opacity,
+    int bases, const CamParams& cam, const float4 gA, const float4 gB, const float4 gC,
+    float4* __restrict__ densif, PrimGrad& out, float gc_out[3], float k[15], int& nb_out) {
     // gA: dmx, dmy, absx, absy; gB: dca, dcb, dcc, dr; gC: dg, db, alpha partial, -
-    const float mx = means[3 * i], my = means[3 * i + 1], mz = means[3 * i + 2];
+    const float mx = pm[0], my = pm[1], mz = pm[2];
 
     // ---- SH backward (kernels_backward.cuh:22-86)
     const float gc[3] = {gB.w, gC.x, gC.y};
@@ -54,9 +55,9 @@ __device__ __forceinline__ void preprocess_backward_one(
         k[2] = -0.48860251190291987f * x;
         int nb = 3;
         for (int c = 0; c < 3; ++c) {
-            gdx[c] = -0.48860251190291987f * load_as_float(shr, 3 * 2 + c);
-            gdy[c] = -0.48860251190291987f * load_as_float(shr, 3 * 0 + c);
-            gdz[c] = 0.48860251190291987f * load_as_float(shr, 3 * 1 + c);
+            gdx[c] = -0.48860251190291987f * shr[3 * 2 + c];
+            gdy[c] = -0.48860251190291987f * shr[3 * 0 + c];
+            gdz[c] = 0.48860251190291987f * shr[3 * 1 + c];
         }
         if (bases > 4) {
             const float xx = x * x, yy = y * y, zz = z * z;
@@ -71,9 +72,9 @@ __device__ __forceinline__ void preprocess_backward_one(
             const float f7y = (float)(-1.0925484305920792 * (double)y);
             const float f5z = (float)(1.8923493915151202 * (double)z);
             for (int c = 0; c < 3; ++c) {
-                const float s3 = load_as_float(shr, 9 + c), s4 = load_as_float(shr, 12 + c);
-                const float s5 = load_as_float(shr, 15 + c), s6 = load_as_float(shr, 18 + c);
-                const float s7 = load_as_float(shr, 21 + c);
+                const float s3 = shr[9 + c], s4 = shr[12 + c];
+                const float s5 = shr[15 + c], s6 = shr[18 + c];
+                const float s7 = shr[21 + c];
                 gdx[c] = gdx[c] + (1.0925484305920792f * y) * s3 + (-1.0925484305920792f * z) * s6 + f7x * s7;
                 gdy[c] = gdy[c] + (1.0925484305920792f * x) * s3 + (-1.0925484305920792f * z) * s4 + f7y * s7;
                 gdz[c] = gdz[c] + (-1.0925484305920792f * y) * s4 + f5z * s5 + (-1.0925484305920792f * x) * s6;
@@ -88,10 +89,10 @@ __device__ __forceinline__ void preprocess_backward_one(
                 k[14] = 0.59004358992664352f * x * (-xx + 3.0f * yy);
                 nb = 15;
                 for (int c = 0; c < 3; ++c) {
-                    const float s8 = load_as_float(shr, 24 + c), s9 = load_as_float(shr, 27 + c);
-                    const float s10 = load_as_float(shr, 30 + c), s11 = load_as_float(shr, 33 + c);
-                    const float s12 = load_as_float(shr, 36 + c), s13 = load_as_float(shr, 39 + c);
-                    const float s14 = load_as_float(shr, 42 + c);
+                    const float s8 = shr[24 + c], s9 = shr[27 + c];
+                    const float s10 = shr[30 + c], s11 = shr[33 + c];
+                    const float s12 = shr[36 + c], s13 = shr[39 + c];
+                    const float s14 = shr[42 + c];
                     gdx[c] = gdx[c] + (-3.5402615395598609f * xy) * s8 + (2.8906114426405538f * yz) * s9 +
                              (0.45704579946446572f - 2.2852289973223288f * zz) * s12 +
                              (2.8906114426405538f * xz) * s13 +
@@ -127,9 +128,9 @@ __device__ __forceinline__ void preprocess_backward_one(
     const float depth = r3[0] * mx + r3[1] * my + r3[2] * mz + r3[3];
     const float x = (r1[0] * mx + r1[1] * my + r1[2] * mz + r1[3]) / depth;
     const float y = (r2[0] * mx + r2[1] * my + r2[2] * mz + r2[3]) / depth;
-    const float e0 = det_expf(scales[3 * i]), e1 = det_expf(scales[3 * i + 1]), e2 = det_expf(scales[3 * i + 2]);
+    const float e0 = det_expf(ps[0]), e1 = det_expf(ps[1]), e2 = det_expf(ps[2]);
     const float vx = e0 * e0, vy = e1 * e1, vz = e2 * e2;
-    const float qr = rots[4 * i], qx = rots[4 * i + 1], qy = rots[4 * i + 2], qz = rots[4 * i + 3];
+    const float qr = pq[0], qx = pq[1], qy = pq[2], qz = pq[3];
     const float qrr = qr * qr, qxx_r = qx * qx, qyy_r = qy * qy, qzz_r = qz * qz;
     const float qn = qrr + qxx_r + qyy_r + qzz_r;
     const float qxx = 2.0f * qxx_r / qn, qyy = 2.0f * qyy_r / qn, qzz = 2.0f * qzz_r / qn;
@@ -231,7 +232,7 @@ __device__ __forceinline__ void preprocess_backward_one(
     out.r[1] = (2.0f * (2.0f * qx * gqxx + qy * gqxy + qz * gqxz + qr * gqrx - qx * hlp) / den);
     out.r[2] = (2.0f * (2.0f * qy * gqyy + qx * gqxy + qz * gqyz + qr * gqry - qy * hlp) / den);
     out.r[3] = (2.0f * (2.0f * qz * gqzz + qx * gqxz + qy * gqyz + qr * gqrz - qz * hlp) / den);
-    out.o = (gC.z * (1.0f - conic_opacity[i].w));
+    out.o = (gC.z * (1.0f - opacity));
     if (densif) {
         float4 d = densif[i];
         d.x += 1.0f;
@@ -243,73 +244,185 @@ __device__ __forceinline__ void preprocess_backward_one(
     }
 }
 
-// Writes n floats from LDS to global memory with 16-byte stores (the global
-// run starts 16-byte aligned), scalar stores for the tail.
-__device__ __forceinline__ void block_store(float* __restrict__ dst, const float* src, int n) {
-    const int nv = n >> 2;
-    for (int v = (int)threadIdx.x; v < nv; v += 256) ((float4*)dst)[v] = ((const float4*)src)[v];
-    for (int e = (nv << 2) + (int)threadIdx.x; e < n; e += 256) dst[e] = src[e];
+// ---- phase 1: classify every primitive, list the live ones
+//
+// Chunk of 2048 consecutive primitives per workgroup (8 striped rounds of
+// 256). A primitive is live when some bucket of the blend backward left a
+// record for it (the counters of all others are zero). Dead visible
+// primitives only count for densification (kernels_backward.cuh:345 adds
+// zero sums); sparse mode records the row mask; assign mode zeroes every
+// gradient row of the chunk (the live rows are overwritten by phase 3).
+// The chunk's live primitives, as (index, record count, first record slot),
+// and its heavy ones (more than kLightRecords records) are listed in the
+// chunk's own slice of the two lists, with the two counts in chunk_counts:
+// no device-wide counter (returning atomics on one address serialise, about
+// 10 ns each on MI355X).
+constexpr int kClassRounds = 8;
+constexpr int kClassChunk = 256 * kClassRounds;
+
+int64_t pb_chunks(int64_t n) { return n > 0 ? (n + kClassChunk - 1) / kClassChunk : 0; }
+
+__device__ __forceinline__ void zero_run(float* __restrict__ dst, int64_t n) {
+    // 16-byte stores when the run is 16-byte aligned (the chunk starts at a
+    // multiple of 2048 rows, so it is whenever the array is)
+    const int64_t nv = ((uintptr_t)dst & 15u) ? 0 : n >> 2;
+    for (int64_t v = threadIdx.x; v < nv; v += 256) ((float4*)dst)[v] = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int64_t e = (nv << 2) + threadIdx.x; e < n; e += 256) dst[e] = 0.f;
+}
+
+__global__ void __launch_bounds__(256) preprocess_backward_classify_kernel(
+    int64_t n, const uint32_t* __restrict__ n_touched, const uint32_t* __restrict__ rec_count,
+    const uint32_t* __restrict__ first_slot, float4* __restrict__ densif, int mode, uint8_t* __restrict__ row_mask,
+    GradView out, uint4* __restrict__ live, uint32_t* __restrict__ heavy, uint2* __restrict__ chunk_counts) {
+    __shared__ uint32_t s_rw[4 * kClassRounds];
+    const uint32_t t = threadIdx.x;
+    const int64_t c0 = (int64_t)blockIdx.x * kClassChunk;
+    const int64_t base = c0 + t;
+    uint32_t nrec[kClassRounds], lv[kClassRounds], hv[kClassRounds], ex[kClassRounds], exh[kClassRounds];
+#pragma unroll
+    for (int r = 0; r < kClassRounds; ++r) {
+        const int64_t i = base + (int64_t)r * 256;
+        nrec[r] = i < n ? rec_count[i] : 0u;
+        lv[r] = nrec[r] ? 1u : 0u;
+        hv[r] = nrec[r] > kLightRecords ? 1u : 0u;
+    }
+    if (densif) {
+#pragma unroll
+        for (int r = 0; r < kClassRounds; ++r) {
+            const int64_t i = base + (int64_t)r * 256;
+            if (i < n && !nrec[r] && n_touched[i] != 0u) densif[i].x += 1.0f;
+        }
+    }
+    if (mode == kGradSparse) {
+#pragma unroll
+        for (int r = 0; r < kClassRounds; ++r) {
+            const int64_t i = base + (int64_t)r * 256;
+            if (i < n) row_mask[i] = (uint8_t)lv[r];
+        }
+    }
+    if (mode == kGradAssign) {
+        const int64_t rows = min((int64_t)kClassChunk, n - c0);
+        zero_run(out.means + 3 * c0, 3 * rows);
+        zero_run(out.scales + 3 * c0, 3 * rows);
+        zero_run(out.rotations + 4 * c0, 4 * rows);
+        zero_run(out.opacities + c0, rows);
+        zero_run(out.sh0 + 3 * c0, 3 * rows);
+        zero_run(out.sh_rest + 45 * c0, 45 * rows);
+    }
+    uint32_t n_live, n_heavy;
+    striped_scan_u32<kClassRounds>(lv, ex, &n_live, s_rw);
+    striped_scan_u32<kClassRounds>(hv, exh, &n_heavy, s_rw);
+    if (t == 0) chunk_counts[blockIdx.x] = make_uint2(n_live, n_heavy);
+#pragma unroll
+    for (int r = 0; r < kClassRounds; ++r) {
+        const uint32_t i = (uint32_t)(base + (int64_t)r * 256);
+        if (lv[r]) live[c0 + ex[r]] = make_uint4(i, nrec[r], first_slot[i], 0u);
+        if (hv[r]) heavy[c0 + exh[r]] = i;
+    }
+}
+
+// ---- phase 2: 2D-gradient sums of the heavy primitives
+//
+// A wave per heavy primitive of the chunk, lanes over its records, then the
+// transposed wave reduction; the sums go to grad2d[12 p] in record layout.
+__global__ void __launch_bounds__(256) gather_heavy_kernel(const uint32_t* __restrict__ heavy,
+                                                           const uint2* __restrict__ chunk_counts,
+                                                           const uint32_t* __restrict__ rec_count,
+                                                           const uint32_t* __restrict__ first_slot,
+                                                           const float4* __restrict__ records,
+                                                           float* __restrict__ grad2d) {
+    const uint32_t w = threadIdx.x >> 6, lane = threadIdx.x & 63u;
+    const uint32_t nh = chunk_counts[blockIdx.x].y;
+    const int q0 = row_value(lane >> 4);
+    const uint32_t* list = heavy + (size_t)blockIdx.x * kClassChunk;
+    for (uint32_t h = w; h < nh; h += 4u) {
+        const uint32_t p = list[h];
+        const uint32_t c = rec_count[p], base = first_slot[p];
+        float v[12];
+#pragma unroll
+        for (int q = 0; q < 12; ++q) v[q] = 0.f;
+        for (uint32_t r = lane; r < c; r += 64u) {
+            const float4* src = records + 3 * (size_t)(base + r);
+            const float4 a = src[0], b = src[1], d = src[2];
+            v[0] += a.x; v[1] += a.y; v[2] += a.z; v[3] += a.w;
+            v[4] += b.x; v[5] += b.y; v[6] += b.z; v[7] += b.w;
+            v[8] += d.x; v[9] += d.y; v[10] += d.z; v[11] += d.w;
+        }
+        float t[3];
+        wave_reduce12(v, t);
+        if ((lane & 15u) == 0u) {
+            float* g = grad2d + (size_t)p * kGradStride;
+            g[q0] = t[0];
+            g[4 + q0] = t[1];
+            g[8 + q0] = t[2];
+        }
+    }
+}
+
+// ---- phase 3: the gradient chain, one thread per live primitive of the chunk
+//
+// Light primitives sum their (at most kLightRecords) records here, heavy ones
+// read grad2d. The record counter is cleared for the next backward. Rows are
+// scattered (live primitives are sparse), so every row access is one request
+// per lane: the 90-byte fp16 SH-rest row is read as 8-byte pieces of its
+// 8-byte-aligned window, realigned through the thread's LDS slot, and the
+// 180-byte SH-rest gradient row is written as 8-byte pairs (which pairs
+// depends on the row's 8-byte phase). Assign / sparse store the rows,
+// accumulate adds to them; the SH-rest gradient row gets k_b * dL/dcolour_c
+// for the active bases b (kernels_backward.cuh:41-65) and, when stored,
+// zero for the others.
+constexpr int kShWin = 13;   // 8-byte words per LDS slot (an odd word stride)
+
+template <typename ShT>
+__device__ __forceinline__ void load_sh_row(const ShT* __restrict__ shr_all, int64_t ip, int nsh, bool vec,
+                                            uint2* slot, float shv[45]) {
+    const ShT* sr = shr_all + 45 * ip;
+#pragma unroll
+    for (int b = 0; b < 45; ++b) shv[b] = b < nsh ? load_as_float(sr, b) : 0.f;
+}
+template <>
+__device__ __forceinline__ void load_sh_row<__half>(const __half* __restrict__ shr_all, int64_t ip, int nsh,
+                                                    bool vec, uint2* slot, float shv[45]) {
+    if (!vec) {
+        const __half* sr = shr_all + 45 * ip;
+#pragma unroll
+        for (int b = 0; b < 45; ++b) shv[b] = b < nsh ? __half2float(sr[b]) : 0.f;
+        return;
+    }
+    // row bytes [B, B + 90), window [a, a + 96) with a = B & ~7, o = B - a in {0, 2, 4, 6}:
+    // 11 whole 8-byte words lie inside the row; of the 12th, only its first o + 2 bytes do
+    const uint64_t B = 90u * (uint64_t)ip, a = B & ~7ull;
+    const uint32_t o = (uint32_t)(B - a);
+    const uint2* win = (const uint2*)((const char*)shr_all + a);
+#pragma unroll
+    for (int q = 0; q < 11; ++q) slot[q] = win[q];
+    const uint16_t* tail = (const uint16_t*)(win + 11);
+    uint16_t* stail = (uint16_t*)(slot + 11);
+#pragma unroll
+    for (uint32_t q = 0; q < 4; ++q)
+        if (2u * q <= o) stail[q] = tail[q];
+    const __half* h = (const __half*)((const char*)slot + o);
+#pragma unroll
+    for (int b = 0; b < 45; ++b) shv[b] = b < nsh ? __half2float(h[b]) : 0.f;
 }
 
 template <typename ShT>
-__global__ void __launch_bounds__(256) preprocess_backward_kernel(
+__global__ void __launch_bounds__(256) preprocess_backward_live_kernel(
     const float* __restrict__ means, const float* __restrict__ scales, const float* __restrict__ rots,
-    const ShT* __restrict__ shr_all, int64_t n, int bases, CamParams cam, const uint32_t* __restrict__ n_touched,
-    const float4* __restrict__ conic_opacity, uint32_t* __restrict__ rec_count,
-    const uint32_t* __restrict__ first_slot, const float4* __restrict__ records, const float* __restrict__ grad2d,
-    float* __restrict__ g_means, float* __restrict__ g_scales, float* __restrict__ g_rots, float* __restrict__ g_opac,
-    float* __restrict__ g_sh0, float* __restrict__ g_shr_all, float4* __restrict__ densif, int mode,
-    uint8_t* __restrict__ row_mask) {
-    // Block of 256 consecutive primitives; each gradient array's rows of the
-    // block are one contiguous run (3, 3, 3, 4, 1 and 45 floats per
-    // primitive). Phase 1 compacts the primitives with 2D-gradient records
-    // into an LDS list; phase 2 runs the gradient chain for them on
-    // consecutive threads (one wave carries a typical block's few live
-    // primitives instead of four waves idling around them); phase 3 writes
-    // the block's rows from LDS with 16-byte stores (assign mode), assigns
-    // only the live rows and writes the block's row mask (sparse mode), or
-    // read-modify-writes only what changes (accumulate mode).
-    __shared__ float s_k[256 * 15];
-    __shared__ float s_gc[256 * 3];
-    __shared__ uint32_t s_nb[256];
-    __shared__ __align__(16) float s_m[256 * 3], s_s[256 * 3], s_h[256 * 3], s_r[256 * 4], s_o[256];
-    __shared__ uint32_t s_live[256];
-    __shared__ uint32_t s_wcnt[4];
-    const int64_t blk0 = (int64_t)blockIdx.x * 256;
-    const int nblk = (int)min((int64_t)256, n - blk0);
-    const int t = (int)threadIdx.x;
-    const uint32_t lane = (uint32_t)t & 63u, w = (uint32_t)t >> 6;
-    const int64_t i = blk0 + t;
-    const bool assign = mode == kGradAssign;
-    const bool sparse = mode == kGradSparse;
-    const bool vis = t < nblk && n_touched[i] != 0;
-    const uint32_t nrec = vis ? rec_count[i] : 0u;
-    s_nb[t] = 0u;
-    if (assign) {
-        for (int c = 0; c < 3; ++c) s_m[3 * t + c] = s_s[3 * t + c] = s_h[3 * t + c] = 0.f;
-        for (int c = 0; c < 4; ++c) s_r[4 * t + c] = 0.f;
-        s_o[t] = 0.f;
-    }
-    // no bucket of any tile reached this primitive: every gradient is exactly
-    // zero (products with zero 2D gradients); densification still counts a
-    // visible primitive (kernels_backward.cuh:345), adding 0 to its sums
-    if (vis && !nrec && densif) densif[i].x += 1.0f;
-    if (sparse && t < nblk) row_mask[i] = nrec ? 1u : 0u;
-    const uint64_t lm = ballot(nrec != 0u);
-    if (lane == 0) s_wcnt[w] = (uint32_t)__builtin_popcountll(lm);
-    __syncthreads();
-    uint32_t woff = 0;
-    for (uint32_t q = 0; q < w; ++q) woff += s_wcnt[q];
-    const uint32_t n_live = s_wcnt[0] + s_wcnt[1] + s_wcnt[2] + s_wcnt[3];
-    if (nrec) s_live[woff + mask_rank(lm)] = (uint32_t)t;
-    __syncthreads();
-    for (uint32_t idx = (uint32_t)t; idx < n_live; idx += 256u) {
-        const uint32_t tl = s_live[idx];
-        const int64_t ip = blk0 + tl;
-        // 2D gradient sums: up to kLightRecords per-(primitive, bucket)
-        // records are summed here; a primitive with more was summed into
-        // grad2d by gather_heavy. The counter is cleared for the next backward.
-        const uint32_t nr = rec_count[ip];
+    const ShT* __restrict__ shr_all, int bases, CamParams cam, const float4* __restrict__ conic_opacity,
+    uint32_t* __restrict__ rec_count, const float4* __restrict__ records, const float* __restrict__ grad2d,
+    GradView out, float4* __restrict__ densif, int mode, const uint4* __restrict__ live,
+    const uint2* __restrict__ chunk_counts, int aligned8) {
+    __shared__ uint2 s_win[256 * kShWin];
+    const uint32_t t = threadIdx.x;
+    const uint32_t nl = chunk_counts[blockIdx.x].x;
+    const uint4* list = live + (size_t)blockIdx.x * kClassChunk;
+    const bool store = mode != kGradAccumulate;
+    const int nsh = 3 * (bases - 1);   // SH-rest coefficients of the active bases
+    for (uint32_t g = t; g < nl; g += 256u) {
+        const uint4 e = list[g];
+        const int64_t ip = e.x;
+        const uint32_t nr = e.y;
         float4 gA = make_float4(0.f, 0.f, 0.f, 0.f), gB = gA, gC = gA;
         if (nr > kLightRecords) {
             const float* gr = grad2d + (size_t)ip * kGradStride;
@@ -317,7 +430,7 @@ __global__ void __launch_bounds__(256) preprocess_backward_kernel(
             gB = *(const float4*)(gr + 4);
             gC = *(const float4*)(gr + 8);
         } else {
-            const float4* rec = records + 3 * (size_t)first_slot[ip];
+            const float4* rec = records + 3 * (size_t)e.z;
             for (uint32_t r = 0; r < nr; ++r) {
                 const float4 a = rec[3 * r], b = rec[3 * r + 1], c = rec[3 * r + 2];
                 gA.x += a.x; gA.y += a.y; gA.z += a.z; gA.w += a.w;
@@ -326,123 +439,90 @@ __global__ void __launch_bounds__(256) preprocess_backward_kernel(
             }
         }
         rec_count[ip] = 0u;
-        PrimGrad g;
+        float pm[3], ps[3], pq[4], shv[45];
+#pragma unroll
+        for (int c = 0; c < 3; ++c) {
+            pm[c] = means[3 * ip + c];
+            ps[c] = scales[3 * ip + c];
+        }
+#pragma unroll
+        for (int c = 0; c < 4; ++c) pq[c] = rots[4 * ip + c];
+        const float opacity = conic_opacity[ip].w;
+        load_sh_row<ShT>(shr_all, ip, nsh, aligned8 != 0, s_win + kShWin * t, shv);
+        PrimGrad pg;
         float gc[3], k[15];
         for (int b = 0; b < 15; ++b) k[b] = 0.f;
         int nb = 0;
-        preprocess_backward_one<ShT>(ip, means, scales, rots, shr_all + 45 * ip, bases, cam, conic_opacity, gA, gB, gC,
-                                     densif, g, gc, k, nb);
-        for (int b = 0; b < 15; ++b) s_k[15 * tl + b] = k[b];
-        for (int c = 0; c < 3; ++c) s_gc[3 * tl + c] = gc[c];
-        s_nb[tl] = (uint32_t)nb;
-        if (assign) {
+        preprocess_backward_one(ip, pm, ps, pq, shv, opacity, bases, cam, gA, gB, gC, densif, pg, gc, k, nb);
+        float* gm = out.means + 3 * ip;
+        float* gs = out.scales + 3 * ip;
+        float* gh = out.sh0 + 3 * ip;
+        float* gq = out.rotations + 4 * ip;
+        if (store) {
             for (int c = 0; c < 3; ++c) {
-                s_m[3 * tl + c] = g.m[c];
-                s_s[3 * tl + c] = g.s[c];
-                s_h[3 * tl + c] = g.sh0[c];
+                gm[c] = pg.m[c];
+                gs[c] = pg.s[c];
+                gh[c] = pg.sh0[c];
             }
-            for (int c = 0; c < 4; ++c) s_r[4 * tl + c] = g.r[c];
-            s_o[tl] = g.o;
-        } else if (sparse) {
-            for (int c = 0; c < 3; ++c) {
-                g_means[3 * ip + c] = g.m[c];
-                g_scales[3 * ip + c] = g.s[c];
-                g_sh0[3 * ip + c] = g.sh0[c];
-            }
-            for (int c = 0; c < 4; ++c) g_rots[4 * ip + c] = g.r[c];
-            g_opac[ip] = g.o;
+            for (int c = 0; c < 4; ++c) gq[c] = pg.r[c];
+            out.opacities[ip] = pg.o;
         } else {
             for (int c = 0; c < 3; ++c) {
-                g_means[3 * ip + c] += g.m[c];
-                g_scales[3 * ip + c] += g.s[c];
-                g_sh0[3 * ip + c] += g.sh0[c];
+                gm[c] += pg.m[c];
+                gs[c] += pg.s[c];
+                gh[c] += pg.sh0[c];
             }
-            for (int c = 0; c < 4; ++c) g_rots[4 * ip + c] += g.r[c];
-            g_opac[ip] += g.o;
+            for (int c = 0; c < 4; ++c) gq[c] += pg.r[c];
+            out.opacities[ip] += pg.o;
         }
-    }
-    __syncthreads();
-    if (assign) {
-        block_store(g_means + 3 * blk0, s_m, 3 * nblk);
-        block_store(g_scales + 3 * blk0, s_s, 3 * nblk);
-        block_store(g_sh0 + 3 * blk0, s_h, 3 * nblk);
-        block_store(g_rots + 4 * blk0, s_r, 4 * nblk);
-        block_store(g_opac + blk0, s_o, nblk);
-    }
-    if (sparse) {
-        // SH-rest rows of the live primitives only, consecutive threads along each row
-        for (int e = t; e < (int)n_live * 45; e += 256) {
-            const int idx = e / 45, r = e - 45 * idx, b = r / 3, c = r - 3 * b;
-            const uint32_t tl = s_live[idx];
-            g_shr_all[(blk0 + (int64_t)tl) * 45 + r] =
-                ((uint32_t)b < s_nb[tl]) ? s_k[15 * tl + b] * s_gc[3 * tl + c] : 0.f;
-        }
-    } else if (bases > 1 || assign) {
-        // grad_sh_rest[i][b][c] += k_b * gc_c (kernels_backward.cuh:41-65), b < active bases - 1
-        float* gbase = g_shr_all + blk0 * 45;
-        const int total = nblk * 45;
-        for (int e0 = 4 * t; e0 < total; e0 += 4 * 256) {
-            if (assign && e0 + 3 < total) {
-                float4 g4;
-                float* gv = (float*)&g4;
+        float v[45];
 #pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    const int e = e0 + q;
-                    const int gi = e / 45, r = e - 45 * gi, b = r / 3, c = r - 3 * b;
-                    gv[q] = ((uint32_t)b < s_nb[gi]) ? s_k[15 * gi + b] * s_gc[3 * gi + c] : 0.f;
-                }
-                *(float4*)(gbase + e0) = g4;
-            } else if (e0 + 3 < total) {
-                bool any = false;
+        for (int b = 0; b < 15; ++b)
 #pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    const int e = e0 + q;
-                    const int gi = e / 45, r = e - 45 * gi, b = r / 3;
-                    any = any || (uint32_t)b < s_nb[gi];
-                }
-                if (any) {
-                    float4 g4 = *(const float4*)(gbase + e0);
-                    float* gv = (float*)&g4;
+            for (int c = 0; c < 3; ++c) v[3 * b + c] = b < nb ? k[b] * gc[c] : 0.f;
+        float* gr = out.sh_rest + 45 * ip;
+        if (store && aligned8) {
+            // row bytes [R, R + 180): s = 1 when R is 4 mod 8; 8-byte pairs at R + 4 s + 8 j
+            // hold elements (s + 2 j, s + 2 j + 1); the one element left over is 0 or 44
+            const uint32_t s1 = (uint32_t)(ip & 1);   // 180 ip = 4 ip (mod 8)
+            float2* pairs = (float2*)(gr + s1);
 #pragma unroll
-                    for (int q = 0; q < 4; ++q) {
-                        const int e = e0 + q;
-                        const int gi = e / 45, r = e - 45 * gi, b = r / 3, c = r - 3 * b;
-                        if ((uint32_t)b < s_nb[gi]) gv[q] = gv[q] + s_k[15 * gi + b] * s_gc[3 * gi + c];
-                    }
-                    *(float4*)(gbase + e0) = g4;
-                }
-            } else {
-                for (int e = e0; e < total; ++e) {
-                    const int gi = e / 45, r = e - 45 * gi, b = r / 3, c = r - 3 * b;
-                    if ((uint32_t)b < s_nb[gi])
-                        gbase[e] = assign ? s_k[15 * gi + b] * s_gc[3 * gi + c]
-                                          : gbase[e] + s_k[15 * gi + b] * s_gc[3 * gi + c];
-                    else if (assign)
-                        gbase[e] = 0.f;
-                }
-            }
+            for (int j = 0; j < 22; ++j)
+                pairs[j] = s1 ? make_float2(v[2 * j + 1], v[2 * j + 2]) : make_float2(v[2 * j], v[2 * j + 1]);
+            if (s1)
+                gr[0] = v[0];
+            else
+                gr[44] = v[44];
+        } else if (store) {
+#pragma unroll
+            for (int j = 0; j < 45; ++j) gr[j] = v[j];
+        } else {
+            for (int j = 0; j < 3 * nb; ++j) gr[j] += v[j];
         }
     }
 }
 
 void launch_preprocess_backward(const GaussianView& g, const CamParams& cam, const uint32_t* n_touched,
                                 const float4* conic_opacity, uint32_t* rec_count, const uint32_t* first_slot,
-                                const float4* records, const float* grad2d, const GradView& out, float* densif,
-                                int mode, uint8_t* row_mask, hipStream_t s) {
+                                const float4* records, float* grad2d, const GradView& out, float* densif, int mode,
+                                uint8_t* row_mask, uint4* live, uint32_t* heavy, uint2* chunk_counts, hipStream_t s) {
     if (g.n <= 0) return;
     const int bases = (g.sh_degree + 1) * (g.sh_degree + 1);
-    const unsigned grid = (unsigned)((g.n + 255) / 256);
-    if (g.sh_dtype == kShF16) {
-        preprocess_backward_kernel<__half><<<grid, 256, 0, s>>>(
-            g.means, g.scales, g.rotations, (const __half*)g.sh_rest, g.n, bases, cam, n_touched, conic_opacity,
-            rec_count, first_slot, records, grad2d, out.means, out.scales, out.rotations, out.opacities, out.sh0,
-            out.sh_rest, (float4*)densif, mode, row_mask);
-    } else {
-        preprocess_backward_kernel<float><<<grid, 256, 0, s>>>(
-            g.means, g.scales, g.rotations, (const float*)g.sh_rest, g.n, bases, cam, n_touched, conic_opacity,
-            rec_count, first_slot, records, grad2d, out.means, out.scales, out.rotations, out.opacities, out.sh0,
-            out.sh_rest, (float4*)densif, mode, row_mask);
-    }
+    const unsigned chunks = (unsigned)pb_chunks(g.n);
+    preprocess_backward_classify_kernel<<<chunks, 256, 0, s>>>(g.n, n_touched, rec_count, first_slot,
+                                                               (float4*)densif, mode, row_mask, out, live, heavy,
+                                                               chunk_counts);
+    gather_heavy_kernel<<<chunks, 256, 0, s>>>(heavy, chunk_counts, rec_count, first_slot, records, grad2d);
+    // 8-byte row pieces need 8-byte-aligned SH-rest parameter and gradient arrays
+    const int aligned8 = (((uintptr_t)g.sh_rest | (uintptr_t)out.sh_rest) & 7u) == 0u ? 1 : 0;
+    if (g.sh_dtype == kShF16)
+        preprocess_backward_live_kernel<__half><<<chunks, 256, 0, s>>>(
+            g.means, g.scales, g.rotations, (const __half*)g.sh_rest, bases, cam, conic_opacity, rec_count, records,
+            grad2d, out, (float4*)densif, mode, live, chunk_counts, aligned8);
+    else
+        preprocess_backward_live_kernel<float><<<chunks, 256, 0, s>>>(
+            g.means, g.scales, g.rotations, (const float*)g.sh_rest, bases, cam, conic_opacity, rec_count, records,
+            grad2d, out, (float4*)densif, mode, live, chunk_counts, aligned8);
 }
 
 }  // namespace tgs
