@@ -206,6 +206,34 @@ def test_backward_accumulates(hip, orc):
     assert normwise_err(got, g1["means"]) < 1e-5
 
 
+def test_misaligned_arrays_rejected(hip):
+    """The kernels move parameter and gradient rows in 8- and 16-byte pieces;
+    the boundary refuses arrays that are not 16-byte aligned instead of
+    running them."""
+    import torch
+    s = scenes.config1(seed=3)
+    run = gpu_render(s, with_debug=False)
+    g = run["g"]
+    t = g.m_sh_coefficients_rest
+    buf = torch.empty(t.numel() + 1, dtype=t.dtype, device=t.device)
+    g.m_sh_coefficients_rest = buf[1:].view_as(t)
+    with pytest.raises(RuntimeError, match="16-byte aligned"):
+        run["r"].forward(run["ctx"])
+    g.m_sh_coefficients_rest = t
+    grads = g.gradient_like()
+    m = grads.m_means
+    buf = torch.zeros(m.numel() + 1, dtype=m.dtype, device=m.device)
+    grads.m_means = buf[1:].view_as(m)
+    from tinygs_amd.core import Image
+    ctx = run["ctx"]
+    run["r"].forward(ctx)
+    ctx.gaussians_grad = grads
+    ctx.grad_output.image = Image.empty(s.camera.shape)
+    ctx.grad_output.image.data.zero_()
+    with pytest.raises(RuntimeError, match="16-byte aligned"):
+        run["r"].backward(ctx)
+
+
 def test_backward_assign_mode(hip, orc):
     """backward with assign=True overwrites every gradient (zero for culled
     Gaussians): equal to zero-then-accumulate, whatever the buffers held."""

@@ -493,7 +493,7 @@ int tgs_rasterizer_backward_ex(tgs_rasterizer* r, const void* grad_image, const 
     hipStream_t s = (hipStream_t)stream;
     const int64_t n = r->n;
     TGS_TRY(ensure(r->grad2d, sizeof(float) * kGradStride * (size_t)(n > 0 ? n : 1), s));
-    TGS_TRY(ensure(r->heavy, sizeof(uint32_t) * (size_t)(n > 0 ? n : 1), s));
+    TGS_TRY(ensure(r->heavy, sizeof(uint4) * (size_t)(n > 0 ? n : 1), s));
     TGS_TRY(ensure(r->live, sizeof(uint4) * (size_t)(n > 0 ? n : 1), s));
     TGS_TRY(ensure(r->chunk_counts, sizeof(uint2) * (size_t)std::max<int64_t>(pb_chunks(n), 1), s));
     if (flags & ~(TGS_BACKWARD_ASSIGN | TGS_BACKWARD_SPARSE))
@@ -524,7 +524,7 @@ int tgs_rasterizer_backward_ex(tgs_rasterizer* r, const void* grad_image, const 
         launch_preprocess_backward(view_of(r->g), cam, r->n_touched.as<uint32_t>(), r->conic_opacity.as<float4>(),
                                    r->rec_count.as<uint32_t>(), r->first_slot.as<uint32_t>(), r->records.as<float4>(),
                                    r->grad2d.as<float>(), gv, (float*)densification_info, mode,
-                                   r->row_mask.as<uint8_t>(), r->live.as<uint4>(), r->heavy.as<uint32_t>(),
+                                   r->row_mask.as<uint8_t>(), r->live.as<uint4>(), r->heavy.as<uint4>(),
                                    r->chunk_counts.as<uint2>(), s);
     }
     TGS_CHECK_LAUNCH();

@@ -125,13 +125,13 @@ void launch_blend_backward(const CamParams& cam, const uint32_t* inst_vals, cons
 // mode: 0 accumulate, 1 assign, 2 sparse (assign rows with gradient, write
 // row_mask[i] = 1 for them and 0 for the others, leave the others untouched).
 enum { kGradAccumulate = 0, kGradAssign = 1, kGradSparse = 2 };
-// Scratch: live (n uint4) and heavy (n u32) lists of the primitives with
+// Scratch: live and heavy (n uint4 each) lists of the primitives with
 // records, chunk_counts (pb_chunks(n) uint2), grad2d (12 n floats).
 int64_t pb_chunks(int64_t n);
 void launch_preprocess_backward(const GaussianView& g, const CamParams& cam, const uint32_t* n_touched,
                                 const float4* conic_opacity, uint32_t* rec_count, const uint32_t* first_slot,
                                 const float4* records, float* grad2d, const GradView& out, float* densif, int mode,
-                                uint8_t* row_mask, uint4* live, uint32_t* heavy, uint2* chunk_counts, hipStream_t s);
+                                uint8_t* row_mask, uint4* live, uint4* heavy, uint2* chunk_counts, hipStream_t s);
 
 // ---- utilities
 void launch_fill_u32(uint32_t* p, uint32_t value, int64_t n, hipStream_t s);

@@ -263,9 +263,9 @@ constexpr int kClassChunk = 256 * kClassRounds;
 int64_t pb_chunks(int64_t n) { return n > 0 ? (n + kClassChunk - 1) / kClassChunk : 0; }
 
 __device__ __forceinline__ void zero_run(float* __restrict__ dst, int64_t n) {
-    // 16-byte stores when the run is 16-byte aligned (the chunk starts at a
-    // multiple of 2048 rows, so it is whenever the array is)
-    const int64_t nv = ((uintptr_t)dst & 15u) ? 0 : n >> 2;
+    // the arrays are 16-byte aligned and the chunk starts at a multiple of
+    // 2048 rows, so the run is too
+    const int64_t nv = n >> 2;
     for (int64_t v = threadIdx.x; v < nv; v += 256) ((float4*)dst)[v] = make_float4(0.f, 0.f, 0.f, 0.f);
     for (int64_t e = (nv << 2) + threadIdx.x; e < n; e += 256) dst[e] = 0.f;
 }
@@ -273,7 +273,7 @@ __device__ __forceinline__ void zero_run(float* __restrict__ dst, int64_t n) {
 __global__ void __launch_bounds__(256) preprocess_backward_classify_kernel(
     int64_t n, const uint32_t* __restrict__ n_touched, const uint32_t* __restrict__ rec_count,
     const uint32_t* __restrict__ first_slot, float4* __restrict__ densif, int mode, uint8_t* __restrict__ row_mask,
-    GradView out, uint4* __restrict__ live, uint32_t* __restrict__ heavy, uint2* __restrict__ chunk_counts) {
+    GradView out, uint4* __restrict__ live, uint4* __restrict__ heavy, uint2* __restrict__ chunk_counts) {
     __shared__ uint32_t s_rw[4 * kClassRounds];
     const uint32_t t = threadIdx.x;
     const int64_t c0 = (int64_t)blockIdx.x * kClassChunk;
@@ -316,45 +316,54 @@ __global__ void __launch_bounds__(256) preprocess_backward_classify_kernel(
 #pragma unroll
     for (int r = 0; r < kClassRounds; ++r) {
         const uint32_t i = (uint32_t)(base + (int64_t)r * 256);
-        if (lv[r]) live[c0 + ex[r]] = make_uint4(i, nrec[r], first_slot[i], 0u);
-        if (hv[r]) heavy[c0 + exh[r]] = i;
+        if (lv[r]) {
+            const uint4 entry = make_uint4(i, nrec[r], first_slot[i], 0u);
+            live[c0 + ex[r]] = entry;
+            if (hv[r]) heavy[c0 + exh[r]] = entry;
+        }
     }
 }
 
 // ---- phase 2: 2D-gradient sums of the heavy primitives
 //
-// A wave per heavy primitive of the chunk, lanes over its records, then the
-// transposed wave reduction; the sums go to grad2d[12 p] in record layout.
-__global__ void __launch_bounds__(256) gather_heavy_kernel(const uint32_t* __restrict__ heavy,
+// Sixteen lanes (one DPP row) per heavy primitive of the chunk, four per
+// wave: the lanes stride over the primitive's records, then a row
+// butterfly leaves the 12 sums in every lane of the row and lanes 0-2 of
+// the row store them to grad2d[12 p] in record layout.
+__global__ void __launch_bounds__(256) gather_heavy_kernel(const uint4* __restrict__ heavy,
                                                            const uint2* __restrict__ chunk_counts,
-                                                           const uint32_t* __restrict__ rec_count,
-                                                           const uint32_t* __restrict__ first_slot,
                                                            const float4* __restrict__ records,
                                                            float* __restrict__ grad2d) {
-    const uint32_t w = threadIdx.x >> 6, lane = threadIdx.x & 63u;
+    const uint32_t row = threadIdx.x >> 4, sub = threadIdx.x & 15u;
     const uint32_t nh = chunk_counts[blockIdx.x].y;
-    const int q0 = row_value(lane >> 4);
-    const uint32_t* list = heavy + (size_t)blockIdx.x * kClassChunk;
-    for (uint32_t h = w; h < nh; h += 4u) {
-        const uint32_t p = list[h];
-        const uint32_t c = rec_count[p], base = first_slot[p];
+    const uint4* list = heavy + (size_t)blockIdx.x * kClassChunk;
+    for (uint32_t h0 = 0; h0 < nh; h0 += 16u) {
+        const uint32_t h = h0 + row;
+        const bool on = h < nh;
+        const uint4 e = on ? list[h] : make_uint4(0u, 0u, 0u, 0u);
         float v[12];
 #pragma unroll
         for (int q = 0; q < 12; ++q) v[q] = 0.f;
-        for (uint32_t r = lane; r < c; r += 64u) {
-            const float4* src = records + 3 * (size_t)(base + r);
+        for (uint32_t r = sub; r < e.y; r += 16u) {
+            const float4* src = records + 3 * (size_t)(e.z + r);
             const float4 a = src[0], b = src[1], d = src[2];
             v[0] += a.x; v[1] += a.y; v[2] += a.z; v[3] += a.w;
             v[4] += b.x; v[5] += b.y; v[6] += b.z; v[7] += b.w;
             v[8] += d.x; v[9] += d.y; v[10] += d.z; v[11] += d.w;
         }
-        float t[3];
-        wave_reduce12(v, t);
-        if ((lane & 15u) == 0u) {
-            float* g = grad2d + (size_t)p * kGradStride;
-            g[q0] = t[0];
-            g[4 + q0] = t[1];
-            g[8 + q0] = t[2];
+#pragma unroll
+        for (int q = 0; q < 12; ++q) {
+            v[q] += dpp_f32<0x128>(v[q]);   // row_ror:8
+            v[q] += dpp_f32<0x124>(v[q]);   // row_ror:4
+            v[q] += dpp_f32<0x122>(v[q]);   // row_ror:2
+            v[q] += dpp_f32<0x121>(v[q]);   // row_ror:1
+        }
+        if (on && sub < 3u) {
+            float4* g = (float4*)(grad2d + (size_t)e.x * kGradStride);
+            const float4 f = sub == 0u ? make_float4(v[0], v[1], v[2], v[3])
+                             : sub == 1u ? make_float4(v[4], v[5], v[6], v[7])
+                                         : make_float4(v[8], v[9], v[10], v[11]);
+            g[sub] = f;
         }
     }
 }
@@ -374,21 +383,15 @@ __global__ void __launch_bounds__(256) gather_heavy_kernel(const uint32_t* __res
 constexpr int kShWin = 13;   // 8-byte words per LDS slot (an odd word stride)
 
 template <typename ShT>
-__device__ __forceinline__ void load_sh_row(const ShT* __restrict__ shr_all, int64_t ip, int nsh, bool vec,
-                                            uint2* slot, float shv[45]) {
+__device__ __forceinline__ void load_sh_row(const ShT* __restrict__ shr_all, int64_t ip, int nsh, uint2* slot,
+                                            float shv[45]) {
     const ShT* sr = shr_all + 45 * ip;
 #pragma unroll
     for (int b = 0; b < 45; ++b) shv[b] = b < nsh ? load_as_float(sr, b) : 0.f;
 }
 template <>
 __device__ __forceinline__ void load_sh_row<__half>(const __half* __restrict__ shr_all, int64_t ip, int nsh,
-                                                    bool vec, uint2* slot, float shv[45]) {
-    if (!vec) {
-        const __half* sr = shr_all + 45 * ip;
-#pragma unroll
-        for (int b = 0; b < 45; ++b) shv[b] = b < nsh ? __half2float(sr[b]) : 0.f;
-        return;
-    }
+                                                    uint2* slot, float shv[45]) {
     // row bytes [B, B + 90), window [a, a + 96) with a = B & ~7, o = B - a in {0, 2, 4, 6}:
     // 11 whole 8-byte words lie inside the row; of the 12th, only its first o + 2 bytes do
     const uint64_t B = 90u * (uint64_t)ip, a = B & ~7ull;
@@ -412,7 +415,7 @@ __global__ void __launch_bounds__(256) preprocess_backward_live_kernel(
     const ShT* __restrict__ shr_all, int bases, CamParams cam, const float4* __restrict__ conic_opacity,
     uint32_t* __restrict__ rec_count, const float4* __restrict__ records, const float* __restrict__ grad2d,
     GradView out, float4* __restrict__ densif, int mode, const uint4* __restrict__ live,
-    const uint2* __restrict__ chunk_counts, int aligned8) {
+    const uint2* __restrict__ chunk_counts) {
     __shared__ uint2 s_win[256 * kShWin];
     const uint32_t t = threadIdx.x;
     const uint32_t nl = chunk_counts[blockIdx.x].x;
@@ -448,7 +451,7 @@ __global__ void __launch_bounds__(256) preprocess_backward_live_kernel(
 #pragma unroll
         for (int c = 0; c < 4; ++c) pq[c] = rots[4 * ip + c];
         const float opacity = conic_opacity[ip].w;
-        load_sh_row<ShT>(shr_all, ip, nsh, aligned8 != 0, s_win + kShWin * t, shv);
+        load_sh_row<ShT>(shr_all, ip, nsh, s_win + kShWin * t, shv);
         PrimGrad pg;
         float gc[3], k[15];
         for (int b = 0; b < 15; ++b) k[b] = 0.f;
@@ -481,7 +484,7 @@ __global__ void __launch_bounds__(256) preprocess_backward_live_kernel(
 #pragma unroll
             for (int c = 0; c < 3; ++c) v[3 * b + c] = b < nb ? k[b] * gc[c] : 0.f;
         float* gr = out.sh_rest + 45 * ip;
-        if (store && aligned8) {
+        if (store) {
             // row bytes [R, R + 180): s = 1 when R is 4 mod 8; 8-byte pairs at R + 4 s + 8 j
             // hold elements (s + 2 j, s + 2 j + 1); the one element left over is 0 or 44
             const uint32_t s1 = (uint32_t)(ip & 1);   // 180 ip = 4 ip (mod 8)
@@ -493,9 +496,6 @@ __global__ void __launch_bounds__(256) preprocess_backward_live_kernel(
                 gr[0] = v[0];
             else
                 gr[44] = v[44];
-        } else if (store) {
-#pragma unroll
-            for (int j = 0; j < 45; ++j) gr[j] = v[j];
         } else {
             for (int j = 0; j < 3 * nb; ++j) gr[j] += v[j];
         }
@@ -505,24 +505,22 @@ __global__ void __launch_bounds__(256) preprocess_backward_live_kernel(
 void launch_preprocess_backward(const GaussianView& g, const CamParams& cam, const uint32_t* n_touched,
                                 const float4* conic_opacity, uint32_t* rec_count, const uint32_t* first_slot,
                                 const float4* records, float* grad2d, const GradView& out, float* densif, int mode,
-                                uint8_t* row_mask, uint4* live, uint32_t* heavy, uint2* chunk_counts, hipStream_t s) {
+                                uint8_t* row_mask, uint4* live, uint4* heavy, uint2* chunk_counts, hipStream_t s) {
     if (g.n <= 0) return;
     const int bases = (g.sh_degree + 1) * (g.sh_degree + 1);
     const unsigned chunks = (unsigned)pb_chunks(g.n);
     preprocess_backward_classify_kernel<<<chunks, 256, 0, s>>>(g.n, n_touched, rec_count, first_slot,
                                                                (float4*)densif, mode, row_mask, out, live, heavy,
                                                                chunk_counts);
-    gather_heavy_kernel<<<chunks, 256, 0, s>>>(heavy, chunk_counts, rec_count, first_slot, records, grad2d);
-    // 8-byte row pieces need 8-byte-aligned SH-rest parameter and gradient arrays
-    const int aligned8 = (((uintptr_t)g.sh_rest | (uintptr_t)out.sh_rest) & 7u) == 0u ? 1 : 0;
+    gather_heavy_kernel<<<chunks, 256, 0, s>>>(heavy, chunk_counts, records, grad2d);
     if (g.sh_dtype == kShF16)
         preprocess_backward_live_kernel<__half><<<chunks, 256, 0, s>>>(
             g.means, g.scales, g.rotations, (const __half*)g.sh_rest, bases, cam, conic_opacity, rec_count, records,
-            grad2d, out, (float4*)densif, mode, live, chunk_counts, aligned8);
+            grad2d, out, (float4*)densif, mode, live, chunk_counts);
     else
         preprocess_backward_live_kernel<float><<<chunks, 256, 0, s>>>(
             g.means, g.scales, g.rotations, (const float*)g.sh_rest, bases, cam, conic_opacity, rec_count, records,
-            grad2d, out, (float4*)densif, mode, live, chunk_counts, aligned8);
+            grad2d, out, (float4*)densif, mode, live, chunk_counts);
 }
 
 }  // namespace tgs
