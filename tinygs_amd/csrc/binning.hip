@@ -270,28 +270,31 @@ __device__ __forceinline__ void rank_keys(const uint32_t key[KPT], int64_t base,
 }
 
 // Per-workgroup digit counts: counts[d * nb + b] (digit-major). Workgroups
-// past the end write zeros.
+// past the end write zeros. Counting needs no ranks: one LDS atomic add per
+// key into the workgroup's histogram.
 template <int KPT>
 __global__ void __launch_bounds__(kThreads) radix_upsweep_kernel(const uint32_t* __restrict__ keys,
                                                                  const uint32_t* d_n, int64_t max_n, int shift,
                                                                  int bits, uint32_t* __restrict__ counts,
                                                                  uint32_t nb) {
-    __shared__ uint32_t s_cnt[4][256];
+    __shared__ uint32_t s_hist[256];
     const uint32_t t = threadIdx.x, lane = t & 63u, w = t >> 6;
-    const uint32_t bins = 1u << bits;
-    for (int k = t; k < 4 * 256; k += kThreads) (&s_cnt[0][0])[k] = 0;
+    const uint32_t bins = 1u << bits, dmask = bins - 1u;
+    s_hist[t] = 0u;
     __syncthreads();
     const int64_t n = resolve_n(d_n, max_n);
     const int64_t base = (int64_t)blockIdx.x * (kThreads * KPT) + (int64_t)w * (64 * KPT);
-    uint32_t key[KPT], pos[KPT];
+    uint32_t key[KPT];
 #pragma unroll
     for (int r = 0; r < KPT; ++r) {
         const int64_t i = base + (int64_t)r * 64 + lane;
         key[r] = i < n ? keys[i] : 0u;
     }
-    rank_keys<KPT>(key, base, n, shift, bits, s_cnt, pos);
+#pragma unroll
+    for (int r = 0; r < KPT; ++r)
+        if (base + (int64_t)r * 64 + lane < n) atomicAdd(&s_hist[(key[r] >> shift) & dmask], 1u);
     __syncthreads();
-    if (t < bins) counts[(size_t)t * nb + blockIdx.x] = s_cnt[0][t] + s_cnt[1][t] + s_cnt[2][t] + s_cnt[3][t];
+    if (t < bins) counts[(size_t)t * nb + blockIdx.x] = s_hist[t];
 }
 
 // In-place exclusive scan of a u32 array of n elements (single pass,
