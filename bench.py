@@ -4,6 +4,7 @@ storage, on one MI355X, plus the HBM roofline of the
 dominant kernel and the CPU oracle's time on the same workload.
 
   python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 3] [--no-cpu-baseline]
+  python bench.py --config 4 [--stress-counts N ...]   (fwd+bwd stress sweep, its own JSON line)
 
 Prints one JSON line on stdout; a per-stage table goes to stderr.
 """
@@ -110,12 +111,114 @@ def calibrate_copy(mib):
     print(json.dumps({"calibrate_copy_bytes": n * 4, "copies": 5}), flush=True)
 
 
+STRESS_METRIC = "ms per fwd+bwd vs Gaussians per tile (config 4 stress, 3840x2160, fp32)"
+
+
+def tile_histogram(rasterizer):
+    """Instances per tile of the last forward (from the tile ranges only)."""
+    import ctypes as C
+
+    import numpy as np
+    import torch
+
+    from tinygs_amd import _lib
+    dv = _lib.tgs_debug_view()
+    _lib.check(_lib.load().tgs_rasterizer_debug_view(rasterizer._h, C.byref(dv)), "debug_view")
+    t = torch.empty(2 * int(dv.n_tiles), dtype=torch.int32, device="cuda")
+    _lib.copy_device(dv.tile_ranges, t.numel() * 4, t)
+    r = t.cpu().numpy().view(np.uint32).reshape(-1, 2).astype(np.int64)
+    return r[:, 1] - r[:, 0]
+
+
+def stress_main(args):
+    """Config 4: forward + backward (no loss, no optimiser) of the high-overlap
+    scene at several Gaussian counts; per count the distribution of Gaussians
+    per tile and the ms per fwd+bwd. The JSON value is the full 3M case."""
+    import numpy as np
+    import torch
+
+    from tinygs_amd import scenes
+    from tinygs_amd.core import GPUBatchInput, GPUGaussian3d, Image, RasterizeContext
+    from tinygs_amd.rasterizer import create_rasterizer
+
+    rows = []
+    for n in args.stress_counts:
+        t0 = time.time()
+        scene = scenes.config4(n=n)
+        g = GPUGaussian3d.from_scene(scene)
+        grads = g.gradient_like()
+        r = create_rasterizer("fastgs")
+        r.set_gaussians(g)
+        ctx = RasterizeContext()
+        ctx.fwd_input = GPUBatchInput.from_camera(scene.camera)
+        ctx.fwd_output.image = Image.empty(scene.camera.shape)
+        ctx.gaussians_grad = grads
+        gimg = scenes.grad_image(44, scene.camera.shape)
+        ctx.grad_output.image = Image(scene.camera.shape, "float32", torch.from_numpy(gimg).cuda())
+        print(f"[bench] config4 n={n}: scene in {time.time() - t0:.1f}s", file=sys.stderr, flush=True)
+
+        def step():
+            r.forward(ctx)
+            r.backward(ctx, assign=True)
+
+        for _ in range(args.warmup):
+            step()
+        torch.cuda.synchronize()
+        a = torch.cuda.Event(enable_timing=True)
+        b = torch.cuda.Event(enable_timing=True)
+        fwd_ms = 0.0
+        stream = torch.cuda.current_stream()
+        a.record(stream)
+        for _ in range(args.steps):
+            step()
+        b.record(stream)
+        torch.cuda.synchronize()
+        ms = a.elapsed_time(b) / args.steps
+        a.record(stream)
+        for _ in range(args.steps):
+            r.forward(ctx)
+        b.record(stream)
+        torch.cuda.synchronize()
+        fwd_ms = a.elapsed_time(b) / args.steps
+        per_tile = tile_histogram(r)
+        V, I, T = r.counts()
+        img = ctx.fwd_output.image.data
+        ok = bool(torch.isfinite(img).all().item()) and all(
+            bool(torch.isfinite(t).all().item()) for t in grads.tensors())
+        row = {"n_gaussians": n, "n_instances": I, "n_tiles": T, "ms_fwd_bwd": round(ms, 3),
+               "ms_fwd": round(fwd_ms, 3),
+               "per_tile": {"median": int(np.median(per_tile)), "p90": int(np.percentile(per_tile, 90)),
+                            "max": int(per_tile.max()), "mean": round(float(per_tile.mean()), 1),
+                            "covered_tiles": int((per_tile > 0).sum()),
+                            "median_covered": int(np.median(per_tile[per_tile > 0])) if (per_tile > 0).any() else 0},
+               "finite": ok}
+        rows.append(row)
+        print(f"[bench] config4 n={n}: {ms:.3f} ms fwd+bwd ({fwd_ms:.3f} fwd), I={I}, Gaussians per tile "
+              f"median {row['per_tile']['median']} (covered tiles {row['per_tile']['covered_tiles']}: median "
+              f"{row['per_tile']['median_covered']}) p90 {row['per_tile']['p90']} max {row['per_tile']['max']}",
+              file=sys.stderr, flush=True)
+        del r, g, grads, ctx
+        torch.cuda.synchronize()
+        torch.cuda.empty_cache()
+    last = rows[-1]
+    out = {"metric": STRESS_METRIC, "value": last["ms_fwd_bwd"], "unit": "ms/iter", "n_gpus": 1,
+           "steps": args.steps, "warmup": args.warmup, "ms_per_step": last["ms_fwd_bwd"], "higher_is_better": False,
+           "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+           "config": {"workload": "config4: fwd + bwd (assign), seeded dL/dimage", "width": 3840, "height": 2160,
+                      "sh_degree": 3, "parallelism": "single GPU"},
+           "sweep": rows}
+    print(json.dumps(out), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--config", type=int, default=3)
+    ap.add_argument("--config", type=int, default=3,
+                    help="3: the headline training iteration; 1, 2: the smaller scenes; 4: the fwd+bwd stress sweep")
+    ap.add_argument("--stress-counts", type=int, nargs="+", default=[375_000, 750_000, 1_500_000, 3_000_000],
+                    help="Gaussian counts of the config-4 sweep")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="instead of the benchmark, run 5 device-to-device copies of MIB MiB (the known-size kernel "
@@ -139,6 +242,8 @@ def main():
         print("bench.py needs a GPU", file=sys.stderr)
         sys.exit(1)
 
+    if args.config == 4:
+        return stress_main(args)
     scene_fn = {1: scenes.config1, 2: scenes.config2, 3: scenes.config3}[args.config]
     t0 = time.time()
     scene = scene_fn()
