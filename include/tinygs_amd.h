@@ -196,6 +196,59 @@ int64_t tgs_adam_global_steps(tgs_adam* a);
 /* Device pointers of a group's moments; group in 0..5 =
  * means, opacities, rotations, scales, sh0, sh_rest. */
 int tgs_adam_moments(tgs_adam* a, int32_t group, float** first, float** second);
+/* SimpleAdam::remove (simple_adam.cu:841-906): moment row k becomes old row
+ * rows[k] for k < n_rows (device int32 array); the moments then hold n_rows
+ * rows and tgs_adam_set_gaussians takes arrays of that size. */
+int tgs_adam_gather(tgs_adam* a, const int32_t* rows, int64_t n_rows, void* stream);
+/* SimpleAdam::duplicate (simple_adam.cu:908-924): n_new zero moment rows
+ * appended. */
+int tgs_adam_append(tgs_adam* a, int64_t n_new, void* stream);
+/* SimpleAdam::reset_opacity (simple_adam.cu:981-985): opacity moments zeroed. */
+int tgs_adam_reset_opacity(tgs_adam* a, void* stream);
+
+/* ---- densification: the device work of DefaultStrategy
+ * (tinygs/src/strategy/default.cu:26-341) and GPUGaussian3d::remove
+ * (tinygs/src/core/gpu_gaussian.cu:117-160). Array sizing (append / remove of
+ * rows) belongs to the caller, as the arrays are the caller's. densif is the
+ * (n, 4) float DensificationInfo array (counter, grad sum, |grad| sum, max
+ * screen radius) a forward / backward with densification info fills. */
+/* pcg32 state (tinygs/include/tinygs/random/pcg32.hpp:35-53). */
+typedef struct tgs_pcg32 {
+    uint64_t state, inc;
+} tgs_pcg32;
+/* pcg32::seed(initstate, initseq) (host only). */
+void tgs_pcg32_seed(tgs_pcg32* rng, uint64_t initstate, uint64_t initseq);
+/* generate_random_logistic(rng, n, out, mean, stddev) (random/device.cuh:38-84):
+ * out[i] = logit(u) * stddev * 0.551328895 + mean with the reference's
+ * assignment of stream positions to elements; rng advanced by n. */
+int tgs_random_logistic(tgs_pcg32* rng, int64_t n, float* out, float mean, float stddev, void* stream);
+/* default.cu:151-214: flags[i] = 0 / 1 (duplicate) / 2 (split) for the n
+ * Gaussians of g; src_indices (device, capacity n) receives the flagged
+ * indices in order; counts on the host. grad_threshold includes the grad
+ * scaler, scale_threshold the scene scale. Synchronises the stream. */
+int tgs_densify_select(const tgs_gaussians* g, const float* densif, float grad_threshold, float scale_threshold,
+                       int32_t absgrad, uint8_t* flags, int32_t* src_indices, int64_t* n_duplicate,
+                       int64_t* n_split, void* stream);
+/* default.cu:235-297: g already holds n_old + n_grow rows; grown row i
+ * (target n_old + i) is made from source src_indices[i] per flags, with the
+ * six logistic numbers rand6[6 i .. 6 i + 5] of a split. */
+int tgs_densify_apply(const tgs_gaussians* g, int64_t n_old, const int32_t* src_indices, int64_t n_grow,
+                      const uint8_t* flags, const float* rand6, void* stream);
+/* default.cu:300-341: alive[i] for the n Gaussians of g (densif rows at or
+ * past n_info count as small on screen); kept_indices (device, capacity n)
+ * receives the alive indices in order, *n_kept their count. Synchronises. */
+int tgs_prune_select(const tgs_gaussians* g, const float* densif, int64_t n_info, float opacity_threshold,
+                     float scale_limit, float radius_limit, int32_t prune_large, uint8_t* alive,
+                     int32_t* kept_indices, int64_t* n_kept, void* stream);
+/* Row k of every array of dst (k < dst->n) = row rows[k] of src (same SH
+ * dtype): the copy of GPUGaussian3d::remove with its mapping. */
+int tgs_gaussians_gather(const tgs_gaussians* src, const tgs_gaussians* dst, const int32_t* rows, void* stream);
+/* thrust::copy_if of the flag indices (default.cu:198-203, gpu_gaussian.cu:120-124): out
+ * (device, capacity n) receives the i < n with flags[i] != 0 in order, *count their number.
+ * Synchronises. */
+int tgs_flags_compact(const uint8_t* flags, int64_t n, int32_t* out, int64_t* count, void* stream);
+/* reset_opacity (default.cu:26-37): opacity = logit(min(sigmoid(opacity), max_opacity)). */
+int tgs_reset_opacity(const tgs_gaussians* g, float max_opacity, void* stream);
 
 /* ---- measurement (no counterpart in the reference, which uses NVTX ranges,
  * tinygs/src/rasterizer/fastgs_ours/nvtx_gs.h): HIP events recorded on the

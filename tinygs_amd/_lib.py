@@ -44,6 +44,10 @@ class tgs_debug_view(C.Structure):
                 ("n_tiles", C.c_int64)]
 
 
+class tgs_pcg32(C.Structure):
+    _fields_ = [("state", C.c_uint64), ("inc", C.c_uint64)]
+
+
 class tgs_loss_context(C.Structure):
     _fields_ = [("pred", C.c_void_p), ("target", C.c_void_p), ("loss", C.c_void_p), ("grad", C.c_void_p),
                 ("width", C.c_uint32), ("height", C.c_uint32), ("channel", C.c_uint32), ("dtype", C.c_int32)]
@@ -87,6 +91,19 @@ SIGNATURES = {
     "tgs_adam_reset": ([P, P], C.c_int),
     "tgs_adam_global_steps": ([P], C.c_int64),
     "tgs_adam_moments": ([P, C.c_int32, C.POINTER(C.c_void_p), C.POINTER(C.c_void_p)], C.c_int),
+    "tgs_adam_gather": ([P, P, C.c_int64, P], C.c_int),
+    "tgs_adam_append": ([P, C.c_int64, P], C.c_int),
+    "tgs_adam_reset_opacity": ([P, P], C.c_int),
+    "tgs_pcg32_seed": ([C.POINTER(tgs_pcg32), C.c_uint64, C.c_uint64], None),
+    "tgs_random_logistic": ([C.POINTER(tgs_pcg32), C.c_int64, P, C.c_float, C.c_float, P], C.c_int),
+    "tgs_densify_select": ([C.POINTER(tgs_gaussians), P, C.c_float, C.c_float, C.c_int32, P, P,
+                            C.POINTER(C.c_int64), C.POINTER(C.c_int64), P], C.c_int),
+    "tgs_densify_apply": ([C.POINTER(tgs_gaussians), C.c_int64, P, C.c_int64, P, P, P], C.c_int),
+    "tgs_prune_select": ([C.POINTER(tgs_gaussians), P, C.c_int64, C.c_float, C.c_float, C.c_float, C.c_int32, P, P,
+                          C.POINTER(C.c_int64), P], C.c_int),
+    "tgs_gaussians_gather": ([C.POINTER(tgs_gaussians), C.POINTER(tgs_gaussians), P, P], C.c_int),
+    "tgs_flags_compact": ([P, C.c_int64, P, C.POINTER(C.c_int64), P], C.c_int),
+    "tgs_reset_opacity": ([C.POINTER(tgs_gaussians), C.c_float, P], C.c_int),
     "tgs_profiling_set": ([C.c_uint32], C.c_int),
     "tgs_profiling_read": ([C.c_int32, C.POINTER(C.c_double), C.POINTER(C.c_int64), C.c_int32], C.c_int),
     "tgs_stage_name": ([C.c_int32], C.c_char_p),

@@ -107,6 +107,29 @@ class GPUGaussian3d:
         g.m_scene_scale = self.m_scene_scale
         return g
 
+    def append(self, num_dup: int):
+        """GPUGaussian3d::append (gpu_gaussian.cu:161-170): num_dup zero rows
+        appended to every array."""
+        if num_dup <= 0:
+            raise RuntimeError("append: num_dup must be positive")
+        torch = _torch()
+        for name in ("m_means", "m_scales", "m_rotations", "m_opacities", "m_sh_coefficient_0",
+                     "m_sh_coefficients_rest"):
+            t = getattr(self, name)
+            z = torch.zeros((num_dup,) + tuple(t.shape[1:]), dtype=t.dtype, device=t.device)
+            setattr(self, name, torch.cat([t, z]))
+
+    def remove(self, kept_rows, num_kept: int, stream=None):
+        """GPUGaussian3d::remove (gpu_gaussian.cu:117-158): keep the rows
+        listed (in order) in the device int32 tensor kept_rows[:num_kept]."""
+        dst = GPUGaussian3d(num_kept, self.sh_dtype, device=self.m_means.device)
+        src_c, dst_c = self.to_c(), dst.to_c()
+        _lib.check(_lib.load().tgs_gaussians_gather(C.byref(src_c), C.byref(dst_c), ptr(kept_rows),
+                                                    stream_ptr(stream)), "GPUGaussian3d::remove")
+        for name in ("m_means", "m_scales", "m_rotations", "m_opacities", "m_sh_coefficient_0",
+                     "m_sh_coefficients_rest"):
+            setattr(self, name, getattr(dst, name))
+
     def gradient_like(self) -> "GPUGaussian3d":
         """Zeroed fp32 gradient buffers of the same size."""
         return GPUGaussian3d(self.size(), DataType.Float32, device=self.m_means.device)

@@ -22,6 +22,7 @@
 #include "../../include/tinygs_amd.h"
 #include "common.h"
 #include "kernels.h"
+#include "pcg32.h"
 
 using namespace tgs;
 
@@ -267,6 +268,7 @@ struct tgs_adam {
     tgs_gaussians params{};
     tgs_gaussians grads{};
     DevBuf m1[6], m2[6];
+    int64_t rows = 0;   // Gaussians the moments are sized for
     tgs_adam_params p{};
     float global_lr = 1.0f;
     int64_t steps = 0;
@@ -699,6 +701,7 @@ int tgs_adam_create(const tgs_gaussians* params, const tgs_gaussians* grads, tgs
     tgs_adam* a = new tgs_adam();
     a->params = *params;
     a->grads = *grads;
+    a->rows = params->n;
     default_adam_params(a->p);
     for (int k = 0; k < 6; ++k) {
         const size_t bytes = sizeof(float) * (size_t)kGroupMult[k] * (size_t)(params->n > 0 ? params->n : 1);
@@ -752,9 +755,10 @@ int tgs_adam_set_gaussians(tgs_adam* a, const tgs_gaussians* params, const tgs_g
     if (!a) return fail(TGS_ERR_INVALID, "NULL argument");
     TGS_TRY(check_gaussians(params, false));
     TGS_TRY(check_gaussians(grads, true));
-    if (params->n != a->params.n || grads->n != a->params.n)
-        return fail(TGS_ERR_INVALID, "size change needs a new optimizer (moments sized for %lld)",
-                    (long long)a->params.n);
+    if (params->n != a->rows || grads->n != a->rows)
+        return fail(TGS_ERR_INVALID, "moments are sized for %lld Gaussians, got %lld / %lld (resize them with "
+                    "tgs_adam_gather / tgs_adam_append)", (long long)a->rows, (long long)params->n,
+                    (long long)grads->n);
     a->params = *params;
     a->grads = *grads;
     return TGS_OK;
@@ -831,6 +835,203 @@ int tgs_adam_moments(tgs_adam* a, int32_t group, float** first, float** second) 
     if (!a || group < 0 || group >= 6) return fail(TGS_ERR_INVALID, "bad group");
     if (first) *first = a->m1[group].as<float>();
     if (second) *second = a->m2[group].as<float>();
+    return TGS_OK;
+}
+
+}  // extern "C"
+
+// Replaces every moment buffer by one of `rows` rows built by `fill(k, dst)`
+// (k: group); the old buffers are released once the stream has finished.
+template <typename F>
+static int adam_rebuild(tgs_adam* a, int64_t rows, hipStream_t s, F fill) {
+    DevBuf n1[6], n2[6];
+    for (int k = 0; k < 6; ++k) {
+        const size_t bytes = sizeof(float) * (size_t)kGroupMult[k] * (size_t)(rows > 0 ? rows : 1);
+        if (ensure(n1[k], bytes, s) != TGS_OK || ensure(n2[k], bytes, s) != TGS_OK) {
+            for (int q = 0; q < 6; ++q) {
+                release(n1[q]);
+                release(n2[q]);
+            }
+            return fail(TGS_ERR_HIP, "moment allocation failed");
+        }
+        fill(k, a->m1[k], n1[k]);
+        fill(k, a->m2[k], n2[k]);
+    }
+    TGS_CHECK_LAUNCH();
+    TGS_HIP(hipStreamSynchronize(s));
+    for (int k = 0; k < 6; ++k) {
+        release(a->m1[k]);
+        release(a->m2[k]);
+        a->m1[k] = n1[k];
+        a->m2[k] = n2[k];
+        n1[k] = DevBuf{};
+        n2[k] = DevBuf{};
+    }
+    a->rows = rows;
+    return TGS_OK;
+}
+
+// Indices of the nonzero flags in index order into `out`; totals of nonzero
+// flags and of flags equal to 1. Synchronises the stream.
+static int compact_flags(const uint8_t* flags, int64_t n, int32_t* out, int64_t* n_nonzero, int64_t* n_ones,
+                         hipStream_t s) {
+    *n_nonzero = 0;
+    if (n_ones) *n_ones = 0;
+    if (n <= 0) return TGS_OK;
+    const int64_t chunks = list_chunks(n);
+    DevBuf counts, offsets;
+    int rc = ensure(counts, sizeof(uint2) * (size_t)chunks, s);
+    if (rc == TGS_OK) rc = ensure(offsets, sizeof(uint32_t) * (size_t)chunks, s);
+    if (rc != TGS_OK) {
+        release(counts);
+        release(offsets);
+        return rc;
+    }
+    std::vector<uint2> h(chunks);
+    std::vector<uint32_t> off(chunks);
+    launch_flag_count(flags, n, counts.as<uint2>(), s);
+    hipError_t e = hipMemcpyAsync(h.data(), counts.p, sizeof(uint2) * (size_t)chunks, hipMemcpyDeviceToHost, s);
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    if (e == hipSuccess) {
+        uint64_t acc = 0, ones = 0;
+        for (int64_t c = 0; c < chunks; ++c) {
+            off[c] = (uint32_t)acc;
+            acc += h[c].x;
+            ones += h[c].y;
+        }
+        *n_nonzero = (int64_t)acc;
+        if (n_ones) *n_ones = (int64_t)ones;
+        e = hipMemcpyAsync(offsets.p, off.data(), sizeof(uint32_t) * (size_t)chunks, hipMemcpyHostToDevice, s);
+    }
+    if (e == hipSuccess) launch_flag_compact(flags, n, offsets.as<uint32_t>(), out, s);
+    if (e == hipSuccess) e = hipGetLastError();
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    release(counts);
+    release(offsets);
+    if (e != hipSuccess) return fail(TGS_ERR_HIP, "flag compaction: %s", hipGetErrorString(e));
+    return TGS_OK;
+}
+
+extern "C" {
+
+int tgs_adam_gather(tgs_adam* a, const int32_t* rows, int64_t n_rows, void* stream) {
+    if (!a || n_rows < 0 || (n_rows > 0 && !rows)) return fail(TGS_ERR_INVALID, "bad argument");
+    hipStream_t s = (hipStream_t)stream;
+    return adam_rebuild(a, n_rows, s, [&](int k, DevBuf& src, DevBuf& dst) {
+        launch_gather_rows(src.p, dst.p, rows, n_rows, 4 * kGroupMult[k], s);
+    });
+}
+
+int tgs_adam_append(tgs_adam* a, int64_t n_new, void* stream) {
+    if (!a || n_new < 0) return fail(TGS_ERR_INVALID, "bad argument");
+    hipStream_t s = (hipStream_t)stream;
+    const int64_t old = a->rows;
+    return adam_rebuild(a, old + n_new, s, [&](int k, DevBuf& src, DevBuf& dst) {
+        const int64_t m = kGroupMult[k];
+        if (old > 0) (void)hipMemcpyAsync(dst.p, src.p, sizeof(float) * (size_t)(m * old), hipMemcpyDeviceToDevice, s);
+        launch_fill_u32(dst.as<uint32_t>() + m * old, 0u, m * n_new, s);
+    });
+}
+
+int tgs_adam_reset_opacity(tgs_adam* a, void* stream) {
+    if (!a) return fail(TGS_ERR_INVALID, "NULL argument");
+    const int64_t words = a->rows > 0 ? a->rows : 0;
+    launch_fill_u32(a->m1[1].as<uint32_t>(), 0u, words, (hipStream_t)stream);
+    launch_fill_u32(a->m2[1].as<uint32_t>(), 0u, words, (hipStream_t)stream);
+    TGS_CHECK_LAUNCH();
+    return TGS_OK;
+}
+
+// ------------------------------------------------------------------ densification
+
+void tgs_pcg32_seed(tgs_pcg32* rng, uint64_t initstate, uint64_t initseq) {
+    if (rng) pcg_seed(rng->state, rng->inc, initstate, initseq);
+}
+
+int tgs_random_logistic(tgs_pcg32* rng, int64_t n, float* out, float mean, float stddev, void* stream) {
+    if (!rng || n < 0 || (n > 0 && !out)) return fail(TGS_ERR_INVALID, "bad argument");
+    launch_random_logistic(rng->state, rng->inc, n, mean, stddev, out, (hipStream_t)stream);
+    TGS_CHECK_LAUNCH();
+    rng->state = pcg_advance(rng->state, rng->inc, (uint64_t)n);
+    return TGS_OK;
+}
+
+int tgs_densify_select(const tgs_gaussians* g, const float* densif, float grad_threshold, float scale_threshold,
+                       int32_t absgrad, uint8_t* flags, int32_t* src_indices, int64_t* n_duplicate,
+                       int64_t* n_split, void* stream) {
+    TGS_TRY(check_gaussians(g, false));
+    if (!n_duplicate || !n_split || (g->n > 0 && (!densif || !flags || !src_indices)))
+        return fail(TGS_ERR_INVALID, "NULL argument");
+    hipStream_t s = (hipStream_t)stream;
+    launch_densify_select(g->n, (const float4*)densif, (const float*)g->scales, grad_threshold, scale_threshold,
+                          absgrad, flags, s);
+    TGS_CHECK_LAUNCH();
+    int64_t grow = 0, dup = 0;
+    TGS_TRY(compact_flags(flags, g->n, src_indices, &grow, &dup, s));
+    *n_duplicate = dup;
+    *n_split = grow - dup;
+    return TGS_OK;
+}
+
+int tgs_densify_apply(const tgs_gaussians* g, int64_t n_old, const int32_t* src_indices, int64_t n_grow,
+                      const uint8_t* flags, const float* rand6, void* stream) {
+    TGS_TRY(check_gaussians(g, false));
+    if (n_old < 0 || n_grow < 0 || n_old + n_grow != g->n)
+        return fail(TGS_ERR_INVALID, "gaussians hold %lld rows, expected %lld + %lld", (long long)g->n,
+                    (long long)n_old, (long long)n_grow);
+    if (n_grow > 0 && (!src_indices || !flags || !rand6)) return fail(TGS_ERR_INVALID, "NULL argument");
+    launch_densify_apply(n_grow, n_old, src_indices, flags, rand6, (float*)g->means, (float*)g->scales,
+                         (float*)g->rotations, (float*)g->opacities, (void*)g->sh0, (void*)g->sh_rest,
+                         g->sh_dtype == TGS_DTYPE_FLOAT16 ? kShF16 : kShF32, (hipStream_t)stream);
+    TGS_CHECK_LAUNCH();
+    return TGS_OK;
+}
+
+int tgs_prune_select(const tgs_gaussians* g, const float* densif, int64_t n_info, float opacity_threshold,
+                     float scale_limit, float radius_limit, int32_t prune_large, uint8_t* alive,
+                     int32_t* kept_indices, int64_t* n_kept, void* stream) {
+    TGS_TRY(check_gaussians(g, false));
+    if (!n_kept || (g->n > 0 && (!alive || !kept_indices)) || n_info < 0 || (n_info > 0 && !densif))
+        return fail(TGS_ERR_INVALID, "NULL argument");
+    hipStream_t s = (hipStream_t)stream;
+    launch_prune_select(g->n, (const float*)g->opacities, (const float*)g->scales, (const float*)g->rotations,
+                        (const float4*)densif, n_info, scale_limit, radius_limit, opacity_threshold, prune_large,
+                        alive, s);
+    TGS_CHECK_LAUNCH();
+    return compact_flags(alive, g->n, kept_indices, n_kept, nullptr, s);
+}
+
+int tgs_gaussians_gather(const tgs_gaussians* src, const tgs_gaussians* dst, const int32_t* rows, void* stream) {
+    TGS_TRY(check_gaussians(src, false));
+    TGS_TRY(check_gaussians(dst, false));
+    if (src->sh_dtype != dst->sh_dtype) return fail(TGS_ERR_INVALID, "SH dtypes differ");
+    if (dst->n > 0 && !rows) return fail(TGS_ERR_INVALID, "rows is NULL");
+    hipStream_t s = (hipStream_t)stream;
+    const int64_t n = dst->n;
+    launch_gather_rows(src->means, dst->means, rows, n, 12, s);
+    launch_gather_rows(src->scales, dst->scales, rows, n, 12, s);
+    launch_gather_rows(src->rotations, dst->rotations, rows, n, 16, s);
+    launch_gather_rows(src->opacities, dst->opacities, rows, n, 4, s);
+    if (src->sh_dtype == TGS_DTYPE_FLOAT16) {
+        launch_gather_rows16(src->sh0, dst->sh0, rows, n, 3, s);
+        launch_gather_rows16(src->sh_rest, dst->sh_rest, rows, n, 45, s);
+    } else {
+        launch_gather_rows(src->sh0, dst->sh0, rows, n, 12, s);
+        launch_gather_rows(src->sh_rest, dst->sh_rest, rows, n, 180, s);
+    }
+    TGS_CHECK_LAUNCH();
+    return TGS_OK;
+}
+
+int tgs_flags_compact(const uint8_t* flags, int64_t n, int32_t* out, int64_t* count, void* stream) {
+    if (!count || n < 0 || (n > 0 && (!flags || !out))) return fail(TGS_ERR_INVALID, "bad argument");
+    return compact_flags(flags, n, out, count, nullptr, (hipStream_t)stream);
+}
+
+int tgs_reset_opacity(const tgs_gaussians* g, float max_opacity, void* stream) {
+    TGS_TRY(check_gaussians(g, false));
+    launch_reset_opacity((float*)g->opacities, g->n, max_opacity, (hipStream_t)stream);
+    TGS_CHECK_LAUNCH();
     return TGS_OK;
 }
 

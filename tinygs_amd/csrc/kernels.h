@@ -133,6 +133,28 @@ void launch_preprocess_backward(const GaussianView& g, const CamParams& cam, con
                                 const float4* records, float* grad2d, const GradView& out, float* densif, int mode,
                                 uint8_t* row_mask, uint4* live, uint4* heavy, uint2* chunk_counts, hipStream_t s);
 
+// ---- densification (tinygs/src/strategy/default.cu, gpu_gaussian.cu:117-170,
+// simple_adam.cu:841-985)
+void launch_random_logistic(uint64_t state, uint64_t inc, int64_t n, float mean, float stddev, float* out,
+                            hipStream_t s);
+int64_t list_chunks(int64_t n);
+// counts[c] = (nonzero flags, flags == 1) of chunk c (list_chunks(n) chunks)
+void launch_flag_count(const uint8_t* flags, int64_t n, uint2* counts, hipStream_t s);
+// indices of the nonzero flags in index order, chunk c's run at offsets[c]
+void launch_flag_compact(const uint8_t* flags, int64_t n, const uint32_t* offsets, int32_t* out, hipStream_t s);
+void launch_densify_select(int64_t n, const float4* info, const float* scales, float grow_grad, float grow_scale,
+                           int absgrad, uint8_t* flags, hipStream_t s);
+void launch_prune_select(int64_t n, const float* opac, const float* scales, const float* rots, const float4* info,
+                         int64_t n_info, float scale_limit, float radius_limit, float min_opacity, int prune_large,
+                         uint8_t* alive, hipStream_t s);
+void launch_densify_apply(int64_t n_grow, int64_t n_old, const int32_t* src, const uint8_t* flags, const float* rnd,
+                          float* means, float* scales, float* rots, float* opac, void* sh0, void* shr, int sh_dtype,
+                          hipStream_t s);
+void launch_gather_rows(const void* src, void* dst, const int32_t* rows, int64_t n_dst, int row_bytes,
+                        hipStream_t s);
+void launch_gather_rows16(const void* src, void* dst, const int32_t* rows, int64_t n_dst, int width, hipStream_t s);
+void launch_reset_opacity(float* opac, int64_t n, float max_opacity, hipStream_t s);
+
 // ---- utilities
 void launch_fill_u32(uint32_t* p, uint32_t value, int64_t n, hipStream_t s);
 

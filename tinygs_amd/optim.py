@@ -66,6 +66,33 @@ class SimpleAdam(OptimizerBase):
     def reset(self, stream=None):
         _lib.check(_lib.load().tgs_adam_reset(self._h, stream_ptr(stream)), "SimpleAdam::reset")
 
+    def remove(self, kept_flag, num_kept: int, stream=None):
+        """SimpleAdam::remove (simple_adam.cu:841-906). The reference builds
+        its row mapping from the optimiser's Gaussians, which StrategyBase has
+        already shrunk to num_kept rows: the kept rows among the first
+        num_kept flags, in order, then row 0 for the remaining moment rows.
+        That mapping is reproduced here."""
+        torch = __import__("torch")
+        rows = torch.zeros(max(num_kept, 1), dtype=torch.int32, device=kept_flag.device)
+        cnt = C.c_int64()
+        L = _lib.load()
+        _lib.check(L.tgs_flags_compact(C.c_void_p(kept_flag.data_ptr()), int(num_kept), C.c_void_p(rows.data_ptr()),
+                                       C.byref(cnt), stream_ptr(stream)), "SimpleAdam::remove")
+        _lib.check(L.tgs_adam_gather(self._h, C.c_void_p(rows.data_ptr()), int(num_kept), stream_ptr(stream)),
+                   "SimpleAdam::remove")
+
+    def duplicate(self, num_duplicate: int, stream=None):
+        """SimpleAdam::duplicate (simple_adam.cu:908-924): zero moment rows
+        for the appended Gaussians."""
+        if num_duplicate <= 0:
+            return
+        _lib.check(_lib.load().tgs_adam_append(self._h, int(num_duplicate), stream_ptr(stream)),
+                   "SimpleAdam::duplicate")
+
+    def reset_opacity(self, stream=None):
+        """SimpleAdam::reset_opacity (simple_adam.cu:981-985)."""
+        _lib.check(_lib.load().tgs_adam_reset_opacity(self._h, stream_ptr(stream)), "SimpleAdam::reset_opacity")
+
     def set_lr(self, lr: float):
         _lib.check(_lib.load().tgs_adam_set_lr(self._h, float(lr)), "set_lr")
 
