@@ -5,6 +5,7 @@ dominant kernel and the CPU oracle's time on the same workload.
 
   python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 3] [--no-cpu-baseline]
   python bench.py --config 4 [--stress-counts N ...]   (fwd+bwd stress sweep, its own JSON line)
+  python bench.py --config 5 [--train-iters K]          (the training loop, its own JSON line)
 
 Prints one JSON line on stdout; a per-stage table goes to stderr.
 """
@@ -210,15 +211,86 @@ def stress_main(args):
     print(json.dumps(out), flush=True)
 
 
+TRAIN_METRIC = "iters/s of the config-5 training loop (fwd+bwd+L1/SSIM+Adam, densification every 100 iters)"
+
+
+def train_main(args):
+    """Config 5: the training loop (Orchestrator with SimpleAdam and
+    DefaultStrategy) on a synthetic 200-view dataset. Reports iterations per
+    second over the whole loop (densification steps included, targets
+    resident in HBM), the Gaussian count, and the mean PSNR over all views at
+    iteration 100 and at the end."""
+    import torch
+
+    from tinygs_amd import scenes
+    from tinygs_amd.data import SimpleDataLoader, SyntheticViewDataset, gaussians_from_arrays
+    from tinygs_amd.optim import create_optimizer
+    from tinygs_amd.rasterizer import create_rasterizer
+    from tinygs_amd.strategy import create_strategy
+    from tinygs_amd.trainer import Orchestrator, OrchestratorConfig
+
+    t0 = time.time()
+    scene = scenes.config5(n_init=args.train_init, n_gt=args.train_gt, n_cameras=args.train_views)
+    ds = SyntheticViewDataset(scene)
+    g = gaussians_from_arrays(scene.init, 0)   # SH degree 0 at the start, as the loop's schedule has it
+    grads = g.gradient_like()
+    opt = create_optimizer("simple_adam", g, grads)
+    strat = create_strategy("default", g, grads, opt)
+    strat.set_params({"refine_every": 100, "start_refine": 100, "end_refine": args.train_iters,
+                      "duplicate_grad_threshold": 2e-4, "pruning_opacity_threshold": 0.005})
+    orch = Orchestrator(OrchestratorConfig(), g, grads, create_rasterizer("fastgs"), opt, SimpleDataLoader(ds),
+                        strategy=strat)
+    torch.cuda.synchronize()
+    print(f"[bench] config5: {args.train_init} initial Gaussians, {args.train_gt} ground truth, "
+          f"{args.train_views} views {scene.width}x{scene.height} (set up in {time.time() - t0:.1f}s)",
+          file=sys.stderr, flush=True)
+    psnr0 = orch.eval_psnr()
+    orch.recompute_scene_scale()
+    first = min(100, args.train_iters)
+    t0 = time.time()
+    for _ in range(first):
+        orch.train_step()
+    torch.cuda.synchronize()
+    t_first = time.time() - t0
+    psnr100 = orch.eval_psnr()
+    n100 = g.size()
+    t1 = time.time()
+    for _ in range(args.train_iters - first):
+        orch.train_step()
+        if orch.m_state.current_step % 100 == 0:
+            print(f"[bench] iter {orch.m_state.current_step}: {g.size()} Gaussians", file=sys.stderr, flush=True)
+    torch.cuda.synchronize()
+    elapsed = t_first + (time.time() - t1)
+    psnr_end = orch.eval_psnr()
+    ips = args.train_iters / elapsed
+    print(f"[bench] {args.train_iters} iterations in {elapsed:.2f}s = {ips:.1f} it/s; PSNR {psnr0:.3f} -> "
+          f"{psnr100:.3f} (iter 100) -> {psnr_end:.3f} dB; {g.size()} Gaussians", file=sys.stderr, flush=True)
+    out = {"metric": TRAIN_METRIC, "value": round(ips, 2), "unit": "iters/s", "n_gpus": 1,
+           "steps": args.train_iters, "warmup": 0, "ms_per_step": round(1e3 / ips, 3), "higher_is_better": True,
+           "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+           "config": {"workload": "config5: Orchestrator loop, SimpleAdam, DefaultStrategy (refine every 100)",
+                      "initial_gaussians": args.train_init, "ground_truth_gaussians": args.train_gt,
+                      "views": args.train_views, "width": scene.width, "height": scene.height,
+                      "parallelism": "single GPU"},
+           "psnr_db": {"start": round(psnr0, 3), "iter100": round(psnr100, 3), "final": round(psnr_end, 3)},
+           "gaussians": {"start": args.train_init, "iter100": n100, "final": g.size()}}
+    print(json.dumps(out), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", type=int, default=3,
-                    help="3: the headline training iteration; 1, 2: the smaller scenes; 4: the fwd+bwd stress sweep")
+                    help="3: the headline training iteration; 1, 2: the smaller scenes; 4: the fwd+bwd stress sweep; "
+                         "5: the training loop")
     ap.add_argument("--stress-counts", type=int, nargs="+", default=[375_000, 750_000, 1_500_000, 3_000_000],
                     help="Gaussian counts of the config-4 sweep")
+    ap.add_argument("--train-iters", type=int, default=1000, help="config 5: training iterations")
+    ap.add_argument("--train-init", type=int, default=500_000, help="config 5: initial Gaussians")
+    ap.add_argument("--train-gt", type=int, default=400_000, help="config 5: ground-truth Gaussians")
+    ap.add_argument("--train-views", type=int, default=200, help="config 5: views")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="instead of the benchmark, run 5 device-to-device copies of MIB MiB (the known-size kernel "
@@ -244,6 +316,8 @@ def main():
 
     if args.config == 4:
         return stress_main(args)
+    if args.config == 5:
+        return train_main(args)
     scene_fn = {1: scenes.config1, 2: scenes.config2, 3: scenes.config3}[args.config]
     t0 = time.time()
     scene = scene_fn()

@@ -166,6 +166,12 @@ int tgs_loss_evaluate(tgs_loss* l, const tgs_loss_context* ctx, float scale, voi
 int tgs_loss_l1_ssim(tgs_loss* l, const tgs_loss_context* ctx, float l1_scale, float ssim_scale, int32_t flags,
                      void* stream);
 
+/* PsnrMetric::evaluate (tinygs/src/loss/psnr.cu:72-128): -10 log10(MSE),
+ * MSE = sum over the padded elements of (saturate(pred) - target)^2 / (W H C),
+ * 100 for a zero MSE. Float32 tiled images of ctx (loss / grad unused).
+ * Synchronises the stream. */
+int tgs_psnr(const tgs_loss_context* ctx, float* psnr, void* stream);
+
 /* ---- SimpleAdam: replaces create_optimizer("simple_adam") / SimpleAdam
  * (tinygs/src/optim/optim.cu:86-105, tinygs/src/optim/simple_adam.cu:406-580). */
 typedef struct tgs_adam_params {
@@ -218,6 +224,9 @@ typedef struct tgs_pcg32 {
 } tgs_pcg32;
 /* pcg32::seed(initstate, initseq) (host only). */
 void tgs_pcg32_seed(tgs_pcg32* rng, uint64_t initstate, uint64_t initseq);
+/* pcg32::next_uint(bound) (pcg32.hpp:68-94, host only): uniform in [0, bound)
+ * by rejection; bound 0 returns next_uint(). */
+uint32_t tgs_pcg32_next_uint(tgs_pcg32* rng, uint32_t bound);
 /* generate_random_logistic(rng, n, out, mean, stddev) (random/device.cuh:38-84):
  * out[i] = logit(u) * stddev * 0.551328895 + mean with the reference's
  * assignment of stream positions to elements; rng advanced by n. */

@@ -95,6 +95,8 @@ SIGNATURES = {
     "tgs_adam_append": ([P, C.c_int64, P], C.c_int),
     "tgs_adam_reset_opacity": ([P, P], C.c_int),
     "tgs_pcg32_seed": ([C.POINTER(tgs_pcg32), C.c_uint64, C.c_uint64], None),
+    "tgs_pcg32_next_uint": ([C.POINTER(tgs_pcg32), C.c_uint32], C.c_uint32),
+    "tgs_psnr": ([C.POINTER(tgs_loss_context), C.POINTER(C.c_float), P], C.c_int),
     "tgs_random_logistic": ([C.POINTER(tgs_pcg32), C.c_int64, P, C.c_float, C.c_float, P], C.c_int),
     "tgs_densify_select": ([C.POINTER(tgs_gaussians), P, C.c_float, C.c_float, C.c_int32, P, P,
                             C.POINTER(C.c_int64), C.POINTER(C.c_int64), P], C.c_int),

@@ -671,6 +671,25 @@ int tgs_loss_l1_ssim(tgs_loss* l, const tgs_loss_context* c, float l1_scale, flo
     return TGS_OK;
 }
 
+int tgs_psnr(const tgs_loss_context* c, float* psnr, void* stream) {
+    if (!c || !psnr || !c->pred || !c->target) return fail(TGS_ERR_INVALID, "NULL argument");
+    if (c->dtype != TGS_DTYPE_FLOAT32) return fail(TGS_ERR_UNSUPPORTED, "PSNR: float32 images only");
+    if (c->width == 0 || c->height == 0 || c->channel == 0) return fail(TGS_ERR_INVALID, "empty image");
+    hipStream_t s = (hipStream_t)stream;
+    static thread_local DevBuf scratch;
+    TGS_TRY(ensure(scratch, sizeof(double) * (size_t)psnr_scratch_doubles(), s));
+    const int64_t npad = (int64_t)((c->width + 7u) / 8u) * ((c->height + 7u) / 8u) * 64 * c->channel;
+    launch_sq_diff_sum((const float*)c->pred, (const float*)c->target, npad, scratch.as<double>(), s);
+    TGS_CHECK_LAUNCH();
+    double sum = 0.0;
+    TGS_HIP(hipMemcpyAsync(&sum, scratch.as<double>() + psnr_scratch_doubles() - 1, sizeof(double),
+                           hipMemcpyDeviceToHost, s));
+    TGS_HIP(hipStreamSynchronize(s));
+    const float mse = (float)sum / (float)((uint64_t)c->width * c->height * c->channel);
+    *psnr = mse == 0.0f ? 100.0f : -10.0f * log10f(mse);
+    return TGS_OK;
+}
+
 // ------------------------------------------------------------------ SimpleAdam
 
 static void default_adam_params(tgs_adam_params& p) {
@@ -946,6 +965,11 @@ int tgs_adam_reset_opacity(tgs_adam* a, void* stream) {
 
 void tgs_pcg32_seed(tgs_pcg32* rng, uint64_t initstate, uint64_t initseq) {
     if (rng) pcg_seed(rng->state, rng->inc, initstate, initseq);
+}
+
+uint32_t tgs_pcg32_next_uint(tgs_pcg32* rng, uint32_t bound) {
+    if (!rng) return 0u;
+    return bound ? pcg_next_bounded(rng->state, rng->inc, bound) : pcg_next(rng->state, rng->inc);
 }
 
 int tgs_random_logistic(tgs_pcg32* rng, int64_t n, float* out, float mean, float stddev, void* stream) {

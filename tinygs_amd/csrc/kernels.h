@@ -133,6 +133,11 @@ void launch_preprocess_backward(const GaussianView& g, const CamParams& cam, con
                                 const float4* records, float* grad2d, const GradView& out, float* densif, int mode,
                                 uint8_t* row_mask, uint4* live, uint4* heavy, uint2* chunk_counts, hipStream_t s);
 
+// ---- PSNR (psnr.cu:72-128): scratch[psnr_scratch_doubles() - 1] receives the
+// sum of (saturate(pred) - target)^2 over the n_padded elements
+int psnr_scratch_doubles();
+void launch_sq_diff_sum(const float* pred, const float* target, int64_t n_padded, double* scratch, hipStream_t s);
+
 // ---- densification (tinygs/src/strategy/default.cu, gpu_gaussian.cu:117-170,
 // simple_adam.cu:841-985)
 void launch_random_logistic(uint64_t state, uint64_t inc, int64_t n, float mean, float stddev, float* out,

@@ -21,6 +21,8 @@
 // term is added before the SSIM term, as two separate reference launches
 // would. SSIM sums differ from the reference's summation order by rounding
 // only (the oracle comparison is normwise 1e-5).
+#include <algorithm>
+
 #include "common.h"
 #include "kernels.h"
 
@@ -351,6 +353,47 @@ void launch_ssim_backward(uint32_t width, uint32_t height, float s, const float*
     if (width == 0 || height == 0) return;
     dim3 grid((width + kOT - 1) / kOT, (height + kOT - 1) / kOT, 3);
     ssim_backward_kernel<<<grid, 256, 0, st>>>(width, height, s, pred, target, grad, dm_mu, dm_s1, dm_s12);
+}
+
+// ------------------------------------------------------------------ PSNR
+
+// psnr.cu:24-36 and :72-128: sum over the padded elements of
+// (saturate(pred) - target)^2. One double partial per workgroup (grid-strided
+// float4 reads, wave then workgroup reduction), then one workgroup adds the
+// partials in index order: the same sum on every run.
+__global__ void __launch_bounds__(256) sq_diff_partial_kernel(const float4* __restrict__ pred,
+                                                               const float4* __restrict__ target, int64_t n4,
+                                                               double* __restrict__ partial) {
+    __shared__ double s_w[4];
+    double acc = 0.0;
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n4; i += (int64_t)gridDim.x * 256) {
+        const float4 p = pred[i], t = target[i];
+        const float d0 = saturate(p.x) - t.x, d1 = saturate(p.y) - t.y;
+        const float d2 = saturate(p.z) - t.z, d3 = saturate(p.w) - t.w;
+        acc += (double)(d0 * d0) + (double)(d1 * d1) + (double)(d2 * d2) + (double)(d3 * d3);
+    }
+    for (int off = 32; off > 0; off >>= 1) acc += __shfl_down(acc, off, 64);
+    if ((threadIdx.x & 63u) == 0u) s_w[threadIdx.x >> 6] = acc;
+    __syncthreads();
+    if (threadIdx.x == 0) partial[blockIdx.x] = (s_w[0] + s_w[1]) + (s_w[2] + s_w[3]);
+}
+
+__global__ void __launch_bounds__(64) sum_partials_kernel(const double* __restrict__ partial, int n,
+                                                          double* __restrict__ out) {
+    double acc = 0.0;
+    for (int i = (int)threadIdx.x; i < n; i += 64) acc += partial[i];
+    for (int off = 32; off > 0; off >>= 1) acc += __shfl_down(acc, off, 64);
+    if (threadIdx.x == 0) *out = acc;
+}
+
+constexpr int kPsnrBlocks = 1024;
+int psnr_scratch_doubles() { return kPsnrBlocks + 1; }
+
+void launch_sq_diff_sum(const float* pred, const float* target, int64_t n_padded, double* scratch, hipStream_t s) {
+    const int64_t n4 = n_padded / 4;   // padded planes hold whole 8x8 blocks
+    const int blocks = (int)std::min<int64_t>(kPsnrBlocks, std::max<int64_t>(1, (n4 + 255) / 256));
+    sq_diff_partial_kernel<<<blocks, 256, 0, s>>>((const float4*)pred, (const float4*)target, n4, scratch);
+    sum_partials_kernel<<<1, 64, 0, s>>>(scratch, blocks, scratch + kPsnrBlocks);
 }
 
 }  // namespace tgs

@@ -42,6 +42,16 @@ TGS_HD float pcg_float(uint64_t& state, uint64_t inc) {
     return u2f((pcg_next(state, inc) >> 9) | 0x3f800000u) - 1.0f;
 }
 
+// pcg32::next_uint(bound) (pcg32.hpp:68-94): rejection of the low
+// (2^32 - bound) % bound outputs keeps the result unbiased
+inline uint32_t pcg_next_bounded(uint64_t& state, uint64_t inc, uint32_t bound) {
+    const uint32_t threshold = (~bound + 1u) % bound;
+    for (;;) {
+        const uint32_t r = pcg_next(state, inc);
+        if (r >= threshold) return r % bound;
+    }
+}
+
 // pcg32::seed(initstate, initseq) (pcg32.hpp:45-53)
 inline void pcg_seed(uint64_t& state, uint64_t& inc, uint64_t initstate, uint64_t initseq) {
     state = 0u;

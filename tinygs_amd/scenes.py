@@ -1,4 +1,4 @@
-"""Seeded synthetic scenes for the FastGS training path (configs 1-4).
+"""Seeded synthetic scenes for the FastGS training path (configs 1-5).
 
 Parameters follow the SoA layout of tinygs's GPUGaussian3d
 (tinygs/include/tinygs/core/gpu_gaussian.hpp:67-72): means (N,3), scales (N,3)
@@ -203,6 +203,48 @@ def config4(seed: int = 4, n: int = 3_000_000, width: int = 3840, height: int = 
     sh_rest = r[5].normal(0.0, 0.05, (n, 15, 3)).astype(np.float32)
     cam = Camera(width, height, focal, focal, width / 2.0, height / 2.0, np.eye(4))
     return Scene(means, scales, rots, opac, sh0, sh_rest, 3, cam, _target(r[6], cam), "config4")
+
+
+def config2_gaussians(seed: int, n: int) -> dict:
+    """Gaussian parameters drawn as in config 2 (means ~N(0,1)^3 clipped to a
+    radius-2 ball, log-scales ~N(-4,0.5), opacity logits ~N(0,1.5), SH degree
+    3: DC ~U(0,1), higher bands ~N(0,0.05))."""
+    r = _streams(seed, 6)
+    means = r[0].standard_normal((n, 3))
+    norm = np.linalg.norm(means, axis=1, keepdims=True)
+    means = np.where(norm > 2.0, means * (2.0 / np.maximum(norm, 1e-12)), means).astype(np.float32)
+    return {"means": means, "scales": r[1].normal(-4.0, 0.5, (n, 3)).astype(np.float32),
+            "rotations": _unit_quats(r[2], n), "opacities": r[3].normal(0.0, 1.5, n).astype(np.float32),
+            "sh0": r[4].uniform(0.0, 1.0, (n, 3)).astype(np.float32),
+            "sh_rest": r[5].normal(0.0, 0.05, (n, 15, 3)).astype(np.float32)}
+
+
+@dataclasses.dataclass
+class TrainingScene:
+    """a ground-truth Gaussian set rendered from many
+    cameras (the targets) and an initial Gaussian set to train."""
+    gt: dict
+    init: dict
+    cameras: list
+    width: int
+    height: int
+    name: str = "config5"
+
+
+def config5(seed: int = 5, n_init: int = 500_000, n_gt: int = 400_000, width: int = 1600, height: int = 1060,
+            n_cameras: int = 200, radius: float = 4.0) -> TrainingScene:
+    """500k initial Gaussians seeded as in config 2,
+    width x height views from n_cameras random cameras on a sphere of the
+    given radius looking at the origin, targets rendered from a fixed seeded
+    ground-truth set of 400k Gaussians (drawn as in config 2, other seed).
+    The focal length keeps config 2's 1100 px per 800 px of width."""
+    r = _streams(seed, 3)
+    f = 1100.0 * width / 800.0
+    # near / far of SimpleDataLoader::next (simple.cpp:60-61)
+    cams = [Camera(width, height, f, f, width / 2.0, height / 2.0, look_at(radius * _random_unit(r[0])), 0.1, 100.0)
+            for _ in range(n_cameras)]
+    return TrainingScene(config2_gaussians(seed + 1000, n_gt), config2_gaussians(seed + 2000, n_init), cams, width,
+                         height)
 
 
 CONFIGS = {1: config1, 2: config2, 3: config3, 4: config4}
