@@ -103,9 +103,11 @@ def render_targets(gt: dict, cameras) -> list:
 
 class Trainer:
     def __init__(self, scene, strategy_params: dict, lr: dict | None = None, eps: float = 1e-8,
-                 sh_degree_interval: int = 1000, max_sh_degree: int = 3, l1_w: float = 0.8, ssim_w: float = 0.2):
+                 sh_degree_interval: int = 1000, max_sh_degree: int = 3, l1_w: float = 0.8, ssim_w: float = 0.2,
+                 targets: list | None = None):
         self.cameras = scene.cameras
-        self.targets = render_targets(scene.gt, scene.cameras)
+        # targets[i] may be None for views the run never reads
+        self.targets = targets if targets is not None else render_targets(scene.gt, scene.cameras)
         self.p = {k: np.asarray(v, F).reshape(v.shape[0], -1).copy() if k != "opacities" else np.asarray(v, F).copy()
                   for k, v in scene.init.items()}
         self.p["sh_rest"] = self.p["sh_rest"].reshape(-1, 45)

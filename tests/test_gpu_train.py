@@ -53,3 +53,26 @@ def test_config5_reduced_trajectory_matches_oracle(hip):
             assert g.size() == traj["gaussians"][key], it
             p = orch.eval_psnr(fx["eval_views"])
             assert abs(p - traj["psnr"][key]) < 0.02, (it, p, traj["psnr"][key])
+
+
+@pytest.mark.parametrize("wh", [(37, 21), (64, 48), (1, 1)])
+def test_psnr_closed_form(hip, wh):
+    """tgs_psnr against -10 log10(MSE) in double precision: MSE over every
+    padded element of (saturate(pred) - target)^2 divided by W H C
+    (psnr.cu:72-128), with prediction values outside [0, 1] and nonzero
+    padding; 100 for identical images."""
+    import torch
+    from tinygs_amd.core import Image
+    from tinygs_amd.image import ImageShape
+    from tinygs_amd.trainer import PsnrMetric
+    shape = ImageShape(*wh)
+    g = np.random.default_rng(wh[0])
+    pred = g.uniform(-0.3, 1.3, shape.padded_size).astype(np.float32)
+    target = g.uniform(0.0, 1.0, shape.padded_size).astype(np.float32)
+    a = Image(shape, data=torch.from_numpy(pred).cuda())
+    b = Image(shape, data=torch.from_numpy(target).cuda())
+    got = PsnrMetric().evaluate(a, b)
+    d = np.clip(pred.astype(np.float64), 0.0, 1.0) - target
+    want = -10.0 * np.log10((d * d).sum() / shape.size())
+    assert abs(got - want) < 1e-4 * max(1.0, abs(want)), (got, want)
+    assert PsnrMetric().evaluate(b, b) == 100.0

@@ -91,3 +91,15 @@ def test_scene_scale_restatement():
     s = T.scene_scale(pts, cams)
     m = pts.mean(0)
     assert abs(s - max(np.linalg.norm(c - m) for c in cams)) < 1e-4
+
+
+def test_oracle_psnr_closed_form():
+    from tinygs_amd.image import ImageShape
+    shape = ImageShape(13, 9)
+    g = np.random.default_rng(3)
+    pred = g.uniform(-0.5, 1.5, shape.padded_size).astype(np.float32)
+    target = g.uniform(0.0, 1.0, shape.padded_size).astype(np.float32)
+    d = np.clip(pred.astype(np.float64), 0.0, 1.0) - target
+    want = -10.0 * math.log10((d * d).sum() / shape.size())
+    assert abs(T.psnr(pred, target, shape) - want) < 1e-4
+    assert T.psnr(target, target, shape) == 100.0
