@@ -32,6 +32,7 @@ extern "C" {
 
 #define TGS_DTYPE_FLOAT32 0
 #define TGS_DTYPE_FLOAT16 1
+#define TGS_DTYPE_UINT8 2   /* images only: tgs_image_* and tgs_convert */
 
 /* SoA Gaussian parameters (or their gradients), as GPUGaussian3d
  * (tinygs/include/tinygs/core/gpu_gaussian.hpp:9-73): means[3n], scales[3n]
@@ -258,6 +259,61 @@ int tgs_gaussians_gather(const tgs_gaussians* src, const tgs_gaussians* dst, con
 int tgs_flags_compact(const uint8_t* flags, int64_t n, int32_t* out, int64_t* count, void* stream);
 /* reset_opacity (default.cu:26-37): opacity = logit(min(sigmoid(opacity), max_opacity)). */
 int tgs_reset_opacity(const tgs_gaussians* g, float max_opacity, void* stream);
+
+/* ---- on-disk formats: PLY (tinygs/src/core/pointcloud.cpp:19-240, written
+ * through hapPLY, tinygs/src/core/happly.h). */
+/* save_ply(filename, gaussians, full_features) (pointcloud.cpp:111-240), as
+ * the orchestrator's export calls it (tinygs/src/orchestrator.cu:581-583) but
+ * from the device arrays of g: a binary little-endian PLY with hapPLY's header
+ * and one "vertex" element of g->n rows: x y z, red green blue (uchar), and
+ * with full_features f_dc_r/g/b, f_rest_{r,g,b}_k (k = 0..14), opacity,
+ * scale_0..2, rot_w rot_x rot_y rot_z. fp16 SH are written as float. The rows
+ * are packed on the device; synchronises the stream. */
+int tgs_ply_save(const char* filename, const tgs_gaussians* g, int32_t full_features, void* stream);
+/* Vertex count and contents of a PLY file (ascii or binary). format: 0 ascii,
+ * 1 binary little endian, 2 binary big endian. has_gaussians: every property
+ * tgs_ply_load_gaussians needs is present. No counterpart in the reference
+ * (its hapPLY reader parses the header in load_ply, pointcloud.cpp:75-92). */
+typedef struct tgs_ply_info {
+    int64_t n_vertices;
+    int32_t format;
+    int32_t has_gaussians;
+    int32_t has_colors;
+} tgs_ply_info;
+int tgs_ply_read_info(const char* filename, tgs_ply_info* info);
+/* The inverse of save_ply with full features, to restart from an exported
+ * file (the reference has no Gaussian reader; it exports PLY at evaluation
+ * and keeps no other checkpoint). g (device arrays, g->n == the file's vertex
+ * count) receives every parameter; properties are found by name in any order
+ * and type, under the reference's names or the common 3DGS ones (f_dc_0..2,
+ * f_rest_i with i = channel * 15 + k, rot_0..3). fp16 SH are rounded to
+ * nearest even. Synchronises the stream. */
+int tgs_ply_load_gaussians(const char* filename, const tgs_gaussians* g, void* stream);
+/* load_point_cloud (pointcloud.cpp:94-109): ".ply" -> load_ply (:75-92,
+ * positions and uchar colours / 255); ".txt" -> load_from_colmap (:19-73,
+ * COLMAP points3D.txt). Host arrays points[3 n], colors[3 n]. With points ==
+ * NULL only *n is set (the count); otherwise *n is the capacity on entry and
+ * the count on return. */
+int tgs_point_cloud_load(const char* filename, int64_t* n, float* points, float* colors);
+
+/* ---- image layout converters (tinygs/src/utils/image_format.cu:68-139;
+ * tinygs/src/dataloader/dataloader.cu:18-95). Tiled images are channel-planar,
+ * 8x8-tiled and padded to multiples of 8, of type TGS_DTYPE_FLOAT32 / FLOAT16
+ * / UINT8; float <- u8 is (1 / 255) * v, u8 <- float is the truncation of
+ * clamp(255 v, 0, 255) (orchestrator.cu:896-937). All device pointers. */
+/* from_cv2 (image_format.cu:68-90) with bgr = 1 (channels must be 3), an RGB /
+ * any-channel interleaved image with bgr = 0; dst_dtype FLOAT32 / FLOAT16 folds
+ * the loader's widening in. The padding is written as zero (the reference
+ * leaves it unwritten). */
+int tgs_image_from_hwc_u8(const uint8_t* src, uint32_t width, uint32_t height, uint32_t channels, int32_t bgr,
+                          void* dst, int32_t dst_dtype, void* stream);
+/* to_cv2 (image_format.cu:93-114) for a UINT8 source, Orchestrator::to_opencv
+ * (orchestrator.cu:896-937) for a FLOAT32 / FLOAT16 one (bgr = 1). */
+int tgs_image_to_hwc_u8(const void* src, int32_t src_dtype, uint32_t width, uint32_t height, uint32_t channels,
+                        int32_t bgr, uint8_t* dst, void* stream);
+/* Elementwise: half_to_float_gpu / float_to_half_gpu (image_format.cu:117-139),
+ * convert_u8_float / convert_u8_half (dataloader.cu:26-95), and u8 <- float. */
+int tgs_convert(const void* src, int32_t src_dtype, void* dst, int32_t dst_dtype, int64_t n, void* stream);
 
 /* ---- measurement (no counterpart in the reference, which uses NVTX ranges,
  * tinygs/src/rasterizer/fastgs_ours/nvtx_gs.h): HIP events recorded on the

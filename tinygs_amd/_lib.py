@@ -16,6 +16,7 @@ LIB_PATH = os.path.join(HERE, "libtinygs_amd.so")
 
 TGS_DTYPE_FLOAT32 = 0
 TGS_DTYPE_FLOAT16 = 1
+TGS_DTYPE_UINT8 = 2
 TGS_LOSS_ASSIGN = 1
 TGS_BACKWARD_ASSIGN = 1
 TGS_BACKWARD_SPARSE = 2
@@ -58,6 +59,11 @@ class tgs_adam_params(C.Structure):
                 ("shs_lr", C.c_float), ("opacities_lr", C.c_float), ("scales_lr", C.c_float),
                 ("rotations_lr", C.c_float), ("max_grad_1", C.c_float), ("opacities_l1", C.c_float),
                 ("scales_l1", C.c_float), ("decay_mean", C.c_int32)]
+
+
+class tgs_ply_info(C.Structure):
+    _fields_ = [("n_vertices", C.c_int64), ("format", C.c_int32), ("has_gaussians", C.c_int32),
+                ("has_colors", C.c_int32)]
 
 
 P = C.c_void_p
@@ -106,6 +112,13 @@ SIGNATURES = {
     "tgs_gaussians_gather": ([C.POINTER(tgs_gaussians), C.POINTER(tgs_gaussians), P, P], C.c_int),
     "tgs_flags_compact": ([P, C.c_int64, P, C.POINTER(C.c_int64), P], C.c_int),
     "tgs_reset_opacity": ([C.POINTER(tgs_gaussians), C.c_float, P], C.c_int),
+    "tgs_ply_save": ([C.c_char_p, C.POINTER(tgs_gaussians), C.c_int32, P], C.c_int),
+    "tgs_ply_read_info": ([C.c_char_p, C.POINTER(tgs_ply_info)], C.c_int),
+    "tgs_ply_load_gaussians": ([C.c_char_p, C.POINTER(tgs_gaussians), P], C.c_int),
+    "tgs_point_cloud_load": ([C.c_char_p, C.POINTER(C.c_int64), P, P], C.c_int),
+    "tgs_image_from_hwc_u8": ([P, C.c_uint32, C.c_uint32, C.c_uint32, C.c_int32, P, C.c_int32, P], C.c_int),
+    "tgs_image_to_hwc_u8": ([P, C.c_int32, C.c_uint32, C.c_uint32, C.c_uint32, C.c_int32, P, P], C.c_int),
+    "tgs_convert": ([P, C.c_int32, P, C.c_int32, C.c_int64, P], C.c_int),
     "tgs_profiling_set": ([C.c_uint32], C.c_int),
     "tgs_profiling_read": ([C.c_int32, C.POINTER(C.c_double), C.POINTER(C.c_int64), C.c_int32], C.c_int),
     "tgs_stage_name": ([C.c_int32], C.c_char_p),

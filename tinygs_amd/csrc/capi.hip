@@ -23,10 +23,11 @@
 #include "common.h"
 #include "kernels.h"
 #include "pcg32.h"
+#include "status.h"
 
 using namespace tgs;
 
-namespace {
+namespace tgs {
 
 thread_local std::string g_error;
 
@@ -40,19 +41,9 @@ int fail(int code, const char* fmt, ...) {
     return code;
 }
 
-#define TGS_HIP(call)                                                                                  \
-    do {                                                                                               \
-        hipError_t e_ = (call);                                                                        \
-        if (e_ != hipSuccess) return fail(TGS_ERR_HIP, "%s failed at %s:%d: %s", #call, __FILE__, __LINE__, \
-                                          hipGetErrorString(e_));                                      \
-    } while (0)
+}  // namespace tgs
 
-#define TGS_CHECK_LAUNCH()                                                                             \
-    do {                                                                                               \
-        hipError_t e_ = hipGetLastError();                                                             \
-        if (e_ != hipSuccess) return fail(TGS_ERR_HIP, "kernel launch failed at %s:%d: %s", __FILE__, __LINE__, \
-                                          hipGetErrorString(e_));                                      \
-    } while (0)
+namespace {
 
 struct DevBuf {
     void* p = nullptr;
@@ -82,12 +73,6 @@ void release(DevBuf& b) {
     b.p = nullptr;
     b.bytes = 0;
 }
-
-#define TGS_TRY(expr)                  \
-    do {                               \
-        int rc_ = (expr);              \
-        if (rc_ != TGS_OK) return rc_; \
-    } while (0)
 
 // ---- stage timing: HIP events recorded on the launch stream around the
 // stages selected by tgs_profiling_set (process-wide, single host thread).
