@@ -104,12 +104,23 @@ int tgs_rasterizer_backward(tgs_rasterizer* r, const void* grad_image, const voi
  * only the marked rows. No counterpart in the reference: it spares writing
  * and re-reading the zero rows (most rows at 1M Gaussians). */
 #define TGS_BACKWARD_SPARSE 2
+/* TGS_BACKWARD_POSE: also compute the pose-optimisation gradient dL/dw2c of
+ * FastGSRasterizer::backward with enable_pose_opt (fastgs.cu:264-271,373-383;
+ * kernels_backward.cuh:256-269; backward.cu:332-348): the sum over the
+ * primitives with a gradient of dL/dmean_cam[k] * (mean, 1) in row k < 3,
+ * row 3 zero; the mean's path only, as in the reference. Read it with
+ * tgs_rasterizer_grad_w2c. Combines with the other flags. */
+#define TGS_BACKWARD_POSE 4
 int tgs_rasterizer_backward_ex(tgs_rasterizer* r, const void* grad_image, const void* image,
                                const tgs_gaussians* grads, void* densification_info, int32_t flags, void* stream);
 /* Device byte mask [n] of the last TGS_BACKWARD_SPARSE backward (1: row
  * assigned, 0: row skipped, its gradient is zero). Valid until the next
  * backward or the next forward that grows the Gaussian count. */
 int tgs_rasterizer_grad_row_mask(tgs_rasterizer* r, const uint8_t** mask);
+/* ctx.grad_input.w2c of the last TGS_BACKWARD_POSE backward (fastgs.cu:373-383):
+ * 16 floats into host memory, glm column-major like tgs_camera.w2c
+ * (w2c_grad[4 c + r] = dL/dw2c(r, c)). Synchronises the stream. */
+int tgs_rasterizer_grad_w2c(tgs_rasterizer* r, float* w2c_grad, void* stream);
 /* Counts of the last forward: visible primitives, instances, tiles. */
 int tgs_rasterizer_counts(tgs_rasterizer* r, int64_t* n_visible, int64_t* n_instances, int64_t* n_tiles);
 

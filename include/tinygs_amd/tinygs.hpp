@@ -448,9 +448,16 @@ public:
         if (ctx.gaussians_grad->size() != m_gaussians->size())
             throw std::runtime_error("FastGSRasterizer::backward: gradient size does not match the Gaussians");
         const tgs_gaussians g = ctx.gaussians_grad->to_c();
+        const int32_t flags = (assign ? TGS_BACKWARD_ASSIGN : 0) | (m_pose_opt ? TGS_BACKWARD_POSE : 0);
         throw_on(tgs_rasterizer_backward_ex(m_handle, ctx.grad_output.image.data, ctx.fwd_output.image.data, &g,
-                                            densif(ctx), assign ? TGS_BACKWARD_ASSIGN : 0, ctx.stream),
+                                            densif(ctx), flags, ctx.stream),
                  "FastGSRasterizer::backward");
+        // fastgs.cu:373-383: grad_input.w2c is the pose gradient, zero without pose optimisation
+        if (m_pose_opt)
+            throw_on(tgs_rasterizer_grad_w2c(m_handle, ctx.grad_input.w2c.data(), ctx.stream),
+                     "FastGSRasterizer::backward");
+        else
+            ctx.grad_input.w2c.fill(0.0f);
     }
 
     // Visible primitives, instances and tiles of the last forward.
@@ -460,16 +467,22 @@ public:
         return {v, i, t};
     }
 
-    ParamMap get_params() const override { return {{"f16_grad_scaler", 1.0}, {"enable_pose_opt", 0.0}}; }
+    // enable_pose_opt turns on the pose gradient (FastGSRasterizerParams,
+    // tinygs/include/tinygs/rasterizer/fastgs.hpp:6-12). The reference's
+    // set_params ignores its argument (fastgs.cu:398), so there the flag keeps
+    // its default (off); here it can be set.
+    ParamMap get_params() const override {
+        return {{"f16_grad_scaler", 1.0}, {"enable_pose_opt", m_pose_opt ? 1.0 : 0.0}};
+    }
     void set_params(const ParamMap& p) override {
         auto it = p.find("enable_pose_opt");
-        if (it != p.end() && it->second != 0.0)
-            throw std::runtime_error("FastGSRasterizer: pose optimisation is not supported");
+        if (it != p.end()) m_pose_opt = it->second != 0.0;
     }
 
     tgs_rasterizer* handle() const { return m_handle; }
 
 private:
+    bool m_pose_opt = false;
     void bind() {
         const tgs_gaussians g = m_gaussians->to_c();
         throw_on(tgs_rasterizer_set_gaussians(m_handle, &g), "FastGSRasterizer::set_gaussians");

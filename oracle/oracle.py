@@ -65,7 +65,7 @@ def _declare(L):
         fn.restype = None
         fn = getattr(L, pfx + "preprocess_backward")
         fn.argtypes = [C.c_int64, rp, rp, rp, rp, C.c_int, rp, u32p, rp, rp, rp, rp,
-                       rp, rp, rp, rp, rp, C.c_void_p, C.c_int]
+                       rp, rp, rp, rp, rp, C.c_void_p, C.c_int, C.c_void_p]
         fn.restype = None
         fn = getattr(L, pfx + "l1")
         fn.argtypes = [C.c_int64, C.c_int64, rp, rp, C.c_void_p, C.c_void_p, R]
@@ -221,7 +221,10 @@ def blend_backward(scene, pre, bins, fwd, grad_image, prec="f", exact_grad=False
     return g
 
 
-def preprocess_backward(scene, pre, g2d, prec="f", prm=None, cam=None, exact_grad=False, densif=None):
+def preprocess_backward(scene, pre, g2d, prec="f", prm=None, cam=None, exact_grad=False, densif=None,
+                        grad_w2c=None):
+    """grad_w2c: optional float array of 16 (column-major) that accumulates
+    the pose gradient."""
     L = lib()
     dt = _dt(prec)
     n = scene.n
@@ -233,7 +236,8 @@ def preprocess_backward(scene, pre, g2d, prec="f", prm=None, cam=None, exact_gra
     getattr(L, f"orc_{prec}_preprocess_backward")(
         n, prm["means"], prm["scales"], prm["rotations"], prm["sh_rest"], bases, cam, pre["n_touched"],
         g2d["grad_mean2d"], g2d["grad_conic"], g2d["absgrad"], g2d["grad_color"],
-        out["means"], out["scales"], out["rotations"], out["sh0"], out["sh_rest"], _ptr(densif), int(exact_grad))
+        out["means"], out["scales"], out["rotations"], out["sh0"], out["sh_rest"], _ptr(densif), int(exact_grad),
+        _ptr(grad_w2c))
     out["opacities"] = g2d["grad_opacity"].copy()
     return out
 

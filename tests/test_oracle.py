@@ -512,3 +512,64 @@ def test_adam_learning_rate_rules(orc):
                         "scales": 5e-3, "shs": 5e-3})
     assert np.isclose(lrs["means"], 3.2e-4) and np.isclose(lrs["sh_rest"], 2.5e-4)
     assert np.isclose(lrs["sh0"], 5e-3)
+
+
+# ---------------------------------------------------------------- pose-optimisation gradient
+
+def test_pose_gradient_translation_matches_fd(orc):
+    """dL/dw2c translation column (kernels_backward.cuh:256-269 summed as
+    backward.cu:332-345) against central differences of the loss in the
+    translation entries of w2c. With SH degree 0 the camera centre does not
+    enter the image, so the mean path the reference differentiates is the
+    whole derivative in t."""
+    s = _fd_scene(31, deg=0)
+    shape = s.camera.shape
+    weights = np.random.default_rng(131).uniform(-1, 1, shape.padded_size)
+    prm = orc.params(s, "d")
+    cam = orc.cam_array(s.camera, "d")
+    pre = orc.preprocess(s, "d", prm=prm, cam=cam)
+    bins = orc.bin(s, pre, "d")
+    fwd = orc.blend_forward(s, pre, bins, "d")
+    g2d = orc.blend_backward(s, pre, bins, fwd, weights, "d", exact_grad=True)
+    gw = np.zeros(16)
+    orc.preprocess_backward(s, pre, g2d, "d", prm=prm, cam=cam, exact_grad=True, grad_w2c=gw)
+    assert np.all(gw[3::4] == 0.0)   # row 3 of the gradient is zero
+
+    def loss(c):
+        p = orc.preprocess(s, "d", prm=prm, cam=c)
+        b = orc.bin(s, p, "d")
+        return float(np.dot(orc.blend_forward(s, p, b, "d")["image"], weights))
+
+    h = 1e-6
+    for k in range(3):
+        cp, cm = cam.copy(), cam.copy()
+        cp[6 + 4 * k + 3] += h
+        cm[6 + 4 * k + 3] -= h
+        fd = (loss(cp) - loss(cm)) / (2 * h)
+        assert abs(gw[12 + k] - fd) <= 1e-5 * (abs(fd) + np.abs(gw).max()), (k, gw[12 + k], fd)
+
+
+def test_pose_gradient_is_outer_product_of_mean_gradients(orc):
+    """With SH degree 0 the mean gradient is R^T dL/dmean_cam, so the pose
+    gradient's rotation block is sum_i (R dL/dmean_i) mean_i^T and its
+    translation column sum_i R dL/dmean_i (a transposed or dropped factor
+    fails this)."""
+    s = _fd_scene(32, n=40, deg=0)
+    weights = np.random.default_rng(132).uniform(-1, 1, s.camera.shape.padded_size)
+    prm = orc.params(s, "d")
+    pre = orc.preprocess(s, "d", prm=prm)
+    bins = orc.bin(s, pre, "d")
+    fwd = orc.blend_forward(s, pre, bins, "d")
+    g2d = orc.blend_backward(s, pre, bins, fwd, weights, "d")
+    gw = np.zeros(16)
+    grads = orc.preprocess_backward(s, pre, g2d, "d", prm=prm, grad_w2c=gw)
+    # R is the float32 rounding of a rotation (R R^T = I to ~5e-8), so the
+    # identity holds to that relative accuracy
+    R = s.camera.w2c[:3, :3].astype(np.float32).astype(np.float64)
+    dc = grads["means"].reshape(-1, 3) @ R.T           # rows: R g_i
+    m = prm["means"].reshape(-1, 3)
+    G = gw.reshape(4, 4).T                               # row-major dL/dw2c
+    tol = 1e-6 * np.abs(G).max()
+    assert np.max(np.abs(G[:3, :3] - dc.T @ m)) < tol
+    assert np.max(np.abs(G[:3, 3] - dc.sum(0))) < tol
+    assert np.abs(G).max() > 0

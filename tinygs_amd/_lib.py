@@ -20,6 +20,7 @@ TGS_DTYPE_UINT8 = 2
 TGS_LOSS_ASSIGN = 1
 TGS_BACKWARD_ASSIGN = 1
 TGS_BACKWARD_SPARSE = 2
+TGS_BACKWARD_POSE = 4
 
 _lib = None
 _hip = None
@@ -94,6 +95,7 @@ SIGNATURES = {
     "tgs_adam_step": ([P, C.c_float, P], C.c_int),
     "tgs_adam_step_masked": ([P, C.c_float, P, P], C.c_int),
     "tgs_rasterizer_grad_row_mask": ([P, PP], C.c_int),
+    "tgs_rasterizer_grad_w2c": ([P, C.POINTER(C.c_float), P], C.c_int),
     "tgs_adam_reset": ([P, P], C.c_int),
     "tgs_adam_global_steps": ([P], C.c_int64),
     "tgs_adam_moments": ([P, C.c_int32, C.POINTER(C.c_void_p), C.POINTER(C.c_void_p)], C.c_int),

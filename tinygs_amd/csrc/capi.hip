@@ -215,6 +215,8 @@ struct tgs_rasterizer {
     DevBuf live, heavy, chunk_counts;   // preprocess backward: per-chunk lists of primitives with records
     DevBuf row_mask;     // per-primitive byte mask of the last sparse backward
     bool row_mask_valid = false;
+    DevBuf pose_partial, pose_grad;   // pose gradient: per-chunk partial sums, the 4 x 4 result
+    bool pose_valid = false;
     // temp
     DevBuf grad2d;
     DevBuf radix_counts;   // per-workgroup digit counts of the radix passes
@@ -301,7 +303,7 @@ int tgs_rasterizer_destroy(tgs_rasterizer* r) {
                      &r->ikeys[1], &r->ivals[0], &r->ivals[1], &r->ranges, &r->tile_max, &r->n_contrib,
                      &r->ckpt, &r->items, &r->tile_loaded, &r->first_slot,
                      &r->rec_count, &r->records, &r->heavy, &r->live, &r->chunk_counts, &r->row_mask, &r->grad2d,
-                     &r->bin_ctl, &r->lb_status};
+                     &r->pose_partial, &r->pose_grad, &r->bin_ctl, &r->lb_status};
     for (DevBuf* b : all) release(*b);
     if (r->h_counters) (void)hipHostFree(r->h_counters);
     if (r->ev_counts) (void)hipEventDestroy(r->ev_counts);
@@ -344,6 +346,7 @@ int tgs_rasterizer_forward(tgs_rasterizer* r, const tgs_camera* camera, void* im
     TGS_TRY(build_camera(camera, cam));
     r->fwd_done = false;
     r->row_mask_valid = false;
+    r->pose_valid = false;
     const int64_t n = r->g.n;
     const uint32_t T = cam.grid_w * cam.grid_h;
     const size_t cs = (size_t)cam.tiled_w * cam.tiled_h * 64u;
@@ -483,13 +486,19 @@ int tgs_rasterizer_backward_ex(tgs_rasterizer* r, const void* grad_image, const 
     TGS_TRY(ensure(r->heavy, sizeof(uint4) * (size_t)(n > 0 ? n : 1), s));
     TGS_TRY(ensure(r->live, sizeof(uint4) * (size_t)(n > 0 ? n : 1), s));
     TGS_TRY(ensure(r->chunk_counts, sizeof(uint2) * (size_t)std::max<int64_t>(pb_chunks(n), 1), s));
-    if (flags & ~(TGS_BACKWARD_ASSIGN | TGS_BACKWARD_SPARSE))
+    if (flags & ~(TGS_BACKWARD_ASSIGN | TGS_BACKWARD_SPARSE | TGS_BACKWARD_POSE))
         return fail(TGS_ERR_INVALID, "unknown backward flags 0x%x", flags);
     if ((flags & TGS_BACKWARD_ASSIGN) && (flags & TGS_BACKWARD_SPARSE))
         return fail(TGS_ERR_INVALID, "TGS_BACKWARD_ASSIGN and TGS_BACKWARD_SPARSE are exclusive");
     const int mode = (flags & TGS_BACKWARD_SPARSE) ? kGradSparse : ((flags & TGS_BACKWARD_ASSIGN) ? kGradAssign : kGradAccumulate);
     if (mode == kGradSparse) TGS_TRY(ensure(r->row_mask, (size_t)(n > 0 ? n : 1), s));
     r->row_mask_valid = false;
+    r->pose_valid = false;
+    const bool pose = (flags & TGS_BACKWARD_POSE) != 0;
+    if (pose) {
+        TGS_TRY(ensure(r->pose_partial, sizeof(float) * 12 * (size_t)std::max<int64_t>(pb_chunks(n), 1), s));
+        TGS_TRY(ensure(r->pose_grad, sizeof(float) * 16, s));
+    }
     const CamParams& cam = r->cam;
     BinCtl* ctl = r->bin_ctl.as<BinCtl>();
     if (!r->bwd_queues_clear)   // a second backward after one forward: clear the queue counters again
@@ -512,10 +521,21 @@ int tgs_rasterizer_backward_ex(tgs_rasterizer* r, const void* grad_image, const 
                                    r->rec_count.as<uint32_t>(), r->first_slot.as<uint32_t>(), r->records.as<float4>(),
                                    r->grad2d.as<float>(), gv, (float*)densification_info, mode,
                                    r->row_mask.as<uint8_t>(), r->live.as<uint4>(), r->heavy.as<uint4>(),
-                                   r->chunk_counts.as<uint2>(), s);
+                                   r->chunk_counts.as<uint2>(), pose ? r->pose_partial.as<float>() : nullptr,
+                                   pose ? r->pose_grad.as<float>() : nullptr, s);
     }
     TGS_CHECK_LAUNCH();
     r->row_mask_valid = mode == kGradSparse;
+    r->pose_valid = pose;
+    return TGS_OK;
+}
+
+int tgs_rasterizer_grad_w2c(tgs_rasterizer* r, float* w2c_grad, void* stream) {
+    if (!r || !w2c_grad) return fail(TGS_ERR_INVALID, "NULL argument");
+    if (!r->pose_valid) return fail(TGS_ERR_STATE, "no TGS_BACKWARD_POSE backward since the last forward");
+    hipStream_t s = (hipStream_t)stream;
+    TGS_HIP(hipMemcpyAsync(w2c_grad, r->pose_grad.p, sizeof(float) * 16, hipMemcpyDeviceToHost, s));
+    TGS_HIP(hipStreamSynchronize(s));
     return TGS_OK;
 }
 

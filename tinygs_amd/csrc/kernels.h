@@ -131,7 +131,8 @@ int64_t pb_chunks(int64_t n);
 void launch_preprocess_backward(const GaussianView& g, const CamParams& cam, const uint32_t* n_touched,
                                 const float4* conic_opacity, uint32_t* rec_count, const uint32_t* first_slot,
                                 const float4* records, float* grad2d, const GradView& out, float* densif, int mode,
-                                uint8_t* row_mask, uint4* live, uint4* heavy, uint2* chunk_counts, hipStream_t s);
+                                uint8_t* row_mask, uint4* live, uint4* heavy, uint2* chunk_counts,
+                                float* pose_partial, float* pose_out, hipStream_t s);
 
 // ---- PSNR (psnr.cu:72-128): scratch[psnr_scratch_doubles() - 1] receives the
 // sum of (saturate(pred) - target)^2 over the n_padded elements

@@ -25,6 +25,7 @@ namespace tgs {
 // Gradients of one primitive's parameters (all but SH-rest).
 struct PrimGrad {
     float m[3], s[3], sh0[3], r[4], o;
+    float dc[3];   // dL/dmean in camera space (the pose gradient's factor)
 };
 
 // Per-primitive part: everything except the SH-rest gradient write, which the
@@ -198,6 +199,9 @@ __device__ __forceinline__ void preprocess_backward_one(
     const float dcx = j11 * (gm2x - dj13c / depth);
     const float dcy = j22 * (gm2y - dj23c / depth);
     const float dcz = -j11 * (x * gm2x + h1 / depth) - j22 * (y * gm2y + h2 / depth);
+    out.dc[0] = dcx;
+    out.dc[1] = dcy;
+    out.dc[2] = dcz;
     const float gmx = r1[0] * dcx + r2[0] * dcy + r3[0] * dcz;
     const float gmy = r1[1] * dcx + r2[1] * dcy + r3[1] * dcz;
     const float gmz = r1[2] * dcx + r2[2] * dcy + r3[2] * dcz;
@@ -409,13 +413,20 @@ __device__ __forceinline__ void load_sh_row<__half>(const __half* __restrict__ s
     for (int b = 0; b < 45; ++b) shv[b] = b < nsh ? __half2float(h[b]) : 0.f;
 }
 
-template <typename ShT>
+// Pose gradient (kernels_backward.cuh:256-269): with kPose, each thread also
+// sums dL/dmean_cam[k] * (mean, 1) over its primitives, and the workgroup's
+// sum of those 12 numbers goes to pose_partial[12 * chunk] (every workgroup
+// writes its slot, zero when it has no live primitive), in a fixed order.
+template <typename ShT, bool kPose>
 __global__ void __launch_bounds__(256) preprocess_backward_live_kernel(
     const float* __restrict__ means, const float* __restrict__ scales, const float* __restrict__ rots,
     const ShT* __restrict__ shr_all, int bases, CamParams cam, const float4* __restrict__ conic_opacity,
     uint32_t* __restrict__ rec_count, const float4* __restrict__ records, const float* __restrict__ grad2d,
     GradView out, float4* __restrict__ densif, int mode, const uint4* __restrict__ live,
-    const uint2* __restrict__ chunk_counts) {
+    const uint2* __restrict__ chunk_counts, float* __restrict__ pose_partial) {
+    float pacc[12];
+#pragma unroll
+    for (int q = 0; q < 12; ++q) pacc[q] = 0.f;
     __shared__ uint2 s_win[256 * kShWin];
     const uint32_t t = threadIdx.x;
     const uint32_t nl = chunk_counts[blockIdx.x].x;
@@ -457,6 +468,15 @@ __global__ void __launch_bounds__(256) preprocess_backward_live_kernel(
         for (int b = 0; b < 15; ++b) k[b] = 0.f;
         int nb = 0;
         preprocess_backward_one(ip, pm, ps, pq, shv, opacity, bases, cam, gA, gB, gC, densif, pg, gc, k, nb);
+        if constexpr (kPose) {
+#pragma unroll
+            for (int r = 0; r < 3; ++r) {
+                pacc[4 * r] += pg.dc[r] * pm[0];
+                pacc[4 * r + 1] += pg.dc[r] * pm[1];
+                pacc[4 * r + 2] += pg.dc[r] * pm[2];
+                pacc[4 * r + 3] += pg.dc[r];
+            }
+        }
         float* gm = out.means + 3 * ip;
         float* gs = out.scales + 3 * ip;
         float* gh = out.sh0 + 3 * ip;
@@ -500,27 +520,94 @@ __global__ void __launch_bounds__(256) preprocess_backward_live_kernel(
             for (int j = 0; j < 3 * nb; ++j) gr[j] += v[j];
         }
     }
+    if constexpr (kPose) {
+        __shared__ float s_pose[4][12];
+#pragma unroll
+        for (int q = 0; q < 12; ++q) {
+            float v = pacc[q];
+            for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
+            pacc[q] = v;
+        }
+        if ((t & 63u) == 0u)
+            for (int q = 0; q < 12; ++q) s_pose[t >> 6][q] = pacc[q];
+        __syncthreads();
+        if (t < 12u)
+            pose_partial[12 * (size_t)blockIdx.x + t] = ((s_pose[0][t] + s_pose[1][t]) + s_pose[2][t]) + s_pose[3][t];
+    }
+}
+
+// Sum of the per-workgroup pose partials in a fixed order (thread j takes
+// chunks j, j + 256, ...; then a fixed tree), written as the 4 x 4 dL/dw2c in
+// column-major order ([4 c + r] = row r, column c) with row 3 zero, as the
+// reference hands it to the caller (fastgs.cu:373-383: the device's row-major
+// block transposed into glm).
+__global__ void __launch_bounds__(256) pose_reduce_kernel(const float* __restrict__ partial, int64_t chunks,
+                                                          float* __restrict__ out) {
+    __shared__ float s_sum[4][12];
+    const uint32_t t = threadIdx.x;
+    float acc[12];
+#pragma unroll
+    for (int q = 0; q < 12; ++q) acc[q] = 0.f;
+    for (int64_t c = t; c < chunks; c += 256)
+#pragma unroll
+        for (int q = 0; q < 12; ++q) acc[q] += partial[12 * c + q];
+#pragma unroll
+    for (int q = 0; q < 12; ++q) {
+        float v = acc[q];
+        for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
+        acc[q] = v;
+    }
+    if ((t & 63u) == 0u)
+        for (int q = 0; q < 12; ++q) s_sum[t >> 6][q] = acc[q];
+    __syncthreads();
+    if (t < 16u) {
+        const uint32_t r = t & 3u, c = t >> 2;   // out[4 c + r]
+        out[t] = r < 3u ? ((s_sum[0][4 * r + c] + s_sum[1][4 * r + c]) + s_sum[2][4 * r + c]) + s_sum[3][4 * r + c]
+                        : 0.f;
+    }
+}
+
+template <typename ShT, bool kPose>
+static void launch_live(const GaussianView& g, int bases, const CamParams& cam, const float4* conic_opacity,
+                        uint32_t* rec_count, const float4* records, const float* grad2d, const GradView& out,
+                        float* densif, int mode, const uint4* live, const uint2* chunk_counts, float* pose_partial,
+                        unsigned chunks, hipStream_t s) {
+    preprocess_backward_live_kernel<ShT, kPose><<<chunks, 256, 0, s>>>(
+        g.means, g.scales, g.rotations, (const ShT*)g.sh_rest, bases, cam, conic_opacity, rec_count, records, grad2d,
+        out, (float4*)densif, mode, live, chunk_counts, pose_partial);
 }
 
 void launch_preprocess_backward(const GaussianView& g, const CamParams& cam, const uint32_t* n_touched,
                                 const float4* conic_opacity, uint32_t* rec_count, const uint32_t* first_slot,
                                 const float4* records, float* grad2d, const GradView& out, float* densif, int mode,
-                                uint8_t* row_mask, uint4* live, uint4* heavy, uint2* chunk_counts, hipStream_t s) {
-    if (g.n <= 0) return;
+                                uint8_t* row_mask, uint4* live, uint4* heavy, uint2* chunk_counts,
+                                float* pose_partial, float* pose_out, hipStream_t s) {
+    if (g.n <= 0) {
+        if (pose_out) launch_fill_u32((uint32_t*)pose_out, 0u, 16, s);
+        return;
+    }
     const int bases = (g.sh_degree + 1) * (g.sh_degree + 1);
     const unsigned chunks = (unsigned)pb_chunks(g.n);
     preprocess_backward_classify_kernel<<<chunks, 256, 0, s>>>(g.n, n_touched, rec_count, first_slot,
                                                                (float4*)densif, mode, row_mask, out, live, heavy,
                                                                chunk_counts);
     gather_heavy_kernel<<<chunks, 256, 0, s>>>(heavy, chunk_counts, records, grad2d);
-    if (g.sh_dtype == kShF16)
-        preprocess_backward_live_kernel<__half><<<chunks, 256, 0, s>>>(
-            g.means, g.scales, g.rotations, (const __half*)g.sh_rest, bases, cam, conic_opacity, rec_count, records,
-            grad2d, out, (float4*)densif, mode, live, chunk_counts);
-    else
-        preprocess_backward_live_kernel<float><<<chunks, 256, 0, s>>>(
-            g.means, g.scales, g.rotations, (const float*)g.sh_rest, bases, cam, conic_opacity, rec_count, records,
-            grad2d, out, (float4*)densif, mode, live, chunk_counts);
+    const bool f16 = g.sh_dtype == kShF16;
+    if (pose_out) {
+        if (f16)
+            launch_live<__half, true>(g, bases, cam, conic_opacity, rec_count, records, grad2d, out, densif, mode, live,
+                                      chunk_counts, pose_partial, chunks, s);
+        else
+            launch_live<float, true>(g, bases, cam, conic_opacity, rec_count, records, grad2d, out, densif, mode, live,
+                                     chunk_counts, pose_partial, chunks, s);
+        pose_reduce_kernel<<<1, 256, 0, s>>>(pose_partial, (int64_t)chunks, pose_out);
+    } else if (f16) {
+        launch_live<__half, false>(g, bases, cam, conic_opacity, rec_count, records, grad2d, out, densif, mode, live,
+                                   chunk_counts, nullptr, chunks, s);
+    } else {
+        launch_live<float, false>(g, bases, cam, conic_opacity, rec_count, records, grad2d, out, densif, mode, live,
+                                  chunk_counts, nullptr, chunks, s);
+    }
 }
 
 }  // namespace tgs

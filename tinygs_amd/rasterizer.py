@@ -11,6 +11,8 @@ from __future__ import annotations
 
 import ctypes as C
 
+import numpy as np
+
 from . import _lib
 from .core import DataType, GPUGaussian3d, RasterizeContext, ptr, stream_ptr
 
@@ -81,11 +83,21 @@ class FastGSRasterizer(RasterizerBase):
             raise RuntimeError("assign and sparse are exclusive")
         g = ctx.gaussians_grad.to_c()
         L = _lib.load()
-        flags = (_lib.TGS_BACKWARD_ASSIGN if assign else 0) | (_lib.TGS_BACKWARD_SPARSE if sparse else 0)
+        pose = bool(self.m_params["enable_pose_opt"])
+        flags = (_lib.TGS_BACKWARD_ASSIGN if assign else 0) | (_lib.TGS_BACKWARD_SPARSE if sparse else 0) | \
+            (_lib.TGS_BACKWARD_POSE if pose else 0)
         _lib.check(L.tgs_rasterizer_backward_ex(self._h, ptr(ctx.grad_output.image.data),
                                                 ptr(ctx.fwd_output.image.data), C.byref(g),
                                                 ptr(ctx.densification_info), flags,
                                                 stream_ptr(ctx.stream)), "backward")
+        # fastgs.cu:373-383: grad_input.w2c is the pose gradient (zero without
+        # pose optimisation); row-major here, like GPUBatchInput.w2c
+        if pose:
+            out = (C.c_float * 16)()
+            _lib.check(L.tgs_rasterizer_grad_w2c(self._h, out, stream_ptr(ctx.stream)), "backward")
+            ctx.grad_input.w2c = np.array(out, dtype=np.float64).reshape(4, 4).T.copy()
+        else:
+            ctx.grad_input.w2c = np.zeros((4, 4))
 
     def grad_row_mask(self) -> int:
         """Device address of the byte mask [n] of the last sparse backward
@@ -140,10 +152,16 @@ class FastGSRasterizer(RasterizerBase):
         return _lib.copy_device(dv.n_contrib, t.numel() * 4, t)
 
     def get_params(self) -> dict:
-        return {"type": "fastgs"}
+        return {"type": "fastgs", **self.m_params}
 
     def set_params(self, params: dict):
-        pass
+        """enable_pose_opt turns on the pose gradient (FastGSRasterizerParams,
+        fastgs.hpp:6-12). The reference's set_params ignores its argument
+        (fastgs.cu:398), so there the flag keeps its default (off)."""
+        if "enable_pose_opt" in params:
+            self.m_params["enable_pose_opt"] = bool(params["enable_pose_opt"])
+        if "f16_grad_scaler" in params:
+            self.m_params["f16_grad_scaler"] = float(params["f16_grad_scaler"])
 
 
 def create_rasterizer(rasterizer_type: str) -> RasterizerBase:
