@@ -165,9 +165,10 @@ __global__ void __launch_bounds__(256) blend_backward_kernel(
                     AG[s] = lk[s] == k ? 0.f : AG[s];
                 }
             }
+            // the four pixels' terms; pixel 0 starts each sum (no add of a zero)
             float acc[12];
-#pragma unroll
-            for (int q = 0; q < 12; ++q) acc[q] = 0.f;
+            acc[11] = 0.f;
+            if constexpr (!ABS) acc[9] = acc[10] = 0.f;
 #pragma unroll
             for (int s = 0; s < 4; ++s) {
                 const float dx = r0.x - pcx[s], dy = r0.y - pcy[s];
@@ -175,35 +176,48 @@ __global__ void __launch_bounds__(256) blend_backward_kernel(
                 const float G = __builtin_amdgcn_exp2f(-__builtin_fmaxf(sg, 0.f));
                 const float ab = __builtin_fminf(r1.y * G, kMaxAlpha);
                 const float wgt = Tb[s] * ab;
-                acc[0] = __builtin_fmaf(wgt, g0[s], acc[0]);
-                acc[1] = __builtin_fmaf(wgt, g1[s], acc[1]);
-                acc[2] = __builtin_fmaf(wgt, g2[s], acc[2]);
                 const float cg = __builtin_fmaf(r2.z, g2[s], __builtin_fmaf(r2.y, g1[s], r2.x * g0[s]));
                 AG[s] = __builtin_fmaf(-wgt, cg, AG[s]);
                 const float ag = AG[s];
                 const float oma = 1.0f - ab;
                 const float dalpha = __builtin_fmaf(Tb[s], cg, -(ag * __builtin_amdgcn_rcpf(oma)));
                 const float pp = ab * dalpha;
-                acc[3] += pp;
                 const float hp = pp * dx, hq = pp * dy;
-                acc[4] = __builtin_fmaf(hp, dx, acc[4]);
-                acc[5] = __builtin_fmaf(hp, dy, acc[5]);
-                acc[6] = __builtin_fmaf(hq, dy, acc[6]);
+                if (s == 0) {
+                    acc[0] = wgt * g0[s];
+                    acc[1] = wgt * g1[s];
+                    acc[2] = wgt * g2[s];
+                    acc[3] = pp;
+                    acc[4] = hp * dx;
+                    acc[5] = hp * dy;
+                    acc[6] = hq * dy;
+                } else {
+                    acc[0] = __builtin_fmaf(wgt, g0[s], acc[0]);
+                    acc[1] = __builtin_fmaf(wgt, g1[s], acc[1]);
+                    acc[2] = __builtin_fmaf(wgt, g2[s], acc[2]);
+                    acc[3] += pp;
+                    acc[4] = __builtin_fmaf(hp, dx, acc[4]);
+                    acc[5] = __builtin_fmaf(hp, dy, acc[5]);
+                    acc[6] = __builtin_fmaf(hq, dy, acc[6]);
+                }
                 if constexpr (ABS) {
                     const float gmx = __builtin_fmaf(hp, r1.z, hq * r2.w);
                     const float gmy = __builtin_fmaf(hp, r2.w, hq * r1.w);
-                    acc[7] += gmx;
-                    acc[8] += gmy;
-                    acc[9] += __builtin_fabsf(gmx);
-                    acc[10] += __builtin_fabsf(gmy);
+                    acc[7] = s == 0 ? gmx : acc[7] + gmx;
+                    acc[8] = s == 0 ? gmy : acc[8] + gmy;
+                    acc[9] = s == 0 ? __builtin_fabsf(gmx) : acc[9] + __builtin_fabsf(gmx);
+                    acc[10] = s == 0 ? __builtin_fabsf(gmy) : acc[10] + __builtin_fabsf(gmy);
                 } else {   // sums of pp dx, pp dy; the conic is applied per Gaussian at the end
-                    acc[7] += hp;
-                    acc[8] += hq;
+                    acc[7] = s == 0 ? hp : acc[7] + hp;
+                    acc[8] = s == 0 ? hq : acc[8] + hq;
                 }
                 Tb[s] *= oma;
             }
             float t[3];
-            wave_reduce12(acc, t);
+            if constexpr (ABS)
+                wave_reduce12(acc, t);
+            else
+                wave_reduce9(acc, t);   // values 9-11 are zero: their swaps are skipped
             if ((lane & 15u) == 0u) {
                 s_part[w][q0][k] = t[0];
                 s_part[w][4 + q0][k] = t[1];

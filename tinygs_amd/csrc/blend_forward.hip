@@ -155,10 +155,12 @@ __global__ void __launch_bounds__(256) blend_forward_kernel(CamParams cam, const
             const bool term = ok && nT < kTransmittanceMin;
             const bool acc = ok && !term;
             done = done || term;
-            const float wgt = T * alpha;
-            C0 = acc ? __builtin_fmaf(wgt, bb.z, C0) : C0;
-            C1 = acc ? __builtin_fmaf(wgt, bb.w, C1) : C1;
-            C2 = acc ? __builtin_fmaf(wgt, cz, C2) : C2;
+            // one select of the weight instead of three of the sums: fma(+0, c, C)
+            // is C itself for the finite colours
+            const float wgt = acc ? T * alpha : 0.f;
+            C0 = __builtin_fmaf(wgt, bb.z, C0);
+            C1 = __builtin_fmaf(wgt, bb.w, C1);
+            C2 = __builtin_fmaf(wgt, cz, C2);
             T = acc ? nT : T;
             ncontrib = acc ? (uint32_t)(j + 1) : ncontrib;
         };

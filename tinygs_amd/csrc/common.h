@@ -58,6 +58,13 @@ __device__ __forceinline__ float dpp_f32(float v) {
     return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, ROW_MASK,
                                                                  BANK_MASK, false));
 }
+// DPP row rotation (row_ror:n, CTRL 0x121..0x12F): every source lane is
+// valid, so bound_ctrl changes nothing and spares the zero "old" operand.
+template <int CTRL>
+__device__ __forceinline__ float dpp_ror_f32(float v) {
+    static_assert(CTRL >= 0x121 && CTRL <= 0x12F, "row_ror only");
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, true));
+}
 template <int CTRL, int ROW_MASK = 0xF, int BANK_MASK = 0xF>
 __device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
     return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, ROW_MASK, BANK_MASK, false);
@@ -173,13 +180,48 @@ __device__ __forceinline__ void wave_reduce12(float v[12], float t[3]) {
         t[m] = a + b;   // rows: values 4m, 4m+2, 4m+1, 4m+3 (quarter sums)
     }
 #pragma unroll
-    for (int m = 0; m < 3; ++m) t[m] += dpp_f32<0x128>(t[m]);
+    for (int m = 0; m < 3; ++m) t[m] += dpp_ror_f32<0x128>(t[m]);
 #pragma unroll
-    for (int m = 0; m < 3; ++m) t[m] += dpp_f32<0x124>(t[m]);
+    for (int m = 0; m < 3; ++m) t[m] += dpp_ror_f32<0x124>(t[m]);
 #pragma unroll
-    for (int m = 0; m < 3; ++m) t[m] += dpp_f32<0x122>(t[m]);
+    for (int m = 0; m < 3; ++m) t[m] += dpp_ror_f32<0x122>(t[m]);
 #pragma unroll
-    for (int m = 0; m < 3; ++m) t[m] += dpp_f32<0x121>(t[m]);
+    for (int m = 0; m < 3; ++m) t[m] += dpp_ror_f32<0x121>(t[m]);
+}
+
+// wave_reduce12 for v[9..11] == 0 on every lane: the same layout of t, with
+// the swaps and adds that would only move zeros left out.
+__device__ __forceinline__ void wave_reduce9(float v[12], float t[3]) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        float a = v[2 * k], b = v[2 * k + 1];
+        swap32(a, b);
+        v[k] = a + b;
+    }
+    {
+        float a = v[8], b = 0.f;
+        swap32(a, b);
+        v[4] = a + b;   // lanes 0-31: value 8, lanes 32-63: zero (value 9)
+    }
+#pragma unroll
+    for (int m = 0; m < 2; ++m) {
+        float a = v[2 * m], b = v[2 * m + 1];
+        swap16(a, b);
+        t[m] = a + b;
+    }
+    {
+        float a = v[4], b = 0.f;
+        swap16(a, b);
+        t[2] = a + b;   // row values 8, 10, 9, 11: only value 8 is nonzero
+    }
+#pragma unroll
+    for (int m = 0; m < 3; ++m) t[m] += dpp_ror_f32<0x128>(t[m]);
+#pragma unroll
+    for (int m = 0; m < 3; ++m) t[m] += dpp_ror_f32<0x124>(t[m]);
+#pragma unroll
+    for (int m = 0; m < 3; ++m) t[m] += dpp_ror_f32<0x122>(t[m]);
+#pragma unroll
+    for (int m = 0; m < 3; ++m) t[m] += dpp_ror_f32<0x121>(t[m]);
 }
 
 // Exclusive scan of R striped values per thread (R <= 16): value r of
