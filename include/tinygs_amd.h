@@ -132,7 +132,7 @@ typedef struct tgs_debug_view {
     const float* mean2d;           /* [2n] */
     const float* conic_opacity;    /* [4n] */
     const float* color;            /* [4n]: r, g, b (unclamped), ln(255 * opacity) */
-    const uint32_t* depth_sorted_keys;  /* [n_visible] depth bits, ascending */
+    const uint32_t* depth_sorted_keys;  /* [n_visible] depth bits - depth_key_base, ascending */
     const uint32_t* depth_sorted_prims; /* [n_visible] */
     const uint32_t* instance_tiles;     /* [n_instances] sorted */
     const uint32_t* instance_prims;     /* [n_instances] */
@@ -143,6 +143,8 @@ typedef struct tgs_debug_view {
     int64_t n_visible;
     int64_t n_instances;
     int64_t n_tiles;
+    uint32_t depth_key_base;            /* bits of the near plane (0 when near <= 0) */
+    uint32_t reserved;
 } tgs_debug_view;
 int tgs_rasterizer_debug_view(tgs_rasterizer* r, tgs_debug_view* out);
 

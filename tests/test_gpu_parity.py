@@ -596,3 +596,18 @@ def test_adam_masked_matches_zeroed_rows(hip):
     for ta, tb in zip(ga.tensors(), gb.tensors()):
         x, y = ta.float().cpu().numpy(), tb.float().cpu().numpy()
         assert np.array_equal(x.view(np.uint32), y.view(np.uint32))
+
+
+@pytest.mark.parametrize("near_far", [(0.0, 100.0), (1e-6, 3.0e38), (0.5, 0.5000001), (2.0, 1e4)])
+def test_depth_sort_key_range_variants(hip, orc, near_far):
+    """The depth sort subtracts bits(near) from the keys and sorts only the
+    bits of bits(far) - bits(near) (1 to 4 passes; 4 full-width passes when
+    near <= 0): the order and the images must be those of the oracle's
+    32-bit sort for every width."""
+    import dataclasses
+    s = scenes.config2(seed=23, n=6000, width=160, height=128)
+    near, far = near_far
+    cam = dataclasses.replace(s.camera, near=near, far=far)
+    s2 = dataclasses.replace(s, camera=cam)
+    print(f"[depth keys] near={near} far={far}", flush=True)
+    _check_forward(s2, orc)

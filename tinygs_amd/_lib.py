@@ -43,7 +43,7 @@ class tgs_debug_view(C.Structure):
                 ("depth_sorted_prims", C.c_void_p), ("instance_tiles", C.c_void_p), ("instance_prims", C.c_void_p),
                 ("tile_ranges", C.c_void_p), ("n_contrib", C.c_void_p), ("tile_max", C.c_void_p),
                 ("grad2d", C.c_void_p), ("n_visible", C.c_int64), ("n_instances", C.c_int64),
-                ("n_tiles", C.c_int64)]
+                ("n_tiles", C.c_int64), ("depth_key_base", C.c_uint32), ("reserved", C.c_uint32)]
 
 
 class tgs_pcg32(C.Structure):

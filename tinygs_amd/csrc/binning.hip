@@ -33,6 +33,8 @@ constexpr int kScanRounds = 16;
 constexpr int kScanChunk = kThreads * kScanRounds;     // 4096 elements per scan workgroup
 constexpr int kDepthKeysPerThread = 8;                  // depth passes: 2048 keys per workgroup
 constexpr int kTileKeysPerThread = 8;                   // tile passes: 2048 keys per workgroup (4096 measured 7 us slower)
+constexpr int kDepthMaxDigits = 512;                    // depth passes: digits of up to 9 bits
+constexpr int kTileMaxDigits = 256;                     // tile passes: digits of up to 8 bits
 
 // ---------------------------------------------------------------- workgroup scans
 
@@ -142,7 +144,7 @@ __device__ __forceinline__ uint64_t match_digit(uint32_t d, int bits, bool valid
 // n_touched) triples; V; I = sum of n_touched.
 __global__ void __launch_bounds__(kThreads) compact_kernel(const uint32_t* __restrict__ n_touched,
                                                            const uint32_t* __restrict__ depth_key, int64_t n,
-                                                           uint32_t* __restrict__ keys_out,
+                                                           uint32_t key_base, uint32_t* __restrict__ keys_out,
                                                            uint32_t* __restrict__ vals_out,
                                                            uint32_t* __restrict__ nt_out, BinCtl* ctl,
                                                            uint64_t* status, uint32_t epoch) {
@@ -184,19 +186,20 @@ __global__ void __launch_bounds__(kThreads) compact_kernel(const uint32_t* __res
     for (int r = 0; r < kScanRounds; ++r) {
         if (vis[r]) {
             const uint32_t pos = b0 + ex[r];
-            keys_out[pos] = key[r];
+            keys_out[pos] = key[r] - key_base;
             vals_out[pos] = (uint32_t)(base + (int64_t)r * kThreads);
             nt_out[pos] = nt[r];
         }
     }
 }
 
-void launch_compact_visible(const uint32_t* n_touched, const uint32_t* depth_key, int64_t n, uint32_t* keys_out,
-                            uint32_t* vals_out, uint32_t* nt_out, BinCtl* ctl, uint64_t* status, uint32_t& epoch,
-                            hipStream_t s) {
+void launch_compact_visible(const uint32_t* n_touched, const uint32_t* depth_key, int64_t n, uint32_t key_base,
+                            uint32_t* keys_out, uint32_t* vals_out, uint32_t* nt_out, BinCtl* ctl, uint64_t* status,
+                            uint32_t& epoch, hipStream_t s) {
     if (n <= 0) return;
     const uint32_t nb = (uint32_t)((n + kScanChunk - 1) / kScanChunk);
-    compact_kernel<<<nb, kThreads, 0, s>>>(n_touched, depth_key, n, keys_out, vals_out, nt_out, ctl, status, ++epoch);
+    compact_kernel<<<nb, kThreads, 0, s>>>(n_touched, depth_key, n, key_base, keys_out, vals_out, nt_out, ctl, status,
+                                           ++epoch);
 }
 
 // ---------------------------------------------------------------- instance offsets
@@ -252,9 +255,9 @@ int64_t scan_status_entries(int64_t max_n) { return (max_n + kScanChunk - 1) / k
 // key blk + w * 64 * KPT + r * 64 + l. Digit ranks come from ballot matching
 // against a wave-private LDS histogram (a wave's LDS operations complete in
 // issue order, so rounds need no barrier).
-template <int KPT>
+template <int KPT, int MAXB>
 __device__ __forceinline__ void rank_keys(const uint32_t key[KPT], int64_t base, int64_t n, int shift, int bits,
-                                          uint32_t (*s_cnt)[256], uint32_t pos[KPT]) {
+                                          uint32_t (*s_cnt)[MAXB], uint32_t pos[KPT]) {
     const uint32_t lane = threadIdx.x & 63u, w = threadIdx.x >> 6;
     const uint32_t dmask = (1u << bits) - 1u;
 #pragma unroll
@@ -272,15 +275,15 @@ __device__ __forceinline__ void rank_keys(const uint32_t key[KPT], int64_t base,
 // Per-workgroup digit counts: counts[d * nb + b] (digit-major). Workgroups
 // past the end write zeros. Counting needs no ranks: one LDS atomic add per
 // key into the workgroup's histogram.
-template <int KPT>
+template <int KPT, int MAXB>
 __global__ void __launch_bounds__(kThreads) radix_upsweep_kernel(const uint32_t* __restrict__ keys,
                                                                  const uint32_t* d_n, int64_t max_n, int shift,
                                                                  int bits, uint32_t* __restrict__ counts,
                                                                  uint32_t nb) {
-    __shared__ uint32_t s_hist[256];
+    __shared__ uint32_t s_hist[MAXB];
     const uint32_t t = threadIdx.x, lane = t & 63u, w = t >> 6;
     const uint32_t bins = 1u << bits, dmask = bins - 1u;
-    s_hist[t] = 0u;
+    for (uint32_t b = t; b < (uint32_t)MAXB; b += kThreads) s_hist[b] = 0u;
     __syncthreads();
     const int64_t n = resolve_n(d_n, max_n);
     const int64_t base = (int64_t)blockIdx.x * (kThreads * KPT) + (int64_t)w * (64 * KPT);
@@ -294,7 +297,7 @@ __global__ void __launch_bounds__(kThreads) radix_upsweep_kernel(const uint32_t*
     for (int r = 0; r < KPT; ++r)
         if (base + (int64_t)r * 64 + lane < n) atomicAdd(&s_hist[(key[r] >> shift) & dmask], 1u);
     __syncthreads();
-    if (t < bins) counts[(size_t)t * nb + blockIdx.x] = s_hist[t];
+    for (uint32_t b = t; b < bins; b += kThreads) counts[(size_t)b * nb + blockIdx.x] = s_hist[b];
 }
 
 // In-place exclusive scan of a u32 array of n elements (single pass,
@@ -335,14 +338,16 @@ __global__ void __launch_bounds__(kThreads) exclusive_scan_kernel(uint32_t* __re
 // The workgroup's keys are first placed in LDS in digit order and written
 // out by consecutive threads, so each store instruction covers contiguous
 // runs.
-template <int KPT, bool PAYLOAD2>
+template <int KPT, bool PAYLOAD2, int MAXB>
 __global__ void __launch_bounds__(kThreads) radix_downsweep_kernel(
     const uint32_t* __restrict__ keys_in, const uint32_t* __restrict__ vals_in, const uint32_t* __restrict__ v2_in,
     uint32_t* __restrict__ keys_out, uint32_t* __restrict__ vals_out, uint32_t* __restrict__ v2_out,
     const uint32_t* d_n, int64_t max_n, int shift, int bits, const uint32_t* __restrict__ offsets, uint32_t nb) {
     constexpr int kChunk = kThreads * KPT;
-    __shared__ uint32_t s_cnt[4][256];
-    __shared__ uint32_t s_gofs[256];
+    constexpr int kBpt = MAXB / kThreads;   // digits per thread in the workgroup scan (1 or 2)
+    static_assert(MAXB == kThreads || MAXB == 2 * kThreads, "256 or 512 digits");
+    __shared__ uint32_t s_cnt[4][MAXB];
+    __shared__ uint32_t s_gofs[MAXB];
     __shared__ uint32_t s_key[kChunk], s_val[kChunk], s_v2[PAYLOAD2 ? kChunk : 1];
     __shared__ uint32_t s_wave[4];
     const uint32_t t = threadIdx.x, lane = t & 63u, w = t >> 6;
@@ -350,8 +355,13 @@ __global__ void __launch_bounds__(kThreads) radix_downsweep_kernel(
     const int64_t n = resolve_n(d_n, max_n);
     const int64_t blk = (int64_t)blockIdx.x * kChunk;
     if (blk >= n) return;
-    for (int k = t; k < 4 * 256; k += kThreads) (&s_cnt[0][0])[k] = 0;
-    const uint32_t gofs = t < bins ? offsets[(size_t)t * nb + blockIdx.x] : 0u;
+    for (int k = t; k < 4 * MAXB; k += kThreads) (&s_cnt[0][0])[k] = 0;
+    uint32_t gofs[kBpt];   // thread t owns digits kBpt t .. kBpt t + kBpt - 1
+#pragma unroll
+    for (int q = 0; q < kBpt; ++q) {
+        const uint32_t d = kBpt * t + (uint32_t)q;
+        gofs[q] = d < bins ? offsets[(size_t)d * nb + blockIdx.x] : 0u;
+    }
     __syncthreads();
     const int64_t base = blk + (int64_t)w * (64 * KPT);
     uint32_t key[KPT], val[KPT], v2[PAYLOAD2 ? KPT : 1], pos[KPT];
@@ -363,18 +373,31 @@ __global__ void __launch_bounds__(kThreads) radix_downsweep_kernel(
         val[r] = valid ? vals_in[i] : 0u;
         if constexpr (PAYLOAD2) v2[r] = valid ? v2_in[i] : 0u;
     }
-    rank_keys<KPT>(key, base, n, shift, bits, s_cnt, pos);
+    rank_keys<KPT, MAXB>(key, base, n, shift, bits, s_cnt, pos);
     __syncthreads();
-    const uint32_t c0 = s_cnt[0][t], c1 = s_cnt[1][t], c2 = s_cnt[2][t];
-    const uint32_t total = t < bins ? c0 + c1 + c2 + s_cnt[3][t] : 0u;
+    uint32_t c[kBpt][3], tot[kBpt], total = 0;
+#pragma unroll
+    for (int q = 0; q < kBpt; ++q) {
+        const uint32_t d = kBpt * t + (uint32_t)q;
+        c[q][0] = s_cnt[0][d];
+        c[q][1] = s_cnt[1][d];
+        c[q][2] = s_cnt[2][d];
+        tot[q] = d < bins ? c[q][0] + c[q][1] + c[q][2] + s_cnt[3][d] : 0u;
+        total += tot[q];
+    }
     uint32_t unused;
-    const uint32_t lstart = block_exclusive_scan(total, s_wave, &unused);   // digit start inside the workgroup
-    if (t < bins) {
-        s_gofs[t] = gofs - lstart;
-        s_cnt[0][t] = lstart;
-        s_cnt[1][t] = lstart + c0;
-        s_cnt[2][t] = lstart + c0 + c1;
-        s_cnt[3][t] = lstart + c0 + c1 + c2;
+    uint32_t lstart = block_exclusive_scan(total, s_wave, &unused);   // digit start inside the workgroup
+#pragma unroll
+    for (int q = 0; q < kBpt; ++q) {
+        const uint32_t d = kBpt * t + (uint32_t)q;
+        if (d < bins) {
+            s_gofs[d] = gofs[q] - lstart;
+            s_cnt[0][d] = lstart;
+            s_cnt[1][d] = lstart + c[q][0];
+            s_cnt[2][d] = lstart + c[q][0] + c[q][1];
+            s_cnt[3][d] = lstart + c[q][0] + c[q][1] + c[q][2];
+        }
+        lstart += tot[q];
     }
     __syncthreads();
 #pragma unroll
@@ -401,10 +424,10 @@ __global__ void __launch_bounds__(kThreads) radix_downsweep_kernel(
 
 int64_t radix_count_entries(int64_t max_n, bool depth) {
     const int64_t chunk = kThreads * (depth ? kDepthKeysPerThread : kTileKeysPerThread);
-    return ((max_n + chunk - 1) / chunk) * 256;
+    return ((max_n + chunk - 1) / chunk) * (depth ? kDepthMaxDigits : kTileMaxDigits);
 }
 
-template <int KPT>
+template <int KPT, int MAXB>
 static int radix_passes(uint32_t* keys[2], uint32_t* vals[2], uint32_t* v2[2], const uint32_t* d_n, int64_t max_n,
                         int n_passes, const int* shifts, const int* bits, uint32_t* counts, uint32_t* tickets,
                         uint64_t* status, uint32_t& epoch, uint32_t* err, hipStream_t s) {
@@ -412,16 +435,18 @@ static int radix_passes(uint32_t* keys[2], uint32_t* vals[2], uint32_t* v2[2], c
     if (max_n <= 0) return cur;
     const uint32_t nb = (uint32_t)((max_n + kThreads * KPT - 1) / (kThreads * KPT));
     for (int p = 0; p < n_passes; ++p) {
+        if ((1 << bits[p]) > MAXB) return -1;
         const int64_t cn = (int64_t)nb << bits[p];
-        radix_upsweep_kernel<KPT><<<nb, kThreads, 0, s>>>(keys[cur], d_n, max_n, shifts[p], bits[p], counts, nb);
+        radix_upsweep_kernel<KPT, MAXB><<<nb, kThreads, 0, s>>>(keys[cur], d_n, max_n, shifts[p], bits[p], counts,
+                                                                 nb);
         exclusive_scan_kernel<<<(unsigned)((cn + kScanChunk - 1) / kScanChunk), kThreads, 0, s>>>(
             counts, cn, tickets + p, status, ++epoch, err);
         if (v2)
-            radix_downsweep_kernel<KPT, true><<<nb, kThreads, 0, s>>>(
+            radix_downsweep_kernel<KPT, true, MAXB><<<nb, kThreads, 0, s>>>(
                 keys[cur], vals[cur], v2[cur], keys[cur ^ 1], vals[cur ^ 1], v2[cur ^ 1], d_n, max_n, shifts[p],
                 bits[p], counts, nb);
         else
-            radix_downsweep_kernel<KPT, false><<<nb, kThreads, 0, s>>>(
+            radix_downsweep_kernel<KPT, false, MAXB><<<nb, kThreads, 0, s>>>(
                 keys[cur], vals[cur], nullptr, keys[cur ^ 1], vals[cur ^ 1], nullptr, d_n, max_n, shifts[p], bits[p],
                 counts, nb);
         cur ^= 1;
@@ -433,10 +458,10 @@ int radix_sort(uint32_t* keys[2], uint32_t* vals[2], uint32_t* v2[2], const uint
                int n_passes, const int* shifts, const int* bits, uint32_t* counts, uint32_t* tickets,
                uint64_t* status, uint32_t& epoch, uint32_t* err, hipStream_t s) {
     if (depth)
-        return radix_passes<kDepthKeysPerThread>(keys, vals, v2, d_n, max_n, n_passes, shifts, bits, counts, tickets,
-                                                 status, epoch, err, s);
-    return radix_passes<kTileKeysPerThread>(keys, vals, v2, d_n, max_n, n_passes, shifts, bits, counts, tickets,
-                                            status, epoch, err, s);
+        return radix_passes<kDepthKeysPerThread, kDepthMaxDigits>(keys, vals, v2, d_n, max_n, n_passes, shifts, bits,
+                                                                  counts, tickets, status, epoch, err, s);
+    return radix_passes<kTileKeysPerThread, kTileMaxDigits>(keys, vals, v2, d_n, max_n, n_passes, shifts, bits,
+                                                            counts, tickets, status, epoch, err, s);
 }
 
 // ---------------------------------------------------------------- instance emission

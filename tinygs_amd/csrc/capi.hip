@@ -217,6 +217,7 @@ struct tgs_rasterizer {
     bool row_mask_valid = false;
     DevBuf pose_partial, pose_grad;   // pose gradient: per-chunk partial sums, the 4 x 4 result
     bool pose_valid = false;
+    uint32_t depth_key_base = 0;   // the sorted depth keys are key - depth_key_base
     // temp
     DevBuf grad2d;
     DevBuf radix_counts;   // per-workgroup digit counts of the radix passes
@@ -396,14 +397,32 @@ int tgs_rasterizer_forward(tgs_rasterizer* r, const tgs_camera* camera, void* im
     int psel;
     {
         StageScope sc(ST_DEPTH, s);
-        launch_compact_visible(r->n_touched.as<uint32_t>(), r->depth_key.as<uint32_t>(), n, pk[0], pv[0], pn[0], ctl,
-                               status, r->epoch, s);
+        // visible depths lie in [near, far] (preprocess culls the rest), so with
+        // near > 0 the keys (float bits) minus bits(near) span only the bits of
+        // bits(far) - bits(near): 27 for near 0.01, far 100, i.e. three passes
+        // of 9-bit digits instead of four of 8
+        uint32_t key_base = 0;
+        int key_bits = 32;
+        if (cam.near_ > 0.f && cam.far_ >= cam.near_ && cam.far_ <= 3.0e38f) {
+            key_base = f2u(cam.near_);
+            const uint32_t range = f2u(cam.far_) - key_base;
+            key_bits = range ? 32 - __builtin_clz(range) : 1;
+        }
+        const int n_dp = key_bits <= 9 ? 1 : key_bits <= 18 ? 2 : key_bits <= 27 ? 3 : 4;
+        int shifts[4] = {0, 0, 0, 0}, bits[4] = {0, 0, 0, 0};
+        for (int p = 0; p < n_dp; ++p) {
+            bits[p] = (key_bits + n_dp - 1) / n_dp;
+            shifts[p] = p * bits[p];
+        }
+        launch_compact_visible(r->n_touched.as<uint32_t>(), r->depth_key.as<uint32_t>(), n, key_base, pk[0], pv[0],
+                               pn[0], ctl, status, r->epoch, s);
         // V, I and the sticky error flag go to the host while the depth sort runs
         TGS_HIP(hipMemcpyAsync(r->h_counters, ctl, 3 * sizeof(uint32_t), hipMemcpyDeviceToHost, s));
         TGS_HIP(hipEventRecord(r->ev_counts, s));
-        const int shifts[4] = {0, 8, 16, 24}, bits[4] = {8, 8, 8, 8};
-        psel = radix_sort(pk, pv, pn, &ctl->V, n, true, 4, shifts, bits, r->radix_counts.as<uint32_t>(),
+        psel = radix_sort(pk, pv, pn, &ctl->V, n, true, n_dp, shifts, bits, r->radix_counts.as<uint32_t>(),
                           ctl->tickets + kTicketDepth, status, r->epoch, &ctl->err, s);
+        if (psel < 0) return fail(TGS_ERR_STATE, "depth sort digit width");
+        r->depth_key_base = key_base;
         launch_instance_offsets(pn[psel], n, r->offs.as<uint32_t>(), ctl, status, r->epoch, s);
     }
     TGS_CHECK_LAUNCH();
@@ -564,6 +583,7 @@ int tgs_rasterizer_debug_view(tgs_rasterizer* r, tgs_debug_view* out) {
     out->conic_opacity = r->conic_opacity.as<float>();
     out->color = r->color.as<float>();
     out->depth_sorted_keys = r->pkeys[r->psel].as<uint32_t>();
+    out->depth_key_base = r->depth_key_base;
     out->depth_sorted_prims = r->pvals[r->psel].as<uint32_t>();
     out->instance_tiles = r->ikeys[r->isel].as<uint32_t>();
     out->instance_prims = r->ivals[r->isel].as<uint32_t>();

@@ -66,9 +66,11 @@ constexpr uint32_t kEpochMask = 0x3fffffffu;   // 30-bit launch epoch of look-ba
 int64_t scan_status_entries(int64_t max_n);
 // Visible primitives (n_touched > 0) in index order -> (depth key, index,
 // n_touched) triples; ctl->V, ctl->I; depth-key digit histograms.
-void launch_compact_visible(const uint32_t* n_touched, const uint32_t* depth_key, int64_t n, uint32_t* keys_out,
-                            uint32_t* vals_out, uint32_t* nt_out, BinCtl* ctl, uint64_t* status, uint32_t& epoch,
-                            hipStream_t s);
+// keys_out receives depth_key - key_base (key_base <= every visible key, so
+// the order is that of the keys).
+void launch_compact_visible(const uint32_t* n_touched, const uint32_t* depth_key, int64_t n, uint32_t key_base,
+                            uint32_t* keys_out, uint32_t* vals_out, uint32_t* nt_out, BinCtl* ctl, uint64_t* status,
+                            uint32_t& epoch, hipStream_t s);
 // offs[k] = exclusive scan of nt_sorted[k] over k < ctl->V; offs[V] = total.
 void launch_instance_offsets(const uint32_t* nt_sorted, int64_t max_count, uint32_t* offs, BinCtl* ctl,
                              uint64_t* status, uint32_t& epoch, hipStream_t s);

@@ -133,7 +133,9 @@ class FastGSRasterizer(RasterizerBase):
             "mean2d": grab(dv.mean2d, 2 * n, torch.float32),
             "conic_opacity": grab(dv.conic_opacity, 4 * n, torch.float32),
             "color": grab(dv.color, 4 * n, torch.float32),
-            "depth_sorted_keys": grab(dv.depth_sorted_keys, V, torch.int32),
+            # the library sorts depth bits minus the near plane's bits; add them back
+            "depth_sorted_keys": ((grab(dv.depth_sorted_keys, V, torch.int32).long() + int(dv.depth_key_base))
+                                  & 0xFFFFFFFF).to(torch.int32),
             "depth_sorted_prims": grab(dv.depth_sorted_prims, V, torch.int32),
             "instance_tiles": grab(dv.instance_tiles, I, torch.int32),
             "instance_prims": grab(dv.instance_prims, I, torch.int32),
