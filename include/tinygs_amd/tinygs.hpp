@@ -23,9 +23,10 @@
 //     replaces thrust::device_vector; vec3/vec4 are spelled as float arrays
 //     (3 or 4 floats per element, same memory layout as glm).
 //   * get_params/set_params take a flat name -> number map instead of json.
-//   * Densification-time mutations (GPUGaussian3d::remove/append/reorder,
-//     OptimizerBase::remove/duplicate/reset(indices)/reorder/reset_opacity)
-//     are not part of the training hot path and throw std::runtime_error.
+//   * Densification (GPUGaussian3d::remove/append, SimpleAdam::remove/
+//     duplicate/reset_opacity, DefaultStrategy) runs through the tgs_densify_*
+//     / tgs_*_gather entry points; Morton reordering and the MCMC-only
+//     OptimizerBase::reset(indices) throw std::runtime_error.
 //   * GPUGaussian3d can store sh0 / sh_rest as fp16 (sh_dtype), the storage
 //     mode of the 1M-Gaussian 1080p benchmark; gradients stay fp32.
 // Every failing call throws std::runtime_error carrying tgs_last_error(), as
@@ -44,6 +45,7 @@
 #include <memory>
 #include <stdexcept>
 #include <string>
+#include <type_traits>
 #include <utility>
 #include <vector>
 
@@ -228,16 +230,60 @@ public:
         return g;
     }
 
-    void remove(char*, int) { throw std::runtime_error("GPUGaussian3d::remove: densification is not supported"); }
-    void reorder(uint32_t*, hipStream_t = nullptr) {
-        throw std::runtime_error("GPUGaussian3d::reorder: densification is not supported");
+    // GPUGaussian3d::remove (gpu_gaussian.cu:117-160): keep the Gaussians with
+    // kept_flag[i] != 0 (device bytes, one per Gaussian), num_kept of them, in order.
+    void remove(char* kept_flag, int num_kept) {
+        if (num_kept < 0 || (size_t)num_kept > m_size)
+            throw std::runtime_error("GPUGaussian3d::remove: num_kept out of range");
+        DeviceArray<int32_t> rows(std::max<size_t>(m_size, 1));
+        int64_t count = 0;
+        throw_on(tgs_flags_compact((const uint8_t*)kept_flag, (int64_t)m_size, rows.data(), &count, nullptr),
+                 "GPUGaussian3d::remove");
+        if (count != num_kept) throw std::runtime_error("GPUGaussian3d::remove: num_kept does not match the flags");
+        gather_rows(rows.data(), (size_t)num_kept);
     }
-    void append(int) { throw std::runtime_error("GPUGaussian3d::append: densification is not supported"); }
+    // The rows rows[0 .. num) (device int32 indices) become the Gaussians.
+    void gather_rows(const int32_t* rows, size_t num) {
+        GPUGaussian3d g(num, m_sh_dtype);
+        const tgs_gaussians src = to_c(), dst = g.to_c();
+        if (num) throw_on(tgs_gaussians_gather(&src, &dst, rows, nullptr), "GPUGaussian3d::remove");
+        hip_check(hipStreamSynchronize(nullptr), "hipStreamSynchronize");
+        adopt(g);
+    }
+    // GPUGaussian3d::append (gpu_gaussian.cu:162-170): num_dup zero rows appended.
+    void append(int num_dup) {
+        if (num_dup <= 0) throw std::runtime_error("GPUGaussian3d::append: num_dup must be positive");
+        GPUGaussian3d g(m_size + (size_t)num_dup, m_sh_dtype);
+        g.memset(0);
+        const size_t shb = m_sh_dtype == DataType::Float16 ? 2 : 4;
+        const size_t bytes[6] = {12 * m_size, 4 * m_size, 16 * m_size, 12 * m_size, 3 * shb * m_size,
+                                 45 * shb * m_size};
+        DeviceArray<float>* src[] = {&m_means, &m_opacities, &m_rotations, &m_scales, &m_sh0, &m_sh_rest};
+        DeviceArray<float>* dst[] = {&g.m_means, &g.m_opacities, &g.m_rotations, &g.m_scales, &g.m_sh0, &g.m_sh_rest};
+        for (int k = 0; k < 6; ++k)
+            if (bytes[k]) hip_check(hipMemcpy(dst[k]->data(), src[k]->data(), bytes[k], hipMemcpyDeviceToDevice),
+                                    "hipMemcpy");
+        adopt(g);
+    }
+    void reorder(uint32_t*, hipStream_t = nullptr) {
+        throw std::runtime_error("GPUGaussian3d::reorder: Morton reordering is not built");
+    }
 
     float scene_scale() const { return m_scene_scale; }
     void set_scene_scale(float s) { m_scene_scale = s; }
     void set_sh_degree(int d) { m_sh_degree = std::min(kMaxSphericalHarmonicsDegree, d); }
     int get_sh_degree() const { return m_sh_degree; }
+
+    // Takes g's arrays (and size) in place of this one's; scene scale and SH degree stay.
+    void adopt(GPUGaussian3d& g) {
+        std::swap(m_means, g.m_means);
+        std::swap(m_opacities, g.m_opacities);
+        std::swap(m_rotations, g.m_rotations);
+        std::swap(m_scales, g.m_scales);
+        std::swap(m_sh0, g.m_sh0);
+        std::swap(m_sh_rest, g.m_sh_rest);
+        std::swap(m_size, g.m_size);
+    }
 
     // C view for the ABI.
     tgs_gaussians to_c() const {
@@ -665,6 +711,34 @@ public:
     void reset() override { throw_on(tgs_adam_reset(m_handle, nullptr), "SimpleAdam::reset"); }
     using OptimizerBase::reset;
 
+    // SimpleAdam::remove (simple_adam.cu:841-906). The reference maps over the
+    // optimiser's Gaussians, which the strategy has already shrunk to num_kept
+    // rows: moment row k = the k-th set flag among the first num_kept flags,
+    // and the rows past those read row 0 (its zero-initialised map).
+    void remove(char* kept_flag, int num_kept) override {
+        if (num_kept <= 0) return;
+        DeviceArray<int32_t> rows((size_t)num_kept);
+        hip_check(hipMemset(rows.data(), 0, rows.bytes()), "hipMemset");
+        int64_t count = 0;
+        throw_on(tgs_flags_compact((const uint8_t*)kept_flag, num_kept, rows.data(), &count, nullptr),
+                 "SimpleAdam::remove");
+        throw_on(tgs_adam_gather(m_handle, rows.data(), num_kept, nullptr), "SimpleAdam::remove");
+        hip_check(hipStreamSynchronize(nullptr), "hipStreamSynchronize");
+    }
+    // SimpleAdam::duplicate (simple_adam.cu:908-924): zero moment rows appended.
+    void duplicate(int*, int*, int num_duplicate) override {
+        if (num_duplicate > 0)
+            throw_on(tgs_adam_append(m_handle, num_duplicate, nullptr), "SimpleAdam::duplicate");
+    }
+    // SimpleAdam::reset_opacity (simple_adam.cu:981-985).
+    void reset_opacity() override { throw_on(tgs_adam_reset_opacity(m_handle, nullptr), "SimpleAdam::reset_opacity"); }
+    // Device pointers of a group's moments (0..5 = means, opacities, rotations, scales, sh0, sh_rest).
+    std::pair<float*, float*> moments(int group) const {
+        float *a = nullptr, *b = nullptr;
+        throw_on(tgs_adam_moments(m_handle, group, &a, &b), "SimpleAdam::moments");
+        return {a, b};
+    }
+
     void set_gaussians(std::shared_ptr<GPUGaussian3d> g, std::shared_ptr<GPUGaussian3d> gg) override {
         if (g->size() != m_gaussians->size())
             throw std::runtime_error("SimpleAdam::set_gaussians: size changes need densification support");
@@ -704,6 +778,233 @@ inline std::unique_ptr<OptimizerBase> create_optimizer(const std::string& type, 
                                                        std::shared_ptr<GPUGaussian3d> gg) {
     if (type == "simple_adam") return std::make_unique<SimpleAdam>(std::move(g), std::move(gg));
     throw std::runtime_error("Unknown optimizer type: " + type);
+}
+
+// ---------------------------------------------------------------- densification strategy
+// StrategyParams / StrategyBase / DefaultStrategy / create_strategy
+// (tinygs/include/tinygs/strategy/strategy.hpp:7-121, tinygs/src/strategy/
+// strategy.cpp:10-177, tinygs/src/strategy/default.cu:17-359): same parameter
+// names, defaults, schedule, RNG (pcg32 seeded with `seed`, stream 1) and
+// order of the Gaussian / gradient / optimiser updates. The device work runs
+// behind tgs_densify_select / tgs_random_logistic / tgs_densify_apply /
+// tgs_prune_select / tgs_gaussians_gather / tgs_reset_opacity.
+
+struct StrategyParams {
+    float pruning_opacity_threshold = 0.005f;
+    float pruning_scale_threshold = 0.1f;
+    float max_screen_size = 10.0f;
+    float duplicate_grad_threshold = 0.0002f;
+    float duplicate_scale_threshold = 0.01f;
+    bool reset_reset_optimizer = false;
+    bool absgrad = false;
+    int refine_every = 100;
+    int start_refine = 500;
+    int end_refine = 15000;
+    int max_num_gaussians = 10000000;
+    int reset_every = 3000;
+    uint64_t seed = 42;
+
+    void from_map(const ParamMap& m) {
+        auto f = [&](const char* k, auto& v) {
+            auto it = m.find(k);
+            if (it != m.end()) v = static_cast<std::remove_reference_t<decltype(v)>>(it->second);
+        };
+        f("pruning_opacity_threshold", pruning_opacity_threshold);
+        f("pruning_scale_threshold", pruning_scale_threshold);
+        f("max_screen_size", max_screen_size);
+        f("duplicate_grad_threshold", duplicate_grad_threshold);
+        f("duplicate_scale_threshold", duplicate_scale_threshold);
+        f("reset_reset_optimizer", reset_reset_optimizer);
+        f("absgrad", absgrad);
+        f("refine_every", refine_every);
+        f("start_refine", start_refine);
+        f("end_refine", end_refine);
+        f("max_num_gaussians", max_num_gaussians);
+        f("reset_every", reset_every);
+        f("seed", seed);
+    }
+};
+
+class StrategyBase {
+public:
+    StrategyBase(std::shared_ptr<GPUGaussian3d> g, std::shared_ptr<GPUGaussian3d> gg, OptimizerBase* optimizer)
+        : m_gaussians(std::move(g)), m_gaussians_grad(std::move(gg)), m_optimizer(optimizer) {}
+    virtual ~StrategyBase() = default;
+    void step(RasterizeContext& ctx) {
+        step_impl(ctx);
+        ++m_step_count;
+    }
+    int this_step() const { return m_step_count; }
+    virtual void set_params(const ParamMap& p) { m_params.from_map(p); }
+    const StrategyParams& params() const { return m_params; }
+
+protected:
+    virtual void step_impl(RasterizeContext& ctx) = 0;
+    // strategy.cpp:19-31: Gaussians, gradients, then the optimiser
+    void on_remove(char* kept_flag, const int32_t* kept_rows, int num_kept) {
+        if (num_kept <= 0) return;
+        if (m_gaussians) m_gaussians->gather_rows(kept_rows, (size_t)num_kept);
+        if (m_gaussians_grad) m_gaussians_grad->gather_rows(kept_rows, (size_t)num_kept);
+        if (m_optimizer) m_optimizer->remove(kept_flag, num_kept);
+    }
+    // strategy.cpp:33-45
+    void on_duplicate(int n) {
+        if (n <= 0) return;
+        if (m_gaussians) m_gaussians->append(n);
+        if (m_gaussians_grad) m_gaussians_grad->append(n);
+        if (m_optimizer) m_optimizer->duplicate(nullptr, nullptr, n);
+    }
+    // strategy.cpp:55-63
+    void on_reset_opacity() {
+        if (!m_optimizer) return;
+        m_optimizer->reset_opacity();
+        if (m_params.reset_reset_optimizer) m_optimizer->reset();
+    }
+
+    std::shared_ptr<GPUGaussian3d> m_gaussians, m_gaussians_grad;
+    OptimizerBase* m_optimizer;
+    StrategyParams m_params;
+    int m_step_count = 0;
+};
+
+class DefaultStrategy final : public StrategyBase {
+public:
+    using StrategyBase::StrategyBase;
+    // default.cu:349-352: set_params reseeds the generator
+    void set_params(const ParamMap& p) override {
+        StrategyBase::set_params(p);
+        tgs_pcg32_seed(&m_rng, m_params.seed, 1);
+    }
+    const tgs_pcg32& rng() const { return m_rng; }
+    int64_t last_duplicated = 0, last_split = 0, last_kept = 0;
+
+protected:
+    // default.cu:40-69
+    void step_impl(RasterizeContext& ctx) override {
+        hip_check(hipStreamSynchronize(ctx.stream), "hipStreamSynchronize");
+        const size_t n = m_gaussians->size();
+        if (!ctx.densification_info) fresh_info(ctx, n);
+        const StrategyParams& p = m_params;
+        const int step = this_step();
+        if (step % p.refine_every == 0 && p.start_refine <= step && step <= p.end_refine) {
+            if ((int64_t)m_gaussians->size() < (int64_t)p.max_num_gaussians) duplicate(ctx);
+            prune(ctx);
+            fresh_info(ctx, m_gaussians->size());
+        }
+        if (p.reset_every > 0 && step % p.reset_every == 0 && p.start_refine <= step && step < p.end_refine) {
+            const tgs_gaussians g = m_gaussians->to_c();
+            throw_on(tgs_reset_opacity(&g, 2.0f * p.pruning_opacity_threshold, ctx.stream), "reset_opacity");
+            on_reset_opacity();
+        }
+    }
+
+private:
+    static void fresh_info(RasterizeContext& ctx, size_t n) {
+        ctx.densification_info = std::make_shared<GPUBuffer<DensificationInfo>>(std::max<size_t>(n, 1));
+        hip_check(hipMemset(ctx.densification_info->data(), 0, ctx.densification_info->bytes()), "hipMemset");
+    }
+    // default.cu:71-297
+    void duplicate(RasterizeContext& ctx) {
+        const size_t n = m_gaussians->size();
+        if (!ctx.densification_info || ctx.densification_info->size() < n) return;
+        DeviceArray<uint8_t> flags(std::max<size_t>(n, 1));
+        DeviceArray<int32_t> src(std::max<size_t>(n, 1));
+        int64_t nd = 0, ns = 0;
+        const tgs_gaussians g = m_gaussians->to_c();
+        throw_on(tgs_densify_select(&g, (const float*)ctx.densification_info->data(),
+                                    m_params.duplicate_grad_threshold * ctx.grad_scaler,
+                                    m_params.duplicate_scale_threshold * m_gaussians->scene_scale(),
+                                    m_params.absgrad ? 1 : 0, flags.data(), src.data(), &nd, &ns, ctx.stream),
+                 "DefaultStrategy::duplicate");
+        last_duplicated = nd;
+        last_split = ns;
+        const int64_t grows = nd + ns;
+        if (grows == 0) return;
+        on_duplicate((int)grows);
+        DeviceArray<float> rnd((size_t)(6 * grows));
+        throw_on(tgs_random_logistic(&m_rng, 6 * grows, rnd.data(), 0.0f, 1.0f, ctx.stream),
+                 "generate_random_logistic");
+        const tgs_gaussians g2 = m_gaussians->to_c();
+        throw_on(tgs_densify_apply(&g2, (int64_t)n, src.data(), grows, flags.data(), rnd.data(), ctx.stream),
+                 "DefaultStrategy::duplicate");
+        hip_check(hipStreamSynchronize(ctx.stream), "hipStreamSynchronize");
+    }
+    // default.cu:300-341
+    void prune(RasterizeContext& ctx) {
+        const size_t n = m_gaussians->size();
+        const int64_t n_info = ctx.densification_info ? (int64_t)ctx.densification_info->size() : 0;
+        DeviceArray<uint8_t> alive(std::max<size_t>(n, 1));
+        DeviceArray<int32_t> kept(std::max<size_t>(n, 1));
+        int64_t nk = 0;
+        const tgs_gaussians g = m_gaussians->to_c();
+        const float limit_ss = (float)std::max(ctx.fwd_input.width, ctx.fwd_input.height) * m_params.max_screen_size;
+        throw_on(tgs_prune_select(&g, (const float*)ctx.densification_info->data(), n_info,
+                                  m_params.pruning_opacity_threshold,
+                                  m_params.pruning_scale_threshold * m_gaussians->scene_scale(), limit_ss,
+                                  this_step() > m_params.reset_every ? 1 : 0, alive.data(), kept.data(), &nk,
+                                  ctx.stream),
+                 "DefaultStrategy::prune");
+        last_kept = nk;
+        on_remove((char*)alive.data(), kept.data(), (int)nk);
+    }
+
+    tgs_pcg32 m_rng{0x853C49E6748FEA9Bull, 0xDA3E39CB94B95BDBull};   // pcg32's default state
+};
+
+inline std::unique_ptr<StrategyBase> create_strategy(const std::string& type, std::shared_ptr<GPUGaussian3d> g,
+                                                     std::shared_ptr<GPUGaussian3d> gg, OptimizerBase* optimizer) {
+    if (type == "default") return std::make_unique<DefaultStrategy>(std::move(g), std::move(gg), optimizer);
+    if (type == "mcmc" || type == "improved")
+        throw std::runtime_error("Strategy '" + type + "' is not built (only 'default')");
+    throw std::runtime_error("Unknown strategy type: " + type);
+}
+
+// ---------------------------------------------------------------- metrics and files
+
+// PsnrMetric::evaluate (tinygs/src/loss/psnr.cu:72-128).
+class PsnrMetric {
+public:
+    float evaluate(const Image& pred, const Image& target, hipStream_t stream = nullptr) const {
+        if (pred.shape.width != target.shape.width || pred.shape.height != target.shape.height ||
+            pred.shape.channel != target.shape.channel)
+            throw std::runtime_error("Prediction and target shapes must match");
+        tgs_loss_context c{pred.data, target.data, nullptr, nullptr, pred.shape.width, pred.shape.height,
+                           pred.shape.channel, TGS_DTYPE_FLOAT32};
+        float v = 0.0f;
+        throw_on(tgs_psnr(&c, &v, stream), "PsnrMetric::evaluate");
+        return v;
+    }
+};
+
+// tinygs/include/tinygs/core/pointcloud.hpp:11-26
+struct PointCloud {
+    std::vector<float> points, colors;   // 3 floats per point each; colours in [0, 1]
+    size_t size() const { return points.size() / 3; }
+};
+inline PointCloud load_point_cloud(const std::string& filename) {
+    int64_t n = 0;
+    throw_on(tgs_point_cloud_load(filename.c_str(), &n, nullptr, nullptr), "load_point_cloud");
+    PointCloud pc;
+    pc.points.resize(3 * (size_t)n);
+    pc.colors.resize(3 * (size_t)n);
+    if (n) throw_on(tgs_point_cloud_load(filename.c_str(), &n, pc.points.data(), pc.colors.data()), "load_point_cloud");
+    return pc;
+}
+// save_ply (pointcloud.cpp:111-240) from the device arrays: byte for byte the reference's file.
+inline void save_ply(const std::string& filename, const GPUGaussian3d& gs, bool full_features = false,
+                     hipStream_t stream = nullptr) {
+    const tgs_gaussians g = gs.to_c();
+    throw_on(tgs_ply_save(filename.c_str(), &g, full_features ? 1 : 0, stream), "save_ply");
+}
+// The Gaussians of a full-feature PLY (the inverse of save_ply; no counterpart in the reference).
+inline std::shared_ptr<GPUGaussian3d> load_gaussians_ply(const std::string& filename,
+                                                         DataType sh_dtype = DataType::Float32) {
+    tgs_ply_info info{};
+    throw_on(tgs_ply_read_info(filename.c_str(), &info), "load_gaussians_ply");
+    auto g = std::make_shared<GPUGaussian3d>((size_t)info.n_vertices, sh_dtype);
+    const tgs_gaussians c = g->to_c();
+    throw_on(tgs_ply_load_gaussians(filename.c_str(), &c, nullptr), "load_gaussians_ply");
+    return g;
 }
 
 }  // namespace tinygs_amd

@@ -68,23 +68,30 @@ def build(jobs: int = 8, extra: list[str] | None = None, verbose: bool = True) -
 
 
 ROOT = os.path.dirname(HERE)
-CPP_TEST_SRC = os.path.join(ROOT, "tests", "cpp", "train_step.cpp")
+CPP_TESTS = ("train_step", "densify_step")   # tests/cpp/<name>.cpp -> tests/cpp/_build/<name>
 CPP_TEST_BIN = os.path.join(ROOT, "tests", "cpp", "_build", "train_step")
 
 
+def cpp_test_bin(name: str) -> str:
+    return os.path.join(ROOT, "tests", "cpp", "_build", name)
+
+
 def build_cpp_test(verbose: bool = True) -> str:
-    """Compiles the C++ consumer of include/tinygs_amd/tinygs.hpp (host code
+    """Compiles the C++ consumers of include/tinygs_amd/tinygs.hpp (host code
     only) against the built library."""
-    os.makedirs(os.path.dirname(CPP_TEST_BIN), exist_ok=True)
-    cmd = [hipcc(), "-std=c++17", "-O2", "-Wall", "-I", os.path.join(ROOT, "include"), CPP_TEST_SRC,
-           "-o", CPP_TEST_BIN + ".tmp", "-L", HERE, "-ltinygs_amd", f"-Wl,-rpath,{HERE}",
-           "-Wl,-rpath,$ORIGIN/../../../tinygs_amd", "-Wl,-rpath,/opt/rocm/lib"]
-    r = subprocess.run(cmd, capture_output=True, text=True)
-    if r.returncode != 0:
-        raise RuntimeError(f"compile failed: {' '.join(cmd)}\n{r.stdout}\n{r.stderr}")
-    os.replace(CPP_TEST_BIN + ".tmp", CPP_TEST_BIN)
-    if verbose:
-        print(f"built {CPP_TEST_BIN}")
+    for name in CPP_TESTS:
+        out = cpp_test_bin(name)
+        os.makedirs(os.path.dirname(out), exist_ok=True)
+        cmd = [hipcc(), "-std=c++17", "-O2", "-Wall", "-I", os.path.join(ROOT, "include"),
+               os.path.join(ROOT, "tests", "cpp", name + ".cpp"),
+               "-o", out + ".tmp", "-L", HERE, "-ltinygs_amd", f"-Wl,-rpath,{HERE}",
+               "-Wl,-rpath,$ORIGIN/../../../tinygs_amd", "-Wl,-rpath,/opt/rocm/lib"]
+        r = subprocess.run(cmd, capture_output=True, text=True)
+        if r.returncode != 0:
+            raise RuntimeError(f"compile failed: {' '.join(cmd)}\n{r.stdout}\n{r.stderr}")
+        os.replace(out + ".tmp", out)
+        if verbose:
+            print(f"built {out}")
     return CPP_TEST_BIN
 
 
