@@ -113,9 +113,10 @@ void launch_blend_forward(const CamParams& cam, const uint2* ranges, const uint3
 // writes 12 floats there: dL/dmean2d (2), |.| sums (2; 0 unless with_abs:
 // only densification reads them), dL/dconic (3),
 // dL/dcolour (3), sum of alpha dL/dalpha, 0. The preprocess backward sums
-// each primitive's records (a wave per primitive above kLightRecords of
-// them, into grad2d[12 p]) and clears rec_count.
-constexpr uint32_t kLightRecords = 4;
+// each primitive's records (16 lanes per primitive above kLightRecords of
+// them, into grad2d[12 p]; the thread of the primitive itself otherwise) and
+// clears rec_count. 16 measured faster than 4, 8 and 32 at config 3.
+constexpr uint32_t kLightRecords = 16;
 // ctl->bwd_queue must be zero on entry (the forward's control reset clears it).
 void launch_blend_backward(const CamParams& cam, const uint32_t* inst_vals, const float2* mean2d,
                            const float4* conic_opacity, const float4* color_pt, const float* image,
