@@ -300,8 +300,8 @@ def main():
         return calibrate_copy(args.calibrate_copy)
 
     if args.gpus != 1:
-        print(f"bench.py runs on exactly one GPU (got --gpus {args.gpus}); multi-GPU sharding of this path "
-              "is a design in DESIGN.md, not a measured configuration", file=sys.stderr)
+        print(f"bench.py runs on exactly one GPU (got --gpus {args.gpus}); this build measures one GPU's "
+              "share of the path, and sharding across GPUs is not implemented", file=sys.stderr)
         sys.exit(2)
 
     import numpy as np
