@@ -184,3 +184,28 @@ def test_point_cloud_load_errors(tmp_path):
     with pytest.raises(RuntimeError, match="list property"):
         io.ply_info(str(bad))
     assert io.ply_info(str(f))["has_colors"] is False
+
+
+@pytest.mark.parametrize("fmt", ["ascii", "binary_little_endian"])
+def test_point_cloud_hostile_counts(tmp_path, fmt):
+    # element counts come from the header: a count far beyond what the file
+    # holds must fail at once (no allocation of it, no loop over it)
+    from tinygs_amd import io
+    vert = "property float x\nproperty float y\nproperty float z\nproperty uchar red\nproperty uchar green\n" \
+           "property uchar blue\n"
+    body = b"0.5 1 2 10 20 30\n" if fmt == "ascii" else struct.pack("<fffBBB", 0.5, 1, 2, 10, 20, 30)
+    huge = 10 ** 15
+    cases = {"vertex": f"element vertex {huge}\n{vert}",
+             "skipped": f"element face {huge}\nproperty int a\nelement vertex 1\n{vert}"}
+    for name, elems in cases.items():
+        f = tmp_path / f"{name}.ply"
+        f.write_bytes(f"ply\nformat {fmt} 1.0\n{elems}end_header\n".encode() + body)
+        with pytest.raises(RuntimeError, match="truncated"):
+            io.load_point_cloud(str(f))
+    # an element without properties holds no bytes, whatever its count
+    f = tmp_path / "empty_elem.ply"
+    f.write_bytes(f"ply\nformat {fmt} 1.0\nelement camera {huge}\nelement vertex 1\n{vert}end_header\n".encode()
+                  + body)
+    pc = io.load_point_cloud(str(f))
+    assert np.array_equal(pc.points, np.array([[0.5, 1, 2]], F))
+    assert np.array_equal(pc.colors, np.array([[10, 20, 30]], F) / F(255.0))

@@ -38,6 +38,7 @@
 #include <algorithm>
 #include <cstdint>
 #include <fstream>
+#include <new>
 #include <sstream>
 #include <string>
 #include <vector>
@@ -462,16 +463,33 @@ int ply_read_vertices(const char* filename, PlyHeader& h, PlyVertices& v, bool l
         v.offsets.push_back(v.stride);
         v.stride += (uint32_t)ply_type_size(p.type);
     }
-    if (!load_rows) return TGS_OK;
     const int64_t n = v.elem->count;
-    v.rows.assign((size_t)n * v.stride, 0);
+    // counts come from the header: bound each by the bytes the file still
+    // holds before allocating or stepping over anything (an ascii value takes
+    // at least one character and one separator)
+    in.seekg(0, std::ios::end);
+    const int64_t file_end = (int64_t)in.tellg();
+    in.seekg(h.data_start);
+    if (file_end < 0 || !in) return fail(TGS_ERR_INVALID, "could not read %s", filename);
+    auto left = [&]() -> int64_t { return file_end - (int64_t)in.tellg(); };
+    if (n > 0 && v.stride == 0)
+        return fail(TGS_ERR_INVALID, "%s: PLY vertex element has no properties", filename);
+    const bool ascii = h.format == 0;
+    if (n > 0 && n > (ascii ? ((left() + 1) / 2) / (int64_t)v.elem->props.size() : left() / (int64_t)v.stride))
+        return fail(TGS_ERR_INVALID, "%s: PLY file truncated (%lld vertices declared)", filename, (long long)n);
+    if (!load_rows) return TGS_OK;
     const bool swap = h.format == 2;
-    if (h.format == 0) {
+    if (ascii) {
+        try {
+            v.rows.assign((size_t)n * v.stride, 0);
+        } catch (const std::bad_alloc&) {
+            return fail(TGS_ERR_INVALID, "%s: no host memory for %lld PLY vertices", filename, (long long)n);
+        }
         // ascii: whitespace-separated tokens, elements in header order
         auto token = [&](std::string& tok) -> bool { return (bool)(in >> tok); };
         std::string tok;
         for (size_t k = 0; k < vi; ++k)
-            for (int64_t i = 0; i < h.elems[k].count; ++i)
+            for (int64_t i = 0; i < h.elems[k].count && !h.elems[k].props.empty(); ++i)
                 for (const PlyProp& p : h.elems[k].props) {
                     if (!token(tok)) return fail(TGS_ERR_INVALID, "%s: PLY file truncated", filename);
                     if (p.is_list) {
@@ -490,8 +508,21 @@ int ply_read_vertices(const char* filename, PlyHeader& h, PlyVertices& v, bool l
         }
         return TGS_OK;
     }
-    // binary: step over the elements before the vertex element
-    for (size_t k = 0; k < vi; ++k)
+    // binary: step over the elements before the vertex element (fixed-size
+    // rows in one seek; rows with lists one by one, each read ends at EOF)
+    for (size_t k = 0; k < vi; ++k) {
+        bool has_list = false;
+        int64_t row_bytes = 0;
+        for (const PlyProp& p : h.elems[k].props) {
+            has_list = has_list || p.is_list;
+            row_bytes += ply_type_size(p.type);
+        }
+        if (!has_list) {
+            if (row_bytes > 0 && h.elems[k].count > left() / row_bytes)
+                return fail(TGS_ERR_INVALID, "%s: PLY file truncated", filename);
+            in.seekg((std::streamoff)(h.elems[k].count * row_bytes), std::ios::cur);
+            continue;
+        }
         for (int64_t i = 0; i < h.elems[k].count; ++i)
             for (const PlyProp& p : h.elems[k].props) {
                 if (p.is_list) {
@@ -505,6 +536,15 @@ int ply_read_vertices(const char* filename, PlyHeader& h, PlyVertices& v, bool l
                     in.seekg(ply_type_size(p.type), std::ios::cur);
                 }
             }
+    }
+    if (!in || (n > 0 && n > left() / (int64_t)v.stride))
+        return fail(TGS_ERR_INVALID, "%s: PLY file truncated (%lld vertices of %u bytes expected)", filename,
+                    (long long)n, v.stride);
+    try {
+        v.rows.assign((size_t)n * v.stride, 0);
+    } catch (const std::bad_alloc&) {
+        return fail(TGS_ERR_INVALID, "%s: no host memory for %lld PLY vertices", filename, (long long)n);
+    }
     if (n > 0 && !in.read((char*)v.rows.data(), (std::streamsize)v.rows.size()))
         return fail(TGS_ERR_INVALID, "%s: PLY file truncated (%lld vertices of %u bytes expected)", filename,
                     (long long)n, v.stride);
