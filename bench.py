@@ -31,6 +31,24 @@ SINGLE_KERNEL = {"preprocess": "tgs::preprocess_kernel", "blend_forward": "tgs::
                  "l1": "tgs::l1_kernel", "blend_backward": "tgs::blend_backward_kernel",
                  "adam": "tgs::adam_kernel"}
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "hbm_traffic_config{}.md")
+COUNTERS_FILE = os.path.join(ROOT, "profiles", "counters_config{}.md")
+# VALU issue peak: one wave64 VALU instruction per CU per clock (4 SIMDs, 4
+# cycles each), 256 CUs at the 2.4 GHz peak engine clock
+VALU_PEAK_GINST_S = 256 * 2.4
+VALU_KERNELS = {"blend_forward": "tgs::blend_forward_kernel", "blend_backward": "tgs::blend_backward_kernel"}
+
+
+def measured_valu_insts(config, kernel):
+    """Wave-level VALU instructions per launch of `kernel` (SQ_INSTS_VALU)
+    from the committed counter summary of this workload, or None."""
+    path = COUNTERS_FILE.format(config)
+    if not os.path.exists(path):
+        return None
+    for line in open(path):
+        m = re.match(r"\|\s*`([^`]+)`\s*\|\s*([0-9.e+]+)\s*\|", line)
+        if m and (m.group(1) == kernel or m.group(1).startswith(kernel + "<")):
+            return float(m.group(2))
+    return None
 
 
 def measured_traffic(config, kernel):
@@ -85,15 +103,52 @@ def algorithmic_bytes(stage, c):
     return 0
 
 
-def cpu_baseline(scene_fn):
+def host_threads():
+    """Cores this process may run on (the GPU box's share), at most 16."""
+    try:
+        n = len(os.sched_getaffinity(0))
+    except AttributeError:
+        n = os.cpu_count() or 1
+    return max(1, min(n, 16))
+
+
+def cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_baseline(scene_fn, config, all_core_iters=3):
+    """The CPU oracle's full iteration on the same seeded scene: the median of
+    `all_core_iters` iterations on all the host cores this process may use
+    (the reported baseline; its results are identical for any thread count),
+    and one iteration on one thread beside it."""
     from oracle import oracle as O
     scene = scene_fn()
     lr = {"means": 1.6e-4, "scene_scale": 1.0, "opacities": 5e-2, "rotations": 1e-3, "scales": 5e-3, "shs": 5e-3}
     O.lib()
-    t0 = time.perf_counter()
-    O.run_iteration(scene, 0.8, 0.2, lr=lr, eps=1e-15)
-    dt = time.perf_counter() - t0
-    return dt * 1e3
+    threads = host_threads()
+
+    def one():
+        t0 = time.perf_counter()
+        O.run_iteration(scene, 0.8, 0.2, lr=lr, eps=1e-15)
+        return (time.perf_counter() - t0) * 1e3
+
+    O.set_threads(threads)
+    all_ms = sorted(one() for _ in range(all_core_iters))
+    O.set_threads(1)
+    one_ms = one()
+    O.set_threads(threads)
+    med = all_ms[len(all_ms) // 2]
+    return {"value": round(med, 1), "unit": "ms/iter", "cores": threads, "kind": "port",
+            "one_thread_ms": round(one_ms, 1), "nproc": os.cpu_count(), "cpu_model": cpu_model(),
+            "sample": f"full config{config} iterations (preprocess, bin, blend fwd, L1+SSIM, blend bwd, preprocess "
+                      f"bwd, SimpleAdam) of the C oracle on the same seeded scene: median of {all_core_iters} on "
+                      f"{threads} OpenMP threads (value), one on 1 thread (one_thread_ms)"}
 
 
 def calibrate_copy(mib):
@@ -391,15 +446,30 @@ def main():
                 "traffic": measured_traffic(args.config, SINGLE_KERNEL[dom[0]]),
                 "algorithmic_bytes": int(dom[2]), "avg_launch_ms": round(dom[1], 5)}
 
+    # VALU roofline of the VALU-bound blend kernels: wave instructions per
+    # launch (counter summary) over the live launch time
+    valu = {}
+    for name, kern in VALU_KERNELS.items():
+        insts = measured_valu_insts(args.config, kern)
+        t = stage_ms[name]
+        if insts is None or t <= 0:
+            valu[name] = None
+            continue
+        ach = insts / (t * 1e-3) / 1e9
+        valu[name] = {"bound": "valu", "achieved": round(ach, 1), "peak": VALU_PEAK_GINST_S,
+                      "unit": "G wave-instructions/s", "frac": round(ach / VALU_PEAK_GINST_S, 4),
+                      "insts_per_launch": insts, "avg_launch_ms": round(t, 5)}
+        print(f"[bench] {name}: {ach:.0f} G VALU wave-instructions/s = {100 * ach / VALU_PEAK_GINST_S:.1f}% of the "
+              f"issue peak", file=sys.stderr)
+
     cpu = None
     if not args.no_cpu_baseline:
-        print("[bench] cpu baseline: one full iteration of the CPU oracle on the same scene, 1 thread",
-              file=sys.stderr, flush=True)
-        cpu_ms = cpu_baseline(scene_fn)
-        cpu = {"value": round(cpu_ms, 1), "unit": "ms/iter", "cores": 1, "kind": "port",
-               "sample": f"one full config{args.config} iteration (preprocess, bin, blend fwd, L1+SSIM, blend bwd, "
-                         "preprocess bwd, SimpleAdam) of the scalar C oracle, single thread, same seeded scene"}
-        print(f"[bench] cpu baseline {cpu_ms:.0f} ms/iter ({cpu_ms / ms:.0f}x the GPU)", file=sys.stderr)
+        print(f"[bench] cpu baseline: full iterations of the CPU oracle on the same scene ({host_threads()} "
+              "threads, then 1)", file=sys.stderr, flush=True)
+        cpu = cpu_baseline(scene_fn, args.config)
+        print(f"[bench] cpu baseline {cpu['value']:.0f} ms/iter on {cpu['cores']} threads "
+              f"({cpu['value'] / ms:.0f}x the GPU), {cpu['one_thread_ms']:.0f} ms on 1 thread; "
+              f"{cpu['cpu_model']}, nproc {cpu['nproc']}", file=sys.stderr)
 
     out = {
         "metric": METRIC, "value": round(ms, 4), "unit": "ms/iter", "n_gpus": 1, "steps": args.steps,
@@ -412,6 +482,7 @@ def main():
                    "parallelism": "single GPU"},
         "stages_ms": {r[0]: round(r[1], 5) for r in rows},
         "roofline": roofline,
+        "valu_roofline": valu,
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)

@@ -29,6 +29,7 @@ extern "C" {
 #define TGS_ERR_HIP 2
 #define TGS_ERR_STATE 3
 #define TGS_ERR_UNSUPPORTED 4
+#define TGS_ERR_CAPACITY 5   /* a no-sync forward needed more instances than reserved */
 
 #define TGS_DTYPE_FLOAT32 0
 #define TGS_DTYPE_FLOAT16 1
@@ -87,6 +88,32 @@ int tgs_rasterizer_set_gaussians(tgs_rasterizer* r, const tgs_gaussians* g);
  * densification_info: optional device float4[n] (max_radii_screen updated). */
 int tgs_rasterizer_forward(tgs_rasterizer* r, const tgs_camera* cam, void* image, int32_t image_dtype,
                            void* densification_info, void* stream);
+/* FastGSRasterizer::forward with flags. TGS_FORWARD_NO_SYNC: the forward
+ * does not wait for the visible / instance counts (the reference waits three
+ * times, forward.cu:133-148,185-187) and sizes the instance buffers by the
+ * capacity of tgs_rasterizer_reserve instead, so a whole iteration can be
+ * queued ahead or captured into a HIP graph. A forward that needs more
+ * instances than reserved renders only the first ones and sets a sticky flag
+ * that tgs_rasterizer_status reports as TGS_ERR_CAPACITY. A captured forward
+ * must not grow a buffer: run one with the same sizes before capturing.
+ * No counterpart in the reference. */
+#define TGS_FORWARD_NO_SYNC 1
+int tgs_rasterizer_forward_ex(tgs_rasterizer* r, const tgs_camera* cam, void* image, int32_t image_dtype,
+                              void* densification_info, int32_t flags, void* stream);
+/* Allocates the instance-sized buffers for up to max_instances instances over
+ * up to grid_tiles tiles (16 x 16 pixels each) and makes that the capacity of
+ * TGS_FORWARD_NO_SYNC forwards. May synchronise the stream. When a buffer has
+ * to grow, the last forward's state is dropped (a backward then needs a new
+ * forward), so reserve before a forward, not between it and its backward.
+ * No counterpart in the reference (its scratch grows inside forward,
+ * fastgs.cu:75-82). */
+int tgs_rasterizer_reserve(tgs_rasterizer* r, int64_t max_instances, int32_t grid_tiles, void* stream);
+/* Synchronises the stream and reports the device-side state of the forwards
+ * queued so far: TGS_ERR_CAPACITY when a no-sync forward overflowed its
+ * capacity (the flag is cleared when clear_capacity_flag is nonzero),
+ * TGS_ERR_STATE when a binning scan failed. Also makes the counts of a no-sync
+ * forward available to tgs_rasterizer_counts without a further wait. */
+int tgs_rasterizer_status(tgs_rasterizer* r, int32_t clear_capacity_flag, void* stream);
 /* FastGSRasterizer::backward (fastgs.cu:238-384). Accumulates (+=) into grads.
  * Must follow a forward on the same Gaussians and camera. */
 int tgs_rasterizer_backward(tgs_rasterizer* r, const void* grad_image, const void* image,
@@ -111,6 +138,13 @@ int tgs_rasterizer_backward(tgs_rasterizer* r, const void* grad_image, const voi
  * row 3 zero; the mean's path only, as in the reference. Read it with
  * tgs_rasterizer_grad_w2c. Combines with the other flags. */
 #define TGS_BACKWARD_POSE 4
+/* TGS_BACKWARD_KEEP_2D: also leave every primitive's summed 2D gradients in
+ * the debug view's grad2d (12 floats per primitive: dL/dmean2d x, y; the
+ * |dL/dmean2d| sums x, y (with densification info); dL/dconic a, b, c;
+ * dL/dcolour r, g, b; the sum of alpha * dL/dalpha; 0), zero for primitives
+ * without a gradient. For parity tests of the blend backward on its own; no
+ * counterpart in the reference. */
+#define TGS_BACKWARD_KEEP_2D 8
 int tgs_rasterizer_backward_ex(tgs_rasterizer* r, const void* grad_image, const void* image,
                                const tgs_gaussians* grads, void* densification_info, int32_t flags, void* stream);
 /* Device byte mask [n] of the last TGS_BACKWARD_SPARSE backward (1: row
@@ -121,7 +155,8 @@ int tgs_rasterizer_grad_row_mask(tgs_rasterizer* r, const uint8_t** mask);
  * 16 floats into host memory, glm column-major like tgs_camera.w2c
  * (w2c_grad[4 c + r] = dL/dw2c(r, c)). Synchronises the stream. */
 int tgs_rasterizer_grad_w2c(tgs_rasterizer* r, float* w2c_grad, void* stream);
-/* Counts of the last forward: visible primitives, instances, tiles. */
+/* Counts of the last forward: visible primitives, instances, tiles. After a
+ * TGS_FORWARD_NO_SYNC forward this waits for the device. */
 int tgs_rasterizer_counts(tgs_rasterizer* r, int64_t* n_visible, int64_t* n_instances, int64_t* n_tiles);
 
 /* Internal buffers of the last forward, for parity tests (device pointers). */
@@ -139,7 +174,7 @@ typedef struct tgs_debug_view {
     const uint32_t* tile_ranges;        /* [2 * n_tiles] */
     const uint32_t* n_contrib;          /* [channel_stride] */
     const uint32_t* tile_max;           /* [n_tiles] */
-    const float* grad2d;                /* NULL: 2D gradients are transient records inside a backward */
+    const float* grad2d;                /* [12n] after a TGS_BACKWARD_KEEP_2D backward, else NULL */
     int64_t n_visible;
     int64_t n_instances;
     int64_t n_tiles;
@@ -225,6 +260,16 @@ int tgs_adam_gather(tgs_adam* a, const int32_t* rows, int64_t n_rows, void* stre
 int tgs_adam_append(tgs_adam* a, int64_t n_new, void* stream);
 /* SimpleAdam::reset_opacity (simple_adam.cu:981-985): opacity moments zeroed. */
 int tgs_adam_reset_opacity(tgs_adam* a, void* stream);
+/* SimpleAdam::reset(int* indices, int num_reset) (simple_adam.cu:944-979):
+ * both moments of rows rows[0 .. n_rows) (device int32) zeroed in every group.
+ * Indices outside the moments' rows are refused before anything is written
+ * (the reference does not check). Synchronises the stream. */
+int tgs_adam_reset_rows(tgs_adam* a, const int32_t* rows, int64_t n_rows, void* stream);
+/* SimpleAdam::reorder(uint* indices) (simple_adam.cu:1037-1097; pure virtual
+ * at optim.hpp:70-73): a gather over all rows, new[i] = old[indices[i]]
+ * (device array of the moments' row count). Refuses out-of-range indices.
+ * Synchronises the stream. */
+int tgs_adam_reorder(tgs_adam* a, const uint32_t* indices, void* stream);
 
 /* ---- densification: the device work of DefaultStrategy
  * (tinygs/src/strategy/default.cu:26-341) and GPUGaussian3d::remove
@@ -266,6 +311,11 @@ int tgs_prune_select(const tgs_gaussians* g, const float* densif, int64_t n_info
 /* Row k of every array of dst (k < dst->n) = row rows[k] of src (same SH
  * dtype): the copy of GPUGaussian3d::remove with its mapping. */
 int tgs_gaussians_gather(const tgs_gaussians* src, const tgs_gaussians* dst, const int32_t* rows, void* stream);
+/* GPUGaussian3d::reorder(uint* indices, stream) (gpu_gaussian.cu:273-310): in
+ * place, row i of every array becomes old row indices[i] (device array of
+ * g->n indices, each in [0, n); out-of-range indices are refused before
+ * anything is written). Uses one temporary array; synchronises the stream. */
+int tgs_gaussians_reorder(const tgs_gaussians* g, const uint32_t* indices, void* stream);
 /* thrust::copy_if of the flag indices (default.cu:198-203, gpu_gaussian.cu:120-124): out
  * (device, capacity n) receives the i < n with flags[i] != 0 in order, *count their number.
  * Synchronises. */

@@ -23,10 +23,10 @@
 //     replaces thrust::device_vector; vec3/vec4 are spelled as float arrays
 //     (3 or 4 floats per element, same memory layout as glm).
 //   * get_params/set_params take a flat name -> number map instead of json.
-//   * Densification (GPUGaussian3d::remove/append, SimpleAdam::remove/
-//     duplicate/reset_opacity, DefaultStrategy) runs through the tgs_densify_*
-//     / tgs_*_gather entry points; Morton reordering and the MCMC-only
-//     OptimizerBase::reset(indices) throw std::runtime_error.
+//   * Densification and reordering (GPUGaussian3d::remove/append/reorder,
+//     SimpleAdam::remove/duplicate/reset(indices)/reorder/reset_opacity,
+//     DefaultStrategy) run through the tgs_densify_* / tgs_*_gather /
+//     tgs_*_reorder / tgs_adam_reset_rows entry points.
 //   * GPUGaussian3d can store sh0 / sh_rest as fp16 (sh_dtype), the storage
 //     mode of the 1M-Gaussian 1080p benchmark; gradients stay fp32.
 // Every failing call throws std::runtime_error carrying tgs_last_error(), as
@@ -265,8 +265,11 @@ public:
                                     "hipMemcpy");
         adopt(g);
     }
-    void reorder(uint32_t*, hipStream_t = nullptr) {
-        throw std::runtime_error("GPUGaussian3d::reorder: Morton reordering is not built");
+    // GPUGaussian3d::reorder (gpu_gaussian.cu:273-310): in place, row i
+    // becomes old row indices[i] (device array of size() indices).
+    void reorder(uint32_t* indices, hipStream_t stream = nullptr) {
+        const tgs_gaussians g = to_c();
+        throw_on(tgs_gaussians_reorder(&g, indices, stream), "GPUGaussian3d::reorder");
     }
 
     float scene_scale() const { return m_scene_scale; }
@@ -635,11 +638,12 @@ public:
     // θ ← Adam(θ, scale · grad); gradients are read, not cleared.
     virtual void step(float scale, hipStream_t stream) = 0;
     virtual void reset() = 0;
-    virtual void remove(char*, int) { throw std::runtime_error("optimizer: densification is not supported"); }
-    virtual void duplicate(int*, int*, int) { throw std::runtime_error("optimizer: densification is not supported"); }
-    virtual void reset(int*, int) { throw std::runtime_error("optimizer: densification is not supported"); }
-    virtual void reorder(uint32_t*) { throw std::runtime_error("optimizer: densification is not supported"); }
-    virtual void reset_opacity() { throw std::runtime_error("optimizer: densification is not supported"); }
+    // optim.hpp:61-76: remove / duplicate default to no-ops, the rest are pure
+    virtual void remove(char*, int) {}
+    virtual void duplicate(int*, int*, int) {}
+    virtual void reset(int* indices, int num_reset) = 0;
+    virtual void reorder(uint32_t* indices) = 0;
+    virtual void reset_opacity() = 0;
     virtual void set_gaussians(std::shared_ptr<GPUGaussian3d> g, std::shared_ptr<GPUGaussian3d> gg) = 0;
     std::shared_ptr<GPUGaussian3d> get_gaussians() const { return m_gaussians; }
     std::shared_ptr<GPUGaussian3d> get_gaussians_grad() const { return m_gaussians_grad; }
@@ -732,6 +736,15 @@ public:
     }
     // SimpleAdam::reset_opacity (simple_adam.cu:981-985).
     void reset_opacity() override { throw_on(tgs_adam_reset_opacity(m_handle, nullptr), "SimpleAdam::reset_opacity"); }
+    // SimpleAdam::reset(int*, int) (simple_adam.cu:944-979): moments of the
+    // rows indices[0 .. num_reset) (device) zeroed.
+    void reset(int* indices, int num_reset) override {
+        throw_on(tgs_adam_reset_rows(m_handle, indices, num_reset, nullptr), "SimpleAdam::reset");
+    }
+    // SimpleAdam::reorder (simple_adam.cu:1037-1097): new row i = old row indices[i].
+    void reorder(uint32_t* indices) override {
+        throw_on(tgs_adam_reorder(m_handle, indices, nullptr), "SimpleAdam::reorder");
+    }
     // Device pointers of a group's moments (0..5 = means, opacities, rotations, scales, sh0, sh_rest).
     std::pair<float*, float*> moments(int group) const {
         float *a = nullptr, *b = nullptr;

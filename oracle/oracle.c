@@ -23,6 +23,7 @@
  *   adam                       closed form (Kingma & Ba 2015)
  */
 #include <math.h>
+#include <omp.h>
 #include <stdint.h>
 #include <stdlib.h>
 #include <string.h>
@@ -80,3 +81,6 @@ void orc_logf_array(int64_t n, const float* x, float* y) { for (int64_t i = 0; i
 void orc_half_bits_array(int64_t n, const float* x, uint16_t* y) { for (int64_t i = 0; i < n; ++i) y[i] = orc_float_to_half_bits(x[i]); }
 void orc_round_half_array(int64_t n, const float* x, float* y) { for (int64_t i = 0; i < n; ++i) y[i] = orc_round_half(x[i]); }
 int orc_version(void) { return 1; }
+/* Threads of the parallel loops (the results do not depend on it). */
+void orc_set_threads(int n) { omp_set_num_threads(n > 0 ? n : 1); }
+int orc_max_threads(void) { return omp_get_max_threads(); }

@@ -76,12 +76,25 @@ def _declare(L):
         fn = getattr(L, pfx + "adam")
         fn.argtypes = [C.c_int64, rp, rp, rp, rp, R, R, R, R, R, R, R, R, C.c_int, C.c_int, R, C.c_int]
         fn.restype = None
+    L.orc_set_threads.argtypes = [C.c_int]
+    L.orc_set_threads.restype = None
+    L.orc_max_threads.argtypes = []
+    L.orc_max_threads.restype = C.c_int
     for name, argt in (("orc_expf_array", [C.c_int64, f32p, f32p]),
                        ("orc_logf_array", [C.c_int64, f32p, f32p]),
                        ("orc_round_half_array", [C.c_int64, f32p, f32p]),
                        ("orc_half_bits_array", [C.c_int64, f32p, u16p])):
         getattr(L, name).argtypes = argt
         getattr(L, name).restype = None
+
+
+def set_threads(n: int):
+    """Threads of the oracle's parallel loops; results are identical for any count."""
+    lib().orc_set_threads(int(n))
+
+
+def max_threads() -> int:
+    return int(lib().orc_max_threads())
 
 
 def _ptr(a):

@@ -63,10 +63,114 @@ def normwise_err(a, b):
     return float(np.abs(a - b).max() / scale)
 
 
-def assert_grads_close(gpu, ref, rtol=GRAD_NORMWISE_RTOL, groups=None):
+# Elementwise bar beside the normwise one: |gpu - cpu| <= 1e-4 |cpu| + atol_g
+# per element, atol_g = GRAD_ELEM_ATOL_FRAC * max |cpu| of the group. The
+# absolute part covers elements whose value is a sum with cancellation: the
+# GPU sums per-(primitive, bucket) records in atomic order and uses the
+# hardware exp in the backward, so the absolute error of such a sum scales
+# with the group's largest terms, not with the (small) result.
+# Measured worst cases: config 3 (1M, 1080p) log-scales, |d| = 5.1e-5 max|cpu|
+# on an element of 1.6e-3 max|cpu| (a large outlier Gaussian whose scale
+# gradient sums ~1e5 pixel terms that cancel); config 2 (100k, 800x800)
+# rotations, |d| up to 1.7e-5 max|cpu|. The p99 of the relative error over
+# the elements above the floor is bounded as well (measured <= 2.4e-4).
+GRAD_ELEM_RTOL = 1e-4
+GRAD_ELEM_ATOL_FRAC = 6e-5
+GRAD_P99_REL = 1e-3
+
+
+def grad_error_stats(a, b, atol_frac=None):
+    """normwise error, elementwise bar violations and the p99 / max relative
+    error over elements with |ref| above the group's absolute floor."""
+    a = np.asarray(a, np.float64)
+    b = np.asarray(b, np.float64)
+    scale = np.abs(b).max() if b.size else 0.0
+    d = np.abs(a - b)
+    atol = (GRAD_ELEM_ATOL_FRAC if atol_frac is None else atol_frac) * scale
+    viol = int(np.count_nonzero(d > GRAD_ELEM_RTOL * np.abs(b) + atol))
+    big = np.abs(b) > atol
+    rel = d[big] / np.abs(b[big]) if big.any() else np.zeros(1)
+    # the elements furthest over the relative part of the bar: (|d| / max|cpu|, |cpu| / max|cpu|)
+    over = d - GRAD_ELEM_RTOL * np.abs(b)
+    top = np.argsort(over)[-3:][::-1] if b.size else []
+    worst = [(float(d[i] / scale) if scale else 0.0, float(abs(b[i]) / scale) if scale else 0.0) for i in top]
+    return {"normwise": normwise_err(a, b), "violations": viol, "p99_rel": float(np.percentile(rel, 99)),
+            "max_rel": float(rel.max()), "n": int(b.size), "worst": worst}
+
+
+def assert_grads_close(gpu, ref, rtol=GRAD_NORMWISE_RTOL, groups=None, elementwise=True, atol_frac=None):
+    """rtol: the normwise bar, a number or a per-group dict; atol_frac: the
+    elementwise floor as a fraction of max |ref| (default GRAD_ELEM_ATOL_FRAC),
+    a number or a per-group dict (groups it omits take the default)."""
     worst = {}
-    for k in groups or ref:
-        e = normwise_err(gpu[k], ref[k])
-        worst[k] = e
-        assert e <= rtol, (k, e, worst)
+    for k in groups or gpu:
+        st = grad_error_stats(gpu[k], ref[k], atol_frac.get(k) if isinstance(atol_frac, dict) else atol_frac)
+        worst[k] = st["normwise"]
+        print(f"[grads] {k}: normwise {st['normwise']:.2e}, p99 rel {st['p99_rel']:.2e}, max rel "
+              f"{st['max_rel']:.2e}, elementwise violations {st['violations']} of {st['n']}; worst "
+              f"(|d|, |ref|) / max|ref|: " + ", ".join(f"({x:.1e}, {y:.1e})" for x, y in st["worst"]), flush=True)
+        bar = rtol[k] if isinstance(rtol, dict) else rtol
+        assert st["normwise"] <= bar, (k, st, worst)
+        if elementwise:
+            assert st["violations"] == 0, (k, st)
+            assert st["p99_rel"] <= GRAD_P99_REL, (k, st)
     return worst
+
+
+def culled_group_scene():
+    """160 Gaussians in five 32-primitive groups, built so that primitives the
+    preprocess culls share a group with survivors:
+
+    * group 0: survivors plus primitives behind the camera, beyond far, with
+      opacity below 1/255, with |q|^2 below 1e-8 (radius still finite) and
+      with q = 0 (radius NaN);
+    * group 1: every primitive culled (behind the camera);
+    * group 2: one survivor (index 80) among culled primitives;
+    * group 3: unchanged;
+    * group 4: one primitive at depth exactly 0.
+    """
+    from tinygs_amd import scenes
+    s = scenes.config1(seed=9, n=160)
+    means, rot, opac = s.means.copy(), s.rotations.copy(), s.opacities.copy()
+    behind = [3, 7] + list(range(32, 64)) + [i for i in range(64, 96) if i % 2 == 0 and i != 80]
+    means[behind, 2] = -4.0                       # depth -1
+    opac[[11] + [i for i in range(64, 96) if i % 2 == 1 and i != 80]] = -9.0
+    means[15, 2] = 197.0                           # depth 200 > far
+    rot[19] = rot[19] * np.float32(1e-5)           # |q|^2 ~ 1e-10
+    rot[23] = 0.0
+    means[140, 2] = -3.0                           # depth exactly 0
+    return scenes.Scene(means, s.scales, rot, opac, s.sh0, s.sh_rest, s.sh_degree, s.camera, s.target)
+
+
+def screen_radius_double(scene, i):
+    """ceil(3 sqrt(lambda_max)) of the dilated 2D covariance of primitive i, in
+    double, with the reference's eigenvalue expression (kernels_forward.cuh:
+    342-348) and its frustum clamp of the Jacobian (:298-307); None when the
+    primitive's radius is not finite."""
+    cam = scene.camera
+    W = cam.w2c.astype(np.float64)
+    t = W[:3, :3] @ scene.means[i].astype(np.float64) + W[:3, 3]
+    q = scene.rotations[i].astype(np.float64)
+    qn = float(q @ q)
+    if qn == 0.0 or t[2] == 0.0:
+        return None
+    r, x, y, z = q / np.sqrt(qn)
+    R = np.array([[1 - 2 * (y * y + z * z), 2 * (x * y - r * z), 2 * (x * z + r * y)],
+                  [2 * (x * y + r * z), 1 - 2 * (x * x + z * z), 2 * (y * z - r * x)],
+                  [2 * (x * z - r * y), 2 * (y * z + r * x), 1 - 2 * (x * x + y * y)]])
+    S2 = np.diag(np.exp(2 * scene.scales[i].astype(np.float64)))
+    Sig = R @ S2 @ R.T
+    lx, rx = (-0.15 * cam.width - cam.cx) / cam.fx, (1.15 * cam.width - cam.cx) / cam.fx
+    ty_, by_ = (-0.15 * cam.height - cam.cy) / cam.fy, (1.15 * cam.height - cam.cy) / cam.fy
+    tx = min(max(t[0] / t[2], lx), rx)
+    ty = min(max(t[1] / t[2], ty_), by_)
+    J = np.array([[cam.fx / t[2], 0, -cam.fx / t[2] * tx], [0, cam.fy / t[2], -cam.fy / t[2] * ty]])
+    c = J @ W[:3, :3] @ Sig @ W[:3, :3].T @ J.T + 0.3 * np.eye(2)
+    det = c[0, 0] * c[1, 1] - c[0, 1] ** 2
+    mid = 0.5 * (c[0, 0] + c[1, 1])
+    l1 = mid + np.sqrt(max(0.1, mid * mid - det))
+    l2 = mid - np.sqrt(max(0.1, mid * mid - det))
+    lam = max(l1, l2)
+    if not np.isfinite(lam) or lam < 0:
+        return None
+    return float(np.ceil(3 * np.sqrt(lam)))

@@ -366,6 +366,20 @@ def test_densification_info(hip, orc):
     assert normwise_err(d[:, 2], dens.reshape(-1, 4)[:, 2]) < 1e-4
 
 
+def test_screen_radius_group_rule(hip, orc):
+    """Culled primitives that share a 32-primitive group with a survivor get
+    their screen radius folded in, as in the reference's warps
+    (kernels_forward.cuh:261-263,342-348); bit-exact against the oracle."""
+    from helpers import culled_group_scene
+    s = culled_group_scene()
+    run = gpu_render(s, densif=True)
+    mr = np.zeros(s.n, np.float32)
+    orc.preprocess(s, "f", max_radii=mr)
+    d = run["ctx"].densification_info.cpu().numpy()
+    assert np.array_equal(d[:, 3].view(np.uint32), mr.view(np.uint32)), np.nonzero(d[:, 3] != mr)
+    assert np.all(d[32:64, 3] == 0) and d[3, 3] > 0
+
+
 # ---------------------------------------------------------------- losses
 
 def _loss_gpu(kind, pred, targ, shape, scale):

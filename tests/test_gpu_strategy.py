@@ -222,3 +222,62 @@ def test_default_strategy_steps_match_oracle(hip, sh_dtype):
         assert int(ctx.densification_info.shape[0]) == g.size()
     assert getattr(st, "last_counts", {}) == ref.counts
     assert g.size() != n
+
+
+@pytest.mark.parametrize("sh_dtype", ["float32", "float16"])
+def test_gaussians_reorder_is_a_gather(hip, sh_dtype):
+    """GPUGaussian3d::reorder (gpu_gaussian.cu:273-310): new row i = old row
+    indices[i], in place, for every array; out-of-range indices are refused
+    before anything changes."""
+    import torch
+    n = 3001
+    p = _rand_params(n, 31)
+    g = _gaussians(p, sh_dtype)
+    before = _host(g)
+    perm = np.random.default_rng(5).permutation(n).astype(np.int32)
+    g.reorder(torch.from_numpy(perm).cuda())
+    torch.cuda.synchronize()
+    after = _host(g)
+    for k in GROUPS:
+        assert np.array_equal(_bits(after[k]), _bits(before[k][perm])), k
+    bad = perm.copy()
+    bad[17] = n
+    with pytest.raises(RuntimeError, match="outside"):
+        g.reorder(torch.from_numpy(bad).cuda())
+    torch.cuda.synchronize()
+    for k, v in _host(g).items():
+        assert np.array_equal(_bits(v), _bits(after[k])), k   # untouched
+
+
+def test_adam_reorder_and_reset_rows(hip):
+    """SimpleAdam::reorder (simple_adam.cu:1037-1097) gathers every moment row;
+    SimpleAdam::reset(indices, n) (:944-979) zeroes both moments of the listed
+    rows and nothing else."""
+    import torch
+    from tinygs_amd.optim import create_optimizer
+    n = 2049
+    p = _rand_params(n, 32)
+    g = _gaussians(p)
+    gg = g.gradient_like()
+    for t in gg.tensors():
+        t.copy_(torch.randn(t.shape, device="cuda"))
+    opt = create_optimizer("simple_adam", g, gg)
+    opt.step(1.0)   # nonzero moments
+    torch.cuda.synchronize()
+    mom = {k: [m.cpu().numpy().reshape(n, -1).copy() for m in opt.moments(k)] for k in GROUPS}
+    perm = np.random.default_rng(6).permutation(n).astype(np.int32)
+    opt.reorder(torch.from_numpy(perm).cuda())
+    torch.cuda.synchronize()
+    for k in GROUPS:
+        for a, b in zip(opt.moments(k), mom[k]):
+            assert np.array_equal(_bits(a.cpu().numpy().reshape(n, -1)), _bits(b[perm])), k
+    rows = np.array([0, 5, 5, 2048, 1000], np.int32)
+    opt.reset_indices(torch.from_numpy(rows).cuda())
+    torch.cuda.synchronize()
+    keep = np.setdiff1d(np.arange(n), rows)
+    for k in GROUPS:
+        for a, b in zip(opt.moments(k), mom[k]):
+            a = a.cpu().numpy().reshape(n, -1)
+            assert np.all(a[rows] == 0) and np.array_equal(_bits(a[keep]), _bits(b[perm][keep])), k
+    with pytest.raises(RuntimeError, match="outside"):
+        opt.reset_indices(torch.tensor([n], dtype=torch.int32, device="cuda"))

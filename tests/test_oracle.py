@@ -573,3 +573,34 @@ def test_pose_gradient_is_outer_product_of_mean_gradients(orc):
     assert np.max(np.abs(G[:3, :3] - dc.T @ m)) < tol
     assert np.max(np.abs(G[:3, 3] - dc.sum(0))) < tol
     assert np.abs(G).max() > 0
+
+
+def test_screen_radius_updated_per_32_primitive_group(orc):
+    """kernels_forward.cuh:261-263,342-348: the screen radius is folded into the
+    densification info by every thread of a 32-lane warp that has a thread
+    still active after the depth / opacity / quaternion culls, culled or not;
+    warps with none leave before it."""
+    from helpers import culled_group_scene, screen_radius_double
+    s = culled_group_scene()
+    mr = np.zeros(s.n, np.float32)
+    pre = orc.preprocess(s, "f", max_radii=mr)
+    vis = pre["n_touched"] > 0
+    assert not vis[32:64].any() and vis[80] and vis[:32].sum() > 10
+    # a group with no active primitive is left untouched
+    assert np.all(mr[32:64] == 0)
+    checked = 0
+    for i in list(range(0, 32)) + list(range(64, 160)):
+        want = screen_radius_double(s, i)
+        if want is None:      # q = 0 (NaN radius) or depth 0: fmaxf keeps the old 0 or takes inf
+            assert mr[i] == 0 or np.isinf(mr[i]), (i, mr[i])
+            continue
+        assert abs(float(mr[i]) - want) <= 1.0, (i, mr[i], want)
+        checked += 1
+    assert checked > 90
+    # culled primitives of live groups do get a radius
+    for i in (3, 7, 11, 15, 19, 64, 65):
+        assert not vis[i] and mr[i] > 0, i
+    # folding is a running max: a second pass with a larger stored value keeps it
+    mr2 = np.full(s.n, 1e6, np.float32)
+    orc.preprocess(s, "f", max_radii=mr2)
+    assert np.all(mr2 == 1e6)

@@ -21,6 +21,9 @@ TGS_LOSS_ASSIGN = 1
 TGS_BACKWARD_ASSIGN = 1
 TGS_BACKWARD_SPARSE = 2
 TGS_BACKWARD_POSE = 4
+TGS_BACKWARD_KEEP_2D = 8
+TGS_FORWARD_NO_SYNC = 1
+TGS_ERR_CAPACITY = 5
 
 _lib = None
 _hip = None
@@ -77,6 +80,9 @@ SIGNATURES = {
     "tgs_rasterizer_destroy": ([P], C.c_int),
     "tgs_rasterizer_set_gaussians": ([P, C.POINTER(tgs_gaussians)], C.c_int),
     "tgs_rasterizer_forward": ([P, C.POINTER(tgs_camera), P, C.c_int32, P, P], C.c_int),
+    "tgs_rasterizer_forward_ex": ([P, C.POINTER(tgs_camera), P, C.c_int32, P, C.c_int32, P], C.c_int),
+    "tgs_rasterizer_reserve": ([P, C.c_int64, C.c_int32, P], C.c_int),
+    "tgs_rasterizer_status": ([P, C.c_int32, P], C.c_int),
     "tgs_rasterizer_backward": ([P, P, P, C.POINTER(tgs_gaussians), P, P], C.c_int),
     "tgs_rasterizer_backward_ex": ([P, P, P, C.POINTER(tgs_gaussians), P, C.c_int32, P], C.c_int),
     "tgs_rasterizer_counts": ([P, C.POINTER(C.c_int64), C.POINTER(C.c_int64), C.POINTER(C.c_int64)], C.c_int),
@@ -102,6 +108,9 @@ SIGNATURES = {
     "tgs_adam_gather": ([P, P, C.c_int64, P], C.c_int),
     "tgs_adam_append": ([P, C.c_int64, P], C.c_int),
     "tgs_adam_reset_opacity": ([P, P], C.c_int),
+    "tgs_adam_reset_rows": ([P, P, C.c_int64, P], C.c_int),
+    "tgs_adam_reorder": ([P, P, P], C.c_int),
+    "tgs_gaussians_reorder": ([C.POINTER(tgs_gaussians), P, P], C.c_int),
     "tgs_pcg32_seed": ([C.POINTER(tgs_pcg32), C.c_uint64, C.c_uint64], None),
     "tgs_pcg32_next_uint": ([C.POINTER(tgs_pcg32), C.c_uint32], C.c_uint32),
     "tgs_psnr": ([C.POINTER(tgs_loss_context), C.POINTER(C.c_float), P], C.c_int),

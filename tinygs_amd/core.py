@@ -119,6 +119,14 @@ class GPUGaussian3d:
             z = torch.zeros((num_dup,) + tuple(t.shape[1:]), dtype=t.dtype, device=t.device)
             setattr(self, name, torch.cat([t, z]))
 
+    def reorder(self, indices, stream=None):
+        """GPUGaussian3d::reorder(uint* indices, stream) (gpu_gaussian.cu:
+        273-310): in place, row i becomes old row indices[i] (device int32 /
+        uint32 tensor of size() indices)."""
+        c = self.to_c()
+        _lib.check(_lib.load().tgs_gaussians_reorder(C.byref(c), ptr(indices), stream_ptr(stream)),
+                   "GPUGaussian3d::reorder")
+
     def remove(self, kept_rows, num_kept: int, stream=None):
         """GPUGaussian3d::remove (gpu_gaussian.cu:117-158): keep the rows
         listed (in order) in the device int32 tensor kept_rows[:num_kept]."""

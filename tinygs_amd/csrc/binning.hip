@@ -113,7 +113,7 @@ __device__ uint32_t wave_look_back(uint64_t* status, uint32_t bid, uint32_t tota
             continue;
         }
         if (++spins > kSpinLimit) {
-            if (lane == 0) atomicOr(err, 1u);
+            if (lane == 0) atomicOr(err, kErrLookBack);
             break;
         }
         __builtin_amdgcn_s_sleep(1);
@@ -500,8 +500,8 @@ __device__ __forceinline__ bool will_contribute_e(float mx, float my, float ca, 
 constexpr uint32_t kEmitStage = 4096;
 
 __global__ void __launch_bounds__(256) emit_kernel(const uint32_t* __restrict__ prims,
-                                                   const uint32_t* __restrict__ offs, const BinCtl* ctl,
-                                                   int64_t max_count, const uint4* __restrict__ rec,
+                                                   const uint32_t* __restrict__ offs, BinCtl* ctl,
+                                                   int64_t max_count, int64_t max_inst, const uint4* __restrict__ rec,
                                                    const uint32_t* __restrict__ tile_bits, uint32_t grid_w,
                                                    uint32_t* __restrict__ inst_keys,
                                                    uint32_t* __restrict__ inst_vals,
@@ -512,12 +512,21 @@ __global__ void __launch_bounds__(256) emit_kernel(const uint32_t* __restrict__ 
     const int64_t k0 = (int64_t)blockIdx.x * blockDim.x;
     if (k0 >= n) return;
     const uint32_t range_a = offs[k0], range_b = offs[min(k0 + (int64_t)blockDim.x, n)];
-    const bool staged = range_b - range_a <= kEmitStage;
+    // Slots come from the offsets scan and stay below the instance count the
+    // buffers were sized for; a slot beyond it (offsets broken by a failed
+    // scan) is dropped and flagged instead of written.
+    const bool in_range = range_a <= range_b && (int64_t)range_b <= max_inst;
+    const bool staged = in_range && range_b - range_a <= kEmitStage;
+    // (past a reserved capacity that the instances exceed is kErrCapacity's case)
+    if (t == 0 && !in_range && (int64_t)ctl->I <= max_inst) atomicOr(&ctl->err, kErrOffsets);
     auto put = [&](uint32_t pos, uint32_t tile, uint32_t prim) {
         if (staged) {
-            s_key[pos - range_a] = tile;
-            s_val[pos - range_a] = prim;
-        } else {
+            const uint32_t l = pos - range_a;   // < kEmitStage whenever the offsets are monotone
+            if (l < kEmitStage) {
+                s_key[l] = tile;
+                s_val[l] = prim;
+            }
+        } else if ((int64_t)pos < max_inst) {
             inst_keys[pos] = tile;
             inst_vals[pos] = prim;
         }
@@ -531,6 +540,9 @@ __global__ void __launch_bounds__(256) emit_kernel(const uint32_t* __restrict__ 
         p = prims[k];
         off = offs[k];
         cap = offs[k + 1] - off;   // slots reserved for this primitive (= its n_touched)
+        // a capacity the instances outgrow (no-sync forward): the slots below
+        // it are still all written, so the sorted prefix holds valid pairs only
+        if ((int64_t)off + cap > max_inst) cap = (int64_t)off < max_inst ? (uint32_t)(max_inst - off) : 0u;
         first_slot[p] = off;
         bits = tile_bits[p];
         const uint4 r0 = rec[2 * (size_t)p], r1 = rec[2 * (size_t)p + 1];
@@ -590,12 +602,13 @@ __global__ void __launch_bounds__(256) emit_kernel(const uint32_t* __restrict__ 
     }
 }
 
-void launch_emit_instances(const uint32_t* prims, const uint32_t* offs, const BinCtl* ctl, int64_t max_count,
-                           const uint4* rec, const uint32_t* tile_bits, uint32_t grid_w, uint32_t* inst_keys,
-                           uint32_t* inst_vals, uint32_t* first_slot, hipStream_t s) {
+void launch_emit_instances(const uint32_t* prims, const uint32_t* offs, BinCtl* ctl, int64_t max_count,
+                           int64_t max_inst, const uint4* rec, const uint32_t* tile_bits, uint32_t grid_w,
+                           uint32_t* inst_keys, uint32_t* inst_vals, uint32_t* first_slot, hipStream_t s) {
     if (max_count <= 0) return;
-    emit_kernel<<<(unsigned)((max_count + 255) / 256), 256, 0, s>>>(prims, offs, ctl, max_count, rec, tile_bits,
-                                                                    grid_w, inst_keys, inst_vals, first_slot);
+    emit_kernel<<<(unsigned)((max_count + 255) / 256), 256, 0, s>>>(prims, offs, ctl, max_count, max_inst, rec,
+                                                                    tile_bits, grid_w, inst_keys, inst_vals,
+                                                                    first_slot);
 }
 
 // ---------------------------------------------------------------- ranges
@@ -625,8 +638,9 @@ void launch_fill_u32(uint32_t* p, uint32_t value, int64_t n, hipStream_t s) {
 // (0 <= i <= n) sits on the boundary between keys[i - 1] and keys[i]
 // (sentinels -1 and n_tiles), closes the previous tile's range, opens the
 // next one and clears the tiles strictly between them.
-__global__ void tile_ranges_kernel(const uint32_t* __restrict__ keys, int64_t n, uint2* __restrict__ ranges,
-                                   uint32_t n_tiles) {
+__global__ void tile_ranges_kernel(const uint32_t* __restrict__ keys, const uint32_t* d_n, int64_t max_n,
+                                   uint2* __restrict__ ranges, uint32_t n_tiles) {
+    const int64_t n = resolve_n(d_n, max_n);
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i > n) return;
     // keys are tile ids < n_tiles; min() keeps a corrupt key from writing out of range
@@ -635,12 +649,36 @@ __global__ void tile_ranges_kernel(const uint32_t* __restrict__ keys, int64_t n,
     if (prev == (int64_t)n_tiles) return;
     if (cur == prev) return;
     if (i > 0) ranges[prev].y = (uint32_t)i;
-    if (i < n) ranges[cur].x = (uint32_t)i;
+    if (i < n && cur < (int64_t)n_tiles) ranges[cur].x = (uint32_t)i;
     for (int64_t tt = prev + 1; tt < cur; ++tt) ranges[tt] = make_uint2(0u, 0u);
 }
 
-void launch_tile_ranges(const uint32_t* inst_keys, int64_t n_inst, uint2* ranges, uint32_t n_tiles, hipStream_t s) {
-    tile_ranges_kernel<<<(unsigned)((n_inst + 1 + 255) / 256), 256, 0, s>>>(inst_keys, n_inst, ranges, n_tiles);
+void launch_tile_ranges(const uint32_t* inst_keys, const uint32_t* d_n, int64_t max_inst, uint2* ranges,
+                        uint32_t n_tiles, hipStream_t s) {
+    tile_ranges_kernel<<<(unsigned)((max_inst + 1 + 255) / 256), 256, 0, s>>>(inst_keys, d_n, max_inst, ranges,
+                                                                            n_tiles);
+}
+
+__global__ void capacity_check_kernel(BinCtl* ctl, int64_t cap) {
+    if (threadIdx.x == 0 && (int64_t)ctl->I > cap) atomicOr(&ctl->err, kErrCapacity);
+}
+
+__global__ void clear_err_bits_kernel(BinCtl* ctl, uint32_t bits) {
+    if (threadIdx.x == 0) atomicAnd(&ctl->err, ~bits);
+}
+
+void launch_capacity_check(BinCtl* ctl, int64_t cap, hipStream_t s) { capacity_check_kernel<<<1, 64, 0, s>>>(ctl, cap); }
+
+void launch_clear_err_bits(BinCtl* ctl, uint32_t bits, hipStream_t s) {
+    clear_err_bits_kernel<<<1, 64, 0, s>>>(ctl, bits);
+}
+
+bool radix_digits_fit(bool depth, int n_passes, const int* bits) {
+    const int maxb = depth ? kDepthMaxDigits : kTileMaxDigits;
+    if (n_passes < 1 || n_passes > 4) return false;
+    for (int p = 0; p < n_passes; ++p)
+        if (bits[p] < 1 || (1 << bits[p]) > maxb) return false;
+    return true;
 }
 
 }  // namespace tgs

@@ -217,6 +217,7 @@ struct tgs_rasterizer {
     bool row_mask_valid = false;
     DevBuf pose_partial, pose_grad;   // pose gradient: per-chunk partial sums, the 4 x 4 result
     bool pose_valid = false;
+    bool grad2d_valid = false;   // grad2d holds every primitive's 2D sums (TGS_BACKWARD_KEEP_2D)
     uint32_t depth_key_base = 0;   // the sorted depth keys are key - depth_key_base
     // temp
     DevBuf grad2d;
@@ -231,6 +232,8 @@ struct tgs_rasterizer {
     bool bwd_queues_clear = false;   // backward queue counters still zero since the last forward
     CamParams cam{};
     int64_t n = 0, V = 0, I = 0;
+    int64_t inst_cap = 0;            // reserved instance capacity (tgs_rasterizer_reserve)
+    bool counts_on_device = false;   // the last forward did not wait for V, I
     int psel = 0, isel = 0;
 };
 
@@ -244,6 +247,21 @@ static int ensure_status(tgs_rasterizer* r, int64_t entries, hipStream_t s) {
         launch_fill_u32(r->lb_status.as<uint32_t>(), 0u, (int64_t)(r->lb_status.bytes / 4), s);
         if (wrap) r->epoch = 0;
     }
+    return TGS_OK;
+}
+
+// Instance-sized buffers for up to `inst` instances over T tiles: sort
+// pairs, blend checkpoints and backward work items, 2D-gradient records.
+static int ensure_instances(tgs_rasterizer* r, int64_t inst, uint32_t T, hipStream_t s) {
+    const int64_t ii = inst > 0 ? inst : 1;
+    for (int k = 0; k < 2; ++k) {
+        TGS_TRY(ensure(r->ikeys[k], 4 * ii, s));
+        TGS_TRY(ensure(r->ivals[k], 4 * ii, s));
+    }
+    const size_t slots = blend_ckpt_slots(inst > 0 ? inst : 0, T);
+    TGS_TRY(ensure(r->ckpt, sizeof(float4) * kTilePixels * slots, s));
+    TGS_TRY(ensure(r->items, sizeof(uint4) * slots, s));
+    TGS_TRY(ensure(r->records, 3 * sizeof(float4) * (size_t)ii, s));
     return TGS_OK;
 }
 
@@ -335,21 +353,69 @@ static GaussianView view_of(const tgs_gaussians& g) {
     return v;
 }
 
-int tgs_rasterizer_forward(tgs_rasterizer* r, const tgs_camera* camera, void* image, int32_t image_dtype,
-                           void* densification_info, void* stream) {
+// Depth-sort digit plan: visible depths lie in [near, far] (preprocess culls
+// the rest), so with near > 0 the keys (float bits) minus bits(near) span
+// only the bits of bits(far) - bits(near): 27 for near 0.01, far 100, i.e.
+// three passes of 9-bit digits instead of four of 8.
+struct SortPlan {
+    uint32_t key_base = 0;
+    int n_dp = 4, dshift[4] = {0, 0, 0, 0}, dbits[4] = {0, 0, 0, 0};
+    int n_tp = 1, tshift[2] = {0, 0}, tbits[2] = {0, 0};
+};
+
+static int plan_sorts(const CamParams& cam, SortPlan& sp) {
+    int key_bits = 32;
+    if (cam.near_ > 0.f && cam.far_ >= cam.near_ && cam.far_ <= 3.0e38f) {
+        sp.key_base = f2u(cam.near_);
+        const uint32_t range = f2u(cam.far_) - sp.key_base;
+        key_bits = range ? 32 - __builtin_clz(range) : 1;
+    }
+    sp.n_dp = key_bits <= 9 ? 1 : key_bits <= 18 ? 2 : key_bits <= 27 ? 3 : 4;
+    for (int p = 0; p < sp.n_dp; ++p) {
+        sp.dbits[p] = (key_bits + sp.n_dp - 1) / sp.n_dp;
+        sp.dshift[p] = p * sp.dbits[p];
+    }
+    // tile key bits: one pass up to 8 bits, else two passes of ceil(bits/2) and the rest
+    const uint32_t T = cam.grid_w * cam.grid_h;
+    int bits = 1;
+    while ((1u << bits) < T) ++bits;
+    sp.n_tp = bits <= 8 ? 1 : 2;
+    sp.tbits[0] = sp.n_tp == 1 ? bits : (bits + 1) / 2;
+    sp.tbits[1] = bits - (bits + 1) / 2;
+    sp.tshift[0] = 0;
+    sp.tshift[1] = sp.tbits[0];
+    if (!radix_digits_fit(true, sp.n_dp, sp.dbits) || !radix_digits_fit(false, sp.n_tp, sp.tbits))
+        return fail(TGS_ERR_UNSUPPORTED, "no radix digit plan for %d depth-key bits / %u tiles", key_bits, T);
+    return TGS_OK;
+}
+
+static int rasterizer_forward(tgs_rasterizer* r, const tgs_camera* camera, void* image, int32_t image_dtype,
+                              void* densification_info, int32_t flags, void* stream) {
     if (!r) return fail(TGS_ERR_INVALID, "rasterizer is NULL");
     if (!r->has_g) return fail(TGS_ERR_STATE, "Gaussians not set");
     if (!image) return fail(TGS_ERR_INVALID, "image is NULL");
     if (image_dtype != TGS_DTYPE_FLOAT32)
         return fail(TGS_ERR_UNSUPPORTED, "image dtype %d: only float32 images are supported", image_dtype);
+    if (flags & ~TGS_FORWARD_NO_SYNC) return fail(TGS_ERR_INVALID, "unknown forward flags 0x%x", flags);
+    const bool nosync = (flags & TGS_FORWARD_NO_SYNC) != 0;
     hipStream_t s = (hipStream_t)stream;
     CamParams cam;
     TGS_TRY(build_camera(camera, cam));
+    const uint32_t T = cam.grid_w * cam.grid_h;
+    // instance tile keys are 16-bit in the reference (kernels_forward.cuh:477,521;
+    // forward.cu:214 sorts 16 bits), which caps the grid at 65,536 tiles
+    if ((uint64_t)cam.grid_w * cam.grid_h > 65536u)
+        return fail(TGS_ERR_UNSUPPORTED, "%ux%u tiles exceed the 65,536 tiles of 16-bit tile keys", cam.grid_w,
+                    cam.grid_h);
+    if (nosync && r->inst_cap <= 0)
+        return fail(TGS_ERR_STATE, "TGS_FORWARD_NO_SYNC needs an instance capacity (tgs_rasterizer_reserve)");
+    SortPlan sp;
+    TGS_TRY(plan_sorts(cam, sp));
     r->fwd_done = false;
     r->row_mask_valid = false;
     r->pose_valid = false;
+    r->grad2d_valid = false;
     const int64_t n = r->g.n;
-    const uint32_t T = cam.grid_w * cam.grid_h;
     const size_t cs = (size_t)cam.tiled_w * cam.tiled_h * 64u;
     const int64_t nn = n > 0 ? n : 1;
     TGS_TRY(ensure(r->n_touched, 4 * nn, s));
@@ -376,8 +442,13 @@ int tgs_rasterizer_forward(tgs_rasterizer* r, const tgs_camera* camera, void* im
     TGS_TRY(ensure(r->tile_max, 4 * (size_t)T, s));
     TGS_TRY(ensure(r->tile_loaded, 4 * (size_t)T, s));
     TGS_TRY(ensure(r->n_contrib, 4 * cs, s));
-    TGS_TRY(ensure(r->radix_counts, 4 * (size_t)radix_count_entries(nn, true), s));
-    TGS_TRY(ensure_status(r, std::max(scan_status_entries(nn), scan_status_entries(radix_count_entries(nn, true))), s));
+    // without a host wait the instance buffers are sized by the reserved capacity up front
+    const int64_t cap0 = nosync ? r->inst_cap : 0;
+    TGS_TRY(ensure(r->radix_counts, 4 * (size_t)std::max(radix_count_entries(nn, true),
+                                                          radix_count_entries(cap0 > 0 ? cap0 : 1, false)), s));
+    TGS_TRY(ensure_status(r, std::max({scan_status_entries(nn), scan_status_entries(radix_count_entries(nn, true)),
+                                       scan_status_entries(radix_count_entries(cap0 > 0 ? cap0 : 1, false))}), s));
+    if (nosync) TGS_TRY(ensure_instances(r, cap0, T, s));
 
     GaussianView gv = view_of(r->g);
     BinCtl* ctl = r->bin_ctl.as<BinCtl>();
@@ -397,75 +468,56 @@ int tgs_rasterizer_forward(tgs_rasterizer* r, const tgs_camera* camera, void* im
     int psel;
     {
         StageScope sc(ST_DEPTH, s);
-        // visible depths lie in [near, far] (preprocess culls the rest), so with
-        // near > 0 the keys (float bits) minus bits(near) span only the bits of
-        // bits(far) - bits(near): 27 for near 0.01, far 100, i.e. three passes
-        // of 9-bit digits instead of four of 8
-        uint32_t key_base = 0;
-        int key_bits = 32;
-        if (cam.near_ > 0.f && cam.far_ >= cam.near_ && cam.far_ <= 3.0e38f) {
-            key_base = f2u(cam.near_);
-            const uint32_t range = f2u(cam.far_) - key_base;
-            key_bits = range ? 32 - __builtin_clz(range) : 1;
+        launch_compact_visible(r->n_touched.as<uint32_t>(), r->depth_key.as<uint32_t>(), n, sp.key_base, pk[0],
+                               pv[0], pn[0], ctl, status, r->epoch, s);
+        if (!nosync) {
+            // V, I and the sticky error flag go to the host while the depth sort runs
+            TGS_HIP(hipMemcpyAsync(r->h_counters, ctl, 3 * sizeof(uint32_t), hipMemcpyDeviceToHost, s));
+            TGS_HIP(hipEventRecord(r->ev_counts, s));
         }
-        const int n_dp = key_bits <= 9 ? 1 : key_bits <= 18 ? 2 : key_bits <= 27 ? 3 : 4;
-        int shifts[4] = {0, 0, 0, 0}, bits[4] = {0, 0, 0, 0};
-        for (int p = 0; p < n_dp; ++p) {
-            bits[p] = (key_bits + n_dp - 1) / n_dp;
-            shifts[p] = p * bits[p];
-        }
-        launch_compact_visible(r->n_touched.as<uint32_t>(), r->depth_key.as<uint32_t>(), n, key_base, pk[0], pv[0],
-                               pn[0], ctl, status, r->epoch, s);
-        // V, I and the sticky error flag go to the host while the depth sort runs
-        TGS_HIP(hipMemcpyAsync(r->h_counters, ctl, 3 * sizeof(uint32_t), hipMemcpyDeviceToHost, s));
-        TGS_HIP(hipEventRecord(r->ev_counts, s));
-        psel = radix_sort(pk, pv, pn, &ctl->V, n, true, n_dp, shifts, bits, r->radix_counts.as<uint32_t>(),
+        psel = radix_sort(pk, pv, pn, &ctl->V, n, true, sp.n_dp, sp.dshift, sp.dbits, r->radix_counts.as<uint32_t>(),
                           ctl->tickets + kTicketDepth, status, r->epoch, &ctl->err, s);
         if (psel < 0) return fail(TGS_ERR_STATE, "depth sort digit width");
-        r->depth_key_base = key_base;
+        r->depth_key_base = sp.key_base;
         launch_instance_offsets(pn[psel], n, r->offs.as<uint32_t>(), ctl, status, r->epoch, s);
     }
     TGS_CHECK_LAUNCH();
-    TGS_HIP(hipEventSynchronize(r->ev_counts));
-    if (r->h_counters[2]) return fail(TGS_ERR_STATE, "binning look-back did not complete (error flag %u)",
-                                      r->h_counters[2]);
-    const int64_t V = r->h_counters[0];
-    const int64_t I = r->h_counters[1];
-    const int64_t ii = I > 0 ? I : 1;
-    for (int k = 0; k < 2; ++k) {
-        TGS_TRY(ensure(r->ikeys[k], 4 * ii, s));
-        TGS_TRY(ensure(r->ivals[k], 4 * ii, s));
+    int64_t V = -1, I = -1, cap = cap0;
+    if (!nosync) {
+        TGS_HIP(hipEventSynchronize(r->ev_counts));
+        // (a capacity flag left by an earlier no-sync forward does not concern this one)
+        if (r->h_counters[2] & ~kErrCapacity)
+            return fail(TGS_ERR_STATE, "binning failed on the device (error flags 0x%x)", r->h_counters[2]);
+        V = r->h_counters[0];
+        I = r->h_counters[1];
+        cap = I;
+        TGS_TRY(ensure(r->radix_counts,
+                       4 * (size_t)std::max(radix_count_entries(I > 0 ? I : 1, false), radix_count_entries(nn, true)),
+                       s));
+        TGS_TRY(ensure_status(r, scan_status_entries(radix_count_entries(I > 0 ? I : 1, false)), s));
+        TGS_TRY(ensure_instances(r, I, T, s));
+        status = r->lb_status.as<uint64_t>();
     }
-    TGS_TRY(ensure(r->radix_counts, 4 * (size_t)std::max(radix_count_entries(ii, false), radix_count_entries(nn, true)),
-                   s));
-    TGS_TRY(ensure_status(r, scan_status_entries(radix_count_entries(ii, false)), s));
-    const size_t slots = blend_ckpt_slots(I, T);
-    TGS_TRY(ensure(r->ckpt, sizeof(float4) * kTilePixels * slots, s));
-    TGS_TRY(ensure(r->items, sizeof(uint4) * slots, s));
-    TGS_TRY(ensure(r->records, 3 * sizeof(float4) * (size_t)ii, s));
-    status = r->lb_status.as<uint64_t>();
-    // tile key bits: one pass up to 8 bits, else two passes of ceil(bits/2) and the rest
-    int bits = 1;
-    while ((1u << bits) < T) ++bits;
-    const int n_tile_passes = bits <= 8 ? 1 : 2;
-    const int tbits[2] = {n_tile_passes == 1 ? bits : (bits + 1) / 2, bits - (bits + 1) / 2};
-    const int tshifts[2] = {0, tbits[0]};
     {
         StageScope sc(ST_EMIT, s);
-        launch_emit_instances(pv[psel], r->offs.as<uint32_t>(), ctl, n, r->rec.as<uint4>(),
+        launch_emit_instances(pv[psel], r->offs.as<uint32_t>(), ctl, n, cap, r->rec.as<uint4>(),
                               r->tile_bits.as<uint32_t>(), cam.grid_w,
                               r->ikeys[0].as<uint32_t>(), r->ivals[0].as<uint32_t>(), r->first_slot.as<uint32_t>(),
                               s);
     }
     uint32_t* ik[2] = {r->ikeys[0].as<uint32_t>(), r->ikeys[1].as<uint32_t>()};
     uint32_t* iv[2] = {r->ivals[0].as<uint32_t>(), r->ivals[1].as<uint32_t>()};
+    // without a host wait the instance count is read on the device (min(I, capacity))
+    const uint32_t* d_inst = nosync ? &ctl->I : nullptr;
     int isel;
     {
         StageScope sc(ST_TILES, s);
-        isel = radix_sort(ik, iv, nullptr, nullptr, I, false, n_tile_passes, tshifts, tbits,
+        isel = radix_sort(ik, iv, nullptr, d_inst, cap, false, sp.n_tp, sp.tshift, sp.tbits,
                           r->radix_counts.as<uint32_t>(), ctl->tickets + kTicketTile, status, r->epoch, &ctl->err, s);
-        launch_tile_ranges(ik[isel], I, r->ranges.as<uint2>(), T, s);
+        if (isel < 0) return fail(TGS_ERR_STATE, "tile sort digit width");
+        launch_tile_ranges(ik[isel], d_inst, cap, r->ranges.as<uint2>(), T, s);
     }
+    if (nosync) launch_capacity_check(ctl, cap, s);
     {
         StageScope sc(ST_BLENDF, s);
         launch_blend_forward(cam, r->ranges.as<uint2>(), iv[isel], r->mean2d.as<float2>(),
@@ -478,10 +530,57 @@ int tgs_rasterizer_forward(tgs_rasterizer* r, const tgs_camera* camera, void* im
     r->n = n;
     r->V = V;
     r->I = I;
+    r->counts_on_device = nosync;
     r->psel = psel;
     r->isel = isel;
     r->fwd_done = true;
     r->bwd_queues_clear = true;
+    return TGS_OK;
+}
+
+int tgs_rasterizer_forward(tgs_rasterizer* r, const tgs_camera* camera, void* image, int32_t image_dtype,
+                           void* densification_info, void* stream) {
+    return rasterizer_forward(r, camera, image, image_dtype, densification_info, 0, stream);
+}
+
+int tgs_rasterizer_forward_ex(tgs_rasterizer* r, const tgs_camera* camera, void* image, int32_t image_dtype,
+                              void* densification_info, int32_t flags, void* stream) {
+    return rasterizer_forward(r, camera, image, image_dtype, densification_info, flags, stream);
+}
+
+int tgs_rasterizer_reserve(tgs_rasterizer* r, int64_t max_instances, int32_t grid_tiles, void* stream) {
+    if (!r) return fail(TGS_ERR_INVALID, "rasterizer is NULL");
+    if (max_instances < 1 || max_instances > (int64_t)0xffffffffll || grid_tiles < 1 || grid_tiles > 65536)
+        return fail(TGS_ERR_INVALID, "reserve: %lld instances, %d tiles", (long long)max_instances, grid_tiles);
+    hipStream_t s = (hipStream_t)stream;
+    const void* before[5] = {r->ikeys[0].p, r->ivals[0].p, r->ckpt.p, r->items.p, r->records.p};
+    TGS_TRY(ensure(r->radix_counts, 4 * (size_t)radix_count_entries(max_instances, false), s));
+    TGS_TRY(ensure_status(r, scan_status_entries(radix_count_entries(max_instances, false)), s));
+    TGS_TRY(ensure_instances(r, max_instances, (uint32_t)grid_tiles, s));
+    const void* after[5] = {r->ikeys[0].p, r->ivals[0].p, r->ckpt.p, r->items.p, r->records.p};
+    // grown buffers do not keep the last forward's instance lists and checkpoints
+    if (memcmp(before, after, sizeof(before)) != 0) r->fwd_done = false;
+    r->inst_cap = max_instances;
+    return TGS_OK;
+}
+
+int tgs_rasterizer_status(tgs_rasterizer* r, int32_t clear_capacity_flag, void* stream) {
+    if (!r) return fail(TGS_ERR_INVALID, "rasterizer is NULL");
+    hipStream_t s = (hipStream_t)stream;
+    uint32_t w[3] = {0, 0, 0};
+    TGS_HIP(hipMemcpyAsync(w, r->bin_ctl.p, sizeof(w), hipMemcpyDeviceToHost, s));
+    TGS_HIP(hipStreamSynchronize(s));
+    if (r->fwd_done && r->counts_on_device) {
+        r->V = w[0];
+        r->I = w[1];
+        r->counts_on_device = false;
+    }
+    if (w[2] & kErrCapacity) {
+        if (clear_capacity_flag) launch_clear_err_bits(r->bin_ctl.as<BinCtl>(), kErrCapacity, s);
+        TGS_CHECK_LAUNCH();
+        return fail(TGS_ERR_CAPACITY, "forward needed %u instances, %lld reserved", w[1], (long long)r->inst_cap);
+    }
+    if (w[2]) return fail(TGS_ERR_STATE, "binning failed on the device (error flags 0x%x)", w[2]);
     return TGS_OK;
 }
 
@@ -505,7 +604,7 @@ int tgs_rasterizer_backward_ex(tgs_rasterizer* r, const void* grad_image, const 
     TGS_TRY(ensure(r->heavy, sizeof(uint4) * (size_t)(n > 0 ? n : 1), s));
     TGS_TRY(ensure(r->live, sizeof(uint4) * (size_t)(n > 0 ? n : 1), s));
     TGS_TRY(ensure(r->chunk_counts, sizeof(uint2) * (size_t)std::max<int64_t>(pb_chunks(n), 1), s));
-    if (flags & ~(TGS_BACKWARD_ASSIGN | TGS_BACKWARD_SPARSE | TGS_BACKWARD_POSE))
+    if (flags & ~(TGS_BACKWARD_ASSIGN | TGS_BACKWARD_SPARSE | TGS_BACKWARD_POSE | TGS_BACKWARD_KEEP_2D))
         return fail(TGS_ERR_INVALID, "unknown backward flags 0x%x", flags);
     if ((flags & TGS_BACKWARD_ASSIGN) && (flags & TGS_BACKWARD_SPARSE))
         return fail(TGS_ERR_INVALID, "TGS_BACKWARD_ASSIGN and TGS_BACKWARD_SPARSE are exclusive");
@@ -514,6 +613,8 @@ int tgs_rasterizer_backward_ex(tgs_rasterizer* r, const void* grad_image, const 
     r->row_mask_valid = false;
     r->pose_valid = false;
     const bool pose = (flags & TGS_BACKWARD_POSE) != 0;
+    const bool keep2d = (flags & TGS_BACKWARD_KEEP_2D) != 0;
+    r->grad2d_valid = false;
     if (pose) {
         TGS_TRY(ensure(r->pose_partial, sizeof(float) * 12 * (size_t)std::max<int64_t>(pb_chunks(n), 1), s));
         TGS_TRY(ensure(r->pose_grad, sizeof(float) * 16, s));
@@ -541,11 +642,12 @@ int tgs_rasterizer_backward_ex(tgs_rasterizer* r, const void* grad_image, const 
                                    r->grad2d.as<float>(), gv, (float*)densification_info, mode,
                                    r->row_mask.as<uint8_t>(), r->live.as<uint4>(), r->heavy.as<uint4>(),
                                    r->chunk_counts.as<uint2>(), pose ? r->pose_partial.as<float>() : nullptr,
-                                   pose ? r->pose_grad.as<float>() : nullptr, s);
+                                   pose ? r->pose_grad.as<float>() : nullptr, keep2d, s);
     }
     TGS_CHECK_LAUNCH();
     r->row_mask_valid = mode == kGradSparse;
     r->pose_valid = pose;
+    r->grad2d_valid = keep2d;
     return TGS_OK;
 }
 
@@ -565,9 +667,23 @@ int tgs_rasterizer_grad_row_mask(tgs_rasterizer* r, const uint8_t** mask) {
     return TGS_OK;
 }
 
+// V and I of a forward that did not wait for them: read from the device
+// once the work queued so far has finished.
+static int sync_counts(tgs_rasterizer* r) {
+    if (!r->counts_on_device) return TGS_OK;
+    uint32_t w[2] = {0, 0};
+    TGS_HIP(hipDeviceSynchronize());
+    TGS_HIP(hipMemcpy(w, r->bin_ctl.p, sizeof(w), hipMemcpyDeviceToHost));
+    r->V = w[0];
+    r->I = w[1];
+    r->counts_on_device = false;
+    return TGS_OK;
+}
+
 int tgs_rasterizer_counts(tgs_rasterizer* r, int64_t* n_visible, int64_t* n_instances, int64_t* n_tiles) {
     if (!r) return fail(TGS_ERR_INVALID, "rasterizer is NULL");
     if (!r->fwd_done) return fail(TGS_ERR_STATE, "no forward yet");
+    TGS_TRY(sync_counts(r));
     if (n_visible) *n_visible = r->V;
     if (n_instances) *n_instances = r->I;
     if (n_tiles) *n_tiles = (int64_t)r->cam.grid_w * r->cam.grid_h;
@@ -577,6 +693,7 @@ int tgs_rasterizer_counts(tgs_rasterizer* r, int64_t* n_visible, int64_t* n_inst
 int tgs_rasterizer_debug_view(tgs_rasterizer* r, tgs_debug_view* out) {
     if (!r || !out) return fail(TGS_ERR_INVALID, "NULL argument");
     if (!r->fwd_done) return fail(TGS_ERR_STATE, "no forward yet");
+    TGS_TRY(sync_counts(r));
     out->n_touched = r->n_touched.as<uint32_t>();
     out->bounds = r->rec.as<uint32_t>();
     out->mean2d = r->mean2d.as<float>();
@@ -590,7 +707,8 @@ int tgs_rasterizer_debug_view(tgs_rasterizer* r, tgs_debug_view* out) {
     out->tile_ranges = r->ranges.as<uint32_t>();
     out->n_contrib = r->n_contrib.as<uint32_t>();
     out->tile_max = r->tile_max.as<uint32_t>();
-    out->grad2d = nullptr;   // 2D gradients live in per-(primitive, bucket) records during a backward only
+    // the summed 2D gradients exist only after a TGS_BACKWARD_KEEP_2D backward
+    out->grad2d = r->grad2d_valid ? r->grad2d.as<float>() : nullptr;
     out->n_visible = r->V;
     out->n_instances = r->I;
     out->n_tiles = (int64_t)r->cam.grid_w * r->cam.grid_h;
@@ -977,6 +1095,51 @@ int tgs_adam_append(tgs_adam* a, int64_t n_new, void* stream) {
     });
 }
 
+// Whether every idx[k], k < n, lies in [0, bound). Synchronises the stream.
+static int indices_in_range(const int32_t* idx, int64_t n, int64_t bound, hipStream_t s, bool* ok) {
+    *ok = true;
+    if (n <= 0) return TGS_OK;
+    DevBuf bad;
+    TGS_TRY(ensure(bad, sizeof(uint32_t), s));
+    uint32_t h = 0;
+    launch_fill_u32(bad.as<uint32_t>(), 0u, 1, s);
+    launch_check_indices(idx, n, bound, bad.as<uint32_t>(), s);
+    hipError_t e = hipGetLastError();
+    if (e == hipSuccess) e = hipMemcpyAsync(&h, bad.p, sizeof(h), hipMemcpyDeviceToHost, s);
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    release(bad);
+    if (e != hipSuccess) return fail(TGS_ERR_HIP, "index check: %s", hipGetErrorString(e));
+    *ok = h == 0;
+    return TGS_OK;
+}
+
+int tgs_adam_reset_rows(tgs_adam* a, const int32_t* rows, int64_t n_rows, void* stream) {
+    if (!a || n_rows < 0 || (n_rows > 0 && !rows)) return fail(TGS_ERR_INVALID, "bad argument");
+    hipStream_t s = (hipStream_t)stream;
+    bool ok = true;
+    TGS_TRY(indices_in_range(rows, n_rows, a->rows, s, &ok));
+    if (!ok) return fail(TGS_ERR_INVALID, "SimpleAdam::reset: an index is outside [0, %lld)", (long long)a->rows);
+    for (int k = 0; k < 6; ++k) {
+        launch_zero_rows(a->m1[k].p, rows, n_rows, kGroupMult[k], s);
+        launch_zero_rows(a->m2[k].p, rows, n_rows, kGroupMult[k], s);
+    }
+    TGS_CHECK_LAUNCH();
+    return TGS_OK;
+}
+
+int tgs_adam_reorder(tgs_adam* a, const uint32_t* indices, void* stream) {
+    if (!a || (a->rows > 0 && !indices)) return fail(TGS_ERR_INVALID, "bad argument");
+    if (a->rows > (int64_t)0x7fffffff) return fail(TGS_ERR_UNSUPPORTED, "reorder of more than 2^31 - 1 rows");
+    hipStream_t s = (hipStream_t)stream;
+    const int32_t* rows = (const int32_t*)indices;
+    bool ok = true;
+    TGS_TRY(indices_in_range(rows, a->rows, a->rows, s, &ok));
+    if (!ok) return fail(TGS_ERR_INVALID, "SimpleAdam::reorder: an index is outside [0, %lld)", (long long)a->rows);
+    return adam_rebuild(a, a->rows, s, [&](int k, DevBuf& src, DevBuf& dst) {
+        launch_gather_rows(src.p, dst.p, rows, a->rows, 4 * kGroupMult[k], s);
+    });
+}
+
 int tgs_adam_reset_opacity(tgs_adam* a, void* stream) {
     if (!a) return fail(TGS_ERR_INVALID, "NULL argument");
     const int64_t words = a->rows > 0 ? a->rows : 0;
@@ -1069,6 +1232,38 @@ int tgs_gaussians_gather(const tgs_gaussians* src, const tgs_gaussians* dst, con
         launch_gather_rows(src->sh_rest, dst->sh_rest, rows, n, 180, s);
     }
     TGS_CHECK_LAUNCH();
+    return TGS_OK;
+}
+
+int tgs_gaussians_reorder(const tgs_gaussians* g, const uint32_t* indices, void* stream) {
+    TGS_TRY(check_gaussians(g, false));
+    const int64_t n = g->n;
+    if (n > 0 && !indices) return fail(TGS_ERR_INVALID, "indices is NULL");
+    if (n > (int64_t)0x7fffffff) return fail(TGS_ERR_UNSUPPORTED, "reorder of more than 2^31 - 1 rows");
+    if (n == 0) return TGS_OK;
+    hipStream_t s = (hipStream_t)stream;
+    const int32_t* rows = (const int32_t*)indices;
+    bool ok = true;
+    TGS_TRY(indices_in_range(rows, n, n, s, &ok));
+    if (!ok) return fail(TGS_ERR_INVALID, "GPUGaussian3d::reorder: an index is outside [0, %lld)", (long long)n);
+    const bool half = g->sh_dtype == TGS_DTYPE_FLOAT16;
+    const size_t shb = half ? 2 : 4;
+    void* arr[6] = {g->means, g->scales, g->rotations, g->opacities, g->sh0, g->sh_rest};
+    const size_t row_bytes[6] = {12, 12, 16, 4, 3 * shb, 45 * shb};
+    DevBuf tmp;
+    TGS_TRY(ensure(tmp, row_bytes[5] * (size_t)n, s));
+    hipError_t e = hipSuccess;
+    for (int k = 0; k < 6 && e == hipSuccess; ++k) {
+        if (k >= 4 && half)
+            launch_gather_rows16(arr[k], tmp.p, rows, n, (int)(row_bytes[k] / 2), s);
+        else
+            launch_gather_rows(arr[k], tmp.p, rows, n, (int)row_bytes[k], s);
+        e = hipGetLastError();
+        if (e == hipSuccess) e = hipMemcpyAsync(arr[k], tmp.p, row_bytes[k] * (size_t)n, hipMemcpyDeviceToDevice, s);
+    }
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    release(tmp);
+    if (e != hipSuccess) return fail(TGS_ERR_HIP, "GPUGaussian3d::reorder: %s", hipGetErrorString(e));
     return TGS_OK;
 }
 

@@ -56,6 +56,14 @@ struct BinCtl {
     uint32_t bwd_queue[kBwdQueues * 32];  // next local index of queue q at [32 q] (one line each, from byte 128)
 };
 static_assert(offsetof(BinCtl, bwd_queue) == 128, "backward queue counters start on their own cache line");
+// Bits of BinCtl::err (sticky across forwards until cleared):
+constexpr uint32_t kErrLookBack = 1u;   // a look-back scan gave up waiting (spin bound)
+constexpr uint32_t kErrOffsets = 2u;    // instance offsets beyond the instance buffers
+constexpr uint32_t kErrCapacity = 4u;   // more instances than the reserved capacity (no-sync forward)
+// Sets kErrCapacity when ctl->I > cap.
+void launch_capacity_check(BinCtl* ctl, int64_t cap, hipStream_t s);
+// Clears the given err bits.
+void launch_clear_err_bits(BinCtl* ctl, uint32_t bits, hipStream_t s);
 // Words of bwd_queue: what a backward needs cleared.
 constexpr int kBwdCtlWords = kBwdQueues * 32;
 // Clears every BinCtl word except err.
@@ -87,12 +95,18 @@ int radix_sort(uint32_t* keys[2], uint32_t* vals[2], uint32_t* v2[2], const uint
 // Instances in depth order: thread per depth-sorted primitive k < ctl->V,
 // slots [offs[k], offs[k + 1]).
 // Also writes first_slot[p] = offs[k] for every visible primitive p = prims[k]:
-// the first of the n_touched[p] instance slots reserved for p.
-void launch_emit_instances(const uint32_t* prims, const uint32_t* offs, const BinCtl* ctl, int64_t max_count,
-                           const uint4* rec, const uint32_t* tile_bits, uint32_t grid_w, uint32_t* inst_keys,
-                           uint32_t* inst_vals, uint32_t* first_slot, hipStream_t s);
-// [start, end) per tile, (0, 0) for empty tiles; every entry written.
-void launch_tile_ranges(const uint32_t* inst_keys, int64_t n_inst, uint2* ranges, uint32_t n_tiles, hipStream_t s);
+// the first of the n_touched[p] instance slots reserved for p. Slots at or
+// beyond max_inst (the instance buffers' size) are never written; offsets
+// that would need them set bit 1 of ctl->err.
+void launch_emit_instances(const uint32_t* prims, const uint32_t* offs, BinCtl* ctl, int64_t max_count,
+                           int64_t max_inst, const uint4* rec, const uint32_t* tile_bits, uint32_t grid_w,
+                           uint32_t* inst_keys, uint32_t* inst_vals, uint32_t* first_slot, hipStream_t s);
+// [start, end) per tile, (0, 0) for empty tiles; every entry written. The
+// instance count is min(*d_n, max_inst) (max_inst when d_n is null).
+void launch_tile_ranges(const uint32_t* inst_keys, const uint32_t* d_n, int64_t max_inst, uint2* ranges,
+                        uint32_t n_tiles, hipStream_t s);
+// Whether radix_sort accepts these digit widths (host check, before any launch).
+bool radix_digits_fit(bool depth, int n_passes, const int* bits);
 
 // ---- blend (kernels_forward.cuh:569-715, kernels_backward.cuh:675-927)
 // Checkpoints: the state (C, T) of every pixel before Gaussian 32 b of its
@@ -135,7 +149,7 @@ void launch_preprocess_backward(const GaussianView& g, const CamParams& cam, con
                                 const float4* conic_opacity, uint32_t* rec_count, const uint32_t* first_slot,
                                 const float4* records, float* grad2d, const GradView& out, float* densif, int mode,
                                 uint8_t* row_mask, uint4* live, uint4* heavy, uint2* chunk_counts,
-                                float* pose_partial, float* pose_out, hipStream_t s);
+                                float* pose_partial, float* pose_out, bool keep2d, hipStream_t s);
 
 // ---- PSNR (psnr.cu:72-128): scratch[psnr_scratch_doubles() - 1] receives the
 // sum of (saturate(pred) - target)^2 over the n_padded elements
@@ -163,6 +177,10 @@ void launch_gather_rows(const void* src, void* dst, const int32_t* rows, int64_t
                         hipStream_t s);
 void launch_gather_rows16(const void* src, void* dst, const int32_t* rows, int64_t n_dst, int width, hipStream_t s);
 void launch_reset_opacity(float* opac, int64_t n, float max_opacity, hipStream_t s);
+// Zeroes rows rows[0 .. n_rows) of an array of `words` 4-byte words per row.
+void launch_zero_rows(void* dst, const int32_t* rows, int64_t n_rows, int words, hipStream_t s);
+// bad[0] |= 1 when some idx[k] (k < n) lies outside [0, bound).
+void launch_check_indices(const int32_t* idx, int64_t n, int64_t bound, uint32_t* bad, hipStream_t s);
 
 // ---- utilities
 void launch_fill_u32(uint32_t* p, uint32_t value, int64_t n, hipStream_t s);

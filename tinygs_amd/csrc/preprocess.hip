@@ -120,10 +120,16 @@ __global__ void __launch_bounds__(256) preprocess_kernel(
     const float qrr = qr * qr, qxx_r = qx * qx, qyy_r = qy * qy, qzz_r = qz * qz;
     const float qn = qrr + qxx_r + qyy_r + qzz_r;
     if (qn < 1e-8f) active = false;
+    // The reference's 32-lane warps leave together only when none of their
+    // threads is still active (kernels_forward.cuh:261-263); every thread of
+    // a warp that stays, culled or not, folds its own screen radius into the
+    // densification info (:342-348). Here a wave64 holds two such groups.
+    const uint64_t live = ballot(active);
+    const bool radius = densif != nullptr && i < n && (lane < 32u ? (uint32_t)live : (uint32_t)(live >> 32)) != 0u;
 
     uint32_t xmin = 0, xmax = 0, ymin = 0, ymax = 0, nmax = 0;
     float ca = 0.f, cb = 0.f, cc = 0.f, m2x = 0.f, m2y = 0.f, pthr = 0.f;
-    if (active) {
+    if (active || radius) {
         const float qxx = 2.0f * qxx_r / qn, qyy = 2.0f * qyy_r / qn, qzz = 2.0f * qzz_r / qn;
         const float qxy = 2.0f * qx * qy / qn, qxz = 2.0f * qx * qz / qn, qyz = 2.0f * qy * qz / qn;
         const float qrx = 2.0f * qr * qx / qn, qry = 2.0f * qr * qy / qn, qrz = 2.0f * qr * qz / qn;
@@ -164,9 +170,18 @@ __global__ void __launch_bounds__(256) preprocess_kernel(
         cv_a += kDilation;
         cv_c += kDilation;
         const float det = cv_a * cv_c - cv_b * cv_b;
-        if (det < 1e-8f) {
-            active = false;
-        } else {
+        if (det < 1e-8f) active = false;
+        if (radius) {
+            // kernels_forward.cuh:342-348: fmaxf(old, r); a NaN radius keeps the old value
+            const float mid = 0.5f * (cv_a + cv_c);
+            const float l1 = mid + __builtin_sqrtf(__builtin_fmaxf(0.1f, mid * mid - det));
+            const float l2 = mid - __builtin_sqrtf(__builtin_fmaxf(0.1f, mid * mid - det));
+            const float rad = __builtin_ceilf(3.0f * __builtin_sqrtf(__builtin_fmaxf(l1, l2)));
+            const float old = densif[ii].w;
+            const float nv = __builtin_fmaxf(old, rad);
+            if (f2u(nv) != f2u(old)) densif[ii].w = nv;
+        }
+        if (active) {
             ca = cv_c / det;
             cb = -cv_b / det;
             cc = cv_a / det;
@@ -184,14 +199,6 @@ __global__ void __launch_bounds__(256) preprocess_kernel(
             xmax = min((uint32_t)max(bx1, 0), cam.grid_w);
             ymin = min((uint32_t)max(by0, 0), cam.grid_h);
             ymax = min((uint32_t)max(by1, 0), cam.grid_h);
-            if (densif) {
-                // kernels_forward.cuh:342-348, for primitives still active here
-                const float mid = 0.5f * (cv_a + cv_c);
-                const float l1 = mid + __builtin_sqrtf(__builtin_fmaxf(0.1f, mid * mid - det));
-                const float l2 = mid - __builtin_sqrtf(__builtin_fmaxf(0.1f, mid * mid - det));
-                const float rad = __builtin_ceilf(3.0f * __builtin_sqrtf(__builtin_fmaxf(l1, l2)));
-                if (rad > densif[ii].w) densif[ii].w = rad;
-            }
             nmax = (xmax - xmin) * (ymax - ymin);
             if (nmax == 0) active = false;
         }

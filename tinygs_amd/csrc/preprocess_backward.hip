@@ -421,9 +421,9 @@ template <typename ShT, bool kPose>
 __global__ void __launch_bounds__(256) preprocess_backward_live_kernel(
     const float* __restrict__ means, const float* __restrict__ scales, const float* __restrict__ rots,
     const ShT* __restrict__ shr_all, int bases, CamParams cam, const float4* __restrict__ conic_opacity,
-    uint32_t* __restrict__ rec_count, const float4* __restrict__ records, const float* __restrict__ grad2d,
+    uint32_t* __restrict__ rec_count, const float4* __restrict__ records, const float* grad2d,
     GradView out, float4* __restrict__ densif, int mode, const uint4* __restrict__ live,
-    const uint2* __restrict__ chunk_counts, float* __restrict__ pose_partial) {
+    const uint2* __restrict__ chunk_counts, float* __restrict__ pose_partial, float* keep2d) {
     float pacc[12];
 #pragma unroll
     for (int q = 0; q < 12; ++q) pacc[q] = 0.f;
@@ -453,6 +453,12 @@ __global__ void __launch_bounds__(256) preprocess_backward_live_kernel(
             }
         }
         rec_count[ip] = 0u;
+        if (keep2d && nr <= kLightRecords) {   // the summed 2D gradients, for parity tests (heavy: already there)
+            float4* k2 = (float4*)(keep2d + (size_t)ip * kGradStride);
+            k2[0] = gA;
+            k2[1] = gB;
+            k2[2] = gC;
+        }
         float pm[3], ps[3], pq[4], shv[45];
 #pragma unroll
         for (int c = 0; c < 3; ++c) {
@@ -569,23 +575,24 @@ __global__ void __launch_bounds__(256) pose_reduce_kernel(const float* __restric
 
 template <typename ShT, bool kPose>
 static void launch_live(const GaussianView& g, int bases, const CamParams& cam, const float4* conic_opacity,
-                        uint32_t* rec_count, const float4* records, const float* grad2d, const GradView& out,
+                        uint32_t* rec_count, const float4* records, float* grad2d, const GradView& out,
                         float* densif, int mode, const uint4* live, const uint2* chunk_counts, float* pose_partial,
-                        unsigned chunks, hipStream_t s) {
+                        bool keep2d, unsigned chunks, hipStream_t s) {
     preprocess_backward_live_kernel<ShT, kPose><<<chunks, 256, 0, s>>>(
         g.means, g.scales, g.rotations, (const ShT*)g.sh_rest, bases, cam, conic_opacity, rec_count, records, grad2d,
-        out, (float4*)densif, mode, live, chunk_counts, pose_partial);
+        out, (float4*)densif, mode, live, chunk_counts, pose_partial, keep2d ? grad2d : nullptr);
 }
 
 void launch_preprocess_backward(const GaussianView& g, const CamParams& cam, const uint32_t* n_touched,
                                 const float4* conic_opacity, uint32_t* rec_count, const uint32_t* first_slot,
                                 const float4* records, float* grad2d, const GradView& out, float* densif, int mode,
                                 uint8_t* row_mask, uint4* live, uint4* heavy, uint2* chunk_counts,
-                                float* pose_partial, float* pose_out, hipStream_t s) {
+                                float* pose_partial, float* pose_out, bool keep2d, hipStream_t s) {
     if (g.n <= 0) {
         if (pose_out) launch_fill_u32((uint32_t*)pose_out, 0u, 16, s);
         return;
     }
+    if (keep2d) launch_fill_u32((uint32_t*)grad2d, 0u, (int64_t)kGradStride * g.n, s);
     const int bases = (g.sh_degree + 1) * (g.sh_degree + 1);
     const unsigned chunks = (unsigned)pb_chunks(g.n);
     preprocess_backward_classify_kernel<<<chunks, 256, 0, s>>>(g.n, n_touched, rec_count, first_slot,
@@ -596,17 +603,17 @@ void launch_preprocess_backward(const GaussianView& g, const CamParams& cam, con
     if (pose_out) {
         if (f16)
             launch_live<__half, true>(g, bases, cam, conic_opacity, rec_count, records, grad2d, out, densif, mode, live,
-                                      chunk_counts, pose_partial, chunks, s);
+                                      chunk_counts, pose_partial, keep2d, chunks, s);
         else
             launch_live<float, true>(g, bases, cam, conic_opacity, rec_count, records, grad2d, out, densif, mode, live,
-                                     chunk_counts, pose_partial, chunks, s);
+                                     chunk_counts, pose_partial, keep2d, chunks, s);
         pose_reduce_kernel<<<1, 256, 0, s>>>(pose_partial, (int64_t)chunks, pose_out);
     } else if (f16) {
         launch_live<__half, false>(g, bases, cam, conic_opacity, rec_count, records, grad2d, out, densif, mode, live,
-                                   chunk_counts, nullptr, chunks, s);
+                                   chunk_counts, nullptr, keep2d, chunks, s);
     } else {
         launch_live<float, false>(g, bases, cam, conic_opacity, rec_count, records, grad2d, out, densif, mode, live,
-                                  chunk_counts, nullptr, chunks, s);
+                                  chunk_counts, nullptr, keep2d, chunks, s);
     }
 }
 

@@ -286,6 +286,35 @@ void launch_gather_rows16(const void* src, void* dst, const int32_t* rows, int64
                                                                         n_dst, width);
 }
 
+// dst row rows[k] = 0 (k < n_rows) of an array of `words` 4-byte words per
+// row (simple_adam.cu:944-979): one thread per word; repeated rows are fine.
+__global__ void zero_rows_kernel(uint32_t* __restrict__ dst, const int32_t* __restrict__ rows, int64_t n_rows,
+                                 int words) {
+    const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (e >= n_rows * words) return;
+    const int64_t k = e / words, w = e - k * words;
+    dst[(int64_t)rows[k] * words + w] = 0u;
+}
+
+void launch_zero_rows(void* dst, const int32_t* rows, int64_t n_rows, int words, hipStream_t s) {
+    if (n_rows <= 0) return;
+    const int64_t total = n_rows * words;
+    zero_rows_kernel<<<(unsigned)((total + 255) / 256), 256, 0, s>>>((uint32_t*)dst, rows, n_rows, words);
+}
+
+// bad[0] |= 1 when some index is negative or >= bound
+__global__ void check_indices_kernel(const int32_t* __restrict__ idx, int64_t n, int64_t bound,
+                                     uint32_t* __restrict__ bad) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    bool b = i < n && (idx[i] < 0 || (int64_t)idx[i] >= bound);
+    if (__any(b) && lane_id() == 0) atomicOr(bad, 1u);
+}
+
+void launch_check_indices(const int32_t* idx, int64_t n, int64_t bound, uint32_t* bad, hipStream_t s) {
+    if (n <= 0) return;
+    check_indices_kernel<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(idx, n, bound, bad);
+}
+
 // default.cu:26-37: opacity = logit(min(logistic(opacity), max_opacity))
 __global__ void reset_opacity_kernel(float* __restrict__ opac, int64_t n, float max_opacity) {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;

@@ -89,6 +89,19 @@ class SimpleAdam(OptimizerBase):
         _lib.check(_lib.load().tgs_adam_append(self._h, int(num_duplicate), stream_ptr(stream)),
                    "SimpleAdam::duplicate")
 
+    def reset_indices(self, indices, num_reset: int | None = None, stream=None):
+        """SimpleAdam::reset(int* indices, int num_reset) (simple_adam.cu:
+        944-979): zero both moments of the given rows (device int32 tensor)."""
+        n = int(indices.numel() if num_reset is None else num_reset)
+        _lib.check(_lib.load().tgs_adam_reset_rows(self._h, C.c_void_p(indices.data_ptr()), n, stream_ptr(stream)),
+                   "SimpleAdam::reset")
+
+    def reorder(self, indices, stream=None):
+        """SimpleAdam::reorder(uint* indices) (simple_adam.cu:1037-1097):
+        new row i = old row indices[i] (device int32/uint32 tensor, one per row)."""
+        _lib.check(_lib.load().tgs_adam_reorder(self._h, C.c_void_p(indices.data_ptr()), stream_ptr(stream)),
+                   "SimpleAdam::reorder")
+
     def reset_opacity(self, stream=None):
         """SimpleAdam::reset_opacity (simple_adam.cu:981-985)."""
         _lib.check(_lib.load().tgs_adam_reset_opacity(self._h, stream_ptr(stream)), "SimpleAdam::reset_opacity")

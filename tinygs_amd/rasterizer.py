@@ -57,7 +57,10 @@ class FastGSRasterizer(RasterizerBase):
         self._cg = gaussians.to_c()
         _lib.check(_lib.load().tgs_rasterizer_set_gaussians(self._h, C.byref(self._cg)), "set_gaussians")
 
-    def forward(self, ctx: RasterizeContext):
+    def forward(self, ctx: RasterizeContext, no_sync: bool = False):
+        """no_sync=True: the forward does not wait for the instance count and
+        uses the capacity of reserve() instead (TGS_FORWARD_NO_SYNC), so it can
+        be queued ahead or captured into a HIP graph; check status() later."""
         if self.m_gaussians is None:
             raise RuntimeError("Gaussians not set")
         # the pointers may have changed (e.g. tensors replaced); rebind
@@ -68,10 +71,27 @@ class FastGSRasterizer(RasterizerBase):
         if img.data_type != DataType.Float32:
             raise RuntimeError("FastGSRasterizer: only float32 images are supported")
         cam = ctx.fwd_input.to_c()
-        _lib.check(L.tgs_rasterizer_forward(self._h, C.byref(cam), ptr(img.data), _lib.TGS_DTYPE_FLOAT32,
-                                            ptr(ctx.densification_info), stream_ptr(ctx.stream)), "forward")
+        _lib.check(L.tgs_rasterizer_forward_ex(self._h, C.byref(cam), ptr(img.data), _lib.TGS_DTYPE_FLOAT32,
+                                               ptr(ctx.densification_info),
+                                               _lib.TGS_FORWARD_NO_SYNC if no_sync else 0,
+                                               stream_ptr(ctx.stream)), "forward")
 
-    def backward(self, ctx: RasterizeContext, assign: bool = False, sparse: bool = False):
+    def reserve(self, max_instances: int, grid_tiles: int, stream=None):
+        """Instance capacity of no-sync forwards (tgs_rasterizer_reserve)."""
+        _lib.check(_lib.load().tgs_rasterizer_reserve(self._h, int(max_instances), int(grid_tiles),
+                                                      stream_ptr(stream)), "reserve")
+
+    def status(self, clear_capacity_flag: bool = False, stream=None) -> int:
+        """Waits for the queued work and returns the device state of the
+        forwards so far: 0, or _lib.TGS_ERR_CAPACITY when a no-sync forward
+        needed more instances than reserved. Other failures raise."""
+        rc = _lib.load().tgs_rasterizer_status(self._h, 1 if clear_capacity_flag else 0, stream_ptr(stream))
+        if rc == _lib.TGS_ERR_CAPACITY:
+            return rc
+        _lib.check(rc, "status")
+        return 0
+
+    def backward(self, ctx: RasterizeContext, assign: bool = False, sparse: bool = False, keep_2d: bool = False):
         """Accumulates into ctx.gaussians_grad (reference contract). assign=True
         writes the gradients instead (zero for culled Gaussians): the caller's
         zeroing fused into the backward. sparse=True writes only the rows that
@@ -85,7 +105,7 @@ class FastGSRasterizer(RasterizerBase):
         L = _lib.load()
         pose = bool(self.m_params["enable_pose_opt"])
         flags = (_lib.TGS_BACKWARD_ASSIGN if assign else 0) | (_lib.TGS_BACKWARD_SPARSE if sparse else 0) | \
-            (_lib.TGS_BACKWARD_POSE if pose else 0)
+            (_lib.TGS_BACKWARD_POSE if pose else 0) | (_lib.TGS_BACKWARD_KEEP_2D if keep_2d else 0)
         _lib.check(L.tgs_rasterizer_backward_ex(self._h, ptr(ctx.grad_output.image.data),
                                                 ptr(ctx.fwd_output.image.data), C.byref(g),
                                                 ptr(ctx.densification_info), flags,
@@ -145,6 +165,24 @@ class FastGSRasterizer(RasterizerBase):
         }
         del cs
         return out
+
+    def debug_grad2d(self) -> dict:
+        """The summed 2D gradients of the last backward run with keep_2d=True,
+        in the oracle's layout (tests only)."""
+        import torch
+        dv = _lib.tgs_debug_view()
+        _lib.check(_lib.load().tgs_rasterizer_debug_view(self._h, C.byref(dv)), "debug_view")
+        if not dv.grad2d:
+            raise RuntimeError("no backward with keep_2d since the last forward")
+        n = self.m_gaussians.size()
+        t = torch.empty(12 * n, dtype=torch.float32, device=self.m_gaussians.means().device)
+        _lib.copy_device(dv.grad2d, t.numel() * 4, t)
+        g = t.cpu().numpy().reshape(n, 12)
+        return {"grad_mean2d": np.ascontiguousarray(g[:, 0:2]).reshape(-1),
+                "absgrad": np.ascontiguousarray(g[:, 2:4]).reshape(-1),
+                "grad_conic": np.ascontiguousarray(g[:, 4:7]).reshape(-1),
+                "grad_color": np.ascontiguousarray(g[:, 7:10]).reshape(-1),
+                "alpha_sum": np.ascontiguousarray(g[:, 10])}
 
     def debug_n_contrib(self, shape) -> "object":
         import torch

@@ -15,7 +15,10 @@ rows that received a gradient and hands Adam the row mask, so zero rows are
 neither written nor read.
 
 Everything runs on one HIP stream; the only host synchronisation is the one
-inside the forward that sizes the instance buffers.
+inside the forward that sizes the instance buffers. With no_sync=True the
+first forward reserves an instance capacity (1.25 x its count) and the later
+ones do not wait at all (TGS_FORWARD_NO_SYNC); check_status() reports a
+forward that outgrew the capacity.
 """
 from __future__ import annotations
 
@@ -28,9 +31,13 @@ from .rasterizer import create_rasterizer
 class TrainStep:
     def __init__(self, scene, l1_weight: float = 0.8, ssim_weight: float = 0.2, grad_scaler: float = 1.0,
                  eps: float = 1e-15, shs_lr: float | None = None, means_lr: float | None = None,
-                 max_grad_1: float | None = None, device: str = "cuda", stream=None, sparse_grads: bool = True):
+                 max_grad_1: float | None = None, device: str = "cuda", stream=None, sparse_grads: bool = True,
+                 no_sync: bool = False):
         import torch
         self.scene = scene
+        self.no_sync = bool(no_sync)
+        self._capacity = None   # (instances, tiles) reserved for the no-sync forwards
+        self._reserved = False
         # sparse_grads: the backward writes only gradient rows that received a
         # gradient and Adam reads only those (the others are zero); same
         # parameters as assigning every row, without moving the zero rows
@@ -88,7 +95,23 @@ class TrainStep:
             self.grad_img.data.zero_()
 
     def forward(self):
+        if self.no_sync and self._capacity:
+            if not self._reserved:   # before the forward: growing drops the previous forward's state
+                self.rasterizer.reserve(*self._capacity, self.stream)
+                self._reserved = True
+            self.rasterizer.forward(self.ctx, no_sync=True)
+            return
         self.rasterizer.forward(self.ctx)
+        if self.no_sync:
+            _, inst, tiles = self.rasterizer.counts()
+            self._capacity = (inst + inst // 4 + 4096, tiles)
+
+    def check_status(self):
+        """Waits for the queued steps; raises when a no-sync forward needed
+        more instances than reserved (its image and gradients are then partial)."""
+        from . import _lib
+        if self.rasterizer.status(clear_capacity_flag=True, stream=self.stream) == _lib.TGS_ERR_CAPACITY:
+            raise RuntimeError("a no-sync forward outgrew its instance capacity")
 
     def losses_and_grad(self):
         if self.fused_losses:
@@ -98,11 +121,11 @@ class TrainStep:
         for loss, w in self.losses:
             loss.evaluate(self.loss_ctx, w * self.grad_scaler)
 
-    def backward(self):
+    def backward(self, keep_2d: bool = False):
         if self.sparse_grads:
-            self.rasterizer.backward(self.ctx, sparse=True)
+            self.rasterizer.backward(self.ctx, sparse=True, keep_2d=keep_2d)
         else:
-            self.rasterizer.backward(self.ctx, assign=True)
+            self.rasterizer.backward(self.ctx, assign=True, keep_2d=keep_2d)
 
     def optimize(self):
         mask = self.rasterizer.grad_row_mask() if self.sparse_grads else None
