@@ -14,7 +14,7 @@ Bars (config-3 column of the baseline plan):
   (a) the blend backward's summed 2D gradients (the sums whose order follows
   atomic order) at the gradient bar of tests/helpers.py, and (b) the 3D
   gradient chain of the preprocess backward given the GPU's own 2D gradients,
-  bit-exact; then (c) end to end, where the chain amplifies (a)'s rounding by
+  exact; then (c) end to end, where the chain amplifies (a)'s rounding by
   a Gaussian's anisotropy (rotations of needle-shaped Gaussians: bar 1e-3);
 * SimpleAdam bit-exact given the GPU's gradients.
 The oracle runs on all host cores (its results do not depend on the count).
@@ -124,10 +124,14 @@ def _run(scene, orc, sparse):
     # (b) the gradient chain (preprocess backward) on the GPU's own 2D gradients
     g2d_gpu["absgrad"] = np.zeros_like(g2d_gpu["absgrad"])
     chain = orc.preprocess_backward(scene, pre, g2d_gpu, "f")
-    # the kernel and the oracle evaluate the same chain in the same operation order
+    # the kernel and the oracle evaluate the same chain in the same operation
+    # order: equal values (a row that no bucket reached keeps the sparse
+    # backward's +0 where the oracle's chain of zeros may give -0)
     for k in grads:
-        assert np.array_equal(grads[k].view(np.uint32), chain[k].astype(np.float32).view(np.uint32)), k
-    print("[fullsize] gradient chain on the GPU's 2D gradients: bit-exact", flush=True)
+        c = chain[k].astype(np.float32)
+        bad = grads[k] != c
+        assert not bad.any(), (k, int(bad.sum()), grads[k][bad][:5], c[bad][:5])
+    print("[fullsize] gradient chain on the GPU's 2D gradients: equal values", flush=True)
     # (c) end to end
     ref = orc.preprocess_backward(scene, pre, g2d, "f")
     print("[fullsize] end to end:", flush=True)
