@@ -320,6 +320,15 @@ int tgs_gaussians_reorder(const tgs_gaussians* g, const uint32_t* indices, void*
  * (device, capacity n) receives the i < n with flags[i] != 0 in order, *count their number.
  * Synchronises. */
 int tgs_flags_compact(const uint8_t* flags, int64_t n, int32_t* out, int64_t* count, void* stream);
+/* tgs_flags_compact without any allocation. No counterpart in the reference:
+ * for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc). Same
+ * arguments and results as tgs_flags_compact; n at most 2^26 (larger n is
+ * refused with TGS_ERR_INVALID before anything runs). Its counts live in a
+ * 384 KiB static device array that each GPU holds until the process ends and
+ * that every call on that GPU shares: calls that overlap on one GPU race.
+ * Synchronises the stream. */
+int tgs_flags_compact_noalloc(const uint8_t* flags, int64_t n, int32_t* out, int64_t* count, void* stream);
 /* reset_opacity (default.cu:26-37): opacity = logit(min(sigmoid(opacity), max_opacity)). */
 int tgs_reset_opacity(const tgs_gaussians* g, float max_opacity, void* stream);
 

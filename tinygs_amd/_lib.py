@@ -122,6 +122,7 @@ SIGNATURES = {
                           C.POINTER(C.c_int64), P], C.c_int),
     "tgs_gaussians_gather": ([C.POINTER(tgs_gaussians), C.POINTER(tgs_gaussians), P, P], C.c_int),
     "tgs_flags_compact": ([P, C.c_int64, P, C.POINTER(C.c_int64), P], C.c_int),
+    "tgs_flags_compact_noalloc": ([P, C.c_int64, P, C.POINTER(C.c_int64), P], C.c_int),
     "tgs_reset_opacity": ([C.POINTER(tgs_gaussians), C.c_float, P], C.c_int),
     "tgs_ply_save": ([C.c_char_p, C.POINTER(tgs_gaussians), C.c_int32, P], C.c_int),
     "tgs_ply_read_info": ([C.c_char_p, C.POINTER(tgs_ply_info)], C.c_int),

@@ -16,6 +16,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -1276,6 +1277,70 @@ int tgs_reset_opacity(const tgs_gaussians* g, float max_opacity, void* stream) {
     TGS_TRY(check_gaussians(g, false));
     launch_reset_opacity((float*)g->opacities, g->n, max_opacity, (hipStream_t)stream);
     TGS_CHECK_LAUNCH();
+    return TGS_OK;
+}
+
+}  // extern "C"
+
+// ------------------------------------------------------------------ index lists without allocation
+//
+// tgs_flags_compact_noalloc keeps its per-chunk counts, offsets and totals in
+// this file-scope array instead of hipMalloc'd buffers. Every GPU the library
+// runs on holds one copy (384 KiB) until the process ends. Its address on a
+// device comes from hipGetSymbolAddress, taken once per device on the first
+// call there; the array's name itself is only a host-side stand-in. Calls on
+// one GPU share the array (each fully writes what it reads before reading
+// it), so calls that overlap on one GPU race.
+constexpr int64_t kNoAllocMaxFlags = 1ll << 26;
+constexpr int64_t kNoAllocChunks = kNoAllocMaxFlags / kListChunkElems;
+constexpr int kNoAllocWords = (int)(3 * kNoAllocChunks + 64);   // counts (uint2), offsets, totals
+static __device__ __align__(256) uint32_t scratch[kNoAllocWords];
+
+constexpr int kMaxDevices = 64;
+static std::mutex g_scratch_mu;
+static uint32_t* g_scratch_ptr[kMaxDevices];
+
+// The current device's copy of `scratch`, looked up on the first call there.
+static int scratch_on_current_device(uint32_t** out) {
+    int dev = -1;
+    TGS_HIP(hipGetDevice(&dev));
+    if (dev < 0 || dev >= kMaxDevices) return fail(TGS_ERR_UNSUPPORTED, "device %d beyond %d devices", dev, kMaxDevices);
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void* p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p)
+            return fail(TGS_ERR_HIP, "hipGetSymbolAddress(scratch) on device %d: %s", dev, hipGetErrorString(e));
+        g_scratch_ptr[dev] = (uint32_t*)p;
+    }
+    *out = g_scratch_ptr[dev];
+    return TGS_OK;
+}
+
+extern "C" {
+
+int tgs_flags_compact_noalloc(const uint8_t* flags, int64_t n, int32_t* out, int64_t* count, void* stream) {
+    if (!count || n < 0 || (n > 0 && (!flags || !out))) return fail(TGS_ERR_INVALID, "bad argument");
+    if (n > kNoAllocMaxFlags)
+        return fail(TGS_ERR_INVALID, "tgs_flags_compact_noalloc: %lld flags, at most %lld", (long long)n,
+                    (long long)kNoAllocMaxFlags);
+    *count = 0;
+    if (n == 0) return TGS_OK;
+    hipStream_t s = (hipStream_t)stream;
+    uint32_t* base = nullptr;
+    TGS_TRY(scratch_on_current_device(&base));
+    const int64_t chunks = list_chunks(n);
+    uint2* counts = (uint2*)base;
+    uint32_t* offsets = base + 2 * kNoAllocChunks;
+    uint32_t* totals = offsets + kNoAllocChunks;
+    launch_flag_count(flags, n, counts, s);
+    launch_chunk_offsets(counts, chunks, offsets, totals, s);
+    launch_flag_compact(flags, n, offsets, out, s);
+    TGS_CHECK_LAUNCH();
+    uint32_t h[2] = {0, 0};
+    TGS_HIP(hipMemcpyAsync(h, totals, sizeof(h), hipMemcpyDeviceToHost, s));
+    TGS_HIP(hipStreamSynchronize(s));
+    *count = h[0];
     return TGS_OK;
 }
 

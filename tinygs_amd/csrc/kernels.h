@@ -161,6 +161,10 @@ void launch_sq_diff_sum(const float* pred, const float* target, int64_t n_padded
 void launch_random_logistic(uint64_t state, uint64_t inc, int64_t n, float mean, float stddev, float* out,
                             hipStream_t s);
 int64_t list_chunks(int64_t n);
+constexpr int64_t kListChunkElems = 2048;   // flags per chunk of the index-list kernels
+// offsets[c] = exclusive prefix over chunks of counts[c].x; totals[0] = sum
+// of .x, totals[1] = sum of .y (one workgroup; chunks of any count)
+void launch_chunk_offsets(const uint2* counts, int64_t chunks, uint32_t* offsets, uint32_t* totals, hipStream_t s);
 // counts[c] = (nonzero flags, flags == 1) of chunk c (list_chunks(n) chunks)
 void launch_flag_count(const uint8_t* flags, int64_t n, uint2* counts, hipStream_t s);
 // indices of the nonzero flags in index order, chunk c's run at offsets[c]

@@ -59,6 +59,7 @@ void launch_random_logistic(uint64_t state, uint64_t inc, int64_t n, float mean,
 
 constexpr int kListRounds = 8;
 constexpr int kListChunk = 256 * kListRounds;
+static_assert(kListChunk == kListChunkElems, "chunk size shared with the host");
 
 int64_t list_chunks(int64_t n) { return n > 0 ? (n + kListChunk - 1) / kListChunk : 0; }
 
@@ -105,6 +106,49 @@ __global__ void __launch_bounds__(256) flag_compact_kernel(const uint8_t* __rest
 #pragma unroll
     for (int r = 0; r < kListRounds; ++r)
         if (v[r]) out[o + ex[r]] = (int32_t)(base + (int64_t)r * 256);
+}
+
+// offsets[c] = exclusive prefix of counts[c].x over the chunks (c < chunks);
+// totals[0] = sum of .x, totals[1] = sum of .y. One 1024-thread workgroup:
+// thread t owns a run of consecutive chunks, a workgroup scan of the run
+// sums places it.
+__global__ void __launch_bounds__(1024) chunk_offsets_kernel(const uint2* __restrict__ counts, int64_t chunks,
+                                                             uint32_t* __restrict__ offsets,
+                                                             uint32_t* __restrict__ totals) {
+    __shared__ uint32_t s_a[16], s_b[16];
+    const uint32_t t = threadIdx.x, lane = t & 63u, w = t >> 6;
+    const int64_t per = (chunks + 1023) / 1024;
+    const int64_t c0 = (int64_t)t * per, c1 = min(c0 + per, chunks);
+    uint32_t a = 0, b = 0;
+    for (int64_t c = c0; c < c1; ++c) {
+        const uint2 v = counts[c];
+        a += v.x;
+        b += v.y;
+    }
+    const uint32_t incl = wave_inclusive_scan_u32(a);
+    const uint32_t wb = wave_sum_u32(b);
+    if (lane == 63u) s_a[w] = incl;
+    if (lane == 0u) s_b[w] = wb;
+    __syncthreads();
+    uint32_t off = 0, ta = 0, tb = 0;
+    for (uint32_t k = 0; k < 16u; ++k) {
+        off += k < w ? s_a[k] : 0u;
+        ta += s_a[k];
+        tb += s_b[k];
+    }
+    uint32_t e = off + incl - a;
+    for (int64_t c = c0; c < c1; ++c) {
+        offsets[c] = e;
+        e += counts[c].x;
+    }
+    if (t == 0) {
+        totals[0] = ta;
+        totals[1] = tb;
+    }
+}
+
+void launch_chunk_offsets(const uint2* counts, int64_t chunks, uint32_t* offsets, uint32_t* totals, hipStream_t s) {
+    chunk_offsets_kernel<<<1, 1024, 0, s>>>(counts, chunks, offsets, totals);
 }
 
 void launch_flag_count(const uint8_t* flags, int64_t n, uint2* counts, hipStream_t s) {
