@@ -404,6 +404,11 @@ int tgs_rasterizer_work_stats(tgs_rasterizer* r, int64_t* fwd_loaded, int64_t* b
 /* ---- self tests (device): deterministic exp/log over arrays, wave primitives. */
 int tgs_selftest_detmath(int32_t op, const float* in, float* out, int64_t n, void* stream);
 int tgs_selftest_wave(const uint32_t* in, uint32_t* out, void* stream);
+/* The fp16 rasterizer's canonical half operations on arrays of half bit
+ * patterns (ops 7, 8 take floats in a): 0 exp2, 1 the hardware v_exp_f16
+ * (measurement only), 2 fma(a, b, c), 3 a * b, 4 a + b, 5 a / b, 6 packed
+ * fma, 7 float -> half nearest, 8 float -> half toward -inf, 9 a - b. Tests only. */
+int tgs_selftest_half(int32_t op, const void* a, const void* b, const void* c, void* out, int64_t n, void* stream);
 
 #ifdef __cplusplus
 }

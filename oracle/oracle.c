@@ -29,6 +29,7 @@
 #include <string.h>
 
 #include "detmath.h"
+#include "halfmath.h"
 
 /* ---------------- float instance (the oracle) ---------------- */
 #define REAL float
@@ -80,6 +81,29 @@ void orc_expf_array(int64_t n, const float* x, float* y) { for (int64_t i = 0; i
 void orc_logf_array(int64_t n, const float* x, float* y) { for (int64_t i = 0; i < n; ++i) y[i] = orc_logf(x[i]); }
 void orc_half_bits_array(int64_t n, const float* x, uint16_t* y) { for (int64_t i = 0; i < n; ++i) y[i] = orc_float_to_half_bits(x[i]); }
 void orc_round_half_array(int64_t n, const float* x, float* y) { for (int64_t i = 0; i < n; ++i) y[i] = orc_round_half(x[i]); }
+/* The canonical half operations of oracle/halfmath.h on arrays of half bit
+ * patterns (ops 7, 8 read floats from a), numbered as tgs_selftest_half. */
+void orc_half_op_array(int op, int64_t n, const void* a, const uint16_t* b, const uint16_t* c, uint16_t* out) {
+    const uint16_t* ah = (const uint16_t*)a;
+    const float* af = (const float*)a;
+    for (int64_t i = 0; i < n; ++i) {
+        uint16_t r = 0;
+        switch (op) {
+            case 0: r = oh_exp2(ah[i]); break;
+            case 2: r = oh_fma(ah[i], b[i], c[i]); break;
+            case 3: r = oh_mul(ah[i], b[i]); break;
+            case 4: r = oh_add(ah[i], b[i]); break;
+            case 5: r = oh_div(ah[i], b[i]); break;
+            case 6: r = (i & 1) ? oh_fma(b[i], c[i], ah[i]) : oh_fma(ah[i], b[i], c[i]); break;
+            case 7: r = oh_rn(af[i]); break;
+            case 8: r = oh_rd(af[i]); break;
+            case 9: r = oh_sub(ah[i], b[i]); break;
+            default: break;
+        }
+        out[i] = r;
+    }
+}
+
 int orc_version(void) { return 1; }
 /* Threads of the parallel loops (the results do not depend on it). */
 void orc_set_threads(int n) { omp_set_num_threads(n > 0 ? n : 1); }

@@ -76,6 +76,8 @@ def _declare(L):
         fn = getattr(L, pfx + "adam")
         fn.argtypes = [C.c_int64, rp, rp, rp, rp, R, R, R, R, R, R, R, R, C.c_int, C.c_int, R, C.c_int]
         fn.restype = None
+    L.orc_half_op_array.argtypes = [C.c_int, C.c_int64, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p]
+    L.orc_half_op_array.restype = None
     L.orc_set_threads.argtypes = [C.c_int]
     L.orc_set_threads.restype = None
     L.orc_max_threads.argtypes = []
@@ -86,6 +88,18 @@ def _declare(L):
                        ("orc_half_bits_array", [C.c_int64, f32p, u16p])):
         getattr(L, name).argtypes = argt
         getattr(L, name).restype = None
+
+
+def half_op(op, a, b=None, c=None):
+    """The oracle's canonical half operation `op` (numbering of
+    tgs_selftest_half) on uint16 bit-pattern arrays (float32 `a` for ops 7, 8)."""
+    a = np.ascontiguousarray(a)
+    n = a.size
+    out = np.zeros(n, np.uint16)
+    b = None if b is None else np.ascontiguousarray(b, np.uint16)
+    c = None if c is None else np.ascontiguousarray(c, np.uint16)
+    lib().orc_half_op_array(int(op), n, a.ctypes.data_as(C.c_void_p), _ptr(b), _ptr(c), out.ctypes.data_as(C.c_void_p))
+    return out
 
 
 def set_threads(n: int):

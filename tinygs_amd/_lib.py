@@ -137,6 +137,7 @@ SIGNATURES = {
     "tgs_rasterizer_work_stats": ([P, C.POINTER(C.c_int64), C.POINTER(C.c_int64), C.c_int32], C.c_int),
     "tgs_selftest_detmath": ([C.c_int32, P, P, C.c_int64, P], C.c_int),
     "tgs_selftest_wave": ([P, P, P], C.c_int),
+    "tgs_selftest_half": ([C.c_int32, P, P, P, P, C.c_int64, P], C.c_int),
 }
 
 

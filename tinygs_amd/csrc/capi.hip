@@ -1405,6 +1405,16 @@ int tgs_selftest_detmath(int32_t op, const float* in, float* out, int64_t n, voi
     return TGS_OK;
 }
 
+int tgs_selftest_half(int32_t op, const void* a, const void* b, const void* c, void* out, int64_t n, void* stream) {
+    if (n < 0 || (n > 0 && (!a || !out))) return fail(TGS_ERR_INVALID, "bad argument");
+    if ((op == 2 || op == 6) && n > 0 && (!b || !c)) return fail(TGS_ERR_INVALID, "bad argument");
+    if ((op == 3 || op == 4 || op == 5 || op == 9) && n > 0 && !b) return fail(TGS_ERR_INVALID, "bad argument");
+    launch_halfmath(op, (const uint16_t*)a, (const uint16_t*)b, (const uint16_t*)c, (uint16_t*)out, n,
+                    (hipStream_t)stream);
+    TGS_CHECK_LAUNCH();
+    return TGS_OK;
+}
+
 int tgs_selftest_wave(const uint32_t* in, uint32_t* out, void* stream) {
     launch_wave_selftest(in, out, (hipStream_t)stream);
     TGS_CHECK_LAUNCH();

@@ -226,5 +226,8 @@ void launch_adam(const AdamArgs& a, hipStream_t s);
 // ---- self tests of wave primitives and deterministic math (debug entry points)
 void launch_detmath(int op, const float* in, float* out, int64_t n, hipStream_t s);
 void launch_wave_selftest(const uint32_t* in, uint32_t* out, hipStream_t s);
+// canonical half operation `op` (tests): out[i] = op(a[i], b[i], c[i]) as bits
+void launch_halfmath(int op, const uint16_t* a, const uint16_t* b, const uint16_t* c, uint16_t* out, int64_t n,
+                     hipStream_t s);
 
 }  // namespace tgs

@@ -63,3 +63,43 @@ void launch_wave_selftest(const uint32_t* in, uint32_t* out, hipStream_t s) {
 }
 
 }  // namespace tgs
+
+#include "halfmath.h"
+
+namespace tgs {
+
+// Canonical half operations on element i: a, b, c are half bit patterns
+// (op 7, 8: a holds floats), out receives the result's bits.
+__global__ void halfmath_kernel(int op, const uint16_t* a, const uint16_t* b, const uint16_t* c, uint16_t* out,
+                                int64_t n) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const h16 x = hfrom(a[i]);
+    h16 r = (h16)0;
+    switch (op) {
+        case 0: r = h_exp2(x); break;
+        case 1: r = __builtin_elementwise_exp2(x); break;   // v_exp_f16 (measured, not canonical)
+        case 2: r = h_fma(x, hfrom(b[i]), hfrom(c[i])); break;
+        case 3: r = x * hfrom(b[i]); break;
+        case 4: r = x + hfrom(b[i]); break;
+        case 5: r = h_div(x, hfrom(b[i])); break;
+        case 6: {   // packed: lanes (a, b) * (b, c) + (c, a)
+            const h16x2 p = h2_fma(h2(x, hfrom(b[i])), h2(hfrom(b[i]), hfrom(c[i])), h2(hfrom(c[i]), x));
+            r = (i & 1) ? p.y : p.x;
+            break;
+        }
+        case 7: r = h_rn(((const float*)a)[i]); break;
+        case 8: r = h_rd(((const float*)a)[i]); break;
+        case 9: r = x - hfrom(b[i]); break;
+        default: break;
+    }
+    out[i] = hbits(r);
+}
+
+void launch_halfmath(int op, const uint16_t* a, const uint16_t* b, const uint16_t* c, uint16_t* out, int64_t n,
+                     hipStream_t s) {
+    if (n <= 0) return;
+    halfmath_kernel<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(op, a, b, c, out, n);
+}
+
+}  // namespace tgs
