@@ -84,8 +84,12 @@ int tgs_rasterizer_create(const char* type, tgs_rasterizer** out);
 int tgs_rasterizer_destroy(tgs_rasterizer* r);
 /* FastGSRasterizer::set_gaussians (fastgs.cu:388-392). Pointers are kept, not copied. */
 int tgs_rasterizer_set_gaussians(tgs_rasterizer* r, const tgs_gaussians* g);
-/* FastGSRasterizer::forward (fastgs.cu:89-236). image: fp32 [3 * channel_stride].
- * densification_info: optional device float4[n] (max_radii_screen updated). */
+/* FastGSRasterizer::forward (fastgs.cu:89-236). image: [3 * channel_stride]
+ * of image_dtype: TGS_DTYPE_FLOAT32, or TGS_DTYPE_FLOAT16 for the fp16-image
+ * rasterizer (fastgs.cu:143-188, fastgs_ours_fp16/: half conic and opacity,
+ * 8-bit colour, 255-scaled blending; the backward then takes a half gradient
+ * image and half image). densification_info: optional device float4[n]
+ * (max_radii_screen updated). */
 int tgs_rasterizer_forward(tgs_rasterizer* r, const tgs_camera* cam, void* image, int32_t image_dtype,
                            void* densification_info, void* stream);
 /* FastGSRasterizer::forward with flags. TGS_FORWARD_NO_SYNC: the forward
@@ -172,14 +176,23 @@ typedef struct tgs_debug_view {
     const uint32_t* instance_tiles;     /* [n_instances] sorted */
     const uint32_t* instance_prims;     /* [n_instances] */
     const uint32_t* tile_ranges;        /* [2 * n_tiles] */
-    const uint32_t* n_contrib;          /* [channel_stride] */
+    const uint32_t* n_contrib;          /* [channel_stride] (fp16 images: uint16_t) */
     const uint32_t* tile_max;           /* [n_tiles] */
     const float* grad2d;                /* [12n] after a TGS_BACKWARD_KEEP_2D backward, else NULL */
     int64_t n_visible;
     int64_t n_instances;
     int64_t n_tiles;
     uint32_t depth_key_base;            /* bits of the near plane (0 when near <= 0) */
-    uint32_t reserved;
+    uint32_t image_dtype;               /* of the last forward. TGS_DTYPE_FLOAT16 (FGS16): the
+                                           records' second half is conic a | b << 16, c | opacity
+                                           << 16 (halves), 0, ln(255 opacity); conic_opacity the
+                                           halves as floats; color the words a | b << 16,
+                                           c | opacity << 16, r | g << 8 | b << 16 (bytes), 0 */
+    const uint32_t* first_slot;         /* [n] first 2D-gradient record slot of each visible primitive */
+    const float* records;               /* [12 * n_instances] 2D-gradient records of the last backward:
+                                           per primitive, the buckets that reached it fill the slots
+                                           first_slot[p], first_slot[p] + 1, ... in completion order
+                                           (FGS16: [11] holds the instance index's bits) */
 } tgs_debug_view;
 int tgs_rasterizer_debug_view(tgs_rasterizer* r, tgs_debug_view* out);
 
@@ -405,10 +418,18 @@ int tgs_rasterizer_work_stats(tgs_rasterizer* r, int64_t* fwd_loaded, int64_t* b
 int tgs_selftest_detmath(int32_t op, const float* in, float* out, int64_t n, void* stream);
 int tgs_selftest_wave(const uint32_t* in, uint32_t* out, void* stream);
 /* The fp16 rasterizer's canonical half operations on arrays of half bit
- * patterns (ops 7, 8 take floats in a): 0 exp2, 1 the hardware v_exp_f16
- * (measurement only), 2 fma(a, b, c), 3 a * b, 4 a + b, 5 a / b, 6 packed
- * fma, 7 float -> half nearest, 8 float -> half toward -inf, 9 a - b. Tests only. */
+ * patterns (ops 7, 8 take floats in a, op 11 int64): 0 exp2, 1 the hardware
+ * v_exp_f16 (measurement only), 2 fma(a, b, c), 3 a * b, 4 a + b, 5 a / b,
+ * 6 packed fma, 7 float -> half nearest, 8 float -> half toward -inf,
+ * 9 a - b, 10 minNum(a, b), 11 the nearest half of a * 2^-24, 12 the lane
+ * shift the fp16 blend backward uses (out[i] = a[i - 1] within each 64-lane
+ * wave, b[i] at lane 0; n a multiple of 64). Tests only. */
 int tgs_selftest_half(int32_t op, const void* a, const void* b, const void* c, void* out, int64_t n, void* stream);
+/* The half division of the fp16 rasterizer over every finite operand pair
+ * with a nonzero divisor, checked on the device against the correctly
+ * rounded quotient. out: device int64[8]: [0] mismatches, [1] pairs checked,
+ * [2..4] a, b, quotient bits of one mismatch. Tests only. */
+int tgs_selftest_half_div_exhaustive(int64_t* out, void* stream);
 
 #ifdef __cplusplus
 }

@@ -11,7 +11,10 @@
  *             (Knuth, TAOCP vol. 2, 4.2.2), and the final rounding to half
  *             takes the error's sign into account at halfway points
  *   oh_exp2   correctly rounded 2^x: double exp2 of the half, rounded to half
- *   oh_min    b < a ? b : a;  oh_relu x > 0 ? x : +0;  oh_sat clamp to [0,1] (NaN -> 0)
+ *   oh_min    IEEE minNum (a NaN operand yields the other);  oh_relu x > 0 ? x : +0;
+ *             oh_sat clamp to [0,1] (NaN -> 0)
+ *   oh_from_fixed  the correctly rounded half of S * 2^-24, S an integer (an
+ *             exact sum of half values: every finite half is a multiple of 2^-24)
  */
 #pragma once
 
@@ -98,9 +101,37 @@ static inline oh16 oh_exp2(oh16 x) {
 }
 
 static inline int oh_lt(oh16 a, oh16 b) { return oh_f(a) < oh_f(b); }
-static inline oh16 oh_min(oh16 a, oh16 b) { return oh_lt(b, a) ? b : a; }
+static inline int oh_isnan(oh16 a) { return (a & 0x7fffu) > 0x7c00u; }
+/* IEEE minNum: a NaN operand yields the other one (the blend never compares
+ * two zeros, so the order of -0 and +0 is not needed) */
+static inline oh16 oh_min(oh16 a, oh16 b) {
+    if (oh_isnan(a)) return b;
+    if (oh_isnan(b)) return a;
+    return oh_lt(b, a) ? b : a;
+}
 static inline oh16 oh_relu(oh16 x) { return oh_f(x) > 0.0f ? x : (oh16)0u; }
 static inline oh16 oh_sat(oh16 x) {
     const float f = oh_f(x);
     return f > 0.0f ? (f < 1.0f ? x : (oh16)0x3c00u) : (oh16)0u;
+}
+
+/* Correctly rounded (to nearest even) half of S * 2^-24, by integer shifts:
+ * the same steps as the kernels' half_of_fixed. */
+static inline oh16 oh_from_fixed(int64_t S) {
+    if (S == 0) return 0u;
+    const uint16_t sign = S < 0 ? 0x8000u : 0u;
+    const uint64_t a = S < 0 ? (uint64_t)0 - (uint64_t)S : (uint64_t)S;
+    if (a >= ((uint64_t)65520u << 24)) return (oh16)(sign | 0x7c00u);   /* rounds to infinity */
+    int msb = 63;
+    while (!((a >> msb) & 1u)) --msb;
+    uint64_t q = a;
+    int shift = 0;
+    if (msb > 10) {
+        shift = msb - 10;
+        q = a >> shift;
+        const uint64_t rem = a - (q << shift), half = (uint64_t)1 << (shift - 1);
+        if (rem > half || (rem == half && (q & 1u))) ++q;
+    }
+    const float v = ldexpf((float)q, shift - 24);   /* exact: q < 2^12 */
+    return (oh16)(sign | oh_rn(v));
 }

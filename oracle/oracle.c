@@ -76,6 +76,9 @@
 #define R_HALF_ROUND(x) (x)
 #include "oracle_impl.inc"
 
+/* ---------------- the fp16-image rasterizer (FGS16), half arithmetic ---------------- */
+#include "fgs16_impl.inc"
+
 /* ---------------- exported helpers ---------------- */
 void orc_expf_array(int64_t n, const float* x, float* y) { for (int64_t i = 0; i < n; ++i) y[i] = orc_expf(x[i]); }
 void orc_logf_array(int64_t n, const float* x, float* y) { for (int64_t i = 0; i < n; ++i) y[i] = orc_logf(x[i]); }
@@ -98,6 +101,9 @@ void orc_half_op_array(int op, int64_t n, const void* a, const uint16_t* b, cons
             case 7: r = oh_rn(af[i]); break;
             case 8: r = oh_rd(af[i]); break;
             case 9: r = oh_sub(ah[i], b[i]); break;
+            case 10: r = oh_min(ah[i], b[i]); break;
+            case 11: r = oh_from_fixed(((const int64_t*)a)[i]); break;
+            case 12: r = (i & 63) ? ah[i - 1] : b[i]; break;   /* wave_shr:1 of 64-lane waves */
             default: break;
         }
         out[i] = r;

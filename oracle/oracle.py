@@ -92,7 +92,8 @@ def _declare(L):
 
 def half_op(op, a, b=None, c=None):
     """The oracle's canonical half operation `op` (numbering of
-    tgs_selftest_half) on uint16 bit-pattern arrays (float32 `a` for ops 7, 8)."""
+    tgs_selftest_half) on uint16 bit-pattern arrays (float32 `a` for ops 7, 8,
+    int64 for op 11)."""
     a = np.ascontiguousarray(a)
     n = a.size
     out = np.zeros(n, np.uint16)
@@ -360,3 +361,120 @@ def run_iteration(scene, l1_w=0.8, ssim_w=0.2, grad_scaler=1.0, lr=None, step=1,
                   sh_half=getattr(scene, "sh_dtype", "float32") == "float16")
         out["theta"], out["m1"], out["m2"] = theta, m1, m2
     return out
+
+
+# ---------------------------------------------------------------- FGS16 (fp16 images)
+
+u8p = np.ctypeslib.ndpointer(dtype=np.uint8, flags="C_CONTIGUOUS")
+
+
+def _declare_h(L):
+    if getattr(L, "_h_declared", False):
+        return
+    L.orc_h_preprocess.argtypes = [C.c_int64, f32p, f32p, f32p, f32p, f32p, f32p, C.c_int, f32p, C.c_uint32,
+                                   C.c_uint32, u32p, u16p, f32p, u16p, u16p, u8p, f32p, f32p, C.c_void_p]
+    L.orc_h_preprocess.restype = None
+    L.orc_h_bin.argtypes = [C.c_int64, u32p, u16p, f32p, u16p, f32p, f32p, C.c_uint32, C.c_uint32, u32p,
+                            C.POINTER(C.c_int64), u32p, u32p, C.c_int64, u32p]
+    L.orc_h_bin.restype = C.c_int64
+    L.orc_h_blend_forward.argtypes = [C.c_int, C.c_int, u32p, u32p, f32p, u16p, u16p, u8p, u16p, u16p, u16p, u32p,
+                                      C.c_void_p]
+    L.orc_h_blend_forward.restype = None
+    L.orc_h_blend_backward.argtypes = [C.c_int, C.c_int, u32p, u32p, f32p, u16p, u16p, u8p, u16p, u16p, u16p, u32p,
+                                       u16p, f32p, u8p]
+    L.orc_h_blend_backward.restype = None
+    L.orc_h_reduce_records.argtypes = [C.c_int64, C.c_int64, u32p, f32p, u8p, f32p, f32p, f32p, f32p, f32p]
+    L.orc_h_reduce_records.restype = None
+    L._h_declared = True
+
+
+def h_preprocess(scene, max_radii=None):
+    """FGS16 preprocess (float inputs; SH in float)."""
+    L = lib()
+    _declare_h(L)
+    prm = params(scene, "f")
+    cam = cam_array(scene.camera, "f")
+    n = scene.n
+    gw, gh = scene.camera.grid
+    out = {"n_touched": np.zeros(n, np.uint32), "bounds": np.zeros(4 * n, np.uint16),
+           "mean2d": np.zeros(2 * n, np.float32), "conic": np.zeros(3 * n, np.uint16),
+           "opacity": np.zeros(n, np.uint16), "rgb": np.zeros(3 * n, np.uint8),
+           "power_thr": np.zeros(n, np.float32), "depth": np.zeros(n, np.float32)}
+    L.orc_h_preprocess(n, prm["means"], prm["scales"], prm["rotations"], prm["opacities"], prm["sh0"],
+                       prm["sh_rest"], (scene.sh_degree + 1) ** 2, cam, gw, gh, out["n_touched"], out["bounds"],
+                       out["mean2d"], out["conic"], out["opacity"], out["rgb"], out["power_thr"], out["depth"],
+                       _ptr(max_radii))
+    return out
+
+
+def h_bin(scene, pre):
+    L = lib()
+    _declare_h(L)
+    gw, gh = scene.camera.grid
+    n = scene.n
+    cap = int(pre["n_touched"].astype(np.int64).sum())
+    out = {"sorted_prims": np.zeros(max(n, 1), np.uint32), "inst_tile": np.zeros(max(cap, 1), np.uint32),
+           "inst_prim": np.zeros(max(cap, 1), np.uint32), "ranges": np.zeros(2 * gw * gh, np.uint32)}
+    nv = C.c_int64(0)
+    I = L.orc_h_bin(n, pre["n_touched"], pre["bounds"], pre["mean2d"], pre["conic"], pre["power_thr"], pre["depth"],
+                    gw, gh, out["sorted_prims"], C.byref(nv), out["inst_tile"], out["inst_prim"], cap, out["ranges"])
+    assert I == cap, (I, cap)
+    out["n_visible"] = nv.value
+    out["n_instances"] = int(I)
+    out["sorted_prims"] = out["sorted_prims"][: nv.value]
+    out["inst_tile"] = out["inst_tile"][:I]
+    out["inst_prim"] = out["inst_prim"][:I]
+    return out
+
+
+def h_blend_forward(scene, pre, bins):
+    L = lib()
+    _declare_h(L)
+    cam = scene.camera
+    gw, gh = cam.grid
+    shape = cam.shape
+    offs = np.zeros(gw * gh, np.uint32)
+    nb = L.orc_f_bucket_offsets(gw, gh, bins["ranges"], offs)
+    image = np.zeros(shape.padded_size, np.uint16)
+    ncontrib = np.zeros(shape.channel_stride, np.uint16)
+    tmax = np.zeros(gw * gh, np.uint16)
+    ckpt = np.zeros(max(nb, 1) * 256 * 4, np.uint16)
+    L.orc_h_blend_forward(cam.width, cam.height, bins["ranges"], _u32(bins["inst_prim"]), pre["mean2d"],
+                          pre["conic"], pre["opacity"], pre["rgb"], image, ncontrib, tmax, offs,
+                          ckpt.ctypes.data_as(C.c_void_p))
+    return {"image": image, "n_contrib": ncontrib, "tile_max": tmax, "bucket_offsets": offs, "ckpt": ckpt,
+            "n_buckets": int(nb)}
+
+
+def h_render(scene):
+    pre = h_preprocess(scene)
+    bins = h_bin(scene, pre)
+    return pre, bins, h_blend_forward(scene, pre, bins)
+
+
+def h_blend_backward(scene, pre, bins, fwd, grad_image_h):
+    """Per-instance records (12 floats; see orc_h_blend_backward) and their
+    per-primitive reduction in the fp32 path's 2D-gradient layout."""
+    L = lib()
+    _declare_h(L)
+    cam = scene.camera
+    I = bins["n_instances"]
+    rec = np.zeros(12 * max(I, 1), np.float32)
+    has = np.zeros(max(I, 1), np.uint8)
+    L.orc_h_blend_backward(cam.width, cam.height, bins["ranges"], _u32(bins["inst_prim"]), pre["mean2d"],
+                           pre["conic"], pre["opacity"], pre["rgb"], fwd["image"],
+                           np.ascontiguousarray(grad_image_h, np.uint16), fwd["tile_max"], fwd["bucket_offsets"],
+                           fwd["ckpt"], rec, has)
+    n = scene.n
+    g = {k: np.zeros(m * n, np.float32) for k, m in
+         (("grad_mean2d", 2), ("absgrad", 2), ("grad_conic", 3), ("grad_color", 3), ("grad_opacity", 1))}
+    L.orc_h_reduce_records(n, I, _u32(bins["inst_prim"]), rec, has, g["grad_mean2d"], g["absgrad"],
+                           g["grad_conic"], g["grad_color"], g["grad_opacity"])
+    return {"records": rec[: 12 * I].reshape(I, 12) if I else rec[:0].reshape(0, 12), "has": has[:I], "g2d": g}
+
+
+def h_preprocess_backward(scene, pre, g2d, densif=None):
+    """The fp32 path's gradient chain (the reference's FGS16 preprocess
+    backward is the same chain on half 2D gradients), with pre's fields as the
+    chain reads them (n_touched only)."""
+    return preprocess_backward(scene, {"n_touched": pre["n_touched"]}, g2d, "f", densif=densif)

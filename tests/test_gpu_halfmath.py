@@ -1,7 +1,9 @@
 """The fp16 rasterizer's canonical half operations on the GPU
 (tinygs_amd/csrc/halfmath.h) against the oracle's (oracle/halfmath.h, pinned
 by tests/test_halfmath_host.py): exp2 over all 65,536 inputs, the arithmetic
-and conversions on random inputs with subnormals, packed and scalar."""
+and conversions on random inputs with subnormals, packed and scalar; the
+rounding of exact fixed-point sums; the lane layout of the DPP shift the fp16
+blend backward uses."""
 import numpy as np
 import pytest
 
@@ -11,7 +13,8 @@ pytestmark = pytest.mark.gpu
 def _gpu(op, a, b=None, c=None):
     import torch
     from tinygs_amd import _lib
-    ta = torch.from_numpy(np.ascontiguousarray(a).view(np.int16 if a.dtype == np.uint16 else np.float32)).cuda()
+    view = {np.dtype(np.uint16): np.int16, np.dtype(np.int64): np.int64}.get(a.dtype, np.float32)
+    ta = torch.from_numpy(np.ascontiguousarray(a).view(view)).cuda()
     tb = None if b is None else torch.from_numpy(b.view(np.int16)).cuda()
     tc = None if c is None else torch.from_numpy(c.view(np.int16)).cuda()
     out = torch.zeros(a.size, dtype=torch.int16, device="cuda")
@@ -38,7 +41,7 @@ def test_exp2_all_inputs(hip, orc):
     assert ok.all(), (np.count_nonzero(~ok), x[~ok][:8], got[~ok][:8], want[~ok][:8])
 
 
-@pytest.mark.parametrize("op", [2, 3, 4, 5, 6, 9])
+@pytest.mark.parametrize("op", [2, 3, 4, 5, 6, 9, 10])
 def test_arithmetic(hip, orc, op):
     rng = np.random.default_rng(op)
     n = 1 << 20
@@ -61,3 +64,26 @@ def test_conversions(hip, orc, op):
                        ).astype(np.float32)
     got, want = _gpu(op, f), orc.half_op(op, f)
     assert np.array_equal(got, want), (op, np.count_nonzero(got != want))
+
+
+def test_fixed_point_rounding(hip, orc):
+    """half_of_fixed: the nearest half of S * 2^-24 (exact integer sums of halves)."""
+    rng = np.random.default_rng(11)
+    mag = rng.integers(0, 43, 1 << 18)
+    s = (rng.integers(0, 1 << 62, 1 << 18) >> (62 - mag)) * rng.choice([-1, 1], 1 << 18)
+    # exact halfway points and their neighbours at several binades
+    q = rng.integers(1 << 10, 1 << 11, 4096)
+    sh = rng.integers(1, 30, 4096)
+    ties = (q << sh) + (1 << (sh - 1))
+    s = np.concatenate([s, ties, ties - 1, ties + 1, -ties, [0, 1, -1, (65520 << 24) - 1, 65520 << 24]]).astype(np.int64)
+    got, want = _gpu(11, s), orc.half_op(11, s)
+    assert np.array_equal(got, want), (np.count_nonzero(got != want), s[got != want][:4])
+
+
+def test_dpp_wave_shift_lane_layout(hip, orc):
+    rng = np.random.default_rng(12)
+    n = 64 * 64
+    a = rng.integers(0, 1 << 16, n).astype(np.uint16)
+    b = rng.integers(0, 1 << 16, n).astype(np.uint16)
+    got, want = _gpu(12, a, b), orc.half_op(12, a, b)
+    assert np.array_equal(got, want), np.count_nonzero(got != want)

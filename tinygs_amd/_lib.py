@@ -46,7 +46,8 @@ class tgs_debug_view(C.Structure):
                 ("depth_sorted_prims", C.c_void_p), ("instance_tiles", C.c_void_p), ("instance_prims", C.c_void_p),
                 ("tile_ranges", C.c_void_p), ("n_contrib", C.c_void_p), ("tile_max", C.c_void_p),
                 ("grad2d", C.c_void_p), ("n_visible", C.c_int64), ("n_instances", C.c_int64),
-                ("n_tiles", C.c_int64), ("depth_key_base", C.c_uint32), ("reserved", C.c_uint32)]
+                ("n_tiles", C.c_int64), ("depth_key_base", C.c_uint32), ("image_dtype", C.c_uint32),
+                ("first_slot", C.c_void_p), ("records", C.c_void_p)]
 
 
 class tgs_pcg32(C.Structure):
@@ -138,6 +139,7 @@ SIGNATURES = {
     "tgs_selftest_detmath": ([C.c_int32, P, P, C.c_int64, P], C.c_int),
     "tgs_selftest_wave": ([P, P, P], C.c_int),
     "tgs_selftest_half": ([C.c_int32, P, P, P, P, C.c_int64, P], C.c_int),
+    "tgs_selftest_half_div_exhaustive": ([P, P], C.c_int),
 }
 
 

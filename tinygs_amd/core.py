@@ -176,9 +176,10 @@ class Image:
     data: object = None  # torch tensor on the device, padded 8x8-tiled
 
     @classmethod
-    def empty(cls, shape: ImageShape, device: str = "cuda") -> "Image":
+    def empty(cls, shape: ImageShape, device: str = "cuda", data_type: str = DataType.Float32) -> "Image":
         torch = _torch()
-        return cls(shape, DataType.Float32, torch.zeros(shape.padded_size, dtype=torch.float32, device=device))
+        dt = torch.float16 if data_type == DataType.Float16 else torch.float32
+        return cls(shape, data_type, torch.zeros(shape.padded_size, dtype=dt, device=device))
 
     def __bool__(self):
         return self.data is not None

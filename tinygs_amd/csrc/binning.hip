@@ -25,6 +25,7 @@
 // wave.
 #include "common.h"
 #include "kernels.h"
+#include "fgs16.h"
 
 namespace tgs {
 
@@ -499,6 +500,19 @@ __device__ __forceinline__ bool will_contribute_e(float mx, float my, float ca, 
 // threads (contiguous stores), otherwise written directly.
 constexpr uint32_t kEmitStage = 4096;
 
+// The tile test of the record's rasterizer: fp32 (conic floats in w0..w2) or
+// FGS16 (half conic a | b << 16 in w0, c | opacity << 16 in w1).
+template <bool kHalf>
+__device__ __forceinline__ bool emit_test(float mx, float my, uint32_t w0, uint32_t w1, uint32_t w2, uint32_t tx,
+                                          uint32_t ty, float pt) {
+    if constexpr (kHalf)
+        return will_contribute_half(mx, my, hfrom((uint16_t)(w0 & 0xffffu)), hfrom((uint16_t)(w0 >> 16)),
+                                    hfrom((uint16_t)(w1 & 0xffffu)), tx, ty, pt);
+    else
+        return will_contribute_e(mx, my, u2f(w0), u2f(w1), u2f(w2), tx, ty, pt);
+}
+
+template <bool kHalf>
 __global__ void __launch_bounds__(256) emit_kernel(const uint32_t* __restrict__ prims,
                                                    const uint32_t* __restrict__ offs, BinCtl* ctl,
                                                    int64_t max_count, int64_t max_inst, const uint4* __restrict__ rec,
@@ -535,7 +549,8 @@ __global__ void __launch_bounds__(256) emit_kernel(const uint32_t* __restrict__ 
     const bool active = k < n;
     const uint32_t lane = lane_id();
     uint32_t p = 0, off = 0, cap = 0, x0 = 0, x1 = 0, y0 = 0, y1 = 0, bits = 0;
-    float smx = 0.f, smy = 0.f, ca = 0.f, cb = 0.f, cc = 0.f, pt = 0.f;
+    float smx = 0.f, smy = 0.f, pt = 0.f;
+    uint32_t cw0 = 0, cw1 = 0, cw2 = 0;
     if (active) {
         p = prims[k];
         off = offs[k];
@@ -549,7 +564,7 @@ __global__ void __launch_bounds__(256) emit_kernel(const uint32_t* __restrict__ 
         x0 = r0.x & 0xffffu; x1 = r0.x >> 16; y0 = r0.y & 0xffffu; y1 = r0.y >> 16;
         smx = u2f(r0.z) - 0.5f;
         smy = u2f(r0.w) - 0.5f;
-        ca = u2f(r1.x); cb = u2f(r1.y); cc = u2f(r1.z); pt = u2f(r1.w);
+        cw0 = r1.x; cw1 = r1.y; cw2 = r1.z; pt = u2f(r1.w);
     }
     const uint32_t bw = x1 - x0;
     const uint32_t nrect = bw * (y1 - y0);
@@ -570,7 +585,7 @@ __global__ void __launch_bounds__(256) emit_kernel(const uint32_t* __restrict__ 
         const uint32_t src = (uint32_t)__builtin_ctzll(coop);
         coop &= coop - 1;
         const float s_mx = readlane_f32(smx, src), s_my = readlane_f32(smy, src);
-        const float s_a = readlane_f32(ca, src), s_b = readlane_f32(cb, src), s_c = readlane_f32(cc, src);
+        const uint32_t s_a = readlane_u32(cw0, src), s_b = readlane_u32(cw1, src), s_c = readlane_u32(cw2, src);
         const float s_t = readlane_f32(pt, src);
         const uint32_t s_x0 = readlane_u32(x0, src), s_y0 = readlane_u32(y0, src);
         const uint32_t s_bw = readlane_u32(bw, src), s_n = readlane_u32(nrect, src);
@@ -585,7 +600,7 @@ __global__ void __launch_bounds__(256) emit_kernel(const uint32_t* __restrict__ 
             if (q < s_n) {
                 tx = s_x0 + q % s_bw;
                 ty = s_y0 + q / s_bw;
-                hit = q < 32u ? ((s_bits >> q) & 1u) != 0u : will_contribute_e(s_mx, s_my, s_a, s_b, s_c, tx, ty, s_t);
+                hit = q < 32u ? ((s_bits >> q) & 1u) != 0u : emit_test<kHalf>(s_mx, s_my, s_a, s_b, s_c, tx, ty, s_t);
             }
             const uint64_t m = ballot(hit);
             const uint32_t pos = s_off + mask_rank(m);
@@ -604,11 +619,16 @@ __global__ void __launch_bounds__(256) emit_kernel(const uint32_t* __restrict__ 
 
 void launch_emit_instances(const uint32_t* prims, const uint32_t* offs, BinCtl* ctl, int64_t max_count,
                            int64_t max_inst, const uint4* rec, const uint32_t* tile_bits, uint32_t grid_w,
-                           uint32_t* inst_keys, uint32_t* inst_vals, uint32_t* first_slot, hipStream_t s) {
+                           uint32_t* inst_keys, uint32_t* inst_vals, uint32_t* first_slot, bool half_test,
+                           hipStream_t s) {
     if (max_count <= 0) return;
-    emit_kernel<<<(unsigned)((max_count + 255) / 256), 256, 0, s>>>(prims, offs, ctl, max_count, max_inst, rec,
-                                                                    tile_bits, grid_w, inst_keys, inst_vals,
-                                                                    first_slot);
+    const unsigned grid = (unsigned)((max_count + 255) / 256);
+    if (half_test)
+        emit_kernel<true><<<grid, 256, 0, s>>>(prims, offs, ctl, max_count, max_inst, rec, tile_bits, grid_w,
+                                               inst_keys, inst_vals, first_slot);
+    else
+        emit_kernel<false><<<grid, 256, 0, s>>>(prims, offs, ctl, max_count, max_inst, rec, tile_bits, grid_w,
+                                                inst_keys, inst_vals, first_slot);
 }
 
 // ---------------------------------------------------------------- ranges

@@ -236,6 +236,7 @@ struct tgs_rasterizer {
     int64_t inst_cap = 0;            // reserved instance capacity (tgs_rasterizer_reserve)
     bool counts_on_device = false;   // the last forward did not wait for V, I
     int psel = 0, isel = 0;
+    bool fgs16 = false;              // the last forward rendered an fp16 image (FGS16)
 };
 
 // Look-back status words for `entries` slots. A (re)allocated array is
@@ -395,8 +396,10 @@ static int rasterizer_forward(tgs_rasterizer* r, const tgs_camera* camera, void*
     if (!r) return fail(TGS_ERR_INVALID, "rasterizer is NULL");
     if (!r->has_g) return fail(TGS_ERR_STATE, "Gaussians not set");
     if (!image) return fail(TGS_ERR_INVALID, "image is NULL");
-    if (image_dtype != TGS_DTYPE_FLOAT32)
-        return fail(TGS_ERR_UNSUPPORTED, "image dtype %d: only float32 images are supported", image_dtype);
+    // fastgs.cu:143-188: the image dtype selects the rasterizer (fp16: FGS16)
+    if (image_dtype != TGS_DTYPE_FLOAT32 && image_dtype != TGS_DTYPE_FLOAT16)
+        return fail(TGS_ERR_UNSUPPORTED, "image dtype %d: float32 or float16 images only", image_dtype);
+    const bool f16 = image_dtype == TGS_DTYPE_FLOAT16;
     if (flags & ~TGS_FORWARD_NO_SYNC) return fail(TGS_ERR_INVALID, "unknown forward flags 0x%x", flags);
     const bool nosync = (flags & TGS_FORWARD_NO_SYNC) != 0;
     hipStream_t s = (hipStream_t)stream;
@@ -457,10 +460,15 @@ static int rasterizer_forward(tgs_rasterizer* r, const tgs_camera* camera, void*
     launch_bin_ctl_reset(ctl, s);
     {
         StageScope sc(ST_PRE, s);
-        launch_preprocess(gv, cam, r->n_touched.as<uint32_t>(), r->tile_bits.as<uint32_t>(), r->rec.as<uint4>(),
-                          r->mean2d.as<float2>(),
-                          r->conic_opacity.as<float4>(), r->color.as<float4>(), r->depth_key.as<uint32_t>(),
-                          (float*)densification_info, s);
+        if (f16)
+            launch_preprocess16(gv, cam, r->n_touched.as<uint32_t>(), r->tile_bits.as<uint32_t>(),
+                                r->rec.as<uint4>(), r->mean2d.as<float2>(), r->conic_opacity.as<float4>(),
+                                r->color.as<uint4>(), r->depth_key.as<uint32_t>(), (float*)densification_info, s);
+        else
+            launch_preprocess(gv, cam, r->n_touched.as<uint32_t>(), r->tile_bits.as<uint32_t>(), r->rec.as<uint4>(),
+                              r->mean2d.as<float2>(),
+                              r->conic_opacity.as<float4>(), r->color.as<float4>(), r->depth_key.as<uint32_t>(),
+                              (float*)densification_info, s);
     }
     TGS_CHECK_LAUNCH();
     uint32_t* pk[2] = {r->pkeys[0].as<uint32_t>(), r->pkeys[1].as<uint32_t>()};
@@ -504,7 +512,7 @@ static int rasterizer_forward(tgs_rasterizer* r, const tgs_camera* camera, void*
         launch_emit_instances(pv[psel], r->offs.as<uint32_t>(), ctl, n, cap, r->rec.as<uint4>(),
                               r->tile_bits.as<uint32_t>(), cam.grid_w,
                               r->ikeys[0].as<uint32_t>(), r->ivals[0].as<uint32_t>(), r->first_slot.as<uint32_t>(),
-                              s);
+                              f16, s);
     }
     uint32_t* ik[2] = {r->ikeys[0].as<uint32_t>(), r->ikeys[1].as<uint32_t>()};
     uint32_t* iv[2] = {r->ivals[0].as<uint32_t>(), r->ivals[1].as<uint32_t>()};
@@ -521,10 +529,15 @@ static int rasterizer_forward(tgs_rasterizer* r, const tgs_camera* camera, void*
     if (nosync) launch_capacity_check(ctl, cap, s);
     {
         StageScope sc(ST_BLENDF, s);
-        launch_blend_forward(cam, r->ranges.as<uint2>(), iv[isel], r->mean2d.as<float2>(),
-                             r->conic_opacity.as<float4>(), r->color.as<float4>(), (float*)image,
-                             r->n_contrib.as<uint32_t>(), r->tile_max.as<uint32_t>(),
-                             r->tile_loaded.as<uint32_t>(), r->ckpt.as<float4>(), r->items.as<uint4>(), ctl, s);
+        if (f16)
+            launch_blend16_forward(cam, r->ranges.as<uint2>(), iv[isel], r->mean2d.as<float2>(), r->color.as<uint4>(),
+                                   (uint16_t*)image, r->n_contrib.as<uint16_t>(), r->tile_max.as<uint32_t>(),
+                                   r->tile_loaded.as<uint32_t>(), r->ckpt.as<uint2>(), r->items.as<uint4>(), ctl, s);
+        else
+            launch_blend_forward(cam, r->ranges.as<uint2>(), iv[isel], r->mean2d.as<float2>(),
+                                 r->conic_opacity.as<float4>(), r->color.as<float4>(), (float*)image,
+                                 r->n_contrib.as<uint32_t>(), r->tile_max.as<uint32_t>(),
+                                 r->tile_loaded.as<uint32_t>(), r->ckpt.as<float4>(), r->items.as<uint4>(), ctl, s);
     }
     TGS_CHECK_LAUNCH();
     r->cam = cam;
@@ -534,6 +547,7 @@ static int rasterizer_forward(tgs_rasterizer* r, const tgs_camera* camera, void*
     r->counts_on_device = nosync;
     r->psel = psel;
     r->isel = isel;
+    r->fgs16 = f16;
     r->fwd_done = true;
     r->bwd_queues_clear = true;
     return TGS_OK;
@@ -626,11 +640,17 @@ int tgs_rasterizer_backward_ex(tgs_rasterizer* r, const void* grad_image, const 
         launch_fill_u32(ctl->bwd_queue, 0u, kBwdCtlWords, s);
     {
         StageScope sc(ST_BLENDB, s);
-        launch_blend_backward(cam, r->ivals[r->isel].as<uint32_t>(), r->mean2d.as<float2>(),
-                              r->conic_opacity.as<float4>(), r->color.as<float4>(), (const float*)image,
-                              (const float*)grad_image, r->n_contrib.as<uint32_t>(), r->ckpt.as<float4>(),
-                              r->items.as<uint4>(), ctl, r->rec_count.as<uint32_t>(), r->first_slot.as<uint32_t>(),
-                              r->records.as<float4>(), densification_info != nullptr, s);
+        if (r->fgs16)   // fastgs.cu:273-274: half image and gradient image
+            launch_blend16_backward(cam, r->ivals[r->isel].as<uint32_t>(), r->mean2d.as<float2>(),
+                                    r->color.as<uint4>(), (const uint16_t*)image, (const uint16_t*)grad_image,
+                                    r->ckpt.as<uint2>(), r->items.as<uint4>(), ctl, r->rec_count.as<uint32_t>(),
+                                    r->first_slot.as<uint32_t>(), r->records.as<float4>(), s);
+        else
+            launch_blend_backward(cam, r->ivals[r->isel].as<uint32_t>(), r->mean2d.as<float2>(),
+                                  r->conic_opacity.as<float4>(), r->color.as<float4>(), (const float*)image,
+                                  (const float*)grad_image, r->n_contrib.as<uint32_t>(), r->ckpt.as<float4>(),
+                                  r->items.as<uint4>(), ctl, r->rec_count.as<uint32_t>(), r->first_slot.as<uint32_t>(),
+                                  r->records.as<float4>(), densification_info != nullptr, s);
     }
     r->bwd_queues_clear = false;
     TGS_CHECK_LAUNCH();
@@ -643,7 +663,7 @@ int tgs_rasterizer_backward_ex(tgs_rasterizer* r, const void* grad_image, const 
                                    r->grad2d.as<float>(), gv, (float*)densification_info, mode,
                                    r->row_mask.as<uint8_t>(), r->live.as<uint4>(), r->heavy.as<uint4>(),
                                    r->chunk_counts.as<uint2>(), pose ? r->pose_partial.as<float>() : nullptr,
-                                   pose ? r->pose_grad.as<float>() : nullptr, keep2d, s);
+                                   pose ? r->pose_grad.as<float>() : nullptr, keep2d, r->fgs16, s);
     }
     TGS_CHECK_LAUNCH();
     r->row_mask_valid = mode == kGradSparse;
@@ -713,6 +733,9 @@ int tgs_rasterizer_debug_view(tgs_rasterizer* r, tgs_debug_view* out) {
     out->n_visible = r->V;
     out->n_instances = r->I;
     out->n_tiles = (int64_t)r->cam.grid_w * r->cam.grid_h;
+    out->image_dtype = r->fgs16 ? TGS_DTYPE_FLOAT16 : TGS_DTYPE_FLOAT32;
+    out->first_slot = r->first_slot.as<uint32_t>();
+    out->records = r->records.as<float>();
     return TGS_OK;
 }
 
@@ -1408,9 +1431,20 @@ int tgs_selftest_detmath(int32_t op, const float* in, float* out, int64_t n, voi
 int tgs_selftest_half(int32_t op, const void* a, const void* b, const void* c, void* out, int64_t n, void* stream) {
     if (n < 0 || (n > 0 && (!a || !out))) return fail(TGS_ERR_INVALID, "bad argument");
     if ((op == 2 || op == 6) && n > 0 && (!b || !c)) return fail(TGS_ERR_INVALID, "bad argument");
-    if ((op == 3 || op == 4 || op == 5 || op == 9) && n > 0 && !b) return fail(TGS_ERR_INVALID, "bad argument");
+    if ((op == 3 || op == 4 || op == 5 || op == 9 || op == 10 || op == 12) && n > 0 && !b)
+        return fail(TGS_ERR_INVALID, "bad argument");
+    if (op < 0 || op > 12 || (op == 12 && n % 64 != 0)) return fail(TGS_ERR_INVALID, "op %d, n %lld", op, (long long)n);
     launch_halfmath(op, (const uint16_t*)a, (const uint16_t*)b, (const uint16_t*)c, (uint16_t*)out, n,
                     (hipStream_t)stream);
+    TGS_CHECK_LAUNCH();
+    return TGS_OK;
+}
+
+int tgs_selftest_half_div_exhaustive(int64_t* out, void* stream) {
+    if (!out) return fail(TGS_ERR_INVALID, "bad argument");
+    hipStream_t s = (hipStream_t)stream;
+    launch_fill_u32((uint32_t*)out, 0u, 16, s);
+    launch_half_div_check((unsigned long long*)out, s);
     TGS_CHECK_LAUNCH();
     return TGS_OK;
 }

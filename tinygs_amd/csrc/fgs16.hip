@@ -1,0 +1,440 @@
+// Blend forward and backward of the fp16-image rasterizer (FGS16).
+//
+// Reference: blend_cu2 (tinygs/src/rasterizer/fastgs_ours_fp16/
+// kernels_forward.cuh:917-1171) and blend_backward_cu2 (kernels_backward.cuh:
+// 861-1389). Their numerics are kept: half mean / conic in 16-pixel tile
+// units with the conic scaled by 16, an 8-bit colour, 255-scaled colour and
+// transmittance, alpha = min(o * 2^(-sigma log2 e), 0.99) with no 1/255 cut,
+// the transmittance stop nT < RD(255e-4) with the stopping Gaussian not
+// composited, a 16-bit saturating count of processed Gaussians per pixel,
+// checkpoints every 32 Gaussians, and a backward that weighs every Gaussian of
+// a bucket at every pixel of the tile (as compiled: TINYGS_SAFE_MATH is never
+// defined). Every half operation is the canonical one of halfmath.h, in the
+// operation order of the CPU oracle (oracle/fgs16_impl.inc), so pixels,
+// counts, checkpoints and the per-(primitive, bucket) gradient records are
+// bit-identical to it.
+//
+// MI355X mapping:
+//   * forward: one wave64 per tile. Lane L owns pixel L of each 8x8 block q
+//     of the tile, i.e. in-tile pixels 64 q + L, held as two half2 pairs
+//     (blocks 0, 1) and (2, 3); every image / count / checkpoint access of a
+//     block is one contiguous run. The tile's Gaussians are staged 64 at a
+//     time, one per lane, and broadcast to the wave with v_readlane (no LDS).
+//   * backward: one (tile, 32-Gaussian bucket) work item per half wave, two
+//     per wave. As in the reference, lane l of the half owns Gaussian l of the
+//     bucket and the tile's 128 pixel pairs stream through the lanes: at step
+//     s lane l processes pair s - l with the state Gaussians 0..l-1 left, then
+//     hands the state to lane l + 1 with one DPP wave_shr:1 per register
+//     (lanes 0 and 32 load the next pair from LDS instead). Each Gaussian so
+//     accumulates its sums over the pairs in the reference's order.
+//   * the per-(primitive, bucket) results are 12-float records in the slots
+//     binning reserved (as the fp32 path); the preprocess backward sums them
+//     exactly (halfmath.h half_of_fixed) instead of the reference's half2
+//     atomics, whose rounding depends on the order buckets finish in.
+#include "common.h"
+#include "fgs16.h"
+#include "kernels.h"
+
+namespace tgs {
+
+namespace {
+
+constexpr uint16_t kH255 = 0x5bf8;   // 255
+constexpr uint16_t kHUnscale = 0x1c04;   // RN(1/255)
+
+__device__ __forceinline__ uint32_t rl(uint32_t v, int lane) { return (uint32_t)__builtin_amdgcn_readlane((int)v, lane); }
+
+// The half pixel-centre offsets of blend_cu2 (kernels_forward.cuh:960-967) in
+// tile units: x of an even in-tile column lx = fma(1/16, lx, 1/32), of an odd
+// one 1/16 + that of lx - 1; y = fma(1/16, ly, 1/32).
+__device__ __forceinline__ h16 offset_x(uint32_t lx) {
+    const h16 base = h_fma((h16)0.0625f, (h16)(float)(lx & ~1u), (h16)(1.0f / 32.0f));
+    return (lx & 1u) ? (h16)0.0625f + base : base;
+}
+__device__ __forceinline__ h16 offset_y(uint32_t ly) {
+    return h_fma((h16)0.0625f, (h16)(float)ly, (h16)(1.0f / 32.0f));
+}
+
+// ge / select on half2 lanes
+__device__ __forceinline__ h16x2 sel2(bool cx, bool cy, h16x2 a, h16x2 b) {
+    return h2(cx ? a.x : b.x, cy ? a.y : b.y);
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------- forward
+
+// info[p] = (conic a | b << 16, c | opacity << 16, r | g << 8 | b << 16, 0)
+// ckpt16: per slot 256 pixels of (C.r | C.g << 16, C.b | T << 16) halves, in-tile index 64 q + L.
+__global__ void __launch_bounds__(256) blend16_forward_kernel(
+    CamParams cam, const uint2* __restrict__ ranges, const uint32_t* __restrict__ inst_vals,
+    const float2* __restrict__ mean2d, const uint4* __restrict__ info, uint16_t* __restrict__ image,
+    uint16_t* __restrict__ n_contrib, uint32_t* __restrict__ tile_max, uint32_t* __restrict__ tile_loaded,
+    uint2* __restrict__ ckpt, uint4* __restrict__ items, BinCtl* __restrict__ ctl) {
+    const uint32_t n_tiles = cam.grid_w * cam.grid_h;
+    const uint32_t tile = blockIdx.x * 4u + (threadIdx.x >> 6);
+    if (tile >= n_tiles) return;   // whole waves
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t gx = tile % cam.grid_w, gy = tile / cam.grid_w;
+    const uint32_t lx = lane & 7u, ly = lane >> 3;
+
+    const h16 thr = h_rd(1e-4f * 255.0f);
+    const h16x2 maxa = h2s((h16)0.99f), unscale = h2s(hfrom(kHUnscale)), h16c = h2s((h16)16.0f),
+                h05 = h2s((h16)0.5f), nlog2e = h2s(-(h16)1.4426950409f);
+    // pair 0: blocks 0, 1 (x + 8); pair 1: blocks 2, 3 (y + 8)
+    const h16x2 offx = h2(offset_x(lx), offset_x(lx + 8u));
+    const h16x2 offy[2] = {h2s(offset_y(ly)), h2s(offset_y(ly + 8u))};
+    bool inside[4];
+#pragma unroll
+    for (uint32_t q = 0; q < 4; ++q) {
+        const uint32_t px = gx * 16u + (q & 1u) * 8u + lx, py = gy * 16u + (q >> 1) * 8u + ly;
+        inside[q] = px < cam.width && py < cam.height;
+    }
+
+    const uint2 range = ranges[tile];
+    const int32_t len = (int32_t)(range.y - range.x);
+    const uint32_t slot0 = range.x / (uint32_t)kBucket + tile;
+
+    h16x2 C0[2], C1[2], C2[2], T[2];
+    uint32_t nc[4] = {0u, 0u, 0u, 0u};
+    bool unf[4];
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+        C0[k] = C1[k] = C2[k] = h2s((h16)0.0f);
+        T[k] = h2s(hfrom(kH255));
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q) unf[q] = inside[q];
+    uint32_t loaded = 0;
+
+    for (int32_t base = 0; base < len; base += 64) {
+        if (!__any(unf[0] || unf[1] || unf[2] || unf[3])) break;
+        const int32_t nb = min(64, len - base);
+        // staging (kernels_forward.cuh:1044-1056): this lane's Gaussian base + lane
+        uint32_t w0 = 0, w1 = 0, w2 = 0, w3 = 0, w4 = 0;
+        if ((int32_t)lane < nb) {
+            const uint32_t p = inst_vals[range.x + (uint32_t)(base + (int32_t)lane)];
+            const float2 m = mean2d[p];
+            const uint4 in = info[p];
+            const h16 mx = h_rn(m.x / 16.0f - (float)gx), my = h_rn(m.y / 16.0f - (float)gy);
+            const h16 cxh = hfrom((uint16_t)(in.x & 0xffffu)) * (h16)16.0f;
+            const h16 cyh = hfrom((uint16_t)(in.x >> 16)) * (h16)16.0f;
+            const h16 czh = hfrom((uint16_t)(in.y & 0xffffu)) * (h16)16.0f;
+            const h16 o = hfrom((uint16_t)(in.y >> 16)) * (h16)1.0f;
+            w0 = (uint32_t)hbits(mx) | ((uint32_t)hbits(my) << 16);
+            w1 = (uint32_t)hbits(cxh) | ((uint32_t)hbits(cyh) << 16);
+            w2 = (uint32_t)hbits(czh) | ((uint32_t)hbits(o) << 16);
+            w3 = (uint32_t)hbits((h16)(float)(in.z & 0xffu)) | ((uint32_t)hbits((h16)(float)((in.z >> 8) & 0xffu)) << 16);
+            w4 = (uint32_t)hbits((h16)(float)((in.z >> 16) & 0xffu));
+        }
+        loaded += (uint32_t)nb;
+        for (int32_t e = 0; e < nb; ++e) {
+            const int32_t j = base + e;
+            if ((j & (kBucket - 1)) == 0 && j > 0) {   // checkpoint before Gaussian j (:1000-1012)
+                uint2* ck = ckpt + (size_t)(slot0 + (uint32_t)(j / kBucket) - 1u) * kTilePixels + lane;
+#pragma unroll
+                for (int k = 0; k < 2; ++k) {
+                    ck[(2 * k) * 64] = make_uint2((uint32_t)hbits(C0[k].x) | ((uint32_t)hbits(C1[k].x) << 16),
+                                                  (uint32_t)hbits(C2[k].x) | ((uint32_t)hbits(T[k].x) << 16));
+                    ck[(2 * k + 1) * 64] = make_uint2((uint32_t)hbits(C0[k].y) | ((uint32_t)hbits(C1[k].y) << 16),
+                                                      (uint32_t)hbits(C2[k].y) | ((uint32_t)hbits(T[k].y) << 16));
+                }
+            }
+            const h16x2 g0 = h2from(rl(w0, e)), g1 = h2from(rl(w1, e)), g2 = h2from(rl(w2, e));
+            const h16x2 g3 = h2from(rl(w3, e)), g4 = h2from(rl(w4, e));
+            const h16x2 mx2 = h2s(g0.x), my2 = h2s(g0.y), cx2 = h2s(g1.x), cy2 = h2s(g1.y);
+            const h16x2 cz2 = h2s(g2.x), o2 = h2s(g2.y), r2 = h2s(g3.x), gg2 = h2s(g3.y), b2 = h2s(g4.x);
+#pragma unroll
+            for (int k = 0; k < 2; ++k) {
+                // :1069-1105
+                const h16x2 dx = mx2 - offx, dy = my2 - offy[k];
+                const h16x2 qxx = dx * (cx2 * dx);
+                const h16x2 qzz = dy * (cz2 * dy);
+                const h16x2 qxy = dx * (cy2 * dy);
+                const h16x2 quad = qxx + qzz;
+                const h16x2 s2 = h2_fma(h05, quad, qxy) * h16c;
+                const h16x2 gss = h2_exp2(s2 * nlog2e);
+                const h16x2 alpha = h2_min(o2 * gss, maxa);
+                const h16x2 nT = h2_fma(-alpha, T[k], T[k]);
+                const bool ax = nT.x >= thr, ay = nT.y >= thr;
+                const bool ex = unf[2 * k] && ax, ey = unf[2 * k + 1] && ay;
+                const h16x2 tah = sel2(ex, ey, (T[k] * alpha) * unscale, h2s((h16)0.0f));
+                C0[k] = h2_fma(r2, tah, C0[k]);
+                C1[k] = h2_fma(gg2, tah, C1[k]);
+                C2[k] = h2_fma(b2, tah, C2[k]);
+                T[k] = sel2(ex, ey, nT, T[k]);
+                nc[2 * k] += (unf[2 * k] && nc[2 * k] < 0xffffu) ? 1u : 0u;
+                nc[2 * k + 1] += (unf[2 * k + 1] && nc[2 * k + 1] < 0xffffu) ? 1u : 0u;
+                unf[2 * k] = ex;
+                unf[2 * k + 1] = ey;
+            }
+            // :1115: after each 32 Gaussians, a saturated count stops the pixel
+            if ((j & (kBucket - 1)) == kBucket - 1 || j + 1 == len) {
+#pragma unroll
+                for (int q = 0; q < 4; ++q) unf[q] = unf[q] && nc[q] < 0xffffu;
+            }
+            if ((e & 7) == 7 && !__any(unf[0] || unf[1] || unf[2] || unf[3])) break;
+        }
+    }
+
+    const uint32_t pw = cam.tiled_w * 8u, ph = cam.tiled_h * 8u;
+    const uint32_t cs = cam.tiled_w * cam.tiled_h * 64u;
+#pragma unroll
+    for (uint32_t q = 0; q < 4; ++q) {
+        const uint32_t px = gx * 16u + (q & 1u) * 8u + lx, py = gy * 16u + (q >> 1) * 8u + ly;
+        if (px < pw && py < ph) {
+            const uint32_t pi = tiled_index(py, px, cam.tiled_w);
+            const int k = (int)(q >> 1);
+            const bool hi = (q & 1u) != 0u;
+            const h16 c0 = hi ? C0[k].y : C0[k].x, c1 = hi ? C1[k].y : C1[k].x, c2 = hi ? C2[k].y : C2[k].x;
+            const h16 us = hfrom(kHUnscale);
+            image[pi] = inside[q] ? hbits(c0 * us) : (uint16_t)0u;
+            image[pi + cs] = inside[q] ? hbits(c1 * us) : (uint16_t)0u;
+            image[pi + 2 * cs] = inside[q] ? hbits(c2 * us) : (uint16_t)0u;
+            n_contrib[pi] = inside[q] ? (uint16_t)nc[q] : (uint16_t)0u;
+        }
+    }
+    const uint32_t tmax = wave_max_u32(max(max(nc[0], nc[1]), max(nc[2], nc[3])));
+    // backward work items: every bucket below the tile's largest count, each
+    // with all its Gaussians (the backward does not stop at a pixel's count)
+    const uint32_t nbk = (tmax + (uint32_t)kBucket - 1u) / (uint32_t)kBucket;
+    uint32_t off = 0;
+    if (lane == 0) {
+        tile_max[tile] = tmax;
+        tile_loaded[tile] = loaded;
+        if (nbk) off = atomicAdd(&ctl->n_items, nbk);
+    }
+    off = (uint32_t)__builtin_amdgcn_readfirstlane((int)off);
+    for (uint32_t b = lane; b < nbk; b += 64u)
+        items[off + b] = make_uint4(tile, b, range.x + b * (uint32_t)kBucket,
+                                    min((uint32_t)kBucket, (uint32_t)len - b * (uint32_t)kBucket));
+}
+
+void launch_blend16_forward(const CamParams& cam, const uint2* ranges, const uint32_t* inst_vals,
+                            const float2* mean2d, const uint4* info, uint16_t* image, uint16_t* n_contrib,
+                            uint32_t* tile_max, uint32_t* tile_loaded, uint2* ckpt, uint4* items, BinCtl* ctl,
+                            hipStream_t s) {
+    const uint32_t n_tiles = cam.grid_w * cam.grid_h;
+    if (n_tiles == 0) return;
+    blend16_forward_kernel<<<(n_tiles + 3u) / 4u, 256, 0, s>>>(cam, ranges, inst_vals, mean2d, info, image,
+                                                                n_contrib, tile_max, tile_loaded, ckpt, items, ctl);
+}
+
+// ---------------------------------------------------------------- backward
+
+namespace {
+
+// per pixel pair: grad r, g, b; colour after r, g, b; transmittance; (offx, offy)
+struct PairState {
+    uint32_t v[8];
+};
+
+__device__ __forceinline__ uint32_t shr1(uint32_t x) {
+    // DPP wave_shr:1: lane l receives lane l - 1 (lane 0 keeps 0)
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x138, 0xf, 0xf, false);
+}
+
+}  // namespace
+
+__global__ void __launch_bounds__(256) blend16_backward_kernel(
+    CamParams cam, const uint32_t* __restrict__ inst_vals, const float2* __restrict__ mean2d,
+    const uint4* __restrict__ info, const uint16_t* __restrict__ image, const uint16_t* __restrict__ grad_image,
+    const uint2* __restrict__ ckpt, const uint4* __restrict__ items, BinCtl* __restrict__ ctl,
+    uint32_t* __restrict__ rec_count, const uint32_t* __restrict__ first_slot, float4* __restrict__ records) {
+    __shared__ uint4 s_pair[4][2][128][2];   // [wave][half][pair][2 x 4 dwords]
+
+    const uint32_t w = threadIdx.x >> 6, lane = threadIdx.x & 63u;
+    const uint32_t half = lane >> 5, l = lane & 31u;
+    const uint32_t n_items = ctl->n_items;
+    const uint32_t cs = cam.tiled_w * cam.tiled_h * 64u;
+    const uint32_t queue = (blockIdx.x * 4u + w) % (uint32_t)kBwdQueues;
+    uint32_t* qctr = &ctl->bwd_queue[queue * 32u];
+    uint32_t next = 0;
+    if (lane == 0) next = atomicAdd(qctr, 1u);
+    next = (uint32_t)__builtin_amdgcn_readfirstlane((int)next);
+
+    const h16x2 h05 = h2s((h16)0.5f), h16c = h2s((h16)16.0f), one = h2s((h16)1.0f), maxa = h2s((h16)0.99f),
+                nlog2e = h2s(-(h16)1.4426950409f), inv16 = h2s((h16)0.0625f);
+
+    while (true) {
+        const uint32_t pr = queue + next * (uint32_t)kBwdQueues;   // item pair
+        if (2u * pr >= n_items) break;
+        uint32_t after = 0;
+        if (lane == 0) after = atomicAdd(qctr, 1u);
+        const uint32_t it = 2u * pr + half;
+        const bool have = it < n_items;
+        const uint4 item = have ? items[it] : make_uint4(0u, 0u, 0u, 0u);
+        const uint32_t tile = item.x, b = item.y, first = item.z;
+        const uint32_t cnt = item.w;   // 0 for a missing second item
+        const uint32_t gx = tile % cam.grid_w, gy = tile / cam.grid_w;
+
+        // ---- this lane's Gaussian (kernels_backward.cuh:1019-1037); its record slot
+        h16x2 mxp = h2s((h16)0.f), my2 = mxp, cx2 = mxp, cy2 = mxp, cz2 = mxp, o2 = mxp;
+        h16x2 cr2 = mxp, cg2 = mxp, cb2 = mxp;
+        uint32_t p = 0, slot = 0;
+        if (l < cnt) {
+            p = inst_vals[first + l];
+            slot = first_slot[p] + atomicAdd(rec_count + p, 1u);
+            const float2 m = mean2d[p];
+            const uint4 in = info[p];
+            const float mfx = m.x / 16.0f - (float)gx, mfy = m.y / 16.0f - (float)gy;
+            const h16 mx0 = h_rn(mfx - 1.0f / 32.0f), my = h_rn(mfy - 1.0f / 32.0f);
+            const h16 mx1 = mx0 - (h16)(1.0f / 16.0f);
+            mxp = h2(mx0, mx1);
+            my2 = h2s(my);
+            cx2 = h2s(hfrom((uint16_t)(in.x & 0xffffu)) * (h16)16.0f);
+            cy2 = h2s(hfrom((uint16_t)(in.x >> 16)) * (h16)16.0f);
+            cz2 = h2s(hfrom((uint16_t)(in.y & 0xffffu)) * (h16)16.0f);
+            o2 = h2s(hfrom((uint16_t)(in.y >> 16)));
+            cr2 = h2s((h16)(float)(in.z & 0xffu));
+            cg2 = h2s((h16)(float)((in.z >> 8) & 0xffu));
+            cb2 = h2s((h16)(float)((in.z >> 16) & 0xffu));
+        }
+
+        // ---- pixel-pair state at the bucket start (:1095-1136), four pairs per lane
+        if (cnt) {
+            const uint32_t slot0 = (first - b * (uint32_t)kBucket) / (uint32_t)kBucket + tile;
+            const uint2* ck = ckpt + (size_t)(b > 0 ? slot0 + b - 1u : 0u) * kTilePixels;
+#pragma unroll
+            for (uint32_t r = 0; r < 4; ++r) {
+                const uint32_t i = l + 32u * r;   // pair index 0..127
+                const uint32_t e = 2u * i, local_tile = e >> 6, intile = e & 63u;
+                const uint32_t dx_ = (intile & 7u) + (local_tile & 1u) * 8u, dy_ = (intile >> 3) + (local_tile >> 1) * 8u;
+                const uint32_t px = gx * 16u + dx_, py = gy * 16u + dy_;
+                const bool start_valid = (gx * 16u + (local_tile & 1u) * 8u < cam.width) &&
+                                         (gy * 16u + (local_tile >> 1) * 8u < cam.height);
+                const bool ok = start_valid && px < cam.width && py < cam.height;
+                uint4 a = make_uint4(0u, 0u, 0u, 0u), c = make_uint4(0u, 0u, 0u, 0u);
+                if (ok) {
+                    const uint32_t pi = tiled_index(py, px, cam.tiled_w);   // even: the pair is one aligned word
+                    const uint32_t* gi = (const uint32_t*)(grad_image + pi);
+                    const uint32_t* im = (const uint32_t*)(image + pi);
+                    const h16x2 G0 = h2from(gi[0]), G1 = h2from(gi[cs / 2u]), G2 = h2from(gi[cs]);
+                    const h16x2 I0 = h2from(im[0]), I1 = h2from(im[cs / 2u]), I2 = h2from(im[cs]);
+                    uint4 k4 = make_uint4(0u, (uint32_t)kH255 << 16, 0u, (uint32_t)kH255 << 16);
+                    if (b > 0) k4 = *(const uint4*)(ck + e);
+                    // (C.r | C.g, C.b | T) of the even pixel in k4.x, k4.y, of the odd one in k4.z, k4.w
+                    const h16x2 K0 = h2(hfrom((uint16_t)(k4.x & 0xffffu)), hfrom((uint16_t)(k4.z & 0xffffu)));
+                    const h16x2 K1 = h2(hfrom((uint16_t)(k4.x >> 16)), hfrom((uint16_t)(k4.z >> 16)));
+                    const h16x2 K2 = h2(hfrom((uint16_t)(k4.y & 0xffffu)), hfrom((uint16_t)(k4.w & 0xffffu)));
+                    const h16x2 KT = h2(hfrom((uint16_t)(k4.y >> 16)), hfrom((uint16_t)(k4.w >> 16)));
+                    const h16x2 sc = h2s(hfrom(kH255));
+                    a = make_uint4(h2bits(G0), h2bits(G1), h2bits(G2), h2bits(h2_fma(I0, sc, -K0)));
+                    c = make_uint4(h2bits(h2_fma(I1, sc, -K1)), h2bits(h2_fma(I2, sc, -K2)),
+                                   h2bits(KT * h2s(hfrom(kHUnscale))), 0u);
+                }
+                c.w = (uint32_t)hbits((h16)(float)dx_) | ((uint32_t)hbits((h16)(float)dy_) << 16);
+                s_pair[w][half][i][0] = a;
+                s_pair[w][half][i][1] = c;
+            }
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+        // ---- the pipeline (:1194-1355)
+        h16x2 a_mx = h2s((h16)0.f), a_my = a_mx, a_ax = a_mx, a_ay = a_mx, a_cx = a_mx, a_cy = a_mx, a_cz = a_mx;
+        h16x2 a_op = a_mx, a_r = a_mx, a_g = a_mx, a_b = a_mx;
+        uint32_t st[8];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) st[q] = 0u;
+        const uint32_t cmax = max(readlane_u32(cnt, 0), readlane_u32(cnt, 32));
+        const uint32_t steps = cmax ? 128u + cmax - 1u : 0u;
+        for (uint32_t s = 0; s < steps; ++s) {
+            if (l == 0 && s < 128u) {   // lanes 0 and 32 take the next pair
+                const uint4 a = s_pair[w][half][s][0], c = s_pair[w][half][s][1];
+                st[0] = a.x; st[1] = a.y; st[2] = a.z; st[3] = a.w;
+                st[4] = c.x; st[5] = c.y; st[6] = c.z; st[7] = c.w;
+            }
+            if (s - l < 128u && l < cnt) {
+                const h16x2 G0 = h2from(st[0]), G1 = h2from(st[1]), G2 = h2from(st[2]);
+                h16x2 Ca0 = h2from(st[3]), Ca1 = h2from(st[4]), Ca2 = h2from(st[5]);
+                const h16x2 T = h2from(st[6]);
+                const h16x2 off = h2from(st[7]);
+                const h16x2 offx = h2s(off.x), offy = h2s(off.y);
+                const h16x2 dlx = h2_fma(inv16, -offx, mxp);
+                const h16x2 dly = h2_fma(inv16, -offy, my2);
+                const h16x2 cx_dx = cx2 * dlx, cy_dx = cy2 * dlx, cz_dy = cz2 * dly, cy_dy = cy2 * dly;
+                const h16x2 cz_dyy = dly * cz_dy, cy_dxy = dlx * cy_dy;
+                const h16x2 quad = h2_fma(dlx, cx_dx, cz_dyy);
+                const h16x2 s2 = h2_relu(h2_fma(h05, quad, cy_dxy)) * h16c;
+                const h16x2 prep_x = cx_dx + cy_dy;
+                const h16x2 gss = h2_exp2(s2 * nlog2e);
+                const h16x2 prep_y = cy_dx + cz_dy;
+                const h16x2 alpha_p = o2 * gss;
+                const h16x2 cdg = h2_fma(cr2, G0, h2_fma(cg2, G1, cb2 * G2));
+                const h16x2 alpha = h2_min(alpha_p, maxa);
+                const h16x2 bw = T * alpha;
+                const h16x2 oma = one - alpha;
+                a_r = h2_fma(bw, G0, a_r);
+                a_g = h2_fma(bw, G1, a_g);
+                a_b = h2_fma(bw, G2, a_b);
+                Ca0 = h2_fma(-bw, cr2, Ca0);
+                Ca1 = h2_fma(-bw, cg2, Ca1);
+                Ca2 = h2_fma(-bw, cb2, Ca2);
+                const h16x2 cadg = h2_fma(Ca0, G0, h2_fma(Ca1, G1, Ca2 * G2));
+                const h16x2 dal = h2_fma(T, cdg, -h2_div(cadg, oma));
+                const h16x2 part = alpha * dal;
+                a_op = part + a_op;
+                const h16x2 dxdx = dlx * dlx, dxdy = dlx * dly, dydy = dly * dly;
+                a_cx = part * dxdx + a_cx;
+                a_cy = part * dxdy + a_cy;
+                a_cz = part * dydy + a_cz;
+                const h16x2 nT = T * oma;
+                const h16x2 dmx = part * prep_x, dmy = part * prep_y;
+                a_mx = dmx + a_mx;
+                a_my = dmy + a_my;
+                a_ax = h2from(h2bits(dmx) & 0x7fff7fffu) + a_ax;
+                a_ay = h2from(h2bits(dmy) & 0x7fff7fffu) + a_ay;
+                st[3] = h2bits(Ca0);
+                st[4] = h2bits(Ca1);
+                st[5] = h2bits(Ca2);
+                st[6] = h2bits(nT);
+            }
+#pragma unroll
+            for (int q = 0; q < 8; ++q) st[q] = shr1(st[q]);
+        }
+
+        // ---- the bucket's record (:1357-1387), rounded as the reference's atomics receive it
+        if (l < cnt) {
+            auto sum = [](h16x2 v) { return (float)v.x + (float)v.y; };
+            float4* dst = records + 3 * (size_t)slot;
+            const float o = (float)o2.x;
+            dst[0] = make_float4((float)h_rn(-sum(a_mx) / 255.0f), (float)h_rn(-sum(a_my) / 255.0f),
+                                 (float)h_rn(sum(a_ax) / 255.0f), (float)h_rn(sum(a_ay) / 255.0f));
+            dst[1] = make_float4((float)h_rn(-128.0f * sum(a_cx) / 255.0f), (float)h_rn(-128.0f * sum(a_cy) / 255.0f),
+                                 (float)h_rn(-128.0f * sum(a_cz) / 255.0f), (float)h_rn(sum(a_r)));
+            // [11]: the instance index (bits), for tests; the sums do not read it
+            dst[2] = make_float4((float)h_rn(sum(a_g)), (float)h_rn(sum(a_b)), (sum(a_op) / 255.0f) * (1.0f - o),
+                                 u2f(first + l));
+        }
+        next = (uint32_t)__builtin_amdgcn_readfirstlane((int)after);
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    }
+}
+
+static int g_blocks16 = 0;
+
+void launch_blend16_backward(const CamParams& cam, const uint32_t* inst_vals, const float2* mean2d,
+                             const uint4* info, const uint16_t* image, const uint16_t* grad_image, const uint2* ckpt,
+                             const uint4* items, BinCtl* ctl, uint32_t* rec_count, const uint32_t* first_slot,
+                             float4* records, hipStream_t s) {
+    const uint32_t n_tiles = cam.grid_w * cam.grid_h;
+    if (n_tiles == 0) return;
+    if (g_blocks16 <= 0) {
+        int dev = 0, cus = 0, per_cu = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+            cus = 256;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, blend16_backward_kernel, 256, 0) != hipSuccess ||
+            per_cu <= 0)
+            per_cu = 4;
+        g_blocks16 = cus * per_cu;
+    }
+    blend16_backward_kernel<<<(uint32_t)g_blocks16, 256, 0, s>>>(cam, inst_vals, mean2d, info, image, grad_image,
+                                                                  ckpt, items, ctl, rec_count, first_slot, records);
+}
+
+}  // namespace tgs

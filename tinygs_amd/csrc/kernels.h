@@ -100,13 +100,34 @@ int radix_sort(uint32_t* keys[2], uint32_t* vals[2], uint32_t* v2[2], const uint
 // that would need them set bit 1 of ctl->err.
 void launch_emit_instances(const uint32_t* prims, const uint32_t* offs, BinCtl* ctl, int64_t max_count,
                            int64_t max_inst, const uint4* rec, const uint32_t* tile_bits, uint32_t grid_w,
-                           uint32_t* inst_keys, uint32_t* inst_vals, uint32_t* first_slot, hipStream_t s);
+                           uint32_t* inst_keys, uint32_t* inst_vals, uint32_t* first_slot, bool half_test,
+                           hipStream_t s);
 // [start, end) per tile, (0, 0) for empty tiles; every entry written. The
 // instance count is min(*d_n, max_inst) (max_inst when d_n is null).
 void launch_tile_ranges(const uint32_t* inst_keys, const uint32_t* d_n, int64_t max_inst, uint2* ranges,
                         uint32_t n_tiles, hipStream_t s);
 // Whether radix_sort accepts these digit widths (host check, before any launch).
 bool radix_digits_fit(bool depth, int n_passes, const int* bits);
+
+// ---- fp16-image rasterizer (FGS16, tinygs/src/rasterizer/fastgs_ours_fp16/)
+// Preprocess: as launch_preprocess with the FGS16 rules; info[i] = (conic a | b
+// << 16, c | opacity << 16 (halves), r | g << 8 | b << 16, 0).
+void launch_preprocess16(const GaussianView& g, const CamParams& cam, uint32_t* n_touched, uint32_t* tile_bits,
+                         uint4* rec, float2* mean2d, float4* conic_opacity, uint4* info, uint32_t* depth_key,
+                         float* densif, hipStream_t s);
+
+// Blend of FGS16 (fgs16.hip): image / grad image are 3 half planes of the
+// padded 8x8-tiled layout, n_contrib u16 per pixel, ckpt 256 uint2 per slot
+// (the fp32 path's slots), items as the fp32 path's but with every Gaussian of
+// the bucket; records as the fp32 path's, half mode.
+void launch_blend16_forward(const CamParams& cam, const uint2* ranges, const uint32_t* inst_vals,
+                            const float2* mean2d, const uint4* info, uint16_t* image, uint16_t* n_contrib,
+                            uint32_t* tile_max, uint32_t* tile_loaded, uint2* ckpt, uint4* items, BinCtl* ctl,
+                            hipStream_t s);
+void launch_blend16_backward(const CamParams& cam, const uint32_t* inst_vals, const float2* mean2d,
+                             const uint4* info, const uint16_t* image, const uint16_t* grad_image, const uint2* ckpt,
+                             const uint4* items, BinCtl* ctl, uint32_t* rec_count, const uint32_t* first_slot,
+                             float4* records, hipStream_t s);
 
 // ---- blend (kernels_forward.cuh:569-715, kernels_backward.cuh:675-927)
 // Checkpoints: the state (C, T) of every pixel before Gaussian 32 b of its
@@ -149,7 +170,7 @@ void launch_preprocess_backward(const GaussianView& g, const CamParams& cam, con
                                 const float4* conic_opacity, uint32_t* rec_count, const uint32_t* first_slot,
                                 const float4* records, float* grad2d, const GradView& out, float* densif, int mode,
                                 uint8_t* row_mask, uint4* live, uint4* heavy, uint2* chunk_counts,
-                                float* pose_partial, float* pose_out, bool keep2d, hipStream_t s);
+                                float* pose_partial, float* pose_out, bool keep2d, bool half_sums, hipStream_t s);
 
 // ---- PSNR (psnr.cu:72-128): scratch[psnr_scratch_doubles() - 1] receives the
 // sum of (saturate(pred) - target)^2 over the n_padded elements
@@ -227,6 +248,8 @@ void launch_adam(const AdamArgs& a, hipStream_t s);
 void launch_detmath(int op, const float* in, float* out, int64_t n, hipStream_t s);
 void launch_wave_selftest(const uint32_t* in, uint32_t* out, hipStream_t s);
 // canonical half operation `op` (tests): out[i] = op(a[i], b[i], c[i]) as bits
+// out[8] (zeroed by the caller): mismatches, pairs checked, a / b / q of one mismatch
+void launch_half_div_check(unsigned long long* out, hipStream_t s);
 void launch_halfmath(int op, const uint16_t* a, const uint16_t* b, const uint16_t* c, uint16_t* out, int64_t n,
                      hipStream_t s);
 

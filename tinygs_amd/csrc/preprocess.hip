@@ -15,6 +15,7 @@
 // bounds and tile counts are bit-identical to it.
 #include "common.h"
 #include "kernels.h"
+#include "fgs16.h"
 
 namespace tgs {
 
@@ -259,6 +260,220 @@ __global__ void __launch_bounds__(256) preprocess_kernel(
     sh_to_color(sh0, s_sh + 45 * threadIdx.x, i, mx, my, mz, cam, bases, col);
     color_pt[i] = make_float4(col[0], col[1], col[2], pthr);
     depth_key[i] = f2u(depth);
+}
+
+// preprocess_cu of the fp16-image rasterizer (FGS16), tinygs/src/rasterizer/
+// fastgs_ours_fp16/kernels_forward.cuh:249-500: the fp32 projection with the
+// logit rounded to half before the sigmoid (and read only for primitives
+// still in [near, far]), the quaternion read only for active primitives, a
+// half conic and opacity, the power threshold from the half opacity, the
+// half tile test (fgs16.h) and an 8-bit colour, saturate(c) * 255 truncated
+// (rasterization_config.h:104-108). Outputs: n_touched, tile_bits and the
+// binning record as the fp32 preprocess (conic and opacity halves in the
+// record's second half), mean2d, conic_opacity (the halves as floats) and
+// info[i] = (a | b << 16, c | opacity << 16, r | g << 8 | b << 16, 0).
+template <typename ShT>
+__global__ void __launch_bounds__(256) preprocess16_kernel(
+    const float* __restrict__ means, const float* __restrict__ scales, const float* __restrict__ rots,
+    const float* __restrict__ opac, const ShT* __restrict__ sh0, const ShT* __restrict__ shr, int64_t n, int bases,
+    CamParams cam, uint32_t* __restrict__ n_touched, uint32_t* __restrict__ tile_bits, uint4* __restrict__ rec,
+    float2* __restrict__ mean2d, float4* __restrict__ conic_opacity, uint4* __restrict__ info,
+    uint32_t* __restrict__ depth_key, float4* __restrict__ densif) {
+    __shared__ __align__(16) ShT s_sh[256 * 45];
+    {
+        const int64_t blk0 = (int64_t)blockIdx.x * 256;
+        const int nblk = (int)min((int64_t)256, n - blk0);
+        if (bases > 1) {
+            const int count = nblk * 45;
+            const int nvec = (count * (int)sizeof(ShT)) >> 4;
+            const uint4* s4 = (const uint4*)(shr + blk0 * 45);
+            uint4* d4 = (uint4*)s_sh;
+            for (int v = (int)threadIdx.x; v < nvec; v += 256) d4[v] = s4[v];
+            for (int e = (nvec << 4) / (int)sizeof(ShT) + (int)threadIdx.x; e < count; e += 256)
+                s_sh[e] = shr[blk0 * 45 + e];
+        }
+        __syncthreads();
+    }
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    bool active = i < n;
+    const int64_t ii = active ? i : n - 1;
+    const uint32_t lane = lane_id();
+
+    const float mx = means[3 * ii], my = means[3 * ii + 1], mz = means[3 * ii + 2];
+    const float depth = cam.r3[0] * mx + cam.r3[1] * my + cam.r3[2] * mz + cam.r3[3];
+    if (depth < cam.near_ || depth > cam.far_) active = false;
+    const h16 raw_o = active ? h_rn(opac[ii]) : (h16)0.0f;
+    const float f_opacity = 1.0f / (1.0f + det_expf(-(float)raw_o));
+    if (f_opacity < kMinAlpha) active = false;
+    const h16 opacity = h_rn(f_opacity);
+    const float e0 = det_expf(scales[3 * ii]), e1 = det_expf(scales[3 * ii + 1]), e2 = det_expf(scales[3 * ii + 2]);
+    const float vx = e0 * e0, vy = e1 * e1, vz = e2 * e2;
+    float qr = 0.f, qx = 0.f, qy = 0.f, qz = 0.f;
+    if (active) {
+        qr = rots[4 * ii];
+        qx = rots[4 * ii + 1];
+        qy = rots[4 * ii + 2];
+        qz = rots[4 * ii + 3];
+    }
+    const float qrr = qr * qr, qxx_r = qx * qx, qyy_r = qy * qy, qzz_r = qz * qz;
+    const float qn = qrr + qxx_r + qyy_r + qzz_r;
+    if (qn < 1e-8f) active = false;
+    // the reference's 32-lane warps: radius folding per 32-primitive group (kernels_forward.cuh:326-329,405-411)
+    const uint64_t live = ballot(active);
+    const bool radius = densif != nullptr && i < n && (lane < 32u ? (uint32_t)live : (uint32_t)(live >> 32)) != 0u;
+
+    uint32_t xmin = 0, xmax = 0, ymin = 0, ymax = 0, nmax = 0;
+    float m2x = 0.f, m2y = 0.f, pthr = 0.f;
+    h16 hca = (h16)0.f, hcb = (h16)0.f, hcc = (h16)0.f;
+    if (active || radius) {
+        const float qxx = 2.0f * qxx_r / qn, qyy = 2.0f * qyy_r / qn, qzz = 2.0f * qzz_r / qn;
+        const float qxy = 2.0f * qx * qy / qn, qxz = 2.0f * qx * qz / qn, qyz = 2.0f * qy * qz / qn;
+        const float qrx = 2.0f * qr * qx / qn, qry = 2.0f * qr * qy / qn, qrz = 2.0f * qr * qz / qn;
+        const float R11 = 1.0f - (qyy + qzz), R12 = qxy - qrz, R13 = qry + qxz;
+        const float R21 = qrz + qxy, R22 = 1.0f - (qxx + qzz), R23 = qyz - qrx;
+        const float R31 = qxz - qry, R32 = qrx + qyz, R33 = 1.0f - (qxx + qyy);
+        const float S11 = R11 * vx, S12 = R12 * vy, S13 = R13 * vz;
+        const float S21 = R21 * vx, S22 = R22 * vy, S23 = R23 * vz;
+        const float S31 = R31 * vx, S32 = R32 * vy, S33 = R33 * vz;
+        const float c11 = S11 * R11 + S12 * R12 + S13 * R13;
+        const float c12 = S11 * R21 + S12 * R22 + S13 * R23;
+        const float c13 = S11 * R31 + S12 * R32 + S13 * R33;
+        const float c22 = S21 * R21 + S22 * R22 + S23 * R23;
+        const float c23 = S21 * R31 + S22 * R32 + S23 * R33;
+        const float c33 = S31 * R31 + S32 * R32 + S33 * R33;
+        const float x = (cam.r1[0] * mx + cam.r1[1] * my + cam.r1[2] * mz + cam.r1[3]) / depth;
+        const float y = (cam.r2[0] * mx + cam.r2[1] * my + cam.r2[2] * mz + cam.r2[3]) / depth;
+        const float clip_left = (-0.15f * cam.w - cam.cx) / cam.fx;
+        const float clip_right = (1.15f * cam.w - cam.cx) / cam.fx;
+        const float clip_top = (-0.15f * cam.h - cam.cy) / cam.fy;
+        const float clip_bottom = (1.15f * cam.h - cam.cy) / cam.fy;
+        const float tx = __builtin_fmaxf(clip_left, __builtin_fminf(x, clip_right));
+        const float ty = __builtin_fmaxf(clip_top, __builtin_fminf(y, clip_bottom));
+        const float j11 = cam.fx / depth, j13 = -j11 * tx, j22 = cam.fy / depth, j23 = -j22 * ty;
+        const float jw1x = j11 * cam.r1[0] + j13 * cam.r3[0], jw1y = j11 * cam.r1[1] + j13 * cam.r3[1],
+                    jw1z = j11 * cam.r1[2] + j13 * cam.r3[2];
+        const float jw2x = j22 * cam.r2[0] + j23 * cam.r3[0], jw2y = j22 * cam.r2[1] + j23 * cam.r3[1],
+                    jw2z = j22 * cam.r2[2] + j23 * cam.r3[2];
+        const float a1x = jw1x * c11 + jw1y * c12 + jw1z * c13;
+        const float a1y = jw1x * c12 + jw1y * c22 + jw1z * c23;
+        const float a1z = jw1x * c13 + jw1y * c23 + jw1z * c33;
+        const float a2x = jw2x * c11 + jw2y * c12 + jw2z * c13;
+        const float a2y = jw2x * c12 + jw2y * c22 + jw2z * c23;
+        const float a2z = jw2x * c13 + jw2y * c23 + jw2z * c33;
+        float cv_a = a1x * jw1x + a1y * jw1y + a1z * jw1z;
+        const float cv_b = a1x * jw2x + a1y * jw2y + a1z * jw2z;
+        float cv_c = a2x * jw2x + a2y * jw2y + a2z * jw2z;
+        cv_a += kDilation;
+        cv_c += kDilation;
+        const float det = cv_a * cv_c - cv_b * cv_b;
+        if (det < 1e-8f) active = false;
+        if (radius) {
+            const float mid = 0.5f * (cv_a + cv_c);
+            const float l1 = mid + __builtin_sqrtf(__builtin_fmaxf(0.1f, mid * mid - det));
+            const float l2 = mid - __builtin_sqrtf(__builtin_fmaxf(0.1f, mid * mid - det));
+            const float rad = __builtin_ceilf(3.0f * __builtin_sqrtf(__builtin_fmaxf(l1, l2)));
+            const float old = densif[ii].w;
+            const float nv = __builtin_fmaxf(old, rad);
+            if (f2u(nv) != f2u(old)) densif[ii].w = nv;
+        }
+        if (active) {
+            const float ca = cv_c / det, cb = -cv_b / det, cc = cv_a / det;
+            m2x = x * cam.fx + cam.cx;
+            m2y = y * cam.fy + cam.cy;
+            hca = h_rn(ca);
+            hcb = h_rn(cb);
+            hcc = h_rn(cc);
+            pthr = det_logf((float)opacity * 255.0f);
+            const float pfac = __builtin_sqrtf(2.0f * pthr);
+            const float ext_x = __builtin_fmaxf(pfac * __builtin_sqrtf(cv_a) - 0.5f, 0.0f);
+            const float ext_y = __builtin_fmaxf(pfac * __builtin_sqrtf(cv_c) - 0.5f, 0.0f);
+            const int32_t bx0 = sat_floor_i32((m2x - ext_x) / 16.0f);
+            const int32_t bx1 = sat_ceil_i32((m2x + ext_x) / 16.0f);
+            const int32_t by0 = sat_floor_i32((m2y - ext_y) / 16.0f);
+            const int32_t by1 = sat_ceil_i32((m2y + ext_y) / 16.0f);
+            xmin = min((uint32_t)max(bx0, 0), cam.grid_w);
+            xmax = min((uint32_t)max(bx1, 0), cam.grid_w);
+            ymin = min((uint32_t)max(by0, 0), cam.grid_h);
+            ymax = min((uint32_t)max(by1, 0), cam.grid_h);
+            nmax = (xmax - xmin) * (ymax - ymin);
+            if (nmax == 0) active = false;
+        }
+    }
+
+    const float smx = m2x - 0.5f, smy = m2y - 0.5f;
+    const uint32_t bw = xmax - xmin;
+    uint32_t cnt = 0, bits = 0;
+    if (active) {
+        const uint32_t first = nmax < 8u ? nmax : 8u;
+        for (uint32_t k = 0; k < first; ++k) {
+            const bool hit = will_contribute_half(smx, smy, hca, hcb, hcc, xmin + k % bw, ymin + k / bw, pthr);
+            cnt += hit ? 1u : 0u;
+            bits |= hit ? (1u << k) : 0u;
+        }
+    }
+    uint64_t coop = ballot(active && nmax > 8u);
+    while (coop) {
+        const uint32_t src = (uint32_t)__builtin_ctzll(coop);
+        coop &= coop - 1;
+        const float s_mx = readlane_f32(smx, src), s_my = readlane_f32(smy, src);
+        const uint32_t s_c01 = readlane_u32((uint32_t)hbits(hca) | ((uint32_t)hbits(hcb) << 16), src);
+        const h16 s_a = hfrom((uint16_t)(s_c01 & 0xffffu)), s_b = hfrom((uint16_t)(s_c01 >> 16));
+        const h16 s_c = hfrom((uint16_t)readlane_u32((uint32_t)hbits(hcc), src));
+        const float s_t = readlane_f32(pthr, src);
+        const uint32_t s_x0 = readlane_u32(xmin, src), s_y0 = readlane_u32(ymin, src);
+        const uint32_t s_bw = readlane_u32(bw, src), s_n = readlane_u32(nmax, src);
+        uint32_t c = 0, b32 = 0;
+        for (uint32_t base = 8u; base < s_n; base += kWave) {
+            const uint32_t k = base + lane;
+            bool hit = false;
+            if (k < s_n) hit = will_contribute_half(s_mx, s_my, s_a, s_b, s_c, s_x0 + k % s_bw, s_y0 + k / s_bw, s_t);
+            const uint64_t hm = ballot(hit);
+            if (base == 8u) b32 = (uint32_t)(hm & 0xffffffu) << 8;
+            c += (uint32_t)__builtin_popcountll(hm);
+        }
+        if (lane == src) {
+            cnt += c;
+            bits |= b32;
+        }
+    }
+
+    if (i >= n) return;
+    if (!active || cnt == 0) {
+        n_touched[i] = 0;
+        return;
+    }
+    n_touched[i] = cnt;
+    tile_bits[i] = bits;
+    const uint32_t c01 = (uint32_t)hbits(hca) | ((uint32_t)hbits(hcb) << 16);
+    const uint32_t c2o = (uint32_t)hbits(hcc) | ((uint32_t)hbits(opacity) << 16);
+    rec[2 * i] = make_uint4(xmin | (xmax << 16), ymin | (ymax << 16), f2u(m2x), f2u(m2y));
+    rec[2 * i + 1] = make_uint4(c01, c2o, 0u, f2u(pthr));
+    mean2d[i] = make_float2(m2x, m2y);
+    conic_opacity[i] = make_float4((float)hca, (float)hcb, (float)hcc, (float)opacity);
+    float col[3];
+    sh_to_color(sh0, s_sh + 45 * threadIdx.x, i, mx, my, mz, cam, bases, col);
+    uint32_t rgb = 0;
+    for (int c = 0; c < 3; ++c) rgb |= (uint32_t)(uint8_t)(saturate(col[c]) * 255.0f) << (8 * c);
+    info[i] = make_uint4(c01, c2o, rgb, 0u);
+    depth_key[i] = f2u(depth);
+}
+
+void launch_preprocess16(const GaussianView& g, const CamParams& cam, uint32_t* n_touched, uint32_t* tile_bits,
+                         uint4* rec, float2* mean2d, float4* conic_opacity, uint4* info, uint32_t* depth_key,
+                         float* densif, hipStream_t s) {
+    if (g.n <= 0) return;
+    const int bases = (g.sh_degree + 1) * (g.sh_degree + 1);
+    const unsigned grid = (unsigned)((g.n + 255) / 256);
+    if (g.sh_dtype == kShF16)
+        preprocess16_kernel<__half><<<grid, 256, 0, s>>>(g.means, g.scales, g.rotations, g.opacities,
+                                                         (const __half*)g.sh0, (const __half*)g.sh_rest, g.n, bases,
+                                                         cam, n_touched, tile_bits, rec, mean2d, conic_opacity, info,
+                                                         depth_key, (float4*)densif);
+    else
+        preprocess16_kernel<float><<<grid, 256, 0, s>>>(g.means, g.scales, g.rotations, g.opacities,
+                                                        (const float*)g.sh0, (const float*)g.sh_rest, g.n, bases, cam,
+                                                        n_touched, tile_bits, rec, mean2d, conic_opacity, info,
+                                                        depth_key, (float4*)densif);
 }
 
 void launch_preprocess(const GaussianView& g, const CamParams& cam, uint32_t* n_touched, uint32_t* tile_bits,

@@ -12,12 +12,23 @@
 // (sum of alpha * dL/dalpha) * (1 - opacity) (:921-922); the blend backward
 // leaves the sum in its 2D-gradient records and it is applied here.
 //
+// The fp16-image rasterizer (FGS16, fastgs_ours_fp16/kernels_backward.cuh:
+// 93-405) runs the same chain on half 2D gradients: its records hold half
+// values (as floats) and the opacity-logit gradient with (1 - opacity)
+// already applied per bucket (:1380). Half mode (kHalf) sums the half fields
+// exactly, as integers in units of 2^-24 (every finite half is a multiple),
+// and rounds each sum to half once (half_of_fixed); infinities and NaNs are
+// tracked apart. The reference adds them with half2 atomics, whose rounding
+// depends on the order the buckets finish in; the exact sum is the same for
+// every order. The opacity gradient is summed in double and rounded to float.
+//
 // Only primitives that some tile's blend backward reached (a nonzero record
 // count) run the chain; for the other visible ones every gradient is exactly
 // zero, so their parameters are never read (at 1M Gaussians most visible
 // primitives sit behind others and fall in this class). SH-rest parameter
 // rows are read per thread, and only for primitives with gradients.
 #include "common.h"
+#include "halfmath.h"
 #include "kernels.h"
 
 namespace tgs {
@@ -248,6 +259,49 @@ __device__ __forceinline__ void preprocess_backward_one(
     }
 }
 
+// ---- exact sums of half records (half mode)
+struct HalfSums {
+    int64_t s[10];
+    uint32_t fl;   // per field q, bits 3q..3q+2: +inf, -inf, NaN seen
+    double op;
+};
+
+__device__ __forceinline__ void hs_zero(HalfSums& h) {
+#pragma unroll
+    for (int q = 0; q < 10; ++q) h.s[q] = 0;
+    h.fl = 0u;
+    h.op = 0.0;
+}
+
+__device__ __forceinline__ void hs_add(HalfSums& h, const float4& a, const float4& b, const float4& c) {
+    const float v[10] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w, c.x, c.y};
+#pragma unroll
+    for (int q = 0; q < 10; ++q) {
+        const float x = v[q];
+        if (x != x)
+            h.fl |= 4u << (3 * q);
+        else if (__builtin_isinf(x))
+            h.fl |= (x > 0.f ? 1u : 2u) << (3 * q);
+        else
+            h.s[q] += (int64_t)(x * 16777216.0f);   // exact: a half times 2^24 is an integer below 2^40
+    }
+    h.op += (double)c.z;
+}
+
+__device__ __forceinline__ float hs_value(const HalfSums& h, int q) {
+    const uint32_t f = (h.fl >> (3 * q)) & 7u;
+    if ((f & 4u) || f == 3u) return __builtin_nanf("");
+    if (f & 1u) return __builtin_inff();
+    if (f & 2u) return -__builtin_inff();
+    return half_of_fixed(h.s[q]);
+}
+
+__device__ __forceinline__ void hs_result(const HalfSums& h, float4& gA, float4& gB, float4& gC) {
+    gA = make_float4(hs_value(h, 0), hs_value(h, 1), hs_value(h, 2), hs_value(h, 3));
+    gB = make_float4(hs_value(h, 4), hs_value(h, 5), hs_value(h, 6), hs_value(h, 7));
+    gC = make_float4(hs_value(h, 8), hs_value(h, 9), (float)h.op, 0.f);
+}
+
 // ---- phase 1: classify every primitive, list the live ones
 //
 // Chunk of 2048 consecutive primitives per workgroup (8 striped rounds of
@@ -334,6 +388,7 @@ __global__ void __launch_bounds__(256) preprocess_backward_classify_kernel(
 // wave: the lanes stride over the primitive's records, then a row
 // butterfly leaves the 12 sums in every lane of the row and lanes 0-2 of
 // the row store them to grad2d[12 p] in record layout.
+template <bool kHalf>
 __global__ void __launch_bounds__(256) gather_heavy_kernel(const uint4* __restrict__ heavy,
                                                            const uint2* __restrict__ chunk_counts,
                                                            const float4* __restrict__ records,
@@ -345,6 +400,30 @@ __global__ void __launch_bounds__(256) gather_heavy_kernel(const uint4* __restri
         const uint32_t h = h0 + row;
         const bool on = h < nh;
         const uint4 e = on ? list[h] : make_uint4(0u, 0u, 0u, 0u);
+        if constexpr (kHalf) {
+            HalfSums hs;
+            hs_zero(hs);
+            for (uint32_t r = sub; r < e.y; r += 16u) {
+                const float4* src = records + 3 * (size_t)(e.z + r);
+                hs_add(hs, src[0], src[1], src[2]);
+            }
+            // exact integer sums and flag unions over the 16 lanes of the row
+            for (int m = 8; m >= 1; m >>= 1) {
+#pragma unroll
+                for (int q = 0; q < 10; ++q) hs.s[q] += __shfl_xor(hs.s[q], m, 16);
+                hs.fl |= (uint32_t)__shfl_xor((int)hs.fl, m, 16);
+                hs.op += __shfl_xor(hs.op, m, 16);
+            }
+            if (on && sub == 0u) {
+                float4 gA, gB, gC;
+                hs_result(hs, gA, gB, gC);
+                float4* g = (float4*)(grad2d + (size_t)e.x * kGradStride);
+                g[0] = gA;
+                g[1] = gB;
+                g[2] = gC;
+            }
+            continue;
+        }
         float v[12];
 #pragma unroll
         for (int q = 0; q < 12; ++q) v[q] = 0.f;
@@ -417,7 +496,7 @@ __device__ __forceinline__ void load_sh_row<__half>(const __half* __restrict__ s
 // sums dL/dmean_cam[k] * (mean, 1) over its primitives, and the workgroup's
 // sum of those 12 numbers goes to pose_partial[12 * chunk] (every workgroup
 // writes its slot, zero when it has no live primitive), in a fixed order.
-template <typename ShT, bool kPose>
+template <typename ShT, bool kPose, bool kHalf>
 __global__ void __launch_bounds__(256) preprocess_backward_live_kernel(
     const float* __restrict__ means, const float* __restrict__ scales, const float* __restrict__ rots,
     const ShT* __restrict__ shr_all, int bases, CamParams cam, const float4* __restrict__ conic_opacity,
@@ -443,6 +522,12 @@ __global__ void __launch_bounds__(256) preprocess_backward_live_kernel(
             gA = *(const float4*)(gr);
             gB = *(const float4*)(gr + 4);
             gC = *(const float4*)(gr + 8);
+        } else if constexpr (kHalf) {
+            const float4* rec = records + 3 * (size_t)e.z;
+            HalfSums hs;
+            hs_zero(hs);
+            for (uint32_t r = 0; r < nr; ++r) hs_add(hs, rec[3 * r], rec[3 * r + 1], rec[3 * r + 2]);
+            hs_result(hs, gA, gB, gC);
         } else {
             const float4* rec = records + 3 * (size_t)e.z;
             for (uint32_t r = 0; r < nr; ++r) {
@@ -467,7 +552,8 @@ __global__ void __launch_bounds__(256) preprocess_backward_live_kernel(
         }
 #pragma unroll
         for (int c = 0; c < 4; ++c) pq[c] = rots[4 * ip + c];
-        const float opacity = conic_opacity[ip].w;
+        // half mode: the records carry (1 - opacity) already
+        const float opacity = kHalf ? 0.0f : conic_opacity[ip].w;
         load_sh_row<ShT>(shr_all, ip, nsh, s_win + kShWin * t, shv);
         PrimGrad pg;
         float gc[3], k[15];
@@ -577,17 +663,22 @@ template <typename ShT, bool kPose>
 static void launch_live(const GaussianView& g, int bases, const CamParams& cam, const float4* conic_opacity,
                         uint32_t* rec_count, const float4* records, float* grad2d, const GradView& out,
                         float* densif, int mode, const uint4* live, const uint2* chunk_counts, float* pose_partial,
-                        bool keep2d, unsigned chunks, hipStream_t s) {
-    preprocess_backward_live_kernel<ShT, kPose><<<chunks, 256, 0, s>>>(
-        g.means, g.scales, g.rotations, (const ShT*)g.sh_rest, bases, cam, conic_opacity, rec_count, records, grad2d,
-        out, (float4*)densif, mode, live, chunk_counts, pose_partial, keep2d ? grad2d : nullptr);
+                        bool keep2d, bool half_sums, unsigned chunks, hipStream_t s) {
+    if (half_sums)
+        preprocess_backward_live_kernel<ShT, kPose, true><<<chunks, 256, 0, s>>>(
+            g.means, g.scales, g.rotations, (const ShT*)g.sh_rest, bases, cam, conic_opacity, rec_count, records,
+            grad2d, out, (float4*)densif, mode, live, chunk_counts, pose_partial, keep2d ? grad2d : nullptr);
+    else
+        preprocess_backward_live_kernel<ShT, kPose, false><<<chunks, 256, 0, s>>>(
+            g.means, g.scales, g.rotations, (const ShT*)g.sh_rest, bases, cam, conic_opacity, rec_count, records,
+            grad2d, out, (float4*)densif, mode, live, chunk_counts, pose_partial, keep2d ? grad2d : nullptr);
 }
 
 void launch_preprocess_backward(const GaussianView& g, const CamParams& cam, const uint32_t* n_touched,
                                 const float4* conic_opacity, uint32_t* rec_count, const uint32_t* first_slot,
                                 const float4* records, float* grad2d, const GradView& out, float* densif, int mode,
                                 uint8_t* row_mask, uint4* live, uint4* heavy, uint2* chunk_counts,
-                                float* pose_partial, float* pose_out, bool keep2d, hipStream_t s) {
+                                float* pose_partial, float* pose_out, bool keep2d, bool half_sums, hipStream_t s) {
     if (g.n <= 0) {
         if (pose_out) launch_fill_u32((uint32_t*)pose_out, 0u, 16, s);
         return;
@@ -598,22 +689,25 @@ void launch_preprocess_backward(const GaussianView& g, const CamParams& cam, con
     preprocess_backward_classify_kernel<<<chunks, 256, 0, s>>>(g.n, n_touched, rec_count, first_slot,
                                                                (float4*)densif, mode, row_mask, out, live, heavy,
                                                                chunk_counts);
-    gather_heavy_kernel<<<chunks, 256, 0, s>>>(heavy, chunk_counts, records, grad2d);
+    if (half_sums)
+        gather_heavy_kernel<true><<<chunks, 256, 0, s>>>(heavy, chunk_counts, records, grad2d);
+    else
+        gather_heavy_kernel<false><<<chunks, 256, 0, s>>>(heavy, chunk_counts, records, grad2d);
     const bool f16 = g.sh_dtype == kShF16;
     if (pose_out) {
         if (f16)
             launch_live<__half, true>(g, bases, cam, conic_opacity, rec_count, records, grad2d, out, densif, mode, live,
-                                      chunk_counts, pose_partial, keep2d, chunks, s);
+                                      chunk_counts, pose_partial, keep2d, half_sums, chunks, s);
         else
             launch_live<float, true>(g, bases, cam, conic_opacity, rec_count, records, grad2d, out, densif, mode, live,
-                                     chunk_counts, pose_partial, keep2d, chunks, s);
+                                     chunk_counts, pose_partial, keep2d, half_sums, chunks, s);
         pose_reduce_kernel<<<1, 256, 0, s>>>(pose_partial, (int64_t)chunks, pose_out);
     } else if (f16) {
         launch_live<__half, false>(g, bases, cam, conic_opacity, rec_count, records, grad2d, out, densif, mode, live,
-                                   chunk_counts, nullptr, keep2d, chunks, s);
+                                   chunk_counts, nullptr, keep2d, half_sums, chunks, s);
     } else {
         launch_live<float, false>(g, bases, cam, conic_opacity, rec_count, records, grad2d, out, densif, mode, live,
-                                  chunk_counts, nullptr, keep2d, chunks, s);
+                                  chunk_counts, nullptr, keep2d, half_sums, chunks, s);
     }
 }
 

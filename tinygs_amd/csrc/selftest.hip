@@ -69,7 +69,9 @@ void launch_wave_selftest(const uint32_t* in, uint32_t* out, hipStream_t s) {
 namespace tgs {
 
 // Canonical half operations on element i: a, b, c are half bit patterns
-// (op 7, 8: a holds floats), out receives the result's bits.
+// (op 7, 8: a holds floats; op 11: a holds int64), out receives the result's
+// bits. Op 12 checks the lane layout of DPP wave_shr:1 (whole waves: n a
+// multiple of 64).
 __global__ void halfmath_kernel(int op, const uint16_t* a, const uint16_t* b, const uint16_t* c, uint16_t* out,
                                 int64_t n) {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -91,6 +93,13 @@ __global__ void halfmath_kernel(int op, const uint16_t* a, const uint16_t* b, co
         case 7: r = h_rn(((const float*)a)[i]); break;
         case 8: r = h_rd(((const float*)a)[i]); break;
         case 9: r = x - hfrom(b[i]); break;
+        case 10: r = h_min(x, hfrom(b[i])); break;
+        case 11: r = h_rn(half_of_fixed(((const int64_t*)a)[i])); break;   // exact: the value is a half
+        case 12: {   // DPP wave_shr:1 of a: lane l receives lane l - 1's value, lane 0 keeps b
+            const uint32_t v = __builtin_amdgcn_update_dpp((uint32_t)b[i], (uint32_t)a[i], 0x138, 0xf, 0xf, false);
+            r = hfrom((uint16_t)v);
+            break;
+        }
         default: break;
     }
     out[i] = hbits(r);
@@ -100,6 +109,70 @@ void launch_halfmath(int op, const uint16_t* a, const uint16_t* b, const uint16_
                      hipStream_t s) {
     if (n <= 0) return;
     halfmath_kernel<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(op, a, b, c, out, n);
+}
+
+// Exhaustive check of h_div: every pair (a, b) of half bit patterns with a
+// finite, b finite and nonzero. q = h_div(a, b) is correctly rounded iff no
+// half lies nearer to a / b (ties: q even), i.e. |a - q b| <= |a - q' b| for
+// both neighbours q' of q (exact double residuals: fma of halves), with the
+// overflow (|a / b| >= 65520 -> inf) and underflow (|a / b| <= 2^-25 -> 0)
+// ends checked directly. out[0] mismatches, out[1] pairs checked, out[2..4]
+// a, b, q of one mismatch.
+__device__ __forceinline__ double hd(uint16_t h) { return (double)(float)hfrom(h); }
+
+__global__ void __launch_bounds__(256) half_div_check_kernel(unsigned long long* out) {
+    const uint32_t t = blockIdx.x * 256u + threadIdx.x;   // 2^24 threads
+    const uint16_t a = (uint16_t)(t >> 8);
+    unsigned long long checked = 0, bad = 0;
+    if ((a & 0x7c00u) != 0x7c00u) {
+        const double da = hd(a);
+        for (uint32_t k = 0; k < 256; ++k) {
+            const uint16_t b = (uint16_t)(((t & 255u) << 8) | k);
+            if ((b & 0x7c00u) == 0x7c00u || (b & 0x7fffu) == 0u) continue;
+            const double db = hd(b);
+            const uint16_t q = hbits(h_div(hfrom(a), hfrom(b)));
+            ++checked;
+            const uint16_t mag = (uint16_t)(q & 0x7fffu);
+            const bool neg = ((a ^ b) & 0x8000u) != 0u;
+            bool ok;
+            const double ax = __builtin_fabs(da), bx = __builtin_fabs(db);
+            if (da == 0.0) {
+                ok = mag == 0u && (((q & 0x8000u) != 0u) == neg);
+            } else if (mag == 0x7c00u) {   // infinity
+                ok = ax >= 65520.0 * bx && (((q & 0x8000u) != 0u) == neg);
+            } else if (mag > 0x7c00u) {    // NaN
+                ok = false;
+            } else if (mag == 0u) {
+                ok = ax <= 0x1p-25 * bx && (((q & 0x8000u) != 0u) == neg);
+            } else {
+                ok = (((q & 0x8000u) != 0u) == neg);
+                const double dq = (double)(float)hfrom(mag);
+                const double r0 = __builtin_fabs(__builtin_fma(-dq, bx, ax));
+                const double dlo = (double)(float)hfrom((uint16_t)(mag - 1u));
+                const double rlo = __builtin_fabs(__builtin_fma(-dlo, bx, ax));
+                // above the largest finite half the next value is 65536 (rounds to infinity)
+                const double dhi = mag == 0x7bffu ? 65536.0 : (double)(float)hfrom((uint16_t)(mag + 1u));
+                const double rhi = __builtin_fabs(__builtin_fma(-dhi, bx, ax));
+                const bool even = (mag & 1u) == 0u;
+                if (r0 > rlo || r0 > rhi) ok = false;
+                if ((r0 == rlo || r0 == rhi) && !even) ok = false;
+            }
+            if (!ok) {
+                if (bad == 0 && atomicAdd(&out[5], 1ull) == 0ull) {
+                    out[2] = a;
+                    out[3] = b;
+                    out[4] = q;
+                }
+                ++bad;
+            }
+        }
+    }
+    if (bad) atomicAdd(&out[0], bad);
+    atomicAdd(&out[1], checked);
+}
+
+void launch_half_div_check(unsigned long long* out, hipStream_t s) {
+    half_div_check_kernel<<<65536u, 256, 0, s>>>(out);
 }
 
 }  // namespace tgs

@@ -68,10 +68,15 @@ class FastGSRasterizer(RasterizerBase):
         L = _lib.load()
         _lib.check(L.tgs_rasterizer_set_gaussians(self._h, C.byref(self._cg)), "set_gaussians")
         img = ctx.fwd_output.image
-        if img.data_type != DataType.Float32:
-            raise RuntimeError("FastGSRasterizer: only float32 images are supported")
+        # fastgs.cu:143-188: a float16 image selects the fp16-image rasterizer (FGS16)
+        if img.data_type == DataType.Float32:
+            dt = _lib.TGS_DTYPE_FLOAT32
+        elif img.data_type == DataType.Float16:
+            dt = _lib.TGS_DTYPE_FLOAT16
+        else:
+            raise RuntimeError("FastGSRasterizer: float32 or float16 images only")
         cam = ctx.fwd_input.to_c()
-        _lib.check(L.tgs_rasterizer_forward_ex(self._h, C.byref(cam), ptr(img.data), _lib.TGS_DTYPE_FLOAT32,
+        _lib.check(L.tgs_rasterizer_forward_ex(self._h, C.byref(cam), ptr(img.data), dt,
                                                ptr(ctx.densification_info),
                                                _lib.TGS_FORWARD_NO_SYNC if no_sync else 0,
                                                stream_ptr(ctx.stream)), "forward")
@@ -162,6 +167,7 @@ class FastGSRasterizer(RasterizerBase):
             "tile_ranges": grab(dv.tile_ranges, 2 * T, torch.int32),
             "tile_max": grab(dv.tile_max, T, torch.int32),
             "n_visible": V, "n_instances": I, "n_tiles": T,
+            "image_dtype": int(dv.image_dtype),
         }
         del cs
         return out
@@ -184,10 +190,28 @@ class FastGSRasterizer(RasterizerBase):
                 "grad_color": np.ascontiguousarray(g[:, 7:10]).reshape(-1),
                 "alpha_sum": np.ascontiguousarray(g[:, 10])}
 
+    def debug_records(self) -> dict:
+        """First record slot per primitive and the 2D-gradient records of the
+        last backward (12 floats per instance slot; tests only)."""
+        import torch
+        dv = _lib.tgs_debug_view()
+        _lib.check(_lib.load().tgs_rasterizer_debug_view(self._h, C.byref(dv)), "debug_view")
+        n = self.m_gaussians.size()
+        dev = self.m_gaussians.means().device
+        fs = torch.empty(max(n, 1), dtype=torch.int32, device=dev)
+        rec = torch.empty(12 * max(int(dv.n_instances), 1), dtype=torch.float32, device=dev)
+        _lib.copy_device(dv.first_slot, fs.numel() * 4, fs)
+        _lib.copy_device(dv.records, rec.numel() * 4, rec)
+        return {"first_slot": fs.cpu().numpy().view(np.uint32)[:n],
+                "records": rec.cpu().numpy()[: 12 * int(dv.n_instances)].reshape(-1, 12)}
+
     def debug_n_contrib(self, shape) -> "object":
         import torch
         dv = _lib.tgs_debug_view()
         _lib.check(_lib.load().tgs_rasterizer_debug_view(self._h, C.byref(dv)), "debug_view")
+        if dv.image_dtype == _lib.TGS_DTYPE_FLOAT16:   # FGS16: 16-bit counts
+            t = torch.empty(shape.channel_stride, dtype=torch.int16, device=self.m_gaussians.means().device)
+            return _lib.copy_device(dv.n_contrib, t.numel() * 2, t)
         t = torch.empty(shape.channel_stride, dtype=torch.int32, device=self.m_gaussians.means().device)
         return _lib.copy_device(dv.n_contrib, t.numel() * 4, t)
 
