@@ -199,7 +199,10 @@ int tgs_rasterizer_debug_view(tgs_rasterizer* r, tgs_debug_view* out);
 /* ---- losses: replace create_loss("l1" | "fused_ssim") and LossBase::evaluate
  * (tinygs/src/loss/loss.cu:13-27, tinygs/include/tinygs/loss/loss.hpp:6-28).
  * Accumulate: loss[i] += ..., grad[i] += ... (loss and grad may be NULL for l1,
- * grad may be NULL for fused_ssim). */
+ * grad may be NULL for fused_ssim). dtype TGS_DTYPE_FLOAT32 or
+ * TGS_DTYPE_FLOAT16 (pred, target, loss and grad all of it; l1.cu:130-146,
+ * fused_ssim.cu:863-906): fp16 computes in float and rounds each stored value
+ * to nearest half. */
 typedef struct tgs_loss_context {
     const void* pred;
     const void* target;

@@ -186,3 +186,126 @@ def test_fgs16_half_division_correctly_rounded(hip):
     o = out.cpu().numpy()
     assert o[1] > 4_000_000_000, o   # pairs checked
     assert o[0] == 0, ("mismatches", o[0], "first a, b, q:", hex(int(o[2])), hex(int(o[3])), hex(int(o[4])))
+
+
+# ---------------------------------------------------------------- fp16 losses
+
+def _h2f(bits):
+    return bits.view(np.float16).astype(np.float32)
+
+
+def _loss16(kind, pred_h, targ_h, l0_h, g0_h, shape, scale):
+    import torch
+    from tinygs_amd.core import DataType, Image, LossContext
+    from tinygs_amd.loss import create_loss
+    dev = lambda a: torch.from_numpy(np.ascontiguousarray(a.view(np.float16))).cuda()
+    ctx = LossContext(Image(shape, DataType.Float16, dev(pred_h)), Image(shape, DataType.Float16, dev(targ_h)),
+                      Image(shape, DataType.Float16, dev(l0_h)), Image(shape, DataType.Float16, dev(g0_h)))
+    create_loss(kind).evaluate(ctx, scale)
+    torch.cuda.synchronize()
+    return ctx.loss.data.cpu().numpy().view(np.uint16), ctx.grad.data.cpu().numpy().view(np.uint16)
+
+
+def _inputs16(shape, seed):
+    rng = np.random.default_rng(seed)
+    targ = rng.random(shape.padded_size).astype(np.float16)
+    pred = np.clip(targ + rng.normal(0, 0.3, shape.padded_size), -0.2, 1.2).astype(np.float16)
+    l0 = rng.random(shape.padded_size).astype(np.float16)
+    g0 = rng.normal(0, 1e-3, shape.padded_size).astype(np.float16)
+    return [a.view(np.uint16) for a in (pred, targ, l0, g0)]
+
+
+@pytest.mark.parametrize("wh", [(64, 64), (61, 45), (800, 600)])
+def test_fp16_l1_bit_exact(hip, orc, wh):
+    """l1_kernel_f16_h2 (l1.cu:67-107): the float result on the half inputs and
+    the half accumulators, rounded to nearest half."""
+    from tinygs_amd.image import ImageShape
+    shape = ImageShape(*wh)
+    pred, targ, l0, g0 = _inputs16(shape, wh[0])
+    lg, gg = _loss16("l1", pred, targ, l0, g0, shape, 0.8)
+    lo, go = orc.l1(_h2f(pred), _h2f(targ), shape, np.float32(0.8), _h2f(l0).copy(), _h2f(g0).copy())
+    assert np.array_equal(lg, lo.astype(np.float16).view(np.uint16))
+    assert np.array_equal(gg, go.astype(np.float16).view(np.uint16))
+
+
+@pytest.mark.parametrize("wh", [(64, 64), (61, 45), (800, 600)])
+def test_fp16_ssim(hip, orc, wh):
+    """fused_ssim_cuda_fp16 / fused_ssim_fp16_backward (fused_ssim.cu:445-693):
+    within one half ulp of the fp32 oracle's result on the half inputs and
+    accumulators, rounded to half (the fp32 sums differ from the oracle's by
+    summation-order rounding)."""
+    from tinygs_amd.image import ImageShape, tiled_index
+    shape = ImageShape(*wh)
+    pred, targ, l0, g0 = _inputs16(shape, wh[0] + 1)
+    lg, gg = _loss16("fused_ssim", pred, targ, l0, g0, shape, 0.2)
+    lo, go = orc.ssim(_h2f(pred), _h2f(targ), shape, np.float32(0.2), _h2f(l0).copy(), _h2f(g0).copy())
+    idx = np.concatenate([c * shape.channel_stride + tiled_index(shape).reshape(-1) for c in range(3)])
+    for got, ref in ((lg, lo), (gg, go)):
+        r16 = ref[idx].astype(np.float16)
+        g = got[idx].view(np.float16).astype(np.float64)
+        ulp = np.abs(np.spacing(r16).astype(np.float64))
+        assert np.all(np.abs(g - r16.astype(np.float64)) <= ulp), np.abs(g - r16.astype(np.float64)).max()
+
+
+@pytest.mark.parametrize("assign", [False, True])
+def test_fp16_fused_l1_ssim_equals_two_launches(hip, assign):
+    import torch
+    from tinygs_amd.core import DataType, Image, LossContext
+    from tinygs_amd.image import ImageShape
+    from tinygs_amd.loss import create_loss, evaluate_l1_ssim
+    shape = ImageShape(246, 182)
+    pred, targ, l0, g0 = _inputs16(shape, 5)
+    if assign:
+        l0 = np.zeros_like(l0)
+        g0 = np.zeros_like(g0)
+    lg, gg = _loss16("l1", pred, targ, l0, g0, shape, 0.8)
+    lg2, gg2 = _loss16("fused_ssim", pred, targ, lg, gg, shape, 0.2)
+    dev = lambda a: torch.from_numpy(np.ascontiguousarray(a.view(np.float16))).cuda()
+    start_l = np.full_like(l0, 0x7e00) if assign else l0   # NaN: assign must write every element
+    start_g = np.full_like(g0, 0x7e00) if assign else g0
+    ctx = LossContext(Image(shape, DataType.Float16, dev(pred)), Image(shape, DataType.Float16, dev(targ)),
+                      Image(shape, DataType.Float16, dev(start_l)), Image(shape, DataType.Float16, dev(start_g)))
+    evaluate_l1_ssim(create_loss("l1"), ctx, 0.8, 0.2, assign=assign)
+    torch.cuda.synchronize()
+    assert np.array_equal(ctx.loss.data.cpu().numpy().view(np.uint16), lg2)
+    assert np.array_equal(ctx.grad.data.cpu().numpy().view(np.uint16), gg2)
+
+
+def test_fgs16_train_step(hip, orc):
+    """One FGS16 iteration as TrainStep runs it (fp16 image, fp16 fused L1 +
+    SSIM, sparse backward, SimpleAdam): pixels bit-exact, the 2D sums
+    bit-exact given the GPU's loss gradient image, Adam bit-exact given the
+    GPU's gradients."""
+    import torch
+    from tinygs_amd.train import TrainStep
+    scene = CASES["config2_246x182"]
+    ts = TrainStep(scene, l1_weight=0.8, ssim_weight=0.2, eps=1e-15, shs_lr=5e-3, sparse_grads=True,
+                   image_dtype="float16")
+    ts.zero()
+    ts.forward()
+    ts.losses_and_grad()
+    ts.backward(keep_2d=True)
+    torch.cuda.synchronize()
+    img = ts.pred.data.cpu().numpy().view(np.uint16)
+    gimg = ts.grad_img.data.cpu().numpy().view(np.uint16)
+    g2d_gpu = ts.rasterizer.debug_grad2d()
+    g = ts.grads
+    grads = {"means": g.means(), "scales": g.scales(), "rotations": g.rotations(), "opacities": g.opacities(),
+             "sh0": g.sh_coefficient_0(), "sh_rest": g.sh_coefficients_rest()}
+    grads = {k: v.cpu().numpy().reshape(-1) for k, v in grads.items()}
+    ts.optimize()
+    torch.cuda.synchronize()
+    theta = ts.params()
+    pre, bins, fwd = orc.h_render(scene)
+    assert np.array_equal(img, fwd["image"])
+    ob = orc.h_blend_backward(scene, pre, bins, fwd, gimg)
+    for key in ("grad_mean2d", "absgrad", "grad_conic", "grad_color"):
+        assert np.array_equal(g2d_gpu[key].view(np.uint32), ob["g2d"][key].view(np.uint32)), key
+    # (rows the sparse backward did not write are zero gradients: Adam leaves them unchanged)
+    th0 = orc.params(scene, "f")
+    m1 = {k: np.zeros_like(v) for k, v in th0.items()}
+    m2 = {k: np.zeros_like(v) for k, v in th0.items()}
+    LR = {"means": 1.6e-4, "scene_scale": 1.0, "opacities": 5e-2, "rotations": 1e-3, "scales": 5e-3, "shs": 5e-3}
+    orc.adam_step(th0, grads, m1, m2, LR, 1, grad_scale=1.0, eps=1e-15, sh_half=scene.sh_dtype == "float16")
+    for k in th0:
+        assert np.array_equal(theta[k].view(np.uint32), th0[k].view(np.uint32)), k

@@ -767,10 +767,31 @@ int tgs_loss_destroy(tgs_loss* l) {
     return TGS_OK;
 }
 
+// One fused forward / SSIM backward pair for either image type.
+static void loss_forward(bool f16, const tgs_loss_context* c, float c1, float c2, float s_ssim, float s_l1,
+                         bool assign, void* loss, void* grad, float* d0, float* d1, float* d2, hipStream_t s) {
+    if (f16)
+        launch_l1_ssim_forward_f16(c->width, c->height, c1, c2, s_ssim, s_l1, assign, c->pred, c->target, loss, grad,
+                                   d0, d1, d2, s);
+    else
+        launch_l1_ssim_forward(c->width, c->height, c1, c2, s_ssim, s_l1, assign, (const float*)c->pred,
+                               (const float*)c->target, (float*)loss, (float*)grad, d0, d1, d2, s);
+}
+static void loss_ssim_backward(bool f16, const tgs_loss_context* c, float s_ssim, const float* d0, const float* d1,
+                               const float* d2, hipStream_t s) {
+    if (f16)
+        launch_ssim_backward_f16(c->width, c->height, s_ssim, c->pred, c->target, c->grad, d0, d1, d2, s);
+    else
+        launch_ssim_backward(c->width, c->height, s_ssim, (const float*)c->pred, (const float*)c->target,
+                             (float*)c->grad, d0, d1, d2, s);
+}
+
 int tgs_loss_evaluate(tgs_loss* l, const tgs_loss_context* c, float scale, void* stream) {
     if (!l || !c) return fail(TGS_ERR_INVALID, "NULL argument");
-    if (c->dtype != TGS_DTYPE_FLOAT32)
-        return fail(TGS_ERR_UNSUPPORTED, "loss dtype %d: only float32 is supported", c->dtype);
+    // l1.cu:109-151, fused_ssim.cu:797-916: float32 and float16 images
+    if (c->dtype != TGS_DTYPE_FLOAT32 && c->dtype != TGS_DTYPE_FLOAT16)
+        return fail(TGS_ERR_UNSUPPORTED, "loss dtype %d: float32 or float16 images only", c->dtype);
+    const bool f16 = c->dtype == TGS_DTYPE_FLOAT16;
     if (!c->pred || !c->target) return fail(TGS_ERR_INVALID, "pred / target is NULL");
     if (c->width == 0 || c->height == 0 || c->channel == 0) return fail(TGS_ERR_INVALID, "empty image");
     hipStream_t s = (hipStream_t)stream;
@@ -780,8 +801,11 @@ int tgs_loss_evaluate(tgs_loss* l, const tgs_loss_context* c, float scale, void*
         // l1.cu:117-121: scale / (W * H * C)
         const int npix = (int)(c->width * c->height * c->channel);
         StageScope sc(ST_L1, s);
-        launch_l1((const float*)c->pred, (const float*)c->target, (float*)c->loss, (float*)c->grad, padded,
-                  scale / (float)npix, s);
+        if (f16)
+            launch_l1_f16(c->pred, c->target, c->loss, c->grad, padded, scale / (float)npix, s);
+        else
+            launch_l1((const float*)c->pred, (const float*)c->target, (float*)c->loss, (float*)c->grad, padded,
+                      scale / (float)npix, s);
         TGS_CHECK_LAUNCH();
         return TGS_OK;
     }
@@ -792,14 +816,11 @@ int tgs_loss_evaluate(tgs_loss* l, const tgs_loss_context* c, float scale, void*
     StageScope sc(ST_SSIM, s);
     if (c->grad) {
         for (auto& b : l->dm) TGS_TRY(ensure(b, sizeof(float) * (size_t)padded, s));
-        launch_l1_ssim_forward(c->width, c->height, C1, C2, actual, 0.0f, false, (const float*)c->pred,
-                               (const float*)c->target, (float*)c->loss, nullptr, l->dm[0].as<float>(),
-                               l->dm[1].as<float>(), l->dm[2].as<float>(), s);
-        launch_ssim_backward(c->width, c->height, actual, (const float*)c->pred, (const float*)c->target,
-                             (float*)c->grad, l->dm[0].as<float>(), l->dm[1].as<float>(), l->dm[2].as<float>(), s);
+        loss_forward(f16, c, C1, C2, actual, 0.0f, false, c->loss, nullptr, l->dm[0].as<float>(),
+                     l->dm[1].as<float>(), l->dm[2].as<float>(), s);
+        loss_ssim_backward(f16, c, actual, l->dm[0].as<float>(), l->dm[1].as<float>(), l->dm[2].as<float>(), s);
     } else {
-        launch_l1_ssim_forward(c->width, c->height, C1, C2, actual, 0.0f, false, (const float*)c->pred,
-                               (const float*)c->target, (float*)c->loss, nullptr, nullptr, nullptr, nullptr, s);
+        loss_forward(f16, c, C1, C2, actual, 0.0f, false, c->loss, nullptr, nullptr, nullptr, nullptr, s);
     }
     TGS_CHECK_LAUNCH();
     return TGS_OK;
@@ -808,8 +829,9 @@ int tgs_loss_evaluate(tgs_loss* l, const tgs_loss_context* c, float scale, void*
 int tgs_loss_l1_ssim(tgs_loss* l, const tgs_loss_context* c, float l1_scale, float ssim_scale, int32_t flags,
                      void* stream) {
     if (!l || !c) return fail(TGS_ERR_INVALID, "NULL argument");
-    if (c->dtype != TGS_DTYPE_FLOAT32)
-        return fail(TGS_ERR_UNSUPPORTED, "loss dtype %d: only float32 is supported", c->dtype);
+    if (c->dtype != TGS_DTYPE_FLOAT32 && c->dtype != TGS_DTYPE_FLOAT16)
+        return fail(TGS_ERR_UNSUPPORTED, "loss dtype %d: float32 or float16 images only", c->dtype);
+    const bool f16 = c->dtype == TGS_DTYPE_FLOAT16;
     if (!c->pred || !c->target) return fail(TGS_ERR_INVALID, "pred / target is NULL");
     if (c->width == 0 || c->height == 0) return fail(TGS_ERR_INVALID, "empty image");
     if (c->channel != 3) return fail(TGS_ERR_UNSUPPORTED, "fused L1 + SSIM needs 3 channels");
@@ -825,14 +847,11 @@ int tgs_loss_l1_ssim(tgs_loss* l, const tgs_loss_context* c, float l1_scale, flo
     StageScope sc(ST_SSIM, s);
     if (c->grad) {
         for (auto& b : l->dm) TGS_TRY(ensure(b, sizeof(float) * (size_t)padded, s));
-        launch_l1_ssim_forward(c->width, c->height, C1, C2, s_ssim, s_l1, assign, (const float*)c->pred,
-                               (const float*)c->target, (float*)c->loss, (float*)c->grad, l->dm[0].as<float>(),
-                               l->dm[1].as<float>(), l->dm[2].as<float>(), s);
-        launch_ssim_backward(c->width, c->height, s_ssim, (const float*)c->pred, (const float*)c->target,
-                             (float*)c->grad, l->dm[0].as<float>(), l->dm[1].as<float>(), l->dm[2].as<float>(), s);
+        loss_forward(f16, c, C1, C2, s_ssim, s_l1, assign, c->loss, c->grad, l->dm[0].as<float>(),
+                     l->dm[1].as<float>(), l->dm[2].as<float>(), s);
+        loss_ssim_backward(f16, c, s_ssim, l->dm[0].as<float>(), l->dm[1].as<float>(), l->dm[2].as<float>(), s);
     } else {
-        launch_l1_ssim_forward(c->width, c->height, C1, C2, s_ssim, s_l1, assign, (const float*)c->pred,
-                               (const float*)c->target, (float*)c->loss, nullptr, nullptr, nullptr, nullptr, s);
+        loss_forward(f16, c, C1, C2, s_ssim, s_l1, assign, c->loss, nullptr, nullptr, nullptr, nullptr, s);
     }
     TGS_CHECK_LAUNCH();
     return TGS_OK;

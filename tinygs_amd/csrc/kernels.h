@@ -221,6 +221,16 @@ void launch_l1_ssim_forward(uint32_t width, uint32_t height, float c1, float c2,
                             float* dm_mu, float* dm_s1, float* dm_s12, hipStream_t st);
 void launch_ssim_backward(uint32_t width, uint32_t height, float s, const float* pred, const float* target,
                           float* grad, const float* dm_mu, const float* dm_s1, const float* dm_s12, hipStream_t st);
+// fp16 images (l1.cu:43-107, fused_ssim.cu:445-693): half pred / target /
+// loss / grad, float arithmetic, each stored value rounded to nearest half
+void launch_l1_f16(const void* pred, const void* target, void* loss, void* grad, int64_t n_padded, float s,
+                   hipStream_t st);
+void launch_l1_ssim_forward_f16(uint32_t width, uint32_t height, float c1, float c2, float s_ssim, float s_l1,
+                                bool assign, const void* pred, const void* target, void* loss, void* grad,
+                                float* dm_mu, float* dm_s1, float* dm_s12, hipStream_t st);
+void launch_ssim_backward_f16(uint32_t width, uint32_t height, float s, const void* pred, const void* target,
+                              void* grad, const float* dm_mu, const float* dm_s1, const float* dm_s12,
+                              hipStream_t st);
 
 // ---- SimpleAdam (simple_adam.cu:104-213, :457-580)
 struct AdamGroup {

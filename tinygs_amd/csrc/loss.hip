@@ -21,12 +21,27 @@
 // term is added before the SSIM term, as two separate reference launches
 // would. SSIM sums differ from the reference's summation order by rounding
 // only (the oracle comparison is normwise 1e-5).
+//
+// fp16 images (l1.cu:43-107, fused_ssim.cu:445-693): the same float
+// arithmetic on the half inputs; each stored loss / gradient value is the
+// float result (including the accumulated half value) rounded to nearest
+// half, once per reference launch (the L1 term's sum is rounded before the
+// SSIM term is added). The three derivative maps stay float.
 #include <algorithm>
 
 #include "common.h"
 #include "kernels.h"
 
 namespace tgs {
+
+// element access of fp32 / fp16 images
+__device__ __forceinline__ float ld(const float* p, size_t i) { return p[i]; }
+__device__ __forceinline__ float ld(const __half* p, size_t i) { return __half2float(p[i]); }
+__device__ __forceinline__ void st(float* p, size_t i, float v) { p[i] = v; }
+__device__ __forceinline__ void st(__half* p, size_t i, float v) { p[i] = __float2half_rn(v); }
+// a value as the image type holds it
+__device__ __forceinline__ float held(const float*, float v) { return v; }
+__device__ __forceinline__ float held(const __half*, float v) { return __half2float(__float2half_rn(v)); }
 
 __constant__ float kGauss[11] = {0.001028380123898387f,  0.0075987582094967365f, 0.036000773310661316f,
                                  0.10936068743467331f,   0.21300552785396576f,   0.26601171493530273f,
@@ -56,12 +71,45 @@ __global__ void l1_kernel(const float4* __restrict__ pred, const float4* __restr
     if (grad) grad[i] = make_float4(g[0], g[1], g[2], g[3]);
 }
 
+// fp16 (l1_kernel_f16_h2, l1.cu:67-107): eight halves per thread
+__global__ void l1_f16_kernel(const uint4* __restrict__ pred, const uint4* __restrict__ target,
+                              uint4* __restrict__ loss, uint4* __restrict__ grad, int64_t n8, float s) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n8) return;
+    const uint4 p4 = pred[i], t4 = target[i];
+    const uint4 l4 = loss ? loss[i] : make_uint4(0u, 0u, 0u, 0u);
+    const uint4 g4 = grad ? grad[i] : make_uint4(0u, 0u, 0u, 0u);
+    const __half* ph = (const __half*)&p4;
+    const __half* th = (const __half*)&t4;
+    const __half* lh = (const __half*)&l4;
+    const __half* gh = (const __half*)&g4;
+    uint4 lo, go;
+    __half* lr = (__half*)&lo;
+    __half* gr = (__half*)&go;
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+        const float d = saturate(__half2float(ph[q])) - __half2float(th[q]);
+        lr[q] = __float2half_rn(__builtin_fmaf(__builtin_fabsf(d), s, __half2float(lh[q])));
+        gr[q] = __float2half_rn(__builtin_fmaf(__builtin_copysignf(1.0f, d), s, __half2float(gh[q])));
+    }
+    if (loss) loss[i] = lo;
+    if (grad) grad[i] = go;
+}
+
 void launch_l1(const float* pred, const float* target, float* loss, float* grad, int64_t n_padded, float s,
                hipStream_t st) {
     if (n_padded <= 0) return;
     const int64_t n4 = n_padded / 4;   // padded planes hold whole 8x8 blocks
     l1_kernel<<<(unsigned)((n4 + 255) / 256), 256, 0, st>>>((const float4*)pred, (const float4*)target,
                                                             (float4*)loss, (float4*)grad, n4, s);
+}
+
+void launch_l1_f16(const void* pred, const void* target, void* loss, void* grad, int64_t n_padded, float s,
+                   hipStream_t st) {
+    if (n_padded <= 0) return;
+    const int64_t n8 = n_padded / 8;   // whole 8x8 blocks: a multiple of 64 halves per plane
+    l1_f16_kernel<<<(unsigned)((n8 + 255) / 256), 256, 0, st>>>((const uint4*)pred, (const uint4*)target,
+                                                                (uint4*)loss, (uint4*)grad, n8, s);
 }
 
 constexpr int kOT = 32;           // output tile edge
@@ -118,11 +166,12 @@ __device__ __forceinline__ void ssim_tile_of(uint32_t& tx, uint32_t& ty, uint32_
 // image, like the reference's L1 over all padded elements. One workgroup per
 // (32x32 tile, channel): no state is carried across channels, which keeps
 // the register footprint small enough for four workgroups per CU.
+template <typename T>
 __global__ void __launch_bounds__(256) l1_ssim_forward_kernel(uint32_t W, uint32_t H, float C1, float C2,
                                                               float s_ssim, float s_l1, int assign,
-                                                              const float* __restrict__ pred,
-                                                              const float* __restrict__ target,
-                                                              float* __restrict__ loss, float* __restrict__ grad,
+                                                              const T* __restrict__ pred,
+                                                              const T* __restrict__ target,
+                                                              T* __restrict__ loss, T* __restrict__ grad,
                                                               float* __restrict__ dm_mu, float* __restrict__ dm_s1,
                                                               float* __restrict__ dm_s12) {
     __shared__ __half2 s_in[kHT][kHT];         // fp16-rounded (pred, target), exactly the values the sums use
@@ -143,9 +192,9 @@ __global__ void __launch_bounds__(256) l1_ssim_forward_kernel(uint32_t W, uint32
 #pragma unroll
         for (int r = 0; r < kHaloRounds; ++r) {
             const HaloRound h = halo_round(r, bx, by, W, H, tw, th);
-            const float* __restrict__ pp = pred + h.base;   // wave-uniform block base
-            const float* __restrict__ tp = target + h.base;
-            const float x = pp[lane], y = tp[lane];
+            const T* __restrict__ pp = pred + h.base;   // wave-uniform block base
+            const T* __restrict__ tp = target + h.base;
+            const float x = ld(pp, lane), y = ld(tp, lane);
             pv[r] = h.in ? x : 0.f;
             tv[r] = h.in ? y : 0.f;
         }
@@ -215,11 +264,11 @@ __global__ void __launch_bounds__(256) l1_ssim_forward_kernel(uint32_t W, uint32
         const int px = bx + vc, py = by + 4 * vr + q;
         if (px >= pw || py >= ph) continue;
         const uint32_t idx = tiled_index((uint32_t)py, (uint32_t)px, tw);
-        float lv = (!assign && loss) ? loss[idx] : 0.f;
-        float gv = (!assign && grad) ? grad[idx] : 0.f;
+        float lv = (!assign && loss) ? ld(loss, idx) : 0.f;
+        float gv = (!assign && grad) ? ld(grad, idx) : 0.f;
         if (s_l1 != 0.f) {
-            const float d = saturate(pred[idx]) - target[idx];
-            lv = __builtin_fmaf(__builtin_fabsf(d), s_l1, lv);
+            const float d = saturate(ld(pred, idx)) - ld(target, idx);
+            lv = held(pred, __builtin_fmaf(__builtin_fabsf(d), s_l1, lv));
             gv = __builtin_fmaf(__builtin_copysignf(1.0f, d), s_l1, gv);
         }
         if (px < (int)W && py < (int)H) {
@@ -241,18 +290,19 @@ __global__ void __launch_bounds__(256) l1_ssim_forward_kernel(uint32_t W, uint32
                 dm_s12[idx] = 2.0f * Cc * inv;
             }
         }
-        if (loss) loss[idx] = lv;
-        if (grad && (assign || s_l1 != 0.f)) grad[idx] = gv;
+        if (loss) st(loss, idx, lv);
+        if (grad && (assign || s_l1 != 0.f)) st(grad, idx, gv);
     }
 }
 
 // SSIM backward: grad += -s (dm_mu * w + 2 p (dm_s1 * w) + t (dm_s12 * w))
 // with * the 11x11 separable convolution (fused_ssim.cu:366-438). One
 // workgroup per (32x32 tile, channel).
+template <typename T>
 __global__ void __launch_bounds__(256) ssim_backward_kernel(uint32_t W, uint32_t H, float s,
-                                                            const float* __restrict__ pred,
-                                                            const float* __restrict__ target,
-                                                            float* __restrict__ grad, const float* __restrict__ dm_mu,
+                                                            const T* __restrict__ pred,
+                                                            const T* __restrict__ target,
+                                                            T* __restrict__ grad, const float* __restrict__ dm_mu,
                                                             const float* __restrict__ dm_s1,
                                                             const float* __restrict__ dm_s12) {
     // s_d: the three maps with halo; s_h: their horizontal sums, overlaying
@@ -355,8 +405,9 @@ __global__ void __launch_bounds__(256) ssim_backward_kernel(uint32_t W, uint32_t
         const int px = bx + vc, py = by + 4 * vr + q;
         if (px >= (int)W || py >= (int)H) continue;
         const uint32_t idx = tiled_index((uint32_t)py, (uint32_t)px, tw);
-        const float dl = __builtin_fmaf(target[idx], o[2][q], __builtin_fmaf(2.0f * pred[idx], o[1][q], o[0][q]));
-        grad[idx] = __builtin_fmaf(-s, dl, grad[idx]);
+        const float dl =
+            __builtin_fmaf(ld(target, idx), o[2][q], __builtin_fmaf(2.0f * ld(pred, idx), o[1][q], o[0][q]));
+        st(grad, idx, __builtin_fmaf(-s, dl, ld(grad, idx)));
     }
 }
 
@@ -365,15 +416,34 @@ void launch_l1_ssim_forward(uint32_t width, uint32_t height, float c1, float c2,
                             float* dm_mu, float* dm_s1, float* dm_s12, hipStream_t st) {
     if (width == 0 || height == 0) return;
     dim3 grid((width + kOT - 1) / kOT, (height + kOT - 1) / kOT, 3);
-    l1_ssim_forward_kernel<<<grid, 256, 0, st>>>(width, height, c1, c2, s_ssim, s_l1, assign ? 1 : 0, pred, target,
-                                                 loss, grad, dm_mu, dm_s1, dm_s12);
+    l1_ssim_forward_kernel<float><<<grid, 256, 0, st>>>(width, height, c1, c2, s_ssim, s_l1, assign ? 1 : 0, pred,
+                                                        target, loss, grad, dm_mu, dm_s1, dm_s12);
+}
+
+void launch_l1_ssim_forward_f16(uint32_t width, uint32_t height, float c1, float c2, float s_ssim, float s_l1,
+                                bool assign, const void* pred, const void* target, void* loss, void* grad,
+                                float* dm_mu, float* dm_s1, float* dm_s12, hipStream_t st) {
+    if (width == 0 || height == 0) return;
+    dim3 grid((width + kOT - 1) / kOT, (height + kOT - 1) / kOT, 3);
+    l1_ssim_forward_kernel<__half><<<grid, 256, 0, st>>>(width, height, c1, c2, s_ssim, s_l1, assign ? 1 : 0,
+                                                         (const __half*)pred, (const __half*)target, (__half*)loss,
+                                                         (__half*)grad, dm_mu, dm_s1, dm_s12);
 }
 
 void launch_ssim_backward(uint32_t width, uint32_t height, float s, const float* pred, const float* target,
                           float* grad, const float* dm_mu, const float* dm_s1, const float* dm_s12, hipStream_t st) {
     if (width == 0 || height == 0) return;
     dim3 grid((width + kOT - 1) / kOT, (height + kOT - 1) / kOT, 3);
-    ssim_backward_kernel<<<grid, 256, 0, st>>>(width, height, s, pred, target, grad, dm_mu, dm_s1, dm_s12);
+    ssim_backward_kernel<float><<<grid, 256, 0, st>>>(width, height, s, pred, target, grad, dm_mu, dm_s1, dm_s12);
+}
+
+void launch_ssim_backward_f16(uint32_t width, uint32_t height, float s, const void* pred, const void* target,
+                              void* grad, const float* dm_mu, const float* dm_s1, const float* dm_s12,
+                              hipStream_t st) {
+    if (width == 0 || height == 0) return;
+    dim3 grid((width + kOT - 1) / kOT, (height + kOT - 1) / kOT, 3);
+    ssim_backward_kernel<__half><<<grid, 256, 0, st>>>(width, height, s, (const __half*)pred, (const __half*)target,
+                                                       (__half*)grad, dm_mu, dm_s1, dm_s12);
 }
 
 // ------------------------------------------------------------------ PSNR

@@ -40,24 +40,18 @@ class _CLoss(LossBase):
     def _context(self, ctx: LossContext):
         if ctx.pred.data_type != ctx.target.data_type:
             raise RuntimeError(f"{self.name()}: prediction and target data type must be the same")
-        if ctx.pred.data_type != DataType.Float32:
-            raise RuntimeError(f"{self.name()}: only float32 is supported")
+        # l1.cu:130-146, fused_ssim.cu:863-906: float32 and float16 images
+        dts = {DataType.Float32: _lib.TGS_DTYPE_FLOAT32, DataType.Float16: _lib.TGS_DTYPE_FLOAT16}
+        if ctx.pred.data_type not in dts:
+            raise RuntimeError(f"{self.name()}: only float32 and float16 are supported")
         shape = ctx.pred.shape
         return _lib.tgs_loss_context(ptr(ctx.pred.data), ptr(ctx.target.data),
                                      ptr(ctx.loss.data) if ctx.loss else None,
                                      ptr(ctx.grad.data) if ctx.grad else None,
-                                     shape.width, shape.height, shape.channel, _lib.TGS_DTYPE_FLOAT32)
+                                     shape.width, shape.height, shape.channel, dts[ctx.pred.data_type])
 
     def evaluate(self, ctx: LossContext, scale: float):
-        if ctx.pred.data_type != ctx.target.data_type:
-            raise RuntimeError(f"{self.name()}: prediction and target data type must be the same")
-        if ctx.pred.data_type != DataType.Float32:
-            raise RuntimeError(f"{self.name()}: only float32 is supported")
-        shape = ctx.pred.shape
-        c = _lib.tgs_loss_context(ptr(ctx.pred.data), ptr(ctx.target.data),
-                                  ptr(ctx.loss.data) if ctx.loss else None,
-                                  ptr(ctx.grad.data) if ctx.grad else None,
-                                  shape.width, shape.height, shape.channel, _lib.TGS_DTYPE_FLOAT32)
+        c = self._context(ctx)
         _lib.check(_lib.load().tgs_loss_evaluate(self._h, C.byref(c), float(scale), stream_ptr(ctx.stream)),
                    self.name())
 

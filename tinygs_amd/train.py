@@ -22,7 +22,7 @@ forward that outgrew the capacity.
 """
 from __future__ import annotations
 
-from .core import GPUBatchInput, GPUGaussian3d, Image, LossContext, RasterizeContext
+from .core import DataType, GPUBatchInput, GPUGaussian3d, Image, LossContext, RasterizeContext
 from .loss import create_loss, evaluate_l1_ssim
 from .optim import create_optimizer
 from .rasterizer import create_rasterizer
@@ -32,7 +32,9 @@ class TrainStep:
     def __init__(self, scene, l1_weight: float = 0.8, ssim_weight: float = 0.2, grad_scaler: float = 1.0,
                  eps: float = 1e-15, shs_lr: float | None = None, means_lr: float | None = None,
                  max_grad_1: float | None = None, device: str = "cuda", stream=None, sparse_grads: bool = True,
-                 no_sync: bool = False):
+                 no_sync: bool = False, image_dtype: str = DataType.Float32):
+        """image_dtype: float32, or float16 for the fp16-image rasterizer
+        (fastgs.cu:143-188) with the fp16 losses; the target is rounded to half."""
         import torch
         self.scene = scene
         self.no_sync = bool(no_sync)
@@ -49,10 +51,11 @@ class TrainStep:
         self.rasterizer.set_gaussians(self.gaussians)
         shape = scene.camera.shape
         self.shape = shape
-        self.pred = Image.empty(shape, device)
-        self.target = Image(shape, "float32", torch.from_numpy(scene.target).to(device))
-        self.loss_img = Image.empty(shape, device)
-        self.grad_img = Image.empty(shape, device)
+        self.pred = Image.empty(shape, device, image_dtype)
+        tdt = torch.float16 if image_dtype == DataType.Float16 else torch.float32
+        self.target = Image(shape, image_dtype, torch.from_numpy(scene.target).to(device).to(tdt))
+        self.loss_img = Image.empty(shape, device, image_dtype)
+        self.grad_img = Image.empty(shape, device, image_dtype)
         self.losses = []
         if l1_weight:
             self.losses.append((create_loss("l1"), float(l1_weight)))
