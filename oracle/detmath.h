@@ -50,6 +50,22 @@ static inline float orc_expf(float x) {
     return ldexpf(p, (int)k);
 }
 
+/* 2^x for -150 <= x <= 0 (the blend forward's alpha = o 2^(-sigma'), sigma'
+ * in log2 units): k = rint(x), r = x - k in [-1/2, 1/2] (exact), 2^r by the
+ * degree-5 minimax polynomial of relative error 7.5e-8 (Remez exchange,
+ * E. Remez 1934), coefficients rounded to float (Horner, fmaf); exact ldexp. */
+static inline float orc_exp2_core(float x) {
+    const float k = rintf(x);
+    const float r = x - k;
+    float p = 0x1.5c08e6p-10f;
+    p = fmaf(p, r, 0x1.3d0c52p-7f);
+    p = fmaf(p, r, 0x1.c6b6e4p-5f);
+    p = fmaf(p, r, 0x1.ebf918p-3f);
+    p = fmaf(p, r, 0x1.62e428p-1f);
+    p = fmaf(p, r, 0x1.000002p+0f);
+    return ldexpf(p, (int)k);
+}
+
 /* natural log for float x > 0; x == 0 gives -inf, x < 0 or NaN gives NaN. */
 static inline float orc_logf(float x) {
     if (!(x > 0.0f)) return (x == 0.0f) ? -INFINITY : NAN;

@@ -45,6 +45,11 @@
 #define R_FABS(a) fabsf(a)
 #define R_COPYSIGN(a, b) copysignf(a, b)
 #define R_HALF_ROUND(x) orc_round_half(x)
+/* the blend forward's sigma in log2 units (conic prescaled by log2 e) and
+ * its 2^(-sigma'), clamped at 150 */
+#define R_SIG_HALF 0x1.715476p-1f
+#define R_SIG_ONE 0x1.715476p+0f
+#define R_ALPHA_EXP(s) orc_exp2_core(-fminf((s), 150.0f))
 #include "oracle_impl.inc"
 #undef REAL
 #undef SFX
@@ -59,6 +64,9 @@
 #undef R_FABS
 #undef R_COPYSIGN
 #undef R_HALF_ROUND
+#undef R_SIG_HALF
+#undef R_SIG_ONE
+#undef R_ALPHA_EXP
 
 /* ---------------- double instance (finite-difference checker) ---------------- */
 #define REAL double
@@ -74,6 +82,9 @@
 #define R_FABS(a) fabs(a)
 #define R_COPYSIGN(a, b) copysign(a, b)
 #define R_HALF_ROUND(x) (x)
+#define R_SIG_HALF 0.5
+#define R_SIG_ONE 1.0
+#define R_ALPHA_EXP(s) exp(-(s))
 #include "oracle_impl.inc"
 
 /* ---------------- the fp16-image rasterizer (FGS16), half arithmetic ---------------- */
@@ -82,6 +93,7 @@
 /* ---------------- exported helpers ---------------- */
 void orc_expf_array(int64_t n, const float* x, float* y) { for (int64_t i = 0; i < n; ++i) y[i] = orc_expf(x[i]); }
 void orc_logf_array(int64_t n, const float* x, float* y) { for (int64_t i = 0; i < n; ++i) y[i] = orc_logf(x[i]); }
+void orc_exp2_core_array(int64_t n, const float* x, float* y) { for (int64_t i = 0; i < n; ++i) y[i] = orc_exp2_core(x[i]); }
 void orc_half_bits_array(int64_t n, const float* x, uint16_t* y) { for (int64_t i = 0; i < n; ++i) y[i] = orc_float_to_half_bits(x[i]); }
 void orc_round_half_array(int64_t n, const float* x, float* y) { for (int64_t i = 0; i < n; ++i) y[i] = orc_round_half(x[i]); }
 /* The canonical half operations of oracle/halfmath.h on arrays of half bit

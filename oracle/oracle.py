@@ -82,7 +82,7 @@ def _declare(L):
     L.orc_set_threads.restype = None
     L.orc_max_threads.argtypes = []
     L.orc_max_threads.restype = C.c_int
-    for name, argt in (("orc_expf_array", [C.c_int64, f32p, f32p]),
+    for name, argt in (("orc_expf_array", [C.c_int64, f32p, f32p]), ("orc_exp2_core_array", [C.c_int64, f32p, f32p]),
                        ("orc_logf_array", [C.c_int64, f32p, f32p]),
                        ("orc_round_half_array", [C.c_int64, f32p, f32p]),
                        ("orc_half_bits_array", [C.c_int64, f32p, u16p])):
@@ -124,6 +124,14 @@ def expf(x):
     x = np.ascontiguousarray(x, dtype=np.float32)
     y = np.empty_like(x)
     lib().orc_expf_array(x.size, x, y)
+    return y
+
+
+def exp2_core(x):
+    """2^x for -150 <= x <= 0 (the blend forward's deterministic exp2)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    y = np.empty_like(x)
+    lib().orc_exp2_core_array(x.size, x, y)
     return y
 
 

@@ -45,13 +45,16 @@ def test_wave_primitives(hip):
         assert red[q] == np.float32(vals.astype(np.float64).sum() + 64 * q), (q, red[q])
 
 
-@pytest.mark.parametrize("op", [0, 1, 2, 3, 4, 5])
+@pytest.mark.parametrize("op", [0, 1, 2, 3, 4, 5, 6])
 def test_detmath_bit_exact_vs_oracle(hip, orc, op):
     import torch
     from tinygs_amd import _lib
     rng = np.random.default_rng(op)
     if op in (0, 2):
         x = np.concatenate([rng.uniform(-110, 90, 1 << 20), rng.uniform(-12, 0, 1 << 20)]).astype(np.float32)
+    elif op == 6:
+        x = np.concatenate([rng.uniform(-150, 0, 1 << 20), rng.uniform(-12, 0, 1 << 20),
+                            -np.arange(0, 301, dtype=np.float64) / 2]).astype(np.float32)
     elif op == 1:
         x = np.concatenate([rng.uniform(1.0, 255.0, 1 << 20), np.exp(rng.uniform(-87, 88, 1 << 20))]).astype(np.float32)
     else:
@@ -67,6 +70,8 @@ def test_detmath_bit_exact_vs_oracle(hip, orc, op):
         ref = orc.logf(x)
     elif op == 2:
         ref = orc.expf(np.where(x <= 0, x, -x).astype(np.float32))
+    elif op == 6:
+        ref = orc.exp2_core(x)
     elif op == 3:
         ref = (x / (x * np.float32(0.7) + np.float32(1.3))).astype(np.float32)
     elif op == 4:

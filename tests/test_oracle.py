@@ -31,6 +31,25 @@ def test_expf_accuracy(orc):
     assert np.all(np.abs(y[sub] - ref[sub]) <= 2 * 1.4e-45)
 
 
+def test_exp2_core_accuracy(orc):
+    """The blend forward's 2^x (degree-5 minimax, -150 <= x <= 0): within
+    2.2e-7 relative (about 4 ulps) of libm's double exp2 over the normal range,
+    2^k times the polynomial's value at 0 at the integers k, and the same
+    relative error plus half a subnormal ulp below 2^-126."""
+    rng = np.random.default_rng(3)
+    x = np.concatenate([rng.uniform(-150, 0, 400000), rng.uniform(-9, 0, 400000), -np.arange(0, 151.0),
+                        np.linspace(-0.5, 0.0, 4001)]).astype(np.float32)
+    y = orc.exp2_core(x).astype(np.float64)
+    ref = np.exp2(x.astype(np.float64))
+    normal = ref > 1.2e-38
+    rel = np.abs(y[normal] - ref[normal]) / ref[normal]
+    assert rel.max() <= 2.2e-7, rel.max()
+    ints = x == np.round(x)
+    assert np.array_equal(y[ints & normal], ref[ints & normal] * float.fromhex("0x1.000002p+0"))
+    sub = ~normal   # the polynomial's error plus half a subnormal ulp from ldexp
+    assert np.all(np.abs(y[sub] - ref[sub]) <= 2.2e-7 * ref[sub] + 0.5 * 2.0 ** -149)
+
+
 def test_expf_special(orc):
     x = np.array([0.0, -0.0, 1.0, -1.0, 89.0, -104.0, np.inf, -np.inf, np.nan], np.float32)
     y = orc.expf(x)

@@ -22,9 +22,13 @@
 // backward work item per 32-Gaussian bucket below its last contributor
 // (tmax <= len, so every bucket of an item is inside the list).
 //
-// Numerics mirror the CPU oracle: sigma = fma(dx, fma(a/2, dx, b*dy),
-// (c/2)*dy*dy), the deterministic exp, fminf alpha clamp, the 1/255 cut and
-// the 1e-4 transmittance stop with the terminating Gaussian not composited.
+// Numerics mirror the CPU oracle: alpha = min(o 2^-sigma', 0.999) with
+// sigma' = fma(dx, fma(a L/2, dx, (b L) dy), ((c L/2) dy) dy) from the conic
+// prescaled by L = log2(e) at staging and the deterministic exp2
+// (det_exp2_core), the 1/255 cut and the 1e-4 transmittance stop with the
+// terminating Gaussian not composited. A pixel that stopped (or lies outside
+// the image) carries T = 0: every later Gaussian then fails the transmittance
+// test and changes nothing, so no separate flag is kept.
 #include "common.h"
 #include "kernels.h"
 
@@ -68,8 +72,8 @@ __global__ void __launch_bounds__(256) blend_forward_kernel(CamParams cam, const
                                                             float4* __restrict__ ckpt,
                                                             uint4* __restrict__ items,
                                                             BinCtl* __restrict__ ctl) {
-    __shared__ float4 s_a[256];       // mx, my, a/2, b
-    __shared__ float4 s_b[256];       // c/2, opacity, r, g (clamped colour)
+    __shared__ float4 s_a[256];       // mx, my, a L/2, b L
+    __shared__ float4 s_b[256];       // c L/2, opacity, r, g (clamped colour)
     __shared__ float s_c[256];        // b (clamped colour)
     __shared__ uint32_t s_mask[256];  // bit q: may reach alpha >= 1/255 in 8x8 block q
     __shared__ uint16_t s_list[4][256];
@@ -87,14 +91,13 @@ __global__ void __launch_bounds__(256) blend_forward_kernel(CamParams cam, const
     const int32_t len = (int32_t)(range.y - range.x);
     const uint32_t slot0 = range.x / (uint32_t)kBucket + tile;   // first checkpoint slot of this tile
 
-    float C0 = 0.f, C1 = 0.f, C2 = 0.f, T = 1.f;
+    float C0 = 0.f, C1 = 0.f, C2 = 0.f, T = inside ? 1.f : 0.f;
     uint32_t ncontrib = 0;
     uint32_t loaded = 0;
-    bool done = !inside;
     int32_t next_ck = kBucket;   // next bucket boundary whose checkpoint this wave still owes
 
     for (int32_t base = 0; base < len; base += 256) {
-        if (__syncthreads_and(done)) break;
+        if (__syncthreads_and(T == 0.f)) break;
         const int32_t nb = min(256, len - base);
         {
             const int32_t j = base + (int32_t)tid;
@@ -104,11 +107,12 @@ __global__ void __launch_bounds__(256) blend_forward_kernel(CamParams cam, const
                 const float2 m = mean2d[p];
                 const float4 co = conic_opacity[p];
                 const float4 c = color_pt[p];
-                s_a[tid] = make_float4(m.x, m.y, 0.5f * co.x, co.y);
-                s_b[tid] = make_float4(0.5f * co.z, co.w, __builtin_fmaxf(c.x, 0.f), __builtin_fmaxf(c.y, 0.f));
+                s_a[tid] = make_float4(m.x, m.y, co.x * kHalfLog2e, co.y * kLog2eF);
+                s_b[tid] = make_float4(co.z * kHalfLog2e, co.w, __builtin_fmaxf(c.x, 0.f), __builtin_fmaxf(c.y, 0.f));
                 s_c[tid] = __builtin_fmaxf(c.z, 0.f);
-                // sigma > ln(255 o) + 1e-3 implies o exp(-sigma) < exp(-1e-3) / 255, below the 1/255 cut by far
-                // more than the error of the deterministic exp / log (< 1e-6 relative)
+                // sigma > ln(255 o) + 1e-3 implies o 2^-sigma' < exp(-1e-3) / 255 (sigma' = sigma L to a few
+                // ulps), below the 1/255 cut by far more than the error of the deterministic exp2 / log
+                // (< 1e-6 relative)
                 const float bound = c.w + 1e-3f;
 #pragma unroll
                 for (uint32_t q = 0; q < 4; ++q) {
@@ -146,26 +150,25 @@ __global__ void __launch_bounds__(256) blend_forward_kernel(CamParams cam, const
             }
             const float dx = a.x - pcx, dy = a.y - pcy;
             const float sigma = __builtin_fmaf(dx, __builtin_fmaf(a.z, dx, a.w * dy), (bb.x * dy) * dy);
-            // exp(-clamp(sigma, 0, 104)): the alpha decisions are those of
-            // det_expf_nonpos(min(-sigma, 0)) (beyond sigma 103.97 both give 0)
+            // (sigma' < 0 is rejected below, so its clamped value does not matter)
             const float alpha =
-                __builtin_fminf(bb.y * det_expf_core(-__builtin_amdgcn_fmed3f(sigma, 0.f, 104.f)), kMaxAlpha);
-            const bool ok = !done && sigma >= 0.f && alpha >= kMinAlpha;
+                __builtin_fminf(bb.y * det_exp2_core(-__builtin_amdgcn_fmed3f(sigma, 0.f, 150.f)), kMaxAlpha);
             const float nT = T * (1.0f - alpha);
-            const bool term = ok && nT < kTransmittanceMin;
-            const bool acc = ok && !term;
-            done = done || term;
+            // a stopped pixel has T = 0, so nT = 0 fails the test
+            const bool ok = sigma >= 0.f && alpha >= kMinAlpha;
+            const bool keep = nT >= kTransmittanceMin;
+            const bool acc = ok && keep;
             // one select of the weight instead of three of the sums: fma(+0, c, C)
             // is C itself for the finite colours
             const float wgt = acc ? T * alpha : 0.f;
             C0 = __builtin_fmaf(wgt, bb.z, C0);
             C1 = __builtin_fmaf(wgt, bb.w, C1);
             C2 = __builtin_fmaf(wgt, cz, C2);
-            T = acc ? nT : T;
+            T = ok ? (keep ? nT : 0.f) : T;
             ncontrib = acc ? (uint32_t)(j + 1) : ncontrib;
         };
         for (int32_t i = 0; i < cnt; i += 2) {
-            if (!__any(!done)) break;   // whole wave finished
+            if (!__any(T != 0.f)) break;   // whole wave finished
             const uint32_t pair = *(const uint32_t*)&s_list[w][i];   // i is even: 4-byte aligned
             const int32_t e0 = __builtin_amdgcn_readfirstlane((int)(pair & 0xffffu));
             const bool two = i + 1 < cnt;

@@ -17,6 +17,8 @@ constexpr float kMinAlpha = 1.0f / 255.0f;
 constexpr float kMaxAlpha = 0.999f;
 constexpr float kTransmittanceMin = 1e-4f;
 constexpr float kDilation = 0.3f;
+constexpr float kLog2eF = 0x1.715476p+0f;      // log2(e) as float
+constexpr float kHalfLog2e = 0x1.715476p-1f;   // log2(e) / 2 (exact)
 constexpr int kGradStride = 12;         // floats of per-primitive 2D gradient record
 
 // Camera and image parameters, passed to kernels by value (no pose-block copy).

@@ -62,6 +62,24 @@ TGS_HD float det_expf_core(float x) {
     return __builtin_ldexpf(p, (int)k);
 }
 
+// 2^x for -150 <= x <= 0: the blend forward's alpha = o 2^(-sigma'), with
+// sigma' = sigma log2(e) evaluated from a conic prescaled by log2(e).
+// k = rint(x), r = x - k in [-1/2, 1/2] (exact), 2^r by the degree-5 minimax
+// polynomial of relative error 7.5e-8 (Remez exchange, E. Remez 1934),
+// coefficients rounded to float; <= 2.1e-7 relative overall; exact ldexp
+// (k = -150 gives 0 or the least subnormal).
+TGS_HD float det_exp2_core(float x) {
+    const float k = __builtin_rintf(x);
+    const float r = x - k;
+    float p = 0x1.5c08e6p-10f;
+    p = __builtin_fmaf(p, r, 0x1.3d0c52p-7f);
+    p = __builtin_fmaf(p, r, 0x1.c6b6e4p-5f);
+    p = __builtin_fmaf(p, r, 0x1.ebf918p-3f);
+    p = __builtin_fmaf(p, r, 0x1.62e428p-1f);
+    p = __builtin_fmaf(p, r, 0x1.000002p+0f);
+    return __builtin_ldexpf(p, (int)k);
+}
+
 // e^x for x <= 0 (the blend's exp(-sigma)); same bits as det_expf there.
 TGS_HD float det_expf_nonpos(float x) {
     x = x < -103.97208404541015625f ? -104.0f : x;  // -104 -> k=-150, ldexp gives 0

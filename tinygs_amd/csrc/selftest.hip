@@ -18,6 +18,7 @@ __global__ void detmath_kernel(int op, const float* in, float* out, int64_t n) {
         case 3: y = x / (x * 0.7f + 1.3f); break;       // correctly rounded division
         case 4: y = __builtin_sqrtf(x); break;           // correctly rounded sqrt
         case 5: y = __half2float(__float2half_rn(x)); break;
+        case 6: y = det_exp2_core(x); break;   // -150 <= x <= 0
         default: y = 0.f; break;
     }
     out[i] = y;
