@@ -32,7 +32,7 @@ namespace tgs {
 constexpr int kThreads = 256;
 constexpr int kScanRounds = 16;
 constexpr int kScanChunk = kThreads * kScanRounds;     // 4096 elements per scan workgroup
-constexpr int kDepthKeysPerThread = 8;                  // depth passes: 2048 keys per workgroup
+constexpr int kDepthKeysPerThread = 16;                 // depth passes: 4096 keys per workgroup
 constexpr int kTileKeysPerThread = 8;                   // tile passes: 2048 keys per workgroup (4096 measured 7 us slower)
 constexpr int kDepthMaxDigits = 512;                    // depth passes: digits of up to 9 bits
 constexpr int kTileMaxDigits = 256;                     // tile passes: digits of up to 8 bits
