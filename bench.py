@@ -97,7 +97,10 @@ def algorithmic_bytes(stage, c):
     if stage == "depth_sort":
         return 8 * V + 8 * V + 8 * V   # read keys/values once, write one permutation
     if stage == "emit_instances":
-        return 44 * V + 12 * I
+        # per visible primitive: index and offset read, 16-byte emission record read, first slot written
+        # (the 32-byte record only for primitives past 32 rect tiles: not counted); per instance: the
+        # (tile, primitive) pair written
+        return 28 * V + 8 * I
     if stage == "tile_sort":
         return 24 * I + 8 * I + 8 * T
     return 0

@@ -492,9 +492,12 @@ __device__ __forceinline__ bool will_contribute_e(float mx, float my, float ca, 
     return max_power <= power_threshold;
 }
 
-// Thread per depth-sorted primitive: its 32-byte binning record is gathered
-// once (one aligned 32-byte read) and its instances fill the slots
-// [offs[k], offs[k + 1]), so the instance array comes out in depth order.
+// Thread per depth-sorted primitive: its 16-byte emission record (bounds and
+// the preprocess's outcomes for rect tiles 0..31) is gathered once, the
+// 32-byte binning record (mean, conic, threshold) only for primitives with
+// more than 32 rect tiles; its instances fill the slots [offs[k], offs[k + 1]),
+// so the instance array comes out in depth order. (The gathers are random:
+// depth order is not index order, and each costs a whole memory line.)
 // The workgroup's 256 primitives own one contiguous slot range; when it fits
 // in LDS the instances are staged there and written out by consecutive
 // threads (contiguous stores), otherwise written directly.
@@ -516,7 +519,7 @@ template <bool kHalf>
 __global__ void __launch_bounds__(256) emit_kernel(const uint32_t* __restrict__ prims,
                                                    const uint32_t* __restrict__ offs, BinCtl* ctl,
                                                    int64_t max_count, int64_t max_inst, const uint4* __restrict__ rec,
-                                                   const uint32_t* __restrict__ tile_bits, uint32_t grid_w,
+                                                   const uint4* __restrict__ erec, uint32_t grid_w,
                                                    uint32_t* __restrict__ inst_keys,
                                                    uint32_t* __restrict__ inst_vals,
                                                    uint32_t* __restrict__ first_slot) {
@@ -559,19 +562,22 @@ __global__ void __launch_bounds__(256) emit_kernel(const uint32_t* __restrict__ 
         // it are still all written, so the sorted prefix holds valid pairs only
         if ((int64_t)off + cap > max_inst) cap = (int64_t)off < max_inst ? (uint32_t)(max_inst - off) : 0u;
         first_slot[p] = off;
-        bits = tile_bits[p];
-        const uint4 r0 = rec[2 * (size_t)p], r1 = rec[2 * (size_t)p + 1];
-        x0 = r0.x & 0xffffu; x1 = r0.x >> 16; y0 = r0.y & 0xffffu; y1 = r0.y >> 16;
-        smx = u2f(r0.z) - 0.5f;
-        smy = u2f(r0.w) - 0.5f;
-        cw0 = r1.x; cw1 = r1.y; cw2 = r1.z; pt = u2f(r1.w);
+        const uint4 e = erec[p];
+        x0 = e.x & 0xffffu; x1 = e.x >> 16; y0 = e.y & 0xffffu; y1 = e.y >> 16;
+        bits = e.z;
+        if ((x1 - x0) * (y1 - y0) > 32u) {   // tiles past the first 32 need the exact test
+            const uint4 r0 = rec[2 * (size_t)p], r1 = rec[2 * (size_t)p + 1];
+            smx = u2f(r0.z) - 0.5f;
+            smy = u2f(r0.w) - 0.5f;
+            cw0 = r1.x; cw1 = r1.y; cw2 = r1.z; pt = u2f(r1.w);
+        }
     }
     const uint32_t bw = x1 - x0;
     const uint32_t nrect = bw * (y1 - y0);
     uint32_t written = 0;
     if (active) {
         const uint32_t first = nrect < 8u ? nrect : 8u;
-        // rect tiles 0..31 were tested by the preprocess (tile_bits)
+        // rect tiles 0..31 were tested by the preprocess (emission record)
         for (uint32_t q = 0; q < first; ++q) {
             const uint32_t tx = x0 + q % bw, ty = y0 + q / bw;
             if (((bits >> q) & 1u) && written < cap) {
@@ -618,16 +624,16 @@ __global__ void __launch_bounds__(256) emit_kernel(const uint32_t* __restrict__ 
 }
 
 void launch_emit_instances(const uint32_t* prims, const uint32_t* offs, BinCtl* ctl, int64_t max_count,
-                           int64_t max_inst, const uint4* rec, const uint32_t* tile_bits, uint32_t grid_w,
+                           int64_t max_inst, const uint4* rec, const uint4* erec, uint32_t grid_w,
                            uint32_t* inst_keys, uint32_t* inst_vals, uint32_t* first_slot, bool half_test,
                            hipStream_t s) {
     if (max_count <= 0) return;
     const unsigned grid = (unsigned)((max_count + 255) / 256);
     if (half_test)
-        emit_kernel<true><<<grid, 256, 0, s>>>(prims, offs, ctl, max_count, max_inst, rec, tile_bits, grid_w,
+        emit_kernel<true><<<grid, 256, 0, s>>>(prims, offs, ctl, max_count, max_inst, rec, erec, grid_w,
                                                inst_keys, inst_vals, first_slot);
     else
-        emit_kernel<false><<<grid, 256, 0, s>>>(prims, offs, ctl, max_count, max_inst, rec, tile_bits, grid_w,
+        emit_kernel<false><<<grid, 256, 0, s>>>(prims, offs, ctl, max_count, max_inst, rec, erec, grid_w,
                                                 inst_keys, inst_vals, first_slot);
 }
 

@@ -36,8 +36,10 @@ struct GradView {
 // ---- preprocess (kernels_forward.cuh:157-412)
 // rec: 2 x uint4 per visible primitive: {x_min | x_max << 16, y_min | y_max << 16, mean2d.x, mean2d.y},
 // {conic a, b, c, ln(255 opacity)} (float bits).
-// tile_bits[i]: exact-test outcome of the primitive's rect tiles 0..31 (row-major in the rect).
-void launch_preprocess(const GaussianView& g, const CamParams& cam, uint32_t* n_touched, uint32_t* tile_bits,
+// erec[i] (emission record, 16 B, the part the instance emission always reads):
+// {x_min | x_max << 16, y_min | y_max << 16, exact-test outcome of the rect
+// tiles 0..31 (bit k: row-major rect tile k), 0}.
+void launch_preprocess(const GaussianView& g, const CamParams& cam, uint32_t* n_touched, uint4* erec,
                        uint4* rec,
                        float2* mean2d, float4* conic_opacity, float4* color_pt, uint32_t* depth_key,
                        float* densif, hipStream_t s);
@@ -99,7 +101,7 @@ int radix_sort(uint32_t* keys[2], uint32_t* vals[2], uint32_t* v2[2], const uint
 // beyond max_inst (the instance buffers' size) are never written; offsets
 // that would need them set bit 1 of ctl->err.
 void launch_emit_instances(const uint32_t* prims, const uint32_t* offs, BinCtl* ctl, int64_t max_count,
-                           int64_t max_inst, const uint4* rec, const uint32_t* tile_bits, uint32_t grid_w,
+                           int64_t max_inst, const uint4* rec, const uint4* erec, uint32_t grid_w,
                            uint32_t* inst_keys, uint32_t* inst_vals, uint32_t* first_slot, bool half_test,
                            hipStream_t s);
 // [start, end) per tile, (0, 0) for empty tiles; every entry written. The
@@ -112,7 +114,7 @@ bool radix_digits_fit(bool depth, int n_passes, const int* bits);
 // ---- fp16-image rasterizer (FGS16, tinygs/src/rasterizer/fastgs_ours_fp16/)
 // Preprocess: as launch_preprocess with the FGS16 rules; info[i] = (conic a | b
 // << 16, c | opacity << 16 (halves), r | g << 8 | b << 16, 0).
-void launch_preprocess16(const GaussianView& g, const CamParams& cam, uint32_t* n_touched, uint32_t* tile_bits,
+void launch_preprocess16(const GaussianView& g, const CamParams& cam, uint32_t* n_touched, uint4* erec,
                          uint4* rec, float2* mean2d, float4* conic_opacity, uint4* info, uint32_t* depth_key,
                          float* densif, hipStream_t s);
 

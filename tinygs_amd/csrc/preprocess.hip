@@ -85,7 +85,7 @@ template <typename ShT>
 __global__ void __launch_bounds__(256) preprocess_kernel(
     const float* __restrict__ means, const float* __restrict__ scales, const float* __restrict__ rots,
     const float* __restrict__ opac, const ShT* __restrict__ sh0, const ShT* __restrict__ shr, int64_t n, int bases,
-    CamParams cam, uint32_t* __restrict__ n_touched, uint32_t* __restrict__ tile_bits, uint4* __restrict__ rec,
+    CamParams cam, uint32_t* __restrict__ n_touched, uint4* __restrict__ erec, uint4* __restrict__ rec,
     float2* __restrict__ mean2d, float4* __restrict__ conic_opacity, float4* __restrict__ color_pt, uint32_t* __restrict__ depth_key,
     float4* __restrict__ densif) {
     // SH-rest coefficients of the block's 256 primitives are one contiguous
@@ -250,7 +250,7 @@ __global__ void __launch_bounds__(256) preprocess_kernel(
         return;
     }
     n_touched[i] = cnt;
-    tile_bits[i] = bits;
+    erec[i] = make_uint4(xmin | (xmax << 16), ymin | (ymax << 16), bits, 0u);
     // 32-byte binning record, gathered once per primitive by the emission
     rec[2 * i] = make_uint4(xmin | (xmax << 16), ymin | (ymax << 16), f2u(m2x), f2u(m2y));
     rec[2 * i + 1] = make_uint4(f2u(ca), f2u(cb), f2u(cc), f2u(pthr));
@@ -268,7 +268,7 @@ __global__ void __launch_bounds__(256) preprocess_kernel(
 // still in [near, far]), the quaternion read only for active primitives, a
 // half conic and opacity, the power threshold from the half opacity, the
 // half tile test (fgs16.h) and an 8-bit colour, saturate(c) * 255 truncated
-// (rasterization_config.h:104-108). Outputs: n_touched, tile_bits and the
+// (rasterization_config.h:104-108). Outputs: n_touched, the emission record and the
 // binning record as the fp32 preprocess (conic and opacity halves in the
 // record's second half), mean2d, conic_opacity (the halves as floats) and
 // info[i] = (a | b << 16, c | opacity << 16, r | g << 8 | b << 16, 0).
@@ -276,7 +276,7 @@ template <typename ShT>
 __global__ void __launch_bounds__(256) preprocess16_kernel(
     const float* __restrict__ means, const float* __restrict__ scales, const float* __restrict__ rots,
     const float* __restrict__ opac, const ShT* __restrict__ sh0, const ShT* __restrict__ shr, int64_t n, int bases,
-    CamParams cam, uint32_t* __restrict__ n_touched, uint32_t* __restrict__ tile_bits, uint4* __restrict__ rec,
+    CamParams cam, uint32_t* __restrict__ n_touched, uint4* __restrict__ erec, uint4* __restrict__ rec,
     float2* __restrict__ mean2d, float4* __restrict__ conic_opacity, uint4* __restrict__ info,
     uint32_t* __restrict__ depth_key, float4* __restrict__ densif) {
     __shared__ __align__(16) ShT s_sh[256 * 45];
@@ -443,7 +443,7 @@ __global__ void __launch_bounds__(256) preprocess16_kernel(
         return;
     }
     n_touched[i] = cnt;
-    tile_bits[i] = bits;
+    erec[i] = make_uint4(xmin | (xmax << 16), ymin | (ymax << 16), bits, 0u);
     const uint32_t c01 = (uint32_t)hbits(hca) | ((uint32_t)hbits(hcb) << 16);
     const uint32_t c2o = (uint32_t)hbits(hcc) | ((uint32_t)hbits(opacity) << 16);
     rec[2 * i] = make_uint4(xmin | (xmax << 16), ymin | (ymax << 16), f2u(m2x), f2u(m2y));
@@ -458,7 +458,7 @@ __global__ void __launch_bounds__(256) preprocess16_kernel(
     depth_key[i] = f2u(depth);
 }
 
-void launch_preprocess16(const GaussianView& g, const CamParams& cam, uint32_t* n_touched, uint32_t* tile_bits,
+void launch_preprocess16(const GaussianView& g, const CamParams& cam, uint32_t* n_touched, uint4* erec,
                          uint4* rec, float2* mean2d, float4* conic_opacity, uint4* info, uint32_t* depth_key,
                          float* densif, hipStream_t s) {
     if (g.n <= 0) return;
@@ -467,16 +467,16 @@ void launch_preprocess16(const GaussianView& g, const CamParams& cam, uint32_t* 
     if (g.sh_dtype == kShF16)
         preprocess16_kernel<__half><<<grid, 256, 0, s>>>(g.means, g.scales, g.rotations, g.opacities,
                                                          (const __half*)g.sh0, (const __half*)g.sh_rest, g.n, bases,
-                                                         cam, n_touched, tile_bits, rec, mean2d, conic_opacity, info,
+                                                         cam, n_touched, erec, rec, mean2d, conic_opacity, info,
                                                          depth_key, (float4*)densif);
     else
         preprocess16_kernel<float><<<grid, 256, 0, s>>>(g.means, g.scales, g.rotations, g.opacities,
                                                         (const float*)g.sh0, (const float*)g.sh_rest, g.n, bases, cam,
-                                                        n_touched, tile_bits, rec, mean2d, conic_opacity, info,
+                                                        n_touched, erec, rec, mean2d, conic_opacity, info,
                                                         depth_key, (float4*)densif);
 }
 
-void launch_preprocess(const GaussianView& g, const CamParams& cam, uint32_t* n_touched, uint32_t* tile_bits,
+void launch_preprocess(const GaussianView& g, const CamParams& cam, uint32_t* n_touched, uint4* erec,
                        uint4* rec, float2* mean2d, float4* conic_opacity, float4* color_pt, uint32_t* depth_key, float* densif,
                        hipStream_t s) {
     if (g.n <= 0) return;
@@ -485,12 +485,12 @@ void launch_preprocess(const GaussianView& g, const CamParams& cam, uint32_t* n_
     if (g.sh_dtype == kShF16) {
         preprocess_kernel<__half><<<grid, 256, 0, s>>>(g.means, g.scales, g.rotations, g.opacities,
                                                        (const __half*)g.sh0, (const __half*)g.sh_rest, g.n, bases,
-                                                       cam, n_touched, tile_bits, rec, mean2d, conic_opacity,
+                                                       cam, n_touched, erec, rec, mean2d, conic_opacity,
                                                        color_pt, depth_key, (float4*)densif);
     } else {
         preprocess_kernel<float><<<grid, 256, 0, s>>>(g.means, g.scales, g.rotations, g.opacities,
                                                       (const float*)g.sh0, (const float*)g.sh_rest, g.n, bases, cam,
-                                                      n_touched, tile_bits, rec, mean2d, conic_opacity, color_pt,
+                                                      n_touched, erec, rec, mean2d, conic_opacity, color_pt,
                                                       depth_key,
                                                       (float4*)densif);
     }
