@@ -261,6 +261,21 @@ int tgs_adam_step(tgs_adam* a, float scale, void* stream);
  * TGS_BACKWARD_SPARSE backward). Same results as tgs_adam_step on gradients
  * whose unmarked rows are zero. No counterpart in the reference. */
 int tgs_adam_step_masked(tgs_adam* a, float scale, const uint8_t* row_mask, void* stream);
+/* tgs_adam_step_masked with flags (row_mask may be NULL). TGS_ADAM_DEVICE_STEP:
+ * the step count and the bias corrections (simple_adam.cu:475-480, in double
+ * rounded to float, the same values as the host computes) live on the device
+ * and are advanced by a kernel of the step, so the launch sequence is the
+ * same every step and a captured step replays with the right count. The
+ * first device step after creation, a host-counted step or a reset seeds the
+ * device count from the host's (capture only after one device step); graph
+ * replays advance only the device count (tgs_adam_device_steps reads it).
+ * No counterpart in the reference (its bias corrections are host
+ * arithmetic per step). */
+#define TGS_ADAM_DEVICE_STEP 1
+int tgs_adam_step_ex(tgs_adam* a, float scale, const uint8_t* row_mask, int32_t flags, void* stream);
+/* The step count of the device-step mode (synchronises the stream; the host
+ * count when no device step was taken since the last host-counted one). */
+int tgs_adam_device_steps(tgs_adam* a, int64_t* steps, void* stream);
 /* OptimizerBase::reset(): zero moments and the step counter. */
 int tgs_adam_reset(tgs_adam* a, void* stream);
 int64_t tgs_adam_global_steps(tgs_adam* a);

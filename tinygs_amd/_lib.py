@@ -17,6 +17,7 @@ LIB_PATH = os.path.join(HERE, "libtinygs_amd.so")
 TGS_DTYPE_FLOAT32 = 0
 TGS_DTYPE_FLOAT16 = 1
 TGS_DTYPE_UINT8 = 2
+TGS_ADAM_DEVICE_STEP = 1
 TGS_LOSS_ASSIGN = 1
 TGS_BACKWARD_ASSIGN = 1
 TGS_BACKWARD_SPARSE = 2
@@ -140,6 +141,8 @@ SIGNATURES = {
     "tgs_selftest_wave": ([P, P, P], C.c_int),
     "tgs_selftest_half": ([C.c_int32, P, P, P, P, C.c_int64, P], C.c_int),
     "tgs_selftest_half_div_exhaustive": ([P, P], C.c_int),
+    "tgs_adam_step_ex": ([P, C.c_float, P, C.c_int32, P], C.c_int),
+    "tgs_adam_device_steps": ([P, C.POINTER(C.c_int64), P], C.c_int),
 }
 
 

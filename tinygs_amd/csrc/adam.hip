@@ -40,7 +40,7 @@ constexpr int kAdamVecPerThread = 2;                       // 4-element vectors 
 constexpr int kAdamChunk = kAdamThreads * kAdamVecPerThread * 4;
 
 __device__ __forceinline__ float adam_one(float th, float gr_raw, float& m, float& v, const AdamGroup& g,
-                                          const AdamArgs& a, float t1, float t2) {
+                                          const AdamArgs& a, float t1, float t2, float bc1, float bc2_sqrt) {
     float gr = a.grad_scale * gr_raw;
     if (g.decay_coef != 0.0f) {
         if (g.decay_kind == 1) {
@@ -59,8 +59,8 @@ __device__ __forceinline__ float adam_one(float th, float gr_raw, float& m, floa
         m = __builtin_fmaf(t1, gr, __builtin_fmaf(-t1, m, m));
         v = __builtin_fmaf(t2, gg, __builtin_fmaf(-t2, v, v));
     }
-    const float mh = m / a.bc1;
-    const float den = __builtin_sqrtf(v) / a.bc2_sqrt + a.eps;
+    const float mh = m / bc1;
+    const float den = __builtin_sqrtf(v) / bc2_sqrt + a.eps;
     return th - (mh * g.lr) / den;
 }
 
@@ -85,6 +85,11 @@ __global__ void __launch_bounds__(kAdamThreads) adam_kernel(AdamLaunch L) {
         if (k < L.a.n_groups && b >= L.block_start[k]) gi = k;
     const AdamGroup& g = L.a.groups[gi];
     const float t1 = 1.0f - L.a.beta1, t2 = 1.0f - L.a.beta2;
+    float bc1 = L.a.bc1, bc2s = L.a.bc2_sqrt;
+    if (L.a.dev_bc) {   // written by adam_bias_kernel just before on the same stream
+        bc1 = u2f(L.a.dev_bc[1]);
+        bc2s = u2f(L.a.dev_bc[2]);
+    }
     const int64_t vbase = (b - L.block_start[gi]) * (kAdamChunk / 4) + threadIdx.x;
     float th[kAdamVecPerThread][4];
     float4 gv[kAdamVecPerThread], mv[kAdamVecPerThread], vv[kAdamVecPerThread];
@@ -121,10 +126,10 @@ __global__ void __launch_bounds__(kAdamThreads) adam_kernel(AdamLaunch L) {
     for (int k = 0; k < kAdamVecPerThread; ++k) {
         const int64_t e0 = 4 * (vbase + (int64_t)k * kAdamThreads);
         if (full[k]) {
-            th[k][0] = adam_one(th[k][0], gv[k].x, mv[k].x, vv[k].x, g, L.a, t1, t2);
-            th[k][1] = adam_one(th[k][1], gv[k].y, mv[k].y, vv[k].y, g, L.a, t1, t2);
-            th[k][2] = adam_one(th[k][2], gv[k].z, mv[k].z, vv[k].z, g, L.a, t1, t2);
-            th[k][3] = adam_one(th[k][3], gv[k].w, mv[k].w, vv[k].w, g, L.a, t1, t2);
+            th[k][0] = adam_one(th[k][0], gv[k].x, mv[k].x, vv[k].x, g, L.a, t1, t2, bc1, bc2s);
+            th[k][1] = adam_one(th[k][1], gv[k].y, mv[k].y, vv[k].y, g, L.a, t1, t2, bc1, bc2s);
+            th[k][2] = adam_one(th[k][2], gv[k].z, mv[k].z, vv[k].z, g, L.a, t1, t2, bc1, bc2s);
+            th[k][3] = adam_one(th[k][3], gv[k].w, mv[k].w, vv[k].w, g, L.a, t1, t2, bc1, bc2s);
             if (g.theta_half) {
                 uint2 hv;
                 __half* h = (__half*)&hv;
@@ -140,7 +145,7 @@ __global__ void __launch_bounds__(kAdamThreads) adam_kernel(AdamLaunch L) {
                 float t = g.theta_half ? __half2float(((const __half*)g.theta)[i]) : ((const float*)g.theta)[i];
                 float m = g.m1[i], v = g.m2[i];
                 const bool live = !L.a.row_mask || L.a.row_mask[row_of((uint32_t)i, g.row_width)] != 0;
-                t = adam_one(t, live ? g.grad[i] : 0.f, m, v, g, L.a, t1, t2);
+                t = adam_one(t, live ? g.grad[i] : 0.f, m, v, g, L.a, t1, t2, bc1, bc2s);
                 if (g.theta_half)
                     ((__half*)g.theta)[i] = __float2half_rn(t);
                 else
@@ -150,6 +155,28 @@ __global__ void __launch_bounds__(kAdamThreads) adam_kernel(AdamLaunch L) {
             }
         }
     }
+}
+
+// The device-side step count of a captured (or replayed) step.
+__global__ void adam_seed_steps_kernel(uint32_t* state, uint32_t steps) {
+    if (threadIdx.x == 0) state[0] = steps;
+}
+
+__global__ void adam_bias_kernel(uint32_t* state, float beta1, float beta2) {
+    if (threadIdx.x != 0) return;
+    const uint32_t t = state[0] + 1u;
+    const double st = (double)t;
+    state[0] = t;
+    state[1] = f2u((float)(1.0 - pow((double)beta1, st)));
+    state[2] = f2u((float)sqrt(1.0 - pow((double)beta2, st)));
+}
+
+void launch_adam_seed_steps(uint32_t* state, uint32_t steps, hipStream_t s) {
+    adam_seed_steps_kernel<<<1, 64, 0, s>>>(state, steps);
+}
+
+void launch_adam_bias(uint32_t* state, float beta1, float beta2, hipStream_t s) {
+    adam_bias_kernel<<<1, 64, 0, s>>>(state, beta1, beta2);
 }
 
 void launch_adam(const AdamArgs& a, hipStream_t s) {

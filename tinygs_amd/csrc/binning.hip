@@ -173,7 +173,7 @@ __global__ void __launch_bounds__(kThreads) compact_kernel(const uint32_t* __res
     uint32_t total;
     striped_scan16_u32(vis, ex, &total, s_rw);   // barriers inside: s_nt visible after it
     if (w == 0) {
-        const uint32_t excl = wave_look_back(status, bid, total, epoch, &ctl->err);
+        const uint32_t excl = wave_look_back(status, bid, total, ctl->epoch_base + epoch, &ctl->err);
         if (lane == 0) {
             s_base = excl;
             if ((int64_t)(bid + 1) * kScanChunk >= n) ctl->V = excl + total;
@@ -226,7 +226,7 @@ __global__ void __launch_bounds__(kThreads) offsets_kernel(const uint32_t* __res
     uint32_t total;
     striped_scan16_u32(c, ex, &total, s_rw);
     if (w == 0) {
-        const uint32_t excl = wave_look_back(status, bid, total, epoch, &ctl->err);
+        const uint32_t excl = wave_look_back(status, bid, total, ctl->epoch_base + epoch, &ctl->err);
         if (lane == 0) {
             s_base = excl;
             if ((int64_t)(bid + 1) * kScanChunk >= n) offs[n] = excl + total;
@@ -306,7 +306,8 @@ __global__ void __launch_bounds__(kThreads) radix_upsweep_kernel(const uint32_t*
 // every (digit, workgroup) output offset: digit start + counts of earlier
 // workgroups for that digit.
 __global__ void __launch_bounds__(kThreads) exclusive_scan_kernel(uint32_t* __restrict__ data, int64_t n,
-                                                                  uint32_t* ticket, uint64_t* status, uint32_t epoch,
+                                                                  uint32_t* ticket, uint64_t* status,
+                                                                  const uint32_t* epoch_base, uint32_t epoch,
                                                                   uint32_t* err) {
     __shared__ uint32_t s_rw[64];
     __shared__ uint32_t s_bid, s_base;
@@ -322,7 +323,7 @@ __global__ void __launch_bounds__(kThreads) exclusive_scan_kernel(uint32_t* __re
     uint32_t total;
     striped_scan16_u32(c, ex, &total, s_rw);
     if (w == 0) {
-        const uint32_t excl = wave_look_back(status, bid, total, epoch, err);
+        const uint32_t excl = wave_look_back(status, bid, total, *epoch_base + epoch, err);
         if (lane == 0) s_base = excl;
     }
     __syncthreads();
@@ -431,7 +432,8 @@ int64_t radix_count_entries(int64_t max_n, bool depth) {
 template <int KPT, int MAXB>
 static int radix_passes(uint32_t* keys[2], uint32_t* vals[2], uint32_t* v2[2], const uint32_t* d_n, int64_t max_n,
                         int n_passes, const int* shifts, const int* bits, uint32_t* counts, uint32_t* tickets,
-                        uint64_t* status, uint32_t& epoch, uint32_t* err, hipStream_t s) {
+                        uint64_t* status, const uint32_t* epoch_base, uint32_t& epoch, uint32_t* err,
+                        hipStream_t s) {
     int cur = 0;
     if (max_n <= 0) return cur;
     const uint32_t nb = (uint32_t)((max_n + kThreads * KPT - 1) / (kThreads * KPT));
@@ -441,7 +443,7 @@ static int radix_passes(uint32_t* keys[2], uint32_t* vals[2], uint32_t* v2[2], c
         radix_upsweep_kernel<KPT, MAXB><<<nb, kThreads, 0, s>>>(keys[cur], d_n, max_n, shifts[p], bits[p], counts,
                                                                  nb);
         exclusive_scan_kernel<<<(unsigned)((cn + kScanChunk - 1) / kScanChunk), kThreads, 0, s>>>(
-            counts, cn, tickets + p, status, ++epoch, err);
+            counts, cn, tickets + p, status, epoch_base, ++epoch, err);
         if (v2)
             radix_downsweep_kernel<KPT, true, MAXB><<<nb, kThreads, 0, s>>>(
                 keys[cur], vals[cur], v2[cur], keys[cur ^ 1], vals[cur ^ 1], v2[cur ^ 1], d_n, max_n, shifts[p],
@@ -457,12 +459,12 @@ static int radix_passes(uint32_t* keys[2], uint32_t* vals[2], uint32_t* v2[2], c
 
 int radix_sort(uint32_t* keys[2], uint32_t* vals[2], uint32_t* v2[2], const uint32_t* d_n, int64_t max_n, bool depth,
                int n_passes, const int* shifts, const int* bits, uint32_t* counts, uint32_t* tickets,
-               uint64_t* status, uint32_t& epoch, uint32_t* err, hipStream_t s) {
+               uint64_t* status, const uint32_t* epoch_base, uint32_t& epoch, uint32_t* err, hipStream_t s) {
     if (depth)
         return radix_passes<kDepthKeysPerThread, kDepthMaxDigits>(keys, vals, v2, d_n, max_n, n_passes, shifts, bits,
-                                                                  counts, tickets, status, epoch, err, s);
+                                                                  counts, tickets, status, epoch_base, epoch, err, s);
     return radix_passes<kTileKeysPerThread, kTileMaxDigits>(keys, vals, v2, d_n, max_n, n_passes, shifts, bits,
-                                                            counts, tickets, status, epoch, err, s);
+                                                            counts, tickets, status, epoch_base, epoch, err, s);
 }
 
 // ---------------------------------------------------------------- instance emission
@@ -644,15 +646,19 @@ __global__ void fill_u32_kernel(uint32_t* p, uint32_t v, int64_t n) {
     if (i < n) p[i] = v;
 }
 
-__global__ void bin_ctl_reset_kernel(uint32_t* p, uint32_t n_words, uint32_t keep) {
+__global__ void bin_ctl_reset_kernel(uint32_t* p, uint32_t n_words, uint32_t keep, uint32_t epoch_word) {
     const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i < n_words && i != keep) p[i] = 0u;
+    if (i == epoch_word)
+        p[i] = (p[i] + kEpochStride) & kEpochMask;
+    else if (i < n_words && i != keep)
+        p[i] = 0u;
 }
 
 void launch_bin_ctl_reset(BinCtl* ctl, hipStream_t s) {
     constexpr uint32_t words = sizeof(BinCtl) / 4;
     bin_ctl_reset_kernel<<<(words + 255) / 256, 256, 0, s>>>((uint32_t*)ctl, words,
-                                                             (uint32_t)(offsetof(BinCtl, err) / 4));
+                                                             (uint32_t)(offsetof(BinCtl, err) / 4),
+                                                             (uint32_t)(offsetof(BinCtl, epoch_base) / 4));
 }
 
 void launch_fill_u32(uint32_t* p, uint32_t value, int64_t n, hipStream_t s) {

@@ -226,7 +226,10 @@ struct tgs_rasterizer {
     DevBuf bin_ctl;     // BinCtl (zeroed at creation; all but err cleared every forward)
     hipEvent_t ev_counts = nullptr;   // recorded after the counts copy of a forward
     DevBuf lb_status;   // look-back status words (u64), epoch-tagged
-    uint32_t epoch = 0; // last look-back epoch used on lb_status
+    // look-back launches of the current forward so far: its k-th launch uses
+    // epoch BinCtl::epoch_base + k (the base advances on the device per forward)
+    uint32_t epoch = 0;
+    uint64_t forwards = 0;   // forwards queued by this host (eager; graph replays not counted)
     uint32_t* h_counters = nullptr;   // pinned copy of BinCtl {V, I, err}
     // state of the last forward
     bool fwd_done = false;
@@ -240,15 +243,13 @@ struct tgs_rasterizer {
 };
 
 // Look-back status words for `entries` slots. A (re)allocated array is
-// cleared (all words "not ready"); the epoch restarts before it could wrap.
+// cleared (all words "not ready"), and so is the array once every 2^22
+// forwards, long before the 30-bit epochs (2^24 forwards apart) could alias.
 static int ensure_status(tgs_rasterizer* r, int64_t entries, hipStream_t s) {
     const void* before = r->lb_status.p;
     TGS_TRY(ensure(r->lb_status, sizeof(uint64_t) * (size_t)(entries > 0 ? entries : 1), s));
-    const bool wrap = r->epoch > kEpochMask - 64u;
-    if (r->lb_status.p != before || wrap) {
+    if (r->lb_status.p != before || (r->forwards & ((1ull << 22) - 1ull)) == 0)
         launch_fill_u32(r->lb_status.as<uint32_t>(), 0u, (int64_t)(r->lb_status.bytes / 4), s);
-        if (wrap) r->epoch = 0;
-    }
     return TGS_OK;
 }
 
@@ -280,6 +281,8 @@ struct tgs_adam {
     tgs_adam_params p{};
     float global_lr = 1.0f;
     int64_t steps = 0;
+    DevBuf dev_state;           // TGS_ADAM_DEVICE_STEP: step count and bias corrections on the device
+    bool dev_seeded = false;    // dev_state's count equals `steps` (set by the first device step)
 };
 
 extern "C" {
@@ -457,6 +460,8 @@ static int rasterizer_forward(tgs_rasterizer* r, const tgs_camera* camera, void*
     GaussianView gv = view_of(r->g);
     BinCtl* ctl = r->bin_ctl.as<BinCtl>();
     uint64_t* status = r->lb_status.as<uint64_t>();
+    // the same launch sequence, epochs included, every forward: what a graph replays
+    r->epoch = 0;
     launch_bin_ctl_reset(ctl, s);
     {
         StageScope sc(ST_PRE, s);
@@ -485,7 +490,7 @@ static int rasterizer_forward(tgs_rasterizer* r, const tgs_camera* camera, void*
             TGS_HIP(hipEventRecord(r->ev_counts, s));
         }
         psel = radix_sort(pk, pv, pn, &ctl->V, n, true, sp.n_dp, sp.dshift, sp.dbits, r->radix_counts.as<uint32_t>(),
-                          ctl->tickets + kTicketDepth, status, r->epoch, &ctl->err, s);
+                          ctl->tickets + kTicketDepth, status, &ctl->epoch_base, r->epoch, &ctl->err, s);
         if (psel < 0) return fail(TGS_ERR_STATE, "depth sort digit width");
         r->depth_key_base = sp.key_base;
         launch_instance_offsets(pn[psel], n, r->offs.as<uint32_t>(), ctl, status, r->epoch, s);
@@ -522,8 +527,10 @@ static int rasterizer_forward(tgs_rasterizer* r, const tgs_camera* camera, void*
     {
         StageScope sc(ST_TILES, s);
         isel = radix_sort(ik, iv, nullptr, d_inst, cap, false, sp.n_tp, sp.tshift, sp.tbits,
-                          r->radix_counts.as<uint32_t>(), ctl->tickets + kTicketTile, status, r->epoch, &ctl->err, s);
+                          r->radix_counts.as<uint32_t>(), ctl->tickets + kTicketTile, status, &ctl->epoch_base,
+                          r->epoch, &ctl->err, s);
         if (isel < 0) return fail(TGS_ERR_STATE, "tile sort digit width");
+        if (r->epoch >= kEpochStride) return fail(TGS_ERR_STATE, "look-back launches per forward exceed the epoch stride");
         launch_tile_ranges(ik[isel], d_inst, cap, r->ranges.as<uint2>(), T, s);
     }
     if (nosync) launch_capacity_check(ctl, cap, s);
@@ -548,6 +555,7 @@ static int rasterizer_forward(tgs_rasterizer* r, const tgs_camera* camera, void*
     r->psel = psel;
     r->isel = isel;
     r->fgs16 = f16;
+    r->forwards += 1;
     r->fwd_done = true;
     r->bwd_queues_clear = true;
     return TGS_OK;
@@ -932,6 +940,7 @@ int tgs_adam_destroy(tgs_adam* a) {
         release(a->m1[k]);
         release(a->m2[k]);
     }
+    release(a->dev_state);
     delete a;
     return TGS_OK;
 }
@@ -969,10 +978,28 @@ int tgs_adam_set_gaussians(tgs_adam* a, const tgs_gaussians* params, const tgs_g
     return TGS_OK;
 }
 
-int tgs_adam_step(tgs_adam* a, float scale, void* stream) { return tgs_adam_step_masked(a, scale, nullptr, stream); }
+int tgs_adam_step(tgs_adam* a, float scale, void* stream) { return tgs_adam_step_ex(a, scale, nullptr, 0, stream); }
 
 int tgs_adam_step_masked(tgs_adam* a, float scale, const uint8_t* row_mask, void* stream) {
+    return tgs_adam_step_ex(a, scale, row_mask, 0, stream);
+}
+
+int tgs_adam_step_ex(tgs_adam* a, float scale, const uint8_t* row_mask, int32_t flags, void* stream) {
     if (!a) return fail(TGS_ERR_INVALID, "NULL argument");
+    if (flags & ~TGS_ADAM_DEVICE_STEP) return fail(TGS_ERR_INVALID, "unknown Adam step flags 0x%x", flags);
+    const bool dev = (flags & TGS_ADAM_DEVICE_STEP) != 0;
+    hipStream_t hs = (hipStream_t)stream;
+    if (dev) {
+        TGS_TRY(ensure(a->dev_state, 16, hs));
+        if (!a->dev_seeded) {   // the device count starts from the host's
+            if (a->steps > 0xfffffffell) return fail(TGS_ERR_INVALID, "step count beyond 32 bits");
+            launch_adam_seed_steps(a->dev_state.as<uint32_t>(), (uint32_t)a->steps, hs);
+            a->dev_seeded = true;
+        }
+        launch_adam_bias(a->dev_state.as<uint32_t>(), a->p.beta1, a->p.beta2, hs);
+    } else {
+        a->dev_seeded = false;   // a later device step restarts from the host count
+    }
     const int64_t n = a->params.n;
     a->steps += 1;
     // simple_adam.cu:475-480: bias corrections in double, rounded to float
@@ -992,6 +1019,7 @@ int tgs_adam_step_masked(tgs_adam* a, float scale, const uint8_t* row_mask, void
     args.bc2_sqrt = bc2;
     args.max_grad = a->p.max_grad_1;
     args.row_mask = row_mask;
+    args.dev_bc = dev ? a->dev_state.as<uint32_t>() : nullptr;
     void* th[6] = {a->params.means, a->params.opacities, a->params.rotations, a->params.scales, a->params.sh0,
                    a->params.sh_rest};
     const float* gr[6] = {(const float*)a->grads.means, (const float*)a->grads.opacities,
@@ -1031,10 +1059,26 @@ int tgs_adam_reset(tgs_adam* a, void* stream) {
     }
     TGS_CHECK_LAUNCH();
     a->steps = 0;
+    a->dev_seeded = false;
     return TGS_OK;
 }
 
 int64_t tgs_adam_global_steps(tgs_adam* a) { return a ? a->steps : -1; }
+
+int tgs_adam_device_steps(tgs_adam* a, int64_t* steps, void* stream) {
+    if (!a || !steps) return fail(TGS_ERR_INVALID, "NULL argument");
+    if (!a->dev_seeded) {
+        *steps = a->steps;
+        return TGS_OK;
+    }
+    uint32_t w = 0;
+    hipStream_t s = (hipStream_t)stream;
+    TGS_HIP(hipMemcpyAsync(&w, a->dev_state.p, sizeof(w), hipMemcpyDeviceToHost, s));
+    TGS_HIP(hipStreamSynchronize(s));
+    a->steps = w;   // graph replays advance the device count only
+    *steps = w;
+    return TGS_OK;
+}
 
 int tgs_adam_moments(tgs_adam* a, int32_t group, float** first, float** second) {
     if (!a || group < 0 || group >= 6) return fail(TGS_ERR_INVALID, "bad group");

@@ -51,7 +51,12 @@ void launch_preprocess(const GaussianView& g, const CamParams& cam, uint32_t* n_
 enum { kTicketCompact = 0, kTicketOffsets = 1, kTicketDepth = 2, kTicketTile = 6, kTicketCount = 8 };
 constexpr int kBwdQueues = 64;   // backward work queues; item i belongs to queue i % kBwdQueues
 struct BinCtl {
-    uint32_t V, I, err, pad;
+    // epoch_base: look-back epochs of the current forward are epoch_base + k
+    // for the forward's k-th look-back launch (k < kEpochStride); advanced by
+    // kEpochStride on the device at the start of every forward, so a
+    // replayed (graph-captured) forward never mistakes the previous replay's
+    // status words for its own
+    uint32_t V, I, err, epoch_base;
     uint32_t tickets[kTicketCount];
     uint32_t n_items;                     // backward work items listed by the blend forward
     uint32_t pad2[19];
@@ -68,9 +73,10 @@ void launch_capacity_check(BinCtl* ctl, int64_t cap, hipStream_t s);
 void launch_clear_err_bits(BinCtl* ctl, uint32_t bits, hipStream_t s);
 // Words of bwd_queue: what a backward needs cleared.
 constexpr int kBwdCtlWords = kBwdQueues * 32;
-// Clears every BinCtl word except err.
+// Clears every BinCtl word except err and advances epoch_base.
 void launch_bin_ctl_reset(BinCtl* ctl, hipStream_t s);
 constexpr uint32_t kEpochMask = 0x3fffffffu;   // 30-bit launch epoch of look-back status words
+constexpr uint32_t kEpochStride = 64u;          // look-back launches per forward, at most
 
 // Status-word entries (u64) needed by a look-back scan over max_n elements.
 int64_t scan_status_entries(int64_t max_n);
@@ -93,7 +99,7 @@ int64_t radix_count_entries(int64_t max_n, bool depth);
 // index (0/1) of the result.
 int radix_sort(uint32_t* keys[2], uint32_t* vals[2], uint32_t* v2[2], const uint32_t* d_n, int64_t max_n, bool depth,
                int n_passes, const int* shifts, const int* bits, uint32_t* counts, uint32_t* tickets,
-               uint64_t* status, uint32_t& epoch, uint32_t* err, hipStream_t s);
+               uint64_t* status, const uint32_t* epoch_base, uint32_t& epoch, uint32_t* err, hipStream_t s);
 // Instances in depth order: thread per depth-sorted primitive k < ctl->V,
 // slots [offs[k], offs[k + 1]).
 // Also writes first_slot[p] = offs[k] for every visible primitive p = prims[k]:
@@ -251,10 +257,19 @@ struct AdamGroup {
 struct AdamArgs {
     AdamGroup groups[6];
     const uint8_t* row_mask;   // optional: row i's gradient read only if row_mask[i] != 0, else zero
+    // optional: the bias corrections (bc1, bc2_sqrt as floats at [1], [2]) come
+    // from this device state instead of bc1 / bc2_sqrt (launch_adam_bias)
+    const uint32_t* dev_bc;
     int n_groups;
     float beta1, beta2, eps, grad_scale, bc1, bc2_sqrt, max_grad;
 };
 void launch_adam(const AdamArgs& a, hipStream_t s);
+// Device-side step count for SimpleAdam (state: [0] steps, [1] bc1, [2]
+// sqrt(bc2) as float bits): seeds state[0] = steps, or advances it by one and
+// writes the bias corrections of the new count (simple_adam.cu:475-480: in
+// double, rounded to float), so a captured step replays with the right count.
+void launch_adam_seed_steps(uint32_t* state, uint32_t steps, hipStream_t s);
+void launch_adam_bias(uint32_t* state, float beta1, float beta2, hipStream_t s);
 
 // ---- self tests of wave primitives and deterministic math (debug entry points)
 void launch_detmath(int op, const float* in, float* out, int64_t n, hipStream_t s);

@@ -51,17 +51,28 @@ class SimpleAdam(OptimizerBase):
         self._cg = self.m_gaussians_grad.to_c()
         _lib.check(_lib.load().tgs_adam_set_gaussians(self._h, C.byref(self._cp), C.byref(self._cg)), "set_gaussians")
 
-    def step(self, scale: float, stream=None, row_mask: int | None = None):
+    def step(self, scale: float, stream=None, row_mask: int | None = None, device_step: bool = False):
         """OptimizerBase::step. row_mask: device address of a per-Gaussian
         byte mask (a sparse backward's); unmarked gradient rows are taken as
-        zero without being read."""
+        zero without being read. device_step=True keeps the step count and
+        bias corrections on the device (TGS_ADAM_DEVICE_STEP), so the step
+        can be captured into a graph and replayed."""
         self._rebind()
         L = _lib.load()
-        if row_mask is None:
+        if device_step:
+            _lib.check(L.tgs_adam_step_ex(self._h, float(scale), C.c_void_p(row_mask) if row_mask else None,
+                                          _lib.TGS_ADAM_DEVICE_STEP, stream_ptr(stream)), "SimpleAdam::step")
+        elif row_mask is None:
             _lib.check(L.tgs_adam_step(self._h, float(scale), stream_ptr(stream)), "SimpleAdam::step")
         else:
             _lib.check(L.tgs_adam_step_masked(self._h, float(scale), C.c_void_p(row_mask), stream_ptr(stream)),
                        "SimpleAdam::step")
+
+    def device_steps(self, stream=None) -> int:
+        """The step count of the device-step mode (waits for the stream)."""
+        v = C.c_int64()
+        _lib.check(_lib.load().tgs_adam_device_steps(self._h, C.byref(v), stream_ptr(stream)), "device_steps")
+        return v.value
 
     def reset(self, stream=None):
         _lib.check(_lib.load().tgs_adam_reset(self._h, stream_ptr(stream)), "SimpleAdam::reset")

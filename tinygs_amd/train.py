@@ -17,8 +17,11 @@ neither written nor read.
 Everything runs on one HIP stream; the only host synchronisation is the one
 inside the forward that sizes the instance buffers. With no_sync=True the
 first forward reserves an instance capacity (1.25 x its count) and the later
-ones do not wait at all (TGS_FORWARD_NO_SYNC); check_status() reports a
-forward that outgrew the capacity.
+ones do not wait at all (TGS_FORWARD_NO_SYNC), and Adam keeps its step count
+on the device (TGS_ADAM_DEVICE_STEP): from the second step on, a step is the
+same launch sequence every time and can be captured into a HIP graph
+(capture_step) and replayed; check_status() reports a forward that outgrew
+the capacity.
 """
 from __future__ import annotations
 
@@ -132,7 +135,8 @@ class TrainStep:
 
     def optimize(self):
         mask = self.rasterizer.grad_row_mask() if self.sparse_grads else None
-        self.optimizer.step(1.0 / self.grad_scaler, self.stream, row_mask=mask)
+        # no_sync: the step count on the device too, so a whole step can be captured
+        self.optimizer.step(1.0 / self.grad_scaler, self.stream, row_mask=mask, device_step=self.no_sync)
 
     def step(self):
         self.zero()
@@ -140,6 +144,18 @@ class TrainStep:
         self.losses_and_grad()
         self.backward()
         self.optimize()
+
+    def capture_step(self):
+        """A torch.cuda.CUDAGraph of one step (no_sync mode, after at least two
+        eager steps: the first sizes the buffers and reserves the capacity, the
+        second seeds the device step count). Replaying it runs a step."""
+        import torch
+        if not self.no_sync or not self._reserved or self.stream is None:
+            raise RuntimeError("capture_step needs no_sync=True, an explicit stream and two eager steps")
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=self.stream):
+            self.step()
+        return g
 
     # host copies (tests / diagnostics)
     def image(self):
