@@ -44,12 +44,6 @@ namespace tgs {
 constexpr int kBwdVals = 11;
 constexpr float kLog2e = 1.4426950408889634f;
 
-__device__ __forceinline__ void wave_lds_sync() {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
-
 // ABS: also sum |dL/dmean2d| per pixel (the densification statistic); the
 // sums are only read when densification info is requested.
 template <bool ABS>
@@ -104,10 +98,13 @@ __global__ void __launch_bounds__(256) blend_backward_kernel(
             s_part[w][kBwdVals][lane] = u2f(mask);
         }
 
-        // ---- per-pixel state at the bucket start
+        // ---- per-pixel state at the bucket start. Pixel s of this lane sits
+        // at column x[s & 1], row y[s >> 1] (two columns and two rows 8 apart)
         const uint32_t gx = tile % cam.grid_w, gy = tile / cam.grid_w;
         const uint32_t slot0 = (first - (uint32_t)j0) / (uint32_t)kBucket + tile;   // tile's first checkpoint slot
-        float pcx[4], pcy[4], g0[4], g1[4], g2[4], Tb[4], AG[4];
+        const float pcx0 = (float)(gx * 16u + (lane & 7u)) + 0.5f, pcx1 = pcx0 + 8.0f;
+        const float pcy0 = (float)(gy * 16u + (lane >> 3)) + 0.5f, pcy1 = pcy0 + 8.0f;
+        float g0[4], g1[4], g2[4], Tb[4], AG[4];
         int32_t lk[4];
         uint32_t pix[4];
         bool in[4];
@@ -118,8 +115,6 @@ __global__ void __launch_bounds__(256) blend_backward_kernel(
         for (int s = 0; s < 4; ++s) {
             const uint32_t px = gx * 16u + (uint32_t)(s & 1) * 8u + (lane & 7u);
             const uint32_t py = gy * 16u + (uint32_t)(s >> 1) * 8u + (lane >> 3);
-            pcx[s] = (float)px + 0.5f;
-            pcy[s] = (float)py + 0.5f;
             in[s] = px < cam.width && py < cam.height;
             // outside pixels read element 0 (always allocated) and are masked below
             pix[s] = in[s] ? tiled_index(py, px, cam.tiled_w) : 0u;
@@ -165,53 +160,52 @@ __global__ void __launch_bounds__(256) blend_backward_kernel(
                     AG[s] = lk[s] == k ? 0.f : AG[s];
                 }
             }
-            // the four pixels' terms; pixel 0 starts each sum (no add of a zero)
+            // offsets of the two columns and rows; sigma' = X (A X + B Y) + C Y^2
+            // with its X and Y^2 parts formed once per column / row
+            const float X[2] = {r0.x - pcx0, r0.x - pcx1}, Y[2] = {r0.y - pcy0, r0.y - pcy1};
+            const float AX[2] = {r0.z * X[0], r0.z * X[1]};
+            const float CYY[2] = {(r1.x * Y[0]) * Y[0], (r1.x * Y[1]) * Y[1]};
             float acc[12];
             acc[11] = 0.f;
             if constexpr (!ABS) acc[9] = acc[10] = 0.f;
+            float pp[4];
 #pragma unroll
             for (int s = 0; s < 4; ++s) {
-                const float dx = r0.x - pcx[s], dy = r0.y - pcy[s];
-                const float sg = __builtin_fmaf(dx, __builtin_fmaf(r0.z, dx, r0.w * dy), (r1.x * dy) * dy);
+                const int xi = s & 1, yi = s >> 1;
+                const float sg = __builtin_fmaf(X[xi], __builtin_fmaf(r0.w, Y[yi], AX[xi]), CYY[yi]);
                 const float G = __builtin_amdgcn_exp2f(-__builtin_fmaxf(sg, 0.f));
                 const float ab = __builtin_fminf(r1.y * G, kMaxAlpha);
                 const float wgt = Tb[s] * ab;
                 const float cg = __builtin_fmaf(r2.z, g2[s], __builtin_fmaf(r2.y, g1[s], r2.x * g0[s]));
                 AG[s] = __builtin_fmaf(-wgt, cg, AG[s]);
-                const float ag = AG[s];
                 const float oma = 1.0f - ab;
-                const float dalpha = __builtin_fmaf(Tb[s], cg, -(ag * __builtin_amdgcn_rcpf(oma)));
-                const float pp = ab * dalpha;
-                const float hp = pp * dx, hq = pp * dy;
-                if (s == 0) {
-                    acc[0] = wgt * g0[s];
-                    acc[1] = wgt * g1[s];
-                    acc[2] = wgt * g2[s];
-                    acc[3] = pp;
-                    acc[4] = hp * dx;
-                    acc[5] = hp * dy;
-                    acc[6] = hq * dy;
-                } else {
-                    acc[0] = __builtin_fmaf(wgt, g0[s], acc[0]);
-                    acc[1] = __builtin_fmaf(wgt, g1[s], acc[1]);
-                    acc[2] = __builtin_fmaf(wgt, g2[s], acc[2]);
-                    acc[3] += pp;
-                    acc[4] = __builtin_fmaf(hp, dx, acc[4]);
-                    acc[5] = __builtin_fmaf(hp, dy, acc[5]);
-                    acc[6] = __builtin_fmaf(hq, dy, acc[6]);
-                }
-                if constexpr (ABS) {
+                const float dalpha = __builtin_fmaf(Tb[s], cg, -(AG[s] * __builtin_amdgcn_rcpf(oma)));
+                pp[s] = ab * dalpha;
+                // colour sums; pixel 0 starts each (no add of a zero)
+                acc[0] = s == 0 ? wgt * g0[s] : __builtin_fmaf(wgt, g0[s], acc[0]);
+                acc[1] = s == 0 ? wgt * g1[s] : __builtin_fmaf(wgt, g1[s], acc[1]);
+                acc[2] = s == 0 ? wgt * g2[s] : __builtin_fmaf(wgt, g2[s], acc[2]);
+                if constexpr (ABS) {   // |dL/dmean2d| needs each pixel's own value
+                    const float hp = pp[s] * X[xi], hq = pp[s] * Y[yi];
                     const float gmx = __builtin_fmaf(hp, r1.z, hq * r2.w);
                     const float gmy = __builtin_fmaf(hp, r2.w, hq * r1.w);
-                    acc[7] = s == 0 ? gmx : acc[7] + gmx;
-                    acc[8] = s == 0 ? gmy : acc[8] + gmy;
                     acc[9] = s == 0 ? __builtin_fabsf(gmx) : acc[9] + __builtin_fabsf(gmx);
                     acc[10] = s == 0 ? __builtin_fabsf(gmy) : acc[10] + __builtin_fabsf(gmy);
-                } else {   // sums of pp dx, pp dy; the conic is applied per Gaussian at the end
-                    acc[7] = s == 0 ? hp : acc[7] + hp;
-                    acc[8] = s == 0 ? hq : acc[8] + hq;
                 }
                 Tb[s] *= oma;
+            }
+            // sums of pp, pp X^2, pp X Y, pp Y^2, pp X, pp Y over the four pixels
+            // from the column sums (pixels 0 + 2, 1 + 3) and row sums (0 + 1, 2 + 3)
+            {
+                const float R0 = pp[0] + pp[1], R1 = pp[2] + pp[3];
+                const float C0 = pp[0] + pp[2], C1 = pp[1] + pp[3];
+                acc[3] = R0 + R1;
+                acc[4] = __builtin_fmaf(X[0] * X[0], C0, (X[1] * X[1]) * C1);
+                acc[5] = __builtin_fmaf(Y[0], __builtin_fmaf(X[0], pp[0], X[1] * pp[1]),
+                                        Y[1] * __builtin_fmaf(X[0], pp[2], X[1] * pp[3]));
+                acc[6] = __builtin_fmaf(Y[0] * Y[0], R0, (Y[1] * Y[1]) * R1);
+                acc[7] = __builtin_fmaf(X[0], C0, X[1] * C1);
+                acc[8] = __builtin_fmaf(Y[0], R0, Y[1] * R1);
             }
             float t[3];
             if constexpr (ABS)
@@ -233,12 +227,10 @@ __global__ void __launch_bounds__(256) blend_backward_kernel(
             auto val = [&](int q) { return ev ? s_part[w][q][k] : 0.f; };
             // record order: mean2d(2), abs(2), conic(3), colour(3), alpha partial, 0
             float4* dst = records + 3 * (size_t)(slot + sub);
-            float gmx = val(7), gmy = val(8);
-            if constexpr (!ABS) {
-                const float a = s_rec[w][1][k].z, c = s_rec[w][1][k].w, bq = s_rec[w][2][k].w;
-                gmx = __builtin_fmaf(a, val(7), bq * val(8));
-                gmy = __builtin_fmaf(bq, val(7), c * val(8));
-            }
+            // dL/dmean2d = conic . (sum pp X, sum pp Y), applied once per Gaussian
+            const float a = s_rec[w][1][k].z, c = s_rec[w][1][k].w, bq = s_rec[w][2][k].w;
+            const float gmx = __builtin_fmaf(a, val(7), bq * val(8));
+            const float gmy = __builtin_fmaf(bq, val(7), c * val(8));
             dst[0] = make_float4(-gmx, -gmy, val(9), val(10));
             dst[1] = make_float4(-0.5f * val(4), -0.5f * val(5), -0.5f * val(6), (mask & 1u) ? val(0) : 0.f);
             dst[2] = make_float4((mask & 2u) ? val(1) : 0.f, (mask & 4u) ? val(2) : 0.f, val(3), 0.f);

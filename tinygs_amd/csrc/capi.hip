@@ -171,6 +171,12 @@ int build_camera(const tgs_camera* c, CamParams& cp) {
     cp.cam_pos[2] = (float)inv[2 * 4 + 3];
     cp.w = (float)c->width;
     cp.h = (float)c->height;
+    // float arithmetic (this file is built without contraction), the same
+    // operations the device would do
+    cp.clip_left = (-0.15f * cp.w - cp.cx) / cp.fx;
+    cp.clip_right = (1.15f * cp.w - cp.cx) / cp.fx;
+    cp.clip_top = (-0.15f * cp.h - cp.cy) / cp.fy;
+    cp.clip_bottom = (1.15f * cp.h - cp.cy) / cp.fy;
     cp.width = c->width;
     cp.height = c->height;
     cp.grid_w = (c->width + 15u) / 16u;

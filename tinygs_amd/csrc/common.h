@@ -27,6 +27,10 @@ struct CamParams {
     float r1[4], r2[4], r3[4];   // rows 0..2 of the row-major world-to-camera matrix
     float cam_pos[3];
     float w, h;                  // image size as float (frustum clamp)
+    // frustum clamp of the projected mean (kernels_forward.cuh:231-236), in
+    // float on the host: (-0.15 w - cx) / fx, (1.15 w - cx) / fx,
+    // (-0.15 h - cy) / fy, (1.15 h - cy) / fy
+    float clip_left, clip_right, clip_top, clip_bottom;
     uint32_t width, height;
     uint32_t grid_w, grid_h;     // 16x16 tiles
     uint32_t tiled_w, tiled_h;   // 8x8 image blocks
@@ -39,6 +43,14 @@ TGS_HD uint32_t tiled_index(uint32_t row, uint32_t col, uint32_t tiled_width) {
 }
 
 __device__ __forceinline__ uint32_t lane_id() { return __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u)); }
+
+// Orders this wave's LDS accesses before and after the call (a wave's own
+// LDS operations need no workgroup barrier).
+__device__ __forceinline__ void wave_lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
 
 // number of set bits of a 64-bit lane mask strictly below this lane
 __device__ __forceinline__ uint32_t mask_rank(uint64_t m) {

@@ -6,9 +6,10 @@
 //
 // MI355X layout: one thread per Gaussian, 256-thread workgroups (4 wave64).
 // Per-primitive outputs are SoA with 8/16-byte records so the blend's LDS
-// staging loads are single dwordx2/x4 transactions. Gaussians whose bounds
-// rectangle exceeds 8 tiles are counted cooperatively by the whole wave
-// (ballot + readlane broadcast), so one outlier does not serialise 63 lanes.
+// staging loads are single dwordx2/x4 transactions. The exact tile count
+// spreads the rect tiles of a wave's 64 primitives over its lanes, 64 tile
+// tests per iteration, so neither outliers nor uneven small rects leave lanes
+// idle.
 //
 // Every floating-point expression here mirrors the CPU oracle operation for
 // operation (this file is compiled with -ffp-contract=off), so visibility,
@@ -42,6 +43,86 @@ __device__ __forceinline__ bool will_contribute(float mx, float my, float ca, fl
     const float ddx = mx - px, ddy = my - py;
     const float max_power = 0.5f * (ca * ddx * ddx + cc * ddy * ddy) + cb * ddx * ddy;
     return max_power <= power_threshold;
+}
+
+// Exact tile counts of the wave's 64 primitives with their rect tiles spread
+// over the wave: task t < sum of the rect sizes is rect tile t - ex[j] (row
+// major in the rect) of lane j's primitive, ex the exclusive prefix of the
+// rect sizes. Each iteration runs 64 tile tests whatever the sizes, so small
+// and large rects share the lanes. The owner j of a task is the last lane
+// whose rect starts at or before it: every rect starting inside the
+// iteration's window marks its start position in LDS, and a prefix maximum
+// over the window (carrying the previous window's last owner) spreads the
+// marks; the owner's values then come over ds_bpermute. Hits are counted,
+// and the outcomes of rect tiles 0..31 kept as a bit mask, with LDS atomics:
+// the results do not depend on the order of the tests. test(par, tile_x,
+// tile_y) sees the owner's NP parameter words. s: this wave's kRectSlice
+// words. Called by the whole wave.
+constexpr int kRectSlice = 3 * 64;
+
+__device__ __forceinline__ uint32_t wave_inclusive_max_u32(uint32_t v) {
+    v = max(v, dpp_u32<0x111>(v));          // row_shr:1
+    v = max(v, dpp_u32<0x112>(v));          // row_shr:2
+    v = max(v, dpp_u32<0x114>(v));          // row_shr:4
+    v = max(v, dpp_u32<0x118>(v));          // row_shr:8
+    v = max(v, dpp_u32<0x142, 0xA>(v));     // row_bcast:15
+    v = max(v, dpp_u32<0x143, 0xC>(v));     // row_bcast:31
+    return v;
+}
+
+__device__ __forceinline__ uint32_t lane_gather(uint32_t j, uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_ds_bpermute((int)(j << 2), (int)v);
+}
+
+template <int NP, class Test>
+__device__ __forceinline__ void wave_rect_tests(uint32_t nrect, uint32_t xmin, uint32_t ymin, uint32_t bw,
+                                                const uint32_t (&par)[NP], uint32_t* s, uint32_t& cnt,
+                                                uint32_t& bits, Test test) {
+    const uint32_t lane = lane_id();
+    uint32_t* s_mark = s;
+    uint32_t* s_cnt = s + 64;
+    uint32_t* s_bits = s + 128;
+    const uint32_t incl = wave_inclusive_scan_u32(nrect);
+    const uint32_t total = readlane_u32(incl, 63);
+    const uint32_t ex = incl - nrect, org = xmin | (ymin << 16);
+    s_cnt[lane] = 0u;
+    s_bits[lane] = 0u;
+    uint32_t carry = 0;   // 1 + owner of the last task of the previous window
+    for (uint32_t base = 0; base < total; base += kWave) {
+        s_mark[lane] = 0u;
+        wave_lds_sync();
+        if (nrect > 0u && ex >= base && ex - base < (uint32_t)kWave) s_mark[ex - base] = lane + 1u;
+        wave_lds_sync();
+        const uint32_t j = max(wave_inclusive_max_u32(s_mark[lane]), carry) - 1u;
+        carry = readlane_u32(j, 63) + 1u;
+        const uint32_t exj = lane_gather(j, ex), orgj = lane_gather(j, org), w = lane_gather(j, bw);
+        uint32_t pj[NP];
+#pragma unroll
+        for (int q = 0; q < NP; ++q) pj[q] = lane_gather(j, par[q]);
+        const uint32_t t = base + lane;
+        if (t < total) {
+            const uint32_t k = t - exj;
+            // k / w through a float reciprocal (k < 2^16 and w <= 2^16, grids
+            // being at most 2^16 tiles, are exact floats; the estimate is off
+            // by at most one, corrected once)
+            uint32_t q = (uint32_t)((float)k * __builtin_amdgcn_rcpf((float)w));
+            int32_t r = (int32_t)k - (int32_t)(q * w);
+            if (r < 0) {
+                --q;
+                r += (int32_t)w;
+            } else if (r >= (int32_t)w) {
+                ++q;
+                r -= (int32_t)w;
+            }
+            if (test(pj, (orgj & 0xffffu) + (uint32_t)r, (orgj >> 16) + q)) {
+                atomicAdd(&s_cnt[j], 1u);
+                if (k < 32u) atomicOr(&s_bits[j], 1u << k);
+            }
+        }
+    }
+    wave_lds_sync();
+    cnt = s_cnt[lane];
+    bits = s_bits[lane];
 }
 
 template <typename ShT>
@@ -91,6 +172,7 @@ __global__ void __launch_bounds__(256) preprocess_kernel(
     // SH-rest coefficients of the block's 256 primitives are one contiguous
     // run: stage it in LDS with 16-byte lane-contiguous loads.
     __shared__ __align__(16) ShT s_sh[256 * 45];
+    __shared__ uint32_t s_rect[4][kRectSlice];
     {
         const int64_t blk0 = (int64_t)blockIdx.x * 256;
         const int nblk = (int)min((int64_t)256, n - blk0);
@@ -148,10 +230,8 @@ __global__ void __launch_bounds__(256) preprocess_kernel(
         const float c33 = S31 * R31 + S32 * R32 + S33 * R33;
         const float x = (cam.r1[0] * mx + cam.r1[1] * my + cam.r1[2] * mz + cam.r1[3]) / depth;
         const float y = (cam.r2[0] * mx + cam.r2[1] * my + cam.r2[2] * mz + cam.r2[3]) / depth;
-        const float clip_left = (-0.15f * cam.w - cam.cx) / cam.fx;
-        const float clip_right = (1.15f * cam.w - cam.cx) / cam.fx;
-        const float clip_top = (-0.15f * cam.h - cam.cy) / cam.fy;
-        const float clip_bottom = (1.15f * cam.h - cam.cy) / cam.fy;
+        const float clip_left = cam.clip_left, clip_right = cam.clip_right;
+        const float clip_top = cam.clip_top, clip_bottom = cam.clip_bottom;
         const float tx = __builtin_fmaxf(clip_left, __builtin_fminf(x, clip_right));
         const float ty = __builtin_fmaxf(clip_top, __builtin_fminf(y, clip_bottom));
         const float j11 = cam.fx / depth, j13 = -j11 * tx, j22 = cam.fy / depth, j23 = -j22 * ty;
@@ -205,43 +285,18 @@ __global__ void __launch_bounds__(256) preprocess_kernel(
         }
     }
 
-    // exact tile count: first 8 tiles per lane, the rest wave-cooperatively.
-    // The outcomes for rect tiles 0..31 (row-major in the rect) are kept as a
-    // bit mask, so the instance emission need not repeat the test there.
+    // exact tile count over the rect (kernels_forward.cuh:87-153); the
+    // outcomes for rect tiles 0..31 (row-major in the rect) are kept as a bit
+    // mask, so the instance emission need not repeat the test there
     const float smx = m2x - 0.5f, smy = m2y - 0.5f;
-    const uint32_t bw = xmax - xmin;
     uint32_t cnt = 0, bits = 0;
-    if (active) {
-        const uint32_t first = nmax < 8u ? nmax : 8u;
-        for (uint32_t k = 0; k < first; ++k) {
-            const uint32_t ty_ = ymin + k / bw, tx_ = xmin + k % bw;
-            const bool hit = will_contribute(smx, smy, ca, cb, cc, tx_, ty_, pthr);
-            cnt += hit ? 1u : 0u;
-            bits |= hit ? (1u << k) : 0u;
-        }
-    }
-    uint64_t coop = ballot(active && nmax > 8u);
-    while (coop) {
-        const uint32_t src = (uint32_t)__builtin_ctzll(coop);
-        coop &= coop - 1;
-        const float s_mx = readlane_f32(smx, src), s_my = readlane_f32(smy, src);
-        const float s_a = readlane_f32(ca, src), s_b = readlane_f32(cb, src), s_c = readlane_f32(cc, src);
-        const float s_t = readlane_f32(pthr, src);
-        const uint32_t s_x0 = readlane_u32(xmin, src), s_y0 = readlane_u32(ymin, src);
-        const uint32_t s_bw = readlane_u32(bw, src), s_n = readlane_u32(nmax, src);
-        uint32_t c = 0, b32 = 0;
-        for (uint32_t base = 8u; base < s_n; base += kWave) {
-            const uint32_t k = base + lane;
-            bool hit = false;
-            if (k < s_n) hit = will_contribute(s_mx, s_my, s_a, s_b, s_c, s_x0 + k % s_bw, s_y0 + k / s_bw, s_t);
-            const uint64_t hm = ballot(hit);
-            if (base == 8u) b32 = (uint32_t)(hm & 0xffffffu) << 8;   // rect tiles 8..31
-            c += (uint32_t)__builtin_popcountll(hm);
-        }
-        if (lane == src) {
-            cnt += c;
-            bits |= b32;
-        }
+    {
+        const uint32_t par[6] = {f2u(smx), f2u(smy), f2u(ca), f2u(cb), f2u(cc), f2u(pthr)};
+        wave_rect_tests(active ? nmax : 0u, xmin, ymin, xmax - xmin, par, s_rect[threadIdx.x >> 6], cnt, bits,
+                        [&](const uint32_t(&pj)[6], uint32_t tx_, uint32_t ty_) {
+                            return will_contribute(u2f(pj[0]), u2f(pj[1]), u2f(pj[2]), u2f(pj[3]), u2f(pj[4]), tx_,
+                                                   ty_, u2f(pj[5]));
+                        });
     }
 
     if (i >= n) return;
@@ -280,6 +335,7 @@ __global__ void __launch_bounds__(256) preprocess16_kernel(
     float2* __restrict__ mean2d, float4* __restrict__ conic_opacity, uint4* __restrict__ info,
     uint32_t* __restrict__ depth_key, float4* __restrict__ densif) {
     __shared__ __align__(16) ShT s_sh[256 * 45];
+    __shared__ uint32_t s_rect[4][kRectSlice];
     {
         const int64_t blk0 = (int64_t)blockIdx.x * 256;
         const int nblk = (int)min((int64_t)256, n - blk0);
@@ -343,10 +399,8 @@ __global__ void __launch_bounds__(256) preprocess16_kernel(
         const float c33 = S31 * R31 + S32 * R32 + S33 * R33;
         const float x = (cam.r1[0] * mx + cam.r1[1] * my + cam.r1[2] * mz + cam.r1[3]) / depth;
         const float y = (cam.r2[0] * mx + cam.r2[1] * my + cam.r2[2] * mz + cam.r2[3]) / depth;
-        const float clip_left = (-0.15f * cam.w - cam.cx) / cam.fx;
-        const float clip_right = (1.15f * cam.w - cam.cx) / cam.fx;
-        const float clip_top = (-0.15f * cam.h - cam.cy) / cam.fy;
-        const float clip_bottom = (1.15f * cam.h - cam.cy) / cam.fy;
+        const float clip_left = cam.clip_left, clip_right = cam.clip_right;
+        const float clip_top = cam.clip_top, clip_bottom = cam.clip_bottom;
         const float tx = __builtin_fmaxf(clip_left, __builtin_fminf(x, clip_right));
         const float ty = __builtin_fmaxf(clip_top, __builtin_fminf(y, clip_bottom));
         const float j11 = cam.fx / depth, j13 = -j11 * tx, j22 = cam.fy / depth, j23 = -j22 * ty;
@@ -401,40 +455,16 @@ __global__ void __launch_bounds__(256) preprocess16_kernel(
     }
 
     const float smx = m2x - 0.5f, smy = m2y - 0.5f;
-    const uint32_t bw = xmax - xmin;
     uint32_t cnt = 0, bits = 0;
-    if (active) {
-        const uint32_t first = nmax < 8u ? nmax : 8u;
-        for (uint32_t k = 0; k < first; ++k) {
-            const bool hit = will_contribute_half(smx, smy, hca, hcb, hcc, xmin + k % bw, ymin + k / bw, pthr);
-            cnt += hit ? 1u : 0u;
-            bits |= hit ? (1u << k) : 0u;
-        }
-    }
-    uint64_t coop = ballot(active && nmax > 8u);
-    while (coop) {
-        const uint32_t src = (uint32_t)__builtin_ctzll(coop);
-        coop &= coop - 1;
-        const float s_mx = readlane_f32(smx, src), s_my = readlane_f32(smy, src);
-        const uint32_t s_c01 = readlane_u32((uint32_t)hbits(hca) | ((uint32_t)hbits(hcb) << 16), src);
-        const h16 s_a = hfrom((uint16_t)(s_c01 & 0xffffu)), s_b = hfrom((uint16_t)(s_c01 >> 16));
-        const h16 s_c = hfrom((uint16_t)readlane_u32((uint32_t)hbits(hcc), src));
-        const float s_t = readlane_f32(pthr, src);
-        const uint32_t s_x0 = readlane_u32(xmin, src), s_y0 = readlane_u32(ymin, src);
-        const uint32_t s_bw = readlane_u32(bw, src), s_n = readlane_u32(nmax, src);
-        uint32_t c = 0, b32 = 0;
-        for (uint32_t base = 8u; base < s_n; base += kWave) {
-            const uint32_t k = base + lane;
-            bool hit = false;
-            if (k < s_n) hit = will_contribute_half(s_mx, s_my, s_a, s_b, s_c, s_x0 + k % s_bw, s_y0 + k / s_bw, s_t);
-            const uint64_t hm = ballot(hit);
-            if (base == 8u) b32 = (uint32_t)(hm & 0xffffffu) << 8;
-            c += (uint32_t)__builtin_popcountll(hm);
-        }
-        if (lane == src) {
-            cnt += c;
-            bits |= b32;
-        }
+    {
+        const uint32_t par[5] = {f2u(smx), f2u(smy), (uint32_t)hbits(hca) | ((uint32_t)hbits(hcb) << 16),
+                                 (uint32_t)hbits(hcc), f2u(pthr)};
+        wave_rect_tests(active ? nmax : 0u, xmin, ymin, xmax - xmin, par, s_rect[threadIdx.x >> 6], cnt, bits,
+                        [&](const uint32_t(&pj)[5], uint32_t tx_, uint32_t ty_) {
+                            return will_contribute_half(u2f(pj[0]), u2f(pj[1]), hfrom((uint16_t)(pj[2] & 0xffffu)),
+                                                        hfrom((uint16_t)(pj[2] >> 16)), hfrom((uint16_t)pj[3]), tx_,
+                                                        ty_, u2f(pj[4]));
+                        });
     }
 
     if (i >= n) return;

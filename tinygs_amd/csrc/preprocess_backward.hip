@@ -160,10 +160,8 @@ __device__ __forceinline__ void preprocess_backward_one(
     const float c22 = S21 * R21 + S22 * R22 + S23 * R23;
     const float c23 = S21 * R31 + S22 * R32 + S23 * R33;
     const float c33 = S31 * R31 + S32 * R32 + S33 * R33;
-    const float clip_left = (-0.15f * cam.w - cam.cx) / cam.fx;
-    const float clip_right = (1.15f * cam.w - cam.cx) / cam.fx;
-    const float clip_top = (-0.15f * cam.h - cam.cy) / cam.fy;
-    const float clip_bottom = (1.15f * cam.h - cam.cy) / cam.fy;
+    const float clip_left = cam.clip_left, clip_right = cam.clip_right;
+    const float clip_top = cam.clip_top, clip_bottom = cam.clip_bottom;
     const float tx = __builtin_fmaxf(clip_left, __builtin_fminf(x, clip_right));
     const float ty = __builtin_fmaxf(clip_top, __builtin_fminf(y, clip_bottom));
     const float j11 = cam.fx / depth, j13 = -j11 * tx, j22 = cam.fy / depth, j23 = -j22 * ty;
