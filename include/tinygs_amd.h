@@ -155,6 +155,15 @@ int tgs_rasterizer_backward_ex(tgs_rasterizer* r, const void* grad_image, const 
  * assigned, 0: row skipped, its gradient is zero). Valid until the next
  * backward or the next forward that grows the Gaussian count. */
 int tgs_rasterizer_grad_row_mask(tgs_rasterizer* r, const uint8_t** mask);
+/* Device byte mask [n] of the rows a TGS_BACKWARD_SPARSE backward after the
+ * last forward will assign, known before that backward runs (queued on the
+ * stream: two small kernels over the forward's work items). It equals the
+ * mask tgs_rasterizer_grad_row_mask returns after that backward. Valid until
+ * the next forward. It lets the optimiser update the rows without gradient
+ * (TGS_ADAM_ROWS_UNMARKED) on another stream while the backward runs, then
+ * the others (TGS_ADAM_ROWS_MARKED | TGS_ADAM_SAME_STEP). No counterpart in
+ * the reference. */
+int tgs_rasterizer_backward_rows(tgs_rasterizer* r, const uint8_t** rows, void* stream);
 /* ctx.grad_input.w2c of the last TGS_BACKWARD_POSE backward (fastgs.cu:373-383):
  * 16 floats into host memory, glm column-major like tgs_camera.w2c
  * (w2c_grad[4 c + r] = dL/dw2c(r, c)). Synchronises the stream. */
@@ -272,6 +281,18 @@ int tgs_adam_step_masked(tgs_adam* a, float scale, const uint8_t* row_mask, void
  * No counterpart in the reference (its bias corrections are host
  * arithmetic per step). */
 #define TGS_ADAM_DEVICE_STEP 1
+/* Row selection (needs row_mask; the two are exclusive): TGS_ADAM_ROWS_UNMARKED
+ * updates only the rows whose mask byte is 0 (as zero-gradient rows, no
+ * gradient read), TGS_ADAM_ROWS_MARKED only the others; nothing of the rows
+ * left out is read or written, so the two parts may be updated at different
+ * times. TGS_ADAM_SAME_STEP: the step count and bias corrections of the
+ * previous call (which must be of the same TGS_ADAM_DEVICE_STEP mode) instead
+ * of a new step; in device-step mode the call must be ordered after that
+ * call's launch. Together: one step in two parts, bit-identical to a single
+ * masked step. No counterpart in the reference. */
+#define TGS_ADAM_ROWS_UNMARKED 2
+#define TGS_ADAM_ROWS_MARKED 4
+#define TGS_ADAM_SAME_STEP 8
 int tgs_adam_step_ex(tgs_adam* a, float scale, const uint8_t* row_mask, int32_t flags, void* stream);
 /* The step count of the device-step mode (synchronises the stream; the host
  * count when no device step was taken since the last host-counted one). */

@@ -174,3 +174,31 @@ def screen_radius_double(scene, i):
     if not np.isfinite(lam) or lam < 0:
         return None
     return float(np.ceil(3 * np.sqrt(lam)))
+
+
+def tile_centred_scene(k=12, seed=4):
+    """k Gaussians per 16x16 tile of a 128x96 view, each projecting within
+    3 px of its tile's centre with a footprint of a few pixels: every Gaussian
+    lands in one tile, so the per-primitive sums of the fp32 blend backward
+    have one record each and a training step is deterministic."""
+    from tinygs_amd import scenes
+    rng = np.random.default_rng(seed)
+    W, H, f = 128, 96, 100.0
+    w2c = np.eye(4)
+    w2c[2, 3] = 3.0
+    cam = scenes.Camera(W, H, f, f, W / 2.0, H / 2.0, w2c)
+    gw, gh = W // 16, H // 16
+    n = gw * gh * k
+    tile = np.repeat(np.arange(gw * gh), k)
+    px = (tile % gw) * 16 + 8 + rng.uniform(-3, 3, n)
+    py = (tile // gw) * 16 + 8 + rng.uniform(-3, 3, n)
+    z = rng.uniform(-0.5, 0.5, n)
+    depth = z + 3.0
+    means = np.stack([(px - W / 2.0) * depth / f, (py - H / 2.0) * depth / f, z], 1).astype(np.float32)
+    scales = rng.normal(-4.6, 0.1, (n, 3)).astype(np.float32)
+    rots = rng.standard_normal((n, 4)).astype(np.float32)
+    opac = rng.normal(0.0, 1.0, n).astype(np.float32)
+    sh0 = rng.uniform(0.0, 1.0, (n, 3)).astype(np.float32)
+    shr = rng.normal(0.0, 0.05, (n, 15, 3)).astype(np.float32)
+    target = rng.random(cam.shape.padded_size).astype(np.float32)
+    return scenes.Scene(means, scales, rots, opac, sh0, shr, 3, cam, target, "tile_centred")

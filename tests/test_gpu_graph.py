@@ -13,7 +13,7 @@ whether or not a graph is used."""
 import numpy as np
 import pytest
 
-from tinygs_amd import scenes
+from helpers import tile_centred_scene
 
 pytestmark = pytest.mark.gpu
 
@@ -32,42 +32,19 @@ def _bits(a):
     return a.view(np.uint16 if a.dtype == np.float16 else np.uint32)
 
 
-def _tile_centred_scene(k=12, seed=4):
-    """k Gaussians per 16x16 tile of a 128x96 view, each projecting within
-    3 px of its tile's centre with a footprint of a few pixels."""
-    rng = np.random.default_rng(seed)
-    W, H, f = 128, 96, 100.0
-    w2c = np.eye(4)
-    w2c[2, 3] = 3.0
-    cam = scenes.Camera(W, H, f, f, W / 2.0, H / 2.0, w2c)
-    gw, gh = W // 16, H // 16
-    n = gw * gh * k
-    tile = np.repeat(np.arange(gw * gh), k)
-    px = (tile % gw) * 16 + 8 + rng.uniform(-3, 3, n)
-    py = (tile // gw) * 16 + 8 + rng.uniform(-3, 3, n)
-    z = rng.uniform(-0.5, 0.5, n)
-    depth = z + 3.0
-    means = np.stack([(px - W / 2.0) * depth / f, (py - H / 2.0) * depth / f, z], 1).astype(np.float32)
-    scales = rng.normal(-4.6, 0.1, (n, 3)).astype(np.float32)
-    rots = rng.standard_normal((n, 4)).astype(np.float32)
-    opac = rng.normal(0.0, 1.0, n).astype(np.float32)
-    sh0 = rng.uniform(0.0, 1.0, (n, 3)).astype(np.float32)
-    shr = rng.normal(0.0, 0.05, (n, 15, 3)).astype(np.float32)
-    target = rng.random(cam.shape.padded_size).astype(np.float32)
-    return scenes.Scene(means, scales, rots, opac, sh0, shr, 3, cam, target, "tile_centred")
-
-
-@pytest.mark.parametrize("image_dtype", ["float32", "float16"])
-def test_captured_step_replays_match_eager_steps(hip, image_dtype):
+@pytest.mark.parametrize("image_dtype,overlap", [("float32", False), ("float16", False), ("float32", True)])
+def test_captured_step_replays_match_eager_steps(hip, image_dtype, overlap):
+    """overlap: Adam's rows without gradient on a second stream (a fork and a
+    join inside the captured step)."""
     import torch
     from tinygs_amd.train import TrainStep
-    scene = _tile_centred_scene()
+    scene = tile_centred_scene()
     s = torch.cuda.Stream()
     kw = dict(l1_weight=0.8, ssim_weight=0.2, eps=1e-15, shs_lr=5e-3, sparse_grads=True, no_sync=True, stream=s,
-              image_dtype=image_dtype)
+              image_dtype=image_dtype, overlap_adam=overlap)
     eager = TrainStep(scene, **kw)
     graphed = TrainStep(scene, **kw)
-    print(f"[graph] {image_dtype}: two eager warm-up steps each", flush=True)
+    print(f"[graph] {image_dtype} overlap={overlap}: two eager warm-up steps each", flush=True)
     with torch.cuda.stream(s):
         for ts in (eager, graphed):
             ts.step()

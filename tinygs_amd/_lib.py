@@ -18,12 +18,20 @@ TGS_DTYPE_FLOAT32 = 0
 TGS_DTYPE_FLOAT16 = 1
 TGS_DTYPE_UINT8 = 2
 TGS_ADAM_DEVICE_STEP = 1
+TGS_ADAM_ROWS_UNMARKED = 2
+TGS_ADAM_ROWS_MARKED = 4
+TGS_ADAM_SAME_STEP = 8
 TGS_LOSS_ASSIGN = 1
 TGS_BACKWARD_ASSIGN = 1
 TGS_BACKWARD_SPARSE = 2
 TGS_BACKWARD_POSE = 4
 TGS_BACKWARD_KEEP_2D = 8
 TGS_FORWARD_NO_SYNC = 1
+TGS_OK = 0
+TGS_ERR_INVALID = 1
+TGS_ERR_HIP = 2
+TGS_ERR_STATE = 3
+TGS_ERR_UNSUPPORTED = 4
 TGS_ERR_CAPACITY = 5
 
 _lib = None
@@ -103,6 +111,7 @@ SIGNATURES = {
     "tgs_adam_step": ([P, C.c_float, P], C.c_int),
     "tgs_adam_step_masked": ([P, C.c_float, P, P], C.c_int),
     "tgs_rasterizer_grad_row_mask": ([P, PP], C.c_int),
+    "tgs_rasterizer_backward_rows": ([P, PP, P], C.c_int),
     "tgs_rasterizer_grad_w2c": ([P, C.POINTER(C.c_float), P], C.c_int),
     "tgs_adam_reset": ([P, P], C.c_int),
     "tgs_adam_global_steps": ([P], C.c_int64),

@@ -91,14 +91,28 @@ __global__ void __launch_bounds__(kAdamThreads) adam_kernel(AdamLaunch L) {
         bc2s = u2f(L.a.dev_bc[2]);
     }
     const int64_t vbase = (b - L.block_start[gi]) * (kAdamChunk / 4) + threadIdx.x;
+    const int sel = L.a.row_mask ? L.a.row_select : 0;
     float th[kAdamVecPerThread][4];
     float4 gv[kAdamVecPerThread], mv[kAdamVecPerThread], vv[kAdamVecPerThread];
     bool full[kAdamVecPerThread];
+    uint32_t upd[kAdamVecPerThread];   // bit q: element q of the vector is updated
 #pragma unroll
     for (int k = 0; k < kAdamVecPerThread; ++k) {
         const int64_t e0 = 4 * (vbase + (int64_t)k * kAdamThreads);
         full[k] = e0 + 3 < g.count;
+        upd[k] = 0xfu;
         if (full[k]) {
+            bool lv[4] = {true, true, true, true};
+            if (L.a.row_mask) {
+#pragma unroll
+                for (int q = 0; q < 4; ++q) lv[q] = L.a.row_mask[row_of((uint32_t)(e0 + q), g.row_width)] != 0;
+                if (sel != 0) {
+                    upd[k] = 0u;
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) upd[k] |= (lv[q] == (sel == kAdamRowsMarked)) ? 1u << q : 0u;
+                }
+            }
+            if (upd[k] == 0u) continue;   // rows of the other part: untouched
             if (g.theta_half) {
                 const uint2 hv = *(const uint2*)((const __half*)g.theta + e0);
                 const __half* h = (const __half*)&hv;
@@ -109,9 +123,6 @@ __global__ void __launch_bounds__(kAdamThreads) adam_kernel(AdamLaunch L) {
             }
             if (L.a.row_mask) {
                 // rows without gradient are zero and not read
-                bool lv[4];
-#pragma unroll
-                for (int q = 0; q < 4; ++q) lv[q] = L.a.row_mask[row_of((uint32_t)(e0 + q), g.row_width)] != 0;
                 float4 gg = make_float4(0.f, 0.f, 0.f, 0.f);
                 if (lv[0] || lv[1] || lv[2] || lv[3]) gg = ntld(g.grad + e0);
                 gv[k] = make_float4(lv[0] ? gg.x : 0.f, lv[1] ? gg.y : 0.f, lv[2] ? gg.z : 0.f, lv[3] ? gg.w : 0.f);
@@ -126,25 +137,41 @@ __global__ void __launch_bounds__(kAdamThreads) adam_kernel(AdamLaunch L) {
     for (int k = 0; k < kAdamVecPerThread; ++k) {
         const int64_t e0 = 4 * (vbase + (int64_t)k * kAdamThreads);
         if (full[k]) {
+            if (upd[k] == 0u) continue;
             th[k][0] = adam_one(th[k][0], gv[k].x, mv[k].x, vv[k].x, g, L.a, t1, t2, bc1, bc2s);
             th[k][1] = adam_one(th[k][1], gv[k].y, mv[k].y, vv[k].y, g, L.a, t1, t2, bc1, bc2s);
             th[k][2] = adam_one(th[k][2], gv[k].z, mv[k].z, vv[k].z, g, L.a, t1, t2, bc1, bc2s);
             th[k][3] = adam_one(th[k][3], gv[k].w, mv[k].w, vv[k].w, g, L.a, t1, t2, bc1, bc2s);
-            if (g.theta_half) {
-                uint2 hv;
-                __half* h = (__half*)&hv;
-                for (int q = 0; q < 4; ++q) h[q] = __float2half_rn(th[k][q]);
-                *(uint2*)((__half*)g.theta + e0) = hv;
-            } else {
-                *(float4*)((float*)g.theta + e0) = make_float4(th[k][0], th[k][1], th[k][2], th[k][3]);
+            if (upd[k] == 0xfu) {
+                if (g.theta_half) {
+                    uint2 hv;
+                    __half* h = (__half*)&hv;
+                    for (int q = 0; q < 4; ++q) h[q] = __float2half_rn(th[k][q]);
+                    *(uint2*)((__half*)g.theta + e0) = hv;
+                } else {
+                    *(float4*)((float*)g.theta + e0) = make_float4(th[k][0], th[k][1], th[k][2], th[k][3]);
+                }
+                ntst(g.m1 + e0, mv[k]);
+                ntst(g.m2 + e0, vv[k]);
+            } else {   // a vector across the two parts: element stores of this part's rows
+                const float mq[4] = {mv[k].x, mv[k].y, mv[k].z, mv[k].w};
+                const float vq[4] = {vv[k].x, vv[k].y, vv[k].z, vv[k].w};
+                for (int q = 0; q < 4; ++q) {
+                    if (!((upd[k] >> q) & 1u)) continue;
+                    if (g.theta_half)
+                        ((__half*)g.theta)[e0 + q] = __float2half_rn(th[k][q]);
+                    else
+                        ((float*)g.theta)[e0 + q] = th[k][q];
+                    g.m1[e0 + q] = mq[q];
+                    g.m2[e0 + q] = vq[q];
+                }
             }
-            ntst(g.m1 + e0, mv[k]);
-            ntst(g.m2 + e0, vv[k]);
         } else if (e0 < g.count) {
             for (int64_t i = e0; i < g.count; ++i) {
+                const bool live = !L.a.row_mask || L.a.row_mask[row_of((uint32_t)i, g.row_width)] != 0;
+                if (sel != 0 && live != (sel == kAdamRowsMarked)) continue;
                 float t = g.theta_half ? __half2float(((const __half*)g.theta)[i]) : ((const float*)g.theta)[i];
                 float m = g.m1[i], v = g.m2[i];
-                const bool live = !L.a.row_mask || L.a.row_mask[row_of((uint32_t)i, g.row_width)] != 0;
                 t = adam_one(t, live ? g.grad[i] : 0.f, m, v, g, L.a, t1, t2, bc1, bc2s);
                 if (g.theta_half)
                     ((__half*)g.theta)[i] = __float2half_rn(t);

@@ -26,6 +26,7 @@
 #include "common.h"
 #include "kernels.h"
 #include "fgs16.h"
+#include "rect_tasks.h"
 
 namespace tgs {
 
@@ -499,7 +500,9 @@ __device__ __forceinline__ bool will_contribute_e(float mx, float my, float ca, 
 // 32-byte binning record (mean, conic, threshold) only for primitives with
 // more than 32 rect tiles; its instances fill the slots [offs[k], offs[k + 1]),
 // so the instance array comes out in depth order. (The gathers are random:
-// depth order is not index order, and each costs a whole memory line.)
+// depth order is not index order, and each costs a whole memory line.) The
+// rect tiles of a wave's 64 primitives are walked as one task list, 64 per
+// step, whatever the rect sizes.
 // The workgroup's 256 primitives own one contiguous slot range; when it fits
 // in LDS the instances are staged there and written out by consecutive
 // threads (contiguous stores), otherwise written directly.
@@ -526,6 +529,7 @@ __global__ void __launch_bounds__(256) emit_kernel(const uint32_t* __restrict__ 
                                                    uint32_t* __restrict__ inst_vals,
                                                    uint32_t* __restrict__ first_slot) {
     __shared__ uint32_t s_key[kEmitStage], s_val[kEmitStage];
+    __shared__ uint32_t s_marks[4][kWave];
     const uint32_t t = threadIdx.x;
     const int64_t n = min((int64_t)ctl->V, max_count);
     const int64_t k0 = (int64_t)blockIdx.x * blockDim.x;
@@ -574,47 +578,50 @@ __global__ void __launch_bounds__(256) emit_kernel(const uint32_t* __restrict__ 
             cw0 = r1.x; cw1 = r1.y; cw2 = r1.z; pt = u2f(r1.w);
         }
     }
+    // The wave's rect tiles as one task list (rect_tasks.h); rect tiles
+    // 0..31 were tested by the preprocess (emission record). A hit's slot is
+    // its primitive's first slot plus the number of its hits before it: the
+    // hits in earlier windows (only the primitive carried into the window has
+    // any) and those of this window on lower lanes of its segment.
     const uint32_t bw = x1 - x0;
-    const uint32_t nrect = bw * (y1 - y0);
-    uint32_t written = 0;
-    if (active) {
-        const uint32_t first = nrect < 8u ? nrect : 8u;
-        // rect tiles 0..31 were tested by the preprocess (emission record)
-        for (uint32_t q = 0; q < first; ++q) {
-            const uint32_t tx = x0 + q % bw, ty = y0 + q / bw;
-            if (((bits >> q) & 1u) && written < cap) {
-                put(off + written, ty * grid_w + tx, p);
-                ++written;
-            }
+    const uint32_t nr = active ? bw * (y1 - y0) : 0u;
+    const uint32_t incl = wave_inclusive_scan_u32(nr);
+    const uint32_t total = readlane_u32(incl, 63);
+    const uint32_t ex = incl - nr, org = x0 | (y0 << 16), end = off + cap;
+    uint32_t* s_mark = s_marks[t >> 6];
+    uint32_t carry = 0, carry_hits = 0;
+    for (uint32_t base = 0; base < total; base += kWave) {
+        const uint32_t prev = carry;
+        const uint32_t j = wave_task_owner(s_mark, nr, ex, base, carry);
+        const uint32_t exj = lane_gather(j, ex), orgj = lane_gather(j, org), wj = lane_gather(j, bw);
+        const uint32_t bitsj = lane_gather(j, bits), offj = lane_gather(j, off), endj = lane_gather(j, end);
+        const uint32_t pj = lane_gather(j, p);
+        const uint32_t tt = base + lane;
+        const uint32_t q = tt - exj;
+        uint32_t tx = 0, ty = 0;
+        bool hit = false;
+        if (tt < total) {
+            uint32_t col, row;
+            rect_tile_of(q, wj, col, row);
+            tx = (orgj & 0xffffu) + col;
+            ty = (orgj >> 16) + row;
+            hit = q < 32u && ((bitsj >> q) & 1u) != 0u;
         }
-    }
-    uint64_t coop = ballot(active && nrect > 8u);
-    while (coop) {
-        const uint32_t src = (uint32_t)__builtin_ctzll(coop);
-        coop &= coop - 1;
-        const float s_mx = readlane_f32(smx, src), s_my = readlane_f32(smy, src);
-        const uint32_t s_a = readlane_u32(cw0, src), s_b = readlane_u32(cw1, src), s_c = readlane_u32(cw2, src);
-        const float s_t = readlane_f32(pt, src);
-        const uint32_t s_x0 = readlane_u32(x0, src), s_y0 = readlane_u32(y0, src);
-        const uint32_t s_bw = readlane_u32(bw, src), s_n = readlane_u32(nrect, src);
-        const uint32_t s_p = readlane_u32(p, src);
-        const uint32_t s_bits = readlane_u32(bits, src);
-        const uint32_t s_end = readlane_u32(off, src) + readlane_u32(cap, src);
-        uint32_t s_off = readlane_u32(off, src) + readlane_u32(written, src);
-        for (uint32_t base = 8u; base < s_n; base += kWave) {
-            const uint32_t q = base + lane;
-            bool hit = false;
-            uint32_t tx = 0, ty = 0;
-            if (q < s_n) {
-                tx = s_x0 + q % s_bw;
-                ty = s_y0 + q / s_bw;
-                hit = q < 32u ? ((s_bits >> q) & 1u) != 0u : emit_test<kHalf>(s_mx, s_my, s_a, s_b, s_c, tx, ty, s_t);
-            }
-            const uint64_t m = ballot(hit);
-            const uint32_t pos = s_off + mask_rank(m);
-            if (hit && pos < s_end) put(pos, ty * grid_w + tx, s_p);
-            s_off += (uint32_t)__builtin_popcountll(m);
+        if (ballot(tt < total && q >= 32u)) {   // the exact test, with the owner's record
+            const float s_mx = u2f(lane_gather(j, f2u(smx))), s_my = u2f(lane_gather(j, f2u(smy)));
+            const uint32_t s_a = lane_gather(j, cw0), s_b = lane_gather(j, cw1), s_c = lane_gather(j, cw2);
+            const float s_t = u2f(lane_gather(j, f2u(pt)));
+            if (tt < total && q >= 32u) hit = emit_test<kHalf>(s_mx, s_my, s_a, s_b, s_c, tx, ty, s_t);
         }
+        const uint64_t hm = ballot(hit);
+        const uint32_t seg = exj > base ? exj - base : 0u;   // the owner's first lane in this window
+        const uint64_t below = hm & ((1ull << lane) - 1ull) & ~((1ull << seg) - 1ull);
+        const uint32_t pos = offj + (j + 1u == prev ? carry_hits : 0u) + (uint32_t)__builtin_popcountll(below);
+        if (hit && pos < endj) put(pos, ty * grid_w + tx, pj);
+        // hits so far of the primitive carried into the next window (lane 63's owner)
+        const uint32_t seg63 = readlane_u32(seg, 63);
+        const uint32_t h63 = (uint32_t)__builtin_popcountll(hm & ~((1ull << seg63) - 1ull));
+        carry_hits = (carry == prev ? carry_hits : 0u) + h63;
     }
     if (staged) {
         __syncthreads();

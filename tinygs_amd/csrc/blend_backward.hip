@@ -240,6 +240,27 @@ __global__ void __launch_bounds__(256) blend_backward_kernel(
     }
 }
 
+// Rows the blend backward will write (each primitive of an item's bucket
+// range takes one record, whatever its pixels), marked from the forward's
+// items: two items per wave, lane & 31 = the bucket's Gaussian. rows is
+// zeroed by the caller.
+__global__ void __launch_bounds__(256) backward_rows_kernel(const uint4* __restrict__ items,
+                                                            const uint32_t* __restrict__ inst_vals,
+                                                            const BinCtl* __restrict__ ctl,
+                                                            uint8_t* __restrict__ rows) {
+    const uint32_t n_items = ctl->n_items;
+    const uint32_t l = threadIdx.x & 31u;
+    for (uint32_t it = blockIdx.x * 8u + (threadIdx.x >> 5); it < n_items; it += gridDim.x * 8u) {
+        const uint4 item = items[it];
+        if (l < item.w) rows[inst_vals[item.z + l]] = 1u;
+    }
+}
+
+void launch_backward_rows(const uint4* items, const uint32_t* inst_vals, const BinCtl* ctl, uint8_t* rows,
+                          hipStream_t s) {
+    backward_rows_kernel<<<1024, 256, 0, s>>>(items, inst_vals, ctl, rows);
+}
+
 static int g_blocks = 0;
 
 void launch_blend_backward(const CamParams& cam, const uint32_t* inst_vals, const float2* mean2d,

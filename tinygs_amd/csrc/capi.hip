@@ -222,6 +222,8 @@ struct tgs_rasterizer {
     DevBuf live, heavy, chunk_counts;   // preprocess backward: per-chunk lists of primitives with records
     DevBuf row_mask;     // per-primitive byte mask of the last sparse backward
     bool row_mask_valid = false;
+    DevBuf bwd_rows;     // rows the backward of the last forward writes (tgs_rasterizer_backward_rows)
+    bool bwd_rows_valid = false;
     DevBuf pose_partial, pose_grad;   // pose gradient: per-chunk partial sums, the 4 x 4 result
     bool pose_valid = false;
     bool grad2d_valid = false;   // grad2d holds every primitive's 2D sums (TGS_BACKWARD_KEEP_2D)
@@ -289,6 +291,7 @@ struct tgs_adam {
     int64_t steps = 0;
     DevBuf dev_state;           // TGS_ADAM_DEVICE_STEP: step count and bias corrections on the device
     bool dev_seeded = false;    // dev_state's count equals `steps` (set by the first device step)
+    bool last_dev = false;      // the last step's mode (TGS_ADAM_SAME_STEP repeats it)
 };
 
 extern "C" {
@@ -333,7 +336,7 @@ int tgs_rasterizer_destroy(tgs_rasterizer* r) {
                      &r->ikeys[1], &r->ivals[0], &r->ivals[1], &r->ranges, &r->tile_max, &r->n_contrib,
                      &r->ckpt, &r->items, &r->tile_loaded, &r->first_slot,
                      &r->rec_count, &r->records, &r->heavy, &r->live, &r->chunk_counts, &r->row_mask, &r->grad2d,
-                     &r->pose_partial, &r->pose_grad, &r->bin_ctl, &r->lb_status};
+                     &r->bwd_rows, &r->pose_partial, &r->pose_grad, &r->bin_ctl, &r->lb_status};
     for (DevBuf* b : all) release(*b);
     if (r->h_counters) (void)hipHostFree(r->h_counters);
     if (r->ev_counts) (void)hipEventDestroy(r->ev_counts);
@@ -426,6 +429,7 @@ static int rasterizer_forward(tgs_rasterizer* r, const tgs_camera* camera, void*
     TGS_TRY(plan_sorts(cam, sp));
     r->fwd_done = false;
     r->row_mask_valid = false;
+    r->bwd_rows_valid = false;
     r->pose_valid = false;
     r->grad2d_valid = false;
     const int64_t n = r->g.n;
@@ -692,6 +696,24 @@ int tgs_rasterizer_grad_w2c(tgs_rasterizer* r, float* w2c_grad, void* stream) {
     hipStream_t s = (hipStream_t)stream;
     TGS_HIP(hipMemcpyAsync(w2c_grad, r->pose_grad.p, sizeof(float) * 16, hipMemcpyDeviceToHost, s));
     TGS_HIP(hipStreamSynchronize(s));
+    return TGS_OK;
+}
+
+int tgs_rasterizer_backward_rows(tgs_rasterizer* r, const uint8_t** rows, void* stream) {
+    if (!r || !rows) return fail(TGS_ERR_INVALID, "NULL argument");
+    if (!r->fwd_done) return fail(TGS_ERR_STATE, "backward rows asked for without a preceding forward");
+    hipStream_t s = (hipStream_t)stream;
+    const int64_t n = r->n;
+    const int64_t words = (n + 3) / 4;
+    TGS_TRY(ensure(r->bwd_rows, (size_t)std::max<int64_t>(words, 1) * 4, s));
+    if (!r->bwd_rows_valid) {
+        launch_fill_u32(r->bwd_rows.as<uint32_t>(), 0u, std::max<int64_t>(words, 1), s);
+        launch_backward_rows(r->items.as<uint4>(), r->ivals[r->isel].as<uint32_t>(), r->bin_ctl.as<BinCtl>(),
+                             r->bwd_rows.as<uint8_t>(), s);
+        TGS_CHECK_LAUNCH();
+        r->bwd_rows_valid = true;
+    }
+    *rows = r->bwd_rows.as<uint8_t>();
     return TGS_OK;
 }
 
@@ -992,10 +1014,19 @@ int tgs_adam_step_masked(tgs_adam* a, float scale, const uint8_t* row_mask, void
 
 int tgs_adam_step_ex(tgs_adam* a, float scale, const uint8_t* row_mask, int32_t flags, void* stream) {
     if (!a) return fail(TGS_ERR_INVALID, "NULL argument");
-    if (flags & ~TGS_ADAM_DEVICE_STEP) return fail(TGS_ERR_INVALID, "unknown Adam step flags 0x%x", flags);
+    if (flags & ~(TGS_ADAM_DEVICE_STEP | TGS_ADAM_ROWS_UNMARKED | TGS_ADAM_ROWS_MARKED | TGS_ADAM_SAME_STEP))
+        return fail(TGS_ERR_INVALID, "unknown Adam step flags 0x%x", flags);
+    const int rows_sel = (flags & TGS_ADAM_ROWS_UNMARKED) ? kAdamRowsUnmarked
+                                                          : ((flags & TGS_ADAM_ROWS_MARKED) ? kAdamRowsMarked : 0);
+    if ((flags & TGS_ADAM_ROWS_UNMARKED) && (flags & TGS_ADAM_ROWS_MARKED))
+        return fail(TGS_ERR_INVALID, "TGS_ADAM_ROWS_UNMARKED and TGS_ADAM_ROWS_MARKED are exclusive");
+    if (rows_sel && !row_mask) return fail(TGS_ERR_INVALID, "a row selection needs the row mask");
     const bool dev = (flags & TGS_ADAM_DEVICE_STEP) != 0;
+    const bool same = (flags & TGS_ADAM_SAME_STEP) != 0;
+    if (same && (a->steps == 0 || dev != a->last_dev || (dev && !a->dev_seeded)))
+        return fail(TGS_ERR_STATE, "TGS_ADAM_SAME_STEP needs a step of the same mode before it");
     hipStream_t hs = (hipStream_t)stream;
-    if (dev) {
+    if (dev && !same) {
         TGS_TRY(ensure(a->dev_state, 16, hs));
         if (!a->dev_seeded) {   // the device count starts from the host's
             if (a->steps > 0xfffffffell) return fail(TGS_ERR_INVALID, "step count beyond 32 bits");
@@ -1003,11 +1034,12 @@ int tgs_adam_step_ex(tgs_adam* a, float scale, const uint8_t* row_mask, int32_t 
             a->dev_seeded = true;
         }
         launch_adam_bias(a->dev_state.as<uint32_t>(), a->p.beta1, a->p.beta2, hs);
-    } else {
+    } else if (!dev) {
         a->dev_seeded = false;   // a later device step restarts from the host count
     }
+    a->last_dev = dev;
     const int64_t n = a->params.n;
-    a->steps += 1;
+    if (!same) a->steps += 1;
     // simple_adam.cu:475-480: bias corrections in double, rounded to float
     const double st = (double)a->steps;
     const float bc1 = (float)(1.0 - pow((double)a->p.beta1, st));
@@ -1025,6 +1057,7 @@ int tgs_adam_step_ex(tgs_adam* a, float scale, const uint8_t* row_mask, int32_t 
     args.bc2_sqrt = bc2;
     args.max_grad = a->p.max_grad_1;
     args.row_mask = row_mask;
+    args.row_select = rows_sel;
     args.dev_bc = dev ? a->dev_state.as<uint32_t>() : nullptr;
     void* th[6] = {a->params.means, a->params.opacities, a->params.rotations, a->params.scales, a->params.sh0,
                    a->params.sh_rest};

@@ -257,12 +257,23 @@ struct AdamGroup {
 struct AdamArgs {
     AdamGroup groups[6];
     const uint8_t* row_mask;   // optional: row i's gradient read only if row_mask[i] != 0, else zero
+    // with row_mask: 0 updates every row; kAdamRowsUnmarked only the rows with
+    // row_mask[i] == 0 (zero gradient, none read), kAdamRowsMarked only the
+    // others; the elements of the rows left out are neither read nor written
+    int row_select;
     // optional: the bias corrections (bc1, bc2_sqrt as floats at [1], [2]) come
     // from this device state instead of bc1 / bc2_sqrt (launch_adam_bias)
     const uint32_t* dev_bc;
     int n_groups;
     float beta1, beta2, eps, grad_scale, bc1, bc2_sqrt, max_grad;
 };
+// Byte mask of the rows (primitives) the blend backward of the last forward
+// writes: one per primitive of every work item's bucket range. rows must be
+// zeroed before.
+void launch_backward_rows(const uint4* items, const uint32_t* inst_vals, const BinCtl* ctl, uint8_t* rows,
+                          hipStream_t s);
+constexpr int kAdamRowsUnmarked = 1;
+constexpr int kAdamRowsMarked = 2;
 void launch_adam(const AdamArgs& a, hipStream_t s);
 // Device-side step count for SimpleAdam (state: [0] steps, [1] bc1, [2]
 // sqrt(bc2) as float bits): seeds state[0] = steps, or advances it by one and

@@ -17,6 +17,7 @@
 #include "common.h"
 #include "kernels.h"
 #include "fgs16.h"
+#include "rect_tasks.h"
 
 namespace tgs {
 
@@ -45,34 +46,12 @@ __device__ __forceinline__ bool will_contribute(float mx, float my, float ca, fl
     return max_power <= power_threshold;
 }
 
-// Exact tile counts of the wave's 64 primitives with their rect tiles spread
-// over the wave: task t < sum of the rect sizes is rect tile t - ex[j] (row
-// major in the rect) of lane j's primitive, ex the exclusive prefix of the
-// rect sizes. Each iteration runs 64 tile tests whatever the sizes, so small
-// and large rects share the lanes. The owner j of a task is the last lane
-// whose rect starts at or before it: every rect starting inside the
-// iteration's window marks its start position in LDS, and a prefix maximum
-// over the window (carrying the previous window's last owner) spreads the
-// marks; the owner's values then come over ds_bpermute. Hits are counted,
-// and the outcomes of rect tiles 0..31 kept as a bit mask, with LDS atomics:
-// the results do not depend on the order of the tests. test(par, tile_x,
-// tile_y) sees the owner's NP parameter words. s: this wave's kRectSlice
-// words. Called by the whole wave.
+// Exact tile counts of the wave's 64 primitives, their rect tiles spread over
+// the wave's lanes (rect_tasks.h). Hits are counted, and the outcomes of rect
+// tiles 0..31 kept as a bit mask, with LDS atomics: the results do not depend
+// on the order of the tests. test(par, tile_x, tile_y) sees the owner's NP
+// parameter words. s: this wave's kRectSlice words. Called by the whole wave.
 constexpr int kRectSlice = 3 * 64;
-
-__device__ __forceinline__ uint32_t wave_inclusive_max_u32(uint32_t v) {
-    v = max(v, dpp_u32<0x111>(v));          // row_shr:1
-    v = max(v, dpp_u32<0x112>(v));          // row_shr:2
-    v = max(v, dpp_u32<0x114>(v));          // row_shr:4
-    v = max(v, dpp_u32<0x118>(v));          // row_shr:8
-    v = max(v, dpp_u32<0x142, 0xA>(v));     // row_bcast:15
-    v = max(v, dpp_u32<0x143, 0xC>(v));     // row_bcast:31
-    return v;
-}
-
-__device__ __forceinline__ uint32_t lane_gather(uint32_t j, uint32_t v) {
-    return (uint32_t)__builtin_amdgcn_ds_bpermute((int)(j << 2), (int)v);
-}
 
 template <int NP, class Test>
 __device__ __forceinline__ void wave_rect_tests(uint32_t nrect, uint32_t xmin, uint32_t ymin, uint32_t bw,
@@ -87,14 +66,9 @@ __device__ __forceinline__ void wave_rect_tests(uint32_t nrect, uint32_t xmin, u
     const uint32_t ex = incl - nrect, org = xmin | (ymin << 16);
     s_cnt[lane] = 0u;
     s_bits[lane] = 0u;
-    uint32_t carry = 0;   // 1 + owner of the last task of the previous window
+    uint32_t carry = 0;
     for (uint32_t base = 0; base < total; base += kWave) {
-        s_mark[lane] = 0u;
-        wave_lds_sync();
-        if (nrect > 0u && ex >= base && ex - base < (uint32_t)kWave) s_mark[ex - base] = lane + 1u;
-        wave_lds_sync();
-        const uint32_t j = max(wave_inclusive_max_u32(s_mark[lane]), carry) - 1u;
-        carry = readlane_u32(j, 63) + 1u;
+        const uint32_t j = wave_task_owner(s_mark, nrect, ex, base, carry);
         const uint32_t exj = lane_gather(j, ex), orgj = lane_gather(j, org), w = lane_gather(j, bw);
         uint32_t pj[NP];
 #pragma unroll
@@ -102,19 +76,9 @@ __device__ __forceinline__ void wave_rect_tests(uint32_t nrect, uint32_t xmin, u
         const uint32_t t = base + lane;
         if (t < total) {
             const uint32_t k = t - exj;
-            // k / w through a float reciprocal (k < 2^16 and w <= 2^16, grids
-            // being at most 2^16 tiles, are exact floats; the estimate is off
-            // by at most one, corrected once)
-            uint32_t q = (uint32_t)((float)k * __builtin_amdgcn_rcpf((float)w));
-            int32_t r = (int32_t)k - (int32_t)(q * w);
-            if (r < 0) {
-                --q;
-                r += (int32_t)w;
-            } else if (r >= (int32_t)w) {
-                ++q;
-                r -= (int32_t)w;
-            }
-            if (test(pj, (orgj & 0xffffu) + (uint32_t)r, (orgj >> 16) + q)) {
+            uint32_t col, row;
+            rect_tile_of(k, w, col, row);
+            if (test(pj, (orgj & 0xffffu) + col, (orgj >> 16) + row)) {
                 atomicAdd(&s_cnt[j], 1u);
                 if (k < 32u) atomicOr(&s_bits[j], 1u << k);
             }

@@ -51,17 +51,26 @@ class SimpleAdam(OptimizerBase):
         self._cg = self.m_gaussians_grad.to_c()
         _lib.check(_lib.load().tgs_adam_set_gaussians(self._h, C.byref(self._cp), C.byref(self._cg)), "set_gaussians")
 
-    def step(self, scale: float, stream=None, row_mask: int | None = None, device_step: bool = False):
+    def step(self, scale: float, stream=None, row_mask: int | None = None, device_step: bool = False,
+             rows: str | None = None, same_step: bool = False):
         """OptimizerBase::step. row_mask: device address of a per-Gaussian
         byte mask (a sparse backward's); unmarked gradient rows are taken as
         zero without being read. device_step=True keeps the step count and
         bias corrections on the device (TGS_ADAM_DEVICE_STEP), so the step
-        can be captured into a graph and replayed."""
+        can be captured into a graph and replayed. rows="unmarked" / "marked"
+        updates only the rows whose mask byte is 0 / nonzero
+        (TGS_ADAM_ROWS_UNMARKED / _MARKED), same_step=True repeats the last
+        call's step count (TGS_ADAM_SAME_STEP): one step in two parts."""
         self._rebind()
         L = _lib.load()
-        if device_step:
+        flags = _lib.TGS_ADAM_DEVICE_STEP if device_step else 0
+        if rows is not None:
+            flags |= {"unmarked": _lib.TGS_ADAM_ROWS_UNMARKED, "marked": _lib.TGS_ADAM_ROWS_MARKED}[rows]
+        if same_step:
+            flags |= _lib.TGS_ADAM_SAME_STEP
+        if flags:
             _lib.check(L.tgs_adam_step_ex(self._h, float(scale), C.c_void_p(row_mask) if row_mask else None,
-                                          _lib.TGS_ADAM_DEVICE_STEP, stream_ptr(stream)), "SimpleAdam::step")
+                                          flags, stream_ptr(stream)), "SimpleAdam::step")
         elif row_mask is None:
             _lib.check(L.tgs_adam_step(self._h, float(scale), stream_ptr(stream)), "SimpleAdam::step")
         else:

@@ -131,6 +131,15 @@ class FastGSRasterizer(RasterizerBase):
         _lib.check(_lib.load().tgs_rasterizer_grad_row_mask(self._h, C.byref(m)), "grad_row_mask")
         return m.value
 
+    def backward_rows(self, stream=None) -> int:
+        """Device address of the byte mask [n] of the rows a sparse backward
+        after the last forward will write, queued on `stream` before that
+        backward runs (equal to grad_row_mask after it)."""
+        m = C.c_void_p()
+        _lib.check(_lib.load().tgs_rasterizer_backward_rows(self._h, C.byref(m), stream_ptr(stream)),
+                   "backward_rows")
+        return m.value
+
     def counts(self):
         v, i, t = C.c_int64(), C.c_int64(), C.c_int64()
         _lib.check(_lib.load().tgs_rasterizer_counts(self._h, C.byref(v), C.byref(i), C.byref(t)), "counts")
