@@ -62,7 +62,7 @@ def test_config5_full_size_iteration100_matches_oracle(hip):
     """The full config-5 loop (500k initial Gaussians, 200 views of
     1600x1060, refine every 100 from 100) at iteration 100 against the CPU
     oracle's run of the same loop (tests/golden/config5_iter100.json, written
-    by make_config5_iter100.py): the mean PSNR over views 0-19 within 0.02 dB,
+    by make_config5_fixture.py): the mean PSNR over views 0-19 within 0.02 dB,
     the Gaussian count within 0.1% (a refine's thresholds meet float sums
     whose rounding differs between the two) and the parameter means."""
     with open(GOLDEN_100) as f:

@@ -77,6 +77,9 @@ __device__ __forceinline__ uint32_t row_of(uint32_t e, int w) {
 // Each thread updates kAdamVecPerThread 4-element vectors with 16-byte loads
 // and stores (8-byte for fp16 theta); lanes of a wave cover consecutive
 // vectors. All loads of a thread are issued before any arithmetic.
+// SEL: 0 every row, kAdamRowsUnmarked / kAdamRowsMarked one part of the rows
+// (a compile-time choice: the selection costs VALU the full step does not need)
+template <int SEL>
 __global__ void __launch_bounds__(kAdamThreads) adam_kernel(AdamLaunch L) {
     const int64_t b = blockIdx.x;
     int gi = 0;
@@ -91,7 +94,7 @@ __global__ void __launch_bounds__(kAdamThreads) adam_kernel(AdamLaunch L) {
         bc2s = u2f(L.a.dev_bc[2]);
     }
     const int64_t vbase = (b - L.block_start[gi]) * (kAdamChunk / 4) + threadIdx.x;
-    const int sel = L.a.row_mask ? L.a.row_select : 0;
+    constexpr int sel = SEL;
     float th[kAdamVecPerThread][4];
     float4 gv[kAdamVecPerThread], mv[kAdamVecPerThread], vv[kAdamVecPerThread];
     bool full[kAdamVecPerThread];
@@ -106,13 +109,13 @@ __global__ void __launch_bounds__(kAdamThreads) adam_kernel(AdamLaunch L) {
             if (L.a.row_mask) {
 #pragma unroll
                 for (int q = 0; q < 4; ++q) lv[q] = L.a.row_mask[row_of((uint32_t)(e0 + q), g.row_width)] != 0;
-                if (sel != 0) {
+                if constexpr (sel != 0) {
                     upd[k] = 0u;
 #pragma unroll
                     for (int q = 0; q < 4; ++q) upd[k] |= (lv[q] == (sel == kAdamRowsMarked)) ? 1u << q : 0u;
                 }
             }
-            if (upd[k] == 0u) continue;   // rows of the other part: untouched
+            if (sel != 0 && upd[k] == 0u) continue;   // rows of the other part: untouched
             if (g.theta_half) {
                 const uint2 hv = *(const uint2*)((const __half*)g.theta + e0);
                 const __half* h = (const __half*)&hv;
@@ -137,12 +140,12 @@ __global__ void __launch_bounds__(kAdamThreads) adam_kernel(AdamLaunch L) {
     for (int k = 0; k < kAdamVecPerThread; ++k) {
         const int64_t e0 = 4 * (vbase + (int64_t)k * kAdamThreads);
         if (full[k]) {
-            if (upd[k] == 0u) continue;
+            if (sel != 0 && upd[k] == 0u) continue;
             th[k][0] = adam_one(th[k][0], gv[k].x, mv[k].x, vv[k].x, g, L.a, t1, t2, bc1, bc2s);
             th[k][1] = adam_one(th[k][1], gv[k].y, mv[k].y, vv[k].y, g, L.a, t1, t2, bc1, bc2s);
             th[k][2] = adam_one(th[k][2], gv[k].z, mv[k].z, vv[k].z, g, L.a, t1, t2, bc1, bc2s);
             th[k][3] = adam_one(th[k][3], gv[k].w, mv[k].w, vv[k].w, g, L.a, t1, t2, bc1, bc2s);
-            if (upd[k] == 0xfu) {
+            if (sel == 0 || upd[k] == 0xfu) {
                 if (g.theta_half) {
                     uint2 hv;
                     __half* h = (__half*)&hv;
@@ -217,7 +220,13 @@ void launch_adam(const AdamArgs& a, hipStream_t s) {
     }
     for (int k = a.n_groups; k < 7; ++k) L.block_start[k] = acc;
     if (acc == 0) return;
-    adam_kernel<<<(unsigned)acc, kAdamThreads, 0, s>>>(L);
+    const int sel = a.row_mask ? a.row_select : 0;
+    if (sel == kAdamRowsUnmarked)
+        adam_kernel<kAdamRowsUnmarked><<<(unsigned)acc, kAdamThreads, 0, s>>>(L);
+    else if (sel == kAdamRowsMarked)
+        adam_kernel<kAdamRowsMarked><<<(unsigned)acc, kAdamThreads, 0, s>>>(L);
+    else
+        adam_kernel<0><<<(unsigned)acc, kAdamThreads, 0, s>>>(L);
 }
 
 }  // namespace tgs
