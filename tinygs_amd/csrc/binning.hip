@@ -276,16 +276,19 @@ __device__ __forceinline__ void rank_keys(const uint32_t key[KPT], int64_t base,
 
 // Per-workgroup digit counts: counts[d * nb + b] (digit-major). Workgroups
 // past the end write zeros. Counting needs no ranks: one LDS atomic add per
-// key into the workgroup's histogram.
+// key into one of kHistCopies histograms (by lane), summed at the end: keys
+// that arrive clustered (the instances of one primitive share their tile
+// digits) would otherwise serialise on one address.
+constexpr int kHistCopies = 8;
 template <int KPT, int MAXB>
 __global__ void __launch_bounds__(kThreads) radix_upsweep_kernel(const uint32_t* __restrict__ keys,
                                                                  const uint32_t* d_n, int64_t max_n, int shift,
                                                                  int bits, uint32_t* __restrict__ counts,
                                                                  uint32_t nb) {
-    __shared__ uint32_t s_hist[MAXB];
+    __shared__ uint32_t s_hist[kHistCopies][MAXB];
     const uint32_t t = threadIdx.x, lane = t & 63u, w = t >> 6;
     const uint32_t bins = 1u << bits, dmask = bins - 1u;
-    for (uint32_t b = t; b < (uint32_t)MAXB; b += kThreads) s_hist[b] = 0u;
+    for (uint32_t b = t; b < (uint32_t)(kHistCopies * MAXB); b += kThreads) (&s_hist[0][0])[b] = 0u;
     __syncthreads();
     const int64_t n = resolve_n(d_n, max_n);
     const int64_t base = (int64_t)blockIdx.x * (kThreads * KPT) + (int64_t)w * (64 * KPT);
@@ -297,9 +300,14 @@ __global__ void __launch_bounds__(kThreads) radix_upsweep_kernel(const uint32_t*
     }
 #pragma unroll
     for (int r = 0; r < KPT; ++r)
-        if (base + (int64_t)r * 64 + lane < n) atomicAdd(&s_hist[(key[r] >> shift) & dmask], 1u);
+        if (base + (int64_t)r * 64 + lane < n) atomicAdd(&s_hist[lane & (kHistCopies - 1)][(key[r] >> shift) & dmask], 1u);
     __syncthreads();
-    for (uint32_t b = t; b < bins; b += kThreads) counts[(size_t)b * nb + blockIdx.x] = s_hist[b];
+    for (uint32_t b = t; b < bins; b += kThreads) {
+        uint32_t c = 0;
+#pragma unroll
+        for (int k = 0; k < kHistCopies; ++k) c += s_hist[k][b];
+        counts[(size_t)b * nb + blockIdx.x] = c;
+    }
 }
 
 // In-place exclusive scan of a u32 array of n elements (single pass,
