@@ -681,29 +681,51 @@ void launch_fill_u32(uint32_t* p, uint32_t value, int64_t n, hipStream_t s) {
     fill_u32_kernel<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(p, value, n);
 }
 
-// kernels_forward.cuh:532-551, plus (0, 0) for the empty tiles: thread i
-// (0 <= i <= n) sits on the boundary between keys[i - 1] and keys[i]
-// (sentinels -1 and n_tiles), closes the previous tile's range, opens the
-// next one and clears the tiles strictly between them.
-__global__ void tile_ranges_kernel(const uint32_t* __restrict__ keys, const uint32_t* d_n, int64_t max_n,
-                                   uint2* __restrict__ ranges, uint32_t n_tiles) {
-    const int64_t n = resolve_n(d_n, max_n);
-    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i > n) return;
-    // keys are tile ids < n_tiles; min() keeps a corrupt key from writing out of range
-    const int64_t cur = i < n ? (int64_t)min(keys[i], n_tiles) : (int64_t)n_tiles;
-    const int64_t prev = i > 0 ? (int64_t)min(keys[i - 1], n_tiles) : -1;
-    if (prev == (int64_t)n_tiles) return;
-    if (cur == prev) return;
+// kernels_forward.cuh:532-551, plus (0, 0) for the empty tiles: boundary i
+// (0 <= i <= n) sits between keys[i - 1] and keys[i] (sentinels -1 and
+// n_tiles), closes the previous tile's range, opens the next one and clears
+// the tiles strictly between them. Each thread takes 8 consecutive
+// boundaries, their keys read as two 16-byte vectors.
+constexpr int kRangeSpan = 8;
+
+__device__ __forceinline__ void tile_boundary(int64_t i, int64_t n, int64_t prev, int64_t cur, uint2* ranges,
+                                              uint32_t n_tiles) {
+    if (prev == (int64_t)n_tiles || cur == prev) return;
     if (i > 0) ranges[prev].y = (uint32_t)i;
     if (i < n && cur < (int64_t)n_tiles) ranges[cur].x = (uint32_t)i;
     for (int64_t tt = prev + 1; tt < cur; ++tt) ranges[tt] = make_uint2(0u, 0u);
 }
 
+__global__ void tile_ranges_kernel(const uint32_t* __restrict__ keys, const uint32_t* d_n, int64_t max_n,
+                                   uint2* __restrict__ ranges, uint32_t n_tiles) {
+    const int64_t n = resolve_n(d_n, max_n);
+    const int64_t i0 = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * kRangeSpan;
+    if (i0 > n) return;
+    // keys are tile ids < n_tiles; min() keeps a corrupt key from writing out of range
+    uint32_t k[kRangeSpan];
+    if (i0 + kRangeSpan <= n) {   // the buffer is 16-byte aligned and i0 a multiple of 8
+        const uint4 a = *(const uint4*)(keys + i0), b = *(const uint4*)(keys + i0 + 4);
+        k[0] = a.x; k[1] = a.y; k[2] = a.z; k[3] = a.w; k[4] = b.x; k[5] = b.y; k[6] = b.z; k[7] = b.w;
+    } else {
+#pragma unroll
+        for (int q = 0; q < kRangeSpan; ++q) k[q] = i0 + q < n ? keys[i0 + q] : n_tiles;
+    }
+    int64_t prev = i0 > 0 ? (int64_t)min(keys[i0 - 1], n_tiles) : -1;
+#pragma unroll
+    for (int q = 0; q < kRangeSpan; ++q) {
+        const int64_t i = i0 + q;
+        if (i > n) break;
+        const int64_t cur = i < n ? (int64_t)min(k[q], n_tiles) : (int64_t)n_tiles;
+        tile_boundary(i, n, prev, cur, ranges, n_tiles);
+        prev = cur;
+    }
+}
+
 void launch_tile_ranges(const uint32_t* inst_keys, const uint32_t* d_n, int64_t max_inst, uint2* ranges,
                         uint32_t n_tiles, hipStream_t s) {
-    tile_ranges_kernel<<<(unsigned)((max_inst + 1 + 255) / 256), 256, 0, s>>>(inst_keys, d_n, max_inst, ranges,
-                                                                            n_tiles);
+    const int64_t threads = (max_inst + 1 + kRangeSpan - 1) / kRangeSpan;
+    tile_ranges_kernel<<<(unsigned)((threads + 255) / 256), 256, 0, s>>>(inst_keys, d_n, max_inst, ranges,
+                                                                        n_tiles);
 }
 
 __global__ void capacity_check_kernel(BinCtl* ctl, int64_t cap) {
