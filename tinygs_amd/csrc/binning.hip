@@ -35,6 +35,9 @@ constexpr int kScanRounds = 16;
 constexpr int kScanChunk = kThreads * kScanRounds;     // 4096 elements per scan workgroup
 constexpr int kDepthKeysPerThread = 16;                 // depth passes: 4096 keys per workgroup
 constexpr int kTileKeysPerThread = 8;                   // tile passes: 2048 keys per workgroup (4096 measured 7 us slower)
+// LDS histograms per digit count (lane & (kHistCopies - 1) picks one): keys
+// that arrive clustered do not serialise their atomic adds on one address
+constexpr int kHistCopies = 8;
 constexpr int kDepthMaxDigits = 512;                    // depth passes: digits of up to 9 bits
 constexpr int kTileMaxDigits = 256;                     // tile passes: digits of up to 8 bits
 
@@ -143,26 +146,37 @@ __device__ __forceinline__ uint64_t match_digit(uint32_t d, int bits, bool valid
 // ---------------------------------------------------------------- compaction
 
 // Visible primitives (n_touched > 0) in index order -> (depth key, index,
-// n_touched) triples; V; I = sum of n_touched.
-__global__ void __launch_bounds__(kThreads) compact_kernel(const uint32_t* __restrict__ n_touched,
-                                                           const uint32_t* __restrict__ depth_key, int64_t n,
-                                                           uint32_t key_base, uint32_t* __restrict__ keys_out,
-                                                           uint32_t* __restrict__ vals_out,
-                                                           uint32_t* __restrict__ nt_out, BinCtl* ctl,
-                                                           uint64_t* status, uint32_t epoch) {
+// n_touched) triples, compacted inside each 4096-primitive block (block b's
+// visible ones at [4096 b, 4096 b + block_n[b]), in index order): the depth
+// sort's first pass takes these blocks as its input blocks, so the same kernel
+// counts their first-pass digits (counts[d * nb + b], the pass's upsweep) and
+// no device-wide scan is needed. V and I = sum of n_touched by one atomic add
+// per block each (integer sums: the same totals in any order).
+static_assert(kScanChunk == kThreads * kDepthKeysPerThread, "compaction blocks are the depth sort's blocks");
+__global__ void __launch_bounds__(kThreads) compact_count_kernel(const uint32_t* __restrict__ n_touched,
+                                                                 const uint32_t* __restrict__ depth_key, int64_t n,
+                                                                 uint32_t key_base, int shift, int bits,
+                                                                 uint32_t* __restrict__ keys_out,
+                                                                 uint32_t* __restrict__ vals_out,
+                                                                 uint32_t* __restrict__ nt_out,
+                                                                 uint32_t* __restrict__ counts,
+                                                                 uint32_t* __restrict__ block_n, BinCtl* ctl) {
     __shared__ uint32_t s_rw[64];
     __shared__ uint32_t s_nt[4];
-    __shared__ uint32_t s_bid, s_base;
+    __shared__ uint32_t s_hist[kHistCopies][kDepthMaxDigits];
     const uint32_t t = threadIdx.x, lane = t & 63u, w = t >> 6;
-    const uint32_t bid = take_ticket(&ctl->tickets[kTicketCompact], &s_bid);
-    const int64_t base = (int64_t)bid * kScanChunk + t;
+    const uint32_t b = blockIdx.x, nb = gridDim.x;
+    const uint32_t bins = 1u << bits, dmask = bins - 1u;
+    for (uint32_t e = t; e < (uint32_t)(kHistCopies * kDepthMaxDigits); e += kThreads) (&s_hist[0][0])[e] = 0u;
+    const int64_t blk = (int64_t)b * kScanChunk;
+    const int64_t base = blk + t;
     uint32_t key[kScanRounds], nt[kScanRounds], vis[kScanRounds], ex[kScanRounds];
     uint32_t ntsum = 0;
 #pragma unroll
     for (int r = 0; r < kScanRounds; ++r) {
         const int64_t i = base + (int64_t)r * kThreads;
         nt[r] = i < n ? n_touched[i] : 0u;
-        key[r] = i < n ? depth_key[i] : 0u;
+        key[r] = i < n ? depth_key[i] - key_base : 0u;
     }
 #pragma unroll
     for (int r = 0; r < kScanRounds; ++r) {
@@ -172,36 +186,39 @@ __global__ void __launch_bounds__(kThreads) compact_kernel(const uint32_t* __res
     const uint32_t wnt = wave_sum_u32(ntsum);
     if (lane == 0) s_nt[w] = wnt;
     uint32_t total;
-    striped_scan16_u32(vis, ex, &total, s_rw);   // barriers inside: s_nt visible after it
-    if (w == 0) {
-        const uint32_t excl = wave_look_back(status, bid, total, ctl->epoch_base + epoch, &ctl->err);
-        if (lane == 0) {
-            s_base = excl;
-            if ((int64_t)(bid + 1) * kScanChunk >= n) ctl->V = excl + total;
-            const uint32_t bsum = s_nt[0] + s_nt[1] + s_nt[2] + s_nt[3];
-            if (bsum) atomicAdd(&ctl->I, bsum);
-        }
-    }
-    __syncthreads();
-    const uint32_t b0 = s_base;
+    striped_scan16_u32(vis, ex, &total, s_rw);   // barriers inside: s_nt and the zeroed histograms visible after it
 #pragma unroll
     for (int r = 0; r < kScanRounds; ++r) {
         if (vis[r]) {
-            const uint32_t pos = b0 + ex[r];
-            keys_out[pos] = key[r] - key_base;
+            const int64_t pos = blk + ex[r];
+            keys_out[pos] = key[r];
             vals_out[pos] = (uint32_t)(base + (int64_t)r * kThreads);
             nt_out[pos] = nt[r];
+            atomicAdd(&s_hist[lane & (kHistCopies - 1)][(key[r] >> shift) & dmask], 1u);
         }
+    }
+    if (t == 0) {
+        block_n[b] = total;
+        if (total) atomicAdd(&ctl->V, total);
+        const uint32_t bsum = s_nt[0] + s_nt[1] + s_nt[2] + s_nt[3];
+        if (bsum) atomicAdd(&ctl->I, bsum);
+    }
+    __syncthreads();
+    for (uint32_t d = t; d < bins; d += kThreads) {
+        uint32_t c = 0;
+#pragma unroll
+        for (int k = 0; k < kHistCopies; ++k) c += s_hist[k][d];
+        counts[(size_t)d * nb + b] = c;
     }
 }
 
 void launch_compact_visible(const uint32_t* n_touched, const uint32_t* depth_key, int64_t n, uint32_t key_base,
-                            uint32_t* keys_out, uint32_t* vals_out, uint32_t* nt_out, BinCtl* ctl, uint64_t* status,
-                            uint32_t& epoch, hipStream_t s) {
+                            int shift, int bits, uint32_t* keys_out, uint32_t* vals_out, uint32_t* nt_out,
+                            uint32_t* counts, uint32_t* block_n, BinCtl* ctl, hipStream_t s) {
     if (n <= 0) return;
     const uint32_t nb = (uint32_t)((n + kScanChunk - 1) / kScanChunk);
-    compact_kernel<<<nb, kThreads, 0, s>>>(n_touched, depth_key, n, key_base, keys_out, vals_out, nt_out, ctl, status,
-                                           ++epoch);
+    compact_count_kernel<<<nb, kThreads, 0, s>>>(n_touched, depth_key, n, key_base, shift, bits, keys_out, vals_out,
+                                                 nt_out, counts, block_n, ctl);
 }
 
 // ---------------------------------------------------------------- instance offsets
@@ -279,7 +296,6 @@ __device__ __forceinline__ void rank_keys(const uint32_t key[KPT], int64_t base,
 // key into one of kHistCopies histograms (by lane), summed at the end: keys
 // that arrive clustered (the instances of one primitive share their tile
 // digits) would otherwise serialise on one address.
-constexpr int kHistCopies = 8;
 template <int KPT, int MAXB>
 __global__ void __launch_bounds__(kThreads) radix_upsweep_kernel(const uint32_t* __restrict__ keys,
                                                                  const uint32_t* d_n, int64_t max_n, int shift,
@@ -353,7 +369,8 @@ template <int KPT, bool PAYLOAD2, int MAXB>
 __global__ void __launch_bounds__(kThreads) radix_downsweep_kernel(
     const uint32_t* __restrict__ keys_in, const uint32_t* __restrict__ vals_in, const uint32_t* __restrict__ v2_in,
     uint32_t* __restrict__ keys_out, uint32_t* __restrict__ vals_out, uint32_t* __restrict__ v2_out,
-    const uint32_t* d_n, int64_t max_n, int shift, int bits, const uint32_t* __restrict__ offsets, uint32_t nb) {
+    const uint32_t* d_n, int64_t max_n, int shift, int bits, const uint32_t* __restrict__ offsets, uint32_t nb,
+    const uint32_t* __restrict__ block_n) {
     constexpr int kChunk = kThreads * KPT;
     constexpr int kBpt = MAXB / kThreads;   // digits per thread in the workgroup scan (1 or 2)
     static_assert(MAXB == kThreads || MAXB == 2 * kThreads, "256 or 512 digits");
@@ -363,8 +380,10 @@ __global__ void __launch_bounds__(kThreads) radix_downsweep_kernel(
     __shared__ uint32_t s_wave[4];
     const uint32_t t = threadIdx.x, lane = t & 63u, w = t >> 6;
     const uint32_t bins = 1u << bits, dmask = bins - 1u;
-    const int64_t n = resolve_n(d_n, max_n);
     const int64_t blk = (int64_t)blockIdx.x * kChunk;
+    // block_n: this block holds block_n[b] keys from its start (a compacted
+    // block of the first depth pass); otherwise the first n keys are dense
+    const int64_t n = block_n ? blk + (int64_t)block_n[blockIdx.x] : resolve_n(d_n, max_n);
     if (blk >= n) return;
     for (int k = t; k < 4 * MAXB; k += kThreads) (&s_cnt[0][0])[k] = 0;
     uint32_t gofs[kBpt];   // thread t owns digits kBpt t .. kBpt t + kBpt - 1
@@ -442,25 +461,28 @@ template <int KPT, int MAXB>
 static int radix_passes(uint32_t* keys[2], uint32_t* vals[2], uint32_t* v2[2], const uint32_t* d_n, int64_t max_n,
                         int n_passes, const int* shifts, const int* bits, uint32_t* counts, uint32_t* tickets,
                         uint64_t* status, const uint32_t* epoch_base, uint32_t& epoch, uint32_t* err,
-                        hipStream_t s) {
+                        const uint32_t* first_block_n, hipStream_t s) {
     int cur = 0;
     if (max_n <= 0) return cur;
     const uint32_t nb = (uint32_t)((max_n + kThreads * KPT - 1) / (kThreads * KPT));
     for (int p = 0; p < n_passes; ++p) {
         if ((1 << bits[p]) > MAXB) return -1;
         const int64_t cn = (int64_t)nb << bits[p];
-        radix_upsweep_kernel<KPT, MAXB><<<nb, kThreads, 0, s>>>(keys[cur], d_n, max_n, shifts[p], bits[p], counts,
-                                                                 nb);
+        // first_block_n: the first pass's blocks and digit counts come from the compaction
+        const uint32_t* block_n = p == 0 ? first_block_n : nullptr;
+        if (!block_n)
+            radix_upsweep_kernel<KPT, MAXB><<<nb, kThreads, 0, s>>>(keys[cur], d_n, max_n, shifts[p], bits[p],
+                                                                     counts, nb);
         exclusive_scan_kernel<<<(unsigned)((cn + kScanChunk - 1) / kScanChunk), kThreads, 0, s>>>(
             counts, cn, tickets + p, status, epoch_base, ++epoch, err);
         if (v2)
             radix_downsweep_kernel<KPT, true, MAXB><<<nb, kThreads, 0, s>>>(
                 keys[cur], vals[cur], v2[cur], keys[cur ^ 1], vals[cur ^ 1], v2[cur ^ 1], d_n, max_n, shifts[p],
-                bits[p], counts, nb);
+                bits[p], counts, nb, block_n);
         else
             radix_downsweep_kernel<KPT, false, MAXB><<<nb, kThreads, 0, s>>>(
                 keys[cur], vals[cur], nullptr, keys[cur ^ 1], vals[cur ^ 1], nullptr, d_n, max_n, shifts[p], bits[p],
-                counts, nb);
+                counts, nb, block_n);
         cur ^= 1;
     }
     return cur;
@@ -468,12 +490,15 @@ static int radix_passes(uint32_t* keys[2], uint32_t* vals[2], uint32_t* v2[2], c
 
 int radix_sort(uint32_t* keys[2], uint32_t* vals[2], uint32_t* v2[2], const uint32_t* d_n, int64_t max_n, bool depth,
                int n_passes, const int* shifts, const int* bits, uint32_t* counts, uint32_t* tickets,
-               uint64_t* status, const uint32_t* epoch_base, uint32_t& epoch, uint32_t* err, hipStream_t s) {
+               uint64_t* status, const uint32_t* epoch_base, uint32_t& epoch, uint32_t* err,
+               const uint32_t* first_block_n, hipStream_t s) {
     if (depth)
         return radix_passes<kDepthKeysPerThread, kDepthMaxDigits>(keys, vals, v2, d_n, max_n, n_passes, shifts, bits,
-                                                                  counts, tickets, status, epoch_base, epoch, err, s);
+                                                                  counts, tickets, status, epoch_base, epoch, err,
+                                                                  first_block_n, s);
     return radix_passes<kTileKeysPerThread, kTileMaxDigits>(keys, vals, v2, d_n, max_n, n_passes, shifts, bits,
-                                                            counts, tickets, status, epoch_base, epoch, err, s);
+                                                            counts, tickets, status, epoch_base, epoch, err,
+                                                            first_block_n, s);
 }
 
 // ---------------------------------------------------------------- instance emission

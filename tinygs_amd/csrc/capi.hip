@@ -231,6 +231,7 @@ struct tgs_rasterizer {
     // temp
     DevBuf grad2d;
     DevBuf radix_counts;   // per-workgroup digit counts of the radix passes
+    DevBuf block_n;        // visible primitives per compaction block (the depth sort's first-pass blocks)
     DevBuf bin_ctl;     // BinCtl (zeroed at creation; all but err cleared every forward)
     hipEvent_t ev_counts = nullptr;   // recorded after the counts copy of a forward
     DevBuf lb_status;   // look-back status words (u64), epoch-tagged
@@ -332,7 +333,7 @@ int tgs_rasterizer_destroy(tgs_rasterizer* r) {
     (void)hipDeviceSynchronize();
     DevBuf* all[] = {&r->n_touched, &r->erec, &r->rec, &r->mean2d, &r->conic_opacity, &r->color, &r->depth_key,
                      &r->offs, &r->pkeys[0], &r->pkeys[1], &r->pvals[0], &r->pvals[1], &r->pnt[0], &r->pnt[1],
-                     &r->radix_counts, &r->ikeys[0],
+                     &r->radix_counts, &r->block_n, &r->ikeys[0],
                      &r->ikeys[1], &r->ivals[0], &r->ivals[1], &r->ranges, &r->tile_max, &r->n_contrib,
                      &r->ckpt, &r->items, &r->tile_loaded, &r->first_slot,
                      &r->rec_count, &r->records, &r->heavy, &r->live, &r->chunk_counts, &r->row_mask, &r->grad2d,
@@ -456,6 +457,7 @@ static int rasterizer_forward(tgs_rasterizer* r, const tgs_camera* camera, void*
         TGS_TRY(ensure(r->pnt[k], 4 * nn, s));
     }
     TGS_TRY(ensure(r->ranges, 8 * (size_t)T, s));
+    TGS_TRY(ensure(r->block_n, 4 * (size_t)std::max<int64_t>(scan_status_entries(nn), 1), s));
     TGS_TRY(ensure(r->tile_max, 4 * (size_t)T, s));
     TGS_TRY(ensure(r->tile_loaded, 4 * (size_t)T, s));
     TGS_TRY(ensure(r->n_contrib, 4 * cs, s));
@@ -492,15 +494,17 @@ static int rasterizer_forward(tgs_rasterizer* r, const tgs_camera* camera, void*
     int psel;
     {
         StageScope sc(ST_DEPTH, s);
-        launch_compact_visible(r->n_touched.as<uint32_t>(), r->depth_key.as<uint32_t>(), n, sp.key_base, pk[0],
-                               pv[0], pn[0], ctl, status, r->epoch, s);
+        launch_compact_visible(r->n_touched.as<uint32_t>(), r->depth_key.as<uint32_t>(), n, sp.key_base,
+                               sp.dshift[0], sp.dbits[0], pk[0], pv[0], pn[0], r->radix_counts.as<uint32_t>(),
+                               r->block_n.as<uint32_t>(), ctl, s);
         if (!nosync) {
             // V, I and the sticky error flag go to the host while the depth sort runs
             TGS_HIP(hipMemcpyAsync(r->h_counters, ctl, 3 * sizeof(uint32_t), hipMemcpyDeviceToHost, s));
             TGS_HIP(hipEventRecord(r->ev_counts, s));
         }
         psel = radix_sort(pk, pv, pn, &ctl->V, n, true, sp.n_dp, sp.dshift, sp.dbits, r->radix_counts.as<uint32_t>(),
-                          ctl->tickets + kTicketDepth, status, &ctl->epoch_base, r->epoch, &ctl->err, s);
+                          ctl->tickets + kTicketDepth, status, &ctl->epoch_base, r->epoch, &ctl->err,
+                          r->block_n.as<uint32_t>(), s);
         if (psel < 0) return fail(TGS_ERR_STATE, "depth sort digit width");
         r->depth_key_base = sp.key_base;
         launch_instance_offsets(pn[psel], n, r->offs.as<uint32_t>(), ctl, status, r->epoch, s);
@@ -538,7 +542,7 @@ static int rasterizer_forward(tgs_rasterizer* r, const tgs_camera* camera, void*
         StageScope sc(ST_TILES, s);
         isel = radix_sort(ik, iv, nullptr, d_inst, cap, false, sp.n_tp, sp.tshift, sp.tbits,
                           r->radix_counts.as<uint32_t>(), ctl->tickets + kTicketTile, status, &ctl->epoch_base,
-                          r->epoch, &ctl->err, s);
+                          r->epoch, &ctl->err, nullptr, s);
         if (isel < 0) return fail(TGS_ERR_STATE, "tile sort digit width");
         if (r->epoch >= kEpochStride) return fail(TGS_ERR_STATE, "look-back launches per forward exceed the epoch stride");
         launch_tile_ranges(ik[isel], d_inst, cap, r->ranges.as<uint2>(), T, s);

@@ -84,9 +84,13 @@ int64_t scan_status_entries(int64_t max_n);
 // n_touched) triples; ctl->V, ctl->I; depth-key digit histograms.
 // keys_out receives depth_key - key_base (key_base <= every visible key, so
 // the order is that of the keys).
+// Compacted inside each depth-sort block: block b's visible primitives at
+// [4096 b, 4096 b + block_n[b]) in index order; counts[d * nb + b] the
+// block's counts of the first depth pass's digit ((key >> shift) & (2^bits -
+// 1)), nb = ceil(n / 4096); V and I added into ctl (zero before).
 void launch_compact_visible(const uint32_t* n_touched, const uint32_t* depth_key, int64_t n, uint32_t key_base,
-                            uint32_t* keys_out, uint32_t* vals_out, uint32_t* nt_out, BinCtl* ctl, uint64_t* status,
-                            uint32_t& epoch, hipStream_t s);
+                            int shift, int bits, uint32_t* keys_out, uint32_t* vals_out, uint32_t* nt_out,
+                            uint32_t* counts, uint32_t* block_n, BinCtl* ctl, hipStream_t s);
 // offs[k] = exclusive scan of nt_sorted[k] over k < ctl->V; offs[V] = total.
 void launch_instance_offsets(const uint32_t* nt_sorted, int64_t max_count, uint32_t* offs, BinCtl* ctl,
                              uint64_t* status, uint32_t& epoch, hipStream_t s);
@@ -96,10 +100,13 @@ int64_t radix_count_entries(int64_t max_n, bool depth);
 // bits[p] bits at shifts[p]. v2 may be NULL. depth selects the workgroup
 // size class. Each pass uses one ticket (tickets[p]) and one epoch for the
 // scan of its count matrix. Ping-pongs between the buffers; returns the
-// index (0/1) of the result.
+// index (0/1) of the result. first_block_n (depth sort): the first pass's
+// input blocks hold first_block_n[b] keys each (launch_compact_visible's
+// blocks) and its digit counts are already in counts.
 int radix_sort(uint32_t* keys[2], uint32_t* vals[2], uint32_t* v2[2], const uint32_t* d_n, int64_t max_n, bool depth,
                int n_passes, const int* shifts, const int* bits, uint32_t* counts, uint32_t* tickets,
-               uint64_t* status, const uint32_t* epoch_base, uint32_t& epoch, uint32_t* err, hipStream_t s);
+               uint64_t* status, const uint32_t* epoch_base, uint32_t& epoch, uint32_t* err,
+               const uint32_t* first_block_n, hipStream_t s);
 // Instances in depth order: thread per depth-sorted primitive k < ctl->V,
 // slots [offs[k], offs[k + 1]).
 // Also writes first_slot[p] = offs[k] for every visible primitive p = prims[k]:
