@@ -40,18 +40,21 @@ constexpr int kTileKeysPerThread = 8;                   // tile passes: 2048 key
 constexpr int kHistCopies = 8;
 constexpr int kDepthMaxDigits = 512;                    // depth passes: digits of up to 9 bits
 constexpr int kTileMaxDigits = 256;                     // tile passes: digits of up to 8 bits
+constexpr int kDepthDownWaves = 16;                     // depth downsweep: 1024 threads x 4 keys
+constexpr int kTileDownWaves = 8;                       // tile downsweep: 512 threads x 4 keys
 
 // ---------------------------------------------------------------- workgroup scans
 
-// Exclusive scan of one value per thread across a 256-thread workgroup.
+// Exclusive scan of one value per thread across a workgroup of NW waves.
 // Returns the exclusive prefix; *total receives the workgroup sum.
+template <int NW = 4>
 __device__ __forceinline__ uint32_t block_exclusive_scan(uint32_t v, uint32_t* s_wave, uint32_t* total) {
     const uint32_t lane = threadIdx.x & 63u, w = threadIdx.x >> 6;
     const uint32_t incl = wave_inclusive_scan_u32(v);
     if (lane == 63u) s_wave[w] = incl;
     __syncthreads();
     uint32_t wave_off = 0, sum = 0;
-    for (uint32_t k = 0; k < 4; ++k) {
+    for (uint32_t k = 0; k < (uint32_t)NW; ++k) {
         const uint32_t c = s_wave[k];
         wave_off += (k < w) ? c : 0u;
         sum += c;
@@ -365,19 +368,20 @@ __global__ void __launch_bounds__(kThreads) exclusive_scan_kernel(uint32_t* __re
 // The workgroup's keys are first placed in LDS in digit order and written
 // out by consecutive threads, so each store instruction covers contiguous
 // runs.
-template <int KPT, bool PAYLOAD2, int MAXB>
-__global__ void __launch_bounds__(kThreads) radix_downsweep_kernel(
+template <int KPT, bool PAYLOAD2, int MAXB, int NW>
+__global__ void __launch_bounds__(64 * NW) radix_downsweep_kernel(
     const uint32_t* __restrict__ keys_in, const uint32_t* __restrict__ vals_in, const uint32_t* __restrict__ v2_in,
     uint32_t* __restrict__ keys_out, uint32_t* __restrict__ vals_out, uint32_t* __restrict__ v2_out,
     const uint32_t* d_n, int64_t max_n, int shift, int bits, const uint32_t* __restrict__ offsets, uint32_t nb,
     const uint32_t* __restrict__ block_n) {
-    constexpr int kChunk = kThreads * KPT;
-    constexpr int kBpt = MAXB / kThreads;   // digits per thread in the workgroup scan (1 or 2)
-    static_assert(MAXB == kThreads || MAXB == 2 * kThreads, "256 or 512 digits");
-    __shared__ uint32_t s_cnt[4][MAXB];
+    constexpr int kNT = 64 * NW;             // threads
+    constexpr int kChunk = kNT * KPT;
+    constexpr int kBpt = MAXB > kNT ? MAXB / kNT : 1;   // digits per thread in the workgroup scan
+    static_assert(MAXB % kNT == 0 || kNT % MAXB == 0, "digits split evenly over the threads");
+    __shared__ uint32_t s_cnt[NW][MAXB];
     __shared__ uint32_t s_gofs[MAXB];
     __shared__ uint32_t s_key[kChunk], s_val[kChunk], s_v2[PAYLOAD2 ? kChunk : 1];
-    __shared__ uint32_t s_wave[4];
+    __shared__ uint32_t s_wave[NW];
     const uint32_t t = threadIdx.x, lane = t & 63u, w = t >> 6;
     const uint32_t bins = 1u << bits, dmask = bins - 1u;
     const int64_t blk = (int64_t)blockIdx.x * kChunk;
@@ -385,7 +389,7 @@ __global__ void __launch_bounds__(kThreads) radix_downsweep_kernel(
     // block of the first depth pass); otherwise the first n keys are dense
     const int64_t n = block_n ? blk + (int64_t)block_n[blockIdx.x] : resolve_n(d_n, max_n);
     if (blk >= n) return;
-    for (int k = t; k < 4 * MAXB; k += kThreads) (&s_cnt[0][0])[k] = 0;
+    for (int k = t; k < NW * MAXB; k += kNT) (&s_cnt[0][0])[k] = 0;
     uint32_t gofs[kBpt];   // thread t owns digits kBpt t .. kBpt t + kBpt - 1
 #pragma unroll
     for (int q = 0; q < kBpt; ++q) {
@@ -405,27 +409,31 @@ __global__ void __launch_bounds__(kThreads) radix_downsweep_kernel(
     }
     rank_keys<KPT, MAXB>(key, base, n, shift, bits, s_cnt, pos);
     __syncthreads();
-    uint32_t c[kBpt][3], tot[kBpt], total = 0;
+    uint32_t c[kBpt][NW], tot[kBpt], total = 0;
 #pragma unroll
     for (int q = 0; q < kBpt; ++q) {
         const uint32_t d = kBpt * t + (uint32_t)q;
-        c[q][0] = s_cnt[0][d];
-        c[q][1] = s_cnt[1][d];
-        c[q][2] = s_cnt[2][d];
-        tot[q] = d < bins ? c[q][0] + c[q][1] + c[q][2] + s_cnt[3][d] : 0u;
+        tot[q] = 0;
+#pragma unroll
+        for (int k = 0; k < NW; ++k) {
+            c[q][k] = d < bins ? s_cnt[k][d] : 0u;
+            tot[q] += c[q][k];
+        }
         total += tot[q];
     }
     uint32_t unused;
-    uint32_t lstart = block_exclusive_scan(total, s_wave, &unused);   // digit start inside the workgroup
+    uint32_t lstart = block_exclusive_scan<NW>(total, s_wave, &unused);   // digit start inside the workgroup
 #pragma unroll
     for (int q = 0; q < kBpt; ++q) {
         const uint32_t d = kBpt * t + (uint32_t)q;
         if (d < bins) {
             s_gofs[d] = gofs[q] - lstart;
-            s_cnt[0][d] = lstart;
-            s_cnt[1][d] = lstart + c[q][0];
-            s_cnt[2][d] = lstart + c[q][0] + c[q][1];
-            s_cnt[3][d] = lstart + c[q][0] + c[q][1] + c[q][2];
+            uint32_t run = lstart;
+#pragma unroll
+            for (int k = 0; k < NW; ++k) {
+                s_cnt[k][d] = run;
+                run += c[q][k];
+            }
         }
         lstart += tot[q];
     }
@@ -441,7 +449,7 @@ __global__ void __launch_bounds__(kThreads) radix_downsweep_kernel(
     }
     __syncthreads();
     const uint32_t cnt = (uint32_t)min((int64_t)kChunk, n - blk);
-    for (uint32_t i = t; i < cnt; i += kThreads) {
+    for (uint32_t i = t; i < cnt; i += kNT) {
         const uint32_t k = s_key[i];
         const uint32_t o = s_gofs[(k >> shift) & dmask] + i;
         if (o < (uint64_t)max_n) {   // always true when the counts match the keys
@@ -457,7 +465,9 @@ int64_t radix_count_entries(int64_t max_n, bool depth) {
     return ((max_n + chunk - 1) / chunk) * (depth ? kDepthMaxDigits : kTileMaxDigits);
 }
 
-template <int KPT, int MAXB>
+// DW: waves per downsweep workgroup; its keys per thread shrink so that a
+// downsweep workgroup covers the same keys as an upsweep one.
+template <int KPT, int MAXB, int DW>
 static int radix_passes(uint32_t* keys[2], uint32_t* vals[2], uint32_t* v2[2], const uint32_t* d_n, int64_t max_n,
                         int n_passes, const int* shifts, const int* bits, uint32_t* counts, uint32_t* tickets,
                         uint64_t* status, const uint32_t* epoch_base, uint32_t& epoch, uint32_t* err,
@@ -475,12 +485,14 @@ static int radix_passes(uint32_t* keys[2], uint32_t* vals[2], uint32_t* v2[2], c
                                                                      counts, nb);
         exclusive_scan_kernel<<<(unsigned)((cn + kScanChunk - 1) / kScanChunk), kThreads, 0, s>>>(
             counts, cn, tickets + p, status, epoch_base, ++epoch, err);
+        constexpr int kDownKpt = KPT * (kThreads / 64) / DW;
+        static_assert(kDownKpt * 64 * DW == KPT * kThreads, "downsweep and upsweep blocks agree");
         if (v2)
-            radix_downsweep_kernel<KPT, true, MAXB><<<nb, kThreads, 0, s>>>(
+            radix_downsweep_kernel<kDownKpt, true, MAXB, DW><<<nb, 64 * DW, 0, s>>>(
                 keys[cur], vals[cur], v2[cur], keys[cur ^ 1], vals[cur ^ 1], v2[cur ^ 1], d_n, max_n, shifts[p],
                 bits[p], counts, nb, block_n);
         else
-            radix_downsweep_kernel<KPT, false, MAXB><<<nb, kThreads, 0, s>>>(
+            radix_downsweep_kernel<kDownKpt, false, MAXB, DW><<<nb, 64 * DW, 0, s>>>(
                 keys[cur], vals[cur], nullptr, keys[cur ^ 1], vals[cur ^ 1], nullptr, d_n, max_n, shifts[p], bits[p],
                 counts, nb, block_n);
         cur ^= 1;
@@ -493,10 +505,10 @@ int radix_sort(uint32_t* keys[2], uint32_t* vals[2], uint32_t* v2[2], const uint
                uint64_t* status, const uint32_t* epoch_base, uint32_t& epoch, uint32_t* err,
                const uint32_t* first_block_n, hipStream_t s) {
     if (depth)
-        return radix_passes<kDepthKeysPerThread, kDepthMaxDigits>(keys, vals, v2, d_n, max_n, n_passes, shifts, bits,
+        return radix_passes<kDepthKeysPerThread, kDepthMaxDigits, kDepthDownWaves>(keys, vals, v2, d_n, max_n, n_passes, shifts, bits,
                                                                   counts, tickets, status, epoch_base, epoch, err,
                                                                   first_block_n, s);
-    return radix_passes<kTileKeysPerThread, kTileMaxDigits>(keys, vals, v2, d_n, max_n, n_passes, shifts, bits,
+    return radix_passes<kTileKeysPerThread, kTileMaxDigits, kTileDownWaves>(keys, vals, v2, d_n, max_n, n_passes, shifts, bits,
                                                             counts, tickets, status, epoch_base, epoch, err,
                                                             first_block_n, s);
 }
