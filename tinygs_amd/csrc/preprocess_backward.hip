@@ -607,7 +607,9 @@ __global__ void __launch_bounds__(256) preprocess_backward_live_kernel(
             else
                 gr[44] = v[44];
         } else {
-            for (int j = 0; j < 3 * nb; ++j) gr[j] += v[j];
+#pragma unroll
+            for (int j = 0; j < 45; ++j)   // constant indices keep v in registers
+                if (j < 3 * nb) gr[j] += v[j];
         }
     }
     if constexpr (kPose) {
