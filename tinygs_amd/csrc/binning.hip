@@ -31,8 +31,10 @@
 namespace tgs {
 
 constexpr int kThreads = 256;
-constexpr int kScanRounds = 16;
-constexpr int kScanChunk = kThreads * kScanRounds;     // 4096 elements per scan workgroup
+constexpr int kScanChunk = 4096;                        // elements per scan / compaction workgroup
+constexpr int kScanWaves = 16;                          // scan / compaction workgroups: 1024 threads x 4 elements
+constexpr int kScanThreads = 64 * kScanWaves;
+constexpr int kScanRounds = kScanChunk / kScanThreads;
 constexpr int kDepthKeysPerThread = 16;                 // depth passes: 4096 keys per workgroup
 constexpr int kTileKeysPerThread = 8;                   // tile passes: 2048 keys per workgroup (4096 measured 7 us slower)
 // LDS histograms per digit count (lane & (kHistCopies - 1) picks one): keys
@@ -40,8 +42,8 @@ constexpr int kTileKeysPerThread = 8;                   // tile passes: 2048 key
 constexpr int kHistCopies = 8;
 constexpr int kDepthMaxDigits = 512;                    // depth passes: digits of up to 9 bits
 constexpr int kTileMaxDigits = 256;                     // tile passes: digits of up to 8 bits
-constexpr int kDepthDownWaves = 16;                     // depth downsweep: 1024 threads x 4 keys
-constexpr int kTileDownWaves = 8;                       // tile downsweep: 512 threads x 4 keys
+constexpr int kDepthSortWaves = 16;                     // depth up / downsweeps: 1024 threads x 4 keys
+constexpr int kTileSortWaves = 8;                       // tile up / downsweeps: 512 threads x 4 keys
 
 // ---------------------------------------------------------------- workgroup scans
 
@@ -156,7 +158,7 @@ __device__ __forceinline__ uint64_t match_digit(uint32_t d, int bits, bool valid
 // no device-wide scan is needed. V and I = sum of n_touched by one atomic add
 // per block each (integer sums: the same totals in any order).
 static_assert(kScanChunk == kThreads * kDepthKeysPerThread, "compaction blocks are the depth sort's blocks");
-__global__ void __launch_bounds__(kThreads) compact_count_kernel(const uint32_t* __restrict__ n_touched,
+__global__ void __launch_bounds__(kScanThreads) compact_count_kernel(const uint32_t* __restrict__ n_touched,
                                                                  const uint32_t* __restrict__ depth_key, int64_t n,
                                                                  uint32_t key_base, int shift, int bits,
                                                                  uint32_t* __restrict__ keys_out,
@@ -165,19 +167,19 @@ __global__ void __launch_bounds__(kThreads) compact_count_kernel(const uint32_t*
                                                                  uint32_t* __restrict__ counts,
                                                                  uint32_t* __restrict__ block_n, BinCtl* ctl) {
     __shared__ uint32_t s_rw[64];
-    __shared__ uint32_t s_nt[4];
+    __shared__ uint32_t s_nt[kScanWaves];
     __shared__ uint32_t s_hist[kHistCopies][kDepthMaxDigits];
     const uint32_t t = threadIdx.x, lane = t & 63u, w = t >> 6;
     const uint32_t b = blockIdx.x, nb = gridDim.x;
     const uint32_t bins = 1u << bits, dmask = bins - 1u;
-    for (uint32_t e = t; e < (uint32_t)(kHistCopies * kDepthMaxDigits); e += kThreads) (&s_hist[0][0])[e] = 0u;
+    for (uint32_t e = t; e < (uint32_t)(kHistCopies * kDepthMaxDigits); e += kScanThreads) (&s_hist[0][0])[e] = 0u;
     const int64_t blk = (int64_t)b * kScanChunk;
     const int64_t base = blk + t;
     uint32_t key[kScanRounds], nt[kScanRounds], vis[kScanRounds], ex[kScanRounds];
     uint32_t ntsum = 0;
 #pragma unroll
     for (int r = 0; r < kScanRounds; ++r) {
-        const int64_t i = base + (int64_t)r * kThreads;
+        const int64_t i = base + (int64_t)r * kScanThreads;
         nt[r] = i < n ? n_touched[i] : 0u;
         key[r] = i < n ? depth_key[i] - key_base : 0u;
     }
@@ -189,13 +191,13 @@ __global__ void __launch_bounds__(kThreads) compact_count_kernel(const uint32_t*
     const uint32_t wnt = wave_sum_u32(ntsum);
     if (lane == 0) s_nt[w] = wnt;
     uint32_t total;
-    striped_scan16_u32(vis, ex, &total, s_rw);   // barriers inside: s_nt and the zeroed histograms visible after it
+    striped_scan_u32<kScanRounds, kScanWaves>(vis, ex, &total, s_rw);   // barriers inside: s_nt and the zeroed histograms visible after it
 #pragma unroll
     for (int r = 0; r < kScanRounds; ++r) {
         if (vis[r]) {
             const int64_t pos = blk + ex[r];
             keys_out[pos] = key[r];
-            vals_out[pos] = (uint32_t)(base + (int64_t)r * kThreads);
+            vals_out[pos] = (uint32_t)(base + (int64_t)r * kScanThreads);
             nt_out[pos] = nt[r];
             atomicAdd(&s_hist[lane & (kHistCopies - 1)][(key[r] >> shift) & dmask], 1u);
         }
@@ -203,11 +205,12 @@ __global__ void __launch_bounds__(kThreads) compact_count_kernel(const uint32_t*
     if (t == 0) {
         block_n[b] = total;
         if (total) atomicAdd(&ctl->V, total);
-        const uint32_t bsum = s_nt[0] + s_nt[1] + s_nt[2] + s_nt[3];
+        uint32_t bsum = 0;
+        for (int k = 0; k < kScanWaves; ++k) bsum += s_nt[k];
         if (bsum) atomicAdd(&ctl->I, bsum);
     }
     __syncthreads();
-    for (uint32_t d = t; d < bins; d += kThreads) {
+    for (uint32_t d = t; d < bins; d += kScanThreads) {
         uint32_t c = 0;
 #pragma unroll
         for (int k = 0; k < kHistCopies; ++k) c += s_hist[k][d];
@@ -220,7 +223,7 @@ void launch_compact_visible(const uint32_t* n_touched, const uint32_t* depth_key
                             uint32_t* counts, uint32_t* block_n, BinCtl* ctl, hipStream_t s) {
     if (n <= 0) return;
     const uint32_t nb = (uint32_t)((n + kScanChunk - 1) / kScanChunk);
-    compact_count_kernel<<<nb, kThreads, 0, s>>>(n_touched, depth_key, n, key_base, shift, bits, keys_out, vals_out,
+    compact_count_kernel<<<nb, kScanThreads, 0, s>>>(n_touched, depth_key, n, key_base, shift, bits, keys_out, vals_out,
                                                  nt_out, counts, block_n, ctl);
 }
 
@@ -228,7 +231,7 @@ void launch_compact_visible(const uint32_t* n_touched, const uint32_t* depth_key
 
 // offs[k] = exclusive scan of nt[k] (n_touched in depth order) over k < V;
 // offs[V] = the total.
-__global__ void __launch_bounds__(kThreads) offsets_kernel(const uint32_t* __restrict__ nt, int64_t max_count,
+__global__ void __launch_bounds__(kScanThreads) offsets_kernel(const uint32_t* __restrict__ nt, int64_t max_count,
                                                            uint32_t* __restrict__ offs, BinCtl* ctl,
                                                            uint64_t* status, uint32_t epoch) {
     __shared__ uint32_t s_rw[64];
@@ -241,11 +244,11 @@ __global__ void __launch_bounds__(kThreads) offsets_kernel(const uint32_t* __res
     uint32_t c[kScanRounds], ex[kScanRounds];
 #pragma unroll
     for (int r = 0; r < kScanRounds; ++r) {
-        const int64_t i = base + (int64_t)r * kThreads;
+        const int64_t i = base + (int64_t)r * kScanThreads;
         c[r] = i < n ? nt[i] : 0u;
     }
     uint32_t total;
-    striped_scan16_u32(c, ex, &total, s_rw);
+    striped_scan_u32<kScanRounds, kScanWaves>(c, ex, &total, s_rw);
     if (w == 0) {
         const uint32_t excl = wave_look_back(status, bid, total, ctl->epoch_base + epoch, &ctl->err);
         if (lane == 0) {
@@ -257,7 +260,7 @@ __global__ void __launch_bounds__(kThreads) offsets_kernel(const uint32_t* __res
     const uint32_t b0 = s_base;
 #pragma unroll
     for (int r = 0; r < kScanRounds; ++r) {
-        const int64_t i = base + (int64_t)r * kThreads;
+        const int64_t i = base + (int64_t)r * kScanThreads;
         if (i < n) offs[i] = b0 + ex[r];
     }
 }
@@ -266,7 +269,7 @@ void launch_instance_offsets(const uint32_t* nt_sorted, int64_t max_count, uint3
                              uint64_t* status, uint32_t& epoch, hipStream_t s) {
     if (max_count <= 0) return;
     const uint32_t nb = (uint32_t)((max_count + kScanChunk - 1) / kScanChunk);
-    offsets_kernel<<<nb, kThreads, 0, s>>>(nt_sorted, max_count, offs, ctl, status, ++epoch);
+    offsets_kernel<<<nb, kScanThreads, 0, s>>>(nt_sorted, max_count, offs, ctl, status, ++epoch);
 }
 
 int64_t scan_status_entries(int64_t max_n) { return (max_n + kScanChunk - 1) / kScanChunk; }
@@ -299,18 +302,19 @@ __device__ __forceinline__ void rank_keys(const uint32_t key[KPT], int64_t base,
 // key into one of kHistCopies histograms (by lane), summed at the end: keys
 // that arrive clustered (the instances of one primitive share their tile
 // digits) would otherwise serialise on one address.
-template <int KPT, int MAXB>
-__global__ void __launch_bounds__(kThreads) radix_upsweep_kernel(const uint32_t* __restrict__ keys,
-                                                                 const uint32_t* d_n, int64_t max_n, int shift,
-                                                                 int bits, uint32_t* __restrict__ counts,
-                                                                 uint32_t nb) {
+template <int KPT, int MAXB, int NW>
+__global__ void __launch_bounds__(64 * NW) radix_upsweep_kernel(const uint32_t* __restrict__ keys,
+                                                                const uint32_t* d_n, int64_t max_n, int shift,
+                                                                int bits, uint32_t* __restrict__ counts,
+                                                                uint32_t nb) {
+    constexpr int kNT = 64 * NW;
     __shared__ uint32_t s_hist[kHistCopies][MAXB];
     const uint32_t t = threadIdx.x, lane = t & 63u, w = t >> 6;
     const uint32_t bins = 1u << bits, dmask = bins - 1u;
-    for (uint32_t b = t; b < (uint32_t)(kHistCopies * MAXB); b += kThreads) (&s_hist[0][0])[b] = 0u;
+    for (uint32_t b = t; b < (uint32_t)(kHistCopies * MAXB); b += kNT) (&s_hist[0][0])[b] = 0u;
     __syncthreads();
     const int64_t n = resolve_n(d_n, max_n);
-    const int64_t base = (int64_t)blockIdx.x * (kThreads * KPT) + (int64_t)w * (64 * KPT);
+    const int64_t base = (int64_t)blockIdx.x * (kNT * KPT) + (int64_t)w * (64 * KPT);
     uint32_t key[KPT];
 #pragma unroll
     for (int r = 0; r < KPT; ++r) {
@@ -321,7 +325,7 @@ __global__ void __launch_bounds__(kThreads) radix_upsweep_kernel(const uint32_t*
     for (int r = 0; r < KPT; ++r)
         if (base + (int64_t)r * 64 + lane < n) atomicAdd(&s_hist[lane & (kHistCopies - 1)][(key[r] >> shift) & dmask], 1u);
     __syncthreads();
-    for (uint32_t b = t; b < bins; b += kThreads) {
+    for (uint32_t b = t; b < bins; b += kNT) {
         uint32_t c = 0;
 #pragma unroll
         for (int k = 0; k < kHistCopies; ++k) c += s_hist[k][b];
@@ -333,7 +337,7 @@ __global__ void __launch_bounds__(kThreads) radix_upsweep_kernel(const uint32_t*
 // decoupled look-back). Applied to the digit-major count matrix it yields
 // every (digit, workgroup) output offset: digit start + counts of earlier
 // workgroups for that digit.
-__global__ void __launch_bounds__(kThreads) exclusive_scan_kernel(uint32_t* __restrict__ data, int64_t n,
+__global__ void __launch_bounds__(kScanThreads) exclusive_scan_kernel(uint32_t* __restrict__ data, int64_t n,
                                                                   uint32_t* ticket, uint64_t* status,
                                                                   const uint32_t* epoch_base, uint32_t epoch,
                                                                   uint32_t* err) {
@@ -345,11 +349,11 @@ __global__ void __launch_bounds__(kThreads) exclusive_scan_kernel(uint32_t* __re
     uint32_t c[kScanRounds], ex[kScanRounds];
 #pragma unroll
     for (int r = 0; r < kScanRounds; ++r) {
-        const int64_t i = base + (int64_t)r * kThreads;
+        const int64_t i = base + (int64_t)r * kScanThreads;
         c[r] = i < n ? data[i] : 0u;
     }
     uint32_t total;
-    striped_scan16_u32(c, ex, &total, s_rw);
+    striped_scan_u32<kScanRounds, kScanWaves>(c, ex, &total, s_rw);
     if (w == 0) {
         const uint32_t excl = wave_look_back(status, bid, total, *epoch_base + epoch, err);
         if (lane == 0) s_base = excl;
@@ -358,7 +362,7 @@ __global__ void __launch_bounds__(kThreads) exclusive_scan_kernel(uint32_t* __re
     const uint32_t b0 = s_base;
 #pragma unroll
     for (int r = 0; r < kScanRounds; ++r) {
-        const int64_t i = base + (int64_t)r * kThreads;
+        const int64_t i = base + (int64_t)r * kScanThreads;
         if (i < n) data[i] = b0 + ex[r];
     }
 }
@@ -465,8 +469,8 @@ int64_t radix_count_entries(int64_t max_n, bool depth) {
     return ((max_n + chunk - 1) / chunk) * (depth ? kDepthMaxDigits : kTileMaxDigits);
 }
 
-// DW: waves per downsweep workgroup; its keys per thread shrink so that a
-// downsweep workgroup covers the same keys as an upsweep one.
+// DW: waves per upsweep / downsweep workgroup; the keys per thread shrink so
+// that a workgroup still covers 256 KPT keys.
 template <int KPT, int MAXB, int DW>
 static int radix_passes(uint32_t* keys[2], uint32_t* vals[2], uint32_t* v2[2], const uint32_t* d_n, int64_t max_n,
                         int n_passes, const int* shifts, const int* bits, uint32_t* counts, uint32_t* tickets,
@@ -475,18 +479,18 @@ static int radix_passes(uint32_t* keys[2], uint32_t* vals[2], uint32_t* v2[2], c
     int cur = 0;
     if (max_n <= 0) return cur;
     const uint32_t nb = (uint32_t)((max_n + kThreads * KPT - 1) / (kThreads * KPT));
+    constexpr int kDownKpt = KPT * (kThreads / 64) / DW;
+    static_assert(kDownKpt * 64 * DW == KPT * kThreads, "blocks of 256 KPT keys");
     for (int p = 0; p < n_passes; ++p) {
         if ((1 << bits[p]) > MAXB) return -1;
         const int64_t cn = (int64_t)nb << bits[p];
         // first_block_n: the first pass's blocks and digit counts come from the compaction
         const uint32_t* block_n = p == 0 ? first_block_n : nullptr;
         if (!block_n)
-            radix_upsweep_kernel<KPT, MAXB><<<nb, kThreads, 0, s>>>(keys[cur], d_n, max_n, shifts[p], bits[p],
-                                                                     counts, nb);
-        exclusive_scan_kernel<<<(unsigned)((cn + kScanChunk - 1) / kScanChunk), kThreads, 0, s>>>(
+            radix_upsweep_kernel<kDownKpt, MAXB, DW><<<nb, 64 * DW, 0, s>>>(keys[cur], d_n, max_n, shifts[p],
+                                                                             bits[p], counts, nb);
+        exclusive_scan_kernel<<<(unsigned)((cn + kScanChunk - 1) / kScanChunk), kScanThreads, 0, s>>>(
             counts, cn, tickets + p, status, epoch_base, ++epoch, err);
-        constexpr int kDownKpt = KPT * (kThreads / 64) / DW;
-        static_assert(kDownKpt * 64 * DW == KPT * kThreads, "downsweep and upsweep blocks agree");
         if (v2)
             radix_downsweep_kernel<kDownKpt, true, MAXB, DW><<<nb, 64 * DW, 0, s>>>(
                 keys[cur], vals[cur], v2[cur], keys[cur ^ 1], vals[cur ^ 1], v2[cur ^ 1], d_n, max_n, shifts[p],
@@ -505,10 +509,10 @@ int radix_sort(uint32_t* keys[2], uint32_t* vals[2], uint32_t* v2[2], const uint
                uint64_t* status, const uint32_t* epoch_base, uint32_t& epoch, uint32_t* err,
                const uint32_t* first_block_n, hipStream_t s) {
     if (depth)
-        return radix_passes<kDepthKeysPerThread, kDepthMaxDigits, kDepthDownWaves>(keys, vals, v2, d_n, max_n, n_passes, shifts, bits,
+        return radix_passes<kDepthKeysPerThread, kDepthMaxDigits, kDepthSortWaves>(keys, vals, v2, d_n, max_n, n_passes, shifts, bits,
                                                                   counts, tickets, status, epoch_base, epoch, err,
                                                                   first_block_n, s);
-    return radix_passes<kTileKeysPerThread, kTileMaxDigits, kTileDownWaves>(keys, vals, v2, d_n, max_n, n_passes, shifts, bits,
+    return radix_passes<kTileKeysPerThread, kTileMaxDigits, kTileSortWaves>(keys, vals, v2, d_n, max_n, n_passes, shifts, bits,
                                                             counts, tickets, status, epoch_base, epoch, err,
                                                             first_block_n, s);
 }

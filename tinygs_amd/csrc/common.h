@@ -238,29 +238,29 @@ __device__ __forceinline__ void wave_reduce9(float v[12], float t[3]) {
     for (int m = 0; m < 3; ++m) t[m] += dpp_ror_f32<0x121>(t[m]);
 }
 
-// Exclusive scan of R striped values per thread (R <= 16): value r of
-// thread t is element r * 256 + t of a 256-thread workgroup's chunk, so
-// consecutive lanes hold consecutive elements in every round. s_rw: 4 R
-// words of LDS.
-template <int R>
+// Exclusive scan of R striped values per thread over a workgroup of NW
+// waves (R NW <= 64): value r of thread t is element r * 64 NW + t of the
+// workgroup's chunk, so consecutive lanes hold consecutive elements in every
+// round. s_rw: R NW words of LDS.
+template <int R, int NW = 4>
 __device__ __forceinline__ void striped_scan_u32(const uint32_t v[R], uint32_t ex[R], uint32_t* total,
                                                  uint32_t* s_rw) {
-    static_assert(R >= 1 && R <= 16, "at most 64 (round, wave) partial sums");
+    static_assert(R >= 1 && R * NW <= 64, "at most 64 (round, wave) partial sums");
     const uint32_t lane = threadIdx.x & 63u, w = threadIdx.x >> 6;
 #pragma unroll
     for (int r = 0; r < R; ++r) {
         const uint32_t incl = wave_inclusive_scan_u32(v[r]);
         ex[r] = incl - v[r];
-        if (lane == 63u) s_rw[r * 4 + w] = incl;
+        if (lane == 63u) s_rw[r * NW + w] = incl;
     }
     __syncthreads();
     // (round, wave) partial sums in element order; every wave scans them itself
-    const uint32_t x = lane < 4u * R ? s_rw[lane] : 0u;
+    const uint32_t x = lane < (uint32_t)(NW * R) ? s_rw[lane] : 0u;
     const uint32_t xi = wave_inclusive_scan_u32(x);
     *total = readlane_u32(xi, 63);
     const uint32_t xe = xi - x;
 #pragma unroll
-    for (int r = 0; r < R; ++r) ex[r] += readlane_u32(xe, (uint32_t)(r * 4) + w);
+    for (int r = 0; r < R; ++r) ex[r] += readlane_u32(xe, (uint32_t)(r * NW) + w);
     __syncthreads();   // s_rw may be reused after this
 }
 __device__ __forceinline__ void striped_scan16_u32(const uint32_t v[16], uint32_t ex[16], uint32_t* total,
