@@ -160,7 +160,11 @@ __device__ __forceinline__ void ssim_tile_of(uint32_t& tx, uint32_t& ty, uint32_
     ch = k / (gx * gy);
 }
 
-// Fused L1 + SSIM forward. s_l1 == 0 disables L1; assign writes loss / grad
+// Fused L1 + SSIM forward. The SSIM value and all three derivative maps
+// depend on the variances only through sigma1^2 + sigma2^2, so the two second
+// moments are filtered as one, E[x^2 + y^2] (the filter is linear): four
+// filtered moments instead of the reference's five, which changes the sums by
+// rounding only. s_l1 == 0 disables L1; assign writes loss / grad
 // instead of accumulating (grad then holds the L1 part, or 0). dm_* may be
 // NULL (loss only). SSIM terms only inside W x H; L1 over the whole padded
 // image, like the reference's L1 over all padded elements. One workgroup per
@@ -175,7 +179,7 @@ __global__ void __launch_bounds__(256) l1_ssim_forward_kernel(uint32_t W, uint32
                                                               float* __restrict__ dm_mu, float* __restrict__ dm_s1,
                                                               float* __restrict__ dm_s12) {
     __shared__ __half2 s_in[kHT][kHT];         // fp16-rounded (pred, target), exactly the values the sums use
-    __shared__ float s_h[5][kIT][kOT + 1];     // horizontal sums: x, x^2, y, y^2, xy
+    __shared__ float s_h[4][kIT][kOT + 1];     // horizontal sums: x, x^2 + y^2, y, xy
     const int t = (int)threadIdx.x;
     uint32_t tx, ty, ch;
     ssim_tile_of(tx, ty, ch);
@@ -208,39 +212,38 @@ __global__ void __launch_bounds__(256) l1_ssim_forward_kernel(uint32_t W, uint32
     // horizontal: row r, output columns 4 g .. 4 g + 3
     for (int wi = t; wi < kIT * 8; wi += 256) {
         const int r = wi >> 3, g = wi & 7;
-        float x[14], y[14];
+        float x[14], y[14], q[14], xy[14];
 #pragma unroll
         for (int d = 0; d < 14; ++d) {
             const float2 v = __half22float2(s_in[r + 3][4 * g + d + 3]);
             x[d] = v.x;
             y[d] = v.y;
+            q[d] = __builtin_fmaf(v.x, v.x, v.y * v.y);
+            xy[d] = v.x * v.y;
         }
 #pragma unroll
         for (int o = 0; o < 4; ++o) {
-            float sx = 0.f, sxx = 0.f, sy = 0.f, syy = 0.f, sxy = 0.f;
+            float sx = 0.f, sq = 0.f, sy = 0.f, sxy = 0.f;
 #pragma unroll
             for (int d = 0; d < 11; ++d) {
                 const float wv = kGauss[d];
-                const float a = x[o + d], b = y[o + d];
-                sx = __builtin_fmaf(a, wv, sx);
-                sxx = __builtin_fmaf(a * a, wv, sxx);
-                sy = __builtin_fmaf(b, wv, sy);
-                syy = __builtin_fmaf(b * b, wv, syy);
-                sxy = __builtin_fmaf(a * b, wv, sxy);
+                sx = __builtin_fmaf(x[o + d], wv, sx);
+                sq = __builtin_fmaf(q[o + d], wv, sq);
+                sy = __builtin_fmaf(y[o + d], wv, sy);
+                sxy = __builtin_fmaf(xy[o + d], wv, sxy);
             }
             s_h[0][r][4 * g + o] = sx;
-            s_h[1][r][4 * g + o] = sxx;
+            s_h[1][r][4 * g + o] = sq;
             s_h[2][r][4 * g + o] = sy;
-            s_h[3][r][4 * g + o] = syy;
-            s_h[4][r][4 * g + o] = sxy;
+            s_h[3][r][4 * g + o] = sxy;
         }
     }
     __syncthreads();
     // vertical: column vc, output rows 4 vr .. 4 vr + 3
     const int vc = t & 31, vr = t >> 5;
-    float o[5][4];
+    float o[4][4];
 #pragma unroll
-    for (int v = 0; v < 5; ++v) {
+    for (int v = 0; v < 4; ++v) {
         float col[14];
 #pragma unroll
         for (int d = 0; d < 14; ++d) col[d] = s_h[v][4 * vr + d][vc];
@@ -274,9 +277,9 @@ __global__ void __launch_bounds__(256) l1_ssim_forward_kernel(uint32_t W, uint32
         if (px < (int)W && py < (int)H) {
             const float mu1 = o[0][q], mu2 = o[2][q];
             const float mu1_sq = mu1 * mu1, mu2_sq = mu2 * mu2;
-            const float s1 = o[1][q] - mu1_sq, s2 = o[3][q] - mu2_sq, s12 = o[4][q] - mu1 * mu2;
+            const float s12 = o[3][q] - mu1 * mu2;
             const float A = mu1_sq + mu2_sq + C1;
-            const float B = s1 + s2 + C2;
+            const float B = ((o[1][q] - mu1_sq) - mu2_sq) + C2;   // sigma1^2 + sigma2^2 + C2
             const float Cc = 2.0f * mu1 * mu2 + C1;
             const float D = 2.0f * s12 + C2;
             // one reciprocal each of A and B replaces the reference's seven divisions
