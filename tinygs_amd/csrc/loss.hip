@@ -241,6 +241,23 @@ __global__ void __launch_bounds__(256) l1_ssim_forward_kernel(uint32_t W, uint32
     __syncthreads();
     // vertical: column vc, output rows 4 vr .. 4 vr + 3
     const int vc = t & 31, vr = t >> 5;
+    if (loss) loss += co;
+    if (grad) grad += co;
+    // the epilogue's own pixels (L1 terms, accumulated values) are loaded
+    // before the vertical pass, so their latency hides behind it
+    const bool acc_l = !assign && loss, acc_g = !assign && grad, l1 = s_l1 != 0.f;
+    uint32_t pidx[4];
+    float pp[4], pt[4], pl[4], pg[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const int px = bx + vc, py = by + 4 * vr + q;
+        const bool in = px < pw && py < ph;
+        pidx[q] = in ? tiled_index((uint32_t)py, (uint32_t)px, tw) : 0u;
+        pp[q] = in && l1 ? ld(pred, pidx[q]) : 0.f;
+        pt[q] = in && l1 ? ld(target, pidx[q]) : 0.f;
+        pl[q] = in && acc_l ? ld(loss, pidx[q]) : 0.f;
+        pg[q] = in && acc_g ? ld(grad, pidx[q]) : 0.f;
+    }
     float o[4][4];
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
@@ -260,17 +277,15 @@ __global__ void __launch_bounds__(256) l1_ssim_forward_kernel(uint32_t W, uint32
         dm_s1 += co;
         dm_s12 += co;
     }
-    if (loss) loss += co;
-    if (grad) grad += co;
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
         const int px = bx + vc, py = by + 4 * vr + q;
         if (px >= pw || py >= ph) continue;
-        const uint32_t idx = tiled_index((uint32_t)py, (uint32_t)px, tw);
-        float lv = (!assign && loss) ? ld(loss, idx) : 0.f;
-        float gv = (!assign && grad) ? ld(grad, idx) : 0.f;
-        if (s_l1 != 0.f) {
-            const float d = saturate(ld(pred, idx)) - ld(target, idx);
+        const uint32_t idx = pidx[q];
+        float lv = pl[q];
+        float gv = pg[q];
+        if (l1) {
+            const float d = saturate(pp[q]) - pt[q];
             lv = held(pred, __builtin_fmaf(__builtin_fabsf(d), s_l1, lv));
             gv = __builtin_fmaf(__builtin_copysignf(1.0f, d), s_l1, gv);
         }
@@ -386,6 +401,22 @@ __global__ void __launch_bounds__(256) ssim_backward_kernel(uint32_t W, uint32_t
     }
     __syncthreads();
     const int vc = t & 31, vr = t >> 5;
+    pred += co;
+    target += co;
+    grad += co;
+    // the epilogue's pixels, loaded before the vertical pass so that their
+    // latency hides behind it
+    uint32_t pidx[4];
+    float pp[4], pt[4], pg[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const int px = bx + vc, py = by + 4 * vr + q;
+        const bool in = px < (int)W && py < (int)H;
+        pidx[q] = in ? tiled_index((uint32_t)py, (uint32_t)px, tw) : 0u;
+        pp[q] = in ? ld(pred, pidx[q]) : 0.f;
+        pt[q] = in ? ld(target, pidx[q]) : 0.f;
+        pg[q] = in ? ld(grad, pidx[q]) : 0.f;
+    }
     float o[3][4];
 #pragma unroll
     for (int v = 0; v < 3; ++v) {
@@ -400,17 +431,12 @@ __global__ void __launch_bounds__(256) ssim_backward_kernel(uint32_t W, uint32_t
             o[v][q] = acc;
         }
     }
-    pred += co;
-    target += co;
-    grad += co;
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
         const int px = bx + vc, py = by + 4 * vr + q;
         if (px >= (int)W || py >= (int)H) continue;
-        const uint32_t idx = tiled_index((uint32_t)py, (uint32_t)px, tw);
-        const float dl =
-            __builtin_fmaf(ld(target, idx), o[2][q], __builtin_fmaf(2.0f * ld(pred, idx), o[1][q], o[0][q]));
-        st(grad, idx, __builtin_fmaf(-s, dl, ld(grad, idx)));
+        const float dl = __builtin_fmaf(pt[q], o[2][q], __builtin_fmaf(2.0f * pp[q], o[1][q], o[0][q]));
+        st(grad, pidx[q], __builtin_fmaf(-s, dl, pg[q]));
     }
 }
 
