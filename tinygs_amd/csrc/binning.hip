@@ -36,14 +36,14 @@ constexpr int kScanWaves = 16;                          // scan / compaction wor
 constexpr int kScanThreads = 64 * kScanWaves;
 constexpr int kScanRounds = kScanChunk / kScanThreads;
 constexpr int kDepthKeysPerThread = 16;                 // depth passes: 4096 keys per workgroup
-constexpr int kTileKeysPerThread = 8;                   // tile passes: 2048 keys per workgroup (4096 measured 7 us slower)
+constexpr int kTileKeysPerThread = 16;                  // tile passes: 4096 keys per workgroup (2048: 3 us slower, 8192: 17 us)
 // LDS histograms per digit count (lane & (kHistCopies - 1) picks one): keys
 // that arrive clustered do not serialise their atomic adds on one address
 constexpr int kHistCopies = 8;
 constexpr int kDepthMaxDigits = 512;                    // depth passes: digits of up to 9 bits
 constexpr int kTileMaxDigits = 256;                     // tile passes: digits of up to 8 bits
 constexpr int kDepthSortWaves = 16;                     // depth up / downsweeps: 1024 threads x 4 keys
-constexpr int kTileSortWaves = 8;                       // tile up / downsweeps: 512 threads x 4 keys
+constexpr int kTileSortWaves = 8;                       // tile up / downsweeps: 512 threads x 8 keys (1024 x 4: 1 us slower)
 
 // ---------------------------------------------------------------- workgroup scans
 
