@@ -126,6 +126,46 @@ __device__ __forceinline__ void sh_to_color(const ShT* __restrict__ sh0, const S
         for (int c = 0; c < 3; ++c) out[c] = out[c] + k[b] * load_as_float(r, 3 * b + c);
 }
 
+// SH-rest coefficients of a workgroup's 256 primitives are one contiguous
+// run, staged in LDS with 16-byte lane-contiguous loads. sh_stage_load issues
+// the loads first and holds them in registers through the projection and the
+// tile tests; sh_stage_store writes them to LDS and synchronises the
+// workgroup just before the colour (every thread must reach it).
+template <typename ShT>
+struct ShStage {
+    static constexpr int kVec = (256 * 45 * (int)sizeof(ShT) + 16 * 256 - 1) / (16 * 256);   // uint4 per thread
+    uint4 v[kVec];
+    int64_t blk0;
+    int count, nvec;
+};
+
+template <typename ShT>
+__device__ __forceinline__ void sh_stage_load(ShStage<ShT>& st, const ShT* __restrict__ shr, int64_t n, int bases) {
+    st.blk0 = (int64_t)blockIdx.x * 256;
+    st.count = bases > 1 ? (int)min((int64_t)256, n - st.blk0) * 45 : 0;
+    st.nvec = (st.count * (int)sizeof(ShT)) >> 4;
+    const uint4* s4 = (const uint4*)(shr + st.blk0 * 45);
+#pragma unroll
+    for (int q = 0; q < ShStage<ShT>::kVec; ++q) {
+        const int v = (int)threadIdx.x + 256 * q;
+        st.v[q] = v < st.nvec ? s4[v] : make_uint4(0u, 0u, 0u, 0u);
+    }
+}
+
+template <typename ShT>
+__device__ __forceinline__ void sh_stage_store(const ShStage<ShT>& st, ShT* s_sh, const ShT* __restrict__ shr) {
+    uint4* d4 = (uint4*)s_sh;
+#pragma unroll
+    for (int q = 0; q < ShStage<ShT>::kVec; ++q) {
+        const int v = (int)threadIdx.x + 256 * q;
+        if (v < st.nvec) d4[v] = st.v[q];
+    }
+    // the elements after the last whole 16 bytes
+    for (int e = (st.nvec << 4) / (int)sizeof(ShT) + (int)threadIdx.x; e < st.count; e += 256)
+        s_sh[e] = shr[st.blk0 * 45 + e];
+    __syncthreads();
+}
+
 template <typename ShT>
 __global__ void __launch_bounds__(256) preprocess_kernel(
     const float* __restrict__ means, const float* __restrict__ scales, const float* __restrict__ rots,
@@ -133,24 +173,10 @@ __global__ void __launch_bounds__(256) preprocess_kernel(
     CamParams cam, uint32_t* __restrict__ n_touched, uint4* __restrict__ erec, uint4* __restrict__ rec,
     float2* __restrict__ mean2d, float4* __restrict__ conic_opacity, float4* __restrict__ color_pt, uint32_t* __restrict__ depth_key,
     float4* __restrict__ densif) {
-    // SH-rest coefficients of the block's 256 primitives are one contiguous
-    // run: stage it in LDS with 16-byte lane-contiguous loads.
     __shared__ __align__(16) ShT s_sh[256 * 45];
     __shared__ uint32_t s_rect[4][kRectSlice];
-    {
-        const int64_t blk0 = (int64_t)blockIdx.x * 256;
-        const int nblk = (int)min((int64_t)256, n - blk0);
-        if (bases > 1) {
-            const int count = nblk * 45;
-            const int nvec = (count * (int)sizeof(ShT)) >> 4;
-            const uint4* s4 = (const uint4*)(shr + blk0 * 45);
-            uint4* d4 = (uint4*)s_sh;
-            for (int v = (int)threadIdx.x; v < nvec; v += 256) d4[v] = s4[v];
-            for (int e = (nvec << 4) / (int)sizeof(ShT) + (int)threadIdx.x; e < count; e += 256)
-                s_sh[e] = shr[blk0 * 45 + e];
-        }
-        __syncthreads();
-    }
+    ShStage<ShT> shs;
+    sh_stage_load(shs, shr, n, bases);
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     bool active = i < n;
     const int64_t ii = active ? i : n - 1;
@@ -263,6 +289,7 @@ __global__ void __launch_bounds__(256) preprocess_kernel(
                         });
     }
 
+    sh_stage_store(shs, s_sh, shr);
     if (i >= n) return;
     if (!active || cnt == 0) {
         n_touched[i] = 0;
@@ -300,20 +327,8 @@ __global__ void __launch_bounds__(256) preprocess16_kernel(
     uint32_t* __restrict__ depth_key, float4* __restrict__ densif) {
     __shared__ __align__(16) ShT s_sh[256 * 45];
     __shared__ uint32_t s_rect[4][kRectSlice];
-    {
-        const int64_t blk0 = (int64_t)blockIdx.x * 256;
-        const int nblk = (int)min((int64_t)256, n - blk0);
-        if (bases > 1) {
-            const int count = nblk * 45;
-            const int nvec = (count * (int)sizeof(ShT)) >> 4;
-            const uint4* s4 = (const uint4*)(shr + blk0 * 45);
-            uint4* d4 = (uint4*)s_sh;
-            for (int v = (int)threadIdx.x; v < nvec; v += 256) d4[v] = s4[v];
-            for (int e = (nvec << 4) / (int)sizeof(ShT) + (int)threadIdx.x; e < count; e += 256)
-                s_sh[e] = shr[blk0 * 45 + e];
-        }
-        __syncthreads();
-    }
+    ShStage<ShT> shs;
+    sh_stage_load(shs, shr, n, bases);
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     bool active = i < n;
     const int64_t ii = active ? i : n - 1;
@@ -431,6 +446,7 @@ __global__ void __launch_bounds__(256) preprocess16_kernel(
                         });
     }
 
+    sh_stage_store(shs, s_sh, shr);
     if (i >= n) return;
     if (!active || cnt == 0) {
         n_touched[i] = 0;
