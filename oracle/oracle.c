@@ -50,6 +50,10 @@
 #define R_SIG_HALF 0x1.715476p-1f
 #define R_SIG_ONE 0x1.715476p+0f
 #define R_ALPHA_EXP(s) orc_exp2_core(-fminf((s), 150.0f))
+/* the blend forward's accept test: 0 <= sigma' <= thr' with thr' = ln(255 o) L
+ * (float product), as one unsigned comparison of the bit patterns (thr' >= 0,
+ * and sigma' is never -0 there). alpha >= 1/255 up to rounding at the edge. */
+#define R_BLEND_ACCEPT(sigma, alpha, thr) (orc_float_to_bits(sigma) <= orc_float_to_bits((thr) * R_SIG_ONE))
 #include "oracle_impl.inc"
 #undef REAL
 #undef SFX
@@ -67,6 +71,7 @@
 #undef R_SIG_HALF
 #undef R_SIG_ONE
 #undef R_ALPHA_EXP
+#undef R_BLEND_ACCEPT
 
 /* ---------------- double instance (finite-difference checker) ---------------- */
 #define REAL double
@@ -85,6 +90,8 @@
 #define R_SIG_HALF 0.5
 #define R_SIG_ONE 1.0
 #define R_ALPHA_EXP(s) exp(-(s))
+/* the reference's tests, kernels_forward.cuh:657-663 */
+#define R_BLEND_ACCEPT(sigma, alpha, thr) ((sigma) >= 0 && (alpha) >= (REAL)(1.0f / 255.0f))
 #include "oracle_impl.inc"
 
 /* ---------------- the fp16-image rasterizer (FGS16), half arithmetic ---------------- */

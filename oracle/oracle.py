@@ -57,7 +57,7 @@ def _declare(L):
         fn.argtypes = [C.c_uint32, C.c_uint32, u32p, u32p]
         fn.restype = C.c_int64
         fn = getattr(L, pfx + "blend_forward")
-        fn.argtypes = [C.c_int, C.c_int, u32p, u32p, rp, rp, rp, rp, u32p, u32p, u32p, C.c_void_p]
+        fn.argtypes = [C.c_int, C.c_int, u32p, u32p, rp, rp, rp, rp, rp, u32p, u32p, u32p, C.c_void_p]
         fn.restype = None
         fn = getattr(L, pfx + "blend_backward")
         fn.argtypes = [C.c_int, C.c_int, u32p, u32p, rp, rp, rp, rp, rp, u32p, u32p, u32p, rp,
@@ -232,8 +232,8 @@ def blend_forward(scene, pre, bins, prec="f", with_ckpt=True):
     tmax = np.zeros(gw * gh, np.uint32)
     ckpt = np.zeros(max(nb, 1) * 256 * 4, dt) if with_ckpt else None
     getattr(L, f"orc_{prec}_blend_forward")(cam.width, cam.height, bins["ranges"], _u32(bins["inst_prim"]),
-                                            pre["mean2d"], pre["conic_opacity"], pre["color"], image, ncontrib,
-                                            tmax, offs, _ptr(ckpt))
+                                            pre["mean2d"], pre["conic_opacity"], pre["color"], pre["power_thr"],
+                                            image, ncontrib, tmax, offs, _ptr(ckpt))
     return {"image": image, "n_contrib": ncontrib, "tile_max": tmax, "bucket_offsets": offs,
             "ckpt": ckpt, "n_buckets": int(nb)}
 

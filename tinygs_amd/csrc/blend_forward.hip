@@ -25,7 +25,9 @@
 // Numerics mirror the CPU oracle: alpha = min(o 2^-sigma', 0.999) with
 // sigma' = fma(dx, fma(a L/2, dx, (b L) dy), ((c L/2) dy) dy) from the conic
 // prescaled by L = log2(e) at staging and the deterministic exp2
-// (det_exp2_core), the 1/255 cut and the 1e-4 transmittance stop with the
+// (det_exp2_core); the reference's sigma >= 0 and alpha >= 1/255 tests as
+// 0 <= sigma' <= ln(255 o) L (the preprocess's power threshold times L, equal
+// up to rounding at the edge), and the 1e-4 transmittance stop with the
 // terminating Gaussian not composited. A pixel that stopped (or lies outside
 // the image) carries T = 0: every later Gaussian then fails the transmittance
 // test and changes nothing, so no separate flag is kept.
@@ -72,9 +74,10 @@ __global__ void __launch_bounds__(256) blend_forward_kernel(CamParams cam, const
                                                             float4* __restrict__ ckpt,
                                                             uint4* __restrict__ items,
                                                             BinCtl* __restrict__ ctl) {
+    // s_a, s_b and s_c are read at one LDS address per Gaussian (offsets 0, 4 and 8 KiB)
     __shared__ float4 s_a[256];       // mx, my, a L/2, b L
     __shared__ float4 s_b[256];       // c L/2, opacity, r, g (clamped colour)
-    __shared__ float s_c[256];        // b (clamped colour)
+    __shared__ float4 s_c[256];       // b (clamped colour), accept threshold ln(255 o) L, -, -
     __shared__ uint32_t s_mask[256];  // bit q: may reach alpha >= 1/255 in 8x8 block q
     __shared__ uint16_t s_list[4][256];
     __shared__ uint32_t s_max[4];
@@ -109,7 +112,7 @@ __global__ void __launch_bounds__(256) blend_forward_kernel(CamParams cam, const
                 const float4 c = color_pt[p];
                 s_a[tid] = make_float4(m.x, m.y, co.x * kHalfLog2e, co.y * kLog2eF);
                 s_b[tid] = make_float4(co.z * kHalfLog2e, co.w, __builtin_fmaxf(c.x, 0.f), __builtin_fmaxf(c.y, 0.f));
-                s_c[tid] = __builtin_fmaxf(c.z, 0.f);
+                s_c[tid] = make_float4(__builtin_fmaxf(c.z, 0.f), c.w * kLog2eF, 0.f, 0.f);
                 // sigma > ln(255 o) + 1e-3 implies o 2^-sigma' < exp(-1e-3) / 255 (sigma' = sigma L to a few
                 // ulps), below the 1/255 cut by far more than the error of the deterministic exp2 / log
                 // (< 1e-6 relative)
@@ -141,7 +144,7 @@ __global__ void __launch_bounds__(256) blend_forward_kernel(CamParams cam, const
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
         // two marked Gaussians per step: both records are read before either is blended
-        auto blend = [&](int32_t e, const float4& a, const float4& bb, float cz) {
+        auto blend = [&](int32_t e, const float4& a, const float4& bb, const float4& cc) {
             const int32_t j = base + e;
             while (next_ck <= j) {   // bucket boundaries passed since the last marked Gaussian
                 ckpt[(size_t)(slot0 + (uint32_t)(next_ck / kBucket) - 1u) * kTilePixels + tid] =
@@ -150,12 +153,13 @@ __global__ void __launch_bounds__(256) blend_forward_kernel(CamParams cam, const
             }
             const float dx = a.x - pcx, dy = a.y - pcy;
             const float sigma = __builtin_fmaf(dx, __builtin_fmaf(a.z, dx, a.w * dy), (bb.x * dy) * dy);
-            // (sigma' < 0 is rejected below, so its clamped value does not matter)
-            const float alpha =
-                __builtin_fminf(bb.y * det_exp2_core(-__builtin_amdgcn_fmed3f(sigma, 0.f, 150.f)), kMaxAlpha);
+            // alpha only matters where ok holds (0 <= sigma' <= ln 255 L), so exp2 needs no clamp
+            const float alpha = __builtin_fminf(bb.y * det_exp2_core(-sigma), kMaxAlpha);
             const float nT = T * (1.0f - alpha);
+            // sigma >= 0 and alpha >= 1/255 as 0 <= sigma' <= thr': one unsigned compare of the
+            // bit patterns (thr' >= 0; sigma' is never -0: its last term (c L/2 dy) dy is >= +0)
+            const bool ok = f2u(sigma) <= f2u(cc.y);
             // a stopped pixel has T = 0, so nT = 0 fails the test
-            const bool ok = sigma >= 0.f && alpha >= kMinAlpha;
             const bool keep = nT >= kTransmittanceMin;
             const bool acc = ok && keep;
             // one select of the weight instead of three of the sums: fma(+0, c, C)
@@ -163,7 +167,7 @@ __global__ void __launch_bounds__(256) blend_forward_kernel(CamParams cam, const
             const float wgt = acc ? T * alpha : 0.f;
             C0 = __builtin_fmaf(wgt, bb.z, C0);
             C1 = __builtin_fmaf(wgt, bb.w, C1);
-            C2 = __builtin_fmaf(wgt, cz, C2);
+            C2 = __builtin_fmaf(wgt, cc.x, C2);
             T = ok ? (keep ? nT : 0.f) : T;
             ncontrib = acc ? (uint32_t)(j + 1) : ncontrib;
         };
@@ -173,10 +177,8 @@ __global__ void __launch_bounds__(256) blend_forward_kernel(CamParams cam, const
             const int32_t e0 = __builtin_amdgcn_readfirstlane((int)(pair & 0xffffu));
             const bool two = i + 1 < cnt;
             const int32_t e1 = two ? __builtin_amdgcn_readfirstlane((int)(pair >> 16)) : e0;
-            const float4 a0 = s_a[e0], b0 = s_b[e0];
-            const float c0 = s_c[e0];
-            const float4 a1 = s_a[e1], b1 = s_b[e1];
-            const float c1 = s_c[e1];
+            const float4 a0 = s_a[e0], b0 = s_b[e0], c0 = s_c[e0];
+            const float4 a1 = s_a[e1], b1 = s_b[e1], c1 = s_c[e1];
             blend(e0, a0, b0, c0);
             if (two) blend(e1, a1, b1, c1);
         }
