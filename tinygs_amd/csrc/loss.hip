@@ -163,8 +163,9 @@ __device__ __forceinline__ void ssim_tile_of(uint32_t& tx, uint32_t& ty, uint32_
 // Fused L1 + SSIM forward. The SSIM value and all three derivative maps
 // depend on the variances only through sigma1^2 + sigma2^2, so the two second
 // moments are filtered as one, E[x^2 + y^2] (the filter is linear): four
-// filtered moments instead of the reference's five, which changes the sums by
-// rounding only. s_l1 == 0 disables L1; assign writes loss / grad
+// filtered moments instead of the reference's five (fused_ssim.cu:232-240
+// uses sigma1^2 and sigma2^2 only in B), which changes the sums by rounding
+// only. s_l1 == 0 disables L1; assign writes loss / grad
 // instead of accumulating (grad then holds the L1 part, or 0). dm_* may be
 // NULL (loss only). SSIM terms only inside W x H; L1 over the whole padded
 // image, like the reference's L1 over all padded elements. One workgroup per
