@@ -175,8 +175,8 @@ int tgs_rasterizer_counts(tgs_rasterizer* r, int64_t* n_visible, int64_t* n_inst
 /* Internal buffers of the last forward, for parity tests (device pointers). */
 typedef struct tgs_debug_view {
     const uint32_t* n_touched;     /* [n] */
-    const uint32_t* bounds;        /* [8n] records: x_min | x_max << 16, y_min | y_max << 16, mean2d.xy,
-                                      conic a, b, c, ln(255 opacity) (float bits) */
+    const uint32_t* bounds;        /* [4n] records: x_min | x_max << 16, y_min | y_max << 16, the exact
+                                      test's outcome for rect tiles 0..31 (bit k: row-major tile k), 0 */
     const float* mean2d;           /* [2n] */
     const float* conic_opacity;    /* [4n] */
     const float* color;            /* [4n]: r, g, b (unclamped), ln(255 * opacity) */

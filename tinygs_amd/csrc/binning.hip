@@ -545,9 +545,9 @@ __device__ __forceinline__ bool will_contribute_e(float mx, float my, float ca, 
 }
 
 // Thread per depth-sorted primitive: its 16-byte emission record (bounds and
-// the preprocess's outcomes for rect tiles 0..31) is gathered once, the
-// 32-byte binning record (mean, conic, threshold) only for primitives with
-// more than 32 rect tiles; its instances fill the slots [offs[k], offs[k + 1]),
+// the preprocess's outcomes for rect tiles 0..31) is gathered once, its mean,
+// conic and threshold only for primitives with more than 32 rect tiles (from
+// the blend's own per-primitive arrays); its instances fill the slots [offs[k], offs[k + 1]),
 // so the instance array comes out in depth order. (The gathers are random:
 // depth order is not index order, and each costs a whole memory line.) The
 // rect tiles of a wave's 64 primitives are walked as one task list, 64 per
@@ -574,7 +574,10 @@ __device__ __forceinline__ bool emit_test(float mx, float my, uint32_t w0, uint3
 template <bool kHalf>
 __global__ void __launch_bounds__(256) emit_kernel(const uint32_t* __restrict__ prims,
                                                    const uint32_t* __restrict__ offs, BinCtl* ctl,
-                                                   int64_t max_count, int64_t max_inst, const uint4* __restrict__ rec,
+                                                   int64_t max_count, int64_t max_inst,
+                                                   const float2* __restrict__ mean2d,
+                                                   const uint4* __restrict__ conic_words,
+                                                   const uint4* __restrict__ thr_words,
                                                    const uint4* __restrict__ erec, uint32_t grid_w,
                                                    uint32_t* __restrict__ inst_keys,
                                                    uint32_t* __restrict__ inst_vals,
@@ -623,10 +626,12 @@ __global__ void __launch_bounds__(256) emit_kernel(const uint32_t* __restrict__ 
         x0 = e.x & 0xffffu; x1 = e.x >> 16; y0 = e.y & 0xffffu; y1 = e.y >> 16;
         bits = e.z;
         if ((x1 - x0) * (y1 - y0) > 32u) {   // tiles past the first 32 need the exact test
-            const uint4 r0 = rec[2 * (size_t)p], r1 = rec[2 * (size_t)p + 1];
-            smx = u2f(r0.z) - 0.5f;
-            smy = u2f(r0.w) - 0.5f;
-            cw0 = r1.x; cw1 = r1.y; cw2 = r1.z; pt = u2f(r1.w);
+            const float2 m = mean2d[p];
+            const uint4 cw = conic_words[p];
+            smx = m.x - 0.5f;
+            smy = m.y - 0.5f;
+            cw0 = cw.x; cw1 = cw.y; cw2 = cw.z;
+            pt = u2f(kHalf ? cw.w : thr_words[p].w);
         }
     }
     // The wave's rect tiles as one task list (rect_tasks.h); rect tiles
@@ -684,17 +689,17 @@ __global__ void __launch_bounds__(256) emit_kernel(const uint32_t* __restrict__ 
 }
 
 void launch_emit_instances(const uint32_t* prims, const uint32_t* offs, BinCtl* ctl, int64_t max_count,
-                           int64_t max_inst, const uint4* rec, const uint4* erec, uint32_t grid_w,
-                           uint32_t* inst_keys, uint32_t* inst_vals, uint32_t* first_slot, bool half_test,
-                           hipStream_t s) {
+                           int64_t max_inst, const float2* mean2d, const uint4* conic_words,
+                           const uint4* thr_words, const uint4* erec, uint32_t grid_w, uint32_t* inst_keys,
+                           uint32_t* inst_vals, uint32_t* first_slot, bool half_test, hipStream_t s) {
     if (max_count <= 0) return;
     const unsigned grid = (unsigned)((max_count + 255) / 256);
     if (half_test)
-        emit_kernel<true><<<grid, 256, 0, s>>>(prims, offs, ctl, max_count, max_inst, rec, erec, grid_w,
-                                               inst_keys, inst_vals, first_slot);
+        emit_kernel<true><<<grid, 256, 0, s>>>(prims, offs, ctl, max_count, max_inst, mean2d, conic_words,
+                                               thr_words, erec, grid_w, inst_keys, inst_vals, first_slot);
     else
-        emit_kernel<false><<<grid, 256, 0, s>>>(prims, offs, ctl, max_count, max_inst, rec, erec, grid_w,
-                                                inst_keys, inst_vals, first_slot);
+        emit_kernel<false><<<grid, 256, 0, s>>>(prims, offs, ctl, max_count, max_inst, mean2d, conic_words,
+                                                thr_words, erec, grid_w, inst_keys, inst_vals, first_slot);
 }
 
 // ---------------------------------------------------------------- ranges

@@ -207,7 +207,7 @@ struct tgs_rasterizer {
     tgs_gaussians g{};
     bool has_g = false;
     // per primitive
-    DevBuf n_touched, erec, rec, mean2d, conic_opacity, color, depth_key, offs;
+    DevBuf n_touched, erec, mean2d, conic_opacity, color, depth_key, offs;
     DevBuf pkeys[2], pvals[2], pnt[2];   // depth sort: key, primitive, n_touched
     // per instance
     DevBuf ikeys[2], ivals[2];
@@ -331,7 +331,7 @@ int tgs_rasterizer_create(const char* type, tgs_rasterizer** out) {
 int tgs_rasterizer_destroy(tgs_rasterizer* r) {
     if (!r) return TGS_OK;
     (void)hipDeviceSynchronize();
-    DevBuf* all[] = {&r->n_touched, &r->erec, &r->rec, &r->mean2d, &r->conic_opacity, &r->color, &r->depth_key,
+    DevBuf* all[] = {&r->n_touched, &r->erec, &r->mean2d, &r->conic_opacity, &r->color, &r->depth_key,
                      &r->offs, &r->pkeys[0], &r->pkeys[1], &r->pvals[0], &r->pvals[1], &r->pnt[0], &r->pnt[1],
                      &r->radix_counts, &r->block_n, &r->ikeys[0],
                      &r->ikeys[1], &r->ivals[0], &r->ivals[1], &r->ranges, &r->tile_max, &r->n_contrib,
@@ -438,7 +438,6 @@ static int rasterizer_forward(tgs_rasterizer* r, const tgs_camera* camera, void*
     const int64_t nn = n > 0 ? n : 1;
     TGS_TRY(ensure(r->n_touched, 4 * nn, s));
     TGS_TRY(ensure(r->erec, 16 * nn, s));
-    TGS_TRY(ensure(r->rec, 32 * nn, s));
     TGS_TRY(ensure(r->mean2d, 8 * nn, s));
     TGS_TRY(ensure(r->conic_opacity, 16 * nn, s));
     TGS_TRY(ensure(r->color, 16 * nn, s));
@@ -479,11 +478,10 @@ static int rasterizer_forward(tgs_rasterizer* r, const tgs_camera* camera, void*
         StageScope sc(ST_PRE, s);
         if (f16)
             launch_preprocess16(gv, cam, r->n_touched.as<uint32_t>(), r->erec.as<uint4>(),
-                                r->rec.as<uint4>(), r->mean2d.as<float2>(), r->conic_opacity.as<float4>(),
+                                r->mean2d.as<float2>(), r->conic_opacity.as<float4>(),
                                 r->color.as<uint4>(), r->depth_key.as<uint32_t>(), (float*)densification_info, s);
         else
-            launch_preprocess(gv, cam, r->n_touched.as<uint32_t>(), r->erec.as<uint4>(), r->rec.as<uint4>(),
-                              r->mean2d.as<float2>(),
+            launch_preprocess(gv, cam, r->n_touched.as<uint32_t>(), r->erec.as<uint4>(), r->mean2d.as<float2>(),
                               r->conic_opacity.as<float4>(), r->color.as<float4>(), r->depth_key.as<uint32_t>(),
                               (float*)densification_info, s);
     }
@@ -528,10 +526,11 @@ static int rasterizer_forward(tgs_rasterizer* r, const tgs_camera* camera, void*
     }
     {
         StageScope sc(ST_EMIT, s);
-        launch_emit_instances(pv[psel], r->offs.as<uint32_t>(), ctl, n, cap, r->rec.as<uint4>(),
-                              r->erec.as<uint4>(), cam.grid_w,
-                              r->ikeys[0].as<uint32_t>(), r->ivals[0].as<uint32_t>(), r->first_slot.as<uint32_t>(),
-                              f16, s);
+        // the exact tile test's words: conic_opacity and color_pt (threshold in w), or FGS16's info
+        const uint4* conic_words = f16 ? r->color.as<uint4>() : r->conic_opacity.as<uint4>();
+        launch_emit_instances(pv[psel], r->offs.as<uint32_t>(), ctl, n, cap, r->mean2d.as<float2>(), conic_words,
+                              r->color.as<uint4>(), r->erec.as<uint4>(), cam.grid_w, r->ikeys[0].as<uint32_t>(),
+                              r->ivals[0].as<uint32_t>(), r->first_slot.as<uint32_t>(), f16, s);
     }
     uint32_t* ik[2] = {r->ikeys[0].as<uint32_t>(), r->ikeys[1].as<uint32_t>()};
     uint32_t* iv[2] = {r->ivals[0].as<uint32_t>(), r->ivals[1].as<uint32_t>()};
@@ -756,7 +755,7 @@ int tgs_rasterizer_debug_view(tgs_rasterizer* r, tgs_debug_view* out) {
     if (!r->fwd_done) return fail(TGS_ERR_STATE, "no forward yet");
     TGS_TRY(sync_counts(r));
     out->n_touched = r->n_touched.as<uint32_t>();
-    out->bounds = r->rec.as<uint32_t>();
+    out->bounds = r->erec.as<uint32_t>();
     out->mean2d = r->mean2d.as<float>();
     out->conic_opacity = r->conic_opacity.as<float>();
     out->color = r->color.as<float>();

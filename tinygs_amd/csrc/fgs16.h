@@ -40,11 +40,4 @@ __device__ __forceinline__ bool will_contribute_half(float mx, float my, h16 cx,
     return max_power <= power_threshold;
 }
 
-// second 16 bytes of an FGS16 binning record: (conic a | b << 16, c | opacity << 16, 0, power threshold bits)
-__device__ __forceinline__ void unpack_conic16(const uint4& r1, h16& cx, h16& cy, h16& cz) {
-    cx = hfrom((uint16_t)(r1.x & 0xffffu));
-    cy = hfrom((uint16_t)(r1.x >> 16));
-    cz = hfrom((uint16_t)(r1.y & 0xffffu));
-}
-
 }  // namespace tgs

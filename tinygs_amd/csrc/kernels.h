@@ -34,13 +34,10 @@ struct GradView {
 };
 
 // ---- preprocess (kernels_forward.cuh:157-412)
-// rec: 2 x uint4 per visible primitive: {x_min | x_max << 16, y_min | y_max << 16, mean2d.x, mean2d.y},
-// {conic a, b, c, ln(255 opacity)} (float bits).
 // erec[i] (emission record, 16 B, the part the instance emission always reads):
 // {x_min | x_max << 16, y_min | y_max << 16, exact-test outcome of the rect
 // tiles 0..31 (bit k: row-major rect tile k), 0}.
 void launch_preprocess(const GaussianView& g, const CamParams& cam, uint32_t* n_touched, uint4* erec,
-                       uint4* rec,
                        float2* mean2d, float4* conic_opacity, float4* color_pt, uint32_t* depth_key,
                        float* densif, hipStream_t s);
 
@@ -109,12 +106,17 @@ int radix_sort(uint32_t* keys[2], uint32_t* vals[2], uint32_t* v2[2], const uint
                const uint32_t* first_block_n, hipStream_t s);
 // Instances in depth order: thread per depth-sorted primitive k < ctl->V,
 // slots [offs[k], offs[k + 1]).
+// Rect tiles past the first 32 take the exact tile test with mean2d[p], the
+// conic words x, y, z of conic_words[p] and the power threshold in the w of
+// thr_words[p] (conic_opacity and color_pt for fp32 images, info for both
+// with FGS16).
 // Also writes first_slot[p] = offs[k] for every visible primitive p = prims[k]:
 // the first of the n_touched[p] instance slots reserved for p. Slots at or
 // beyond max_inst (the instance buffers' size) are never written; offsets
 // that would need them set bit 1 of ctl->err.
 void launch_emit_instances(const uint32_t* prims, const uint32_t* offs, BinCtl* ctl, int64_t max_count,
-                           int64_t max_inst, const uint4* rec, const uint4* erec, uint32_t grid_w,
+                           int64_t max_inst, const float2* mean2d, const uint4* conic_words,
+                           const uint4* thr_words, const uint4* erec, uint32_t grid_w,
                            uint32_t* inst_keys, uint32_t* inst_vals, uint32_t* first_slot, bool half_test,
                            hipStream_t s);
 // [start, end) per tile, (0, 0) for empty tiles; every entry written. The
@@ -126,9 +128,10 @@ bool radix_digits_fit(bool depth, int n_passes, const int* bits);
 
 // ---- fp16-image rasterizer (FGS16, tinygs/src/rasterizer/fastgs_ours_fp16/)
 // Preprocess: as launch_preprocess with the FGS16 rules; info[i] = (conic a | b
-// << 16, c | opacity << 16 (halves), r | g << 8 | b << 16, 0).
+// << 16, c | opacity << 16 (halves), r | g << 8 | b << 16, power threshold
+// (float bits)).
 void launch_preprocess16(const GaussianView& g, const CamParams& cam, uint32_t* n_touched, uint4* erec,
-                         uint4* rec, float2* mean2d, float4* conic_opacity, uint4* info, uint32_t* depth_key,
+                         float2* mean2d, float4* conic_opacity, uint4* info, uint32_t* depth_key,
                          float* densif, hipStream_t s);
 
 // Blend of FGS16 (fgs16.hip): image / grad image are 3 half planes of the

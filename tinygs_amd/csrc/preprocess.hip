@@ -170,7 +170,7 @@ template <typename ShT>
 __global__ void __launch_bounds__(256) preprocess_kernel(
     const float* __restrict__ means, const float* __restrict__ scales, const float* __restrict__ rots,
     const float* __restrict__ opac, const ShT* __restrict__ sh0, const ShT* __restrict__ shr, int64_t n, int bases,
-    CamParams cam, uint32_t* __restrict__ n_touched, uint4* __restrict__ erec, uint4* __restrict__ rec,
+    CamParams cam, uint32_t* __restrict__ n_touched, uint4* __restrict__ erec,
     float2* __restrict__ mean2d, float4* __restrict__ conic_opacity, float4* __restrict__ color_pt, uint32_t* __restrict__ depth_key,
     float4* __restrict__ densif) {
     __shared__ __align__(16) ShT s_sh[256 * 45];
@@ -297,9 +297,6 @@ __global__ void __launch_bounds__(256) preprocess_kernel(
     }
     n_touched[i] = cnt;
     erec[i] = make_uint4(xmin | (xmax << 16), ymin | (ymax << 16), bits, 0u);
-    // 32-byte binning record, gathered once per primitive by the emission
-    rec[2 * i] = make_uint4(xmin | (xmax << 16), ymin | (ymax << 16), f2u(m2x), f2u(m2y));
-    rec[2 * i + 1] = make_uint4(f2u(ca), f2u(cb), f2u(cc), f2u(pthr));
     mean2d[i] = make_float2(m2x, m2y);
     conic_opacity[i] = make_float4(ca, cb, cc, opacity);
     float col[3];
@@ -314,15 +311,15 @@ __global__ void __launch_bounds__(256) preprocess_kernel(
 // still in [near, far]), the quaternion read only for active primitives, a
 // half conic and opacity, the power threshold from the half opacity, the
 // half tile test (fgs16.h) and an 8-bit colour, saturate(c) * 255 truncated
-// (rasterization_config.h:104-108). Outputs: n_touched, the emission record and the
-// binning record as the fp32 preprocess (conic and opacity halves in the
-// record's second half), mean2d, conic_opacity (the halves as floats) and
-// info[i] = (a | b << 16, c | opacity << 16, r | g << 8 | b << 16, 0).
+// (rasterization_config.h:104-108). Outputs: n_touched, the emission record
+// as the fp32 preprocess, mean2d, conic_opacity (the halves as floats) and
+// info[i] = (a | b << 16, c | opacity << 16, r | g << 8 | b << 16, power
+// threshold bits), which the instance emission's exact test also reads.
 template <typename ShT>
 __global__ void __launch_bounds__(256) preprocess16_kernel(
     const float* __restrict__ means, const float* __restrict__ scales, const float* __restrict__ rots,
     const float* __restrict__ opac, const ShT* __restrict__ sh0, const ShT* __restrict__ shr, int64_t n, int bases,
-    CamParams cam, uint32_t* __restrict__ n_touched, uint4* __restrict__ erec, uint4* __restrict__ rec,
+    CamParams cam, uint32_t* __restrict__ n_touched, uint4* __restrict__ erec,
     float2* __restrict__ mean2d, float4* __restrict__ conic_opacity, uint4* __restrict__ info,
     uint32_t* __restrict__ depth_key, float4* __restrict__ densif) {
     __shared__ __align__(16) ShT s_sh[256 * 45];
@@ -456,20 +453,18 @@ __global__ void __launch_bounds__(256) preprocess16_kernel(
     erec[i] = make_uint4(xmin | (xmax << 16), ymin | (ymax << 16), bits, 0u);
     const uint32_t c01 = (uint32_t)hbits(hca) | ((uint32_t)hbits(hcb) << 16);
     const uint32_t c2o = (uint32_t)hbits(hcc) | ((uint32_t)hbits(opacity) << 16);
-    rec[2 * i] = make_uint4(xmin | (xmax << 16), ymin | (ymax << 16), f2u(m2x), f2u(m2y));
-    rec[2 * i + 1] = make_uint4(c01, c2o, 0u, f2u(pthr));
     mean2d[i] = make_float2(m2x, m2y);
     conic_opacity[i] = make_float4((float)hca, (float)hcb, (float)hcc, (float)opacity);
     float col[3];
     sh_to_color(sh0, s_sh + 45 * threadIdx.x, i, mx, my, mz, cam, bases, col);
     uint32_t rgb = 0;
     for (int c = 0; c < 3; ++c) rgb |= (uint32_t)(uint8_t)(saturate(col[c]) * 255.0f) << (8 * c);
-    info[i] = make_uint4(c01, c2o, rgb, 0u);
+    info[i] = make_uint4(c01, c2o, rgb, f2u(pthr));
     depth_key[i] = f2u(depth);
 }
 
 void launch_preprocess16(const GaussianView& g, const CamParams& cam, uint32_t* n_touched, uint4* erec,
-                         uint4* rec, float2* mean2d, float4* conic_opacity, uint4* info, uint32_t* depth_key,
+                         float2* mean2d, float4* conic_opacity, uint4* info, uint32_t* depth_key,
                          float* densif, hipStream_t s) {
     if (g.n <= 0) return;
     const int bases = (g.sh_degree + 1) * (g.sh_degree + 1);
@@ -477,17 +472,17 @@ void launch_preprocess16(const GaussianView& g, const CamParams& cam, uint32_t* 
     if (g.sh_dtype == kShF16)
         preprocess16_kernel<__half><<<grid, 256, 0, s>>>(g.means, g.scales, g.rotations, g.opacities,
                                                          (const __half*)g.sh0, (const __half*)g.sh_rest, g.n, bases,
-                                                         cam, n_touched, erec, rec, mean2d, conic_opacity, info,
+                                                         cam, n_touched, erec, mean2d, conic_opacity, info,
                                                          depth_key, (float4*)densif);
     else
         preprocess16_kernel<float><<<grid, 256, 0, s>>>(g.means, g.scales, g.rotations, g.opacities,
                                                         (const float*)g.sh0, (const float*)g.sh_rest, g.n, bases, cam,
-                                                        n_touched, erec, rec, mean2d, conic_opacity, info,
+                                                        n_touched, erec, mean2d, conic_opacity, info,
                                                         depth_key, (float4*)densif);
 }
 
 void launch_preprocess(const GaussianView& g, const CamParams& cam, uint32_t* n_touched, uint4* erec,
-                       uint4* rec, float2* mean2d, float4* conic_opacity, float4* color_pt, uint32_t* depth_key, float* densif,
+                       float2* mean2d, float4* conic_opacity, float4* color_pt, uint32_t* depth_key, float* densif,
                        hipStream_t s) {
     if (g.n <= 0) return;
     const int bases = (g.sh_degree + 1) * (g.sh_degree + 1);
@@ -495,12 +490,12 @@ void launch_preprocess(const GaussianView& g, const CamParams& cam, uint32_t* n_
     if (g.sh_dtype == kShF16) {
         preprocess_kernel<__half><<<grid, 256, 0, s>>>(g.means, g.scales, g.rotations, g.opacities,
                                                        (const __half*)g.sh0, (const __half*)g.sh_rest, g.n, bases,
-                                                       cam, n_touched, erec, rec, mean2d, conic_opacity,
+                                                       cam, n_touched, erec, mean2d, conic_opacity,
                                                        color_pt, depth_key, (float4*)densif);
     } else {
         preprocess_kernel<float><<<grid, 256, 0, s>>>(g.means, g.scales, g.rotations, g.opacities,
                                                       (const float*)g.sh0, (const float*)g.sh_rest, g.n, bases, cam,
-                                                      n_touched, erec, rec, mean2d, conic_opacity, color_pt,
+                                                      n_touched, erec, mean2d, conic_opacity, color_pt,
                                                       depth_key,
                                                       (float4*)densif);
     }

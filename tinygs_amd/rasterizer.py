@@ -163,7 +163,7 @@ class FastGSRasterizer(RasterizerBase):
 
         out = {
             "n_touched": grab(dv.n_touched, n, torch.int32),
-            "bounds": grab(dv.bounds, 8 * n, torch.int32).view(-1, 8)[:, :2].reshape(-1),
+            "bounds": grab(dv.bounds, 4 * n, torch.int32).view(-1, 4)[:, :2].reshape(-1),
             "mean2d": grab(dv.mean2d, 2 * n, torch.float32),
             "conic_opacity": grab(dv.conic_opacity, 4 * n, torch.float32),
             "color": grab(dv.color, 4 * n, torch.float32),
