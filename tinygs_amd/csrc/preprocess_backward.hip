@@ -401,7 +401,20 @@ __global__ void __launch_bounds__(256) gather_heavy_kernel(const uint4* __restri
         if constexpr (kHalf) {
             HalfSums hs;
             hs_zero(hs);
-            for (uint32_t r = sub; r < e.y; r += 16u) {
+            uint32_t r = sub;
+            for (; r + 48u < e.y; r += 64u) {   // four strides' loads issued together (exact sums: any order)
+                float4 a[4], b[4], d[4];
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    const float4* src = records + 3 * (size_t)(e.z + r + 16u * (uint32_t)u);
+                    a[u] = src[0];
+                    b[u] = src[1];
+                    d[u] = src[2];
+                }
+#pragma unroll
+                for (int u = 0; u < 4; ++u) hs_add(hs, a[u], b[u], d[u]);
+            }
+            for (; r < e.y; r += 16u) {
                 const float4* src = records + 3 * (size_t)(e.z + r);
                 hs_add(hs, src[0], src[1], src[2]);
             }
@@ -425,7 +438,24 @@ __global__ void __launch_bounds__(256) gather_heavy_kernel(const uint4* __restri
         float v[12];
 #pragma unroll
         for (int q = 0; q < 12; ++q) v[q] = 0.f;
-        for (uint32_t r = sub; r < e.y; r += 16u) {
+        uint32_t r = sub;
+        for (; r + 48u < e.y; r += 64u) {   // four strides' loads issued together; the same order of adds
+            float4 a[4], b[4], d[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const float4* src = records + 3 * (size_t)(e.z + r + 16u * (uint32_t)u);
+                a[u] = src[0];
+                b[u] = src[1];
+                d[u] = src[2];
+            }
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                v[0] += a[u].x; v[1] += a[u].y; v[2] += a[u].z; v[3] += a[u].w;
+                v[4] += b[u].x; v[5] += b[u].y; v[6] += b[u].z; v[7] += b[u].w;
+                v[8] += d[u].x; v[9] += d[u].y; v[10] += d[u].z; v[11] += d[u].w;
+            }
+        }
+        for (; r < e.y; r += 16u) {
             const float4* src = records + 3 * (size_t)(e.z + r);
             const float4 a = src[0], b = src[1], d = src[2];
             v[0] += a.x; v[1] += a.y; v[2] += a.z; v[3] += a.w;
