@@ -709,20 +709,9 @@ __global__ void fill_u32_kernel(uint32_t* p, uint32_t v, int64_t n) {
     if (i < n) p[i] = v;
 }
 
-__global__ void bin_ctl_reset_kernel(uint32_t* p, uint32_t n_words, uint32_t keep, uint32_t epoch_word) {
-    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i == epoch_word)
-        p[i] = (p[i] + kEpochStride) & kEpochMask;
-    else if (i < n_words && i != keep)
-        p[i] = 0u;
-}
+__global__ void __launch_bounds__(256) bin_ctl_reset_kernel(BinCtl* ctl) { bin_ctl_reset_block(ctl); }
 
-void launch_bin_ctl_reset(BinCtl* ctl, hipStream_t s) {
-    constexpr uint32_t words = sizeof(BinCtl) / 4;
-    bin_ctl_reset_kernel<<<(words + 255) / 256, 256, 0, s>>>((uint32_t*)ctl, words,
-                                                             (uint32_t)(offsetof(BinCtl, err) / 4),
-                                                             (uint32_t)(offsetof(BinCtl, epoch_base) / 4));
-}
+void launch_bin_ctl_reset(BinCtl* ctl, hipStream_t s) { bin_ctl_reset_kernel<<<1, 256, 0, s>>>(ctl); }
 
 void launch_fill_u32(uint32_t* p, uint32_t value, int64_t n, hipStream_t s) {
     if (n <= 0) return;

@@ -473,17 +473,18 @@ static int rasterizer_forward(tgs_rasterizer* r, const tgs_camera* camera, void*
     uint64_t* status = r->lb_status.as<uint64_t>();
     // the same launch sequence, epochs included, every forward: what a graph replays
     r->epoch = 0;
-    launch_bin_ctl_reset(ctl, s);
     {
+        // (the preprocess's first workgroup resets ctl, advancing the look-back epoch base)
         StageScope sc(ST_PRE, s);
         if (f16)
             launch_preprocess16(gv, cam, r->n_touched.as<uint32_t>(), r->erec.as<uint4>(),
                                 r->mean2d.as<float2>(), r->conic_opacity.as<float4>(),
-                                r->color.as<uint4>(), r->depth_key.as<uint32_t>(), (float*)densification_info, s);
+                                r->color.as<uint4>(), r->depth_key.as<uint32_t>(), (float*)densification_info, ctl,
+                                s);
         else
             launch_preprocess(gv, cam, r->n_touched.as<uint32_t>(), r->erec.as<uint4>(), r->mean2d.as<float2>(),
                               r->conic_opacity.as<float4>(), r->color.as<float4>(), r->depth_key.as<uint32_t>(),
-                              (float*)densification_info, s);
+                              (float*)densification_info, ctl, s);
     }
     TGS_CHECK_LAUNCH();
     uint32_t* pk[2] = {r->pkeys[0].as<uint32_t>(), r->pkeys[1].as<uint32_t>()};

@@ -36,10 +36,12 @@ struct GradView {
 // ---- preprocess (kernels_forward.cuh:157-412)
 // erec[i] (emission record, 16 B, the part the instance emission always reads):
 // {x_min | x_max << 16, y_min | y_max << 16, exact-test outcome of the rect
-// tiles 0..31 (bit k: row-major rect tile k), 0}.
+// tiles 0..31 (bit k: row-major rect tile k), 0}. ctl (may be null): the
+// binning control block, reset by the first workgroup (bin_ctl_reset_block).
+struct BinCtl;
 void launch_preprocess(const GaussianView& g, const CamParams& cam, uint32_t* n_touched, uint4* erec,
                        float2* mean2d, float4* conic_opacity, float4* color_pt, uint32_t* depth_key,
-                       float* densif, hipStream_t s);
+                       float* densif, BinCtl* ctl, hipStream_t s);
 
 // ---- scans / compaction / sort / binning
 // Device control block of the binning launches. Everything but `err` is
@@ -70,10 +72,24 @@ void launch_capacity_check(BinCtl* ctl, int64_t cap, hipStream_t s);
 void launch_clear_err_bits(BinCtl* ctl, uint32_t bits, hipStream_t s);
 // Words of bwd_queue: what a backward needs cleared.
 constexpr int kBwdCtlWords = kBwdQueues * 32;
-// Clears every BinCtl word except err and advances epoch_base.
+// Clears every BinCtl word except err and advances epoch_base (the
+// forward's reset; the preprocess does it in its first workgroup, this
+// launch only when there is no primitive to preprocess).
 void launch_bin_ctl_reset(BinCtl* ctl, hipStream_t s);
 constexpr uint32_t kEpochMask = 0x3fffffffu;   // 30-bit launch epoch of look-back status words
 constexpr uint32_t kEpochStride = 64u;          // look-back launches per forward, at most
+// The reset by the threads of one workgroup.
+__device__ __forceinline__ void bin_ctl_reset_block(BinCtl* ctl) {
+    uint32_t* p = (uint32_t*)ctl;
+    constexpr uint32_t words = sizeof(BinCtl) / 4;
+    constexpr uint32_t keep = offsetof(BinCtl, err) / 4, ep = offsetof(BinCtl, epoch_base) / 4;
+    for (uint32_t i = threadIdx.x; i < words; i += blockDim.x) {
+        if (i == ep)
+            p[i] = (p[i] + kEpochStride) & kEpochMask;
+        else if (i != keep)
+            p[i] = 0u;
+    }
+}
 
 // Status-word entries (u64) needed by a look-back scan over max_n elements.
 int64_t scan_status_entries(int64_t max_n);
@@ -132,7 +148,7 @@ bool radix_digits_fit(bool depth, int n_passes, const int* bits);
 // (float bits)).
 void launch_preprocess16(const GaussianView& g, const CamParams& cam, uint32_t* n_touched, uint4* erec,
                          float2* mean2d, float4* conic_opacity, uint4* info, uint32_t* depth_key,
-                         float* densif, hipStream_t s);
+                         float* densif, BinCtl* ctl, hipStream_t s);
 
 // Blend of FGS16 (fgs16.hip): image / grad image are 3 half planes of the
 // padded 8x8-tiled layout, n_contrib u16 per pixel, ckpt 256 uint2 per slot

@@ -172,9 +172,10 @@ __global__ void __launch_bounds__(256) preprocess_kernel(
     const float* __restrict__ opac, const ShT* __restrict__ sh0, const ShT* __restrict__ shr, int64_t n, int bases,
     CamParams cam, uint32_t* __restrict__ n_touched, uint4* __restrict__ erec,
     float2* __restrict__ mean2d, float4* __restrict__ conic_opacity, float4* __restrict__ color_pt, uint32_t* __restrict__ depth_key,
-    float4* __restrict__ densif) {
+    float4* __restrict__ densif, BinCtl* __restrict__ ctl) {
     __shared__ __align__(16) ShT s_sh[256 * 45];
     __shared__ uint32_t s_rect[4][kRectSlice];
+    if (ctl != nullptr && blockIdx.x == 0) bin_ctl_reset_block(ctl);   // (read first by the compaction)
     ShStage<ShT> shs;
     sh_stage_load(shs, shr, n, bases);
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -321,9 +322,10 @@ __global__ void __launch_bounds__(256) preprocess16_kernel(
     const float* __restrict__ opac, const ShT* __restrict__ sh0, const ShT* __restrict__ shr, int64_t n, int bases,
     CamParams cam, uint32_t* __restrict__ n_touched, uint4* __restrict__ erec,
     float2* __restrict__ mean2d, float4* __restrict__ conic_opacity, uint4* __restrict__ info,
-    uint32_t* __restrict__ depth_key, float4* __restrict__ densif) {
+    uint32_t* __restrict__ depth_key, float4* __restrict__ densif, BinCtl* __restrict__ ctl) {
     __shared__ __align__(16) ShT s_sh[256 * 45];
     __shared__ uint32_t s_rect[4][kRectSlice];
+    if (ctl != nullptr && blockIdx.x == 0) bin_ctl_reset_block(ctl);   // (read first by the compaction)
     ShStage<ShT> shs;
     sh_stage_load(shs, shr, n, bases);
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -465,39 +467,44 @@ __global__ void __launch_bounds__(256) preprocess16_kernel(
 
 void launch_preprocess16(const GaussianView& g, const CamParams& cam, uint32_t* n_touched, uint4* erec,
                          float2* mean2d, float4* conic_opacity, uint4* info, uint32_t* depth_key,
-                         float* densif, hipStream_t s) {
-    if (g.n <= 0) return;
+                         float* densif, BinCtl* ctl, hipStream_t s) {
+    if (g.n <= 0) {
+        if (ctl) launch_bin_ctl_reset(ctl, s);
+        return;
+    }
     const int bases = (g.sh_degree + 1) * (g.sh_degree + 1);
     const unsigned grid = (unsigned)((g.n + 255) / 256);
     if (g.sh_dtype == kShF16)
         preprocess16_kernel<__half><<<grid, 256, 0, s>>>(g.means, g.scales, g.rotations, g.opacities,
                                                          (const __half*)g.sh0, (const __half*)g.sh_rest, g.n, bases,
                                                          cam, n_touched, erec, mean2d, conic_opacity, info,
-                                                         depth_key, (float4*)densif);
+                                                         depth_key, (float4*)densif, ctl);
     else
         preprocess16_kernel<float><<<grid, 256, 0, s>>>(g.means, g.scales, g.rotations, g.opacities,
                                                         (const float*)g.sh0, (const float*)g.sh_rest, g.n, bases, cam,
                                                         n_touched, erec, mean2d, conic_opacity, info,
-                                                        depth_key, (float4*)densif);
+                                                        depth_key, (float4*)densif, ctl);
 }
 
 void launch_preprocess(const GaussianView& g, const CamParams& cam, uint32_t* n_touched, uint4* erec,
                        float2* mean2d, float4* conic_opacity, float4* color_pt, uint32_t* depth_key, float* densif,
-                       hipStream_t s) {
-    if (g.n <= 0) return;
+                       BinCtl* ctl, hipStream_t s) {
+    if (g.n <= 0) {
+        if (ctl) launch_bin_ctl_reset(ctl, s);
+        return;
+    }
     const int bases = (g.sh_degree + 1) * (g.sh_degree + 1);
     const unsigned grid = (unsigned)((g.n + 255) / 256);
     if (g.sh_dtype == kShF16) {
         preprocess_kernel<__half><<<grid, 256, 0, s>>>(g.means, g.scales, g.rotations, g.opacities,
                                                        (const __half*)g.sh0, (const __half*)g.sh_rest, g.n, bases,
                                                        cam, n_touched, erec, mean2d, conic_opacity,
-                                                       color_pt, depth_key, (float4*)densif);
+                                                       color_pt, depth_key, (float4*)densif, ctl);
     } else {
         preprocess_kernel<float><<<grid, 256, 0, s>>>(g.means, g.scales, g.rotations, g.opacities,
                                                       (const float*)g.sh0, (const float*)g.sh_rest, g.n, bases, cam,
                                                       n_touched, erec, mean2d, conic_opacity, color_pt,
-                                                      depth_key,
-                                                      (float4*)densif);
+                                                      depth_key, (float4*)densif, ctl);
     }
 }
 
