@@ -149,7 +149,9 @@ __global__ void __launch_bounds__(256) blend_backward_kernel(
         stops = wave_or_u32(stops);
         wave_lds_sync();
 
-        for (int32_t k = 0; k < kmax; ++k) {
+        // Gaussian k of the bucket: updates the pixels' state and leaves the
+        // wave's per-lane sums in acc[0..8] (and the |dL/dmean2d| sums in 9, 10)
+        auto gaussian = [&](int32_t k, float* acc) {
             const float4 r0 = s_rec[w][0][k];   // mx, my, a/2 L, b L
             const float4 r1 = s_rec[w][1][k];   // c/2 L, opacity, a, c
             const float4 r2 = s_rec[w][2][k];   // clamped colour, b
@@ -165,7 +167,6 @@ __global__ void __launch_bounds__(256) blend_backward_kernel(
             const float X[2] = {r0.x - pcx0, r0.x - pcx1}, Y[2] = {r0.y - pcy0, r0.y - pcy1};
             const float AX[2] = {r0.z * X[0], r0.z * X[1]};
             const float CYY[2] = {(r1.x * Y[0]) * Y[0], (r1.x * Y[1]) * Y[1]};
-            float acc[12];
             acc[11] = 0.f;
             if constexpr (!ABS) acc[9] = acc[10] = 0.f;
             float pp[4];
@@ -207,16 +208,47 @@ __global__ void __launch_bounds__(256) blend_backward_kernel(
                 acc[7] = __builtin_fmaf(X[0], C0, X[1] * C1);
                 acc[8] = __builtin_fmaf(Y[0], R0, Y[1] * R1);
             }
+        };
+        auto store = [&](int32_t k, const float* t, int nt) {
+            if ((lane & 15u) == 0u)
+                for (int m = 0; m < nt; ++m)
+                    if (4 * m + q0 < kBwdVals) s_part[w][4 * m + q0][k] = t[m];
+        };
+        int32_t k = 0;
+        if constexpr (!ABS) {
+            // two Gaussians per reduction (values 9 and 10 stay the zeros written below)
+            for (; k + 1 < kmax; k += 2) {
+                float acc2[18], acc1[12];
+                gaussian(k, acc1);
+#pragma unroll
+                for (int q = 0; q < 9; ++q) acc2[q] = acc1[q];
+                gaussian(k + 1, acc1);
+#pragma unroll
+                for (int q = 0; q < 9; ++q) acc2[9 + q] = acc1[q];
+                float t[5];
+                wave_reduce18(acc2, t);
+                if ((lane & 15u) == 0u) {
+#pragma unroll
+                    for (int m = 0; m < 5; ++m) {
+                        const int i = 4 * m + q0;   // value i % 9 of Gaussian k + i / 9
+                        if (i < 18) s_part[w][i % 9][k + i / 9] = t[m];
+                    }
+                    if (q0 == 0) {
+                        s_part[w][9][k] = s_part[w][10][k] = 0.f;
+                        s_part[w][9][k + 1] = s_part[w][10][k + 1] = 0.f;
+                    }
+                }
+            }
+        }
+        for (; k < kmax; ++k) {
+            float acc[12];
+            gaussian(k, acc);
             float t[3];
             if constexpr (ABS)
                 wave_reduce12(acc, t);
             else
                 wave_reduce9(acc, t);   // values 9-11 are zero: their swaps are skipped
-            if ((lane & 15u) == 0u) {
-                s_part[w][q0][k] = t[0];
-                s_part[w][4 + q0][k] = t[1];
-                if (8 + q0 < kBwdVals) s_part[w][8 + q0][k] = t[2];
-            }
+            store(k, t, 3);
         }
         wave_lds_sync();
 
