@@ -171,16 +171,21 @@ __device__ __forceinline__ void ssim_tile_of(uint32_t& tx, uint32_t& ty, uint32_
 // image, like the reference's L1 over all padded elements. One workgroup per
 // (32x32 tile, channel): no state is carried across channels, which keeps
 // the register footprint small enough for four workgroups per CU.
-template <typename T>
+template <typename T, bool ASSIGN>
 __global__ void __launch_bounds__(256) l1_ssim_forward_kernel(uint32_t W, uint32_t H, float C1, float C2,
-                                                              float s_ssim, float s_l1, int assign,
+                                                              float s_ssim, float s_l1,
                                                               const T* __restrict__ pred,
                                                               const T* __restrict__ target,
                                                               T* __restrict__ loss, T* __restrict__ grad,
                                                               float* __restrict__ dm_mu, float* __restrict__ dm_s1,
                                                               float* __restrict__ dm_s12) {
-    __shared__ __half2 s_in[kHT][kHT];         // fp16-rounded (pred, target), exactly the values the sums use
-    __shared__ float s_h[4][kIT][kOT + 1];     // horizontal sums: x, x^2 + y^2, y, xy
+    // s_in: the fp16-rounded (pred, target) halo, exactly the values the sums
+    // use; s_h: the horizontal sums x, x^2 + y^2, y, xy, overlaying s_in once
+    // every thread holds its sums in registers (22 KB of LDS instead of 31 KB)
+    __shared__ float s_buf[4 * kIT * (kOT + 1)];
+    static_assert(kHT * kHT <= 4 * kIT * (kOT + 1), "s_in fits inside s_h");
+    auto s_in = reinterpret_cast<__half2 (*)[kHT]>(s_buf);
+    auto s_h = reinterpret_cast<float (*)[kIT][kOT + 1]>(s_buf);
     const int t = (int)threadIdx.x;
     uint32_t tx, ty, ch;
     ssim_tile_of(tx, ty, ch);
@@ -210,8 +215,13 @@ __global__ void __launch_bounds__(256) l1_ssim_forward_kernel(uint32_t W, uint32
         }
     }
     __syncthreads();
-    // horizontal: row r, output columns 4 g .. 4 g + 3
-    for (int wi = t; wi < kIT * 8; wi += 256) {
+    // horizontal: row r, output columns 4 g .. 4 g + 3; items t and t + 256
+    static_assert(kIT * 8 <= 2 * 256, "two horizontal items per thread");
+    float hs[2][4][4];
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+        const int wi = t + 256 * k;
+        if (wi >= kIT * 8) break;
         const int r = wi >> 3, g = wi & 7;
         float x[14], y[14], q[14], xy[14];
 #pragma unroll
@@ -233,11 +243,22 @@ __global__ void __launch_bounds__(256) l1_ssim_forward_kernel(uint32_t W, uint32
                 sy = __builtin_fmaf(y[o + d], wv, sy);
                 sxy = __builtin_fmaf(xy[o + d], wv, sxy);
             }
-            s_h[0][r][4 * g + o] = sx;
-            s_h[1][r][4 * g + o] = sq;
-            s_h[2][r][4 * g + o] = sy;
-            s_h[3][r][4 * g + o] = sxy;
+            hs[k][0][o] = sx;
+            hs[k][1][o] = sq;
+            hs[k][2][o] = sy;
+            hs[k][3][o] = sxy;
         }
+    }
+    __syncthreads();   // every s_in read done before s_h overwrites it
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+        const int wi = t + 256 * k;
+        if (wi >= kIT * 8) break;
+        const int r = wi >> 3, g = wi & 7;
+#pragma unroll
+        for (int v = 0; v < 4; ++v)
+#pragma unroll
+            for (int o = 0; o < 4; ++o) s_h[v][r][4 * g + o] = hs[k][v][o];
     }
     __syncthreads();
     // vertical: column vc, output rows 4 vr .. 4 vr + 3
@@ -246,7 +267,7 @@ __global__ void __launch_bounds__(256) l1_ssim_forward_kernel(uint32_t W, uint32
     if (grad) grad += co;
     // the epilogue's own pixels (L1 terms, accumulated values) are loaded
     // before the vertical pass, so their latency hides behind it
-    const bool acc_l = !assign && loss, acc_g = !assign && grad, l1 = s_l1 != 0.f;
+    const bool acc_l = !ASSIGN && loss, acc_g = !ASSIGN && grad, l1 = s_l1 != 0.f;
     uint32_t pidx[4];
     float pp[4], pt[4], pl[4], pg[4];
 #pragma unroll
@@ -310,7 +331,7 @@ __global__ void __launch_bounds__(256) l1_ssim_forward_kernel(uint32_t W, uint32
             }
         }
         if (loss) st(loss, idx, lv);
-        if (grad && (assign || s_l1 != 0.f)) st(grad, idx, gv);
+        if (grad && (ASSIGN || s_l1 != 0.f)) st(grad, idx, gv);
     }
 }
 
@@ -446,8 +467,12 @@ void launch_l1_ssim_forward(uint32_t width, uint32_t height, float c1, float c2,
                             float* dm_mu, float* dm_s1, float* dm_s12, hipStream_t st) {
     if (width == 0 || height == 0) return;
     dim3 grid((width + kOT - 1) / kOT, (height + kOT - 1) / kOT, 3);
-    l1_ssim_forward_kernel<float><<<grid, 256, 0, st>>>(width, height, c1, c2, s_ssim, s_l1, assign ? 1 : 0, pred,
-                                                        target, loss, grad, dm_mu, dm_s1, dm_s12);
+    if (assign)
+        l1_ssim_forward_kernel<float, true><<<grid, 256, 0, st>>>(width, height, c1, c2, s_ssim, s_l1, pred, target,
+                                                                  loss, grad, dm_mu, dm_s1, dm_s12);
+    else
+        l1_ssim_forward_kernel<float, false><<<grid, 256, 0, st>>>(width, height, c1, c2, s_ssim, s_l1, pred, target,
+                                                                   loss, grad, dm_mu, dm_s1, dm_s12);
 }
 
 void launch_l1_ssim_forward_f16(uint32_t width, uint32_t height, float c1, float c2, float s_ssim, float s_l1,
@@ -455,9 +480,14 @@ void launch_l1_ssim_forward_f16(uint32_t width, uint32_t height, float c1, float
                                 float* dm_mu, float* dm_s1, float* dm_s12, hipStream_t st) {
     if (width == 0 || height == 0) return;
     dim3 grid((width + kOT - 1) / kOT, (height + kOT - 1) / kOT, 3);
-    l1_ssim_forward_kernel<__half><<<grid, 256, 0, st>>>(width, height, c1, c2, s_ssim, s_l1, assign ? 1 : 0,
-                                                         (const __half*)pred, (const __half*)target, (__half*)loss,
-                                                         (__half*)grad, dm_mu, dm_s1, dm_s12);
+    if (assign)
+        l1_ssim_forward_kernel<__half, true><<<grid, 256, 0, st>>>(width, height, c1, c2, s_ssim, s_l1,
+                                                                   (const __half*)pred, (const __half*)target,
+                                                                   (__half*)loss, (__half*)grad, dm_mu, dm_s1, dm_s12);
+    else
+        l1_ssim_forward_kernel<__half, false><<<grid, 256, 0, st>>>(width, height, c1, c2, s_ssim, s_l1,
+                                                                    (const __half*)pred, (const __half*)target,
+                                                                    (__half*)loss, (__half*)grad, dm_mu, dm_s1, dm_s12);
 }
 
 void launch_ssim_backward(uint32_t width, uint32_t height, float s, const float* pred, const float* target,
