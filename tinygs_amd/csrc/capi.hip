@@ -219,7 +219,7 @@ struct tgs_rasterizer {
     // count (kept zero between backwards), records (3 float4 per instance
     // slot), heavy-gather list
     DevBuf first_slot, rec_count, records;
-    DevBuf live, heavy, chunk_counts;   // preprocess backward: per-chunk lists of primitives with records
+    DevBuf live, heavy;   // preprocess backward: per-chunk lists of primitives with records
     DevBuf row_mask;     // per-primitive byte mask of the last sparse backward
     bool row_mask_valid = false;
     DevBuf bwd_rows;     // rows the backward of the last forward writes (tgs_rasterizer_backward_rows)
@@ -336,7 +336,7 @@ int tgs_rasterizer_destroy(tgs_rasterizer* r) {
                      &r->radix_counts, &r->block_n, &r->ikeys[0],
                      &r->ikeys[1], &r->ivals[0], &r->ivals[1], &r->ranges, &r->tile_max, &r->n_contrib,
                      &r->ckpt, &r->items, &r->tile_loaded, &r->first_slot,
-                     &r->rec_count, &r->records, &r->heavy, &r->live, &r->chunk_counts, &r->row_mask, &r->grad2d,
+                     &r->rec_count, &r->records, &r->heavy, &r->live, &r->row_mask, &r->grad2d,
                      &r->bwd_rows, &r->pose_partial, &r->pose_grad, &r->bin_ctl, &r->lb_status};
     for (DevBuf* b : all) release(*b);
     if (r->h_counters) (void)hipHostFree(r->h_counters);
@@ -640,7 +640,6 @@ int tgs_rasterizer_backward_ex(tgs_rasterizer* r, const void* grad_image, const 
     TGS_TRY(ensure(r->grad2d, sizeof(float) * kGradStride * (size_t)(n > 0 ? n : 1), s));
     TGS_TRY(ensure(r->heavy, sizeof(uint4) * (size_t)(n > 0 ? n : 1), s));
     TGS_TRY(ensure(r->live, sizeof(uint4) * (size_t)(n > 0 ? n : 1), s));
-    TGS_TRY(ensure(r->chunk_counts, sizeof(uint2) * (size_t)std::max<int64_t>(pb_chunks(n), 1), s));
     if (flags & ~(TGS_BACKWARD_ASSIGN | TGS_BACKWARD_SPARSE | TGS_BACKWARD_POSE | TGS_BACKWARD_KEEP_2D))
         return fail(TGS_ERR_INVALID, "unknown backward flags 0x%x", flags);
     if ((flags & TGS_BACKWARD_ASSIGN) && (flags & TGS_BACKWARD_SPARSE))
@@ -684,7 +683,7 @@ int tgs_rasterizer_backward_ex(tgs_rasterizer* r, const void* grad_image, const 
                                    r->rec_count.as<uint32_t>(), r->first_slot.as<uint32_t>(), r->records.as<float4>(),
                                    r->grad2d.as<float>(), gv, (float*)densification_info, mode,
                                    r->row_mask.as<uint8_t>(), r->live.as<uint4>(), r->heavy.as<uint4>(),
-                                   r->chunk_counts.as<uint2>(), pose ? r->pose_partial.as<float>() : nullptr,
+                                   pose ? r->pose_partial.as<float>() : nullptr,
                                    pose ? r->pose_grad.as<float>() : nullptr, keep2d, r->fgs16, s);
     }
     TGS_CHECK_LAUNCH();

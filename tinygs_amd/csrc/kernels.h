@@ -198,13 +198,13 @@ void launch_blend_backward(const CamParams& cam, const uint32_t* inst_vals, cons
 // row_mask[i] = 1 for them and 0 for the others, leave the others untouched).
 enum { kGradAccumulate = 0, kGradAssign = 1, kGradSparse = 2 };
 // Scratch: live and heavy (n uint4 each) lists of the primitives with
-// records, chunk_counts (pb_chunks(n) uint2), grad2d (12 n floats).
+// records, grad2d (12 n floats).
 int64_t pb_chunks(int64_t n);
 void launch_preprocess_backward(const GaussianView& g, const CamParams& cam, const uint32_t* n_touched,
                                 const float4* conic_opacity, uint32_t* rec_count, const uint32_t* first_slot,
                                 const float4* records, float* grad2d, const GradView& out, float* densif, int mode,
-                                uint8_t* row_mask, uint4* live, uint4* heavy, uint2* chunk_counts,
-                                float* pose_partial, float* pose_out, bool keep2d, bool half_sums, hipStream_t s);
+                                uint8_t* row_mask, uint4* live, uint4* heavy, float* pose_partial, float* pose_out,
+                                bool keep2d, bool half_sums, hipStream_t s);
 
 // ---- PSNR (psnr.cu:72-128): scratch[psnr_scratch_doubles() - 1] receives the
 // sum of (saturate(pred) - target)^2 over the n_padded elements

@@ -300,19 +300,21 @@ __device__ __forceinline__ void hs_result(const HalfSums& h, float4& gA, float4&
     gC = make_float4(hs_value(h, 8), hs_value(h, 9), (float)h.op, 0.f);
 }
 
+// One workgroup per chunk of 2048 consecutive primitives runs three phases
+// (one launch; the chunk's lists and heavy sums never leave the workgroup's
+// own slices, so the phases only need workgroup barriers).
+//
 // ---- phase 1: classify every primitive, list the live ones
 //
-// Chunk of 2048 consecutive primitives per workgroup (8 striped rounds of
-// 256). A primitive is live when some bucket of the blend backward left a
-// record for it (the counters of all others are zero). Dead visible
-// primitives only count for densification (kernels_backward.cuh:345 adds
-// zero sums); sparse mode records the row mask; assign mode zeroes every
-// gradient row of the chunk (the live rows are overwritten by phase 3).
-// The chunk's live primitives, as (index, record count, first record slot),
-// and its heavy ones (more than kLightRecords records) are listed in the
-// chunk's own slice of the two lists, with the two counts in chunk_counts:
-// no device-wide counter (returning atomics on one address serialise, about
-// 10 ns each on MI355X).
+// 8 striped rounds of 256. A primitive is live when some bucket of the blend
+// backward left a record for it (the counters of all others are zero). Dead
+// visible primitives only count for densification (kernels_backward.cuh:345
+// adds zero sums); sparse mode records the row mask; assign mode zeroes
+// every gradient row of the chunk (the live rows are overwritten by phase
+// 3). The chunk's live primitives, as (index, record count, first record
+// slot), and its heavy ones (more than kLightRecords records) are listed in
+// the chunk's own slice of the two lists: no device-wide counter (returning
+// atomics on one address serialise, about 10 ns each on MI355X).
 constexpr int kClassRounds = 8;
 constexpr int kClassChunk = 256 * kClassRounds;
 
@@ -326,11 +328,12 @@ __device__ __forceinline__ void zero_run(float* __restrict__ dst, int64_t n) {
     for (int64_t e = (nv << 2) + threadIdx.x; e < n; e += 256) dst[e] = 0.f;
 }
 
-__global__ void __launch_bounds__(256) preprocess_backward_classify_kernel(
-    int64_t n, const uint32_t* __restrict__ n_touched, const uint32_t* __restrict__ rec_count,
-    const uint32_t* __restrict__ first_slot, float4* __restrict__ densif, int mode, uint8_t* __restrict__ row_mask,
-    GradView out, uint4* __restrict__ live, uint4* __restrict__ heavy, uint2* __restrict__ chunk_counts) {
-    __shared__ uint32_t s_rw[4 * kClassRounds];
+__device__ __forceinline__ void classify_chunk(int64_t n, const uint32_t* __restrict__ n_touched,
+                                               const uint32_t* __restrict__ rec_count,
+                                               const uint32_t* __restrict__ first_slot, float4* __restrict__ densif,
+                                               int mode, uint8_t* __restrict__ row_mask, const GradView& out,
+                                               uint4* __restrict__ live, uint4* __restrict__ heavy, uint32_t* s_rw,
+                                               uint32_t& n_live, uint32_t& n_heavy) {
     const uint32_t t = threadIdx.x;
     const int64_t c0 = (int64_t)blockIdx.x * kClassChunk;
     const int64_t base = c0 + t;
@@ -365,10 +368,8 @@ __global__ void __launch_bounds__(256) preprocess_backward_classify_kernel(
         zero_run(out.sh0 + 3 * c0, 3 * rows);
         zero_run(out.sh_rest + 45 * c0, 45 * rows);
     }
-    uint32_t n_live, n_heavy;
     striped_scan_u32<kClassRounds>(lv, ex, &n_live, s_rw);
     striped_scan_u32<kClassRounds>(hv, exh, &n_heavy, s_rw);
-    if (t == 0) chunk_counts[blockIdx.x] = make_uint2(n_live, n_heavy);
 #pragma unroll
     for (int r = 0; r < kClassRounds; ++r) {
         const uint32_t i = (uint32_t)(base + (int64_t)r * 256);
@@ -387,13 +388,9 @@ __global__ void __launch_bounds__(256) preprocess_backward_classify_kernel(
 // butterfly leaves the 12 sums in every lane of the row and lanes 0-2 of
 // the row store them to grad2d[12 p] in record layout.
 template <bool kHalf>
-__global__ void __launch_bounds__(256) gather_heavy_kernel(const uint4* __restrict__ heavy,
-                                                           const uint2* __restrict__ chunk_counts,
-                                                           const float4* __restrict__ records,
-                                                           float* __restrict__ grad2d) {
+__device__ __forceinline__ void gather_heavy_chunk(const uint4* __restrict__ list, uint32_t nh,
+                                                   const float4* __restrict__ records, float* __restrict__ grad2d) {
     const uint32_t row = threadIdx.x >> 4, sub = threadIdx.x & 15u;
-    const uint32_t nh = chunk_counts[blockIdx.x].y;
-    const uint4* list = heavy + (size_t)blockIdx.x * kClassChunk;
     for (uint32_t h0 = 0; h0 < nh; h0 += 16u) {
         const uint32_t h = h0 + row;
         const bool on = h < nh;
@@ -525,18 +522,28 @@ __device__ __forceinline__ void load_sh_row<__half>(const __half* __restrict__ s
 // sum of those 12 numbers goes to pose_partial[12 * chunk] (every workgroup
 // writes its slot, zero when it has no live primitive), in a fixed order.
 template <typename ShT, bool kPose, bool kHalf>
-__global__ void __launch_bounds__(256) preprocess_backward_live_kernel(
+__global__ void __launch_bounds__(256) preprocess_backward_chunk_kernel(
+    int64_t n, const uint32_t* __restrict__ n_touched, const uint32_t* __restrict__ first_slot,
+    uint8_t* __restrict__ row_mask, uint4* __restrict__ live, uint4* __restrict__ heavy,
     const float* __restrict__ means, const float* __restrict__ scales, const float* __restrict__ rots,
     const ShT* __restrict__ shr_all, int bases, CamParams cam, const float4* __restrict__ conic_opacity,
-    uint32_t* __restrict__ rec_count, const float4* __restrict__ records, const float* grad2d,
-    GradView out, float4* __restrict__ densif, int mode, const uint4* __restrict__ live,
-    const uint2* __restrict__ chunk_counts, float* __restrict__ pose_partial, float* keep2d) {
+    uint32_t* __restrict__ rec_count, const float4* __restrict__ records, float* grad2d,
+    GradView out, float4* __restrict__ densif, int mode, float* __restrict__ pose_partial, float* keep2d) {
+    __shared__ uint32_t s_rw[4 * kClassRounds];
+    __shared__ uint2 s_win[256 * kShWin];
+    const uint32_t t = threadIdx.x;
+    // phase 1: the chunk's lists; phase 2: its heavy primitives' sums into grad2d
+    uint32_t nl, nh;
+    classify_chunk(n, n_touched, rec_count, first_slot, densif, mode, row_mask, out, live, heavy, s_rw, nl, nh);
+    __syncthreads();   // the lists (global, this chunk's slices) seen by the whole workgroup
+    if (nh) {
+        gather_heavy_chunk<kHalf>(heavy + (size_t)blockIdx.x * kClassChunk, nh, records, grad2d);
+        __syncthreads();   // grad2d rows of the heavy primitives
+    }
+    // phase 3
     float pacc[12];
 #pragma unroll
     for (int q = 0; q < 12; ++q) pacc[q] = 0.f;
-    __shared__ uint2 s_win[256 * kShWin];
-    const uint32_t t = threadIdx.x;
-    const uint32_t nl = chunk_counts[blockIdx.x].x;
     const uint4* list = live + (size_t)blockIdx.x * kClassChunk;
     const bool store = mode != kGradAccumulate;
     const int nsh = 3 * (bases - 1);   // SH-rest coefficients of the active bases
@@ -690,25 +697,28 @@ __global__ void __launch_bounds__(256) pose_reduce_kernel(const float* __restric
 }
 
 template <typename ShT, bool kPose>
-static void launch_live(const GaussianView& g, int bases, const CamParams& cam, const float4* conic_opacity,
-                        uint32_t* rec_count, const float4* records, float* grad2d, const GradView& out,
-                        float* densif, int mode, const uint4* live, const uint2* chunk_counts, float* pose_partial,
-                        bool keep2d, bool half_sums, unsigned chunks, hipStream_t s) {
+static void launch_chunks(const GaussianView& g, int bases, const CamParams& cam, const uint32_t* n_touched,
+                          const uint32_t* first_slot, uint8_t* row_mask, uint4* live, uint4* heavy,
+                          const float4* conic_opacity, uint32_t* rec_count, const float4* records, float* grad2d,
+                          const GradView& out, float* densif, int mode, float* pose_partial, bool keep2d,
+                          bool half_sums, unsigned chunks, hipStream_t s) {
     if (half_sums)
-        preprocess_backward_live_kernel<ShT, kPose, true><<<chunks, 256, 0, s>>>(
-            g.means, g.scales, g.rotations, (const ShT*)g.sh_rest, bases, cam, conic_opacity, rec_count, records,
-            grad2d, out, (float4*)densif, mode, live, chunk_counts, pose_partial, keep2d ? grad2d : nullptr);
+        preprocess_backward_chunk_kernel<ShT, kPose, true><<<chunks, 256, 0, s>>>(
+            g.n, n_touched, first_slot, row_mask, live, heavy, g.means, g.scales, g.rotations,
+            (const ShT*)g.sh_rest, bases, cam, conic_opacity, rec_count, records, grad2d, out, (float4*)densif, mode,
+            pose_partial, keep2d ? grad2d : nullptr);
     else
-        preprocess_backward_live_kernel<ShT, kPose, false><<<chunks, 256, 0, s>>>(
-            g.means, g.scales, g.rotations, (const ShT*)g.sh_rest, bases, cam, conic_opacity, rec_count, records,
-            grad2d, out, (float4*)densif, mode, live, chunk_counts, pose_partial, keep2d ? grad2d : nullptr);
+        preprocess_backward_chunk_kernel<ShT, kPose, false><<<chunks, 256, 0, s>>>(
+            g.n, n_touched, first_slot, row_mask, live, heavy, g.means, g.scales, g.rotations,
+            (const ShT*)g.sh_rest, bases, cam, conic_opacity, rec_count, records, grad2d, out, (float4*)densif, mode,
+            pose_partial, keep2d ? grad2d : nullptr);
 }
 
 void launch_preprocess_backward(const GaussianView& g, const CamParams& cam, const uint32_t* n_touched,
                                 const float4* conic_opacity, uint32_t* rec_count, const uint32_t* first_slot,
                                 const float4* records, float* grad2d, const GradView& out, float* densif, int mode,
-                                uint8_t* row_mask, uint4* live, uint4* heavy, uint2* chunk_counts,
-                                float* pose_partial, float* pose_out, bool keep2d, bool half_sums, hipStream_t s) {
+                                uint8_t* row_mask, uint4* live, uint4* heavy, float* pose_partial, float* pose_out,
+                                bool keep2d, bool half_sums, hipStream_t s) {
     if (g.n <= 0) {
         if (pose_out) launch_fill_u32((uint32_t*)pose_out, 0u, 16, s);
         return;
@@ -716,28 +726,25 @@ void launch_preprocess_backward(const GaussianView& g, const CamParams& cam, con
     if (keep2d) launch_fill_u32((uint32_t*)grad2d, 0u, (int64_t)kGradStride * g.n, s);
     const int bases = (g.sh_degree + 1) * (g.sh_degree + 1);
     const unsigned chunks = (unsigned)pb_chunks(g.n);
-    preprocess_backward_classify_kernel<<<chunks, 256, 0, s>>>(g.n, n_touched, rec_count, first_slot,
-                                                               (float4*)densif, mode, row_mask, out, live, heavy,
-                                                               chunk_counts);
-    if (half_sums)
-        gather_heavy_kernel<true><<<chunks, 256, 0, s>>>(heavy, chunk_counts, records, grad2d);
-    else
-        gather_heavy_kernel<false><<<chunks, 256, 0, s>>>(heavy, chunk_counts, records, grad2d);
     const bool f16 = g.sh_dtype == kShF16;
     if (pose_out) {
         if (f16)
-            launch_live<__half, true>(g, bases, cam, conic_opacity, rec_count, records, grad2d, out, densif, mode, live,
-                                      chunk_counts, pose_partial, keep2d, half_sums, chunks, s);
+            launch_chunks<__half, true>(g, bases, cam, n_touched, first_slot, row_mask, live, heavy, conic_opacity,
+                                        rec_count, records, grad2d, out, densif, mode, pose_partial, keep2d,
+                                        half_sums, chunks, s);
         else
-            launch_live<float, true>(g, bases, cam, conic_opacity, rec_count, records, grad2d, out, densif, mode, live,
-                                     chunk_counts, pose_partial, keep2d, half_sums, chunks, s);
+            launch_chunks<float, true>(g, bases, cam, n_touched, first_slot, row_mask, live, heavy, conic_opacity,
+                                       rec_count, records, grad2d, out, densif, mode, pose_partial, keep2d, half_sums,
+                                       chunks, s);
         pose_reduce_kernel<<<1, 256, 0, s>>>(pose_partial, (int64_t)chunks, pose_out);
     } else if (f16) {
-        launch_live<__half, false>(g, bases, cam, conic_opacity, rec_count, records, grad2d, out, densif, mode, live,
-                                   chunk_counts, nullptr, keep2d, half_sums, chunks, s);
+        launch_chunks<__half, false>(g, bases, cam, n_touched, first_slot, row_mask, live, heavy, conic_opacity,
+                                     rec_count, records, grad2d, out, densif, mode, nullptr, keep2d, half_sums, chunks,
+                                     s);
     } else {
-        launch_live<float, false>(g, bases, cam, conic_opacity, rec_count, records, grad2d, out, densif, mode, live,
-                                  chunk_counts, nullptr, keep2d, half_sums, chunks, s);
+        launch_chunks<float, false>(g, bases, cam, n_touched, first_slot, row_mask, live, heavy, conic_opacity,
+                                    rec_count, records, grad2d, out, densif, mode, nullptr, keep2d, half_sums, chunks,
+                                    s);
     }
 }
 
