@@ -90,7 +90,7 @@
 #define R_SIG_HALF 0.5
 #define R_SIG_ONE 1.0
 #define R_ALPHA_EXP(s) exp(-(s))
-/* the reference's tests, kernels_forward.cuh:657-663 */
+/* the reference's tests, kernels_forward.cuh:660-665 */
 #define R_BLEND_ACCEPT(sigma, alpha, thr) ((sigma) >= 0 && (alpha) >= (REAL)(1.0f / 255.0f))
 #include "oracle_impl.inc"
 
