@@ -302,34 +302,51 @@ __device__ __forceinline__ void rank_keys(const uint32_t key[KPT], int64_t base,
 // key into one of kHistCopies histograms (by lane), summed at the end: keys
 // that arrive clustered (the instances of one primitive share their tile
 // digits) would otherwise serialise on one address.
-template <int KPT, int MAXB, int NW>
+// NTSUM (the depth sort's last pass): the same matrix of the payload's sums
+// (n_touched) per (digit, workgroup) goes to ntsums, from which the last
+// downsweep writes the instance offsets.
+template <int KPT, int MAXB, int NW, bool NTSUM = false>
 __global__ void __launch_bounds__(64 * NW) radix_upsweep_kernel(const uint32_t* __restrict__ keys,
+                                                                const uint32_t* __restrict__ v2,
                                                                 const uint32_t* d_n, int64_t max_n, int shift,
                                                                 int bits, uint32_t* __restrict__ counts,
-                                                                uint32_t nb) {
+                                                                uint32_t* __restrict__ ntsums, uint32_t nb) {
     constexpr int kNT = 64 * NW;
     __shared__ uint32_t s_hist[kHistCopies][MAXB];
+    __shared__ uint32_t s_hsum[NTSUM ? kHistCopies : 1][NTSUM ? MAXB : 1];
     const uint32_t t = threadIdx.x, lane = t & 63u, w = t >> 6;
     const uint32_t bins = 1u << bits, dmask = bins - 1u;
-    for (uint32_t b = t; b < (uint32_t)(kHistCopies * MAXB); b += kNT) (&s_hist[0][0])[b] = 0u;
+    for (uint32_t b = t; b < (uint32_t)(kHistCopies * MAXB); b += kNT) {
+        (&s_hist[0][0])[b] = 0u;
+        if constexpr (NTSUM) (&s_hsum[0][0])[b] = 0u;
+    }
     __syncthreads();
     const int64_t n = resolve_n(d_n, max_n);
     const int64_t base = (int64_t)blockIdx.x * (kNT * KPT) + (int64_t)w * (64 * KPT);
-    uint32_t key[KPT];
+    uint32_t key[KPT], nt[NTSUM ? KPT : 1];
 #pragma unroll
     for (int r = 0; r < KPT; ++r) {
         const int64_t i = base + (int64_t)r * 64 + lane;
         key[r] = i < n ? keys[i] : 0u;
+        if constexpr (NTSUM) nt[r] = i < n ? v2[i] : 0u;
     }
 #pragma unroll
     for (int r = 0; r < KPT; ++r)
-        if (base + (int64_t)r * 64 + lane < n) atomicAdd(&s_hist[lane & (kHistCopies - 1)][(key[r] >> shift) & dmask], 1u);
+        if (base + (int64_t)r * 64 + lane < n) {
+            const uint32_t d = (key[r] >> shift) & dmask, c = lane & (kHistCopies - 1);
+            atomicAdd(&s_hist[c][d], 1u);
+            if constexpr (NTSUM) atomicAdd(&s_hsum[c][d], nt[r]);
+        }
     __syncthreads();
     for (uint32_t b = t; b < bins; b += kNT) {
-        uint32_t c = 0;
+        uint32_t c = 0, sum = 0;
 #pragma unroll
-        for (int k = 0; k < kHistCopies; ++k) c += s_hist[k][b];
+        for (int k = 0; k < kHistCopies; ++k) {
+            c += s_hist[k][b];
+            if constexpr (NTSUM) sum += s_hsum[k][b];
+        }
         counts[(size_t)b * nb + blockIdx.x] = c;
+        if constexpr (NTSUM) ntsums[(size_t)b * nb + blockIdx.x] = sum;
     }
 }
 
@@ -372,20 +389,31 @@ __global__ void __launch_bounds__(kScanThreads) exclusive_scan_kernel(uint32_t* 
 // The workgroup's keys are first placed in LDS in digit order and written
 // out by consecutive threads, so each store instruction covers contiguous
 // runs.
-template <int KPT, bool PAYLOAD2, int MAXB, int NW>
+//
+// OFFS (the depth sort's last pass, payload 2 = n_touched): instead of the
+// sorted n_touched, writes offs[o] = the sum of n_touched over the sorted
+// positions before o (the instance offsets) and offs[n] = the total. ntscan
+// is the exclusive scan of [counts, ntsums] (one look-back scan of both
+// matrices): ntscan[j] - ntscan[0] is the n_touched sum of the keys of
+// digit < d plus those of digit d in earlier workgroups, for j = d nb + b;
+// the workgroup adds its own sum before the key, from one scan of its keys in
+// LDS (digit) order less that scan at the start of the key's digit run.
+template <int KPT, bool PAYLOAD2, int MAXB, int NW, bool OFFS = false>
 __global__ void __launch_bounds__(64 * NW) radix_downsweep_kernel(
     const uint32_t* __restrict__ keys_in, const uint32_t* __restrict__ vals_in, const uint32_t* __restrict__ v2_in,
     uint32_t* __restrict__ keys_out, uint32_t* __restrict__ vals_out, uint32_t* __restrict__ v2_out,
     const uint32_t* d_n, int64_t max_n, int shift, int bits, const uint32_t* __restrict__ offsets, uint32_t nb,
-    const uint32_t* __restrict__ block_n) {
+    const uint32_t* __restrict__ block_n, const uint32_t* __restrict__ ntscan, uint32_t* __restrict__ offs) {
     constexpr int kNT = 64 * NW;             // threads
     constexpr int kChunk = kNT * KPT;
     constexpr int kBpt = MAXB > kNT ? MAXB / kNT : 1;   // digits per thread in the workgroup scan
     static_assert(MAXB % kNT == 0 || kNT % MAXB == 0, "digits split evenly over the threads");
+    static_assert(!OFFS || (PAYLOAD2 && KPT * NW <= 64), "offsets from the n_touched payload, one striped scan");
     __shared__ uint32_t s_cnt[NW][MAXB];
     __shared__ uint32_t s_gofs[MAXB];
     __shared__ uint32_t s_key[kChunk], s_val[kChunk], s_v2[PAYLOAD2 ? kChunk : 1];
     __shared__ uint32_t s_wave[NW];
+    __shared__ uint32_t s_ntg[OFFS ? MAXB : 1], s_est[OFFS ? MAXB : 1], s_rw[OFFS ? 64 : 1];
     const uint32_t t = threadIdx.x, lane = t & 63u, w = t >> 6;
     const uint32_t bins = 1u << bits, dmask = bins - 1u;
     const int64_t blk = (int64_t)blockIdx.x * kChunk;
@@ -399,6 +427,8 @@ __global__ void __launch_bounds__(64 * NW) radix_downsweep_kernel(
     for (int q = 0; q < kBpt; ++q) {
         const uint32_t d = kBpt * t + (uint32_t)q;
         gofs[q] = d < bins ? offsets[(size_t)d * nb + blockIdx.x] : 0u;
+        if constexpr (OFFS)
+            if (d < bins) s_ntg[d] = ntscan[(size_t)d * nb + blockIdx.x] - ntscan[0];
     }
     __syncthreads();
     const int64_t base = blk + (int64_t)w * (64 * KPT);
@@ -453,6 +483,41 @@ __global__ void __launch_bounds__(64 * NW) radix_downsweep_kernel(
     }
     __syncthreads();
     const uint32_t cnt = (uint32_t)min((int64_t)kChunk, n - blk);
+    if constexpr (OFFS) {
+        // n_touched prefix over the LDS (digit) order; the prefix at each digit run's start
+        uint32_t nt[KPT], ex[KPT], sum;
+#pragma unroll
+        for (int r = 0; r < KPT; ++r) {
+            const uint32_t i = t + (uint32_t)r * kNT;
+            nt[r] = i < cnt ? s_v2[i] : 0u;
+        }
+        striped_scan_u32<KPT, NW>(nt, ex, &sum, s_rw);
+#pragma unroll
+        for (int r = 0; r < KPT; ++r) {
+            const uint32_t i = t + (uint32_t)r * kNT;
+            if (i < cnt) {
+                const uint32_t d = (s_key[i] >> shift) & dmask;
+                if (i == 0u || ((s_key[i - 1] >> shift) & dmask) != d) s_est[d] = ex[r];
+            }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int r = 0; r < KPT; ++r) {
+            const uint32_t i = t + (uint32_t)r * kNT;
+            if (i < cnt) {
+                const uint32_t k = s_key[i], d = (k >> shift) & dmask;
+                const uint32_t o = s_gofs[d] + i;
+                if (o < (uint64_t)max_n) {   // always true when the counts match the keys
+                    const uint32_t off = s_ntg[d] + (ex[r] - s_est[d]);
+                    keys_out[o] = k;
+                    vals_out[o] = s_val[i];
+                    offs[o] = off;
+                    if ((int64_t)o + 1 == n) offs[n] = off + nt[r];   // the total after the last key
+                }
+            }
+        }
+        return;
+    }
     for (uint32_t i = t; i < cnt; i += kNT) {
         const uint32_t k = s_key[i];
         const uint32_t o = s_gofs[(k >> shift) & dmask] + i;
@@ -466,17 +531,22 @@ __global__ void __launch_bounds__(64 * NW) radix_downsweep_kernel(
 
 int64_t radix_count_entries(int64_t max_n, bool depth) {
     const int64_t chunk = kThreads * (depth ? kDepthKeysPerThread : kTileKeysPerThread);
-    return ((max_n + chunk - 1) / chunk) * (depth ? kDepthMaxDigits : kTileMaxDigits);
+    // the depth sort's last pass also holds the n_touched sums
+    return ((max_n + chunk - 1) / chunk) * (depth ? 2 * kDepthMaxDigits : kTileMaxDigits);
 }
 
 // DW: waves per upsweep / downsweep workgroup; the keys per thread shrink so
 // that a workgroup still covers 256 KPT keys.
+// offs (depth sort, n_touched in v2): the last pass writes the instance
+// offsets (offs_done = true) when it has its own upsweep (two passes or
+// more); otherwise the caller scans them (launch_instance_offsets).
 template <int KPT, int MAXB, int DW>
 static int radix_passes(uint32_t* keys[2], uint32_t* vals[2], uint32_t* v2[2], const uint32_t* d_n, int64_t max_n,
                         int n_passes, const int* shifts, const int* bits, uint32_t* counts, uint32_t* tickets,
                         uint64_t* status, const uint32_t* epoch_base, uint32_t& epoch, uint32_t* err,
-                        const uint32_t* first_block_n, hipStream_t s) {
+                        const uint32_t* first_block_n, uint32_t* offs, bool* offs_done, hipStream_t s) {
     int cur = 0;
+    if (offs_done) *offs_done = false;
     if (max_n <= 0) return cur;
     const uint32_t nb = (uint32_t)((max_n + kThreads * KPT - 1) / (kThreads * KPT));
     constexpr int kDownKpt = KPT * (kThreads / 64) / DW;
@@ -486,19 +556,34 @@ static int radix_passes(uint32_t* keys[2], uint32_t* vals[2], uint32_t* v2[2], c
         const int64_t cn = (int64_t)nb << bits[p];
         // first_block_n: the first pass's blocks and digit counts come from the compaction
         const uint32_t* block_n = p == 0 ? first_block_n : nullptr;
+        const bool with_offs = offs && offs_done && v2 && p == n_passes - 1 && p > 0;
+        if constexpr (MAXB == kDepthMaxDigits) {
+            if (with_offs) {
+                radix_upsweep_kernel<kDownKpt, MAXB, DW, true><<<nb, 64 * DW, 0, s>>>(
+                    keys[cur], v2[cur], d_n, max_n, shifts[p], bits[p], counts, counts + cn, nb);
+                exclusive_scan_kernel<<<(unsigned)((2 * cn + kScanChunk - 1) / kScanChunk), kScanThreads, 0, s>>>(
+                    counts, 2 * cn, tickets + p, status, epoch_base, ++epoch, err);
+                radix_downsweep_kernel<kDownKpt, true, MAXB, DW, true><<<nb, 64 * DW, 0, s>>>(
+                    keys[cur], vals[cur], v2[cur], keys[cur ^ 1], vals[cur ^ 1], nullptr, d_n, max_n, shifts[p],
+                    bits[p], counts, nb, nullptr, counts + cn, offs);
+                *offs_done = true;
+                cur ^= 1;
+                continue;
+            }
+        }
         if (!block_n)
-            radix_upsweep_kernel<kDownKpt, MAXB, DW><<<nb, 64 * DW, 0, s>>>(keys[cur], d_n, max_n, shifts[p],
-                                                                             bits[p], counts, nb);
+            radix_upsweep_kernel<kDownKpt, MAXB, DW><<<nb, 64 * DW, 0, s>>>(keys[cur], nullptr, d_n, max_n, shifts[p],
+                                                                             bits[p], counts, nullptr, nb);
         exclusive_scan_kernel<<<(unsigned)((cn + kScanChunk - 1) / kScanChunk), kScanThreads, 0, s>>>(
             counts, cn, tickets + p, status, epoch_base, ++epoch, err);
         if (v2)
             radix_downsweep_kernel<kDownKpt, true, MAXB, DW><<<nb, 64 * DW, 0, s>>>(
                 keys[cur], vals[cur], v2[cur], keys[cur ^ 1], vals[cur ^ 1], v2[cur ^ 1], d_n, max_n, shifts[p],
-                bits[p], counts, nb, block_n);
+                bits[p], counts, nb, block_n, nullptr, nullptr);
         else
             radix_downsweep_kernel<kDownKpt, false, MAXB, DW><<<nb, 64 * DW, 0, s>>>(
                 keys[cur], vals[cur], nullptr, keys[cur ^ 1], vals[cur ^ 1], nullptr, d_n, max_n, shifts[p], bits[p],
-                counts, nb, block_n);
+                counts, nb, block_n, nullptr, nullptr);
         cur ^= 1;
     }
     return cur;
@@ -507,14 +592,14 @@ static int radix_passes(uint32_t* keys[2], uint32_t* vals[2], uint32_t* v2[2], c
 int radix_sort(uint32_t* keys[2], uint32_t* vals[2], uint32_t* v2[2], const uint32_t* d_n, int64_t max_n, bool depth,
                int n_passes, const int* shifts, const int* bits, uint32_t* counts, uint32_t* tickets,
                uint64_t* status, const uint32_t* epoch_base, uint32_t& epoch, uint32_t* err,
-               const uint32_t* first_block_n, hipStream_t s) {
+               const uint32_t* first_block_n, uint32_t* offs, bool* offs_done, hipStream_t s) {
     if (depth)
-        return radix_passes<kDepthKeysPerThread, kDepthMaxDigits, kDepthSortWaves>(keys, vals, v2, d_n, max_n, n_passes, shifts, bits,
-                                                                  counts, tickets, status, epoch_base, epoch, err,
-                                                                  first_block_n, s);
-    return radix_passes<kTileKeysPerThread, kTileMaxDigits, kTileSortWaves>(keys, vals, v2, d_n, max_n, n_passes, shifts, bits,
-                                                            counts, tickets, status, epoch_base, epoch, err,
-                                                            first_block_n, s);
+        return radix_passes<kDepthKeysPerThread, kDepthMaxDigits, kDepthSortWaves>(
+            keys, vals, v2, d_n, max_n, n_passes, shifts, bits, counts, tickets, status, epoch_base, epoch, err,
+            first_block_n, offs, offs_done, s);
+    return radix_passes<kTileKeysPerThread, kTileMaxDigits, kTileSortWaves>(
+        keys, vals, v2, d_n, max_n, n_passes, shifts, bits, counts, tickets, status, epoch_base, epoch, err,
+        first_block_n, nullptr, offs_done, s);
 }
 
 // ---------------------------------------------------------------- instance emission

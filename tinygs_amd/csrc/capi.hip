@@ -501,12 +501,13 @@ static int rasterizer_forward(tgs_rasterizer* r, const tgs_camera* camera, void*
             TGS_HIP(hipMemcpyAsync(r->h_counters, ctl, 3 * sizeof(uint32_t), hipMemcpyDeviceToHost, s));
             TGS_HIP(hipEventRecord(r->ev_counts, s));
         }
+        bool offs_done = false;
         psel = radix_sort(pk, pv, pn, &ctl->V, n, true, sp.n_dp, sp.dshift, sp.dbits, r->radix_counts.as<uint32_t>(),
                           ctl->tickets + kTicketDepth, status, &ctl->epoch_base, r->epoch, &ctl->err,
-                          r->block_n.as<uint32_t>(), s);
+                          r->block_n.as<uint32_t>(), r->offs.as<uint32_t>(), &offs_done, s);
         if (psel < 0) return fail(TGS_ERR_STATE, "depth sort digit width");
         r->depth_key_base = sp.key_base;
-        launch_instance_offsets(pn[psel], n, r->offs.as<uint32_t>(), ctl, status, r->epoch, s);
+        if (!offs_done) launch_instance_offsets(pn[psel], n, r->offs.as<uint32_t>(), ctl, status, r->epoch, s);
     }
     TGS_CHECK_LAUNCH();
     int64_t V = -1, I = -1, cap = cap0;
@@ -542,7 +543,7 @@ static int rasterizer_forward(tgs_rasterizer* r, const tgs_camera* camera, void*
         StageScope sc(ST_TILES, s);
         isel = radix_sort(ik, iv, nullptr, d_inst, cap, false, sp.n_tp, sp.tshift, sp.tbits,
                           r->radix_counts.as<uint32_t>(), ctl->tickets + kTicketTile, status, &ctl->epoch_base,
-                          r->epoch, &ctl->err, nullptr, s);
+                          r->epoch, &ctl->err, nullptr, nullptr, nullptr, s);
         if (isel < 0) return fail(TGS_ERR_STATE, "tile sort digit width");
         if (r->epoch >= kEpochStride) return fail(TGS_ERR_STATE, "look-back launches per forward exceed the epoch stride");
         launch_tile_ranges(ik[isel], d_inst, cap, r->ranges.as<uint2>(), T, s);

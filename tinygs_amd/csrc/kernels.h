@@ -115,11 +115,15 @@ int64_t radix_count_entries(int64_t max_n, bool depth);
 // scan of its count matrix. Ping-pongs between the buffers; returns the
 // index (0/1) of the result. first_block_n (depth sort): the first pass's
 // input blocks hold first_block_n[b] keys each (launch_compact_visible's
-// blocks) and its digit counts are already in counts.
+// blocks) and its digit counts are already in counts. offs (depth sort, v2 =
+// n_touched): with two passes or more the last pass writes the instance
+// offsets (offs[k] = sum of v2 over sorted positions < k, offs[n] = the
+// total) instead of the sorted v2, and sets *offs_done; otherwise the
+// caller runs launch_instance_offsets on the sorted v2.
 int radix_sort(uint32_t* keys[2], uint32_t* vals[2], uint32_t* v2[2], const uint32_t* d_n, int64_t max_n, bool depth,
                int n_passes, const int* shifts, const int* bits, uint32_t* counts, uint32_t* tickets,
                uint64_t* status, const uint32_t* epoch_base, uint32_t& epoch, uint32_t* err,
-               const uint32_t* first_block_n, hipStream_t s);
+               const uint32_t* first_block_n, uint32_t* offs, bool* offs_done, hipStream_t s);
 // Instances in depth order: thread per depth-sorted primitive k < ctl->V,
 // slots [offs[k], offs[k + 1]).
 // Rect tiles past the first 32 take the exact tile test with mean2d[p], the
