@@ -310,8 +310,13 @@ __global__ void __launch_bounds__(64 * NW) radix_upsweep_kernel(const uint32_t* 
                                                                 const uint32_t* __restrict__ v2,
                                                                 const uint32_t* d_n, int64_t max_n, int shift,
                                                                 int bits, uint32_t* __restrict__ counts,
-                                                                uint32_t* __restrict__ ntsums, uint32_t nb) {
+                                                                uint32_t* __restrict__ ntsums, uint32_t nb,
+                                                                uint2* __restrict__ rinit, uint32_t n_tiles) {
     constexpr int kNT = 64 * NW;
+    // rinit: the tile ranges the next downsweep reduces into, set to (UINT32_MAX, 0)
+    if (rinit)
+        for (uint32_t j = blockIdx.x * kNT + threadIdx.x; j < n_tiles; j += gridDim.x * kNT)
+            rinit[j] = make_uint2(0xffffffffu, 0u);
     __shared__ uint32_t s_hist[kHistCopies][MAXB];
     __shared__ uint32_t s_hsum[NTSUM ? kHistCopies : 1][NTSUM ? MAXB : 1];
     const uint32_t t = threadIdx.x, lane = t & 63u, w = t >> 6;
@@ -398,12 +403,22 @@ __global__ void __launch_bounds__(kScanThreads) exclusive_scan_kernel(uint32_t* 
 // digit < d plus those of digit d in earlier workgroups, for j = d nb + b;
 // the workgroup adds its own sum before the key, from one scan of its keys in
 // LDS (digit) order less that scan at the start of the key's digit run.
-template <int KPT, bool PAYLOAD2, int MAXB, int NW, bool OFFS = false>
+//
+// RANGES (the tile sort's last pass, all key bits sorted): also reduces the
+// per-tile instance ranges. The output is then sorted by the whole key, and a
+// workgroup's keys in LDS order are its runs of equal keys; the first key of
+// each run takes atomicMin into ranges[key].x and the last atomicMax of its
+// position + 1 into ranges[key].y (set to (UINT32_MAX, 0) by the upsweep), so
+// a tile's range ends as the first and past-the-last position of its key:
+// the global first key of a tile is always the first of a workgroup run.
+// Empty tiles keep (UINT32_MAX, 0) (the forward blend writes (0, 0) there).
+template <int KPT, bool PAYLOAD2, int MAXB, int NW, bool OFFS = false, bool RANGES = false>
 __global__ void __launch_bounds__(64 * NW) radix_downsweep_kernel(
     const uint32_t* __restrict__ keys_in, const uint32_t* __restrict__ vals_in, const uint32_t* __restrict__ v2_in,
     uint32_t* __restrict__ keys_out, uint32_t* __restrict__ vals_out, uint32_t* __restrict__ v2_out,
     const uint32_t* d_n, int64_t max_n, int shift, int bits, const uint32_t* __restrict__ offsets, uint32_t nb,
-    const uint32_t* __restrict__ block_n, const uint32_t* __restrict__ ntscan, uint32_t* __restrict__ offs) {
+    const uint32_t* __restrict__ block_n, const uint32_t* __restrict__ ntscan, uint32_t* __restrict__ offs,
+    uint2* __restrict__ ranges, uint32_t n_tiles) {
     constexpr int kNT = 64 * NW;             // threads
     constexpr int kChunk = kNT * KPT;
     constexpr int kBpt = MAXB > kNT ? MAXB / kNT : 1;   // digits per thread in the workgroup scan
@@ -525,6 +540,12 @@ __global__ void __launch_bounds__(64 * NW) radix_downsweep_kernel(
             keys_out[o] = k;
             vals_out[o] = s_val[i];
             if constexpr (PAYLOAD2) v2_out[o] = s_v2[i];
+            if constexpr (RANGES) {
+                if (k < n_tiles) {
+                    if (i == 0u || s_key[i - 1u] != k) atomicMin(&ranges[k].x, o);
+                    if (i + 1u == cnt || s_key[i + 1u] != k) atomicMax(&ranges[k].y, o + 1u);
+                }
+            }
         }
     }
 }
@@ -540,13 +561,18 @@ int64_t radix_count_entries(int64_t max_n, bool depth) {
 // offs (depth sort, n_touched in v2): the last pass writes the instance
 // offsets (offs_done = true) when it has its own upsweep (two passes or
 // more); otherwise the caller scans them (launch_instance_offsets).
+// ranges (tile sort): the last pass reduces the tile ranges (ranges_done =
+// true) whenever it runs; otherwise the caller derives them
+// (launch_tile_ranges).
 template <int KPT, int MAXB, int DW>
 static int radix_passes(uint32_t* keys[2], uint32_t* vals[2], uint32_t* v2[2], const uint32_t* d_n, int64_t max_n,
                         int n_passes, const int* shifts, const int* bits, uint32_t* counts, uint32_t* tickets,
                         uint64_t* status, const uint32_t* epoch_base, uint32_t& epoch, uint32_t* err,
-                        const uint32_t* first_block_n, uint32_t* offs, bool* offs_done, hipStream_t s) {
+                        const uint32_t* first_block_n, uint32_t* offs, bool* offs_done, uint2* ranges,
+                        uint32_t n_tiles, bool* ranges_done, hipStream_t s) {
     int cur = 0;
     if (offs_done) *offs_done = false;
+    if (ranges_done) *ranges_done = false;
     if (max_n <= 0) return cur;
     const uint32_t nb = (uint32_t)((max_n + kThreads * KPT - 1) / (kThreads * KPT));
     constexpr int kDownKpt = KPT * (kThreads / 64) / DW;
@@ -560,30 +586,37 @@ static int radix_passes(uint32_t* keys[2], uint32_t* vals[2], uint32_t* v2[2], c
         if constexpr (MAXB == kDepthMaxDigits) {
             if (with_offs) {
                 radix_upsweep_kernel<kDownKpt, MAXB, DW, true><<<nb, 64 * DW, 0, s>>>(
-                    keys[cur], v2[cur], d_n, max_n, shifts[p], bits[p], counts, counts + cn, nb);
+                    keys[cur], v2[cur], d_n, max_n, shifts[p], bits[p], counts, counts + cn, nb, nullptr, 0u);
                 exclusive_scan_kernel<<<(unsigned)((2 * cn + kScanChunk - 1) / kScanChunk), kScanThreads, 0, s>>>(
                     counts, 2 * cn, tickets + p, status, epoch_base, ++epoch, err);
                 radix_downsweep_kernel<kDownKpt, true, MAXB, DW, true><<<nb, 64 * DW, 0, s>>>(
                     keys[cur], vals[cur], v2[cur], keys[cur ^ 1], vals[cur ^ 1], nullptr, d_n, max_n, shifts[p],
-                    bits[p], counts, nb, nullptr, counts + cn, offs);
+                    bits[p], counts, nb, nullptr, counts + cn, offs, nullptr, 0u);
                 *offs_done = true;
                 cur ^= 1;
                 continue;
             }
         }
+        const bool with_ranges = ranges && ranges_done && !v2 && !block_n && p == n_passes - 1;
         if (!block_n)
-            radix_upsweep_kernel<kDownKpt, MAXB, DW><<<nb, 64 * DW, 0, s>>>(keys[cur], nullptr, d_n, max_n, shifts[p],
-                                                                             bits[p], counts, nullptr, nb);
+            radix_upsweep_kernel<kDownKpt, MAXB, DW><<<nb, 64 * DW, 0, s>>>(
+                keys[cur], nullptr, d_n, max_n, shifts[p], bits[p], counts, nullptr, nb,
+                with_ranges ? ranges : nullptr, n_tiles);
         exclusive_scan_kernel<<<(unsigned)((cn + kScanChunk - 1) / kScanChunk), kScanThreads, 0, s>>>(
             counts, cn, tickets + p, status, epoch_base, ++epoch, err);
         if (v2)
             radix_downsweep_kernel<kDownKpt, true, MAXB, DW><<<nb, 64 * DW, 0, s>>>(
                 keys[cur], vals[cur], v2[cur], keys[cur ^ 1], vals[cur ^ 1], v2[cur ^ 1], d_n, max_n, shifts[p],
-                bits[p], counts, nb, block_n, nullptr, nullptr);
-        else
+                bits[p], counts, nb, block_n, nullptr, nullptr, nullptr, 0u);
+        else if (with_ranges) {
+            radix_downsweep_kernel<kDownKpt, false, MAXB, DW, false, true><<<nb, 64 * DW, 0, s>>>(
+                keys[cur], vals[cur], nullptr, keys[cur ^ 1], vals[cur ^ 1], nullptr, d_n, max_n, shifts[p], bits[p],
+                counts, nb, nullptr, nullptr, nullptr, ranges, n_tiles);
+            *ranges_done = true;
+        } else
             radix_downsweep_kernel<kDownKpt, false, MAXB, DW><<<nb, 64 * DW, 0, s>>>(
                 keys[cur], vals[cur], nullptr, keys[cur ^ 1], vals[cur ^ 1], nullptr, d_n, max_n, shifts[p], bits[p],
-                counts, nb, block_n, nullptr, nullptr);
+                counts, nb, block_n, nullptr, nullptr, nullptr, 0u);
         cur ^= 1;
     }
     return cur;
@@ -592,14 +625,15 @@ static int radix_passes(uint32_t* keys[2], uint32_t* vals[2], uint32_t* v2[2], c
 int radix_sort(uint32_t* keys[2], uint32_t* vals[2], uint32_t* v2[2], const uint32_t* d_n, int64_t max_n, bool depth,
                int n_passes, const int* shifts, const int* bits, uint32_t* counts, uint32_t* tickets,
                uint64_t* status, const uint32_t* epoch_base, uint32_t& epoch, uint32_t* err,
-               const uint32_t* first_block_n, uint32_t* offs, bool* offs_done, hipStream_t s) {
+               const uint32_t* first_block_n, uint32_t* offs, bool* offs_done, uint2* ranges, uint32_t n_tiles,
+               bool* ranges_done, hipStream_t s) {
     if (depth)
         return radix_passes<kDepthKeysPerThread, kDepthMaxDigits, kDepthSortWaves>(
             keys, vals, v2, d_n, max_n, n_passes, shifts, bits, counts, tickets, status, epoch_base, epoch, err,
-            first_block_n, offs, offs_done, s);
+            first_block_n, offs, offs_done, nullptr, 0u, ranges_done, s);
     return radix_passes<kTileKeysPerThread, kTileMaxDigits, kTileSortWaves>(
         keys, vals, v2, d_n, max_n, n_passes, shifts, bits, counts, tickets, status, epoch_base, epoch, err,
-        first_block_n, nullptr, offs_done, s);
+        first_block_n, nullptr, offs_done, ranges, n_tiles, ranges_done, s);
 }
 
 // ---------------------------------------------------------------- instance emission

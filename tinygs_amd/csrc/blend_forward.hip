@@ -62,7 +62,7 @@ __device__ __forceinline__ float sigma_box_lower_bound(float a, float b, float c
     return m - slack;
 }
 
-__global__ void __launch_bounds__(256) blend_forward_kernel(CamParams cam, const uint2* __restrict__ ranges,
+__global__ void __launch_bounds__(256) blend_forward_kernel(CamParams cam, uint2* __restrict__ ranges,
                                                             const uint32_t* __restrict__ inst_vals,
                                                             const float2* __restrict__ mean2d,
                                                             const float4* __restrict__ conic_opacity,
@@ -90,7 +90,11 @@ __global__ void __launch_bounds__(256) blend_forward_kernel(CamParams cam, const
     const bool inside = px < cam.width && py < cam.height;
     const float pcx = (float)px + 0.5f, pcy = (float)py + 0.5f;
 
-    const uint2 range = ranges[tile];
+    uint2 range = ranges[tile];
+    if (range.y == 0u) {   // an empty tile, left as (UINT32_MAX, 0) by the tile sort: stored as (0, 0)
+        range.x = 0u;
+        if (tid == 0u) ranges[tile] = range;
+    }
     const int32_t len = (int32_t)(range.y - range.x);
     const uint32_t slot0 = range.x / (uint32_t)kBucket + tile;   // first checkpoint slot of this tile
 
@@ -217,7 +221,7 @@ size_t blend_ckpt_slots(int64_t n_instances, uint32_t n_tiles) {
     return (size_t)(n_instances > 0 ? n_instances : 0) / kBucket + n_tiles + 1;
 }
 
-void launch_blend_forward(const CamParams& cam, const uint2* ranges, const uint32_t* inst_vals, const float2* mean2d,
+void launch_blend_forward(const CamParams& cam, uint2* ranges, const uint32_t* inst_vals, const float2* mean2d,
                           const float4* conic_opacity, const float4* color_pt, float* image, uint32_t* n_contrib,
                           uint32_t* tile_max, uint32_t* tile_loaded, float4* ckpt, uint4* items, BinCtl* ctl,
                           hipStream_t s) {

@@ -504,7 +504,7 @@ static int rasterizer_forward(tgs_rasterizer* r, const tgs_camera* camera, void*
         bool offs_done = false;
         psel = radix_sort(pk, pv, pn, &ctl->V, n, true, sp.n_dp, sp.dshift, sp.dbits, r->radix_counts.as<uint32_t>(),
                           ctl->tickets + kTicketDepth, status, &ctl->epoch_base, r->epoch, &ctl->err,
-                          r->block_n.as<uint32_t>(), r->offs.as<uint32_t>(), &offs_done, s);
+                          r->block_n.as<uint32_t>(), r->offs.as<uint32_t>(), &offs_done, nullptr, 0u, nullptr, s);
         if (psel < 0) return fail(TGS_ERR_STATE, "depth sort digit width");
         r->depth_key_base = sp.key_base;
         if (!offs_done) launch_instance_offsets(pn[psel], n, r->offs.as<uint32_t>(), ctl, status, r->epoch, s);
@@ -539,14 +539,16 @@ static int rasterizer_forward(tgs_rasterizer* r, const tgs_camera* camera, void*
     // without a host wait the instance count is read on the device (min(I, capacity))
     const uint32_t* d_inst = nosync ? &ctl->I : nullptr;
     int isel;
+    bool ranges_done = false;   // the tile sort's last pass reduced the tile ranges
     {
         StageScope sc(ST_TILES, s);
         isel = radix_sort(ik, iv, nullptr, d_inst, cap, false, sp.n_tp, sp.tshift, sp.tbits,
                           r->radix_counts.as<uint32_t>(), ctl->tickets + kTicketTile, status, &ctl->epoch_base,
-                          r->epoch, &ctl->err, nullptr, nullptr, nullptr, s);
+                          r->epoch, &ctl->err, nullptr, nullptr, nullptr, r->ranges.as<uint2>(), (uint32_t)T,
+                          &ranges_done, s);
         if (isel < 0) return fail(TGS_ERR_STATE, "tile sort digit width");
         if (r->epoch >= kEpochStride) return fail(TGS_ERR_STATE, "look-back launches per forward exceed the epoch stride");
-        launch_tile_ranges(ik[isel], d_inst, cap, r->ranges.as<uint2>(), T, s);
+        if (!ranges_done) launch_tile_ranges(ik[isel], d_inst, cap, r->ranges.as<uint2>(), T, s);
     }
     if (nosync) launch_capacity_check(ctl, cap, s);
     {

@@ -67,7 +67,7 @@ __device__ __forceinline__ h16x2 sel2(bool cx, bool cy, h16x2 a, h16x2 b) {
 // info[p] = (conic a | b << 16, c | opacity << 16, r | g << 8 | b << 16, 0)
 // ckpt16: per slot 256 pixels of (C.r | C.g << 16, C.b | T << 16) halves, in-tile index 64 q + L.
 __global__ void __launch_bounds__(256) blend16_forward_kernel(
-    CamParams cam, const uint2* __restrict__ ranges, const uint32_t* __restrict__ inst_vals,
+    CamParams cam, uint2* __restrict__ ranges, const uint32_t* __restrict__ inst_vals,
     const float2* __restrict__ mean2d, const uint4* __restrict__ info, uint16_t* __restrict__ image,
     uint16_t* __restrict__ n_contrib, uint32_t* __restrict__ tile_max, uint32_t* __restrict__ tile_loaded,
     uint2* __restrict__ ckpt, uint4* __restrict__ items, BinCtl* __restrict__ ctl) {
@@ -91,7 +91,11 @@ __global__ void __launch_bounds__(256) blend16_forward_kernel(
         inside[q] = px < cam.width && py < cam.height;
     }
 
-    const uint2 range = ranges[tile];
+    uint2 range = ranges[tile];
+    if (range.y == 0u) {   // an empty tile, left as (UINT32_MAX, 0) by the tile sort: stored as (0, 0)
+        range.x = 0u;
+        if (lane == 0u) ranges[tile] = range;
+    }
     const int32_t len = (int32_t)(range.y - range.x);
     const uint32_t slot0 = range.x / (uint32_t)kBucket + tile;
 
@@ -210,7 +214,7 @@ __global__ void __launch_bounds__(256) blend16_forward_kernel(
                                     min((uint32_t)kBucket, (uint32_t)len - b * (uint32_t)kBucket));
 }
 
-void launch_blend16_forward(const CamParams& cam, const uint2* ranges, const uint32_t* inst_vals,
+void launch_blend16_forward(const CamParams& cam, uint2* ranges, const uint32_t* inst_vals,
                             const float2* mean2d, const uint4* info, uint16_t* image, uint16_t* n_contrib,
                             uint32_t* tile_max, uint32_t* tile_loaded, uint2* ckpt, uint4* items, BinCtl* ctl,
                             hipStream_t s) {

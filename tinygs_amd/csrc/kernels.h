@@ -119,11 +119,16 @@ int64_t radix_count_entries(int64_t max_n, bool depth);
 // n_touched): with two passes or more the last pass writes the instance
 // offsets (offs[k] = sum of v2 over sorted positions < k, offs[n] = the
 // total) instead of the sorted v2, and sets *offs_done; otherwise the
-// caller runs launch_instance_offsets on the sorted v2.
+// caller runs launch_instance_offsets on the sorted v2. ranges (tile sort,
+// n_tiles tiles): the last pass also reduces each tile's instance range
+// [x, y) into ranges and sets *ranges_done; empty tiles are left as
+// (UINT32_MAX, 0), which the forward blend rewrites as (0, 0). Without
+// *ranges_done the caller runs launch_tile_ranges on the sorted keys.
 int radix_sort(uint32_t* keys[2], uint32_t* vals[2], uint32_t* v2[2], const uint32_t* d_n, int64_t max_n, bool depth,
                int n_passes, const int* shifts, const int* bits, uint32_t* counts, uint32_t* tickets,
                uint64_t* status, const uint32_t* epoch_base, uint32_t& epoch, uint32_t* err,
-               const uint32_t* first_block_n, uint32_t* offs, bool* offs_done, hipStream_t s);
+               const uint32_t* first_block_n, uint32_t* offs, bool* offs_done, uint2* ranges, uint32_t n_tiles,
+               bool* ranges_done, hipStream_t s);
 // Instances in depth order: thread per depth-sorted primitive k < ctl->V,
 // slots [offs[k], offs[k + 1]).
 // Rect tiles past the first 32 take the exact tile test with mean2d[p], the
@@ -158,7 +163,7 @@ void launch_preprocess16(const GaussianView& g, const CamParams& cam, uint32_t* 
 // padded 8x8-tiled layout, n_contrib u16 per pixel, ckpt 256 uint2 per slot
 // (the fp32 path's slots), items as the fp32 path's but with every Gaussian of
 // the bucket; records as the fp32 path's, half mode.
-void launch_blend16_forward(const CamParams& cam, const uint2* ranges, const uint32_t* inst_vals,
+void launch_blend16_forward(const CamParams& cam, uint2* ranges, const uint32_t* inst_vals,
                             const float2* mean2d, const uint4* info, uint16_t* image, uint16_t* n_contrib,
                             uint32_t* tile_max, uint32_t* tile_loaded, uint2* ckpt, uint4* items, BinCtl* ctl,
                             hipStream_t s);
@@ -176,7 +181,7 @@ void launch_blend16_backward(const CamParams& cam, const uint32_t* inst_vals, co
 // ctl->n_items (at most I / 32 + T entries). tile_loaded[t]: Gaussians the
 // tile staged before it finished (a work statistic).
 size_t blend_ckpt_slots(int64_t n_instances, uint32_t n_tiles);
-void launch_blend_forward(const CamParams& cam, const uint2* ranges, const uint32_t* inst_vals, const float2* mean2d,
+void launch_blend_forward(const CamParams& cam, uint2* ranges, const uint32_t* inst_vals, const float2* mean2d,
                           const float4* conic_opacity, const float4* color_pt, float* image, uint32_t* n_contrib,
                           uint32_t* tile_max, uint32_t* tile_loaded, float4* ckpt, uint4* items, BinCtl* ctl,
                           hipStream_t s);
