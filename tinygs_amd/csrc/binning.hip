@@ -412,6 +412,8 @@ __global__ void __launch_bounds__(kScanThreads) exclusive_scan_kernel(uint32_t* 
 // a tile's range ends as the first and past-the-last position of its key:
 // the global first key of a tile is always the first of a workgroup run.
 // Empty tiles keep (UINT32_MAX, 0) (the forward blend writes (0, 0) there).
+// The sorted keys are not written: the ranges hold them
+// (launch_keys_from_ranges restores them).
 template <int KPT, bool PAYLOAD2, int MAXB, int NW, bool OFFS = false, bool RANGES = false>
 __global__ void __launch_bounds__(64 * NW) radix_downsweep_kernel(
     const uint32_t* __restrict__ keys_in, const uint32_t* __restrict__ vals_in, const uint32_t* __restrict__ v2_in,
@@ -537,7 +539,7 @@ __global__ void __launch_bounds__(64 * NW) radix_downsweep_kernel(
         const uint32_t k = s_key[i];
         const uint32_t o = s_gofs[(k >> shift) & dmask] + i;
         if (o < (uint64_t)max_n) {   // always true when the counts match the keys
-            keys_out[o] = k;
+            if constexpr (!RANGES) keys_out[o] = k;
             vals_out[o] = s_val[i];
             if constexpr (PAYLOAD2) v2_out[o] = s_v2[i];
             if constexpr (RANGES) {
@@ -875,6 +877,22 @@ __global__ void tile_ranges_kernel(const uint32_t* __restrict__ keys, const uint
         tile_boundary(i, n, prev, cur, ranges, n_tiles);
         prev = cur;
     }
+}
+
+// keys[i] = t for i in ranges[t] (workgroup per tile): the sorted tile keys
+// of a tile sort whose last pass wrote only the ranges
+__global__ void keys_from_ranges_kernel(const uint2* __restrict__ ranges, uint32_t n_tiles, int64_t max_n,
+                                        uint32_t* __restrict__ keys) {
+    const uint32_t t = blockIdx.x;
+    if (t >= n_tiles) return;
+    const uint2 r = ranges[t];
+    const uint32_t end = (uint32_t)min((int64_t)r.y, max_n);
+    for (uint32_t i = r.x + threadIdx.x; i < end; i += blockDim.x) keys[i] = t;
+}
+
+void launch_keys_from_ranges(const uint2* ranges, uint32_t n_tiles, int64_t max_inst, uint32_t* inst_keys,
+                             hipStream_t s) {
+    if (n_tiles) keys_from_ranges_kernel<<<n_tiles, 256, 0, s>>>(ranges, n_tiles, max_inst, inst_keys);
 }
 
 void launch_tile_ranges(const uint32_t* inst_keys, const uint32_t* d_n, int64_t max_inst, uint2* ranges,

@@ -242,6 +242,8 @@ struct tgs_rasterizer {
     uint32_t* h_counters = nullptr;   // pinned copy of BinCtl {V, I, err}
     // state of the last forward
     bool fwd_done = false;
+    bool ikeys_from_ranges = false;   // the sorted tile keys exist only as the tile ranges
+    int64_t tile_sort_cap = 0;        // the tile sort's key capacity (instances past it are dropped)
     bool bwd_queues_clear = false;   // backward queue counters still zero since the last forward
     CamParams cam{};
     int64_t n = 0, V = 0, I = 0;
@@ -549,6 +551,8 @@ static int rasterizer_forward(tgs_rasterizer* r, const tgs_camera* camera, void*
         if (isel < 0) return fail(TGS_ERR_STATE, "tile sort digit width");
         if (r->epoch >= kEpochStride) return fail(TGS_ERR_STATE, "look-back launches per forward exceed the epoch stride");
         if (!ranges_done) launch_tile_ranges(ik[isel], d_inst, cap, r->ranges.as<uint2>(), T, s);
+        r->ikeys_from_ranges = ranges_done;
+        r->tile_sort_cap = cap;
     }
     if (nosync) launch_capacity_check(ctl, cap, s);
     {
@@ -765,6 +769,14 @@ int tgs_rasterizer_debug_view(tgs_rasterizer* r, tgs_debug_view* out) {
     out->depth_sorted_keys = r->pkeys[r->psel].as<uint32_t>();
     out->depth_key_base = r->depth_key_base;
     out->depth_sorted_prims = r->pvals[r->psel].as<uint32_t>();
+    if (r->ikeys_from_ranges) {   // the tile sort kept its keys only as ranges: written out here
+        const uint32_t T = r->cam.grid_w * r->cam.grid_h;
+        TGS_HIP(hipDeviceSynchronize());
+        launch_keys_from_ranges(r->ranges.as<uint2>(), T, r->tile_sort_cap, r->ikeys[r->isel].as<uint32_t>(), nullptr);
+        TGS_HIP(hipGetLastError());
+        TGS_HIP(hipDeviceSynchronize());
+        r->ikeys_from_ranges = false;
+    }
     out->instance_tiles = r->ikeys[r->isel].as<uint32_t>();
     out->instance_prims = r->ivals[r->isel].as<uint32_t>();
     out->tile_ranges = r->ranges.as<uint32_t>();

@@ -122,8 +122,10 @@ int64_t radix_count_entries(int64_t max_n, bool depth);
 // caller runs launch_instance_offsets on the sorted v2. ranges (tile sort,
 // n_tiles tiles): the last pass also reduces each tile's instance range
 // [x, y) into ranges and sets *ranges_done; empty tiles are left as
-// (UINT32_MAX, 0), which the forward blend rewrites as (0, 0). Without
-// *ranges_done the caller runs launch_tile_ranges on the sorted keys.
+// (UINT32_MAX, 0), which the forward blend rewrites as (0, 0); that pass
+// writes no sorted keys (launch_keys_from_ranges restores them from the
+// ranges). Without *ranges_done the caller runs launch_tile_ranges on the
+// sorted keys.
 int radix_sort(uint32_t* keys[2], uint32_t* vals[2], uint32_t* v2[2], const uint32_t* d_n, int64_t max_n, bool depth,
                int n_passes, const int* shifts, const int* bits, uint32_t* counts, uint32_t* tickets,
                uint64_t* status, const uint32_t* epoch_base, uint32_t& epoch, uint32_t* err,
@@ -146,6 +148,10 @@ void launch_emit_instances(const uint32_t* prims, const uint32_t* offs, BinCtl* 
                            hipStream_t s);
 // [start, end) per tile, (0, 0) for empty tiles; every entry written. The
 // instance count is min(*d_n, max_inst) (max_inst when d_n is null).
+// inst_keys[i] = t for every i in the range [x, min(y, max_inst)) of tile t
+// (ranges as the forward blend leaves them)
+void launch_keys_from_ranges(const uint2* ranges, uint32_t n_tiles, int64_t max_inst, uint32_t* inst_keys,
+                             hipStream_t s);
 void launch_tile_ranges(const uint32_t* inst_keys, const uint32_t* d_n, int64_t max_inst, uint2* ranges,
                         uint32_t n_tiles, hipStream_t s);
 // Whether radix_sort accepts these digit widths (host check, before any launch).
