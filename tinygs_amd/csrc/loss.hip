@@ -172,7 +172,7 @@ __device__ __forceinline__ void ssim_tile_of(uint32_t& tx, uint32_t& ty, uint32_
 // (32x32 tile, channel): no state is carried across channels, which keeps
 // the register footprint small enough for four workgroups per CU.
 template <typename T, bool ASSIGN>
-__global__ void __launch_bounds__(256) l1_ssim_forward_kernel(uint32_t W, uint32_t H, float C1, float C2,
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(6))) l1_ssim_forward_kernel(uint32_t W, uint32_t H, float C1, float C2,
                                                               float s_ssim, float s_l1,
                                                               const T* __restrict__ pred,
                                                               const T* __restrict__ target,
@@ -265,20 +265,24 @@ __global__ void __launch_bounds__(256) l1_ssim_forward_kernel(uint32_t W, uint32
     const int vc = t & 31, vr = t >> 5;
     if (loss) loss += co;
     if (grad) grad += co;
-    // the epilogue's own pixels (L1 terms, accumulated values) are loaded
-    // before the vertical pass, so their latency hides behind it
+    // epilogue in 8x8-block order: wave w takes blocks w, w + 4, w + 8, w + 12
+    // of the tile (4 x 4 blocks), lane = pixel of the block, so each of its
+    // loads and stores is one 256-byte run. Its own pixels (L1 terms,
+    // accumulated values) are loaded before the vertical pass, so their
+    // latency hides behind it.
+    const int lane = t & 63, wv = t >> 6;
     const bool acc_l = !ASSIGN && loss, acc_g = !ASSIGN && grad, l1 = s_l1 != 0.f;
-    uint32_t pidx[4];
     float pp[4], pt[4], pl[4], pg[4];
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-        const int px = bx + vc, py = by + 4 * vr + q;
+        const int b = wv + 4 * q;
+        const int px = bx + 8 * (b & 3) + (lane & 7), py = by + 8 * (b >> 2) + (lane >> 3);
         const bool in = px < pw && py < ph;
-        pidx[q] = in ? tiled_index((uint32_t)py, (uint32_t)px, tw) : 0u;
-        pp[q] = in && l1 ? ld(pred, pidx[q]) : 0.f;
-        pt[q] = in && l1 ? ld(target, pidx[q]) : 0.f;
-        pl[q] = in && acc_l ? ld(loss, pidx[q]) : 0.f;
-        pg[q] = in && acc_g ? ld(grad, pidx[q]) : 0.f;
+        const uint32_t idx = in ? tiled_index((uint32_t)py, (uint32_t)px, tw) : 0u;
+        pp[q] = in && l1 ? ld(pred, idx) : 0.f;
+        pt[q] = in && l1 ? ld(target, idx) : 0.f;
+        pl[q] = in && acc_l ? ld(loss, idx) : 0.f;
+        pg[q] = in && acc_g ? ld(grad, idx) : 0.f;
     }
     float o[4][4];
 #pragma unroll
@@ -294,6 +298,16 @@ __global__ void __launch_bounds__(256) l1_ssim_forward_kernel(uint32_t W, uint32
             o[v][q] = acc;
         }
     }
+    // the four filtered moments change hands through LDS (over s_h, once every
+    // thread has read its columns)
+    auto s_o = reinterpret_cast<float (*)[kOT][kOT + 1]>(s_buf);
+    static_assert(4 * kOT * (kOT + 1) <= 4 * kIT * (kOT + 1), "moments fit in s_buf");
+    __syncthreads();
+#pragma unroll
+    for (int v = 0; v < 4; ++v)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) s_o[v][4 * vr + q][vc] = o[v][q];
+    __syncthreads();
     if (dm_mu) {
         dm_mu += co;
         dm_s1 += co;
@@ -301,9 +315,11 @@ __global__ void __launch_bounds__(256) l1_ssim_forward_kernel(uint32_t W, uint32
     }
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-        const int px = bx + vc, py = by + 4 * vr + q;
+        const int b = wv + 4 * q;
+        const int lx = 8 * (b & 3) + (lane & 7), ly = 8 * (b >> 2) + (lane >> 3);
+        const int px = bx + lx, py = by + ly;
         if (px >= pw || py >= ph) continue;
-        const uint32_t idx = pidx[q];
+        const uint32_t idx = tiled_index((uint32_t)py, (uint32_t)px, tw);
         float lv = pl[q];
         float gv = pg[q];
         if (l1) {
@@ -312,11 +328,11 @@ __global__ void __launch_bounds__(256) l1_ssim_forward_kernel(uint32_t W, uint32
             gv = __builtin_fmaf(__builtin_copysignf(1.0f, d), s_l1, gv);
         }
         if (px < (int)W && py < (int)H) {
-            const float mu1 = o[0][q], mu2 = o[2][q];
+            const float mu1 = s_o[0][ly][lx], mu2 = s_o[2][ly][lx];
             const float mu1_sq = mu1 * mu1, mu2_sq = mu2 * mu2;
-            const float s12 = o[3][q] - mu1 * mu2;
+            const float s12 = s_o[3][ly][lx] - mu1 * mu2;
             const float A = mu1_sq + mu2_sq + C1;
-            const float B = ((o[1][q] - mu1_sq) - mu2_sq) + C2;   // sigma1^2 + sigma2^2 + C2
+            const float B = ((s_o[1][ly][lx] - mu1_sq) - mu2_sq) + C2;   // sigma1^2 + sigma2^2 + C2
             const float Cc = 2.0f * mu1 * mu2 + C1;
             const float D = 2.0f * s12 + C2;
             // one reciprocal each of A and B replaces the reference's seven divisions
