@@ -183,8 +183,11 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(6))) l
     // use; s_h: the horizontal sums x, x^2 + y^2, y, xy, overlaying s_in once
     // every thread holds its sums in registers (22 KB of LDS instead of 31 KB)
     __shared__ float s_buf[4 * kIT * (kOT + 1)];
-    static_assert(kHT * kHT <= 4 * kIT * (kOT + 1), "s_in fits inside s_h");
-    auto s_in = reinterpret_cast<__half2 (*)[kHT]>(s_buf);
+    // s_in rows of 49 words: the horizontal pass's lanes (8 rows x 8 groups of
+    // 4 columns) then meet 2-way bank conflicts instead of 4-way
+    constexpr int kInStride = kHT + 1;
+    static_assert(kHT * kInStride <= 4 * kIT * (kOT + 1), "s_in fits inside s_h");
+    auto s_in = reinterpret_cast<__half2 (*)[kInStride]>(s_buf);
     auto s_h = reinterpret_cast<float (*)[kIT][kOT + 1]>(s_buf);
     const int t = (int)threadIdx.x;
     uint32_t tx, ty, ch;
@@ -299,9 +302,11 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(6))) l
         }
     }
     // the four filtered moments change hands through LDS (over s_h, once every
-    // thread has read its columns)
-    auto s_o = reinterpret_cast<float (*)[kOT][kOT + 1]>(s_buf);
-    static_assert(4 * kOT * (kOT + 1) <= 4 * kIT * (kOT + 1), "moments fit in s_buf");
+    // thread has read its columns); rows of 40 words: conflict-free for the
+    // column-order writes and the block-order reads on 64 banks
+    constexpr int kOStride = kOT + 8;
+    auto s_o = reinterpret_cast<float (*)[kOT][kOStride]>(s_buf);
+    static_assert(4 * kOT * kOStride <= 4 * kIT * (kOT + 1), "moments fit in s_buf");
     __syncthreads();
 #pragma unroll
     for (int v = 0; v < 4; ++v)
