@@ -36,10 +36,15 @@ pytestmark = pytest.mark.gpu
 # (log-scales about -5.5, -1.4, -5.2) the rotation gradient differs from the
 # oracle's by up to 6.3e-4 normwise (measured) while the 2D sums differ by
 # 2.7e-6 and the chain itself is bit-exact; the GPU's own run-to-run variation
-# there is 2.3e-4.
-END_TO_END_RTOL = {"means": 1e-4, "scales": 1e-4, "rotations": 1e-3, "opacities": 1e-4, "sh0": 1e-4,
+# there is 2.3e-4. The log-scale elementwise floor is 1.5e-4 max|cpu|: one
+# outlier Gaussian's scale gradient sums about 1e5 cancelling pixel terms,
+# and since the 2D-gradient records are added in the order the blend
+# buckets finish (as the reference's float atomics are), its error varies
+# between runs of the same build: 1.5e-5 to 7.1e-5 max|cpu| measured (the
+# normwise figure is that same element, so its bar is 1.5e-4 too).
+END_TO_END_RTOL = {"means": 1e-4, "scales": 1.5e-4, "rotations": 1e-3, "opacities": 1e-4, "sh0": 1e-4,
                    "sh_rest": 1e-4}
-END_TO_END_ATOL_FRAC = {"rotations": 1e-3}
+END_TO_END_ATOL_FRAC = {"rotations": 1e-3, "scales": 1.5e-4}
 
 LR = {"means": 1.6e-4, "scene_scale": 1.0, "opacities": 5e-2, "rotations": 1e-3, "scales": 5e-3, "shs": 5e-3}
 
