@@ -182,9 +182,10 @@ typedef struct tgs_debug_view {
     const float* color;            /* [4n]: r, g, b (unclamped), ln(255 * opacity) */
     const uint32_t* depth_sorted_keys;  /* [n_visible] depth bits - depth_key_base, ascending */
     const uint32_t* depth_sorted_prims; /* [n_visible] */
-    const uint32_t* instance_tiles;     /* [n_instances] sorted */
+    const uint32_t* instance_tiles;     /* [n_instances] sorted (written from tile_ranges by this call:
+                                           the tile sort keeps them only as ranges) */
     const uint32_t* instance_prims;     /* [n_instances] */
-    const uint32_t* tile_ranges;        /* [2 * n_tiles] */
+    const uint32_t* tile_ranges;        /* [2 * n_tiles]: [start, end) per tile, (0, 0) when empty */
     const uint32_t* n_contrib;          /* [channel_stride] (fp16 images: uint16_t) */
     const uint32_t* tile_max;           /* [n_tiles] */
     const float* grad2d;                /* [12n] after a TGS_BACKWARD_KEEP_2D backward, else NULL */
