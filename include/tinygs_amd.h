@@ -12,7 +12,8 @@
  * different handles may run concurrently on different streams.
  * Memory: parameters, gradients, images and loss buffers are owned by the
  * caller; every handle owns its grow-only device scratch.
- * Images are fp32, channel-planar, padded to multiples of 8 and 8x8-tiled
+ * Images are fp32 (or fp16 for the fp16-image rasterizer and losses),
+ * channel-planar, padded to multiples of 8 and 8x8-tiled
  * (tinygs/include/tinygs/common.hpp:366-414).
  */
 #ifndef TINYGS_AMD_H
@@ -115,8 +116,12 @@ int tgs_rasterizer_reserve(tgs_rasterizer* r, int64_t max_instances, int32_t gri
 /* Synchronises the stream and reports the device-side state of the forwards
  * queued so far: TGS_ERR_CAPACITY when a no-sync forward overflowed its
  * capacity (the flag is cleared when clear_capacity_flag is nonzero),
- * TGS_ERR_STATE when a binning scan failed. Also makes the counts of a no-sync
- * forward available to tgs_rasterizer_counts without a further wait. */
+ * TGS_ERR_STATE when a binning scan failed (those flags are cleared once
+ * reported; the forwards that saw them rendered nothing). Also makes the
+ * counts of a no-sync forward available to tgs_rasterizer_counts without a
+ * further wait. A forward that waits (no TGS_FORWARD_NO_SYNC) reports a
+ * failed binning scan itself: it fails with TGS_ERR_STATE, and a backward
+ * after it is refused. */
 int tgs_rasterizer_status(tgs_rasterizer* r, int32_t clear_capacity_flag, void* stream);
 /* FastGSRasterizer::backward (fastgs.cu:238-384). Accumulates (+=) into grads.
  * Must follow a forward on the same Gaussians and camera. */
@@ -369,6 +374,20 @@ int tgs_gaussians_gather(const tgs_gaussians* src, const tgs_gaussians* dst, con
  * g->n indices, each in [0, n); out-of-range indices are refused before
  * anything is written). Uses one temporary array; synchronises the stream. */
 int tgs_gaussians_reorder(const tgs_gaussians* g, const uint32_t* indices, void* stream);
+/* The reorder() of Orchestrator::reorder_gaussians (orchestrator.cu:26-90):
+ * indices (device, n) receives the Gaussians' order by the 30-bit Morton
+ * code of their means (means: device float[3n]) in the means' bounding box
+ * (per axis (v - min) / max(max - min, 1e-8), clamped to [0, 1], times 1023,
+ * truncated), stable for equal codes, as CUB's radix sort over bits 0..29.
+ * Feed it to tgs_gaussians_reorder / tgs_adam_reorder. Allocates its scratch
+ * and synchronises the stream. */
+int tgs_morton_order(const float* means, int64_t n, uint32_t* indices, void* stream);
+/* densification_update of Orchestrator::reorder_gaussians
+ * (orchestrator.cu:1023-1032, 1052-1059): out[i] = info[indices[i]] for the
+ * n DensificationInfo rows (device float4[n] each; out must not alias info).
+ * Out-of-range indices are refused before anything is written
+ * (synchronises the stream for that check). */
+int tgs_densification_reorder(const void* info, void* out, const uint32_t* indices, int64_t n, void* stream);
 /* thrust::copy_if of the flag indices (default.cu:198-203, gpu_gaussian.cu:120-124): out
  * (device, capacity n) receives the i < n with flags[i] != 0 in order, *count their number.
  * Synchronises. */
@@ -470,6 +489,14 @@ int tgs_selftest_half(int32_t op, const void* a, const void* b, const void* c, v
  * rounded quotient. out: device int64[8]: [0] mismatches, [1] pairs checked,
  * [2..4] a, b, quotient bits of one mismatch. Tests only. */
 int tgs_selftest_half_div_exhaustive(int64_t* out, void* stream);
+/* Spin bound of the binning's look-back waits on the current device, for
+ * tests of the error path: 0 makes every look-back that has a predecessor
+ * give up at once (as a wait that ran out would), setting the look-back error
+ * flag; every kernel still runs to its end, and the emission and the blend
+ * skip their work when the flag is set. spins = 0xffffffff restores the
+ * default bound. Process-wide; not for use while forwards are queued. No
+ * counterpart in the reference. */
+int tgs_selftest_lookback_spins(uint32_t spins);
 
 #ifdef __cplusplus
 }

@@ -65,6 +65,9 @@ using ParamMap = std::map<std::string, double>;
 
 enum class DataType { Float32 = 0, Float16 = 1 };
 
+// The C ABI's element type of an image or parameter array.
+inline int32_t c_dtype(DataType t) { return t == DataType::Float16 ? TGS_DTYPE_FLOAT16 : TGS_DTYPE_FLOAT32; }
+
 // ---------------------------------------------------------------- device memory
 
 template <class T>
@@ -468,20 +471,24 @@ public:
         bind();
     }
 
-    // Renders ctx.fwd_input into ctx.fwd_output.image (fp32, every padded
-    // element written; padding zero). Updates densification max radii when
+    // Renders ctx.fwd_input into ctx.fwd_output.image (every padded element
+    // written; padding zero). The image's data type selects the rasterizer as
+    // in fastgs.cu:143-188: Float32 the fp32 path, Float16 the fp16-image
+    // rasterizer (FGS16: half conic and opacity, 8-bit colour, 255-scaled
+    // blending). Updates densification max radii when
     // ctx.densification_info is set.
     void forward(const RasterizeContext& ctx) override {
         if (!m_gaussians) throw std::runtime_error("FastGSRasterizer::forward: Gaussians not set");
         const Image& img = ctx.fwd_output.image;
-        if (img.data_type != DataType::Float32)
-            throw std::runtime_error("FastGSRasterizer::forward: only float32 images are supported");
         if (img.shape.width != ctx.fwd_input.width || img.shape.height != ctx.fwd_input.height)
             throw std::runtime_error("FastGSRasterizer::forward: image shape does not match the camera");
         bind();
         const tgs_camera cam = ctx.fwd_input.to_c();
-        throw_on(tgs_rasterizer_forward(m_handle, &cam, img.data, TGS_DTYPE_FLOAT32, densif(ctx), ctx.stream),
+        m_fwd_dtype = img.data_type;
+        m_fwd_valid = false;
+        throw_on(tgs_rasterizer_forward(m_handle, &cam, img.data, c_dtype(img.data_type), densif(ctx), ctx.stream),
                  "FastGSRasterizer::forward");
+        m_fwd_valid = true;
     }
 
     // Accumulates (+=) dL/dparams into ctx.gaussians_grad from
@@ -496,6 +503,13 @@ public:
             throw std::runtime_error("FastGSRasterizer::backward: Gaussians or gradient Gaussians not set");
         if (ctx.gaussians_grad->size() != m_gaussians->size())
             throw std::runtime_error("FastGSRasterizer::backward: gradient size does not match the Gaussians");
+        // fastgs.cu:273-274: the forward's image type picks the backward (half
+        // image and half gradient image after an fp16 forward); the buffers
+        // are read with that element size, so they must all be of it
+        if (m_fwd_valid && (ctx.fwd_output.image.data_type != m_fwd_dtype ||
+                            ctx.grad_output.image.data_type != m_fwd_dtype))
+            throw std::runtime_error("FastGSRasterizer::backward: image / gradient image data type differs from "
+                                     "the forward's image");
         const tgs_gaussians g = ctx.gaussians_grad->to_c();
         const int32_t flags = (assign ? TGS_BACKWARD_ASSIGN : 0) | (m_pose_opt ? TGS_BACKWARD_POSE : 0);
         throw_on(tgs_rasterizer_backward_ex(m_handle, ctx.grad_output.image.data, ctx.fwd_output.image.data, &g,
@@ -532,6 +546,8 @@ public:
 
 private:
     bool m_pose_opt = false;
+    DataType m_fwd_dtype = DataType::Float32;   // image type of the last forward
+    bool m_fwd_valid = false;
     void bind() {
         const tgs_gaussians g = m_gaussians->to_c();
         throw_on(tgs_rasterizer_set_gaussians(m_handle, &g), "FastGSRasterizer::set_gaussians");
@@ -573,11 +589,16 @@ public:
     FusedLoss(const FusedLoss&) = delete;
     FusedLoss& operator=(const FusedLoss&) = delete;
 
+    // l1.cu:109-151, fused_ssim.cu:797-916: the target's data type selects
+    // the fp32 or fp16 kernels; prediction, loss and gradient images are of it.
     void evaluate(LossContext ctx, float scale) override {
         if (ctx.pred.shape != ctx.target.shape)
             throw std::runtime_error(m_name + ": prediction and target shapes differ");
-        if (ctx.pred.data_type != DataType::Float32 || ctx.target.data_type != DataType::Float32)
-            throw std::runtime_error(m_name + ": only float32 images are supported");
+        const DataType dt = ctx.target.data_type;
+        if (ctx.pred.data_type != dt)
+            throw std::runtime_error(m_name + ": prediction and target data type must be the same");
+        if ((ctx.loss && ctx.loss.data_type != dt) || (ctx.grad && ctx.grad.data_type != dt))
+            throw std::runtime_error(m_name + ": loss / gradient image data type differs from the target's");
         tgs_loss_context c{};
         c.pred = ctx.pred.data;
         c.target = ctx.target.data;
@@ -586,7 +607,7 @@ public:
         c.width = ctx.pred.shape.width;
         c.height = ctx.pred.shape.height;
         c.channel = ctx.pred.shape.channel;
-        c.dtype = TGS_DTYPE_FLOAT32;
+        c.dtype = c_dtype(dt);
         throw_on(tgs_loss_evaluate(m_handle, &c, scale, ctx.stream), m_name.c_str());
     }
     std::string name() const override { return m_name; }
@@ -981,8 +1002,10 @@ public:
         if (pred.shape.width != target.shape.width || pred.shape.height != target.shape.height ||
             pred.shape.channel != target.shape.channel)
             throw std::runtime_error("Prediction and target shapes must match");
+        if (pred.data_type != target.data_type)
+            throw std::runtime_error("PSNR: prediction and target data type must be the same");
         tgs_loss_context c{pred.data, target.data, nullptr, nullptr, pred.shape.width, pred.shape.height,
-                           pred.shape.channel, TGS_DTYPE_FLOAT32};
+                           pred.shape.channel, c_dtype(pred.data_type)};
         float v = 0.0f;
         throw_on(tgs_psnr(&c, &v, stream), "PsnrMetric::evaluate");
         return v;

@@ -4,11 +4,13 @@
 // forward, L1 / fused SSIM losses, backward (accumulating), SimpleAdam step.
 //
 // Usage: train_step <input.bin> <output.bin>
-// input  (little endian): int64 n; int32 sh_degree, sh_half; uint32 width, height;
+// input  (little endian): int64 n; int32 sh_degree, sh_half, image_half; uint32 width, height;
 //        float near, far, K[9], w2c[16], l1_weight, ssim_weight, grad_scaler, epsilon, shs_lr;
 //        float means[3n], scales[3n], rotations[4n], opacities[n], sh0[3n], sh_rest[45n];
-//        float target[3 * channel_stride] (8x8-tiled planar)
-// output: float image[3 * channel_stride], grad_image[3 * channel_stride];
+//        target[3 * channel_stride] (8x8-tiled planar; float, or half bits when image_half)
+// output: image[3 * channel_stride], grad_image[3 * channel_stride] (float, or half bits
+//         when image_half: the training data type of the reference's float16 configs,
+//         configs/default.json:99, which renders with the fp16-image rasterizer);
 //         gradients means, scales, rotations, opacities, sh0, sh_rest (fp32);
 //         parameters after the step in the same order (SH as float);
 //         int64 n_visible, n_instances, n_tiles.
@@ -40,12 +42,13 @@ int main(int argc, char** argv) {
         std::ifstream in(argv[1], std::ios::binary);
         if (!in) throw std::runtime_error("cannot open input");
         int64_t n;
-        int32_t sh_degree, sh_half;
+        int32_t sh_degree, sh_half, image_half;
         GPUBatchInput cam;
         float l1_w, ssim_w, grad_scaler, eps, shs_lr;
         rd(in, &n, 1);
         rd(in, &sh_degree, 1);
         rd(in, &sh_half, 1);
+        rd(in, &image_half, 1);
         rd(in, &cam.width, 1);
         rd(in, &cam.height, 1);
         rd(in, &cam.near, 1);
@@ -72,16 +75,20 @@ int main(int argc, char** argv) {
         rd(in, host.sh_coefficients_rest.data(), 45 * n);
         const ImageShape shape{cam.width, cam.height, 3};
         const size_t img_n = (size_t)shape.padded_size();
-        std::vector<float> target(img_n);
-        rd(in, target.data(), img_n);
+        const DataType img_dt = image_half ? DataType::Float16 : DataType::Float32;
+        // images as 4-byte words: a half image fills the first half of its buffer
+        const size_t img_words = image_half ? (img_n + 1) / 2 : img_n;
+        const size_t img_bytes = image_half ? 2 * img_n : 4 * img_n;
+        std::vector<float> target(img_words);
+        rd(in, reinterpret_cast<char*>(target.data()), img_bytes);
 
         auto gaussians = std::make_shared<GPUGaussian3d>(0, sh_half ? DataType::Float16 : DataType::Float32);
         gaussians->copy_from_host(host);
         gaussians->set_sh_degree(sh_degree);
         auto grads = gaussians->gradient_like();
 
-        DeviceArray<float> pred(img_n), tgt, loss(img_n), grad(img_n);
-        tgt.copy_from_host(target.data(), img_n);
+        DeviceArray<float> pred(img_words), tgt, loss(img_words), grad(img_words);
+        tgt.copy_from_host(target.data(), img_words);
 
         hipStream_t stream;
         hip_check(hipStreamCreate(&stream), "hipStreamCreate");
@@ -98,11 +105,11 @@ int main(int argc, char** argv) {
         ctx.stream = stream;
         ctx.grad_scaler = grad_scaler;
         ctx.fwd_input = cam;
-        ctx.fwd_output.image = Image(shape, DataType::Float32, pred.data());
-        ctx.grad_output.image = Image(shape, DataType::Float32, grad.data());
+        ctx.fwd_output.image = Image(shape, img_dt, pred.data());
+        ctx.grad_output.image = Image(shape, img_dt, grad.data());
         ctx.gaussians_grad = grads;
-        LossContext lctx{ctx.fwd_output.image, Image(shape, DataType::Float32, tgt.data()),
-                         Image(shape, DataType::Float32, loss.data()), ctx.grad_output.image, stream};
+        LossContext lctx{ctx.fwd_output.image, Image(shape, img_dt, tgt.data()), Image(shape, img_dt, loss.data()),
+                         ctx.grad_output.image, stream};
 
         // Orchestrator::train_step
         grads->memset_async(0, stream);
@@ -116,8 +123,8 @@ int main(int argc, char** argv) {
 
         std::ofstream out(argv[2], std::ios::binary);
         const std::vector<float> img_h = pred.to_host(), grad_h = grad.to_host();
-        wr(out, img_h.data(), img_n);
-        wr(out, grad_h.data(), img_n);
+        out.write(reinterpret_cast<const char*>(img_h.data()), (std::streamsize)img_bytes);
+        out.write(reinterpret_cast<const char*>(grad_h.data()), (std::streamsize)img_bytes);
         Gaussian3d gh, ph;
         grads->copy_to_host(gh);
         gaussians->copy_to_host(ph);
@@ -134,10 +141,28 @@ int main(int argc, char** argv) {
         if (!out) throw std::runtime_error("cannot write output");
         hip_check(hipStreamDestroy(stream), "hipStreamDestroy");
 
-        // error path: the reference throws on an unknown type
+        // error paths: the reference throws on an unknown type and on a
+        // prediction / target data type mismatch (l1.cu:110-115)
         try {
             create_loss("l3");
             std::cerr << "expected an exception for an unknown loss\n";
+            return 1;
+        } catch (const std::runtime_error&) {
+        }
+        try {
+            LossContext bad = lctx;
+            bad.target.data_type = image_half ? DataType::Float32 : DataType::Float16;
+            create_loss("l1")->evaluate(bad, 1.0f);
+            std::cerr << "expected an exception for mixed image data types\n";
+            return 1;
+        } catch (const std::runtime_error&) {
+        }
+        // a backward whose gradient image is not of the forward's data type is refused
+        try {
+            RasterizeContext bad = ctx;
+            bad.grad_output.image.data_type = image_half ? DataType::Float32 : DataType::Float16;
+            rasterizer->backward(bad);
+            std::cerr << "expected an exception for a gradient image of another data type\n";
             return 1;
         } catch (const std::runtime_error&) {
         }

@@ -109,6 +109,10 @@ def test_no_sync_capacity_overflow_reported(hip, orc):
     assert r.status(clear_capacity_flag=True) == _lib.TGS_ERR_CAPACITY
     assert r.counts()[1] == I          # the true count is still reported
     assert r.status() == 0             # the flag was cleared
+    # the debug view covers only the instances the buffers hold
+    dv = r.debug_view()
+    assert dv["n_instances"] == I // 2 and dv["instance_prims"].numel() == I // 2
+    assert r.debug_records()["records"].shape[0] <= I // 2
     # enough capacity: a no-sync forward on the same handle renders exactly
     r.reserve(I, s.camera.grid[0] * s.camera.grid[1])
     r.forward(run["ctx"], no_sync=True)
@@ -162,3 +166,75 @@ def test_reserve_that_grows_drops_forward_state(hip):
                                          torch.from_numpy(_grad_image(s)).cuda())
     with pytest.raises(RuntimeError, match="without a preceding forward"):
         run["r"].backward(run["ctx"])
+
+
+def test_no_sync_train_step_capacity_check_raises_and_regrows(hip):
+    """A TrainStep whose scene grows past the reserved instance capacity
+    (larger Gaussians, as after densification) raises at its next capacity
+    check, and the step after that runs with room for the new count."""
+    import torch
+    from tinygs_amd.train import TrainStep
+    s = scenes.config2(seed=13, n=8000, width=256, height=192)
+    ts = TrainStep(s, l1_weight=0.8, ssim_weight=0.2, eps=1e-15, no_sync=True, check_interval=1)
+    print("[no-sync] capacity check: two steps", flush=True)
+    ts.step()          # waits once: sizes and reserves the capacity
+    ts.step()          # no-sync from here on
+    ts.check_status()
+    before = ts._capacity[0]
+    with torch.no_grad():
+        ts.gaussians.scales().add_(1.5)   # every Gaussian 4.5x larger: several times the instances
+    ts.step()          # checks the earlier steps (fine), then overflows
+    with pytest.raises(RuntimeError, match="outgrew its instance capacity"):
+        ts.step()
+    assert ts._capacity[0] > before
+    ts.step()          # reserves the new capacity first
+    ts.check_status()
+
+
+def test_binning_scan_give_up_reported_by_its_forward(hip, orc):
+    """A look-back wait of the binning that gives up is reported by the call
+    that queued it. The give-up is forced from the host (spin bound 0: each
+    look-back with a predecessor stops at once and sets the flag, so every
+    kernel still runs to its end; the emission and the blend then skip their
+    work). The waiting forward fails and the backward after it is refused; a
+    no-sync forward's failure is reported once by status(); with the bound
+    restored the same handle renders like the oracle."""
+    import torch
+    from tinygs_amd import _lib
+    from tinygs_amd.core import GPUBatchInput, GPUGaussian3d, Image, RasterizeContext
+    from tinygs_amd.rasterizer import create_rasterizer
+    s = scenes.config2(seed=14, n=50000, width=320, height=240)   # several scan workgroups per pass
+    pre, bins, fwd = orc.render(s, "f")
+    g = GPUGaussian3d.from_scene(s)
+    r = create_rasterizer("fastgs")
+    r.set_gaussians(g)
+    ctx = RasterizeContext()
+    ctx.fwd_input = GPUBatchInput.from_camera(s.camera)
+    ctx.fwd_output.image = Image.empty(s.camera.shape)
+    ctx.gaussians_grad = g.gradient_like()
+    ctx.grad_output.image = Image(s.camera.shape, "float32", torch.from_numpy(_grad_image(s)).cuda())
+    L = _lib.load()
+    torch.cuda.synchronize()
+    print("[give-up] waiting forward with the look-back bound at 0", flush=True)
+    _lib.check(L.tgs_selftest_lookback_spins(0), "spins")
+    try:
+        with pytest.raises(RuntimeError, match="binning failed on the device"):
+            r.forward(ctx)
+        torch.cuda.synchronize()
+        with pytest.raises(RuntimeError, match="without a preceding forward"):
+            r.backward(ctx)
+        print("[give-up] no-sync forward with the look-back bound at 0", flush=True)
+        r.reserve(bins["n_instances"] + 1000, s.camera.grid[0] * s.camera.grid[1])
+        r.forward(ctx, no_sync=True)
+        with pytest.raises(RuntimeError, match="binning failed on the device"):
+            r.status()
+        assert r.status() == 0   # reported once
+    finally:
+        torch.cuda.synchronize()
+        _lib.check(L.tgs_selftest_lookback_spins(0xFFFFFFFF), "spins")
+    print("[give-up] bound restored", flush=True)
+    r.forward(ctx)
+    torch.cuda.synchronize()
+    img = ctx.fwd_output.image.data.cpu().numpy()
+    assert np.array_equal(img.view(np.uint32), fwd["image"].astype(np.float32).view(np.uint32))
+    r.backward(ctx)

@@ -73,3 +73,18 @@ def test_captured_step_replays_match_eager_steps(hip, image_dtype, overlap):
     graphed.check_status()
     assert graphed.optimizer.device_steps(s) == 6
     assert eager.optimizer.device_steps(s) == 6
+    # the replays advanced only the device count: the host count follows it,
+    # and a host-counted step after them continues at step 7 in both twins
+    assert graphed.optimizer.global_steps() == 6 and eager.optimizer.global_steps() == 6
+    with torch.cuda.stream(s):
+        for ts in (eager, graphed):
+            ts.zero()
+            ts.forward()
+            ts.losses_and_grad()
+            ts.backward()
+            ts.optimizer.step(1.0 / ts.grad_scaler, s, row_mask=ts.rasterizer.grad_row_mask(), device_step=False)
+    s.synchronize()
+    a, b = _state(eager), _state(graphed)
+    for k in a:
+        assert np.array_equal(_bits(a[k]), _bits(b[k])), ("host step", k)
+    assert graphed.optimizer.global_steps() == 7 and eager.optimizer.global_steps() == 7

@@ -108,3 +108,27 @@ def test_psnr_closed_form(hip, wh):
     want = -10.0 * np.log10((d * d).sum() / shape.size())
     assert abs(got - want) < 1e-4 * max(1.0, abs(want)), (got, want)
     assert PsnrMetric().evaluate(b, b) == 100.0
+
+
+@pytest.mark.parametrize("wh", [(64, 48), (101, 67)])
+def test_psnr_float16_closed_form(hip, wh):
+    """tgs_psnr on half images (psnr.cu:38-70, 72-128): each half widened to
+    float, saturate(pred) - target squared in float, summed over the padded
+    elements and divided by W H C; against the same in double precision."""
+    import torch
+    from tinygs_amd.core import DataType, Image
+    from tinygs_amd.image import ImageShape
+    from tinygs_amd.trainer import PsnrMetric
+    shape = ImageShape(*wh)
+    g = np.random.default_rng(wh[1])
+    pred = g.uniform(-0.3, 1.3, shape.padded_size).astype(np.float16)
+    target = g.uniform(0.0, 1.0, shape.padded_size).astype(np.float16)
+    a = Image(shape, DataType.Float16, torch.from_numpy(pred).cuda())
+    b = Image(shape, DataType.Float16, torch.from_numpy(target).cuda())
+    got = PsnrMetric().evaluate(a, b)
+    d = np.clip(pred.astype(np.float64), 0.0, 1.0) - target.astype(np.float64)
+    want = -10.0 * np.log10((d * d).sum() / shape.size())
+    assert abs(got - want) < 1e-4 * max(1.0, abs(want)), (got, want)
+    assert PsnrMetric().evaluate(b, b) == 100.0
+    with pytest.raises(RuntimeError):
+        PsnrMetric().evaluate(a, Image(shape, DataType.Float32, torch.zeros(shape.padded_size).cuda()))

@@ -122,6 +122,8 @@ SIGNATURES = {
     "tgs_adam_reset_rows": ([P, P, C.c_int64, P], C.c_int),
     "tgs_adam_reorder": ([P, P, P], C.c_int),
     "tgs_gaussians_reorder": ([C.POINTER(tgs_gaussians), P, P], C.c_int),
+    "tgs_morton_order": ([P, C.c_int64, P, P], C.c_int),
+    "tgs_densification_reorder": ([P, P, P, C.c_int64, P], C.c_int),
     "tgs_pcg32_seed": ([C.POINTER(tgs_pcg32), C.c_uint64, C.c_uint64], None),
     "tgs_pcg32_next_uint": ([C.POINTER(tgs_pcg32), C.c_uint32], C.c_uint32),
     "tgs_psnr": ([C.POINTER(tgs_loss_context), C.POINTER(C.c_float), P], C.c_int),
@@ -150,6 +152,7 @@ SIGNATURES = {
     "tgs_selftest_wave": ([P, P, P], C.c_int),
     "tgs_selftest_half": ([C.c_int32, P, P, P, P, C.c_int64, P], C.c_int),
     "tgs_selftest_half_div_exhaustive": ([P, P], C.c_int),
+    "tgs_selftest_lookback_spins": ([C.c_uint32], C.c_int),
     "tgs_adam_step_ex": ([P, C.c_float, P, C.c_int32, P], C.c_int),
     "tgs_adam_device_steps": ([P, C.POINTER(C.c_int64), P], C.c_int),
 }

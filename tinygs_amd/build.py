@@ -18,7 +18,7 @@ CSRC = os.path.join(HERE, "csrc")
 OUT_DIR = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libtinygs_amd.so")
 SOURCES = ["preprocess.hip", "binning.hip", "blend_forward.hip", "blend_backward.hip", "fgs16.hip",
-           "preprocess_backward.hip", "loss.hip", "adam.hip", "strategy.hip", "formats.hip", "selftest.hip", "capi.hip"]
+           "preprocess_backward.hip", "loss.hip", "adam.hip", "strategy.hip", "morton.hip", "formats.hip", "selftest.hip", "capi.hip"]
 ARCH = os.environ.get("TGS_OFFLOAD_ARCH", "gfx950")
 
 COMMON_FLAGS = [

@@ -97,6 +97,16 @@ class GPUGaussian3d:
 
     memset_async = memset
 
+    def zero_(self, stream=None):
+        """memset_async(0) ordered on `stream` (the caller's gradient zeroing
+        at the start of an accumulation cycle, orchestrator.cu:351-353)."""
+        torch = _torch()
+        if stream is None:
+            self.memset(0)
+            return
+        with torch.cuda.stream(stream):
+            self.memset(0)
+
     def clone(self) -> "GPUGaussian3d":
         g = GPUGaussian3d.__new__(GPUGaussian3d)
         for name in ("m_means", "m_scales", "m_rotations", "m_opacities", "m_sh_coefficient_0",

@@ -74,6 +74,9 @@ constexpr uint64_t kFlagMask = 3ull << 62;
 constexpr uint64_t kFlagAggregate = 1ull << 62;
 constexpr uint64_t kFlagPrefix = 2ull << 62;
 constexpr uint32_t kSpinLimit = 1u << 22;
+// The bound in force (tgs_selftest_lookback_spins changes it for tests of
+// the error path; 0 gives up at once wherever a predecessor must be read).
+__device__ uint32_t g_lookback_spins = kSpinLimit;
 
 __device__ __forceinline__ uint64_t status_word(uint64_t flag, uint32_t epoch, uint32_t value) {
     return flag | ((uint64_t)(epoch & kEpochMask) << 32) | (uint64_t)value;
@@ -105,9 +108,14 @@ __device__ uint32_t wave_look_back(uint64_t* status, uint32_t bid, uint32_t tota
     if (lane == 0) store_status(status + bid, status_word(bid == 0 ? kFlagPrefix : kFlagAggregate, epoch, total));
     if (bid == 0) return 0;
     const uint32_t ep = epoch & kEpochMask;
+    const uint32_t spin_limit = g_lookback_spins;
     uint32_t excl = 0, spins = 0;
     int64_t j = (int64_t)bid - 1;
     while (true) {
+        if (spin_limit == 0u) {   // (tests: the bounded wait gives up at once)
+            if (lane == 0) atomicOr(err, kErrLookBack);
+            break;
+        }
         const int64_t src = j - (int64_t)lane;
         const uint64_t v = src >= 0 ? load_status(status + src) : kFlagPrefix;   // before ticket 0: prefix 0
         const uint64_t fl = v & kFlagMask;
@@ -122,7 +130,7 @@ __device__ uint32_t wave_look_back(uint64_t* status, uint32_t bid, uint32_t tota
             j -= 64;
             continue;
         }
-        if (++spins > kSpinLimit) {
+        if (++spins > spin_limit) {
             if (lane == 0) atomicOr(err, kErrLookBack);
             break;
         }
@@ -709,6 +717,9 @@ __global__ void __launch_bounds__(256) emit_kernel(const uint32_t* __restrict__ 
     const int64_t n = min((int64_t)ctl->V, max_count);
     const int64_t k0 = (int64_t)blockIdx.x * blockDim.x;
     if (k0 >= n) return;
+    // a failed look-back scan of the depth sort (set before this launch, so
+    // the same for every thread) leaves a partial order: nothing is emitted
+    if (ctl->err & kErrLookBack) return;
     const uint32_t range_a = offs[k0], range_b = offs[min(k0 + (int64_t)blockDim.x, n)];
     // Slots come from the offsets scan and stay below the instance count the
     // buffers were sized for; a slot beyond it (offsets broken by a failed
@@ -914,6 +925,10 @@ void launch_capacity_check(BinCtl* ctl, int64_t cap, hipStream_t s) { capacity_c
 
 void launch_clear_err_bits(BinCtl* ctl, uint32_t bits, hipStream_t s) {
     clear_err_bits_kernel<<<1, 64, 0, s>>>(ctl, bits);
+}
+
+int set_lookback_spin_limit(uint32_t spins) {
+    return hipMemcpyToSymbol(HIP_SYMBOL(g_lookback_spins), &spins, sizeof(spins)) == hipSuccess ? 0 : -1;
 }
 
 bool radix_digits_fit(bool depth, int n_passes, const int* bits) {

@@ -234,12 +234,13 @@ struct tgs_rasterizer {
     DevBuf block_n;        // visible primitives per compaction block (the depth sort's first-pass blocks)
     DevBuf bin_ctl;     // BinCtl (zeroed at creation; all but err cleared every forward)
     hipEvent_t ev_counts = nullptr;   // recorded after the counts copy of a forward
+    hipEvent_t ev_err = nullptr;      // recorded after the error-word copy that follows the tile sort
     DevBuf lb_status;   // look-back status words (u64), epoch-tagged
     // look-back launches of the current forward so far: its k-th launch uses
     // epoch BinCtl::epoch_base + k (the base advances on the device per forward)
     uint32_t epoch = 0;
     uint64_t forwards = 0;   // forwards queued by this host (eager; graph replays not counted)
-    uint32_t* h_counters = nullptr;   // pinned copy of BinCtl {V, I, err}
+    uint32_t* h_counters = nullptr;   // pinned copy of BinCtl {V, I, err}; [4]: err after the tile sort
     // state of the last forward
     bool fwd_done = false;
     bool ikeys_from_ranges = false;   // the sorted tile keys exist only as the tile ranges
@@ -318,10 +319,12 @@ int tgs_rasterizer_create(const char* type, tgs_rasterizer** out) {
         e = hipMemset(r->bin_ctl.p, 0, sizeof(BinCtl));
     }
     if (e == hipSuccess) e = hipEventCreateWithFlags(&r->ev_counts, hipEventDisableTiming);
+    if (e == hipSuccess) e = hipEventCreateWithFlags(&r->ev_err, hipEventDisableTiming);
     if (e == hipSuccess) e = hipDeviceSynchronize();
     if (e != hipSuccess) {
         if (r->h_counters) (void)hipHostFree(r->h_counters);
         if (r->ev_counts) (void)hipEventDestroy(r->ev_counts);
+        if (r->ev_err) (void)hipEventDestroy(r->ev_err);
         release(r->bin_ctl);
         delete r;
         return fail(TGS_ERR_HIP, "rasterizer allocation: %s", hipGetErrorString(e));
@@ -343,6 +346,7 @@ int tgs_rasterizer_destroy(tgs_rasterizer* r) {
     for (DevBuf* b : all) release(*b);
     if (r->h_counters) (void)hipHostFree(r->h_counters);
     if (r->ev_counts) (void)hipEventDestroy(r->ev_counts);
+    if (r->ev_err) (void)hipEventDestroy(r->ev_err);
     delete r;
     return TGS_OK;
 }
@@ -516,8 +520,10 @@ static int rasterizer_forward(tgs_rasterizer* r, const tgs_camera* camera, void*
     if (!nosync) {
         TGS_HIP(hipEventSynchronize(r->ev_counts));
         // (a capacity flag left by an earlier no-sync forward does not concern this one)
-        if (r->h_counters[2] & ~kErrCapacity)
-            return fail(TGS_ERR_STATE, "binning failed on the device (error flags 0x%x)", r->h_counters[2]);
+        if (const uint32_t bad = r->h_counters[2] & ~kErrCapacity) {
+            launch_clear_err_bits(ctl, bad, s);   // reported once
+            return fail(TGS_ERR_STATE, "binning failed on the device (error flags 0x%x)", bad);
+        }
         V = r->h_counters[0];
         I = r->h_counters[1];
         cap = I;
@@ -555,6 +561,14 @@ static int rasterizer_forward(tgs_rasterizer* r, const tgs_camera* camera, void*
         r->tile_sort_cap = cap;
     }
     if (nosync) launch_capacity_check(ctl, cap, s);
+    if (!nosync) {
+        // the depth and tile sorts' look-back scans and the emission's offset
+        // check ran after the counts copy: their error word, read once the
+        // blend below is queued (the blend and the emission skip their work
+        // when it is set, so a failed scan's partial output is never read)
+        TGS_HIP(hipMemcpyAsync(r->h_counters + 4, &ctl->err, sizeof(uint32_t), hipMemcpyDeviceToHost, s));
+        TGS_HIP(hipEventRecord(r->ev_err, s));
+    }
     {
         StageScope sc(ST_BLENDF, s);
         if (f16)
@@ -568,6 +582,13 @@ static int rasterizer_forward(tgs_rasterizer* r, const tgs_camera* camera, void*
                                  r->tile_loaded.as<uint32_t>(), r->ckpt.as<float4>(), r->items.as<uint4>(), ctl, s);
     }
     TGS_CHECK_LAUNCH();
+    if (!nosync) {
+        TGS_HIP(hipEventSynchronize(r->ev_err));
+        if (const uint32_t bad = r->h_counters[4] & ~kErrCapacity) {
+            launch_clear_err_bits(ctl, bad, s);   // reported once
+            return fail(TGS_ERR_STATE, "binning failed on the device (error flags 0x%x)", bad);
+        }
+    }
     r->cam = cam;
     r->n = n;
     r->V = V;
@@ -624,7 +645,11 @@ int tgs_rasterizer_status(tgs_rasterizer* r, int32_t clear_capacity_flag, void* 
         TGS_CHECK_LAUNCH();
         return fail(TGS_ERR_CAPACITY, "forward needed %u instances, %lld reserved", w[1], (long long)r->inst_cap);
     }
-    if (w[2]) return fail(TGS_ERR_STATE, "binning failed on the device (error flags 0x%x)", w[2]);
+    if (w[2]) {
+        launch_clear_err_bits(r->bin_ctl.as<BinCtl>(), w[2], s);   // reported once
+        TGS_CHECK_LAUNCH();
+        return fail(TGS_ERR_STATE, "binning failed on the device (error flags 0x%x)", w[2]);
+    }
     return TGS_OK;
 }
 
@@ -785,7 +810,10 @@ int tgs_rasterizer_debug_view(tgs_rasterizer* r, tgs_debug_view* out) {
     // the summed 2D gradients exist only after a TGS_BACKWARD_KEEP_2D backward
     out->grad2d = r->grad2d_valid ? r->grad2d.as<float>() : nullptr;
     out->n_visible = r->V;
-    out->n_instances = r->I;
+    // a no-sync forward past its capacity counted more instances than its
+    // buffers hold; the view covers the ones the tile sort kept (the true
+    // count stays with tgs_rasterizer_counts)
+    out->n_instances = std::min<int64_t>(r->I, r->tile_sort_cap);
     out->n_tiles = (int64_t)r->cam.grid_w * r->cam.grid_h;
     out->image_dtype = r->fgs16 ? TGS_DTYPE_FLOAT16 : TGS_DTYPE_FLOAT32;
     out->first_slot = r->first_slot.as<uint32_t>();
@@ -913,13 +941,18 @@ int tgs_loss_l1_ssim(tgs_loss* l, const tgs_loss_context* c, float l1_scale, flo
 
 int tgs_psnr(const tgs_loss_context* c, float* psnr, void* stream) {
     if (!c || !psnr || !c->pred || !c->target) return fail(TGS_ERR_INVALID, "NULL argument");
-    if (c->dtype != TGS_DTYPE_FLOAT32) return fail(TGS_ERR_UNSUPPORTED, "PSNR: float32 images only");
+    // psnr.cu:72-128: float32 and float16 images
+    if (c->dtype != TGS_DTYPE_FLOAT32 && c->dtype != TGS_DTYPE_FLOAT16)
+        return fail(TGS_ERR_UNSUPPORTED, "PSNR: float32 or float16 images only");
     if (c->width == 0 || c->height == 0 || c->channel == 0) return fail(TGS_ERR_INVALID, "empty image");
     hipStream_t s = (hipStream_t)stream;
     static thread_local DevBuf scratch;
     TGS_TRY(ensure(scratch, sizeof(double) * (size_t)psnr_scratch_doubles(), s));
     const int64_t npad = (int64_t)((c->width + 7u) / 8u) * ((c->height + 7u) / 8u) * 64 * c->channel;
-    launch_sq_diff_sum((const float*)c->pred, (const float*)c->target, npad, scratch.as<double>(), s);
+    if (c->dtype == TGS_DTYPE_FLOAT16)
+        launch_sq_diff_sum_f16(c->pred, c->target, npad, scratch.as<double>(), s);
+    else
+        launch_sq_diff_sum((const float*)c->pred, (const float*)c->target, npad, scratch.as<double>(), s);
     TGS_CHECK_LAUNCH();
     double sum = 0.0;
     TGS_HIP(hipMemcpyAsync(&sum, scratch.as<double>() + psnr_scratch_doubles() - 1, sizeof(double),
@@ -1030,6 +1063,16 @@ int tgs_adam_step_masked(tgs_adam* a, float scale, const uint8_t* row_mask, void
     return tgs_adam_step_ex(a, scale, row_mask, 0, stream);
 }
 
+// The device-step count (TGS_ADAM_DEVICE_STEP) becomes the host's: graph
+// replays advance only the device count. Waits for the stream.
+static int adam_sync_steps(tgs_adam* a, hipStream_t s) {
+    uint32_t w = 0;
+    TGS_HIP(hipMemcpyAsync(&w, a->dev_state.p, sizeof(w), hipMemcpyDeviceToHost, s));
+    TGS_HIP(hipStreamSynchronize(s));
+    a->steps = w;
+    return TGS_OK;
+}
+
 int tgs_adam_step_ex(tgs_adam* a, float scale, const uint8_t* row_mask, int32_t flags, void* stream) {
     if (!a) return fail(TGS_ERR_INVALID, "NULL argument");
     if (flags & ~(TGS_ADAM_DEVICE_STEP | TGS_ADAM_ROWS_UNMARKED | TGS_ADAM_ROWS_MARKED | TGS_ADAM_SAME_STEP))
@@ -1044,6 +1087,9 @@ int tgs_adam_step_ex(tgs_adam* a, float scale, const uint8_t* row_mask, int32_t 
     if (same && (a->steps == 0 || dev != a->last_dev || (dev && !a->dev_seeded)))
         return fail(TGS_ERR_STATE, "TGS_ADAM_SAME_STEP needs a step of the same mode before it");
     hipStream_t hs = (hipStream_t)stream;
+    // graph replays advance only the device count: a host-counted step after
+    // device steps continues from it (one wait on the stream)
+    if (!dev && a->dev_seeded) TGS_TRY(adam_sync_steps(a, hs));
     if (dev && !same) {
         TGS_TRY(ensure(a->dev_state, 16, hs));
         if (!a->dev_seeded) {   // the device count starts from the host's
@@ -1120,20 +1166,17 @@ int tgs_adam_reset(tgs_adam* a, void* stream) {
     return TGS_OK;
 }
 
-int64_t tgs_adam_global_steps(tgs_adam* a) { return a ? a->steps : -1; }
+int64_t tgs_adam_global_steps(tgs_adam* a) {
+    if (!a) return -1;
+    // device steps may have run (graph replays) that the host did not count
+    if (a->dev_seeded && (hipDeviceSynchronize() != hipSuccess || adam_sync_steps(a, nullptr) != TGS_OK)) return -1;
+    return a->steps;
+}
 
 int tgs_adam_device_steps(tgs_adam* a, int64_t* steps, void* stream) {
     if (!a || !steps) return fail(TGS_ERR_INVALID, "NULL argument");
-    if (!a->dev_seeded) {
-        *steps = a->steps;
-        return TGS_OK;
-    }
-    uint32_t w = 0;
-    hipStream_t s = (hipStream_t)stream;
-    TGS_HIP(hipMemcpyAsync(&w, a->dev_state.p, sizeof(w), hipMemcpyDeviceToHost, s));
-    TGS_HIP(hipStreamSynchronize(s));
-    a->steps = w;   // graph replays advance the device count only
-    *steps = w;
+    if (a->dev_seeded) TGS_TRY(adam_sync_steps(a, (hipStream_t)stream));
+    *steps = a->steps;
     return TGS_OK;
 }
 
@@ -1411,6 +1454,52 @@ int tgs_gaussians_reorder(const tgs_gaussians* g, const uint32_t* indices, void*
     return TGS_OK;
 }
 
+int tgs_morton_order(const float* means, int64_t n, uint32_t* indices, void* stream) {
+    if (n < 0 || (n > 0 && (!means || !indices))) return fail(TGS_ERR_INVALID, "bad argument");
+    if (n > (int64_t)0x7fffffff) return fail(TGS_ERR_UNSUPPORTED, "Morton order of more than 2^31 - 1 means");
+    if (n == 0) return TGS_OK;
+    hipStream_t s = (hipStream_t)stream;
+    DevBuf scratch, status, ctl;
+    int rc = TGS_OK;
+    const int64_t st_entries = scan_status_entries(radix_count_entries(n, true));
+    if ((rc = ensure(scratch, sizeof(uint32_t) * (size_t)morton_scratch_words(n), s)) == TGS_OK &&
+        (rc = ensure(status, sizeof(uint64_t) * (size_t)std::max<int64_t>(st_entries, 1), s)) == TGS_OK &&
+        (rc = ensure(ctl, sizeof(BinCtl), s)) == TGS_OK) {
+        // zero status words (not published) and a zero control block (tickets, epoch base, error)
+        launch_fill_u32(status.as<uint32_t>(), 0u, (int64_t)(status.bytes / 4), s);
+        launch_fill_u32(ctl.as<uint32_t>(), 0u, (int64_t)(sizeof(BinCtl) / 4), s);
+        if (morton_order(means, n, indices, scratch.as<uint32_t>(), status.as<uint64_t>(), ctl.as<BinCtl>(), s) != 0)
+            rc = fail(TGS_ERR_STATE, "Morton order: radix digit plan");
+        uint32_t err = 0;
+        hipError_t e = hipGetLastError();
+        if (e == hipSuccess) e = hipMemcpyAsync(&err, (const char*)ctl.p + offsetof(BinCtl, err), sizeof(err),
+                                                hipMemcpyDeviceToHost, s);
+        if (e == hipSuccess) e = hipStreamSynchronize(s);
+        if (e != hipSuccess)
+            rc = fail(TGS_ERR_HIP, "Morton order: %s", hipGetErrorString(e));
+        else if (rc == TGS_OK && err)
+            rc = fail(TGS_ERR_STATE, "Morton order: the sort failed on the device (error flags 0x%x)", err);
+    }
+    release(scratch);
+    release(status);
+    release(ctl);
+    return rc;
+}
+
+int tgs_densification_reorder(const void* info, void* out, const uint32_t* indices, int64_t n, void* stream) {
+    if (n < 0 || (n > 0 && (!info || !out || !indices))) return fail(TGS_ERR_INVALID, "bad argument");
+    if (n > (int64_t)0x7fffffff) return fail(TGS_ERR_UNSUPPORTED, "reorder of more than 2^31 - 1 rows");
+    if (info == out) return fail(TGS_ERR_INVALID, "densification reorder: out must not alias info");
+    if (n == 0) return TGS_OK;
+    hipStream_t s = (hipStream_t)stream;
+    bool ok = true;
+    TGS_TRY(indices_in_range((const int32_t*)indices, n, n, s, &ok));
+    if (!ok) return fail(TGS_ERR_INVALID, "densification reorder: an index is outside [0, %lld)", (long long)n);
+    launch_rows16_gather(info, out, indices, n, s);
+    TGS_CHECK_LAUNCH();
+    return TGS_OK;
+}
+
 int tgs_flags_compact(const uint8_t* flags, int64_t n, int32_t* out, int64_t* count, void* stream) {
     if (!count || n < 0 || (n > 0 && (!flags || !out))) return fail(TGS_ERR_INVALID, "bad argument");
     return compact_flags(flags, n, out, count, nullptr, (hipStream_t)stream);
@@ -1566,6 +1655,12 @@ int tgs_selftest_half_div_exhaustive(int64_t* out, void* stream) {
     launch_fill_u32((uint32_t*)out, 0u, 16, s);
     launch_half_div_check((unsigned long long*)out, s);
     TGS_CHECK_LAUNCH();
+    return TGS_OK;
+}
+
+int tgs_selftest_lookback_spins(uint32_t spins) {
+    if (set_lookback_spin_limit(spins == 0xffffffffu ? (1u << 22) : spins) != 0)
+        return fail(TGS_ERR_HIP, "look-back spin bound: %s", hipGetErrorString(hipGetLastError()));
     return TGS_OK;
 }
 

@@ -92,6 +92,9 @@ __global__ void __launch_bounds__(256) blend16_forward_kernel(
     }
 
     uint2 range = ranges[tile];
+    // a failed binning scan (reported by the host) leaves partial instance
+    // lists: every tile renders as empty instead of reading them
+    if (ctl->err & (kErrLookBack | kErrOffsets)) range = make_uint2(0u, 0u);
     if (range.y == 0u) {   // an empty tile, left as (UINT32_MAX, 0) by the tile sort: stored as (0, 0)
         range.x = 0u;
         if (lane == 0u) ranges[tile] = range;

@@ -154,8 +154,23 @@ void launch_keys_from_ranges(const uint2* ranges, uint32_t n_tiles, int64_t max_
                              hipStream_t s);
 void launch_tile_ranges(const uint32_t* inst_keys, const uint32_t* d_n, int64_t max_inst, uint2* ranges,
                         uint32_t n_tiles, hipStream_t s);
+// Sets the spin bound of every look-back wait on the current device (default
+// 2^22 polls; 0: give up at once). Returns 0, or -1 on a HIP error.
+int set_lookback_spin_limit(uint32_t spins);
 // Whether radix_sort accepts these digit widths (host check, before any launch).
 bool radix_digits_fit(bool depth, int n_passes, const int* bits);
+
+// ---- Morton order (orchestrator.cu:26-90)
+// u32 words of scratch morton_order needs for n means.
+int64_t morton_scratch_words(int64_t n);
+// indices[i] = the i-th mean in stable order of its 30-bit Morton code in the
+// means' bounding box. status: zeroed look-back words for a depth-class sort
+// of n keys; ctl: a zeroed control block (tickets, epoch base, error flag).
+// Returns -1 when the sort's digit plan is refused (nothing launched after).
+int morton_order(const float* means, int64_t n, uint32_t* indices, uint32_t* scratch, uint64_t* status,
+                 BinCtl* ctl, hipStream_t s);
+// dst[i] = src[indices[i]] for 16-byte rows (densification info).
+void launch_rows16_gather(const void* src, void* dst, const uint32_t* indices, int64_t n, hipStream_t s);
 
 // ---- fp16-image rasterizer (FGS16, tinygs/src/rasterizer/fastgs_ours_fp16/)
 // Preprocess: as launch_preprocess with the FGS16 rules; info[i] = (conic a | b
@@ -225,6 +240,7 @@ void launch_preprocess_backward(const GaussianView& g, const CamParams& cam, con
 // sum of (saturate(pred) - target)^2 over the n_padded elements
 int psnr_scratch_doubles();
 void launch_sq_diff_sum(const float* pred, const float* target, int64_t n_padded, double* scratch, hipStream_t s);
+void launch_sq_diff_sum_f16(const void* pred, const void* target, int64_t n_padded, double* scratch, hipStream_t s);
 
 // ---- densification (tinygs/src/strategy/default.cu, gpu_gaussian.cu:117-170,
 // simple_adam.cu:841-985)

@@ -550,6 +550,31 @@ __global__ void __launch_bounds__(256) sq_diff_partial_kernel(const float4* __re
     if (threadIdx.x == 0) partial[blockIdx.x] = (s_w[0] + s_w[1]) + (s_w[2] + s_w[3]);
 }
 
+// The same over half images (psnr.cu:38-70): each half widened to float
+// before saturate; 16-byte loads of 8 halves.
+__global__ void __launch_bounds__(256) sq_diff_partial_f16_kernel(const uint4* __restrict__ pred,
+                                                                   const uint4* __restrict__ target, int64_t n8,
+                                                                   double* __restrict__ partial) {
+    __shared__ double s_w[4];
+    double acc = 0.0;
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n8; i += (int64_t)gridDim.x * 256) {
+        const uint4 p = pred[i], t = target[i];
+        const uint32_t pw[4] = {p.x, p.y, p.z, p.w}, tw[4] = {t.x, t.y, t.z, t.w};
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const __half* ph = (const __half*)&pw[k];
+            const __half* th = (const __half*)&tw[k];
+            const float d0 = saturate(__half2float(ph[0])) - __half2float(th[0]);
+            const float d1 = saturate(__half2float(ph[1])) - __half2float(th[1]);
+            acc += (double)(d0 * d0) + (double)(d1 * d1);
+        }
+    }
+    for (int off = 32; off > 0; off >>= 1) acc += __shfl_down(acc, off, 64);
+    if ((threadIdx.x & 63u) == 0u) s_w[threadIdx.x >> 6] = acc;
+    __syncthreads();
+    if (threadIdx.x == 0) partial[blockIdx.x] = (s_w[0] + s_w[1]) + (s_w[2] + s_w[3]);
+}
+
 __global__ void __launch_bounds__(64) sum_partials_kernel(const double* __restrict__ partial, int n,
                                                           double* __restrict__ out) {
     double acc = 0.0;
@@ -565,6 +590,13 @@ void launch_sq_diff_sum(const float* pred, const float* target, int64_t n_padded
     const int64_t n4 = n_padded / 4;   // padded planes hold whole 8x8 blocks
     const int blocks = (int)std::min<int64_t>(kPsnrBlocks, std::max<int64_t>(1, (n4 + 255) / 256));
     sq_diff_partial_kernel<<<blocks, 256, 0, s>>>((const float4*)pred, (const float4*)target, n4, scratch);
+    sum_partials_kernel<<<1, 64, 0, s>>>(scratch, blocks, scratch + kPsnrBlocks);
+}
+
+void launch_sq_diff_sum_f16(const void* pred, const void* target, int64_t n_padded, double* scratch, hipStream_t s) {
+    const int64_t n8 = n_padded / 8;   // padded planes hold whole 8x8 blocks
+    const int blocks = (int)std::min<int64_t>(kPsnrBlocks, std::max<int64_t>(1, (n8 + 255) / 256));
+    sq_diff_partial_f16_kernel<<<blocks, 256, 0, s>>>((const uint4*)pred, (const uint4*)target, n8, scratch);
     sum_partials_kernel<<<1, 64, 0, s>>>(scratch, blocks, scratch + kPsnrBlocks);
 }
 

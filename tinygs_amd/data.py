@@ -16,7 +16,7 @@ import dataclasses
 import numpy as np
 
 from . import _lib
-from .core import GPUBatchInput, GPUGaussian3d, Image, RasterizeContext
+from .core import DataType, GPUBatchInput, GPUGaussian3d, Image, RasterizeContext
 from .rasterizer import create_rasterizer
 
 
@@ -37,25 +37,37 @@ def gaussians_from_arrays(p: dict, sh_degree: int = 3, device: str = "cuda") -> 
 @dataclasses.dataclass
 class View:
     camera: object      # scenes.Camera
-    target: Image       # device image, 8x8-tiled float32
+    target: Image       # device image, 8x8-tiled, of the dataset's data type
 
 
 class SyntheticViewDataset:
     """DatasetBase over synthetic views: camera i and its target, the render
-    of the ground-truth Gaussians (SH degree 3) from camera i."""
+    of the ground-truth Gaussians (SH degree 3) from camera i. data_type is
+    the dataset's image type (the reference's "data_type", e.g.
+    configs/default.json:4): float16 targets are the float32 renders
+    rounded to nearest half on the device (float_to_half_gpu,
+    image_format.cu:117-139)."""
 
-    def __init__(self, scene, device: str = "cuda"):
+    def __init__(self, scene, device: str = "cuda", data_type: str = DataType.Float32):
         import torch
         gt = gaussians_from_arrays(scene.gt, 3, device)
         r = create_rasterizer("fastgs")
         r.set_gaussians(gt)
         self.views = []
+        self.data_type = data_type
         for cam in scene.cameras:
             ctx = RasterizeContext()
             ctx.fwd_input = GPUBatchInput.from_camera(cam)
             ctx.fwd_output.image = Image.empty(cam.shape, device)
             r.forward(ctx)
-            self.views.append(View(cam, ctx.fwd_output.image))
+            target = ctx.fwd_output.image
+            if data_type == DataType.Float16:
+                half = Image.empty(cam.shape, device, DataType.Float16)
+                _lib.check(_lib.load().tgs_convert(target.data.data_ptr(), _lib.TGS_DTYPE_FLOAT32,
+                                                   half.data.data_ptr(), _lib.TGS_DTYPE_FLOAT16,
+                                                   target.data.numel(), None), "float_to_half")
+                target = half
+            self.views.append(View(cam, target))
         torch.cuda.synchronize()
         self.width, self.height = scene.width, scene.height
 

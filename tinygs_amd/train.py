@@ -21,7 +21,10 @@ ones do not wait at all (TGS_FORWARD_NO_SYNC), and Adam keeps its step count
 on the device (TGS_ADAM_DEVICE_STEP): from the second step on, a step is the
 same launch sequence every time and can be captured into a HIP graph
 (capture_step) and replayed; check_status() reports a forward that outgrew
-the capacity.
+the capacity and reserves room for the next forward. step() checks it every
+check_interval eager steps (a wait for the device then), so a scene that grew
+(more instances after densification or new parameters) fails loudly instead
+of training on partial images.
 """
 from __future__ import annotations
 
@@ -35,7 +38,8 @@ class TrainStep:
     def __init__(self, scene, l1_weight: float = 0.8, ssim_weight: float = 0.2, grad_scaler: float = 1.0,
                  eps: float = 1e-15, shs_lr: float | None = None, means_lr: float | None = None,
                  max_grad_1: float | None = None, device: str = "cuda", stream=None, sparse_grads: bool = True,
-                 no_sync: bool = False, image_dtype: str = DataType.Float32, overlap_adam: bool = False):
+                 no_sync: bool = False, image_dtype: str = DataType.Float32, overlap_adam: bool = False,
+                 check_interval: int = 64):
         """image_dtype: float32, or float16 for the fp16-image rasterizer
         (fastgs.cu:143-188) with the fp16 losses; the target is rounded to half.
         overlap_adam (needs sparse_grads): Adam updates the rows without
@@ -48,6 +52,8 @@ class TrainStep:
         self.no_sync = bool(no_sync)
         self._capacity = None   # (instances, tiles) reserved for the no-sync forwards
         self._reserved = False
+        self.check_interval = int(check_interval)   # no_sync: eager steps between capacity checks (0: never)
+        self._eager_steps = 0
         # sparse_grads: the backward writes only gradient rows that received a
         # gradient and Adam reads only those (the others are zero); same
         # parameters as assigning every row, without moving the zero rows
@@ -124,10 +130,15 @@ class TrainStep:
 
     def check_status(self):
         """Waits for the queued steps; raises when a no-sync forward needed
-        more instances than reserved (its image and gradients are then partial)."""
+        more instances than reserved (its image and gradients are then partial),
+        after reserving room (1.25x the count it needed) for the next forward."""
         from . import _lib
         if self.rasterizer.status(clear_capacity_flag=True, stream=self.stream) == _lib.TGS_ERR_CAPACITY:
-            raise RuntimeError("a no-sync forward outgrew its instance capacity")
+            _, inst, tiles = self.rasterizer.counts()
+            self._capacity = (inst + inst // 4 + 4096, tiles)
+            self._reserved = False   # the next forward reserves the new capacity first
+            raise RuntimeError(f"a no-sync forward outgrew its instance capacity ({inst} instances needed); "
+                               "the capacity was raised for the next step")
 
     def losses_and_grad(self):
         if self.fused_losses:
@@ -175,6 +186,12 @@ class TrainStep:
                             same_step=True)
 
     def step(self):
+        if self.no_sync and self.check_interval > 0 and self._reserved:
+            import torch
+            if not torch.cuda.is_current_stream_capturing():
+                self._eager_steps += 1
+                if self._eager_steps % self.check_interval == 0:
+                    self.check_status()
         self.zero()
         self.forward()
         if self.overlap_adam:
