@@ -154,6 +154,9 @@ int tgs_rasterizer_backward(tgs_rasterizer* r, const void* grad_image, const voi
  * without a gradient. For parity tests of the blend backward on its own; no
  * counterpart in the reference. */
 #define TGS_BACKWARD_KEEP_2D 8
+/* (fp32 images: the 12th float of each grad2d row then carries, as bits, the
+ * primitive's mask word of written records of ranks 0..31; see
+ * tgs_debug_view.record_bits) */
 int tgs_rasterizer_backward_ex(tgs_rasterizer* r, const void* grad_image, const void* image,
                                const tgs_gaussians* grads, void* densification_info, int32_t flags, void* stream);
 /* Device byte mask [n] of the last TGS_BACKWARD_SPARSE backward (1: row
@@ -204,10 +207,20 @@ typedef struct tgs_debug_view {
                                            halves as floats; color the words a | b << 16,
                                            c | opacity << 16, r | g << 8 | b << 16 (bytes), 0 */
     const uint32_t* first_slot;         /* [n] first 2D-gradient record slot of each visible primitive */
-    const float* records;               /* [12 * n_instances] 2D-gradient records of the last backward:
-                                           per primitive, the buckets that reached it fill the slots
+    const float* records;               /* [12 * n_instances] 2D-gradient records of the last backward.
+                                           fp32 images: the record of the instance of rank k among
+                                           primitive p's instances (instance_ranks) sits at slot
+                                           first_slot[p] + k; for k < 32 its mark is bit k of p's mask
+                                           word (grad2d[12 p + 11] after a TGS_BACKWARD_KEEP_2D
+                                           backward), for k >= 32 bit first_slot[p] + k of record_bits.
+                                           FGS16: the buckets that reached p fill
                                            first_slot[p], first_slot[p] + 1, ... in completion order
-                                           (FGS16: [11] holds the instance index's bits) */
+                                           ([11] holds the instance index's bits) */
+    const uint16_t* instance_ranks;     /* [n_instances] fp32 images: each sorted instance's rank
+                                           among its primitive's instances (in tile order); else NULL */
+    const uint32_t* record_bits;        /* [ceil(n_instances / 32)] fp32 images: one bit per record
+                                           slot, set for the records of rank >= 32 the last backward
+                                           wrote; else NULL */
 } tgs_debug_view;
 int tgs_rasterizer_debug_view(tgs_rasterizer* r, tgs_debug_view* out);
 

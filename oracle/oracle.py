@@ -61,7 +61,7 @@ def _declare(L):
         fn.restype = None
         fn = getattr(L, pfx + "blend_backward")
         fn.argtypes = [C.c_int, C.c_int, u32p, u32p, rp, rp, rp, rp, rp, u32p, u32p, u32p, rp,
-                       rp, rp, rp, rp, rp, C.c_int]
+                       rp, rp, rp, rp, rp, C.c_int, C.c_int64, C.c_void_p]
         fn.restype = None
         fn = getattr(L, pfx + "preprocess_backward")
         fn.argtypes = [C.c_int64, rp, rp, rp, rp, C.c_int, rp, u32p, rp, rp, rp, rp,
@@ -242,18 +242,33 @@ def _u32(a):
     return np.ascontiguousarray(a if a.size else np.zeros(1, np.uint32), dtype=np.uint32)
 
 
-def blend_backward(scene, pre, bins, fwd, grad_image, prec="f", exact_grad=False):
+def first_slots(pre, bins) -> np.ndarray:
+    """Each visible primitive's first instance slot: the exclusive scan of
+    n_touched in depth order (the emission's offsets)."""
+    n = pre["n_touched"].size
+    fs = np.zeros(max(n, 1), np.uint32)
+    order = np.asarray(bins["sorted_prims"], np.int64)
+    nt = pre["n_touched"].astype(np.int64)[order]
+    fs[order] = (np.cumsum(nt) - nt).astype(np.uint32)
+    return fs
+
+
+def blend_backward(scene, pre, bins, fwd, grad_image, prec="f", exact_grad=False, library_order=True):
+    """library_order: each primitive's records summed in the library's fixed
+    order (rank order up to 16 records, the 16-lane split by 8-slot bytes
+    and xor butterfly above); otherwise in instance order."""
     L = lib()
     dt = _dt(prec)
     n = scene.n
     cam = scene.camera
     g = {k: np.zeros(m * n, dt) for k, m in
          (("grad_mean2d", 2), ("absgrad", 2), ("grad_conic", 3), ("grad_color", 3), ("grad_opacity", 1))}
+    fs = first_slots(pre, bins) if library_order else None
     getattr(L, f"orc_{prec}_blend_backward")(
         cam.width, cam.height, bins["ranges"], _u32(bins["inst_prim"]), pre["mean2d"], pre["conic_opacity"],
         pre["color"], fwd["image"], np.ascontiguousarray(grad_image, dtype=dt), fwd["n_contrib"], fwd["tile_max"],
         fwd["bucket_offsets"], fwd["ckpt"], g["grad_mean2d"], g["absgrad"], g["grad_conic"], g["grad_color"],
-        g["grad_opacity"], int(exact_grad))
+        g["grad_opacity"], int(exact_grad), n, _ptr(fs))
     return g
 
 

@@ -66,14 +66,15 @@ def normwise_err(a, b):
 # Elementwise bar beside the normwise one: |gpu - cpu| <= 1e-4 |cpu| + atol_g
 # per element, atol_g = GRAD_ELEM_ATOL_FRAC * max |cpu| of the group. The
 # absolute part covers elements whose value is a sum with cancellation: the
-# GPU sums per-(primitive, bucket) records in atomic order and uses the
-# hardware exp in the backward, so the absolute error of such a sum scales
-# with the group's largest terms, not with the (small) result.
-# Measured worst cases: config 3 (1M, 1080p) log-scales, |d| = 5.1e-5 max|cpu|
-# on an element of 1.6e-3 max|cpu| (a large outlier Gaussian whose scale
-# gradient sums ~1e5 pixel terms that cancel); config 2 (100k, 800x800)
-# rotations, |d| up to 1.7e-5 max|cpu|. The p99 of the relative error over
-# the elements above the floor is bounded as well (measured <= 2.4e-4).
+# GPU sums each primitive's per-(primitive, bucket) records in the same fixed
+# order as the oracle, but each record carries its own rounding (the hardware
+# exp2 in the backward, another order of the pixel sums inside a bucket), and
+# the absolute error of a cancelling sum scales with the group's largest
+# terms, not with the (small) result. Measured worst cases: config 3 (1M,
+# 1080p) log-scales, |d| = 3.7e-5 max|cpu| (one outlier Gaussian whose scale
+# gradient sums ~1e5 cancelling pixel terms); config 2 (100k, 800x800)
+# rotations, |d| up to 2.2e-5 max|cpu|. The p99 of the relative error over
+# the elements above the floor is bounded as well (measured <= 1.4e-4).
 GRAD_ELEM_RTOL = 1e-4
 GRAD_ELEM_ATOL_FRAC = 6e-5
 GRAD_P99_REL = 1e-3
@@ -202,3 +203,90 @@ def tile_centred_scene(k=12, seed=4):
     shr = rng.normal(0.0, 0.05, (n, 15, 3)).astype(np.float32)
     target = rng.random(cam.shape.padded_size).astype(np.float32)
     return scenes.Scene(means, scales, rots, opac, sh0, shr, 3, cam, target, "tile_centred")
+
+
+def marked_slots(bits, masks, first_slot, n_instances):
+    """Sorted record slots the fp32 backward marked: rank k < 32 of
+    primitive p as bit k of masks[p] (slot first_slot[p] + k), the others as
+    their slot's bit in bits."""
+    I = int(n_instances)
+    from_bits = np.nonzero(np.unpackbits(np.ascontiguousarray(bits, np.uint32).view(np.uint8),
+                                         bitorder="little")[:I])[0].astype(np.int64)
+    m = np.asarray(masks, np.uint32)
+    p, k = np.nonzero((m[:, None] >> np.arange(32, dtype=np.uint32)) & 1)
+    from_masks = first_slot[p].astype(np.int64) + k
+    return np.sort(np.concatenate([from_bits, from_masks]))
+
+
+def library_order_sums(records, bits, masks, first_slot, n_touched, n_instances):
+    """The per-primitive sums of the 2D-gradient records (12 floats each) in
+    the order the preprocess backward forms them on fp32 images: a
+    primitive's marked slots (marked_slots) among [first_slot, first_slot +
+    n_touched) in slot order; up to 16 records added one after another from
+    0; above 16, the record at slot s = first_slot + k (rank k) goes to lane
+    k mod 16 for k < 32 and otherwise to lane (s // 8 - (first_slot + 32) //
+    8) mod 16, each lane adds its records in slot order from 0, and the lane
+    sums are combined by an xor butterfly (partners 8, 4, 2, 1). Float32
+    adds, so the result is bit-exact with the kernel's. Returns (n, 12)
+    float32."""
+    n = first_slot.size
+    I = int(n_instances)
+    out = np.zeros((n, 12), np.float32)
+    if I == 0:
+        return out
+    marked = marked_slots(bits, masks, first_slot, I)
+    if marked.size == 0:
+        return out
+    vis = np.nonzero(n_touched > 0)[0]
+    order = vis[np.argsort(first_slot[vis].astype(np.int64), kind="stable")]
+    starts = first_slot[order].astype(np.int64)
+    owner = order[np.searchsorted(starts, marked, side="right") - 1]
+    assert np.all(marked < first_slot[owner].astype(np.int64) + n_touched[owner]), "a mark outside its range"
+    rec = records[marked].astype(np.float32)
+    # marked slots ascend and each primitive's slots are contiguous: its marks form one run
+    run_start = np.ones(marked.size, bool)
+    run_start[1:] = owner[1:] != owner[:-1]
+    first_idx = np.maximum.accumulate(np.where(run_start, np.arange(marked.size), 0))
+    pos = np.arange(marked.size) - first_idx
+    count = np.bincount(owner, minlength=n)
+    light = count[owner] <= 16
+    for q in range(16):
+        sel = light & (pos == q)
+        out[owner[sel]] += rec[sel]
+    hv = ~light
+    if hv.any():
+        ho, hr = owner[hv], rec[hv]
+        fs = first_slot[ho].astype(np.int64)
+        k = marked[hv] - fs
+        lane = np.where(k < 32, k, marked[hv] // 8 - (fs + 32) // 8) & 15
+        heavy_ids, hid = np.unique(ho, return_inverse=True)
+        key = hid * 16 + lane
+        srt = np.argsort(key, kind="stable")          # slot order kept within a (primitive, lane)
+        key, hr = key[srt], hr[srt]
+        ks = np.ones(key.size, bool)
+        ks[1:] = key[1:] != key[:-1]
+        kpos = np.arange(key.size) - np.maximum.accumulate(np.where(ks, np.arange(key.size), 0))
+        lanes = np.zeros((heavy_ids.size * 16, 12), np.float32)
+        for q in range(int(kpos.max()) + 1):
+            sel = kpos == q
+            lanes[key[sel]] += hr[sel]
+        v = lanes.reshape(-1, 16, 12)
+        for m in (8, 4, 2, 1):
+            v = v + v[:, np.arange(16) ^ m]
+        out[heavy_ids] = v[:, 0]
+    return out
+
+
+def instance_ranks(inst_prim, n):
+    """Each instance's rank among its primitive's instances, in instance order."""
+    p = np.asarray(inst_prim, np.int64)
+    if p.size == 0:
+        return np.zeros(0, np.int64)
+    srt = np.argsort(p, kind="stable")
+    ps = p[srt]
+    st = np.ones(ps.size, bool)
+    st[1:] = ps[1:] != ps[:-1]
+    r = np.arange(ps.size) - np.maximum.accumulate(np.where(st, np.arange(ps.size), 0))
+    out = np.empty(p.size, np.int64)
+    out[srt] = r
+    return out

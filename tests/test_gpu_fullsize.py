@@ -11,11 +11,14 @@ Bars (config-3 column of the baseline plan):
   per-channel tolerance 2^-10 absolute and 1e-5 relative are asserted too);
 * the loss gradient image: L1 exact, SSIM within 1e-5 normwise;
 * the rasterizer backward, fed the GPU's loss gradient image, in two parts:
-  (a) the blend backward's summed 2D gradients (the sums whose order follows
-  atomic order) at the gradient bar of tests/helpers.py, and (b) the 3D
-  gradient chain of the preprocess backward given the GPU's own 2D gradients,
-  exact; then (c) end to end, where the chain amplifies (a)'s rounding by
-  a Gaussian's anisotropy (rotations of needle-shaped Gaussians: bar 1e-3);
+  (a) the blend backward's summed 2D gradients (records summed in the fixed
+  order the oracle restates) at the gradient bar of tests/helpers.py, and
+  (b) the 3D gradient chain of the preprocess backward given the GPU's own
+  2D gradients, exact; then (c) end to end, where the chain amplifies (a)'s
+  per-record rounding by a Gaussian's anisotropy (rotations of needle-shaped
+  Gaussians: bar 1e-3);
+* the gradients of a second backward after the same forward are bit-identical
+  to the first's;
 * SimpleAdam bit-exact given the GPU's gradients.
 The oracle runs on all host cores (its results do not depend on the count).
 """
@@ -31,20 +34,21 @@ from helpers import PIXEL_ATOL, PIXEL_RTOL, assert_grads_close, normwise_err
 
 pytestmark = pytest.mark.gpu
 
-# (c) end to end, per group: the 3D chain amplifies the rounding of the 2D sums
-# by a Gaussian's anisotropy. For the needle-shaped Gaussians of config 3
-# (log-scales about -5.5, -1.4, -5.2) the rotation gradient differs from the
-# oracle's by up to 6.3e-4 normwise (measured) while the 2D sums differ by
-# 2.7e-6 and the chain itself is bit-exact; the GPU's own run-to-run variation
-# there is 2.3e-4. The log-scale elementwise floor is 1.5e-4 max|cpu|: one
-# outlier Gaussian's scale gradient sums about 1e5 cancelling pixel terms,
-# and since the 2D-gradient records are added in the order the blend
-# buckets finish (as the reference's float atomics are), its error varies
-# between runs of the same build: 1.5e-5 to 7.1e-5 max|cpu| measured (the
-# normwise figure is that same element, so its bar is 1.5e-4 too).
-END_TO_END_RTOL = {"means": 1e-4, "scales": 1.5e-4, "rotations": 1e-3, "opacities": 1e-4, "sh0": 1e-4,
+# (c) end to end, per group: the common bars (normwise 1e-4, elementwise floor
+# 6e-5 max|cpu|), except rotations. The 2D-gradient records are summed in a
+# fixed order that the oracle restates (rank order, and above 16 records the
+# 16-lane split by 8-slot bytes with an xor butterfly), so what is left
+# between GPU and oracle is each record's own rounding: the hardware exp2
+# (v_exp_f32) and the order of the pixel sums inside a bucket. The 3D chain
+# amplifies that by a Gaussian's anisotropy: for the needle-shaped Gaussians
+# of config 3 (log-scales about -5.5, -1.4, -5.2) the rotation gradient
+# differs from the oracle's by 4.4e-4 normwise (measured; worst element
+# 4.4e-4 max|cpu| on one of 0.13 max|cpu|) while the 2D sums differ by 4e-6
+# and the chain itself is bit-exact; config 2's rotations measure 2.2e-5.
+# Log-scales measured 3.7e-5 (config 3), within the common bars.
+END_TO_END_RTOL = {"means": 1e-4, "scales": 1e-4, "rotations": 1e-3, "opacities": 1e-4, "sh0": 1e-4,
                    "sh_rest": 1e-4}
-END_TO_END_ATOL_FRAC = {"rotations": 1e-3, "scales": 1.5e-4}
+END_TO_END_ATOL_FRAC = {"rotations": 1e-3}
 
 LR = {"means": 1.6e-4, "scene_scale": 1.0, "opacities": 5e-2, "rotations": 1e-3, "scales": 5e-3, "shs": 5e-3}
 
@@ -79,6 +83,11 @@ def _run(scene, orc, sparse):
     grads = {"means": g.means(), "scales": g.scales(), "rotations": g.rotations(), "opacities": g.opacities(),
              "sh0": g.sh_coefficient_0(), "sh_rest": g.sh_coefficients_rest()}
     grads = {k: v.cpu().numpy().reshape(-1) for k, v in grads.items()}
+    # the same backward again: bit-identical gradients (a fixed summation order)
+    ts.backward()
+    torch.cuda.synchronize()
+    for k, t in zip(grads, g.tensors()):
+        assert np.array_equal(t.detach().cpu().numpy().reshape(-1).view(np.uint32), grads[k].view(np.uint32)), k
     ts.optimize()
     torch.cuda.synchronize()
     theta = ts.params()

@@ -5,11 +5,11 @@ with the step count on the device. Each replay is checked against an eager
 twin fed the same scene, with eager work and synchronisation between the
 replays: parameters, image and loss gradient bit-exact after every step.
 
-The scene keeps every Gaussian inside one tile (small Gaussians near tile
-centres), so each has one 2D-gradient record per step and the step is
-deterministic: the per-primitive sums of several records follow the order
-in which buckets finish, which would make twins drift apart by rounding
-whether or not a graph is used."""
+fp32 images run a general scene: each primitive's 2D-gradient records are
+summed in a fixed order, so a step repeats bit for bit. The fp16-image
+rasterizer sums its half records exactly but adds the opacity-logit parts in
+double in the order the buckets finish, so its case keeps every Gaussian
+inside one tile (one record each), which makes its step deterministic too."""
 import numpy as np
 import pytest
 
@@ -37,8 +37,10 @@ def test_captured_step_replays_match_eager_steps(hip, image_dtype, overlap):
     """overlap: Adam's rows without gradient on a second stream (a fork and a
     join inside the captured step)."""
     import torch
+    from tinygs_amd import scenes
     from tinygs_amd.train import TrainStep
-    scene = tile_centred_scene()
+    one_tile = image_dtype == "float16"
+    scene = tile_centred_scene() if one_tile else scenes.config3(seed=41, n=20000, width=256, height=160)
     s = torch.cuda.Stream()
     kw = dict(l1_weight=0.8, ssim_weight=0.2, eps=1e-15, shs_lr=5e-3, sparse_grads=True, no_sync=True, stream=s,
               image_dtype=image_dtype, overlap_adam=overlap)
@@ -50,9 +52,11 @@ def test_captured_step_replays_match_eager_steps(hip, image_dtype, overlap):
             ts.step()
             ts.step()
     s.synchronize()
-    # the premise: one tile, so one record, per Gaussian
     v, inst, _ = eager.rasterizer.counts()
-    assert inst == v, (inst, v)
+    if one_tile:   # the premise: one tile, so one record, per Gaussian
+        assert inst == v, (inst, v)
+    else:
+        assert inst > v, (inst, v)   # primitives over several tiles: several records each
     a, b = _state(eager), _state(graphed)
     for k in a:
         assert np.array_equal(_bits(a[k]), _bits(b[k])), k

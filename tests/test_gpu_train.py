@@ -132,3 +132,130 @@ def test_psnr_float16_closed_form(hip, wh):
     assert PsnrMetric().evaluate(b, b) == 100.0
     with pytest.raises(RuntimeError):
         PsnrMetric().evaluate(a, Image(shape, DataType.Float32, torch.zeros(shape.padded_size).cuda()))
+
+
+def _small_loop(data_type="float32", accum=1, views=4):
+    from tinygs_amd import scenes
+    from tinygs_amd.data import SimpleDataLoader, SyntheticViewDataset, gaussians_from_arrays
+    from tinygs_amd.optim import create_optimizer
+    from tinygs_amd.rasterizer import create_rasterizer
+    from tinygs_amd.trainer import Orchestrator, OrchestratorConfig
+    sc = scenes.config5(n_init=3000, n_gt=2000, n_cameras=views, width=96, height=64)
+    ds = SyntheticViewDataset(sc, data_type=data_type)
+    g = gaussians_from_arrays(sc.init, 0)
+    grads = g.gradient_like()
+    opt = create_optimizer("simple_adam", g, grads)
+    cfg = OrchestratorConfig(train_data_type=data_type, eval_data_type=data_type, accumulate_grad_steps=accum,
+                             reorder_gaussians_interval=0, grad_scaler=4.0)
+    return sc, ds, Orchestrator(cfg, g, grads, create_rasterizer("fastgs"), opt, SimpleDataLoader(ds)), g, opt
+
+
+def _twin(sc, ds, data_type):
+    """The same Gaussians and Adam state driven by the bare entry points."""
+    from tinygs_amd.core import Image, LossContext, RasterizeContext
+    from tinygs_amd.data import SimpleDataLoader, gaussians_from_arrays
+    from tinygs_amd.loss import create_loss
+    from tinygs_amd.optim import create_optimizer
+    from tinygs_amd.rasterizer import create_rasterizer
+    from tinygs_amd.image import ImageShape
+    g = gaussians_from_arrays(sc.init, 0)
+    grads = g.gradient_like()
+    opt = create_optimizer("simple_adam", g, grads)
+    r = create_rasterizer("fastgs")
+    r.set_gaussians(g)
+    shape = ImageShape(ds.width, ds.height, 3)
+    ctx = RasterizeContext(grad_scaler=4.0)
+    ctx.fwd_output.image = Image.empty(shape, data_type=data_type)
+    ctx.grad_output.image = Image.empty(shape, data_type=data_type)
+    ctx.gaussians_grad = grads
+    return {"g": g, "grads": grads, "opt": opt, "r": r, "ctx": ctx, "loader": SimpleDataLoader(ds),
+            "loss": Image.empty(shape, data_type=data_type), "l1": create_loss("l1")}
+
+
+def _state(g):
+    return [t.detach().cpu().numpy().copy() for t in g.tensors()]
+
+
+@pytest.mark.parametrize("data_type", ["float32", "float16"])
+def test_orchestrator_step_equals_bare_entry_points(hip, data_type):
+    """One Orchestrator step at train_data_type float32 / float16 (dataset
+    images of the same type; grad_scaler 4) is the bare sequence forward ->
+    fused L1 + SSIM (weights x grad_scaler) -> sparse backward -> masked Adam
+    with scale 1 / grad_scaler, bit for bit; training then raises the PSNR
+    (fp16 PsnrMetric on fp16 images)."""
+    import numpy as np
+    import torch
+    from tinygs_amd.core import LossContext
+    from tinygs_amd.loss import evaluate_l1_ssim
+    sc, ds, orch, g, opt = _small_loop(data_type)
+    t = _twin(sc, ds, data_type)
+    print(f"[loop] one step, {data_type} images", flush=True)
+    orch.recompute_scene_scale()
+    t["g"].set_scene_scale(g.scene_scale())
+    orch.train_step()
+    cam, target = t["loader"].next()
+    ctx = t["ctx"]
+    ctx.fwd_input = cam
+    t["r"].forward(ctx)
+    lctx = LossContext(ctx.fwd_output.image, target, t["loss"], ctx.grad_output.image, None)
+    evaluate_l1_ssim(t["l1"], lctx, 0.8 * 4.0, 0.2 * 4.0, assign=True)
+    t["r"].backward(ctx, sparse=True)
+    t["opt"].step(float(np.float32(1.0) / np.float32(4.0)), None, row_mask=t["r"].grad_row_mask())
+    torch.cuda.synchronize()
+    assert orch.m_pred.data.dtype == (torch.float16 if data_type == "float16" else torch.float32)
+    for a, b in zip(_state(g), _state(t["g"])):
+        assert np.array_equal(a.view(np.uint8), b.view(np.uint8))
+    p0 = orch.eval_psnr()
+    orch.train(40)
+    p1 = orch.eval_psnr()
+    print(f"[loop] {data_type}: PSNR {p0:.3f} -> {p1:.3f} dB after 40 steps", flush=True)
+    assert p1 > p0 + 0.5
+
+
+def test_gradient_accumulation_over_two_steps(hip, orc):
+    """accumulate_grad_steps = 2 (orchestrator.cu:343-353, 390-404): the
+    gradients are zeroed at the cycle start, both backwards accumulate, and
+    only the second step runs Adam, scaled by 1 / (grad_scaler * 2). The
+    accumulated gradients equal the sum of the two views' oracle gradients
+    (within the gradient bars), and the step is Adam bit-exact on them."""
+    import numpy as np
+    import torch
+    from helpers import assert_grads_close
+    sc, ds, orch, g, opt = _small_loop("float32", accum=2)
+    orch.recompute_scene_scale()
+    theta0 = _state(g)
+    orch.train_step()
+    torch.cuda.synchronize()
+    assert all(np.array_equal(a, b) for a, b in zip(theta0, _state(g)))   # no step after the first view
+    orch.train_step()
+    torch.cuda.synchronize()
+    got_grads = _state(orch.m_gradients)
+    # the oracle: both views' gradients at the initial parameters, summed
+    from oracle import train as T
+    from tinygs_amd.data import SimpleDataLoader
+    ld = SimpleDataLoader(ds)
+    names = ("means", "scales", "rotations", "opacities", "sh0", "sh_rest")
+    init = {k: np.asarray(v, np.float32).reshape(v.shape[0], -1) if k != "opacities" else np.asarray(v, np.float32)
+            for k, v in sc.init.items()}
+    init["sh_rest"] = init["sh_rest"].reshape(-1, 45)
+    ref = {k: 0.0 for k in names}
+    for _ in range(2):
+        view = ds[ld.m_permutation[ld.m_current_index]]
+        ld.next()
+        v = T._View(init, 0, view.camera, view.target.data.cpu().numpy())
+        out = orc.run_iteration(v, 0.8 * 4.0, 0.2 * 4.0, lr=None, eps=1e-8)
+        for k in names:
+            ref[k] = ref[k] + out["grads"][k].astype(np.float64)
+    assert_grads_close({k: a.reshape(-1) for k, a in zip(names, got_grads)},
+                       {k: ref[k].astype(np.float32) for k in names})
+    # Adam on the accumulated gradients, scale 1 / (4 * 2)
+    th = orc.params(v, "f")
+    m1 = {k: np.zeros_like(a) for k, a in th.items()}
+    m2 = {k: np.zeros_like(a) for k, a in th.items()}
+    lr = {"means": 1.6e-4, "scene_scale": g.scene_scale(), "opacities": 5e-2, "rotations": 1e-3,
+          "scales": 5e-3, "shs": 2.5e-3}
+    scale = float(np.float32(np.float32(1.0) / np.float32(4.0)) / np.float32(2.0))
+    orc.adam_step(th, {k: a.reshape(-1) for k, a in zip(names, got_grads)}, m1, m2, lr, 1, grad_scale=scale,
+                  eps=1e-8)
+    for k, a in zip(names, _state(g)):
+        assert np.array_equal(a.reshape(-1).view(np.uint32), th[k].view(np.uint32)), k

@@ -56,7 +56,8 @@ class tgs_debug_view(C.Structure):
                 ("tile_ranges", C.c_void_p), ("n_contrib", C.c_void_p), ("tile_max", C.c_void_p),
                 ("grad2d", C.c_void_p), ("n_visible", C.c_int64), ("n_instances", C.c_int64),
                 ("n_tiles", C.c_int64), ("depth_key_base", C.c_uint32), ("image_dtype", C.c_uint32),
-                ("first_slot", C.c_void_p), ("records", C.c_void_p)]
+                ("first_slot", C.c_void_p), ("records", C.c_void_p), ("instance_ranks", C.c_void_p),
+                ("record_bits", C.c_void_p)]
 
 
 class tgs_pcg32(C.Structure):

@@ -319,12 +319,18 @@ __global__ void __launch_bounds__(64 * NW) radix_upsweep_kernel(const uint32_t* 
                                                                 const uint32_t* d_n, int64_t max_n, int shift,
                                                                 int bits, uint32_t* __restrict__ counts,
                                                                 uint32_t* __restrict__ ntsums, uint32_t nb,
-                                                                uint2* __restrict__ rinit, uint32_t n_tiles) {
+                                                                uint2* __restrict__ rinit, uint32_t n_tiles,
+                                                                uint32_t* __restrict__ clear_bits) {
     constexpr int kNT = 64 * NW;
     // rinit: the tile ranges the next downsweep reduces into, set to (UINT32_MAX, 0)
     if (rinit)
         for (uint32_t j = blockIdx.x * kNT + threadIdx.x; j < n_tiles; j += gridDim.x * kNT)
             rinit[j] = make_uint2(0xffffffffu, 0u);
+    // clear_bits: one bit per key position (the 2D-gradient record marks of
+    // the next backward); this workgroup's 64 KPT NW positions are whole words
+    if (clear_bits)
+        for (uint32_t j = threadIdx.x; j < (uint32_t)(KPT * NW * 2); j += kNT)
+            clear_bits[(size_t)blockIdx.x * (KPT * NW * 2) + j] = 0u;
     __shared__ uint32_t s_hist[kHistCopies][MAXB];
     __shared__ uint32_t s_hsum[NTSUM ? kHistCopies : 1][NTSUM ? MAXB : 1];
     const uint32_t t = threadIdx.x, lane = t & 63u, w = t >> 6;
@@ -428,7 +434,7 @@ __global__ void __launch_bounds__(64 * NW) radix_downsweep_kernel(
     uint32_t* __restrict__ keys_out, uint32_t* __restrict__ vals_out, uint32_t* __restrict__ v2_out,
     const uint32_t* d_n, int64_t max_n, int shift, int bits, const uint32_t* __restrict__ offsets, uint32_t nb,
     const uint32_t* __restrict__ block_n, const uint32_t* __restrict__ ntscan, uint32_t* __restrict__ offs,
-    uint2* __restrict__ ranges, uint32_t n_tiles) {
+    uint2* __restrict__ ranges, uint32_t n_tiles, uint16_t* __restrict__ ranks) {
     constexpr int kNT = 64 * NW;             // threads
     constexpr int kChunk = kNT * KPT;
     constexpr int kBpt = MAXB > kNT ? MAXB / kNT : 1;   // digits per thread in the workgroup scan
@@ -543,6 +549,10 @@ __global__ void __launch_bounds__(64 * NW) radix_downsweep_kernel(
         }
         return;
     }
+    // RANGES: the key's sorted bits (all bits below shift + bits) are the
+    // tile; bits above them carry the instance's rank among its primitive's
+    // instances (fp32 images), written to ranks
+    const uint32_t tmask = shift + bits >= 32 ? 0xffffffffu : (1u << (shift + bits)) - 1u;
     for (uint32_t i = t; i < cnt; i += kNT) {
         const uint32_t k = s_key[i];
         const uint32_t o = s_gofs[(k >> shift) & dmask] + i;
@@ -551,9 +561,11 @@ __global__ void __launch_bounds__(64 * NW) radix_downsweep_kernel(
             vals_out[o] = s_val[i];
             if constexpr (PAYLOAD2) v2_out[o] = s_v2[i];
             if constexpr (RANGES) {
-                if (k < n_tiles) {
-                    if (i == 0u || s_key[i - 1u] != k) atomicMin(&ranges[k].x, o);
-                    if (i + 1u == cnt || s_key[i + 1u] != k) atomicMax(&ranges[k].y, o + 1u);
+                const uint32_t tk = k & tmask;
+                if (ranks) ranks[o] = (uint16_t)(k >> 16);
+                if (tk < n_tiles) {
+                    if (i == 0u || (s_key[i - 1u] & tmask) != tk) atomicMin(&ranges[tk].x, o);
+                    if (i + 1u == cnt || (s_key[i + 1u] & tmask) != tk) atomicMax(&ranges[tk].y, o + 1u);
                 }
             }
         }
@@ -579,7 +591,7 @@ static int radix_passes(uint32_t* keys[2], uint32_t* vals[2], uint32_t* v2[2], c
                         int n_passes, const int* shifts, const int* bits, uint32_t* counts, uint32_t* tickets,
                         uint64_t* status, const uint32_t* epoch_base, uint32_t& epoch, uint32_t* err,
                         const uint32_t* first_block_n, uint32_t* offs, bool* offs_done, uint2* ranges,
-                        uint32_t n_tiles, bool* ranges_done, hipStream_t s) {
+                        uint32_t n_tiles, bool* ranges_done, uint16_t* ranks, uint32_t* clear_bits, hipStream_t s) {
     int cur = 0;
     if (offs_done) *offs_done = false;
     if (ranges_done) *ranges_done = false;
@@ -596,12 +608,13 @@ static int radix_passes(uint32_t* keys[2], uint32_t* vals[2], uint32_t* v2[2], c
         if constexpr (MAXB == kDepthMaxDigits) {
             if (with_offs) {
                 radix_upsweep_kernel<kDownKpt, MAXB, DW, true><<<nb, 64 * DW, 0, s>>>(
-                    keys[cur], v2[cur], d_n, max_n, shifts[p], bits[p], counts, counts + cn, nb, nullptr, 0u);
+                    keys[cur], v2[cur], d_n, max_n, shifts[p], bits[p], counts, counts + cn, nb, nullptr, 0u,
+                    nullptr);
                 exclusive_scan_kernel<<<(unsigned)((2 * cn + kScanChunk - 1) / kScanChunk), kScanThreads, 0, s>>>(
                     counts, 2 * cn, tickets + p, status, epoch_base, ++epoch, err);
                 radix_downsweep_kernel<kDownKpt, true, MAXB, DW, true><<<nb, 64 * DW, 0, s>>>(
                     keys[cur], vals[cur], v2[cur], keys[cur ^ 1], vals[cur ^ 1], nullptr, d_n, max_n, shifts[p],
-                    bits[p], counts, nb, nullptr, counts + cn, offs, nullptr, 0u);
+                    bits[p], counts, nb, nullptr, counts + cn, offs, nullptr, 0u, nullptr);
                 *offs_done = true;
                 cur ^= 1;
                 continue;
@@ -611,22 +624,22 @@ static int radix_passes(uint32_t* keys[2], uint32_t* vals[2], uint32_t* v2[2], c
         if (!block_n)
             radix_upsweep_kernel<kDownKpt, MAXB, DW><<<nb, 64 * DW, 0, s>>>(
                 keys[cur], nullptr, d_n, max_n, shifts[p], bits[p], counts, nullptr, nb,
-                with_ranges ? ranges : nullptr, n_tiles);
+                with_ranges ? ranges : nullptr, n_tiles, p == 0 ? clear_bits : nullptr);
         exclusive_scan_kernel<<<(unsigned)((cn + kScanChunk - 1) / kScanChunk), kScanThreads, 0, s>>>(
             counts, cn, tickets + p, status, epoch_base, ++epoch, err);
         if (v2)
             radix_downsweep_kernel<kDownKpt, true, MAXB, DW><<<nb, 64 * DW, 0, s>>>(
                 keys[cur], vals[cur], v2[cur], keys[cur ^ 1], vals[cur ^ 1], v2[cur ^ 1], d_n, max_n, shifts[p],
-                bits[p], counts, nb, block_n, nullptr, nullptr, nullptr, 0u);
+                bits[p], counts, nb, block_n, nullptr, nullptr, nullptr, 0u, nullptr);
         else if (with_ranges) {
             radix_downsweep_kernel<kDownKpt, false, MAXB, DW, false, true><<<nb, 64 * DW, 0, s>>>(
                 keys[cur], vals[cur], nullptr, keys[cur ^ 1], vals[cur ^ 1], nullptr, d_n, max_n, shifts[p], bits[p],
-                counts, nb, nullptr, nullptr, nullptr, ranges, n_tiles);
+                counts, nb, nullptr, nullptr, nullptr, ranges, n_tiles, ranks);
             *ranges_done = true;
         } else
             radix_downsweep_kernel<kDownKpt, false, MAXB, DW><<<nb, 64 * DW, 0, s>>>(
                 keys[cur], vals[cur], nullptr, keys[cur ^ 1], vals[cur ^ 1], nullptr, d_n, max_n, shifts[p], bits[p],
-                counts, nb, block_n, nullptr, nullptr, nullptr, 0u);
+                counts, nb, block_n, nullptr, nullptr, nullptr, 0u, nullptr);
         cur ^= 1;
     }
     return cur;
@@ -636,14 +649,19 @@ int radix_sort(uint32_t* keys[2], uint32_t* vals[2], uint32_t* v2[2], const uint
                int n_passes, const int* shifts, const int* bits, uint32_t* counts, uint32_t* tickets,
                uint64_t* status, const uint32_t* epoch_base, uint32_t& epoch, uint32_t* err,
                const uint32_t* first_block_n, uint32_t* offs, bool* offs_done, uint2* ranges, uint32_t n_tiles,
-               bool* ranges_done, hipStream_t s) {
+               bool* ranges_done, uint16_t* ranks, uint32_t* clear_bits, hipStream_t s) {
     if (depth)
         return radix_passes<kDepthKeysPerThread, kDepthMaxDigits, kDepthSortWaves>(
             keys, vals, v2, d_n, max_n, n_passes, shifts, bits, counts, tickets, status, epoch_base, epoch, err,
-            first_block_n, offs, offs_done, nullptr, 0u, ranges_done, s);
+            first_block_n, offs, offs_done, nullptr, 0u, ranges_done, nullptr, nullptr, s);
     return radix_passes<kTileKeysPerThread, kTileMaxDigits, kTileSortWaves>(
         keys, vals, v2, d_n, max_n, n_passes, shifts, bits, counts, tickets, status, epoch_base, epoch, err,
-        first_block_n, nullptr, offs_done, ranges, n_tiles, ranges_done, s);
+        first_block_n, nullptr, offs_done, ranges, n_tiles, ranges_done, ranks, clear_bits, s);
+}
+
+int64_t record_bit_words(int64_t max_inst) {
+    const int64_t chunk = kThreads * kTileKeysPerThread;   // the tile passes' workgroup positions
+    return ((max_inst > 0 ? max_inst : 1) + chunk - 1) / chunk * (chunk / 32);
 }
 
 // ---------------------------------------------------------------- instance emission
@@ -805,7 +823,9 @@ __global__ void __launch_bounds__(256) emit_kernel(const uint32_t* __restrict__ 
         const uint32_t seg = exj > base ? exj - base : 0u;   // the owner's first lane in this window
         const uint64_t below = hm & ((1ull << lane) - 1ull) & ~((1ull << seg) - 1ull);
         const uint32_t pos = offj + (j + 1u == prev ? carry_hits : 0u) + (uint32_t)__builtin_popcountll(below);
-        if (hit && pos < endj) put(pos, ty * grid_w + tx, pj);
+        // fp32 images: the key's bits from 16 up carry the instance's rank
+        // among its primitive's instances (tile keys there are below 2^16)
+        if (hit && pos < endj) put(pos, (ty * grid_w + tx) | (kHalf ? 0u : (pos - offj) << 16), pj);
         // hits so far of the primitive carried into the next window (lane 63's owner)
         const uint32_t seg63 = readlane_u32(seg, 63);
         const uint32_t h63 = (uint32_t)__builtin_popcountll(hm & ~((1ull << seg63) - 1ull));

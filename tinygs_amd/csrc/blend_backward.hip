@@ -33,9 +33,15 @@
 // one DRAM read-modify-write each): [0,1] dL/dmean2d, [2,3] |.| sums
 // (absgrad), [4..6] dL/dconic (a, b, c), [7..9] dL/dcolour (masked by
 // colour >= 0), [10] sum of alpha * dL/dalpha (times (1 - opacity) later).
-// The record index comes from one counter atomic per (primitive, bucket) into
-// the instance slots binning reserved for the primitive; the per-primitive
-// sums are formed by the preprocess backward.
+// The record of the instance with rank k among its primitive's instances
+// (carried through the tile sort) goes to slot first_slot[p] + k of the
+// instance slots binning reserved for the primitive; a bit (a non-returning
+// atomic OR: for ranks below 32 in the primitive's own mask word, for the
+// others in a per-slot bit array) marks it written and a per-primitive
+// counter (a non-returning atomic add) counts it: where a record lands does not
+// depend on the order in which the buckets finish, so the preprocess
+// backward's per-primitive sums run in a fixed order (rank order, the order
+// of the primitive's tiles) and a step's gradients repeat bit for bit.
 #include "common.h"
 #include "kernels.h"
 
@@ -48,10 +54,11 @@ constexpr float kLog2e = 1.4426950408889634f;
 // sums are only read when densification info is requested.
 template <bool ABS>
 __global__ void __launch_bounds__(256) blend_backward_kernel(
-    CamParams cam, const uint32_t* __restrict__ inst_vals, const float2* __restrict__ mean2d,
-    const float4* __restrict__ conic_opacity, const float4* __restrict__ color_pt, const float* __restrict__ image,
-    const float* __restrict__ grad_image, const uint32_t* __restrict__ n_contrib, const float4* __restrict__ ckpt,
-    const uint4* __restrict__ items, BinCtl* __restrict__ ctl, uint32_t* __restrict__ rec_count,
+    CamParams cam, const uint32_t* __restrict__ inst_vals, const uint16_t* __restrict__ inst_ranks,
+    const float2* __restrict__ mean2d, const float4* __restrict__ conic_opacity, const float4* __restrict__ color_pt,
+    const float* __restrict__ image, const float* __restrict__ grad_image, const uint32_t* __restrict__ n_contrib,
+    const float4* __restrict__ ckpt, const uint4* __restrict__ items, BinCtl* __restrict__ ctl,
+    uint32_t* __restrict__ rec_bits, uint32_t* __restrict__ rec_mask, uint32_t* __restrict__ rec_count,
     const uint32_t* __restrict__ first_slot, float4* __restrict__ records) {
     __shared__ float4 s_rec[4][3][kBucket];
     __shared__ float s_part[4][kBwdVals + 1][kBucket + 1];   // +1: the four row writers hit four banks
@@ -79,13 +86,12 @@ __global__ void __launch_bounds__(256) blend_backward_kernel(
         const int32_t cnt = (int32_t)item.w;
 
         // ---- stage the bucket's records (wave-private LDS slice); each of
-        // its primitives takes one 2D-gradient record index now and fills it
-        // at the end of the item
-        uint32_t p = 0, sub = 0, slot = 0;
+        // its primitives fills its 2D-gradient record slot at the end of the item
+        uint32_t p = 0, slot = 0, rank = 0;
         if ((int32_t)lane < cnt) {
             p = inst_vals[first + lane];
-            sub = atomicAdd(rec_count + p, 1u);
-            slot = first_slot[p];
+            rank = inst_ranks[first + lane];
+            slot = first_slot[p] + rank;
             const float2 m = mean2d[p];
             const float4 co = conic_opacity[p];
             const float4 c = color_pt[p];
@@ -258,7 +264,7 @@ __global__ void __launch_bounds__(256) blend_backward_kernel(
             const uint32_t mask = f2u(s_part[w][kBwdVals][k]);
             auto val = [&](int q) { return ev ? s_part[w][q][k] : 0.f; };
             // record order: mean2d(2), abs(2), conic(3), colour(3), alpha partial, 0
-            float4* dst = records + 3 * (size_t)(slot + sub);
+            float4* dst = records + 3 * (size_t)slot;
             // dL/dmean2d = conic . (sum pp X, sum pp Y), applied once per Gaussian
             const float a = s_rec[w][1][k].z, c = s_rec[w][1][k].w, bq = s_rec[w][2][k].w;
             const float gmx = __builtin_fmaf(a, val(7), bq * val(8));
@@ -266,6 +272,13 @@ __global__ void __launch_bounds__(256) blend_backward_kernel(
             dst[0] = make_float4(-gmx, -gmy, val(9), val(10));
             dst[1] = make_float4(-0.5f * val(4), -0.5f * val(5), -0.5f * val(6), (mask & 1u) ? val(0) : 0.f);
             dst[2] = make_float4((mask & 2u) ? val(1) : 0.f, (mask & 4u) ? val(2) : 0.f, val(3), 0.f);
+            // the mark: ranks below 32 in the primitive's own mask word, the rest by slot
+            if (rank < 32u)
+                __hip_atomic_fetch_or(rec_mask + p, 1u << rank, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            else
+                __hip_atomic_fetch_or(rec_bits + (slot >> 5), 1u << (slot & 31u), __ATOMIC_RELAXED,
+                                      __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_fetch_add(rec_count + p, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
         next = (uint32_t)__builtin_amdgcn_readfirstlane((int)after);
         wave_lds_sync();
@@ -295,11 +308,12 @@ void launch_backward_rows(const uint4* items, const uint32_t* inst_vals, const B
 
 static int g_blocks = 0;
 
-void launch_blend_backward(const CamParams& cam, const uint32_t* inst_vals, const float2* mean2d,
-                           const float4* conic_opacity, const float4* color_pt, const float* image,
-                           const float* grad_image, const uint32_t* n_contrib, const float4* ckpt,
-                           const uint4* items, BinCtl* ctl, uint32_t* rec_count, const uint32_t* first_slot,
-                           float4* records, bool with_abs, hipStream_t s) {
+void launch_blend_backward(const CamParams& cam, const uint32_t* inst_vals, const uint16_t* inst_ranks,
+                           const float2* mean2d, const float4* conic_opacity, const float4* color_pt,
+                           const float* image, const float* grad_image, const uint32_t* n_contrib, const float4* ckpt,
+                           const uint4* items, BinCtl* ctl, uint32_t* rec_bits, uint32_t* rec_mask,
+                           uint32_t* rec_count, const uint32_t* first_slot, float4* records, bool with_abs,
+                           hipStream_t s) {
     const uint32_t n_tiles = cam.grid_w * cam.grid_h;
     if (n_tiles == 0) return;
     if (g_blocks <= 0) {
@@ -315,13 +329,13 @@ void launch_blend_backward(const CamParams& cam, const uint32_t* inst_vals, cons
         g_blocks = cus * per_cu;
     }
     if (with_abs)
-        blend_backward_kernel<true><<<(uint32_t)g_blocks, 256, 0, s>>>(cam, inst_vals, mean2d, conic_opacity,
-                                                                       color_pt, image, grad_image, n_contrib, ckpt,
-                                                                       items, ctl, rec_count, first_slot, records);
+        blend_backward_kernel<true><<<(uint32_t)g_blocks, 256, 0, s>>>(
+            cam, inst_vals, inst_ranks, mean2d, conic_opacity, color_pt, image, grad_image, n_contrib, ckpt, items,
+            ctl, rec_bits, rec_mask, rec_count, first_slot, records);
     else
-        blend_backward_kernel<false><<<(uint32_t)g_blocks, 256, 0, s>>>(cam, inst_vals, mean2d, conic_opacity,
-                                                                        color_pt, image, grad_image, n_contrib, ckpt,
-                                                                        items, ctl, rec_count, first_slot, records);
+        blend_backward_kernel<false><<<(uint32_t)g_blocks, 256, 0, s>>>(
+            cam, inst_vals, inst_ranks, mean2d, conic_opacity, color_pt, image, grad_image, n_contrib, ckpt, items,
+            ctl, rec_bits, rec_mask, rec_count, first_slot, records);
 }
 
 }  // namespace tgs

@@ -219,6 +219,12 @@ struct tgs_rasterizer {
     // count (kept zero between backwards), records (3 float4 per instance
     // slot), heavy-gather list
     DevBuf first_slot, rec_count, records;
+    // fp32 images: each instance's rank among its primitive's instances
+    // (u16, sorted with the tile keys) and one bit per instance slot marking
+    // the records the last backward wrote (record of instance rank k of p at
+    // slot first_slot[p] + k, so the per-primitive sums run in a fixed order)
+    DevBuf iranks, rec_bits;
+    DevBuf rec_mask;   // fp32 images: per primitive, the record marks of ranks 0..31 (zero between backwards)
     DevBuf live, heavy;   // preprocess backward: per-chunk lists of primitives with records
     DevBuf row_mask;     // per-primitive byte mask of the last sparse backward
     bool row_mask_valid = false;
@@ -277,6 +283,8 @@ static int ensure_instances(tgs_rasterizer* r, int64_t inst, uint32_t T, hipStre
     TGS_TRY(ensure(r->ckpt, sizeof(float4) * kTilePixels * slots, s));
     TGS_TRY(ensure(r->items, sizeof(uint4) * slots, s));
     TGS_TRY(ensure(r->records, 3 * sizeof(float4) * (size_t)ii, s));
+    TGS_TRY(ensure(r->iranks, sizeof(uint16_t) * (size_t)ii, s));
+    TGS_TRY(ensure(r->rec_bits, sizeof(uint32_t) * (size_t)record_bit_words(ii), s));
     return TGS_OK;
 }
 
@@ -341,7 +349,9 @@ int tgs_rasterizer_destroy(tgs_rasterizer* r) {
                      &r->radix_counts, &r->block_n, &r->ikeys[0],
                      &r->ikeys[1], &r->ivals[0], &r->ivals[1], &r->ranges, &r->tile_max, &r->n_contrib,
                      &r->ckpt, &r->items, &r->tile_loaded, &r->first_slot,
-                     &r->rec_count, &r->records, &r->heavy, &r->live, &r->row_mask, &r->grad2d,
+                     &r->rec_count, &r->records, &r->iranks, &r->rec_bits, &r->rec_mask, &r->heavy, &r->live,
+                     &r->row_mask,
+                     &r->grad2d,
                      &r->bwd_rows, &r->pose_partial, &r->pose_grad, &r->bin_ctl, &r->lb_status};
     for (DevBuf* b : all) release(*b);
     if (r->h_counters) (void)hipHostFree(r->h_counters);
@@ -455,6 +465,10 @@ static int rasterizer_forward(tgs_rasterizer* r, const tgs_camera* camera, void*
         TGS_TRY(ensure(r->rec_count, 4 * nn, s));
         if (r->rec_count.p != before)   // counters are zero between backwards; a new buffer starts so
             launch_fill_u32(r->rec_count.as<uint32_t>(), 0u, (int64_t)(r->rec_count.bytes / 4), s);
+        const void* mbefore = r->rec_mask.p;
+        TGS_TRY(ensure(r->rec_mask, 4 * nn, s));
+        if (r->rec_mask.p != mbefore)   // (the same for the mask words)
+            launch_fill_u32(r->rec_mask.as<uint32_t>(), 0u, (int64_t)(r->rec_mask.bytes / 4), s);
     }
     for (int k = 0; k < 2; ++k) {
         TGS_TRY(ensure(r->pkeys[k], 4 * nn, s));
@@ -510,7 +524,8 @@ static int rasterizer_forward(tgs_rasterizer* r, const tgs_camera* camera, void*
         bool offs_done = false;
         psel = radix_sort(pk, pv, pn, &ctl->V, n, true, sp.n_dp, sp.dshift, sp.dbits, r->radix_counts.as<uint32_t>(),
                           ctl->tickets + kTicketDepth, status, &ctl->epoch_base, r->epoch, &ctl->err,
-                          r->block_n.as<uint32_t>(), r->offs.as<uint32_t>(), &offs_done, nullptr, 0u, nullptr, s);
+                          r->block_n.as<uint32_t>(), r->offs.as<uint32_t>(), &offs_done, nullptr, 0u, nullptr,
+                          nullptr, nullptr, s);
         if (psel < 0) return fail(TGS_ERR_STATE, "depth sort digit width");
         r->depth_key_base = sp.key_base;
         if (!offs_done) launch_instance_offsets(pn[psel], n, r->offs.as<uint32_t>(), ctl, status, r->epoch, s);
@@ -550,10 +565,12 @@ static int rasterizer_forward(tgs_rasterizer* r, const tgs_camera* camera, void*
     bool ranges_done = false;   // the tile sort's last pass reduced the tile ranges
     {
         StageScope sc(ST_TILES, s);
+        // fp32: the instances' ranks out of the keys' high bits, record bits cleared
         isel = radix_sort(ik, iv, nullptr, d_inst, cap, false, sp.n_tp, sp.tshift, sp.tbits,
                           r->radix_counts.as<uint32_t>(), ctl->tickets + kTicketTile, status, &ctl->epoch_base,
                           r->epoch, &ctl->err, nullptr, nullptr, nullptr, r->ranges.as<uint2>(), (uint32_t)T,
-                          &ranges_done, s);
+                          &ranges_done, f16 ? nullptr : r->iranks.as<uint16_t>(),
+                          f16 ? nullptr : r->rec_bits.as<uint32_t>(), s);
         if (isel < 0) return fail(TGS_ERR_STATE, "tile sort digit width");
         if (r->epoch >= kEpochStride) return fail(TGS_ERR_STATE, "look-back launches per forward exceed the epoch stride");
         if (!ranges_done) launch_tile_ranges(ik[isel], d_inst, cap, r->ranges.as<uint2>(), T, s);
@@ -699,11 +716,13 @@ int tgs_rasterizer_backward_ex(tgs_rasterizer* r, const void* grad_image, const 
                                     r->ckpt.as<uint2>(), r->items.as<uint4>(), ctl, r->rec_count.as<uint32_t>(),
                                     r->first_slot.as<uint32_t>(), r->records.as<float4>(), s);
         else
-            launch_blend_backward(cam, r->ivals[r->isel].as<uint32_t>(), r->mean2d.as<float2>(),
-                                  r->conic_opacity.as<float4>(), r->color.as<float4>(), (const float*)image,
-                                  (const float*)grad_image, r->n_contrib.as<uint32_t>(), r->ckpt.as<float4>(),
-                                  r->items.as<uint4>(), ctl, r->rec_count.as<uint32_t>(), r->first_slot.as<uint32_t>(),
-                                  r->records.as<float4>(), densification_info != nullptr, s);
+            launch_blend_backward(cam, r->ivals[r->isel].as<uint32_t>(), r->iranks.as<uint16_t>(),
+                                  r->mean2d.as<float2>(), r->conic_opacity.as<float4>(), r->color.as<float4>(),
+                                  (const float*)image, (const float*)grad_image, r->n_contrib.as<uint32_t>(),
+                                  r->ckpt.as<float4>(), r->items.as<uint4>(), ctl, r->rec_bits.as<uint32_t>(),
+                                  r->rec_mask.as<uint32_t>(), r->rec_count.as<uint32_t>(),
+                                  r->first_slot.as<uint32_t>(), r->records.as<float4>(),
+                                  densification_info != nullptr, s);
     }
     r->bwd_queues_clear = false;
     TGS_CHECK_LAUNCH();
@@ -712,7 +731,9 @@ int tgs_rasterizer_backward_ex(tgs_rasterizer* r, const void* grad_image, const 
     {
         StageScope sc(ST_PREB, s);
         launch_preprocess_backward(view_of(r->g), cam, r->n_touched.as<uint32_t>(), r->conic_opacity.as<float4>(),
-                                   r->rec_count.as<uint32_t>(), r->first_slot.as<uint32_t>(), r->records.as<float4>(),
+                                   r->rec_count.as<uint32_t>(), r->rec_mask.as<uint32_t>(),
+                                   r->rec_bits.as<uint32_t>(), r->tile_sort_cap,
+                                   r->first_slot.as<uint32_t>(), r->records.as<float4>(),
                                    r->grad2d.as<float>(), gv, (float*)densification_info, mode,
                                    r->row_mask.as<uint8_t>(), r->live.as<uint4>(), r->heavy.as<uint4>(),
                                    pose ? r->pose_partial.as<float>() : nullptr,
@@ -818,6 +839,8 @@ int tgs_rasterizer_debug_view(tgs_rasterizer* r, tgs_debug_view* out) {
     out->image_dtype = r->fgs16 ? TGS_DTYPE_FLOAT16 : TGS_DTYPE_FLOAT32;
     out->first_slot = r->first_slot.as<uint32_t>();
     out->records = r->records.as<float>();
+    out->instance_ranks = r->fgs16 ? nullptr : r->iranks.as<uint16_t>();
+    out->record_bits = r->fgs16 ? nullptr : r->rec_bits.as<uint32_t>();
     return TGS_OK;
 }
 

@@ -126,11 +126,19 @@ int64_t radix_count_entries(int64_t max_n, bool depth);
 // writes no sorted keys (launch_keys_from_ranges restores them from the
 // ranges). Without *ranges_done the caller runs launch_tile_ranges on the
 // sorted keys.
+// ranks (tile sort, with ranges): the last pass also writes ranks[o] = the
+// key's bits 16..31 of sorted position o (the emission's per-primitive
+// instance rank on fp32 images; the tile is then the key's sorted bits).
+// clear_bits (tile sort): the first pass's upsweep zeroes
+// record_bit_words(max_n) words there (one bit per instance position).
 int radix_sort(uint32_t* keys[2], uint32_t* vals[2], uint32_t* v2[2], const uint32_t* d_n, int64_t max_n, bool depth,
                int n_passes, const int* shifts, const int* bits, uint32_t* counts, uint32_t* tickets,
                uint64_t* status, const uint32_t* epoch_base, uint32_t& epoch, uint32_t* err,
                const uint32_t* first_block_n, uint32_t* offs, bool* offs_done, uint2* ranges, uint32_t n_tiles,
-               bool* ranges_done, hipStream_t s);
+               bool* ranges_done, uint16_t* ranks, uint32_t* clear_bits, hipStream_t s);
+// Words of the record-bit array for up to max_inst instances (whole
+// workgroups of the tile sort's first upsweep).
+int64_t record_bit_words(int64_t max_inst);
 // Instances in depth order: thread per depth-sorted primitive k < ctl->V,
 // slots [offs[k], offs[k + 1]).
 // Rect tiles past the first 32 take the exact tile test with mean2d[p], the
@@ -207,21 +215,28 @@ void launch_blend_forward(const CamParams& cam, uint2* ranges, const uint32_t* i
                           uint32_t* tile_max, uint32_t* tile_loaded, float4* ckpt, uint4* items, BinCtl* ctl,
                           hipStream_t s);
 // 2D gradient records: each (primitive p, bucket) the backward processes
-// takes record index first_slot[p] + atomicAdd(rec_count[p], 1) (below
-// first_slot[p] + n_touched[p]: a primitive is in a tile's list once) and
-// writes 12 floats there: dL/dmean2d (2), |.| sums (2; 0 unless with_abs:
-// only densification reads them), dL/dconic (3),
+// writes 12 floats at record index first_slot[p] + k, k the instance's rank
+// among p's instances (inst_ranks, from the tile sort; below n_touched[p]: a
+// primitive is in a tile's list once), marks it (bit k of rec_mask[p] for
+// k < 32, zero between backwards; bit first_slot[p] + k of rec_bits, cleared
+// by the forward's tile sort, otherwise) and counts it in rec_count[p] (zero
+// between backwards): dL/dmean2d (2), |.| sums
+// (2; 0 unless with_abs: only densification reads them), dL/dconic (3),
 // dL/dcolour (3), sum of alpha dL/dalpha, 0. The preprocess backward sums
-// each primitive's records (16 lanes per primitive above kLightRecords of
-// them, into grad2d[12 p]; the thread of the primitive itself otherwise) and
-// clears rec_count. 16 measured faster than 4, 8 and 32 at config 3.
+// each primitive's marked records in a fixed order: in rank order in the
+// primitive's own thread up to kLightRecords of them, otherwise 16 lanes,
+// lane l summing (in rank order) the primitive's records l, l + 16, ...,
+// then an xor butterfly over the 16 lane sums (into grad2d[12 p]). 16 measured
+// faster than 4, 8 and 32 at config 3. (The fp16-image backward packs its
+// records at first_slot[p] + a counter: its sums are exact, in any order.)
 constexpr uint32_t kLightRecords = 16;
 // ctl->bwd_queue must be zero on entry (the forward's control reset clears it).
-void launch_blend_backward(const CamParams& cam, const uint32_t* inst_vals, const float2* mean2d,
-                           const float4* conic_opacity, const float4* color_pt, const float* image,
-                           const float* grad_image, const uint32_t* n_contrib, const float4* ckpt,
-                           const uint4* items, BinCtl* ctl, uint32_t* rec_count, const uint32_t* first_slot,
-                           float4* records, bool with_abs, hipStream_t s);
+void launch_blend_backward(const CamParams& cam, const uint32_t* inst_vals, const uint16_t* inst_ranks,
+                           const float2* mean2d, const float4* conic_opacity, const float4* color_pt,
+                           const float* image, const float* grad_image, const uint32_t* n_contrib, const float4* ckpt,
+                           const uint4* items, BinCtl* ctl, uint32_t* rec_bits, uint32_t* rec_mask,
+                           uint32_t* rec_count, const uint32_t* first_slot, float4* records, bool with_abs,
+                           hipStream_t s);
 
 // ---- preprocess backward (kernels_backward.cuh:88-352)
 // mode: 0 accumulate, 1 assign, 2 sparse (assign rows with gradient, write
@@ -230,11 +245,16 @@ enum { kGradAccumulate = 0, kGradAssign = 1, kGradSparse = 2 };
 // Scratch: live and heavy (n uint4 each) lists of the primitives with
 // records, grad2d (12 n floats).
 int64_t pb_chunks(int64_t n);
+// Records are counted by rec_count (cleared here for the next backward) and
+// on fp32 images marked by rec_mask (cleared here) and rec_bits.
+// slot_limit: the instance capacity of the forward (records lie below it).
 void launch_preprocess_backward(const GaussianView& g, const CamParams& cam, const uint32_t* n_touched,
-                                const float4* conic_opacity, uint32_t* rec_count, const uint32_t* first_slot,
-                                const float4* records, float* grad2d, const GradView& out, float* densif, int mode,
-                                uint8_t* row_mask, uint4* live, uint4* heavy, float* pose_partial, float* pose_out,
-                                bool keep2d, bool half_sums, hipStream_t s);
+                                const float4* conic_opacity, uint32_t* rec_count, uint32_t* rec_mask,
+                                const uint32_t* rec_bits,
+                                int64_t slot_limit, const uint32_t* first_slot, const float4* records, float* grad2d,
+                                const GradView& out, float* densif, int mode, uint8_t* row_mask, uint4* live,
+                                uint4* heavy, float* pose_partial, float* pose_out, bool keep2d, bool half_sums,
+                                hipStream_t s);
 
 // ---- PSNR (psnr.cu:72-128): scratch[psnr_scratch_doubles() - 1] receives the
 // sum of (saturate(pred) - target)^2 over the n_padded elements

@@ -131,7 +131,7 @@ int morton_order(const float* means, int64_t n, uint32_t* indices, uint32_t* scr
     uint32_t epoch = 0;
     const int sel = radix_sort(keys, vals, nullptr, nullptr, n, true, 4, shifts, bits, counts,
                                ctl->tickets + kTicketDepth, status, &ctl->epoch_base, epoch, &ctl->err, nullptr,
-                               nullptr, nullptr, nullptr, 0u, nullptr, s);
+                               nullptr, nullptr, nullptr, 0u, nullptr, nullptr, nullptr, s);
     if (sel < 0) return -1;
     // (a failed copy surfaces at the caller's error check after the wait)
     (void)hipMemcpyAsync(indices, vals[sel], sizeof(uint32_t) * (size_t)n, hipMemcpyDeviceToDevice, s);

@@ -311,10 +311,13 @@ __device__ __forceinline__ void hs_result(const HalfSums& h, float4& gA, float4&
 // visible primitives only count for densification (kernels_backward.cuh:345
 // adds zero sums); sparse mode records the row mask; assign mode zeroes
 // every gradient row of the chunk (the live rows are overwritten by phase
-// 3). The chunk's live primitives, as (index, record count, first record
-// slot), and its heavy ones (more than kLightRecords records) are listed in
-// the chunk's own slice of the two lists: no device-wide counter (returning
-// atomics on one address serialise, about 10 ns each on MI355X).
+// 3). The chunk's live primitives and its heavy ones (more than
+// kLightRecords records) are listed in the chunk's own slice of the two
+// lists: no device-wide counter (returning atomics on one address
+// serialise, about 10 ns each on MI355X). Entries: fp32 images, live
+// (index, min(count, kLightRecords + 1) | span << 5, first slot, mask word of
+// ranks 0..31) and heavy (index, first slot + span, first slot, mask word);
+// fp16 images (index, count, first slot, 0) in both lists.
 constexpr int kClassRounds = 8;
 constexpr int kClassChunk = 256 * kClassRounds;
 
@@ -328,28 +331,43 @@ __device__ __forceinline__ void zero_run(float* __restrict__ dst, int64_t n) {
     for (int64_t e = (nv << 2) + threadIdx.x; e < n; e += 256) dst[e] = 0.f;
 }
 
-__device__ __forceinline__ void classify_chunk(int64_t n, const uint32_t* __restrict__ n_touched,
-                                               const uint32_t* __restrict__ rec_count,
-                                               const uint32_t* __restrict__ first_slot, float4* __restrict__ densif,
-                                               int mode, uint8_t* __restrict__ row_mask, const GradView& out,
-                                               uint4* __restrict__ live, uint4* __restrict__ heavy, uint32_t* s_rw,
-                                               uint32_t& n_live, uint32_t& n_heavy) {
+template <bool kHalf>
+__device__ __forceinline__ void classify_chunk(int64_t n, const uint32_t* __restrict__ rec_count,
+                                               const uint32_t* __restrict__ rec_mask,
+                                               const uint32_t* __restrict__ first_slot, const uint32_t* n_touched,
+                                               float4* __restrict__ densif, int mode, uint8_t* __restrict__ row_mask,
+                                               const GradView& out, uint4* __restrict__ live,
+                                               uint4* __restrict__ heavy, uint32_t slot_limit, uint32_t* s_rw,
+                                               uint32_t& n_live,
+                                               uint32_t& n_heavy) {
     const uint32_t t = threadIdx.x;
     const int64_t c0 = (int64_t)blockIdx.x * kClassChunk;
     const int64_t base = c0 + t;
-    uint32_t nrec[kClassRounds], lv[kClassRounds], hv[kClassRounds], ex[kClassRounds], exh[kClassRounds];
+    uint32_t nrec[kClassRounds], msk[kClassRounds], lv[kClassRounds], hv[kClassRounds], ex[kClassRounds],
+        exh[kClassRounds];
 #pragma unroll
     for (int r = 0; r < kClassRounds; ++r) {
         const int64_t i = base + (int64_t)r * 256;
         nrec[r] = i < n ? rec_count[i] : 0u;
+        msk[r] = !kHalf && i < n ? rec_mask[i] : 0u;
         lv[r] = nrec[r] ? 1u : 0u;
         hv[r] = nrec[r] > kLightRecords ? 1u : 0u;
+    }
+    // first slots of the live primitives, tile counts of the fp32 live ones
+    // (their entries carry the span of their slots) and, for densification,
+    // of the dead ones: all loads issued together
+    uint32_t fsr[kClassRounds], ntr[kClassRounds];
+#pragma unroll
+    for (int r = 0; r < kClassRounds; ++r) {
+        const int64_t i = base + (int64_t)r * 256;
+        fsr[r] = lv[r] ? first_slot[i] : 0u;
+        ntr[r] = i < n && ((!kHalf && lv[r]) || (densif && !nrec[r])) ? n_touched[i] : 0u;
     }
     if (densif) {
 #pragma unroll
         for (int r = 0; r < kClassRounds; ++r) {
             const int64_t i = base + (int64_t)r * 256;
-            if (i < n && !nrec[r] && n_touched[i] != 0u) densif[i].x += 1.0f;
+            if (i < n && !nrec[r] && ntr[r] != 0u) densif[i].x += 1.0f;
         }
     }
     if (mode == kGradSparse) {
@@ -374,22 +392,115 @@ __device__ __forceinline__ void classify_chunk(int64_t n, const uint32_t* __rest
     for (int r = 0; r < kClassRounds; ++r) {
         const uint32_t i = (uint32_t)(base + (int64_t)r * 256);
         if (lv[r]) {
-            const uint4 entry = make_uint4(i, nrec[r], first_slot[i], 0u);
-            live[c0 + ex[r]] = entry;
-            if (hv[r]) heavy[c0 + exh[r]] = entry;
+            const uint32_t fs = fsr[r];
+            if constexpr (kHalf) {
+                const uint4 entry = make_uint4(i, nrec[r], fs, 0u);
+                live[c0 + ex[r]] = entry;
+                if (hv[r]) heavy[c0 + exh[r]] = entry;
+            } else {
+                // the slots that can hold its records: [fs, fs + n_touched),
+                // cut at the instance capacity (a no-sync forward that outgrew
+                // it emitted no slot past it); spans are at most 65,536
+                const uint32_t span = fs < slot_limit ? min(ntr[r], slot_limit - fs) : 0u;
+                live[c0 + ex[r]] = make_uint4(i, min(nrec[r], kLightRecords + 1u) | (span << 5), fs, msk[r]);
+                if (hv[r]) heavy[c0 + exh[r]] = make_uint4(i, fs + span, fs, msk[r]);
+            }
         }
+    }
+}
+
+// Adds the records at the slots of the (up to) four lowest set bits of m
+// (bit i: slot base + off(i); off increasing) into v, in bit order, and
+// clears those bits; m must not be zero. The four loads are issued
+// unconditionally (a missing record re-reads the first one) so that they are
+// all in flight together; a record's adds are skipped when it is missing
+// (adding zero would turn a -0 sum into +0).
+template <typename Off>
+__device__ __forceinline__ void add_records4(const float4* __restrict__ records, uint32_t base, uint32_t& m,
+                                             float v[12], Off off) {
+    uint32_t sl[4];
+    bool on[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        on[u] = m != 0u;
+        sl[u] = on[u] ? base + off((uint32_t)__builtin_ctz(m)) : sl[0];
+        m &= m - 1u;   // (0 stays 0)
+    }
+    float4 a[4], b[4], d[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        const float4* src = records + 3 * (size_t)sl[u];
+        a[u] = src[0];
+        b[u] = src[1];
+        d[u] = src[2];
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+        if (on[u]) {
+            v[0] += a[u].x; v[1] += a[u].y; v[2] += a[u].z; v[3] += a[u].w;
+            v[4] += b[u].x; v[5] += b[u].y; v[6] += b[u].z; v[7] += b[u].w;
+            v[8] += d[u].x; v[9] += d[u].y; v[10] += d[u].z; v[11] += d[u].w;
+        }
+}
+struct SlotBit {   // bit i of a mask over consecutive slots
+    __device__ uint32_t operator()(uint32_t i) const { return i; }
+};
+struct SlotByteStride {   // bit 8 q + i of four slot bytes 16 apart: slot 128 q + i
+    __device__ uint32_t operator()(uint32_t i) const { return ((i >> 3) << 7) + (i & 7u); }
+};
+
+// Sums, in rank order, the records of the nr (at most 16) marked slots of a
+// primitive with marked-slot span [fs, fs + span) into v: ranks below 32
+// from its mask word m (slot fs + rank), the others (primitives over more
+// than 32 tiles only) from rec_bits over [fs + 32, fs + span).
+__device__ __forceinline__ void add_marked_light(const uint32_t* __restrict__ rec_bits,
+                                                 const float4* __restrict__ records, uint32_t fs, uint32_t m,
+                                                 uint32_t nr, uint32_t span, float v[12]) {
+    uint32_t taken = (uint32_t)__builtin_popcount(m);
+    const uint32_t a = fs + 32u, e = fs + span;
+    const bool more = taken < nr && a < e;
+    // slot words over [a, e), four loaded at a time (the first four before
+    // the mask ranks' records), until all nr are found
+    const uint32_t first = a >> 5, last = more ? (e - 1u) >> 5 : 0u;
+    const uint32_t head = ~0u << (a & 31u), tail = (e & 31u) ? (1u << (e & 31u)) - 1u : ~0u;
+    uint32_t mw[4];
+    auto load4 = [&](uint32_t w0) {
+#pragma unroll
+        for (uint32_t q = 0; q < 4u; ++q) mw[q] = more && w0 + q <= last ? rec_bits[w0 + q] : 0u;
+    };
+    load4(first);
+    while (m) add_records4(records, fs, m, v, SlotBit{});
+    for (uint32_t w0 = first; more && w0 <= last && taken < nr;) {
+#pragma unroll
+        for (uint32_t q = 0; q < 4u; ++q) {
+            const uint32_t w = w0 + q;
+            if (w == first) mw[q] &= head;
+            if (w == last) mw[q] &= tail;
+            taken += (uint32_t)__builtin_popcount(mw[q]);
+            while (mw[q]) add_records4(records, w << 5, mw[q], v, SlotBit{});
+        }
+        w0 += 4u;
+        if (w0 <= last && taken < nr) load4(w0);
     }
 }
 
 // ---- phase 2: 2D-gradient sums of the heavy primitives
 //
 // Sixteen lanes (one DPP row) per heavy primitive of the chunk, four per
-// wave: the lanes stride over the primitive's records, then a row
-// butterfly leaves the 12 sums in every lane of the row and lanes 0-2 of
-// the row store them to grad2d[12 p] in record layout.
+// wave. fp32 images: the record of rank k (slot fs + k) goes to lane k mod 16
+// for k < 32, and otherwise to lane (b - b_first) mod 16, where b = (fs + k)
+// / 8 is its 8-slot byte of the slot bits and b_first = (fs + 32) / 8; each
+// lane adds its records in rank order, and an xor butterfly (partners 8, 4,
+// 2, 1) then leaves the same 12 sums in every lane: a fixed order, whatever
+// order the buckets finished in. Lane l reads mask bits l and l + 16 and
+// slot bytes b_first + l + 16 q, four bytes and four records at a time.
+// fp16 images: the lanes stride over the packed records with exact sums.
+// Lanes 0-2 of the row store the sums to grad2d[12 p] in record layout.
 template <bool kHalf>
 __device__ __forceinline__ void gather_heavy_chunk(const uint4* __restrict__ list, uint32_t nh,
-                                                   const float4* __restrict__ records, float* __restrict__ grad2d) {
+                                                   const float4* __restrict__ records,
+                                                   const uint32_t* __restrict__ rec_bits,
+                                                   float* __restrict__ grad2d) {
     const uint32_t row = threadIdx.x >> 4, sub = threadIdx.x & 15u;
     for (uint32_t h0 = 0; h0 < nh; h0 += 16u) {
         const uint32_t h = h0 + row;
@@ -435,37 +546,45 @@ __device__ __forceinline__ void gather_heavy_chunk(const uint4* __restrict__ lis
         float v[12];
 #pragma unroll
         for (int q = 0; q < 12; ++q) v[q] = 0.f;
-        uint32_t r = sub;
-        for (; r + 48u < e.y; r += 64u) {   // four strides' loads issued together; the same order of adds
-            float4 a[4], b[4], d[4];
+        if (on) {
+            // e.y: the end of the primitive's marked slots, e.z its first slot
+            const uint32_t a0 = e.z + 32u;
+            const bool wide = e.y > a0;
+            const uint32_t bfirst = a0 >> 3, blast = wide ? (e.y - 1u) >> 3 : 0u;
+            const uint32_t head = (0xffu << (a0 & 7u)) & 0xffu, tail = (e.y & 7u) ? (1u << (e.y & 7u)) - 1u : 0xffu;
+            // bytes b0 + 16 q (q < 4) as one mask: bit 8 q + i is slot 8 (b0 + 16 q) + i
+            // (the first four loaded before the mask ranks' records)
+            uint32_t wd[4];
+            auto load4 = [&](uint32_t b0) {
 #pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                const float4* src = records + 3 * (size_t)(e.z + r + 16u * (uint32_t)u);
-                a[u] = src[0];
-                b[u] = src[1];
-                d[u] = src[2];
+                for (uint32_t q = 0; q < 4u; ++q) {
+                    const uint32_t bb = b0 + 16u * q;
+                    wd[q] = wide && bb <= blast ? rec_bits[bb >> 2] : 0u;
+                }
+            };
+            load4(bfirst + sub);
+            uint32_t mm = ((e.w >> sub) & 1u) | (((e.w >> (sub + 16u)) & 1u) << 16);
+            if (mm) add_records4(records, e.z + sub, mm, v, SlotBit{});   // ranks sub, sub + 16
+            for (uint32_t b0 = bfirst + sub; wide && b0 <= blast;) {
+                uint32_t m4 = 0;
+#pragma unroll
+                for (uint32_t q = 0; q < 4u; ++q) {
+                    const uint32_t bb = b0 + 16u * q;
+                    uint32_t byte = (wd[q] >> (8u * (bb & 3u))) & 0xffu;
+                    if (bb == bfirst) byte &= head;
+                    if (bb == blast) byte &= tail;
+                    m4 |= byte << (8u * q);
+                }
+                const uint32_t base = b0 << 3;
+                b0 += 64u;
+                if (b0 <= blast) load4(b0);
+                while (m4) add_records4(records, base, m4, v, SlotByteStride{});
             }
+        }
+        // a + b == b + a: both partners of each step hold the same sum after it
+        for (int m = 8; m >= 1; m >>= 1)
 #pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                v[0] += a[u].x; v[1] += a[u].y; v[2] += a[u].z; v[3] += a[u].w;
-                v[4] += b[u].x; v[5] += b[u].y; v[6] += b[u].z; v[7] += b[u].w;
-                v[8] += d[u].x; v[9] += d[u].y; v[10] += d[u].z; v[11] += d[u].w;
-            }
-        }
-        for (; r < e.y; r += 16u) {
-            const float4* src = records + 3 * (size_t)(e.z + r);
-            const float4 a = src[0], b = src[1], d = src[2];
-            v[0] += a.x; v[1] += a.y; v[2] += a.z; v[3] += a.w;
-            v[4] += b.x; v[5] += b.y; v[6] += b.z; v[7] += b.w;
-            v[8] += d.x; v[9] += d.y; v[10] += d.z; v[11] += d.w;
-        }
-#pragma unroll
-        for (int q = 0; q < 12; ++q) {
-            v[q] += dpp_f32<0x128>(v[q]);   // row_ror:8
-            v[q] += dpp_f32<0x124>(v[q]);   // row_ror:4
-            v[q] += dpp_f32<0x122>(v[q]);   // row_ror:2
-            v[q] += dpp_f32<0x121>(v[q]);   // row_ror:1
-        }
+            for (int q = 0; q < 12; ++q) v[q] += __shfl_xor(v[q], m, 16);
         if (on && sub < 3u) {
             float4* g = (float4*)(grad2d + (size_t)e.x * kGradStride);
             const float4 f = sub == 0u ? make_float4(v[0], v[1], v[2], v[3])
@@ -527,17 +646,19 @@ __global__ void __launch_bounds__(256) preprocess_backward_chunk_kernel(
     uint8_t* __restrict__ row_mask, uint4* __restrict__ live, uint4* __restrict__ heavy,
     const float* __restrict__ means, const float* __restrict__ scales, const float* __restrict__ rots,
     const ShT* __restrict__ shr_all, int bases, CamParams cam, const float4* __restrict__ conic_opacity,
-    uint32_t* __restrict__ rec_count, const float4* __restrict__ records, float* grad2d,
-    GradView out, float4* __restrict__ densif, int mode, float* __restrict__ pose_partial, float* keep2d) {
+    uint32_t* __restrict__ rec_count, uint32_t* __restrict__ rec_mask, const uint32_t* __restrict__ rec_bits,
+    uint32_t slot_limit, const float4* __restrict__ records, float* grad2d, GradView out,
+    float4* __restrict__ densif, int mode, float* __restrict__ pose_partial, float* keep2d) {
     __shared__ uint32_t s_rw[4 * kClassRounds];
     __shared__ uint2 s_win[256 * kShWin];
     const uint32_t t = threadIdx.x;
     // phase 1: the chunk's lists; phase 2: its heavy primitives' sums into grad2d
     uint32_t nl, nh;
-    classify_chunk(n, n_touched, rec_count, first_slot, densif, mode, row_mask, out, live, heavy, s_rw, nl, nh);
+    classify_chunk<kHalf>(n, rec_count, rec_mask, first_slot, n_touched, densif, mode, row_mask, out, live, heavy,
+                          slot_limit, s_rw, nl, nh);
     __syncthreads();   // the lists (global, this chunk's slices) seen by the whole workgroup
     if (nh) {
-        gather_heavy_chunk<kHalf>(heavy + (size_t)blockIdx.x * kClassChunk, nh, records, grad2d);
+        gather_heavy_chunk<kHalf>(heavy + (size_t)blockIdx.x * kClassChunk, nh, records, rec_bits, grad2d);
         __syncthreads();   // grad2d rows of the heavy primitives
     }
     // phase 3
@@ -550,7 +671,7 @@ __global__ void __launch_bounds__(256) preprocess_backward_chunk_kernel(
     for (uint32_t g = t; g < nl; g += 256u) {
         const uint4 e = list[g];
         const int64_t ip = e.x;
-        const uint32_t nr = e.y;
+        const uint32_t nr = kHalf ? e.y : e.y & 31u;   // (fp32: the count, capped at kLightRecords + 1)
         float4 gA = make_float4(0.f, 0.f, 0.f, 0.f), gB = gA, gC = gA;
         if (nr > kLightRecords) {
             const float* gr = grad2d + (size_t)ip * kGradStride;
@@ -564,20 +685,26 @@ __global__ void __launch_bounds__(256) preprocess_backward_chunk_kernel(
             for (uint32_t r = 0; r < nr; ++r) hs_add(hs, rec[3 * r], rec[3 * r + 1], rec[3 * r + 2]);
             hs_result(hs, gA, gB, gC);
         } else {
-            const float4* rec = records + 3 * (size_t)e.z;
-            for (uint32_t r = 0; r < nr; ++r) {
-                const float4 a = rec[3 * r], b = rec[3 * r + 1], c = rec[3 * r + 2];
-                gA.x += a.x; gA.y += a.y; gA.z += a.z; gA.w += a.w;
-                gB.x += b.x; gB.y += b.y; gB.z += b.z; gB.w += b.w;
-                gC.x += c.x; gC.y += c.y; gC.z += c.z;
-            }
+            // the marked slots in slot (rank) order
+            float v[12];
+#pragma unroll
+            for (int q = 0; q < 12; ++q) v[q] = 0.f;
+            // (the thread's SH staging slot holds its slot list until the SH row is read)
+            add_marked_light(rec_bits, records, e.z, e.w, nr, e.y >> 5, v);
+            gA = make_float4(v[0], v[1], v[2], v[3]);
+            gB = make_float4(v[4], v[5], v[6], v[7]);
+            gC = make_float4(v[8], v[9], v[10], 0.f);
         }
         rec_count[ip] = 0u;
-        if (keep2d && nr <= kLightRecords) {   // the summed 2D gradients, for parity tests (heavy: already there)
+        if constexpr (!kHalf) rec_mask[ip] = 0u;
+        if (keep2d) {   // the summed 2D gradients, for parity tests (heavy: already there)
             float4* k2 = (float4*)(keep2d + (size_t)ip * kGradStride);
-            k2[0] = gA;
-            k2[1] = gB;
-            k2[2] = gC;
+            if (nr <= kLightRecords) {
+                k2[0] = gA;
+                k2[1] = gB;
+            }
+            // fp32: the 12th float carries the mask word of record ranks 0..31
+            k2[2] = make_float4(gC.x, gC.y, gC.z, kHalf ? gC.w : u2f(e.w));
         }
         float pm[3], ps[3], pq[4], shv[45];
 #pragma unroll
@@ -699,26 +826,32 @@ __global__ void __launch_bounds__(256) pose_reduce_kernel(const float* __restric
 template <typename ShT, bool kPose>
 static void launch_chunks(const GaussianView& g, int bases, const CamParams& cam, const uint32_t* n_touched,
                           const uint32_t* first_slot, uint8_t* row_mask, uint4* live, uint4* heavy,
-                          const float4* conic_opacity, uint32_t* rec_count, const float4* records, float* grad2d,
-                          const GradView& out, float* densif, int mode, float* pose_partial, bool keep2d,
-                          bool half_sums, unsigned chunks, hipStream_t s) {
+                          const float4* conic_opacity, uint32_t* rec_count, uint32_t* rec_mask,
+                          const uint32_t* rec_bits, uint32_t slot_limit, const float4* records, float* grad2d,
+                          const GradView& out,
+                          float* densif, int mode, float* pose_partial, bool keep2d, bool half_sums, unsigned chunks,
+                          hipStream_t s) {
     if (half_sums)
         preprocess_backward_chunk_kernel<ShT, kPose, true><<<chunks, 256, 0, s>>>(
             g.n, n_touched, first_slot, row_mask, live, heavy, g.means, g.scales, g.rotations,
-            (const ShT*)g.sh_rest, bases, cam, conic_opacity, rec_count, records, grad2d, out, (float4*)densif, mode,
-            pose_partial, keep2d ? grad2d : nullptr);
+            (const ShT*)g.sh_rest, bases, cam, conic_opacity, rec_count, rec_mask, rec_bits, slot_limit, records, grad2d,
+            out,
+            (float4*)densif, mode, pose_partial, keep2d ? grad2d : nullptr);
     else
         preprocess_backward_chunk_kernel<ShT, kPose, false><<<chunks, 256, 0, s>>>(
             g.n, n_touched, first_slot, row_mask, live, heavy, g.means, g.scales, g.rotations,
-            (const ShT*)g.sh_rest, bases, cam, conic_opacity, rec_count, records, grad2d, out, (float4*)densif, mode,
-            pose_partial, keep2d ? grad2d : nullptr);
+            (const ShT*)g.sh_rest, bases, cam, conic_opacity, rec_count, rec_mask, rec_bits, slot_limit, records, grad2d,
+            out,
+            (float4*)densif, mode, pose_partial, keep2d ? grad2d : nullptr);
 }
 
 void launch_preprocess_backward(const GaussianView& g, const CamParams& cam, const uint32_t* n_touched,
-                                const float4* conic_opacity, uint32_t* rec_count, const uint32_t* first_slot,
-                                const float4* records, float* grad2d, const GradView& out, float* densif, int mode,
-                                uint8_t* row_mask, uint4* live, uint4* heavy, float* pose_partial, float* pose_out,
-                                bool keep2d, bool half_sums, hipStream_t s) {
+                                const float4* conic_opacity, uint32_t* rec_count, uint32_t* rec_mask,
+                                const uint32_t* rec_bits, int64_t slot_limit, const uint32_t* first_slot,
+                                const float4* records, float* grad2d,
+                                const GradView& out, float* densif, int mode, uint8_t* row_mask, uint4* live,
+                                uint4* heavy, float* pose_partial, float* pose_out, bool keep2d, bool half_sums,
+                                hipStream_t s) {
     if (g.n <= 0) {
         if (pose_out) launch_fill_u32((uint32_t*)pose_out, 0u, 16, s);
         return;
@@ -727,24 +860,25 @@ void launch_preprocess_backward(const GaussianView& g, const CamParams& cam, con
     const int bases = (g.sh_degree + 1) * (g.sh_degree + 1);
     const unsigned chunks = (unsigned)pb_chunks(g.n);
     const bool f16 = g.sh_dtype == kShF16;
+    const uint32_t lim = (uint32_t)std::min<int64_t>(std::max<int64_t>(slot_limit, 0), 0xffffffffll);
     if (pose_out) {
         if (f16)
             launch_chunks<__half, true>(g, bases, cam, n_touched, first_slot, row_mask, live, heavy, conic_opacity,
-                                        rec_count, records, grad2d, out, densif, mode, pose_partial, keep2d,
+                                        rec_count, rec_mask, rec_bits, lim, records, grad2d, out, densif, mode, pose_partial, keep2d,
                                         half_sums, chunks, s);
         else
             launch_chunks<float, true>(g, bases, cam, n_touched, first_slot, row_mask, live, heavy, conic_opacity,
-                                       rec_count, records, grad2d, out, densif, mode, pose_partial, keep2d, half_sums,
-                                       chunks, s);
+                                       rec_count, rec_mask, rec_bits, lim, records, grad2d, out, densif, mode, pose_partial, keep2d,
+                                       half_sums, chunks, s);
         pose_reduce_kernel<<<1, 256, 0, s>>>(pose_partial, (int64_t)chunks, pose_out);
     } else if (f16) {
         launch_chunks<__half, false>(g, bases, cam, n_touched, first_slot, row_mask, live, heavy, conic_opacity,
-                                     rec_count, records, grad2d, out, densif, mode, nullptr, keep2d, half_sums, chunks,
-                                     s);
+                                     rec_count, rec_mask, rec_bits, lim, records, grad2d, out, densif, mode, nullptr, keep2d,
+                                     half_sums, chunks, s);
     } else {
         launch_chunks<float, false>(g, bases, cam, n_touched, first_slot, row_mask, live, heavy, conic_opacity,
-                                    rec_count, records, grad2d, out, densif, mode, nullptr, keep2d, half_sums, chunks,
-                                    s);
+                                    rec_count, rec_mask, rec_bits, lim, records, grad2d, out, densif, mode, nullptr, keep2d,
+                                    half_sums, chunks, s);
     }
 }
 

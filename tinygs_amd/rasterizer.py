@@ -197,22 +197,35 @@ class FastGSRasterizer(RasterizerBase):
                 "absgrad": np.ascontiguousarray(g[:, 2:4]).reshape(-1),
                 "grad_conic": np.ascontiguousarray(g[:, 4:7]).reshape(-1),
                 "grad_color": np.ascontiguousarray(g[:, 7:10]).reshape(-1),
-                "alpha_sum": np.ascontiguousarray(g[:, 10])}
+                "alpha_sum": np.ascontiguousarray(g[:, 10]),
+                # fp32 images: each primitive's marks of written records of ranks 0..31
+                "record_masks": np.ascontiguousarray(g[:, 11]).view(np.uint32)}
 
     def debug_records(self) -> dict:
         """First record slot per primitive and the 2D-gradient records of the
-        last backward (12 floats per instance slot; tests only)."""
+        last backward (12 floats per instance slot); with fp32 images also
+        each sorted instance's rank among its primitive's instances and the
+        bits of the written record slots (tests only)."""
         import torch
         dv = _lib.tgs_debug_view()
         _lib.check(_lib.load().tgs_rasterizer_debug_view(self._h, C.byref(dv)), "debug_view")
         n = self.m_gaussians.size()
+        I = int(dv.n_instances)
         dev = self.m_gaussians.means().device
         fs = torch.empty(max(n, 1), dtype=torch.int32, device=dev)
-        rec = torch.empty(12 * max(int(dv.n_instances), 1), dtype=torch.float32, device=dev)
+        rec = torch.empty(12 * max(I, 1), dtype=torch.float32, device=dev)
         _lib.copy_device(dv.first_slot, fs.numel() * 4, fs)
         _lib.copy_device(dv.records, rec.numel() * 4, rec)
-        return {"first_slot": fs.cpu().numpy().view(np.uint32)[:n],
-                "records": rec.cpu().numpy()[: 12 * int(dv.n_instances)].reshape(-1, 12)}
+        out = {"first_slot": fs.cpu().numpy().view(np.uint32)[:n],
+               "records": rec.cpu().numpy()[: 12 * I].reshape(-1, 12)}
+        if dv.instance_ranks:
+            rk = torch.empty(max(I, 1), dtype=torch.int16, device=dev)
+            bits = torch.empty(max((I + 31) // 32, 1), dtype=torch.int32, device=dev)
+            _lib.copy_device(dv.instance_ranks, rk.numel() * 2, rk)
+            _lib.copy_device(dv.record_bits, bits.numel() * 4, bits)
+            out["ranks"] = rk.cpu().numpy().view(np.uint16)[:I]
+            out["bits"] = bits.cpu().numpy().view(np.uint32)[: (I + 31) // 32]
+        return out
 
     def debug_n_contrib(self, shape) -> "object":
         import torch
