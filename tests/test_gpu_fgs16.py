@@ -128,11 +128,15 @@ def test_fgs16_backward_records_and_sums(hip, orc, case, gscale):
     scene = CASES[case]
     run = _render16(scene)
     pre, bins, fwd = _check_forward(scene, orc, run)
+    _check_backward(scene, orc, run, pre, bins, fwd, gscale)
+
+
+def _check_backward(scene, orc, run, pre, bins, fwd, gscale):
     shape = scene.camera.shape
     g32 = scenes.grad_image(7, shape, scale=gscale)
     grad_h = g32.astype(np.float16).view(np.uint16)
     grads = _backward16(run, grad_h)
-    print(f"[fgs16] backward {case} gscale={gscale}", flush=True)
+    print(f"[fgs16] backward {scene.name} gscale={gscale}", flush=True)
     ob = orc.h_blend_backward(scene, pre, bins, fwd, grad_h)
     rec_o, has = ob["records"], ob["has"].astype(bool)
     J = np.nonzero(has)[0]
@@ -172,6 +176,72 @@ def test_fgs16_backward_records_and_sums(hip, orc, case, gscale):
         bad = grads[key] != c
         assert not bad.any(), (key, int(bad.sum()), grads[key][bad][:5], c[bad][:5])
     print("[fgs16] sums and gradient chain equal", flush=True)
+
+
+def _with_camera(s, width, height, f):
+    cam = scenes.Camera(width, height, f, f, width / 2.0, height / 2.0, s.camera.w2c)
+    return scenes.Scene(s.means, s.scales, s.rotations, s.opacities, s.sh0, s.sh_rest, s.sh_degree, cam,
+                        np.zeros(cam.shape.padded_size, np.float32), s.name + f"_{width}x{height}", s.sh_dtype)
+
+
+def test_fgs16_grid_beyond_65536_tiles(hip, orc):
+    """5000 x 4000: 313 x 250 = 78,250 tiles. The fp16 path sorts 32-bit tile
+    keys (fastgs_ours_fp16/kernels_forward.cuh:622-623, forward.cu:205-211),
+    here 17 bits in three passes; forward and backward bit-exact."""
+    s = _with_camera(scenes.config1(seed=5, n=1500), 5000, 4000, 4000.0)
+    run = _render16(s)
+    assert run["dv"]["n_tiles"] == 78250
+    pre, bins, fwd = _check_forward(s, orc, run)
+    assert int((bins["inst_tile"] >= 65536).sum()) > 10_000   # keys past 16 bits, sorted and reduced
+    _check_backward(s, orc, run, pre, bins, fwd, None)
+
+
+def test_fgs16_config2_full_size(hip, orc):
+    """BASELINE config 2 at full size (100k Gaussians, 800 x 800, SH 3)."""
+    s = scenes.config2()
+    run = _render16(s)
+    pre, bins, fwd = _check_forward(s, orc, run)
+    _check_backward(s, orc, run, pre, bins, fwd, None)
+
+
+def test_fgs16_config3_geometry(hip, orc):
+    """The config-3 geometry the fp16 path is timed on (1M Gaussians,
+    1920 x 1080, SH 3 stored as fp16): binning, pixels, counts and tile
+    maxima bit-exact."""
+    s = scenes.config3()
+    run = _render16(s)
+    _check_forward(s, orc, run)
+
+
+def saturating_tile_scene(n=70_000, seed=3):
+    """32 x 32 pixels (2 x 2 tiles); n small Gaussians near pixel (3, 3) of
+    tile 0, all in that tile only. Their footprint (about 0.6 px standard
+    deviation) leaves the tile's far pixels at alpha 0 in half arithmetic, so
+    those pixels process every Gaussian until their 16-bit count saturates at
+    65,535 (fastgs_ours_fp16/kernels_forward.cuh:1104-1115)."""
+    rng = np.random.default_rng(seed)
+    w2c = np.eye(4)
+    w2c[2, 3] = 3.0
+    cam = scenes.Camera(32, 32, 32.0, 32.0, 16.0, 16.0, w2c)
+    x0 = (3.0 - 16.0) * 3.0 / 32.0
+    means = np.stack([x0 + rng.uniform(-0.01, 0.01, n), x0 + rng.uniform(-0.01, 0.01, n),
+                      rng.uniform(-0.5, 0.5, n)], 1).astype(np.float32)
+    scales = np.full((n, 3), np.log(0.02), np.float32)
+    rots = np.tile(np.array([1.0, 0.0, 0.0, 0.0], np.float32), (n, 1))
+    opac = rng.normal(0.0, 0.5, n).astype(np.float32)
+    sh0 = rng.uniform(0.0, 1.0, (n, 3)).astype(np.float32)
+    sh_rest = np.zeros((n, 15, 3), np.float32)
+    return scenes.Scene(means, scales, rots, opac, sh0, sh_rest, 0, cam,
+                        np.zeros(cam.shape.padded_size, np.float32), "saturating_tile")
+
+
+def test_fgs16_saturating_count(hip, orc):
+    s = saturating_tile_scene()
+    run = _render16(s)
+    pre, bins, fwd = _check_forward(s, orc, run)
+    assert bins["ranges"].reshape(-1, 2)[0, 1] - bins["ranges"].reshape(-1, 2)[0, 0] == s.n   # all in tile 0
+    assert int(fwd["n_contrib"].max()) == 0xffff and int(run["n_contrib"].max()) == 0xffff
+    _check_backward(s, orc, run, pre, bins, fwd, None)
 
 
 def test_fgs16_half_division_correctly_rounded(hip):

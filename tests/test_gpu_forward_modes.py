@@ -1,8 +1,10 @@
 """Forward entry checks and the forward that does not wait for its counts.
 
-* A tile grid beyond the 65,536 tiles of the reference's 16-bit tile keys
-  (kernels_forward.cuh:477,521; forward.cu:214) is refused before anything is
-  launched; the largest allowed grid renders like the oracle.
+* fp32 images: a tile grid beyond the 65,536 tiles of the reference's 16-bit
+  tile keys (kernels_forward.cuh:477,521; forward.cu:214) is refused before
+  anything is launched; the largest allowed grid renders like the oracle.
+  (fp16 images sort 32-bit tile keys: tests/test_gpu_fgs16.py renders a
+  78,250-tile grid.)
 * TGS_FORWARD_NO_SYNC: same binning, pixels and gradients as the forward that
   waits, and a forward that outgrows its reserved instance capacity is
   reported by tgs_rasterizer_status without touching memory out of bounds.
@@ -24,7 +26,7 @@ def _with_camera(s, width, height, f):
                         np.zeros(cam.shape.padded_size, np.float32))
 
 
-def test_tile_grid_beyond_16_bit_keys_refused_before_launch(hip):
+def test_fp32_tile_grid_beyond_16_bit_keys_refused_before_launch(hip):
     import torch
     from tinygs_amd.core import GPUBatchInput, GPUGaussian3d, Image, RasterizeContext
     from tinygs_amd.rasterizer import create_rasterizer

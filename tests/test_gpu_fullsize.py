@@ -17,8 +17,8 @@ Bars (config-3 column of the baseline plan):
   2D gradients, exact; then (c) end to end, where the chain amplifies (a)'s
   per-record rounding by a Gaussian's anisotropy (rotations of needle-shaped
   Gaussians: bar 1e-3);
-* the gradients of a second backward after the same forward are bit-identical
-  to the first's;
+* the gradients of a second backward after the same forward, and of a whole
+  second iteration of a twin, are bit-identical to the first's;
 * SimpleAdam bit-exact given the GPU's gradients.
 The oracle runs on all host cores (its results do not depend on the count).
 """
@@ -83,11 +83,24 @@ def _run(scene, orc, sparse):
     grads = {"means": g.means(), "scales": g.scales(), "rotations": g.rotations(), "opacities": g.opacities(),
              "sh0": g.sh_coefficient_0(), "sh_rest": g.sh_coefficients_rest()}
     grads = {k: v.cpu().numpy().reshape(-1) for k, v in grads.items()}
-    # the same backward again: bit-identical gradients (a fixed summation order)
+    # the same backward again, and a whole second iteration (forward, loss,
+    # backward) of a twin: bit-identical gradients (a fixed summation order)
     ts.backward()
     torch.cuda.synchronize()
     for k, t in zip(grads, g.tensors()):
         assert np.array_equal(t.detach().cpu().numpy().reshape(-1).view(np.uint32), grads[k].view(np.uint32)), k
+    twin = TrainStep(scene, l1_weight=0.8, ssim_weight=0.2, eps=1e-15, shs_lr=5e-3, sparse_grads=sparse)
+    twin.zero()
+    twin.forward()
+    twin.losses_and_grad()
+    twin.backward()
+    torch.cuda.synchronize()
+    # (both start from zeroed gradient arrays, so the rows a sparse backward
+    # leaves unwritten agree too)
+    for k, t in zip(grads, twin.grads.tensors()):
+        got = t.detach().cpu().numpy().reshape(-1)
+        assert np.array_equal(got.view(np.uint32), grads[k].view(np.uint32)), ("twin", k)
+    del twin
     ts.optimize()
     torch.cuda.synchronize()
     theta = ts.params()

@@ -78,6 +78,9 @@ void release(DevBuf& b) {
 // ---- stage timing: HIP events recorded on the launch stream around the
 // stages selected by tgs_profiling_set (process-wide, single host thread).
 constexpr int kStageCount = 10;
+// Largest tile grid of fp16 images (27-bit tile keys: four sort passes of at
+// most 8 bits; ranges and tile maxima alone take 12 B per tile)
+constexpr uint32_t kMaxTiles16 = 1u << 27;
 const char* const kStageNames[kStageCount] = {
     "preprocess", "depth_sort", "emit_instances", "tile_sort", "blend_forward",
     "l1", "fused_ssim", "blend_backward", "preprocess_backward", "adam"};
@@ -391,7 +394,7 @@ static GaussianView view_of(const tgs_gaussians& g) {
 struct SortPlan {
     uint32_t key_base = 0;
     int n_dp = 4, dshift[4] = {0, 0, 0, 0}, dbits[4] = {0, 0, 0, 0};
-    int n_tp = 1, tshift[2] = {0, 0}, tbits[2] = {0, 0};
+    int n_tp = 1, tshift[4] = {0, 0, 0, 0}, tbits[4] = {0, 0, 0, 0};
 };
 
 static int plan_sorts(const CamParams& cam, SortPlan& sp) {
@@ -406,15 +409,18 @@ static int plan_sorts(const CamParams& cam, SortPlan& sp) {
         sp.dbits[p] = (key_bits + sp.n_dp - 1) / sp.n_dp;
         sp.dshift[p] = p * sp.dbits[p];
     }
-    // tile key bits: one pass up to 8 bits, else two passes of ceil(bits/2) and the rest
+    // tile key bits: passes of at most 8 bits, as even as possible (the
+    // earlier passes take the odd bits): 16 bits (65,536 tiles, the fp32
+    // limit) in two passes, up to 24 in three, up to 27 (fp16 images) in four
     const uint32_t T = cam.grid_w * cam.grid_h;
     int bits = 1;
-    while ((1u << bits) < T) ++bits;
-    sp.n_tp = bits <= 8 ? 1 : 2;
-    sp.tbits[0] = sp.n_tp == 1 ? bits : (bits + 1) / 2;
-    sp.tbits[1] = bits - (bits + 1) / 2;
-    sp.tshift[0] = 0;
-    sp.tshift[1] = sp.tbits[0];
+    while (bits < 32 && (1u << bits) < T) ++bits;
+    sp.n_tp = (bits + 7) / 8;
+    for (int p = 0, sh = 0; p < sp.n_tp; ++p) {
+        sp.tbits[p] = bits / sp.n_tp + (p < bits % sp.n_tp ? 1 : 0);
+        sp.tshift[p] = sh;
+        sh += sp.tbits[p];
+    }
     if (!radix_digits_fit(true, sp.n_dp, sp.dbits) || !radix_digits_fit(false, sp.n_tp, sp.tbits))
         return fail(TGS_ERR_UNSUPPORTED, "no radix digit plan for %d depth-key bits / %u tiles", key_bits, T);
     return TGS_OK;
@@ -434,12 +440,19 @@ static int rasterizer_forward(tgs_rasterizer* r, const tgs_camera* camera, void*
     hipStream_t s = (hipStream_t)stream;
     CamParams cam;
     TGS_TRY(build_camera(camera, cam));
-    const uint32_t T = cam.grid_w * cam.grid_h;
-    // instance tile keys are 16-bit in the reference (kernels_forward.cuh:477,521;
-    // forward.cu:214 sorts 16 bits), which caps the grid at 65,536 tiles
-    if ((uint64_t)cam.grid_w * cam.grid_h > 65536u)
+    const uint64_t T64 = (uint64_t)cam.grid_w * cam.grid_h;
+    // fp32 images: instance tile keys are 16-bit in the reference
+    // (kernels_forward.cuh:477,521; forward.cu:214 sorts 16 bits), which caps
+    // the grid at 65,536 tiles. fp16 images: 32-bit tile keys
+    // (fastgs_ours_fp16/kernels_forward.cuh:622-623, forward.cu:205-211);
+    // here up to kMaxTiles16 (2^27) tiles, four sort passes
+    if (!f16 && T64 > 65536u)
         return fail(TGS_ERR_UNSUPPORTED, "%ux%u tiles exceed the 65,536 tiles of 16-bit tile keys", cam.grid_w,
                     cam.grid_h);
+    if (f16 && T64 > kMaxTiles16)
+        return fail(TGS_ERR_UNSUPPORTED, "%ux%u tiles exceed the %u tiles of fp16-image tile keys", cam.grid_w,
+                    cam.grid_h, kMaxTiles16);
+    const uint32_t T = (uint32_t)T64;
     if (nosync && r->inst_cap <= 0)
         return fail(TGS_ERR_STATE, "TGS_FORWARD_NO_SYNC needs an instance capacity (tgs_rasterizer_reserve)");
     SortPlan sp;
@@ -632,7 +645,8 @@ int tgs_rasterizer_forward_ex(tgs_rasterizer* r, const tgs_camera* camera, void*
 
 int tgs_rasterizer_reserve(tgs_rasterizer* r, int64_t max_instances, int32_t grid_tiles, void* stream) {
     if (!r) return fail(TGS_ERR_INVALID, "rasterizer is NULL");
-    if (max_instances < 1 || max_instances > (int64_t)0xffffffffll || grid_tiles < 1 || grid_tiles > 65536)
+    if (max_instances < 1 || max_instances > (int64_t)0xffffffffll || grid_tiles < 1 ||
+        (uint32_t)grid_tiles > kMaxTiles16)
         return fail(TGS_ERR_INVALID, "reserve: %lld instances, %d tiles", (long long)max_instances, grid_tiles);
     hipStream_t s = (hipStream_t)stream;
     const void* before[5] = {r->ikeys[0].p, r->ivals[0].p, r->ckpt.p, r->items.p, r->records.p};

@@ -47,7 +47,7 @@ void launch_preprocess(const GaussianView& g, const CamParams& cam, uint32_t* n_
 // Device control block of the binning launches. Everything but `err` is
 // cleared at the start of every forward; err (look-back error flag) is
 // sticky so that a failure is reported by the next host check.
-enum { kTicketCompact = 0, kTicketOffsets = 1, kTicketDepth = 2, kTicketTile = 6, kTicketCount = 8 };
+enum { kTicketCompact = 0, kTicketOffsets = 1, kTicketDepth = 2, kTicketTile = 6, kTicketCount = 10 };
 constexpr int kBwdQueues = 64;   // backward work queues; item i belongs to queue i % kBwdQueues
 struct BinCtl {
     // epoch_base: look-back epochs of the current forward are epoch_base + k
@@ -58,7 +58,7 @@ struct BinCtl {
     uint32_t V, I, err, epoch_base;
     uint32_t tickets[kTicketCount];
     uint32_t n_items;                     // backward work items listed by the blend forward
-    uint32_t pad2[19];
+    uint32_t pad2[17];
     uint32_t bwd_queue[kBwdQueues * 32];  // next local index of queue q at [32 q] (one line each, from byte 128)
 };
 static_assert(offsetof(BinCtl, bwd_queue) == 128, "backward queue counters start on their own cache line");
