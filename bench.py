@@ -3,7 +3,8 @@ of the FastGS path at 1M Gaussians, 1920x1080, SH degree 3 with fp16 SH
 storage, on one MI355X, plus the HBM roofline of the
 dominant kernel and the CPU oracle's time on the same workload.
 
-  python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 3] [--no-cpu-baseline]
+  python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 3] [--image-dtype float32|float16]
+                  [--no-cpu-baseline]
   python bench.py --config 4 [--stress-counts N ...]   (fwd+bwd stress sweep, its own JSON line)
   python bench.py --config 5 [--train-iters K]          (the training loop, its own JSON line)
 
@@ -26,36 +27,48 @@ HBM_PEAK_GBS = 8000.0
 
 STAGES = ["preprocess", "depth_sort", "emit_instances", "tile_sort", "blend_forward", "l1", "fused_ssim",
           "blend_backward", "preprocess_backward", "adam"]
-# stages that are one kernel launch, and that kernel's symbol in rocprofv3 output
+# stages that are one kernel launch, and that kernel's symbol in rocprofv3
+# output, per image dtype (fp16 images: the FGS16 blend kernels)
 SINGLE_KERNEL = {"preprocess": "tgs::preprocess_kernel", "blend_forward": "tgs::blend_forward_kernel",
                  "l1": "tgs::l1_kernel", "blend_backward": "tgs::blend_backward_kernel",
                  "adam": "tgs::adam_kernel"}
-TRAFFIC_FILE = os.path.join(ROOT, "profiles", "hbm_traffic_config{}.md")
-COUNTERS_FILE = os.path.join(ROOT, "profiles", "counters_config{}.md")
+SINGLE_KERNEL16 = dict(SINGLE_KERNEL, preprocess="tgs::preprocess16_kernel",
+                       blend_forward="tgs::blend16_forward_kernel", blend_backward="tgs::blend16_backward_kernel")
+# committed counter summaries of this workload ({} = config, then "_fp16" for fp16 images)
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "hbm_traffic_config{}{}.md")
+COUNTERS_FILE = os.path.join(ROOT, "profiles", "counters_config{}{}.md")
 # VALU issue peak: one wave64 VALU instruction per CU per clock (4 SIMDs, 4
-# cycles each), 256 CUs at the 2.4 GHz peak engine clock
+# cycles each), 256 CUs at the 2.4 GHz peak engine clock. The engine clock
+# under load can sit below its peak, so the counter run's VALU-busy figure
+# (SQ_ACTIVE_INST_VALU over the GPU's own busy cycles) is printed beside it.
 VALU_PEAK_GINST_S = 256 * 2.4
-VALU_KERNELS = {"blend_forward": "tgs::blend_forward_kernel", "blend_backward": "tgs::blend_backward_kernel"}
 
 
-def measured_valu_insts(config, kernel):
-    """Wave-level VALU instructions per launch of `kernel` (SQ_INSTS_VALU)
-    from the committed counter summary of this workload, or None."""
-    path = COUNTERS_FILE.format(config)
+def _suffix(image_dtype):
+    return "_fp16" if image_dtype == "float16" else ""
+
+
+def measured_valu(config, kernel, image_dtype="float32"):
+    """(wave-level VALU instructions per launch (SQ_INSTS_VALU), VALU busy %)
+    of `kernel` from the committed counter summary of this workload, or
+    (None, None)."""
+    path = COUNTERS_FILE.format(config, _suffix(image_dtype))
     if not os.path.exists(path):
-        return None
+        return None, None
     for line in open(path):
         m = re.match(r"\|\s*`([^`]+)`\s*\|\s*([0-9.e+]+)\s*\|", line)
         if m and (m.group(1) == kernel or m.group(1).startswith(kernel + "<")):
-            return float(m.group(2))
-    return None
+            cells = [c.strip() for c in line.strip().strip("|").split("|")]
+            busy = float(cells[5].rstrip("%")) if len(cells) > 5 and cells[5].endswith("%") else None
+            return float(m.group(2)), busy
+    return None, None
 
 
-def measured_traffic(config, kernel):
+def measured_traffic(config, kernel, image_dtype="float32"):
     """HBM bytes per launch of `kernel` from the committed FETCH_SIZE /
     WRITE_SIZE summary of this workload (two rocprofv3 --pmc runs of this
     script, scaled by a copy of known size), or None if there is none."""
-    path = TRAFFIC_FILE.format(config)
+    path = TRAFFIC_FILE.format(config, _suffix(image_dtype))
     if not os.path.exists(path):
         return None
     for line in open(path):
@@ -73,7 +86,7 @@ def algorithmic_bytes(stage, c):
     formulas are the sparse ones with L = N."""
     N, V, I, T, P = c["N"], c["V"], c["I"], c["T"], c["P"]
     L = c["L"]
-    s, K, e = c["sh_bytes"], c["sh_bases"], 4
+    s, K, e = c["sh_bytes"], c["sh_bases"], c["image_bytes"]
     if stage == "preprocess":
         return 44 * N + 3 * K * s * V + 4 * N + 52 * V
     if stage == "blend_forward":
@@ -349,6 +362,9 @@ def main():
     ap.add_argument("--train-init", type=int, default=500_000, help="config 5: initial Gaussians")
     ap.add_argument("--train-gt", type=int, default=400_000, help="config 5: ground-truth Gaussians")
     ap.add_argument("--train-views", type=int, default=200, help="config 5: views")
+    ap.add_argument("--image-dtype", choices=["float32", "float16"], default="float32",
+                    help="config 1-3: image data type; float16 runs the fp16-image rasterizer (FGS16) and the fp16 "
+                         "losses, the reference's train_data_type float16")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="instead of the benchmark, run 5 device-to-device copies of MIB MiB (the known-size kernel "
@@ -382,7 +398,8 @@ def main():
     print(f"[bench] scene config{args.config}: N={scene.n} {scene.camera.width}x{scene.camera.height} "
           f"sh_degree={scene.sh_degree} sh_storage={scene.sh_dtype} (generated in {time.time() - t0:.1f}s)",
           file=sys.stderr, flush=True)
-    ts = TrainStep(scene, l1_weight=0.8, ssim_weight=0.2, eps=1e-15, shs_lr=5e-3)
+    f16 = args.image_dtype == "float16"
+    ts = TrainStep(scene, l1_weight=0.8, ssim_weight=0.2, eps=1e-15, shs_lr=5e-3, image_dtype=args.image_dtype)
     L = _lib.load()
     stream = torch.cuda.current_stream()
 
@@ -429,7 +446,9 @@ def main():
         live = scene.n
     counts = {"N": scene.n, "V": V, "I": I, "T": T, "P": cam.width * cam.height, "L": live,
               "I_f": fl.value, "I_b": bp.value,
-              "sh_bytes": 2 if scene.sh_dtype == "float16" else 4, "sh_bases": (scene.sh_degree + 1) ** 2}
+              "sh_bytes": 2 if scene.sh_dtype == "float16" else 4, "sh_bases": (scene.sh_degree + 1) ** 2,
+              "image_bytes": 2 if f16 else 4}
+    single = SINGLE_KERNEL16 if f16 else SINGLE_KERNEL
 
     print(f"[bench] {ms:.3f} ms/iter over {args.steps} steps; V={V} I={I} T={T} "
           f"I_f={counts['I_f']:.0f} I_b={counts['I_b']:.0f} gradient rows L={live}", file=sys.stderr)
@@ -443,17 +462,18 @@ def main():
         print(f"[bench] {name:22s} {t:8.4f} {gbs:8.1f} {100 * gbs / HBM_PEAK_GBS:6.1f}", file=sys.stderr)
     print(f"[bench] sum of stages {sum(r[1] for r in rows):.3f} ms", file=sys.stderr, flush=True)
 
-    dom = max((r for r in rows if r[0] in SINGLE_KERNEL), key=lambda r: r[1])
+    dom = max((r for r in rows if r[0] in single), key=lambda r: r[1])
     roofline = {"bound": "hbm", "kernel": dom[0], "achieved": round(dom[3], 2), "peak": HBM_PEAK_GBS,
                 "unit": "GB/s", "frac": round(dom[3] / HBM_PEAK_GBS, 4),
-                "traffic": measured_traffic(args.config, SINGLE_KERNEL[dom[0]]),
+                "traffic": measured_traffic(args.config, single[dom[0]], args.image_dtype),
                 "algorithmic_bytes": int(dom[2]), "avg_launch_ms": round(dom[1], 5)}
 
     # VALU roofline of the VALU-bound blend kernels: wave instructions per
-    # launch (counter summary) over the live launch time
+    # launch (counter summary) over the live launch time, and the counter
+    # run's own VALU-busy figure beside it
     valu = {}
-    for name, kern in VALU_KERNELS.items():
-        insts = measured_valu_insts(args.config, kern)
+    for name in ("blend_forward", "blend_backward"):
+        insts, busy = measured_valu(args.config, single[name], args.image_dtype)
         t = stage_ms[name]
         if insts is None or t <= 0:
             valu[name] = None
@@ -461,12 +481,13 @@ def main():
         ach = insts / (t * 1e-3) / 1e9
         valu[name] = {"bound": "valu", "achieved": round(ach, 1), "peak": VALU_PEAK_GINST_S,
                       "unit": "G wave-instructions/s", "frac": round(ach / VALU_PEAK_GINST_S, 4),
-                      "insts_per_launch": insts, "avg_launch_ms": round(t, 5)}
+                      "insts_per_launch": insts, "avg_launch_ms": round(t, 5),
+                      "counter_valu_busy_pct": busy}
         print(f"[bench] {name}: {ach:.0f} G VALU wave-instructions/s = {100 * ach / VALU_PEAK_GINST_S:.1f}% of the "
-              f"issue peak", file=sys.stderr)
+              f"issue peak at 2.4 GHz; counter run VALU busy {busy}%", file=sys.stderr)
 
     cpu = None
-    if not args.no_cpu_baseline:
+    if not args.no_cpu_baseline and not f16:
         print(f"[bench] cpu baseline: full iterations of the CPU oracle on the same scene ({host_threads()} "
               "threads, then 1)", file=sys.stderr, flush=True)
         cpu = cpu_baseline(scene_fn, args.config)
@@ -477,10 +498,13 @@ def main():
     out = {
         "metric": METRIC, "value": round(ms, 4), "unit": "ms/iter", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": False, "scaling": "weak",
-        "vs_baseline": None, "dtype": "f32", "data": "synthetic",
-        "config": {"workload": f"config{args.config}: fwd + 0.8 L1 + 0.2 (1-SSIM) + bwd + SimpleAdam",
+        "vs_baseline": None, "dtype": "f16 images (half blending and losses), f32 geometry and Adam" if f16 else "f32",
+        "data": "synthetic",
+        "config": {"workload": f"config{args.config}: fwd + 0.8 L1 + 0.2 (1-SSIM) + bwd + SimpleAdam"
+                               + (", float16 images (FGS16)" if f16 else ""),
                    "n_gaussians": scene.n, "width": cam.width, "height": cam.height, "sh_degree": scene.sh_degree,
-                   "sh_storage": scene.sh_dtype, "n_visible": V, "n_instances": I, "n_tiles": T,
+                   "sh_storage": scene.sh_dtype, "image_dtype": args.image_dtype, "n_visible": V,
+                   "n_instances": I, "n_tiles": T,
                    "gradient_rows": live, "sparse_gradients": ts.sparse_grads,
                    "parallelism": "single GPU"},
         "stages_ms": {r[0]: round(r[1], 5) for r in rows},

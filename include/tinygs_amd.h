@@ -502,6 +502,15 @@ int tgs_selftest_half(int32_t op, const void* a, const void* b, const void* c, v
  * rounded quotient. out: device int64[8]: [0] mismatches, [1] pairs checked,
  * [2..4] a, b, quotient bits of one mismatch. Tests only. */
 int tgs_selftest_half_div_exhaustive(int64_t* out, void* stream);
+/* The FGS16 backward's division (fastgs_ours_fp16/kernels_backward.cuh
+ * __h2div(cadg, 1 - alpha)) is Markstein's iteration on the half reciprocal,
+ * correctly rounded for divisors in [0x1.4p-7, 1]. Checks it against the
+ * correctly rounded division for every half dividend and every positive
+ * divisor with bits in [b_lo, b_hi], and the half reciprocal against the
+ * correctly rounded one for those divisors. out (device int64[16]): [0]
+ * quotient mismatches, [1] reciprocal mismatches, [2..4] a, b, quotient of one
+ * mismatch. No counterpart in the reference. */
+int tgs_selftest_half_div_blend(int64_t* out, uint32_t b_lo, uint32_t b_hi, void* stream);
 /* Spin bound of the binning's look-back waits on the current device, for
  * tests of the error path: 0 makes every look-back that has a predecessor
  * give up at once (as a wait that ran out would), setting the look-back error

@@ -157,7 +157,7 @@ def _check_backward(scene, orc, run, pre, bins, fwd, gscale):
     a = by_j[J, :11].view(np.uint32)
     b = rec_o[J, :11].view(np.uint32)
     bad = a != b
-    assert not bad.any(), (int(bad.sum()), np.argwhere(bad)[:5], by_j[J][bad][:5], rec_o[J][bad][:5])
+    assert not bad.any(), (int(bad.sum()), np.argwhere(bad)[:5], by_j[J, :11][bad][:5], rec_o[J, :11][bad][:5])
     print(f"[fgs16] {J.size} records bit-exact", flush=True)
     # per-primitive sums
     g2d_gpu = run["r"].debug_grad2d()
@@ -256,6 +256,30 @@ def test_fgs16_half_division_correctly_rounded(hip):
     o = out.cpu().numpy()
     assert o[1] > 4_000_000_000, o   # pairs checked
     assert o[0] == 0, ("mismatches", o[0], "first a, b, q:", hex(int(o[2])), hex(int(o[3])), hex(int(o[4])))
+
+
+def test_fgs16_blend_division_correctly_rounded(hip):
+    """h2_div_blend, the backward's cadg / (1 - alpha) by Markstein's
+    iteration on the half reciprocal: equal to the correctly rounded quotient
+    (h_div, checked over all pairs above) for every half dividend and every
+    divisor 1 - alpha can take (alpha in [0, RN(0.99)]: bits 0x2100 ..
+    0x3c00); the half reciprocal equals the correctly rounded one for every
+    positive finite half."""
+    import torch
+    from tinygs_amd import _lib
+    L = _lib.load()
+    out = torch.zeros(16, dtype=torch.int64, device="cuda")
+    lo = int(np.float16(np.float16(1.0) - np.float16(0.99)).view(np.uint16))
+    assert lo == 0x2100
+    _lib.check(L.tgs_selftest_half_div_blend(out.data_ptr(), lo, 0x3c00, None), "division check")
+    torch.cuda.synchronize()
+    o = out.cpu().numpy()
+    assert o[0] == 0, ("quotient mismatches", o[0], hex(int(o[2])), hex(int(o[3])), hex(int(o[4])))
+    assert o[1] == 0, ("reciprocal mismatches", o[1])
+    out.zero_()
+    _lib.check(L.tgs_selftest_half_div_blend(out.data_ptr(), 0x0001, 0x7bff, None), "reciprocal check")
+    torch.cuda.synchronize()
+    assert int(out[1].item()) == 0, ("reciprocal mismatches over all positive halves", int(out[1].item()))
 
 
 # ---------------------------------------------------------------- fp16 losses

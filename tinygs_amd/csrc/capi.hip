@@ -1695,6 +1695,15 @@ int tgs_selftest_half_div_exhaustive(int64_t* out, void* stream) {
     return TGS_OK;
 }
 
+int tgs_selftest_half_div_blend(int64_t* out, uint32_t b_lo, uint32_t b_hi, void* stream) {
+    if (!out || b_lo == 0u || b_lo > b_hi || b_hi >= 0x7c00u) return fail(TGS_ERR_INVALID, "bad argument");
+    hipStream_t s = (hipStream_t)stream;
+    launch_fill_u32((uint32_t*)out, 0u, 16, s);
+    launch_half_div_blend_check((unsigned long long*)out, b_lo, b_hi, s);
+    TGS_CHECK_LAUNCH();
+    return TGS_OK;
+}
+
 int tgs_selftest_lookback_spins(uint32_t spins) {
     if (set_lookback_spin_limit(spins == 0xffffffffu ? (1u << 22) : spins) != 0)
         return fail(TGS_ERR_HIP, "look-back spin bound: %s", hipGetErrorString(hipGetLastError()));

@@ -15,11 +15,11 @@
 // bit-identical to it.
 //
 // MI355X mapping:
-//   * forward: one wave64 per tile. Lane L owns pixel L of each 8x8 block q
-//     of the tile, i.e. in-tile pixels 64 q + L, held as two half2 pairs
-//     (blocks 0, 1) and (2, 3); every image / count / checkpoint access of a
-//     block is one contiguous run. The tile's Gaussians are staged 64 at a
-//     time, one per lane, and broadcast to the wave with v_readlane (no LDS).
+//   * forward: two wave64s per tile. Wave k owns blocks 2k and 2k + 1 of
+//     the tile, lane L pixel L of each (in-tile pixels 64 q + L), held as
+//     one half2; every image / count / checkpoint access of a block is one
+//     contiguous run. Each wave stages the tile's Gaussians 64 at a time,
+//     one per lane, and broadcasts them with v_readlane (no LDS).
 //   * backward: one (tile, 32-Gaussian bucket) work item per half wave, two
 //     per wave. As in the reference, lane l of the half owns Gaussian l of the
 //     bucket and the tile's 128 pixel pairs stream through the lanes: at step
@@ -64,97 +64,118 @@ __device__ __forceinline__ h16x2 sel2(bool cx, bool cy, h16x2 a, h16x2 b) {
 
 // ---------------------------------------------------------------- forward
 
+namespace {
+typedef int16_t i16x2 __attribute__((ext_vector_type(2)));
+// 0xffff in each 16-bit half whose half value is negative (sign bit set)
+__device__ __forceinline__ uint32_t neg_mask16(h16x2 d) {
+    return __builtin_bit_cast(uint32_t, __builtin_bit_cast(i16x2, d) >> (i16x2){15, 15});
+}
+// m ? a : b, bit by bit
+__device__ __forceinline__ uint32_t bsel(uint32_t m, uint32_t a, uint32_t b) { return (a & m) | (b & ~m); }
+}  // namespace
+
 // info[p] = (conic a | b << 16, c | opacity << 16, r | g << 8 | b << 16, 0)
 // ckpt16: per slot 256 pixels of (C.r | C.g << 16, C.b | T << 16) halves, in-tile index 64 q + L.
+//
+// Two waves per tile (two tiles per 256-thread workgroup): wave k of a tile
+// owns blocks 2k and 2k + 1, lane L their pixel L as the two halves of a
+// half2, so a tile's pixels are split over two waves (the heaviest tiles set
+// the kernel's length). A pixel's state is (C, T) plus a 16-bit mask, all
+// ones while the pixel is unfinished: the accept test nT >= thr is the sign
+// of nT - thr (exact: a half difference is zero only for equal operands),
+// and the masks select T, the composited weight and the count with bit
+// operations. An unfinished pixel has processed every Gaussian so far, so
+// its count after Gaussian j is min(j + 1, 65535): one select per Gaussian,
+// and the saturation stop (:1115) is the same for every unfinished pixel.
 __global__ void __launch_bounds__(256) blend16_forward_kernel(
     CamParams cam, uint2* __restrict__ ranges, const uint32_t* __restrict__ inst_vals,
     const float2* __restrict__ mean2d, const uint4* __restrict__ info, uint16_t* __restrict__ image,
     uint16_t* __restrict__ n_contrib, uint32_t* __restrict__ tile_max, uint32_t* __restrict__ tile_loaded,
     uint2* __restrict__ ckpt, uint4* __restrict__ items, BinCtl* __restrict__ ctl) {
+    __shared__ uint32_t s_tmax[4], s_loaded[4];
     const uint32_t n_tiles = cam.grid_w * cam.grid_h;
-    const uint32_t tile = blockIdx.x * 4u + (threadIdx.x >> 6);
-    if (tile >= n_tiles) return;   // whole waves
-    const uint32_t lane = threadIdx.x & 63u;
-    const uint32_t gx = tile % cam.grid_w, gy = tile / cam.grid_w;
+    const uint32_t w = threadIdx.x >> 6, lane = threadIdx.x & 63u;
+    const uint32_t tile = blockIdx.x * 2u + (w >> 1), k = w & 1u;
+    const bool tile_ok = tile < n_tiles;   // (no early return: the workgroup meets at a barrier)
+    const uint32_t gx = tile_ok ? tile % cam.grid_w : 0u, gy = tile_ok ? tile / cam.grid_w : 0u;
     const uint32_t lx = lane & 7u, ly = lane >> 3;
 
     const h16 thr = h_rd(1e-4f * 255.0f);
     const h16x2 maxa = h2s((h16)0.99f), unscale = h2s(hfrom(kHUnscale)), h16c = h2s((h16)16.0f),
-                h05 = h2s((h16)0.5f), nlog2e = h2s(-(h16)1.4426950409f);
-    // pair 0: blocks 0, 1 (x + 8); pair 1: blocks 2, 3 (y + 8)
+                h05 = h2s((h16)0.5f), nlog2e = h2s(-(h16)1.4426950409f), nthr = h2s(-thr);
+    // .x: block 2k (in-tile column lx), .y: block 2k + 1 (column lx + 8); row 8k + ly
     const h16x2 offx = h2(offset_x(lx), offset_x(lx + 8u));
-    const h16x2 offy[2] = {h2s(offset_y(ly)), h2s(offset_y(ly + 8u))};
-    bool inside[4];
-#pragma unroll
-    for (uint32_t q = 0; q < 4; ++q) {
-        const uint32_t px = gx * 16u + (q & 1u) * 8u + lx, py = gy * 16u + (q >> 1) * 8u + ly;
-        inside[q] = px < cam.width && py < cam.height;
-    }
+    const h16x2 offy = h2s(offset_y(ly + 8u * k));
+    const uint32_t px0 = gx * 16u + lx, py = gy * 16u + 8u * k + ly;
+    const bool in0 = tile_ok && px0 < cam.width && py < cam.height;
+    const bool in1 = tile_ok && px0 + 8u < cam.width && py < cam.height;
 
-    uint2 range = ranges[tile];
+    uint2 range = tile_ok ? ranges[tile] : make_uint2(0u, 0u);
     // a failed binning scan (reported by the host) leaves partial instance
     // lists: every tile renders as empty instead of reading them
     if (ctl->err & (kErrLookBack | kErrOffsets)) range = make_uint2(0u, 0u);
     if (range.y == 0u) {   // an empty tile, left as (UINT32_MAX, 0) by the tile sort: stored as (0, 0)
         range.x = 0u;
-        if (lane == 0u) ranges[tile] = range;
+        if (tile_ok && k == 0u && lane == 0u) ranges[tile] = range;
     }
     const int32_t len = (int32_t)(range.y - range.x);
     const uint32_t slot0 = range.x / (uint32_t)kBucket + tile;
 
-    h16x2 C0[2], C1[2], C2[2], T[2];
-    uint32_t nc[4] = {0u, 0u, 0u, 0u};
-    bool unf[4];
-#pragma unroll
-    for (int k = 0; k < 2; ++k) {
-        C0[k] = C1[k] = C2[k] = h2s((h16)0.0f);
-        T[k] = h2s(hfrom(kH255));
-    }
-#pragma unroll
-    for (int q = 0; q < 4; ++q) unf[q] = inside[q];
+    h16x2 C0 = h2s((h16)0.0f), C1 = C0, C2 = C0, T = h2s(hfrom(kH255));
+    uint32_t live = (in0 ? 0x0000ffffu : 0u) | (in1 ? 0xffff0000u : 0u);
+    uint32_t nc = 0;   // the two pixels' counts, u16 each
     uint32_t loaded = 0;
+    uint32_t jn = 0;   // Gaussians processed
 
+    // staging (kernels_forward.cuh:1044-1056), 64 Gaussians at a time, one
+    // per lane: the next batch's indices are loaded when a batch starts and
+    // their rows after its first group of 8, so the loads overlap the blend
+    uint32_t pn = (int32_t)lane < len ? inst_vals[range.x + lane] : 0u;
+    float2 mn = (int32_t)lane < len ? mean2d[pn] : make_float2(0.f, 0.f);
+    uint4 inn = (int32_t)lane < len ? info[pn] : make_uint4(0u, 0u, 0u, 0u);
     for (int32_t base = 0; base < len; base += 64) {
-        if (!__any(unf[0] || unf[1] || unf[2] || unf[3])) break;
+        if (!__any(live != 0u)) break;
         const int32_t nb = min(64, len - base);
-        // staging (kernels_forward.cuh:1044-1056): this lane's Gaussian base + lane
         uint32_t w0 = 0, w1 = 0, w2 = 0, w3 = 0, w4 = 0;
         if ((int32_t)lane < nb) {
-            const uint32_t p = inst_vals[range.x + (uint32_t)(base + (int32_t)lane)];
-            const float2 m = mean2d[p];
-            const uint4 in = info[p];
-            const h16 mx = h_rn(m.x / 16.0f - (float)gx), my = h_rn(m.y / 16.0f - (float)gy);
-            const h16 cxh = hfrom((uint16_t)(in.x & 0xffffu)) * (h16)16.0f;
-            const h16 cyh = hfrom((uint16_t)(in.x >> 16)) * (h16)16.0f;
-            const h16 czh = hfrom((uint16_t)(in.y & 0xffffu)) * (h16)16.0f;
-            const h16 o = hfrom((uint16_t)(in.y >> 16)) * (h16)1.0f;
+            const h16 mx = h_rn(mn.x / 16.0f - (float)gx), my = h_rn(mn.y / 16.0f - (float)gy);
+            const h16 cxh = hfrom((uint16_t)(inn.x & 0xffffu)) * (h16)16.0f;
+            const h16 cyh = hfrom((uint16_t)(inn.x >> 16)) * (h16)16.0f;
+            const h16 czh = hfrom((uint16_t)(inn.y & 0xffffu)) * (h16)16.0f;
+            const h16 o = hfrom((uint16_t)(inn.y >> 16)) * (h16)1.0f;
             w0 = (uint32_t)hbits(mx) | ((uint32_t)hbits(my) << 16);
             w1 = (uint32_t)hbits(cxh) | ((uint32_t)hbits(cyh) << 16);
             w2 = (uint32_t)hbits(czh) | ((uint32_t)hbits(o) << 16);
-            w3 = (uint32_t)hbits((h16)(float)(in.z & 0xffu)) | ((uint32_t)hbits((h16)(float)((in.z >> 8) & 0xffu)) << 16);
-            w4 = (uint32_t)hbits((h16)(float)((in.z >> 16) & 0xffu));
+            w3 = (uint32_t)hbits((h16)(float)(inn.z & 0xffu)) |
+                 ((uint32_t)hbits((h16)(float)((inn.z >> 8) & 0xffu)) << 16);
+            w4 = (uint32_t)hbits((h16)(float)((inn.z >> 16) & 0xffu));
         }
+        const int32_t nxt = len - base - 64;   // Gaussians after this batch
+        pn = (int32_t)lane < nxt ? inst_vals[range.x + (uint32_t)(base + 64) + lane] : 0u;
         loaded += (uint32_t)nb;
-        for (int32_t e = 0; e < nb; ++e) {
-            const int32_t j = base + e;
-            if ((j & (kBucket - 1)) == 0 && j > 0) {   // checkpoint before Gaussian j (:1000-1012)
-                uint2* ck = ckpt + (size_t)(slot0 + (uint32_t)(j / kBucket) - 1u) * kTilePixels + lane;
-#pragma unroll
-                for (int k = 0; k < 2; ++k) {
-                    ck[(2 * k) * 64] = make_uint2((uint32_t)hbits(C0[k].x) | ((uint32_t)hbits(C1[k].x) << 16),
-                                                  (uint32_t)hbits(C2[k].x) | ((uint32_t)hbits(T[k].x) << 16));
-                    ck[(2 * k + 1) * 64] = make_uint2((uint32_t)hbits(C0[k].y) | ((uint32_t)hbits(C1[k].y) << 16),
-                                                      (uint32_t)hbits(C2[k].y) | ((uint32_t)hbits(T[k].y) << 16));
-                }
+        for (int32_t e0 = 0; e0 < nb; e0 += 8) {
+            if (e0 == 8 && nxt > 0) {
+                mn = (int32_t)lane < nxt ? mean2d[pn] : make_float2(0.f, 0.f);
+                inn = (int32_t)lane < nxt ? info[pn] : make_uint4(0u, 0u, 0u, 0u);
             }
-            const h16x2 g0 = h2from(rl(w0, e)), g1 = h2from(rl(w1, e)), g2 = h2from(rl(w2, e));
-            const h16x2 g3 = h2from(rl(w3, e)), g4 = h2from(rl(w4, e));
-            const h16x2 mx2 = h2s(g0.x), my2 = h2s(g0.y), cx2 = h2s(g1.x), cy2 = h2s(g1.y);
-            const h16x2 cz2 = h2s(g2.x), o2 = h2s(g2.y), r2 = h2s(g3.x), gg2 = h2s(g3.y), b2 = h2s(g4.x);
-#pragma unroll
-            for (int k = 0; k < 2; ++k) {
+            const int32_t j0 = base + e0;
+            if ((j0 & (kBucket - 1)) == 0 && j0 > 0) {   // checkpoint before Gaussian j0 (:1000-1012)
+                uint2* ck = ckpt + (size_t)(slot0 + (uint32_t)(j0 / kBucket) - 1u) * kTilePixels + lane;
+                ck[(2u * k) * 64u] = make_uint2((uint32_t)hbits(C0.x) | ((uint32_t)hbits(C1.x) << 16),
+                                                (uint32_t)hbits(C2.x) | ((uint32_t)hbits(T.x) << 16));
+                ck[(2u * k + 1u) * 64u] = make_uint2((uint32_t)hbits(C0.y) | ((uint32_t)hbits(C1.y) << 16),
+                                                     (uint32_t)hbits(C2.y) | ((uint32_t)hbits(T.y) << 16));
+            }
+            const int32_t ng = min(8, nb - e0);
+            // one Gaussian: its power, exp2 and alpha do not depend on the
+            // pixel state, so a full group's eight interleave freely
+            auto blend_one = [&](int32_t e, int32_t j) {
+                const h16x2 g0 = h2from(rl(w0, e)), g1 = h2from(rl(w1, e)), g2 = h2from(rl(w2, e));
+                const h16x2 g3 = h2from(rl(w3, e)), g4 = h2from(rl(w4, e));
+                const h16x2 mx2 = h2s(g0.x), my2 = h2s(g0.y), cx2 = h2s(g1.x), cy2 = h2s(g1.y);
+                const h16x2 cz2 = h2s(g2.x), o2 = h2s(g2.y), r2 = h2s(g3.x), gg2 = h2s(g3.y), b2 = h2s(g4.x);
                 // :1069-1105
-                const h16x2 dx = mx2 - offx, dy = my2 - offy[k];
+                const h16x2 dx = mx2 - offx, dy = my2 - offy;
                 const h16x2 qxx = dx * (cx2 * dx);
                 const h16x2 qzz = dy * (cz2 * dy);
                 const h16x2 qxy = dx * (cy2 * dy);
@@ -162,53 +183,75 @@ __global__ void __launch_bounds__(256) blend16_forward_kernel(
                 const h16x2 s2 = h2_fma(h05, quad, qxy) * h16c;
                 const h16x2 gss = h2_exp2(s2 * nlog2e);
                 const h16x2 alpha = h2_min(o2 * gss, maxa);
-                const h16x2 nT = h2_fma(-alpha, T[k], T[k]);
-                const bool ax = nT.x >= thr, ay = nT.y >= thr;
-                const bool ex = unf[2 * k] && ax, ey = unf[2 * k + 1] && ay;
-                const h16x2 tah = sel2(ex, ey, (T[k] * alpha) * unscale, h2s((h16)0.0f));
-                C0[k] = h2_fma(r2, tah, C0[k]);
-                C1[k] = h2_fma(gg2, tah, C1[k]);
-                C2[k] = h2_fma(b2, tah, C2[k]);
-                T[k] = sel2(ex, ey, nT, T[k]);
-                nc[2 * k] += (unf[2 * k] && nc[2 * k] < 0xffffu) ? 1u : 0u;
-                nc[2 * k + 1] += (unf[2 * k + 1] && nc[2 * k + 1] < 0xffffu) ? 1u : 0u;
-                unf[2 * k] = ex;
-                unf[2 * k + 1] = ey;
-            }
-            // :1115: after each 32 Gaussians, a saturated count stops the pixel
-            if ((j & (kBucket - 1)) == kBucket - 1 || j + 1 == len) {
+                const h16x2 nT = h2_fma(-alpha, T, T);
+                // enabled: unfinished and nT >= thr
+                const uint32_t en = live & ~neg_mask16(nT + nthr);
+                const h16x2 tah = h2from(h2bits((T * alpha) * unscale) & en);
+                C0 = h2_fma(r2, tah, C0);
+                C1 = h2_fma(gg2, tah, C1);
+                C2 = h2_fma(b2, tah, C2);
+                T = h2from(bsel(en, h2bits(nT), h2bits(T)));
+                nc = bsel(live, min((uint32_t)j + 1u, 0xffffu) * 0x10001u, nc);
+                live = en;
+            };
+            if (ng == 8) {
 #pragma unroll
-                for (int q = 0; q < 4; ++q) unf[q] = unf[q] && nc[q] < 0xffffu;
+                for (int32_t u = 0; u < 8; ++u) blend_one(e0 + u, j0 + u);
+            } else {
+                for (int32_t u = 0; u < ng; ++u) blend_one(e0 + u, j0 + u);
             }
-            if ((e & 7) == 7 && !__any(unf[0] || unf[1] || unf[2] || unf[3])) break;
+            const int32_t jl = j0 + ng - 1;   // the group's last Gaussian
+            jn = (uint32_t)jl + 1u;
+            // :1115: after each 32 Gaussians, a saturated count stops the pixel
+            // (bucket ends and the last Gaussian close a group)
+            if (((jl & (kBucket - 1)) == kBucket - 1 || jl + 1 == len) && (uint32_t)jl + 1u >= 0xffffu) live = 0u;
+            if (!__any(live != 0u)) break;
         }
     }
 
     const uint32_t pw = cam.tiled_w * 8u, ph = cam.tiled_h * 8u;
     const uint32_t cs = cam.tiled_w * cam.tiled_h * 64u;
+    const h16 us = hfrom(kHUnscale);
 #pragma unroll
-    for (uint32_t q = 0; q < 4; ++q) {
-        const uint32_t px = gx * 16u + (q & 1u) * 8u + lx, py = gy * 16u + (q >> 1) * 8u + ly;
-        if (px < pw && py < ph) {
+    for (uint32_t hi = 0; hi < 2u; ++hi) {
+        const uint32_t px = px0 + 8u * hi;
+        if (tile_ok && px < pw && py < ph) {
             const uint32_t pi = tiled_index(py, px, cam.tiled_w);
-            const int k = (int)(q >> 1);
-            const bool hi = (q & 1u) != 0u;
-            const h16 c0 = hi ? C0[k].y : C0[k].x, c1 = hi ? C1[k].y : C1[k].x, c2 = hi ? C2[k].y : C2[k].x;
-            const h16 us = hfrom(kHUnscale);
-            image[pi] = inside[q] ? hbits(c0 * us) : (uint16_t)0u;
-            image[pi + cs] = inside[q] ? hbits(c1 * us) : (uint16_t)0u;
-            image[pi + 2 * cs] = inside[q] ? hbits(c2 * us) : (uint16_t)0u;
-            n_contrib[pi] = inside[q] ? (uint16_t)nc[q] : (uint16_t)0u;
+            const bool in = hi ? in1 : in0;
+            const h16 c0 = hi ? C0.y : C0.x, c1 = hi ? C1.y : C1.x, c2 = hi ? C2.y : C2.x;
+            image[pi] = in ? hbits(c0 * us) : (uint16_t)0u;
+            image[pi + cs] = in ? hbits(c1 * us) : (uint16_t)0u;
+            image[pi + 2 * cs] = in ? hbits(c2 * us) : (uint16_t)0u;
+            n_contrib[pi] = in ? (uint16_t)(hi ? nc >> 16 : nc & 0xffffu) : (uint16_t)0u;
         }
     }
-    const uint32_t tmax = wave_max_u32(max(max(nc[0], nc[1]), max(nc[2], nc[3])));
+    const uint32_t wmax = wave_max_u32(max(nc & 0xffffu, nc >> 16));
+    if (lane == 0u) {
+        s_tmax[w] = wmax;
+        s_loaded[w] = loaded;
+    }
+    __syncthreads();
+    if (!tile_ok) return;
+    const uint32_t w0 = w & ~1u;
+    const uint32_t tmax = max(s_tmax[w0], s_tmax[w0 + 1u]);
     // backward work items: every bucket below the tile's largest count, each
     // with all its Gaussians (the backward does not stop at a pixel's count)
     const uint32_t nbk = (tmax + (uint32_t)kBucket - 1u) / (uint32_t)kBucket;
+    // the checkpoints of buckets below that count which this wave stopped
+    // short of (the other wave of the tile ran on): its pixels were all
+    // finished, so their state there is the final one
+    for (uint32_t m = jn ? (jn - 1u) / (uint32_t)kBucket + 1u : 1u; m < nbk; ++m) {
+        uint2* ck = ckpt + (size_t)(slot0 + m - 1u) * kTilePixels + lane;
+        ck[(2u * k) * 64u] = make_uint2((uint32_t)hbits(C0.x) | ((uint32_t)hbits(C1.x) << 16),
+                                        (uint32_t)hbits(C2.x) | ((uint32_t)hbits(T.x) << 16));
+        ck[(2u * k + 1u) * 64u] = make_uint2((uint32_t)hbits(C0.y) | ((uint32_t)hbits(C1.y) << 16),
+                                             (uint32_t)hbits(C2.y) | ((uint32_t)hbits(T.y) << 16));
+    }
+    if (k != 0u) return;
     uint32_t off = 0;
     if (lane == 0) {
         tile_max[tile] = tmax;
-        tile_loaded[tile] = loaded;
+        tile_loaded[tile] = max(s_loaded[w], s_loaded[w + 1u]);
         if (nbk) off = atomicAdd(&ctl->n_items, nbk);
     }
     off = (uint32_t)__builtin_amdgcn_readfirstlane((int)off);
@@ -223,7 +266,7 @@ void launch_blend16_forward(const CamParams& cam, uint2* ranges, const uint32_t*
                             hipStream_t s) {
     const uint32_t n_tiles = cam.grid_w * cam.grid_h;
     if (n_tiles == 0) return;
-    blend16_forward_kernel<<<(n_tiles + 3u) / 4u, 256, 0, s>>>(cam, ranges, inst_vals, mean2d, info, image,
+    blend16_forward_kernel<<<(n_tiles + 1u) / 2u, 256, 0, s>>>(cam, ranges, inst_vals, mean2d, info, image,
                                                                 n_contrib, tile_max, tile_loaded, ckpt, items, ctl);
 }
 
@@ -237,8 +280,8 @@ struct PairState {
 };
 
 __device__ __forceinline__ uint32_t shr1(uint32_t x) {
-    // DPP wave_shr:1: lane l receives lane l - 1 (lane 0 keeps 0)
-    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x138, 0xf, 0xf, false);
+    // DPP wave_shr:1: lane l receives lane l - 1 (lane 0: 0, bound_ctrl)
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x138, 0xf, 0xf, true);
 }
 
 }  // namespace
@@ -248,7 +291,10 @@ __global__ void __launch_bounds__(256) blend16_backward_kernel(
     const uint4* __restrict__ info, const uint16_t* __restrict__ image, const uint16_t* __restrict__ grad_image,
     const uint2* __restrict__ ckpt, const uint4* __restrict__ items, BinCtl* __restrict__ ctl,
     uint32_t* __restrict__ rec_count, const uint32_t* __restrict__ first_slot, float4* __restrict__ records) {
-    __shared__ uint4 s_pair[4][2][128][2];   // [wave][half][pair][2 x 4 dwords]
+    // per wave and half wave, per pixel pair: the static words (grad r, g, b,
+    // (offx, offy)) and the state at the bucket start (colour after r, g, b, T)
+    __shared__ uint4 s_static[4][2][128];
+    __shared__ uint4 s_init[4][2][128];
 
     const uint32_t w = threadIdx.x >> 6, lane = threadIdx.x & 63u;
     const uint32_t half = lane >> 5, l = lane & 31u;
@@ -331,8 +377,8 @@ __global__ void __launch_bounds__(256) blend16_backward_kernel(
                                    h2bits(KT * h2s(hfrom(kHUnscale))), 0u);
                 }
                 c.w = (uint32_t)hbits((h16)(float)dx_) | ((uint32_t)hbits((h16)(float)dy_) << 16);
-                s_pair[w][half][i][0] = a;
-                s_pair[w][half][i][1] = c;
+                s_static[w][half][i] = make_uint4(a.x, a.y, a.z, c.w);
+                s_init[w][half][i] = make_uint4(a.w, c.x, c.y, c.z);
             }
         }
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -342,22 +388,27 @@ __global__ void __launch_bounds__(256) blend16_backward_kernel(
         // ---- the pipeline (:1194-1355)
         h16x2 a_mx = h2s((h16)0.f), a_my = a_mx, a_ax = a_mx, a_ay = a_mx, a_cx = a_mx, a_cy = a_mx, a_cz = a_mx;
         h16x2 a_op = a_mx, a_r = a_mx, a_g = a_mx, a_b = a_mx;
-        uint32_t st[8];
-#pragma unroll
-        for (int q = 0; q < 8; ++q) st[q] = 0u;
+        // lane l at step s works on pair s - l: its static words from LDS
+        // (loaded a step ahead), its state (colour after, T) from lane l - 1
+        // (lanes 0 and 32: the pair's state at the bucket start, from LDS)
+        uint32_t st[4] = {0u, 0u, 0u, 0u};
+        const uint4* sst = s_static[w][half];
+        const uint4* sin = s_init[w][half];
         const uint32_t cmax = max(readlane_u32(cnt, 0), readlane_u32(cnt, 32));
         const uint32_t steps = cmax ? 128u + cmax - 1u : 0u;
+        uint4 cur = sst[min(0u - l, 127u)];
         for (uint32_t s = 0; s < steps; ++s) {
-            if (l == 0 && s < 128u) {   // lanes 0 and 32 take the next pair
-                const uint4 a = s_pair[w][half][s][0], c = s_pair[w][half][s][1];
-                st[0] = a.x; st[1] = a.y; st[2] = a.z; st[3] = a.w;
-                st[4] = c.x; st[5] = c.y; st[6] = c.z; st[7] = c.w;
+            const uint32_t i = s - l;
+            const uint4 nxt = sst[min(i + 1u, 127u)];
+            if (l == 0u && s < 128u) {
+                const uint4 c = sin[s];
+                st[0] = c.x; st[1] = c.y; st[2] = c.z; st[3] = c.w;
             }
-            if (s - l < 128u && l < cnt) {
-                const h16x2 G0 = h2from(st[0]), G1 = h2from(st[1]), G2 = h2from(st[2]);
-                h16x2 Ca0 = h2from(st[3]), Ca1 = h2from(st[4]), Ca2 = h2from(st[5]);
-                const h16x2 T = h2from(st[6]);
-                const h16x2 off = h2from(st[7]);
+            if (i < 128u && l < cnt) {
+                const h16x2 G0 = h2from(cur.x), G1 = h2from(cur.y), G2 = h2from(cur.z);
+                h16x2 Ca0 = h2from(st[0]), Ca1 = h2from(st[1]), Ca2 = h2from(st[2]);
+                const h16x2 T = h2from(st[3]);
+                const h16x2 off = h2from(cur.w);
                 const h16x2 offx = h2s(off.x), offy = h2s(off.y);
                 const h16x2 dlx = h2_fma(inv16, -offx, mxp);
                 const h16x2 dly = h2_fma(inv16, -offy, my2);
@@ -380,7 +431,7 @@ __global__ void __launch_bounds__(256) blend16_backward_kernel(
                 Ca1 = h2_fma(-bw, cg2, Ca1);
                 Ca2 = h2_fma(-bw, cb2, Ca2);
                 const h16x2 cadg = h2_fma(Ca0, G0, h2_fma(Ca1, G1, Ca2 * G2));
-                const h16x2 dal = h2_fma(T, cdg, -h2_div(cadg, oma));
+                const h16x2 dal = h2_fma(T, cdg, -h2_div_blend(cadg, oma));   // oma in [0x1.4p-7, 1]
                 const h16x2 part = alpha * dal;
                 a_op = part + a_op;
                 const h16x2 dxdx = dlx * dlx, dxdy = dlx * dly, dydy = dly * dly;
@@ -393,13 +444,14 @@ __global__ void __launch_bounds__(256) blend16_backward_kernel(
                 a_my = dmy + a_my;
                 a_ax = h2from(h2bits(dmx) & 0x7fff7fffu) + a_ax;
                 a_ay = h2from(h2bits(dmy) & 0x7fff7fffu) + a_ay;
-                st[3] = h2bits(Ca0);
-                st[4] = h2bits(Ca1);
-                st[5] = h2bits(Ca2);
-                st[6] = h2bits(nT);
+                st[0] = h2bits(Ca0);
+                st[1] = h2bits(Ca1);
+                st[2] = h2bits(Ca2);
+                st[3] = h2bits(nT);
             }
 #pragma unroll
-            for (int q = 0; q < 8; ++q) st[q] = shr1(st[q]);
+            for (int q = 0; q < 4; ++q) st[q] = shr1(st[q]);
+            cur = nxt;
         }
 
         // ---- the bucket's record (:1357-1387), rounded as the reference's atomics receive it

@@ -16,6 +16,9 @@
 //             rounded to half (float's 24 bits >= 2 * 11 + 2, so the double
 //             rounding is innocuous; S. A. Figueroa, "When is double rounding
 //             innocuous?", SIGNUM 1995)
+//   h_div_blend  correctly rounded for divisors in [0x1.4p-7, 1] (Markstein's
+//             iteration on v_rcp_f16; checked over all dividends and those
+//             divisors)
 //   h_exp2    correctly rounded 2^x of a half x (v_exp_f16; checked over all
 //             65,536 inputs against the oracle's)
 //   h_min     IEEE minNum: a NaN operand yields the other (the blend never
@@ -63,6 +66,25 @@ __device__ __forceinline__ h16 h_fma(h16 a, h16 b, h16 c) { return __builtin_ele
 __device__ __forceinline__ h16x2 h2_fma(h16x2 a, h16x2 b, h16x2 c) { return __builtin_elementwise_fma(a, b, c); }
 
 __device__ __forceinline__ h16 h_div(h16 a, h16 b) { return (h16)((float)a / (float)b); }
+// a / b correctly rounded for a divisor b in [0x1.4p-7, 1] (bits 0x2100 ..
+// 0x3c00: the blend backward's 1 - alpha, alpha in [0, RN(0.99)]), by
+// Markstein's iteration: y = RN(1 / b) (v_rcp_f16, equal to the correctly
+// rounded reciprocal of every positive finite half), q0 = RN(a y) clamped to
+// the finite halves, the residual r = b q0 - a exactly in float (its sign
+// keeps a zero quotient's sign), q = RN(q0 - r y) (rounded to float, then to
+// half: innocuous, 24 >= 2 * 11 + 2). Equal to h_div for every half a and
+// every b of that range (all 4.5e8 pairs, tgs_selftest_half_div_blend); other
+// divisors are not covered. P. Markstein, "Computation of elementary
+// functions on the IBM RISC System/6000 processor", IBM J. Res. Dev. 34, 1990.
+__device__ __forceinline__ h16x2 h2_div_blend(h16x2 a, h16x2 b) {
+    const h16x2 y = h2(__builtin_amdgcn_rcph(b.x), __builtin_amdgcn_rcph(b.y));
+    const h16x2 lim = h2((h16)65504.0f, (h16)65504.0f);
+    const h16x2 q0 = __builtin_elementwise_max(__builtin_elementwise_min(a * y, lim), -lim);
+    const float rx = __builtin_fmaf((float)b.x, (float)q0.x, -(float)a.x);
+    const float ry = __builtin_fmaf((float)b.y, (float)q0.y, -(float)a.y);
+    return h2((h16)__builtin_fmaf(-rx, (float)y.x, (float)q0.x), (h16)__builtin_fmaf(-ry, (float)y.y, (float)q0.y));
+}
+__device__ __forceinline__ h16 h_div_blend(h16 a, h16 b) { return h2_div_blend(h2s(a), h2s(b)).x; }
 __device__ __forceinline__ h16x2 h2_div(h16x2 a, h16x2 b) { return h2(h_div(a.x, b.x), h_div(a.y, b.y)); }
 
 // 2^x: v_exp_f16, which is correctly rounded for every half input (checked

@@ -365,6 +365,7 @@ void launch_wave_selftest(const uint32_t* in, uint32_t* out, hipStream_t s);
 // canonical half operation `op` (tests): out[i] = op(a[i], b[i], c[i]) as bits
 // out[8] (zeroed by the caller): mismatches, pairs checked, a / b / q of one mismatch
 void launch_half_div_check(unsigned long long* out, hipStream_t s);
+void launch_half_div_blend_check(unsigned long long* out, uint32_t blo, uint32_t bhi, hipStream_t s);
 void launch_halfmath(int op, const uint16_t* a, const uint16_t* b, const uint16_t* c, uint16_t* out, int64_t n,
                      hipStream_t s);
 

@@ -176,4 +176,37 @@ void launch_half_div_check(unsigned long long* out, hipStream_t s) {
     half_div_check_kernel<<<65536u, 256, 0, s>>>(out);
 }
 
+// h_div_blend against h_div (itself checked over all pairs above) for every
+// half a and every positive b with bits in [blo, bhi], and v_rcp_f16 against
+// h_div(1, b) for those b. out: [0] quotient mismatches, [1] reciprocal
+// mismatches, [2..4] a, b, quotient of one mismatch, [5] claim flag.
+__global__ void __launch_bounds__(256) half_div_blend_check_kernel(unsigned long long* out, uint32_t blo,
+                                                                   uint32_t bhi) {
+    const uint64_t t = (uint64_t)blockIdx.x * 256u + threadIdx.x;
+    const bool on = t < 65536ull * (bhi - blo + 1u);
+    const uint16_t a = (uint16_t)(t & 0xffffu);
+    const uint16_t b = (uint16_t)(blo + (uint32_t)(t >> 16));
+    bool rbad = false, bad = false;
+    if (on) {
+        if (a == 0u) rbad = hbits(__builtin_amdgcn_rcph(hfrom(b))) != hbits(h_div((h16)1.0f, hfrom(b)));
+        const uint16_t q = hbits(h_div_blend(hfrom(a), hfrom(b)));
+        bad = q != hbits(h_div(hfrom(a), hfrom(b)));
+        if (bad && atomicAdd(&out[5], 1ull) == 0ull) {
+            out[2] = a;
+            out[3] = b;
+            out[4] = q;
+        }
+    }
+    const unsigned long long nbad = __popcll(__ballot(bad)), nr = __popcll(__ballot(rbad));
+    if ((threadIdx.x & 63u) == 0u) {
+        if (nbad) atomicAdd(&out[0], nbad);
+        if (nr) atomicAdd(&out[1], nr);
+    }
+}
+
+void launch_half_div_blend_check(unsigned long long* out, uint32_t blo, uint32_t bhi, hipStream_t s) {
+    const uint64_t n = 65536ull * (bhi - blo + 1u);
+    half_div_blend_check_kernel<<<(unsigned)((n + 255u) / 256u), 256, 0, s>>>(out, blo, bhi);
+}
+
 }  // namespace tgs
