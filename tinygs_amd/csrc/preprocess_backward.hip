@@ -258,6 +258,44 @@ __device__ __forceinline__ void preprocess_backward_one(
 }
 
 // ---- exact sums of half records (half mode)
+//
+// Every record field is a half: a multiple of 2^-24 below 2^16 in magnitude.
+// A double sum of up to 8192 of them is therefore exact (its magnitude stays
+// below 2^29), and infinities and NaNs propagate as IEEE sums do (+inf and
+// -inf give NaN). The exact sum is rounded to half once (double -> float ->
+// half: innocuous, 24 >= 2 * 11 + 2). Heavy primitives with more records
+// (only grids of more than 8192 tiles) take the integer sums below.
+struct HalfSumsD {
+    double s[10];
+    double op;
+};
+
+__device__ __forceinline__ void hsd_zero(HalfSumsD& h) {
+#pragma unroll
+    for (int q = 0; q < 10; ++q) h.s[q] = 0.0;
+    h.op = 0.0;
+}
+
+__device__ __forceinline__ void hsd_add(HalfSumsD& h, const float4& a, const float4& b, const float4& c) {
+    const float v[10] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w, c.x, c.y};
+#pragma unroll
+    for (int q = 0; q < 10; ++q) h.s[q] += (double)v[q];
+    h.op += (double)c.z;
+}
+
+__device__ __forceinline__ float hsd_value(double s) {
+    const float v = (float)(_Float16)(float)s;
+    return v != v ? __builtin_nanf("") : v;
+}
+
+__device__ __forceinline__ void hsd_result(const HalfSumsD& h, float4& gA, float4& gB, float4& gC) {
+    gA = make_float4(hsd_value(h.s[0]), hsd_value(h.s[1]), hsd_value(h.s[2]), hsd_value(h.s[3]));
+    gB = make_float4(hsd_value(h.s[4]), hsd_value(h.s[5]), hsd_value(h.s[6]), hsd_value(h.s[7]));
+    gC = make_float4(hsd_value(h.s[8]), hsd_value(h.s[9]), (float)h.op, 0.f);
+}
+
+constexpr uint32_t kHalfDoubleRecords = 8192;   // exact double sums up to this many records
+
 struct HalfSums {
     int64_t s[10];
     uint32_t fl;   // per field q, bits 3q..3q+2: +inf, -inf, NaN seen
@@ -507,6 +545,41 @@ __device__ __forceinline__ void gather_heavy_chunk(const uint4* __restrict__ lis
         const bool on = h < nh;
         const uint4 e = on ? list[h] : make_uint4(0u, 0u, 0u, 0u);
         if constexpr (kHalf) {
+            if (e.y <= kHalfDoubleRecords) {   // (row-uniform)
+                HalfSumsD hs;
+                hsd_zero(hs);
+                uint32_t r = sub;
+                for (; r + 48u < e.y; r += 64u) {   // four strides' loads issued together (exact sums: any order)
+                    float4 a[4], b[4], d[4];
+#pragma unroll
+                    for (int u = 0; u < 4; ++u) {
+                        const float4* src = records + 3 * (size_t)(e.z + r + 16u * (uint32_t)u);
+                        a[u] = src[0];
+                        b[u] = src[1];
+                        d[u] = src[2];
+                    }
+#pragma unroll
+                    for (int u = 0; u < 4; ++u) hsd_add(hs, a[u], b[u], d[u]);
+                }
+                for (; r < e.y; r += 16u) {
+                    const float4* src = records + 3 * (size_t)(e.z + r);
+                    hsd_add(hs, src[0], src[1], src[2]);
+                }
+                for (int m = 8; m >= 1; m >>= 1) {
+#pragma unroll
+                    for (int q = 0; q < 10; ++q) hs.s[q] += __shfl_xor(hs.s[q], m, 16);
+                    hs.op += __shfl_xor(hs.op, m, 16);
+                }
+                if (on && sub == 0u) {
+                    float4 gA, gB, gC;
+                    hsd_result(hs, gA, gB, gC);
+                    float4* g = (float4*)(grad2d + (size_t)e.x * kGradStride);
+                    g[0] = gA;
+                    g[1] = gB;
+                    g[2] = gC;
+                }
+                continue;
+            }
             HalfSums hs;
             hs_zero(hs);
             uint32_t r = sub;
@@ -680,10 +753,10 @@ __global__ void __launch_bounds__(256) preprocess_backward_chunk_kernel(
             gC = *(const float4*)(gr + 8);
         } else if constexpr (kHalf) {
             const float4* rec = records + 3 * (size_t)e.z;
-            HalfSums hs;
-            hs_zero(hs);
-            for (uint32_t r = 0; r < nr; ++r) hs_add(hs, rec[3 * r], rec[3 * r + 1], rec[3 * r + 2]);
-            hs_result(hs, gA, gB, gC);
+            HalfSumsD hs;
+            hsd_zero(hs);
+            for (uint32_t r = 0; r < nr; ++r) hsd_add(hs, rec[3 * r], rec[3 * r + 1], rec[3 * r + 2]);
+            hsd_result(hs, gA, gB, gC);
         } else {
             // the marked slots in slot (rank) order
             float v[12];
