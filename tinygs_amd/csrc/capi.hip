@@ -218,6 +218,7 @@ struct tgs_rasterizer {
     DevBuf ranges, tile_max, n_contrib;
     DevBuf ckpt, items;   // blend checkpoints (float4 x 256 per slot), backward work items (uint4)
     DevBuf tile_loaded;   // Gaussians staged per tile by the last forward (work statistic)
+    DevBuf tile_order;    // tiles, heavy first, for the fp16-image forward
     // backward 2D-gradient records: per primitive first instance slot, record
     // count (kept zero between backwards), records (3 float4 per instance
     // slot), heavy-gather list
@@ -351,7 +352,7 @@ int tgs_rasterizer_destroy(tgs_rasterizer* r) {
                      &r->offs, &r->pkeys[0], &r->pkeys[1], &r->pvals[0], &r->pvals[1], &r->pnt[0], &r->pnt[1],
                      &r->radix_counts, &r->block_n, &r->ikeys[0],
                      &r->ikeys[1], &r->ivals[0], &r->ivals[1], &r->ranges, &r->tile_max, &r->n_contrib,
-                     &r->ckpt, &r->items, &r->tile_loaded, &r->first_slot,
+                     &r->ckpt, &r->items, &r->tile_loaded, &r->tile_order, &r->first_slot,
                      &r->rec_count, &r->records, &r->iranks, &r->rec_bits, &r->rec_mask, &r->heavy, &r->live,
                      &r->row_mask,
                      &r->grad2d,
@@ -492,6 +493,7 @@ static int rasterizer_forward(tgs_rasterizer* r, const tgs_camera* camera, void*
     TGS_TRY(ensure(r->block_n, 4 * (size_t)std::max<int64_t>(scan_status_entries(nn), 1), s));
     TGS_TRY(ensure(r->tile_max, 4 * (size_t)T, s));
     TGS_TRY(ensure(r->tile_loaded, 4 * (size_t)T, s));
+    TGS_TRY(ensure(r->tile_order, 4 * (size_t)T, s));
     TGS_TRY(ensure(r->n_contrib, 4 * cs, s));
     // without a host wait the instance buffers are sized by the reserved capacity up front
     const int64_t cap0 = nosync ? r->inst_cap : 0;
@@ -604,7 +606,8 @@ static int rasterizer_forward(tgs_rasterizer* r, const tgs_camera* camera, void*
         if (f16)
             launch_blend16_forward(cam, r->ranges.as<uint2>(), iv[isel], r->mean2d.as<float2>(), r->color.as<uint4>(),
                                    (uint16_t*)image, r->n_contrib.as<uint16_t>(), r->tile_max.as<uint32_t>(),
-                                   r->tile_loaded.as<uint32_t>(), r->ckpt.as<uint2>(), r->items.as<uint4>(), ctl, s);
+                                   r->tile_loaded.as<uint32_t>(), r->ckpt.as<uint2>(), r->items.as<uint4>(), ctl,
+                                   r->tile_order.as<uint32_t>(), s);
         else
             launch_blend_forward(cam, r->ranges.as<uint2>(), iv[isel], r->mean2d.as<float2>(),
                                  r->conic_opacity.as<float4>(), r->color.as<float4>(), (float*)image,

@@ -19,7 +19,9 @@
 //     the tile, lane L pixel L of each (in-tile pixels 64 q + L), held as
 //     one half2; every image / count / checkpoint access of a block is one
 //     contiguous run. Each wave stages the tile's Gaussians 64 at a time,
-//     one per lane, and broadcasts them with v_readlane (no LDS).
+//     one per lane, and broadcasts them with v_readlane (no LDS). Tiles are
+//     taken long ones first (tile_order_kernel): the kernel's length was
+//     set by long tiles whose waves started late.
 //   * backward: one (tile, 32-Gaussian bucket) work item per half wave, two
 //     per wave. As in the reference, lane l of the half owns Gaussian l of the
 //     bucket and the tile's 128 pixel pairs stream through the lanes: at step
@@ -87,16 +89,50 @@ __device__ __forceinline__ uint32_t bsel(uint32_t m, uint32_t a, uint32_t b) { r
 // operations. An unfinished pixel has processed every Gaussian so far, so
 // its count after Gaussian j is min(j + 1, 65535): one select per Gaussian,
 // and the saturation stop (:1115) is the same for every unfinished pixel.
+// Tiles in decreasing order of the bit length of their instance counts,
+// for the forward to start with the heavy tiles: its length is set by the
+// waves that start last. (Order within a bucket: whatever the LDS atomics
+// give; it only affects scheduling.)
+constexpr uint32_t kOrderMaxTiles = 1u << 20;   // one workgroup orders at most this many tiles
+__global__ void __launch_bounds__(1024) tile_order_kernel(const uint2* __restrict__ ranges, uint32_t n_tiles,
+                                                          uint32_t* __restrict__ order,
+                                                          const BinCtl* __restrict__ ctl) {
+    __shared__ uint32_t s_off[33];
+    const uint32_t t = threadIdx.x;
+    if (t < 33u) s_off[t] = 0u;
+    __syncthreads();
+    const bool failed = (ctl->err & (kErrLookBack | kErrOffsets)) != 0u;
+    auto slot = [&](uint32_t i) {
+        const uint2 r = ranges[i];
+        const uint32_t len = failed || r.y <= r.x ? 0u : r.y - r.x;   // empty: (UINT32_MAX, 0)
+        return len ? (uint32_t)__builtin_clz(len) : 32u;               // 32 - bit length
+    };
+    for (uint32_t i = t; i < n_tiles; i += 1024u) atomicAdd(&s_off[slot(i)], 1u);
+    __syncthreads();
+    if (t == 0u) {
+        uint32_t run = 0;
+        for (uint32_t b = 0; b < 33u; ++b) {
+            const uint32_t c = s_off[b];
+            s_off[b] = run;
+            run += c;
+        }
+    }
+    __syncthreads();
+    for (uint32_t i = t; i < n_tiles; i += 1024u) order[atomicAdd(&s_off[slot(i)], 1u)] = i;
+}
+
 __global__ void __launch_bounds__(256) blend16_forward_kernel(
     CamParams cam, uint2* __restrict__ ranges, const uint32_t* __restrict__ inst_vals,
     const float2* __restrict__ mean2d, const uint4* __restrict__ info, uint16_t* __restrict__ image,
     uint16_t* __restrict__ n_contrib, uint32_t* __restrict__ tile_max, uint32_t* __restrict__ tile_loaded,
-    uint2* __restrict__ ckpt, uint4* __restrict__ items, BinCtl* __restrict__ ctl) {
+    uint2* __restrict__ ckpt, uint4* __restrict__ items, BinCtl* __restrict__ ctl,
+    const uint32_t* __restrict__ order) {
     __shared__ uint32_t s_tmax[4], s_loaded[4];
     const uint32_t n_tiles = cam.grid_w * cam.grid_h;
     const uint32_t w = threadIdx.x >> 6, lane = threadIdx.x & 63u;
-    const uint32_t tile = blockIdx.x * 2u + (w >> 1), k = w & 1u;
-    const bool tile_ok = tile < n_tiles;   // (no early return: the workgroup meets at a barrier)
+    const uint32_t opos = blockIdx.x * 2u + (w >> 1), k = w & 1u;
+    const bool tile_ok = opos < n_tiles;   // (no early return: the workgroup meets at a barrier)
+    const uint32_t tile = tile_ok && order ? order[opos] : opos;
     const uint32_t gx = tile_ok ? tile % cam.grid_w : 0u, gy = tile_ok ? tile / cam.grid_w : 0u;
     const uint32_t lx = lane & 7u, ly = lane >> 3;
 
@@ -263,11 +299,14 @@ __global__ void __launch_bounds__(256) blend16_forward_kernel(
 void launch_blend16_forward(const CamParams& cam, uint2* ranges, const uint32_t* inst_vals,
                             const float2* mean2d, const uint4* info, uint16_t* image, uint16_t* n_contrib,
                             uint32_t* tile_max, uint32_t* tile_loaded, uint2* ckpt, uint4* items, BinCtl* ctl,
-                            hipStream_t s) {
+                            uint32_t* order, hipStream_t s) {
     const uint32_t n_tiles = cam.grid_w * cam.grid_h;
     if (n_tiles == 0) return;
+    if (n_tiles > kOrderMaxTiles) order = nullptr;   // tiles in index order
+    if (order) tile_order_kernel<<<1, 1024, 0, s>>>(ranges, n_tiles, order, ctl);
     blend16_forward_kernel<<<(n_tiles + 1u) / 2u, 256, 0, s>>>(cam, ranges, inst_vals, mean2d, info, image,
-                                                                n_contrib, tile_max, tile_loaded, ckpt, items, ctl);
+                                                                n_contrib, tile_max, tile_loaded, ckpt, items, ctl,
+                                                                order);
 }
 
 // ---------------------------------------------------------------- backward

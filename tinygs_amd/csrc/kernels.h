@@ -195,7 +195,7 @@ void launch_preprocess16(const GaussianView& g, const CamParams& cam, uint32_t* 
 void launch_blend16_forward(const CamParams& cam, uint2* ranges, const uint32_t* inst_vals,
                             const float2* mean2d, const uint4* info, uint16_t* image, uint16_t* n_contrib,
                             uint32_t* tile_max, uint32_t* tile_loaded, uint2* ckpt, uint4* items, BinCtl* ctl,
-                            hipStream_t s);
+                            uint32_t* order, hipStream_t s);
 void launch_blend16_backward(const CamParams& cam, const uint32_t* inst_vals, const float2* mean2d,
                              const uint4* info, const uint16_t* image, const uint16_t* grad_image, const uint2* ckpt,
                              const uint4* items, BinCtl* ctl, uint32_t* rec_count, const uint32_t* first_slot,
