@@ -62,6 +62,43 @@ __device__ __forceinline__ float sigma_box_lower_bound(float a, float b, float c
     return m - slack;
 }
 
+// Tiles in decreasing order of the bit length of their instance counts,
+// for the forward to start with the heavy tiles: its length is set by the
+// waves that start last. (Order within a bucket: whatever the LDS atomics
+// give; it only affects scheduling.)
+__global__ void __launch_bounds__(1024) tile_order_kernel(const uint2* __restrict__ ranges, uint32_t n_tiles,
+                                                          uint32_t* __restrict__ order,
+                                                          const BinCtl* __restrict__ ctl) {
+    __shared__ uint32_t s_off[33];
+    const uint32_t t = threadIdx.x;
+    if (t < 33u) s_off[t] = 0u;
+    __syncthreads();
+    const bool failed = (ctl->err & (kErrLookBack | kErrOffsets)) != 0u;
+    auto slot = [&](uint32_t i) {
+        const uint2 r = ranges[i];
+        const uint32_t len = failed || r.y <= r.x ? 0u : r.y - r.x;   // empty: (UINT32_MAX, 0)
+        return len ? (uint32_t)__builtin_clz(len) : 32u;               // 32 - bit length
+    };
+    for (uint32_t i = t; i < n_tiles; i += 1024u) atomicAdd(&s_off[slot(i)], 1u);
+    __syncthreads();
+    if (t == 0u) {
+        uint32_t run = 0;
+        for (uint32_t b = 0; b < 33u; ++b) {
+            const uint32_t c = s_off[b];
+            s_off[b] = run;
+            run += c;
+        }
+    }
+    __syncthreads();
+    for (uint32_t i = t; i < n_tiles; i += 1024u) order[atomicAdd(&s_off[slot(i)], 1u)] = i;
+}
+
+bool launch_tile_order(const uint2* ranges, uint32_t n_tiles, uint32_t* order, const BinCtl* ctl, hipStream_t s) {
+    if (!order || n_tiles == 0u || n_tiles > kOrderMaxTiles) return false;
+    tile_order_kernel<<<1, 1024, 0, s>>>(ranges, n_tiles, order, ctl);
+    return true;
+}
+
 __global__ void __launch_bounds__(256) blend_forward_kernel(CamParams cam, uint2* __restrict__ ranges,
                                                             const uint32_t* __restrict__ inst_vals,
                                                             const float2* __restrict__ mean2d,
@@ -73,7 +110,8 @@ __global__ void __launch_bounds__(256) blend_forward_kernel(CamParams cam, uint2
                                                             uint32_t* __restrict__ tile_loaded,
                                                             float4* __restrict__ ckpt,
                                                             uint4* __restrict__ items,
-                                                            BinCtl* __restrict__ ctl) {
+                                                            BinCtl* __restrict__ ctl,
+                                                            const uint32_t* __restrict__ order) {
     // s_a, s_b and s_c are read at one LDS address per Gaussian (offsets 0, 4 and 8 KiB)
     __shared__ float4 s_a[256];       // mx, my, a L/2, b L
     __shared__ float4 s_b[256];       // c L/2, opacity, r, g (clamped colour)
@@ -82,7 +120,7 @@ __global__ void __launch_bounds__(256) blend_forward_kernel(CamParams cam, uint2
     __shared__ uint16_t s_list[4][256];
     __shared__ uint32_t s_max[4];
 
-    const uint32_t tile = blockIdx.x;
+    const uint32_t tile = order ? order[blockIdx.x] : blockIdx.x;   // long tiles first
     const uint32_t gx = tile % cam.grid_w, gy = tile / cam.grid_w;
     const uint32_t tid = threadIdx.x, w = tid >> 6, lane = tid & 63u;
     const uint32_t px = gx * 16u + (w & 1u) * 8u + (lane & 7u);
@@ -227,11 +265,12 @@ size_t blend_ckpt_slots(int64_t n_instances, uint32_t n_tiles) {
 void launch_blend_forward(const CamParams& cam, uint2* ranges, const uint32_t* inst_vals, const float2* mean2d,
                           const float4* conic_opacity, const float4* color_pt, float* image, uint32_t* n_contrib,
                           uint32_t* tile_max, uint32_t* tile_loaded, float4* ckpt, uint4* items, BinCtl* ctl,
-                          hipStream_t s) {
+                          uint32_t* order, hipStream_t s) {
     const uint32_t n_tiles = cam.grid_w * cam.grid_h;
     if (n_tiles == 0) return;
+    if (!launch_tile_order(ranges, n_tiles, order, ctl, s)) order = nullptr;
     blend_forward_kernel<<<n_tiles, 256, 0, s>>>(cam, ranges, inst_vals, mean2d, conic_opacity, color_pt, image,
-                                                 n_contrib, tile_max, tile_loaded, ckpt, items, ctl);
+                                                 n_contrib, tile_max, tile_loaded, ckpt, items, ctl, order);
 }
 
 }  // namespace tgs

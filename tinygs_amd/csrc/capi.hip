@@ -218,7 +218,7 @@ struct tgs_rasterizer {
     DevBuf ranges, tile_max, n_contrib;
     DevBuf ckpt, items;   // blend checkpoints (float4 x 256 per slot), backward work items (uint4)
     DevBuf tile_loaded;   // Gaussians staged per tile by the last forward (work statistic)
-    DevBuf tile_order;    // tiles, heavy first, for the fp16-image forward
+    DevBuf tile_order;    // tiles, long ones first, for the fp16-image blend forward
     // backward 2D-gradient records: per primitive first instance slot, record
     // count (kept zero between backwards), records (3 float4 per instance
     // slot), heavy-gather list
@@ -612,7 +612,8 @@ static int rasterizer_forward(tgs_rasterizer* r, const tgs_camera* camera, void*
             launch_blend_forward(cam, r->ranges.as<uint2>(), iv[isel], r->mean2d.as<float2>(),
                                  r->conic_opacity.as<float4>(), r->color.as<float4>(), (float*)image,
                                  r->n_contrib.as<uint32_t>(), r->tile_max.as<uint32_t>(),
-                                 r->tile_loaded.as<uint32_t>(), r->ckpt.as<float4>(), r->items.as<uint4>(), ctl, s);
+                                 r->tile_loaded.as<uint32_t>(), r->ckpt.as<float4>(), r->items.as<uint4>(), ctl,
+                                 nullptr, s);
     }
     TGS_CHECK_LAUNCH();
     if (!nosync) {

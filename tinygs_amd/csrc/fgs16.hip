@@ -89,38 +89,6 @@ __device__ __forceinline__ uint32_t bsel(uint32_t m, uint32_t a, uint32_t b) { r
 // operations. An unfinished pixel has processed every Gaussian so far, so
 // its count after Gaussian j is min(j + 1, 65535): one select per Gaussian,
 // and the saturation stop (:1115) is the same for every unfinished pixel.
-// Tiles in decreasing order of the bit length of their instance counts,
-// for the forward to start with the heavy tiles: its length is set by the
-// waves that start last. (Order within a bucket: whatever the LDS atomics
-// give; it only affects scheduling.)
-constexpr uint32_t kOrderMaxTiles = 1u << 20;   // one workgroup orders at most this many tiles
-__global__ void __launch_bounds__(1024) tile_order_kernel(const uint2* __restrict__ ranges, uint32_t n_tiles,
-                                                          uint32_t* __restrict__ order,
-                                                          const BinCtl* __restrict__ ctl) {
-    __shared__ uint32_t s_off[33];
-    const uint32_t t = threadIdx.x;
-    if (t < 33u) s_off[t] = 0u;
-    __syncthreads();
-    const bool failed = (ctl->err & (kErrLookBack | kErrOffsets)) != 0u;
-    auto slot = [&](uint32_t i) {
-        const uint2 r = ranges[i];
-        const uint32_t len = failed || r.y <= r.x ? 0u : r.y - r.x;   // empty: (UINT32_MAX, 0)
-        return len ? (uint32_t)__builtin_clz(len) : 32u;               // 32 - bit length
-    };
-    for (uint32_t i = t; i < n_tiles; i += 1024u) atomicAdd(&s_off[slot(i)], 1u);
-    __syncthreads();
-    if (t == 0u) {
-        uint32_t run = 0;
-        for (uint32_t b = 0; b < 33u; ++b) {
-            const uint32_t c = s_off[b];
-            s_off[b] = run;
-            run += c;
-        }
-    }
-    __syncthreads();
-    for (uint32_t i = t; i < n_tiles; i += 1024u) order[atomicAdd(&s_off[slot(i)], 1u)] = i;
-}
-
 __global__ void __launch_bounds__(256) blend16_forward_kernel(
     CamParams cam, uint2* __restrict__ ranges, const uint32_t* __restrict__ inst_vals,
     const float2* __restrict__ mean2d, const uint4* __restrict__ info, uint16_t* __restrict__ image,
@@ -302,8 +270,7 @@ void launch_blend16_forward(const CamParams& cam, uint2* ranges, const uint32_t*
                             uint32_t* order, hipStream_t s) {
     const uint32_t n_tiles = cam.grid_w * cam.grid_h;
     if (n_tiles == 0) return;
-    if (n_tiles > kOrderMaxTiles) order = nullptr;   // tiles in index order
-    if (order) tile_order_kernel<<<1, 1024, 0, s>>>(ranges, n_tiles, order, ctl);
+    if (!launch_tile_order(ranges, n_tiles, order, ctl, s)) order = nullptr;   // tiles in index order
     blend16_forward_kernel<<<(n_tiles + 1u) / 2u, 256, 0, s>>>(cam, ranges, inst_vals, mean2d, info, image,
                                                                 n_contrib, tile_max, tile_loaded, ckpt, items, ctl,
                                                                 order);

@@ -188,6 +188,17 @@ void launch_preprocess16(const GaussianView& g, const CamParams& cam, uint32_t* 
                          float2* mean2d, float4* conic_opacity, uint4* info, uint32_t* depth_key,
                          float* densif, BinCtl* ctl, hipStream_t s);
 
+// Fills order (u32[n_tiles]) with the tiles in decreasing order of the bit
+// length of their instance counts (from the ranges; all tiles count as empty
+// after a failed binning scan), for a blend forward to take long tiles first
+// (order null: index order). One workgroup: returns false, and launches
+// nothing, beyond kOrderMaxTiles tiles or without an order buffer. The fp16
+// forward uses it (one wave pair per tile: long tiles that start late set its
+// length); the fp32 forward measured slower with it (index order keeps
+// neighbouring tiles, which share Gaussians, together in the caches).
+constexpr uint32_t kOrderMaxTiles = 1u << 20;
+bool launch_tile_order(const uint2* ranges, uint32_t n_tiles, uint32_t* order, const BinCtl* ctl, hipStream_t s);
+
 // Blend of FGS16 (fgs16.hip): image / grad image are 3 half planes of the
 // padded 8x8-tiled layout, n_contrib u16 per pixel, ckpt 256 uint2 per slot
 // (the fp32 path's slots), items as the fp32 path's but with every Gaussian of
@@ -213,7 +224,7 @@ size_t blend_ckpt_slots(int64_t n_instances, uint32_t n_tiles);
 void launch_blend_forward(const CamParams& cam, uint2* ranges, const uint32_t* inst_vals, const float2* mean2d,
                           const float4* conic_opacity, const float4* color_pt, float* image, uint32_t* n_contrib,
                           uint32_t* tile_max, uint32_t* tile_loaded, float4* ckpt, uint4* items, BinCtl* ctl,
-                          hipStream_t s);
+                          uint32_t* order, hipStream_t s);
 // 2D gradient records: each (primitive p, bucket) the backward processes
 // writes 12 floats at record index first_slot[p] + k, k the instance's rank
 // among p's instances (inst_ranks, from the tile sort; below n_touched[p]: a
