@@ -66,20 +66,53 @@ __device__ __forceinline__ float sigma_box_lower_bound(float a, float b, float c
 // for the forward to start with the heavy tiles: its length is set by the
 // waves that start last. (Order within a bucket: whatever the LDS atomics
 // give; it only affects scheduling.)
+constexpr uint32_t kOrderLdsTiles = 65536;   // bins kept in LDS (one byte per tile) up to this many tiles
+
 __global__ void __launch_bounds__(1024) tile_order_kernel(const uint2* __restrict__ ranges, uint32_t n_tiles,
                                                           uint32_t* __restrict__ order,
                                                           const BinCtl* __restrict__ ctl) {
     __shared__ uint32_t s_off[33];
-    const uint32_t t = threadIdx.x;
+    __shared__ uint8_t s_bin[kOrderLdsTiles];
+    const uint32_t t = threadIdx.x, lane = t & 63u;
     if (t < 33u) s_off[t] = 0u;
     __syncthreads();
     const bool failed = (ctl->err & (kErrLookBack | kErrOffsets)) != 0u;
-    auto slot = [&](uint32_t i) {
-        const uint2 r = ranges[i];
+    const bool in_lds = n_tiles <= kOrderLdsTiles;
+    // bin: 32 - the bit length of the tile's instance count (0 for the longest)
+    auto bin_of = [&](uint2 r) {
         const uint32_t len = failed || r.y <= r.x ? 0u : r.y - r.x;   // empty: (UINT32_MAX, 0)
-        return len ? (uint32_t)__builtin_clz(len) : 32u;               // 32 - bit length
+        return len ? (uint32_t)__builtin_clz(len) : 32u;
     };
-    for (uint32_t i = t; i < n_tiles; i += 1024u) atomicAdd(&s_off[slot(i)], 1u);
+    // the lanes of the wave with the same bin (6 ballots), so that one lane
+    // per bin and wave touches the LDS counters
+    auto peers_of = [&](uint32_t bin, bool valid) {
+        uint64_t m = __ballot(valid);
+#pragma unroll
+        for (int k = 0; k < 6; ++k) {
+            const uint64_t b = __ballot(((bin >> k) & 1u) != 0u);
+            m &= ((bin >> k) & 1u) ? b : ~b;
+        }
+        return m;
+    };
+    // pass 1: counts per bin, eight tiles per thread loaded together
+    for (uint32_t q0 = 0; q0 < n_tiles; q0 += 8u * 1024u) {
+        uint2 r[8];
+#pragma unroll
+        for (uint32_t u = 0; u < 8u; ++u) {
+            const uint32_t i = q0 + u * 1024u + t;
+            r[u] = i < n_tiles ? ranges[i] : make_uint2(0u, 0u);
+        }
+#pragma unroll
+        for (uint32_t u = 0; u < 8u; ++u) {
+            const uint32_t i = q0 + u * 1024u + t;
+            const bool valid = i < n_tiles;
+            const uint32_t bin = valid ? bin_of(r[u]) : 0u;
+            if (valid && in_lds) s_bin[i] = (uint8_t)bin;
+            const uint64_t peers = peers_of(bin, valid);
+            if (valid && (peers & ((1ull << lane) - 1ull)) == 0ull)
+                atomicAdd(&s_off[bin], (uint32_t)__popcll(peers));
+        }
+    }
     __syncthreads();
     if (t == 0u) {
         uint32_t run = 0;
@@ -90,7 +123,19 @@ __global__ void __launch_bounds__(1024) tile_order_kernel(const uint2* __restric
         }
     }
     __syncthreads();
-    for (uint32_t i = t; i < n_tiles; i += 1024u) order[atomicAdd(&s_off[slot(i)], 1u)] = i;
+    // pass 2: positions
+    for (uint32_t q = 0; q < n_tiles; q += 1024u) {
+        const uint32_t i = q + t;
+        const bool valid = i < n_tiles;
+        const uint32_t bin = !valid ? 0u : in_lds ? (uint32_t)s_bin[i] : bin_of(ranges[i]);
+        const uint64_t peers = peers_of(bin, valid);
+        const uint64_t below = peers & ((1ull << lane) - 1ull);
+        const uint32_t leader = valid ? (uint32_t)__builtin_ctzll(peers) : 0u;
+        uint32_t base = 0;
+        if (valid && below == 0ull) base = atomicAdd(&s_off[bin], (uint32_t)__popcll(peers));
+        base = (uint32_t)__shfl((int)base, (int)leader);
+        if (valid) order[base + (uint32_t)__popcll(below)] = i;
+    }
 }
 
 bool launch_tile_order(const uint2* ranges, uint32_t n_tiles, uint32_t* order, const BinCtl* ctl, hipStream_t s) {
