@@ -38,8 +38,11 @@ constexpr int kScanRounds = kScanChunk / kScanThreads;
 constexpr int kDepthKeysPerThread = 16;                 // depth passes: 4096 keys per workgroup
 constexpr int kTileKeysPerThread = 16;                  // tile passes: 4096 keys per workgroup (2048: 3 us slower, 8192: 17 us)
 // LDS histograms per digit count (lane & (kHistCopies - 1) picks one): keys
-// that arrive clustered do not serialise their atomic adds on one address
+// that arrive clustered do not serialise their atomic adds on one address.
+// The copies are kHistPad words longer than the digit count, so the copies
+// of one digit fall into different LDS banks.
 constexpr int kHistCopies = 8;
+constexpr int kHistPad = 1;
 constexpr int kDepthMaxDigits = 512;                    // depth passes: digits of up to 9 bits
 constexpr int kTileMaxDigits = 256;                     // tile passes: digits of up to 8 bits
 constexpr int kDepthSortWaves = 16;                     // depth up / downsweeps: 1024 threads x 4 keys
@@ -176,11 +179,12 @@ __global__ void __launch_bounds__(kScanThreads) compact_count_kernel(const uint3
                                                                  uint32_t* __restrict__ block_n, BinCtl* ctl) {
     __shared__ uint32_t s_rw[64];
     __shared__ uint32_t s_nt[kScanWaves];
-    __shared__ uint32_t s_hist[kHistCopies][kDepthMaxDigits];
+    __shared__ uint32_t s_hist[kHistCopies][kDepthMaxDigits + kHistPad];
     const uint32_t t = threadIdx.x, lane = t & 63u, w = t >> 6;
     const uint32_t b = blockIdx.x, nb = gridDim.x;
     const uint32_t bins = 1u << bits, dmask = bins - 1u;
-    for (uint32_t e = t; e < (uint32_t)(kHistCopies * kDepthMaxDigits); e += kScanThreads) (&s_hist[0][0])[e] = 0u;
+    for (uint32_t e = t; e < (uint32_t)(kHistCopies * (kDepthMaxDigits + kHistPad)); e += kScanThreads)
+        (&s_hist[0][0])[e] = 0u;
     const int64_t blk = (int64_t)b * kScanChunk;
     const int64_t base = blk + t;
     uint32_t key[kScanRounds], nt[kScanRounds], vis[kScanRounds], ex[kScanRounds];
@@ -331,11 +335,11 @@ __global__ void __launch_bounds__(64 * NW) radix_upsweep_kernel(const uint32_t* 
     if (clear_bits)
         for (uint32_t j = threadIdx.x; j < (uint32_t)(KPT * NW * 2); j += kNT)
             clear_bits[(size_t)blockIdx.x * (KPT * NW * 2) + j] = 0u;
-    __shared__ uint32_t s_hist[kHistCopies][MAXB];
-    __shared__ uint32_t s_hsum[NTSUM ? kHistCopies : 1][NTSUM ? MAXB : 1];
+    __shared__ uint32_t s_hist[kHistCopies][MAXB + kHistPad];
+    __shared__ uint32_t s_hsum[NTSUM ? kHistCopies : 1][NTSUM ? MAXB + kHistPad : 1];
     const uint32_t t = threadIdx.x, lane = t & 63u, w = t >> 6;
     const uint32_t bins = 1u << bits, dmask = bins - 1u;
-    for (uint32_t b = t; b < (uint32_t)(kHistCopies * MAXB); b += kNT) {
+    for (uint32_t b = t; b < (uint32_t)(kHistCopies * (MAXB + kHistPad)); b += kNT) {
         (&s_hist[0][0])[b] = 0u;
         if constexpr (NTSUM) (&s_hsum[0][0])[b] = 0u;
     }
