@@ -114,13 +114,10 @@ __global__ void __launch_bounds__(1024) tile_order_kernel(const uint2* __restric
         }
     }
     __syncthreads();
-    if (t == 0u) {
-        uint32_t run = 0;
-        for (uint32_t b = 0; b < 33u; ++b) {
-            const uint32_t c = s_off[b];
-            s_off[b] = run;
-            run += c;
-        }
+    if (t < 64u) {   // exclusive scan of the 33 bin counts (one wave)
+        const uint32_t c = t < 33u ? s_off[t] : 0u;
+        const uint32_t incl = wave_inclusive_scan_u32(c);
+        if (t < 33u) s_off[t] = incl - c;
     }
     __syncthreads();
     // pass 2: positions

@@ -43,6 +43,10 @@ namespace {
 
 constexpr uint16_t kH255 = 0x5bf8;   // 255
 constexpr uint16_t kHUnscale = 0x1c04;   // RN(1/255)
+// 16 RN(-log2 e) = -23.078125, exact. The reference scales the power by 16,
+// then by RN(-log2 e): (x * 16) * k and x * (16 k) are the same half for
+// every half x (16 x is exact, and where it overflows so does x * 16 k).
+constexpr uint16_t kHNeg16Log2e = 0xcdc5;
 
 __device__ __forceinline__ uint32_t rl(uint32_t v, int lane) { return (uint32_t)__builtin_amdgcn_readlane((int)v, lane); }
 
@@ -96,6 +100,7 @@ __global__ void __launch_bounds__(256) blend16_forward_kernel(
     uint2* __restrict__ ckpt, uint4* __restrict__ items, BinCtl* __restrict__ ctl,
     const uint32_t* __restrict__ order) {
     __shared__ uint32_t s_tmax[4], s_loaded[4];
+    __shared__ uint4 s_gw[4][64][2];   // per wave, the staged batch: five words per Gaussian
     const uint32_t n_tiles = cam.grid_w * cam.grid_h;
     const uint32_t w = threadIdx.x >> 6, lane = threadIdx.x & 63u;
     const uint32_t opos = blockIdx.x * 2u + (w >> 1), k = w & 1u;
@@ -105,8 +110,8 @@ __global__ void __launch_bounds__(256) blend16_forward_kernel(
     const uint32_t lx = lane & 7u, ly = lane >> 3;
 
     const h16 thr = h_rd(1e-4f * 255.0f);
-    const h16x2 maxa = h2s((h16)0.99f), unscale = h2s(hfrom(kHUnscale)), h16c = h2s((h16)16.0f),
-                h05 = h2s((h16)0.5f), nlog2e = h2s(-(h16)1.4426950409f), nthr = h2s(-thr);
+    const h16x2 maxa = h2s((h16)0.99f), unscale = h2s(hfrom(kHUnscale)), h05 = h2s((h16)0.5f),
+                nthr = h2s(-thr);
     // .x: block 2k (in-tile column lx), .y: block 2k + 1 (column lx + 8); row 8k + ly
     const h16x2 offx = h2(offset_x(lx), offset_x(lx + 8u));
     const h16x2 offy = h2s(offset_y(ly + 8u * k));
@@ -154,6 +159,15 @@ __global__ void __launch_bounds__(256) blend16_forward_kernel(
                  ((uint32_t)hbits((h16)(float)((inn.z >> 8) & 0xffu)) << 16);
             w4 = (uint32_t)hbits((h16)(float)((inn.z >> 16) & 0xffu));
         }
+        // the batch to LDS: each Gaussian's words reach every lane as a
+        // broadcast read (no VALU), and the previous batch's reads are done
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        s_gw[w][lane][0] = make_uint4(w0, w1, w2, w3);
+        s_gw[w][lane][1].x = w4;
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
         const int32_t nxt = len - base - 64;   // Gaussians after this batch
         pn = (int32_t)lane < nxt ? inst_vals[range.x + (uint32_t)(base + 64) + lane] : 0u;
         loaded += (uint32_t)nb;
@@ -174,8 +188,9 @@ __global__ void __launch_bounds__(256) blend16_forward_kernel(
             // one Gaussian: its power, exp2 and alpha do not depend on the
             // pixel state, so a full group's eight interleave freely
             auto blend_one = [&](int32_t e, int32_t j) {
-                const h16x2 g0 = h2from(rl(w0, e)), g1 = h2from(rl(w1, e)), g2 = h2from(rl(w2, e));
-                const h16x2 g3 = h2from(rl(w3, e)), g4 = h2from(rl(w4, e));
+                const uint4 q = s_gw[w][e][0];
+                const h16x2 g0 = h2from(q.x), g1 = h2from(q.y), g2 = h2from(q.z);
+                const h16x2 g3 = h2from(q.w), g4 = h2from(s_gw[w][e][1].x);
                 const h16x2 mx2 = h2s(g0.x), my2 = h2s(g0.y), cx2 = h2s(g1.x), cy2 = h2s(g1.y);
                 const h16x2 cz2 = h2s(g2.x), o2 = h2s(g2.y), r2 = h2s(g3.x), gg2 = h2s(g3.y), b2 = h2s(g4.x);
                 // :1069-1105
@@ -184,8 +199,7 @@ __global__ void __launch_bounds__(256) blend16_forward_kernel(
                 const h16x2 qzz = dy * (cz2 * dy);
                 const h16x2 qxy = dx * (cy2 * dy);
                 const h16x2 quad = qxx + qzz;
-                const h16x2 s2 = h2_fma(h05, quad, qxy) * h16c;
-                const h16x2 gss = h2_exp2(s2 * nlog2e);
+                const h16x2 gss = h2_exp2(h2_fma(h05, quad, qxy) * h2s(hfrom(kHNeg16Log2e)));
                 const h16x2 alpha = h2_min(o2 * gss, maxa);
                 const h16x2 nT = h2_fma(-alpha, T, T);
                 // enabled: unfinished and nT >= thr
@@ -312,8 +326,8 @@ __global__ void __launch_bounds__(256) blend16_backward_kernel(
     if (lane == 0) next = atomicAdd(qctr, 1u);
     next = (uint32_t)__builtin_amdgcn_readfirstlane((int)next);
 
-    const h16x2 h05 = h2s((h16)0.5f), h16c = h2s((h16)16.0f), one = h2s((h16)1.0f), maxa = h2s((h16)0.99f),
-                nlog2e = h2s(-(h16)1.4426950409f), inv16 = h2s((h16)0.0625f);
+    const h16x2 h05 = h2s((h16)0.5f), one = h2s((h16)1.0f), maxa = h2s((h16)0.99f),
+                nk = h2s(hfrom(kHNeg16Log2e)), inv16 = h2s((h16)0.0625f);
 
     while (true) {
         const uint32_t pr = queue + next * (uint32_t)kBwdQueues;   // item pair
@@ -421,9 +435,8 @@ __global__ void __launch_bounds__(256) blend16_backward_kernel(
                 const h16x2 cx_dx = cx2 * dlx, cy_dx = cy2 * dlx, cz_dy = cz2 * dly, cy_dy = cy2 * dly;
                 const h16x2 cz_dyy = dly * cz_dy, cy_dxy = dlx * cy_dy;
                 const h16x2 quad = h2_fma(dlx, cx_dx, cz_dyy);
-                const h16x2 s2 = h2_relu(h2_fma(h05, quad, cy_dxy)) * h16c;
                 const h16x2 prep_x = cx_dx + cy_dy;
-                const h16x2 gss = h2_exp2(s2 * nlog2e);
+                const h16x2 gss = h2_exp2(h2_relu(h2_fma(h05, quad, cy_dxy)) * nk);
                 const h16x2 prep_y = cy_dx + cz_dy;
                 const h16x2 alpha_p = o2 * gss;
                 const h16x2 cdg = h2_fma(cr2, G0, h2_fma(cg2, G1, cb2 * G2));
