@@ -19,7 +19,8 @@
 //     the tile, lane L pixel L of each (in-tile pixels 64 q + L), held as
 //     one half2; every image / count / checkpoint access of a block is one
 //     contiguous run. Each wave stages the tile's Gaussians 64 at a time,
-//     one per lane, and broadcasts them with v_readlane (no LDS). Tiles are
+//     one per lane, in LDS; each Gaussian's words then reach every lane as
+//     a broadcast read (no VALU). Tiles are
 //     taken long ones first (tile_order_kernel): the kernel's length was
 //     set by long tiles whose waves started late.
 //   * backward: one (tile, 32-Gaussian bucket) work item per half wave, two
@@ -48,7 +49,6 @@ constexpr uint16_t kHUnscale = 0x1c04;   // RN(1/255)
 // every half x (16 x is exact, and where it overflows so does x * 16 k).
 constexpr uint16_t kHNeg16Log2e = 0xcdc5;
 
-__device__ __forceinline__ uint32_t rl(uint32_t v, int lane) { return (uint32_t)__builtin_amdgcn_readlane((int)v, lane); }
 
 // The half pixel-centre offsets of blend_cu2 (kernels_forward.cuh:960-967) in
 // tile units: x of an even in-tile column lx = fma(1/16, lx, 1/32), of an odd
