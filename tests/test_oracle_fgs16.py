@@ -289,3 +289,22 @@ def test_from_fixed_matches_numpy(orc):
     with np.errstate(over="ignore"):   # |s| < 2^53: exact doubles; beyond 65520 -> inf
         want = (s.astype(np.float64) * 2.0 ** -24).astype(np.float16).view(np.uint16)
     assert np.array_equal(got, want), np.count_nonzero(got != want)
+
+
+def test_exp2_argument_one_multiply(orc):
+    """The blend kernels scale the power by 16 RN(-log2 e) = -23.078125 in one
+    multiply where the reference (and the oracle) multiply by 16, then by
+    RN(-log2 e): the same half for every half input, and so the same exp2."""
+    x = np.arange(1 << 16, dtype=np.uint32).astype(np.uint16)
+    k = np.float16(-1.4426950409)
+    big = (np.float16(16.0) * k).view(np.uint16)
+    assert big == 0xcdc5 and float(np.float16(16.0) * k) == 16.0 * float(k)
+    n = x.size
+    two = orc.half_op(3, orc.half_op(3, x, np.full(n, np.float16(16.0).view(np.uint16))),
+                      np.full(n, k.view(np.uint16)))
+    one = orc.half_op(3, x, np.full(n, big, np.uint16))
+    nan = (two & 0x7c00 == 0x7c00) & (two & 0x3ff != 0)
+    assert np.array_equal(nan, (one & 0x7c00 == 0x7c00) & (one & 0x3ff != 0))
+    assert np.array_equal(two[~nan], one[~nan])
+    # and hence every exp2 the kernels evaluate
+    assert np.array_equal(orc.half_op(0, two[~nan]), orc.half_op(0, one[~nan]))
