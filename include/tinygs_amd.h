@@ -511,6 +511,14 @@ int tgs_selftest_half_div_exhaustive(int64_t* out, void* stream);
  * quotient mismatches, [1] reciprocal mismatches, [2..4] a, b, quotient of one
  * mismatch. No counterpart in the reference. */
 int tgs_selftest_half_div_blend(int64_t* out, uint32_t b_lo, uint32_t b_hi, void* stream);
+/* The shader (core) clock of the current device under a VALU load, in MHz:
+ * a probe kernel at eight waves per SIMD runs packed-half fma chains for
+ * about a millisecond and reads the shader clock counter and the
+ * constant-rate counter around them (their ratio times the wall clock rate).
+ * Synchronises the stream. For the VALU issue peak a measurement quotes (one
+ * wave64 VALU instruction per CU per clock). No counterpart in the
+ * reference. */
+int tgs_selftest_clock(double* core_mhz, void* stream);
 /* Spin bound of the binning's look-back waits on the current device, for
  * tests of the error path: 0 makes every look-back that has a predecessor
  * give up at once (as a wait that ran out would), setting the look-back error

@@ -46,6 +46,16 @@ def test_wave_primitives(hip):
         assert red[q] == np.float32(vals.astype(np.float64).sum() + 64 * q), (q, red[q])
 
 
+def test_shader_clock_probe(hip):
+    """The clock the bench quotes its VALU issue peak at: a shader clock
+    between 0.5 GHz and the part's 2.4 GHz peak (plus margin)."""
+    import ctypes as C
+    from tinygs_amd import _lib
+    mhz = C.c_double(0.0)
+    _lib.check(_lib.load().tgs_selftest_clock(C.byref(mhz), None))
+    assert 500.0 < mhz.value < 2600.0, mhz.value
+
+
 @pytest.mark.parametrize("op", [0, 1, 2, 3, 4, 5, 6])
 def test_detmath_bit_exact_vs_oracle(hip, orc, op):
     import torch

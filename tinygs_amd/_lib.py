@@ -155,6 +155,7 @@ SIGNATURES = {
     "tgs_selftest_half_div_exhaustive": ([P, P], C.c_int),
     "tgs_selftest_half_div_blend": ([P, C.c_uint32, C.c_uint32, P], C.c_int),
     "tgs_selftest_lookback_spins": ([C.c_uint32], C.c_int),
+    "tgs_selftest_clock": ([C.POINTER(C.c_double), P], C.c_int),
     "tgs_adam_step_ex": ([P, C.c_float, P, C.c_int32, P], C.c_int),
     "tgs_adam_device_steps": ([P, C.POINTER(C.c_int64), P], C.c_int),
 }

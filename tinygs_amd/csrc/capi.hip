@@ -1708,6 +1708,34 @@ int tgs_selftest_half_div_blend(int64_t* out, uint32_t b_lo, uint32_t b_hi, void
     return TGS_OK;
 }
 
+int tgs_selftest_clock(double* core_mhz, void* stream) {
+    if (!core_mhz) return fail(TGS_ERR_INVALID, "bad argument");
+    hipStream_t s = (hipStream_t)stream;
+    int dev = 0, cus = 0, wall_khz = 0;
+    TGS_HIP(hipGetDevice(&dev));
+    TGS_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+    TGS_HIP(hipDeviceGetAttribute(&wall_khz, hipDeviceAttributeWallClockRate, dev));
+    if (cus <= 0 || wall_khz <= 0) return fail(TGS_ERR_HIP, "no compute units or wall clock rate reported");
+    const uint32_t blocks = (uint32_t)cus * 8u;   // eight waves per SIMD
+    std::vector<unsigned long long> h(2u * blocks);
+    unsigned long long* d = nullptr;
+    TGS_HIP(hipMalloc(&d, h.size() * sizeof(unsigned long long)));
+    launch_clock_probe(d, blocks, 8192u, s);
+    hipError_t e = hipGetLastError();
+    if (e == hipSuccess) e = hipMemcpyAsync(h.data(), d, h.size() * sizeof(unsigned long long), hipMemcpyDeviceToHost, s);
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    (void)hipFree(d);
+    if (e != hipSuccess) return fail(TGS_ERR_HIP, "clock probe: %s", hipGetErrorString(e));
+    double cycles = 0.0, ticks = 0.0;
+    for (uint32_t b = 0; b < blocks; ++b) {
+        cycles += (double)h[2u * b];
+        ticks += (double)h[2u * b + 1u];
+    }
+    if (ticks <= 0.0) return fail(TGS_ERR_HIP, "clock probe: no constant-rate ticks");
+    *core_mhz = cycles / ticks * (double)wall_khz / 1000.0;
+    return TGS_OK;
+}
+
 int tgs_selftest_lookback_spins(uint32_t spins) {
     if (set_lookback_spin_limit(spins == 0xffffffffu ? (1u << 22) : spins) != 0)
         return fail(TGS_ERR_HIP, "look-back spin bound: %s", hipGetErrorString(hipGetLastError()));

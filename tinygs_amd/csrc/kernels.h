@@ -377,6 +377,10 @@ void launch_wave_selftest(const uint32_t* in, uint32_t* out, hipStream_t s);
 // out[8] (zeroed by the caller): mismatches, pairs checked, a / b / q of one mismatch
 void launch_half_div_check(unsigned long long* out, hipStream_t s);
 void launch_half_div_blend_check(unsigned long long* out, uint32_t blo, uint32_t bhi, hipStream_t s);
+// clock_probe_kernel over `blocks` workgroups of 256 threads: out[2 b] the
+// shader clock cycles, out[2 b + 1] the constant-rate counter ticks of
+// workgroup b's timed loop
+void launch_clock_probe(unsigned long long* out, uint32_t blocks, uint32_t iters, hipStream_t s);
 void launch_halfmath(int op, const uint16_t* a, const uint16_t* b, const uint16_t* c, uint16_t* out, int64_t n,
                      hipStream_t s);
 

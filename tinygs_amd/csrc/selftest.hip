@@ -209,4 +209,35 @@ void launch_half_div_blend_check(unsigned long long* out, uint32_t blo, uint32_t
     half_div_blend_check_kernel<<<(unsigned)((n + 255u) / 256u), 256, 0, s>>>(out, blo, bhi);
 }
 
+// The shader clock under a VALU load: each lane runs eight independent
+// chains of packed-half fmas, and wave 0 of each workgroup reads the shader
+// clock counter (s_memtime) and the constant-rate counter (s_memrealtime)
+// before and after; out[2 b] and out[2 b + 1] are workgroup b's differences.
+__global__ void __launch_bounds__(256) clock_probe_kernel(unsigned long long* out, uint32_t iters, float seed) {
+    h16x2 a[8];
+#pragma unroll
+    for (int c = 0; c < 8; ++c)
+        a[c] = h2((h16)(seed * (float)(threadIdx.x + c) * 1e-4f), (h16)(-seed * (float)c * 1e-3f));
+    const h16x2 q = h2s((h16)0.25f);
+    __syncthreads();
+    const unsigned long long t0 = __builtin_amdgcn_s_memtime(), r0 = __builtin_amdgcn_s_memrealtime();
+    for (uint32_t i = 0; i < iters; ++i) {
+#pragma unroll
+        for (int c = 0; c < 8; ++c) a[c] = h2_fma(a[c], a[c], q);
+    }
+    float sum = 0.f;
+#pragma unroll
+    for (int c = 0; c < 8; ++c) sum += (float)a[c].x + (float)a[c].y;
+    const unsigned long long t1 = __builtin_amdgcn_s_memtime(), r1 = __builtin_amdgcn_s_memrealtime();
+    if (threadIdx.x == 0u) {
+        out[2u * blockIdx.x] = t1 - t0;
+        out[2u * blockIdx.x + 1u] = r1 - r0;
+    }
+    if (sum == 12345.0f) out[0] = 0ull;   // keeps the chains
+}
+
+void launch_clock_probe(unsigned long long* out, uint32_t blocks, uint32_t iters, hipStream_t s) {
+    clock_probe_kernel<<<blocks, 256, 0, s>>>(out, iters, 1.0f);
+}
+
 }  // namespace tgs
