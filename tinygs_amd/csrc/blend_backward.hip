@@ -67,7 +67,7 @@ __global__ void __launch_bounds__(256) blend_backward_kernel(
     const int q0 = row_value(lane >> 4);   // first value index this lane's row holds after wave_reduce12
     const uint32_t n_items = ctl->n_items;
     const uint32_t cs = cam.tiled_w * cam.tiled_h * 64u;
-    // this wave's queue: items q, q + Q, q + 2Q, ...; its counter has a cache line to itself
+    // this wave's queue (its items: bwd_queue_item); its counter has a cache line to itself
     const uint32_t queue = (blockIdx.x * 4u + w) % (uint32_t)kBwdQueues;
     uint32_t* qctr = &ctl->bwd_queue[queue * 32u];
     uint32_t next = 0;
@@ -75,7 +75,7 @@ __global__ void __launch_bounds__(256) blend_backward_kernel(
     next = (uint32_t)__builtin_amdgcn_readfirstlane((int)next);
 
     while (true) {
-        const uint32_t it = queue + next * (uint32_t)kBwdQueues;
+        const uint32_t it = bwd_queue_item(queue, next);   // increasing in next
         if (it >= n_items) break;
         // fetch the following index now; its latency hides behind this item
         uint32_t after = 0;

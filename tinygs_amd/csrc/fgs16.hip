@@ -330,7 +330,7 @@ __global__ void __launch_bounds__(256) blend16_backward_kernel(
                 nk = h2s(hfrom(kHNeg16Log2e)), inv16 = h2s((h16)0.0625f);
 
     while (true) {
-        const uint32_t pr = queue + next * (uint32_t)kBwdQueues;   // item pair
+        const uint32_t pr = bwd_queue_item(queue, next);   // item pair, increasing in next
         if (2u * pr >= n_items) break;
         uint32_t after = 0;
         if (lane == 0) after = atomicAdd(qctr, 1u);

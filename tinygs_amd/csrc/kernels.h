@@ -48,7 +48,18 @@ void launch_preprocess(const GaussianView& g, const CamParams& cam, uint32_t* n_
 // cleared at the start of every forward; err (look-back error flag) is
 // sticky so that a failure is reported by the next host check.
 enum { kTicketCompact = 0, kTicketOffsets = 1, kTicketDepth = 2, kTicketTile = 6, kTicketCount = 10 };
-constexpr int kBwdQueues = 64;   // backward work queues; item i belongs to queue i % kBwdQueues
+// Backward work queues. Queue q hands out its items in runs of kBwdRun
+// consecutive ones: item R (q + Q (n / R)) + n % R is its n-th (R = kBwdRun,
+// Q = kBwdQueues), so a tile's buckets (consecutive items) mostly go to one
+// queue. The backward kernels serve queue q from workgroups b with 4 b + w =
+// q (mod Q), which all sit on the XCD b mod 8 (workgroups go to the 8 XCDs
+// in turn), so that XCD's L2 holds the tile's image, gradient and checkpoint
+// lines for the tile's later buckets.
+constexpr int kBwdQueues = 64;
+constexpr int kBwdRun = 4;
+__device__ __forceinline__ uint32_t bwd_queue_item(uint32_t q, uint32_t n) {
+    return (uint32_t)kBwdRun * (q + (n / (uint32_t)kBwdRun) * (uint32_t)kBwdQueues) + n % (uint32_t)kBwdRun;
+}
 struct BinCtl {
     // epoch_base: look-back epochs of the current forward are epoch_base + k
     // for the forward's k-th look-back launch (k < kEpochStride); advanced by
