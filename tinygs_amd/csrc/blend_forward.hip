@@ -62,24 +62,28 @@ __device__ __forceinline__ float sigma_box_lower_bound(float a, float b, float c
     return m - slack;
 }
 
-// Tiles in decreasing order of the bit length of their instance counts,
-// for the forward to start with the heavy tiles: its length is set by the
-// waves that start last. (Order within a bucket: whatever the LDS atomics
-// give; it only affects scheduling.)
-constexpr uint32_t kOrderLdsTiles = 65536;   // bins kept in LDS (one byte per tile) up to this many tiles
+// Tiles in roughly decreasing order of the bit length of their instance
+// counts, for the forward to start with the heavy tiles: its length is set by
+// the waves that start last. Workgroup c of kOrderChunks sorts the tiles
+// t = c (mod kOrderChunks) by that bit length and writes its k-th tile to
+// position k kOrderChunks + c, so the positions are a permutation of the
+// tiles and each run of kOrderChunks positions holds one tile of every chunk
+// in the same rank. (Order within a bin: whatever the LDS atomics give; it
+// only affects scheduling.)
+constexpr uint32_t kOrderChunks = 16;
 
-__global__ void __launch_bounds__(1024) tile_order_kernel(const uint2* __restrict__ ranges, uint32_t n_tiles,
-                                                          uint32_t* __restrict__ order,
-                                                          const BinCtl* __restrict__ ctl) {
+__global__ void __launch_bounds__(512) tile_order_kernel(const uint2* __restrict__ ranges, uint32_t n_tiles,
+                                                         uint32_t* __restrict__ order,
+                                                         const BinCtl* __restrict__ ctl) {
     __shared__ uint32_t s_off[33];
-    __shared__ uint8_t s_bin[kOrderLdsTiles];
-    const uint32_t t = threadIdx.x, lane = t & 63u;
+    const uint32_t t = threadIdx.x, lane = t & 63u, c = blockIdx.x;
     if (t < 33u) s_off[t] = 0u;
     __syncthreads();
     const bool failed = (ctl->err & (kErrLookBack | kErrOffsets)) != 0u;
-    const bool in_lds = n_tiles <= kOrderLdsTiles;
+    const uint32_t n_c = n_tiles > c ? (n_tiles - c + kOrderChunks - 1u) / kOrderChunks : 0u;   // this chunk's tiles
     // bin: 32 - the bit length of the tile's instance count (0 for the longest)
-    auto bin_of = [&](uint2 r) {
+    auto bin_at = [&](uint32_t k) {
+        const uint2 r = ranges[c + k * kOrderChunks];
         const uint32_t len = failed || r.y <= r.x ? 0u : r.y - r.x;   // empty: (UINT32_MAX, 0)
         return len ? (uint32_t)__builtin_clz(len) : 32u;
     };
@@ -88,56 +92,47 @@ __global__ void __launch_bounds__(1024) tile_order_kernel(const uint2* __restric
     auto peers_of = [&](uint32_t bin, bool valid) {
         uint64_t m = __ballot(valid);
 #pragma unroll
-        for (int k = 0; k < 6; ++k) {
-            const uint64_t b = __ballot(((bin >> k) & 1u) != 0u);
-            m &= ((bin >> k) & 1u) ? b : ~b;
+        for (int q = 0; q < 6; ++q) {
+            const uint64_t bq = __ballot(((bin >> q) & 1u) != 0u);
+            m &= ((bin >> q) & 1u) ? bq : ~bq;
         }
         return m;
     };
-    // pass 1: counts per bin, eight tiles per thread loaded together
-    for (uint32_t q0 = 0; q0 < n_tiles; q0 += 8u * 1024u) {
-        uint2 r[8];
-#pragma unroll
-        for (uint32_t u = 0; u < 8u; ++u) {
-            const uint32_t i = q0 + u * 1024u + t;
-            r[u] = i < n_tiles ? ranges[i] : make_uint2(0u, 0u);
-        }
-#pragma unroll
-        for (uint32_t u = 0; u < 8u; ++u) {
-            const uint32_t i = q0 + u * 1024u + t;
-            const bool valid = i < n_tiles;
-            const uint32_t bin = valid ? bin_of(r[u]) : 0u;
-            if (valid && in_lds) s_bin[i] = (uint8_t)bin;
-            const uint64_t peers = peers_of(bin, valid);
-            if (valid && (peers & ((1ull << lane) - 1ull)) == 0ull)
-                atomicAdd(&s_off[bin], (uint32_t)__popcll(peers));
-        }
+    // pass 1: counts per bin (the first 512 bins stay in registers for pass 2)
+    uint32_t bin0 = 0u;
+    for (uint32_t q = 0; q < n_c; q += 512u) {
+        const uint32_t k = q + t;
+        const bool valid = k < n_c;
+        const uint32_t bin = valid ? bin_at(k) : 0u;
+        if (q == 0u) bin0 = bin;
+        const uint64_t peers = peers_of(bin, valid);
+        if (valid && (peers & ((1ull << lane) - 1ull)) == 0ull) atomicAdd(&s_off[bin], (uint32_t)__popcll(peers));
     }
     __syncthreads();
     if (t < 64u) {   // exclusive scan of the 33 bin counts (one wave)
-        const uint32_t c = t < 33u ? s_off[t] : 0u;
-        const uint32_t incl = wave_inclusive_scan_u32(c);
-        if (t < 33u) s_off[t] = incl - c;
+        const uint32_t v = t < 33u ? s_off[t] : 0u;
+        const uint32_t incl = wave_inclusive_scan_u32(v);
+        if (t < 33u) s_off[t] = incl - v;
     }
     __syncthreads();
     // pass 2: positions
-    for (uint32_t q = 0; q < n_tiles; q += 1024u) {
-        const uint32_t i = q + t;
-        const bool valid = i < n_tiles;
-        const uint32_t bin = !valid ? 0u : in_lds ? (uint32_t)s_bin[i] : bin_of(ranges[i]);
+    for (uint32_t q = 0; q < n_c; q += 512u) {
+        const uint32_t k = q + t;
+        const bool valid = k < n_c;
+        const uint32_t bin = !valid ? 0u : q == 0u ? bin0 : bin_at(k);
         const uint64_t peers = peers_of(bin, valid);
         const uint64_t below = peers & ((1ull << lane) - 1ull);
         const uint32_t leader = valid ? (uint32_t)__builtin_ctzll(peers) : 0u;
         uint32_t base = 0;
         if (valid && below == 0ull) base = atomicAdd(&s_off[bin], (uint32_t)__popcll(peers));
         base = (uint32_t)__shfl((int)base, (int)leader);
-        if (valid) order[base + (uint32_t)__popcll(below)] = i;
+        if (valid) order[(base + (uint32_t)__popcll(below)) * kOrderChunks + c] = c + k * kOrderChunks;
     }
 }
 
 bool launch_tile_order(const uint2* ranges, uint32_t n_tiles, uint32_t* order, const BinCtl* ctl, hipStream_t s) {
     if (!order || n_tiles == 0u || n_tiles > kOrderMaxTiles) return false;
-    tile_order_kernel<<<1, 1024, 0, s>>>(ranges, n_tiles, order, ctl);
+    tile_order_kernel<<<kOrderChunks, 512, 0, s>>>(ranges, n_tiles, order, ctl);
     return true;
 }
 
