@@ -77,6 +77,26 @@ __device__ __forceinline__ uint32_t row_of(uint32_t e, int w) {
 // Each thread updates kAdamVecPerThread 4-element vectors with 16-byte loads
 // and stores (8-byte for fp16 theta); lanes of a wave cover consecutive
 // vectors. All loads of a thread are issued before any arithmetic.
+// simple_adam.cu:475-480: the bias corrections of step t, in double, rounded
+// to float (1 - beta1^t and sqrt(1 - beta2^t)), as float bits at out[0], out[1]
+__device__ __forceinline__ void adam_state_corrections(uint32_t* out, uint32_t t, float beta1, float beta2) {
+    const double st = (double)t;
+    out[0] = f2u((float)(1.0 - pow((double)beta1, st)));
+    out[1] = f2u((float)sqrt(1.0 - pow((double)beta2, st)));
+}
+
+// Device step state [0] count t, [1..2] the corrections of t, [3..4] those of
+// t + 1: one step on (an advancing launch used [3..4]); the next step's
+// corrections are computed here, once per launch, so a launch's workgroups
+// only read them.
+__device__ __forceinline__ void adam_state_advance(uint32_t* state, float beta1, float beta2) {
+    const uint32_t t = state[0] + 1u;
+    state[0] = t;
+    state[1] = state[3];
+    state[2] = state[4];
+    adam_state_corrections(state + 3, t + 1u, beta1, beta2);
+}
+
 // SEL: 0 every row, kAdamRowsUnmarked / kAdamRowsMarked one part of the rows
 // (a compile-time choice: the selection costs VALU the full step does not need)
 template <int SEL>
@@ -89,9 +109,9 @@ __global__ void __launch_bounds__(kAdamThreads) adam_kernel(AdamLaunch L) {
     const AdamGroup& g = L.a.groups[gi];
     const float t1 = 1.0f - L.a.beta1, t2 = 1.0f - L.a.beta2;
     float bc1 = L.a.bc1, bc2s = L.a.bc2_sqrt;
-    if (L.a.dev_bc) {   // written by adam_bias_kernel just before on the same stream
-        bc1 = u2f(L.a.dev_bc[1]);
-        bc2s = u2f(L.a.dev_bc[2]);
+    if (L.a.dev_bc) {   // this count's corrections ([1], [2]) or the next one's ([3], [4])
+        bc1 = u2f(L.a.dev_bc[L.a.dev_advance ? 3 : 1]);
+        bc2s = u2f(L.a.dev_bc[L.a.dev_advance ? 4 : 2]);
     }
     const int64_t vbase = (b - L.block_start[gi]) * (kAdamChunk / 4) + threadIdx.x;
     constexpr int sel = SEL;
@@ -185,24 +205,59 @@ __global__ void __launch_bounds__(kAdamThreads) adam_kernel(AdamLaunch L) {
             }
         }
     }
+    // the last workgroup to finish stores the advanced count and its
+    // corrections (every workgroup read [0] before counting itself done).
+    // Workgroups count themselves done in kAdamDoneGroups counters on their
+    // own cache lines (workgroup b in b mod kAdamDoneGroups), so no address
+    // takes more than a group's share of the atomics; the last of a group
+    // counts the group into one more counter.
+    if (L.a.dev_bc && L.a.dev_advance && threadIdx.x == 0) {
+        const uint32_t g = blockIdx.x % kAdamDoneGroups;
+        const uint32_t quota = (gridDim.x - g + kAdamDoneGroups - 1u) / kAdamDoneGroups;
+        uint32_t* grp = L.a.dev_bc + kAdamDoneStride * (1u + g);
+        if (atomicAdd(grp, 1u) == quota - 1u) {
+            *grp = 0u;
+            __threadfence();
+            uint32_t* all = L.a.dev_bc + kAdamDoneStride * (1u + kAdamDoneGroups);
+            const uint32_t groups = min(gridDim.x, kAdamDoneGroups);
+            if (atomicAdd(all, 1u) == groups - 1u) {
+                *all = 0u;
+                adam_state_advance(L.a.dev_bc, L.a.beta1, L.a.beta2);
+            }
+        }
+    }
 }
 
 // The device-side step count of a captured (or replayed) step.
-__global__ void adam_seed_steps_kernel(uint32_t* state, uint32_t steps) {
-    if (threadIdx.x == 0) state[0] = steps;
+__global__ void adam_seed_steps_kernel(uint32_t* state, uint32_t steps, float beta1, float beta2) {
+    if (threadIdx.x == 0) {
+        state[0] = steps;
+        adam_state_corrections(state + 1, steps, beta1, beta2);
+        adam_state_corrections(state + 3, steps + 1u, beta1, beta2);
+    }
+    // the done counters of an advancing Adam launch
+    for (uint32_t g = threadIdx.x; g <= kAdamDoneGroups; g += blockDim.x) state[kAdamDoneStride * (1u + g)] = 0u;
 }
 
+// The stored corrections of the device count t and of t + 1 under new betas.
+__global__ void adam_rebeta_kernel(uint32_t* state, float beta1, float beta2) {
+    if (threadIdx.x == 0) {
+        adam_state_corrections(state + 1, state[0], beta1, beta2);
+        adam_state_corrections(state + 3, state[0] + 1u, beta1, beta2);
+    }
+}
+
+// An advancing step without an Adam launch (no rows).
 __global__ void adam_bias_kernel(uint32_t* state, float beta1, float beta2) {
-    if (threadIdx.x != 0) return;
-    const uint32_t t = state[0] + 1u;
-    const double st = (double)t;
-    state[0] = t;
-    state[1] = f2u((float)(1.0 - pow((double)beta1, st)));
-    state[2] = f2u((float)sqrt(1.0 - pow((double)beta2, st)));
+    if (threadIdx.x == 0) adam_state_advance(state, beta1, beta2);
 }
 
-void launch_adam_seed_steps(uint32_t* state, uint32_t steps, hipStream_t s) {
-    adam_seed_steps_kernel<<<1, 64, 0, s>>>(state, steps);
+void launch_adam_seed_steps(uint32_t* state, uint32_t steps, float beta1, float beta2, hipStream_t s) {
+    adam_seed_steps_kernel<<<1, 64, 0, s>>>(state, steps, beta1, beta2);
+}
+
+void launch_adam_rebeta(uint32_t* state, float beta1, float beta2, hipStream_t s) {
+    adam_rebeta_kernel<<<1, 64, 0, s>>>(state, beta1, beta2);
 }
 
 void launch_adam_bias(uint32_t* state, float beta1, float beta2, hipStream_t s) {
@@ -219,7 +274,10 @@ void launch_adam(const AdamArgs& a, hipStream_t s) {
         acc += (a.groups[k].count + kAdamChunk - 1) / kAdamChunk;
     }
     for (int k = a.n_groups; k < 7; ++k) L.block_start[k] = acc;
-    if (acc == 0) return;
+    if (acc == 0) {   // no rows: the count still advances
+        if (a.dev_bc && a.dev_advance) launch_adam_bias(a.dev_bc, a.beta1, a.beta2, s);
+        return;
+    }
     const int sel = a.row_mask ? a.row_select : 0;
     if (sel == kAdamRowsUnmarked)
         adam_kernel<kAdamRowsUnmarked><<<(unsigned)acc, kAdamThreads, 0, s>>>(L);

@@ -736,6 +736,10 @@ __global__ void __launch_bounds__(256) emit_kernel(const uint32_t* __restrict__ 
     __shared__ uint32_t s_key[kEmitStage], s_val[kEmitStage];
     __shared__ uint32_t s_marks[4][kWave];
     const uint32_t t = threadIdx.x;
+    // more instances than the buffers hold (a no-sync forward's reserved
+    // capacity; a waiting forward sizes them to the count): flagged for
+    // tgs_rasterizer_status, the slots beyond it are not written
+    if (blockIdx.x == 0 && t == 0 && (int64_t)ctl->I > max_inst) atomicOr(&ctl->err, kErrCapacity);
     const int64_t n = min((int64_t)ctl->V, max_count);
     const int64_t k0 = (int64_t)blockIdx.x * blockDim.x;
     if (k0 >= n) return;
@@ -937,15 +941,9 @@ void launch_tile_ranges(const uint32_t* inst_keys, const uint32_t* d_n, int64_t 
                                                                         n_tiles);
 }
 
-__global__ void capacity_check_kernel(BinCtl* ctl, int64_t cap) {
-    if (threadIdx.x == 0 && (int64_t)ctl->I > cap) atomicOr(&ctl->err, kErrCapacity);
-}
-
 __global__ void clear_err_bits_kernel(BinCtl* ctl, uint32_t bits) {
     if (threadIdx.x == 0) atomicAnd(&ctl->err, ~bits);
 }
-
-void launch_capacity_check(BinCtl* ctl, int64_t cap, hipStream_t s) { capacity_check_kernel<<<1, 64, 0, s>>>(ctl, cap); }
 
 void launch_clear_err_bits(BinCtl* ctl, uint32_t bits, hipStream_t s) {
     clear_err_bits_kernel<<<1, 64, 0, s>>>(ctl, bits);

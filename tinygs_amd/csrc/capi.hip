@@ -307,6 +307,7 @@ struct tgs_adam {
     int64_t steps = 0;
     DevBuf dev_state;           // TGS_ADAM_DEVICE_STEP: step count and bias corrections on the device
     bool dev_seeded = false;    // dev_state's count equals `steps` (set by the first device step)
+    float dev_beta1 = 0.f, dev_beta2 = 0.f;   // the betas dev_state's corrections were computed with
     bool last_dev = false;      // the last step's mode (TGS_ADAM_SAME_STEP repeats it)
 };
 
@@ -592,7 +593,7 @@ static int rasterizer_forward(tgs_rasterizer* r, const tgs_camera* camera, void*
         r->ikeys_from_ranges = ranges_done;
         r->tile_sort_cap = cap;
     }
-    if (nosync) launch_capacity_check(ctl, cap, s);
+    // (a no-sync forward's capacity check is in the emission)
     if (!nosync) {
         // the depth and tile sorts' look-back scans and the emission's offset
         // check ran after the counts copy: their error word, read once the
@@ -1132,13 +1133,17 @@ int tgs_adam_step_ex(tgs_adam* a, float scale, const uint8_t* row_mask, int32_t 
     // device steps continues from it (one wait on the stream)
     if (!dev && a->dev_seeded) TGS_TRY(adam_sync_steps(a, hs));
     if (dev && !same) {
-        TGS_TRY(ensure(a->dev_state, 16, hs));
+        TGS_TRY(ensure(a->dev_state, 4 * (size_t)kAdamStateWords, hs));
         if (!a->dev_seeded) {   // the device count starts from the host's
             if (a->steps > 0xfffffffell) return fail(TGS_ERR_INVALID, "step count beyond 32 bits");
-            launch_adam_seed_steps(a->dev_state.as<uint32_t>(), (uint32_t)a->steps, hs);
+            launch_adam_seed_steps(a->dev_state.as<uint32_t>(), (uint32_t)a->steps, a->p.beta1, a->p.beta2, hs);
             a->dev_seeded = true;
+        } else if (a->p.beta1 != a->dev_beta1 || a->p.beta2 != a->dev_beta2) {
+            // betas changed since: the stored corrections again, at the device count
+            launch_adam_rebeta(a->dev_state.as<uint32_t>(), a->p.beta1, a->p.beta2, hs);
         }
-        launch_adam_bias(a->dev_state.as<uint32_t>(), a->p.beta1, a->p.beta2, hs);
+        a->dev_beta1 = a->p.beta1;
+        a->dev_beta2 = a->p.beta2;
     } else if (!dev) {
         a->dev_seeded = false;   // a later device step restarts from the host count
     }
@@ -1164,6 +1169,7 @@ int tgs_adam_step_ex(tgs_adam* a, float scale, const uint8_t* row_mask, int32_t 
     args.row_mask = row_mask;
     args.row_select = rows_sel;
     args.dev_bc = dev ? a->dev_state.as<uint32_t>() : nullptr;
+    args.dev_advance = dev && !same;   // the Adam launch advances the device count itself
     void* th[6] = {a->params.means, a->params.opacities, a->params.rotations, a->params.scales, a->params.sh0,
                    a->params.sh_rest};
     const float* gr[6] = {(const float*)a->grads.means, (const float*)a->grads.opacities,

@@ -77,8 +77,6 @@ static_assert(offsetof(BinCtl, bwd_queue) == 128, "backward queue counters start
 constexpr uint32_t kErrLookBack = 1u;   // a look-back scan gave up waiting (spin bound)
 constexpr uint32_t kErrOffsets = 2u;    // instance offsets beyond the instance buffers
 constexpr uint32_t kErrCapacity = 4u;   // more instances than the reserved capacity (no-sync forward)
-// Sets kErrCapacity when ctl->I > cap.
-void launch_capacity_check(BinCtl* ctl, int64_t cap, hipStream_t s);
 // Clears the given err bits.
 void launch_clear_err_bits(BinCtl* ctl, uint32_t bits, hipStream_t s);
 // Words of bwd_queue: what a backward needs cleared.
@@ -360,9 +358,15 @@ struct AdamArgs {
     // row_mask[i] == 0 (zero gradient, none read), kAdamRowsMarked only the
     // others; the elements of the rows left out are neither read nor written
     int row_select;
-    // optional: the bias corrections (bc1, bc2_sqrt as floats at [1], [2]) come
-    // from this device state instead of bc1 / bc2_sqrt (launch_adam_bias)
-    const uint32_t* dev_bc;
+    // optional: the bias corrections come from this device state
+    // (kAdamStateWords words: [0] step count t, [1] bc1 and [2] bc2_sqrt of t,
+    // [3] and [4] those of t + 1, as float bits; done counters from word
+    // kAdamDoneStride on) instead of bc1 / bc2_sqrt. dev_advance: this launch
+    // is step t + 1 (reads [3], [4]; its last workgroup to finish advances the
+    // state, no separate launch_adam_bias); otherwise it repeats step t
+    // (reads [1], [2])
+    uint32_t* dev_bc;
+    int dev_advance;
     int n_groups;
     float beta1, beta2, eps, grad_scale, bc1, bc2_sqrt, max_grad;
 };
@@ -371,15 +375,21 @@ struct AdamArgs {
 // zeroed before.
 void launch_backward_rows(const uint4* items, const uint32_t* inst_vals, const BinCtl* ctl, uint8_t* rows,
                           hipStream_t s);
+constexpr uint32_t kAdamDoneGroups = 64;   // done counters of an advancing Adam launch
+constexpr uint32_t kAdamDoneStride = 32;   // words between them (one 128-byte line each)
+constexpr uint32_t kAdamStateWords = kAdamDoneStride * (kAdamDoneGroups + 2u);
 constexpr int kAdamRowsUnmarked = 1;
 constexpr int kAdamRowsMarked = 2;
 void launch_adam(const AdamArgs& a, hipStream_t s);
-// Device-side step count for SimpleAdam (state: [0] steps, [1] bc1, [2]
-// sqrt(bc2) as float bits): seeds state[0] = steps, or advances it by one and
-// writes the bias corrections of the new count (simple_adam.cu:475-480: in
-// double, rounded to float), so a captured step replays with the right count.
-void launch_adam_seed_steps(uint32_t* state, uint32_t steps, hipStream_t s);
+// Device-side step count for SimpleAdam (the state of AdamArgs::dev_bc):
+// seeds it at `steps` (with the corrections of steps and steps + 1, and the
+// done counters cleared), or advances it by one step without an Adam launch
+// (simple_adam.cu:475-480: corrections in double, rounded to float), so a
+// captured step replays with the right count.
+void launch_adam_seed_steps(uint32_t* state, uint32_t steps, float beta1, float beta2, hipStream_t s);
 void launch_adam_bias(uint32_t* state, float beta1, float beta2, hipStream_t s);
+// Recomputes the stored corrections for new betas, keeping the count.
+void launch_adam_rebeta(uint32_t* state, float beta1, float beta2, hipStream_t s);
 
 // ---- self tests of wave primitives and deterministic math (debug entry points)
 void launch_detmath(int op, const float* in, float* out, int64_t n, hipStream_t s);
