@@ -414,7 +414,12 @@ def main():
           f"sh_degree={scene.sh_degree} sh_storage={scene.sh_dtype} (generated in {time.time() - t0:.1f}s)",
           file=sys.stderr, flush=True)
     f16 = args.image_dtype == "float16"
-    ts = TrainStep(scene, l1_weight=0.8, ssim_weight=0.2, eps=1e-15, shs_lr=5e-3, image_dtype=args.image_dtype)
+    # the no-sync step (no host waits inside the step; the first warmup step
+    # sizes the buffers and reserves 1.25x its instance count), checked for a
+    # capacity overflow after the timed steps: the same kernels and results
+    # as the waiting step (tests/test_gpu_forward_modes.py)
+    ts = TrainStep(scene, l1_weight=0.8, ssim_weight=0.2, eps=1e-15, shs_lr=5e-3, image_dtype=args.image_dtype,
+                   no_sync=True)
     L = _lib.load()
     stream = torch.cuda.current_stream()
 
@@ -434,6 +439,7 @@ def main():
     stop.record(stream)
     torch.cuda.synchronize()
     ms = start.elapsed_time(stop) / args.steps
+    ts.check_status()   # raises if a timed step outgrew the reserved instance capacity
 
     # per-stage breakdown: K more steps with one event pair per stage per step
     # (the events add gaps of their own, so these steps are not the timed ones)
@@ -525,6 +531,7 @@ def main():
                    "sh_storage": scene.sh_dtype, "image_dtype": args.image_dtype, "n_visible": V,
                    "n_instances": I, "n_tiles": T,
                    "gradient_rows": live, "sparse_gradients": ts.sparse_grads,
+                   "step_mode": "no-sync (reserved instance capacity, no host wait inside a step)",
                    "parallelism": "single GPU"},
         "stages_ms": {r[0]: round(r[1], 5) for r in rows},
         "roofline": roofline,
