@@ -205,22 +205,23 @@ __global__ void __launch_bounds__(kAdamThreads) adam_kernel(AdamLaunch L) {
             }
         }
     }
-    // the last workgroup to finish stores the advanced count and its
-    // corrections (every workgroup read [0] before counting itself done).
-    // Workgroups count themselves done in kAdamDoneGroups counters on their
-    // own cache lines (workgroup b in b mod kAdamDoneGroups), so no address
-    // takes more than a group's share of the atomics; the last of a group
-    // counts the group into one more counter.
+    // An advancing launch: the last workgroup to finish stores the advanced
+    // count and the next corrections (every workgroup read them before
+    // counting itself done). Workgroups count themselves done in
+    // kAdamDoneGroups counters on their own cache lines (workgroup b in
+    // b mod kAdamDoneGroups), so no address takes more than a group's share
+    // of the atomics; the last of a group counts the group in one more
+    // counter. (Relaxed atomics: the counters' resets and the new state are
+    // read only by later launches.)
+    if (L.a.dev_bc && L.a.dev_advance) __syncthreads();   // every wave of the workgroup has read them
     if (L.a.dev_bc && L.a.dev_advance && threadIdx.x == 0) {
         const uint32_t g = blockIdx.x % kAdamDoneGroups;
         const uint32_t quota = (gridDim.x - g + kAdamDoneGroups - 1u) / kAdamDoneGroups;
         uint32_t* grp = L.a.dev_bc + kAdamDoneStride * (1u + g);
         if (atomicAdd(grp, 1u) == quota - 1u) {
             *grp = 0u;
-            __threadfence();
             uint32_t* all = L.a.dev_bc + kAdamDoneStride * (1u + kAdamDoneGroups);
-            const uint32_t groups = min(gridDim.x, kAdamDoneGroups);
-            if (atomicAdd(all, 1u) == groups - 1u) {
+            if (atomicAdd(all, 1u) == min(gridDim.x, kAdamDoneGroups) - 1u) {
                 *all = 0u;
                 adam_state_advance(L.a.dev_bc, L.a.beta1, L.a.beta2);
             }
