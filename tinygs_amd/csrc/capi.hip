@@ -614,7 +614,7 @@ static int rasterizer_forward(tgs_rasterizer* r, const tgs_camera* camera, void*
                                  r->conic_opacity.as<float4>(), r->color.as<float4>(), (float*)image,
                                  r->n_contrib.as<uint32_t>(), r->tile_max.as<uint32_t>(),
                                  r->tile_loaded.as<uint32_t>(), r->ckpt.as<float4>(), r->items.as<uint4>(), ctl,
-                                 nullptr, s);
+                                 cap >= (int64_t)T * kOrderHeavyTile ? r->tile_order.as<uint32_t>() : nullptr, s);
     }
     TGS_CHECK_LAUNCH();
     if (!nosync) {

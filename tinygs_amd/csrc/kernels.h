@@ -206,6 +206,13 @@ void launch_preprocess16(const GaussianView& g, const CamParams& cam, uint32_t* 
 // length); the fp32 forward measured slower with it (index order keeps
 // neighbouring tiles, which share Gaussians, together in the caches).
 constexpr uint32_t kOrderMaxTiles = 1u << 20;
+// The fp32 blend forward takes tiles long ones first only from this many
+// instances per tile on average (heavy scenes): measured 12% slower at 632
+// per tile (the order costs locality between neighbouring tiles), even at
+// 8.4k; at 16.8k (3M Gaussians at 3840x2160) fwd + bwd took 16.1-17.7 ms
+// ordered against 16.1-18.2 ms in index order over three runs each (the
+// runs there split into a fast and a slow mode either way).
+constexpr int64_t kOrderHeavyTile = 8192;
 bool launch_tile_order(const uint2* ranges, uint32_t n_tiles, uint32_t* order, const BinCtl* ctl, hipStream_t s);
 
 // Blend of FGS16 (fgs16.hip): image / grad image are 3 half planes of the
