@@ -411,15 +411,20 @@ static int plan_sorts(const CamParams& cam, SortPlan& sp) {
         sp.dbits[p] = (key_bits + sp.n_dp - 1) / sp.n_dp;
         sp.dshift[p] = p * sp.dbits[p];
     }
-    // tile key bits: passes of at most 8 bits, as even as possible (the
-    // earlier passes take the odd bits): 16 bits (65,536 tiles, the fp32
-    // limit) in two passes, up to 24 in three, up to 27 (fp16 images) in four
+    // tile key bits: passes of at most 8 bits, as even as possible, the later
+    // passes taking the odd bits: 16 bits (65,536 tiles, the fp32 limit) in
+    // two passes, up to 24 in three, up to 27 (fp16 images) in four. The
+    // first pass reads the instances in emission order, where one
+    // primitive's keys run over consecutive tiles, and scatters into fewer
+    // buckets that way: at 545M instances over 15 tile bits its downsweep
+    // took 3.9-4.0 ms with 128 buckets, against 3.6 or 5.4 ms (varying from
+    // run to run) with 256
     const uint32_t T = cam.grid_w * cam.grid_h;
     int bits = 1;
     while (bits < 32 && (1u << bits) < T) ++bits;
     sp.n_tp = (bits + 7) / 8;
     for (int p = 0, sh = 0; p < sp.n_tp; ++p) {
-        sp.tbits[p] = bits / sp.n_tp + (p < bits % sp.n_tp ? 1 : 0);
+        sp.tbits[p] = bits / sp.n_tp + (p >= sp.n_tp - bits % sp.n_tp ? 1 : 0);
         sp.tshift[p] = sh;
         sh += sp.tbits[p];
     }
