@@ -74,9 +74,6 @@ __device__ __forceinline__ uint32_t row_of(uint32_t e, int w) {
     }
 }
 
-// Each thread updates kAdamVecPerThread 4-element vectors with 16-byte loads
-// and stores (8-byte for fp16 theta); lanes of a wave cover consecutive
-// vectors. All loads of a thread are issued before any arithmetic.
 // simple_adam.cu:475-480: the bias corrections of step t, in double, rounded
 // to float (1 - beta1^t and sqrt(1 - beta2^t)), as float bits at out[0], out[1]
 __device__ __forceinline__ void adam_state_corrections(uint32_t* out, uint32_t t, float beta1, float beta2) {
@@ -97,6 +94,9 @@ __device__ __forceinline__ void adam_state_advance(uint32_t* state, float beta1,
     adam_state_corrections(state + 3, t + 1u, beta1, beta2);
 }
 
+// Each thread updates kAdamVecPerThread 4-element vectors with 16-byte loads
+// and stores (8-byte for fp16 theta); lanes of a wave cover consecutive
+// vectors. All loads of a thread are issued before any arithmetic.
 // SEL: 0 every row, kAdamRowsUnmarked / kAdamRowsMarked one part of the rows
 // (a compile-time choice: the selection costs VALU the full step does not need)
 template <int SEL>
