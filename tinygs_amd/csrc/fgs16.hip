@@ -20,9 +20,9 @@
 //     one half2; every image / count / checkpoint access of a block is one
 //     contiguous run. Each wave stages the tile's Gaussians 64 at a time,
 //     one per lane, in LDS; each Gaussian's words then reach every lane as
-//     a broadcast read (no VALU). Tiles are
-//     taken long ones first (tile_order_kernel): the kernel's length was
-//     set by long tiles whose waves started late.
+//     a broadcast read (no VALU). Tiles are taken roughly long ones first
+//     (tile_order_kernel): the kernel's length was set by long tiles whose
+//     waves started late.
 //   * backward: one (tile, 32-Gaussian bucket) work item per half wave, two
 //     per wave. As in the reference, lane l of the half owns Gaussian l of the
 //     bucket and the tile's 128 pixel pairs stream through the lanes: at step
