@@ -490,12 +490,14 @@ int tgs_rasterizer_work_stats(tgs_rasterizer* r, int64_t* fwd_loaded, int64_t* b
 int tgs_selftest_detmath(int32_t op, const float* in, float* out, int64_t n, void* stream);
 int tgs_selftest_wave(const uint32_t* in, uint32_t* out, void* stream);
 /* The fp16 rasterizer's canonical half operations on arrays of half bit
- * patterns (ops 7, 8 take floats in a, op 11 int64): 0 exp2, 1 the hardware
- * v_exp_f16 (measurement only), 2 fma(a, b, c), 3 a * b, 4 a + b, 5 a / b,
- * 6 packed fma, 7 float -> half nearest, 8 float -> half toward -inf,
- * 9 a - b, 10 minNum(a, b), 11 the nearest half of a * 2^-24, 12 the lane
- * shift the fp16 blend backward uses (out[i] = a[i - 1] within each 64-lane
- * wave, b[i] at lane 0; n a multiple of 64). Tests only. */
+ * patterns (ops 7, 8 take floats in a, op 11 int64, op 14 doubles): 0 exp2,
+ * 1 the hardware v_exp_f16 (measurement only), 2 fma(a, b, c), 3 a * b,
+ * 4 a + b, 5 a / b, 6 packed fma, 7 float -> half nearest, 8 float -> half
+ * toward -inf, 9 a - b, 10 minNum(a, b), 11 the nearest half of a * 2^-24,
+ * 12 the lane shift the fp16 blend backward uses (out[i] = a[i - 1] within
+ * each 64-lane wave, b[i] at lane 0; n a multiple of 64), 13 the packed exp2
+ * of the pair (a[i], b[i]), out[i] its lane i & 1, 14 the nearest half of an
+ * exact double sum of halves. Tests only. */
 int tgs_selftest_half(int32_t op, const void* a, const void* b, const void* c, void* out, int64_t n, void* stream);
 /* The half division of the fp16 rasterizer over every finite operand pair
  * with a nonzero divisor, checked on the device against the correctly

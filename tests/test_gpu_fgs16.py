@@ -261,10 +261,10 @@ def test_fgs16_half_division_correctly_rounded(hip):
 def test_fgs16_blend_division_correctly_rounded(hip):
     """h2_div_blend, the backward's cadg / (1 - alpha) by Markstein's
     iteration on the half reciprocal: equal to the correctly rounded quotient
-    (h_div, checked over all pairs above) for every half dividend and every
-    divisor 1 - alpha can take (alpha in [0, RN(0.99)]: bits 0x2100 ..
-    0x3c00); the half reciprocal equals the correctly rounded one for every
-    positive finite half."""
+    (h_div, checked over all pairs above) in both lanes for every half
+    dividend and every divisor 1 - alpha can take (alpha in [0, RN(0.99)]:
+    bits 0x2100 .. 0x3c00); the half reciprocal equals the correctly rounded
+    one for every positive finite half."""
     import torch
     from tinygs_amd import _lib
     L = _lib.load()

@@ -1,9 +1,9 @@
 """The fp16 rasterizer's canonical half operations on the GPU
 (tinygs_amd/csrc/halfmath.h) against the oracle's (oracle/halfmath.h, pinned
-by tests/test_halfmath_host.py): exp2 over all 65,536 inputs, the arithmetic
-and conversions on random inputs with subnormals, packed and scalar; the
-rounding of exact fixed-point sums; the lane layout of the DPP shift the fp16
-blend backward uses."""
+by tests/test_halfmath_host.py): exp2 over all 65,536 inputs in both lanes of
+the packed form, the arithmetic and conversions on random inputs with
+subnormals, packed and scalar; the rounding of exact fixed-point and double
+sums; the lane layout of the DPP shift the fp16 blend backward uses."""
 import numpy as np
 import pytest
 
@@ -13,7 +13,8 @@ pytestmark = pytest.mark.gpu
 def _gpu(op, a, b=None, c=None):
     import torch
     from tinygs_amd import _lib
-    view = {np.dtype(np.uint16): np.int16, np.dtype(np.int64): np.int64}.get(a.dtype, np.float32)
+    view = {np.dtype(np.uint16): np.int16, np.dtype(np.int64): np.int64,
+            np.dtype(np.float64): np.float64}.get(a.dtype, np.float32)
     ta = torch.from_numpy(np.ascontiguousarray(a).view(view)).cuda()
     tb = None if b is None else torch.from_numpy(b.view(np.int16)).cuda()
     tc = None if c is None else torch.from_numpy(c.view(np.int16)).cuda()
@@ -39,6 +40,21 @@ def test_exp2_all_inputs(hip, orc):
           f"of 65536 inputs: {x[bad_hw][:8]}", flush=True)
     ok = _same(got, want)
     assert ok.all(), (np.count_nonzero(~ok), x[~ok][:8], got[~ok][:8], want[~ok][:8])
+
+
+def test_packed_exp2_both_lanes(hip, orc):
+    """The packed exp2 (two v_exp_f16, the second written into the high half)
+    equals the canonical exp2 in both lanes for every input: element i takes
+    lane i & 1 of exp2((a[i], b[i])); the second call swaps the roles, so
+    every input passes through each lane."""
+    x = np.arange(1 << 16, dtype=np.uint32).astype(np.uint16)
+    xr = np.roll(x, 1)
+    odd = (np.arange(x.size) & 1).astype(bool)
+    for a, b in ((x, xr), (xr, x)):
+        got = _gpu(13, a, b)
+        want = orc.half_op(0, np.where(odd, b, a))
+        ok = _same(got, want)
+        assert ok.all(), (np.count_nonzero(~ok), a[~ok][:4], b[~ok][:4], got[~ok][:4], want[~ok][:4])
 
 
 @pytest.mark.parametrize("op", [2, 3, 4, 5, 6, 9, 10])
@@ -78,6 +94,33 @@ def test_fixed_point_rounding(hip, orc):
     s = np.concatenate([s, ties, ties - 1, ties + 1, -ties, [0, 1, -1, (65520 << 24) - 1, 65520 << 24]]).astype(np.int64)
     got, want = _gpu(11, s), orc.half_op(11, s)
     assert np.array_equal(got, want), (np.count_nonzero(got != want), s[got != want][:4])
+
+
+def test_double_sum_rounding(hip, orc):
+    """half_of_double_sum (the fp16 preprocess backward's rounding of its exact
+    double sums of half records) equals the correctly rounded half of the
+    same value as an exact fixed-point integer, including sums a float ulp
+    (or less) from a half midpoint, where rounding through float would round
+    twice: m + 2^-24 for a midpoint m in [1, 2) is a float midpoint."""
+    rng = np.random.default_rng(14)
+    e = rng.integers(-13, 16, 4096)   # binade of the midpoint (sums of halves: multiples of 2^-24)
+    q = rng.integers(1 << 10, 1 << 11, 4096)   # half significand
+    mid = (2 * q + 1).astype(np.float64) * np.exp2(e - 11.0)   # a half midpoint
+    k = rng.integers(-3, 4, 4096)
+    near = np.concatenate([mid + k * 2.0 ** -24, mid, -(mid + 2.0 ** -24), mid + 2.0 ** -24])
+    near = near[np.abs(near) < 2.0 ** 29]
+    rand = rng.integers(-(1 << 52), 1 << 52, 1 << 16) >> rng.integers(0, 50, 1 << 16)
+    s = np.concatenate([near, rand.astype(np.float64) * 2.0 ** -24, [0.0, 65519.0, 65520.0, -65520.0]])
+    fixed = np.rint(s * 2.0 ** 24).astype(np.int64)
+    assert np.array_equal(fixed.astype(np.float64) * 2.0 ** -24, s)   # exact: multiples of 2^-24
+    got, want = _gpu(14, s), orc.half_op(11, fixed)
+    assert np.array_equal(got, want), (np.count_nonzero(got != want), s[got != want][:4])
+    # through float the midpoint cases round twice; at least one of them differs
+    with np.errstate(over="ignore"):
+        twice = s.astype(np.float32).astype(np.float16).view(np.uint16)
+    assert np.count_nonzero(twice != want) > 0
+    special = _gpu(14, np.array([np.inf, -np.inf, np.nan]))
+    assert special[0] == 0x7c00 and special[1] == 0xfc00 and np.isnan(special[2:].view(np.float16)).all()
 
 
 def test_dpp_wave_shift_lane_layout(hip, orc):

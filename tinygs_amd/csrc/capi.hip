@@ -1692,9 +1692,9 @@ int tgs_selftest_detmath(int32_t op, const float* in, float* out, int64_t n, voi
 int tgs_selftest_half(int32_t op, const void* a, const void* b, const void* c, void* out, int64_t n, void* stream) {
     if (n < 0 || (n > 0 && (!a || !out))) return fail(TGS_ERR_INVALID, "bad argument");
     if ((op == 2 || op == 6) && n > 0 && (!b || !c)) return fail(TGS_ERR_INVALID, "bad argument");
-    if ((op == 3 || op == 4 || op == 5 || op == 9 || op == 10 || op == 12) && n > 0 && !b)
+    if ((op == 3 || op == 4 || op == 5 || op == 9 || op == 10 || op == 12 || op == 13) && n > 0 && !b)
         return fail(TGS_ERR_INVALID, "bad argument");
-    if (op < 0 || op > 12 || (op == 12 && n % 64 != 0)) return fail(TGS_ERR_INVALID, "op %d, n %lld", op, (long long)n);
+    if (op < 0 || op > 14 || (op == 12 && n % 64 != 0)) return fail(TGS_ERR_INVALID, "op %d, n %lld", op, (long long)n);
     launch_halfmath(op, (const uint16_t*)a, (const uint16_t*)b, (const uint16_t*)c, (uint16_t*)out, n,
                     (hipStream_t)stream);
     TGS_CHECK_LAUNCH();

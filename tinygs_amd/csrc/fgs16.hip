@@ -34,6 +34,8 @@
 //     binning reserved (as the fp32 path); the preprocess backward sums them
 //     exactly (halfmath.h half_of_fixed) instead of the reference's half2
 //     atomics, whose rounding depends on the order buckets finish in.
+#include <type_traits>
+
 #include "common.h"
 #include "fgs16.h"
 #include "kernels.h"
@@ -294,10 +296,19 @@ void launch_blend16_forward(const CamParams& cam, uint2* ranges, const uint32_t*
 
 namespace {
 
-// per pixel pair: grad r, g, b; colour after r, g, b; transmittance; (offx, offy)
-struct PairState {
-    uint32_t v[8];
-};
+// LDS byte address of a __shared__ object, and the 16 bytes at one
+typedef uint32_t v4u32 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) const v4u32 lds_v4;
+__device__ __forceinline__ uint32_t lds_addr(const uint4* p) { return (uint32_t)(uintptr_t)(lds_v4*)p; }
+__device__ __forceinline__ uint4 lds_u4_at(uint32_t a) {
+    const v4u32 v = *(lds_v4*)(uintptr_t)a;
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+// s_pair[0]: per wave, half wave and pixel pair the static words (grad r, g,
+// b, (offx, offy)); s_pair[1] the state at the bucket start (colour after r,
+// g, b, T), kPairInitOfs bytes after the pair's static words
+constexpr uint32_t kPairInitOfs = 4u * 2u * 128u * 16u;
 
 __device__ __forceinline__ uint32_t shr1(uint32_t x) {
     // DPP wave_shr:1: lane l receives lane l - 1 (lane 0: 0, bound_ctrl)
@@ -311,10 +322,7 @@ __global__ void __launch_bounds__(256) blend16_backward_kernel(
     const uint4* __restrict__ info, const uint16_t* __restrict__ image, const uint16_t* __restrict__ grad_image,
     const uint2* __restrict__ ckpt, const uint4* __restrict__ items, BinCtl* __restrict__ ctl,
     uint32_t* __restrict__ rec_count, const uint32_t* __restrict__ first_slot, float4* __restrict__ records) {
-    // per wave and half wave, per pixel pair: the static words (grad r, g, b,
-    // (offx, offy)) and the state at the bucket start (colour after r, g, b, T)
-    __shared__ uint4 s_static[4][2][128];
-    __shared__ uint4 s_init[4][2][128];
+    __shared__ uint4 s_pair[2][4][2][128];   // static words, then the bucket-start state
 
     const uint32_t w = threadIdx.x >> 6, lane = threadIdx.x & 63u;
     const uint32_t half = lane >> 5, l = lane & 31u;
@@ -397,8 +405,8 @@ __global__ void __launch_bounds__(256) blend16_backward_kernel(
                                    h2bits(KT * h2s(hfrom(kHUnscale))), 0u);
                 }
                 c.w = (uint32_t)hbits((h16)(float)dx_) | ((uint32_t)hbits((h16)(float)dy_) << 16);
-                s_static[w][half][i] = make_uint4(a.x, a.y, a.z, c.w);
-                s_init[w][half][i] = make_uint4(a.w, c.x, c.y, c.z);
+                s_pair[0][w][half][i] = make_uint4(a.x, a.y, a.z, c.w);
+                s_pair[1][w][half][i] = make_uint4(a.w, c.x, c.y, c.z);
             }
         }
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -410,67 +418,101 @@ __global__ void __launch_bounds__(256) blend16_backward_kernel(
         h16x2 a_op = a_mx, a_r = a_mx, a_g = a_mx, a_b = a_mx;
         // lane l at step s works on pair s - l: its static words from LDS
         // (loaded a step ahead), its state (colour after, T) from lane l - 1
-        // (lanes 0 and 32: the pair's state at the bucket start, from LDS)
+        // (lanes 0 and 32: the pair's state at the bucket start, from LDS).
+        // Steps 31..127 have every lane on a pair (no per-lane test) and steps
+        // below 128 start a pair at lanes 0 and 32; the loops run two steps
+        // per iteration, so the staged words need no register copy.
         uint32_t st[4] = {0u, 0u, 0u, 0u};
-        const uint4* sst = s_static[w][half];
-        const uint4* sin = s_init[w][half];
+        const uint32_t a_lo = lds_addr(&s_pair[0][w][half][0]), a_hi = a_lo + 127u * 16u;
+        uint32_t a = a_lo + 16u * (1u - l);   // entry s - l + 1 at step s (unclamped)
         const uint32_t cmax = max(readlane_u32(cnt, 0), readlane_u32(cnt, 32));
         const uint32_t steps = cmax ? 128u + cmax - 1u : 0u;
-        uint4 cur = sst[min(0u - l, 127u)];
-        for (uint32_t s = 0; s < steps; ++s) {
-            const uint32_t i = s - l;
-            const uint4 nxt = sst[min(i + 1u, 127u)];
-            if (l == 0u && s < 128u) {
-                const uint4 c = sin[s];
-                st[0] = c.x; st[1] = c.y; st[2] = c.z; st[3] = c.w;
-            }
-            if (i < 128u && l < cnt) {
-                const h16x2 G0 = h2from(cur.x), G1 = h2from(cur.y), G2 = h2from(cur.z);
-                h16x2 Ca0 = h2from(st[0]), Ca1 = h2from(st[1]), Ca2 = h2from(st[2]);
-                const h16x2 T = h2from(st[3]);
-                const h16x2 off = h2from(cur.w);
-                const h16x2 offx = h2s(off.x), offy = h2s(off.y);
-                const h16x2 dlx = h2_fma(inv16, -offx, mxp);
-                const h16x2 dly = h2_fma(inv16, -offy, my2);
-                const h16x2 cx_dx = cx2 * dlx, cy_dx = cy2 * dlx, cz_dy = cz2 * dly, cy_dy = cy2 * dly;
-                const h16x2 cz_dyy = dly * cz_dy, cy_dxy = dlx * cy_dy;
-                const h16x2 quad = h2_fma(dlx, cx_dx, cz_dyy);
-                const h16x2 prep_x = cx_dx + cy_dy;
-                const h16x2 gss = h2_exp2(h2_relu(h2_fma(h05, quad, cy_dxy)) * nk);
-                const h16x2 prep_y = cy_dx + cz_dy;
-                const h16x2 alpha_p = o2 * gss;
-                const h16x2 cdg = h2_fma(cr2, G0, h2_fma(cg2, G1, cb2 * G2));
-                const h16x2 alpha = h2_min(alpha_p, maxa);
-                const h16x2 bw = T * alpha;
-                const h16x2 oma = one - alpha;
-                a_r = h2_fma(bw, G0, a_r);
-                a_g = h2_fma(bw, G1, a_g);
-                a_b = h2_fma(bw, G2, a_b);
-                Ca0 = h2_fma(-bw, cr2, Ca0);
-                Ca1 = h2_fma(-bw, cg2, Ca1);
-                Ca2 = h2_fma(-bw, cb2, Ca2);
-                const h16x2 cadg = h2_fma(Ca0, G0, h2_fma(Ca1, G1, Ca2 * G2));
-                const h16x2 dal = h2_fma(T, cdg, -h2_div_blend(cadg, oma));   // oma in [0x1.4p-7, 1]
-                const h16x2 part = alpha * dal;
-                a_op = part + a_op;
-                const h16x2 dxdx = dlx * dlx, dxdy = dlx * dly, dydy = dly * dly;
-                a_cx = part * dxdx + a_cx;
-                a_cy = part * dxdy + a_cy;
-                a_cz = part * dydy + a_cz;
-                const h16x2 nT = T * oma;
-                const h16x2 dmx = part * prep_x, dmy = part * prep_y;
-                a_mx = dmx + a_mx;
-                a_my = dmy + a_my;
-                a_ax = h2from(h2bits(dmx) & 0x7fff7fffu) + a_ax;
-                a_ay = h2from(h2bits(dmy) & 0x7fff7fffu) + a_ay;
-                st[0] = h2bits(Ca0);
-                st[1] = h2bits(Ca1);
-                st[2] = h2bits(Ca2);
-                st[3] = h2bits(nT);
+        uint4 cur = lds_u4_at(min(max(a - 16u, a_lo), a_hi));
+        auto step = [&](uint32_t s, const uint4& cur, auto start, auto check) {
+            if constexpr (decltype(start)::value)
+                if (l == 0u) {   // pair s's state at the bucket start: entry s of the init words
+                    const uint4 c = lds_u4_at(a - 16u + kPairInitOfs);
+                    st[0] = c.x; st[1] = c.y; st[2] = c.z; st[3] = c.w;
+                }
+            bool act = l < cnt;
+            if constexpr (decltype(check)::value) act = act && s - l < 128u;
+            if (act) {
+                    const h16x2 G0 = h2from(cur.x), G1 = h2from(cur.y), G2 = h2from(cur.z);
+                    h16x2 Ca0 = h2from(st[0]), Ca1 = h2from(st[1]), Ca2 = h2from(st[2]);
+                    const h16x2 T = h2from(st[3]);
+                    const h16x2 off = h2from(cur.w);
+                    const h16x2 offx = h2s(off.x), offy = h2s(off.y);
+                    const h16x2 dlx = h2_fma(inv16, -offx, mxp);
+                    const h16x2 dly = h2_fma(inv16, -offy, my2);
+                    const h16x2 cx_dx = cx2 * dlx, cy_dx = cy2 * dlx, cz_dy = cz2 * dly, cy_dy = cy2 * dly;
+                    const h16x2 cz_dyy = dly * cz_dy, cy_dxy = dlx * cy_dy;
+                    const h16x2 quad = h2_fma(dlx, cx_dx, cz_dyy);
+                    const h16x2 prep_x = cx_dx + cy_dy;
+                    const h16x2 gss = h2_exp2(h2_relu(h2_fma(h05, quad, cy_dxy)) * nk);
+                    const h16x2 prep_y = cy_dx + cz_dy;
+                    const h16x2 alpha_p = o2 * gss;
+                    const h16x2 cdg = h2_fma(cr2, G0, h2_fma(cg2, G1, cb2 * G2));
+                    const h16x2 alpha = h2_min(alpha_p, maxa);
+                    const h16x2 bw = T * alpha;
+                    const h16x2 oma = one - alpha;
+                    a_r = h2_fma(bw, G0, a_r);
+                    a_g = h2_fma(bw, G1, a_g);
+                    a_b = h2_fma(bw, G2, a_b);
+                    Ca0 = h2_fma(-bw, cr2, Ca0);
+                    Ca1 = h2_fma(-bw, cg2, Ca1);
+                    Ca2 = h2_fma(-bw, cb2, Ca2);
+                    const h16x2 cadg = h2_fma(Ca0, G0, h2_fma(Ca1, G1, Ca2 * G2));
+                    const h16x2 dal = h2_fma(T, cdg, -h2_div_blend(cadg, oma));   // oma in [0x1.4p-7, 1]
+                    const h16x2 part = alpha * dal;
+                    a_op = part + a_op;
+                    const h16x2 dxdx = dlx * dlx, dxdy = dlx * dly, dydy = dly * dly;
+                    a_cx = part * dxdx + a_cx;
+                    a_cy = part * dxdy + a_cy;
+                    a_cz = part * dydy + a_cz;
+                    const h16x2 nT = T * oma;
+                    const h16x2 dmx = part * prep_x, dmy = part * prep_y;
+                    a_mx = dmx + a_mx;
+                    a_my = dmy + a_my;
+                    a_ax = h2from(h2bits(dmx) & 0x7fff7fffu) + a_ax;
+                    a_ay = h2from(h2bits(dmy) & 0x7fff7fffu) + a_ay;
+                    st[0] = h2bits(Ca0);
+                    st[1] = h2bits(Ca1);
+                    st[2] = h2bits(Ca2);
+                    st[3] = h2bits(nT);
             }
 #pragma unroll
             for (int q = 0; q < 4; ++q) st[q] = shr1(st[q]);
-            cur = nxt;
+            a += 16u;
+        };
+        // the next step's static words; clamped to the half's entries where
+        // some lane is off its pair (steps 31..127 read entries 1..128: entry
+        // 128, the word after the half's last, lies inside s_pair and is read
+        // only by lane 0 for step 128, where it is off its pair)
+        auto next_words = [&](auto check) {
+            if constexpr (decltype(check)::value)
+                return lds_u4_at(min(max(a, a_lo), a_hi));
+            else
+                return lds_u4_at(a);
+        };
+        auto run = [&](uint32_t s, uint32_t end, auto start, auto check) {
+            for (; s + 1u < end; s += 2u) {
+                const uint4 n = next_words(check);
+                step(s, cur, start, check);
+                cur = next_words(check);
+                step(s + 1u, n, start, check);
+            }
+            if (s < end) {
+                const uint4 n = next_words(check);
+                step(s, cur, start, check);
+                cur = n;
+            }
+        };
+        using yes = std::true_type;
+        using no = std::false_type;
+        if (steps) {
+            run(0u, 31u, yes{}, yes{});        // lanes l <= s on a pair
+            run(31u, 128u, yes{}, no{});       // every lane on a pair
+            run(128u, steps, no{}, yes{});     // lanes l > s - 128 on a pair
         }
 
         // ---- the bucket's record (:1357-1387), rounded as the reference's atomics receive it

@@ -25,7 +25,9 @@
 //             compares two zeros)        h_relu  x > 0 ? x : +0 (NaN -> +0)
 //   h_sat     clamp to [0, 1], NaN -> 0
 //   half_of_fixed  the correctly rounded half of S * 2^-24 (an exact integer
-//             sum of half values), by integer shifts as in the oracle
+//             sum of half values), by integer shifts as in the oracle;
+//             half_of_double_sum the same for a double (through float
+//             rounded toward odd)
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -65,15 +67,40 @@ __device__ __forceinline__ h16 h_rd(float x) {
 __device__ __forceinline__ h16 h_fma(h16 a, h16 b, h16 c) { return __builtin_elementwise_fma(a, b, c); }
 __device__ __forceinline__ h16x2 h2_fma(h16x2 a, h16x2 b, h16x2 c) { return __builtin_elementwise_fma(a, b, c); }
 
+// v_exp_f16 (no packed form) on both halves of x, the high result written
+// straight into the high half of the low result's register (SDWA
+// dst_sel:WORD_1, dst_unused:UNUSED_PRESERVE) instead of a separate pack. The
+// s_nop 0s are the wait states around a transcendental op's operand and
+// result. (For the reciprocal the pack costs nothing: the division's
+// finishing fmas write the two halves directly only when each reciprocal has
+// its own register.)
+__device__ __forceinline__ uint32_t h2_trans_exp(uint32_t x) {
+    uint32_t r;
+    asm(
+        "s_nop 0\n\t"
+        "v_exp_f16_e32 %0, %1\n\t"
+        "s_nop 0\n\t"
+        "v_exp_f16_sdwa %0, %1 dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE src0_sel:WORD_1\n\t"
+        "s_nop 0"
+        : "=&v"(r)
+        : "v"(x));
+    return r;
+}
+
 __device__ __forceinline__ h16 h_div(h16 a, h16 b) { return (h16)((float)a / (float)b); }
 // a / b correctly rounded for a divisor b in [0x1.4p-7, 1] (bits 0x2100 ..
 // 0x3c00: the blend backward's 1 - alpha, alpha in [0, RN(0.99)]), by
 // Markstein's iteration: y = RN(1 / b) (v_rcp_f16, equal to the correctly
 // rounded reciprocal of every positive finite half), q0 = RN(a y) clamped to
 // the finite halves, the residual r = b q0 - a exactly in float (its sign
-// keeps a zero quotient's sign), q = RN(q0 - r y) (rounded to float, then to
-// half: innocuous, 24 >= 2 * 11 + 2). Equal to h_div for every half a and
-// every b of that range (all 4.5e8 pairs, tgs_selftest_half_div_blend); other
+// keeps a zero quotient's sign), q = RN(q0 - r y) rounded once from the
+// exact value: v_fma_mixlo_f16 / v_fma_mixhi_f16 round the fused result
+// straight to half. Rounding it to float first is not innocuous here (r y
+// carries more bits than a half operation): a = 0x828d, b = 0x2353 lands on
+// a half midpoint in float and rounds to 0x9992 instead of 0x9993. So the
+// last step is written as those two instructions, not left to instruction
+// selection. Equal to h_div in both lanes for every half a and every b of
+// that range (all 4.5e8 pairs per lane, tgs_selftest_half_div_blend); other
 // divisors are not covered. P. Markstein, "Computation of elementary
 // functions on the IBM RISC System/6000 processor", IBM J. Res. Dev. 34, 1990.
 __device__ __forceinline__ h16x2 h2_div_blend(h16x2 a, h16x2 b) {
@@ -82,7 +109,14 @@ __device__ __forceinline__ h16x2 h2_div_blend(h16x2 a, h16x2 b) {
     const h16x2 q0 = __builtin_elementwise_max(__builtin_elementwise_min(a * y, lim), -lim);
     const float rx = __builtin_fmaf((float)b.x, (float)q0.x, -(float)a.x);
     const float ry = __builtin_fmaf((float)b.y, (float)q0.y, -(float)a.y);
-    return h2((h16)__builtin_fmaf(-rx, (float)y.x, (float)q0.x), (h16)__builtin_fmaf(-ry, (float)y.y, (float)q0.y));
+    // q.x = RN16(-rx y.x + q0.x), q.y = RN16(-ry y.y + q0.y); op_sel picks the
+    // high halves of y and q0 for the high lane (op_sel_hi: f16 sources)
+    uint32_t q;
+    asm("v_fma_mixlo_f16 %0, -%1, %3, %4 op_sel_hi:[0,1,1]\n\t"
+        "v_fma_mixhi_f16 %0, -%2, %3, %4 op_sel:[0,1,1] op_sel_hi:[0,1,1]"
+        : "=&v"(q)
+        : "v"(rx), "v"(ry), "v"(h2bits(y)), "v"(h2bits(q0)));
+    return h2from(q);
 }
 __device__ __forceinline__ h16 h_div_blend(h16 a, h16 b) { return h2_div_blend(h2s(a), h2s(b)).x; }
 __device__ __forceinline__ h16x2 h2_div(h16x2 a, h16x2 b) { return h2(h_div(a.x, b.x), h_div(a.y, b.y)); }
@@ -90,7 +124,7 @@ __device__ __forceinline__ h16x2 h2_div(h16x2 a, h16x2 b) { return h2(h_div(a.x,
 // 2^x: v_exp_f16, which is correctly rounded for every half input (checked
 // over all 65,536 inputs against the oracle's correctly rounded exp2)
 __device__ __forceinline__ h16 h_exp2(h16 x) { return __builtin_elementwise_exp2(x); }
-__device__ __forceinline__ h16x2 h2_exp2(h16x2 x) { return h2(h_exp2(x.x), h_exp2(x.y)); }
+__device__ __forceinline__ h16x2 h2_exp2(h16x2 x) { return h2from(h2_trans_exp(h2bits(x))); }
 
 // IEEE minNum (v_min_f16 / v_pk_min_f16): a NaN operand yields the other
 __device__ __forceinline__ h16 h_min(h16 a, h16 b) { return __builtin_elementwise_min(a, b); }
@@ -115,6 +149,25 @@ __device__ __forceinline__ float half_of_fixed(int64_t S) {
     }
     const float v = __builtin_ldexpf((float)q, shift - 24);   // exact: q < 2^12
     return S < 0 ? -v : v;
+}
+
+// The correctly rounded half of a double s (the exact double sums of half
+// records), returned as float; infinities pass, NaN gives NaN. Rounding s to
+// float and then to half would round twice: s = m + 2^-24 just above a half
+// midpoint m in [1, 2) is a float midpoint, rounds to m in float and then to
+// even in half. Rounding to float toward odd instead (truncate, then set the
+// last bit when inexact) keeps a sticky bit, and float's 24 bits >= 11 + 2
+// make the second rounding exact (S. Boldo, G. Melquiond, "When double
+// rounding is odd", IMACS 2005).
+__device__ __forceinline__ float half_of_double_sum(double s) {
+    if (s != s) return __builtin_nanf("");
+    float f = (float)s;
+    if ((double)f != s) {
+        uint32_t u = __builtin_bit_cast(uint32_t, f);
+        if (__builtin_fabs((double)f) > __builtin_fabs(s)) u -= 1u;   // the neighbour toward zero
+        f = __builtin_bit_cast(float, u | 1u);
+    }
+    return (float)(h16)f;
 }
 
 }  // namespace tgs

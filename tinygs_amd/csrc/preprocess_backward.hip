@@ -262,9 +262,10 @@ __device__ __forceinline__ void preprocess_backward_one(
 // Every record field is a half: a multiple of 2^-24 below 2^16 in magnitude.
 // A double sum of up to 8192 of them is therefore exact (its magnitude stays
 // below 2^29), and infinities and NaNs propagate as IEEE sums do (+inf and
-// -inf give NaN). The exact sum is rounded to half once (double -> float ->
-// half: innocuous, 24 >= 2 * 11 + 2). Heavy primitives with more records
-// (only grids of more than 8192 tiles) take the integer sums below.
+// -inf give NaN). The exact sum is rounded to half once (half_of_double_sum:
+// through float rounded toward odd; rounding to nearest float first would
+// round twice). Heavy primitives with more records (only grids of more than
+// 8192 tiles) take the integer sums below.
 struct HalfSumsD {
     double s[10];
     double op;
@@ -283,10 +284,7 @@ __device__ __forceinline__ void hsd_add(HalfSumsD& h, const float4& a, const flo
     h.op += (double)c.z;
 }
 
-__device__ __forceinline__ float hsd_value(double s) {
-    const float v = (float)(_Float16)(float)s;
-    return v != v ? __builtin_nanf("") : v;
-}
+__device__ __forceinline__ float hsd_value(double s) { return half_of_double_sum(s); }
 
 __device__ __forceinline__ void hsd_result(const HalfSumsD& h, float4& gA, float4& gB, float4& gC) {
     gA = make_float4(hsd_value(h.s[0]), hsd_value(h.s[1]), hsd_value(h.s[2]), hsd_value(h.s[3]));

@@ -70,9 +70,10 @@ void launch_wave_selftest(const uint32_t* in, uint32_t* out, hipStream_t s) {
 namespace tgs {
 
 // Canonical half operations on element i: a, b, c are half bit patterns
-// (op 7, 8: a holds floats; op 11: a holds int64), out receives the result's
-// bits. Op 12 checks the lane layout of DPP wave_shr:1 (whole waves: n a
-// multiple of 64).
+// (op 7, 8: a holds floats; op 11: a holds int64; op 14: doubles), out
+// receives the result's bits. Op 12 checks the lane layout of DPP
+// wave_shr:1 (whole waves: n a multiple of 64); op 13 is the packed exp2,
+// one lane per element.
 __global__ void halfmath_kernel(int op, const uint16_t* a, const uint16_t* b, const uint16_t* c, uint16_t* out,
                                 int64_t n) {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -99,6 +100,12 @@ __global__ void halfmath_kernel(int op, const uint16_t* a, const uint16_t* b, co
         case 12: {   // DPP wave_shr:1 of a: lane l receives lane l - 1's value, lane 0 keeps b
             const uint32_t v = __builtin_amdgcn_update_dpp((uint32_t)b[i], (uint32_t)a[i], 0x138, 0xf, 0xf, false);
             r = hfrom((uint16_t)v);
+            break;
+        }
+        case 14: r = h_rn(half_of_double_sum(((const double*)a)[i])); break;   // exact: the value is a half
+        case 13: {   // packed exp2 of lanes (a, b): element i takes lane i & 1
+            const h16x2 p = h2_exp2(h2(x, hfrom(b[i])));
+            r = (i & 1) ? p.y : p.x;
             break;
         }
         default: break;
@@ -176,10 +183,12 @@ void launch_half_div_check(unsigned long long* out, hipStream_t s) {
     half_div_check_kernel<<<65536u, 256, 0, s>>>(out);
 }
 
-// h_div_blend against h_div (itself checked over all pairs above) for every
-// half a and every positive b with bits in [blo, bhi], and v_rcp_f16 against
-// h_div(1, b) for those b. out: [0] quotient mismatches, [1] reciprocal
-// mismatches, [2..4] a, b, quotient of one mismatch, [5] claim flag.
+// h2_div_blend against h_div (itself checked over all pairs above) for every
+// half a and every positive b with bits in [blo, bhi], in both lanes (the low
+// lane divides a, the high lane a ^ 1, so each lane sees every dividend), and
+// v_rcp_f16 against h_div(1, b) for those b. out: [0] quotient mismatches,
+// [1] reciprocal mismatches, [2..4] a, b, quotient of one mismatch, [5] claim
+// flag.
 __global__ void __launch_bounds__(256) half_div_blend_check_kernel(unsigned long long* out, uint32_t blo,
                                                                    uint32_t bhi) {
     const uint64_t t = (uint64_t)blockIdx.x * 256u + threadIdx.x;
@@ -189,12 +198,15 @@ __global__ void __launch_bounds__(256) half_div_blend_check_kernel(unsigned long
     bool rbad = false, bad = false;
     if (on) {
         if (a == 0u) rbad = hbits(__builtin_amdgcn_rcph(hfrom(b))) != hbits(h_div((h16)1.0f, hfrom(b)));
-        const uint16_t q = hbits(h_div_blend(hfrom(a), hfrom(b)));
-        bad = q != hbits(h_div(hfrom(a), hfrom(b)));
+        const uint16_t a1 = (uint16_t)(a ^ 1u);
+        const h16x2 q2 = h2_div_blend(h2(hfrom(a), hfrom(a1)), h2s(hfrom(b)));
+        const bool bad0 = hbits(q2.x) != hbits(h_div(hfrom(a), hfrom(b)));
+        const bool bad1 = hbits(q2.y) != hbits(h_div(hfrom(a1), hfrom(b)));
+        bad = bad0 || bad1;
         if (bad && atomicAdd(&out[5], 1ull) == 0ull) {
-            out[2] = a;
+            out[2] = bad0 ? a : a1;
             out[3] = b;
-            out[4] = q;
+            out[4] = bad0 ? hbits(q2.x) : hbits(q2.y);
         }
     }
     const unsigned long long nbad = __popcll(__ballot(bad)), nr = __popcll(__ballot(rbad));
