@@ -322,6 +322,31 @@ def test_fp16_l1_bit_exact(hip, orc, wh):
     assert np.array_equal(gg, go.astype(np.float16).view(np.uint16))
 
 
+def test_fp16_l1_rounds_through_float(hip, orc):
+    """The fp16 L1 rounds its float fmaf result to half (l1.cu:93-103), i.e.
+    twice: with s = 2^-11 + 2^-34 (scale 6 + 2^-20 over 64 x 64 x 3) and the
+    accumulators at +-1, the fma's float result is the half midpoint
+    1 + 2^-11, which rounds to even (1.0); rounding the exact value once (a
+    fused v_fma_mixlo_f16) would give 1 + 2^-10."""
+    from tinygs_amd.image import ImageShape
+    shape = ImageShape(64, 64)
+    n = shape.padded_size
+    neg = (np.arange(n) & 1).astype(bool)   # odd elements: pred 0, target 1, gradient -1
+    h = lambda v: np.asarray(v, dtype=np.float16).view(np.uint16)
+    pred = np.where(neg, h(0.0), h(1.0)).astype(np.uint16)
+    targ = np.where(neg, h(1.0), h(0.0)).astype(np.uint16)
+    l0 = np.full(n, h(1.0), dtype=np.uint16)
+    g0 = np.where(neg, h(-1.0), h(1.0)).astype(np.uint16)
+    scale = np.float32(6.0 + 2.0 ** -20)
+    assert scale / np.float32(12288) == np.float32(2.0 ** -11 + 2.0 ** -34)
+    lg, gg = _loss16("l1", pred, targ, l0, g0, shape, float(scale))
+    lo, go = orc.l1(_h2f(pred), _h2f(targ), shape, scale, _h2f(l0).copy(), _h2f(g0).copy())
+    want_l, want_g = lo.astype(np.float16).view(np.uint16), go.astype(np.float16).view(np.uint16)
+    assert (want_l == 0x3c00).all() and (want_g == np.where(neg, 0xbc00, 0x3c00)).all()
+    assert np.array_equal(lg, want_l), np.unique(lg)
+    assert np.array_equal(gg, want_g), np.unique(gg)
+
+
 @pytest.mark.parametrize("wh", [(64, 64), (61, 45), (800, 600)])
 def test_fp16_ssim(hip, orc, wh):
     """fused_ssim_cuda_fp16 / fused_ssim_fp16_backward (fused_ssim.cu:445-693):

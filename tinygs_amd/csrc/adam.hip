@@ -169,7 +169,7 @@ __global__ void __launch_bounds__(kAdamThreads) adam_kernel(AdamLaunch L) {
                 if (g.theta_half) {
                     uint2 hv;
                     __half* h = (__half*)&hv;
-                    for (int q = 0; q < 4; ++q) h[q] = __float2half_rn(th[k][q]);
+                    for (int q = 0; q < 4; ++q) h[q] = f2h_rn(th[k][q]);
                     *(uint2*)((__half*)g.theta + e0) = hv;
                 } else {
                     *(float4*)((float*)g.theta + e0) = make_float4(th[k][0], th[k][1], th[k][2], th[k][3]);
@@ -182,7 +182,7 @@ __global__ void __launch_bounds__(kAdamThreads) adam_kernel(AdamLaunch L) {
                 for (int q = 0; q < 4; ++q) {
                     if (!((upd[k] >> q) & 1u)) continue;
                     if (g.theta_half)
-                        ((__half*)g.theta)[e0 + q] = __float2half_rn(th[k][q]);
+                        ((__half*)g.theta)[e0 + q] = f2h_rn(th[k][q]);
                     else
                         ((float*)g.theta)[e0 + q] = th[k][q];
                     g.m1[e0 + q] = mq[q];
@@ -197,7 +197,7 @@ __global__ void __launch_bounds__(kAdamThreads) adam_kernel(AdamLaunch L) {
                 float m = g.m1[i], v = g.m2[i];
                 t = adam_one(t, live ? g.grad[i] : 0.f, m, v, g, L.a, t1, t2, bc1, bc2s);
                 if (g.theta_half)
-                    ((__half*)g.theta)[i] = __float2half_rn(t);
+                    ((__half*)g.theta)[i] = f2h_rn(t);
                 else
                     ((float*)g.theta)[i] = t;
                 g.m1[i] = m;

@@ -21,6 +21,19 @@ constexpr float kLog2eF = 0x1.715476p+0f;      // log2(e) as float
 constexpr float kHalfLog2e = 0x1.715476p-1f;   // log2(e) / 2 (exact)
 constexpr int kGradStride = 12;         // floats of per-primitive 2D gradient record
 
+// v as computed, hidden from instruction selection. A float fma or multiply
+// followed by a conversion to half is otherwise fused into v_fma_mixlo_f16 /
+// v_fma_mixhi_f16, which round the exact value to half once; the source (and
+// the reference, whose float fmaf result is then converted) rounds to float
+// first, and the two differ where the float result lands on a half midpoint
+// (1 + 2^-11 + 2^-34 gives 1 through float, 1 + 2^-10 directly).
+__device__ __forceinline__ float f32_opaque(float v) {
+    asm("" : "+v"(v));
+    return v;
+}
+// float -> __half to nearest even of the float value as computed
+__device__ __forceinline__ __half f2h_rn(float v) { return __float2half_rn(f32_opaque(v)); }
+
 // Camera and image parameters, passed to kernels by value (no pose-block copy).
 struct CamParams {
     float fx, fy, cx, cy, near_, far_;

@@ -163,7 +163,7 @@ __device__ __forceinline__ ShT sh_store(float v);
 template <>
 __device__ __forceinline__ float sh_store<float>(float v) { return v; }
 template <>
-__device__ __forceinline__ __half sh_store<__half>(float v) { return __float2half_rn(v); }
+__device__ __forceinline__ __half sh_store<__half>(float v) { return f2h_rn(v); }
 
 struct PlyDst {
     float* means;
@@ -216,7 +216,7 @@ __device__ __forceinline__ uint32_t u8_narrow(float v) {
 template <int T>
 __device__ __forceinline__ void img_store(void* dst, size_t i, uint32_t v) {
     if constexpr (T == IT_F32) ((float*)dst)[i] = u8_widen(v);
-    else if constexpr (T == IT_F16) ((__half*)dst)[i] = __float2half_rn(u8_widen(v));
+    else if constexpr (T == IT_F16) ((__half*)dst)[i] = f2h_rn(u8_widen(v));
     else ((uint8_t*)dst)[i] = (uint8_t)v;
 }
 template <int T>
@@ -298,7 +298,7 @@ __global__ void __launch_bounds__(256) convert_kernel(const void* __restrict__ s
     } else {
         const float v = S == IT_F32 ? ((const float*)src)[i] : __half2float(((const __half*)src)[i]);
         if constexpr (D == IT_F32) ((float*)dst)[i] = v;
-        else ((__half*)dst)[i] = __float2half_rn(v);
+        else ((__half*)dst)[i] = f2h_rn(v);
     }
 }
 

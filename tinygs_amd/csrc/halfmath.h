@@ -33,6 +33,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "common.h"
+
 namespace tgs {
 
 typedef _Float16 h16;
@@ -50,7 +52,7 @@ __device__ __forceinline__ h16x2 h2(h16 a, h16 b) {
 }
 __device__ __forceinline__ h16x2 h2s(h16 a) { return h2(a, a); }
 
-__device__ __forceinline__ h16 h_rn(float x) { return (h16)x; }
+__device__ __forceinline__ h16 h_rn(float x) { return (h16)f32_opaque(x); }   // of x as computed (common.h)
 __device__ __forceinline__ float h2f(h16 x) { return (float)x; }
 
 // next half toward -inf of a finite or infinite non-NaN half

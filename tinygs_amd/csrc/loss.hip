@@ -38,10 +38,10 @@ namespace tgs {
 __device__ __forceinline__ float ld(const float* p, size_t i) { return p[i]; }
 __device__ __forceinline__ float ld(const __half* p, size_t i) { return __half2float(p[i]); }
 __device__ __forceinline__ void st(float* p, size_t i, float v) { p[i] = v; }
-__device__ __forceinline__ void st(__half* p, size_t i, float v) { p[i] = __float2half_rn(v); }
+__device__ __forceinline__ void st(__half* p, size_t i, float v) { p[i] = f2h_rn(v); }
 // a value as the image type holds it
 __device__ __forceinline__ float held(const float*, float v) { return v; }
-__device__ __forceinline__ float held(const __half*, float v) { return __half2float(__float2half_rn(v)); }
+__device__ __forceinline__ float held(const __half*, float v) { return __half2float(f2h_rn(v)); }
 
 __constant__ float kGauss[11] = {0.001028380123898387f,  0.0075987582094967365f, 0.036000773310661316f,
                                  0.10936068743467331f,   0.21300552785396576f,   0.26601171493530273f,
@@ -89,8 +89,8 @@ __global__ void l1_f16_kernel(const uint4* __restrict__ pred, const uint4* __res
 #pragma unroll
     for (int q = 0; q < 8; ++q) {
         const float d = saturate(__half2float(ph[q])) - __half2float(th[q]);
-        lr[q] = __float2half_rn(__builtin_fmaf(__builtin_fabsf(d), s, __half2float(lh[q])));
-        gr[q] = __float2half_rn(__builtin_fmaf(__builtin_copysignf(1.0f, d), s, __half2float(gh[q])));
+        lr[q] = f2h_rn(__builtin_fmaf(__builtin_fabsf(d), s, __half2float(lh[q])));
+        gr[q] = f2h_rn(__builtin_fmaf(__builtin_copysignf(1.0f, d), s, __half2float(gh[q])));
     }
     if (loss) loss[i] = lo;
     if (grad) grad[i] = go;
