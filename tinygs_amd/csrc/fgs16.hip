@@ -428,7 +428,7 @@ __global__ void __launch_bounds__(256) blend16_backward_kernel(
         const uint32_t cmax = max(readlane_u32(cnt, 0), readlane_u32(cnt, 32));
         const uint32_t steps = cmax ? 128u + cmax - 1u : 0u;
         uint4 cur = lds_u4_at(min(max(a - 16u, a_lo), a_hi));
-        auto step = [&](uint32_t s, const uint4& cur, auto start, auto check) {
+        auto step = [&](uint32_t s, const uint4& words, auto start, auto check) {
             if constexpr (decltype(start)::value)
                 if (l == 0u) {   // pair s's state at the bucket start: entry s of the init words
                     const uint4 c = lds_u4_at(a - 16u + kPairInitOfs);
@@ -437,48 +437,48 @@ __global__ void __launch_bounds__(256) blend16_backward_kernel(
             bool act = l < cnt;
             if constexpr (decltype(check)::value) act = act && s - l < 128u;
             if (act) {
-                    const h16x2 G0 = h2from(cur.x), G1 = h2from(cur.y), G2 = h2from(cur.z);
-                    h16x2 Ca0 = h2from(st[0]), Ca1 = h2from(st[1]), Ca2 = h2from(st[2]);
-                    const h16x2 T = h2from(st[3]);
-                    const h16x2 off = h2from(cur.w);
-                    const h16x2 offx = h2s(off.x), offy = h2s(off.y);
-                    const h16x2 dlx = h2_fma(inv16, -offx, mxp);
-                    const h16x2 dly = h2_fma(inv16, -offy, my2);
-                    const h16x2 cx_dx = cx2 * dlx, cy_dx = cy2 * dlx, cz_dy = cz2 * dly, cy_dy = cy2 * dly;
-                    const h16x2 cz_dyy = dly * cz_dy, cy_dxy = dlx * cy_dy;
-                    const h16x2 quad = h2_fma(dlx, cx_dx, cz_dyy);
-                    const h16x2 prep_x = cx_dx + cy_dy;
-                    const h16x2 gss = h2_exp2(h2_relu(h2_fma(h05, quad, cy_dxy)) * nk);
-                    const h16x2 prep_y = cy_dx + cz_dy;
-                    const h16x2 alpha_p = o2 * gss;
-                    const h16x2 cdg = h2_fma(cr2, G0, h2_fma(cg2, G1, cb2 * G2));
-                    const h16x2 alpha = h2_min(alpha_p, maxa);
-                    const h16x2 bw = T * alpha;
-                    const h16x2 oma = one - alpha;
-                    a_r = h2_fma(bw, G0, a_r);
-                    a_g = h2_fma(bw, G1, a_g);
-                    a_b = h2_fma(bw, G2, a_b);
-                    Ca0 = h2_fma(-bw, cr2, Ca0);
-                    Ca1 = h2_fma(-bw, cg2, Ca1);
-                    Ca2 = h2_fma(-bw, cb2, Ca2);
-                    const h16x2 cadg = h2_fma(Ca0, G0, h2_fma(Ca1, G1, Ca2 * G2));
-                    const h16x2 dal = h2_fma(T, cdg, -h2_div_blend(cadg, oma));   // oma in [0x1.4p-7, 1]
-                    const h16x2 part = alpha * dal;
-                    a_op = part + a_op;
-                    const h16x2 dxdx = dlx * dlx, dxdy = dlx * dly, dydy = dly * dly;
-                    a_cx = part * dxdx + a_cx;
-                    a_cy = part * dxdy + a_cy;
-                    a_cz = part * dydy + a_cz;
-                    const h16x2 nT = T * oma;
-                    const h16x2 dmx = part * prep_x, dmy = part * prep_y;
-                    a_mx = dmx + a_mx;
-                    a_my = dmy + a_my;
-                    a_ax = h2from(h2bits(dmx) & 0x7fff7fffu) + a_ax;
-                    a_ay = h2from(h2bits(dmy) & 0x7fff7fffu) + a_ay;
-                    st[0] = h2bits(Ca0);
-                    st[1] = h2bits(Ca1);
-                    st[2] = h2bits(Ca2);
-                    st[3] = h2bits(nT);
+                const h16x2 G0 = h2from(words.x), G1 = h2from(words.y), G2 = h2from(words.z);
+                h16x2 Ca0 = h2from(st[0]), Ca1 = h2from(st[1]), Ca2 = h2from(st[2]);
+                const h16x2 T = h2from(st[3]);
+                const h16x2 off = h2from(words.w);
+                const h16x2 offx = h2s(off.x), offy = h2s(off.y);
+                const h16x2 dlx = h2_fma(inv16, -offx, mxp);
+                const h16x2 dly = h2_fma(inv16, -offy, my2);
+                const h16x2 cx_dx = cx2 * dlx, cy_dx = cy2 * dlx, cz_dy = cz2 * dly, cy_dy = cy2 * dly;
+                const h16x2 cz_dyy = dly * cz_dy, cy_dxy = dlx * cy_dy;
+                const h16x2 quad = h2_fma(dlx, cx_dx, cz_dyy);
+                const h16x2 prep_x = cx_dx + cy_dy;
+                const h16x2 gss = h2_exp2(h2_relu(h2_fma(h05, quad, cy_dxy)) * nk);
+                const h16x2 prep_y = cy_dx + cz_dy;
+                const h16x2 alpha_p = o2 * gss;
+                const h16x2 cdg = h2_fma(cr2, G0, h2_fma(cg2, G1, cb2 * G2));
+                const h16x2 alpha = h2_min(alpha_p, maxa);
+                const h16x2 bw = T * alpha;
+                const h16x2 oma = one - alpha;
+                a_r = h2_fma(bw, G0, a_r);
+                a_g = h2_fma(bw, G1, a_g);
+                a_b = h2_fma(bw, G2, a_b);
+                Ca0 = h2_fma(-bw, cr2, Ca0);
+                Ca1 = h2_fma(-bw, cg2, Ca1);
+                Ca2 = h2_fma(-bw, cb2, Ca2);
+                const h16x2 cadg = h2_fma(Ca0, G0, h2_fma(Ca1, G1, Ca2 * G2));
+                const h16x2 dal = h2_fma(T, cdg, -h2_div_blend(cadg, oma));   // oma in [0x1.4p-7, 1]
+                const h16x2 part = alpha * dal;
+                a_op = part + a_op;
+                const h16x2 dxdx = dlx * dlx, dxdy = dlx * dly, dydy = dly * dly;
+                a_cx = part * dxdx + a_cx;
+                a_cy = part * dxdy + a_cy;
+                a_cz = part * dydy + a_cz;
+                const h16x2 nT = T * oma;
+                const h16x2 dmx = part * prep_x, dmy = part * prep_y;
+                a_mx = dmx + a_mx;
+                a_my = dmy + a_my;
+                a_ax = h2from(h2bits(dmx) & 0x7fff7fffu) + a_ax;
+                a_ay = h2from(h2bits(dmy) & 0x7fff7fffu) + a_ay;
+                st[0] = h2bits(Ca0);
+                st[1] = h2bits(Ca1);
+                st[2] = h2bits(Ca2);
+                st[3] = h2bits(nT);
             }
 #pragma unroll
             for (int q = 0; q < 4; ++q) st[q] = shr1(st[q]);
