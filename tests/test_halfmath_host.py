@@ -3,7 +3,8 @@ which the fp16 rasterizer's kernels share: add / sub / mul / div against
 numpy's float16 arithmetic (correctly rounded), fma against exact rational
 arithmetic, exp2 against a 40-digit decimal evaluation, the directed
 conversion against its definition, all with subnormal, overflow and signed
-zero cases."""
+zero cases; and the method the device uses to round exact double sums to
+half (through float rounded toward odd)."""
 import decimal
 from fractions import Fraction
 
@@ -107,3 +108,38 @@ def test_directed_conversion(orc):
     # the largest half not above f: the next half up exceeds f
     nxt = np.nextafter(rd.astype(np.float16), np.float16(np.inf)).astype(np.float64)
     assert np.all((nxt > f) | np.isinf(rd))
+
+
+def _round_to_odd_f32(s):
+    """Round float64 values to float32 toward odd: truncate toward zero, then
+    set the last bit when inexact (the device's half_of_double_sum)."""
+    f = s.astype(np.float32)
+    inexact = f.astype(np.float64) != s
+    u = f.view(np.uint32).copy()
+    away = np.abs(f.astype(np.float64)) > np.abs(s)
+    u[inexact & away] -= 1
+    u[inexact] |= 1
+    return u.view(np.float32)
+
+
+def test_double_sum_rounding_method():
+    """The method of half_of_double_sum (tinygs_amd/csrc/halfmath.h): round
+    an exact double sum of halves to float toward odd, then to nearest half,
+    equals the direct nearest half (numpy's double -> half conversion,
+    correctly rounded), while rounding to nearest float first does not:
+    near half midpoints (m + k 2^-24, |k| <= 40, at every binade a sum of
+    halves can reach) and on random multiples of 2^-24."""
+    rng = np.random.default_rng(5)
+    e = rng.integers(-13, 16, 100000)
+    q = rng.integers(1 << 10, 1 << 11, 100000)
+    mid = (2 * q + 1).astype(np.float64) * np.exp2(e - 11.0)
+    k = rng.integers(-40, 41, 100000)
+    near = np.concatenate([mid + k * 2.0 ** -24, -(mid + k * 2.0 ** -24), mid])
+    rand = (rng.integers(-(1 << 52), 1 << 52, 1 << 18) >> rng.integers(0, 52, 1 << 18)).astype(np.float64)
+    s = np.concatenate([near, rand * 2.0 ** -24, [0.0, 2.0 ** -24, 65504.0, 65519.0, 65520.0, -65520.0]])
+    with np.errstate(over="ignore"):
+        want = s.astype(np.float16).view(np.uint16)
+        odd = _round_to_odd_f32(s).astype(np.float16).view(np.uint16)
+        nearest = s.astype(np.float32).astype(np.float16).view(np.uint16)
+    assert np.array_equal(odd, want)
+    assert np.count_nonzero(nearest != want) > 100   # the double rounding it avoids
